@@ -1,0 +1,155 @@
+/*
+ * pdhip.h — the C ABI of libpdhip.so, the gfx950 (MI355X) execution backend
+ * for the kernels pdum.dsl's fusion templates produce.
+ *
+ * The reference has no C ABI of its own: its one device seat is the Python
+ * runner returned by
+ *     compile_tile(region, launch=(), prune=()) -> run(values)
+ * (conformance/triton_tile.py:662-698), which uploads f32 arrays, launches
+ * one generated Triton program per fusion group and downloads the result.
+ * Each entry point below replaces the device half of that runner for one
+ * template row of the fusion registry (packages/tensorlib/src/pdum/tl/fusion.py):
+ *
+ *   pdh_row_softmax    <- template "row-normalization"  (fusion.py:818-825, 371-400)
+ *   pdh_layernorm      <- template "row-statistics"     (fusion.py:826-843, 403-443)
+ *   pdh_flash_fwd      <- template "flash" (+ artifacts m, den) (fusion.py:480-615)
+ *   pdh_flash_bwd      <- the backward carves of the flash joint
+ *                         (autodiff.py:102-122 + partition.py:586-607: dQ, dK, dV, D)
+ *   pdh_attn_decode    <- the flash row at one query row per head, split over
+ *                         the key axis and merged with the associative
+ *                         online-softmax combine (zoo/attention.py:40-62)
+ *
+ * Conventions
+ *   - Every function returns 0 on success and a nonzero PDH_E* status on
+ *     failure; nothing is launched when a shape, stride or dtype check fails.
+ *     pdh_last_error() copies the calling thread's last message.
+ *   - Pointers are caller-owned device pointers (non-owning). The library never
+ *     allocates or frees caller memory; workspaces are passed in.
+ *   - `stream` is a hipStream_t (NULL = the default stream). Calls are
+ *     stream-ordered and asynchronous; calls on distinct streams are re-entrant.
+ *   - Strides are in ELEMENTS. The innermost (feature / column) stride is 1.
+ */
+#ifndef PDHIP_H
+#define PDHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define PDH_OK 0
+#define PDH_EINVAL 1       /* bad shape / stride / pointer / dtype combination */
+#define PDH_EUNSUPPORTED 2 /* a legal request this build has no kernel for     */
+#define PDH_ELAUNCH 3      /* the HIP runtime refused the launch               */
+
+/* element types */
+#define PDH_F32 0
+#define PDH_BF16 1
+#define PDH_F16 2
+
+/* score masks: key s is live for query row t iff
+ *   PDH_MASK_NONE : always
+ *   PDH_MASK_BAND : band_lo <= s - t <= band_hi
+ * Causal (le(iota_s, iota_t)) is BAND with band_lo = INT64_MIN, band_hi = 0;
+ * strict causal (lt) is band_hi = -1; a sliding window of width W is
+ * band_lo = 1 - W, band_hi = 0. Masked scores take the value `fill`
+ * (the reference fills with -1e9, fusion.py:508-512, zoo/tiles.py:220). */
+#define PDH_MASK_NONE 0
+#define PDH_MASK_BAND 1
+
+/* Attention geometry. Instances are (batch, head); query head h reads key/value
+ * head h / (heads_q / heads_kv) (grouped-query attention when heads_kv < heads_q).
+ * Row statistics (m, den, lse, delta) are dense fp32 [batch, heads_q, t]. */
+typedef struct pdh_attn_geom {
+  int64_t batch, heads_q, heads_kv;
+  int64_t t;  /* query rows                  (reference dim "t") */
+  int64_t s;  /* key / value rows            (reference dim "s") */
+  int64_t e;  /* q/k feature, contracted     (reference dim "e") */
+  int64_t od; /* v feature                   (reference dim "o") */
+  int64_t q_sb, q_sh, q_st; /* element strides: batch, head, row */
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+} pdh_attn_geom;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int pdh_version(void);
+
+/* Copy the calling thread's last error text (NUL-terminated, truncated to n).
+ * Returns the full length of the message. */
+size_t pdh_last_error(char* buf, size_t n);
+
+/* Number of compute units of the current device (0 on failure). */
+int pdh_device_cus(void);
+
+/* Row softmax over the last axis, fp32:
+ *   y[r, :] = exp(x[r, :] - max x[r, :]) / sum exp(x[r, :] - max x[r, :])
+ * Replaces the "row-normalization" group's runner (fusion.py:371-400 match,
+ * :339-350 stage generator; conformance/triton_tile.py:442-469 lowering).
+ * Rows are strided by ldx / ldy elements; columns are contiguous. */
+int pdh_row_softmax(const float* x, float* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy,
+                    void* stream);
+
+/* Two-pass layernorm over the last axis, fp32 (zoo/zoo_common.py:56-60, 69-72):
+ *   mu = mean x; xc = x - mu; y = xc / sqrt(mean(xc*xc) + eps) [* gamma] [+ beta]
+ * gamma / beta may be NULL (the bare "row-statistics" core, fusion.py:403-443). */
+int pdh_layernorm(const float* x, const float* gamma, const float* beta, float* y, int64_t rows,
+                  int64_t cols, int64_t ldx, int64_t ldy, float eps, void* stream);
+
+/* Flash-attention forward: the online-softmax fold of _generate_flash
+ * (fusion.py:542-615) over every (batch, head) instance:
+ *   sc[t, s]  = scale * sum_e q[t, e] k[s, e]         (masked entries -> fill)
+ *   m[t]      = max_s sc[t, s]
+ *   den[t]    = sum_s exp(sc[t, s] - m[t])
+ *   o[t, :]   = sum_s exp(sc[t, s] - m[t]) v[s, :] / den[t]
+ *   lse[t]    = m[t] + log(den[t])
+ * dtype PDH_BF16 / PDH_F16: q, k, v, o in that type, MFMA with fp32 accumulation
+ *   (e == od in {64, 128}). PDH_F32: q, k, v, o fp32, any e / od.
+ * m_out, den_out, lse_out are optional (NULL = not stored): (m, den) are the
+ * reference's artifact outputs, yield order (out, m, den) (fusion.py:611-613).
+ * prune != 0 lets kernels skip key tiles that the mask makes entirely inert;
+ * it is ignored (everything is swept) when some query row has no live key,
+ * the fully-masked-row law of fusion.py:659-690. */
+int pdh_flash_fwd(const void* q, const void* k, const void* v, void* o, float* m_out, float* den_out,
+                  float* lse_out, const pdh_attn_geom* geom, int dtype, float scale, float fill,
+                  int mask_kind, int64_t band_lo, int64_t band_hi, int prune, void* stream);
+
+/* Flash-attention backward (the closed form of the flash joint's gradients,
+ * autodiff.py:102-122 over zoo/tiles.py:238-252's naive twin):
+ *   P = exp(scale*q k^T - lse), dV = P^T dO, dP = dO v^T, delta = rowsum(dO * o),
+ *   dS = P * (dP - delta), dQ = scale * dS k, dK = scale * dS^T q.
+ * dout / dq share o / q's strides; dk / dv share k / v's strides.
+ * delta_ws: fp32 workspace of batch*heads_q*t elements (written).
+ * dtype PDH_BF16 / PDH_F16 with e == od in {64, 128}; heads_q == heads_kv. */
+int pdh_flash_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                  const float* lse, void* dq, void* dk, void* dv, float* delta_ws,
+                  const pdh_attn_geom* geom, int dtype, float scale, int mask_kind,
+                  int64_t band_lo, int64_t band_hi, void* stream);
+
+/* Decode attention (t query rows per head, small t), split over the key axis:
+ * each of `nsplit` chunks writes partial (m, den, o) to `ws`, and a merge pass
+ * applies the associative online-softmax combine (zoo/attention.py:40-46).
+ * Grouped-query: heads_q / heads_kv query heads share one key/value head and
+ * are packed into one workgroup so each key/value byte is read once.
+ * No mask (every cache row is live). lse_out optional.
+ * ws must hold pdh_attn_decode_workspace(geom, nsplit) bytes. */
+size_t pdh_attn_decode_workspace(const pdh_attn_geom* geom, int nsplit);
+int pdh_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse_out,
+                    const pdh_attn_geom* geom, int dtype, float scale, int nsplit, void* ws,
+                    size_t ws_bytes, void* stream);
+
+/* MFMA lane-layout probe (test support): multiplies one 32x16 by 16x32 bf16
+ * tile with v_mfma_f32_32x32x16_bf16 and one 16x32 by 32x16 tile with
+ * v_mfma_f32_16x16x32_bf16, each lane loading operands by the layout the
+ * attention kernels assume; c32 (32x32) and c16 (16x16) are row-major fp32. */
+int pdh_probe_mfma(const uint16_t* a32, const uint16_t* b32, float* c32, const uint16_t* a16,
+                   const uint16_t* b16, float* c16, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PDHIP_H */

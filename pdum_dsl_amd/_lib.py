@@ -1,0 +1,114 @@
+"""ctypes binding of libpdhip.so (the C ABI declared in include/pdhip.h).
+
+The library is loaded once per process. There is no fallback: a missing or
+stale library raises, so nothing on the execution path can silently run
+anywhere but the HIP kernels."""
+
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libpdhip.so"
+
+PDH_OK, PDH_EINVAL, PDH_EUNSUPPORTED, PDH_ELAUNCH = 0, 1, 2, 3
+PDH_F32, PDH_BF16, PDH_F16 = 0, 1, 2
+PDH_MASK_NONE, PDH_MASK_BAND = 0, 1
+
+I64_MIN = -(2**63)
+I64_MAX = 2**63 - 1
+
+# every symbol include/pdhip.h declares (checked by the CPU test suite)
+EXPORTS = (
+    "pdh_version",
+    "pdh_last_error",
+    "pdh_device_cus",
+    "pdh_row_softmax",
+    "pdh_layernorm",
+    "pdh_flash_fwd",
+    "pdh_flash_bwd",
+    "pdh_attn_decode_workspace",
+    "pdh_attn_decode",
+    "pdh_probe_mfma",
+)
+
+
+class PdhError(RuntimeError):
+    """A nonzero status from libpdhip, with the library's own message."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        self.fn, self.code = fn, code
+        super().__init__(f"{fn} failed (status {code}): {msg}")
+
+
+class AttnGeom(C.Structure):
+    """pdh_attn_geom: instance / shape / element-stride description."""
+
+    _fields_ = [
+        (n, C.c_int64)
+        for n in (
+            "batch heads_q heads_kv t s e od "
+            "q_sb q_sh q_st k_sb k_sh k_st v_sb v_sh v_st o_sb o_sh o_st"
+        ).split()
+    ]
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def _declare(lib) -> None:
+    vp, i64, i32, f32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
+    fp = C.POINTER(C.c_float)
+    gp = C.POINTER(AttnGeom)
+    sigs = {
+        "pdh_version": (i32, []),
+        "pdh_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
+        "pdh_device_cus": (i32, []),
+        "pdh_row_softmax": (i32, [vp, vp, i64, i64, i64, i64, vp]),
+        "pdh_layernorm": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, f32, vp]),
+        "pdh_flash_fwd": (i32, [vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, i32, vp]),
+        "pdh_flash_bwd": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, i32, i64, i64, vp]),
+        "pdh_attn_decode_workspace": (C.c_size_t, [gp, i32]),
+        "pdh_attn_decode": (i32, [vp, vp, vp, vp, vp, gp, i32, f32, i32, vp, C.c_size_t, vp]),
+        "pdh_probe_mfma": (i32, [vp, vp, vp, vp, vp, vp, vp]),
+    }
+    del fp
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def lib():
+    """The loaded library; raises if libpdhip.so has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise RuntimeError(
+                        f"{LIB_PATH} is missing: build the HIP backend first "
+                        "(python -m pdum_dsl_amd.build or __graft_entry__.build())"
+                    )
+                handle = C.CDLL(str(LIB_PATH))
+                _declare(handle)
+                _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    buf = C.create_string_buffer(1024)
+    lib().pdh_last_error(buf, len(buf))
+    return buf.value.decode(errors="replace")
+
+
+def check(fn: str, code: int) -> None:
+    if code != PDH_OK:
+        raise PdhError(fn, code, last_error())
+
+
+def call(fn: str, *args) -> None:
+    """Call a status-returning entry point; raise PdhError on failure."""
+    check(fn, getattr(lib(), fn)(*args))

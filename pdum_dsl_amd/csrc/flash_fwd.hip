@@ -1,0 +1,466 @@
+// Flash-attention forward — the "flash" template row of the fusion registry
+// (fusion.py:480-615): the online-softmax fold over key tiles, with the
+// (out, m, den) artifacts of the §7.8 variant and lse = m + log(den).
+//
+// MFMA kernel (bf16 / f16 in, fp32 accumulate), e == od == D in {64, 128}:
+//   * workgroup = 4 waves x 32 query rows = 128 rows; key tiles of 64 rows,
+//     double-buffered in LDS, filled from registers one tile ahead;
+//   * scores are computed TRANSPOSED, S^T = K Q^T with v_mfma_f32_32x32x16,
+//     so lane l owns query row (l % 32): the running max / denominator live in
+//     registers and the row max needs one cross-half shuffle per tile;
+//   * K rows are written to LDS in a permuted order (kperm_inv below) chosen so
+//     that the S^T accumulator registers ARE the B operand of the P V MFMA
+//     (O^T = V^T P^T) — no register shuffles between the two contractions;
+//   * V is transposed 8x(DG) in registers on its way into LDS (V^T rows), so
+//     every MFMA operand read is one 128-bit LDS read;
+//   * exp runs as exp2 on pre-multiplied log2(e) scores (v_exp_f32);
+//   * causal / band masks prune dead tiles (the mask-derived bounds of
+//     fusion.py:659-690) and mask only the tiles the band cuts;
+//   * heavy (late) query blocks launch first, and the workgroup index is
+//     remapped so each XCD works through whole (batch, head) instances — the
+//     instance's K/V stays in that XCD's L2.
+//
+// Generic fp32 kernel (any e, od, t, s): one wave per query row, keys in
+// chunks of 64 (one per lane), the same recurrence in fp32 — the column the
+// reference's f32 Triton runner occupies (conformance/triton_tile.py:662-698).
+#include "attn_common.h"
+
+namespace pdh {
+namespace {
+
+constexpr float kInf = __builtin_inff();
+
+struct FwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* m_out;
+  float* den_out;
+  float* lse_out;
+  int64_t heads_q, heads_kv;
+  int64_t t, s;
+  int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
+  float c2;     // scale * log2(e)
+  float fill2;  // fill * log2(e)
+  int masked;   // 0: no mask, 1: band
+  int64_t band_lo, band_hi;
+  int prune;    // skip dead tiles
+  int nqb;      // query blocks per instance
+  int xcd_remap;
+};
+
+template <int D>
+struct FwdCfg {
+  static constexpr int BM = 128;            // query rows per workgroup
+  static constexpr int BN = 64;             // key rows per tile
+  static constexpr int KROW = D * 2 + 16;   // LDS bytes per K row (16 B pad)
+  static constexpr int VROW = BN * 2 + 16;  // LDS bytes per V^T row
+  static constexpr int KBYTES = BN * KROW;
+  static constexpr int VBYTES = D * VROW;
+  static constexpr int STAGE = KBYTES + VBYTES;
+  static constexpr int LDS = 2 * STAGE;
+  static constexpr int KCH = BN * (D / 8) / 256;  // 16-byte K chunks per thread
+  static constexpr int DG = D / 32;               // V features per thread (8 keys x DG)
+};
+
+// One K/V tile held in registers between its global load and its LDS write.
+template <int D>
+struct TileRegs {
+  u32x4 k[FwdCfg<D>::KCH];
+  uint32_t v[8][FwdCfg<D>::DG / 2];
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void load_tile(TileRegs<D>& r, const uint16_t* kp, const uint16_t* vp, int64_t k_st,
+                                          int64_t v_st, int key0, int64_t S, int tid) {
+  using C = FwdCfg<D>;
+  constexpr int CPR = D / 8;      // 16-byte chunks per K row
+  constexpr int RPI = 256 / CPR;  // K rows per load instruction
+  const uint32_t k_lane = static_cast<uint32_t>((tid / CPR) * k_st * 2 + (tid % CPR) * 16);
+#pragma unroll
+  for (int i = 0; i < C::KCH; ++i) {
+    const int64_t row0 = key0 + i * RPI;  // uniform
+    r.k[i] = row0 + tid / CPR < S ? gload<u32x4>(kp + row0 * k_st, k_lane) : u32x4{0u, 0u, 0u, 0u};
+  }
+  const int dgrp = tid & 31, kgrp = tid >> 5;
+  const uint32_t v_lane = static_cast<uint32_t>(kgrp * 8 * v_st * 2 + dgrp * C::DG * 2);
+#pragma unroll
+  for (int rr = 0; rr < 8; ++rr) {
+    const int64_t key = key0 + kgrp * 8 + rr;
+    const uint16_t* base = vp + (key0 + rr) * v_st;  // uniform
+    if constexpr (C::DG == 4) {
+      const u32x2 x = key < S ? gload<u32x2>(base, v_lane) : u32x2{0u, 0u};
+      r.v[rr][0] = x.x;
+      r.v[rr][1] = x.y;
+    } else {
+      r.v[rr][0] = key < S ? gload<uint32_t>(base, v_lane) : 0u;
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void store_tile(const TileRegs<D>& r, unsigned char* stage, int tid) {
+  using C = FwdCfg<D>;
+  constexpr int CPR = D / 8;
+#pragma unroll
+  for (int i = 0; i < C::KCH; ++i) {
+    const int c = i * 256 + tid;
+    const int row = c / CPR, ch = c % CPR;
+    const int lrow = (row & ~31) + kperm_inv(row & 31);
+    *reinterpret_cast<u32x4*>(stage + lrow * C::KROW + ch * 16) = r.k[i];
+  }
+  unsigned char* vt = stage + C::KBYTES;
+  const int dgrp = tid & 31, kgrp = tid >> 5;
+#pragma unroll
+  for (int d = 0; d < C::DG; ++d) {
+    // element (key rr, feature d) sits in dword d/2, half d%2 of r.v[rr]
+    const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 w;
+    w.x = __builtin_amdgcn_perm(r.v[1][d >> 1], r.v[0][d >> 1], sel);
+    w.y = __builtin_amdgcn_perm(r.v[3][d >> 1], r.v[2][d >> 1], sel);
+    w.z = __builtin_amdgcn_perm(r.v[5][d >> 1], r.v[4][d >> 1], sel);
+    w.w = __builtin_amdgcn_perm(r.v[7][d >> 1], r.v[6][d >> 1], sel);
+    *reinterpret_cast<u32x4*>(vt + (dgrp * C::DG + d) * C::VROW + kgrp * 16) = w;
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void flash_fwd_mfma(FwdArgs a) {
+  using C = FwdCfg<D>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+
+  // workgroup -> (instance, query block); heavy (late) query blocks first
+  int bid = blockIdx.x;
+  if (a.xcd_remap) {
+    const int per = gridDim.x >> 3;
+    bid = (bid & 7) * per + (bid >> 3);
+  }
+  const int64_t inst = bid / a.nqb;
+  const int qb = a.nqb - 1 - (bid % a.nqb);
+  const int64_t b = inst / a.heads_q, hq = inst % a.heads_q;
+  const int64_t hk = hq / (a.heads_q / a.heads_kv);
+  const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.q_sb + hq * a.q_sh;
+  const uint16_t* kp = static_cast<const uint16_t*>(a.k) + b * a.k_sb + hk * a.k_sh;
+  const uint16_t* vp = static_cast<const uint16_t*>(a.v) + b * a.v_sb + hk * a.v_sh;
+  uint16_t* op = static_cast<uint16_t*>(a.o) + b * a.o_sb + hq * a.o_sh;
+  const int64_t T_ = a.t, S_ = a.s;
+  const int q0 = qb * C::BM;
+  const int qw0 = q0 + 32 * w;  // this wave's first row
+  const int qrow = qw0 + r32;   // this lane's row
+
+  // Q as the B operand of S^T = K Q^T: lane holds q[row][16 ks + 8 g .. +8]
+  u32x4 qreg[D / 16];
+  {
+    const uint16_t* qbase = qp + static_cast<int64_t>(qw0) * a.q_st;  // wave-uniform
+    const uint32_t q_lane = static_cast<uint32_t>(r32 * a.q_st * 2 + g * 16);
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+      qreg[ks] = qrow < T_ ? gload<u32x4>(qbase + ks * 16, q_lane) : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // key-tile range of the workgroup (mask-derived prune, absolute tile grid)
+  const int ntiles = static_cast<int>((S_ + C::BN - 1) / C::BN);
+  int kt_lo = 0, kt_hi = ntiles;
+  if (a.masked && a.prune) {
+    const int64_t qlast = (q0 + C::BM - 1 < T_ ? q0 + C::BM - 1 : T_ - 1);
+    if (a.band_hi < INT64_MAX / 4) {
+      const int64_t smax = qlast + a.band_hi;  // last live key of the block
+      kt_hi = smax < 0 ? 0 : static_cast<int>(smax / C::BN + 1 < ntiles ? smax / C::BN + 1 : ntiles);
+    }
+    if (a.band_lo > INT64_MIN / 4) {
+      const int64_t smin = q0 + a.band_lo;  // first live key of the block
+      kt_lo = smin <= 0 ? 0 : static_cast<int>(smin / C::BN);
+    }
+  }
+
+  float m2 = -kInf, lsum = 0.f;
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) oacc[db] = f32x16{};
+
+  TileRegs<D> pre;
+  if (kt_lo < kt_hi) {
+    load_tile<T, D>(pre, kp, vp, a.k_st, a.v_st, kt_lo * C::BN, S_, tid);
+    store_tile<D>(pre, smem, tid);
+  }
+  for (int kt = kt_lo; kt < kt_hi; ++kt) {
+    __syncthreads();
+    unsigned char* stage = smem + ((kt - kt_lo) & 1) * C::STAGE;
+    const bool more = kt + 1 < kt_hi;
+    if (more) load_tile<T, D>(pre, kp, vp, a.k_st, a.v_st, (kt + 1) * C::BN, S_, tid);
+
+    // classify this tile for this wave: dead (skip), full (no mask), or cut
+    const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
+    const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + C::BN - 1 - qw0;
+    bool dead = false, cut = key0 + C::BN > S_;
+    if (a.masked) {
+      dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
+      cut = cut || dmin < a.band_lo || dmax > a.band_hi;
+    }
+    if (!dead) {
+      f32x16 sacc[2] = {f32x16{}, f32x16{}};
+      const unsigned char* kt_lds = stage + r32 * C::KROW + g * 16;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const u32x4 kv = *reinterpret_cast<const u32x4*>(kt_lds + kb * 32 * C::KROW + ks * 32);
+          sacc[kb] = mfma32<T>(kv, qreg[ks], sacc[kb]);
+        }
+      }
+      float mloc = -kInf;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float x = sacc[kb][i] * a.c2;
+          if (cut) {
+            const int64_t key = key0 + kb * 32 + (i >> 3) * 16 + g * 8 + (i & 7);
+            const int64_t d = key - qrow;
+            if (key >= S_) x = -kInf;
+            else if (a.masked && (d < a.band_lo || d > a.band_hi)) x = a.fill2;
+          }
+          sacc[kb][i] = x;
+          mloc = fmaxf(mloc, x);
+        }
+      }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float mnew = fmaxf(m2, mloc);
+      const float alpha = fast_exp2(m2 - mnew);
+      m2 = mnew;
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
+      u32x4 p[4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float e[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            e[j] = fast_exp2(sacc[kb][8 * h + j] - mnew);
+            lsum += e[j];
+          }
+          p[2 * kb + h] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
+                                pack2<T>(e[6], e[7])};
+        }
+      }
+      const unsigned char* vt_lds = stage + C::KBYTES + r32 * C::VROW + g * 16;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+          const u32x4 vv = *reinterpret_cast<const u32x4*>(vt_lds + db * 32 * C::VROW + s * 32);
+          oacc[db] = mfma32<T>(vv, p[s], oacc[db]);
+        }
+      }
+    }
+    if (more) store_tile<D>(pre, smem + ((kt + 1 - kt_lo) & 1) * C::STAGE, tid);
+  }
+
+  // epilogue: combine the two lane halves' partial denominators, normalize, store
+  const float den = lsum + __shfl_xor(lsum, 32, 64);
+  if (qrow < T_) {
+    const float inv = den > 0.f ? 1.0f / den : 0.f;
+    uint16_t* obase = op + static_cast<int64_t>(qw0) * a.o_st;  // wave-uniform
+    const uint32_t o_lane = static_cast<uint32_t>(r32 * a.o_st * 2 + g * 8);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d0 = db * 32 + a4 * 8;  // + 4 g, carried by o_lane
+        const u32x2 wv = {pack2<T>(oacc[db][4 * a4 + 0] * inv, oacc[db][4 * a4 + 1] * inv),
+                          pack2<T>(oacc[db][4 * a4 + 2] * inv, oacc[db][4 * a4 + 3] * inv)};
+        gstore<u32x2>(obase + d0, o_lane, wv);
+      }
+    }
+    if (g == 0) {
+      const int64_t srow = inst * T_ + qrow;
+      const float m_nat = m2 * kLn2;
+      if (a.m_out) a.m_out[srow] = m_nat;
+      if (a.den_out) a.den_out[srow] = den;
+      if (a.lse_out) a.lse_out[srow] = (m2 + __log2f(den)) * kLn2;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- generic fp32
+
+struct GenArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  float* m_out;
+  float* den_out;
+  float* lse_out;
+  int64_t heads_q, heads_kv, t, s, e, od;
+  int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
+  float scale, fill;
+  int masked;
+  int64_t band_lo, band_hi;
+  int prune;
+};
+
+constexpr int kGenOdPerLane = 8;  // od <= 512 handled in registers
+
+// One wave per (instance, query row); keys in absolute chunks of 64.
+__global__ __launch_bounds__(256) void flash_fwd_generic_f32(GenArgs a, int64_t nrows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t grow = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (grow >= nrows) return;
+  const int64_t inst = grow / a.t, t = grow % a.t;
+  const int64_t b = inst / a.heads_q, hq = inst % a.heads_q, hk = hq / (a.heads_q / a.heads_kv);
+  const float* qr = a.q + b * a.q_sb + hq * a.q_sh + t * a.q_st;
+  const float* kp = a.k + b * a.k_sb + hk * a.k_sh;
+  const float* vp = a.v + b * a.v_sb + hk * a.v_sh;
+  float* orow = a.o + b * a.o_sb + hq * a.o_sh + t * a.o_st;
+
+  int64_t c_lo = 0, c_hi = (a.s + 63) / 64;
+  if (a.masked && a.prune) {
+    if (a.band_hi < INT64_MAX / 4) {
+      const int64_t smax = t + a.band_hi;
+      c_hi = smax < 0 ? 0 : (smax / 64 + 1 < c_hi ? smax / 64 + 1 : c_hi);
+    }
+    if (a.band_lo > INT64_MIN / 4) {
+      const int64_t smin = t + a.band_lo;
+      c_lo = smin <= 0 ? 0 : smin / 64;
+    }
+  }
+  float m = -kInf, l = 0.f;
+  float acc[kGenOdPerLane];
+#pragma unroll
+  for (int j = 0; j < kGenOdPerLane; ++j) acc[j] = 0.f;
+  for (int64_t c = c_lo; c < c_hi; ++c) {
+    const int64_t key = c * 64 + lane;
+    float sc = -kInf;
+    if (key < a.s) {
+      const float* kr = kp + key * a.k_st;
+      float dot = 0.f;
+      for (int64_t e = 0; e < a.e; ++e) dot = __builtin_fmaf(qr[e], kr[e], dot);
+      sc = dot * a.scale;
+      if (a.masked) {
+        const int64_t d = key - t;
+        if (d < a.band_lo || d > a.band_hi) sc = a.fill;
+      }
+    }
+    const float mnew = fmaxf(m, wave_max(sc));
+    const float alpha = __expf(m - mnew);
+    const float p = key < a.s ? __expf(sc - mnew) : 0.f;
+    l = l * alpha + wave_sum(p);
+    m = mnew;
+#pragma unroll
+    for (int j = 0; j < kGenOdPerLane; ++j) acc[j] *= alpha;
+    const int64_t nk = (a.s - c * 64) < 64 ? (a.s - c * 64) : 64;
+    for (int kk = 0; kk < nk; ++kk) {
+      const float pk = __shfl(p, kk, 64);
+      const float* vr = vp + (c * 64 + kk) * a.v_st;
+#pragma unroll
+      for (int j = 0; j < kGenOdPerLane; ++j) {
+        const int64_t d = j * 64 + lane;
+        if (d < a.od) acc[j] = __builtin_fmaf(pk, vr[d], acc[j]);
+      }
+    }
+  }
+  const float inv = 1.0f / l;
+#pragma unroll
+  for (int j = 0; j < kGenOdPerLane; ++j) {
+    const int64_t d = j * 64 + lane;
+    if (d < a.od) orow[d] = acc[j] * inv;
+  }
+  if (lane == 0) {
+    if (a.m_out) a.m_out[grow] = m;
+    if (a.den_out) a.den_out[grow] = l;
+    if (a.lse_out) a.lse_out[grow] = m + __logf(l);
+  }
+}
+
+bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
+  // row t has a live key iff max(0, t + lo) <= min(S - 1, t + hi); the
+  // tightest rows are t = 0 (needs hi >= 0) and t = T - 1 (needs T-1+lo <= S-1)
+  if (lo > hi) return true;
+  if (hi < 0) return true;
+  if (lo > INT64_MIN / 4 && (T - 1) + lo > S - 1) return true;
+  return false;
+}
+
+template <typename T, int D>
+int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
+  using C = FwdCfg<D>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&flash_fwd_mfma<T, D>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+    attr_set = true;
+  }
+  const int64_t nblk = ninst * a.nqb;
+  PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: grid too large (%lld workgroups)", (long long)nblk);
+  FwdArgs aa = a;
+  aa.xcd_remap = (nblk % 8 == 0) ? 1 : 0;
+  flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, C::LDS, st>>>(aa);
+  return check_launch("pdh_flash_fwd");
+}
+
+}  // namespace
+}  // namespace pdh
+
+using namespace pdh;
+
+extern "C" int pdh_flash_fwd(const void* q, const void* k, const void* v, void* o, float* m_out, float* den_out,
+                             float* lse_out, const pdh_attn_geom* gm, int dtype, float scale, float fill,
+                             int mask_kind, int64_t band_lo, int64_t band_hi, int prune, void* stream) {
+  PDH_REQUIRE(gm != nullptr, PDH_EINVAL, "pdh_flash_fwd: null geometry");
+  const pdh_attn_geom G = *gm;
+  PDH_REQUIRE(G.batch >= 0 && G.heads_q >= 1 && G.heads_kv >= 1 && G.t >= 0 && G.s >= 1 && G.e >= 1 && G.od >= 1,
+              PDH_EINVAL, "pdh_flash_fwd: bad shape (batch %lld heads %lld/%lld t %lld s %lld e %lld od %lld)",
+              (long long)G.batch, (long long)G.heads_q, (long long)G.heads_kv, (long long)G.t, (long long)G.s,
+              (long long)G.e, (long long)G.od);
+  PDH_REQUIRE(G.heads_q % G.heads_kv == 0, PDH_EINVAL,
+              "pdh_flash_fwd: heads_q (%lld) must be a multiple of heads_kv (%lld)", (long long)G.heads_q,
+              (long long)G.heads_kv);
+  PDH_REQUIRE(mask_kind == PDH_MASK_NONE || mask_kind == PDH_MASK_BAND, PDH_EINVAL,
+              "pdh_flash_fwd: unknown mask kind %d", mask_kind);
+  PDH_REQUIRE(q && k && v && o, PDH_EINVAL, "pdh_flash_fwd: null tensor pointer");
+  const int64_t ninst = G.batch * G.heads_q;
+  if (ninst == 0 || G.t == 0) return PDH_OK;
+  const int masked = mask_kind == PDH_MASK_BAND;
+  const int prune_ok = prune && masked && !band_has_empty_row(G.t, G.s, band_lo, band_hi);
+  hipStream_t st = as_stream(stream);
+
+  if (dtype == PDH_F32) {
+    PDH_REQUIRE(G.od <= 64 * kGenOdPerLane, PDH_EUNSUPPORTED, "pdh_flash_fwd: fp32 od > %d not supported",
+                64 * kGenOdPerLane);
+    GenArgs ga{static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+               static_cast<float*>(o), m_out, den_out, lse_out, G.heads_q, G.heads_kv, G.t, G.s, G.e, G.od,
+               G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st, G.o_sb, G.o_sh, G.o_st,
+               scale, fill, masked, band_lo, band_hi, prune_ok};
+    const int64_t nrows = ninst * G.t;
+    PDH_REQUIRE((nrows + 3) / 4 <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: too many rows");
+    flash_fwd_generic_f32<<<dim3(static_cast<unsigned>((nrows + 3) / 4)), 256, 0, st>>>(ga, nrows);
+    return check_launch("pdh_flash_fwd");
+  }
+  PDH_REQUIRE(dtype == PDH_BF16 || dtype == PDH_F16, PDH_EINVAL, "pdh_flash_fwd: unknown dtype %d", dtype);
+  PDH_REQUIRE(G.e == G.od && (G.e == 64 || G.e == 128), PDH_EUNSUPPORTED,
+              "pdh_flash_fwd: 16-bit kernels need e == od in {64, 128} (got e %lld od %lld)", (long long)G.e,
+              (long long)G.od);
+  PDH_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o), PDH_EINVAL,
+              "pdh_flash_fwd: q/k/v/o must be 16-byte aligned");
+  PDH_REQUIRE(G.q_st % 8 == 0 && G.k_st % 8 == 0 && G.v_st % 8 == 0 && G.o_st % 8 == 0 && G.q_sh % 8 == 0 &&
+                  G.k_sh % 8 == 0 && G.v_sh % 8 == 0 && G.o_sh % 8 == 0 && G.q_sb % 8 == 0 && G.k_sb % 8 == 0 &&
+                  G.v_sb % 8 == 0 && G.o_sb % 8 == 0,
+              PDH_EINVAL, "pdh_flash_fwd: 16-bit strides must be multiples of 8 elements");
+  PDH_REQUIRE(G.t <= INT32_MAX / 2 && G.s <= INT32_MAX / 2, PDH_EINVAL, "pdh_flash_fwd: sequence too long");
+  PDH_REQUIRE(G.q_st < (1 << 24) && G.k_st < (1 << 24) && G.v_st < (1 << 24) && G.o_st < (1 << 24), PDH_EINVAL,
+              "pdh_flash_fwd: row strides must be < 2^24 elements");
+  FwdArgs a{q, k, v, o, m_out, den_out, lse_out, G.heads_q, G.heads_kv, G.t, G.s,
+            G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st, G.o_sb, G.o_sh, G.o_st,
+            scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi, prune_ok,
+            static_cast<int>((G.t + 127) / 128), 0};
+  if (dtype == PDH_BF16) {
+    return G.e == 128 ? launch_mfma<__hip_bfloat16, 128>(a, ninst, st) : launch_mfma<__hip_bfloat16, 64>(a, ninst, st);
+  }
+  return G.e == 128 ? launch_mfma<_Float16, 128>(a, ninst, st) : launch_mfma<_Float16, 64>(a, ninst, st);
+}

@@ -1,0 +1,265 @@
+"""Device-resident entry points: torch tensors in, torch tensors out, every
+call a launch of the HIP kernels behind libpdhip's C ABI on the current
+stream (no host copies, no synchronization).
+
+Torch is plumbing here — device memory and streams. Shapes follow the
+reference's dims: attention tensors are [batch, heads, rows, features]
+(the reference template's 2-D q:(t,e), k:(s,e), v:(s,o) per instance,
+fusion.py:517-523, with batch and head as independent instances)."""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import (
+    I64_MAX,
+    I64_MIN,
+    PDH_BF16,
+    PDH_F16,
+    PDH_F32,
+    PDH_MASK_BAND,
+    PDH_MASK_NONE,
+    AttnGeom,
+)
+
+_DT = {torch.float32: PDH_F32, torch.bfloat16: PDH_BF16, torch.float16: PDH_F16}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _require_cuda(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("HIP kernels take device tensors (got a CPU tensor)")
+
+
+@dataclass(frozen=True)
+class Band:
+    """Score mask: key s is live for query row t iff lo <= s - t <= hi.
+    ``None`` ends are unbounded. Causal le(iota_s, iota_t) is Band(None, 0)."""
+
+    lo: int | None = None
+    hi: int | None = None
+
+    def c_args(self):
+        return (
+            I64_MIN if self.lo is None else int(self.lo),
+            I64_MAX if self.hi is None else int(self.hi),
+        )
+
+
+CAUSAL = Band(None, 0)
+
+
+# ---------------------------------------------------------------------- rows
+
+
+def row_softmax(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """softmax over the last axis of an fp32 tensor (rows = all leading dims)."""
+    _require_cuda(x)
+    if x.dtype != torch.float32:
+        raise ValueError(f"row_softmax is fp32 (got {x.dtype})")
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    y = torch.empty_like(x2) if out is None else out.reshape(-1, x.shape[-1])
+    _lib.call(
+        "pdh_row_softmax",
+        _ptr(x2), _ptr(y), x2.shape[0], x2.shape[1], x2.stride(0), y.stride(0), C.c_void_p(_stream()),
+    )
+    return y.reshape(x.shape)
+
+
+def layernorm(
+    x: torch.Tensor,
+    gamma: torch.Tensor | None = None,
+    beta: torch.Tensor | None = None,
+    eps: float = 1e-5,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Two-pass layernorm over the last axis, fp32, optional affine epilogue."""
+    _require_cuda(x, gamma, beta)
+    for t in (x, gamma, beta):
+        if t is not None and t.dtype != torch.float32:
+            raise ValueError("layernorm is fp32")
+    n = x.shape[-1]
+    for nm, t in (("gamma", gamma), ("beta", beta)):
+        if t is not None and (t.numel() != n or not t.is_contiguous()):
+            raise ValueError(f"{nm} must be a contiguous vector of {n} elements")
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    y = torch.empty_like(x2) if out is None else out.reshape(-1, n)
+    _lib.call(
+        "pdh_layernorm",
+        _ptr(x2), _ptr(gamma), _ptr(beta), _ptr(y), x2.shape[0], n, x2.stride(0), y.stride(0),
+        C.c_float(eps), C.c_void_p(_stream()),
+    )
+    return y.reshape(x.shape)
+
+
+# ----------------------------------------------------------------- attention
+
+
+def _geom(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor) -> AttnGeom:
+    for nm, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+        if t.dim() != 4:
+            raise ValueError(f"{nm} must be [batch, heads, rows, features] (got shape {tuple(t.shape)})")
+        if t.stride(-1) != 1:
+            raise ValueError(f"{nm}'s feature axis must be contiguous")
+    B, Hq, T, E = q.shape
+    Bk, Hkv, S, Ek = k.shape
+    if (Bk, Ek) != (B, E) or v.shape[:3] != k.shape[:3] or o.shape[:3] != q.shape[:3] or o.shape[3] != v.shape[3]:
+        raise ValueError(
+            f"shape mismatch: q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)} o {tuple(o.shape)}"
+        )
+    if Hq % Hkv:
+        raise ValueError(f"query heads ({Hq}) must be a multiple of key/value heads ({Hkv})")
+    g = AttnGeom()
+    g.batch, g.heads_q, g.heads_kv, g.t, g.s, g.e, g.od = B, Hq, Hkv, T, S, E, v.shape[3]
+    g.q_sb, g.q_sh, g.q_st = q.stride(0), q.stride(1), q.stride(2)
+    g.k_sb, g.k_sh, g.k_st = k.stride(0), k.stride(1), k.stride(2)
+    g.v_sb, g.v_sh, g.v_st = v.stride(0), v.stride(1), v.stride(2)
+    g.o_sb, g.o_sh, g.o_st = o.stride(0), o.stride(1), o.stride(2)
+    return g
+
+
+@dataclass
+class FlashOut:
+    o: torch.Tensor
+    lse: torch.Tensor | None
+    m: torch.Tensor | None
+    den: torch.Tensor | None
+
+
+def flash_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    scale: float | None = None,
+    band: Band | None = None,
+    fill: float = -1e9,
+    prune: bool = True,
+    want_lse: bool = True,
+    want_artifacts: bool = False,
+    out: torch.Tensor | None = None,
+) -> FlashOut:
+    """Flash-attention forward over [B, H, T, E] q and [B, Hkv, S, E] k / v.
+
+    ``band`` None means every key is live; masked scores take ``fill``.
+    Returns the output plus lse and, with ``want_artifacts``, the reference's
+    (m, den) artifacts ([B, H, T] fp32)."""
+    _require_cuda(q, k, v)
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DT:
+        raise ValueError(f"q/k/v must share one dtype of f32/bf16/f16 (got {q.dtype}, {k.dtype}, {v.dtype})")
+    B, H, T, _ = q.shape
+    o = torch.empty(q.shape[:3] + (v.shape[3],), dtype=q.dtype, device=q.device) if out is None else out
+    g = _geom(q, k, v, o)
+    st = dict(dtype=torch.float32, device=q.device)
+    lse = torch.empty((B, H, T), **st) if want_lse else None
+    m = torch.empty((B, H, T), **st) if want_artifacts else None
+    den = torch.empty((B, H, T), **st) if want_artifacts else None
+    sc = 1.0 / math.sqrt(q.shape[3]) if scale is None else float(scale)
+    kind, (lo, hi) = (PDH_MASK_NONE, (0, 0)) if band is None else (PDH_MASK_BAND, band.c_args())
+    _lib.call(
+        "pdh_flash_fwd",
+        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(m), _ptr(den), _ptr(lse), C.byref(g), _DT[q.dtype],
+        C.c_float(sc), C.c_float(fill), kind, lo, hi, int(bool(prune)), C.c_void_p(_stream()),
+    )
+    return FlashOut(o, lse, m, den)
+
+
+def flash_bwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    do: torch.Tensor,
+    lse: torch.Tensor,
+    *,
+    scale: float | None = None,
+    band: Band | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients (dq, dk, dv) of flash attention given the forward's lse."""
+    _require_cuda(q, k, v, o, do, lse)
+    if do.shape != o.shape or do.stride() != o.stride():
+        raise ValueError("dO must match O's shape and strides")
+    g = _geom(q, k, v, o)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    if dq.stride() != q.stride() or dk.stride() != k.stride() or dv.stride() != v.stride():
+        raise ValueError("q/k/v must be dense (their gradients share their strides)")
+    if lse.dtype != torch.float32 or not lse.is_contiguous() or lse.shape != q.shape[:3]:
+        raise ValueError("lse must be contiguous fp32 [batch, heads, rows]")
+    delta = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+    sc = 1.0 / math.sqrt(q.shape[3]) if scale is None else float(scale)
+    kind, (lo, hi) = (PDH_MASK_NONE, (0, 0)) if band is None else (PDH_MASK_BAND, band.c_args())
+    _lib.call(
+        "pdh_flash_bwd",
+        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta),
+        C.byref(g), _DT[q.dtype], C.c_float(sc), kind, lo, hi, C.c_void_p(_stream()),
+    )
+    return dq, dk, dv
+
+
+def attn_decode(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    scale: float | None = None,
+    nsplit: int | None = None,
+    want_lse: bool = True,
+    workspace: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Split-K decode attention: q [B, Hq, t, D] (small t) against the cache
+    k / v [B, Hkv, S, D]; every cache row is live."""
+    _require_cuda(q, k, v)
+    B, Hq, T, D = q.shape
+    o = torch.empty((B, Hq, T, v.shape[3]), dtype=q.dtype, device=q.device)
+    g = _geom(q, k, v, o)
+    if nsplit is None:
+        nsplit = pick_decode_splits(B * k.shape[1], k.shape[2])
+    need = _lib.lib().pdh_attn_decode_workspace(C.byref(g), int(nsplit))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty((max(need, 16) + 3) // 4, dtype=torch.float32, device=q.device)
+    lse = torch.empty((B, Hq, T), dtype=torch.float32, device=q.device) if want_lse else None
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    _lib.call(
+        "pdh_attn_decode",
+        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), C.byref(g), _DT[q.dtype], C.c_float(sc), int(nsplit),
+        _ptr(workspace), C.c_size_t(workspace.numel() * workspace.element_size()), C.c_void_p(_stream()),
+    )
+    return o, lse
+
+
+def pick_decode_splits(groups: int, s: int, cus: int | None = None) -> int:
+    """Splits so the (batch x kv-head x split) grid covers the chip ~8 deep,
+    with at least 256 keys per split."""
+    if cus is None:
+        cus = _lib.lib().pdh_device_cus() or 256
+    want = max(1, (8 * cus + groups - 1) // groups)
+    return int(max(1, min(want, s // 256 if s >= 256 else 1)))
+
+
+def probe_mfma(a32, b32, a16, b16):
+    """Run the MFMA lane-layout probe; inputs are bf16 device tensors."""
+    c32 = torch.empty((32, 32), dtype=torch.float32, device=a32.device)
+    c16 = torch.empty((16, 16), dtype=torch.float32, device=a32.device)
+    _lib.call(
+        "pdh_probe_mfma", _ptr(a32), _ptr(b32), _ptr(c32), _ptr(a16), _ptr(b16), _ptr(c16), C.c_void_p(_stream())
+    )
+    return c32, c16

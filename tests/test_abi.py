@@ -1,0 +1,47 @@
+"""The C ABI boundary on the CPU: the built library loads and exports every
+symbol include/pdhip.h declares; no compute is launched."""
+
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "pdhip.h").read_text()
+    return sorted(set(re.findall(r"\b(pdh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_table():
+    from pdum_dsl_amd._lib import EXPORTS
+
+    assert _declared() == sorted(EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    from pdum_dsl_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libpdhip.so is not built: run __graft_entry__.build() first")
+    lib = _lib.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.pdh_version() == 100
+
+
+def test_validation_errors_need_no_device():
+    """Shape checks fire before any HIP call, so they run here without a GPU."""
+    import ctypes as C
+
+    from pdum_dsl_amd import _lib
+
+    lib = _lib.lib()
+    rc = lib.pdh_row_softmax(None, None, 4, 0, 0, 0, None)
+    assert rc == _lib.PDH_EINVAL and "cols >= 1" in _lib.last_error()
+    g = _lib.AttnGeom()
+    g.batch, g.heads_q, g.heads_kv, g.t, g.s, g.e, g.od = 1, 3, 2, 8, 8, 64, 64
+    rc = lib.pdh_flash_fwd(None, None, None, None, None, None, None, C.byref(g), 1, 1.0, -1e9, 0, 0, 0, 1, None)
+    assert rc == _lib.PDH_EINVAL and "multiple of heads_kv" in _lib.last_error()
+    assert lib.pdh_attn_decode_workspace(C.byref(g), 4) == 1 * 3 * 8 * 4 * (2 + 64) * 4

@@ -1,0 +1,212 @@
+"""Kernel-level parity on the GPU: every libpdhip entry point against the
+float64 oracle (oracle/closed_forms.py) on seeded inputs, plus the
+reference's structural laws (pruned == unpruned bit-exact,
+fusion.py:659-690 / conformance/test_fusion_triton.py:140-159; the
+fully-masked row keeps uniform-softmax semantics, test_launch.py:82-111)."""
+
+import numpy as np
+import pytest
+
+from oracle import closed_forms as cf
+from tests.tolerances import assert_fp32, assert_lowp
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def K():
+    from pdum_dsl_amd import kernels
+
+    return kernels
+
+
+def _dev(a, dtype=torch.float32):
+    return torch.as_tensor(np.ascontiguousarray(a)).to(dtype=dtype, device="cuda")
+
+
+def _host(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+# ------------------------------------------------------------------ MFMA probe
+
+
+def test_mfma_lane_layouts_match_a_matmul(K):
+    rng = np.random.default_rng(0)
+    a32, b32 = rng.standard_normal((32, 16)), rng.standard_normal((16, 32))
+    a16, b16 = rng.standard_normal((16, 32)), rng.standard_normal((32, 16))
+    ta32, tb32, ta16, tb16 = (_dev(x, torch.bfloat16) for x in (a32, b32, a16, b16))
+    c32, c16 = K.probe_mfma(ta32, tb32, ta16, tb16)
+    torch.cuda.synchronize()
+    want32 = _host(ta32) @ _host(tb32)
+    want16 = _host(ta16) @ _host(tb16)
+    np.testing.assert_allclose(_host(c32), want32, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(_host(c16), want16, rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- row kernels
+
+
+@pytest.mark.parametrize(
+    "rows,cols",
+    [(1, 1), (3, 7), (64, 256), (37, 1000), (128, 4096), (5, 4099), (8, 12000), (2, 64)],
+)
+def test_row_softmax_matches_oracle(K, rows, cols):
+    rng = np.random.default_rng(rows * 7919 + cols)
+    x = rng.standard_normal((rows, cols)) * 3.0
+    y = K.row_softmax(_dev(x))
+    torch.cuda.synchronize()
+    xf = x.astype(np.float32).astype(np.float64)
+    assert_fp32(_host(y), cf.np_softmax(xf, axis=1), what=f"softmax {rows}x{cols}")
+
+
+def test_row_softmax_strided_rows(K):
+    rng = np.random.default_rng(5)
+    base = _dev(rng.standard_normal((16, 300)))
+    x = base[:, 10:266]  # row stride 300, 16-byte misaligned start -> streaming kernel
+    y = K.row_softmax(x)
+    torch.cuda.synchronize()
+    assert_fp32(_host(y), cf.np_softmax(_host(x), axis=1), what="strided softmax")
+
+
+@pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("rows,cols", [(4, 4), (33, 768), (64, 4096), (3, 5000), (7, 129)])
+def test_layernorm_matches_oracle(K, rows, cols, affine):
+    rng = np.random.default_rng(rows + 31 * cols)
+    x = rng.standard_normal((rows, cols)) + 0.5
+    g = 1 + 0.1 * rng.standard_normal(cols) if affine else None
+    b = 0.1 * rng.standard_normal(cols) if affine else None
+    y = K.layernorm(_dev(x), None if g is None else _dev(g), None if b is None else _dev(b), eps=1e-5)
+    torch.cuda.synchronize()
+    f = lambda a: None if a is None else a.astype(np.float32).astype(np.float64)  # noqa: E731
+    want = cf.np_layernorm(f(x), f(g), f(b), eps=1e-5)
+    assert_fp32(_host(y), want, rtol=1e-5, atol=1e-5, what=f"layernorm {rows}x{cols}")
+
+
+# ---------------------------------------------------------- flash forward
+
+
+def _qkv(rng, B, Hq, Hkv, T, S, E, OD, dtype):
+    q = _dev(rng.standard_normal((B, Hq, T, E)), dtype)
+    k = _dev(rng.standard_normal((B, Hkv, S, E)), dtype)
+    v = _dev(rng.standard_normal((B, Hkv, S, OD)), dtype)
+    return q, k, v
+
+
+def _check_fwd(res, q, k, v, scale, band, lowp):
+    Q, Kh, V = _host(q), _host(k), _host(v)
+    want = cf.attention_batched(Q, Kh, V, scale=scale, band=band)
+    o, lse = _host(res.o), _host(res.lse)
+    m = _host(res.m) if res.m is not None else None
+    den = _host(res.den) if res.den is not None else None
+    for (b, h), (wo, wm, wden, wlse) in want.items():
+        if lowp:
+            assert_lowp(o[b, h], wo, what=f"out[{b},{h}]")
+        else:
+            assert_fp32(o[b, h], wo, rtol=1e-5, atol=1e-5, what=f"out[{b},{h}]")
+        np.testing.assert_allclose(lse[b, h], wlse, rtol=1e-4, atol=1e-4, err_msg=f"lse[{b},{h}]")
+        if m is not None:
+            np.testing.assert_allclose(m[b, h], wm, rtol=1e-5, atol=1e-5, err_msg=f"m[{b},{h}]")
+            np.testing.assert_allclose(den[b, h], wden, rtol=1e-4, atol=1e-5, err_msg=f"den[{b},{h}]")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,T,S,D,causal",
+    [
+        (1, 2, 2, 128, 128, 128, True),
+        (2, 2, 2, 256, 256, 128, False),
+        (1, 4, 2, 200, 200, 128, True),  # ragged rows and keys, GQA
+        (1, 2, 1, 77, 333, 64, False),
+        (2, 1, 1, 384, 384, 64, True),
+        (1, 1, 1, 1, 1, 128, True),
+    ],
+)
+def test_flash_fwd_mfma_matches_oracle(K, dtype, B, Hq, Hkv, T, S, D, causal):
+    rng = np.random.default_rng(B * 1000 + T + S + D)
+    q, k, v = _qkv(rng, B, Hq, Hkv, T, S, D, D, dtype)
+    band = (None, 0) if causal else None
+    scale = 1.0 / np.sqrt(D)
+    res = K.flash_fwd(q, k, v, scale=scale, band=K.Band(*band) if band else None, want_artifacts=True)
+    torch.cuda.synchronize()
+    _check_fwd(res, q, k, v, scale, band, lowp=True)
+
+
+@pytest.mark.parametrize(
+    "T,S,E,OD,causal",
+    [(6, 6, 3, 2, True), (256, 256, 64, 64, False), (100, 70, 33, 17, True), (5, 130, 8, 200, False)],
+)
+def test_flash_fwd_fp32_generic_matches_oracle(K, T, S, E, OD, causal):
+    rng = np.random.default_rng(T * 31 + S)
+    q, k, v = _qkv(rng, 1, 2, 2, T, S, E, OD, torch.float32)
+    band = (None, 0) if causal else None
+    res = K.flash_fwd(q, k, v, scale=0.125, band=K.Band(*band) if band else None, want_artifacts=True)
+    torch.cuda.synchronize()
+    _check_fwd(res, q, k, v, 0.125, band, lowp=False)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_pruned_sweep_is_bit_equal_to_the_full_sweep(K, dtype):
+    rng = np.random.default_rng(11)
+    D = 128 if dtype != torch.float32 else 40
+    q, k, v = _qkv(rng, 1, 2, 2, 320, 320, D, D, dtype)
+    full = K.flash_fwd(q, k, v, band=K.CAUSAL, prune=False, want_artifacts=True)
+    pruned = K.flash_fwd(q, k, v, band=K.CAUSAL, prune=True, want_artifacts=True)
+    torch.cuda.synchronize()
+    assert torch.equal(full.o, pruned.o)
+    assert torch.equal(full.m, pruned.m) and torch.equal(full.den, pruned.den)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_a_fully_masked_row_keeps_uniform_softmax(K, dtype):
+    """Strict causal (lt) masks row 0 entirely: its softmax is uniform over
+    the fill, so the kernel must sweep every tile for it (no pruning)."""
+    rng = np.random.default_rng(3)
+    D = 64
+    q, k, v = _qkv(rng, 1, 1, 1, 130, 130, D, D, dtype)
+    band = (None, -1)
+    res = K.flash_fwd(q, k, v, scale=0.125, band=K.Band(*band), prune=True, want_artifacts=True)
+    torch.cuda.synchronize()
+    _check_fwd(res, q, k, v, 0.125, band, lowp=dtype != torch.float32)
+    np.testing.assert_allclose(_host(res.o)[0, 0, 0], _host(v)[0, 0].mean(axis=0), rtol=2e-2, atol=2e-2)
+
+
+def test_sliding_window_band(K):
+    rng = np.random.default_rng(21)
+    q, k, v = _qkv(rng, 1, 2, 2, 300, 300, 128, 128, torch.bfloat16)
+    band = (-63, 0)  # t - s < 64
+    res = K.flash_fwd(q, k, v, band=K.Band(*band), want_artifacts=True)
+    torch.cuda.synchronize()
+    _check_fwd(res, q, k, v, 1 / np.sqrt(128), band, lowp=True)
+
+
+# ------------------------------------------------------------------- decode
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,T,S,D,nsplit",
+    [(2, 8, 2, 1, 1000, 128, 3), (1, 4, 4, 1, 64, 64, 1), (3, 32, 8, 1, 2048, 128, None), (1, 4, 1, 2, 777, 128, 4)],
+)
+def test_decode_matches_oracle(K, dtype, B, Hq, Hkv, T, S, D, nsplit):
+    rng = np.random.default_rng(S + Hq)
+    q, k, v = _qkv(rng, B, Hq, Hkv, T, S, D, D, dtype)
+    o, lse = K.attn_decode(q, k, v, nsplit=nsplit)
+    torch.cuda.synchronize()
+    want = cf.attention_batched(_host(q), _host(k), _host(v), scale=1 / np.sqrt(D))
+    O, L = _host(o), _host(lse)
+    for (b, h), (wo, _, _, wlse) in want.items():
+        assert_lowp(O[b, h], wo, what=f"decode out[{b},{h}]")
+        np.testing.assert_allclose(L[b, h], wlse, rtol=1e-4, atol=1e-4)
+
+
+def test_entry_points_refuse_bad_shapes_without_launching(K):
+    from pdum_dsl_amd._lib import PdhError
+
+    q = torch.zeros((1, 1, 8, 96), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(PdhError, match="e == od"):
+        K.flash_fwd(q, q, q)
+    with pytest.raises(ValueError, match="fp32"):
+        K.row_softmax(q)
