@@ -121,13 +121,21 @@ int pdh_flash_fwd(const void* q, const void* k, const void* v, void* o, float* m
  * autodiff.py:102-122 over zoo/tiles.py:238-252's naive twin):
  *   P = exp(scale*q k^T - lse), dV = P^T dO, dP = dO v^T, delta = rowsum(dO * o),
  *   dS = P * (dP - delta), dQ = scale * dS k, dK = scale * dS^T q.
+ * Row statistics come from the forward: lse (required), and optionally the
+ * (m, den) artifacts. Masked scores take `fill` (as in the forward) and carry
+ * no gradient. A row whose keys are ALL masked has uniform probabilities
+ * 1/den (the reference's fully-masked-row semantics); fp32 cannot hold that
+ * row's lse = fill + log(den) exactly, so with (m, den) given the kernels
+ * use exp(fill - m) / den, and without them a row whose lse lies within
+ * 2^6 of the fill (in log2 units) is taken as fully masked (P = 1/s).
  * dout / dq share o / q's strides; dk / dv share k / v's strides.
- * delta_ws: fp32 workspace of batch*heads_q*t elements (written).
+ * ws: fp32 workspace of 3*batch*heads_q*t elements (delta, log2-domain
+ * statistic, masked-entry probability per row; written).
  * dtype PDH_BF16 / PDH_F16 with e == od in {64, 128}; heads_q == heads_kv. */
 int pdh_flash_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
-                  const float* lse, void* dq, void* dk, void* dv, float* delta_ws,
-                  const pdh_attn_geom* geom, int dtype, float scale, int mask_kind,
-                  int64_t band_lo, int64_t band_hi, void* stream);
+                  const float* lse, const float* m_in, const float* den_in, void* dq, void* dk, void* dv,
+                  float* ws, const pdh_attn_geom* geom, int dtype, float scale, float fill,
+                  int mask_kind, int64_t band_lo, int64_t band_hi, void* stream);
 
 /* Decode attention (t query rows per head, small t), split over the key axis:
  * each of `nsplit` chunks writes partial (m, den, o) to `ws`, and a merge pass

@@ -69,7 +69,7 @@ def _declare(lib) -> None:
         "pdh_row_softmax": (i32, [vp, vp, i64, i64, i64, i64, vp]),
         "pdh_layernorm": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, f32, vp]),
         "pdh_flash_fwd": (i32, [vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, i32, vp]),
-        "pdh_flash_bwd": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, i32, i64, i64, vp]),
+        "pdh_flash_bwd": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, vp]),
         "pdh_attn_decode_workspace": (C.c_size_t, [gp, i32]),
         "pdh_attn_decode": (i32, [vp, vp, vp, vp, vp, gp, i32, f32, i32, vp, C.c_size_t, vp]),
         "pdh_probe_mfma": (i32, [vp, vp, vp, vp, vp, vp, vp]),

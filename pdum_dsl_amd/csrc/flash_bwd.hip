@@ -4,7 +4,10 @@
 // Like the reference's carving, every output is owned by exactly one program
 // (330 §7.8 ruling 4): no atomics.
 //
-//   bwd_delta : delta[t] = sum_d dO[t, d] O[t, d]                  (HBM-bound)
+//   bwd_stats : per query row: delta = sum_d dO O, the log2-domain statistic
+//               lse2 (P = exp2(x - lse2) for live scores) and pm, the
+//               probability of a MASKED score (0 unless every key of the
+//               row is masked; then 1/den, the uniform-softmax row)  (HBM-bound)
 //   bwd_dkdv  : grid over 128-key blocks (4 waves x 32 keys); sweeps query
 //               tiles; each wave keeps its K and V rows in registers and
 //               accumulates dK^T, dV^T:
@@ -19,8 +22,8 @@
 // kperm_inv row permutation, so the score accumulators feed the next
 // contraction's k operand directly (see attn_common.h). Transposed copies
 // (Q^T, dO^T, K^T) are formed in registers on the way into LDS.
-// Masks: masked scores take the fill (P = exp(fill - lse) = 0 for any row
-// with a live key) and carry no gradient (dS = 0), as the where() adjoint.
+// Masks: a masked score's probability is the row's pm (0 for any row with a
+// live key) and carries no gradient (dS = 0), as the where() adjoint.
 #include "attn_common.h"
 
 namespace pdh {
@@ -33,10 +36,13 @@ struct BwdArgs {
   const uint16_t* o;
   const uint16_t* dout;
   const float* lse;
+  const float* m_in;    // optional forward artifacts (exact fully-masked rows)
+  const float* den_in;
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
-  float* delta;
+  float* ws;            // [3][rows]: delta, lse2, pm
+  int64_t rows;         // batch * heads * t
   int64_t heads, t, s;
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
   float scale, c2, fill2;
@@ -46,15 +52,13 @@ struct BwdArgs {
   int nblk;  // blocks per instance (query blocks for dq, key blocks for dkdv)
 };
 
-constexpr float kInf = __builtin_inff();
-
-// ---------------------------------------------------------------- delta
+// ---------------------------------------------------------------- row stats
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void bwd_delta(BwdArgs a, int64_t nrows) {
+__global__ __launch_bounds__(256) void bwd_stats(BwdArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= nrows) return;
+  if (row >= a.rows) return;
   const int64_t inst = row / a.t, tq = row % a.t;
   const int64_t b = inst / a.heads, h = inst % a.heads;
   const uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + tq * a.o_st;
@@ -64,7 +68,21 @@ __global__ __launch_bounds__(256) void bwd_delta(BwdArgs a, int64_t nrows) {
   for (int j = 0; j < D / 64; ++j)
     acc += Elem<T>::to_f32(orow[j * 64 + lane]) * Elem<T>::to_f32(drow[j * 64 + lane]);
   acc = wave_sum(acc);
-  if (lane == 0) a.delta[row] = acc;
+  if (lane == 0) {
+    float lse2, pm = 0.f;
+    if (a.m_in != nullptr) {
+      const float m2 = a.m_in[row] * kLog2e, den = a.den_in[row];
+      lse2 = m2 + __log2f(den);
+      if (a.masked) pm = fast_exp2(a.fill2 - m2) / den;  // exact 1/den for a fully-masked row
+    } else {
+      lse2 = a.lse[row] * kLog2e;
+      // fully masked: lse = fill + log(s) is the fill in fp32 (uniform row, P = 1/s)
+      if (a.masked) pm = (lse2 - a.fill2 < 64.f) ? 1.0f / static_cast<float>(a.s) : fast_exp2(a.fill2 - lse2);
+    }
+    a.ws[row] = acc;
+    a.ws[a.rows + row] = lse2;
+    a.ws[2 * a.rows + row] = pm;
+  }
 }
 
 // ---------------------------------------------------------- tile staging
@@ -83,17 +101,22 @@ template <int ROWS, int D>
 __device__ __forceinline__ void tload(TileT<ROWS, D>& t, const uint16_t* base, int64_t ld, int64_t nvalid,
                                       int tid) {
   constexpr int DG = TileT<ROWS, D>::DG, NDG = TileT<ROWS, D>::NDG;
+  // Rows past nvalid (>= 1) re-read the last valid row and are zeroed by a
+  // select: no divergent branches around the loads.
   const int dgrp = tid % NDG, rgrp = tid / NDG;
-  const uint32_t off = static_cast<uint32_t>(rgrp * 8 * ld * 2 + dgrp * DG * 2);
+  const int last = static_cast<int>(nvalid < ROWS ? nvalid - 1 : ROWS - 1);
 #pragma unroll
   for (int rr = 0; rr < 8; ++rr) {
-    const bool ok = rgrp * 8 + rr < nvalid;
+    const int row = rgrp * 8 + rr;
+    const bool ok = row <= last;
+    const uint32_t off = static_cast<uint32_t>((ok ? row : last) * ld * 2 + dgrp * DG * 2);
     if constexpr (DG == 4) {
-      const u32x2 x = ok ? gload<u32x2>(base + rr * ld, off) : u32x2{0u, 0u};
-      t.r[rr][0] = x.x;
-      t.r[rr][1] = x.y;
+      const u32x2 x = gload<u32x2>(base, off);
+      t.r[rr][0] = ok ? x.x : 0u;
+      t.r[rr][1] = ok ? x.y : 0u;
     } else {
-      t.r[rr][0] = ok ? gload<uint32_t>(base + rr * ld, off) : 0u;
+      const uint32_t x = gload<uint32_t>(base, off);
+      t.r[rr][0] = ok ? x : 0u;
     }
   }
 }
@@ -159,12 +182,13 @@ struct DkdvCfg {
   static constexpr int QTR = D * TS;
   static constexpr int OFF_QT = QR, OFF_DO = QR + QTR, OFF_DOT = 2 * QR + QTR, OFF_LSE = 2 * QR + 2 * QTR;
   static constexpr int OFF_DEL = OFF_LSE + QT * 4;
-  static constexpr int STAGE = OFF_DEL + QT * 4;
+  static constexpr int OFF_PM = OFF_DEL + QT * 4;
+  static constexpr int STAGE = OFF_PM + QT * 4;
   static constexpr int LDS = 2 * STAGE;
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void bwd_dkdv(BwdArgs a) {
+__global__ __launch_bounds__(256, 1) void bwd_dkdv(BwdArgs a) {
   using C = DkdvCfg<D>;
   constexpr int QT = C::QT, NQB = QT / 32;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -176,8 +200,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv(BwdArgs a) {
   const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
   const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
   const uint16_t* dop = a.dout + b * a.o_sb + h * a.o_sh;
-  const float* lsep = a.lse + inst * a.t;
-  const float* delp = a.delta + inst * a.t;
+  const float* delp = a.ws + inst * a.t;
+  const float* lsep = a.ws + a.rows + inst * a.t;
+  const float* pmp = a.ws + 2 * a.rows + inst * a.t;
   const int64_t T_ = a.t, S_ = a.s;
   const int k0 = kblk * C::KB;
   const int kw0 = k0 + 32 * w;
@@ -219,7 +244,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv(BwdArgs a) {
   }
 
   TileT<QT, D> tq, tdo;
-  float pl = 0.f, pd = 0.f;  // this thread's lse / delta staging value (tid < QT)
+  float pl = 0.f, pd = 0.f, pq = 0.f;  // this thread's lse2 / delta / pm staging values (tid < QT)
   auto fetch = [&](int qt) {
     const int64_t q0 = static_cast<int64_t>(qt) * QT;
     const int64_t nv = T_ - q0;
@@ -227,8 +252,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv(BwdArgs a) {
     tload<QT, D>(tdo, dop + q0 * a.o_st, a.o_st, nv, tid);
     if (tid < QT) {
       const bool ok = q0 + tid < T_;
-      pl = ok ? lsep[q0 + tid] * kLog2e : 0.f;
+      pl = ok ? lsep[q0 + tid] : 0.f;
       pd = ok ? delp[q0 + tid] : 0.f;
+      pq = ok ? pmp[q0 + tid] : 0.f;
     }
   };
   auto stage_in = [&](unsigned char* st) {
@@ -239,6 +265,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv(BwdArgs a) {
     if (tid < QT) {
       reinterpret_cast<float*>(st + C::OFF_LSE)[tid] = pl;
       reinterpret_cast<float*>(st + C::OFF_DEL)[tid] = pd;
+      reinterpret_cast<float*>(st + C::OFF_PM)[tid] = pq;
     }
   };
 
@@ -276,6 +303,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv(BwdArgs a) {
           pacc[qb] = mfma32<T>(*reinterpret_cast<const u32x4*>(drows + qb * 32 * C::RS + ks * 32), vreg[ks], pacc[qb]);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);  // keep the phases' live ranges apart
       const float* lse_l = reinterpret_cast<const float*>(st + C::OFF_LSE);
       const float* del_l = reinterpret_cast<const float*>(st + C::OFF_DEL);
 #pragma unroll
@@ -292,25 +320,25 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv(BwdArgs a) {
             const int i = 8 * hh + j;
             const float lv = j < 4 ? l0[j] : l1[j - 4];
             const float dv = j < 4 ? d0[j] : d1[j - 4];
-            float x = sacc[qb][i] * a.c2;
+            float p = fast_exp2(sacc[qb][i] * a.c2 - lv);
             bool live = true;
             if (cut) {
               const int64_t qq = q0 + rbase + j;
               const int64_t dd = static_cast<int64_t>(krow) - qq;
               if (qq >= T_ || krow >= S_) {
                 live = false;
-                x = -kInf;
+                p = 0.f;
               } else if (a.masked && (dd < a.band_lo || dd > a.band_hi)) {
                 live = false;
-                x = a.fill2;
+                p = reinterpret_cast<const float*>(st + C::OFF_PM)[rbase + j];
               }
             }
-            const float p = fast_exp2(x - lv);
             sacc[qb][i] = p;
             pacc[qb][i] = live ? p * (pacc[qb][i] - dv) : 0.f;
           }
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
       const unsigned char* dot_l = st + C::OFF_DOT + r32 * C::TS + g * 16;
       const unsigned char* qt_l = st + C::OFF_QT + r32 * C::TS + g * 16;
 #pragma unroll
@@ -350,7 +378,7 @@ struct DqCfg {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void bwd_dq(BwdArgs a) {
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void bwd_dq(BwdArgs a) {
   using C = DqCfg<D>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
@@ -378,8 +406,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq(BwdArgs a) {
       doreg[ks] = qrow < T_ ? gload<u32x4>(obs + ks * 16, ooff) : u32x4{0u, 0u, 0u, 0u};
     }
   }
-  const float lse2 = qrow < T_ ? a.lse[inst * T_ + qrow] * kLog2e : 0.f;
-  const float dl = qrow < T_ ? a.delta[inst * T_ + qrow] : 0.f;
+  const int64_t srow = inst * T_ + qrow;
+  const float dl = qrow < T_ ? a.ws[srow] : 0.f;
+  const float lse2 = qrow < T_ ? a.ws[a.rows + srow] : 0.f;
 
   const int ntiles = static_cast<int>((S_ + C::BN - 1) / C::BN);
   int kt_lo = 0, kt_hi = ntiles;
@@ -444,23 +473,17 @@ __global__ __launch_bounds__(256, 2) void bwd_dq(BwdArgs a) {
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          float x = sacc[kb][i] * a.c2;
+          const float p = fast_exp2(sacc[kb][i] * a.c2 - lse2);
           bool live = true;
           if (cut) {
             const int64_t key = key0 + kb * 32 + acc_row(i, g);
             const int64_t dd = key - qrow;
-            if (key >= S_ || qrow >= T_) {
-              live = false;
-              x = -kInf;
-            } else if (a.masked && (dd < a.band_lo || dd > a.band_hi)) {
-              live = false;
-              x = a.fill2;
-            }
+            if (key >= S_ || qrow >= T_ || (a.masked && (dd < a.band_lo || dd > a.band_hi))) live = false;
           }
-          const float p = fast_exp2(x - lse2);
           pacc[kb][i] = live ? p * (pacc[kb][i] - dl) : 0.f;
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
       const unsigned char* kt_l = st + C::OFF_KT + r32 * C::TS + g * 16;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -487,9 +510,8 @@ bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
 
 template <typename T, int D>
 int launch_bwd(BwdArgs a, int64_t ninst, hipStream_t st) {
-  const int64_t nrows = ninst * a.t;
-  bwd_delta<T, D><<<dim3(static_cast<unsigned>((nrows + 3) / 4)), 256, 0, st>>>(a, nrows);
-  int rc = check_launch("pdh_flash_bwd (delta)");
+  bwd_stats<T, D><<<dim3(static_cast<unsigned>((a.rows + 3) / 4)), 256, 0, st>>>(a);
+  int rc = check_launch("pdh_flash_bwd (row stats)");
   if (rc) return rc;
   {
     using C = DkdvCfg<D>;
@@ -519,9 +541,9 @@ int launch_bwd(BwdArgs a, int64_t ninst, hipStream_t st) {
 using namespace pdh;
 
 extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
-                             const float* lse, void* dq, void* dk, void* dv, float* delta_ws,
-                             const pdh_attn_geom* gm, int dtype, float scale, int mask_kind, int64_t band_lo,
-                             int64_t band_hi, void* stream) {
+                             const float* lse, const float* m_in, const float* den_in, void* dq, void* dk,
+                             void* dv, float* ws, const pdh_attn_geom* gm, int dtype, float scale, float fill, int mask_kind,
+                             int64_t band_lo, int64_t band_hi, void* stream) {
   PDH_REQUIRE(gm != nullptr, PDH_EINVAL, "pdh_flash_bwd: null geometry");
   const pdh_attn_geom G = *gm;
   PDH_REQUIRE(G.batch >= 0 && G.heads_q >= 1 && G.t >= 0 && G.s >= 1, PDH_EINVAL, "pdh_flash_bwd: bad shape");
@@ -533,8 +555,8 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
               "pdh_flash_bwd: need e == od in {64, 128} (got %lld, %lld)", (long long)G.e, (long long)G.od);
   PDH_REQUIRE(mask_kind == PDH_MASK_NONE || mask_kind == PDH_MASK_BAND, PDH_EINVAL,
               "pdh_flash_bwd: unknown mask kind %d", mask_kind);
-  PDH_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && delta_ws, PDH_EINVAL,
-              "pdh_flash_bwd: null pointer");
+  PDH_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && ws, PDH_EINVAL, "pdh_flash_bwd: null pointer");
+  PDH_REQUIRE((m_in == nullptr) == (den_in == nullptr), PDH_EINVAL, "pdh_flash_bwd: pass both m and den, or neither");
   PDH_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && aligned16(dout) && aligned16(dq) &&
                   aligned16(dk) && aligned16(dv) && aligned16(lse),
               PDH_EINVAL, "pdh_flash_bwd: tensors must be 16-byte aligned");
@@ -550,10 +572,10 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
   const int masked = mask_kind == PDH_MASK_BAND;
   const int prune_ok = masked && !band_has_empty_row(G.t, G.s, band_lo, band_hi);
   BwdArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-            static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), lse,
-            static_cast<uint16_t*>(dq), static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv), delta_ws,
-            G.heads_q, G.t, G.s, G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st,
-            G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, -1e9f * kLog2e, masked, band_lo, band_hi, prune_ok, 0};
+            static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), lse, m_in, den_in,
+            static_cast<uint16_t*>(dq), static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv), ws,
+            ninst * G.t, G.heads_q, G.t, G.s, G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st,
+            G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi, prune_ok, 0};
   hipStream_t st = as_stream(stream);
   if (dtype == PDH_BF16)
     return G.e == 128 ? launch_bwd<__hip_bfloat16, 128>(a, ninst, st) : launch_bwd<__hip_bfloat16, 64>(a, ninst, st);

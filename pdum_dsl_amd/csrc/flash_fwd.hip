@@ -77,24 +77,32 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& r, const uint16_t* kp, co
   using C = FwdCfg<D>;
   constexpr int CPR = D / 8;      // 16-byte chunks per K row
   constexpr int RPI = 256 / CPR;  // K rows per load instruction
-  const uint32_t k_lane = static_cast<uint32_t>((tid / CPR) * k_st * 2 + (tid % CPR) * 16);
+  // Rows past the last key re-read that key's row and are zeroed by a select:
+  // no divergent branches around the loads. Full tiles take the plain path.
+  const uint16_t* kb = kp + static_cast<int64_t>(key0) * k_st;  // uniform
+  const uint16_t* vb = vp + static_cast<int64_t>(key0) * v_st;
+  const int last = static_cast<int>(S - key0 < C::BN ? S - key0 - 1 : C::BN - 1);
+  const int dgrp = tid & 31, kgrp = tid >> 5;
 #pragma unroll
   for (int i = 0; i < C::KCH; ++i) {
-    const int64_t row0 = key0 + i * RPI;  // uniform
-    r.k[i] = row0 + tid / CPR < S ? gload<u32x4>(kp + row0 * k_st, k_lane) : u32x4{0u, 0u, 0u, 0u};
+    const int row = i * RPI + tid / CPR;
+    const bool ok = row <= last;
+    const uint32_t off = static_cast<uint32_t>((ok ? row : last) * k_st * 2 + (tid % CPR) * 16);
+    const u32x4 x = gload<u32x4>(kb, off);
+    r.k[i] = ok ? x : u32x4{0u, 0u, 0u, 0u};
   }
-  const int dgrp = tid & 31, kgrp = tid >> 5;
-  const uint32_t v_lane = static_cast<uint32_t>(kgrp * 8 * v_st * 2 + dgrp * C::DG * 2);
 #pragma unroll
   for (int rr = 0; rr < 8; ++rr) {
-    const int64_t key = key0 + kgrp * 8 + rr;
-    const uint16_t* base = vp + (key0 + rr) * v_st;  // uniform
+    const int row = kgrp * 8 + rr;
+    const bool ok = row <= last;
+    const uint32_t off = static_cast<uint32_t>((ok ? row : last) * v_st * 2 + dgrp * C::DG * 2);
     if constexpr (C::DG == 4) {
-      const u32x2 x = key < S ? gload<u32x2>(base, v_lane) : u32x2{0u, 0u};
-      r.v[rr][0] = x.x;
-      r.v[rr][1] = x.y;
+      const u32x2 x = gload<u32x2>(vb, off);
+      r.v[rr][0] = ok ? x.x : 0u;
+      r.v[rr][1] = ok ? x.y : 0u;
     } else {
-      r.v[rr][0] = key < S ? gload<uint32_t>(base, v_lane) : 0u;
+      const uint32_t x = gload<uint32_t>(vb, off);
+      r.v[rr][0] = ok ? x : 0u;
     }
   }
 }

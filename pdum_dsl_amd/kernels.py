@@ -189,11 +189,15 @@ def flash_bwd(
     do: torch.Tensor,
     lse: torch.Tensor,
     *,
+    m: torch.Tensor | None = None,
+    den: torch.Tensor | None = None,
     scale: float | None = None,
     band: Band | None = None,
+    fill: float = -1e9,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Gradients (dq, dk, dv) of flash attention given the forward's lse."""
-    _require_cuda(q, k, v, o, do, lse)
+    """Gradients (dq, dk, dv) of flash attention given the forward's lse
+    (and optionally its (m, den) artifacts, exact for fully-masked rows)."""
+    _require_cuda(q, k, v, o, do, lse, m, den)
     if do.shape != o.shape or do.stride() != o.stride():
         raise ValueError("dO must match O's shape and strides")
     g = _geom(q, k, v, o)
@@ -202,15 +206,18 @@ def flash_bwd(
     dv = torch.empty_like(v)
     if dq.stride() != q.stride() or dk.stride() != k.stride() or dv.stride() != v.stride():
         raise ValueError("q/k/v must be dense (their gradients share their strides)")
-    if lse.dtype != torch.float32 or not lse.is_contiguous() or lse.shape != q.shape[:3]:
-        raise ValueError("lse must be contiguous fp32 [batch, heads, rows]")
-    delta = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+    for nm, t in (("lse", lse), ("m", m), ("den", den)):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous() or t.shape != q.shape[:3]):
+            raise ValueError(f"{nm} must be contiguous fp32 [batch, heads, rows]")
+    if (m is None) != (den is None):
+        raise ValueError("pass both m and den, or neither")
+    ws = torch.empty((3,) + tuple(q.shape[:3]), dtype=torch.float32, device=q.device)
     sc = 1.0 / math.sqrt(q.shape[3]) if scale is None else float(scale)
     kind, (lo, hi) = (PDH_MASK_NONE, (0, 0)) if band is None else (PDH_MASK_BAND, band.c_args())
     _lib.call(
         "pdh_flash_bwd",
-        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta),
-        C.byref(g), _DT[q.dtype], C.c_float(sc), kind, lo, hi, C.c_void_p(_stream()),
+        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(m), _ptr(den), _ptr(dq), _ptr(dk), _ptr(dv),
+        _ptr(ws), C.byref(g), _DT[q.dtype], C.c_float(sc), C.c_float(fill), kind, lo, hi, C.c_void_p(_stream()),
     )
     return dq, dk, dv
 

@@ -1,0 +1,226 @@
+"""The tl op family this backend reads, with the alignment law as type rules.
+
+Restates the subset of the reference's tl dialect that the fusion templates
+emit and consume (packages/tensorlib/src/pdum/tl/dialect.py:115-487):
+
+  core.param / core.const / core.tuple / core.yield
+  tl.pointwise  f=<marker>      operands aligned BY NAME; scalars broadcast
+  tl.reduce     f, dims         sum | max | min | prod | mean (mean = sum / N)
+  tl.repeat_like x, like        adds like's missing dims (stride-0 broadcast)
+  tl.repeat     name, extent    adds one stride-0 dim
+  tl.split      name, parts     x -> (outer .. inner) blocking, x = sum w_j i_j
+  tl.stage      level[, order]  a copy to a residence level (identity in value)
+  tl.select     coords          fixes dims to points
+  tl.iota       name            the coordinate field along a dim of the lattice
+  tl.const      value, dims     a constant field
+  tl.fold       dim, state, element, out, step region
+  tl.argtopk    (typed only: a non-template op the planner must refuse)
+"""
+
+from __future__ import annotations
+
+from .ir import F64, BOOL, Builder, Dim, OpDef, Region, Scalar, TensorType, TupleType, minus_dim, walk
+
+MARKERS = (
+    "add sub mul div neg exp log maximum minimum tanh sqrt sin cos abs floor "
+    "where eq ne le lt ge gt stop_gradient"
+).split()
+REDUCERS = ("sum", "max", "min", "prod", "mean")
+
+
+def _dims_arg(v) -> tuple:
+    return (v,) if isinstance(v, str) else tuple(v)
+
+
+def _aligned(ts: list[TensorType]) -> None:
+    ref = {d.name: d for d in ts[0].dims}
+    for t in ts[1:]:
+        other = {d.name: d for d in t.dims}
+        if set(other) != set(ref):
+            raise TypeError(f"tl.pointwise wants ALIGNED operands: dims {sorted(ref)} vs {sorted(other)}")
+        for n, d in other.items():
+            if (d.start, d.stop) != (ref[n].start, ref[n].stop):
+                raise TypeError(
+                    f"tl.pointwise wants ALIGNED operands: dim {n!r} domain "
+                    f"[{ref[n].start}, {ref[n].stop}) vs [{d.start}, {d.stop})"
+                )
+
+
+def _r_pointwise(args, at, regions):
+    if at["f"] not in MARKERS:
+        raise TypeError(f"unknown pointwise marker {at['f']!r}")
+    ts = [a for a in args if isinstance(a, TensorType)]
+    if not ts:
+        raise TypeError("tl.pointwise wants at least one tensor operand")
+    _aligned(ts)
+    return TensorType(ts[0].dims)
+
+
+def _r_reduce(args, at, regions):
+    (x,) = args
+    dims = _dims_arg(at["dims"])
+    if at["f"] not in REDUCERS:
+        raise TypeError(f"unknown reducer {at['f']!r}")
+    for d in dims:
+        x.dim(d)
+    return TensorType(tuple(d for d in x.dims if d.name not in dims))
+
+
+def _r_repeat_like(args, at, regions):
+    x, like = args
+    have = set(x.names)
+    return TensorType(x.dims + tuple(d for d in like.dims if d.name not in have))
+
+
+def _range(extent):
+    return (int(extent[0]), int(extent[1])) if isinstance(extent, tuple) else (0, int(extent))
+
+
+def _r_repeat(args, at, regions):
+    (x,) = args
+    if x.has(at["name"]):
+        raise TypeError(f"dim {at['name']!r} already exists")
+    lo, hi = _range(at["extent"])
+    return TensorType(x.dims + (Dim(at["name"], lo, hi),))
+
+
+def _r_split(args, at, regions):
+    (x,) = args
+    d = x.dim(at["name"])
+    parts = tuple(at["parts"])
+    n = 1
+    for _, size in parts:
+        n *= int(size)
+    if n != d.size:
+        raise TypeError(f"tl.split: parts {parts} do not tile dim {d.name!r} of size {d.size}")
+    if d.start != 0:
+        raise TypeError("tl.split: only dims starting at 0 split here")
+    out = []
+    for e in x.dims:
+        if e.name == d.name:
+            out.extend(Dim(pn, 0, int(ps)) for pn, ps in parts)
+        else:
+            if any(e.name == pn for pn, _ in parts):
+                raise TypeError(f"part name {e.name!r} collides with an existing dim")
+            out.append(e)
+    return TensorType(tuple(out))
+
+
+def _r_stage(args, at, regions):
+    (x,) = args
+    order = at.get("order")
+    if order:
+        return TensorType(tuple(x.dim(n) for n in order))
+    return TensorType(x.dims)
+
+
+def _r_select(args, at, regions):
+    (x,) = args
+    coords = dict(at["coords"])
+    for n, i in coords.items():
+        d = x.dim(n)
+        if not d.start <= i < d.stop:
+            raise TypeError(f"select {n}={i} outside [{d.start}, {d.stop})")
+    return TensorType(tuple(d for d in x.dims if d.name not in coords))
+
+
+def _r_iota(args, at, regions):
+    (x,) = args
+    if not isinstance(x, TensorType) or not x.has(at["name"]):
+        raise TypeError(f"tl.iota: the lattice has no dim {at['name']!r}")
+    return TensorType(x.dims)
+
+
+def _r_const(args, at, regions):
+    return TensorType(tuple(Dim(n, *_range(e)) for n, e in at["dims"]))
+
+
+def _frames(t: TensorType):
+    return sorted(((d.name, d.start, d.stop) for d in t.dims))
+
+
+def _r_fold(args, at, regions):
+    state, element = tuple(at["state"]), tuple(at["element"])
+    k, m = len(state), len(element)
+    if k < 1 or len(args) != k + m:
+        raise TypeError(f"tl.fold takes {k} state init(s) + {m} element source(s), got {len(args)} operands")
+    (step,) = regions
+    dim = at["dim"]
+    inits, srcs = args[:k], args[k:]
+    for s in srcs:
+        if not s.has(dim):
+            raise TypeError(f"tl.fold: element source has no scan dim {dim!r}")
+    want = tuple(inits) + tuple(minus_dim(s, dim) for s in srcs)
+    binders = tuple(p.type for p in step.params)
+    if len(binders) != len(want) or any(_frames(a) != _frames(b) for a, b in zip(binders, want)):
+        raise TypeError("tl.fold: step binders do not match (state inits + element slices)")
+    y = step.body[-1].args[0]
+    ytypes = tuple(a.type for a in y.args) if y.op == "core.tuple" else (y.type,)
+    if len(ytypes) != k:
+        raise TypeError(f"tl.fold: the step must yield the {k} next state(s)")
+    for i in range(k):
+        if _frames(ytypes[i]) != _frames(inits[i]):
+            raise TypeError(f"tl.fold: carry {state[i]!r} changes the state type")
+    out = tuple(at["out"])
+    if out[0] != "final":
+        raise TypeError("tl.fold: only out=('final', i) folds are read by this backend")
+    return inits[out[1]]
+
+
+def _r_tuple(args, at, regions):
+    return TupleType(tuple(args))
+
+
+def _r_yield(args, at, regions):
+    return args[0] if len(args) == 1 else TupleType(tuple(args))
+
+
+def _r_argtopk(args, at, regions):
+    (x,) = args
+    return TensorType(tuple(Dim(at["k_name"], 0, at["k"]) if d.name == at["dim"] else d for d in x.dims))
+
+
+OPS: dict[str, OpDef] = {
+    "core.param": OpDef("core.param"),
+    "core.const": OpDef("core.const"),
+    "core.tuple": OpDef("core.tuple", _r_tuple),
+    "core.yield": OpDef("core.yield", _r_yield),
+    "tl.pointwise": OpDef("tl.pointwise", _r_pointwise),
+    "tl.reduce": OpDef("tl.reduce", _r_reduce),
+    "tl.repeat_like": OpDef("tl.repeat_like", _r_repeat_like),
+    "tl.repeat": OpDef("tl.repeat", _r_repeat),
+    "tl.split": OpDef("tl.split", _r_split),
+    "tl.stage": OpDef("tl.stage", _r_stage),
+    "tl.select": OpDef("tl.select", _r_select),
+    "tl.iota": OpDef("tl.iota", _r_iota),
+    "tl.const": OpDef("tl.const", _r_const),
+    "tl.fold": OpDef("tl.fold", _r_fold, nregions=1),
+    "tl.argtopk": OpDef("tl.argtopk", _r_argtopk),
+}
+
+TILE_OPS = frozenset(OPS) - {"tl.argtopk"}
+
+
+def builder() -> Builder:
+    return Builder(OPS)
+
+
+def const(b: Builder, value: float):
+    return b.emit("core.const", type=F64, value=float(value))
+
+
+def check_tier(region: Region, tier: str = "tile") -> Region:
+    """The tile-tier gate (dialect.py:1150-1180): every op the region (and
+    its fold steps) carries must be tile vocabulary; the first violation
+    refuses, naming the op."""
+    if tier != "tile":
+        raise ValueError(f"only the tile tier is checked here (got {tier!r})")
+    for n in walk(region):
+        if n.op not in TILE_OPS:
+            raise ValueError(f"{n.op} is a host citizen here — it has no tile-tier meaning (290)")
+        for r in n.regions:
+            check_tier(r, "tile")
+    return region
+
+
+__all__ = ["OPS", "MARKERS", "REDUCERS", "builder", "const", "check_tier", "F64", "BOOL", "Scalar", "TensorType"]

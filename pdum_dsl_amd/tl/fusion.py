@@ -1,0 +1,503 @@
+"""The fusion registry rows this backend serves, and the plan they produce.
+
+Restates the reference's packages/tensorlib/src/pdum/tl/fusion.py for the
+template rows on the HIP hot path:
+
+  flash               contraction -> closed mask -> row softmax -> contraction
+                      over the same dim (fusion.py:480-615); the generator
+                      emits the online-softmax fold; certified licensed-
+                      differential under flash.online-softmax with the
+                      template's own adversarial families (fusion.py:618-656),
+                      on a twin shrunk to extent <= 128 (fusion.py:693-759);
+                      with a machine, the mask-derived prune (fusion.py:659-690)
+  row-normalization   the softmax chain over a param: rows staged once,
+                      proved-exact by stage erasure (fusion.py:371-400, 818-825)
+  row-statistics      the two-pass layernorm core + scale/shift epilogue
+                      (fusion.py:403-443, 826-843)
+  map-chain / stencil recognized as plans (fusion.py:844-854); the HIP seat
+                      refuses them (not in this build)
+
+Everything else is a RED "uncompiled" group with the reason — never an
+exception (fusion.py:855-868). Plans are data.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field, replace
+
+import numpy as np
+
+from .certify import Certificate, certify
+from .dialect import OPS, check_tier
+from .interp import Field
+from .ir import F64, Builder, Dim, Region, TensorType, minus_dim, walk
+from .licenses import FLASH_ONLINE_SOFTMAX
+from .launch import fit_affine, propose, tri_eval
+
+_MAP_OPS = frozenset(
+    {"core.param", "core.const", "core.yield", "tl.pointwise", "tl.iota", "tl.const", "tl.select", "tl.split",
+     "tl.repeat", "tl.repeat_like"}
+)
+_EXACT_OPS = frozenset({"tl.pointwise", "tl.repeat_like", "tl.repeat", "tl.iota", "core.const", "tl.const"})
+
+
+@dataclass(frozen=True)
+class Group:
+    """One fusion group (fusion.py:127-141): the claiming template, the
+    generated tile kernel, its certificate, the confidence color, plan
+    parameters, the refusal reason, launch, prune and surfaced artifacts."""
+
+    template: str
+    kernel: Region | None = field(repr=False)
+    certificate: Certificate | None
+    confidence: str
+    params: tuple = ()
+    reason: str = ""
+    launch: tuple = ()
+    prune: tuple = ()
+    artifacts: tuple = ()
+
+
+@dataclass(frozen=True)
+class Plan:
+    groups: tuple
+
+
+def _dims_of(n) -> tuple:
+    d = n.attr("dims")
+    return (d,) if isinstance(d, str) else tuple(d)
+
+
+def pick_ki(extent: int) -> int:
+    """The v1 tile width: the largest divisor <= min(32, extent/2), else extent (fusion.py:259-265)."""
+    for ki in range(min(32, extent // 2), 0, -1):
+        if extent % ki == 0:
+            return ki
+    return extent
+
+
+# ------------------------------------------------------------ matchers
+
+
+def match_softmax(pr):
+    """div(exp(sm - rl(max_s sm)), rl(sum_s exp(...))) over one dim -> {sm, s, max, den}."""
+    if pr.op != "tl.pointwise" or pr.attr("f") != "div" or len(pr.args) != 2:
+        return None
+    e, rld = pr.args
+    if e.op != "tl.pointwise" or e.attr("f") != "exp" or rld.op != "tl.repeat_like":
+        return None
+    sume = rld.args[0]
+    if sume.op != "tl.reduce" or sume.attr("f") != "sum" or sume.args[0] is not e:
+        return None
+    sub = e.args[0]
+    if sub.op != "tl.pointwise" or sub.attr("f") != "sub" or len(sub.args) != 2:
+        return None
+    sm, rlm = sub.args
+    if rlm.op != "tl.repeat_like":
+        return None
+    mx = rlm.args[0]
+    if mx.op != "tl.reduce" or mx.attr("f") != "max" or mx.args[0] is not sm:
+        return None
+    if rlm.args[1] is not sm or rld.args[1] not in (sm, e):
+        return None
+    sd, md = _dims_of(sume), _dims_of(mx)
+    if sd != md or len(sd) != 1:
+        return None
+    return {"sm": sm, "s": sd[0], "max": mx, "den": sume}
+
+
+def match_rowstat(pr):
+    """div(xc, rl(sqrt(mean(xc*xc) + eps))) with xc = x - rl(mean x), one feat dim -> {x, feat, eps, node}."""
+    if pr.op != "tl.pointwise" or pr.attr("f") != "div" or len(pr.args) != 2:
+        return None
+    xc, rld = pr.args
+    if rld.op != "tl.repeat_like":
+        return None
+    sd = rld.args[0]
+    if sd.op != "tl.pointwise" or sd.attr("f") != "sqrt":
+        return None
+    add = sd.args[0]
+    if add.op != "tl.pointwise" or add.attr("f") != "add" or len(add.args) != 2:
+        return None
+    var, eps = add.args
+    if eps.op not in ("core.const", "tl.const") or var.op != "tl.reduce" or var.attr("f") != "mean":
+        return None
+    sq = var.args[0]
+    if sq.op != "tl.pointwise" or sq.attr("f") != "mul" or sq.args[0] is not sq.args[1] or sq.args[0] is not xc:
+        return None
+    if xc.op != "tl.pointwise" or xc.attr("f") != "sub" or len(xc.args) != 2:
+        return None
+    x, rlm = xc.args
+    if rlm.op != "tl.repeat_like":
+        return None
+    mu = rlm.args[0]
+    if mu.op != "tl.reduce" or mu.attr("f") != "mean" or mu.args[0] is not x:
+        return None
+    vd, md = _dims_of(var), _dims_of(mu)
+    if vd != md or len(vd) != 1:
+        return None
+    return {"x": x, "feat": vd[0], "eps": float(eps.attr("value")), "node": pr}
+
+
+def contract_core(red, kname=None):
+    """reduce(sum, mul(rl(x, y), rl(y, x)), (dim,)) -> (x, y, dim)."""
+    if red.op != "tl.reduce" or red.attr("f") != "sum":
+        return None
+    dims = _dims_of(red)
+    if len(dims) != 1 or (kname is not None and dims[0] != kname):
+        return None
+    prod = red.args[0]
+    if prod.op != "tl.pointwise" or prod.attr("f") != "mul" or len(prod.args) != 2:
+        return None
+    ra, rb = prod.args
+    if ra.op != "tl.repeat_like" or rb.op != "tl.repeat_like":
+        return None
+    x, y = ra.args[0], rb.args[0]
+    if rb.args[1] is not x or ra.args[1] is not y:
+        return None
+    return x, y, dims[0]
+
+
+def forest_is_closed(n) -> bool:
+    """A mask forest is CLOSED when it reads no data: pointwise/consts over iota leaves."""
+    if n.op in ("tl.iota", "core.const", "tl.const"):
+        return True
+    if n.op in _MAP_OPS and n.op != "core.param":
+        return all(forest_is_closed(x) for x in n.args)
+    return False
+
+
+def match_flash(region: Region):
+    """The flash composition over bare params q:(t,e), k:(s,e), v:(s,o), with
+    an optional artifact yield (out, max, den) (fusion.py:480-539)."""
+    y = region.body[-1].args[0]
+    artifacts = False
+    if y.op == "core.tuple":
+        if len(y.args) != 3:
+            return None
+        y, m_out, den_out = y.args
+        artifacts = True
+    out = contract_core(y)
+    if out is None:
+        return None
+    pr, v, s = out
+    sm_m = match_softmax(pr)
+    if sm_m is None or sm_m["s"] != s:
+        return None
+    if artifacts and (m_out is not sm_m["max"] or den_out is not sm_m["den"]):
+        return None
+    if v.op != "core.param":
+        return None
+    smn = sm_m["sm"]
+    if smn.op != "tl.pointwise" or smn.attr("f") != "where" or len(smn.args) != 3:
+        return None
+    mask, sc, fill = smn.args
+    if fill.op not in ("core.const", "tl.const") or not forest_is_closed(mask):
+        return None
+    core = contract_core(sc)
+    if core is None:
+        return None
+    q, k, e = core
+    if q.op != "core.param" or k.op != "core.param":
+        return None
+    if {id(q), id(k), id(v)} != {id(p) for p in region.params}:
+        return None
+    qd, kd, vd = (p.type.names for p in (q, k, v))
+    if len(qd) != 2 or kd != (s, e) or len(vd) != 2 or vd[0] != s:
+        return None
+    sdim = k.type.dim(s)
+    if sdim.start != 0:
+        return None
+    return {
+        "q": q, "k": k, "v": v, "mask": mask, "fill": float(fill.attr("value")),
+        "t": next(nm for nm in qd if nm != e), "s": s, "e": e, "o": vd[1], "extent": sdim.stop,
+        "artifacts": artifacts,
+    }
+
+
+# ----------------------------------------------------------- generators
+
+
+def rebuild_into(b: Builder, memo: dict, n):
+    """Re-emit ``n`` with a seeded memo (params, holes)."""
+    if id(n) in memo:
+        return memo[id(n)]
+    args = tuple(rebuild_into(b, memo, x) for x in n.args)
+    explicit = {} if OPS[n.op].type_rule is not None else {"type": n.type}
+    out = b.emit(n.op, *args, regions=n.regions, loc=n.loc, **explicit, **dict(n.attrs))
+    memo[id(n)] = out
+    return out
+
+
+def stage_params(region: Region, staged_ids) -> Region:
+    """The same chain with the named params staged once to "shared" (fusion.py:339-350)."""
+    b = Builder(OPS)
+    newp = {id(p): b.param(i, p.type) for i, p in enumerate(region.params)}
+    memo: dict = dict(newp)
+    for pid in staged_ids:
+        memo[pid] = b.emit("tl.stage", newp[pid], level="shared")
+    y = rebuild_into(b, memo, region.body[-1].args[0])
+    return check_tier(Region(params=tuple(newp[id(p)] for p in region.params), body=(b.emit("core.yield", y),)))
+
+
+def flash_step(types: tuple, e: str, fill: float) -> Region:
+    """The online-softmax step over (m, den, o | q, k-tile, v-tile, mask-tile):
+        sc = sum_e q k; sm = where(mask, sc, fill); m' = max(m, max_si sm)
+        a = exp(m - m'); p = exp(sm - m'); den' = den a + sum_si p
+        o' = o a + sum_si p v
+    (fusion.py:570-604). Shared by the generator and the HIP recognizer, so
+    a tile kernel is recognized exactly when its step has this content key."""
+    sb = Builder(OPS)
+    p_m, p_den, p_o, p_q, p_k, p_v, p_mk = (sb.param(i, t) for i, t in enumerate(types))
+    ks = sb.emit("tl.stage", p_k, level="shared")
+    vs = sb.emit("tl.stage", p_v, level="shared")
+    prod = sb.emit("tl.pointwise", sb.emit("tl.repeat_like", p_q, ks), sb.emit("tl.repeat_like", ks, p_q), f="mul")
+    sc = sb.emit("tl.reduce", prod, dims=(e,), f="sum")
+    sm = sb.emit("tl.pointwise", p_mk, sc, sb.emit("core.const", type=F64, value=float(fill)), f="where")
+    m_new = sb.emit("tl.pointwise", p_m, sb.emit("tl.reduce", sm, dims=("si",), f="max"), f="maximum")
+    alpha = sb.emit("tl.pointwise", sb.emit("tl.pointwise", p_m, m_new, f="sub"), f="exp")
+    p_w = sb.emit("tl.pointwise", sb.emit("tl.pointwise", sm, sb.emit("tl.repeat_like", m_new, sm), f="sub"), f="exp")
+    den_new = sb.emit(
+        "tl.pointwise", sb.emit("tl.pointwise", p_den, alpha, f="mul"), sb.emit("tl.reduce", p_w, dims=("si",), f="sum"),
+        f="add",
+    )
+    pv = sb.emit("tl.pointwise", sb.emit("tl.repeat_like", p_w, vs), sb.emit("tl.repeat_like", vs, p_w), f="mul")
+    o_new = sb.emit(
+        "tl.pointwise",
+        sb.emit("tl.pointwise", p_o, sb.emit("tl.repeat_like", alpha, p_o), f="mul"),
+        sb.emit("tl.reduce", pv, dims=("si",), f="sum"),
+        f="add",
+    )
+    return Region(
+        params=(p_m, p_den, p_o, p_q, p_k, p_v, p_mk),
+        body=(sb.emit("core.yield", sb.emit("core.tuple", m_new, den_new, o_new)),),
+    )
+
+
+FOLD_KW = dict(dim="so", state=("m", "den", "o"), element=("q", "k", "v", "mask"))
+
+
+def generate_flash(region: Region, m: dict, si: int) -> Region:
+    """The online-softmax tile region (fusion.py:542-615): the mask forest
+    re-rooted on a const (t, s) lattice and split along s as an element
+    source, K/V split (so, si), q as a stride-0 repeat over so, two (three
+    with artifacts) fold nodes sharing one step for the finals."""
+    s, t, fill = m["s"], m["t"], m["fill"]
+    so = m["extent"] // si
+    tdim = m["q"].type.dim(t)
+    odim = m["v"].type.dim(m["o"])
+    b = Builder(OPS)
+    newp = {id(p): b.param(i, p.type) for i, p in enumerate(region.params)}
+    nq, nk, nv = newp[id(m["q"])], newp[id(m["k"])], newp[id(m["v"])]
+    lattice = b.emit("tl.const", value=0.0, dims=((t, tdim.stop), (s, m["extent"])))
+    memo: dict = dict(newp)
+    for n in walk(region):  # iota backings re-root on the lattice: values were never read
+        if n.op == "tl.iota":
+            memo[id(n)] = b.emit("tl.iota", lattice, name=n.attr("name"))
+    mask = rebuild_into(b, memo, m["mask"])
+    parts = (("so", so), ("si", si))
+    kt = b.emit("tl.split", nk, name=s, parts=parts)
+    vt = b.emit("tl.split", nv, name=s, parts=parts)
+    mt = b.emit("tl.split", mask, name=s, parts=parts)
+    qr = b.emit("tl.repeat", nq, name="so", extent=so)
+    m0 = b.emit("tl.const", value=-1e30, dims=((t, tdim.stop),))
+    den0 = b.emit("tl.const", value=0.0, dims=((t, tdim.stop),))
+    o0 = b.emit("tl.const", value=0.0, dims=((t, tdim.stop), (m["o"], odim.stop)))
+    types = (m0.type, den0.type, o0.type, minus_dim(qr.type, "so"), minus_dim(kt.type, "so"),
+             minus_dim(vt.type, "so"), minus_dim(mt.type, "so"))
+    step = flash_step(types, m["e"], fill)
+    args = (m0, den0, o0, qr, kt, vt, mt)
+    f_o = b.emit("tl.fold", *args, regions=(step,), out=("final", 2), **FOLD_KW)
+    f_den = b.emit("tl.fold", *args, regions=(step,), out=("final", 1), **FOLD_KW)
+    out = b.emit("tl.pointwise", f_o, b.emit("tl.repeat_like", f_den, f_o), f="div")
+    if m.get("artifacts"):
+        f_m = b.emit("tl.fold", *args, regions=(step,), out=("final", 0), **FOLD_KW)
+        out = b.emit("core.tuple", out, f_m, f_den)
+    fused = Region(params=tuple(newp[id(p)] for p in region.params), body=(b.emit("core.yield", out),))
+    return check_tier(fused)
+
+
+# ------------------------------------------------------- certification
+
+
+def score_families(region: Region, seed: int = 11):
+    """Adversarial families (fusion.py:618-656): unit gaussians, wide scores
+    (x8), and a dominant key (row 0 of param 1 x40). Params consumed as
+    where-conditions draw as boolean masks."""
+    masks = set()
+    for n in walk(region):
+        if n.op == "tl.pointwise" and n.attr("f", "").startswith("where"):
+            r = n.args[0]
+            while r.op in ("tl.repeat_like", "tl.repeat", "tl.select"):
+                r = r.args[0]
+            if r.op == "core.param":
+                masks.add(id(r))
+
+    def draw(scale, subseed, spike=False):
+        def factory():
+            rng = np.random.default_rng(subseed)
+            out = []
+            for i, p in enumerate(region.params):
+                shape = p.type.shape
+                if id(p) in masks:
+                    out.append(Field(rng.random(shape) < 0.5, p.type.dims))
+                    continue
+                arr = scale * rng.standard_normal(shape)
+                if spike and i == 1:
+                    arr[0] *= 40.0
+                out.append(Field(arr, p.type.dims))
+            return out
+
+        return factory
+
+    return (
+        ("gaussian", draw(1.0, seed)),
+        ("wide-scores", draw(8.0, seed + 1)),
+        ("dominant-key", draw(1.0, seed + 2, spike=True)),
+    )
+
+
+CERT_CAP = 128
+_CERTS: dict = {}
+
+
+def _cert_fact(tile: Region, naive: Region, kind: str) -> Certificate:
+    key = (tile.key, naive.key, kind)
+    if key not in _CERTS:
+        if kind == "flash":
+            _CERTS[key] = certify(tile, naive, licenses=FLASH_ONLINE_SOFTMAX, families=score_families(naive))
+        else:
+            _CERTS[key] = certify(tile, naive)
+    return _CERTS[key]
+
+
+def shrink(region: Region, cap: int) -> Region | None:
+    """The same program over extents clamped to ``cap`` (fusion.py:718-755)."""
+    if any(d.start != 0 for p in region.params for d in p.type.dims):
+        return None
+    b = Builder(OPS)
+    memo: dict = {}
+    for i, p in enumerate(region.params):
+        memo[id(p)] = b.param(i, TensorType(tuple(Dim(d.name, 0, min(d.stop, cap)) for d in p.type.dims)))
+
+    def clamp(e):
+        return (e[0], min(int(e[1]), cap)) if isinstance(e, tuple) else min(int(e), cap)
+
+    def rebuild(n):
+        if id(n) in memo:
+            return memo[id(n)]
+        args = tuple(rebuild(x) for x in n.args)
+        at = dict(n.attrs)
+        if n.op == "tl.const" and "dims" in at:
+            at["dims"] = tuple((nm, clamp(e)) for nm, e in at["dims"])
+        if n.op == "tl.repeat" and "extent" in at:
+            at["extent"] = clamp(at["extent"])
+        explicit = {} if OPS[n.op].type_rule is not None else {"type": n.type}
+        out = b.emit(n.op, *args, regions=n.regions, loc=n.loc, **explicit, **at)
+        memo[id(n)] = out
+        return out
+
+    y = rebuild(region.body[-1].args[0])
+    return Region(params=tuple(memo[id(p)] for p in region.params), body=(b.emit("core.yield", y),))
+
+
+def oversized(region: Region, cap: int) -> bool:
+    return any(d.size > cap for p in region.params for d in p.type.dims)
+
+
+def prune_flash(region: Region, *, tile: int, si: int):
+    """Mask-derived fold bounds (fusion.py:659-690): per t-program [lo, hi)
+    over s-tiles, as exact floor-affine fits, or None when any program or
+    row is fully masked (uniform-softmax semantics)."""
+    fm = match_flash(region)
+    if fm is None:
+        return None
+    t, s, mask, S = fm["t"], fm["s"], fm["mask"], fm["extent"]
+    so = S // si
+    td = fm["q"].type.dim(t)
+    sbox = [(q * si, (q + 1) * si - 1) for q in range(so)]
+    los, his = [], []
+    for g in range(-((td.start - td.stop) // tile)):
+        tb = (td.start + g * tile, min(td.start + (g + 1) * tile, td.stop) - 1)
+        act = [q for q in range(so) if tri_eval(mask, {t: tb, s: sbox[q]})[1] != "F"]
+        if not act:
+            return None
+        los.append(act[0])
+        his.append(act[-1] + 1)
+    for r in range(td.start, td.stop):
+        if all(tri_eval(mask, {t: (r, r), s: sb})[1] == "F" for sb in sbox):
+            return None
+    flo, fhi = fit_affine(los, 0, so), fit_affine(his, 0, so)
+    return (flo, fhi) if flo is not None and fhi is not None else None
+
+
+# ----------------------------------------------------------------- plan
+
+
+def plan_region(region: Region, machine=None, floor: int = 1024) -> Plan:
+    """Recognize the whole region against the registry, certify, and (with a
+    machine) attach the analytic default launch and the flash prune
+    (fusion.py:762-785)."""
+    plan = _recognize(region)
+    if machine is None:
+        return plan
+    groups = []
+    for g in plan.groups:
+        cands = propose(g.kernel, machine, floor) if g.kernel is not None else ()
+        if cands:
+            g = replace(g, launch=cands[0])
+        if g.template == "flash" and len(g.launch) == 1:
+            pr = prune_flash(region, tile=g.launch[0][1], si=dict(g.params)["si"])
+            if pr is not None:
+                g = replace(g, prune=(("so", *pr),))
+        groups.append(g)
+    return Plan(tuple(groups))
+
+
+def _is_map_chain(region: Region):
+    for n in walk(region):
+        if n.op not in _MAP_OPS:
+            return n.op
+    return None
+
+
+def _recognize(region: Region) -> Plan:
+    fm = match_flash(region)
+    if fm is not None:
+        si = pick_ki(fm["extent"])
+        kernel = generate_flash(region, fm, si)
+        csrc, ckern = region, kernel
+        if oversized(region, CERT_CAP):  # certify the shrunk twin: the program, not the size
+            shr = shrink(region, CERT_CAP)
+            fm2 = match_flash(shr) if shr is not None else None
+            if fm2 is not None:
+                csrc, ckern = shr, generate_flash(shr, fm2, pick_ki(fm2["extent"]))
+        cert = _cert_fact(ckern, csrc, "flash")
+        arts = ("m", "den") if fm["artifacts"] else ()
+        return Plan((Group("flash", kernel, cert, "yellow", params=(("si", si),), artifacts=arts),))
+    sm = match_softmax(region.body[-1].args[0])
+    if sm is not None:
+        rows = frozenset(id(p) for p in region.params if p.type.has(sm["s"]))
+        kernel = stage_params(region, rows)
+        return Plan((Group("row-normalization", kernel, _cert_fact(kernel, region, "exact"), "yellow"),))
+    rs = next((m for n in walk(region) if (m := match_rowstat(n)) is not None), None)
+    if rs is not None:
+        reduces = [n for n in walk(region) if n.op == "tl.reduce"]
+        feat_ok = all(r.attr("f") == "mean" and _dims_of(r) == (rs["feat"],) for r in reduces)
+        vocab_ok = all(n.op in _EXACT_OPS or n.op in ("core.yield", "core.param", "tl.reduce") for n in walk(region))
+        if len(reduces) == 2 and feat_ok and vocab_ok:
+            rows = frozenset(id(p) for p in region.params if p.type.has(rs["feat"]))
+            kernel = stage_params(region, rows)
+            return Plan((Group("row-statistics", kernel, _cert_fact(kernel, region, "exact"), "yellow"),))
+    offender = _is_map_chain(region)
+    if offender is None:
+        kernel = check_tier(region)
+        return Plan((Group("map-chain", kernel, _cert_fact(kernel, region, "exact"), "yellow"),))
+    return Plan(
+        (
+            Group(
+                "uncompiled", None, None, "red",
+                reason=f"no recognized schedule: {offender} has no template row — the reference serves this group",
+            ),
+        )
+    )

@@ -1,0 +1,165 @@
+"""Plan-time reference interpreter for certification.
+
+The reference's planner certifies every template kernel against its naive
+twin by EVALUATING both (certify.py:567-609 calls dialect.run_region,
+dialect.py:1349-1473). This module is that evaluator for the tile
+vocabulary of pdum_dsl_amd.tl.dialect, in float64 numpy, used ONLY by
+``certify`` to decide a Group's certificate at plan time. It is never on the
+execution path: compile_tile_hip's runners launch HIP kernels and nothing
+else.
+
+Semantics follow the reference: pointwise aligns operands by dim NAME
+(compute.py:95-123), reduce is the numpy ufunc reduce with the reducer's
+identity (max has none; mean = sum / static N, compute.py:184-214), fold
+iterates its scan dim and hands the step each element source SELECTED at the
+absolute coordinate (dialect.py:1448-1470).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from .ir import Dim, Node, Region, TensorType
+
+_PW = {
+    "add": np.add, "sub": np.subtract, "mul": np.multiply, "div": np.divide, "neg": np.negative,
+    "exp": np.exp, "log": np.log, "maximum": np.maximum, "minimum": np.minimum, "tanh": np.tanh,
+    "sqrt": np.sqrt, "sin": np.sin, "cos": np.cos, "abs": np.abs, "floor": np.floor, "where": np.where,
+    "eq": np.equal, "ne": np.not_equal, "le": np.less_equal, "lt": np.less, "ge": np.greater_equal,
+    "gt": np.greater, "stop_gradient": np.positive,
+}
+_RED = {"sum": (np.add, 0.0), "prod": (np.multiply, 1.0), "max": (np.maximum, None), "min": (np.minimum, None)}
+
+
+@dataclass
+class Field:
+    """A named-dim array: ``arr`` axes follow ``dims``."""
+
+    arr: np.ndarray
+    dims: tuple[Dim, ...]
+
+    @property
+    def names(self):
+        return tuple(d.name for d in self.dims)
+
+    def to_numpy(self, order=None) -> np.ndarray:
+        if order is None:
+            return self.arr
+        return np.transpose(self.arr, [self.names.index(n) for n in order])
+
+    def aligned_to(self, names) -> np.ndarray:
+        return self.to_numpy(tuple(names))
+
+    def select(self, name: str, i: int) -> "Field":
+        ax = self.names.index(name)
+        d = self.dims[ax]
+        return Field(np.take(self.arr, i - d.start, axis=ax), tuple(x for x in self.dims if x.name != name))
+
+
+def field(arr, names) -> Field:
+    arr = np.asarray(arr)
+    return Field(arr, tuple(Dim(n, 0, s) for n, s in zip(names, arr.shape)))
+
+
+def _as_field(x, ref: Field) -> np.ndarray:
+    if isinstance(x, Field):
+        return x.aligned_to(ref.names)
+    return np.full(ref.arr.shape, float(x))
+
+
+def run_region(region: Region, values: list):
+    """Evaluate ``region`` over Field values (positional per param)."""
+    memo: dict[int, object] = {}
+    bind = {id(p): v for p, v in zip(region.params, values)}
+
+    def ev(n: Node):
+        k = id(n)
+        if k not in memo:
+            memo[k] = _ev(n)
+        return memo[k]
+
+    def _ev(n: Node):
+        if id(n) in bind:
+            return bind[id(n)]
+        op = n.op
+        if op == "core.const":
+            return float(n.attr("value"))
+        if op == "core.yield":
+            return ev(n.args[0])
+        if op == "core.tuple":
+            return tuple(ev(a) for a in n.args)
+        if op == "tl.pointwise":
+            vals = [ev(a) for a in n.args]
+            ref = next(v for v in vals if isinstance(v, Field))
+            arrs = [_as_field(v, ref) for v in vals]
+            return Field(np.asarray(_PW[n.attr("f")](*arrs)), ref.dims)
+        if op == "tl.reduce":
+            x = ev(n.args[0])
+            dims = n.attr("dims")
+            dims = (dims,) if isinstance(dims, str) else tuple(dims)
+            axes = tuple(x.names.index(d) for d in dims)
+            f = n.attr("f")
+            arr = x.arr.astype(np.float64) if x.arr.dtype == bool else x.arr
+            if f == "mean":
+                cnt = 1
+                for ax in axes:
+                    cnt *= arr.shape[ax]
+                out = np.add.reduce(arr, axis=axes) / cnt
+            else:
+                fn, ident = _RED[f]
+                out = fn.reduce(arr, axis=axes) if ident is None else fn.reduce(arr, axis=axes, initial=ident)
+            return Field(np.asarray(out), tuple(d for d in x.dims if d.name not in dims))
+        if op == "tl.repeat_like":
+            x, like = ev(n.args[0]), ev(n.args[1])
+            extra = tuple(d for d in like.dims if d.name not in x.names)
+            arr = x.arr.reshape(x.arr.shape + (1,) * len(extra))
+            return Field(np.broadcast_to(arr, x.arr.shape + tuple(d.size for d in extra)), x.dims + extra)
+        if op == "tl.repeat":
+            x = ev(n.args[0])
+            (d,) = [e for e in n.type.dims if e.name == n.attr("name")]
+            return Field(np.broadcast_to(x.arr[..., None], x.arr.shape + (d.size,)), x.dims + (d,))
+        if op == "tl.split":
+            x = ev(n.args[0])
+            name = n.attr("name")
+            ax = x.names.index(name)
+            sizes = tuple(int(s) for _, s in n.attr("parts"))
+            arr = x.arr.reshape(x.arr.shape[:ax] + sizes + x.arr.shape[ax + 1:])
+            return Field(arr, n.type.dims)
+        if op == "tl.stage":
+            x = ev(n.args[0])
+            order = n.attr("order")
+            return Field(x.to_numpy(tuple(order)), n.type.dims) if order else x
+        if op == "tl.select":
+            x = ev(n.args[0])
+            for name, i in n.attr("coords"):
+                x = x.select(name, i)
+            return x
+        if op == "tl.iota":  # a closed form: the lattice's values are never read
+            tt: TensorType = n.type
+            name = n.attr("name")
+            ax = tt.names.index(name)
+            d = tt.dims[ax]
+            shape = [1] * len(tt.dims)
+            shape[ax] = d.size
+            coords = np.arange(d.start, d.stop, dtype=np.int64).reshape(shape)
+            return Field(np.broadcast_to(coords, tt.shape), tt.dims)
+        if op == "tl.const":
+            tt = n.type
+            return Field(np.full(tt.shape, float(n.attr("value"))), tt.dims)
+        if op == "tl.fold":
+            state = tuple(n.attr("state"))
+            k = len(state)
+            dim = n.attr("dim")
+            vals = [ev(a) for a in n.args]
+            carried, srcs = list(vals[:k]), vals[k:]
+            d = n.args[k].type.dim(dim)
+            step = n.regions[0]
+            for q in range(d.start, d.stop):
+                res = run_region(step, carried + [s.select(dim, q) for s in srcs])
+                carried = list(res) if isinstance(res, tuple) else [res]
+            return carried[n.attr("out")[1]]
+        raise NotImplementedError(f"run_region: {op} has no evaluation rule here")
+
+    return ev(region.body[-1])
