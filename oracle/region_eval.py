@@ -1,0 +1,200 @@
+"""ORACLE — test infrastructure only (the checker, never the product).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this package.
+
+A float64 region evaluator on torch's CPU backend: the restatement of the
+reference's second oracle, the substrate-generic interpreter with its torch
+substrate (conformance/region_evaluator.py:167-471 + conformance/
+torch_evaluator.py:27-139, float64 by default). It interprets the same
+regions pdum_dsl_amd.tl builds — the naive twins (the denotation) and the
+generated tile programs — by its own dispatch, independent of the
+planner's numpy interpreter, so each can check the other:
+
+  tl.pointwise   operands aligned by dim NAME, scalars broadcast
+                 (region_evaluator.py:289-318; compute.py:95-123)
+  tl.reduce      sum/prod/max/min via torch reductions; mean = sum / N
+                 (compute.py:184-214; region_evaluator.py:320-352)
+  tl.repeat_like / tl.repeat / tl.split / tl.stage / tl.select / tl.iota /
+  tl.const       layout views (region_evaluator.py:372-430)
+  tl.fold        a Python loop over the scan dim, each element source
+                 selected at the ABSOLUTE coordinate (dialect.py:1448-1470;
+                 region_evaluator.py:431-465)
+
+Values are (tensor, names) pairs; every float is float64.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+_PW = {
+    "add": torch.add, "sub": torch.sub, "mul": torch.mul, "div": torch.div, "neg": torch.neg,
+    "exp": torch.exp, "log": torch.log, "maximum": torch.maximum, "minimum": torch.minimum,
+    "tanh": torch.tanh, "sqrt": torch.sqrt, "sin": torch.sin, "cos": torch.cos, "abs": torch.abs,
+    "floor": torch.floor, "eq": torch.eq, "ne": torch.ne, "le": torch.le, "lt": torch.lt, "ge": torch.ge,
+    "gt": torch.gt, "stop_gradient": lambda x: x,
+}
+
+
+class V:
+    """A named-dim float64 (or bool) tensor; dims = tuple of (name, start, stop)."""
+
+    __slots__ = ("t", "dims")
+
+    def __init__(self, t: torch.Tensor, dims):
+        self.t, self.dims = t, tuple(dims)
+
+    @property
+    def names(self):
+        return tuple(d[0] for d in self.dims)
+
+    def order(self, names) -> torch.Tensor:
+        return self.t.permute([self.names.index(n) for n in names])
+
+    def numpy(self, names=None) -> np.ndarray:
+        t = self.t if names is None else self.order(names)
+        return t.detach().cpu().numpy()
+
+
+def value(arr, ir_type) -> V:
+    """Wrap a numpy array as a value of a TensorType (axes in type-dim order)."""
+    dims = tuple((d.name, d.start, d.stop) for d in ir_type.dims)
+    t = torch.as_tensor(np.asarray(arr))
+    if t.dtype != torch.bool:
+        t = t.to(torch.float64)
+    return V(t, dims)
+
+
+def _dims_arg(d):
+    return (d,) if isinstance(d, str) else tuple(d)
+
+
+def evaluate(region, values: list):
+    """Evaluate ``region`` on V values positional per param; returns V or a tuple of V."""
+    memo: dict[int, object] = {}
+    params = {id(p): v for p, v in zip(region.params, values)}
+
+    def ev(n):
+        k = id(n)
+        if k in memo:
+            return memo[k]
+        r = params[k] if k in params else _dispatch(n, ev)
+        memo[k] = r
+        return r
+
+    return ev(region.body[-1])
+
+
+def _attr(n, name, default=None):
+    for k, v in n.attrs:
+        if k == name:
+            return v
+    return default
+
+
+def _dispatch(n, ev):
+    op = n.op
+    if op == "core.const":
+        return float(_attr(n, "value"))
+    if op == "core.yield":
+        return ev(n.args[0])
+    if op == "core.tuple":
+        return tuple(ev(a) for a in n.args)
+    if op == "tl.pointwise":
+        vals = [ev(a) for a in n.args]
+        ref = next(v for v in vals if isinstance(v, V))
+        ts = [v.order(ref.names) if isinstance(v, V) else v for v in vals]
+        f = _attr(n, "f")
+        if f == "where":
+            c, a, b = ts
+            a = a if torch.is_tensor(a) else torch.tensor(a, dtype=torch.float64)
+            b = b if torch.is_tensor(b) else torch.tensor(b, dtype=torch.float64)
+            out = torch.where(c.bool(), a, b)
+        else:
+            ts = [t if torch.is_tensor(t) else torch.tensor(t, dtype=torch.float64) for t in ts]
+            out = _PW[f](*ts)
+        return V(out, ref.dims)
+    if op == "tl.reduce":
+        x = ev(n.args[0])
+        dims = _dims_arg(_attr(n, "dims"))
+        axes = [x.names.index(d) for d in dims]
+        f = _attr(n, "f")
+        t = x.t.to(torch.float64) if x.t.dtype == torch.bool else x.t
+        if f in ("sum", "mean"):
+            out = t.sum(dim=axes) if axes else t
+            if f == "mean":
+                cnt = 1
+                for a in axes:
+                    cnt *= t.shape[a]
+                out = out / cnt
+        elif f == "prod":
+            out = t
+            for a in sorted(axes, reverse=True):
+                out = out.prod(dim=a)
+        else:
+            out = t
+            for a in sorted(axes, reverse=True):
+                out = out.amax(dim=a) if f == "max" else out.amin(dim=a)
+        return V(out, tuple(d for d in x.dims if d[0] not in dims))
+    if op == "tl.repeat_like":
+        x, like = ev(n.args[0]), ev(n.args[1])
+        extra = tuple(d for d in like.dims if d[0] not in x.names)
+        t = x.t.reshape(tuple(x.t.shape) + (1,) * len(extra))
+        return V(t.expand(tuple(x.t.shape) + tuple(d[2] - d[1] for d in extra)), x.dims + extra)
+    if op == "tl.repeat":
+        x = ev(n.args[0])
+        ext = _attr(n, "extent")
+        lo, hi = (ext if isinstance(ext, tuple) else (0, ext))
+        return V(x.t.unsqueeze(-1).expand(tuple(x.t.shape) + (hi - lo,)), x.dims + ((_attr(n, "name"), lo, hi),))
+    if op == "tl.split":
+        x = ev(n.args[0])
+        name = _attr(n, "name")
+        ax = x.names.index(name)
+        parts = tuple(_attr(n, "parts"))
+        sizes = tuple(int(s) for _, s in parts)
+        t = x.t.reshape(tuple(x.t.shape[:ax]) + sizes + tuple(x.t.shape[ax + 1:]))
+        dims = x.dims[:ax] + tuple((p, 0, int(s)) for p, s in parts) + x.dims[ax + 1:]
+        return V(t, dims)
+    if op == "tl.stage":
+        x = ev(n.args[0])
+        order = _attr(n, "order")
+        if order:
+            return V(x.order(order), tuple(x.dims[x.names.index(o)] for o in order))
+        return x
+    if op == "tl.select":
+        x = ev(n.args[0])
+        for name, i in _attr(n, "coords"):
+            ax = x.names.index(name)
+            x = V(x.t.select(ax, i - x.dims[ax][1]), x.dims[:ax] + x.dims[ax + 1:])
+        return x
+    if op == "tl.iota":
+        dims = tuple((d.name, d.start, d.stop) for d in n.type.dims)
+        name = _attr(n, "name")
+        ax = [d[0] for d in dims].index(name)
+        lo, hi = dims[ax][1], dims[ax][2]
+        shape = [1] * len(dims)
+        shape[ax] = hi - lo
+        coords = torch.arange(lo, hi, dtype=torch.float64).reshape(shape)
+        return V(coords.expand([d[2] - d[1] for d in dims]), dims)
+    if op == "tl.const":
+        dims = tuple((d.name, d.start, d.stop) for d in n.type.dims)
+        return V(torch.full([d[2] - d[1] for d in dims], float(_attr(n, "value")), dtype=torch.float64), dims)
+    if op == "tl.fold":
+        state = tuple(_attr(n, "state"))
+        k = len(state)
+        dim = _attr(n, "dim")
+        vals = [ev(a) for a in n.args]
+        carried, srcs = list(vals[:k]), vals[k:]
+        d = next(x for x in srcs[0].dims if x[0] == dim)
+        step = n.regions[0]
+        for q in range(d[1], d[2]):
+            sel = []
+            for s in srcs:
+                ax = s.names.index(dim)
+                sel.append(V(s.t.select(ax, q - s.dims[ax][1]), s.dims[:ax] + s.dims[ax + 1:]))
+            res = evaluate(step, carried + sel)
+            carried = list(res) if isinstance(res, tuple) else [res]
+        return carried[_attr(n, "out")[1]]
+    raise NotImplementedError(f"oracle evaluator: no rule for {op}")

@@ -1,0 +1,412 @@
+"""compile_tile_hip — the HIP seat of the reference's tile runner.
+
+Same contract as compile_tile (conformance/triton_tile.py:662-698):
+
+    run = compile_tile_hip(region, launch=(), prune=())
+    out = run(values)   # numpy arrays positional per param, each in its
+                        # param's type-dim order; returns one array in the
+                        # yield's dim order, or (out, m, den) for artifacts
+    run.source          # readable kernel-selection descriptor
+    run.grid            # program count of the plan's launch (prod of cdivs)
+    run.checked
+
+Instead of emitting code node by node, the seat RECOGNIZES the tile region
+a fusion template generated and binds it to a hand-written gfx950 kernel:
+
+  flash tile (fusion.py:542-615)          -> pdh_flash_fwd (mask forest -> band)
+  staged row softmax (fusion.py:339-350)  -> pdh_row_softmax
+  staged row statistics (layernorm core + gamma/beta epilogue) -> pdh_layernorm
+
+Anything else raises Untranslatable naming what it could not bind — the
+refusal law of triton_tile.py:216-226 and :617-621. The runner uploads,
+launches, synchronizes and downloads like the reference's; nothing in it
+computes on the host.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from .tl.fusion import FOLD_KW, contract_core, flash_step, forest_is_closed, match_rowstat, match_softmax
+from .tl.ir import Region, walk, walk_deep
+
+HIP_FP = ("tile_hip", "gfx950")
+
+
+class Untranslatable(Exception):
+    """The region (or launch) has no binding to a HIP kernel."""
+
+
+# --------------------------------------------------------------- helpers
+
+
+def _carried_dims(region: Region) -> set:
+    out = set()
+    for n in walk_deep(region):
+        if n.op == "tl.fold":
+            out.add(n.attr("dim"))
+        if n.op == "tl.reduce":
+            d = n.attr("dims")
+            out.update((d,) if isinstance(d, str) else d)
+    return out
+
+
+def _grid(region: Region, launch: tuple) -> int:
+    """Launch legality and the derived program count (triton_tile.py:598-632)."""
+    y = region.body[-1].args[0]
+    if y.op == "core.tuple":
+        y = y.args[0]
+    out_dims = {d.name: d for d in y.type.dims}
+    carried = _carried_dims(region)
+    grid = 1
+    for name, tile in launch:
+        if name not in out_dims:
+            raise Untranslatable(f"launch dim {name!r} is not an output dim")
+        if name in carried:
+            raise Untranslatable(f"launch dim {name!r} is carried/reduced — not griddable")
+        grid *= -(-out_dims[name].size // int(tile))
+    return grid
+
+
+def _unstage(n):
+    while n.op == "tl.stage":
+        n = n.args[0]
+    return n
+
+
+_CLOSED_PW = {
+    "add": np.add, "sub": np.subtract, "mul": np.multiply, "neg": np.negative, "maximum": np.maximum,
+    "minimum": np.minimum, "le": np.less_equal, "lt": np.less, "ge": np.greater_equal, "gt": np.greater,
+    "eq": np.equal, "ne": np.not_equal, "where": np.where, "abs": np.abs,
+}
+
+
+def _eval_closed(n, t: str, s: str, ti: np.ndarray, si: np.ndarray):
+    """Evaluate a closed mask forest at coordinates (ti[:, None], si[None, :])."""
+    if n.op == "tl.iota":
+        nm = n.attr("name")
+        if nm == t:
+            return ti[:, None]
+        if nm == s:
+            return si[None, :]
+        raise Untranslatable(f"mask iota over dim {nm!r} (only {t!r}, {s!r} index the score lattice)")
+    if n.op in ("core.const", "tl.const"):
+        return float(n.attr("value"))
+    if n.op in ("tl.repeat_like", "tl.repeat"):
+        return _eval_closed(n.args[0], t, s, ti, si)
+    if n.op == "tl.pointwise" and n.attr("f") in _CLOSED_PW:
+        return _CLOSED_PW[n.attr("f")](*(_eval_closed(a, t, s, ti, si) for a in n.args))
+    raise Untranslatable(f"mask op {n.op} ({n.attr('f')}) has no closed-form binding")
+
+
+def mask_to_band(mask, t: str, s: str, T: int, S: int, block: int = 1024):
+    """The closed mask forest as a band lo <= s - t <= hi (None = unbounded),
+    or ("none",) when every score is live. Exact: the band is re-evaluated
+    against the forest on the whole lattice; a forest that is not a band
+    refuses."""
+    s_idx = np.arange(S)
+    lo_c, hi_c = set(), set()
+    all_live = True
+    firsts, lasts, empty = np.empty(T, np.int64), np.empty(T, np.int64), np.zeros(T, bool)
+    for r0 in range(0, T, block):
+        r1 = min(T, r0 + block)
+        live = np.broadcast_to(np.asarray(_eval_closed(mask, t, s, np.arange(r0, r1), s_idx), dtype=bool),
+                               (r1 - r0, S))
+        if not live.all():
+            all_live = False
+        any_ = live.any(axis=1)
+        first = np.argmax(live, axis=1)
+        last = S - 1 - np.argmax(live[:, ::-1], axis=1)
+        if np.any(any_ & (live.sum(axis=1) != last - first + 1)):
+            raise Untranslatable("mask forest is not a band (a row's live keys are not contiguous)")
+        firsts[r0:r1], lasts[r0:r1], empty[r0:r1] = first, last, ~any_
+    if all_live:
+        return ("none",)
+    rows = np.arange(T)
+    ok = ~empty
+    lo_c = set((firsts - rows)[ok & (firsts > 0)].tolist())
+    hi_c = set((lasts - rows)[ok & (lasts < S - 1)].tolist())
+    if len(lo_c) > 1 or len(hi_c) > 1:
+        raise Untranslatable("mask forest is not a band (the live window's offsets vary by row)")
+    lo = lo_c.pop() if lo_c else None
+    hi = hi_c.pop() if hi_c else None
+    if empty.any() and hi is None and lo is None:
+        raise Untranslatable("mask forest masks whole rows without a band shape")
+    if empty.all():  # every row masked: a band no key satisfies
+        return ("band", 1, 0)
+    # verify exactly, block by block
+    for r0 in range(0, T, block):
+        r1 = min(T, r0 + block)
+        d = s_idx[None, :] - np.arange(r0, r1)[:, None]
+        want = np.ones_like(d, dtype=bool)
+        if lo is not None:
+            want &= d >= lo
+        if hi is not None:
+            want &= d <= hi
+        got = np.broadcast_to(np.asarray(_eval_closed(mask, t, s, np.arange(r0, r1), s_idx), dtype=bool), want.shape)
+        if not np.array_equal(got, want):
+            raise Untranslatable("mask forest is not a band")
+    return ("band", lo, hi)
+
+
+# --------------------------------------------------------- recognizers
+
+
+def recognize_flash(region: Region):
+    """Bind a flash tile region: (out | (out, m, den)) over two/three fold
+    nodes sharing the online-softmax step. Returns a binding dict or None."""
+    y = region.body[-1].args[0]
+    f_m = None
+    if y.op == "core.tuple":
+        if len(y.args) != 3:
+            return None
+        y, f_m, f_den_a = y.args
+    if y.op != "tl.pointwise" or y.attr("f") != "div" or len(y.args) != 2:
+        return None
+    f_o, rl = y.args
+    if f_o.op != "tl.fold" or rl.op != "tl.repeat_like" or rl.args[1] is not f_o:
+        return None
+    f_den = rl.args[0]
+    folds = [f_o, f_den] + ([f_m] if f_m is not None else [])
+    outs = (("final", 2), ("final", 1), ("final", 0))
+    for fnode, want in zip(folds, outs):
+        if fnode.op != "tl.fold" or tuple(fnode.attr("out")) != want:
+            return None
+        if fnode.args != f_o.args or fnode.regions != f_o.regions:
+            return None
+        for k, v in FOLD_KW.items():
+            if fnode.attr(k) != v:
+                return None
+    if f_m is not None and f_den_a is not f_den:
+        return None
+    m0, den0, o0, qr, kt, vt, mt = f_o.args
+    for c, val in ((m0, -1e30), (den0, 0.0), (o0, 0.0)):
+        if c.op != "tl.const" or float(c.attr("value")) != val:
+            return None
+    if qr.op != "tl.repeat" or qr.attr("name") != "so" or qr.args[0].op != "core.param":
+        return None
+    if not (kt.op == vt.op == mt.op == "tl.split"):
+        return None
+    s = kt.attr("name")
+    parts = kt.attr("parts")
+    if vt.attr("name") != s or mt.attr("name") != s or vt.attr("parts") != parts or mt.attr("parts") != parts:
+        return None
+    if tuple(p for p, _ in parts) != ("so", "si"):
+        return None
+    q, k, v = qr.args[0], kt.args[0], vt.args[0]
+    if k.op != "core.param" or v.op != "core.param":
+        return None
+    if len(region.params) != 3 or {id(q), id(k), id(v)} != {id(p) for p in region.params}:
+        return None
+    step = f_o.regions[0]
+    # the step's contracted dim and fill, then the step must BE the template's step
+    red_e = [n for n in walk(step) if n.op == "tl.reduce" and n.attr("f") == "sum" and contract_core(n) is not None
+             and n.attr("dims") != ("si",)]
+    wh = [n for n in walk(step) if n.op == "tl.pointwise" and n.attr("f") == "where"]
+    if len(red_e) != 1 or len(wh) != 1 or wh[0].args[2].op != "core.const":
+        return None
+    e = red_e[0].attr("dims")[0]
+    fill = float(wh[0].args[2].attr("value"))
+    types = tuple(p.type for p in step.params)
+    if step.key != flash_step(types, e, fill).key:
+        return None
+    t = next(nm for nm in q.type.names if nm != e)
+    o = next(nm for nm in v.type.names if nm != s)
+    mask = mt.args[0]
+    if not forest_is_closed(mask):
+        raise Untranslatable("flash mask forest reads data (the template needs a closed form)")
+    if q.type.names != (t, e) and q.type.names != (e, t):
+        return None
+    return {
+        "q": q, "k": k, "v": v, "mask": mask, "fill": fill, "t": t, "s": s, "e": e, "o": o,
+        "T": q.type.dim(t).size, "S": k.type.dim(s).size, "E": q.type.dim(e).size, "OD": v.type.dim(o).size,
+        "si": int(dict(parts)["si"]), "artifacts": f_m is not None,
+    }
+
+
+def recognize_softmax(region: Region):
+    sm = match_softmax(region.body[-1].args[0])
+    if sm is None or len(region.params) != 1:
+        return None
+    x = _unstage(sm["sm"])
+    if x is not region.params[0]:
+        return None
+    return {"x": x, "s": sm["s"]}
+
+
+def recognize_layernorm(region: Region):
+    y = region.body[-1].args[0]
+    gamma = beta = None
+    node = y
+    if node.op == "tl.pointwise" and node.attr("f") == "add" and len(node.args) == 2 and node.args[1].op == "tl.repeat_like":
+        beta = _unstage(node.args[1].args[0])
+        node = node.args[0]
+    if node.op == "tl.pointwise" and node.attr("f") == "mul" and len(node.args) == 2 and node.args[1].op == "tl.repeat_like":
+        gamma = _unstage(node.args[1].args[0])
+        node = node.args[0]
+    rs = match_rowstat(node)
+    if rs is None:
+        return None
+    x = _unstage(rs["x"])
+    feat = rs["feat"]
+    want = [p for p in (x, gamma, beta) if p is not None]
+    if any(p.op != "core.param" for p in want) or {id(p) for p in want} != {id(p) for p in region.params}:
+        return None
+    for p in (gamma, beta):
+        if p is not None and p.type.names != (feat,):
+            return None
+    return {"x": x, "feat": feat, "eps": rs["eps"], "gamma": gamma, "beta": beta}
+
+
+# ------------------------------------------------------------- runners
+
+
+def _torch():
+    import torch
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("compile_tile_hip runners launch HIP kernels: no GPU is visible")
+    return torch
+
+
+def _index(region, node):
+    return next(i for i, p in enumerate(region.params) if p is node)
+
+
+def compile_tile_hip(region: Region, launch: tuple = (), prune: tuple = (), *, dtype: str = "f32"):
+    """Bind a template tile region to a gfx950 kernel; see the module doc."""
+    grid = _grid(region, tuple(launch))
+    if dtype not in ("f32", "bf16", "f16"):
+        raise Untranslatable(f"element type {dtype!r} (f32, bf16, f16)")
+
+    fb = recognize_flash(region)
+    if fb is not None:
+        return _flash_runner(region, fb, grid, bool(prune), dtype)
+    if dtype != "f32":
+        raise Untranslatable(f"row templates run fp32 only (asked {dtype})")
+    sb = recognize_softmax(region)
+    if sb is not None:
+        return _softmax_runner(region, sb, grid)
+    lb = recognize_layernorm(region)
+    if lb is not None:
+        return _layernorm_runner(region, lb, grid)
+    ops = sorted({n.op for n in walk(region)} - {"core.param", "core.yield"})
+    raise Untranslatable(
+        f"no HIP binding for this tile region (ops: {', '.join(ops)}); bound templates: flash, "
+        "row-normalization, row-statistics"
+    )
+
+
+def _finish(run, source: str, grid: int, template: str):
+    run.source = source
+    run.grid = grid
+    run.checked = True  # precision is by construction: the MFMA / VALU instruction is chosen, not inferred
+    run.template = template
+    return run
+
+
+def _flash_runner(region, fb, grid, prune, dtype):
+    from . import kernels as K
+
+    T, S, E, OD = fb["T"], fb["S"], fb["E"], fb["OD"]
+    band = mask_to_band(fb["mask"], fb["t"], fb["s"], T, S)
+    kband = None if band[0] == "none" else K.Band(band[1], band[2])
+    if dtype != "f32" and not (E == OD and E in (64, 128)):
+        raise Untranslatable(f"{dtype} flash needs e == od in {{64, 128}} (got {E}, {OD})")
+    iq, ik, iv = (_index(region, fb[x]) for x in ("q", "k", "v"))
+    tq = fb["q"].type.names
+
+    def run(values):
+        torch = _torch()
+        tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+        qa = np.asarray(values[iq], dtype=np.float32)
+        if tq != (fb["t"], fb["e"]):
+            qa = qa.T
+        dev = torch.device("cuda")
+        q = torch.as_tensor(np.ascontiguousarray(qa)).to(device=dev, dtype=tdt).view(1, 1, T, E)
+        k = torch.as_tensor(np.ascontiguousarray(values[ik], dtype=np.float32)).to(device=dev, dtype=tdt)
+        v = torch.as_tensor(np.ascontiguousarray(values[iv], dtype=np.float32)).to(device=dev, dtype=tdt)
+        if fb["k"].type.names != (fb["s"], fb["e"]):
+            k = k.t().contiguous()
+        if fb["v"].type.names != (fb["s"], fb["o"]):
+            v = v.t().contiguous()
+        res = K.flash_fwd(q, k.view(1, 1, S, E), v.view(1, 1, S, OD), scale=1.0, band=kband, fill=fb["fill"],
+                          prune=prune, want_lse=False, want_artifacts=fb["artifacts"])
+        torch.cuda.synchronize()
+        out = res.o.view(T, OD).float().cpu().numpy()
+        if fb["artifacts"]:
+            return out, res.m.view(T).cpu().numpy(), res.den.view(T).cpu().numpy()
+        return out
+
+    kern = "flash_fwd_generic_f32" if dtype == "f32" else f"flash_fwd_mfma<{dtype},{E}>"
+    bdesc = "all" if kband is None else f"band({band[1]},{band[2]})"
+    src = (
+        f"hip:{kern} t={T} s={S} e={E} od={OD} si={fb['si']} mask={bdesc} fill={fb['fill']:g} "
+        f"prune={'on' if prune else 'off'} sweeps=1 stores={3 if fb['artifacts'] else 1}"
+    )
+    return _finish(run, src, grid, "flash")
+
+
+def _to_rows(arr: np.ndarray, names: tuple, s: str):
+    """Move dim s last and flatten the rest into rows."""
+    order = tuple(n for n in names if n != s) + (s,)
+    perm = [names.index(n) for n in order]
+    a = np.ascontiguousarray(np.transpose(np.asarray(arr, dtype=np.float32), perm))
+    return a.reshape(-1, a.shape[-1]), a.shape, perm
+
+
+def _from_rows(y: np.ndarray, shape, perm):
+    inv = np.argsort(perm)
+    return np.transpose(y.reshape(shape), inv)
+
+
+def _softmax_runner(region, sb, grid):
+    from . import kernels as K
+
+    names = sb["x"].type.names
+    s = sb["s"]
+    out_names = region.body[-1].args[0].type.names
+
+    def run(values):
+        torch = _torch()
+        rows, shape, perm = _to_rows(values[0], names, s)
+        y = K.row_softmax(torch.as_tensor(rows, device="cuda"))
+        torch.cuda.synchronize()
+        full = _from_rows(y.cpu().numpy(), shape, perm)  # param's dim order
+        return np.transpose(full, [names.index(n) for n in out_names])
+
+    n_rows = math.prod(d.size for d in sb["x"].type.dims if d.name != s)
+    src = f"hip:row_softmax rows={n_rows} cols={sb['x'].type.dim(s).size} reduce={s} sweeps=1 stores=1"
+    return _finish(run, src, grid, "row-normalization")
+
+
+def _layernorm_runner(region, lb, grid):
+    from . import kernels as K
+
+    names = lb["x"].type.names
+    feat = lb["feat"]
+    out_names = region.body[-1].args[0].type.names
+    ix = _index(region, lb["x"])
+    ig = _index(region, lb["gamma"]) if lb["gamma"] is not None else None
+    ib = _index(region, lb["beta"]) if lb["beta"] is not None else None
+
+    def run(values):
+        torch = _torch()
+        rows, shape, perm = _to_rows(values[ix], names, feat)
+        g = None if ig is None else torch.as_tensor(np.asarray(values[ig], dtype=np.float32), device="cuda")
+        b = None if ib is None else torch.as_tensor(np.asarray(values[ib], dtype=np.float32), device="cuda")
+        y = K.layernorm(torch.as_tensor(rows, device="cuda"), g, b, eps=lb["eps"])
+        torch.cuda.synchronize()
+        full = _from_rows(y.cpu().numpy(), shape, perm)
+        return np.transpose(full, [names.index(n) for n in out_names])
+
+    n_rows = math.prod(d.size for d in lb["x"].type.dims if d.name != feat)
+    src = (
+        f"hip:layernorm rows={n_rows} cols={lb['x'].type.dim(feat).size} mean/N=/ {lb['x'].type.dim(feat).size} "
+        f"eps={lb['eps']:g} affine={'gamma' if ig is not None else ''}{'+beta' if ib is not None else ''} "
+        "sweeps=1 stores=1"
+    )
+    return _finish(run, src, grid, "row-statistics")
+

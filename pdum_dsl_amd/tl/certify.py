@@ -105,12 +105,6 @@ def normalize(region: Region) -> Region:
     return cur
 
 
-def _rekey_params(region: Region, like: Region) -> Region:
-    """Twin comparison is over the program, so params are compared by
-    (index, type) — the region keys already include them."""
-    return region
-
-
 def certify(tile: Region, naive: Region, *, licenses=(), families=()) -> Certificate:
     norm_t = normalize(erase_stages(tile))
     norm_n = normalize(naive)

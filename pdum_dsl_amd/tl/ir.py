@@ -230,8 +230,19 @@ def walk(region: Region):
 
 
 def walk_deep(region: Region):
-    """walk() including nodes of sub-regions (fold steps)."""
-    for n in walk(region):
-        yield n
-        for r in n.regions:
-            yield from walk_deep(r)
+    """Every node of the region and of its sub-regions (fold steps), each
+    ONCE: a step region shared by several fold nodes is visited once."""
+    seen: set[int] = set()
+    todo = [region]
+    seen_regions: set[int] = set()
+    while todo:
+        r = todo.pop()
+        if id(r) in seen_regions:
+            continue
+        seen_regions.add(id(r))
+        for n in walk(r):
+            if id(n) in seen:
+                continue
+            seen.add(id(n))
+            yield n
+            todo.extend(n.regions)

@@ -1,0 +1,195 @@
+"""Subject regions for the template rows, spelled op by op with the Builder.
+
+The reference spells these in packages/tensorlib/src/pdum/tl/zoo/tiles.py
+(flash_tile: the hand-written online-softmax tile and its naive twin,
+:143-264) and zoo/zoo_common.py (softmax, causal_softmax, layernorm,
+:56-86). Masks are CLOSED forms over iota (the template refuses data masks);
+the reference fills masked scores with -1e9.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable
+
+import numpy as np
+
+from .dialect import OPS, check_tier
+from .interp import Field
+from .ir import F64, Builder, Region, minus_dim, tensor_type
+
+FILL = -1e9
+
+
+@dataclass(frozen=True)
+class Subject:
+    region: Region  # the naive twin (the denotation the planner reads)
+    inputs: list  # Field values, positional per param
+    oracle: Callable | None = None  # list[np.ndarray] -> np.ndarray (float64 closed form)
+    tile: Region | None = None  # a hand-written tile program, where one exists
+
+    def numpy_inputs(self) -> list:
+        return [f.arr for f in self.inputs]
+
+
+def _c(b: Builder, v: float):
+    return b.emit("core.const", type=F64, value=float(v))
+
+
+def scores(b: Builder, q, k, e: str = "e"):
+    """sc[t, s] = sum_e q[t, e] k[s, e] — the contract idiom."""
+    prod = b.emit("tl.pointwise", b.emit("tl.repeat_like", q, k), b.emit("tl.repeat_like", k, q), f="mul")
+    return b.emit("tl.reduce", prod, dims=(e,), f="sum")
+
+
+def softmax_chain(b: Builder, sm, s: str):
+    """div(exp(sm - rl(max_s sm)), rl(sum_s exp(...))) — zoo_common.softmax."""
+    mx = b.emit("tl.reduce", sm, dims=(s,), f="max")
+    ex = b.emit("tl.pointwise", b.emit("tl.pointwise", sm, b.emit("tl.repeat_like", mx, sm), f="sub"), f="exp")
+    den = b.emit("tl.reduce", ex, dims=(s,), f="sum")
+    return b.emit("tl.pointwise", ex, b.emit("tl.repeat_like", den, ex), f="div"), mx, den
+
+
+def mask_forest(b: Builder, lattice, kind, T: int, S: int):
+    """A closed mask over the (t, s) lattice:
+    "causal"  le(iota_s, iota_t)      "strict" lt(iota_s, iota_t)
+    "all"     lt(iota_s, const S)      ("window", W): causal AND t - s < W."""
+    it_s = b.emit("tl.iota", lattice, name="s")
+    it_t = b.emit("tl.iota", lattice, name="t")
+    if kind == "causal":
+        return b.emit("tl.pointwise", it_s, it_t, f="le")
+    if kind == "strict":
+        return b.emit("tl.pointwise", it_s, it_t, f="lt")
+    if kind == "all":
+        return b.emit("tl.pointwise", it_s, _c(b, S), f="lt")
+    if isinstance(kind, tuple) and kind[0] == "window":
+        causal = b.emit("tl.pointwise", it_s, it_t, f="le")
+        inwin = b.emit("tl.pointwise", b.emit("tl.pointwise", it_t, it_s, f="sub"), _c(b, kind[1]), f="lt")
+        return b.emit("tl.pointwise", causal, inwin, f="mul")  # bool AND
+    raise ValueError(f"unknown mask kind {kind!r}")
+
+
+def attention(T=6, S=None, E=3, OD=2, *, mask="causal", artifacts=False, seed=7, scale=1.0) -> Subject:
+    """The naive attention region softmax(where(mask, q k^T, -1e9)) v over
+    q:(t,e), k:(s,e), v:(s,o) params; ``artifacts`` yields (out, max, den).
+    ``scale`` multiplies the drawn q (the template has no score scale)."""
+    S = T if S is None else S
+    rng = np.random.default_rng(seed)
+    Q = scale * rng.standard_normal((T, E))
+    Kv = rng.standard_normal((S, E))
+    V = rng.standard_normal((S, OD))
+    b = Builder(OPS)
+    pq = b.param(0, tensor_type(("t", "e"), Q.shape))
+    pk = b.param(1, tensor_type(("s", "e"), Kv.shape))
+    pv = b.param(2, tensor_type(("s", "o"), V.shape))
+    sc = scores(b, pq, pk)
+    m = mask_forest(b, sc, mask, T, S)
+    sm = b.emit("tl.pointwise", m, sc, _c(b, FILL), f="where")
+    pr, mx, den = softmax_chain(b, sm, "s")
+    prod = b.emit("tl.pointwise", b.emit("tl.repeat_like", pr, pv), b.emit("tl.repeat_like", pv, pr), f="mul")
+    out = b.emit("tl.reduce", prod, dims=("s",), f="sum")
+    y = b.emit("core.tuple", out, mx, den) if artifacts else out
+    region = Region(params=(pq, pk, pv), body=(b.emit("core.yield", y),))
+    inputs = [Field(Q, pq.type.dims), Field(Kv, pk.type.dims), Field(V, pv.type.dims)]
+
+    def oracle(arrs):
+        q, k, v = (np.asarray(a, dtype=np.float64) for a in arrs)
+        sc = q @ k.T
+        t_i, s_i = np.arange(T)[:, None], np.arange(S)[None, :]
+        live = {
+            "causal": s_i <= t_i,
+            "strict": s_i < t_i,
+            "all": np.ones((T, S), dtype=bool),
+        }.get(mask) if not isinstance(mask, tuple) else (s_i <= t_i) & (t_i - s_i < mask[1])
+        sm = np.where(live, sc, FILL)
+        p = np.exp(sm - sm.max(axis=1, keepdims=True))
+        return (p / p.sum(axis=1, keepdims=True)) @ v
+
+    return Subject(region, inputs, oracle)
+
+
+def flash_tile(T=6, E=3, OD=2, SI=2, seed=7) -> Subject:
+    """The hand-written flash tile (zoo/tiles.py:143-264): the causal mask as
+    a closed form on a (t, s) lattice built from q, split along s and riding
+    as an element source; q as a stride-0 repeat over so; (m, den, o)
+    carried through a fold whose step is shared by the o and den finals."""
+    from .fusion import FOLD_KW, flash_step
+
+    nv = attention(T, T, E, OD, mask="causal", seed=seed)
+    SO = T // SI
+    b = Builder(OPS)
+    pq = b.param(0, nv.region.params[0].type)
+    pk = b.param(1, nv.region.params[1].type)
+    pv = b.param(2, nv.region.params[2].type)
+    ts = b.emit("tl.repeat", b.emit("tl.select", pq, coords=(("e", 0),)), name="s", extent=T)
+    mask = b.emit("tl.pointwise", b.emit("tl.iota", ts, name="s"), b.emit("tl.iota", ts, name="t"), f="le")
+    parts = (("so", SO), ("si", SI))
+    kt = b.emit("tl.split", pk, name="s", parts=parts)
+    vt = b.emit("tl.split", pv, name="s", parts=parts)
+    mt = b.emit("tl.split", mask, name="s", parts=parts)
+    qr = b.emit("tl.repeat", pq, name="so", extent=SO)
+    m0 = b.emit("tl.const", value=-1e30, dims=(("t", T),))
+    den0 = b.emit("tl.const", value=0.0, dims=(("t", T),))
+    o0 = b.emit("tl.const", value=0.0, dims=(("t", T), ("o", OD)))
+    types = (m0.type, den0.type, o0.type, minus_dim(qr.type, "so"), minus_dim(kt.type, "so"),
+             minus_dim(vt.type, "so"), minus_dim(mt.type, "so"))
+    step = flash_step(types, "e", FILL)
+    args = (m0, den0, o0, qr, kt, vt, mt)
+    f_o = b.emit("tl.fold", *args, regions=(step,), out=("final", 2), **FOLD_KW)
+    f_den = b.emit("tl.fold", *args, regions=(step,), out=("final", 1), **FOLD_KW)
+    out = b.emit("tl.pointwise", f_o, b.emit("tl.repeat_like", f_den, f_o), f="div")
+    tile = check_tier(Region(params=(pq, pk, pv), body=(b.emit("core.yield", out),)))
+    return Subject(nv.region, nv.inputs, nv.oracle, tile)
+
+
+def row_softmax(rows=4, cols=6, seed=9, names=("t", "s")) -> Subject:
+    """softmax over the last name of a 2-D param (test_fusion.py:102-120's subject)."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((rows, cols))
+    b = Builder(OPS)
+    p = b.param(0, tensor_type(names, X.shape))
+    pr, _, _ = softmax_chain(b, p, names[-1])
+    region = Region(params=(p,), body=(b.emit("core.yield", pr),))
+
+    def oracle(arrs):
+        x = np.asarray(arrs[0], dtype=np.float64)
+        e = np.exp(x - x.max(axis=1, keepdims=True))
+        return e / e.sum(axis=1, keepdims=True)
+
+    return Subject(region, [Field(X, p.type.dims)], oracle)
+
+
+def layernorm(rows=4, feat=6, *, affine=True, eps=1e-5, seed=2) -> Subject:
+    """Two-pass layernorm over feat with the gamma/beta epilogue (zoo_common.py:56-60)."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((rows, feat))
+    G = 1 + 0.1 * rng.standard_normal(feat)
+    Bt = 0.1 * rng.standard_normal(feat)
+    b = Builder(OPS)
+    px = b.param(0, tensor_type(("t", "d"), X.shape))
+    params = [px]
+    mu = b.emit("tl.reduce", px, dims=("d",), f="mean")
+    xc = b.emit("tl.pointwise", px, b.emit("tl.repeat_like", mu, px), f="sub")
+    var = b.emit("tl.reduce", b.emit("tl.pointwise", xc, xc, f="mul"), dims=("d",), f="mean")
+    sd = b.emit("tl.pointwise", b.emit("tl.pointwise", var, _c(b, eps), f="add"), f="sqrt")
+    y = b.emit("tl.pointwise", xc, b.emit("tl.repeat_like", sd, px), f="div")
+    inputs = [Field(X, px.type.dims)]
+    if affine:
+        pg = b.param(1, tensor_type(("d",), (feat,)))
+        pb = b.param(2, tensor_type(("d",), (feat,)))
+        y = b.emit("tl.pointwise", y, b.emit("tl.repeat_like", pg, px), f="mul")
+        y = b.emit("tl.pointwise", y, b.emit("tl.repeat_like", pb, px), f="add")
+        params += [pg, pb]
+        inputs += [Field(G, pg.type.dims), Field(Bt, pb.type.dims)]
+    region = Region(params=tuple(params), body=(b.emit("core.yield", y),))
+
+    def oracle(arrs):
+        x = np.asarray(arrs[0], dtype=np.float64)
+        m = x.mean(axis=1, keepdims=True)
+        v = ((x - m) ** 2).mean(axis=1, keepdims=True)
+        out = (x - m) / np.sqrt(v + eps)
+        if affine:
+            out = out * np.asarray(arrs[1]) + np.asarray(arrs[2])
+        return out
+
+    return Subject(region, inputs, oracle)
