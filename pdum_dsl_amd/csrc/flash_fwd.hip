@@ -25,6 +25,8 @@
 // reference's f32 Triton runner occupies (conformance/triton_tile.py:662-698).
 #include "attn_common.h"
 
+#include <type_traits>
+
 namespace pdh {
 namespace {
 
@@ -41,8 +43,9 @@ struct FwdArgs {
   int64_t heads_q, heads_kv;
   int64_t t, s;
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
-  float c2;     // scale * log2(e)
-  float fill2;  // fill * log2(e)
+  float scale;     // > 0
+  float c2;        // scale * log2(e)
+  float fill_raw;  // fill / scale: the masked raw score
   int masked;   // 0: no mask, 1: band
   int64_t band_lo, band_hi;
   int prune;    // skip dead tiles
@@ -71,38 +74,25 @@ struct TileRegs {
   uint32_t v[8][FwdCfg<D>::DG / 2];
 };
 
-template <typename T, int D>
-__device__ __forceinline__ void load_tile(TileRegs<D>& r, const uint16_t* kp, const uint16_t* vp, int64_t k_st,
-                                          int64_t v_st, int key0, int64_t S, int tid) {
+// Issue the buffer loads of one K/V tile: one loop-invariant VGPR offset per
+// operand, the tile/row step in the scalar offset; rows past the last key read
+// as zero (the buffer range ends at the last key). The loaded values are not
+// touched here, so the loads stay in flight across the current tile's compute.
+template <int D>
+__device__ __forceinline__ void load_tile(TileRegs<D>& r, rsrc_t kr, rsrc_t vr, uint32_t k_row_bytes,
+                                          uint32_t v_row_bytes, int key0, uint32_t k_lane, uint32_t v_lane) {
   using C = FwdCfg<D>;
-  constexpr int CPR = D / 8;      // 16-byte chunks per K row
-  constexpr int RPI = 256 / CPR;  // K rows per load instruction
-  // Rows past the last key re-read that key's row and are zeroed by a select:
-  // no divergent branches around the loads. Full tiles take the plain path.
-  const uint16_t* kb = kp + static_cast<int64_t>(key0) * k_st;  // uniform
-  const uint16_t* vb = vp + static_cast<int64_t>(key0) * v_st;
-  const int last = static_cast<int>(S - key0 < C::BN ? S - key0 - 1 : C::BN - 1);
-  const int dgrp = tid & 31, kgrp = tid >> 5;
+  constexpr int RPI = 256 / (D / 8);  // K rows per load instruction
 #pragma unroll
-  for (int i = 0; i < C::KCH; ++i) {
-    const int row = i * RPI + tid / CPR;
-    const bool ok = row <= last;
-    const uint32_t off = static_cast<uint32_t>((ok ? row : last) * k_st * 2 + (tid % CPR) * 16);
-    const u32x4 x = gload<u32x4>(kb, off);
-    r.k[i] = ok ? x : u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int i = 0; i < C::KCH; ++i) r.k[i] = bload128(kr, k_lane, (key0 + i * RPI) * k_row_bytes);
 #pragma unroll
   for (int rr = 0; rr < 8; ++rr) {
-    const int row = kgrp * 8 + rr;
-    const bool ok = row <= last;
-    const uint32_t off = static_cast<uint32_t>((ok ? row : last) * v_st * 2 + dgrp * C::DG * 2);
     if constexpr (C::DG == 4) {
-      const u32x2 x = gload<u32x2>(vb, off);
-      r.v[rr][0] = ok ? x.x : 0u;
-      r.v[rr][1] = ok ? x.y : 0u;
+      const u32x2 x = bload64(vr, v_lane, (key0 + rr) * v_row_bytes);
+      r.v[rr][0] = x.x;
+      r.v[rr][1] = x.y;
     } else {
-      const uint32_t x = gload<uint32_t>(vb, off);
-      r.v[rr][0] = ok ? x : 0u;
+      r.v[rr][0] = bload32(vr, v_lane, (key0 + rr) * v_row_bytes);
     }
   }
 }
@@ -125,10 +115,10 @@ __device__ __forceinline__ void store_tile(const TileRegs<D>& r, unsigned char* 
     // element (key rr, feature d) sits in dword d/2, half d%2 of r.v[rr]
     const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
     u32x4 w;
-    w.x = __builtin_amdgcn_perm(r.v[1][d >> 1], r.v[0][d >> 1], sel);
-    w.y = __builtin_amdgcn_perm(r.v[3][d >> 1], r.v[2][d >> 1], sel);
-    w.z = __builtin_amdgcn_perm(r.v[5][d >> 1], r.v[4][d >> 1], sel);
-    w.w = __builtin_amdgcn_perm(r.v[7][d >> 1], r.v[6][d >> 1], sel);
+    w.x = perm_halves(r.v[1][d >> 1], r.v[0][d >> 1], sel);
+    w.y = perm_halves(r.v[3][d >> 1], r.v[2][d >> 1], sel);
+    w.z = perm_halves(r.v[5][d >> 1], r.v[4][d >> 1], sel);
+    w.w = perm_halves(r.v[7][d >> 1], r.v[6][d >> 1], sel);
     *reinterpret_cast<u32x4*>(vt + (dgrp * C::DG + d) * C::VROW + kgrp * 16) = w;
   }
 }
@@ -183,91 +173,146 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma(FwdArgs a) {
     }
   }
 
-  float m2 = -kInf, lsum = 0.f;
+  // Online-softmax state per lane (query row r32, this lane-half's keys):
+  // mraw is the running max of the RAW scores q.k (scale > 0 commutes with
+  // max), so each probability is one fma + exp2: exp2(s * c2 - mraw * c2).
+  float mraw = -kInf, lsum = 0.f;
   f32x16 oacc[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) oacc[db] = f32x16{};
 
-  TileRegs<D> pre;
-  if (kt_lo < kt_hi) {
-    load_tile<T, D>(pre, kp, vp, a.k_st, a.v_st, kt_lo * C::BN, S_, tid);
-    store_tile<D>(pre, smem, tid);
-  }
-  for (int kt = kt_lo; kt < kt_hi; ++kt) {
-    __syncthreads();
-    unsigned char* stage = smem + ((kt - kt_lo) & 1) * C::STAGE;
-    const bool more = kt + 1 < kt_hi;
-    if (more) load_tile<T, D>(pre, kp, vp, a.k_st, a.v_st, (kt + 1) * C::BN, S_, tid);
-
-    // classify this tile for this wave: dead (skip), full (no mask), or cut
-    const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
-    const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + C::BN - 1 - qw0;
-    bool dead = false, cut = key0 + C::BN > S_;
-    if (a.masked) {
-      dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
-      cut = cut || dmin < a.band_lo || dmax > a.band_hi;
-    }
-    if (!dead) {
-      f32x16 sacc[2] = {f32x16{}, f32x16{}};
-      const unsigned char* kt_lds = stage + r32 * C::KROW + g * 16;
+  // One key tile: S^T = K Q^T, the masked (CUT) or unmasked softmax update,
+  // then O^T += V^T P^T. CUT is a compile-time branch, so the common full
+  // tile carries no per-element mask code.
+  auto tile = [&](const unsigned char* stage, int64_t key0, auto cutc) {
+    constexpr bool CUT = decltype(cutc)::value;
+    f32x16 sacc[2] = {f32x16{}, f32x16{}};
+    const unsigned char* kt_lds = stage + r32 * C::KROW + g * 16;
 #pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
+    for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const u32x4 kv = *reinterpret_cast<const u32x4*>(kt_lds + kb * 32 * C::KROW + ks * 32);
-          sacc[kb] = mfma32<T>(kv, qreg[ks], sacc[kb]);
-        }
+      for (int kb = 0; kb < 2; ++kb) {
+        const u32x4 kv = *reinterpret_cast<const u32x4*>(kt_lds + kb * 32 * C::KROW + ks * 32);
+        sacc[kb] = mfma32<T>(kv, qreg[ks], sacc[kb]);
       }
-      float mloc = -kInf;
+    }
+    if constexpr (CUT) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          float x = sacc[kb][i] * a.c2;
-          if (cut) {
-            const int64_t key = key0 + kb * 32 + (i >> 3) * 16 + g * 8 + (i & 7);
-            const int64_t d = key - qrow;
-            if (key >= S_) x = -kInf;
-            else if (a.masked && (d < a.band_lo || d > a.band_hi)) x = a.fill2;
-          }
-          sacc[kb][i] = x;
-          mloc = fmaxf(mloc, x);
-        }
-      }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float mnew = fmaxf(m2, mloc);
-      const float alpha = fast_exp2(m2 - mnew);
-      m2 = mnew;
-      lsum *= alpha;
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
-      u32x4 p[4];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float e[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            e[j] = fast_exp2(sacc[kb][8 * h + j] - mnew);
-            lsum += e[j];
-          }
-          p[2 * kb + h] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
-                                pack2<T>(e[6], e[7])};
-        }
-      }
-      const unsigned char* vt_lds = stage + C::KBYTES + r32 * C::VROW + g * 16;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
-          const u32x4 vv = *reinterpret_cast<const u32x4*>(vt_lds + db * 32 * C::VROW + s * 32);
-          oacc[db] = mfma32<T>(vv, p[s], oacc[db]);
+          const int64_t key = key0 + kb * 32 + acc_row(i, g);
+          const int64_t d = key - qrow;
+          if (key >= S_)
+            sacc[kb][i] = -kInf;
+          else if (a.masked && (d < a.band_lo || d > a.band_hi))
+            sacc[kb][i] = a.fill_raw;
         }
       }
     }
-    if (more) store_tile<D>(pre, smem + ((kt + 1 - kt_lo) & 1) * C::STAGE, tid);
+    float mloc = -kInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, sacc[kb][i]);
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float mnew = fmaxf(mraw, mloc);
+    // rescale only when some row's max moved (alpha == 1 exactly otherwise)
+    if (__builtin_amdgcn_ballot_w64(mnew > mraw) != 0) {
+      const float alpha = fast_exp2((mraw - mnew) * a.c2);
+      mraw = mnew;
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
+    }
+    const float mc = mraw * a.c2;
+    u32x4 p[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          // Full tiles hold live (bounded) scores: one fma. Masked tiles may hold
+          // fill-level scores equal to the running max, where only (s - m) * c
+          // cancels exactly (a fully-masked row: every p is exp2(0) = 1).
+          e[j] = CUT ? fast_exp2((sacc[kb][8 * h + j] - mraw) * a.c2)
+                     : fast_exp2(__builtin_fmaf(sacc[kb][8 * h + j], a.c2, -mc));
+          lsum += e[j];
+        }
+        p[2 * kb + h] =
+            u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
+      }
+    }
+    const unsigned char* vt_lds = stage + C::KBYTES + r32 * C::VROW + g * 16;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        const u32x4 vv = *reinterpret_cast<const u32x4*>(vt_lds + db * 32 * C::VROW + s * 32);
+        oacc[db] = mfma32<T>(vv, p[s], oacc[db]);
+      }
+    }
+  };
+
+  // Tiles that are fully live for every row of the workgroup form one
+  // contiguous run [kf_lo, kf_hi); the tiles before it (a window's left edge)
+  // and after it (the diagonal, the key tail) take the masked body. Three
+  // loops over one tile sequence, so each loop body holds one tile variant.
+  int kf_lo = kt_lo, kf_hi = kt_hi;
+  {
+    const int64_t full_end_keys = S_ / C::BN;  // tiles past this hold the key tail
+    kf_hi = kf_hi < full_end_keys ? kf_hi : static_cast<int>(full_end_keys);
+    if (a.masked) {
+      const int64_t qlo = q0, qhi = q0 + C::BM - 1;
+      if (a.band_hi < INT64_MAX / 4) {  // key0 + BN - 1 - qlo <= hi
+        const int64_t lim = qlo + a.band_hi - (C::BN - 1);
+        const int64_t n = lim < 0 ? 0 : lim / C::BN + 1;
+        kf_hi = kf_hi < n ? kf_hi : static_cast<int>(n);
+      }
+      if (a.band_lo > INT64_MIN / 4) {  // key0 - qhi >= lo
+        const int64_t lim = qhi + a.band_lo;
+        const int64_t n = lim <= 0 ? 0 : (lim + C::BN - 1) / C::BN;
+        kf_lo = kf_lo > n ? kf_lo : static_cast<int>(n);
+      }
+    }
+    if (kf_lo > kf_hi) kf_lo = kf_hi = kt_hi;
   }
+
+  constexpr int CPR = D / 8;
+  const uint32_t k_row_bytes = static_cast<uint32_t>(a.k_st * 2), v_row_bytes = static_cast<uint32_t>(a.v_st * 2);
+  const rsrc_t kr = make_rsrc(kp, static_cast<uint32_t>((S_ - 1) * a.k_st * 2 + D * 2));
+  const rsrc_t vr = make_rsrc(vp, static_cast<uint32_t>((S_ - 1) * a.v_st * 2 + D * 2));
+  const uint32_t k_lane = static_cast<uint32_t>((tid / CPR) * k_row_bytes + (tid % CPR) * 16);
+  const uint32_t v_lane = static_cast<uint32_t>((tid >> 5) * 8 * v_row_bytes + (tid & 31) * C::DG * 2);
+  TileRegs<D> pre;
+  if (kt_lo < kt_hi) {
+    load_tile<D>(pre, kr, vr, k_row_bytes, v_row_bytes, kt_lo * C::BN, k_lane, v_lane);
+    store_tile<D>(pre, smem, tid);
+  }
+  auto sweep = [&](int from, int to, auto cutc) {
+    for (int kt = from; kt < to; ++kt) {
+      __syncthreads();
+      const unsigned char* stage = smem + ((kt - kt_lo) & 1) * C::STAGE;
+      // the next tile's loads, issued unconditionally: past the last tile they
+      // read beyond the buffer range (zeros) and land in the idle buffer — no
+      // branch, so no control-flow join for the wait-count pass to merge
+      load_tile<D>(pre, kr, vr, k_row_bytes, v_row_bytes, (kt + 1) * C::BN, k_lane, v_lane);
+      const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
+      bool dead = false;
+      if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's rows see no live key here
+        const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + C::BN - 1 - qw0;
+        dead = dmin > a.band_hi || dmax < a.band_lo;
+      }
+      if (!dead) tile(stage, key0, cutc);
+      store_tile<D>(pre, smem + ((kt + 1 - kt_lo) & 1) * C::STAGE, tid);
+    }
+  };
+  sweep(kt_lo, kf_lo, std::true_type{});
+  sweep(kf_lo, kf_hi, std::false_type{});
+  sweep(kf_hi, kt_hi, std::true_type{});
 
   // epilogue: combine the two lane halves' partial denominators, normalize, store
   const float den = lsum + __shfl_xor(lsum, 32, 64);
@@ -287,10 +332,10 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma(FwdArgs a) {
     }
     if (g == 0) {
       const int64_t srow = inst * T_ + qrow;
-      const float m_nat = m2 * kLn2;
+      const float m_nat = mraw * a.scale;  // the running max of the scaled scores
       if (a.m_out) a.m_out[srow] = m_nat;
       if (a.den_out) a.den_out[srow] = den;
-      if (a.lse_out) a.lse_out[srow] = (m2 + __log2f(den)) * kLn2;
+      if (a.lse_out) a.lse_out[srow] = m_nat + __logf(den);
     }
   }
 }
@@ -451,6 +496,7 @@ extern "C" int pdh_flash_fwd(const void* q, const void* k, const void* v, void* 
     return check_launch("pdh_flash_fwd");
   }
   PDH_REQUIRE(dtype == PDH_BF16 || dtype == PDH_F16, PDH_EINVAL, "pdh_flash_fwd: unknown dtype %d", dtype);
+  PDH_REQUIRE(scale > 0.f, PDH_EINVAL, "pdh_flash_fwd: the 16-bit kernels need scale > 0 (got %g)", (double)scale);
   PDH_REQUIRE(G.e == G.od && (G.e == 64 || G.e == 128), PDH_EUNSUPPORTED,
               "pdh_flash_fwd: 16-bit kernels need e == od in {64, 128} (got e %lld od %lld)", (long long)G.e,
               (long long)G.od);
@@ -463,9 +509,11 @@ extern "C" int pdh_flash_fwd(const void* q, const void* k, const void* v, void* 
   PDH_REQUIRE(G.t <= INT32_MAX / 2 && G.s <= INT32_MAX / 2, PDH_EINVAL, "pdh_flash_fwd: sequence too long");
   PDH_REQUIRE(G.q_st < (1 << 24) && G.k_st < (1 << 24) && G.v_st < (1 << 24) && G.o_st < (1 << 24), PDH_EINVAL,
               "pdh_flash_fwd: row strides must be < 2^24 elements");
+  PDH_REQUIRE(G.s * G.k_st * 2 < INT32_MAX && G.s * G.v_st * 2 < INT32_MAX, PDH_EINVAL,
+              "pdh_flash_fwd: one instance's K / V rows must span < 2 GiB");
   FwdArgs a{q, k, v, o, m_out, den_out, lse_out, G.heads_q, G.heads_kv, G.t, G.s,
             G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st, G.o_sb, G.o_sh, G.o_st,
-            scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi, prune_ok,
+            scale, scale * kLog2e, fill / scale, masked, band_lo, band_hi, prune_ok,
             static_cast<int>((G.t + 127) / 128), 0};
   if (dtype == PDH_BF16) {
     return G.e == 128 ? launch_mfma<__hip_bfloat16, 128>(a, ninst, st) : launch_mfma<__hip_bfloat16, 64>(a, ninst, st);
