@@ -36,7 +36,30 @@ def _args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--quick", action="store_true", help="skip the secondary configs and the CPU baseline")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument(
+        "--copy-probe",
+        action="store_true",
+        help="also run a plain device copy of known size (the calibration kernel of the FETCH_SIZE / WRITE_SIZE runs)",
+    )
     return p.parse_args()
+
+
+COPY_PROBE_BYTES = 256 << 20  # bytes read (and bytes written) by one calibration copy
+PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "flash_fwd_mfma_c3_pmc.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the C3 forward, as the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary states it (a line
+    `traffic_bytes_per_launch: N`), or None when no such summary exists."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1].strip()))
+    except OSError:
+        return None
+    return None
 
 
 def causal_flops(B, H, S, D):
@@ -100,6 +123,14 @@ def main():
         assert err <= 2e-2 and lerr <= 1e-3, f"flash fwd parity failed at {bh}: out {err}, lse {lerr}"
         verify.append({"instance": list(bh), "max_abs_err_out": err, "max_abs_err_lse": lerr})
 
+    if a.copy_probe:  # a plain copy of known size, for scaling the HBM byte counters
+        src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
@@ -146,7 +177,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "algorithmic_flop_per_launch": flops,
         },
         "verify": verify,
