@@ -47,4 +47,62 @@ __device__ __forceinline__ uint32_t perm_halves(uint32_t hi_src, uint32_t lo_src
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
+
+// ------------------------------------------------ LDS staging for key tiles
+//
+// Key/value tiles are copied HBM -> LDS by direct buffer loads (no VGPR round
+// trip): one buffer_load_dwordx4 ... lds writes 16 bytes per lane to
+// M0 + 16 * lane, i.e. 1 KB contiguous per wave. Rows are D * 2 bytes with no
+// padding; instead, the 16-byte slot that holds chunk c of row r is
+// c ^ swz(r), chosen so that the operand reads below hit distinct banks.
+
+__device__ __forceinline__ int swap_bits23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+// K rows are read as MFMA A operands, lane l reading row swap_bits23(l % 32)
+// (see kperm_inv) at one 16-byte chunk: rows {0..3, 8..11} (8 lanes) and
+// rows 0..15 (16 lanes) land on distinct 16-byte bank groups.
+template <int D>
+__device__ __forceinline__ int swz_k(int row) {
+  return swap_bits23(row & 15) & (D / 8 - 1);
+}
+
+// V rows are read with ds_read_b64_tr_b16: each 16-lane group reads 4
+// consecutive rows x 32 contiguous bytes (two slots). These masks spread the
+// 4 rows' slot pairs over distinct banks for 32- and 64-bank LDS.
+template <int D>
+__device__ __forceinline__ int swz_v(int row) {
+  const int kk = row & 3;
+  return D == 128 ? ((kk << 2) ^ ((kk >> 1) << 1)) : (kk << 1);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 16 bytes per lane, buffer -> LDS (lane i's bytes land at lds + 16 i; lds is
+// wave-uniform). Inline asm keeps the compiler's wait-count pass from making
+// every later LDS read wait for it: callers wait with s_waitcnt vmcnt(0) and a
+// barrier before reading the tile.
+__device__ __forceinline__ void dma16(rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+  const uint32_t m0 =
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)lds)));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: listed so the compiler knows it changes
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ds_read_b64_tr_b16: in each 16-lane group, lane 4k + c supplies the address
+// of 8 bytes (4 elements); lane i of the group receives element (i % 4) of the
+// chunk addressed by lane 4k + i / 4, for k = 0..3. Pointing lane 4k + c at
+// row k, features 4c..4c+3 of a row-major tile gives lane i the 4 rows' values
+// of feature i: a transposed (k-contiguous) MFMA operand.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 ds_read_tr16(const unsigned char* p) {
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 }  // namespace pdh

@@ -3,17 +3,21 @@
 // (out, m, den) artifacts of the §7.8 variant and lse = m + log(den).
 //
 // MFMA kernel (bf16 / f16 in, fp32 accumulate), e == od == D in {64, 128}:
-//   * workgroup = 4 waves x 32 query rows = 128 rows; key tiles of 64 rows,
-//     double-buffered in LDS, filled from registers one tile ahead;
+//   * workgroup = 4 waves x 32 query rows = 128 rows; key tiles of 32 rows,
+//     double-buffered in LDS (32 KB at D = 128): three workgroups share a CU,
+//     so three waves per SIMD overlap each other's LDS / MFMA / VALU latency;
+//   * K and V tiles go HBM -> LDS by direct buffer loads (no VGPR staging, no
+//     LDS write instructions) into unpadded rows whose 16-byte slots are
+//     XOR-swizzled so every operand read is bank-conflict free;
 //   * scores are computed TRANSPOSED, S^T = K Q^T with v_mfma_f32_32x32x16,
 //     so lane l owns query row (l % 32): the running max / denominator live in
-//     registers and the row max needs one cross-half shuffle per tile;
-//   * K rows are written to LDS in a permuted order (kperm_inv below) chosen so
-//     that the S^T accumulator registers ARE the B operand of the P V MFMA
-//     (O^T = V^T P^T) — no register shuffles between the two contractions;
-//   * V is transposed 8x(DG) in registers on its way into LDS (V^T rows), so
-//     every MFMA operand read is one 128-bit LDS read;
-//   * exp runs as exp2 on pre-multiplied log2(e) scores (v_exp_f32);
+//     registers and the row max needs one cross-half shuffle per tile. Lane l
+//     reads K row swap_bits23(l % 32), which makes the S^T accumulators of a
+//     lane-half exactly the B operand (8 consecutive keys) of O^T += V^T P^T —
+//     no register shuffles between the two contractions;
+//   * V stays row-major in LDS and is read transposed by ds_read_b64_tr_b16;
+//   * exp runs as exp2 on log2(e)-scaled scores (v_exp_f32); the running max
+//     is rescaled lazily (only when it grows by more than 2^8);
 //   * causal / band masks prune dead tiles (the mask-derived bounds of
 //     fusion.py:659-690) and mask only the tiles the band cuts;
 //   * heavy (late) query blocks launch first, and the workgroup index is
@@ -55,78 +59,34 @@ struct FwdArgs {
 
 template <int D>
 struct FwdCfg {
-  static constexpr int BM = 128;            // query rows per workgroup
-  static constexpr int BN = 64;             // key rows per tile
-  static constexpr int KROW = D * 2 + 16;   // LDS bytes per K row (16 B pad)
-  static constexpr int VROW = BN * 2 + 16;  // LDS bytes per V^T row
-  static constexpr int KBYTES = BN * KROW;
-  static constexpr int VBYTES = D * VROW;
-  static constexpr int STAGE = KBYTES + VBYTES;
-  static constexpr int LDS = 2 * STAGE;
-  static constexpr int KCH = BN * (D / 8) / 256;  // 16-byte K chunks per thread
-  static constexpr int DG = D / 32;               // V features per thread (8 keys x DG)
+  static constexpr int WAVES = 4;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int BM = 32 * WAVES;          // query rows per workgroup (32 per wave)
+  static constexpr int BN = 32;                  // keys per tile
+  static constexpr int ROWB = D * 2;             // LDS bytes per key row (swizzled, unpadded)
+  static constexpr int CPR = D / 8;              // 16-byte chunks per row
+  static constexpr int TILEB = BN * ROWB;        // one K or V tile
+  static constexpr int KBUF = 0, VBUF = 2 * TILEB;
+  static constexpr int LDS = 4 * TILEB;          // K and V, double buffered: 32 KB at D = 128
+  static constexpr int RPK = 1024 / ROWB;        // rows per 1 KB direct-load block
+  static constexpr int NBLK = TILEB / 1024;      // 1 KB blocks per tile
+  static constexpr int NDMA = (NBLK + WAVES - 1) / WAVES;
+  static constexpr int KS = D / 16;              // k-steps of Q K^T
+  static constexpr int DB = D / 32;              // 32-feature blocks of O
+  static constexpr int NPV = 2 * DB;             // (16-key step, feature block) operands of P V
+  static constexpr int PF = 3;                   // V operands in flight ahead of their MFMA
 };
 
-// One K/V tile held in registers between its global load and its LDS write.
-template <int D>
-struct TileRegs {
-  u32x4 k[FwdCfg<D>::KCH];
-  uint32_t v[8][FwdCfg<D>::DG / 2];
-};
-
-// Issue the buffer loads of one K/V tile: one loop-invariant VGPR offset per
-// operand, the tile/row step in the scalar offset; rows past the last key read
-// as zero (the buffer range ends at the last key). The loaded values are not
-// touched here, so the loads stay in flight across the current tile's compute.
-template <int D>
-__device__ __forceinline__ void load_tile(TileRegs<D>& r, rsrc_t kr, rsrc_t vr, uint32_t k_row_bytes,
-                                          uint32_t v_row_bytes, int key0, uint32_t k_lane, uint32_t v_lane) {
-  using C = FwdCfg<D>;
-  constexpr int RPI = 256 / (D / 8);  // K rows per load instruction
-#pragma unroll
-  for (int i = 0; i < C::KCH; ++i) r.k[i] = bload128(kr, k_lane, (key0 + i * RPI) * k_row_bytes);
-#pragma unroll
-  for (int rr = 0; rr < 8; ++rr) {
-    if constexpr (C::DG == 4) {
-      const u32x2 x = bload64(vr, v_lane, (key0 + rr) * v_row_bytes);
-      r.v[rr][0] = x.x;
-      r.v[rr][1] = x.y;
-    } else {
-      r.v[rr][0] = bload32(vr, v_lane, (key0 + rr) * v_row_bytes);
-    }
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void store_tile(const TileRegs<D>& r, unsigned char* stage, int tid) {
-  using C = FwdCfg<D>;
-  constexpr int CPR = D / 8;
-#pragma unroll
-  for (int i = 0; i < C::KCH; ++i) {
-    const int c = i * 256 + tid;
-    const int row = c / CPR, ch = c % CPR;
-    const int lrow = (row & ~31) + kperm_inv(row & 31);
-    *reinterpret_cast<u32x4*>(stage + lrow * C::KROW + ch * 16) = r.k[i];
-  }
-  unsigned char* vt = stage + C::KBYTES;
-  const int dgrp = tid & 31, kgrp = tid >> 5;
-#pragma unroll
-  for (int d = 0; d < C::DG; ++d) {
-    // element (key rr, feature d) sits in dword d/2, half d%2 of r.v[rr]
-    const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
-    u32x4 w;
-    w.x = perm_halves(r.v[1][d >> 1], r.v[0][d >> 1], sel);
-    w.y = perm_halves(r.v[3][d >> 1], r.v[2][d >> 1], sel);
-    w.z = perm_halves(r.v[5][d >> 1], r.v[4][d >> 1], sel);
-    w.w = perm_halves(r.v[7][d >> 1], r.v[6][d >> 1], sel);
-    *reinterpret_cast<u32x4*>(vt + (dgrp * C::DG + d) * C::VROW + kgrp * 16) = w;
-  }
-}
+// Lazy rescaling: the running max used for the exponentials only moves when a
+// row's max grows by more than 2^kTau (log2 units); probabilities then stay
+// <= 2^kTau, the O accumulators are rescaled rarely, and the result is the
+// same quotient (exact in real arithmetic).
+constexpr float kTau = 8.0f;
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void flash_fwd_mfma(FwdArgs a) {
+__global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs a) {
   using C = FwdCfg<D>;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
 
   // workgroup -> (instance, query block); heavy (late) query blocks first
@@ -149,12 +109,12 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma(FwdArgs a) {
   const int qrow = qw0 + r32;   // this lane's row
 
   // Q as the B operand of S^T = K Q^T: lane holds q[row][16 ks + 8 g .. +8]
-  u32x4 qreg[D / 16];
+  u32x4 qreg[C::KS];
   {
     const uint16_t* qbase = qp + static_cast<int64_t>(qw0) * a.q_st;  // wave-uniform
     const uint32_t q_lane = static_cast<uint32_t>(r32 * a.q_st * 2 + g * 16);
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
+    for (int ks = 0; ks < C::KS; ++ks)
       qreg[ks] = qrow < T_ ? gload<u32x4>(qbase + ks * 16, q_lane) : u32x4{0u, 0u, 0u, 0u};
   }
 
@@ -172,98 +132,12 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma(FwdArgs a) {
       kt_lo = smin <= 0 ? 0 : static_cast<int>(smin / C::BN);
     }
   }
-
-  // Online-softmax state per lane (query row r32, this lane-half's keys):
-  // mraw is the running max of the RAW scores q.k (scale > 0 commutes with
-  // max), so each probability is one fma + exp2: exp2(s * c2 - mraw * c2).
-  float mraw = -kInf, lsum = 0.f;
-  f32x16 oacc[D / 32];
-#pragma unroll
-  for (int db = 0; db < D / 32; ++db) oacc[db] = f32x16{};
-
-  // One key tile: S^T = K Q^T, the masked (CUT) or unmasked softmax update,
-  // then O^T += V^T P^T. CUT is a compile-time branch, so the common full
-  // tile carries no per-element mask code.
-  auto tile = [&](const unsigned char* stage, int64_t key0, auto cutc) {
-    constexpr bool CUT = decltype(cutc)::value;
-    f32x16 sacc[2] = {f32x16{}, f32x16{}};
-    const unsigned char* kt_lds = stage + r32 * C::KROW + g * 16;
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 kv = *reinterpret_cast<const u32x4*>(kt_lds + kb * 32 * C::KROW + ks * 32);
-        sacc[kb] = mfma32<T>(kv, qreg[ks], sacc[kb]);
-      }
-    }
-    if constexpr (CUT) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int64_t key = key0 + kb * 32 + acc_row(i, g);
-          const int64_t d = key - qrow;
-          if (key >= S_)
-            sacc[kb][i] = -kInf;
-          else if (a.masked && (d < a.band_lo || d > a.band_hi))
-            sacc[kb][i] = a.fill_raw;
-        }
-      }
-    }
-    float mloc = -kInf;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, sacc[kb][i]);
-    }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float mnew = fmaxf(mraw, mloc);
-    // rescale only when some row's max moved (alpha == 1 exactly otherwise)
-    if (__builtin_amdgcn_ballot_w64(mnew > mraw) != 0) {
-      const float alpha = fast_exp2((mraw - mnew) * a.c2);
-      mraw = mnew;
-      lsum *= alpha;
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
-    }
-    const float mc = mraw * a.c2;
-    u32x4 p[4];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        float e[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          // Full tiles hold live (bounded) scores: one fma. Masked tiles may hold
-          // fill-level scores equal to the running max, where only (s - m) * c
-          // cancels exactly (a fully-masked row: every p is exp2(0) = 1).
-          e[j] = CUT ? fast_exp2((sacc[kb][8 * h + j] - mraw) * a.c2)
-                     : fast_exp2(__builtin_fmaf(sacc[kb][8 * h + j], a.c2, -mc));
-          lsum += e[j];
-        }
-        p[2 * kb + h] =
-            u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
-      }
-    }
-    const unsigned char* vt_lds = stage + C::KBYTES + r32 * C::VROW + g * 16;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-        const u32x4 vv = *reinterpret_cast<const u32x4*>(vt_lds + db * 32 * C::VROW + s * 32);
-        oacc[db] = mfma32<T>(vv, p[s], oacc[db]);
-      }
-    }
-  };
-
-  // Tiles that are fully live for every row of the workgroup form one
-  // contiguous run [kf_lo, kf_hi); the tiles before it (a window's left edge)
-  // and after it (the diagonal, the key tail) take the masked body. Three
-  // loops over one tile sequence, so each loop body holds one tile variant.
+  // Tiles fully live for every row of the workgroup form one run [kf_lo, kf_hi);
+  // the tiles before it (a window's left edge) and after it (the diagonal, the
+  // key tail) take the masked body.
   int kf_lo = kt_lo, kf_hi = kt_hi;
   {
-    const int64_t full_end_keys = S_ / C::BN;  // tiles past this hold the key tail
+    const int64_t full_end_keys = S_ / C::BN;
     kf_hi = kf_hi < full_end_keys ? kf_hi : static_cast<int>(full_end_keys);
     if (a.masked) {
       const int64_t qlo = q0, qhi = q0 + C::BM - 1;
@@ -281,38 +155,156 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma(FwdArgs a) {
     if (kf_lo > kf_hi) kf_lo = kf_hi = kt_hi;
   }
 
-  constexpr int CPR = D / 8;
-  const uint32_t k_row_bytes = static_cast<uint32_t>(a.k_st * 2), v_row_bytes = static_cast<uint32_t>(a.v_st * 2);
+  // ---- staging: each wave copies 1 KB blocks of the next K and V tiles
+  // straight into LDS; rows past the last key read as zero (buffer range check)
+  const uint32_t grk = static_cast<uint32_t>(a.k_st * 2), grv = static_cast<uint32_t>(a.v_st * 2);
   const rsrc_t kr = make_rsrc(kp, static_cast<uint32_t>((S_ - 1) * a.k_st * 2 + D * 2));
   const rsrc_t vr = make_rsrc(vp, static_cast<uint32_t>((S_ - 1) * a.v_st * 2 + D * 2));
-  const uint32_t k_lane = static_cast<uint32_t>((tid / CPR) * k_row_bytes + (tid % CPR) * 16);
-  const uint32_t v_lane = static_cast<uint32_t>((tid >> 5) * 8 * v_row_bytes + (tid & 31) * C::DG * 2);
-  TileRegs<D> pre;
-  if (kt_lo < kt_hi) {
-    load_tile<D>(pre, kr, vr, k_row_bytes, v_row_bytes, kt_lo * C::BN, k_lane, v_lane);
-    store_tile<D>(pre, smem, tid);
+  const int lrow = lane / C::CPR, slot = lane % C::CPR;  // row within a 1 KB block, 16-byte slot
+  uint32_t dk[C::NDMA];
+#pragma unroll
+  for (int i = 0; i < C::NDMA; ++i) {
+    const int rho = (i * C::WAVES + w) * C::RPK + lrow;
+    dk[i] = lrow * grk + ((slot ^ swz_k<D>(rho)) << 4);
   }
+  const uint32_t dv = lrow * grv + ((slot ^ swz_v<D>(lrow)) << 4);  // RPK is a multiple of 4
+  auto stage = [&](int tile, int buf) {
+#pragma unroll
+    for (int i = 0; i < C::NDMA; ++i) {
+      const int blk = i * C::WAVES + w;
+      if (C::NBLK % C::WAVES != 0 && blk >= C::NBLK) break;
+      const uint32_t row0 = static_cast<uint32_t>(tile * C::BN + blk * C::RPK);
+      dma16(kr, smem + C::KBUF + buf * C::TILEB + blk * 1024, dk[i], row0 * grk);
+      dma16(vr, smem + C::VBUF + buf * C::TILEB + blk * 1024, dv, row0 * grv);
+    }
+  };
+
+  // ---- per-lane operand offsets (tile and buffer parts are immediates)
+  int ka[C::KS];  // K row swap_bits23(r32), chunk 2 ks + g
+  {
+    const int row = swap_bits23(r32);
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) ka[ks] = row * C::ROWB + (((2 * ks + g) ^ swz_k<D>(row)) << 4);
+  }
+  int va[C::DB];  // transposed V reads: rows 8 (G / 2) + kk (+16 s + 4 h), features 32 db + 16 (G % 2) + 4 c
+  {
+    const int G = lane >> 4, kk = (lane >> 2) & 3, c4 = lane & 3;
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db)
+      va[db] = (8 * (G >> 1) + kk) * C::ROWB + (((4 * db + 2 * (G & 1) + (c4 >> 1)) ^ swz_v<D>(kk)) << 4) +
+               ((c4 & 1) << 3);
+  }
+
+  // Online-softmax state per lane (query row r32, this lane-half's keys):
+  // mused is the max the exponentials are referred to (raw scores q.k; scale > 0
+  // commutes with max), mtrue the true running max (the m artifact).
+  float mused = -kInf, mtrue = -kInf, lsum = 0.f;
+  f32x16 oacc[C::DB];
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db) oacc[db] = f32x16{};
+
+  auto vfrag = [&](const unsigned char* vt, int n) {  // operand n = (16-key step s, feature block db)
+    const int s_ = n / C::DB, db = n % C::DB;
+    const u32x2 lo = ds_read_tr16(vt + (16 * s_) * C::ROWB + va[db]);
+    const u32x2 hi = ds_read_tr16(vt + (16 * s_ + 4) * C::ROWB + va[db]);
+    return u32x4{lo.x, lo.y, hi.x, hi.y};
+  };
+
+  // One key tile: S^T = K Q^T, the masked (CUT) or unmasked softmax update,
+  // then O^T += V^T P^T. CUT is a compile-time branch, so the common full tile
+  // carries no per-element mask code.
+  auto tile = [&](int buf, int64_t key0, auto cutc) {
+    constexpr bool CUT = decltype(cutc)::value;
+    const unsigned char* kt = smem + C::KBUF + buf * C::TILEB;
+    const unsigned char* vt = smem + C::VBUF + buf * C::TILEB;
+    f32x16 sacc = f32x16{};
+    u32x4 kf[2];
+    kf[0] = *reinterpret_cast<const u32x4*>(kt + ka[0]);
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+      if (ks + 1 < C::KS) kf[(ks + 1) & 1] = *reinterpret_cast<const u32x4*>(kt + ka[ks + 1]);
+      sacc = mfma32<T>(kf[ks & 1], qreg[ks], sacc);
+    }
+    u32x4 vf[C::PF];  // first V operands, in flight during the softmax
+#pragma unroll
+    for (int n = 0; n < C::PF; ++n) vf[n] = vfrag(vt, n);
+
+    if constexpr (CUT) {
+      // 32-bit offsets from this lane's first key kl = key0 + 8 g: accumulator
+      // i holds key kl + 16 (i / 8) + i % 8; band limits clamped to the tile
+      const int64_t kl = key0 + 8 * g;
+      const int rem = static_cast<int>(S_ - kl < 1024 ? S_ - kl : 1024);
+      const int64_t dl = kl - qrow;
+      auto clampi = [](int64_t x) { return static_cast<int>(x < -4096 ? -4096 : (x > 4096 ? 4096 : x)); };
+      const int lo = a.masked ? clampi(a.band_lo - dl) : -4096;
+      const int hi = a.masked ? clampi(a.band_hi - dl) : 4096;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int c = (i >> 3) * 16 + (i & 7);
+        if (c >= rem)
+          sacc[i] = -kInf;
+        else if (c < lo || c > hi)
+          sacc[i] = a.fill_raw;
+      }
+    }
+    float mloc = -kInf;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, sacc[i]);
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    mtrue = fmaxf(mtrue, mloc);
+    if (__builtin_amdgcn_ballot_w64((mloc - mused) * a.c2 > kTau) != 0) {
+      const float mnew = fmaxf(mused, mloc);
+      const float alpha = fast_exp2((mused - mnew) * a.c2);
+      mused = mnew;
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
+    }
+    const float mc = mused * a.c2;
+    u32x4 p[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // Full tiles hold live (bounded) scores: one fma. Masked tiles may hold
+        // fill-level scores equal to the running max, where only (s - m) * c
+        // cancels exactly (a fully-masked row: every p is exp2(0) = 1).
+        e[j] = CUT ? fast_exp2((sacc[8 * h + j] - mused) * a.c2) : fast_exp2(__builtin_fmaf(sacc[8 * h + j], a.c2, -mc));
+        lsum += e[j];  // fp32 probabilities: lse / den keep fp32 accuracy
+      }
+      p[h] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
+    }
+#pragma unroll
+    for (int n = 0; n < C::NPV; ++n) {
+      const u32x4 vv = vf[n % C::PF];
+      if (n + C::PF < C::NPV) vf[n % C::PF] = vfrag(vt, n + C::PF);
+      oacc[n % C::DB] = mfma32<T>(vv, p[n / C::DB], oacc[n % C::DB]);
+    }
+  };
+
+  if (kt_lo < kt_hi) stage(kt_lo, 0);
   auto sweep = [&](int from, int to, auto cutc) {
     for (int kt = from; kt < to; ++kt) {
-      __syncthreads();
-      const unsigned char* stage = smem + ((kt - kt_lo) & 1) * C::STAGE;
-      // the next tile's loads, issued unconditionally: past the last tile they
-      // read beyond the buffer range (zeros) and land in the idle buffer — no
-      // branch, so no control-flow join for the wait-count pass to merge
-      load_tile<D>(pre, kr, vr, k_row_bytes, v_row_bytes, (kt + 1) * C::BN, k_lane, v_lane);
+      const int buf = (kt - kt_lo) & 1;
+      wait_vmcnt0();  // this wave's share of tile kt has landed
+      __syncthreads();  // ... and everyone's; everyone is done with tile kt - 1
+      // Past the last tile these loads read beyond the buffer range (zeros) into
+      // the idle buffer: no branch, and the last tile's loads are drained below.
+      stage(kt + 1, buf ^ 1);
       const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
       bool dead = false;
       if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's rows see no live key here
         const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + C::BN - 1 - qw0;
         dead = dmin > a.band_hi || dmax < a.band_lo;
       }
-      if (!dead) tile(stage, key0, cutc);
-      store_tile<D>(pre, smem + ((kt + 1 - kt_lo) & 1) * C::STAGE, tid);
+      if (!dead) tile(buf, key0, cutc);
     }
   };
   sweep(kt_lo, kf_lo, std::true_type{});
   sweep(kf_lo, kf_hi, std::false_type{});
   sweep(kf_hi, kt_hi, std::true_type{});
+  wait_vmcnt0();  // no load may be in flight into LDS when the workgroup exits
 
   // epilogue: combine the two lane halves' partial denominators, normalize, store
   const float den = lsum + __shfl_xor(lsum, 32, 64);
@@ -321,7 +313,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma(FwdArgs a) {
     uint16_t* obase = op + static_cast<int64_t>(qw0) * a.o_st;  // wave-uniform
     const uint32_t o_lane = static_cast<uint32_t>(r32 * a.o_st * 2 + g * 8);
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db) {
+    for (int db = 0; db < C::DB; ++db) {
 #pragma unroll
       for (int a4 = 0; a4 < 4; ++a4) {
         const int d0 = db * 32 + a4 * 8;  // + 4 g, carried by o_lane
@@ -332,10 +324,10 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma(FwdArgs a) {
     }
     if (g == 0) {
       const int64_t srow = inst * T_ + qrow;
-      const float m_nat = mraw * a.scale;  // the running max of the scaled scores
-      if (a.m_out) a.m_out[srow] = m_nat;
-      if (a.den_out) a.den_out[srow] = den;
-      if (a.lse_out) a.lse_out[srow] = m_nat + __logf(den);
+      // den sums exp(s - mused); the artifacts are referred to the true max
+      if (a.m_out) a.m_out[srow] = mtrue * a.scale;
+      if (a.den_out) a.den_out[srow] = den * fast_exp2((mused - mtrue) * a.c2);
+      if (a.lse_out) a.lse_out[srow] = mused * a.scale + __logf(den);
     }
   }
 }
@@ -443,17 +435,12 @@ bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
 template <typename T, int D>
 int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
   using C = FwdCfg<D>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&flash_fwd_mfma<T, D>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
-    attr_set = true;
-  }
+  static_assert(C::LDS <= 64 * 1024, "the forward's LDS fits the default dynamic limit");
   const int64_t nblk = ninst * a.nqb;
   PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: grid too large (%lld workgroups)", (long long)nblk);
   FwdArgs aa = a;
   aa.xcd_remap = (nblk % 8 == 0) ? 1 : 0;
-  flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, C::LDS, st>>>(aa);
+  flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk)), C::THREADS, C::LDS, st>>>(aa);
   return check_launch("pdh_flash_fwd");
 }
 
@@ -514,7 +501,7 @@ extern "C" int pdh_flash_fwd(const void* q, const void* k, const void* v, void* 
   FwdArgs a{q, k, v, o, m_out, den_out, lse_out, G.heads_q, G.heads_kv, G.t, G.s,
             G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st, G.o_sb, G.o_sh, G.o_st,
             scale, scale * kLog2e, fill / scale, masked, band_lo, band_hi, prune_ok,
-            static_cast<int>((G.t + 127) / 128), 0};
+            static_cast<int>((G.t + FwdCfg<128>::BM - 1) / FwdCfg<128>::BM), 0};
   if (dtype == PDH_BF16) {
     return G.e == 128 ? launch_mfma<__hip_bfloat16, 128>(a, ninst, st) : launch_mfma<__hip_bfloat16, 64>(a, ninst, st);
   }
