@@ -91,7 +91,10 @@ __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* lds, uint32_t vof
 #pragma clang diagnostic pop
 }
 
-__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima), issued through
+// the builtin so the compiler's own wait-count tracking sees it and adds no
+// later vector-memory waits of its own.
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
 // ds_read_b64_tr_b16: in each 16-lane group, lane 4k + c supplies the address
 // of 8 bytes (4 elements); lane i of the group receives element (i % 4) of the

@@ -220,6 +220,10 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
     f32x16 sacc = f32x16{};
     u32x4 kf[2];
     kf[0] = *reinterpret_cast<const u32x4*>(kt + ka[0]);
+    // MFMA stretches run at raised wave priority, the softmax at the base one:
+    // the SIMD's arbiter then prefers feeding the matrix core from whichever
+    // wave has MFMAs ready while the others' VALU work fills in behind it
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
       if (ks + 1 < C::KS) kf[(ks + 1) & 1] = *reinterpret_cast<const u32x4*>(kt + ka[ks + 1]);
@@ -228,6 +232,7 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
     u32x4 vf[C::PF];  // first V operands, in flight during the softmax
 #pragma unroll
     for (int n = 0; n < C::PF; ++n) vf[n] = vfrag(vt, n);
+    __builtin_amdgcn_s_setprio(0);
 
     if constexpr (CUT) {
       // 32-bit offsets from this lane's first key kl = key0 + 8 g: accumulator
@@ -275,12 +280,14 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
       }
       p[h] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
     }
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int n = 0; n < C::NPV; ++n) {
       const u32x4 vv = vf[n % C::PF];
       if (n + C::PF < C::NPV) vf[n % C::PF] = vfrag(vt, n + C::PF);
       oacc[n % C::DB] = mfma32<T>(vv, p[n / C::DB], oacc[n % C::DB]);
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   if (kt_lo < kt_hi) stage(kt_lo, 0);
