@@ -75,6 +75,17 @@ __device__ __forceinline__ int swz_v(int row) {
   return D == 128 ? ((kk << 2) ^ ((kk >> 1) << 1)) : (kk << 1);
 }
 
+// Tiles read BOTH as rows (b128 A operands, lane row swap_bits23(l % 32)) and
+// transposed (ds_read_b64_tr_b16) — the backward's Q / dO / K tiles — use one
+// table per row % 16, found by exhaustive check to keep both read patterns
+// conflict-free for 32- and 64-bank LDS (the conditions are pinned by
+// tests/test_abi.py): entry i is the XOR mask of row i's 16-byte slots.
+template <int D>
+__device__ __forceinline__ int swz_rt(int row) {
+  constexpr uint64_t kTable = D == 128 ? 0x0c7a42f8e9356d1bull : 0x1265314603742057ull;
+  return static_cast<int>((kTable >> (4 * (row & 15))) & 15u);
+}
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // 16 bytes per lane, buffer -> LDS (lane i's bytes land at lds + 16 i; lds is
@@ -94,6 +105,17 @@ __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* lds, uint32_t vof
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima), issued through
 // the builtin so the compiler's own wait-count tracking sees it and adds no
 // later vector-memory waits of its own.
+// 4 bytes per lane, buffer -> LDS (lane i's dword lands at lds + 4 i).
+__device__ __forceinline__ void dma4(rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+  const uint32_t m0 =
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)lds)));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(m0), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
 // ds_read_b64_tr_b16: in each 16-lane group, lane 4k + c supplies the address

@@ -50,25 +50,32 @@ struct BwdArgs {
   int64_t band_lo, band_hi;
   int prune;
   int nblk;  // blocks per instance (query blocks for dq, key blocks for dkdv)
+  int xcd_remap;
 };
 
 // ---------------------------------------------------------------- row stats
 
+// One row per D/8 lanes (16 bytes of O and dO each): 8 rows per wave at D = 64.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void bwd_stats(BwdArgs a) {
+  constexpr int LPR = D / 8, RPW = 64 / LPR;
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= a.rows) return;
-  const int64_t inst = row / a.t, tq = row % a.t;
-  const int64_t b = inst / a.heads, h = inst % a.heads;
-  const uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + tq * a.o_st;
-  const uint16_t* drow = a.dout + b * a.o_sb + h * a.o_sh + tq * a.o_st;
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const int sub = lane % LPR;
   float acc = 0.f;
+  if (row < a.rows) {
+    const int64_t inst = row / a.t, tq = row % a.t;
+    const int64_t b = inst / a.heads, h = inst % a.heads;
+    const int64_t off = b * a.o_sb + h * a.o_sh + tq * a.o_st + sub * 8;
+    const u32x4 o4 = *reinterpret_cast<const u32x4*>(a.o + off);
+    const u32x4 d4 = *reinterpret_cast<const u32x4*>(a.dout + off);
 #pragma unroll
-  for (int j = 0; j < D / 64; ++j)
-    acc += Elem<T>::to_f32(orow[j * 64 + lane]) * Elem<T>::to_f32(drow[j * 64 + lane]);
-  acc = wave_sum(acc);
-  if (lane == 0) {
+    for (int j = 0; j < 4; ++j)
+      acc += lo_f32<T>(o4[j]) * lo_f32<T>(d4[j]) + hi_f32<T>(o4[j]) * hi_f32<T>(d4[j]);
+  }
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (row < a.rows && sub == 0) {
     float lse2, pm = 0.f;
     if (a.m_in != nullptr) {
       const float m2 = a.m_in[row] * kLog2e, den = a.den_in[row];
@@ -82,73 +89,6 @@ __global__ __launch_bounds__(256) void bwd_stats(BwdArgs a) {
     a.ws[row] = acc;
     a.ws[a.rows + row] = lse2;
     a.ws[2 * a.rows + row] = pm;
-  }
-}
-
-// ---------------------------------------------------------- tile staging
-
-// A ROWS x D tile of 16-bit elements in registers: thread (rgrp, dgrp) holds
-// rows [8 rgrp, 8 rgrp + 8) x features [DG dgrp, DG dgrp + DG).
-template <int ROWS, int D>
-struct TileT {
-  static constexpr int DG = ROWS * D / 2048;
-  static constexpr int NDG = D / DG;
-  static_assert(DG == 2 || DG == 4, "tile shape");
-  uint32_t r[8][DG / 2];
-};
-
-template <int ROWS, int D>
-__device__ __forceinline__ void tload(TileT<ROWS, D>& t, const uint16_t* base, int64_t ld, int64_t nvalid,
-                                      int tid) {
-  constexpr int DG = TileT<ROWS, D>::DG, NDG = TileT<ROWS, D>::NDG;
-  // Rows past nvalid (>= 1) re-read the last valid row and are zeroed by a
-  // select: no divergent branches around the loads.
-  const int dgrp = tid % NDG, rgrp = tid / NDG;
-  const int last = static_cast<int>(nvalid < ROWS ? nvalid - 1 : ROWS - 1);
-#pragma unroll
-  for (int rr = 0; rr < 8; ++rr) {
-    const int row = rgrp * 8 + rr;
-    const bool ok = row <= last;
-    const uint32_t off = static_cast<uint32_t>((ok ? row : last) * ld * 2 + dgrp * DG * 2);
-    if constexpr (DG == 4) {
-      const u32x2 x = gload<u32x2>(base, off);
-      t.r[rr][0] = ok ? x.x : 0u;
-      t.r[rr][1] = ok ? x.y : 0u;
-    } else {
-      const uint32_t x = gload<uint32_t>(base, off);
-      t.r[rr][0] = ok ? x : 0u;
-    }
-  }
-}
-
-// Row-major copy, rows permuted by kperm_inv within each 32-row block.
-template <int ROWS, int D>
-__device__ __forceinline__ void tstore_rows(const TileT<ROWS, D>& t, unsigned char* lds, int rs, int tid) {
-  constexpr int DG = TileT<ROWS, D>::DG, NDG = TileT<ROWS, D>::NDG;
-  const int dgrp = tid % NDG, rgrp = tid / NDG;
-#pragma unroll
-  for (int rr = 0; rr < 8; ++rr) {
-    const int row = rgrp * 8 + rr;
-    unsigned char* dst = lds + ((row & ~31) + kperm_inv(row & 31)) * rs + dgrp * DG * 2;
-    if constexpr (DG == 4)
-      *reinterpret_cast<u32x2*>(dst) = u32x2{t.r[rr][0], t.r[rr][1]};
-    else
-      *reinterpret_cast<uint32_t*>(dst) = t.r[rr][0];
-  }
-}
-
-// Transposed copy: LDS row d holds the tile's column d (ROWS elements).
-template <int ROWS, int D>
-__device__ __forceinline__ void tstore_trans(const TileT<ROWS, D>& t, unsigned char* lds, int ts, int tid) {
-  constexpr int DG = TileT<ROWS, D>::DG, NDG = TileT<ROWS, D>::NDG;
-  const int dgrp = tid % NDG, rgrp = tid / NDG;
-#pragma unroll
-  for (int d = 0; d < DG; ++d) {
-    const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
-    const int c = d >> 1;
-    const u32x4 w = {perm_halves(t.r[1][c], t.r[0][c], sel), perm_halves(t.r[3][c], t.r[2][c], sel),
-                     perm_halves(t.r[5][c], t.r[4][c], sel), perm_halves(t.r[7][c], t.r[6][c], sel)};
-    *reinterpret_cast<u32x4*>(lds + (dgrp * DG + d) * ts + rgrp * 16) = w;
   }
 }
 
@@ -170,62 +110,254 @@ __device__ __forceinline__ void store_rows_t(uint16_t* base, int64_t ld, int r32
   }
 }
 
-// ---------------------------------------------------------------- dK / dV
-
+// A 32-row tile of a [rows, D] 16-bit operand in LDS: unpadded rows of D * 2
+// bytes whose 16-byte slots are XOR-swizzled by swz_rt, filled by direct
+// buffer loads (1 KB per wave instruction). The same tile is read as rows
+// (b128, MFMA A operand) and transposed (ds_read_b64_tr_b16, MFMA A operand
+// with the row index as k).
 template <int D>
-struct DkdvCfg {
-  static constexpr int KB = 128;               // keys per workgroup
-  static constexpr int QT = D == 64 ? 64 : 32;  // query rows per tile
-  static constexpr int RS = D * 2 + 16;        // row-major row stride (bytes)
-  static constexpr int TS = QT * 2 + 16;       // transposed row stride
-  static constexpr int QR = QT * RS;
-  static constexpr int QTR = D * TS;
-  static constexpr int OFF_QT = QR, OFF_DO = QR + QTR, OFF_DOT = 2 * QR + QTR, OFF_LSE = 2 * QR + 2 * QTR;
-  static constexpr int OFF_DEL = OFF_LSE + QT * 4;
-  static constexpr int OFF_PM = OFF_DEL + QT * 4;
-  static constexpr int STAGE = OFF_PM + QT * 4;
-  static constexpr int LDS = 2 * STAGE;
+struct Tile32 {
+  static constexpr int ROWB = D * 2, CPR = D / 8, BYTES = 32 * ROWB, RPK = 1024 / ROWB, NBLK = BYTES / 1024;
+  static constexpr int KS = D / 16, DB = D / 32;
 };
 
+// Per-lane offsets of the tile's three access patterns.
+template <int D>
+struct TileLane {
+  using TT = Tile32<D>;
+  uint32_t dma[(TT::NBLK + 3) / 4];  // direct-load offsets (4 waves share the blocks)
+  int rowr[TT::KS];                 // row reads: row swap_bits23(r32), chunk 2 ks + g
+  int tr[2][TT::DB];                // transposed reads, half h, feature block db (+ 16 s rows: immediate)
+
+  __device__ __forceinline__ void init(int lane, int w, int r32, int g, uint32_t grb) {
+    const int lrow = lane / TT::CPR, slot = lane % TT::CPR;
+#pragma unroll
+    for (int i = 0; i < (TT::NBLK + 3) / 4; ++i) {
+      const int rho = (i * 4 + w) * TT::RPK + lrow;
+      dma[i] = lrow * grb + ((slot ^ swz_rt<D>(rho)) << 4);
+    }
+    const int row = swap_bits23(r32);
+#pragma unroll
+    for (int ks = 0; ks < TT::KS; ++ks) rowr[ks] = row * TT::ROWB + (((2 * ks + g) ^ swz_rt<D>(row)) << 4);
+    const int G = lane >> 4, kk = (lane >> 2) & 3, c4 = lane & 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int trow = 8 * (G >> 1) + 4 * h + kk;
+#pragma unroll
+      for (int db = 0; db < TT::DB; ++db)
+        tr[h][db] = trow * TT::ROWB + (((4 * db + 2 * (G & 1) + (c4 >> 1)) ^ swz_rt<D>(trow)) << 4) + ((c4 & 1) << 3);
+    }
+  }
+  // rows [row0, row0 + 32) of a buffer into an LDS tile (all 4 waves call this)
+  __device__ __forceinline__ void stage(rsrc_t r, unsigned char* lds, uint32_t row0, uint32_t grb, int w) const {
+#pragma unroll
+    for (int i = 0; i < (TT::NBLK + 3) / 4; ++i) {
+      const int blk = i * 4 + w;
+      if (TT::NBLK % 4 != 0 && blk >= TT::NBLK) break;
+      dma16(r, lds + blk * 1024, dma[i], (row0 + blk * TT::RPK) * grb);
+    }
+  }
+  // MFMA A operand: 32 rows x 16 features (k-step ks) of the tile
+  __device__ __forceinline__ u32x4 row_frag(const unsigned char* t, int ks) const {
+    return *reinterpret_cast<const u32x4*>(t + rowr[ks]);
+  }
+  // MFMA A operand, transposed: features 32 db .. +32 x tile rows 16 s .. +16
+  __device__ __forceinline__ u32x4 tr_frag(const unsigned char* t, int s, int db) const {
+    const u32x2 lo = ds_read_tr16(t + 16 * s * TT::ROWB + tr[0][db]);
+    const u32x2 hi = ds_read_tr16(t + 16 * s * TT::ROWB + tr[1][db]);
+    return u32x4{lo.x, lo.y, hi.x, hi.y};
+  }
+};
+
+// -------------------------------------------------------------------- dQ
+//
+// Workgroup: 4 waves x 32 query rows; key tiles of 32 rows (K, V) staged by
+// direct loads, double buffered. Per wave and tile:
+//   S^T = K Q^T, dP^T = V dO^T       (A = K / V rows, B = Q / dO in registers)
+//   dS^T = P^T (dP^T - delta)        (lane = query row: lse, delta are scalars)
+//   dQ^T += K^T dS^T                 (A = K transposed from LDS)
+
 template <typename T, int D>
-__global__ __launch_bounds__(256, 1) void bwd_dkdv(BwdArgs a) {
-  using C = DkdvCfg<D>;
-  constexpr int QT = C::QT, NQB = QT / 32;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+__global__ __launch_bounds__(256, D == 64 ? 3 : 2) void bwd_dq(BwdArgs a) {
+  using TT = Tile32<D>;
+  constexpr int KS = TT::KS, DB = TT::DB, BM = 128, BN = 32;
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];  // K[2], V[2]
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
-  const int64_t inst = blockIdx.x / a.nblk;
-  const int kblk = blockIdx.x % a.nblk;  // early key blocks see the most queries: launched first
+  int bid = blockIdx.x;
+  if (a.xcd_remap) {
+    const int per = gridDim.x >> 3;
+    bid = (bid & 7) * per + (bid >> 3);
+  }
+  const int64_t inst = bid / a.nblk;
+  const int qb = a.nblk - 1 - (bid % a.nblk);  // heavy (late) query blocks first
   const int64_t b = inst / a.heads, h = inst % a.heads;
   const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
   const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
   const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
   const uint16_t* dop = a.dout + b * a.o_sb + h * a.o_sh;
-  const float* delp = a.ws + inst * a.t;
-  const float* lsep = a.ws + a.rows + inst * a.t;
-  const float* pmp = a.ws + 2 * a.rows + inst * a.t;
   const int64_t T_ = a.t, S_ = a.s;
-  const int k0 = kblk * C::KB;
+  const int q0 = qb * BM;
+  const int qw0 = q0 + 32 * w;
+  const int qrow = qw0 + r32;
+
+  u32x4 qreg[KS], doreg[KS];
+  {
+    const uint32_t qoff = static_cast<uint32_t>(r32 * a.q_st * 2 + g * 16);
+    const uint32_t ooff = static_cast<uint32_t>(r32 * a.o_st * 2 + g * 16);
+    const uint16_t* qbs = qp + static_cast<int64_t>(qw0) * a.q_st;
+    const uint16_t* obs = dop + static_cast<int64_t>(qw0) * a.o_st;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qreg[ks] = qrow < T_ ? gload<u32x4>(qbs + ks * 16, qoff) : u32x4{0u, 0u, 0u, 0u};
+      doreg[ks] = qrow < T_ ? gload<u32x4>(obs + ks * 16, ooff) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  const int64_t srow = inst * T_ + qrow;
+  const float dl = qrow < T_ ? a.ws[srow] : 0.f;
+  const float lse2 = qrow < T_ ? a.ws[a.rows + srow] : 0.f;
+
+  const int ntiles = static_cast<int>((S_ + BN - 1) / BN);
+  int kt_lo = 0, kt_hi = ntiles;
+  if (a.masked && a.prune) {
+    const int64_t qlast = (q0 + BM - 1 < T_ ? q0 + BM - 1 : T_ - 1);
+    if (a.band_hi < INT64_MAX / 4) {
+      const int64_t smax = qlast + a.band_hi;
+      kt_hi = smax < 0 ? 0 : static_cast<int>(smax / BN + 1 < ntiles ? smax / BN + 1 : ntiles);
+    }
+    if (a.band_lo > INT64_MIN / 4) {
+      const int64_t smin = q0 + a.band_lo;
+      kt_lo = smin <= 0 ? 0 : static_cast<int>(smin / BN);
+    }
+  }
+
+  const uint32_t grk = static_cast<uint32_t>(a.k_st * 2), grv = static_cast<uint32_t>(a.v_st * 2);
+  const rsrc_t kr = make_rsrc(kp, static_cast<uint32_t>((S_ - 1) * a.k_st * 2 + D * 2));
+  const rsrc_t vr = make_rsrc(vp, static_cast<uint32_t>((S_ - 1) * a.v_st * 2 + D * 2));
+  TileLane<D> kl, vl;  // K and V tiles share the slot layout; only the source stride differs
+  kl.init(lane, w, r32, g, grk);
+  vl.init(lane, w, r32, g, grv);
+  auto kbuf = [&](int buf) { return smem + buf * TT::BYTES; };
+  auto vbuf = [&](int buf) { return smem + (2 + buf) * TT::BYTES; };
+  auto stage = [&](int tile, int buf) {
+    kl.stage(kr, kbuf(buf), static_cast<uint32_t>(tile * BN), grk, w);
+    vl.stage(vr, vbuf(buf), static_cast<uint32_t>(tile * BN), grv, w);
+  };
+
+  f32x16 dqacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
+
+  if (kt_lo < kt_hi) stage(kt_lo, 0);
+  for (int kt = kt_lo; kt < kt_hi; ++kt) {
+    const int buf = (kt - kt_lo) & 1;
+    wait_vmcnt0();
+    __syncthreads();
+    stage(kt + 1, buf ^ 1);  // past the last tile: zeros into the idle buffer
+
+    const int64_t key0 = static_cast<int64_t>(kt) * BN;
+    const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + BN - 1 - qw0;
+    bool dead = false, cut = key0 + BN > S_ || qw0 + 32 > T_;
+    if (a.masked) {
+      dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
+      cut = cut || dmin < a.band_lo || dmax > a.band_hi;
+    }
+    if (dead) continue;
+    const unsigned char* kt_l = kbuf(buf);
+    const unsigned char* vt_l = vbuf(buf);
+    __builtin_amdgcn_s_setprio(1);
+    f32x16 sacc = f32x16{}, pacc = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      sacc = mfma32<T>(kl.row_frag(kt_l, ks), qreg[ks], sacc);
+      pacc = mfma32<T>(vl.row_frag(vt_l, ks), doreg[ks], pacc);
+    }
+    __builtin_amdgcn_s_setprio(0);
+    // accumulator i of lane-half g: key key0 + 16 (i / 8) + 8 g + i % 8, query qrow
+    if (cut) {
+      const int64_t kl0 = key0 + 8 * g;
+      const int rem = static_cast<int>(S_ - kl0 < 1024 ? S_ - kl0 : 1024);
+      const int64_t dl0 = kl0 - qrow;
+      auto clampi = [](int64_t x) { return static_cast<int>(x < -4096 ? -4096 : (x > 4096 ? 4096 : x)); };
+      const int lo = a.masked ? clampi(a.band_lo - dl0) : -4096;
+      const int hi = a.masked ? clampi(a.band_hi - dl0) : 4096;
+      const bool rowok = qrow < T_;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int c = (i >> 3) * 16 + (i & 7);
+        const bool live = rowok && c < rem && c >= lo && c <= hi;
+        pacc[i] = live ? fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * (pacc[i] - dl) : 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pacc[i] = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * (pacc[i] - dl);
+    }
+    const u32x4 ds0 = pack8<T>(pacc, 0), ds1 = pack8<T>(pacc, 1);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      dqacc[db] = mfma32<T>(kl.tr_frag(kt_l, 0, db), ds0, dqacc[db]);
+      dqacc[db] = mfma32<T>(kl.tr_frag(kt_l, 1, db), ds1, dqacc[db]);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+  wait_vmcnt0();
+
+  if (qrow < T_)
+    store_rows_t<T, D>(a.dq + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(qw0) * a.q_st, a.q_st, r32, g, dqacc,
+                       a.scale);
+}
+
+// ---------------------------------------------------------------- dK / dV
+//
+// Workgroup: 4 waves x 32 key rows (K, V in registers as B operands); query
+// tiles of 32 rows (Q, dO and the rows' delta / lse2 / pm) staged by direct
+// loads, double buffered. Per wave and tile:
+//   S = Q K^T, dP = dO V^T           (A = Q / dO rows; lane = key, acc = query)
+//   P = exp2(S c2 - lse2), dS = P (dP - delta)
+//   dV^T += dO^T P, dK^T += Q^T dS   (A = dO / Q transposed from LDS)
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_dkdv(BwdArgs a) {
+  using TT = Tile32<D>;
+  constexpr int KS = TT::KS, DB = TT::DB, BK = 128, QT = 32;
+  constexpr int STATB = 4 * TT::BYTES;  // [2][delta | lse2 | pm] x 32 floats
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];  // Q[2], dO[2], stats[2]
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+  int bid = blockIdx.x;
+  if (a.xcd_remap) {
+    const int per = gridDim.x >> 3;
+    bid = (bid & 7) * per + (bid >> 3);
+  }
+  const int64_t inst = bid / a.nblk;
+  const int kblk = bid % a.nblk;  // early key blocks see the most queries under causal masks: launched first
+  const int64_t b = inst / a.heads, h = inst % a.heads;
+  const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+  const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
+  const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+  const uint16_t* dop = a.dout + b * a.o_sb + h * a.o_sh;
+  const int64_t T_ = a.t, S_ = a.s;
+  const int k0 = kblk * BK;
   const int kw0 = k0 + 32 * w;
   const int krow = kw0 + r32;
 
   // this wave's K and V rows as B operands (lane: row r32, features 16 ks + 8 g .. +8)
-  u32x4 kreg[D / 16], vreg[D / 16];
+  u32x4 kreg[KS], vreg[KS];
   {
     const uint32_t koff = static_cast<uint32_t>(r32 * a.k_st * 2 + g * 16);
     const uint32_t voff = static_cast<uint32_t>(r32 * a.v_st * 2 + g * 16);
-    const uint16_t* kb = kp + static_cast<int64_t>(kw0) * a.k_st;
-    const uint16_t* vb = vp + static_cast<int64_t>(kw0) * a.v_st;
+    const uint16_t* kbs = kp + static_cast<int64_t>(kw0) * a.k_st;
+    const uint16_t* vbs = vp + static_cast<int64_t>(kw0) * a.v_st;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      kreg[ks] = krow < S_ ? gload<u32x4>(kb + ks * 16, koff) : u32x4{0u, 0u, 0u, 0u};
-      vreg[ks] = krow < S_ ? gload<u32x4>(vb + ks * 16, voff) : u32x4{0u, 0u, 0u, 0u};
+    for (int ks = 0; ks < KS; ++ks) {
+      kreg[ks] = krow < S_ ? gload<u32x4>(kbs + ks * 16, koff) : u32x4{0u, 0u, 0u, 0u};
+      vreg[ks] = krow < S_ ? gload<u32x4>(vbs + ks * 16, voff) : u32x4{0u, 0u, 0u, 0u};
     }
   }
 
   const int nqt = static_cast<int>((T_ + QT - 1) / QT);
   int qt_lo = 0, qt_hi = nqt;
   if (a.masked && a.prune) {
-    const int64_t klast = (k0 + C::KB - 1 < S_ ? k0 + C::KB - 1 : S_ - 1);
+    const int64_t klast = (k0 + BK - 1 < S_ ? k0 + BK - 1 : S_ - 1);
     if (a.band_hi < INT64_MAX / 4) {  // q >= key - hi
       const int64_t qmin = k0 - a.band_hi;
       qt_lo = qmin <= 0 ? 0 : static_cast<int>(qmin / QT < nqt ? qmin / QT : nqt);
@@ -236,48 +368,42 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BwdArgs a) {
     }
   }
 
-  f32x16 dkacc[D / 32], dvacc[D / 32];
+  const uint32_t grq = static_cast<uint32_t>(a.q_st * 2), gro = static_cast<uint32_t>(a.o_st * 2);
+  const rsrc_t qr = make_rsrc(qp, static_cast<uint32_t>((T_ - 1) * a.q_st * 2 + D * 2));
+  const rsrc_t orr = make_rsrc(dop, static_cast<uint32_t>((T_ - 1) * a.o_st * 2 + D * 2));
+  const rsrc_t sr = make_rsrc(a.ws, static_cast<uint32_t>(3 * a.rows * 4));
+  TileLane<D> ql, ol;
+  ql.init(lane, w, r32, g, grq);
+  ol.init(lane, w, r32, g, gro);
+  // stats: wave 0 loads delta (lanes 0-31) and lse2 (32-63), then pm (0-31)
+  const uint32_t st_off0 = static_cast<uint32_t>(((lane >> 5) * a.rows + inst * T_ + r32) * 4);
+  const uint32_t st_off1 = static_cast<uint32_t>((2 * a.rows + inst * T_ + r32) * 4);
+  auto qbuf = [&](int buf) { return smem + buf * TT::BYTES; };
+  auto obuf = [&](int buf) { return smem + (2 + buf) * TT::BYTES; };
+  auto sbuf = [&](int buf) { return reinterpret_cast<float*>(smem + STATB + buf * 3 * QT * 4); };
+  auto stage = [&](int qt, int buf) {
+    ql.stage(qr, qbuf(buf), static_cast<uint32_t>(qt * QT), grq, w);
+    ol.stage(orr, obuf(buf), static_cast<uint32_t>(qt * QT), gro, w);
+    if (w == 0) {
+      unsigned char* sl = reinterpret_cast<unsigned char*>(sbuf(buf));
+      dma4(sr, sl, st_off0, static_cast<uint32_t>(qt * QT * 4));
+      if (lane < 32) dma4(sr, sl + 2 * QT * 4, st_off1, static_cast<uint32_t>(qt * QT * 4));
+    }
+  };
+
+  f32x16 dkacc[DB], dvacc[DB];
 #pragma unroll
-  for (int db = 0; db < D / 32; ++db) {
+  for (int db = 0; db < DB; ++db) {
     dkacc[db] = f32x16{};
     dvacc[db] = f32x16{};
   }
 
-  TileT<QT, D> tq, tdo;
-  float pl = 0.f, pd = 0.f, pq = 0.f;  // this thread's lse2 / delta / pm staging values (tid < QT)
-  auto fetch = [&](int qt) {
-    const int64_t q0 = static_cast<int64_t>(qt) * QT;
-    const int64_t nv = T_ - q0;
-    tload<QT, D>(tq, qp + q0 * a.q_st, a.q_st, nv, tid);
-    tload<QT, D>(tdo, dop + q0 * a.o_st, a.o_st, nv, tid);
-    if (tid < QT) {
-      const bool ok = q0 + tid < T_;
-      pl = ok ? lsep[q0 + tid] : 0.f;
-      pd = ok ? delp[q0 + tid] : 0.f;
-      pq = ok ? pmp[q0 + tid] : 0.f;
-    }
-  };
-  auto stage_in = [&](unsigned char* st) {
-    tstore_rows<QT, D>(tq, st, C::RS, tid);
-    tstore_trans<QT, D>(tq, st + C::OFF_QT, C::TS, tid);
-    tstore_rows<QT, D>(tdo, st + C::OFF_DO, C::RS, tid);
-    tstore_trans<QT, D>(tdo, st + C::OFF_DOT, C::TS, tid);
-    if (tid < QT) {
-      reinterpret_cast<float*>(st + C::OFF_LSE)[tid] = pl;
-      reinterpret_cast<float*>(st + C::OFF_DEL)[tid] = pd;
-      reinterpret_cast<float*>(st + C::OFF_PM)[tid] = pq;
-    }
-  };
-
-  if (qt_lo < qt_hi) {
-    fetch(qt_lo);
-    stage_in(smem);
-  }
+  if (qt_lo < qt_hi) stage(qt_lo, 0);
   for (int qt = qt_lo; qt < qt_hi; ++qt) {
+    const int buf = (qt - qt_lo) & 1;
+    wait_vmcnt0();
     __syncthreads();
-    unsigned char* st = smem + ((qt - qt_lo) & 1) * C::STAGE;
-    const bool more = qt + 1 < qt_hi;
-    if (more) fetch(qt + 1);
+    stage(qt + 1, buf ^ 1);  // past the last tile: zeros / ignored rows into the idle buffer
 
     const int64_t q0 = static_cast<int64_t>(qt) * QT;
     const int64_t dmin = kw0 - (q0 + QT - 1), dmax = kw0 + 31 - q0;  // key - q over the tile
@@ -286,74 +412,61 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BwdArgs a) {
       dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
       cut = cut || dmin < a.band_lo || dmax > a.band_hi;
     }
-    if (!dead) {
-      f32x16 sacc[NQB], pacc[NQB];
+    if (dead) continue;
+    const unsigned char* q_l = qbuf(buf);
+    const unsigned char* o_l = obuf(buf);
+    const float* stl = sbuf(buf);
+    __builtin_amdgcn_s_setprio(1);
+    f32x16 sacc = f32x16{}, pacc = f32x16{};
 #pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) {
-        sacc[qb] = f32x16{};
-        pacc[qb] = f32x16{};
-      }
-      const unsigned char* qrows = st + r32 * C::RS + g * 16;
-      const unsigned char* drows = st + C::OFF_DO + r32 * C::RS + g * 16;
+    for (int ks = 0; ks < KS; ++ks) {
+      sacc = mfma32<T>(ql.row_frag(q_l, ks), kreg[ks], sacc);
+      pacc = mfma32<T>(ol.row_frag(o_l, ks), vreg[ks], pacc);
+    }
+    __builtin_amdgcn_s_setprio(0);
+    // accumulator i of lane-half g: query q0 + 16 (i / 8) + 8 g + i % 8, key krow
 #pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
+    for (int hh = 0; hh < 2; ++hh) {
+      const int rb = 16 * hh + 8 * g;
+      const f32x4 d0 = *reinterpret_cast<const f32x4*>(stl + rb);
+      const f32x4 d1 = *reinterpret_cast<const f32x4*>(stl + rb + 4);
+      const f32x4 l0 = *reinterpret_cast<const f32x4*>(stl + QT + rb);
+      const f32x4 l1 = *reinterpret_cast<const f32x4*>(stl + QT + rb + 4);
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) {
-          sacc[qb] = mfma32<T>(*reinterpret_cast<const u32x4*>(qrows + qb * 32 * C::RS + ks * 32), kreg[ks], sacc[qb]);
-          pacc[qb] = mfma32<T>(*reinterpret_cast<const u32x4*>(drows + qb * 32 * C::RS + ks * 32), vreg[ks], pacc[qb]);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);  // keep the phases' live ranges apart
-      const float* lse_l = reinterpret_cast<const float*>(st + C::OFF_LSE);
-      const float* del_l = reinterpret_cast<const float*>(st + C::OFF_DEL);
-#pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int rbase = qb * 32 + hh * 16 + g * 8;  // tile rows of accumulators [8hh, 8hh+8)
-          const f32x4 l0 = *reinterpret_cast<const f32x4*>(lse_l + rbase);
-          const f32x4 l1 = *reinterpret_cast<const f32x4*>(lse_l + rbase + 4);
-          const f32x4 d0 = *reinterpret_cast<const f32x4*>(del_l + rbase);
-          const f32x4 d1 = *reinterpret_cast<const f32x4*>(del_l + rbase + 4);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int i = 8 * hh + j;
-            const float lv = j < 4 ? l0[j] : l1[j - 4];
-            const float dv = j < 4 ? d0[j] : d1[j - 4];
-            float p = fast_exp2(sacc[qb][i] * a.c2 - lv);
-            bool live = true;
-            if (cut) {
-              const int64_t qq = q0 + rbase + j;
-              const int64_t dd = static_cast<int64_t>(krow) - qq;
-              if (qq >= T_ || krow >= S_) {
-                live = false;
-                p = 0.f;
-              } else if (a.masked && (dd < a.band_lo || dd > a.band_hi)) {
-                live = false;
-                p = reinterpret_cast<const float*>(st + C::OFF_PM)[rbase + j];
-              }
-            }
-            sacc[qb][i] = p;
-            pacc[qb][i] = live ? p * (pacc[qb][i] - dv) : 0.f;
+      for (int j = 0; j < 8; ++j) {
+        const int i = 8 * hh + j;
+        const float lv = j < 4 ? l0[j] : l1[j - 4];
+        const float dv = j < 4 ? d0[j] : d1[j - 4];
+        float p = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lv));
+        float ds = p * (pacc[i] - dv);
+        if (cut) {
+          const int64_t qq = q0 + rb + j;
+          const int64_t dd = static_cast<int64_t>(krow) - qq;
+          if (qq >= T_ || krow >= S_) {
+            p = 0.f;
+            ds = 0.f;
+          } else if (a.masked && (dd < a.band_lo || dd > a.band_hi)) {
+            p = stl[2 * QT + rb + j];  // the row's masked-score probability (0 unless fully masked)
+            ds = 0.f;
           }
         }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      const unsigned char* dot_l = st + C::OFF_DOT + r32 * C::TS + g * 16;
-      const unsigned char* qt_l = st + C::OFF_QT + r32 * C::TS + g * 16;
-#pragma unroll
-      for (int s = 0; s < QT / 16; ++s) {
-        const u32x4 pp = pack8<T>(sacc[s >> 1], s & 1);
-        const u32x4 ds = pack8<T>(pacc[s >> 1], s & 1);
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
-          dvacc[db] = mfma32<T>(*reinterpret_cast<const u32x4*>(dot_l + db * 32 * C::TS + s * 32), pp, dvacc[db]);
-          dkacc[db] = mfma32<T>(*reinterpret_cast<const u32x4*>(qt_l + db * 32 * C::TS + s * 32), ds, dkacc[db]);
-        }
+        sacc[i] = p;
+        pacc[i] = ds;
       }
     }
-    if (more) stage_in(smem + ((qt + 1 - qt_lo) & 1) * C::STAGE);
+    const u32x4 p0 = pack8<T>(sacc, 0), p1 = pack8<T>(sacc, 1);
+    const u32x4 s0 = pack8<T>(pacc, 0), s1 = pack8<T>(pacc, 1);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      dvacc[db] = mfma32<T>(ol.tr_frag(o_l, 0, db), p0, dvacc[db]);
+      dvacc[db] = mfma32<T>(ol.tr_frag(o_l, 1, db), p1, dvacc[db]);
+      dkacc[db] = mfma32<T>(ql.tr_frag(q_l, 0, db), s0, dkacc[db]);
+      dkacc[db] = mfma32<T>(ql.tr_frag(q_l, 1, db), s1, dkacc[db]);
+    }
+    __builtin_amdgcn_s_setprio(0);
   }
+  wait_vmcnt0();
 
   if (krow < S_) {
     store_rows_t<T, D>(a.dk + b * a.k_sb + h * a.k_sh + static_cast<int64_t>(kw0) * a.k_st, a.k_st, r32, g, dkacc,
@@ -361,144 +474,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BwdArgs a) {
     store_rows_t<T, D>(a.dv + b * a.v_sb + h * a.v_sh + static_cast<int64_t>(kw0) * a.v_st, a.v_st, r32, g, dvacc,
                        1.0f);
   }
-}
-
-// -------------------------------------------------------------------- dQ
-
-template <int D>
-struct DqCfg {
-  static constexpr int BM = 128;  // query rows per workgroup
-  static constexpr int BN = 64;   // keys per tile
-  static constexpr int RS = D * 2 + 16;
-  static constexpr int TS = BN * 2 + 16;
-  static constexpr int KR = BN * RS;
-  static constexpr int OFF_V = KR, OFF_KT = 2 * KR;
-  static constexpr int STAGE = 2 * KR + D * TS;
-  static constexpr int LDS = 2 * STAGE;
-};
-
-template <typename T, int D>
-__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void bwd_dq(BwdArgs a) {
-  using C = DqCfg<D>;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
-  const int64_t inst = blockIdx.x / a.nblk;
-  const int qb = a.nblk - 1 - static_cast<int>(blockIdx.x % a.nblk);  // heavy (late) blocks first
-  const int64_t b = inst / a.heads, h = inst % a.heads;
-  const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-  const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-  const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
-  const uint16_t* dop = a.dout + b * a.o_sb + h * a.o_sh;
-  const int64_t T_ = a.t, S_ = a.s;
-  const int q0 = qb * C::BM;
-  const int qw0 = q0 + 32 * w;
-  const int qrow = qw0 + r32;
-
-  u32x4 qreg[D / 16], doreg[D / 16];
-  {
-    const uint32_t qoff = static_cast<uint32_t>(r32 * a.q_st * 2 + g * 16);
-    const uint32_t ooff = static_cast<uint32_t>(r32 * a.o_st * 2 + g * 16);
-    const uint16_t* qbs = qp + static_cast<int64_t>(qw0) * a.q_st;
-    const uint16_t* obs = dop + static_cast<int64_t>(qw0) * a.o_st;
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      qreg[ks] = qrow < T_ ? gload<u32x4>(qbs + ks * 16, qoff) : u32x4{0u, 0u, 0u, 0u};
-      doreg[ks] = qrow < T_ ? gload<u32x4>(obs + ks * 16, ooff) : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  const int64_t srow = inst * T_ + qrow;
-  const float dl = qrow < T_ ? a.ws[srow] : 0.f;
-  const float lse2 = qrow < T_ ? a.ws[a.rows + srow] : 0.f;
-
-  const int ntiles = static_cast<int>((S_ + C::BN - 1) / C::BN);
-  int kt_lo = 0, kt_hi = ntiles;
-  if (a.masked && a.prune) {
-    const int64_t qlast = (q0 + C::BM - 1 < T_ ? q0 + C::BM - 1 : T_ - 1);
-    if (a.band_hi < INT64_MAX / 4) {
-      const int64_t smax = qlast + a.band_hi;
-      kt_hi = smax < 0 ? 0 : static_cast<int>(smax / C::BN + 1 < ntiles ? smax / C::BN + 1 : ntiles);
-    }
-    if (a.band_lo > INT64_MIN / 4) {
-      const int64_t smin = q0 + a.band_lo;
-      kt_lo = smin <= 0 ? 0 : static_cast<int>(smin / C::BN);
-    }
-  }
-
-  f32x16 dqacc[D / 32];
-#pragma unroll
-  for (int db = 0; db < D / 32; ++db) dqacc[db] = f32x16{};
-
-  TileT<64, D> tk, tv;
-  auto fetch = [&](int kt) {
-    const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
-    tload<64, D>(tk, kp + key0 * a.k_st, a.k_st, S_ - key0, tid);
-    tload<64, D>(tv, vp + key0 * a.v_st, a.v_st, S_ - key0, tid);
-  };
-  auto stage_in = [&](unsigned char* st) {
-    tstore_rows<64, D>(tk, st, C::RS, tid);
-    tstore_rows<64, D>(tv, st + C::OFF_V, C::RS, tid);
-    tstore_trans<64, D>(tk, st + C::OFF_KT, C::TS, tid);
-  };
-
-  if (kt_lo < kt_hi) {
-    fetch(kt_lo);
-    stage_in(smem);
-  }
-  for (int kt = kt_lo; kt < kt_hi; ++kt) {
-    __syncthreads();
-    unsigned char* st = smem + ((kt - kt_lo) & 1) * C::STAGE;
-    const bool more = kt + 1 < kt_hi;
-    if (more) fetch(kt + 1);
-
-    const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
-    const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + C::BN - 1 - qw0;
-    bool dead = false, cut = key0 + C::BN > S_ || qw0 + 32 > T_;
-    if (a.masked) {
-      dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
-      cut = cut || dmin < a.band_lo || dmax > a.band_hi;
-    }
-    if (!dead) {
-      f32x16 sacc[2] = {f32x16{}, f32x16{}}, pacc[2] = {f32x16{}, f32x16{}};
-      const unsigned char* krows = st + r32 * C::RS + g * 16;
-      const unsigned char* vrows = st + C::OFF_V + r32 * C::RS + g * 16;
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          sacc[kb] = mfma32<T>(*reinterpret_cast<const u32x4*>(krows + kb * 32 * C::RS + ks * 32), qreg[ks], sacc[kb]);
-          pacc[kb] = mfma32<T>(*reinterpret_cast<const u32x4*>(vrows + kb * 32 * C::RS + ks * 32), doreg[ks], pacc[kb]);
-        }
-      }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float p = fast_exp2(sacc[kb][i] * a.c2 - lse2);
-          bool live = true;
-          if (cut) {
-            const int64_t key = key0 + kb * 32 + acc_row(i, g);
-            const int64_t dd = key - qrow;
-            if (key >= S_ || qrow >= T_ || (a.masked && (dd < a.band_lo || dd > a.band_hi))) live = false;
-          }
-          pacc[kb][i] = live ? p * (pacc[kb][i] - dl) : 0.f;
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      const unsigned char* kt_l = st + C::OFF_KT + r32 * C::TS + g * 16;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x4 ds = pack8<T>(pacc[s >> 1], s & 1);
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db)
-          dqacc[db] = mfma32<T>(*reinterpret_cast<const u32x4*>(kt_l + db * 32 * C::TS + s * 32), ds, dqacc[db]);
-      }
-    }
-    if (more) stage_in(smem + ((kt + 1 - kt_lo) & 1) * C::STAGE);
-  }
-
-  if (qrow < T_)
-    store_rows_t<T, D>(a.dq + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(qw0) * a.q_st, a.q_st, r32, g, dqacc,
-                       a.scale);
 }
 
 bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
@@ -510,26 +485,29 @@ bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
 
 template <typename T, int D>
 int launch_bwd(BwdArgs a, int64_t ninst, hipStream_t st) {
-  bwd_stats<T, D><<<dim3(static_cast<unsigned>((a.rows + 3) / 4)), 256, 0, st>>>(a);
+  constexpr int RPB = 4 * (64 / (D / 8));  // rows per stats workgroup
+  bwd_stats<T, D><<<dim3(static_cast<unsigned>((a.rows + RPB - 1) / RPB)), 256, 0, st>>>(a);
   int rc = check_launch("pdh_flash_bwd (row stats)");
   if (rc) return rc;
+  constexpr int TB = Tile32<D>::BYTES;
   {
-    using C = DkdvCfg<D>;
     BwdArgs ak = a;
-    ak.nblk = static_cast<int>((a.s + C::KB - 1) / C::KB);
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_dkdv<T, D>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                        C::LDS);
-    bwd_dkdv<T, D><<<dim3(static_cast<unsigned>(ninst * ak.nblk)), 256, C::LDS, st>>>(ak);
+    ak.nblk = static_cast<int>((a.s + 127) / 128);
+    const int64_t nblk = ninst * ak.nblk;
+    PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_flash_bwd: grid too large");
+    ak.xcd_remap = nblk % 8 == 0;
+    constexpr int lds = 4 * TB + 2 * 3 * 32 * 4;
+    bwd_dkdv<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, lds, st>>>(ak);
     rc = check_launch("pdh_flash_bwd (dk, dv)");
     if (rc) return rc;
   }
   {
-    using C = DqCfg<D>;
     BwdArgs aq = a;
-    aq.nblk = static_cast<int>((a.t + C::BM - 1) / C::BM);
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_dq<T, D>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                        C::LDS);
-    bwd_dq<T, D><<<dim3(static_cast<unsigned>(ninst * aq.nblk)), 256, C::LDS, st>>>(aq);
+    aq.nblk = static_cast<int>((a.t + 127) / 128);
+    const int64_t nblk = ninst * aq.nblk;
+    PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_flash_bwd: grid too large");
+    aq.xcd_remap = nblk % 8 == 0;
+    bwd_dq<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, 4 * TB, st>>>(aq);
     rc = check_launch("pdh_flash_bwd (dq)");
   }
   return rc;
@@ -567,6 +545,11 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
   PDH_REQUIRE(G.q_st < (1 << 24) && G.k_st < (1 << 24) && G.v_st < (1 << 24) && G.o_st < (1 << 24), PDH_EINVAL,
               "pdh_flash_bwd: row strides must be < 2^24 elements");
   PDH_REQUIRE(G.t <= INT32_MAX / 2 && G.s <= INT32_MAX / 2, PDH_EINVAL, "pdh_flash_bwd: sequence too long");
+  PDH_REQUIRE(G.s * G.k_st * 2 < INT32_MAX && G.s * G.v_st * 2 < INT32_MAX && G.t * G.q_st * 2 < INT32_MAX &&
+                  G.t * G.o_st * 2 < INT32_MAX,
+              PDH_EINVAL, "pdh_flash_bwd: one instance's rows must span < 2 GiB");
+  PDH_REQUIRE(G.batch * G.heads_q * G.t * 12 < INT32_MAX, PDH_EINVAL,
+              "pdh_flash_bwd: the row-statistics workspace must span < 2 GiB");
   const int64_t ninst = G.batch * G.heads_q;
   if (ninst == 0 || G.t == 0) return PDH_OK;
   const int masked = mask_kind == PDH_MASK_BAND;
@@ -575,7 +558,7 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
             static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), lse, m_in, den_in,
             static_cast<uint16_t*>(dq), static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv), ws,
             ninst * G.t, G.heads_q, G.t, G.s, G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st,
-            G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi, prune_ok, 0};
+            G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi, prune_ok, 0, 0};
   hipStream_t st = as_stream(stream);
   if (dtype == PDH_BF16)
     return G.e == 128 ? launch_bwd<__hip_bfloat16, 128>(a, ninst, st) : launch_bwd<__hip_bfloat16, 64>(a, ninst, st);
