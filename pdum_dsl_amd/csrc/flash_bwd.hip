@@ -49,7 +49,8 @@ struct BwdArgs {
   int masked;
   int64_t band_lo, band_hi;
   int prune;
-  int nblk;  // blocks per instance (query blocks for dq, key blocks for dkdv)
+  int ninst;          // batch * heads
+  int nkblk, nqblk;   // 128-key blocks (dK, dV) and 128-query blocks (dQ) per instance
   int xcd_remap;
 };
 
@@ -178,18 +179,12 @@ struct TileLane {
 //   dQ^T += K^T dS^T                 (A = K transposed from LDS)
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, D == 64 ? 3 : 2) void bwd_dq(BwdArgs a) {
+__device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char* smem) {  // smem: K[2], V[2]
   using TT = Tile32<D>;
   constexpr int KS = TT::KS, DB = TT::DB, BM = 128, BN = 32;
-  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];  // K[2], V[2]
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
-  int bid = blockIdx.x;
-  if (a.xcd_remap) {
-    const int per = gridDim.x >> 3;
-    bid = (bid & 7) * per + (bid >> 3);
-  }
-  const int64_t inst = bid / a.nblk;
-  const int qb = a.nblk - 1 - (bid % a.nblk);  // heavy (late) query blocks first
+  const int64_t inst = bid / a.nqblk;
+  const int qb = a.nqblk - 1 - (bid % a.nqblk);  // heavy (late) query blocks first
   const int64_t b = inst / a.heads, h = inst % a.heads;
   const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
   const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
@@ -317,19 +312,13 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void bwd_dq(BwdArgs a) {
 //   dV^T += dO^T P, dK^T += Q^T dS   (A = dO / Q transposed from LDS)
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_dkdv(BwdArgs a) {
+__device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned char* smem) {  // Q[2], dO[2], stats[2]
   using TT = Tile32<D>;
   constexpr int KS = TT::KS, DB = TT::DB, BK = 128, QT = 32;
   constexpr int STATB = 4 * TT::BYTES;  // [2][delta | lse2 | pm] x 32 floats
-  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];  // Q[2], dO[2], stats[2]
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
-  int bid = blockIdx.x;
-  if (a.xcd_remap) {
-    const int per = gridDim.x >> 3;
-    bid = (bid & 7) * per + (bid >> 3);
-  }
-  const int64_t inst = bid / a.nblk;
-  const int kblk = bid % a.nblk;  // early key blocks see the most queries under causal masks: launched first
+  const int64_t inst = bid / a.nkblk;
+  const int kblk = bid % a.nkblk;  // early key blocks see the most queries under causal masks: launched first
   const int64_t b = inst / a.heads, h = inst % a.heads;
   const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
   const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
@@ -476,6 +465,33 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_dkdv(BwdArgs a) {
   }
 }
 
+// dK/dV and dQ blocks share one launch (they depend only on the row
+// statistics): logical blocks alternate between the two roles so the heavy
+// causal blocks of both go first and each fills the other's tail.
+template <typename T, int D>
+__global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_main(BwdArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  int bid = blockIdx.x;
+  if (a.xcd_remap) {  // consecutive logical blocks (one instance's) share an XCD's L2
+    const int per = gridDim.x >> 3;
+    bid = (bid & 7) * per + (bid >> 3);
+  }
+  const int nk = a.ninst * a.nkblk, nq = a.ninst * a.nqblk;
+  const int both = 2 * (nk < nq ? nk : nq);
+  int role, idx;
+  if (bid < both) {
+    role = bid & 1;
+    idx = bid >> 1;
+  } else {
+    role = nk > nq ? 0 : 1;
+    idx = both / 2 + (bid - both);
+  }
+  if (role == 0)
+    bwd_dkdv<T, D>(a, idx, smem);
+  else
+    bwd_dq<T, D>(a, idx, smem);
+}
+
 bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
   if (lo > hi) return true;
   if (hi < 0) return true;
@@ -484,33 +500,17 @@ bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
 }
 
 template <typename T, int D>
-int launch_bwd(BwdArgs a, int64_t ninst, hipStream_t st) {
+int launch_bwd(BwdArgs a, hipStream_t st) {
   constexpr int RPB = 4 * (64 / (D / 8));  // rows per stats workgroup
   bwd_stats<T, D><<<dim3(static_cast<unsigned>((a.rows + RPB - 1) / RPB)), 256, 0, st>>>(a);
   int rc = check_launch("pdh_flash_bwd (row stats)");
   if (rc) return rc;
   constexpr int TB = Tile32<D>::BYTES;
-  {
-    BwdArgs ak = a;
-    ak.nblk = static_cast<int>((a.s + 127) / 128);
-    const int64_t nblk = ninst * ak.nblk;
-    PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_flash_bwd: grid too large");
-    ak.xcd_remap = nblk % 8 == 0;
-    constexpr int lds = 4 * TB + 2 * 3 * 32 * 4;
-    bwd_dkdv<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, lds, st>>>(ak);
-    rc = check_launch("pdh_flash_bwd (dk, dv)");
-    if (rc) return rc;
-  }
-  {
-    BwdArgs aq = a;
-    aq.nblk = static_cast<int>((a.t + 127) / 128);
-    const int64_t nblk = ninst * aq.nblk;
-    PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_flash_bwd: grid too large");
-    aq.xcd_remap = nblk % 8 == 0;
-    bwd_dq<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, 4 * TB, st>>>(aq);
-    rc = check_launch("pdh_flash_bwd (dq)");
-  }
-  return rc;
+  constexpr int lds = 4 * TB + 2 * 3 * 32 * 4;  // the larger of the two roles' needs (dK/dV)
+  const int64_t nblk = static_cast<int64_t>(a.ninst) * (a.nkblk + a.nqblk);
+  a.xcd_remap = nblk % 8 == 0;
+  bwd_main<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, lds, st>>>(a);
+  return check_launch("pdh_flash_bwd (dk, dv, dq)");
 }
 
 }  // namespace
@@ -548,6 +548,8 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
   PDH_REQUIRE(G.s * G.k_st * 2 < INT32_MAX && G.s * G.v_st * 2 < INT32_MAX && G.t * G.q_st * 2 < INT32_MAX &&
                   G.t * G.o_st * 2 < INT32_MAX,
               PDH_EINVAL, "pdh_flash_bwd: one instance's rows must span < 2 GiB");
+  PDH_REQUIRE(G.batch * G.heads_q * ((G.s + 127) / 128 + (G.t + 127) / 128) < INT32_MAX / 2, PDH_EINVAL,
+              "pdh_flash_bwd: grid too large");
   PDH_REQUIRE(G.batch * G.heads_q * G.t * 12 < INT32_MAX, PDH_EINVAL,
               "pdh_flash_bwd: the row-statistics workspace must span < 2 GiB");
   const int64_t ninst = G.batch * G.heads_q;
@@ -558,9 +560,10 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
             static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), lse, m_in, den_in,
             static_cast<uint16_t*>(dq), static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv), ws,
             ninst * G.t, G.heads_q, G.t, G.s, G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st,
-            G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi, prune_ok, 0, 0};
+            G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi, prune_ok,
+            static_cast<int>(ninst), static_cast<int>((G.s + 127) / 128), static_cast<int>((G.t + 127) / 128), 0};
   hipStream_t st = as_stream(stream);
   if (dtype == PDH_BF16)
-    return G.e == 128 ? launch_bwd<__hip_bfloat16, 128>(a, ninst, st) : launch_bwd<__hip_bfloat16, 64>(a, ninst, st);
-  return G.e == 128 ? launch_bwd<_Float16, 128>(a, ninst, st) : launch_bwd<_Float16, 64>(a, ninst, st);
+    return G.e == 128 ? launch_bwd<__hip_bfloat16, 128>(a, st) : launch_bwd<__hip_bfloat16, 64>(a, st);
+  return G.e == 128 ? launch_bwd<_Float16, 128>(a, st) : launch_bwd<_Float16, 64>(a, st);
 }
