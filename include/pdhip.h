@@ -131,7 +131,9 @@ int pdh_flash_fwd(const void* q, const void* k, const void* v, void* o, float* m
  * dout / dq share o / q's strides; dk / dv share k / v's strides.
  * ws: fp32 workspace of 3*batch*heads_q*t elements (delta, log2-domain
  * statistic, masked-entry probability per row; written).
- * dtype PDH_BF16 / PDH_F16 with e == od in {64, 128}; heads_q == heads_kv. */
+ * dtype PDH_BF16 / PDH_F16: MFMA kernels, e == od in {64, 128}, 16-byte
+ * aligned tensors, strides multiples of 8 elements. PDH_F32: the fp32 column
+ * (VALU), any 1 <= e, od <= 512. heads_q == heads_kv. */
 int pdh_flash_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
                   const float* lse, const float* m_in, const float* den_in, void* dq, void* dk, void* dv,
                   float* ws, const pdh_attn_geom* geom, int dtype, float scale, float fill,

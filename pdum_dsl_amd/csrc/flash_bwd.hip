@@ -492,6 +492,159 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_main(BwdArgs a) {
     bwd_dq<T, D>(a, idx, smem);
 }
 
+// ---------------------------------------------------------------- fp32 column
+//
+// The fp32 backward (any e, od <= 512): the column the reference's f32 runner
+// occupies for the backward carves (conformance/triton_tile.py). VALU only,
+// one wave per row: bwd_rows_f32<0> owns a query row (dQ), <1> a key row
+// (dK, dV); keys / queries in chunks of 64, one per lane. Row statistics come
+// from the same workspace layout as the 16-bit path (delta, lse2, pm).
+
+struct GenBwdArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* o;
+  const float* dout;
+  const float* lse;
+  const float* m_in;
+  const float* den_in;
+  float* dq;
+  float* dk;
+  float* dv;
+  float* ws;
+  int64_t rows, heads, t, s, e, od;
+  int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
+  float scale, c2, fill2;
+  int masked;
+  int64_t band_lo, band_hi;
+  int prune;
+};
+
+constexpr int kGenPerLane = 8;  // e, od <= 512 held in registers
+
+__global__ __launch_bounds__(256) void bwd_stats_f32(GenBwdArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int64_t inst = row / a.t, tq = row % a.t;
+  const int64_t b = inst / a.heads, h = inst % a.heads;
+  const float* orow = a.o + b * a.o_sb + h * a.o_sh + tq * a.o_st;
+  const float* drow = a.dout + b * a.o_sb + h * a.o_sh + tq * a.o_st;
+  float acc = 0.f;
+  for (int64_t d = lane; d < a.od; d += 64) acc = __builtin_fmaf(orow[d], drow[d], acc);
+  acc = wave_sum(acc);
+  if (lane == 0) {
+    float lse2, pm = 0.f;
+    if (a.m_in != nullptr) {
+      const float m2 = a.m_in[row] * kLog2e, den = a.den_in[row];
+      lse2 = m2 + __log2f(den);
+      if (a.masked) pm = fast_exp2(a.fill2 - m2) / den;
+    } else {
+      lse2 = a.lse[row] * kLog2e;
+      if (a.masked) pm = (lse2 - a.fill2 < 64.f) ? 1.0f / static_cast<float>(a.s) : fast_exp2(a.fill2 - lse2);
+    }
+    a.ws[row] = acc;
+    a.ws[a.rows + row] = lse2;
+    a.ws[2 * a.rows + row] = pm;
+  }
+}
+
+// ROLE 0: wave per query row (dQ); ROLE 1: wave per key row (dK, dV).
+template <int ROLE>
+__global__ __launch_bounds__(256) void bwd_rows_f32(GenBwdArgs a, int64_t nrows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t grow = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (grow >= nrows) return;
+  const int64_t len = ROLE == 0 ? a.t : a.s;  // rows per instance of the owned side
+  const int64_t inst = grow / len, r = grow % len;
+  const int64_t b = inst / a.heads, h = inst % a.heads;
+  const float* qp = a.q + b * a.q_sb + h * a.q_sh;
+  const float* kp = a.k + b * a.k_sb + h * a.k_sh;
+  const float* vp = a.v + b * a.v_sb + h * a.v_sh;
+  const float* dop = a.dout + b * a.o_sb + h * a.o_sh;
+  const float* delp = a.ws + inst * a.t;
+  const float* lsep = a.ws + a.rows + inst * a.t;
+  const float* pmp = a.ws + 2 * a.rows + inst * a.t;
+  const int64_t other = ROLE == 0 ? a.s : a.t;  // the swept side
+  // swept range: live pairs satisfy band_lo <= key - query <= band_hi
+  int64_t lo = 0, hi = other;
+  if (a.masked && a.prune) {
+    if (ROLE == 0) {
+      if (a.band_lo > INT64_MIN / 4) lo = r + a.band_lo > 0 ? r + a.band_lo : 0;
+      if (a.band_hi < INT64_MAX / 4) hi = r + a.band_hi + 1 < other ? r + a.band_hi + 1 : other;
+    } else {
+      if (a.band_hi < INT64_MAX / 4) lo = r - a.band_hi > 0 ? r - a.band_hi : 0;
+      if (a.band_lo > INT64_MIN / 4) hi = r - a.band_lo + 1 < other ? r - a.band_lo + 1 : other;
+    }
+    if (hi < lo) hi = lo;
+  }
+  float acc0[kGenPerLane], acc1[kGenPerLane];  // dq | dk, dv
+#pragma unroll
+  for (int j = 0; j < kGenPerLane; ++j) acc0[j] = acc1[j] = 0.f;
+  for (int64_t c0 = lo - (lo % 64); c0 < hi; c0 += 64) {
+    const int64_t x = c0 + lane;  // this lane's key (ROLE 0) or query (ROLE 1)
+    const int64_t tq = ROLE == 0 ? r : x, sk = ROLE == 0 ? x : r;
+    float p = 0.f, ds = 0.f;
+    if (x >= lo && x < hi) {
+      const float* qr = qp + tq * a.q_st;
+      const float* kr = kp + sk * a.k_st;
+      const float* vr = vp + sk * a.v_st;
+      const float* dr = dop + tq * a.o_st;
+      float sc = 0.f, dp = 0.f;
+      for (int64_t e = 0; e < a.e; ++e) sc = __builtin_fmaf(qr[e], kr[e], sc);
+      for (int64_t o = 0; o < a.od; ++o) dp = __builtin_fmaf(dr[o], vr[o], dp);
+      const int64_t d = sk - tq;
+      if (a.masked && (d < a.band_lo || d > a.band_hi)) {
+        p = pmp[tq];  // masked score: the row's masked-entry probability, no gradient
+      } else {
+        p = fast_exp2(__builtin_fmaf(sc, a.c2, -lsep[tq]));
+        ds = p * (dp - delp[tq]);
+      }
+    }
+    const int64_t n = (hi - c0) < 64 ? (hi - c0) : 64;
+    for (int kk = 0; kk < n; ++kk) {
+      const float pk = __shfl(p, kk, 64), dk_ = __shfl(ds, kk, 64);
+      const int64_t xx = c0 + kk;
+      if (xx < lo) continue;
+      if (ROLE == 0) {  // dq_r += ds_(r, key xx) k_xx
+        const float* kr = kp + xx * a.k_st;
+#pragma unroll
+        for (int j = 0; j < kGenPerLane; ++j) {
+          const int64_t e = j * 64 + lane;
+          if (e < a.e) acc0[j] = __builtin_fmaf(dk_, kr[e], acc0[j]);
+        }
+      } else {  // dk_r += ds_(query xx, r) q_xx ; dv_r += p_(xx, r) dO_xx
+        const float* qr = qp + xx * a.q_st;
+        const float* dr = dop + xx * a.o_st;
+#pragma unroll
+        for (int j = 0; j < kGenPerLane; ++j) {
+          const int64_t e = j * 64 + lane;
+          if (e < a.e) acc0[j] = __builtin_fmaf(dk_, qr[e], acc0[j]);
+          if (e < a.od) acc1[j] = __builtin_fmaf(pk, dr[e], acc1[j]);
+        }
+      }
+    }
+  }
+  if (ROLE == 0) {
+    float* out = a.dq + b * a.q_sb + h * a.q_sh + r * a.q_st;
+#pragma unroll
+    for (int j = 0; j < kGenPerLane; ++j) {
+      const int64_t e = j * 64 + lane;
+      if (e < a.e) out[e] = acc0[j] * a.scale;
+    }
+  } else {
+    float* ok = a.dk + b * a.k_sb + h * a.k_sh + r * a.k_st;
+    float* ov = a.dv + b * a.v_sb + h * a.v_sh + r * a.v_st;
+#pragma unroll
+    for (int j = 0; j < kGenPerLane; ++j) {
+      const int64_t e = j * 64 + lane;
+      if (e < a.e) ok[e] = acc0[j] * a.scale;
+      if (e < a.od) ov[e] = acc1[j];
+    }
+  }
+}
+
 bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
   if (lo > hi) return true;
   if (hi < 0) return true;
@@ -528,13 +681,39 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
   PDH_REQUIRE(G.heads_q == G.heads_kv, PDH_EUNSUPPORTED,
               "pdh_flash_bwd: grouped-query backward (heads_q %lld != heads_kv %lld) is not supported",
               (long long)G.heads_q, (long long)G.heads_kv);
-  PDH_REQUIRE(dtype == PDH_BF16 || dtype == PDH_F16, PDH_EUNSUPPORTED, "pdh_flash_bwd: dtype must be bf16 or f16");
-  PDH_REQUIRE(G.e == G.od && (G.e == 64 || G.e == 128), PDH_EUNSUPPORTED,
-              "pdh_flash_bwd: need e == od in {64, 128} (got %lld, %lld)", (long long)G.e, (long long)G.od);
   PDH_REQUIRE(mask_kind == PDH_MASK_NONE || mask_kind == PDH_MASK_BAND, PDH_EINVAL,
               "pdh_flash_bwd: unknown mask kind %d", mask_kind);
   PDH_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && ws, PDH_EINVAL, "pdh_flash_bwd: null pointer");
   PDH_REQUIRE((m_in == nullptr) == (den_in == nullptr), PDH_EINVAL, "pdh_flash_bwd: pass both m and den, or neither");
+  if (dtype == PDH_F32) {
+    PDH_REQUIRE(G.e >= 1 && G.od >= 1 && G.e <= 64 * kGenPerLane && G.od <= 64 * kGenPerLane, PDH_EUNSUPPORTED,
+                "pdh_flash_bwd: fp32 needs 1 <= e, od <= %d (got %lld, %lld)", 64 * kGenPerLane, (long long)G.e,
+                (long long)G.od);
+    const int64_t ninst = G.batch * G.heads_q;
+    if (ninst == 0 || G.t == 0) return PDH_OK;
+    PDH_REQUIRE((ninst * G.t + 3) / 4 <= INT32_MAX && (ninst * G.s + 3) / 4 <= INT32_MAX, PDH_EINVAL,
+                "pdh_flash_bwd: too many rows");
+    const int masked = mask_kind == PDH_MASK_BAND;
+    GenBwdArgs ga{static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+                  static_cast<const float*>(o), static_cast<const float*>(dout), lse, m_in, den_in,
+                  static_cast<float*>(dq), static_cast<float*>(dk), static_cast<float*>(dv), ws, ninst * G.t,
+                  G.heads_q, G.t, G.s, G.e, G.od, G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh,
+                  G.v_st, G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi,
+                  masked && !band_has_empty_row(G.t, G.s, band_lo, band_hi)};
+    hipStream_t st = as_stream(stream);
+    bwd_stats_f32<<<dim3(static_cast<unsigned>((ga.rows + 3) / 4)), 256, 0, st>>>(ga);
+    int rc = check_launch("pdh_flash_bwd (fp32 row stats)");
+    if (rc) return rc;
+    bwd_rows_f32<0><<<dim3(static_cast<unsigned>((ninst * G.t + 3) / 4)), 256, 0, st>>>(ga, ninst * G.t);
+    rc = check_launch("pdh_flash_bwd (fp32 dq)");
+    if (rc) return rc;
+    bwd_rows_f32<1><<<dim3(static_cast<unsigned>((ninst * G.s + 3) / 4)), 256, 0, st>>>(ga, ninst * G.s);
+    return check_launch("pdh_flash_bwd (fp32 dk, dv)");
+  }
+  PDH_REQUIRE(dtype == PDH_BF16 || dtype == PDH_F16, PDH_EINVAL, "pdh_flash_bwd: unknown dtype %d", dtype);
+  PDH_REQUIRE(G.e == G.od && (G.e == 64 || G.e == 128), PDH_EUNSUPPORTED,
+              "pdh_flash_bwd: 16-bit kernels need e == od in {64, 128} (got %lld, %lld)", (long long)G.e,
+              (long long)G.od);
   PDH_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && aligned16(dout) && aligned16(dq) &&
                   aligned16(dk) && aligned16(dv) && aligned16(lse),
               PDH_EINVAL, "pdh_flash_bwd: tensors must be 16-byte aligned");

@@ -14,6 +14,8 @@ Instead of emitting code node by node, the seat RECOGNIZES the tile region
 a fusion template generated and binds it to a hand-written gfx950 kernel:
 
   flash tile (fusion.py:542-615)          -> pdh_flash_fwd (mask forest -> band)
+  flash joint (autodiff.grad of a flash,  -> pdh_flash_fwd with (m, den) artifacts, then
+    claimed whole by partition.plan_model)   pdh_flash_bwd: yields (out, *grads)
   staged row softmax (fusion.py:339-350)  -> pdh_row_softmax
   staged row statistics (layernorm core + gamma/beta epilogue) -> pdh_layernorm
 
@@ -30,7 +32,7 @@ import math
 import numpy as np
 
 from .tl.fusion import FOLD_KW, contract_core, flash_step, forest_is_closed, match_rowstat, match_softmax
-from .tl.ir import Region, walk, walk_deep
+from .tl.ir import Node, Region, walk, walk_deep
 
 HIP_FP = ("tile_hip", "gfx950")
 
@@ -42,9 +44,15 @@ class Untranslatable(Exception):
 # --------------------------------------------------------------- helpers
 
 
-def _carried_dims(region: Region) -> set:
+def _carried_dims(region: Region, root=None) -> set:
+    """Dims a fold scans or a reduce contracts, among the nodes ``root``
+    depends on (the whole region when ``root`` is None), fold steps included."""
+    if root is None:
+        nodes = walk_deep(region)
+    else:
+        nodes = walk_deep(Region(params=region.params, body=(Node("core.yield", root.type, (root,)),)))
     out = set()
-    for n in walk_deep(region):
+    for n in nodes:
         if n.op == "tl.fold":
             out.add(n.attr("dim"))
         if n.op == "tl.reduce":
@@ -59,7 +67,7 @@ def _grid(region: Region, launch: tuple) -> int:
     if y.op == "core.tuple":
         y = y.args[0]
     out_dims = {d.name: d for d in y.type.dims}
-    carried = _carried_dims(region)
+    carried = _carried_dims(region, y)  # what the first output depends on (a joint's grads reduce over t)
     grid = 1
     for name, tile in launch:
         if name not in out_dims:
@@ -284,6 +292,11 @@ def compile_tile_hip(region: Region, launch: tuple = (), prune: tuple = (), *, d
     fb = recognize_flash(region)
     if fb is not None:
         return _flash_runner(region, fb, grid, bool(prune), dtype)
+    from .tl.partition import match_flash_joint
+
+    fj = match_flash_joint(region)
+    if fj is not None:
+        return _flash_joint_runner(region, fj, grid, dtype)
     if dtype != "f32":
         raise Untranslatable(f"row templates run fp32 only (asked {dtype})")
     sb = recognize_softmax(region)
@@ -295,7 +308,7 @@ def compile_tile_hip(region: Region, launch: tuple = (), prune: tuple = (), *, d
     ops = sorted({n.op for n in walk(region)} - {"core.param", "core.yield"})
     raise Untranslatable(
         f"no HIP binding for this tile region (ops: {', '.join(ops)}); bound templates: flash, "
-        "row-normalization, row-statistics"
+        "row-normalization, row-statistics, flash-joint"
     )
 
 
@@ -410,3 +423,58 @@ def _layernorm_runner(region, lb, grid):
     )
     return _finish(run, src, grid, "row-statistics")
 
+
+def _flash_joint_runner(region, fj, grid, dtype):
+    """(out, *grads) of a flash joint: the forward with its (m, den)
+    artifacts, then the fused backward seeded by the joint's last param."""
+    from . import kernels as K
+
+    q_, k_, v_ = fj["q"], fj["k"], fj["v"]
+    t, s, e, o = fj["t"], fj["s"], fj["e"], fj["o"]
+    T, S, E, OD = q_.type.dim(t).size, k_.type.dim(s).size, q_.type.dim(e).size, v_.type.dim(o).size
+    band = mask_to_band(fj["mask"], t, s, T, S)
+    kband = None if band[0] == "none" else K.Band(band[1], band[2])
+    if dtype != "f32" and not (E == OD and E in (64, 128)):
+        raise Untranslatable(f"{dtype} flash joint needs e == od in {{64, 128}} (got {E}, {OD})")
+    iq, ik, iv = (_index(region, x) for x in (q_, k_, v_))
+    iseed = len(region.params) - 1
+    y = region.body[-1].args[0]
+    grad_types = [g.type for g in y.args[1:]]
+    wrt = fj["wrt"]
+    out_names = y.args[0].type.names
+
+    def run(values):
+        torch = _torch()
+        tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+        dev = torch.device("cuda")
+
+        def up(i, node, order, rows, cols):
+            a = np.asarray(values[i], dtype=np.float32)
+            a = np.transpose(a, [node.type.names.index(n) for n in order])
+            return torch.as_tensor(np.ascontiguousarray(a)).to(device=dev, dtype=tdt).view(1, 1, rows, cols)
+
+        q = up(iq, q_, (t, e), T, E)
+        k = up(ik, k_, (s, e), S, E)
+        v = up(iv, v_, (s, o), S, OD)
+        seed_node = region.params[iseed]
+        do = up(iseed, seed_node, (t, o), T, OD)
+        res = K.flash_fwd(q, k, v, scale=1.0, band=kband, fill=fj["fill"], want_artifacts=True)
+        dq, dk, dv = K.flash_bwd(q, k, v, res.o, do, res.lse, m=res.m, den=res.den, scale=1.0, band=kband,
+                                 fill=fj["fill"])
+        torch.cuda.synchronize()
+        host = lambda x, rows, cols: x.view(rows, cols).float().cpu().numpy()  # noqa: E731
+        outs = {"q": (host(dq, T, E), (t, e)), "k": (host(dk, S, E), (s, e)), "v": (host(dv, S, OD), (s, o))}
+        out = host(res.o, T, OD)
+        ys = [np.transpose(out, [(t, o).index(n) for n in out_names])]
+        for nm, gt in zip(wrt, grad_types):
+            arr, order = outs[nm]
+            ys.append(np.transpose(arr, [order.index(n) for n in gt.names]))
+        return tuple(ys)
+
+    kern = "flash_fwd_generic_f32 + bwd_rows_f32" if dtype == "f32" else f"flash_fwd_mfma<{dtype},{E}> + bwd_main<{dtype},{E}>"
+    bdesc = "all" if kband is None else f"band({band[1]},{band[2]})"
+    src = (
+        f"hip:{kern} t={T} s={S} e={E} od={OD} mask={bdesc} fill={fj['fill']:g} wrt={','.join(wrt)} "
+        "artifacts=m,den launches=fwd+bwd"
+    )
+    return _finish(run, src, grid, "flash-joint")

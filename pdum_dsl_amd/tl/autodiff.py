@@ -1,0 +1,269 @@
+"""Reverse-mode AD over a tile-vocabulary region: the joint (target, *grads).
+
+Restates the contract of the reference's ``autodiff.grad``
+(packages/tensorlib/src/pdum/tl/autodiff.py:102-148): a region, the name of
+its target, a SEED (the target's cotangent, a runtime input appended as the
+joint's LAST param) and the names of the inputs to differentiate; the result
+is a ``RegionGrad`` whose joint region yields ``(target, *grads)``.
+
+This is the part of the reference's AD the fusion templates' backward is
+built from (the naive attention twin of zoo/tiles.py:238-252 and the row
+templates), over the vocabulary this backend reads:
+
+  tl.pointwise   the derivative of each numpy marker (dsl/derivative.py's
+                 table restated per marker below)
+  tl.reduce      sum -> broadcast; mean -> broadcast / N;
+                 max / min -> the cotangent split over the positions that
+                 attain the extremum (the reference sends it to the FIRST
+                 such position through a tl.scan, autodiff.py:635-665; the
+                 two agree whenever the extremum is attained once, and in
+                 the softmax chain the extremum's total cotangent is zero
+                 by shift invariance, so either choice leaves q, k, v's
+                 gradients unchanged)
+  tl.repeat_like / tl.repeat   -> sum over the added dims
+  tl.stage       identity
+  core.const / tl.const / tl.iota / comparisons / stop_gradient: no flow
+
+Anything else (fold, split, select, argtopk) refuses by name: a primitive
+joins the AD with its linearization, or not at all.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from .dialect import OPS
+from .ir import F64, Builder, Node, Region, TensorType
+
+# markers through which no gradient flows (piecewise-constant or boolean)
+_FLAT = frozenset({"eq", "ne", "le", "lt", "ge", "gt", "floor", "stop_gradient"})
+
+
+@dataclass(frozen=True)
+class RegionGrad:
+    """The joint region and its naming (autodiff.py:136-148): ``region``
+    yields (target, *grads); ``outputs`` names the yield slots in order;
+    ``grads`` maps each requested input name to its gradient's name (None:
+    no gradient flows); ``names`` maps node ids to names; ``nodes`` maps the
+    yielded names to nodes. The seed is the joint's LAST param."""
+
+    region: Region
+    grads: dict
+    names: dict
+    outputs: tuple
+    nodes: dict
+
+
+def region_names(region: Region, param_names, outputs=("out",)) -> dict:
+    """The naming assignment grad joins on: params by position, then the
+    yielded value(s) (dialect.region_names in the reference)."""
+    if len(param_names) != len(region.params):
+        raise ValueError(f"{len(region.params)} params need {len(region.params)} names, got {len(param_names)}")
+    names = {id(p): nm for p, nm in zip(region.params, param_names)}
+    y = region.body[-1].args[0]
+    ys = y.args if y.op == "core.tuple" else (y,)
+    if len(outputs) != len(ys):
+        raise ValueError(f"{len(ys)} yielded value(s) need {len(ys)} output name(s)")
+    for n, nm in zip(ys, outputs):
+        names[id(n)] = nm
+    return names
+
+
+def _is_tensor(n) -> bool:
+    return isinstance(n.type, TensorType)
+
+
+def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None = None, *, names=None) -> RegionGrad:
+    """Reverse-mode AD of ``region``'s node named ``target`` (autodiff.py:102).
+
+    ``seed`` names the target's cotangent (required for a non-scalar target:
+    reverse mode computes vector-Jacobian products); it becomes the joint's
+    last param. ``wrt`` names the params to differentiate (all params by
+    default)."""
+    if names is None:
+        raise ValueError("grad joins on names — pass names=region_names(region, param_names)")
+    by_name: dict = {}
+    for p in region.params:
+        by_name.setdefault(names[id(p)], p)
+    for n in _ancestors(region.body[-1]):
+        nm = names.get(id(n))
+        if nm is not None:
+            by_name.setdefault(nm, n)
+    if target not in by_name:
+        raise KeyError(f"target {target!r} is not defined by the program")
+    if seed is not None and seed in by_name:
+        raise ValueError(f"seed name {seed!r} collides with a program variable; pick a fresh name")
+    tnode = by_name[target]
+    if wrt is None:
+        wrt = tuple(names[id(p)] for p in region.params)
+    for nm in wrt:
+        if nm not in by_name or by_name[nm].op != "core.param":
+            raise KeyError(f"{nm!r} names no param of the program")
+
+    b = Builder(OPS)
+    const = lambda v: b.emit("core.const", type=F64, value=float(v))  # noqa: E731
+    pw = lambda f, *xs: b.emit("tl.pointwise", *xs, f=f)  # noqa: E731
+    rl = lambda x, like: b.emit("tl.repeat_like", x, like)  # noqa: E731
+
+    if seed is None:
+        if _is_tensor(tnode) and tnode.type.dims:
+            raise ValueError(
+                f"target {target!r} is not a scalar; pass seed= (the name of a runtime input aligned with the "
+                "target) — reverse mode computes vector-Jacobian products"
+            )
+        seed_node = const(1.0)
+        seed_param = None
+    else:
+        seed_param = b.param(("grad.seed",), tnode.type)
+        seed_node = seed_param
+
+    cot: dict[int, list] = {id(tnode): [seed_node]}
+
+    def contribute(n, g):
+        if n.op in ("core.const", "tl.const", "tl.iota"):
+            return
+        cot.setdefault(id(n), []).append(g)
+
+    def total(n):
+        parts = cot.get(id(n))
+        if not parts:
+            return None
+        acc = parts[0]
+        for p in parts[1:]:
+            acc = pw("add", acc, p)
+        return acc
+
+    order = [n for n in _ancestors_of(tnode)]
+    final: dict[int, Node] = {}
+    for n in reversed(order):
+        c = total(n)
+        final[id(n)] = c
+        if c is None or n.op == "core.param":
+            continue
+        op = n.op
+        if op in ("core.const", "tl.const", "tl.iota"):
+            continue
+        if op == "tl.stage":
+            contribute(n.args[0], c)
+        elif op == "tl.pointwise":
+            _pointwise_rule(n, c, contribute, pw, const)
+        elif op == "tl.reduce":
+            x = n.args[0]
+            f = n.attr("f")
+            dims = n.attr("dims")
+            dims = (dims,) if isinstance(dims, str) else tuple(dims)
+            if f == "sum":
+                contribute(x, rl(c, x))
+            elif f == "mean":
+                cnt = 1
+                for d in dims:
+                    cnt *= x.type.dim(d).size
+                contribute(x, rl(pw("div", c, const(cnt)), x))
+            elif f in ("max", "min"):
+                hit = pw("eq", x, rl(n, x))
+                ones = pw("where", hit, const(1.0), const(0.0))
+                share = pw("div", c, b.emit("tl.reduce", ones, dims=dims, f="sum"))
+                contribute(x, pw("where", hit, rl(share, x), const(0.0)))
+            else:
+                raise NotImplementedError(f"tl.reduce {f!r} has no adjoint rule here")
+        elif op == "tl.repeat_like":
+            x, like = n.args
+            added = tuple(d.name for d in like.type.dims if not x.type.has(d.name))
+            contribute(x, b.emit("tl.reduce", c, dims=added, f="sum") if added else c)
+        elif op == "tl.repeat":
+            contribute(n.args[0], b.emit("tl.reduce", c, dims=(n.attr("name"),), f="sum"))
+        else:
+            raise NotImplementedError(
+                f"{op} has no adjoint rule in this build (a primitive joins the AD with its linearization)"
+            )
+
+    grads, nodes = {}, {target: tnode}
+    ys = [tnode]
+    outputs = [target]
+    jnames = dict(names)
+    for nm in wrt:
+        g = final.get(id(by_name[nm]))
+        if g is None:
+            grads[nm] = None
+            continue
+        gname = f"d{nm}"
+        grads[nm] = gname
+        ys.append(g)
+        outputs.append(gname)
+        nodes[gname] = g
+        jnames[id(g)] = gname
+    params = tuple(region.params) + ((seed_param,) if seed_param is not None else ())
+    if seed_param is not None:
+        jnames[id(seed_param)] = seed
+    y = b.emit("core.tuple", *ys) if len(ys) > 1 else ys[0]
+    joint = Region(params=params, body=(b.emit("core.yield", y),))
+    return RegionGrad(joint, grads, jnames, tuple(outputs), nodes)
+
+
+def _pointwise_rule(n, c, contribute, pw, const):
+    f = n.attr("f")
+    A = n.args
+    if f in _FLAT:
+        return
+    if f == "add":
+        for a in A:
+            contribute(a, c)
+    elif f == "sub":
+        contribute(A[0], c)
+        contribute(A[1], pw("neg", c))
+    elif f == "neg":
+        contribute(A[0], pw("neg", c))
+    elif f == "mul":
+        contribute(A[0], pw("mul", c, A[1]))
+        contribute(A[1], pw("mul", c, A[0]))
+    elif f == "div":
+        contribute(A[0], pw("div", c, A[1]))
+        contribute(A[1], pw("neg", pw("div", pw("mul", c, n), A[1])))  # -c a / b^2 = -(c (a/b)) / b
+    elif f == "exp":
+        contribute(A[0], pw("mul", c, n))
+    elif f == "log":
+        contribute(A[0], pw("div", c, A[0]))
+    elif f == "sqrt":
+        contribute(A[0], pw("div", c, pw("mul", n, const(2.0))))
+    elif f == "tanh":
+        contribute(A[0], pw("mul", c, pw("sub", const(1.0), pw("mul", n, n))))
+    elif f == "sin":
+        contribute(A[0], pw("mul", c, pw("cos", A[0])))
+    elif f == "cos":
+        contribute(A[0], pw("neg", pw("mul", c, pw("sin", A[0]))))
+    elif f == "abs":
+        contribute(A[0], pw("where", pw("ge", A[0], const(0.0)), c, pw("neg", c)))
+    elif f in ("maximum", "minimum"):
+        first = pw("ge" if f == "maximum" else "le", A[0], A[1])
+        contribute(A[0], pw("where", first, c, const(0.0)))
+        contribute(A[1], pw("where", first, const(0.0), c))
+    elif f == "where":
+        m, x, y = A
+        contribute(x, pw("where", m, c, const(0.0)))
+        contribute(y, pw("where", m, const(0.0), c))
+    else:
+        raise NotImplementedError(f"marker {f!r} has no entry in the derivative table")
+
+
+def _ancestors_of(root: Node):
+    """Nodes the root depends on, operands before users (each once)."""
+    seen: set[int] = set()
+    out: list = []
+    stack = [(root, False)]
+    while stack:
+        x, done = stack.pop()
+        if done:
+            out.append(x)
+            continue
+        if id(x) in seen:
+            continue
+        seen.add(id(x))
+        stack.append((x, True))
+        for a in reversed(x.args):
+            if id(a) not in seen:
+                stack.append((a, False))
+    return out
+
+
+def _ancestors(yield_node: Node):
+    return _ancestors_of(yield_node)

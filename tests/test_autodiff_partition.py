@@ -1,0 +1,151 @@
+"""autodiff.grad and partition.plan_model (CPU).
+
+The reference's own batteries for these layers are CPU tests against the
+oracle (packages/tensorlib/tests/test_partition.py:124-193: the flash joint
+executes to the naive joint at 1e-9; autodiff tests against numpy / finite
+differences). Here the joint region ``grad`` builds is evaluated by BOTH
+interpreters (the planner's numpy one and the oracle's torch-f64 one) and
+checked against the closed-form gradients (oracle.closed_forms.attention_bwd,
+itself pinned by torch.autograd and finite differences in test_oracle.py),
+and row templates' joints against torch.autograd in float64."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import closed_forms as cf
+from oracle import region_eval as rev
+from pdum_dsl_amd.tl import interp, zoo
+from pdum_dsl_amd.tl.autodiff import grad, region_names
+from pdum_dsl_amd.tl.launch import TileLevel, TileMachine
+from pdum_dsl_amd.tl.partition import match_flash_joint, plan_model
+
+RTX4090 = TileMachine((TileLevel("shared", 128, 101376),))
+MASKS = [("causal", (None, 0)), ("all", None), ("strict", (None, -1)), (("window", 3), (-2, 0))]
+
+
+def _joint(subj, wrt=("q", "k", "v")):
+    names = region_names(subj.region, ("q", "k", "v"), ("out",))
+    return grad(subj.region, "out", seed="dO", wrt=wrt, names=names)
+
+
+@pytest.mark.parametrize("mask,band", MASKS)
+def test_attention_joint_equals_the_closed_form_on_both_interpreters(mask, band):
+    subj = zoo.attention(T=9, S=9, E=5, OD=4, mask=mask, seed=3)
+    rg = _joint(subj)
+    assert rg.outputs == ("out", "dq", "dk", "dv")
+    assert rg.grads == {"q": "dq", "k": "dk", "v": "dv"}
+    dO = np.random.default_rng(0).standard_normal((9, 4))
+    q, k, v = subj.numpy_inputs()
+    wq, wk, wv = cf.attention_bwd(q, k, v, dO, scale=1.0, band=band)
+    wo = cf.attention(q, k, v, scale=1.0, band=band)[0]
+    # planner's numpy interpreter
+    res = interp.run_region(rg.region, subj.inputs + [interp.field(dO, ("t", "o"))])
+    got = [res[0].to_numpy(("t", "o")), res[1].to_numpy(("t", "e")), res[2].to_numpy(("s", "e")),
+           res[3].to_numpy(("s", "o"))]
+    for g, w in zip(got, (wo, wq, wk, wv)):
+        np.testing.assert_allclose(g, w, rtol=1e-9, atol=1e-12)
+    # the oracle's torch-f64 evaluator, independently
+    vals = [rev.value(a, p.type) for a, p in zip([q, k, v, dO], rg.region.params)]
+    res2 = rev.evaluate(rg.region, vals)
+    got2 = [res2[0].numpy(("t", "o")), res2[1].numpy(("t", "e")), res2[2].numpy(("s", "e")), res2[3].numpy(("s", "o"))]
+    for g, w in zip(got2, (wo, wq, wk, wv)):
+        np.testing.assert_allclose(g, w, rtol=1e-9, atol=1e-12)
+
+
+def test_a_partial_wrt_yields_only_those_grads_in_order():
+    subj = zoo.attention(T=6, E=3, OD=2, mask="causal", seed=7)
+    rg = _joint(subj, wrt=("v", "q"))
+    assert rg.outputs == ("out", "dv", "dq")
+    assert len(rg.region.params) == 4 and rg.names[id(rg.region.params[-1])] == "dO"
+
+
+def _autograd_rows(fn, x, extra, seed):
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    ex = [torch.tensor(e, dtype=torch.float64, requires_grad=True) for e in extra]
+    y = fn(xt, *ex)
+    y.backward(torch.tensor(seed, dtype=torch.float64))
+    return [xt.grad.numpy()] + [e.grad.numpy() for e in ex]
+
+
+def test_row_softmax_joint_matches_torch_autograd():
+    subj = zoo.row_softmax(rows=5, cols=7, seed=4)
+    names = region_names(subj.region, ("x",), ("y",))
+    rg = grad(subj.region, "y", seed="dy", names=names)
+    dy = np.random.default_rng(1).standard_normal((5, 7))
+    res = interp.run_region(rg.region, subj.inputs + [interp.field(dy, ("t", "s"))])
+    (want,) = _autograd_rows(lambda x: torch.softmax(x, dim=1), subj.numpy_inputs()[0], [], dy)
+    np.testing.assert_allclose(res[1].to_numpy(("t", "s")), want, rtol=1e-9, atol=1e-12)
+
+
+def test_layernorm_joint_matches_torch_autograd():
+    subj = zoo.layernorm(rows=4, feat=6, seed=2)
+    names = region_names(subj.region, ("x", "g", "b"), ("y",))
+    rg = grad(subj.region, "y", seed="dy", names=names)
+    dy = np.random.default_rng(2).standard_normal((4, 6))
+    res = interp.run_region(rg.region, subj.inputs + [interp.field(dy, ("t", "d"))])
+    x, g, b = subj.numpy_inputs()
+    want = _autograd_rows(
+        lambda x, g, b: torch.nn.functional.layer_norm(x, (6,), g, b, eps=1e-5), x, [g, b], dy
+    )
+    got = [res[1].to_numpy(("t", "d")), res[2].to_numpy(("d",)), res[3].to_numpy(("d",))]
+    for a, w in zip(got, want):
+        np.testing.assert_allclose(a, w, rtol=1e-8, atol=1e-10)
+
+
+def test_grad_refuses_what_it_cannot_linearize():
+    f = zoo.flash_tile(T=6, E=3, OD=2, SI=2, seed=7)
+    names = region_names(f.tile, ("q", "k", "v"), ("out",))
+    with pytest.raises(NotImplementedError, match="tl.fold"):
+        grad(f.tile, "out", seed="dO", names=names)
+    subj = zoo.attention(T=6, E=3, OD=2, seed=7)
+    with pytest.raises(ValueError, match="not a scalar"):
+        grad(subj.region, "out", names=region_names(subj.region, ("q", "k", "v")))
+    with pytest.raises(ValueError, match="collides"):
+        grad(subj.region, "out", seed="q", names=region_names(subj.region, ("q", "k", "v")))
+    with pytest.raises(KeyError, match="not defined"):
+        grad(subj.region, "nope", seed="dO", names=region_names(subj.region, ("q", "k", "v")))
+
+
+# ------------------------------------------------------------ plan_model
+
+
+@pytest.mark.parametrize("wrt", [("q", "k", "v"), ("v", "q"), ("k",)])
+def test_plan_model_claims_the_flash_joint_whole(wrt):
+    subj = zoo.attention(T=128, S=128, E=32, OD=32, mask="causal", seed=3)
+    rg = _joint(subj, wrt)
+    mp = plan_model(rg.region, machine=RTX4090)
+    assert len(mp.carves) == 1 and mp.coverage() == 1.0 and mp.distinct_kernels() == 1
+    g = mp.carves[0].group
+    assert (g.template, g.confidence) == ("flash-joint", "yellow")
+    assert dict(g.params)["wrt"] == wrt and dict(g.params)["forward"] == "flash"
+    assert dict(g.params)["si"] == 32
+    assert g.certificate.verdict == "proved-exact" and g.certificate.licenses == ("flash.online-softmax",)
+    # the forward's launch and mask-derived prune ride along (test_launch.py:114-117's answer)
+    assert g.launch == (("t", 32),)  # smallest t-tile at or above the 1024-element floor
+    assert g.prune == (("so", (0, 0, 1), (1, 1, 1)),)
+    assert g.artifacts == ("m", "den")
+    assert mp.carves[0].root_op == "tl.reduce"
+
+
+def test_a_tampered_joint_is_not_a_flash_joint():
+    subj = zoo.attention(T=8, E=4, OD=4, mask="causal", seed=3)
+    rg = _joint(subj)
+    from pdum_dsl_amd.tl.dialect import OPS
+    from pdum_dsl_amd.tl.ir import F64, Builder, Region
+
+    b = Builder(OPS)
+    y = rg.region.body[-1].args[0]
+    dq2 = b.emit("tl.pointwise", y.args[1], b.emit("core.const", type=F64, value=2.0), f="mul")
+    bad = Region(params=rg.region.params, body=(b.emit("core.yield", b.emit("core.tuple", y.args[0], dq2, *y.args[2:])),))
+    assert match_flash_joint(bad) is None
+    mp = plan_model(bad)
+    assert mp.carves[0].group.template != "flash-joint"
+
+
+def test_plan_model_of_a_single_template_region_is_its_plan_region():
+    for subj, tmpl in ((zoo.row_softmax(), "row-normalization"), (zoo.layernorm(), "row-statistics"),
+                       (zoo.attention(T=8, E=4, OD=4), "flash")):
+        mp = plan_model(subj.region)
+        assert [c.group.template for c in mp.carves] == [tmpl]
+        assert mp.coverage() == 1.0
