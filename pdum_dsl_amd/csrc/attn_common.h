@@ -93,8 +93,8 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // every later LDS read wait for it: callers wait with s_waitcnt vmcnt(0) and a
 // barrier before reading the tile.
 __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
-  const uint32_t m0 =
-      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)lds)));
+  // the low 32 bits of a generic LDS address are its LDS offset (no address-space cast needed)
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: listed so the compiler knows it changes
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0), "v"(voff), "s"(r), "s"(soff)
@@ -107,8 +107,8 @@ __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* lds, uint32_t vof
 // later vector-memory waits of its own.
 // 4 bytes per lane, buffer -> LDS (lane i's dword lands at lds + 4 i).
 __device__ __forceinline__ void dma4(rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
-  const uint32_t m0 =
-      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)lds)));
+  // the low 32 bits of a generic LDS address are its LDS offset (no address-space cast needed)
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(m0), "v"(voff), "s"(r), "s"(soff)

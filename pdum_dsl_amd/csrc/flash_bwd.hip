@@ -247,7 +247,7 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
     const int buf = (kt - kt_lo) & 1;
     wait_vmcnt0();
     __syncthreads();
-    stage(kt + 1, buf ^ 1);  // past the last tile: zeros into the idle buffer
+    if (kt + 1 < kt_hi) stage(kt + 1, buf ^ 1);  // the next tile, into the idle buffer
 
     const int64_t key0 = static_cast<int64_t>(kt) * BN;
     const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + BN - 1 - qw0;
@@ -392,7 +392,7 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
     const int buf = (qt - qt_lo) & 1;
     wait_vmcnt0();
     __syncthreads();
-    stage(qt + 1, buf ^ 1);  // past the last tile: zeros / ignored rows into the idle buffer
+    if (qt + 1 < qt_hi) stage(qt + 1, buf ^ 1);  // the next tile, into the idle buffer
 
     const int64_t q0 = static_cast<int64_t>(qt) * QT;
     const int64_t dmin = kw0 - (q0 + QT - 1), dmax = kw0 + 31 - q0;  // key - q over the tile

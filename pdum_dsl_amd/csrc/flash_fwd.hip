@@ -296,9 +296,7 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
       const int buf = (kt - kt_lo) & 1;
       wait_vmcnt0();  // this wave's share of tile kt has landed
       __syncthreads();  // ... and everyone's; everyone is done with tile kt - 1
-      // Past the last tile these loads read beyond the buffer range (zeros) into
-      // the idle buffer: no branch, and the last tile's loads are drained below.
-      stage(kt + 1, buf ^ 1);
+      if (kt + 1 < kt_hi) stage(kt + 1, buf ^ 1);  // the next tile, into the idle buffer
       const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
       bool dead = false;
       if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's rows see no live key here
