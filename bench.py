@@ -36,6 +36,7 @@ def _args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--quick", action="store_true", help="skip the secondary configs and the CPU baseline")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--gemm-ref", action="store_true", help="also time a plain bf16 GEMM (hipBLASLt) for reference")
     p.add_argument(
         "--copy-probe",
         action="store_true",
@@ -185,6 +186,8 @@ def main():
 
     if not a.quick:
         line["secondary"] = secondary(torch, K, cf, h, dev)
+    if a.gemm_ref:
+        line["gemm_reference"] = gemm_reference(torch, dev)
     if not a.quick and not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline(cf)
     print(json.dumps(line), flush=True)
@@ -272,46 +275,55 @@ def secondary(torch, K, cf, h, dev):
     return out
 
 
-def _blas_threads() -> int:
-    try:
-        from threadpoolctl import threadpool_info
-
-        n = [i.get("num_threads", 0) for i in threadpool_info() if i.get("user_api") == "blas"]
-        if n:
-            return int(max(n))
-    except Exception:
-        pass
-    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-
-
 def cpu_baseline(cf):
-    """The float64 oracle's attention (the reference CPU path restated) on a
-    bounded sample of C3: one (b, h) instance, the first R query rows against
-    their causal keys, timed on this host's cores; reported as TFLOP/s of the
-    same algorithmic count the GPU line uses."""
-    rng = np.random.default_rng(3)
-    S, D, R = 4096, 128, 1024
-    q = rng.standard_normal((R, D)).astype(np.float32).astype(np.float64)
-    k = rng.standard_normal((S, D)).astype(np.float32).astype(np.float64)
-    v = rng.standard_normal((S, D)).astype(np.float32).astype(np.float64)
-    kk, vv = k[:R], v[:R]  # causal rows [0, R) only see keys [0, R)
+    """The reference's CPU path restated — the flash template's generated tile
+    program (fusion.plan_region over the naive attention region, the online-
+    softmax fold of fusion.py:542-615) evaluated by the float64 region
+    interpreter (oracle.region_eval: dense per-node evaluation, the fold as a
+    Python loop, as dialect.run_region / the torch-CPU Evaluator run it) — on
+    a bounded sample of C3: one (b, h) instance, its first R query rows against
+    their causal keys, repeated for ~10 s on this host's cores; reported as
+    TFLOP/s of the same causal algorithmic count the GPU line uses."""
+    import torch
+
+    from oracle import region_eval as rev
+    from pdum_dsl_amd.tl import fusion, zoo
+
+    R, D = 1024, 128
+    subj = zoo.attention(T=R, S=R, E=D, OD=D, mask="causal", seed=3, scale=D**-0.5)
+    (g,) = fusion.plan_region(subj.region).groups
+    vals = [rev.value(f.arr, p.type) for f, p in zip(subj.inputs, g.kernel.params)]
+    want = cf.attention(*subj.numpy_inputs(), scale=1.0, band=(None, 0))[0]
     t0 = time.perf_counter()
     reps = 0
     while True:
-        cf.attention(q, kk, vv, scale=D**-0.5, band=(None, 0))
+        out = rev.evaluate(g.kernel, vals)
         reps += 1
         if time.perf_counter() - t0 > 10.0:
             break
     el = time.perf_counter() - t0
+    err = float(np.abs(out.numpy(("t", "o")) - want).max())
+    assert err < 1e-9, f"CPU baseline disagrees with the closed form: {err}"  # verify-before-report
     fl = 4.0 * D * (R * (R + 1) / 2) * reps
     return {
-        "value": round(fl / el / 1e12, 6),
+        "value": round(fl / el / 1e12, 8),
         "unit": "TFLOP/s",
-        "cores": _blas_threads(),
+        "cores": int(torch.get_num_threads()),
         "kind": "port",
-        "sample": f"oracle.closed_forms.attention (float64 numpy) on one C3 head, query rows [0,{R}) with their "
-        f"causal keys, {reps} reps in {el:.1f} s; host os.cpu_count()={os.cpu_count()}",
+        "sample": f"oracle.region_eval (float64 torch-CPU interpreter) of the generated flash tile program "
+        f"(si={dict(g.params)['si']}) on one C3 head, query rows [0,{R}) x their causal keys, {reps} reps in "
+        f"{el:.1f} s; host os.cpu_count()={os.cpu_count()}",
     }
+
+
+def gemm_reference(torch, dev):
+    """A plain bf16 GEMM through torch (hipBLASLt) on the same device: the
+    practical MFMA ceiling the attention kernels are read against."""
+    n = 16384
+    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    ms = time_events(lambda: a @ b, 5, warmup=2)
+    return {"op": f"torch.matmul bf16 {n}x{n}x{n}", "ms": round(ms, 4), "TFLOP/s": round(2 * n**3 / ms / 1e9, 1)}
 
 
 if __name__ == "__main__":
