@@ -79,7 +79,7 @@ __device__ __forceinline__ int swz_v(int row) {
 // transposed (ds_read_b64_tr_b16) — the backward's Q / dO / K tiles — use one
 // table per row % 16, found by exhaustive check to keep both read patterns
 // conflict-free for 32- and 64-bank LDS (the conditions are pinned by
-// tests/test_abi.py): entry i is the XOR mask of row i's 16-byte slots.
+// tests/test_lds_layout.py): entry i is the XOR mask of row i's 16-byte slots.
 template <int D>
 __device__ __forceinline__ int swz_rt(int row) {
   constexpr uint64_t kTable = D == 128 ? 0x0c7a42f8e9356d1bull : 0x1265314603742057ull;
