@@ -328,6 +328,9 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
   const int k0 = kblk * BK;
   const int kw0 = k0 + 32 * w;
   const int krow = kw0 + r32;
+  auto clamp30 = [](int64_t x) { return static_cast<int>(x < -(1 << 30) ? -(1 << 30) : (x > (1 << 30) ? (1 << 30) : x)); };
+  const int blo = a.masked ? clamp30(a.band_lo) : -(1 << 30);
+  const int bhi = a.masked ? clamp30(a.band_hi) : (1 << 30);
 
   // this wave's K and V rows as B operands (lane: row r32, features 16 ks + 8 g .. +8)
   u32x4 kreg[KS], vreg[KS];
@@ -413,7 +416,10 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
       pacc = mfma32<T>(ol.row_frag(o_l, ks), vreg[ks], pacc);
     }
     __builtin_amdgcn_s_setprio(0);
-    // accumulator i of lane-half g: query q0 + 16 (i / 8) + 8 g + i % 8, key krow
+    // accumulator i of lane-half g: query q0 + 16 (i / 8) + 8 g + i % 8, key krow;
+    // masks in 32-bit offsets from the tile (band limits clamped to +-2^30)
+    const int dk0 = static_cast<int>(krow - q0);
+    const int qlim = krow < S_ ? static_cast<int>(T_ - q0 < (1 << 30) ? T_ - q0 : (1 << 30)) : 0;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int rb = 16 * hh + 8 * g;
@@ -429,12 +435,11 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
         float p = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lv));
         float ds = p * (pacc[i] - dv);
         if (cut) {
-          const int64_t qq = q0 + rb + j;
-          const int64_t dd = static_cast<int64_t>(krow) - qq;
-          if (qq >= T_ || krow >= S_) {
+          const int dd = dk0 - rb - j;  // key - query
+          if (rb + j >= qlim) {
             p = 0.f;
             ds = 0.f;
-          } else if (a.masked && (dd < a.band_lo || dd > a.band_hi)) {
+          } else if (dd < blo || dd > bhi) {
             p = stl[2 * QT + rb + j];  // the row's masked-score probability (0 unless fully masked)
             ds = 0.f;
           }
