@@ -35,6 +35,23 @@ __device__ __forceinline__ f32x16 mfma32<_Float16>(u32x4 a, u32x4 b, f32x16 c) {
                                                 0);
 }
 
+// v_mfma_f32_16x16x32: lane l holds A[l % 16][8 (l / 16) + j] and
+// B[8 (l / 16) + j][l % 16], j = 0..7, and receives D[4 (l / 16) + i][l % 16].
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c);
+
+template <>
+__device__ __forceinline__ f32x4 mfma16<__hip_bfloat16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+
+template <>
+__device__ __forceinline__ f32x4 mfma16<_Float16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
+}
+
 // Pack accumulators [8h, 8h+8) of a 32x32 tile into one 16-bit k-operand.
 template <typename T>
 __device__ __forceinline__ u32x4 pack8(const f32x16& a, int h) {
@@ -102,9 +119,6 @@ __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* lds, uint32_t vof
 #pragma clang diagnostic pop
 }
 
-// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima), issued through
-// the builtin so the compiler's own wait-count tracking sees it and adds no
-// later vector-memory waits of its own.
 // 4 bytes per lane, buffer -> LDS (lane i's dword lands at lds + 4 i).
 __device__ __forceinline__ void dma4(rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
   // the low 32 bits of a generic LDS address are its LDS offset (no address-space cast needed)
@@ -116,6 +130,9 @@ __device__ __forceinline__ void dma4(rsrc_t r, unsigned char* lds, uint32_t voff
 #pragma clang diagnostic pop
 }
 
+// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima), issued through
+// the builtin so the compiler's own wait-count tracking sees it and adds no
+// later vector-memory waits of its own.
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
 // ds_read_b64_tr_b16: in each 16-lane group, lane 4k + c supplies the address

@@ -2,26 +2,31 @@
 // query rows per head, where the work is reading the key/value cache once.
 //
 // Pass 1 (decode_split): one workgroup per (batch, kv head, split). The
-// heads_q / heads_kv query heads of the group (x t query rows) are packed
-// into the workgroup, so every cache byte is read from HBM exactly once.
-// Each wave sweeps 64-key blocks of its split: the block's K rows arrive with
-// 128-bit coalesced loads into a wave-private LDS tile, each lane then owns
-// one key and forms its scores with v_dot2 bf16/f16 dot products against the
-// queries (LDS broadcast reads); the P V update runs with lanes owning feature
-// pairs and each key's probability broadcast by v_readlane. Each wave carries
-// its own online-softmax state; the four waves combine through LDS and the
-// workgroup writes one partial (m, den, o) per query row.
+// heads_q / heads_kv query heads of the group (x t query rows, at most 16)
+// are packed into the workgroup, so every cache byte is read from HBM exactly
+// once. Each wave sweeps every fourth 32-key block of its split, with the next
+// block's K and V rows in flight (registers) while the current one computes:
+//   S^T = K Q^T    v_mfma_f32_16x16x32, K rows straight from the loads as the
+//                  A operand (16 keys x 32 features per lane group), the query
+//                  rows as the B operand (16 columns; unused ones are zero)
+//   online softmax per query column (lane = column; max over the 4 lane groups)
+//   O^T += V^T P^T the probabilities stay in registers as the B operand; V goes
+//                  through a wave-private LDS tile and comes back transposed
+//                  (ds_read_b64_tr_b16) as the A operand.
+// The waves' states combine through LDS and the workgroup writes one partial
+// (m, den, o) per query row. The work per cache byte is a few MFMA cycles, so
+// the sweep runs at the rate the loads arrive.
 //
 // Pass 2 (decode_merge): one wave per query row folds the splits' partials
 // with the associative online-softmax combine (flashsm, zoo/attention.py:40-46):
 //   m = max(mL, mR); den = denL e^(mL-m) + denR e^(mR-m); o likewise.
-#include "common.h"
+#include "attn_common.h"
 
 namespace pdh {
 namespace {
 
 constexpr float kInf = __builtin_inff();
-constexpr int kMaxNq = 8;  // query rows per workgroup (heads_q / heads_kv * t)
+constexpr int kMaxNq = 16;  // query rows per workgroup (heads_q / heads_kv * t): the MFMA's 16 columns
 
 struct DecArgs {
   const uint16_t* q;
@@ -31,40 +36,33 @@ struct DecArgs {
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st;
   float c2;  // scale * log2(e)
   int nsplit;
-  int64_t chunk;  // keys per split (multiple of 64)
+  int64_t chunk;  // keys per split (multiple of 32)
   float* ws;      // [batch*heads_q*t][nsplit][2 + D]
 };
 
-template <typename T>
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c);
-
-template <>
-__device__ __forceinline__ float dot2<__hip_bfloat16>(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
-}
-
-template <>
-__device__ __forceinline__ float dot2<_Float16>(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
-}
-
+// Block geometry: 32 keys per block (two 16-key score tiles).
 template <int D>
 struct DecCfg {
-  static constexpr int KROW = D * 2 + 16;  // LDS bytes per K row (16 B pad)
-  static constexpr int WAVE_LDS = 64 * KROW;
-  static constexpr int DPL = D / 64;  // value features per lane in the P V update
+  static constexpr int KB = 32;
+  static constexpr int KS = D / 32;       // k-steps of the score product (16x16x32)
+  static constexpr int ET = D / 16;       // 16-feature tiles of the output product
+  static constexpr int CPR = D / 8;       // 16-byte chunks per cache row
+  static constexpr int RPI = 64 / CPR;    // value rows per 1 KB wave load
+  static constexpr int VL = KB / RPI;     // value loads per block
+  static constexpr int VROW = D * 2 + 32; // LDS bytes per value row (32-byte pad: conflict-free transposed reads)
+  static constexpr int VTILE = KB * VROW; // one wave's value tile
+  static constexpr int RS = 2 + D;        // floats per (wave, query row) record
+  static constexpr int RED = 4 * kMaxNq * RS * 4;
+  static constexpr int LDS = 4 * VTILE > RED ? 4 * VTILE : RED;
 };
 
-template <typename T, int D, int NQ>
+template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void decode_split(DecArgs a) {
   using C = DecCfg<D>;
-  extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
-  unsigned char* kl = dsm;                                         // 4 wave-private K tiles
-  uint32_t* ql = reinterpret_cast<uint32_t*>(dsm + 4 * C::WAVE_LDS);  // staged query rows
-  float* pl = reinterpret_cast<float*>(dsm + 4 * C::WAVE_LDS + kMaxNq * D * 2);  // [wave][NQ][64] probabilities
-  float* red = reinterpret_cast<float*>(dsm);                      // reuses the K tiles at the end
-
+  constexpr int KS = C::KS, ET = C::ET, VL = C::VL;
+  extern __shared__ __attribute__((aligned(1024))) unsigned char dsm[];
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int col = lane & 15, g = lane >> 4;  // MFMA column (query row) and lane group
   const int R = static_cast<int>(a.heads_q / a.heads_kv);
   const int64_t nsplit = a.nsplit;
   const int64_t split = blockIdx.x % nsplit;
@@ -72,140 +70,151 @@ __global__ __launch_bounds__(256, 2) void decode_split(DecArgs a) {
   const int64_t b = grp / a.heads_kv, hk = grp % a.heads_kv;
   const uint16_t* kp = a.k + b * a.k_sb + hk * a.k_sh;
   const uint16_t* vp = a.v + b * a.v_sb + hk * a.v_sh;
-
-  // stage the group's query rows (row qi = r * t + tq) in LDS as 16-bit pairs
   const int nq = R * static_cast<int>(a.t);
-  for (int c = tid; c < NQ * D / 8; c += 256) {
-    const int qi = c / (D / 8), ch = c % (D / 8);
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (qi < nq) {
-      const int64_t hq = hk * R + qi / a.t, tq = qi % a.t;
-      val = *reinterpret_cast<const u32x4*>(a.q + b * a.q_sb + hq * a.q_sh + tq * a.q_st + ch * 8);
+
+  // query rows as the score product's B operand: lane (col, g) holds row col
+  // (= r * t + tq), features 32 s + 8 g .. +8; columns past nq are zero
+  u32x4 qb[KS];
+  {
+    const bool live = col < nq;
+    const int qc = live ? col : 0;
+    const int64_t hq = hk * R + qc / a.t, tq = qc % a.t;
+    const uint16_t* qrow = a.q + b * a.q_sb + hq * a.q_sh + tq * a.q_st;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qrow + s * 32 + g * 8);
+      qb[s] = live ? v : u32x4{0u, 0u, 0u, 0u};
     }
-    *reinterpret_cast<u32x4*>(&ql[qi * D / 2 + ch * 4]) = val;
   }
-  __syncthreads();
 
   const int64_t k_begin = split * a.chunk;
   const int64_t k_end = (k_begin + a.chunk < a.s) ? k_begin + a.chunk : a.s;
-  unsigned char* kw = kl + w * C::WAVE_LDS;
-  constexpr int CPR = D / 8;  // 16-byte chunks per K row
+  unsigned char* vt = dsm + w * C::VTILE;
+  const uint32_t kst2 = static_cast<uint32_t>(a.k_st * 2), vst2 = static_cast<uint32_t>(a.v_st * 2);
+  const int vrow = lane / C::CPR, vch = lane % C::CPR;  // value loads: row j * RPI + vrow, chunk vch
+  // transposed value reads: lane 4k + c of group g addresses row 4 g + k, features 4 c .. +3 (+ 16 t)
+  const int trb = (4 * g + (col >> 2)) * C::VROW + (col & 3) * 8;
 
-  float m[NQ], lp[NQ], o[NQ][C::DPL];
+  // Cache rows past k_end are clamped to the last live row (their scores are masked).
+  auto load = [&](int64_t kb, u32x4(&kr)[2 * KS], u32x4(&vr)[VL]) {
+    const int lim = static_cast<int>(k_end - 1 - kb < 31 ? k_end - 1 - kb : 31);
+    const uint16_t* kbase = kp + kb * a.k_st;
+    const uint16_t* vbase = vp + kb * a.v_st;
 #pragma unroll
-  for (int qi = 0; qi < NQ; ++qi) {
-    m[qi] = -kInf;
-    lp[qi] = 0.f;
+    for (int kt = 0; kt < 2; ++kt) {
+      const int r = 16 * kt + col < lim ? 16 * kt + col : lim;
+      const uint32_t off = static_cast<uint32_t>(r) * kst2 + g * 16;
 #pragma unroll
-    for (int j = 0; j < C::DPL; ++j) o[qi][j] = 0.f;
-  }
-
-  // K block of 64 keys: global (coalesced, 64/CPR rows per instruction) -> registers -> LDS
-  constexpr int RPI = 64 / CPR;  // rows per load instruction
-  const uint32_t k_lane = static_cast<uint32_t>((lane / CPR) * a.k_st * 2 + (lane % CPR) * 16);
-  const int k_lds = (lane / CPR) * C::KROW + (lane % CPR) * 16;
-  u32x4 kreg[CPR];
-  auto load_k = [&](int64_t kb0) {
+      for (int s = 0; s < KS; ++s) kr[kt * KS + s] = gload<u32x4>(kbase, off + s * 64);
+    }
 #pragma unroll
-    for (int i = 0; i < CPR; ++i) {
-      const int64_t row0 = kb0 + i * RPI;  // uniform
-      const bool ok = row0 + lane / CPR < k_end;
-      kreg[i] = ok ? gload<u32x4>(kp + row0 * a.k_st, k_lane) : u32x4{0u, 0u, 0u, 0u};
+    for (int j = 0; j < VL; ++j) {
+      const int r = j * C::RPI + vrow < lim ? j * C::RPI + vrow : lim;
+      vr[j] = gload<u32x4>(vbase, static_cast<uint32_t>(r) * vst2 + vch * 16);
     }
   };
-  auto store_k = [&]() {
+
+  float m = -kInf, lsum = 0.f;  // running max (log2 units) and partial sum of query row col
+  f32x4 o[ET];                  // O^T: o[t][i] = feature 16 t + 4 g + i of query row col
 #pragma unroll
-    for (int i = 0; i < CPR; ++i) *reinterpret_cast<u32x4*>(kw + i * RPI * C::KROW + k_lds) = kreg[i];
+  for (int t = 0; t < ET; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto block = [&](int64_t kb, const u32x4(&kr)[2 * KS], const u32x4(&vr)[VL]) {
+    // value rows -> this wave's LDS tile (row-major, padded rows)
+#pragma unroll
+    for (int j = 0; j < VL; ++j) *reinterpret_cast<u32x4*>(vt + (j * C::RPI + vrow) * C::VROW + vch * 16) = vr[j];
+    // S^T = K Q^T for keys kb + 16 kt + 4 g + i (accumulator i), query row col
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      s0 = mfma16<T>(kr[s], qb[s], s0);
+      s1 = mfma16<T>(kr[KS + s], qb[s], s1);
+    }
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = s0[i] * a.c2;
+      x[4 + i] = s1[i] * a.c2;
+    }
+    if (kb + C::KB > k_end) {  // the split's last block: keys past k_end are masked
+      const int live = static_cast<int>(k_end - kb);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (4 * g + i >= live) x[i] = -kInf;
+        if (16 + 4 * g + i >= live) x[4 + i] = -kInf;
+      }
+    }
+    float mx = x[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, x[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float mnew = fmaxf(m, mx);  // finite: every block holds a live key
+    if (__builtin_amdgcn_ballot_w64(mnew > m) != 0) {  // some row's max grew: rescale (rare after warm-up)
+      const float alpha = fast_exp2(m - mnew);
+      lsum *= alpha;
+#pragma unroll
+      for (int t = 0; t < ET; ++t) o[t] *= alpha;
+      m = mnew;
+    }
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = fast_exp2(x[i] - m);
+      lsum += p[i];
+    }
+    // P^T as the output product's B operand: slot j < 4 is key 4 g + j, j >= 4 key 16 + 4 g + j - 4
+    const u32x4 pb = {pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]), pack2<T>(p[6], p[7])};
+    // O^T += V^T P^T: A operand lane (e = 16 t + col, group g) holds those 8 keys' values
+#pragma unroll
+    for (int t = 0; t < ET; ++t) {
+      const u32x2 lo = ds_read_tr16(vt + trb + 32 * t);
+      const u32x2 hi = ds_read_tr16(vt + trb + 16 * C::VROW + 32 * t);
+      o[t] = mfma16<T>(u32x4{lo.x, lo.y, hi.x, hi.y}, pb, o[t]);
+    }
   };
 
-  const uint32_t v_lane = static_cast<uint32_t>(lane * C::DPL * 2);
-  for (int64_t kb = k_begin + 64 * w; kb < k_end; kb += 256) {
-    // this block's K rows and value rows in flight together; K lands in LDS first
-    load_k(kb);
-    uint32_t vreg[64];
-    const int nk = (k_end - kb) < 64 ? static_cast<int>(k_end - kb) : 64;
-    const uint16_t* vblk = vp + kb * a.v_st;
-#pragma unroll
-    for (int kk = 0; kk < 64; ++kk) {
-      if constexpr (C::DPL == 2)
-        vreg[kk] = kk < nk ? gload<uint32_t>(vblk + kk * a.v_st, v_lane) : 0u;
-      else
-        vreg[kk] = kk < nk ? static_cast<uint32_t>(gload<uint16_t>(vblk + kk * a.v_st, v_lane)) : 0u;
+  // Each wave takes every fourth block; the next block's K and V rows are in
+  // flight (registers) while this one is computed. The loads are issued
+  // unconditionally (past the wave's last block they re-read that block, an
+  // L2 hit) so the compiler's wait counts stay exact: a block waits only for
+  // its own rows, never for the prefetch behind them.
+  const int64_t stride = 4 * C::KB;
+  const int64_t kb0 = k_begin + C::KB * w;
+  if (kb0 < k_end) {
+    const int64_t kb_last = kb0 + (k_end - 1 - kb0) / stride * stride;
+    auto next = [&](int64_t kb) { return kb + stride < kb_last ? kb + stride : kb_last; };
+    u32x4 ka0[2 * KS], va0[VL], ka1[2 * KS], va1[VL];
+    int64_t kb = kb0;
+    load(kb, ka0, va0);
+    for (;;) {
+      load(next(kb), ka1, va1);
+      block(kb, ka0, va0);
+      kb += stride;
+      if (kb >= k_end) break;
+      load(next(kb), ka0, va0);
+      block(kb, ka1, va1);
+      kb += stride;
+      if (kb >= k_end) break;
     }
-    store_k();
-    __builtin_amdgcn_wave_barrier();
-
-    // lane = key: scores against every query row (K row from LDS, q broadcast).
-    // The query offset is laundered each iteration so the compiler re-reads the
-    // (loop-invariant) query rows from LDS instead of pinning them in registers.
-    int qoff = 0;
-    asm volatile("" : "+v"(qoff));
-    const int64_t key = kb + lane;
-    float sc[NQ];
-#pragma unroll
-    for (int qi = 0; qi < NQ; ++qi) sc[qi] = 0.f;
-#pragma unroll 2
-    for (int ch = 0; ch < CPR; ++ch) {
-      const u32x4 kv = *reinterpret_cast<const u32x4*>(kw + lane * C::KROW + ch * 16);
-#pragma unroll
-      for (int qi = 0; qi < NQ; ++qi) {
-        const u32x4 qv = *reinterpret_cast<const u32x4*>(&ql[qoff + qi * D / 2 + ch * 4]);
-        float acc = sc[qi];
-        acc = dot2<T>(kv.x, qv.x, acc);
-        acc = dot2<T>(kv.y, qv.y, acc);
-        acc = dot2<T>(kv.z, qv.z, acc);
-        acc = dot2<T>(kv.w, qv.w, acc);
-        sc[qi] = acc;
-      }
-    }
-    float* pw = pl + w * NQ * 64;
-#pragma unroll
-    for (int qi = 0; qi < NQ; ++qi) {
-      const float x = key < k_end ? sc[qi] * a.c2 : -kInf;
-      const float mnew = fmaxf(m[qi], wave_max(x));
-      const float alpha = fast_exp2(m[qi] - mnew);
-      const float p = fast_exp2(x - mnew);
-      pw[qi * 64 + lane] = p;
-      lp[qi] = lp[qi] * alpha + p;
-      m[qi] = mnew;
-#pragma unroll
-      for (int j = 0; j < C::DPL; ++j) o[qi][j] *= alpha;
-    }
-    __builtin_amdgcn_wave_barrier();
-    // P V: lanes own features; each key's probability is an LDS broadcast read
-#pragma unroll
-    for (int k4 = 0; k4 < 64; k4 += 4) {
-#pragma unroll
-      for (int qi = 0; qi < NQ; ++qi) {
-        const f32x4 pk = *reinterpret_cast<const f32x4*>(pw + qi * 64 + k4);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t vw = vreg[k4 + u];
-          if constexpr (C::DPL == 2) {
-            o[qi][0] = __builtin_fmaf(pk[u], lo_f32<T>(vw), o[qi][0]);
-            o[qi][1] = __builtin_fmaf(pk[u], hi_f32<T>(vw), o[qi][1]);
-          } else {
-            o[qi][0] = __builtin_fmaf(pk[u], lo_f32<T>(vw), o[qi][0]);
-          }
-        }
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
   }
+  lsum += __shfl_xor(lsum, 16, kWave);
+  lsum += __shfl_xor(lsum, 32, kWave);
 
-  // per-wave state -> LDS (over the K tiles), then combine the four waves
+  // per-wave state -> LDS (over the value tiles), then combine the four waves
   __syncthreads();
-  constexpr int RS = 2 + D;  // floats per (wave, query row) record
-#pragma unroll
-  for (int qi = 0; qi < NQ; ++qi) {
-    const float l = wave_sum(lp[qi]);
-    float* rec = red + (w * NQ + qi) * RS;
-    if (lane == 0) {
-      rec[0] = m[qi];
-      rec[1] = l;
+  constexpr int RS = C::RS;
+  float* red = reinterpret_cast<float*>(dsm);
+  if (col < nq) {
+    float* rec = red + (w * kMaxNq + col) * RS;
+    if (g == 0) {
+      rec[0] = m;
+      rec[1] = lsum;
     }
 #pragma unroll
-    for (int j = 0; j < C::DPL; ++j) rec[2 + lane * C::DPL + j] = o[qi][j];
+    for (int t = 0; t < ET; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rec[2 + 16 * t + 4 * g + i] = o[t][i];
   }
   __syncthreads();
   const int64_t q_row0 = (b * a.heads_q + hk * R) * a.t;  // first stats row of the group
@@ -213,16 +222,16 @@ __global__ __launch_bounds__(256, 2) void decode_split(DecArgs a) {
     const int qi = c / RS, f = c % RS;
     float mm = -kInf;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) mm = fmaxf(mm, red[(ww * NQ + qi) * RS]);
+    for (int ww = 0; ww < 4; ++ww) mm = fmaxf(mm, red[(ww * kMaxNq + qi) * RS]);
     float val = 0.f;
     if (f == 0) {
       val = mm;
     } else {
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) {
-        const float mw = red[(ww * NQ + qi) * RS];
+        const float mw = red[(ww * kMaxNq + qi) * RS];
         const float sc = mw == -kInf ? 0.f : fast_exp2(mw - mm);
-        val += red[(ww * NQ + qi) * RS + f] * sc;
+        val += red[(ww * kMaxNq + qi) * RS + f] * sc;
       }
     }
     // qi = r * t + tq matches the stats row order (head-major, then row)
@@ -261,24 +270,15 @@ __global__ __launch_bounds__(256) void decode_merge(const float* __restrict__ ws
 }
 
 template <typename T, int D>
-int launch_decode(const DecArgs& a, int nq, int64_t nrows, uint16_t* o, float* lse, int64_t o_sb, int64_t o_sh,
+int launch_decode(const DecArgs& a, int64_t nrows, uint16_t* o, float* lse, int64_t o_sb, int64_t o_sh,
                   int64_t o_st, int64_t groups, hipStream_t st) {
   const int64_t nblk = groups * a.nsplit;
   PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_attn_decode: grid too large");
   const dim3 grid(static_cast<unsigned>(nblk));
-  const int lds = 4 * DecCfg<D>::WAVE_LDS + kMaxNq * D * 2 + 4 * kMaxNq * 64 * 4;
-  auto go = [&](auto kern) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    kern<<<grid, 256, lds, st>>>(a);
-  };
-  if (nq <= 1)
-    go(decode_split<T, D, 1>);
-  else if (nq <= 2)
-    go(decode_split<T, D, 2>);
-  else if (nq <= 4)
-    go(decode_split<T, D, 4>);
-  else
-    go(decode_split<T, D, 8>);
+  constexpr int lds = DecCfg<D>::LDS;
+  hipFuncSetAttribute(reinterpret_cast<const void*>(decode_split<T, D>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                      lds);
+  decode_split<T, D><<<grid, 256, lds, st>>>(a);
   int rc = check_launch("pdh_attn_decode (split)");
   if (rc) return rc;
   decode_merge<T, D><<<dim3(static_cast<unsigned>((nrows + 3) / 4)), 256, 0, st>>>(
@@ -325,7 +325,7 @@ extern "C" int pdh_attn_decode(const void* q, const void* k, const void* v, void
   PDH_REQUIRE(ws_bytes >= need, PDH_EINVAL, "pdh_attn_decode: workspace %zu bytes < required %zu", ws_bytes, need);
   if (G.batch == 0) return PDH_OK;
   int64_t chunk = (G.s + nsplit - 1) / nsplit;
-  chunk = (chunk + 63) / 64 * 64;
+  chunk = (chunk + 31) / 32 * 32;
   DecArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
             G.heads_q, G.heads_kv, G.t, G.s, G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh,
             G.v_st, scale * kLog2e, nsplit, chunk, static_cast<float*>(ws)};
@@ -334,11 +334,11 @@ extern "C" int pdh_attn_decode(const void* q, const void* k, const void* v, void
   hipStream_t st = as_stream(stream);
   uint16_t* op = static_cast<uint16_t*>(o);
   if (dtype == PDH_BF16)
-    return G.e == 128 ? launch_decode<__hip_bfloat16, 128>(a, (int)nq, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st,
+    return G.e == 128 ? launch_decode<__hip_bfloat16, 128>(a, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st,
                                                            groups, st)
-                      : launch_decode<__hip_bfloat16, 64>(a, (int)nq, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st,
+                      : launch_decode<__hip_bfloat16, 64>(a, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st,
                                                           groups, st);
   return G.e == 128
-             ? launch_decode<_Float16, 128>(a, (int)nq, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st, groups, st)
-             : launch_decode<_Float16, 64>(a, (int)nq, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st, groups, st);
+             ? launch_decode<_Float16, 128>(a, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st, groups, st)
+             : launch_decode<_Float16, 64>(a, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st, groups, st);
 }

@@ -188,7 +188,10 @@ def test_sliding_window_band(K):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize(
     "B,Hq,Hkv,T,S,D,nsplit",
-    [(2, 8, 2, 1, 1000, 128, 3), (1, 4, 4, 1, 64, 64, 1), (3, 32, 8, 1, 2048, 128, None), (1, 4, 1, 2, 777, 128, 4)],
+    [(2, 8, 2, 1, 1000, 128, 3), (1, 4, 4, 1, 64, 64, 1), (3, 32, 8, 1, 2048, 128, None), (1, 4, 1, 2, 777, 128, 4),
+     # 16 query rows per kv head (the MFMA's full width), t > 1 at D = 64, a cache shorter than one
+     # 32-key block, and splits past the cache's end (S = 33 in 4 splits of 32 keys: two are empty)
+     (1, 16, 1, 1, 300, 128, 2), (2, 4, 2, 3, 100, 64, 3), (1, 2, 2, 1, 5, 128, 1), (1, 8, 2, 1, 33, 128, 4)],
 )
 def test_decode_matches_oracle(K, dtype, B, Hq, Hkv, T, S, D, nsplit):
     rng = np.random.default_rng(S + Hq)
