@@ -432,20 +432,32 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
         const int i = 8 * hh + j;
         const float lv = j < 4 ? l0[j] : l1[j - 4];
         const float dv = j < 4 ? d0[j] : d1[j - 4];
-        float p = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lv));
-        float ds = p * (pacc[i] - dv);
-        if (cut) {
-          const int dd = dk0 - rb - j;  // key - query
-          if (rb + j >= qlim) {
-            p = 0.f;
-            ds = 0.f;
-          } else if (dd < blo || dd > bhi) {
-            p = stl[2 * QT + rb + j];  // the row's masked-score probability (0 unless fully masked)
-            ds = 0.f;
-          }
-        }
+        const float p = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lv));
+        pacc[i] = p * (pacc[i] - dv);
         sacc[i] = p;
-        pacc[i] = ds;
+      }
+    }
+    // Masked tiles (uniform branch) fix up the probabilities with selects that
+    // read the rows' pm values as vectors: no per-element branches, which
+    // would split the tile into basic blocks the scheduler cannot interleave
+    // with the MFMAs.
+    if (cut) {
+      asm volatile("" ::: "memory");  // keeps the branch: if-converted, every tile would pay the selects
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int rb = 16 * hh + 8 * g;
+        const f32x4 m0 = *reinterpret_cast<const f32x4*>(stl + 2 * QT + rb);
+        const f32x4 m1 = *reinterpret_cast<const f32x4*>(stl + 2 * QT + rb + 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int i = 8 * hh + j;
+          const float pm = j < 4 ? m0[j] : m1[j - 4];  // the row's masked-score probability (0 unless fully masked)
+          const int dd = dk0 - rb - j;                  // key - query
+          const bool row_live = rb + j < qlim;
+          const bool in_band = dd >= blo && dd <= bhi;
+          sacc[i] = row_live ? (in_band ? sacc[i] : pm) : 0.f;
+          pacc[i] = row_live && in_band ? pacc[i] : 0.f;
+        }
       }
     }
     const u32x4 p0 = pack8<T>(sacc, 0), p1 = pack8<T>(sacc, 1);
