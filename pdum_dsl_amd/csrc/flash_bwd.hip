@@ -122,6 +122,10 @@ struct Tile32 {
   static constexpr int KS = D / 16, DB = D / 32;
 };
 
+// Tiles staged per barrier: each stage holds kSub consecutive 32-row tiles,
+// so a wave runs kSub tiles of MFMA / softmax work between barriers.
+constexpr int kSub = 2;
+
 // Per-lane offsets of the tile's three access patterns.
 template <int D>
 struct TileLane {
@@ -173,7 +177,7 @@ struct TileLane {
 // -------------------------------------------------------------------- dQ
 //
 // Workgroup: 4 waves x 32 query rows; key tiles of 32 rows (K, V) staged by
-// direct loads, double buffered. Per wave and tile:
+// direct loads kSub tiles per barrier, double buffered. Per wave and tile:
 //   S^T = K Q^T, dP^T = V dO^T       (A = K / V rows, B = Q / dO in registers)
 //   dS^T = P^T (dP^T - delta)        (lane = query row: lse, delta are scalars)
 //   dQ^T += K^T dS^T                 (A = K transposed from LDS)
@@ -231,11 +235,15 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
   TileLane<D> kl, vl;  // K and V tiles share the slot layout; only the source stride differs
   kl.init(lane, w, r32, g, grk);
   vl.init(lane, w, r32, g, grv);
-  auto kbuf = [&](int buf) { return smem + buf * TT::BYTES; };
-  auto vbuf = [&](int buf) { return smem + (2 + buf) * TT::BYTES; };
-  auto stage = [&](int tile, int buf) {
-    kl.stage(kr, kbuf(buf), static_cast<uint32_t>(tile * BN), grk, w);
-    vl.stage(vr, vbuf(buf), static_cast<uint32_t>(tile * BN), grv, w);
+  auto kbuf = [&](int buf, int sub) { return smem + (buf * kSub + sub) * TT::BYTES; };
+  auto vbuf = [&](int buf, int sub) { return smem + ((2 + buf) * kSub + sub) * TT::BYTES; };
+  auto stage = [&](int tile0, int buf) {  // tiles tile0 .. tile0 + kSub - 1 that the sweep reads
+#pragma unroll
+    for (int sub = 0; sub < kSub; ++sub) {
+      if (tile0 + sub >= kt_hi) break;
+      kl.stage(kr, kbuf(buf, sub), static_cast<uint32_t>((tile0 + sub) * BN), grk, w);
+      vl.stage(vr, vbuf(buf, sub), static_cast<uint32_t>((tile0 + sub) * BN), grv, w);
+    }
   };
 
   f32x16 dqacc[DB];
@@ -243,57 +251,61 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
 
   if (kt_lo < kt_hi) stage(kt_lo, 0);
-  for (int kt = kt_lo; kt < kt_hi; ++kt) {
-    const int buf = (kt - kt_lo) & 1;
+  for (int kt0 = kt_lo; kt0 < kt_hi; kt0 += kSub) {
+    const int buf = ((kt0 - kt_lo) / kSub) & 1;
     wait_vmcnt0();
     __syncthreads();
-    if (kt + 1 < kt_hi) stage(kt + 1, buf ^ 1);  // the next tile, into the idle buffer
-
-    const int64_t key0 = static_cast<int64_t>(kt) * BN;
-    const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + BN - 1 - qw0;
-    bool dead = false, cut = key0 + BN > S_ || qw0 + 32 > T_;
-    if (a.masked) {
-      dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
-      cut = cut || dmin < a.band_lo || dmax > a.band_hi;
-    }
-    if (dead) continue;
-    const unsigned char* kt_l = kbuf(buf);
-    const unsigned char* vt_l = vbuf(buf);
-    __builtin_amdgcn_s_setprio(1);
-    f32x16 sacc = f32x16{}, pacc = f32x16{};
+    if (kt0 + kSub < kt_hi) stage(kt0 + kSub, buf ^ 1);  // the next stage, into the idle buffers
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      sacc = mfma32<T>(kl.row_frag(kt_l, ks), qreg[ks], sacc);
-      pacc = mfma32<T>(vl.row_frag(vt_l, ks), doreg[ks], pacc);
-    }
-    __builtin_amdgcn_s_setprio(0);
-    // accumulator i of lane-half g: key key0 + 16 (i / 8) + 8 g + i % 8, query qrow
-    if (cut) {
-      const int64_t kl0 = key0 + 8 * g;
-      const int rem = static_cast<int>(S_ - kl0 < 1024 ? S_ - kl0 : 1024);
-      const int64_t dl0 = kl0 - qrow;
-      auto clampi = [](int64_t x) { return static_cast<int>(x < -4096 ? -4096 : (x > 4096 ? 4096 : x)); };
-      const int lo = a.masked ? clampi(a.band_lo - dl0) : -4096;
-      const int hi = a.masked ? clampi(a.band_hi - dl0) : 4096;
-      const bool rowok = qrow < T_;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int c = (i >> 3) * 16 + (i & 7);
-        const bool live = rowok && c < rem && c >= lo && c <= hi;
-        pacc[i] = live ? fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * (pacc[i] - dl) : 0.f;
+    for (int sub = 0; sub < kSub; ++sub) {
+      const int kt = kt0 + sub;
+      if (kt >= kt_hi) break;
+      const int64_t key0 = static_cast<int64_t>(kt) * BN;
+      const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + BN - 1 - qw0;
+      bool dead = false, cut = key0 + BN > S_ || qw0 + 32 > T_;
+      if (a.masked) {
+        dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
+        cut = cut || dmin < a.band_lo || dmax > a.band_hi;
       }
-    } else {
+      if (dead) continue;
+      const unsigned char* kt_l = kbuf(buf, sub);
+      const unsigned char* vt_l = vbuf(buf, sub);
+      __builtin_amdgcn_s_setprio(1);
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
 #pragma unroll
-      for (int i = 0; i < 16; ++i) pacc[i] = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * (pacc[i] - dl);
-    }
-    const u32x4 ds0 = pack8<T>(pacc, 0), ds1 = pack8<T>(pacc, 1);
-    __builtin_amdgcn_s_setprio(1);
+      for (int ks = 0; ks < KS; ++ks) {
+        sacc = mfma32<T>(kl.row_frag(kt_l, ks), qreg[ks], sacc);
+        pacc = mfma32<T>(vl.row_frag(vt_l, ks), doreg[ks], pacc);
+      }
+      __builtin_amdgcn_s_setprio(0);
+      // accumulator i of lane-half g: key key0 + 16 (i / 8) + 8 g + i % 8, query qrow
+      if (cut) {
+        const int64_t kl0 = key0 + 8 * g;
+        const int rem = static_cast<int>(S_ - kl0 < 1024 ? S_ - kl0 : 1024);
+        const int64_t dl0 = kl0 - qrow;
+        auto clampi = [](int64_t x) { return static_cast<int>(x < -4096 ? -4096 : (x > 4096 ? 4096 : x)); };
+        const int lo = a.masked ? clampi(a.band_lo - dl0) : -4096;
+        const int hi = a.masked ? clampi(a.band_hi - dl0) : 4096;
+        const bool rowok = qrow < T_;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      dqacc[db] = mfma32<T>(kl.tr_frag(kt_l, 0, db), ds0, dqacc[db]);
-      dqacc[db] = mfma32<T>(kl.tr_frag(kt_l, 1, db), ds1, dqacc[db]);
+        for (int i = 0; i < 16; ++i) {
+          const int c = (i >> 3) * 16 + (i & 7);
+          const bool live = rowok && c < rem && c >= lo && c <= hi;
+          pacc[i] = live ? fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * (pacc[i] - dl) : 0.f;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) pacc[i] = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * (pacc[i] - dl);
+      }
+      const u32x4 ds0 = pack8<T>(pacc, 0), ds1 = pack8<T>(pacc, 1);
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        dqacc[db] = mfma32<T>(kl.tr_frag(kt_l, 0, db), ds0, dqacc[db]);
+        dqacc[db] = mfma32<T>(kl.tr_frag(kt_l, 1, db), ds1, dqacc[db]);
+      }
+      __builtin_amdgcn_s_setprio(0);
     }
-    __builtin_amdgcn_s_setprio(0);
   }
   wait_vmcnt0();
 
@@ -306,7 +318,7 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
 //
 // Workgroup: 4 waves x 32 key rows (K, V in registers as B operands); query
 // tiles of 32 rows (Q, dO and the rows' delta / lse2 / pm) staged by direct
-// loads, double buffered. Per wave and tile:
+// loads kSub tiles per barrier, double buffered. Per wave and tile:
 //   S = Q K^T, dP = dO V^T           (A = Q / dO rows; lane = key, acc = query)
 //   P = exp2(S c2 - lse2), dS = P (dP - delta)
 //   dV^T += dO^T P, dK^T += Q^T dS   (A = dO / Q transposed from LDS)
@@ -315,7 +327,7 @@ template <typename T, int D>
 __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned char* smem) {  // Q[2], dO[2], stats[2]
   using TT = Tile32<D>;
   constexpr int KS = TT::KS, DB = TT::DB, BK = 128, QT = 32;
-  constexpr int STATB = 4 * TT::BYTES;  // [2][delta | lse2 | pm] x 32 floats
+  constexpr int STATB = 4 * kSub * TT::BYTES;  // [2][kSub][delta | lse2 | pm] x 32 floats
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
   const int64_t inst = bid / a.nkblk;
   const int kblk = bid % a.nkblk;  // early key blocks see the most queries under causal masks: launched first
@@ -370,16 +382,23 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
   // stats: wave 0 loads delta (lanes 0-31) and lse2 (32-63), then pm (0-31)
   const uint32_t st_off0 = static_cast<uint32_t>(((lane >> 5) * a.rows + inst * T_ + r32) * 4);
   const uint32_t st_off1 = static_cast<uint32_t>((2 * a.rows + inst * T_ + r32) * 4);
-  auto qbuf = [&](int buf) { return smem + buf * TT::BYTES; };
-  auto obuf = [&](int buf) { return smem + (2 + buf) * TT::BYTES; };
-  auto sbuf = [&](int buf) { return reinterpret_cast<float*>(smem + STATB + buf * 3 * QT * 4); };
-  auto stage = [&](int qt, int buf) {
-    ql.stage(qr, qbuf(buf), static_cast<uint32_t>(qt * QT), grq, w);
-    ol.stage(orr, obuf(buf), static_cast<uint32_t>(qt * QT), gro, w);
-    if (w == 0) {
-      unsigned char* sl = reinterpret_cast<unsigned char*>(sbuf(buf));
-      dma4(sr, sl, st_off0, static_cast<uint32_t>(qt * QT * 4));
-      if (lane < 32) dma4(sr, sl + 2 * QT * 4, st_off1, static_cast<uint32_t>(qt * QT * 4));
+  auto qbuf = [&](int buf, int sub) { return smem + (buf * kSub + sub) * TT::BYTES; };
+  auto obuf = [&](int buf, int sub) { return smem + ((2 + buf) * kSub + sub) * TT::BYTES; };
+  auto sbuf = [&](int buf, int sub) {
+    return reinterpret_cast<float*>(smem + STATB + (buf * kSub + sub) * 3 * QT * 4);
+  };
+  auto stage = [&](int qt0, int buf) {  // tiles qt0 .. qt0 + kSub - 1 that the sweep reads
+#pragma unroll
+    for (int sub = 0; sub < kSub; ++sub) {
+      const int qt = qt0 + sub;
+      if (qt >= qt_hi) break;
+      ql.stage(qr, qbuf(buf, sub), static_cast<uint32_t>(qt * QT), grq, w);
+      ol.stage(orr, obuf(buf, sub), static_cast<uint32_t>(qt * QT), gro, w);
+      if (w == 0) {
+        unsigned char* sl = reinterpret_cast<unsigned char*>(sbuf(buf, sub));
+        dma4(sr, sl, st_off0, static_cast<uint32_t>(qt * QT * 4));
+        if (lane < 32) dma4(sr, sl + 2 * QT * 4, st_off1, static_cast<uint32_t>(qt * QT * 4));
+      }
     }
   };
 
@@ -391,86 +410,90 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
   }
 
   if (qt_lo < qt_hi) stage(qt_lo, 0);
-  for (int qt = qt_lo; qt < qt_hi; ++qt) {
-    const int buf = (qt - qt_lo) & 1;
+  for (int qt0 = qt_lo; qt0 < qt_hi; qt0 += kSub) {
+    const int buf = ((qt0 - qt_lo) / kSub) & 1;
     wait_vmcnt0();
     __syncthreads();
-    if (qt + 1 < qt_hi) stage(qt + 1, buf ^ 1);  // the next tile, into the idle buffer
-
-    const int64_t q0 = static_cast<int64_t>(qt) * QT;
-    const int64_t dmin = kw0 - (q0 + QT - 1), dmax = kw0 + 31 - q0;  // key - q over the tile
-    bool dead = false, cut = q0 + QT > T_ || kw0 + 32 > S_;
-    if (a.masked) {
-      dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
-      cut = cut || dmin < a.band_lo || dmax > a.band_hi;
-    }
-    if (dead) continue;
-    const unsigned char* q_l = qbuf(buf);
-    const unsigned char* o_l = obuf(buf);
-    const float* stl = sbuf(buf);
-    __builtin_amdgcn_s_setprio(1);
-    f32x16 sacc = f32x16{}, pacc = f32x16{};
+    if (qt0 + kSub < qt_hi) stage(qt0 + kSub, buf ^ 1);  // the next stage, into the idle buffers
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      sacc = mfma32<T>(ql.row_frag(q_l, ks), kreg[ks], sacc);
-      pacc = mfma32<T>(ol.row_frag(o_l, ks), vreg[ks], pacc);
-    }
-    __builtin_amdgcn_s_setprio(0);
-    // accumulator i of lane-half g: query q0 + 16 (i / 8) + 8 g + i % 8, key krow;
-    // masks in 32-bit offsets from the tile (band limits clamped to +-2^30)
-    const int dk0 = static_cast<int>(krow - q0);
-    const int qlim = krow < S_ ? static_cast<int>(T_ - q0 < (1 << 30) ? T_ - q0 : (1 << 30)) : 0;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int rb = 16 * hh + 8 * g;
-      const f32x4 d0 = *reinterpret_cast<const f32x4*>(stl + rb);
-      const f32x4 d1 = *reinterpret_cast<const f32x4*>(stl + rb + 4);
-      const f32x4 l0 = *reinterpret_cast<const f32x4*>(stl + QT + rb);
-      const f32x4 l1 = *reinterpret_cast<const f32x4*>(stl + QT + rb + 4);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = 8 * hh + j;
-        const float lv = j < 4 ? l0[j] : l1[j - 4];
-        const float dv = j < 4 ? d0[j] : d1[j - 4];
-        const float p = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lv));
-        pacc[i] = p * (pacc[i] - dv);
-        sacc[i] = p;
+    for (int sub = 0; sub < kSub; ++sub) {
+      const int qt = qt0 + sub;
+      if (qt >= qt_hi) break;
+      const int64_t q0 = static_cast<int64_t>(qt) * QT;
+      const int64_t dmin = kw0 - (q0 + QT - 1), dmax = kw0 + 31 - q0;  // key - q over the tile
+      bool dead = false, cut = q0 + QT > T_ || kw0 + 32 > S_;
+      if (a.masked) {
+        dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
+        cut = cut || dmin < a.band_lo || dmax > a.band_hi;
       }
-    }
-    // Masked tiles (uniform branch) fix up the probabilities with selects that
-    // read the rows' pm values as vectors: no per-element branches, which
-    // would split the tile into basic blocks the scheduler cannot interleave
-    // with the MFMAs.
-    if (cut) {
-      asm volatile("" ::: "memory");  // keeps the branch: if-converted, every tile would pay the selects
+      if (dead) continue;
+      const unsigned char* q_l = qbuf(buf, sub);
+      const unsigned char* o_l = obuf(buf, sub);
+      const float* stl = sbuf(buf, sub);
+      __builtin_amdgcn_s_setprio(1);
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        sacc = mfma32<T>(ql.row_frag(q_l, ks), kreg[ks], sacc);
+        pacc = mfma32<T>(ol.row_frag(o_l, ks), vreg[ks], pacc);
+      }
+      __builtin_amdgcn_s_setprio(0);
+      // accumulator i of lane-half g: query q0 + 16 (i / 8) + 8 g + i % 8, key krow;
+      // masks in 32-bit offsets from the tile (band limits clamped to +-2^30)
+      const int dk0 = static_cast<int>(krow - q0);
+      const int qlim = krow < S_ ? static_cast<int>(T_ - q0 < (1 << 30) ? T_ - q0 : (1 << 30)) : 0;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int rb = 16 * hh + 8 * g;
-        const f32x4 m0 = *reinterpret_cast<const f32x4*>(stl + 2 * QT + rb);
-        const f32x4 m1 = *reinterpret_cast<const f32x4*>(stl + 2 * QT + rb + 4);
+        const f32x4 d0 = *reinterpret_cast<const f32x4*>(stl + rb);
+        const f32x4 d1 = *reinterpret_cast<const f32x4*>(stl + rb + 4);
+        const f32x4 l0 = *reinterpret_cast<const f32x4*>(stl + QT + rb);
+        const f32x4 l1 = *reinterpret_cast<const f32x4*>(stl + QT + rb + 4);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int i = 8 * hh + j;
-          const float pm = j < 4 ? m0[j] : m1[j - 4];  // the row's masked-score probability (0 unless fully masked)
-          const int dd = dk0 - rb - j;                  // key - query
-          const bool row_live = rb + j < qlim;
-          const bool in_band = dd >= blo && dd <= bhi;
-          sacc[i] = row_live ? (in_band ? sacc[i] : pm) : 0.f;
-          pacc[i] = row_live && in_band ? pacc[i] : 0.f;
+          const float lv = j < 4 ? l0[j] : l1[j - 4];
+          const float dv = j < 4 ? d0[j] : d1[j - 4];
+          const float p = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lv));
+          pacc[i] = p * (pacc[i] - dv);
+          sacc[i] = p;
         }
       }
-    }
-    const u32x4 p0 = pack8<T>(sacc, 0), p1 = pack8<T>(sacc, 1);
-    const u32x4 s0 = pack8<T>(pacc, 0), s1 = pack8<T>(pacc, 1);
-    __builtin_amdgcn_s_setprio(1);
+      // Masked tiles (uniform branch) fix up the probabilities with selects that
+      // read the rows' pm values as vectors: no per-element branches, which
+      // would split the tile into basic blocks the scheduler cannot interleave
+      // with the MFMAs.
+      if (cut) {
+        asm volatile("" ::: "memory");  // keeps the branch: if-converted, every tile would pay the selects
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      dvacc[db] = mfma32<T>(ol.tr_frag(o_l, 0, db), p0, dvacc[db]);
-      dvacc[db] = mfma32<T>(ol.tr_frag(o_l, 1, db), p1, dvacc[db]);
-      dkacc[db] = mfma32<T>(ql.tr_frag(q_l, 0, db), s0, dkacc[db]);
-      dkacc[db] = mfma32<T>(ql.tr_frag(q_l, 1, db), s1, dkacc[db]);
+        for (int hh = 0; hh < 2; ++hh) {
+          const int rb = 16 * hh + 8 * g;
+          const f32x4 m0 = *reinterpret_cast<const f32x4*>(stl + 2 * QT + rb);
+          const f32x4 m1 = *reinterpret_cast<const f32x4*>(stl + 2 * QT + rb + 4);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int i = 8 * hh + j;
+            const float pm = j < 4 ? m0[j] : m1[j - 4];  // the row's masked-score probability (0 unless fully masked)
+            const int dd = dk0 - rb - j;                  // key - query
+            const bool row_live = rb + j < qlim;
+            const bool in_band = dd >= blo && dd <= bhi;
+            sacc[i] = row_live ? (in_band ? sacc[i] : pm) : 0.f;
+            pacc[i] = row_live && in_band ? pacc[i] : 0.f;
+          }
+        }
+      }
+      const u32x4 p0 = pack8<T>(sacc, 0), p1 = pack8<T>(sacc, 1);
+      const u32x4 s0 = pack8<T>(pacc, 0), s1 = pack8<T>(pacc, 1);
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        dvacc[db] = mfma32<T>(ol.tr_frag(o_l, 0, db), p0, dvacc[db]);
+        dvacc[db] = mfma32<T>(ol.tr_frag(o_l, 1, db), p1, dvacc[db]);
+        dkacc[db] = mfma32<T>(ql.tr_frag(q_l, 0, db), s0, dkacc[db]);
+        dkacc[db] = mfma32<T>(ql.tr_frag(q_l, 1, db), s1, dkacc[db]);
+      }
+      __builtin_amdgcn_s_setprio(0);
     }
-    __builtin_amdgcn_s_setprio(0);
   }
   wait_vmcnt0();
 
@@ -676,7 +699,7 @@ int launch_bwd(BwdArgs a, hipStream_t st) {
   int rc = check_launch("pdh_flash_bwd (row stats)");
   if (rc) return rc;
   constexpr int TB = Tile32<D>::BYTES;
-  constexpr int lds = 4 * TB + 2 * 3 * 32 * 4;  // the larger of the two roles' needs (dK/dV)
+  constexpr int lds = 4 * kSub * TB + 2 * kSub * 3 * 32 * 4;  // the larger of the two roles' needs (dK/dV)
   const int64_t nblk = static_cast<int64_t>(a.ninst) * (a.nkblk + a.nqblk);
   a.xcd_remap = nblk % 8 == 0;
   bwd_main<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, lds, st>>>(a);
