@@ -4,7 +4,7 @@
 // Like the reference's carving, every output is owned by exactly one program
 // (330 §7.8 ruling 4): no atomics.
 //
-//   bwd_stats : per query row: delta = sum_d dO O, the log2-domain statistic
+//   bwd_stats : per query row: -delta (delta = sum_d dO O), the log2-domain statistic
 //               lse2 (P = exp2(x - lse2) for live scores) and pm, the
 //               probability of a MASKED score (0 unless every key of the
 //               row is masked; then 1/den, the uniform-softmax row)  (HBM-bound)
@@ -41,7 +41,7 @@ struct BwdArgs {
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
-  float* ws;            // [3][rows]: delta, lse2, pm
+  float* ws;            // [3][rows]: -delta, lse2, pm
   int64_t rows;         // batch * heads * t
   int64_t heads, t, s;
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void bwd_stats(BwdArgs a) {
       // fully masked: lse = fill + log(s) is the fill in fp32 (uniform row, P = 1/s)
       if (a.masked) pm = (lse2 - a.fill2 < 64.f) ? 1.0f / static_cast<float>(a.s) : fast_exp2(a.fill2 - lse2);
     }
-    a.ws[row] = acc;
+    a.ws[row] = -acc;  // -delta: the dP accumulators start from it
     a.ws[a.rows + row] = lse2;
     a.ws[2 * a.rows + row] = pm;
   }
@@ -212,7 +212,7 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
     }
   }
   const int64_t srow = inst * T_ + qrow;
-  const float dl = qrow < T_ ? a.ws[srow] : 0.f;
+  const float ndl = qrow < T_ ? a.ws[srow] : 0.f;  // -delta
   const float lse2 = qrow < T_ ? a.ws[a.rows + srow] : 0.f;
 
   const int ntiles = static_cast<int>((S_ + BN - 1) / BN);
@@ -271,7 +271,8 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
       const unsigned char* kt_l = kbuf(buf, sub);
       const unsigned char* vt_l = vbuf(buf, sub);
       __builtin_amdgcn_s_setprio(1);
-      f32x16 sacc = f32x16{}, pacc = f32x16{};
+      f32x16 sacc = f32x16{};
+      f32x16 pacc = ndl - f32x16{};  // dP^T - delta accumulates from -delta
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         sacc = mfma32<T>(kl.row_frag(kt_l, ks), qreg[ks], sacc);
@@ -291,11 +292,11 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
         for (int i = 0; i < 16; ++i) {
           const int c = (i >> 3) * 16 + (i & 7);
           const bool live = rowok && c < rem && c >= lo && c <= hi;
-          pacc[i] = live ? fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * (pacc[i] - dl) : 0.f;
+          pacc[i] = live ? fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * pacc[i] : 0.f;
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) pacc[i] = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * (pacc[i] - dl);
+        for (int i = 0; i < 16; ++i) pacc[i] = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * pacc[i];
       }
       const u32x4 ds0 = pack8<T>(pacc, 0), ds1 = pack8<T>(pacc, 1);
       __builtin_amdgcn_s_setprio(1);
@@ -445,7 +446,7 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int rb = 16 * hh + 8 * g;
-        const f32x4 d0 = *reinterpret_cast<const f32x4*>(stl + rb);
+        const f32x4 d0 = *reinterpret_cast<const f32x4*>(stl + rb);  // -delta
         const f32x4 d1 = *reinterpret_cast<const f32x4*>(stl + rb + 4);
         const f32x4 l0 = *reinterpret_cast<const f32x4*>(stl + QT + rb);
         const f32x4 l1 = *reinterpret_cast<const f32x4*>(stl + QT + rb + 4);
@@ -453,9 +454,9 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
         for (int j = 0; j < 8; ++j) {
           const int i = 8 * hh + j;
           const float lv = j < 4 ? l0[j] : l1[j - 4];
-          const float dv = j < 4 ? d0[j] : d1[j - 4];
+          const float ndv = j < 4 ? d0[j] : d1[j - 4];
           const float p = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lv));
-          pacc[i] = p * (pacc[i] - dv);
+          pacc[i] = p * (pacc[i] + ndv);
           sacc[i] = p;
         }
       }
@@ -538,7 +539,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_main(BwdArgs a) {
 // occupies for the backward carves (conformance/triton_tile.py). VALU only,
 // one wave per row: bwd_rows_f32<0> owns a query row (dQ), <1> a key row
 // (dK, dV); keys / queries in chunks of 64, one per lane. Row statistics come
-// from the same workspace layout as the 16-bit path (delta, lse2, pm).
+// from the same workspace layout as the 16-bit path (-delta, lse2, pm).
 
 struct GenBwdArgs {
   const float* q;
@@ -584,7 +585,7 @@ __global__ __launch_bounds__(256) void bwd_stats_f32(GenBwdArgs a) {
       lse2 = a.lse[row] * kLog2e;
       if (a.masked) pm = (lse2 - a.fill2 < 64.f) ? 1.0f / static_cast<float>(a.s) : fast_exp2(a.fill2 - lse2);
     }
-    a.ws[row] = acc;
+    a.ws[row] = -acc;  // -delta: the dP accumulators start from it
     a.ws[a.rows + row] = lse2;
     a.ws[2 * a.rows + row] = pm;
   }
@@ -639,7 +640,7 @@ __global__ __launch_bounds__(256) void bwd_rows_f32(GenBwdArgs a, int64_t nrows)
         p = pmp[tq];  // masked score: the row's masked-entry probability, no gradient
       } else {
         p = fast_exp2(__builtin_fmaf(sc, a.c2, -lsep[tq]));
-        ds = p * (dp - delp[tq]);
+        ds = p * (dp + delp[tq]);  // delp holds -delta
       }
     }
     const int64_t n = (hi - c0) < 64 ? (hi - c0) : 64;
