@@ -129,7 +129,7 @@ int pdh_flash_fwd(const void* q, const void* k, const void* v, void* o, float* m
  * use exp(fill - m) / den, and without them a row whose lse lies within
  * 2^6 of the fill (in log2 units) is taken as fully masked (P = 1/s).
  * dout / dq share o / q's strides; dk / dv share k / v's strides.
- * ws: fp32 workspace of 3*batch*heads_q*t elements (delta, log2-domain
+ * ws: fp32 workspace of 3*batch*heads_q*t elements (-delta, log2-domain
  * statistic, masked-entry probability per row; written).
  * dtype PDH_BF16 / PDH_F16: MFMA kernels, e == od in {64, 128}, 16-byte
  * aligned tensors, strides multiples of 8 elements. PDH_F32: the fp32 column
