@@ -18,6 +18,11 @@
  *   pdh_attn_decode    <- the flash row at one query row per head, split over
  *                         the key axis and merged with the associative
  *                         online-softmax combine (zoo/attention.py:40-62)
+ *   pdh_map_chain      <- template "map-chain" (fusion.py:844-854): a pointwise
+ *                         program over one output lattice
+ *   pdh_contract       <- template "contraction-epilogue" (fusion.py:159-324),
+ *                         GEMM shape: sum over k of a broadcast product, the
+ *                         epilogue program fused onto the accumulator
  *
  * Conventions
  *   - Every function returns 0 on success and a nonzero PDH_E* status on
@@ -150,6 +155,71 @@ size_t pdh_attn_decode_workspace(const pdh_attn_geom* geom, int nsplit);
 int pdh_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse_out,
                     const pdh_attn_geom* geom, int dtype, float scale, int nsplit, void* ws,
                     size_t ws_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Elementwise programs. The pointwise chains of the map-chain template and
+ * of a contraction's epilogue are lowered to a small register program, run
+ * per output element by an interpreter whose instruction stream is uniform
+ * across the wave (scalar decode, VGPR-indexed register file): no runtime
+ * compilation. Registers hold fp32.
+ *
+ *   LOAD   r[dst] = operand a at the element (its strides over the output
+ *                   dims; stride 0 broadcasts)
+ *   ACC    r[dst] = the contraction accumulator (pdh_contract epilogues only)
+ *   CONST  r[dst] = imm
+ *   IOTA   r[dst] = coordinate along output dim a, plus that dim's start
+ *   unary  r[dst] = f(r[a])            NEG EXP LOG SQRT TANH SIN COS ABS FLOOR
+ *   binary r[dst] = f(r[a], r[b])      ADD SUB MUL DIV MAX MIN, and the
+ *                                      comparisons EQ NE LT LE GT GE (1 or 0)
+ *   WHERE  r[dst] = r[a] != 0 ? r[b] : r[c]
+ * The result is r[out_reg]. Marker semantics follow the reference's numpy
+ * markers (dsl/markers.py): maximum / minimum, where on a 0/1 mask. */
+#define PDH_EW_MAX_INSNS 64
+#define PDH_EW_MAX_REGS 16
+#define PDH_EW_MAX_OPERANDS 8
+#define PDH_EW_MAX_DIMS 4
+
+enum pdh_ew_op {
+  PDH_EW_LOAD = 0, PDH_EW_ACC, PDH_EW_CONST, PDH_EW_IOTA,
+  PDH_EW_NEG, PDH_EW_EXP, PDH_EW_LOG, PDH_EW_SQRT, PDH_EW_TANH, PDH_EW_SIN, PDH_EW_COS, PDH_EW_ABS, PDH_EW_FLOOR,
+  PDH_EW_ADD, PDH_EW_SUB, PDH_EW_MUL, PDH_EW_DIV, PDH_EW_MAX, PDH_EW_MIN,
+  PDH_EW_EQ, PDH_EW_NE, PDH_EW_LT, PDH_EW_LE, PDH_EW_GT, PDH_EW_GE,
+  PDH_EW_WHERE,
+  PDH_EW_NOPS
+};
+
+typedef struct pdh_ew_insn {
+  uint8_t op, dst, a, b, c, pad0, pad1, pad2;
+  float imm;
+} pdh_ew_insn;
+
+typedef struct pdh_ew_program {
+  int32_t n_insns, n_operands, ndim, out_reg;
+  int64_t shape[PDH_EW_MAX_DIMS];  /* output extents, outermost first (the last dim is fastest) */
+  int64_t start[PDH_EW_MAX_DIMS];  /* each output dim's domain start (IOTA adds it) */
+  int64_t out_stride[PDH_EW_MAX_DIMS];
+  int64_t in_stride[PDH_EW_MAX_OPERANDS][PDH_EW_MAX_DIMS];
+  pdh_ew_insn insns[PDH_EW_MAX_INSNS];
+} pdh_ew_program;
+
+/* The map-chain template: out[c] = program(operands at c) for every
+ * coordinate c of the output lattice (prog->shape, at most 2^31 - 1 elements).
+ * operands[i] / out: device pointers of `dtype` (PDH_F32, PDH_BF16, PDH_F16);
+ * the program computes in fp32 and rounds once on the store. */
+int pdh_map_chain(const pdh_ew_program* prog, const void* const* operands, void* out, int dtype, void* stream);
+
+/* The contraction-epilogue template, GEMM shape, batched:
+ *   acc[b, m, n] = sum_k a[b, m, k] * bt[b, n, k]
+ *   out[b, m, n] = epi(acc[b, m, n], operands at (b, m, n))
+ * a: [batch][m][kp], bt: [batch][n][kp], row-major with kp (the row stride)
+ * a multiple of 64 and columns k..kp-1 zero (the caller pads). The epilogue
+ * program's output dims are (b, m, n) (ndim 3, shape {batch, m, n}); it reads
+ * the accumulator with PDH_EW_ACC and may not LOAD more than n_operands.
+ * dtype PDH_BF16 / PDH_F16: v_mfma_f32_32x32x16, fp32 accumulate, 128x128
+ * workgroup tiles; PDH_F32: the fp32 column (VALU, fp32 throughout). The
+ * sum over k is re-bracketed by 64-wide k tiles (license gemm.k-reassoc). */
+int pdh_contract(const void* a, const void* bt, int64_t batch, int64_t m, int64_t n, int64_t k, int64_t kp,
+                 const pdh_ew_program* epi, const void* const* operands, void* out, int dtype, void* stream);
 
 /* MFMA lane-layout probe (test support): multiplies one 32x16 by 16x32 bf16
  * tile with v_mfma_f32_32x32x16_bf16 and one 16x32 by 32x16 tile with

@@ -30,6 +30,8 @@ EXPORTS = (
     "pdh_flash_bwd",
     "pdh_attn_decode_workspace",
     "pdh_attn_decode",
+    "pdh_map_chain",
+    "pdh_contract",
     "pdh_probe_mfma",
 )
 
@@ -54,6 +56,31 @@ class AttnGeom(C.Structure):
     ]
 
 
+# elementwise programs (pdh_ew_program): limits and opcodes, as include/pdhip.h
+EW_MAX_INSNS, EW_MAX_REGS, EW_MAX_OPERANDS, EW_MAX_DIMS = 64, 16, 8, 4
+EW_OPS = (
+    "LOAD ACC CONST IOTA NEG EXP LOG SQRT TANH SIN COS ABS FLOOR ADD SUB MUL DIV MAX MIN "
+    "EQ NE LT LE GT GE WHERE"
+).split()
+EW = {name: i for i, name in enumerate(EW_OPS)}
+
+
+class EwInsn(C.Structure):
+    _fields_ = [("op", C.c_uint8), ("dst", C.c_uint8), ("a", C.c_uint8), ("b", C.c_uint8), ("c", C.c_uint8),
+                ("pad0", C.c_uint8), ("pad1", C.c_uint8), ("pad2", C.c_uint8), ("imm", C.c_float)]
+
+
+class EwProgram(C.Structure):
+    """pdh_ew_program: a register program over one output lattice."""
+
+    _fields_ = [
+        ("n_insns", C.c_int32), ("n_operands", C.c_int32), ("ndim", C.c_int32), ("out_reg", C.c_int32),
+        ("shape", C.c_int64 * EW_MAX_DIMS), ("start", C.c_int64 * EW_MAX_DIMS),
+        ("out_stride", C.c_int64 * EW_MAX_DIMS), ("in_stride", (C.c_int64 * EW_MAX_DIMS) * EW_MAX_OPERANDS),
+        ("insns", EwInsn * EW_MAX_INSNS),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -72,6 +99,8 @@ def _declare(lib) -> None:
         "pdh_flash_bwd": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, vp]),
         "pdh_attn_decode_workspace": (C.c_size_t, [gp, i32]),
         "pdh_attn_decode": (i32, [vp, vp, vp, vp, vp, gp, i32, f32, i32, vp, C.c_size_t, vp]),
+        "pdh_map_chain": (i32, [C.POINTER(EwProgram), C.POINTER(vp), vp, i32, vp]),
+        "pdh_contract": (i32, [vp, vp, i64, i64, i64, i64, i64, C.POINTER(EwProgram), C.POINTER(vp), vp, i32, vp]),
         "pdh_probe_mfma": (i32, [vp, vp, vp, vp, vp, vp, vp]),
     }
     del fp

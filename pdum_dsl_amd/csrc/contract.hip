@@ -1,0 +1,389 @@
+// The map-chain and contraction-epilogue templates (fusion.py:844-854 and
+// fusion.py:159-324): a pointwise program over one output lattice, and a
+// batched GEMM-shaped contraction with that program fused onto the
+// accumulator before the one store.
+//
+//   map_chain_kernel    one lane = EPT consecutive elements of the output's
+//                       last dim; the program runs in registers (ew.h)
+//   contract_mfma<T>    bf16 / f16: 128 x 128 workgroup tiles, 4 waves of
+//                       64 x 64 (2 x 2 v_mfma_f32_32x32x16), 64-wide k tiles
+//                       copied HBM -> LDS by direct buffer loads, double
+//                       buffered; XOR-swizzled 16-byte slots keep the b128
+//                       operand reads conflict-free for 32- and 64-bank LDS
+//   contract_f32        the fp32 column: 64 x 64 tiles, 4 x 4 outputs per
+//                       lane, VALU fma, k tiles of 16 through LDS
+// The epilogue program runs on the accumulators before the one store:
+// out = epi(acc, operands); the output never makes an HBM round trip.
+#include "attn_common.h"
+#include "ew.h"
+
+namespace pdh {
+namespace {
+
+// ---------------------------------------------------------------- map chain
+
+template <int EPT>
+__global__ __launch_bounds__(256) void map_chain_kernel(pdh_ew_program p, EwOperands ops, void* out, int dtype,
+                                                        uint32_t total) {
+  const uint32_t i0 = (static_cast<uint32_t>(blockIdx.x) * 256u + threadIdx.x) * EPT;
+  if (i0 >= total) return;
+  const int ndim = p.ndim;
+  int c[PDH_EW_MAX_DIMS] = {0, 0, 0, 0};
+  uint32_t rem = i0;
+#pragma unroll
+  for (int d = PDH_EW_MAX_DIMS - 1; d >= 0; --d) {
+    if (d < ndim) {
+      const uint32_t ext = static_cast<uint32_t>(p.shape[d]);
+      c[d] = static_cast<int>(rem % ext);
+      rem /= ext;
+    }
+  }
+  int coord[EPT][PDH_EW_MAX_DIMS];
+  float acc[EPT], res[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+#pragma unroll
+    for (int d = 0; d < PDH_EW_MAX_DIMS; ++d) coord[e][d] = c[d] + (d == ndim - 1 ? e : 0);
+    acc[e] = 0.f;
+  }
+  ew_run<EPT>(p, ops, dtype, coord, acc, res);
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    int64_t off = 0;
+#pragma unroll
+    for (int d = 0; d < PDH_EW_MAX_DIMS; ++d)
+      if (d < ndim) off += static_cast<int64_t>(coord[e][d]) * p.out_stride[d];
+    ew_store(out, off, res[e], dtype);
+  }
+}
+
+// -------------------------------------------------------- contraction (MFMA)
+
+struct ContractArgs {
+  const void* a;
+  const void* bt;
+  void* out;
+  int batch, m, n, k, kp;
+  int tiles_m, tiles_n;
+  int dtype;
+};
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kRowB = kBK * 2;                 // LDS bytes per tile row (64 16-bit k values)
+constexpr int kTileB = kBM * kRowB;            // 16 KB per operand tile
+constexpr int kAccRow = 68;                    // floats per accumulator row in LDS (64 + pad)
+constexpr int kContractLds = 4 * kTileB > 4 * 64 * kAccRow * 4 ? 4 * kTileB : 4 * 64 * kAccRow * 4;
+
+// 16-byte slot of chunk c (0..7) of tile row r is c ^ swz_gemm(r): conflict
+// free for the b128 reads below (16 lanes = rows r0..r0+15 at one chunk on
+// 64 banks, 8 lanes on 32 banks).
+__device__ __forceinline__ int swz_gemm(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// Epilogue coordinates past the output are clamped for the program's loads
+// and never stored.
+template <int EPT>
+__device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const EwOperands& ops, const ContractArgs& a,
+                                                  int b, const int (&rows)[EPT], const int (&cols)[EPT],
+                                                  const float (&acc)[EPT]) {
+  int coord[EPT][PDH_EW_MAX_DIMS];
+  float res[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    coord[e][0] = b;
+    coord[e][1] = rows[e] < a.m ? rows[e] : a.m - 1;
+    coord[e][2] = cols[e] < a.n ? cols[e] : a.n - 1;
+    coord[e][3] = 0;
+  }
+  ew_run<EPT>(p, ops, a.dtype, coord, acc, res);
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    if (rows[e] < a.m && cols[e] < a.n) {
+      const int64_t off = static_cast<int64_t>(b) * p.out_stride[0] + static_cast<int64_t>(rows[e]) * p.out_stride[1] +
+                          static_cast<int64_t>(cols[e]) * p.out_stride[2];
+      ew_store(a.out, off, res[e], a.dtype);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256, 2) void contract_mfma(ContractArgs a, pdh_ew_program p, EwOperands ops) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+  const int wy = w >> 1, wx = w & 1;  // the wave's 64 x 64 quadrant
+  const int per = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x / per, rest = blockIdx.x % per;
+  const int m0 = (rest / a.tiles_n) * kBM, n0 = (rest % a.tiles_n) * kBN;
+  const uint32_t rowb = static_cast<uint32_t>(a.kp) * 2u;
+  const uint16_t* abase = static_cast<const uint16_t*>(a.a) + static_cast<int64_t>(b) * a.m * a.kp;
+  const uint16_t* bbase = static_cast<const uint16_t*>(a.bt) + static_cast<int64_t>(b) * a.n * a.kp;
+  // rows past m (n) read as zero: the buffer ends at the batch slice's last row
+  const rsrc_t ar = make_rsrc(abase, static_cast<uint32_t>(static_cast<int64_t>(a.m) * rowb));
+  const rsrc_t br = make_rsrc(bbase, static_cast<uint32_t>(static_cast<int64_t>(a.n) * rowb));
+
+  // direct loads: 1 KB = 8 tile rows; lane i -> row i / 8, slot i % 8 holds chunk slot ^ swz(row)
+  const int lrow = lane >> 3, slot = lane & 7;
+  uint32_t dma_off[2];  // tile-row parity of the 8-row block decides the swizzle of row 8 j + lrow
+#pragma unroll
+  for (int par = 0; par < 2; ++par) dma_off[par] = lrow * rowb + ((slot ^ swz_gemm(8 * par + lrow)) << 4);
+  auto stage = [&](int kt, int buf) {
+    unsigned char* at = smem + buf * kTileB;
+    unsigned char* bt = smem + (2 + buf) * kTileB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int blk = 4 * i + w;  // 16 blocks of 8 rows per operand tile
+      const uint32_t koff = static_cast<uint32_t>(kt) * kBK * 2u;
+      dma16(ar, at + blk * 1024, dma_off[blk & 1], static_cast<uint32_t>(m0 + 8 * blk) * rowb + koff);
+      dma16(br, bt + blk * 1024, dma_off[blk & 1], static_cast<uint32_t>(n0 + 8 * blk) * rowb + koff);
+    }
+  };
+  // operand reads: row (64 q + 32 t + r32) of a tile, chunk 2 ks + g
+  int rd[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int row = 32 * t + r32;  // + 64 q: a multiple of 16 rows, so the swizzle is unchanged
+      rd[t][ks] = row * kRowB + (((2 * ks + g) ^ swz_gemm(row)) << 4);
+    }
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  const int nkt = a.kp / kBK;
+  stage(0, 0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int buf = kt & 1;
+    wait_vmcnt0();
+    __syncthreads();
+    if (kt + 1 < nkt) stage(kt + 1, buf ^ 1);
+    const unsigned char* at = smem + buf * kTileB + 64 * wy * kRowB;
+    const unsigned char* bt = smem + (2 + buf) * kTileB + 64 * wx * kRowB;
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      u32x4 af[2], bf[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        af[t] = *reinterpret_cast<const u32x4*>(at + rd[t][ks]);
+        bf[t] = *reinterpret_cast<const u32x4*>(bt + rd[t][ks]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<T>(af[i], bf[j], acc[i][j]);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+  wait_vmcnt0();
+
+  // The epilogue reads the accumulators back from LDS (each wave its own
+  // 64 x 64 block, rows padded to 68 floats): one runtime loop, four
+  // consecutive columns per lane, so one copy of the program interpreter.
+  // Accumulator v of tile (i, j) is row 32 i + 8 (v / 4) + 4 g + v % 4,
+  // column 32 j + r32 of the wave's block.
+  __syncthreads();  // every wave is done with the operand tiles
+  float* blkf = reinterpret_cast<float*>(smem) + w * 64 * kAccRow;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) blkf[(32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * kAccRow + 32 * j + r32] = acc[i][j][v];
+  __builtin_amdgcn_wave_barrier();  // the block is wave-private: in-order LDS, no workgroup barrier
+  for (int it = 0; it < 16; ++it) {
+    const int idx = it * 256 + lane * 4;
+    const int row = idx >> 6, col = idx & 63;
+    const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * kAccRow + col);
+    int rows[4], cols[4];
+    float av[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      rows[e] = m0 + 64 * wy + row;
+      cols[e] = n0 + 64 * wx + col + e;
+      av[e] = av4[e];
+    }
+    contract_epilogue<4>(p, ops, a, b, rows, cols, av);
+  }
+}
+
+// ---------------------------------------------------------- contraction (f32)
+
+constexpr int kFT = 64, kFK = 16;
+
+__global__ __launch_bounds__(256) void contract_f32(ContractArgs a, pdh_ew_program p, EwOperands ops) {
+  __shared__ float as[kFK][kFT + 4];  // k-major copies of the two 64-row tiles
+  __shared__ float bs[kFK][kFT + 4];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int per = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x / per, rest = blockIdx.x % per;
+  const int m0 = (rest / a.tiles_n) * kFT, n0 = (rest % a.tiles_n) * kFT;
+  const float* abase = static_cast<const float*>(a.a) + static_cast<int64_t>(b) * a.m * a.kp;
+  const float* bbase = static_cast<const float*>(a.bt) + static_cast<int64_t>(b) * a.n * a.kp;
+  const int lr = tid >> 2, lc = (tid & 3) * 4;  // this lane's tile row and 4 k values per load
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < a.kp; k0 += kFK) {
+    const int am = m0 + lr, bn = n0 + lr;
+    f32x4 av = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f};
+    if (am < a.m) av = *reinterpret_cast<const f32x4*>(abase + static_cast<int64_t>(am) * a.kp + k0 + lc);
+    if (bn < a.n) bv = *reinterpret_cast<const f32x4*>(bbase + static_cast<int64_t>(bn) * a.kp + k0 + lc);
+    __syncthreads();  // the previous tile's reads are done
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      as[lc + j][lr] = av[j];
+      bs[lc + j][lr] = bv[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kFK; ++kk) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(&as[kk][4 * ty]);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(&bs[kk][4 * tx]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(x[i], y[j], acc[i][j]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int rows[4], cols[4];
+    float av[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      rows[j] = m0 + 4 * ty + i;
+      cols[j] = n0 + 4 * tx + j;
+      av[j] = acc[i][j];
+    }
+    contract_epilogue<4>(p, ops, a, b, rows, cols, av);
+  }
+}
+
+// -------------------------------------------------------------- validation
+
+// A program is checked in full on the host before any launch: opcodes,
+// register numbers, operand slots and dims in range.
+int check_program(const pdh_ew_program* p, int ndim, bool allow_acc, const char* fn) {
+  PDH_REQUIRE(p != nullptr, PDH_EINVAL, "%s: null program", fn);
+  PDH_REQUIRE(p->n_insns >= 1 && p->n_insns <= PDH_EW_MAX_INSNS, PDH_EINVAL, "%s: %d instructions (1..%d)", fn,
+              p->n_insns, PDH_EW_MAX_INSNS);
+  PDH_REQUIRE(p->n_operands >= 0 && p->n_operands <= PDH_EW_MAX_OPERANDS, PDH_EINVAL, "%s: %d operands (max %d)", fn,
+              p->n_operands, PDH_EW_MAX_OPERANDS);
+  PDH_REQUIRE(p->ndim >= 1 && p->ndim <= PDH_EW_MAX_DIMS && (ndim < 0 || p->ndim == ndim), PDH_EINVAL,
+              "%s: program ndim %d", fn, p->ndim);
+  PDH_REQUIRE(p->out_reg >= 0 && p->out_reg < PDH_EW_MAX_REGS, PDH_EINVAL, "%s: out_reg %d", fn, p->out_reg);
+  for (int d = 0; d < p->ndim; ++d) PDH_REQUIRE(p->shape[d] >= 1, PDH_EINVAL, "%s: shape[%d] = %lld", fn, d, (long long)p->shape[d]);
+  for (int i = 0; i < p->n_insns; ++i) {
+    const pdh_ew_insn& in = p->insns[i];
+    PDH_REQUIRE(in.op < PDH_EW_NOPS, PDH_EINVAL, "%s: instruction %d: opcode %d", fn, i, in.op);
+    PDH_REQUIRE(in.dst < PDH_EW_MAX_REGS && in.a < PDH_EW_MAX_REGS && in.b < PDH_EW_MAX_REGS && in.c < PDH_EW_MAX_REGS,
+                PDH_EINVAL, "%s: instruction %d: register out of range", fn, i);
+    if (in.op == PDH_EW_LOAD)
+      PDH_REQUIRE(in.a < p->n_operands, PDH_EINVAL, "%s: instruction %d loads operand %d of %d", fn, i, in.a,
+                  p->n_operands);
+    if (in.op == PDH_EW_IOTA)
+      PDH_REQUIRE(in.a < p->ndim, PDH_EINVAL, "%s: instruction %d: iota over dim %d of %d", fn, i, in.a, p->ndim);
+    if (in.op == PDH_EW_ACC) PDH_REQUIRE(allow_acc, PDH_EINVAL, "%s: instruction %d reads an accumulator", fn, i);
+  }
+  return PDH_OK;
+}
+
+// The largest element offset a view with these strides reaches over the
+// program's shape (strides are non-negative: checked).
+int check_view(const pdh_ew_program* p, const int64_t* stride, const char* fn, const char* what) {
+  for (int d = 0; d < p->ndim; ++d)
+    PDH_REQUIRE(stride[d] >= 0, PDH_EINVAL, "%s: %s stride[%d] = %lld (strides are non-negative)", fn, what, d,
+                (long long)stride[d]);
+  return PDH_OK;
+}
+
+int dtype_ok(int dtype) { return dtype == PDH_F32 || dtype == PDH_BF16 || dtype == PDH_F16; }
+
+}  // namespace
+}  // namespace pdh
+
+using namespace pdh;
+
+extern "C" int pdh_map_chain(const pdh_ew_program* prog, const void* const* operands, void* out, int dtype,
+                             void* stream) {
+  int rc = check_program(prog, -1, false, "pdh_map_chain");
+  if (rc) return rc;
+  PDH_REQUIRE(dtype_ok(dtype), PDH_EUNSUPPORTED, "pdh_map_chain: dtype %d", dtype);
+  PDH_REQUIRE(out != nullptr, PDH_EINVAL, "pdh_map_chain: null output");
+  PDH_REQUIRE(prog->n_operands == 0 || operands != nullptr, PDH_EINVAL, "pdh_map_chain: null operand table");
+  int64_t total = 1;
+  for (int d = 0; d < prog->ndim; ++d) total *= prog->shape[d];
+  PDH_REQUIRE(total <= INT32_MAX, PDH_EINVAL, "pdh_map_chain: %lld elements (at most 2^31 - 1 per call)",
+              (long long)total);
+  if ((rc = check_view(prog, prog->out_stride, "pdh_map_chain", "output"))) return rc;
+  EwOperands ops{};
+  for (int i = 0; i < prog->n_operands; ++i) {
+    PDH_REQUIRE(operands[i] != nullptr, PDH_EINVAL, "pdh_map_chain: operand %d is null", i);
+    if ((rc = check_view(prog, prog->in_stride[i], "pdh_map_chain", "operand"))) return rc;
+    ops.p[i] = operands[i];
+  }
+  hipStream_t st = as_stream(stream);
+  const int64_t last = prog->shape[prog->ndim - 1];
+  if (last % 4 == 0) {
+    const int64_t nthreads = total / 4;
+    map_chain_kernel<4><<<dim3(static_cast<unsigned>((nthreads + 255) / 256)), 256, 0, st>>>(
+        *prog, ops, out, dtype, static_cast<uint32_t>(total));
+  } else {
+    map_chain_kernel<1><<<dim3(static_cast<unsigned>((total + 255) / 256)), 256, 0, st>>>(
+        *prog, ops, out, dtype, static_cast<uint32_t>(total));
+  }
+  return check_launch("pdh_map_chain");
+}
+
+extern "C" int pdh_contract(const void* a, const void* bt, int64_t batch, int64_t m, int64_t n, int64_t k,
+                            int64_t kp, const pdh_ew_program* epi, const void* const* operands, void* out, int dtype,
+                            void* stream) {
+  int rc = check_program(epi, 3, true, "pdh_contract");
+  if (rc) return rc;
+  PDH_REQUIRE(dtype_ok(dtype), PDH_EUNSUPPORTED, "pdh_contract: dtype %d", dtype);
+  PDH_REQUIRE(a && bt && out, PDH_EINVAL, "pdh_contract: null pointer");
+  PDH_REQUIRE(batch >= 1 && m >= 1 && n >= 1 && k >= 1, PDH_EINVAL, "pdh_contract: bad shape");
+  PDH_REQUIRE(kp >= k && kp % kBK == 0, PDH_EINVAL, "pdh_contract: kp = %lld must be >= k and a multiple of %d",
+              (long long)kp, kBK);
+  PDH_REQUIRE(epi->shape[0] == batch && epi->shape[1] == m && epi->shape[2] == n, PDH_EINVAL,
+              "pdh_contract: epilogue shape must be {batch, m, n}");
+  PDH_REQUIRE(batch * m * n <= INT32_MAX && m <= INT32_MAX / 2 && n <= INT32_MAX / 2, PDH_EINVAL,
+              "pdh_contract: output too large for one call");
+  PDH_REQUIRE(aligned16(a) && aligned16(bt), PDH_EINVAL, "pdh_contract: a / bt must be 16-byte aligned");
+  PDH_REQUIRE(epi->n_operands == 0 || operands != nullptr, PDH_EINVAL, "pdh_contract: null operand table");
+  if ((rc = check_view(epi, epi->out_stride, "pdh_contract", "output"))) return rc;
+  EwOperands ops{};
+  for (int i = 0; i < epi->n_operands; ++i) {
+    PDH_REQUIRE(operands[i] != nullptr, PDH_EINVAL, "pdh_contract: operand %d is null", i);
+    if ((rc = check_view(epi, epi->in_stride[i], "pdh_contract", "operand"))) return rc;
+    ops.p[i] = operands[i];
+  }
+  hipStream_t st = as_stream(stream);
+  ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+                  static_cast<int>(kp), 0, 0, dtype};
+  if (dtype == PDH_F32) {
+    ca.tiles_m = static_cast<int>((m + kFT - 1) / kFT);
+    ca.tiles_n = static_cast<int>((n + kFT - 1) / kFT);
+    const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
+    PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_contract: grid too large");
+    contract_f32<<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
+    return check_launch("pdh_contract (f32)");
+  }
+  PDH_REQUIRE(m * kp * 2 <= UINT32_MAX && n * kp * 2 <= UINT32_MAX, PDH_EINVAL,
+              "pdh_contract: one batch slice of a / bt must stay under 4 GiB");
+  ca.tiles_m = static_cast<int>((m + kBM - 1) / kBM);
+  ca.tiles_n = static_cast<int>((n + kBN - 1) / kBN);
+  const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
+  PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_contract: grid too large");
+  auto go = [&](auto kern) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                        kContractLds);
+    kern<<<dim3(static_cast<unsigned>(nblk)), 256, kContractLds, st>>>(ca, *epi, ops);
+  };
+  if (dtype == PDH_BF16)
+    go(contract_mfma<__hip_bfloat16>);
+  else
+    go(contract_mfma<_Float16>);
+  return check_launch("pdh_contract (mfma)");
+}

@@ -1,0 +1,190 @@
+"""Lowering of pointwise chains to the elementwise register programs that
+libpdhip's interpreter runs (pdh_ew_program, include/pdhip.h).
+
+A chain is a DAG of tl.pointwise / consts / iotas / broadcasts over LEAVES:
+params (or any node the caller materializes) read with LOAD, and, in a
+contraction epilogue, the accumulator read with ACC. Every node is evaluated
+at the coordinates of one output lattice (``dims``); a leaf whose dims are a
+subset of the lattice is read with stride 0 along the missing dims, which is
+exactly the reference's broadcast (tl.repeat_like / tl.repeat add stride-0
+dims, dialect.py:175-205).
+
+Registers are allocated over a topological order with last-use freeing; a
+chain that needs more than PDH_EW_MAX_REGS live values, more operands than
+PDH_EW_MAX_OPERANDS or more instructions than PDH_EW_MAX_INSNS refuses.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from . import _lib as L
+
+# tl.pointwise markers -> opcodes (the reference's numpy markers, dsl/markers.py)
+_UNARY = {"neg": "NEG", "exp": "EXP", "log": "LOG", "sqrt": "SQRT", "tanh": "TANH", "sin": "SIN", "cos": "COS",
+          "abs": "ABS", "floor": "FLOOR"}
+_BINARY = {"add": "ADD", "sub": "SUB", "mul": "MUL", "div": "DIV", "maximum": "MAX", "minimum": "MIN",
+           "eq": "EQ", "ne": "NE", "lt": "LT", "le": "LE", "gt": "GT", "ge": "GE"}
+_VIEW = ("tl.repeat_like", "tl.repeat", "tl.stage")
+
+
+class Unlowerable(Exception):
+    """The chain has a node the elementwise program cannot express."""
+
+
+@dataclass
+class Lowered:
+    insns: list  # (op, dst, a, b, c, imm)
+    out_reg: int
+    operands: tuple  # leaf nodes in LOAD-slot order
+    dims: tuple  # output lattice dims (ir.Dim), outermost first
+
+    def program(self, out_strides, operand_strides) -> L.EwProgram:
+        """The C struct, given the output's and each operand's element
+        strides over ``dims`` (0 where an operand lacks a dim)."""
+        p = L.EwProgram()
+        p.n_insns = len(self.insns)
+        p.n_operands = len(self.operands)
+        p.ndim = len(self.dims)
+        p.out_reg = self.out_reg
+        for d, dim in enumerate(self.dims):
+            p.shape[d] = dim.size
+            p.start[d] = dim.start
+            p.out_stride[d] = int(out_strides[d])
+        for i, st in enumerate(operand_strides):
+            for d in range(len(self.dims)):
+                p.in_stride[i][d] = int(st[d])
+        for j, (op, dst, a, b, c, imm) in enumerate(self.insns):
+            ins = p.insns[j]
+            ins.op, ins.dst, ins.a, ins.b, ins.c, ins.imm = L.EW[op], dst, a, b, c, float(imm)
+        return p
+
+
+def _const_value(n):
+    if n.op in ("core.const", "tl.const"):
+        return float(n.attr("value"))
+    return None
+
+
+def lower(root, dims, leaves: dict, acc=None) -> Lowered:
+    """Lower the chain ending at ``root``. ``leaves`` maps id(node) -> node
+    for nodes read with LOAD (slot order = first use); ``acc`` is the node
+    read with ACC (a contraction's fold), if any."""
+    names = tuple(d.name for d in dims)
+    order: list = []
+    seen: set = set()
+
+    def visit(n):  # post-order over the chain, stopping at leaves
+        stack = [(n, False)]
+        while stack:
+            x, done = stack.pop()
+            if done:
+                order.append(x)
+                continue
+            if id(x) in seen:
+                continue
+            seen.add(id(x))
+            stack.append((x, True))
+            if id(x) in leaves or (acc is not None and x is acc):
+                continue
+            if x.op in _VIEW:
+                stack.append((x.args[0], False))
+            elif x.op == "tl.pointwise":
+                for a in reversed(x.args):
+                    stack.append((a, False))
+
+    visit(root)
+
+    def skip_view(x):
+        while x.op in _VIEW and id(x) not in leaves and x is not acc:
+            x = x.args[0]
+        return x
+
+    uses: dict[int, int] = {}
+    for x in order:
+        if x.op == "tl.pointwise" and id(x) not in leaves and x is not acc:
+            for a in x.args:
+                a = skip_view(a)
+                uses[id(a)] = uses.get(id(a), 0) + 1
+    root_v = skip_view(root)
+    uses[id(root_v)] = uses.get(id(root_v), 0) + 1
+
+    insns: list = []
+    reg: dict[int, int] = {}
+    free = list(range(L.EW_MAX_REGS - 1, -1, -1))
+    slots: list = []
+
+    def alloc():
+        if not free:
+            raise Unlowerable(f"the chain needs more than {L.EW_MAX_REGS} live registers")
+        return free.pop()
+
+    def release(x):
+        uses[id(x)] -= 1
+        if uses[id(x)] == 0 and x is not root_v:
+            free.append(reg[id(x)])
+
+    for x in order:
+        if x.op in _VIEW and id(x) not in leaves and x is not acc:
+            continue
+        if id(x) in reg:
+            continue
+        if acc is not None and x is acc:
+            r = alloc()
+            insns.append(("ACC", r, 0, 0, 0, 0.0))
+        elif id(x) in leaves:
+            if len(slots) >= L.EW_MAX_OPERANDS:
+                raise Unlowerable(f"the chain reads more than {L.EW_MAX_OPERANDS} operands")
+            for nm in x.type.names:
+                if nm not in names:
+                    raise Unlowerable(f"operand dim {nm!r} is not an output dim")
+            slots.append(x)
+            r = alloc()
+            insns.append(("LOAD", r, len(slots) - 1, 0, 0, 0.0))
+        elif _const_value(x) is not None:
+            r = alloc()
+            insns.append(("CONST", r, 0, 0, 0, _const_value(x)))
+        elif x.op == "tl.iota":
+            nm = x.attr("name")
+            if nm not in names:
+                raise Unlowerable(f"iota over {nm!r}, which is not an output dim")
+            r = alloc()
+            insns.append(("IOTA", r, names.index(nm), 0, 0, 0.0))
+        elif x.op == "tl.pointwise":
+            f = x.attr("f")
+            srcs = [skip_view(a) for a in x.args]
+            regs = [reg[id(a)] for a in srcs]
+            for a in srcs:
+                release(a)
+            if f == "stop_gradient":  # identity in value: max(x, x) is a move
+                r = alloc()
+                insns.append(("MAX", r, regs[0], regs[0], 0, 0.0))
+            elif f in _UNARY:
+                r = alloc()
+                insns.append((_UNARY[f], r, regs[0], 0, 0, 0.0))
+            elif f in _BINARY:
+                r = alloc()
+                insns.append((_BINARY[f], r, regs[0], regs[1], 0, 0.0))
+            elif f == "where":
+                r = alloc()
+                insns.append(("WHERE", r, regs[0], regs[1], regs[2], 0.0))
+            else:
+                raise Unlowerable(f"marker {f!r} has no opcode")
+        else:
+            raise Unlowerable(f"{x.op} is not elementwise-program vocabulary")
+        reg[id(x)] = r
+    if len(insns) > L.EW_MAX_INSNS:
+        raise Unlowerable(f"{len(insns)} instructions (max {L.EW_MAX_INSNS})")
+    return Lowered(insns, reg[id(root_v)], tuple(slots), tuple(dims))
+
+
+def strides_over(arr_strides, arr_names, dims) -> list:
+    """Element strides of an array (dims ``arr_names``) over the lattice
+    ``dims``: the array's stride where it has the dim, 0 (broadcast) where not."""
+    out = []
+    for d in dims:
+        out.append(arr_strides[arr_names.index(d.name)] if d.name in arr_names else 0)
+    return out
+
+
+__all__ = ["Lowered", "Unlowerable", "lower", "strides_over"]

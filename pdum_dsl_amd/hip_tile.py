@@ -18,6 +18,12 @@ a fusion template generated and binds it to a hand-written gfx950 kernel:
     claimed whole by partition.plan_model)   pdh_flash_bwd: yields (out, *grads)
   staged row softmax (fusion.py:339-350)  -> pdh_row_softmax
   staged row statistics (layernorm core + gamma/beta epilogue) -> pdh_layernorm
+  map-chain (fusion.py:844-854)           -> pdh_map_chain: the chain lowered to
+                                             an elementwise register program
+  contraction-epilogue, GEMM shape        -> pdh_contract: the k-tiled fold's
+    (fusion.py:268-324)                      operands (prologue chains run first
+                                             through pdh_map_chain), the epilogue
+                                             program fused onto the accumulator
 
 Anything else raises Untranslatable naming what it could not bind — the
 refusal law of triton_tile.py:216-226 and :617-621. The runner uploads,
@@ -297,18 +303,25 @@ def compile_tile_hip(region: Region, launch: tuple = (), prune: tuple = (), *, d
     fj = match_flash_joint(region)
     if fj is not None:
         return _flash_joint_runner(region, fj, grid, dtype)
-    if dtype != "f32":
-        raise Untranslatable(f"row templates run fp32 only (asked {dtype})")
     sb = recognize_softmax(region)
+    if sb is not None and dtype != "f32":
+        raise Untranslatable(f"row templates run fp32 only (asked {dtype})")
     if sb is not None:
         return _softmax_runner(region, sb, grid)
     lb = recognize_layernorm(region)
+    if lb is not None and dtype != "f32":
+        raise Untranslatable(f"row templates run fp32 only (asked {dtype})")
     if lb is not None:
         return _layernorm_runner(region, lb, grid)
+    cb = recognize_contraction(region)
+    if cb is not None:
+        return _contraction_runner(region, cb, grid, dtype)
+    if recognize_map_chain(region):
+        return _map_chain_runner(region, grid, dtype)
     ops = sorted({n.op for n in walk(region)} - {"core.param", "core.yield"})
     raise Untranslatable(
         f"no HIP binding for this tile region (ops: {', '.join(ops)}); bound templates: flash, "
-        "row-normalization, row-statistics, flash-joint"
+        "row-normalization, row-statistics, flash-joint, map-chain, contraction-epilogue (GEMM shape)"
     )
 
 
@@ -478,3 +491,188 @@ def _flash_joint_runner(region, fj, grid, dtype):
         "artifacts=m,den launches=fwd+bwd"
     )
     return _finish(run, src, grid, "flash-joint")
+
+
+# ------------------------------------------- map-chain and contraction-epilogue
+
+_CHAIN_OPS = {"core.param", "core.yield", "core.const", "tl.const", "tl.iota", "tl.pointwise", "tl.repeat_like",
+              "tl.repeat", "tl.stage"}
+_TORCH_DT = {"f32": "float32", "bf16": "bfloat16", "f16": "float16"}
+
+
+def recognize_map_chain(region: Region) -> bool:
+    y = region.body[-1].args[0]
+    if y.op == "core.tuple" or not hasattr(y.type, "dims") or not y.type.dims:
+        return False
+    return all(n.op in _CHAIN_OPS for n in walk(region))
+
+
+def _upload(torch, arr, names, order, dtype, pad_last=None, zero_fill=False):
+    """A param's numpy array (dims ``names``) as a contiguous device tensor
+    with dims ``order`` (absent dims as size 1), optionally zero-padded in the
+    last dim to ``pad_last``."""
+    a = np.asarray(arr, dtype=np.float32)
+    perm = [names.index(n) for n in order if n in names]
+    a = np.transpose(a, perm)
+    shape = [a.shape[perm.index(names.index(n))] if n in names else 1 for n in order]
+    a = a.reshape(shape)
+    t = torch.as_tensor(np.ascontiguousarray(a)).to(device="cuda", dtype=getattr(torch, _TORCH_DT[dtype]))
+    if pad_last is not None and pad_last != shape[-1]:
+        full = torch.zeros(shape[:-1] + [pad_last], device="cuda", dtype=t.dtype)
+        full[..., : shape[-1]] = t
+        t = full
+    return t
+
+
+def _map_chain_runner(region, grid, dtype):
+    from . import ewprog
+    from . import kernels as K
+
+    y = region.body[-1].args[0]
+    dims = y.type.dims
+    leaves = {id(p): p for p in region.params}
+    try:
+        low = ewprog.lower(y, dims, leaves)
+    except ewprog.Unlowerable as exc:
+        raise Untranslatable(f"map-chain: {exc}") from None
+    idx = [_index(region, p) for p in low.operands]
+    out_names = y.type.names
+
+    def run(values):
+        torch = _torch()
+        ops = [_upload(torch, values[i], p.type.names, p.type.names, dtype) for i, p in zip(idx, low.operands)]
+        strides = [ewprog.strides_over(t.stride(), p.type.names, dims) for t, p in zip(ops, low.operands)]
+        out = torch.empty(tuple(d.size for d in dims), device="cuda", dtype=getattr(torch, _TORCH_DT[dtype]))
+        prog = low.program(out.stride(), strides)
+        K.map_chain(prog, ops, out)
+        torch.cuda.synchronize()
+        return out.float().cpu().numpy().reshape(tuple(d.size for d in dims))
+
+    src = (f"hip:map_chain lattice=({','.join(out_names)}) insns={len(low.insns)} operands={len(low.operands)} "
+           "sweeps=1 stores=1")
+    return _finish(run, src, grid, "map-chain")
+
+
+def recognize_contraction(region: Region):
+    """Bind a contraction-epilogue tile (fusion.py:268-324): the k-tiled
+    accumulation fold over split operand chains, an epilogue over its result.
+    Returns the binding or None; shapes other than GEMM raise Untranslatable."""
+    folds = [n for n in walk(region) if n.op == "tl.fold"]
+    if len(folds) != 1:
+        return None
+    f = folds[0]
+    if tuple(f.attr("state")) != ("acc",) or f.attr("dim") != "ko" or tuple(f.attr("out")) != ("final", 0):
+        return None
+    init, *srcs = f.args
+    if init.op != "tl.const" or float(init.attr("value")) != 0.0:
+        return None
+    if not srcs or any(x.op != "tl.split" for x in srcs):
+        return None
+    k = srcs[0].attr("name")
+    parts = tuple(srcs[0].attr("parts"))
+    if tuple(p for p, _ in parts) != ("ko", "ki") or any(x.attr("name") != k or tuple(x.attr("parts")) != parts
+                                                        for x in srcs):
+        return None
+    step = f.regions[0]
+    y = step.body[-1].args[0]
+    if y.op != "tl.pointwise" or y.attr("f") != "add" or y.args[0] is not step.params[0]:
+        return None
+    part = y.args[1]
+    if part.op != "tl.reduce" or part.attr("f") != "sum":
+        return None
+    rdims = (part.attr("dims"),) if isinstance(part.attr("dims"), str) else tuple(part.attr("dims"))
+    if len(srcs) != 2:
+        raise Untranslatable("contraction-epilogue: only the GEMM shape runs on HIP (plain sum refused)")
+    prod = part.args[0]
+    a_s = b_s = None
+    if prod.op == "tl.pointwise" and prod.attr("f") == "mul" and all(x.op == "tl.repeat_like" for x in prod.args):
+        a_s, b_s = prod.args[0].args[0], prod.args[1].args[0]
+    if a_s is None or a_s.op != "tl.stage" or b_s.op != "tl.stage" or a_s.args[0] is not step.params[1] \
+            or b_s.args[0] is not step.params[2]:
+        raise Untranslatable("contraction-epilogue: only the GEMM shape runs on HIP (rowsum refused)")
+    if rdims != ("ki",):
+        raise Untranslatable(f"contraction-epilogue: one contracted dim on HIP (the step reduces {rdims})")
+    ca, cb = srcs[0].args[0], srcs[1].args[0]
+    keep_a = [nm for nm in ca.type.names if nm != k]
+    keep_b = [nm for nm in cb.type.names if nm != k]
+    riders = [nm for nm in keep_a if nm in keep_b]
+    mdims = [nm for nm in keep_a if nm not in riders]
+    ndims = [nm for nm in keep_b if nm not in riders]
+    if len(riders) > 1 or len(mdims) > 1 or len(ndims) > 1:
+        raise Untranslatable("contraction-epilogue: at most one batch, one m and one n dim on HIP")
+    return {"fold": f, "k": k, "a": ca, "b": cb, "rider": riders[0] if riders else None,
+            "m": mdims[0] if mdims else None, "n": ndims[0] if ndims else None,
+            "K": ca.type.dim(k).size}
+
+
+def _contraction_runner(region, cb, grid, dtype):
+    from . import ewprog
+    from .tl.ir import Dim
+    from . import kernels as K
+
+    y = region.body[-1].args[0]
+    if y.op == "core.tuple":
+        raise Untranslatable("contraction-epilogue with several yields")
+    fold = cb["fold"]
+    out_t = fold.type
+    size = {d.name: d for d in out_t.dims}
+    lattice = tuple(size[nm] if nm is not None else Dim(f"_unit{i}", 0, 1)
+                    for i, nm in enumerate((cb["rider"], cb["m"], cb["n"])))
+    lnames = tuple(d.name for d in lattice)
+    leaves = {id(p): p for p in region.params}
+    try:
+        epi = ewprog.lower(y, lattice, leaves, acc=fold)
+    except ewprog.Unlowerable as exc:
+        raise Untranslatable(f"contraction epilogue: {exc}") from None
+    Kdim = cb["K"]
+    KP = -(-Kdim // 64) * 64
+    k = cb["k"]
+    B_, M_, N_ = (d.size for d in lattice)
+    a_order = (lnames[0], lnames[1], k)
+    b_order = (lnames[0], lnames[2], k)
+
+    def operand(node, order):
+        """A param uploads as is; a prologue chain runs first through pdh_map_chain."""
+        if node.op == "core.param":
+            return ("param", _index(region, node))
+        adims = tuple(size.get(nm) or (node.type.dim(nm) if node.type.has(nm) else Dim(nm, 0, 1)) for nm in order)
+        try:
+            low = ewprog.lower(node, adims, leaves)
+        except ewprog.Unlowerable as exc:
+            raise Untranslatable(f"contraction prologue: {exc}") from None
+        return ("chain", low)
+
+    pa, pb = operand(cb["a"], a_order), operand(cb["b"], b_order)
+    epi_idx = [_index(region, p) for p in epi.operands]
+
+    def run(values):
+        torch = _torch()
+        tdt = getattr(torch, _TORCH_DT[dtype])
+
+        def build(spec, node, order, rows):
+            if spec[0] == "param":
+                return _upload(torch, values[spec[1]], node.type.names, order, dtype, pad_last=KP)
+            low = spec[1]
+            ins = [_upload(torch, values[_index(region, p)], p.type.names, p.type.names, dtype) for p in low.operands]
+            st = [ewprog.strides_over(t.stride(), p.type.names, low.dims) for t, p in zip(ins, low.operands)]
+            buf = torch.zeros((low.dims[0].size, rows, KP), device="cuda", dtype=tdt)
+            prog = low.program(buf.stride(), st)
+            K.map_chain(prog, ins, buf)
+            return buf
+
+        a = build(pa, cb["a"], a_order, M_)
+        bt = build(pb, cb["b"], b_order, N_)
+        ops = [_upload(torch, values[i], p.type.names, p.type.names, dtype) for i, p in zip(epi_idx, epi.operands)]
+        st = [ewprog.strides_over(t.stride(), p.type.names, lattice) for t, p in zip(ops, epi.operands)]
+        out = torch.empty((B_, M_, N_), device="cuda", dtype=tdt)
+        prog = epi.program(out.stride(), st)
+        K.contract(a, bt, Kdim, prog, ops, out)
+        torch.cuda.synchronize()
+        present = [nm for nm in lnames if nm in y.type.names]  # the unit stand-ins drop out
+        full = out.float().cpu().numpy().reshape(tuple(size[nm].size for nm in present))
+        return np.transpose(full, [present.index(nm) for nm in y.type.names])
+
+    kern = "contract_f32" if dtype == "f32" else f"contract_mfma<{dtype}>"
+    src = (f"hip:{kern} batch={B_} m={M_} n={N_} k={Kdim} kp={KP} prologue={pa[0]},{pb[0]} "
+           f"epilogue_insns={len(epi.insns)} operands={len(epi.operands)} stores=1")
+    return _finish(run, src, grid, "contraction-epilogue")

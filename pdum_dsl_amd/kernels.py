@@ -253,6 +253,62 @@ def attn_decode(
     return o, lse
 
 
+# ------------------------------------------------- elementwise programs
+
+
+def _max_offset(prog, strides, ndim) -> int:
+    return sum((int(prog.shape[d]) - 1) * int(strides[d]) for d in range(ndim))
+
+
+def _check_views(prog, operands, out, ndim):
+    """Every view the program reads or writes stays inside its tensor."""
+    if len(operands) != prog.n_operands:
+        raise ValueError(f"program reads {prog.n_operands} operands, {len(operands)} given")
+    dt = out.dtype
+    for i, t in enumerate(operands):
+        if t.dtype != dt:
+            raise ValueError(f"operand {i} is {t.dtype}, the output {dt}: one element type per call")
+        if _max_offset(prog, prog.in_stride[i], ndim) >= t.numel() or t.storage_offset() < 0:
+            raise ValueError(f"operand {i}: the program's view reaches past the tensor")
+    if _max_offset(prog, prog.out_stride, ndim) >= out.numel():
+        raise ValueError("the program's output view reaches past the output tensor")
+
+
+def map_chain(prog: _lib.EwProgram, operands: list, out: torch.Tensor) -> torch.Tensor:
+    """Run an elementwise program (ewprog.lower) over its output lattice:
+    operands and ``out`` share one element type; strides come from the program."""
+    _require_cuda(out, *operands)
+    if out.dtype not in _DT:
+        raise ValueError(f"element type {out.dtype} (f32, bf16, f16)")
+    _check_views(prog, operands, out, prog.ndim)
+    table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
+    _lib.call("pdh_map_chain", C.byref(prog), table, _ptr(out), _DT[out.dtype], C.c_void_p(_stream()))
+    return out
+
+
+def contract(a: torch.Tensor, bt: torch.Tensor, k: int, epi: _lib.EwProgram, operands: list,
+             out: torch.Tensor) -> torch.Tensor:
+    """acc[b, m, n] = sum_k a[b, m, k] bt[b, n, k]; out = epi(acc, operands).
+    a: [batch, m, kp], bt: [batch, n, kp] contiguous, kp % 64 == 0, columns
+    k..kp-1 zero. The epilogue program's lattice is (batch, m, n)."""
+    _require_cuda(a, bt, out, *operands)
+    if a.dim() != 3 or bt.dim() != 3 or not a.is_contiguous() or not bt.is_contiguous():
+        raise ValueError("a and bt must be contiguous [batch, rows, kp]")
+    B, M, KP = a.shape
+    if bt.shape[0] != B or bt.shape[2] != KP or a.dtype != bt.dtype or out.dtype != a.dtype:
+        raise ValueError("a / bt / out shapes or dtypes disagree")
+    N = bt.shape[1]
+    if tuple(epi.shape[d] for d in range(3)) != (B, M, N) or epi.ndim != 3:
+        raise ValueError("the epilogue's lattice must be (batch, m, n)")
+    _check_views(epi, operands, out, 3)
+    table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
+    _lib.call(
+        "pdh_contract", _ptr(a), _ptr(bt), B, M, N, int(k), KP, C.byref(epi), table, _ptr(out), _DT[a.dtype],
+        C.c_void_p(_stream()),
+    )
+    return out
+
+
 def pick_decode_splits(groups: int, s: int, cus: int | None = None) -> int:
     """Splits so the (batch x kv-head x split) grid covers the chip ~8 deep,
     with at least 256 keys per split."""

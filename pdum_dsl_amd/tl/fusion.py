@@ -12,10 +12,15 @@ template rows on the HIP hot path:
                       with a machine, the mask-derived prune (fusion.py:659-690)
   row-normalization   the softmax chain over a param: rows staged once,
                       proved-exact by stage erasure (fusion.py:371-400, 818-825)
+  contraction-epilogue  one sum over a two-operand product (or of one
+                      operand), prologue / epilogue pointwise chains around
+                      it (fusion.py:159-324); the generator emits the k-tiled
+                      accumulation fold, certified proved-licensed under
+                      gemm.k-reassoc (the fold inlines back to one sum)
   row-statistics      the two-pass layernorm core + scale/shift epilogue
                       (fusion.py:403-443, 826-843)
-  map-chain / stencil recognized as plans (fusion.py:844-854); the HIP seat
-                      refuses them (not in this build)
+  map-chain           a pointwise chain over params, consts and iotas
+                      (fusion.py:844-854); proved-exact
 
 Everything else is a RED "uncompiled" group with the reason — never an
 exception (fusion.py:855-868). Plans are data.
@@ -31,7 +36,7 @@ from .certify import Certificate, certify
 from .dialect import OPS, check_tier
 from .interp import Field
 from .ir import F64, Builder, Dim, Region, TensorType, minus_dim, walk
-from .licenses import FLASH_ONLINE_SOFTMAX
+from .licenses import FLASH_ONLINE_SOFTMAX, GEMM_K_REASSOC
 from .launch import fit_affine, propose, tri_eval
 
 _MAP_OPS = frozenset(
@@ -215,6 +220,159 @@ def match_flash(region: Region):
     }
 
 
+# -------------------------------------------------- contraction-epilogue
+
+
+def _uncore(x):
+    """A contraction operand's core: broadcasts peeled (fusion.py:98-122)."""
+    while x.op in ("tl.repeat_like", "tl.repeat"):
+        x = x.args[0]
+    return x
+
+
+def _cone(n) -> set:
+    out, stack = set(), list(n.args)
+    while stack:
+        x = stack.pop()
+        if id(x) in out:
+            continue
+        out.add(id(x))
+        stack.extend(x.args)
+    return out
+
+
+def match_contraction_epilogue(region: Region):
+    """The contraction row (fusion.py:158-254): exactly one OUTER reduce —
+    sum or mean over one or two dims of a two-operand product whose operands
+    both carry the contracted dims (or of a single operand, the plain shape)
+    — and every other node drawn from the recompute-exact vocabulary.
+    Operands may be computed chains; a broadcast pair is the GEMM shape,
+    same-space operands the ROWSUM shape. Anything else declines."""
+    y = region.body[-1].args[0]
+    if y.op == "core.tuple":
+        return None
+    reduces = [n for n in walk(region) if n.op == "tl.reduce"]
+    red = None
+    if len(reduces) == 1:
+        red = reduces[0]
+    else:  # tile-local reduces may live in operand prologues: the outer one's cone holds the rest
+        for r in reduces:
+            cone = _cone(r)
+            if all(o is r or id(o) in cone for o in reduces):
+                red = r
+                break
+    if red is None:
+        return None
+    f = red.attr("f")
+    dims = _dims_of(red)
+    if f not in ("sum", "mean") or len(dims) not in (1, 2):
+        return None
+    for r in reduces:  # a prologue reduce must be tile-local: disjoint from the swept dims
+        if r is not red and set(_dims_of(r)) & set(dims):
+            return None
+    prod = red.args[0]
+    if prod.op == "tl.pointwise" and prod.attr("f") == "mul" and len(prod.args) == 2:
+        cores = [_uncore(x) for x in prod.args]
+    else:  # PLAIN: a sum with no product (bias gradients)
+        cores = [prod]
+    if any(not c.type.has(k) for c in cores for k in dims if isinstance(c.type, TensorType)):
+        return None
+    if any(not isinstance(c.type, TensorType) for c in cores):
+        return None
+    keeps = [tuple(nm for nm in c.type.names if nm not in dims) for c in cores]
+    out = red.type.names
+    if set(out) != set().union(*map(set, keeps)):
+        return None
+    ca = cores[0]
+    cb = cores[1] if len(cores) == 2 else None
+    if cb is None:
+        shape = "plain"
+    else:
+        shape = "rowsum" if ca.type.names == cb.type.names else "gemm"
+    core = {id(red), id(prod)} | {id(r) for r in reduces}
+    for n in walk(region):  # the whole region is exact vocabulary, or decline
+        if id(n) in core or n.op in ("core.yield", "core.param"):
+            continue
+        if n.op not in _EXACT_OPS:
+            return None
+    total = 1
+    for k in dims:
+        kd = ca.type.dim(k)
+        kb = kd if cb is None else cb.type.dim(k)
+        if (kd.start, kd.stop) != (kb.start, kb.stop) or kd.start != 0:
+            return None
+        total *= kd.stop
+    if any(d.start != 0 for d in red.type.dims):
+        return None
+    # the fold runs over the WIDEST contracted dim; the rest reduce inside the step whole
+    k = max(dims, key=lambda nm: ca.type.dim(nm).stop)
+    return {
+        "reduce": red, "k": k, "extent": ca.type.dim(k).stop, "rest": tuple(nm for nm in dims if nm != k),
+        "total": total, "a": ca, "b": cb, "shape": shape, "f": f,
+    }
+
+
+def generate_contraction(region: Region, m: dict, ki: int) -> Region:
+    """The fused tile kernel (fusion.py:268-324): split k into (ko, ki), fold
+    over ko with staged operand slices, the epilogue rebuilt over the
+    accumulator; prologue chains rebuild ahead of the split."""
+    k, extent, red = m["k"], m["extent"], m["reduce"]
+    ko = extent // ki
+    b = Builder(OPS)
+    newp = {id(p): b.param(i, p.type) for i, p in enumerate(region.params)}
+    memo: dict = dict(newp)
+    shape = m["shape"]
+    at = b.emit("tl.split", rebuild_into(b, memo, m["a"]), name=k, parts=(("ko", ko), ("ki", ki)))
+    bt = None
+    if shape != "plain":
+        bt = b.emit("tl.split", rebuild_into(b, memo, m["b"]), name=k, parts=(("ko", ko), ("ki", ki)))
+    acc0 = b.emit("tl.const", value=0.0, dims=tuple((d.name, d.stop) for d in red.type.dims))
+
+    sb = Builder(OPS)
+    p_acc = sb.param(0, acc0.type)
+    p_a = sb.param(1, minus_dim(at.type, "ko"))
+    a_s = sb.emit("tl.stage", p_a, level="shared")
+    if shape == "plain":
+        prod, params = a_s, (p_acc, p_a)
+    else:
+        p_b = sb.param(2, minus_dim(bt.type, "ko"))
+        b_s = sb.emit("tl.stage", p_b, level="shared")
+        params = (p_acc, p_a, p_b)
+        if shape == "rowsum":
+            prod = sb.emit("tl.pointwise", a_s, b_s, f="mul")
+        else:
+            prod = sb.emit("tl.pointwise", sb.emit("tl.repeat_like", a_s, b_s), sb.emit("tl.repeat_like", b_s, a_s),
+                           f="mul")
+    part = sb.emit("tl.reduce", prod, dims=("ki", *m["rest"]), f="sum")
+    nxt = sb.emit("tl.pointwise", p_acc, part, f="add")
+    step = Region(params=params, body=(sb.emit("core.yield", nxt),))
+    srcs = (at,) if shape == "plain" else (at, bt)
+    names = ("a",) if shape == "plain" else ("a", "b")
+    fold = b.emit("tl.fold", acc0, *srcs, regions=(step,), dim="ko", state=("acc",), element=names, out=("final", 0))
+    memo[id(red)] = fold
+    if m["f"] == "mean":  # the divide-by-N finalize: N static, one scalar op
+        memo[id(red)] = b.emit("tl.pointwise", fold, b.emit("core.const", type=F64, value=1.0 / m["total"]), f="mul")
+    y = rebuild_into(b, memo, region.body[-1].args[0])
+    fused = Region(params=tuple(newp[id(p)] for p in region.params), body=(b.emit("core.yield", y),))
+    return check_tier(fused)
+
+
+def contraction_families(region: Region, seed: int = 5):
+    """Adversarial draws for a contraction's differential tier (used when
+    normalization cannot walk back, e.g. a mean's finalize): unit-normal and
+    wide-magnitude operands."""
+    from .interp import field
+
+    def draw(scale, s):
+        def factory():
+            rng = np.random.default_rng(s)
+            return [field(rng.standard_normal(p.type.shape) * scale, p.type.names) for p in region.params]
+
+        return factory
+
+    return (("unit", draw(1.0, seed)), ("wide", draw(64.0, seed + 1)))
+
+
 # ----------------------------------------------------------- generators
 
 
@@ -366,6 +524,8 @@ def _cert_fact(tile: Region, naive: Region, kind: str) -> Certificate:
     if key not in _CERTS:
         if kind == "flash":
             _CERTS[key] = certify(tile, naive, licenses=FLASH_ONLINE_SOFTMAX, families=score_families(naive))
+        elif kind == "contraction":
+            _CERTS[key] = certify(tile, naive, licenses=GEMM_K_REASSOC, families=contraction_families(naive))
         else:
             _CERTS[key] = certify(tile, naive)
     return _CERTS[key]
@@ -475,6 +635,18 @@ def _recognize(region: Region) -> Plan:
         cert = _cert_fact(ckern, csrc, "flash")
         arts = ("m", "den") if fm["artifacts"] else ()
         return Plan((Group("flash", kernel, cert, "yellow", params=(("si", si),), artifacts=arts),))
+    cm = match_contraction_epilogue(region)
+    if cm is not None:
+        ki = pick_ki(cm["extent"])
+        kernel = generate_contraction(region, cm, ki)
+        csrc, ckern = region, kernel
+        if oversized(region, CERT_CAP):  # certify the shrunk twin: the program, not the size
+            shr = shrink(region, CERT_CAP)
+            cm2 = match_contraction_epilogue(shr) if shr is not None else None
+            if cm2 is not None:
+                csrc, ckern = shr, generate_contraction(shr, cm2, pick_ki(cm2["extent"]))
+        cert = _cert_fact(ckern, csrc, "contraction")
+        return Plan((Group("contraction-epilogue", kernel, cert, "yellow", params=(("ki", ki), ("shape", cm["shape"]))),))
     sm = match_softmax(region.body[-1].args[0])
     if sm is not None:
         rows = frozenset(id(p) for p in region.params if p.type.has(sm["s"]))

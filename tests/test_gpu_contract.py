@@ -1,0 +1,156 @@
+"""The map-chain and contraction-epilogue kernels on silicon.
+
+Through the HIP seat (compile_tile_hip on the planner's generated kernels)
+against the float64 oracle evaluation of the naive region
+(oracle.region_eval) and numpy closed forms, at the reference's own subject
+(relu(a @ b + bias), test_fusion.py:21-42) and at ragged and larger shapes;
+and the C ABI directly against a plain fp32 torch reference (pdh_contract with
+an identity epilogue is a batched GEMM), plus the refusal of malformed
+programs before any launch."""
+
+import numpy as np
+import pytest
+
+from tests.test_contraction_mapchain import _oracle, chain_subject, gemm_subject
+from tests.tolerances import assert_fp32, assert_lowp
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _gelu_chain_subject(M, K, N, seed=7):
+    """gelu_tanh(x) @ w + b: a computed prologue operand, then a bias epilogue."""
+    from pdum_dsl_amd.tl.dialect import OPS
+    from pdum_dsl_amd.tl.ir import F64, Builder, Region, tensor_type
+
+    rng = np.random.default_rng(seed)
+    b = Builder(OPS)
+    c = lambda v: b.emit("core.const", type=F64, value=float(v))  # noqa: E731
+    x = b.param(0, tensor_type(("t", "d"), (M, K)))
+    w = b.param(1, tensor_type(("d", "f"), (K, N)))
+    bias = b.param(2, tensor_type(("f",), (N,)))
+    x3 = b.emit("tl.pointwise", b.emit("tl.pointwise", x, x, f="mul"), x, f="mul")
+    inner = b.emit("tl.pointwise", b.emit("tl.pointwise", x, b.emit("tl.pointwise", x3, c(0.044715), f="mul"),
+                                          f="add"), c(0.7978845608028654), f="mul")
+    gx = b.emit("tl.pointwise", b.emit("tl.pointwise", x, c(0.5), f="mul"),
+                b.emit("tl.pointwise", b.emit("tl.pointwise", inner, f="tanh"), c(1.0), f="add"), f="mul")
+    prod = b.emit("tl.pointwise", b.emit("tl.repeat_like", gx, w), b.emit("tl.repeat_like", w, gx), f="mul")
+    z = b.emit("tl.reduce", prod, dims=("d",), f="sum")
+    y = b.emit("tl.pointwise", z, b.emit("tl.repeat_like", bias, z), f="add")
+    region = Region(params=(x, w, bias), body=(b.emit("core.yield", y),))
+    return region, [rng.standard_normal((M, K)) * 0.5, rng.standard_normal((K, N)) * K**-0.5,
+                    rng.standard_normal(N)]
+
+
+def _seat(region, dtype):
+    from pdum_dsl_amd.hip_tile import compile_tile_hip
+    from pdum_dsl_amd.tl import fusion
+
+    (g,) = fusion.plan_region(region).groups
+    return g, compile_tile_hip(g.kernel, g.launch, g.prune, dtype=dtype)
+
+
+def _check(got, want, dtype, what, k=1):
+    if dtype == "f32":
+        # fp32 accumulation over k terms: 1e-5 of the result's scale per sqrt(k / 64) of summation depth
+        assert_fp32(got, want, rtol=0.0, atol=1e-5 * max(1.0, float(np.abs(want).max())) * max(1.0, (k / 64) ** 0.5),
+                    what=what)
+    else:
+        assert_lowp(got, want, what=what)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(5, 7), (300, 1000), (129, 1001)])  # 1001: one element per lane
+def test_map_chain_matches_the_oracle(dtype, shape):
+    from pdum_dsl_amd.hip_tile import compile_tile_hip
+
+    region, vals = chain_subject(seed=sum(shape), I=shape[0], J=shape[1])
+    run = compile_tile_hip(region, dtype=dtype)
+    assert run.template == "map-chain" and run.source.startswith("hip:map_chain")
+    got = run(vals)
+    y = region.body[-1].args[0]
+    want = _oracle(region, vals if dtype == "f32" else [_bf16(v) for v in vals], y.type.names)
+    _check(got, want, dtype, f"map chain {shape}")
+
+
+def _bf16(v):
+    return torch.as_tensor(np.asarray(v, dtype=np.float32)).to(torch.bfloat16).float().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize(
+    "M,K,N,epi,rider",
+    [(6, 8, 5, "relu_bias", None), (200, 100, 130, "relu_bias", None), (256, 768, 384, "gelu_tanh", None),
+     (64, 96, 80, None, ("h", 3)), (1, 64, 1, None, None)],
+)
+def test_contraction_epilogue_matches_the_oracle(dtype, M, K, N, epi, rider):
+    region, vals = gemm_subject(M=M, K=K, N=N, epilogue=epi, rider=rider, seed=M + N)
+    g, run = _seat(region, dtype)
+    assert g.template == "contraction-epilogue" and run.template == "contraction-epilogue"
+    got = run(vals)
+    names = region.body[-1].args[0].type.names
+    want = _oracle(region, vals if dtype == "f32" else [_bf16(v) for v in vals], names)
+    _check(got, want, dtype, f"{M}x{K}x{N} {epi} {rider}", k=K)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_a_prologue_chain_runs_before_the_contraction(dtype):
+    region, vals = _gelu_chain_subject(96, 160, 72)
+    g, run = _seat(region, dtype)
+    assert "prologue=chain,param" in run.source
+    got = run(vals)
+    want = _oracle(region, vals if dtype == "f32" else [_bf16(v) for v in vals], ("t", "f"))
+    _check(got, want, dtype, "gelu(x) @ w + b", k=160)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_the_abi_is_a_batched_gemm_with_an_identity_epilogue(dt):
+    from pdum_dsl_amd import _lib as L
+    from pdum_dsl_amd import kernels as K
+
+    g = torch.Generator(device="cuda").manual_seed(11)
+    B, M, N, Kd = 2, 300, 260, 200
+    KP = 256
+    a = torch.zeros(B, M, KP, device="cuda", dtype=dt)
+    bt = torch.zeros(B, N, KP, device="cuda", dtype=dt)
+    a[..., :Kd] = torch.randn(B, M, Kd, device="cuda", generator=g).to(dt)
+    bt[..., :Kd] = torch.randn(B, N, Kd, device="cuda", generator=g).to(dt)
+    out = torch.empty(B, M, N, device="cuda", dtype=dt)
+    p = L.EwProgram()
+    p.n_insns, p.n_operands, p.ndim, p.out_reg = 1, 0, 3, 0
+    for d, (ext, st) in enumerate(zip((B, M, N), out.stride())):
+        p.shape[d], p.out_stride[d] = ext, st
+    p.insns[0].op = L.EW["ACC"]
+    K.contract(a, bt, Kd, p, [], out)
+    torch.cuda.synchronize()
+    ref = torch.bmm(a.float(), bt.float().transpose(1, 2).contiguous())  # fp32 reference on the same inputs
+    if dt == torch.float32:
+        torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-4)
+    else:
+        assert_lowp(out.float().cpu().numpy(), ref.cpu().numpy(), what="bf16 gemm")
+
+
+def test_malformed_programs_refuse_without_launching():
+    from pdum_dsl_amd import _lib as L
+    from pdum_dsl_amd import kernels as K
+
+    x = torch.zeros(4, 8, device="cuda")
+    out = torch.empty(4, 8, device="cuda")
+    p = L.EwProgram()
+    p.n_insns, p.n_operands, p.ndim, p.out_reg = 1, 1, 2, 0
+    p.shape[0], p.shape[1] = 4, 8
+    p.out_stride[0], p.out_stride[1] = 8, 1
+    p.in_stride[0][0], p.in_stride[0][1] = 8, 1
+    p.insns[0].op, p.insns[0].dst = L.EW["LOAD"], 16  # register 16 of 16
+    with pytest.raises(L.PdhError, match="register out of range"):
+        K.map_chain(p, [x], out)
+    p.insns[0].dst, p.insns[0].op = 0, L.EW["ACC"]
+    with pytest.raises(L.PdhError, match="accumulator"):
+        K.map_chain(p, [x], out)
+    p.insns[0].op, p.insns[0].a = L.EW["LOAD"], 3  # operand 3 of 1
+    with pytest.raises(L.PdhError, match="loads operand"):
+        K.map_chain(p, [x], out)
+    p.insns[0].a, p.in_stride[0][0] = 0, 9  # a view past the operand's storage
+    with pytest.raises(ValueError, match="reaches past"):
+        K.map_chain(p, [x], out)

@@ -175,9 +175,18 @@ def test_the_seat_binds_the_hand_written_tile_and_the_row_templates():
 def test_the_seat_refuses_what_it_cannot_bind():
     b = Builder(OPS)
     x = b.param(0, tensor_type(("t", "s"), (4, 6)))
-    y = b.emit("tl.pointwise", x, f="tanh")
+    y = b.emit("tl.reduce", b.emit("tl.pointwise", x, f="tanh"), dims=("s",), f="prod")
     with pytest.raises(H.Untranslatable, match="no HIP binding"):
         H.compile_tile_hip(Region(params=(x,), body=(b.emit("core.yield", y),)))
+    # a rowsum-shaped contraction is planned, but only the GEMM shape has a HIP kernel
+    b = Builder(OPS)
+    x = b.param(0, tensor_type(("t", "s"), (4, 64)))
+    z = b.param(1, tensor_type(("t", "s"), (4, 64)))
+    y = b.emit("tl.reduce", b.emit("tl.pointwise", x, z, f="mul"), dims=("s",), f="sum")
+    (g,) = fusion.plan_region(Region(params=(x, z), body=(b.emit("core.yield", y),))).groups
+    assert g.template == "contraction-epilogue" and dict(g.params)["shape"] == "rowsum"
+    with pytest.raises(H.Untranslatable, match="GEMM shape"):
+        H.compile_tile_hip(g.kernel)
 
 
 def test_launching_a_carried_dim_refuses_with_the_dim_named():
