@@ -38,23 +38,17 @@ __global__ __launch_bounds__(256) void map_chain_kernel(pdh_ew_program p, EwOper
       rem /= ext;
     }
   }
-  int coord[EPT][PDH_EW_MAX_DIMS];
   float acc[EPT], res[EPT];
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) {
+  for (int e = 0; e < EPT; ++e) acc[e] = 0.f;
+  ew_run<EPT>(p, ops, dtype, c, acc, res);
+  int off = 0;
 #pragma unroll
-    for (int d = 0; d < PDH_EW_MAX_DIMS; ++d) coord[e][d] = c[d] + (d == ndim - 1 ? e : 0);
-    acc[e] = 0.f;
-  }
-  ew_run<EPT>(p, ops, dtype, coord, acc, res);
+  for (int d = 0; d < PDH_EW_MAX_DIMS; ++d)
+    if (d < ndim) off += c[d] * static_cast<int>(p.out_stride[d]);
+  const int step = static_cast<int>(p.out_stride[ndim - 1]);
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    int64_t off = 0;
-#pragma unroll
-    for (int d = 0; d < PDH_EW_MAX_DIMS; ++d)
-      if (d < ndim) off += static_cast<int64_t>(coord[e][d]) * p.out_stride[d];
-    ew_store(out, off, res[e], dtype);
-  }
+  for (int e = 0; e < EPT; ++e) ew_store(out, off + e * step, res[e], dtype);
 }
 
 // -------------------------------------------------------- contraction (MFMA)
@@ -79,29 +73,31 @@ constexpr int kContractLds = 4 * kTileB > 4 * 64 * kAccRow * 4 ? 4 * kTileB : 4 
 // 64 banks, 8 lanes on 32 banks).
 __device__ __forceinline__ int swz_gemm(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-// Epilogue coordinates past the output are clamped for the program's loads
-// and never stored.
+// Epilogue for EPT consecutive columns col0.. of one row. Elements past the
+// output are neither computed nor stored, so every operand read stays inside
+// its view: a full group runs once for all EPT columns, a ragged right edge
+// one column at a time.
 template <int EPT>
 __device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const EwOperands& ops, const ContractArgs& a,
-                                                  int b, const int (&rows)[EPT], const int (&cols)[EPT],
-                                                  const float (&acc)[EPT]) {
-  int coord[EPT][PDH_EW_MAX_DIMS];
-  float res[EPT];
+                                                  int b, int row, int col0, const float (&acc)[EPT]) {
+  if (row >= a.m) return;
+  const int64_t rbase = static_cast<int64_t>(b) * p.out_stride[0] + static_cast<int64_t>(row) * p.out_stride[1];
+  if (col0 + EPT <= a.n) {
+    const int c0[PDH_EW_MAX_DIMS] = {b, row, col0, 0};
+    float res[EPT];
+    ew_run<EPT>(p, ops, a.dtype, c0, acc, res);
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    coord[e][0] = b;
-    coord[e][1] = rows[e] < a.m ? rows[e] : a.m - 1;
-    coord[e][2] = cols[e] < a.n ? cols[e] : a.n - 1;
-    coord[e][3] = 0;
+    for (int e = 0; e < EPT; ++e) ew_store(a.out, rbase + static_cast<int64_t>(col0 + e) * p.out_stride[2], res[e], a.dtype);
+    return;
   }
-  ew_run<EPT>(p, ops, a.dtype, coord, acc, res);
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
-    if (rows[e] < a.m && cols[e] < a.n) {
-      const int64_t off = static_cast<int64_t>(b) * p.out_stride[0] + static_cast<int64_t>(rows[e]) * p.out_stride[1] +
-                          static_cast<int64_t>(cols[e]) * p.out_stride[2];
-      ew_store(a.out, off, res[e], a.dtype);
-    }
+    if (col0 + e >= a.n) break;
+    const int c1[PDH_EW_MAX_DIMS] = {b, row, col0 + e, 0};
+    const float a1[1] = {acc[e]};
+    float r1[1];
+    ew_run<1>(p, ops, a.dtype, c1, a1, r1);
+    ew_store(a.out, rbase + static_cast<int64_t>(col0 + e) * p.out_stride[2], r1[0], a.dtype);
   }
 }
 
@@ -197,15 +193,8 @@ __global__ __launch_bounds__(256, 2) void contract_mfma(ContractArgs a, pdh_ew_p
     const int idx = it * 256 + lane * 4;
     const int row = idx >> 6, col = idx & 63;
     const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * kAccRow + col);
-    int rows[4], cols[4];
-    float av[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      rows[e] = m0 + 64 * wy + row;
-      cols[e] = n0 + 64 * wx + col + e;
-      av[e] = av4[e];
-    }
-    contract_epilogue<4>(p, ops, a, b, rows, cols, av);
+    const float av[4] = {av4[0], av4[1], av4[2], av4[3]};
+    contract_epilogue<4>(p, ops, a, b, m0 + 64 * wy + row, n0 + 64 * wx + col, av);
   }
 }
 
@@ -248,15 +237,8 @@ __global__ __launch_bounds__(256) void contract_f32(ContractArgs a, pdh_ew_progr
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    int rows[4], cols[4];
-    float av[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      rows[j] = m0 + 4 * ty + i;
-      cols[j] = n0 + 4 * tx + j;
-      av[j] = acc[i][j];
-    }
-    contract_epilogue<4>(p, ops, a, b, rows, cols, av);
+    const float av[4] = {acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+    contract_epilogue<4>(p, ops, a, b, m0 + 4 * ty + i, n0 + 4 * tx, av);
   }
 }
 
@@ -289,12 +271,17 @@ int check_program(const pdh_ew_program* p, int ndim, bool allow_acc, const char*
   return PDH_OK;
 }
 
-// The largest element offset a view with these strides reaches over the
-// program's shape (strides are non-negative: checked).
+// A view of the program's lattice with these strides: non-negative strides,
+// and its largest element offset under 2^31 (the interpreter's offsets are
+// 32-bit).
 int check_view(const pdh_ew_program* p, const int64_t* stride, const char* fn, const char* what) {
-  for (int d = 0; d < p->ndim; ++d)
-    PDH_REQUIRE(stride[d] >= 0, PDH_EINVAL, "%s: %s stride[%d] = %lld (strides are non-negative)", fn, what, d,
+  int64_t reach = 0;
+  for (int d = 0; d < p->ndim; ++d) {
+    PDH_REQUIRE(stride[d] >= 0 && stride[d] <= INT32_MAX, PDH_EINVAL, "%s: %s stride[%d] = %lld", fn, what, d,
                 (long long)stride[d]);
+    reach += (p->shape[d] - 1) * stride[d];
+    PDH_REQUIRE(reach <= INT32_MAX, PDH_EINVAL, "%s: the %s view spans more than 2^31 elements", fn, what);
+  }
   return PDH_OK;
 }
 

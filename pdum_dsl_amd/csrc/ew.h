@@ -16,7 +16,7 @@ struct EwOperands {
   const void* p[PDH_EW_MAX_OPERANDS];
 };
 
-__device__ __forceinline__ float ew_load(const void* base, int64_t off, int dtype) {
+__device__ __forceinline__ float ew_load(const void* base, int off, int dtype) {
   if (dtype == PDH_F32) return static_cast<const float*>(base)[off];
   const uint16_t b = static_cast<const uint16_t*>(base)[off];
   return dtype == PDH_BF16 ? Elem<__hip_bfloat16>::to_f32(b) : Elem<_Float16>::to_f32(b);
@@ -31,17 +31,22 @@ __device__ __forceinline__ void ew_store(void* base, int64_t off, float v, int d
     static_cast<uint16_t*>(base)[off] = Elem<_Float16>::from_f32(v);
 }
 
-// Runs program p for EPT elements whose output coordinates are coord[e][d]
-// (d < p.ndim); acc[e] is what PDH_EW_ACC reads. Returns r[out_reg] in res.
+// Runs program p for EPT elements: the element at output coordinates c0
+// and the next EPT - 1 along the last output dim (every caller's elements
+// are consecutive there). acc[e] is what PDH_EW_ACC reads; returns
+// r[out_reg] in res. Each instruction is decoded and dispatched once for
+// all EPT elements; operand offsets are 32-bit (callers keep every view
+// under 2^31 elements).
 template <int EPT>
 __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands& ops, int dtype,
-                                       const int (&coord)[EPT][PDH_EW_MAX_DIMS], const float (&acc)[EPT],
+                                       const int (&c0)[PDH_EW_MAX_DIMS], const float (&acc)[EPT],
                                        float (&res)[EPT]) {
   f32x16 r[EPT];
 #pragma unroll
   for (int e = 0; e < EPT; ++e) r[e] = f32x16{};
   const int n = __builtin_amdgcn_readfirstlane(p.n_insns);
   const int ndim = __builtin_amdgcn_readfirstlane(p.ndim);
+  const int last = ndim - 1;
   for (int pc = 0; pc < n; ++pc) {
     const pdh_ew_insn in = p.insns[pc];
     const int op = __builtin_amdgcn_readfirstlane(in.op);
@@ -49,53 +54,69 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
     const int ia = __builtin_amdgcn_readfirstlane(in.a);
     const int ib = __builtin_amdgcn_readfirstlane(in.b);
     const int ic = __builtin_amdgcn_readfirstlane(in.c);
+    auto un = [&](auto f) {
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const float x = r[e][ia], y = r[e][ib];
-      float v;
-      switch (op) {
-        case PDH_EW_LOAD: {
-          int64_t off = 0;
+      for (int e = 0; e < EPT; ++e) r[e][d] = f(r[e][ia]);
+    };
+    auto bin = [&](auto f) {
 #pragma unroll
-          for (int dd = 0; dd < PDH_EW_MAX_DIMS; ++dd)
-            if (dd < ndim) off += static_cast<int64_t>(coord[e][dd]) * p.in_stride[ia][dd];
-          v = ew_load(ops.p[ia], off, dtype);
-          break;
-        }
-        case PDH_EW_ACC: v = acc[e]; break;
-        case PDH_EW_CONST: v = in.imm; break;
-        case PDH_EW_IOTA: {
-          int64_t c = 0;
+      for (int e = 0; e < EPT; ++e) r[e][d] = f(r[e][ia], r[e][ib]);
+    };
+    switch (op) {
+      case PDH_EW_LOAD: {
+        int off = 0;
 #pragma unroll
-          for (int dd = 0; dd < PDH_EW_MAX_DIMS; ++dd)
-            if (dd == ia) c = coord[e][dd] + p.start[dd];
-          v = static_cast<float>(c);
-          break;
-        }
-        case PDH_EW_NEG: v = -x; break;
-        case PDH_EW_EXP: v = expf(x); break;
-        case PDH_EW_LOG: v = logf(x); break;
-        case PDH_EW_SQRT: v = sqrtf(x); break;
-        case PDH_EW_TANH: v = tanhf(x); break;
-        case PDH_EW_SIN: v = sinf(x); break;
-        case PDH_EW_COS: v = cosf(x); break;
-        case PDH_EW_ABS: v = fabsf(x); break;
-        case PDH_EW_FLOOR: v = floorf(x); break;
-        case PDH_EW_ADD: v = x + y; break;
-        case PDH_EW_SUB: v = x - y; break;
-        case PDH_EW_MUL: v = x * y; break;
-        case PDH_EW_DIV: v = x / y; break;
-        case PDH_EW_MAX: v = fmaxf(x, y); break;
-        case PDH_EW_MIN: v = fminf(x, y); break;
-        case PDH_EW_EQ: v = x == y ? 1.f : 0.f; break;
-        case PDH_EW_NE: v = x != y ? 1.f : 0.f; break;
-        case PDH_EW_LT: v = x < y ? 1.f : 0.f; break;
-        case PDH_EW_LE: v = x <= y ? 1.f : 0.f; break;
-        case PDH_EW_GT: v = x > y ? 1.f : 0.f; break;
-        case PDH_EW_GE: v = x >= y ? 1.f : 0.f; break;
-        default: v = x != 0.f ? y : r[e][ic]; break;  // PDH_EW_WHERE
+        for (int dd = 0; dd < PDH_EW_MAX_DIMS; ++dd)
+          if (dd < ndim) off += c0[dd] * static_cast<int>(p.in_stride[ia][dd]);
+        const int step = static_cast<int>(p.in_stride[ia][last]);
+        const void* base = ops.p[ia];
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) r[e][d] = ew_load(base, off + e * step, dtype);
+        break;
       }
-      r[e][d] = v;
+      case PDH_EW_ACC:
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) r[e][d] = acc[e];
+        break;
+      case PDH_EW_CONST:
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) r[e][d] = in.imm;
+        break;
+      case PDH_EW_IOTA: {
+        int c = 0;
+#pragma unroll
+        for (int dd = 0; dd < PDH_EW_MAX_DIMS; ++dd)
+          if (dd == ia) c = c0[dd] + static_cast<int>(p.start[dd]);
+        const int inc = ia == last ? 1 : 0;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) r[e][d] = static_cast<float>(c + e * inc);
+        break;
+      }
+      case PDH_EW_NEG: un([](float x) { return -x; }); break;
+      case PDH_EW_EXP: un([](float x) { return expf(x); }); break;
+      case PDH_EW_LOG: un([](float x) { return logf(x); }); break;
+      case PDH_EW_SQRT: un([](float x) { return sqrtf(x); }); break;
+      case PDH_EW_TANH: un([](float x) { return tanhf(x); }); break;
+      case PDH_EW_SIN: un([](float x) { return sinf(x); }); break;
+      case PDH_EW_COS: un([](float x) { return cosf(x); }); break;
+      case PDH_EW_ABS: un([](float x) { return fabsf(x); }); break;
+      case PDH_EW_FLOOR: un([](float x) { return floorf(x); }); break;
+      case PDH_EW_ADD: bin([](float x, float y) { return x + y; }); break;
+      case PDH_EW_SUB: bin([](float x, float y) { return x - y; }); break;
+      case PDH_EW_MUL: bin([](float x, float y) { return x * y; }); break;
+      case PDH_EW_DIV: bin([](float x, float y) { return x / y; }); break;
+      case PDH_EW_MAX: bin([](float x, float y) { return fmaxf(x, y); }); break;
+      case PDH_EW_MIN: bin([](float x, float y) { return fminf(x, y); }); break;
+      case PDH_EW_EQ: bin([](float x, float y) { return x == y ? 1.f : 0.f; }); break;
+      case PDH_EW_NE: bin([](float x, float y) { return x != y ? 1.f : 0.f; }); break;
+      case PDH_EW_LT: bin([](float x, float y) { return x < y ? 1.f : 0.f; }); break;
+      case PDH_EW_LE: bin([](float x, float y) { return x <= y ? 1.f : 0.f; }); break;
+      case PDH_EW_GT: bin([](float x, float y) { return x > y ? 1.f : 0.f; }); break;
+      case PDH_EW_GE: bin([](float x, float y) { return x >= y ? 1.f : 0.f; }); break;
+      default:  // PDH_EW_WHERE
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) r[e][d] = r[e][ia] != 0.f ? r[e][ib] : r[e][ic];
+        break;
     }
   }
   const int o = __builtin_amdgcn_readfirstlane(p.out_reg);
