@@ -47,21 +47,24 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
   const int n = __builtin_amdgcn_readfirstlane(p.n_insns);
   const int ndim = __builtin_amdgcn_readfirstlane(p.ndim);
   const int last = ndim - 1;
+  // the next instruction's scalar load is issued before this one executes
+  pdh_ew_insn cur = p.insns[0];
   for (int pc = 0; pc < n; ++pc) {
-    const pdh_ew_insn in = p.insns[pc];
-    const int op = __builtin_amdgcn_readfirstlane(in.op);
-    const int d = __builtin_amdgcn_readfirstlane(in.dst);
-    const int ia = __builtin_amdgcn_readfirstlane(in.a);
-    const int ib = __builtin_amdgcn_readfirstlane(in.b);
-    const int ic = __builtin_amdgcn_readfirstlane(in.c);
-    auto un = [&](auto f) {
+    const pdh_ew_insn nxt = p.insns[pc + 1 < n ? pc + 1 : pc];
+    const int op = __builtin_amdgcn_readfirstlane(cur.op);
+    const int d = __builtin_amdgcn_readfirstlane(cur.dst);
+    const int ia = __builtin_amdgcn_readfirstlane(cur.a);
+    const int ib = __builtin_amdgcn_readfirstlane(cur.b);
+    const int ic = __builtin_amdgcn_readfirstlane(cur.c);
+    // operands read once, results written once: the register file is only
+    // ever touched by single indexed moves, never copied
+    float x[EPT], y[EPT], z[EPT], v[EPT];
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) r[e][d] = f(r[e][ia]);
-    };
-    auto bin = [&](auto f) {
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) r[e][d] = f(r[e][ia], r[e][ib]);
-    };
+    for (int e = 0; e < EPT; ++e) {
+      x[e] = r[e][ia];
+      y[e] = r[e][ib];
+      z[e] = r[e][ic];
+    }
     switch (op) {
       case PDH_EW_LOAD: {
         int off = 0;
@@ -71,16 +74,16 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
         const int step = static_cast<int>(p.in_stride[ia][last]);
         const void* base = ops.p[ia];
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) r[e][d] = ew_load(base, off + e * step, dtype);
+        for (int e = 0; e < EPT; ++e) v[e] = ew_load(base, off + e * step, dtype);
         break;
       }
       case PDH_EW_ACC:
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) r[e][d] = acc[e];
+        for (int e = 0; e < EPT; ++e) v[e] = acc[e];
         break;
       case PDH_EW_CONST:
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) r[e][d] = in.imm;
+        for (int e = 0; e < EPT; ++e) v[e] = cur.imm;
         break;
       case PDH_EW_IOTA: {
         int c = 0;
@@ -89,35 +92,47 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
           if (dd == ia) c = c0[dd] + static_cast<int>(p.start[dd]);
         const int inc = ia == last ? 1 : 0;
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) r[e][d] = static_cast<float>(c + e * inc);
+        for (int e = 0; e < EPT; ++e) v[e] = static_cast<float>(c + e * inc);
         break;
       }
-      case PDH_EW_NEG: un([](float x) { return -x; }); break;
-      case PDH_EW_EXP: un([](float x) { return expf(x); }); break;
-      case PDH_EW_LOG: un([](float x) { return logf(x); }); break;
-      case PDH_EW_SQRT: un([](float x) { return sqrtf(x); }); break;
-      case PDH_EW_TANH: un([](float x) { return tanhf(x); }); break;
-      case PDH_EW_SIN: un([](float x) { return sinf(x); }); break;
-      case PDH_EW_COS: un([](float x) { return cosf(x); }); break;
-      case PDH_EW_ABS: un([](float x) { return fabsf(x); }); break;
-      case PDH_EW_FLOOR: un([](float x) { return floorf(x); }); break;
-      case PDH_EW_ADD: bin([](float x, float y) { return x + y; }); break;
-      case PDH_EW_SUB: bin([](float x, float y) { return x - y; }); break;
-      case PDH_EW_MUL: bin([](float x, float y) { return x * y; }); break;
-      case PDH_EW_DIV: bin([](float x, float y) { return x / y; }); break;
-      case PDH_EW_MAX: bin([](float x, float y) { return fmaxf(x, y); }); break;
-      case PDH_EW_MIN: bin([](float x, float y) { return fminf(x, y); }); break;
-      case PDH_EW_EQ: bin([](float x, float y) { return x == y ? 1.f : 0.f; }); break;
-      case PDH_EW_NE: bin([](float x, float y) { return x != y ? 1.f : 0.f; }); break;
-      case PDH_EW_LT: bin([](float x, float y) { return x < y ? 1.f : 0.f; }); break;
-      case PDH_EW_LE: bin([](float x, float y) { return x <= y ? 1.f : 0.f; }); break;
-      case PDH_EW_GT: bin([](float x, float y) { return x > y ? 1.f : 0.f; }); break;
-      case PDH_EW_GE: bin([](float x, float y) { return x >= y ? 1.f : 0.f; }); break;
+#define PDH_EW_CASE(OPC, EXPR)             \
+  case OPC:                                \
+    _Pragma("unroll") for (int e = 0; e < EPT; ++e) { \
+      const float a_ = x[e], b_ = y[e];    \
+      (void)b_;                            \
+      v[e] = (EXPR);                       \
+    }                                      \
+    break;
+      PDH_EW_CASE(PDH_EW_NEG, -a_)
+      PDH_EW_CASE(PDH_EW_EXP, expf(a_))
+      PDH_EW_CASE(PDH_EW_LOG, logf(a_))
+      PDH_EW_CASE(PDH_EW_SQRT, sqrtf(a_))
+      PDH_EW_CASE(PDH_EW_TANH, tanhf(a_))
+      PDH_EW_CASE(PDH_EW_SIN, sinf(a_))
+      PDH_EW_CASE(PDH_EW_COS, cosf(a_))
+      PDH_EW_CASE(PDH_EW_ABS, fabsf(a_))
+      PDH_EW_CASE(PDH_EW_FLOOR, floorf(a_))
+      PDH_EW_CASE(PDH_EW_ADD, a_ + b_)
+      PDH_EW_CASE(PDH_EW_SUB, a_ - b_)
+      PDH_EW_CASE(PDH_EW_MUL, a_ * b_)
+      PDH_EW_CASE(PDH_EW_DIV, a_ / b_)
+      PDH_EW_CASE(PDH_EW_MAX, fmaxf(a_, b_))
+      PDH_EW_CASE(PDH_EW_MIN, fminf(a_, b_))
+      PDH_EW_CASE(PDH_EW_EQ, a_ == b_ ? 1.f : 0.f)
+      PDH_EW_CASE(PDH_EW_NE, a_ != b_ ? 1.f : 0.f)
+      PDH_EW_CASE(PDH_EW_LT, a_ < b_ ? 1.f : 0.f)
+      PDH_EW_CASE(PDH_EW_LE, a_ <= b_ ? 1.f : 0.f)
+      PDH_EW_CASE(PDH_EW_GT, a_ > b_ ? 1.f : 0.f)
+      PDH_EW_CASE(PDH_EW_GE, a_ >= b_ ? 1.f : 0.f)
+#undef PDH_EW_CASE
       default:  // PDH_EW_WHERE
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) r[e][d] = r[e][ia] != 0.f ? r[e][ib] : r[e][ic];
+        for (int e = 0; e < EPT; ++e) v[e] = x[e] != 0.f ? y[e] : z[e];
         break;
     }
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) r[e][d] = v[e];
+    cur = nxt;
   }
   const int o = __builtin_amdgcn_readfirstlane(p.out_reg);
 #pragma unroll
