@@ -37,7 +37,9 @@
 #ifndef PDHIP_H
 #define PDHIP_H
 
+#if !defined(__HIPCC_RTC__) /* hipRTC's builtins provide size_t */
 #include <stddef.h>
+#endif
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -220,6 +222,25 @@ int pdh_map_chain(const pdh_ew_program* prog, const void* const* operands, void*
  * sum over k is re-bracketed by 64-wide k tiles (license gemm.k-reassoc). */
 int pdh_contract(const void* a, const void* bt, int64_t batch, int64_t m, int64_t n, int64_t k, int64_t kp,
                  const pdh_ew_program* epi, const void* const* operands, void* out, int dtype, void* stream);
+
+/* Runtime specialization of elementwise programs. pdh_map_chain and
+ * pdh_contract first compile the program into straight-line code with hipRTC
+ * (once per distinct program and element type, cached for the process) and
+ * fall back to the interpreter kernels when that is disabled or fails.
+ * pdh_ew_set_jit(0) disables it (1 enables; the default is on unless the
+ * environment sets PDH_JIT=0) and returns the previous setting;
+ * pdh_ew_jit_stats fills {programs compiled, launches through specialized
+ * kernels, compile failures}. */
+int pdh_ew_set_jit(int enable);
+void pdh_ew_jit_stats(int64_t* stats3);
+/* The generated source of a program's specialized kernels (kind 0: map
+ * chain, 1: contraction epilogue) for `dtype`, NUL-terminated into buf
+ * (truncated to n); returns its full length (0 for a malformed program).
+ * The readable counterpart of the reference runner's run.source. */
+size_t pdh_ew_jit_source(const pdh_ew_program* prog, int kind, int dtype, char* buf, size_t n);
+/* Compile that source with hipRTC without loading it (no GPU needed):
+ * PDH_OK, or PDH_ELAUNCH with the compiler log in pdh_last_error(). */
+int pdh_ew_jit_compile(const pdh_ew_program* prog, int kind, int dtype);
 
 /* MFMA lane-layout probe (test support): multiplies one 32x16 by 16x32 bf16
  * tile with v_mfma_f32_32x32x16_bf16 and one 16x32 by 32x16 tile with

@@ -105,19 +105,7 @@ __device__ __forceinline__ int swz_rt(int row) {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// 16 bytes per lane, buffer -> LDS (lane i's bytes land at lds + 16 i; lds is
-// wave-uniform). Inline asm keeps the compiler's wait-count pass from making
-// every later LDS read wait for it: callers wait with s_waitcnt vmcnt(0) and a
-// barrier before reading the tile.
-__device__ __forceinline__ void dma16(rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
-  // the low 32 bits of a generic LDS address are its LDS offset (no address-space cast needed)
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: listed so the compiler knows it changes
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0), "v"(voff), "s"(r), "s"(soff)
-               : "memory", "m0");
-#pragma clang diagnostic pop
-}
+// (dma16 and wait_vmcnt0: dev.h)
 
 // 4 bytes per lane, buffer -> LDS (lane i's dword lands at lds + 4 i).
 __device__ __forceinline__ void dma4(rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
@@ -129,11 +117,6 @@ __device__ __forceinline__ void dma4(rsrc_t r, unsigned char* lds, uint32_t voff
                : "memory", "m0");
 #pragma clang diagnostic pop
 }
-
-// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima), issued through
-// the builtin so the compiler's own wait-count tracking sees it and adds no
-// later vector-memory waits of its own.
-__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
 // ds_read_b64_tr_b16: in each 16-lane group, lane 4k + c supplies the address
 // of 8 bytes (4 elements); lane i of the group receives element (i % 4) of the

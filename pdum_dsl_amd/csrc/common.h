@@ -11,6 +11,7 @@
 #include <string>
 
 #include "../../include/pdhip.h"
+#include "dev.h"
 
 namespace pdh {
 
@@ -45,13 +46,6 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 constexpr int kWave = 64;
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
@@ -77,17 +71,10 @@ __device__ __forceinline__ void gstore(void* base, uint32_t off, V v) {
   *reinterpret_cast<V*>(reinterpret_cast<char*>(base) + off) = v;
 }
 
-// Raw buffer loads: a scalar V# resource over [base, base + bytes), a 32-bit
-// per-lane VGPR offset and a 32-bit scalar offset. Reads past `bytes` return 0
-// (the hardware range check), which zero-pads tail tiles for free, and the
-// address stays one long-lived VGPR instead of a 64-bit pair per load.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int kBufferWord3 = 0x00020000;  // gfx9-family dword3: 32-bit data format, untyped access
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
-                                           kBufferWord3);
-}
+// Raw buffer loads (make_rsrc: dev.h): a 32-bit per-lane VGPR offset and a
+// 32-bit scalar offset. Reads past the resource's end return 0 (the hardware
+// range check), which zero-pads tail tiles for free, and the address stays
+// one long-lived VGPR instead of a 64-bit pair per load.
 __device__ __forceinline__ u32x4 bload128(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
@@ -97,9 +84,6 @@ __device__ __forceinline__ u32x2 bload64(rsrc_t r, uint32_t voff, uint32_t soff)
 __device__ __forceinline__ uint32_t bload32(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
 }
-
-// Wave index as a scalar (uniform) value.
-__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // exp2 of an fp32 argument on the hardware transcendental unit (v_exp_f32).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

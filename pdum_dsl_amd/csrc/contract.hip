@@ -1,245 +1,31 @@
 // The map-chain and contraction-epilogue templates (fusion.py:844-854 and
-// fusion.py:159-324): a pointwise program over one output lattice, and a
-// batched GEMM-shaped contraction with that program fused onto the
-// accumulator before the one store.
-//
-//   map_chain_kernel    one lane = EPT consecutive elements of the output's
-//                       last dim; the program runs in registers (ew.h)
-//   contract_mfma<T>    bf16 / f16: 128 x 128 workgroup tiles, 4 waves of
-//                       64 x 64 (2 x 2 v_mfma_f32_32x32x16), 64-wide k tiles
-//                       copied HBM -> LDS by direct buffer loads, double
-//                       buffered; XOR-swizzled 16-byte slots keep the b128
-//                       operand reads conflict-free for 32- and 64-bank LDS
-//   contract_f32        the fp32 column: 64 x 64 tiles, 4 x 4 outputs per
-//                       lane, VALU fma, k tiles of 16 through LDS
-// The epilogue program runs on the accumulators before the one store:
-// out = epi(acc, operands); the output never makes an HBM round trip.
-#include "attn_common.h"
-#include "ew.h"
+// fusion.py:159-324): the C ABI, its validation, and the launch of either
+// the runtime-specialized kernels (jit.hip) or the interpreter kernels
+// (the bodies of contract_core.h with the program interpreter of ew.h).
+#include <type_traits>
+
+#include "common.h"
+#include "contract_core.h"
+#include "jit.h"
 
 namespace pdh {
 namespace {
 
-// ---------------------------------------------------------------- map chain
+// The interpreter kernels: the bodies of contract_core.h with InterpEval.
 
-template <int EPT>
-__global__ __launch_bounds__(256) void map_chain_kernel(pdh_ew_program p, EwOperands ops, void* out, int dtype,
-                                                        uint32_t total) {
-  const uint32_t i0 = (static_cast<uint32_t>(blockIdx.x) * 256u + threadIdx.x) * EPT;
-  if (i0 >= total) return;
-  const int ndim = p.ndim;
-  int c[PDH_EW_MAX_DIMS] = {0, 0, 0, 0};
-  uint32_t rem = i0;
-#pragma unroll
-  for (int d = PDH_EW_MAX_DIMS - 1; d >= 0; --d) {
-    if (d < ndim) {
-      const uint32_t ext = static_cast<uint32_t>(p.shape[d]);
-      c[d] = static_cast<int>(rem % ext);
-      rem /= ext;
-    }
-  }
-  float acc[EPT], res[EPT];
-#pragma unroll
-  for (int e = 0; e < EPT; ++e) acc[e] = 0.f;
-  ew_run<EPT>(p, ops, dtype, c, acc, res);
-  int off = 0;
-#pragma unroll
-  for (int d = 0; d < PDH_EW_MAX_DIMS; ++d)
-    if (d < ndim) off += c[d] * static_cast<int>(p.out_stride[d]);
-  const int step = static_cast<int>(p.out_stride[ndim - 1]);
-#pragma unroll
-  for (int e = 0; e < EPT; ++e) ew_store(out, off + e * step, res[e], dtype);
+template <int DT, int EPT>
+__global__ __launch_bounds__(256) void map_chain_kernel(pdh_ew_program p, EwOperands ops, void* out, uint32_t total) {
+  map_chain_body<DT, EPT, InterpEval>(p, ops, out, total);
 }
 
-// -------------------------------------------------------- contraction (MFMA)
-
-struct ContractArgs {
-  const void* a;
-  const void* bt;
-  void* out;
-  int batch, m, n, k, kp;
-  int tiles_m, tiles_n;
-  int dtype;
-};
-
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kRowB = kBK * 2;                 // LDS bytes per tile row (64 16-bit k values)
-constexpr int kTileB = kBM * kRowB;            // 16 KB per operand tile
-constexpr int kAccRow = 68;                    // floats per accumulator row in LDS (64 + pad)
-constexpr int kContractLds = 4 * kTileB > 4 * 64 * kAccRow * 4 ? 4 * kTileB : 4 * 64 * kAccRow * 4;
-
-// 16-byte slot of chunk c (0..7) of tile row r is c ^ swz_gemm(r): conflict
-// free for the b128 reads below (16 lanes = rows r0..r0+15 at one chunk on
-// 64 banks, 8 lanes on 32 banks).
-__device__ __forceinline__ int swz_gemm(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-
-// Epilogue for EPT consecutive columns col0.. of one row. Elements past the
-// output are neither computed nor stored, so every operand read stays inside
-// its view: a full group runs once for all EPT columns, a ragged right edge
-// one column at a time.
-template <int EPT>
-__device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const EwOperands& ops, const ContractArgs& a,
-                                                  int b, int row, int col0, const float (&acc)[EPT]) {
-  if (row >= a.m) return;
-  const int64_t rbase = static_cast<int64_t>(b) * p.out_stride[0] + static_cast<int64_t>(row) * p.out_stride[1];
-  if (col0 + EPT <= a.n) {
-    const int c0[PDH_EW_MAX_DIMS] = {b, row, col0, 0};
-    float res[EPT];
-    ew_run<EPT>(p, ops, a.dtype, c0, acc, res);
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) ew_store(a.out, rbase + static_cast<int64_t>(col0 + e) * p.out_stride[2], res[e], a.dtype);
-    return;
-  }
-#pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    if (col0 + e >= a.n) break;
-    const int c1[PDH_EW_MAX_DIMS] = {b, row, col0 + e, 0};
-    const float a1[1] = {acc[e]};
-    float r1[1];
-    ew_run<1>(p, ops, a.dtype, c1, a1, r1);
-    ew_store(a.out, rbase + static_cast<int64_t>(col0 + e) * p.out_stride[2], r1[0], a.dtype);
-  }
-}
-
-template <typename T>
+template <int DT>
 __global__ __launch_bounds__(256, 2) void contract_mfma(ContractArgs a, pdh_ew_program p, EwOperands ops) {
-  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
-  const int wy = w >> 1, wx = w & 1;  // the wave's 64 x 64 quadrant
-  const int per = a.tiles_m * a.tiles_n;
-  const int b = blockIdx.x / per, rest = blockIdx.x % per;
-  const int m0 = (rest / a.tiles_n) * kBM, n0 = (rest % a.tiles_n) * kBN;
-  const uint32_t rowb = static_cast<uint32_t>(a.kp) * 2u;
-  const uint16_t* abase = static_cast<const uint16_t*>(a.a) + static_cast<int64_t>(b) * a.m * a.kp;
-  const uint16_t* bbase = static_cast<const uint16_t*>(a.bt) + static_cast<int64_t>(b) * a.n * a.kp;
-  // rows past m (n) read as zero: the buffer ends at the batch slice's last row
-  const rsrc_t ar = make_rsrc(abase, static_cast<uint32_t>(static_cast<int64_t>(a.m) * rowb));
-  const rsrc_t br = make_rsrc(bbase, static_cast<uint32_t>(static_cast<int64_t>(a.n) * rowb));
-
-  // direct loads: 1 KB = 8 tile rows; lane i -> row i / 8, slot i % 8 holds chunk slot ^ swz(row)
-  const int lrow = lane >> 3, slot = lane & 7;
-  uint32_t dma_off[2];  // tile-row parity of the 8-row block decides the swizzle of row 8 j + lrow
-#pragma unroll
-  for (int par = 0; par < 2; ++par) dma_off[par] = lrow * rowb + ((slot ^ swz_gemm(8 * par + lrow)) << 4);
-  auto stage = [&](int kt, int buf) {
-    unsigned char* at = smem + buf * kTileB;
-    unsigned char* bt = smem + (2 + buf) * kTileB;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int blk = 4 * i + w;  // 16 blocks of 8 rows per operand tile
-      const uint32_t koff = static_cast<uint32_t>(kt) * kBK * 2u;
-      dma16(ar, at + blk * 1024, dma_off[blk & 1], static_cast<uint32_t>(m0 + 8 * blk) * rowb + koff);
-      dma16(br, bt + blk * 1024, dma_off[blk & 1], static_cast<uint32_t>(n0 + 8 * blk) * rowb + koff);
-    }
-  };
-  // operand reads: row (64 q + 32 t + r32) of a tile, chunk 2 ks + g
-  int rd[2][4];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int row = 32 * t + r32;  // + 64 q: a multiple of 16 rows, so the swizzle is unchanged
-      rd[t][ks] = row * kRowB + (((2 * ks + g) ^ swz_gemm(row)) << 4);
-    }
-
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-  const int nkt = a.kp / kBK;
-  stage(0, 0);
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    wait_vmcnt0();
-    __syncthreads();
-    if (kt + 1 < nkt) stage(kt + 1, buf ^ 1);
-    const unsigned char* at = smem + buf * kTileB + 64 * wy * kRowB;
-    const unsigned char* bt = smem + (2 + buf) * kTileB + 64 * wx * kRowB;
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      u32x4 af[2], bf[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        af[t] = *reinterpret_cast<const u32x4*>(at + rd[t][ks]);
-        bf[t] = *reinterpret_cast<const u32x4*>(bt + rd[t][ks]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<T>(af[i], bf[j], acc[i][j]);
-    }
-    __builtin_amdgcn_s_setprio(0);
-  }
-  wait_vmcnt0();
-
-  // The epilogue reads the accumulators back from LDS (each wave its own
-  // 64 x 64 block, rows padded to 68 floats): one runtime loop, four
-  // consecutive columns per lane, so one copy of the program interpreter.
-  // Accumulator v of tile (i, j) is row 32 i + 8 (v / 4) + 4 g + v % 4,
-  // column 32 j + r32 of the wave's block.
-  __syncthreads();  // every wave is done with the operand tiles
-  float* blkf = reinterpret_cast<float*>(smem) + w * 64 * kAccRow;
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) blkf[(32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * kAccRow + 32 * j + r32] = acc[i][j][v];
-  __builtin_amdgcn_wave_barrier();  // the block is wave-private: in-order LDS, no workgroup barrier
-  for (int it = 0; it < 16; ++it) {
-    const int idx = it * 256 + lane * 4;
-    const int row = idx >> 6, col = idx & 63;
-    const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * kAccRow + col);
-    const float av[4] = {av4[0], av4[1], av4[2], av4[3]};
-    contract_epilogue<4>(p, ops, a, b, m0 + 64 * wy + row, n0 + 64 * wx + col, av);
-  }
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kContractLds];
+  contract_mfma_body<DT, InterpEval>(a, p, ops, smem);
 }
-
-// ---------------------------------------------------------- contraction (f32)
-
-constexpr int kFT = 64, kFK = 16;
 
 __global__ __launch_bounds__(256) void contract_f32(ContractArgs a, pdh_ew_program p, EwOperands ops) {
-  __shared__ float as[kFK][kFT + 4];  // k-major copies of the two 64-row tiles
-  __shared__ float bs[kFK][kFT + 4];
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  const int per = a.tiles_m * a.tiles_n;
-  const int b = blockIdx.x / per, rest = blockIdx.x % per;
-  const int m0 = (rest / a.tiles_n) * kFT, n0 = (rest % a.tiles_n) * kFT;
-  const float* abase = static_cast<const float*>(a.a) + static_cast<int64_t>(b) * a.m * a.kp;
-  const float* bbase = static_cast<const float*>(a.bt) + static_cast<int64_t>(b) * a.n * a.kp;
-  const int lr = tid >> 2, lc = (tid & 3) * 4;  // this lane's tile row and 4 k values per load
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < a.kp; k0 += kFK) {
-    const int am = m0 + lr, bn = n0 + lr;
-    f32x4 av = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f};
-    if (am < a.m) av = *reinterpret_cast<const f32x4*>(abase + static_cast<int64_t>(am) * a.kp + k0 + lc);
-    if (bn < a.n) bv = *reinterpret_cast<const f32x4*>(bbase + static_cast<int64_t>(bn) * a.kp + k0 + lc);
-    __syncthreads();  // the previous tile's reads are done
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      as[lc + j][lr] = av[j];
-      bs[lc + j][lr] = bv[j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < kFK; ++kk) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(&as[kk][4 * ty]);
-      const f32x4 y = *reinterpret_cast<const f32x4*>(&bs[kk][4 * tx]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(x[i], y[j], acc[i][j]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float av[4] = {acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
-    contract_epilogue<4>(p, ops, a, b, m0 + 4 * ty + i, n0 + 4 * tx, av);
-  }
+  contract_f32_body<InterpEval>(a, p, ops);
 }
 
 // -------------------------------------------------------------- validation
@@ -311,15 +97,32 @@ extern "C" int pdh_map_chain(const pdh_ew_program* prog, const void* const* oper
     ops.p[i] = operands[i];
   }
   hipStream_t st = as_stream(stream);
-  const int64_t last = prog->shape[prog->ndim - 1];
-  if (last % 4 == 0) {
-    const int64_t nthreads = total / 4;
-    map_chain_kernel<4><<<dim3(static_cast<unsigned>((nthreads + 255) / 256)), 256, 0, st>>>(
-        *prog, ops, out, dtype, static_cast<uint32_t>(total));
-  } else {
-    map_chain_kernel<1><<<dim3(static_cast<unsigned>((total + 255) / 256)), 256, 0, st>>>(
-        *prog, ops, out, dtype, static_cast<uint32_t>(total));
+  const bool four = prog->shape[prog->ndim - 1] % 4 == 0;  // four consecutive elements per lane
+  const int64_t nthreads = four ? total / 4 : total;
+  const dim3 grid(static_cast<unsigned>((nthreads + 255) / 256));
+  uint32_t tot = static_cast<uint32_t>(total);
+  hipFunction_t fns[2];
+  if (jit_get(JitKind::MapChain, *prog, dtype, fns)) {
+    pdh_ew_program pa = *prog;
+    void* args[] = {&pa, &ops, &out, &tot};
+    if (hipModuleLaunchKernel(four ? fns[0] : fns[1], grid.x, 1, 1, 256, 1, 1, 0, st, args, nullptr) != hipSuccess)
+      PDH_REQUIRE(false, PDH_ELAUNCH, "pdh_map_chain: specialized launch failed");
+    jit_count_launch();
+    return PDH_OK;
   }
+  auto go = [&](auto dt) {
+    constexpr int DT = decltype(dt)::value;
+    if (four)
+      map_chain_kernel<DT, 4><<<grid, 256, 0, st>>>(*prog, ops, out, tot);
+    else
+      map_chain_kernel<DT, 1><<<grid, 256, 0, st>>>(*prog, ops, out, tot);
+  };
+  if (dtype == PDH_F32)
+    go(std::integral_constant<int, PDH_F32>{});
+  else if (dtype == PDH_BF16)
+    go(std::integral_constant<int, PDH_BF16>{});
+  else
+    go(std::integral_constant<int, PDH_F16>{});
   return check_launch("pdh_map_chain");
 }
 
@@ -349,11 +152,22 @@ extern "C" int pdh_contract(const void* a, const void* bt, int64_t batch, int64_
   hipStream_t st = as_stream(stream);
   ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
                   static_cast<int>(kp), 0, 0, dtype};
+  hipFunction_t fns[2];
+  const bool spec = jit_get(JitKind::Contract, *epi, dtype, fns);
+  pdh_ew_program pe = *epi;
+  void* args[] = {&ca, &pe, &ops};
   if (dtype == PDH_F32) {
     ca.tiles_m = static_cast<int>((m + kFT - 1) / kFT);
     ca.tiles_n = static_cast<int>((n + kFT - 1) / kFT);
     const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
     PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_contract: grid too large");
+    if (spec) {
+      PDH_REQUIRE(hipModuleLaunchKernel(fns[0], static_cast<unsigned>(nblk), 1, 1, 256, 1, 1, 0, st, args, nullptr) ==
+                      hipSuccess,
+                  PDH_ELAUNCH, "pdh_contract: specialized launch failed");
+      jit_count_launch();
+      return PDH_OK;
+    }
     contract_f32<<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
     return check_launch("pdh_contract (f32)");
   }
@@ -363,14 +177,16 @@ extern "C" int pdh_contract(const void* a, const void* bt, int64_t batch, int64_
   ca.tiles_n = static_cast<int>((n + kBN - 1) / kBN);
   const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
   PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_contract: grid too large");
-  auto go = [&](auto kern) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                        kContractLds);
-    kern<<<dim3(static_cast<unsigned>(nblk)), 256, kContractLds, st>>>(ca, *epi, ops);
-  };
+  if (spec) {
+    PDH_REQUIRE(hipModuleLaunchKernel(fns[0], static_cast<unsigned>(nblk), 1, 1, 256, 1, 1, 0, st, args, nullptr) ==
+                    hipSuccess,
+                PDH_ELAUNCH, "pdh_contract: specialized launch failed");
+    jit_count_launch();
+    return PDH_OK;
+  }
   if (dtype == PDH_BF16)
-    go(contract_mfma<__hip_bfloat16>);
+    contract_mfma<PDH_BF16><<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
   else
-    go(contract_mfma<_Float16>);
+    contract_mfma<PDH_F16><<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
   return check_launch("pdh_contract (mfma)");
 }

@@ -1,0 +1,245 @@
+// Kernel bodies of the map-chain and contraction-epilogue templates,
+// parameterized on the element type (DT) and on the evaluator policy (Eval)
+// that runs the pointwise program: the interpreter (ew.h) in the library
+// build, or a generated straight-line evaluator in the kernels the library
+// specializes at run time (hipRTC compiles this same header).
+//
+//   map_chain_body     one lane = EPT consecutive elements of the output's
+//                      last dim
+//   contract_mfma_body bf16 / f16: 128 x 128 workgroup tiles, 4 waves of
+//                      64 x 64 (2 x 2 v_mfma_f32_32x32x16), 64-wide k tiles
+//                      copied HBM -> LDS by direct buffer loads, double
+//                      buffered; XOR-swizzled 16-byte slots keep the b128
+//                      operand reads conflict-free for 32- and 64-bank LDS
+//   contract_f32_body  the fp32 column: 64 x 64 tiles, 4 x 4 outputs per
+//                      lane, VALU fma, k tiles of 16 through LDS
+// The epilogue program runs on the accumulators before the one store:
+// out = epi(acc, operands); the output never makes an HBM round trip.
+#pragma once
+
+#include "ew.h"
+
+namespace pdh {
+
+struct ContractArgs {
+  const void* a;
+  const void* bt;
+  void* out;
+  int batch, m, n, k, kp;
+  int tiles_m, tiles_n;
+  int dtype;
+};
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kRowB = kBK * 2;       // LDS bytes per tile row (64 16-bit k values)
+constexpr int kTileB = kBM * kRowB;  // 16 KB per operand tile
+constexpr int kAccRow = 68;          // floats per accumulator row in LDS (64 + pad)
+constexpr int kContractLds = 4 * kTileB > 4 * 64 * kAccRow * 4 ? 4 * kTileB : 4 * 64 * kAccRow * 4;
+constexpr int kFT = 64, kFK = 16;    // fp32 column tiles
+
+// ---------------------------------------------------------------- map chain
+
+template <int DT, int EPT, typename Eval>
+__device__ __forceinline__ void map_chain_body(const pdh_ew_program& p, const EwOperands& ops, void* out,
+                                               uint32_t total) {
+  const uint32_t i0 = (static_cast<uint32_t>(blockIdx.x) * 256u + threadIdx.x) * EPT;
+  if (i0 >= total) return;
+  const int ndim = p.ndim;
+  int c[PDH_EW_MAX_DIMS] = {0, 0, 0, 0};
+  uint32_t rem = i0;
+#pragma unroll
+  for (int d = PDH_EW_MAX_DIMS - 1; d >= 0; --d) {
+    if (d < ndim) {
+      const uint32_t ext = static_cast<uint32_t>(p.shape[d]);
+      c[d] = static_cast<int>(rem % ext);
+      rem /= ext;
+    }
+  }
+  float acc[EPT], res[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) acc[e] = 0.f;
+  Eval::template run<EPT>(p, ops, DT, c, acc, res);
+  int off = 0;
+#pragma unroll
+  for (int d = 0; d < PDH_EW_MAX_DIMS; ++d)
+    if (d < ndim) off += c[d] * static_cast<int>(p.out_stride[d]);
+  const int step = static_cast<int>(p.out_stride[ndim - 1]);
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) st_dt<DT>(out, off + e * step, res[e]);
+}
+
+// ------------------------------------------------------------ contraction
+
+// 16-byte slot of chunk c (0..7) of tile row r is c ^ swz_gemm(r): conflict
+// free for the b128 reads below (16 lanes = rows r0..r0+15 at one chunk on
+// 64 banks, 8 lanes on 32 banks).
+__device__ __forceinline__ int swz_gemm(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// Epilogue for EPT consecutive columns col0.. of one row. Elements past the
+// output are neither computed nor stored, so every operand read stays inside
+// its view: a full group runs once for all EPT columns, a ragged right edge
+// one column at a time.
+template <int DT, int EPT, typename Eval>
+__device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const EwOperands& ops, const ContractArgs& a,
+                                                  int b, int row, int col0, const float (&acc)[EPT]) {
+  if (row >= a.m) return;
+  const long long rbase = static_cast<long long>(b) * p.out_stride[0] + static_cast<long long>(row) * p.out_stride[1];
+  if (col0 + EPT <= a.n) {
+    const int c0[PDH_EW_MAX_DIMS] = {b, row, col0, 0};
+    float res[EPT];
+    Eval::template run<EPT>(p, ops, DT, c0, acc, res);
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) st_dt<DT>(a.out, rbase + static_cast<long long>(col0 + e) * p.out_stride[2], res[e]);
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    if (col0 + e >= a.n) break;
+    const int c1[PDH_EW_MAX_DIMS] = {b, row, col0 + e, 0};
+    const float a1[1] = {acc[e]};
+    float r1[1];
+    Eval::template run<1>(p, ops, DT, c1, a1, r1);
+    st_dt<DT>(a.out, rbase + static_cast<long long>(col0 + e) * p.out_stride[2], r1[0]);
+  }
+}
+
+template <int DT, typename Eval>
+__device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const pdh_ew_program& p,
+                                                   const EwOperands& ops, unsigned char* smem) {
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+  const int wy = w >> 1, wx = w & 1;  // the wave's 64 x 64 quadrant
+  const int per = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x / per, rest = blockIdx.x % per;
+  const int m0 = (rest / a.tiles_n) * kBM, n0 = (rest % a.tiles_n) * kBN;
+  const uint32_t rowb = static_cast<uint32_t>(a.kp) * 2u;
+  const uint16_t* abase = static_cast<const uint16_t*>(a.a) + static_cast<long long>(b) * a.m * a.kp;
+  const uint16_t* bbase = static_cast<const uint16_t*>(a.bt) + static_cast<long long>(b) * a.n * a.kp;
+  // rows past m (n) read as zero: the buffer ends at the batch slice's last row
+  const rsrc_t ar = make_rsrc(abase, static_cast<uint32_t>(static_cast<long long>(a.m) * rowb));
+  const rsrc_t br = make_rsrc(bbase, static_cast<uint32_t>(static_cast<long long>(a.n) * rowb));
+
+  // direct loads: 1 KB = 8 tile rows; lane i -> row i / 8, slot i % 8 holds chunk slot ^ swz(row)
+  const int lrow = lane >> 3, slot = lane & 7;
+  uint32_t dma_off[2];  // tile-row parity of the 8-row block decides the swizzle of row 8 j + lrow
+#pragma unroll
+  for (int par = 0; par < 2; ++par) dma_off[par] = lrow * rowb + ((slot ^ swz_gemm(8 * par + lrow)) << 4);
+  auto stage = [&](int kt, int buf) {
+    unsigned char* at = smem + buf * kTileB;
+    unsigned char* bt = smem + (2 + buf) * kTileB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int blk = 4 * i + w;  // 16 blocks of 8 rows per operand tile
+      const uint32_t koff = static_cast<uint32_t>(kt) * kBK * 2u;
+      dma16(ar, at + blk * 1024, dma_off[blk & 1], static_cast<uint32_t>(m0 + 8 * blk) * rowb + koff);
+      dma16(br, bt + blk * 1024, dma_off[blk & 1], static_cast<uint32_t>(n0 + 8 * blk) * rowb + koff);
+    }
+  };
+  // operand reads: row (64 q + 32 t + r32) of a tile, chunk 2 ks + g
+  int rd[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int row = 32 * t + r32;  // + 64 q: a multiple of 16 rows, so the swizzle is unchanged
+      rd[t][ks] = row * kRowB + (((2 * ks + g) ^ swz_gemm(row)) << 4);
+    }
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  const int nkt = a.kp / kBK;
+  stage(0, 0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int buf = kt & 1;
+    wait_vmcnt0();
+    __syncthreads();
+    if (kt + 1 < nkt) stage(kt + 1, buf ^ 1);
+    const unsigned char* at = smem + buf * kTileB + 64 * wy * kRowB;
+    const unsigned char* bt = smem + (2 + buf) * kTileB + 64 * wx * kRowB;
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      u32x4 af[2], bf[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        af[t] = *reinterpret_cast<const u32x4*>(at + rd[t][ks]);
+        bf[t] = *reinterpret_cast<const u32x4*>(bt + rd[t][ks]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32_dt<DT>(af[i], bf[j], acc[i][j]);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+  wait_vmcnt0();
+
+  // The epilogue reads the accumulators back from LDS (each wave its own
+  // 64 x 64 block, rows padded to 68 floats): one runtime loop, four
+  // consecutive columns per lane, so one copy of the program's code.
+  // Accumulator v of tile (i, j) is row 32 i + 8 (v / 4) + 4 g + v % 4,
+  // column 32 j + r32 of the wave's block.
+  __syncthreads();  // every wave is done with the operand tiles
+  float* blkf = reinterpret_cast<float*>(smem) + w * 64 * kAccRow;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) blkf[(32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * kAccRow + 32 * j + r32] = acc[i][j][v];
+  __builtin_amdgcn_wave_barrier();  // the block is wave-private: in-order LDS, no workgroup barrier
+  for (int it = 0; it < 16; ++it) {
+    const int idx = it * 256 + lane * 4;
+    const int row = idx >> 6, col = idx & 63;
+    const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * kAccRow + col);
+    const float av[4] = {av4[0], av4[1], av4[2], av4[3]};
+    contract_epilogue<DT, 4, Eval>(p, ops, a, b, m0 + 64 * wy + row, n0 + 64 * wx + col, av);
+  }
+}
+
+template <typename Eval>
+__device__ __forceinline__ void contract_f32_body(const ContractArgs& a, const pdh_ew_program& p,
+                                                  const EwOperands& ops) {
+  __shared__ float as[kFK][kFT + 4];  // k-major copies of the two 64-row tiles
+  __shared__ float bs[kFK][kFT + 4];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int per = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x / per, rest = blockIdx.x % per;
+  const int m0 = (rest / a.tiles_n) * kFT, n0 = (rest % a.tiles_n) * kFT;
+  const float* abase = static_cast<const float*>(a.a) + static_cast<long long>(b) * a.m * a.kp;
+  const float* bbase = static_cast<const float*>(a.bt) + static_cast<long long>(b) * a.n * a.kp;
+  const int lr = tid >> 2, lc = (tid & 3) * 4;  // this lane's tile row and 4 k values per load
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < a.kp; k0 += kFK) {
+    const int am = m0 + lr, bn = n0 + lr;
+    f32x4 av = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f};
+    if (am < a.m) av = *reinterpret_cast<const f32x4*>(abase + static_cast<long long>(am) * a.kp + k0 + lc);
+    if (bn < a.n) bv = *reinterpret_cast<const f32x4*>(bbase + static_cast<long long>(bn) * a.kp + k0 + lc);
+    __syncthreads();  // the previous tile's reads are done
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      as[lc + j][lr] = av[j];
+      bs[lc + j][lr] = bv[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kFK; ++kk) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(&as[kk][4 * ty]);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(&bs[kk][4 * tx]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(x[i], y[j], acc[i][j]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float av[4] = {acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+    contract_epilogue<PDH_F32, 4, Eval>(p, ops, a, b, m0 + 4 * ty + i, n0 + 4 * tx, av);
+  }
+}
+
+}  // namespace pdh

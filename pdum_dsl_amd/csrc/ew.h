@@ -8,7 +8,7 @@
 // EPT elements per lane share each decoded instruction.
 #pragma once
 
-#include "common.h"
+#include "dev.h"
 
 namespace pdh {
 
@@ -17,19 +17,22 @@ struct EwOperands {
 };
 
 __device__ __forceinline__ float ew_load(const void* base, int off, int dtype) {
-  if (dtype == PDH_F32) return static_cast<const float*>(base)[off];
-  const uint16_t b = static_cast<const uint16_t*>(base)[off];
-  return dtype == PDH_BF16 ? Elem<__hip_bfloat16>::to_f32(b) : Elem<_Float16>::to_f32(b);
+  if (dtype == PDH_F32) return ld_dt<PDH_F32>(base, off);
+  return dtype == PDH_BF16 ? ld_dt<PDH_BF16>(base, off) : ld_dt<PDH_F16>(base, off);
 }
 
-__device__ __forceinline__ void ew_store(void* base, int64_t off, float v, int dtype) {
+__device__ __forceinline__ void ew_store(void* base, long long off, float v, int dtype) {
   if (dtype == PDH_F32)
-    static_cast<float*>(base)[off] = v;
+    st_dt<PDH_F32>(base, off, v);
   else if (dtype == PDH_BF16)
-    static_cast<uint16_t*>(base)[off] = Elem<__hip_bfloat16>::from_f32(v);
+    st_dt<PDH_BF16>(base, off, v);
   else
-    static_cast<uint16_t*>(base)[off] = Elem<_Float16>::from_f32(v);
+    st_dt<PDH_F16>(base, off, v);
 }
+
+// The interpreter as an evaluator policy (the runtime-specialized kernels
+// substitute a generated one with the same interface).
+struct InterpEval;
 
 // Runs program p for EPT elements: the element at output coordinates c0
 // and the next EPT - 1 along the last output dim (every caller's elements
@@ -138,5 +141,14 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
 #pragma unroll
   for (int e = 0; e < EPT; ++e) res[e] = r[e][o];
 }
+
+struct InterpEval {
+  template <int EPT>
+  static __device__ __forceinline__ void run(const pdh_ew_program& p, const EwOperands& ops, int dtype,
+                                             const int (&c0)[PDH_EW_MAX_DIMS], const float (&acc)[EPT],
+                                             float (&res)[EPT]) {
+    ew_run<EPT>(p, ops, dtype, c0, acc, res);
+  }
+};
 
 }  // namespace pdh

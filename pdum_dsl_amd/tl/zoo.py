@@ -193,3 +193,57 @@ def layernorm(rows=4, feat=6, *, affine=True, eps=1e-5, seed=2) -> Subject:
         return out
 
     return Subject(region, inputs, oracle)
+
+
+def linear_gelu(T=8, D=16, F=12, seed=5) -> Subject:
+    """gelu_tanh(x @ w + b): a transformer MLP's up-projection with its bias
+    and activation (the contraction-epilogue row's motivating shape, the
+    reference's relu(a @ b + bias) subject of test_fusion.py:21-42 with the
+    tanh-approximated gelu of gpt2's MLP)."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((T, D))
+    W = rng.standard_normal((D, F)) * D**-0.5
+    Bv = 0.1 * rng.standard_normal(F)
+    b = Builder(OPS)
+    px = b.param(0, tensor_type(("t", "d"), X.shape))
+    pw = b.param(1, tensor_type(("d", "f"), W.shape))
+    pb = b.param(2, tensor_type(("f",), Bv.shape))
+    prod = b.emit("tl.pointwise", b.emit("tl.repeat_like", px, pw), b.emit("tl.repeat_like", pw, px), f="mul")
+    acc = b.emit("tl.reduce", prod, dims=("d",), f="sum")
+    z = b.emit("tl.pointwise", acc, b.emit("tl.repeat_like", pb, acc), f="add")
+    z3 = b.emit("tl.pointwise", b.emit("tl.pointwise", z, z, f="mul"), z, f="mul")
+    inner = b.emit("tl.pointwise", b.emit("tl.pointwise", z, b.emit("tl.pointwise", z3, _c(b, 0.044715), f="mul"),
+                                          f="add"), _c(b, 0.7978845608028654), f="mul")
+    y = b.emit("tl.pointwise", b.emit("tl.pointwise", z, _c(b, 0.5), f="mul"),
+               b.emit("tl.pointwise", b.emit("tl.pointwise", inner, f="tanh"), _c(b, 1.0), f="add"), f="mul")
+    region = Region(params=(px, pw, pb), body=(b.emit("core.yield", y),))
+
+    def oracle(arrs):
+        zz = np.asarray(arrs[0]) @ np.asarray(arrs[1]) + np.asarray(arrs[2])
+        return 0.5 * zz * (1.0 + np.tanh(0.7978845608028654 * (zz + 0.044715 * zz**3)))
+
+    return Subject(region, [Field(X, px.type.dims), Field(W, pw.type.dims), Field(Bv, pb.type.dims)], oracle)
+
+
+def masked_activation(I=5, J=7, seed=1) -> Subject:
+    """where(iota_j > iota_i, tanh(x * s_j) + exp(-|x|), 0): a map chain over
+    a broadcast operand, coordinates and a closed mask."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((I, J))
+    Sv = rng.standard_normal(J)
+    b = Builder(OPS)
+    x = b.param(0, tensor_type(("i", "j"), (I, J)))
+    s = b.param(1, tensor_type(("j",), (J,)))
+    t = b.emit("tl.pointwise", b.emit("tl.pointwise", x, b.emit("tl.repeat_like", s, x), f="mul"), f="tanh")
+    e = b.emit("tl.pointwise", b.emit("tl.pointwise", b.emit("tl.pointwise", x, f="abs"), f="neg"), f="exp")
+    lat = b.emit("tl.const", value=0.0, dims=(("i", I), ("j", J)))
+    m = b.emit("tl.pointwise", b.emit("tl.iota", lat, name="j"), b.emit("tl.iota", lat, name="i"), f="gt")
+    y = b.emit("tl.pointwise", m, b.emit("tl.pointwise", t, e, f="add"), _c(b, 0.0), f="where")
+    region = Region(params=(x, s), body=(b.emit("core.yield", y),))
+
+    def oracle(arrs):
+        xx, ss = np.asarray(arrs[0]), np.asarray(arrs[1])
+        ii, jj = np.meshgrid(np.arange(xx.shape[0]), np.arange(xx.shape[1]), indexing="ij")
+        return np.where(jj > ii, np.tanh(xx * ss) + np.exp(-np.abs(xx)), 0.0)
+
+    return Subject(region, [Field(X, x.type.dims), Field(Sv, s.type.dims)], oracle)

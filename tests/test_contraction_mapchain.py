@@ -15,6 +15,7 @@ of the same region — the lowering, not the kernel, is what this checks; the
 kernel is pinned on the GPU (test_gpu_contract.py)."""
 
 import ctypes as C
+import re
 import subprocess
 import tempfile
 from pathlib import Path
@@ -283,3 +284,42 @@ def test_contraction_binding_reads_riders_and_refuses_more():
     cb = H.recognize_contraction(g.kernel)
     assert (cb["rider"], cb["m"], cb["n"]) == ("h", "m", "n")
     assert sum(1 for n in walk_deep(g.kernel) if n.op == "tl.fold") == 1
+
+
+# --------------------------------------------- runtime specialization (hipRTC)
+
+
+def _zoo_programs():
+    from pdum_dsl_amd.tl import zoo
+
+    subj = zoo.linear_gelu(T=64, D=128, F=96)
+    (g,) = fusion.plan_region(subj.region).groups
+    cb = H.recognize_contraction(g.kernel)
+    lat = (Dim("_u", 0, 1), cb["fold"].type.dim("t"), cb["fold"].type.dim("f"))
+    low = ewprog.lower(g.kernel.body[-1].args[0], lat, {id(p): p for p in g.kernel.params}, acc=cb["fold"])
+    epi = low.program([0, 96, 1], [[0, 0, 1]])
+    m = zoo.masked_activation(I=8, J=16)
+    (g2,) = fusion.plan_region(m.region).groups
+    y = g2.kernel.body[-1].args[0]
+    low2 = ewprog.lower(y, y.type.dims, {id(p): p for p in g2.kernel.params})
+    chain = low2.program([16, 1], [[16, 1], [0, 1]])
+    return epi, chain
+
+
+def test_specialized_kernels_compile_offline_for_every_element_type():
+    """The generated straight-line evaluators compile with hipRTC (no GPU
+    needed) for both templates and all three element types, and the source
+    carries the program: constants as exact hex floats, one statement per
+    instruction."""
+    lib = L.lib()
+    epi, chain = _zoo_programs()
+    for kind, prog in ((1, epi), (0, chain)):
+        for dt in (L.PDH_F32, L.PDH_BF16, L.PDH_F16):
+            rc = lib.pdh_ew_jit_compile(C.byref(prog), kind, dt)
+            assert rc == 0, L.last_error()
+    buf = C.create_string_buffer(1 << 16)
+    n = lib.pdh_ew_jit_source(C.byref(epi), 1, L.PDH_BF16, buf, len(buf))
+    src = buf.value.decode()
+    assert n == len(src) and "0x1.988454p-1f" in src and "tanhf(" in src and "acc[e]" in src
+    assert len(re.findall(r"^      r\d+ = ", src, re.M)) == epi.n_insns  # one statement per instruction
+    assert "contract_mfma_body<PDH_BF16, pdh::GenEval>" in src

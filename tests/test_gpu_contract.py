@@ -154,3 +154,36 @@ def test_malformed_programs_refuse_without_launching():
     p.insns[0].a, p.in_stride[0][0] = 0, 9  # a view past the operand's storage
     with pytest.raises(ValueError, match="reaches past"):
         K.map_chain(p, [x], out)
+
+
+@pytest.mark.parametrize("jit", [True, False])
+def test_the_interpreter_and_the_specialized_kernels_agree(jit):
+    """Both evaluators of one program (pdh_ew_set_jit): the runtime-specialized
+    kernels and the interpreter kernels, each against the oracle; the
+    specialized path is the one that ran when enabled."""
+    import ctypes as C
+
+    from pdum_dsl_amd import _lib as L
+
+    lib = L.lib()
+    prev = lib.pdh_ew_set_jit(1 if jit else 0)
+    try:
+        before = (C.c_int64 * 3)()
+        lib.pdh_ew_jit_stats(before)
+        region, vals = gemm_subject(M=130, K=96, N=70, epilogue="gelu_tanh", seed=3)
+        _, run = _seat(region, "bf16")
+        got = run(vals)
+        want = _oracle(region, [_bf16(v) for v in vals], ("m", "n"))
+        _check(got, want, "bf16", f"gemm jit={jit}", k=96)
+        chain, cvals = chain_subject(seed=4, I=33, J=64)
+        from pdum_dsl_amd.hip_tile import compile_tile_hip
+
+        got = compile_tile_hip(chain, dtype="f32")(cvals)
+        _check(got, _oracle(chain, cvals, ("i", "j")), "f32", f"chain jit={jit}")
+        after = (C.c_int64 * 3)()
+        lib.pdh_ew_jit_stats(after)
+        launched = after[1] - before[1]
+        assert after[2] == before[2], "a specialization failed to compile"
+        assert (launched >= 2) if jit else (launched == 0)
+    finally:
+        lib.pdh_ew_set_jit(prev)
