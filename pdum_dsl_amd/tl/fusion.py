@@ -32,6 +32,7 @@ from dataclasses import dataclass, field, replace
 
 import numpy as np
 
+from .analysis import defanalysis
 from .certify import Certificate, certify
 from .dialect import OPS, check_tier
 from .interp import Field
@@ -516,19 +517,22 @@ def score_families(region: Region, seed: int = 11):
 
 
 CERT_CAP = 128
-_CERTS: dict = {}
+
+
+@defanalysis("fusion.certify", 1)
+def _certify_analysis(tile: Region, naive: Region, *, kind: str) -> Certificate:
+    if kind == "flash":
+        return certify(tile, naive, licenses=FLASH_ONLINE_SOFTMAX, families=score_families(naive))
+    if kind == "contraction":
+        return certify(tile, naive, licenses=GEMM_K_REASSOC, families=contraction_families(naive))
+    return certify(tile, naive)
 
 
 def _cert_fact(tile: Region, naive: Region, kind: str) -> Certificate:
-    key = (tile.key, naive.key, kind)
-    if key not in _CERTS:
-        if kind == "flash":
-            _CERTS[key] = certify(tile, naive, licenses=FLASH_ONLINE_SOFTMAX, families=score_families(naive))
-        elif kind == "contraction":
-            _CERTS[key] = certify(tile, naive, licenses=GEMM_K_REASSOC, families=contraction_families(naive))
-        else:
-            _CERTS[key] = certify(tile, naive)
-    return _CERTS[key]
+    """Certification as a cached fact keyed by both regions' content
+    (the reference caches it the same way, fusion.py:696-715): a warm
+    re-plan certifies nothing."""
+    return _certify_analysis(tile, naive, kind=kind).value
 
 
 def shrink(region: Region, cap: int) -> Region | None:
