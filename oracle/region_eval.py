@@ -17,6 +17,7 @@ planner's numpy interpreter, so each can check the other:
                  (compute.py:184-214; region_evaluator.py:320-352)
   tl.repeat_like / tl.repeat / tl.split / tl.stage / tl.select / tl.iota /
   tl.const       layout views (region_evaluator.py:372-430)
+  tl.rename / tl.take   a relabeling; the gather (indexing.py:120-230)
   tl.fold        a Python loop over the scan dim, each element source
                  selected at the ABSOLUTE coordinate (dialect.py:1448-1470;
                  region_evaluator.py:431-465)
@@ -35,6 +36,7 @@ _PW = {
     "tanh": torch.tanh, "sqrt": torch.sqrt, "sin": torch.sin, "cos": torch.cos, "abs": torch.abs,
     "floor": torch.floor, "eq": torch.eq, "ne": torch.ne, "le": torch.le, "lt": torch.lt, "ge": torch.ge,
     "gt": torch.gt, "stop_gradient": lambda x: x,
+    "zoo.gelu": lambda x: 0.5 * x * (1 + torch.tanh(0.7978845608028654 * (x + 0.044715 * x * x * x))),
 }
 
 
@@ -178,6 +180,20 @@ def _dispatch(n, ev):
         shape[ax] = hi - lo
         coords = torch.arange(lo, hi, dtype=torch.float64).reshape(shape)
         return V(coords.expand([d[2] - d[1] for d in dims]), dims)
+    if op == "tl.rename":  # layout.py rename: a relabeling, no data moves
+        x = ev(n.args[0])
+        return V(x.t, tuple((d.name, d.start, d.stop) for d in n.type.dims))
+    if op == "tl.take":  # indexing.py:192-230: the taken dim replaced in place by idx's dims
+        table, idx = ev(n.args[0]), ev(n.args[1])
+        name = _attr(n, "dim")
+        ax = table.names.index(name)
+        lo, hi = table.dims[ax][1], table.dims[ax][2]
+        it = idx.t.to(torch.int64)
+        if it.numel() and (int(it.min()) < lo or int(it.max()) >= hi):
+            raise IndexError(f"tl.take: index outside [{lo}, {hi}) along {name!r}")
+        got = torch.index_select(table.t, ax, (it - lo).reshape(-1))
+        shape = tuple(table.t.shape[:ax]) + tuple(it.shape) + tuple(table.t.shape[ax + 1:])
+        return V(got.reshape(shape), tuple((d.name, d.start, d.stop) for d in n.type.dims))
     if op == "tl.const":
         dims = tuple((d.name, d.start, d.stop) for d in n.type.dims)
         return V(torch.full([d[2] - d[1] for d in dims], float(_attr(n, "value")), dtype=torch.float64), dims)

@@ -14,6 +14,8 @@ emit and consume (packages/tensorlib/src/pdum/tl/dialect.py:115-487):
   tl.iota       name            the coordinate field along a dim of the lattice
   tl.const      value, dims     a constant field
   tl.fold       dim, state, element, out, step region
+  tl.rename     mapping         renames dims in place (a view: no data moves)
+  tl.take       dim             out = table[idx, rest]: a gather, no template row
   tl.argtopk    (typed only: a non-template op the planner must refuse)
 """
 
@@ -23,7 +25,7 @@ from .ir import F64, BOOL, Builder, Dim, OpDef, Region, Scalar, TensorType, Tupl
 
 MARKERS = (
     "add sub mul div neg exp log maximum minimum tanh sqrt sin cos abs floor "
-    "where eq ne le lt ge gt stop_gradient"
+    "where eq ne le lt ge gt stop_gradient zoo.gelu"
 ).split()
 REDUCERS = ("sum", "max", "min", "prod", "mean")
 
@@ -167,6 +169,30 @@ def _r_fold(args, at, regions):
     return inits[out[1]]
 
 
+def _r_rename(args, at, regions):
+    (x,) = args
+    mapping = dict(at["mapping"])
+    for old in mapping:
+        x.dim(old)
+    return TensorType(tuple(Dim(mapping.get(d.name, d.name), d.start, d.stop) for d in x.dims))
+
+
+def _r_take(args, at, regions):
+    """out = table[idx, rest]: the taken dim is replaced IN PLACE by idx's dims
+    (indexing.py:120-138); idx dims the table already carries must align."""
+    table, idx = args
+    d = table.dim(at["dim"])
+    survivors = {x.name: x for x in table.dims if x.name != d.name}
+    for n in idx.dims:
+        if n.name in survivors and (survivors[n.name].start, survivors[n.name].stop) != (n.start, n.stop):
+            raise TypeError(f"tl.take: idx dim {n.name!r} does not align with the table's")
+    spliced = tuple(n for n in idx.dims if n.name not in survivors)
+    out = []
+    for x in table.dims:
+        out.extend(spliced if x.name == d.name else (x,))
+    return TensorType(tuple(out))
+
+
 def _r_tuple(args, at, regions):
     return TupleType(tuple(args))
 
@@ -196,9 +222,11 @@ OPS: dict[str, OpDef] = {
     "tl.const": OpDef("tl.const", _r_const),
     "tl.fold": OpDef("tl.fold", _r_fold, nregions=1),
     "tl.argtopk": OpDef("tl.argtopk", _r_argtopk),
+    "tl.rename": OpDef("tl.rename", _r_rename),
+    "tl.take": OpDef("tl.take", _r_take),
 }
 
-TILE_OPS = frozenset(OPS) - {"tl.argtopk"}
+TILE_OPS = frozenset(OPS) - {"tl.argtopk", "tl.take"}
 
 
 def builder() -> Builder:

@@ -42,9 +42,10 @@ from .launch import fit_affine, propose, tri_eval
 
 _MAP_OPS = frozenset(
     {"core.param", "core.const", "core.yield", "tl.pointwise", "tl.iota", "tl.const", "tl.select", "tl.split",
-     "tl.repeat", "tl.repeat_like"}
+     "tl.repeat", "tl.repeat_like", "tl.rename"}
 )
-_EXACT_OPS = frozenset({"tl.pointwise", "tl.repeat_like", "tl.repeat", "tl.iota", "core.const", "tl.const"})
+_EXACT_OPS = frozenset({"tl.pointwise", "tl.repeat_like", "tl.rename", "tl.repeat", "tl.iota", "core.const",
+                        "tl.const"})
 
 
 @dataclass(frozen=True)

@@ -29,6 +29,8 @@ _PW = {
     "sqrt": np.sqrt, "sin": np.sin, "cos": np.cos, "abs": np.abs, "floor": np.floor, "where": np.where,
     "eq": np.equal, "ne": np.not_equal, "le": np.less_equal, "lt": np.less, "ge": np.greater_equal,
     "gt": np.greater, "stop_gradient": np.positive,
+    # the composite marker zoo_common.py:20 registers: 0.5 x (1 + tanh(c (x + 0.044715 x^3)))
+    "zoo.gelu": lambda x: 0.5 * x * (1 + np.tanh(0.7978845608028654 * (x + 0.044715 * x * x * x))),
 }
 _RED = {"sum": (np.add, 0.0), "prod": (np.multiply, 1.0), "max": (np.maximum, None), "min": (np.minimum, None)}
 
@@ -145,6 +147,24 @@ def run_region(region: Region, values: list):
             shape[ax] = d.size
             coords = np.arange(d.start, d.stop, dtype=np.int64).reshape(shape)
             return Field(np.broadcast_to(coords, tt.shape), tt.dims)
+        if op == "tl.rename":
+            x = ev(n.args[0])
+            return Field(x.arr, n.type.dims)
+        if op == "tl.take":
+            table, idx = ev(n.args[0]), ev(n.args[1])
+            dim = n.attr("dim")
+            d = table.dims[table.names.index(dim)]
+            ia = np.asarray(idx.arr)
+            if ia.size and (ia.min() < d.start or ia.max() >= d.stop):
+                raise IndexError(f"tl.take: index outside [{d.start}, {d.stop}) along {dim!r}")
+            surv = [x.name for x in table.dims if x.name != dim]
+            aligned = [nm for nm in idx.names if nm in surv]
+            spliced = [nm for nm in idx.names if nm not in surv]
+            if aligned:
+                raise NotImplementedError("run_region: batched tl.take (aligned idx dims) is not evaluated here")
+            ax = table.names.index(dim)
+            got = np.take(table.arr, ia.astype(np.int64) - d.start, axis=ax)
+            return Field(got.reshape(table.arr.shape[:ax] + ia.shape + table.arr.shape[ax + 1:]), n.type.dims)
         if op == "tl.const":
             tt = n.type
             return Field(np.full(tt.shape, float(n.attr("value"))), tt.dims)

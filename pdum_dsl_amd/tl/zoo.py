@@ -247,3 +247,188 @@ def masked_activation(I=5, J=7, seed=1) -> Subject:
         return np.where(jj > ii, np.tanh(xx * ss) + np.exp(-np.abs(xx)), 0.0)
 
     return Subject(region, [Field(X, x.type.dims), Field(Sv, s.type.dims)], oracle)
+
+
+# ------------------------------------------------------------------ gpt2
+
+GELU_C = 0.7978845608028654  # sqrt(2/pi), the tanh-approximated gelu's constant
+
+
+def np_gelu(x):
+    return 0.5 * x * (1 + np.tanh(GELU_C * (x + 0.044715 * x**3)))
+
+
+def np_layernorm(x, g, beta, eps, axis=-1):
+    mu = x.mean(axis=axis, keepdims=True)
+    v = ((x - mu) ** 2).mean(axis=axis, keepdims=True)
+    return (x - mu) / np.sqrt(v + eps) * g + beta
+
+
+def np_softmax(s, axis):
+    e = np.exp(s - s.max(axis=axis, keepdims=True))
+    return e / e.sum(axis=axis, keepdims=True)
+
+
+@dataclass(frozen=True)
+class GPT2Config:
+    """The reference's default toy (zoo/gpt2.py:34-42) unless sized up."""
+
+    t: int = 4  # sequence
+    d: int = 6  # model width
+    nh: int = 2  # heads
+    hk: int = 3  # head width
+    m: int = 8  # mlp width
+    layers: int = 2
+    v: int = 5  # vocab (the embedding table is tied to the head)
+    eps: float = 1e-5
+
+
+@dataclass(frozen=True)
+class Model:
+    """A whole-model subject (zoo_common.py ZooModel): the region, inputs by
+    name, the numpy denotation, the output's dim order and the names of the
+    region's params."""
+
+    region: Region
+    inputs: dict  # name -> np.ndarray in the param's type-dim order
+    ref: Callable  # dict[name, ndarray] -> ndarray
+    order: tuple
+    names: dict  # id(param) -> name
+
+    def values(self) -> list:
+        """Inputs positional per region param."""
+        return [self.inputs[self.names[id(p)]] for p in self.region.params]
+
+
+class _B:
+    """Tensor-level spellings over the Builder, mirroring compute.py's
+    (contract, reduce, repeat_like, pointwise)."""
+
+    def __init__(self):
+        self.b = Builder(OPS)
+
+    def pw(self, f, *xs):
+        return self.b.emit("tl.pointwise", *xs, f=f)
+
+    def rl(self, x, like):
+        return self.b.emit("tl.repeat_like", x, like)
+
+    def red(self, f, x, dims):
+        return self.b.emit("tl.reduce", x, dims=(dims,) if isinstance(dims, str) else tuple(dims), f=f)
+
+    def c(self, v):
+        return _c(self.b, v)
+
+    def contract(self, x, y, axis):
+        """reduce(sum, mul(rl(x, y), rl(y, x)), axis): compute.py:148-154."""
+        return self.red("sum", self.pw("mul", self.rl(x, y), self.rl(y, x)), axis)
+
+    def rename(self, x, **mapping):
+        return self.b.emit("tl.rename", x, mapping=tuple(sorted(mapping.items())))
+
+    def layernorm(self, x, g, beta, feat, eps):
+        """zoo_common.py:56-60, two-pass, eps inside the sqrt."""
+        mu = self.red("mean", x, feat)
+        xc = self.pw("sub", x, self.rl(mu, x))
+        sd = self.pw("sqrt", self.pw("add", self.red("mean", self.pw("mul", xc, xc), feat), self.c(eps)))
+        y = self.pw("div", xc, self.rl(sd, x))
+        return self.pw("add", self.pw("mul", y, self.rl(g, x)), self.rl(beta, x))
+
+    def causal_softmax(self, sc, q="t", k="s"):
+        """zoo_common.py:83-86: le(iota_k, iota_q) mask, fill -1e9, softmax over k."""
+        mask = self.pw("le", self.b.emit("tl.iota", sc, name=k), self.b.emit("tl.iota", sc, name=q))
+        sm = self.pw("where", mask, sc, self.c(FILL))
+        e = self.pw("exp", self.pw("sub", sm, self.rl(self.red("max", sm, k), sm)))
+        return self.pw("div", e, self.rl(self.red("sum", e, k), sm))
+
+
+def gpt2(cfg: GPT2Config = GPT2Config(), seed: int = 7) -> Model:
+    """GPT-2 from token ids to tied-head logits (zoo/gpt2.py:46-166): embedding
+    gather + learned positions, ``layers`` pre-norm blocks (causal attention
+    with heads as a dim, gelu MLP), final layernorm, head contracted against
+    the embedding table. Inputs draw from ``default_rng(seed)``: ids first,
+    then every weight in declaration order, std 0.1 for wpe and 0.4 else."""
+    D, H, K, M = cfg.d, cfg.nh, cfg.hk, cfg.m
+    rng = np.random.default_rng(seed)
+    inputs = {"ids": rng.integers(0, cfg.v, cfg.t)}
+    shapes: dict = {}
+
+    def declare(name, **dims):
+        shapes[name] = dims
+        std = 0.1 if name == "wpe" else 0.4
+        inputs[name] = std * rng.standard_normal(tuple(dims.values()))
+
+    declare("wte", v=cfg.v, d=D)
+    declare("wpe", t=cfg.t, d=D)
+    declare("lnfg", d=D)
+    declare("lnfb", d=D)
+    for i in range(cfg.layers):
+        p = f"h.{i}."
+        declare(p + "attn.ln1g", d=D)
+        declare(p + "attn.ln1b", d=D)
+        declare(p + "attn.wq", d=D, nh=H, hk=K)
+        declare(p + "attn.wk", d=D, nh=H, hk=K)
+        declare(p + "attn.wv", d=D, nh=H, hk=K)
+        declare(p + "attn.wo", nh=H, hk=K, d=D)
+        declare(p + "mlp.ln2g", d=D)
+        declare(p + "mlp.ln2b", d=D)
+        declare(p + "mlp.w1", d=D, m=M)
+        declare(p + "mlp.b1", m=M)
+        declare(p + "mlp.w2", m=M, d=D)
+        declare(p + "mlp.b2", d=D)
+
+    t = _B()
+    params, names = [], {}
+    ids = t.b.param(0, tensor_type(("t",), (cfg.t,)))
+    params.append(ids)
+    names[id(ids)] = "ids"
+    P = {}
+    for name, dims in shapes.items():
+        p = t.b.param(len(params), tensor_type(tuple(dims), tuple(dims.values())))
+        params.append(p)
+        names[id(p)] = name
+        P[name] = p
+
+    h = t.pw("add", t.b.emit("tl.take", P["wte"], ids, dim="v"), P["wpe"])
+    scale = 1.0 / np.sqrt(K)
+    for i in range(cfg.layers):
+        p = f"h.{i}."
+        a = t.layernorm(h, P[p + "attn.ln1g"], P[p + "attn.ln1b"], "d", cfg.eps)
+        q = t.contract(a, P[p + "attn.wq"], "d")
+        k = t.contract(t.rename(a, t="s"), P[p + "attn.wk"], "d")
+        v = t.contract(t.rename(a, t="s"), P[p + "attn.wv"], "d")
+        sc = t.contract(t.pw("mul", q, t.c(scale)), k, "hk")
+        pr = t.causal_softmax(sc)
+        cx = t.contract(pr, v, "s")
+        h = t.pw("add", h, t.contract(cx, P[p + "attn.wo"], ("nh", "hk")))
+        a2 = t.layernorm(h, P[p + "mlp.ln2g"], P[p + "mlp.ln2b"], "d", cfg.eps)
+        u = t.contract(a2, P[p + "mlp.w1"], "d")
+        mm = t.pw("zoo.gelu", t.pw("add", u, t.rl(P[p + "mlp.b1"], u)))
+        h = t.pw("add", t.pw("add", h, t.contract(mm, P[p + "mlp.w2"], "m")), t.rl(P[p + "mlp.b2"], h))
+    hf = t.layernorm(h, P["lnfg"], P["lnfb"], "d", cfg.eps)
+    logits = t.contract(hf, P["wte"], "d")
+    region = Region(params=tuple(params), body=(t.b.emit("core.yield", logits),))
+
+    T_, eps = cfg.t, cfg.eps
+
+    def ref(inp):
+        hh = inp["wte"][inp["ids"]] + inp["wpe"]
+        mask = np.tril(np.ones((T_, T_), dtype=bool))
+        for i in range(cfg.layers):
+            p = f"h.{i}."
+            a = np_layernorm(hh, inp[p + "attn.ln1g"], inp[p + "attn.ln1b"], eps)
+            q = np.einsum("td,dhk->thk", a, inp[p + "attn.wq"]) / np.sqrt(K)
+            kk = np.einsum("sd,dhk->shk", a, inp[p + "attn.wk"])
+            vv = np.einsum("sd,dhk->shk", a, inp[p + "attn.wv"])
+            sc = np.einsum("thk,shk->tsh", q, kk)
+            sc = np.where(mask[:, :, None], sc, FILL)
+            pr = np_softmax(sc, axis=1)
+            ctx = np.einsum("tsh,shk->thk", pr, vv)
+            hh = hh + np.einsum("thk,hkd->td", ctx, inp[p + "attn.wo"])
+            a2 = np_layernorm(hh, inp[p + "mlp.ln2g"], inp[p + "mlp.ln2b"], eps)
+            mm = np_gelu(a2 @ inp[p + "mlp.w1"] + inp[p + "mlp.b1"])
+            hh = hh + mm @ inp[p + "mlp.w2"] + inp[p + "mlp.b2"]
+        hf_ = np_layernorm(hh, inp["lnfg"], inp["lnfb"], eps)
+        return hf_ @ inp["wte"].T
+
+    return Model(region, inputs, ref, ("t", "v"), names)
