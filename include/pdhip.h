@@ -106,6 +106,25 @@ int pdh_row_softmax(const float* x, float* y, int64_t rows, int64_t cols, int64_
 int pdh_layernorm(const float* x, const float* gamma, const float* beta, float* y, int64_t rows,
                   int64_t cols, int64_t ldx, int64_t ldy, float eps, void* stream);
 
+/* The same two row kernels over PDH_F32 / PDH_BF16 / PDH_F16 storage (x, y,
+ * gamma and beta all of `dtype`), computing in fp32. These serve the carved
+ * plan executor, whose boundary tensors carry the model's element type (the
+ * reference runs its row groups at f32 only, triton_tile.py:442-469). */
+int pdh_row_softmax_dt(const void* x, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int dtype,
+                       void* stream);
+int pdh_layernorm_dt(const void* x, const void* gamma, const void* beta, void* y, int64_t rows, int64_t cols,
+                     int64_t ldx, int64_t ldy, float eps, int dtype, void* stream);
+
+/* Row gather: out[i, :] = table[idx[i], :] for i < n_idx, rows of row_elems
+ * elements (strides ld_table / ld_out), the device form of tl.take along the
+ * table's leading dim (indexing.py:192-230). The reference plans a take as a
+ * red group and runs it on the CPU (partition.py:586-607 with its executor,
+ * tests/test_partition.py:15-37); the carved-plan executor runs it here. An
+ * index outside [0, n_rows) writes a zero row and adds 1 to *bad (device int,
+ * may be NULL), which the caller clears before and reads after. */
+int pdh_take_rows(const void* table, const int64_t* idx, void* out, int64_t n_idx, int64_t row_elems,
+                  int64_t n_rows, int64_t ld_table, int64_t ld_out, int dtype, int* bad, void* stream);
+
 /* Flash-attention forward: the online-softmax fold of _generate_flash
  * (fusion.py:542-615) over every (batch, head) instance:
  *   sc[t, s]  = scale * sum_e q[t, e] k[s, e]         (masked entries -> fill)

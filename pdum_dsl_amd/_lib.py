@@ -26,6 +26,9 @@ EXPORTS = (
     "pdh_device_cus",
     "pdh_row_softmax",
     "pdh_layernorm",
+    "pdh_row_softmax_dt",
+    "pdh_layernorm_dt",
+    "pdh_take_rows",
     "pdh_flash_fwd",
     "pdh_flash_bwd",
     "pdh_attn_decode_workspace",
@@ -99,6 +102,9 @@ def _declare(lib) -> None:
         "pdh_device_cus": (i32, []),
         "pdh_row_softmax": (i32, [vp, vp, i64, i64, i64, i64, vp]),
         "pdh_layernorm": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, f32, vp]),
+        "pdh_row_softmax_dt": (i32, [vp, vp, i64, i64, i64, i64, i32, vp]),
+        "pdh_layernorm_dt": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, f32, i32, vp]),
+        "pdh_take_rows": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, vp]),
         "pdh_flash_fwd": (i32, [vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, i32, vp]),
         "pdh_flash_bwd": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, vp]),
         "pdh_attn_decode_workspace": (C.c_size_t, [gp, i32]),

@@ -26,6 +26,7 @@ _UNARY = {"neg": "NEG", "exp": "EXP", "log": "LOG", "sqrt": "SQRT", "tanh": "TAN
 _BINARY = {"add": "ADD", "sub": "SUB", "mul": "MUL", "div": "DIV", "maximum": "MAX", "minimum": "MIN",
            "eq": "EQ", "ne": "NE", "lt": "LT", "le": "LE", "gt": "GT", "ge": "GE"}
 _VIEW = ("tl.repeat_like", "tl.repeat", "tl.stage")
+_GELU_C = 0.7978845608028654  # sqrt(2/pi), the composite zoo.gelu marker's constant (zoo_common.py:19-20)
 
 
 class Unlowerable(Exception):
@@ -36,8 +37,9 @@ class Unlowerable(Exception):
 class Lowered:
     insns: list  # (op, dst, a, b, c, imm)
     out_reg: int
-    operands: tuple  # leaf nodes in LOAD-slot order
+    operands: tuple  # the node each LOAD slot reads (a leaf, or a tl.rename of one), slot order
     dims: tuple  # output lattice dims (ir.Dim), outermost first
+    bases: tuple = ()  # the leaf under each slot (renames peeled)
 
     def program(self, out_strides, operand_strides) -> L.EwProgram:
         """The C struct, given the output's and each operand's element
@@ -66,13 +68,23 @@ def _const_value(n):
     return None
 
 
-def lower(root, dims, leaves: dict, acc=None) -> Lowered:
+def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None) -> Lowered:
     """Lower the chain ending at ``root``. ``leaves`` maps id(node) -> node
-    for nodes read with LOAD (slot order = first use); ``acc`` is the node
-    read with ACC (a contraction's fold), if any."""
+    for nodes read with LOAD (slot order = first use); a tl.rename of a leaf
+    is read as a LOAD of that leaf under the renamed dims (a rename moves no
+    data). ``acc`` is the node read with ACC (a contraction's fold), if any;
+    ``acc_scale`` multiplies it (a mean's finalize)."""
     names = tuple(d.name for d in dims)
     order: list = []
     seen: set = set()
+
+    def base_of(x):
+        while x.op == "tl.rename" and id(x) not in leaves:
+            x = x.args[0]
+        return x if id(x) in leaves else None
+
+    def is_leaf(x):
+        return id(x) in leaves or (x.op == "tl.rename" and base_of(x) is not None)
 
     def visit(n):  # post-order over the chain, stopping at leaves
         stack = [(n, False)]
@@ -85,7 +97,7 @@ def lower(root, dims, leaves: dict, acc=None) -> Lowered:
                 continue
             seen.add(id(x))
             stack.append((x, True))
-            if id(x) in leaves or (acc is not None and x is acc):
+            if is_leaf(x) or (acc is not None and x is acc):
                 continue
             if x.op in _VIEW:
                 stack.append((x.args[0], False))
@@ -102,7 +114,7 @@ def lower(root, dims, leaves: dict, acc=None) -> Lowered:
 
     uses: dict[int, int] = {}
     for x in order:
-        if x.op == "tl.pointwise" and id(x) not in leaves and x is not acc:
+        if x.op == "tl.pointwise" and not is_leaf(x) and x is not acc:
             for a in x.args:
                 a = skip_view(a)
                 uses[id(a)] = uses.get(id(a), 0) + 1
@@ -132,7 +144,12 @@ def lower(root, dims, leaves: dict, acc=None) -> Lowered:
         if acc is not None and x is acc:
             r = alloc()
             insns.append(("ACC", r, 0, 0, 0, 0.0))
-        elif id(x) in leaves:
+            if acc_scale is not None:
+                k = alloc()
+                insns.append(("CONST", k, 0, 0, 0, float(acc_scale)))
+                insns.append(("MUL", r, r, k, 0, 0.0))
+                free.append(k)
+        elif is_leaf(x):
             if len(slots) >= L.EW_MAX_OPERANDS:
                 raise Unlowerable(f"the chain reads more than {L.EW_MAX_OPERANDS} operands")
             for nm in x.type.names:
@@ -150,6 +167,19 @@ def lower(root, dims, leaves: dict, acc=None) -> Lowered:
                 raise Unlowerable(f"iota over {nm!r}, which is not an output dim")
             r = alloc()
             insns.append(("IOTA", r, names.index(nm), 0, 0, 0.0))
+        elif x.op == "tl.pointwise" and x.attr("f") == "zoo.gelu":
+            # the composite marker, expanded in its own association order:
+            # 0.5 * x * (1 + tanh(c * (x + 0.044715 * x * x * x)))
+            src = skip_view(x.args[0])
+            xr = reg[id(src)]
+            r, c = alloc(), alloc()  # x stays live until the last instruction reads it
+            insns += [("CONST", c, 0, 0, 0, 0.044715), ("MUL", r, c, xr, 0, 0.0), ("MUL", r, r, xr, 0, 0.0),
+                      ("MUL", r, r, xr, 0, 0.0), ("ADD", r, xr, r, 0, 0.0), ("CONST", c, 0, 0, 0, _GELU_C),
+                      ("MUL", r, c, r, 0, 0.0), ("TANH", r, r, 0, 0, 0.0), ("CONST", c, 0, 0, 0, 1.0),
+                      ("ADD", r, c, r, 0, 0.0), ("CONST", c, 0, 0, 0, 0.5), ("MUL", c, c, xr, 0, 0.0),
+                      ("MUL", r, c, r, 0, 0.0)]
+            free.append(c)
+            release(src)
         elif x.op == "tl.pointwise":
             f = x.attr("f")
             srcs = [skip_view(a) for a in x.args]
@@ -175,7 +205,7 @@ def lower(root, dims, leaves: dict, acc=None) -> Lowered:
         reg[id(x)] = r
     if len(insns) > L.EW_MAX_INSNS:
         raise Unlowerable(f"{len(insns)} instructions (max {L.EW_MAX_INSNS})")
-    return Lowered(insns, reg[id(root_v)], tuple(slots), tuple(dims))
+    return Lowered(insns, reg[id(root_v)], tuple(slots), tuple(dims), tuple(base_of(x) for x in slots))
 
 
 def strides_over(arr_strides, arr_names, dims) -> list:

@@ -1,0 +1,541 @@
+"""The carved-plan executor on the device: a whole model run carve by carve
+on MI355X, every boundary tensor resident in HBM.
+
+The reference carves a model (partition.plan_model) and runs the carves in
+dependency order on its CPU oracle only (packages/tensorlib/tests/
+test_partition.py:15-37, 124-193: a worklist, free views resolved at the
+edges, red groups through the evaluator). Here the same plan runs on HIP
+kernels, one step per carve:
+
+  contraction-epilogue  operand packs (pdh_map_chain: prologue chains,
+                        transposes, zero padding of k) + pdh_contract with the
+                        epilogue program; several m, n or k dims flatten into
+                        one, a single rider dim is the batch
+  row-normalization     the softmax input materialized first when it is
+                        computed (a dissolved score contraction, or a map
+                        chain), then pdh_row_softmax_dt over the reduced dim
+  row-statistics        pdh_layernorm_dt with the affine epilogue
+  map-chain             pdh_map_chain
+  red, tl.take          pdh_take_rows for the gather, the rest of the carve
+                        as a map chain; any other red carve refuses
+
+Layout policy: every value (parameter, boundary, output) is a dense tensor in
+its IR type's dim order, so every program's strides are fixed when the
+executor is built; a run allocates, launches and frees (a value is released
+after its last consumer). A rename is a view (the same memory under new
+names). Parameters are converted to the executor's element type once, at
+``bind``; the token ids stay int64.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+from . import _lib as L
+from . import ewprog
+from .hip_tile import Untranslatable, recognize_layernorm
+from .tl.dialect import OPS
+from .tl.fusion import match_contraction_epilogue, match_softmax, plan_region
+from .tl.ir import Builder, Dim, Region, walk
+
+_TORCH_DT = {"f32": "float32", "bf16": "bfloat16", "f16": "float16"}
+
+
+def _torch():
+    import torch
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("the carved-plan executor launches HIP kernels: no GPU is visible")
+    return torch
+
+
+def _dense_strides(shape) -> list:
+    out, acc = [0] * len(shape), 1
+    for i in range(len(shape) - 1, -1, -1):
+        out[i] = acc
+        acc *= shape[i]
+    return out
+
+
+def _strides_by_name(names, shape) -> dict:
+    return dict(zip(names, _dense_strides(shape)))
+
+
+def _yielding(k: Region, node) -> Region:
+    """The region over k's params that yields ``node``."""
+    return Region(params=k.params, body=(Builder(OPS).emit("core.yield", node),))
+
+
+def _base(n):
+    while n.op == "tl.rename":
+        n = n.args[0]
+    return n
+
+
+def _over(view_names, view_shape, lattice) -> list:
+    """Element strides of a dense value (dims ``view_names``) over ``lattice``
+    (0 where the value lacks a dim: a broadcast)."""
+    st = _strides_by_name(view_names, view_shape)
+    return [st.get(d.name, 0) for d in lattice]
+
+
+def _merge_program(prog, groups):
+    """Merge groups of consecutive lattice dims of a lowered program into one
+    dim each (e.g. (unit, t, nh, hk) -> (unit, t, nh*hk)). A group merges when
+    every view's strides over it compose densely (outer = inner * size) or
+    are all zero; an IOTA over a dim in a group of several refuses."""
+    n_old = prog.ndim
+    sizes = [int(prog.shape[d]) for d in range(n_old)]
+    for j in range(prog.n_insns):
+        ins = prog.insns[j]
+        if ins.op == L.EW["IOTA"]:
+            g = next(gi for gi, grp in enumerate(groups) if ins.a in grp)
+            if len(groups[g]) > 1:
+                raise Untranslatable("an iota over a flattened dim has no merged form")
+    if any(int(prog.start[d]) != 0 for grp in groups if len(grp) > 1 for d in grp):
+        raise Untranslatable("a flattened dim must start at 0")
+
+    def merge(strides):
+        out = []
+        for grp in groups:
+            st = [int(strides[d]) for d in grp]
+            if all(s == 0 for s in st):
+                out.append(0)
+                continue
+            for a, b in zip(grp[:-1], grp[1:]):
+                if int(strides[a]) != int(strides[b]) * sizes[b]:
+                    raise Untranslatable("a view's strides do not compose across a flattened dim")
+            out.append(st[-1])
+        return out
+
+    out_st = merge(prog.out_stride)
+    in_st = [merge(prog.in_stride[i]) for i in range(prog.n_operands)]
+    iota_dim = {d: gi for gi, grp in enumerate(groups) for d in grp}
+    new = L.EwProgram()
+    new.n_insns, new.n_operands, new.ndim, new.out_reg = prog.n_insns, prog.n_operands, len(groups), prog.out_reg
+    for gi, grp in enumerate(groups):
+        new.shape[gi] = math.prod(sizes[d] for d in grp)
+        new.start[gi] = int(prog.start[grp[0]]) if len(grp) == 1 else 0
+        new.out_stride[gi] = out_st[gi]
+        for i in range(prog.n_operands):
+            new.in_stride[i][gi] = in_st[i][gi]
+    for j in range(prog.n_insns):
+        src, dst = prog.insns[j], new.insns[j]
+        dst.op, dst.dst, dst.a, dst.b, dst.c, dst.imm = src.op, src.dst, src.a, src.b, src.c, src.imm
+        if src.op == L.EW["IOTA"]:
+            dst.a = iota_dim[src.a]
+    return new
+
+
+@dataclass
+class _Pack:
+    """One contraction operand laid out [batch][rows][kp] (k contiguous, zero
+    past k): the input itself (``direct``), or a map-chain program over the
+    kernel's params; a dissolved contraction in the operand's chain is first
+    materialized by ``pre`` (its value is program slot None, or used as is
+    when ``pre_direct``)."""
+
+    direct: int | None  # kernel param index used as is
+    prog: object = None
+    slots: tuple = ()  # kernel param index per program operand (None: the pre value)
+    shape: tuple = ()
+    zero: bool = False
+    pre: object = None
+    pre_direct: bool = False
+
+
+@dataclass
+class Step:
+    """One launched carve: ``ins`` are value ids (positional per kernel param),
+    ``out`` the value id it defines."""
+
+    kind: str
+    ins: tuple
+    out: int
+    out_shape: tuple
+    run: object = field(repr=False)
+    source: str = ""
+
+
+class PlanExecutor:
+    """Runs a ModelPlan of ``region`` on the device. ``dtype`` is the element
+    type of every floating value (f32, bf16 or f16)."""
+
+    def __init__(self, plan, region: Region, dtype: str = "bf16"):
+        if dtype not in _TORCH_DT:
+            raise ValueError(f"dtype {dtype!r}: f32, bf16 or f16")
+        self.region, self.dtype = region, dtype
+        self.dt_code = {"f32": L.PDH_F32, "bf16": L.PDH_BF16, "f16": L.PDH_F16}[dtype]
+        self.params = region.params
+        self.nested: list = []
+        self._bad: list = []
+        have = {id(p) for p in region.params}
+        self.alias: dict = {}  # rename view id -> the value id it reads
+        pending = [c for c in plan.carves if c.root is not None]
+        rootless = [c for c in plan.carves if c.root is None]
+        if rootless:
+            raise Untranslatable(f"a multi-output residue cannot run on the device: {rootless[0].group.reason}")
+        self.steps: list = []
+        while pending:
+            for c in pending:
+                ins = [self._resolve(b, have) for b in c.bounds]
+                if all(i is not None for i in ins):
+                    self.steps.append(self._step(c, tuple(ins)))
+                    have.add(id(c.root))
+                    pending.remove(c)
+                    break
+            else:
+                raise Untranslatable("plan stalled: a carve's boundary is never produced")
+        y = region.body[-1].args[0]
+        self.output = self._resolve(y, have)
+        if self.output is None:
+            raise Untranslatable("the model's output is not produced by any carve")
+        self.out_names = y.type.names
+        last: dict = {}
+        for k, st in enumerate(self.steps):
+            for i in st.ins:
+                last[i] = k
+        self.release = [[i for i, k in last.items() if k == s and i != self.output] for s in range(len(self.steps))]
+        self.bound: dict | None = None
+
+    # ------------------------------------------------------------ building
+
+    def _resolve(self, node, have):
+        """The value id a boundary node reads: itself, or (a rename) the value
+        under it."""
+        if id(node) in have:
+            return id(node)
+        if node.op == "tl.rename":
+            src = self._resolve(node.args[0], have)
+            if src is not None:
+                self.alias[id(node)] = src
+                return src
+        return None
+
+    def _step(self, carve, ins):
+        tmpl = carve.group.template
+        k = carve.kernel
+        if tmpl == "contraction-epilogue":
+            run, src = self._contraction(k)
+        elif tmpl == "row-normalization":
+            run, src = self._softmax(k)
+        elif tmpl == "row-statistics":
+            run, src = self._layernorm(k)
+        elif tmpl == "map-chain":
+            run, src = self._map_chain(k)
+        elif carve.group.confidence == "red" and any(n.op == "tl.take" for n in walk(k)):
+            run, src = self._take(k)
+        else:
+            raise Untranslatable(f"carve {tmpl} ({carve.group.reason or carve.root_op}) has no device step")
+        y = k.body[-1].args[0]
+        return Step(tmpl, ins, id(carve.root), y.type.shape, run, src)
+
+    def _index(self, region, node):
+        return next(i for i, p in enumerate(region.params) if p is node)
+
+    def _map_prog(self, region, root, lattice, out_strides, extra_leaves=()):
+        leaves = {id(p): p for p in region.params}
+        for n in extra_leaves:
+            leaves[id(n)] = n
+        try:
+            low = ewprog.lower(root, lattice, leaves)
+        except ewprog.Unlowerable as exc:
+            raise Untranslatable(f"map chain: {exc}") from None
+        strides = [_over(op.type.names, op.type.shape, lattice) for op in low.operands]
+        return low, low.program(out_strides, strides)
+
+    def _materialize(self, k, node):
+        """A callable computing ``node`` (a value inside carve kernel ``k``)
+        from k's param values. Carves dissolved into ``node`` (re-derived per
+        tile in the reference's plan) are split back out: the sub-region
+        yielding it is carved with every claim root materialized
+        (plan_model(dissolve=False)) and run by a nested executor."""
+        from .tl.partition import plan_model
+
+        sub = _yielding(k, node)
+        nested = PlanExecutor(plan_model(sub, dissolve=False), sub, self.dtype)
+        self.nested.append(nested)
+
+        def run(vals):
+            return nested._run({id(p): v for p, v in zip(sub.params, vals)}, self._bad)
+
+        return run
+
+    def _map_chain(self, k):
+        y = k.body[-1].args[0]
+        low, prog = self._map_prog(k, y, y.type.dims, _dense_strides(y.type.shape))
+        slots = tuple(self._index(k, b) for b in low.bases)
+        shape = y.type.shape
+
+        def run(vals):
+            torch = _torch()
+            from . import kernels as K
+
+            out = torch.empty(shape, device="cuda", dtype=getattr(torch, _TORCH_DT[self.dtype]))
+            K.map_chain(prog, [vals[i] for i in slots], out)
+            return out
+
+        return run, f"map_chain insns={len(low.insns)}"
+
+    def _contraction(self, k, yroot=None):
+        """GEMM-shaped contraction with its epilogue (and prologue chains)."""
+        m = match_contraction_epilogue(k)
+        if m is None:
+            raise Untranslatable("contraction carve does not match the contraction row")
+        if m["shape"] != "gemm":
+            raise Untranslatable(f"contraction-epilogue: only the GEMM shape runs on the device ({m['shape']})")
+        red = m["reduce"]
+        kd = (red.attr("dims"),) if isinstance(red.attr("dims"), str) else tuple(red.attr("dims"))
+        ca, cb = m["a"], m["b"]
+        keep_a = [nm for nm in ca.type.names if nm not in kd]
+        keep_b = [nm for nm in cb.type.names if nm not in kd]
+        out_names = red.type.names
+        riders = [nm for nm in out_names if nm in keep_a and nm in keep_b]
+        mdims = [nm for nm in out_names if nm in keep_a and nm not in riders]
+        ndims = [nm for nm in out_names if nm in keep_b and nm not in riders]
+        if len(riders) > 1:
+            raise Untranslatable("contraction-epilogue: at most one batch (rider) dim on the device")
+        size = {d.name: d for d in red.type.dims}
+        kdim = {nm: ca.type.dim(nm) for nm in kd}
+        # absent groups stand in as unit dims, so the lattice is always (batch, m.., n..)
+        bdim = size[riders[0]] if riders else Dim("_unit_b", 0, 1)
+        if not mdims:
+            size["_unit_m"] = Dim("_unit_m", 0, 1)
+            mdims = ["_unit_m"]
+        if not ndims:
+            size["_unit_n"] = Dim("_unit_n", 0, 1)
+            ndims = ["_unit_n"]
+        B = bdim.size
+        M = math.prod(size[nm].size for nm in mdims)
+        N = math.prod(size[nm].size for nm in ndims)
+        Kx = math.prod(kdim[nm].size for nm in kd)
+        KP = -(-Kx // 64) * 64
+        if any(kdim[nm].start != 0 for nm in kd):
+            raise Untranslatable("contracted dims must start at 0")
+
+        def pack(core, rows_names, nrows):
+            """[B][rows][KP] from the operand chain ``core``."""
+            lat = (bdim,) + tuple(size[nm] for nm in rows_names) + tuple(kdim[nm] for nm in kd)
+            if len(lat) > L.EW_MAX_DIMS:
+                raise Untranslatable(f"an operand pack over {len(lat)} dims (max {L.EW_MAX_DIMS})")
+            base = _base(core)
+            want = tuple(riders) + tuple(nm for nm in rows_names if not nm.startswith("_unit")) + tuple(kd)
+            if base.op == "core.param" and core.type.names == want and Kx == KP:
+                return _Pack(direct=self._index(k, base))
+            pre = None
+            if any(n.op == "tl.reduce" for n in walk(_yielding(k, core))):
+                # carves dissolved into this operand (the traffic gate's
+                # re-derivation per tile): materialized once, by their own plan
+                pre = self._materialize(k, core)
+                if core.type.names == want and Kx == KP:
+                    return _Pack(direct=None, pre=pre, pre_direct=True)
+            rs = KP * math.prod(size[nm].size for nm in rows_names)
+            out_st = [rs if riders else 0]
+            acc = KP
+            row_st = []
+            for nm in reversed(rows_names):
+                row_st.insert(0, acc)
+                acc *= size[nm].size
+            out_st += row_st
+            kst, acc = [], 1
+            for nm in reversed(kd):
+                kst.insert(0, acc)
+                acc *= kdim[nm].size
+            out_st += kst
+            low, prog = self._map_prog(k, core, lat, out_st, extra_leaves=(core,) if pre is not None else ())
+            slots = tuple(None if (pre is not None and b is core) else self._index(k, b) for b in low.bases)
+            return _Pack(None, prog, slots, (B, nrows, KP), KP != Kx, pre)
+
+        pa, pb = pack(ca, mdims, M), pack(cb, ndims, N)
+        y = k.body[-1].args[0] if yroot is None else yroot
+        if y.type.names and set(y.type.names) != set(out_names):
+            raise Untranslatable("the epilogue changes the contraction's lattice")
+        lat = (bdim,) + tuple(size[nm] for nm in mdims) + tuple(size[nm] for nm in ndims)
+        if len(lat) > L.EW_MAX_DIMS:
+            raise Untranslatable(f"an epilogue over {len(lat)} dims (max {L.EW_MAX_DIMS})")
+        leaves = {id(p): p for p in k.params}
+        try:
+            epi = ewprog.lower(y, lat, leaves, acc=red, acc_scale=(1.0 / Kx) if m["f"] == "mean" else None)
+        except ewprog.Unlowerable as exc:
+            raise Untranslatable(f"contraction epilogue: {exc}") from None
+        out_st = _over(y.type.names, y.type.shape, lat)
+        prog = epi.program(out_st, [_over(op.type.names, op.type.shape, lat) for op in epi.operands])
+        groups = [[0], list(range(1, 1 + len(mdims))), list(range(1 + len(mdims), len(lat)))]
+        prog = _merge_program(prog, groups)
+        eslots = tuple(self._index(k, b) for b in epi.bases)
+        shape = y.type.shape
+        tdt = _TORCH_DT[self.dtype]
+
+        def run(vals):
+            torch = _torch()
+            from . import kernels as K
+
+            dt = getattr(torch, tdt)
+
+            def build(p):
+                if p.direct is not None:
+                    return vals[p.direct].reshape(B, -1, KP)
+                pv = p.pre(vals) if p.pre is not None else None
+                if p.pre_direct:
+                    return pv.reshape(B, -1, KP)
+                buf = (torch.zeros if p.zero else torch.empty)(p.shape, device="cuda", dtype=dt)
+                K.map_chain(p.prog, [pv if i is None else vals[i] for i in p.slots], buf)
+                return buf
+
+            a, bt = build(pa), build(pb)
+            out = torch.empty(shape, device="cuda", dtype=dt)
+            K.contract(a, bt, Kx, prog, [vals[i] for i in eslots], out)
+            return out
+
+        def how(p):
+            return "direct" if p.direct is not None else ("contract" if p.pre_direct else
+                                                          ("contract+pack" if p.pre else "pack"))
+
+        src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
+        return run, src
+
+    def _softmax(self, k):
+        y = k.body[-1].args[0]
+        sm = match_softmax(y)
+        if sm is None:
+            raise Untranslatable("row-normalization carve without the softmax chain")
+        s = sm["s"]
+        x = sm["sm"]
+        if x.type.names[-1] != s or y.type.names != x.type.names:
+            raise Untranslatable("row-normalization: the reduced dim must be the input's last")
+        rows = math.prod(d.size for d in x.type.dims[:-1])
+        cols = x.type.dim(s).size
+        if _base(x).op == "core.param":
+            xi = self._index(k, _base(x))
+            pre, pre_src = None, "input"
+        else:  # a computed input (the dissolved score contraction): materialized first
+            sub = _yielding(k, x)
+            tmpl = plan_region(sub).groups[0].template
+            if tmpl == "contraction-epilogue":
+                pre, pre_src = self._contraction(sub)
+            else:
+                pre, pre_src = self._materialize(k, x), "plan"
+            xi = None
+        shape = y.type.shape
+
+        def run(vals):
+            from . import kernels as K
+
+            xin = vals[xi] if pre is None else pre(vals)
+            return K.row_softmax(xin.reshape(rows, cols)).reshape(shape)
+
+        return run, f"row_softmax rows={rows} cols={cols} input={pre_src}"
+
+    def _layernorm(self, k):
+        lb = recognize_layernorm(k)
+        if lb is None:
+            raise Untranslatable("row-statistics carve is not an (affine) layernorm over params")
+        x, feat = lb["x"], lb["feat"]
+        if x.type.names[-1] != feat:
+            raise Untranslatable("row-statistics: the feature dim must be the input's last")
+        ix = self._index(k, x)
+        ig = None if lb["gamma"] is None else self._index(k, lb["gamma"])
+        ib = None if lb["beta"] is None else self._index(k, lb["beta"])
+        eps = lb["eps"]
+        cols = x.type.dim(feat).size
+        y = k.body[-1].args[0]
+        if y.type.names != x.type.names:
+            raise Untranslatable("row-statistics: the output's dims must follow the input's")
+
+        def run(vals):
+            from . import kernels as K
+
+            xin = vals[ix]
+            g = None if ig is None else vals[ig]
+            b = None if ib is None else vals[ib]
+            return K.layernorm(xin.reshape(-1, cols), g, b, eps=eps).reshape(xin.shape)
+
+        return run, f"layernorm cols={cols} eps={eps:g} affine={ig is not None or ib is not None}"
+
+    def _take(self, k):
+        takes = [n for n in walk(k) if n.op == "tl.take"]
+        specs = []
+        for t in takes:
+            table, idx = t.args
+            if _base(table).op != "core.param" or _base(idx).op != "core.param":
+                raise Untranslatable("tl.take over computed operands")
+            dim = t.attr("dim")
+            if table.type.names[0] != dim:
+                raise Untranslatable("tl.take runs along the table's leading dim only")
+            specs.append((self._index(k, _base(table)), self._index(k, _base(idx)), t.type.shape))
+        y = k.body[-1].args[0]
+        shape = y.type.shape
+        if y.op == "tl.take":
+            low = prog = None
+        else:
+            low, prog = self._map_prog(k, y, y.type.dims, _dense_strides(shape), extra_leaves=takes)
+        tdt = _TORCH_DT[self.dtype]
+
+        def run(vals):
+            torch = _torch()
+            from . import kernels as K
+
+            bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+            got = {}
+            for t, (ti, ii, tshape) in zip(takes, specs):
+                got[id(t)] = K.take_rows(vals[ti], vals[ii], bad=bad).reshape(tshape)
+            self._bad.append(bad)
+            if prog is None:
+                return got[id(takes[0])]
+            ops = [got[id(b)] if id(b) in got else vals[self._index(k, b)] for b in low.bases]
+            out = torch.empty(shape, device="cuda", dtype=getattr(torch, tdt))
+            K.map_chain(prog, ops, out)
+            return out
+
+        return run, f"take_rows x{len(takes)}" + ("" if prog is None else f" + map_chain insns={len(low.insns)}")
+
+    # ------------------------------------------------------------- running
+
+    def bind(self, inputs: list) -> None:
+        """Upload / convert the region's params (positional) once: floating
+        values to the executor's type, dense in their type order; integer
+        arrays (token ids) to int64."""
+        torch = _torch()
+        dt = getattr(torch, _TORCH_DT[self.dtype])
+        bound = {}
+        for p, v in zip(self.params, inputs):
+            t = torch.as_tensor(v)
+            if t.shape != tuple(p.type.shape):
+                raise ValueError(f"param {p.attr('index')}: shape {tuple(t.shape)} != {p.type.shape}")
+            if t.dtype in (torch.int32, torch.int64):
+                t = t.to(device="cuda", dtype=torch.int64)
+            else:
+                t = t.to(device="cuda", dtype=dt)
+            bound[id(p)] = t.contiguous()
+        self.bound = bound
+
+    def run(self):
+        """One pass over the plan; returns the output (device tensor, dims in
+        the region's yield order). Raises if a gather saw an index out of range."""
+        if self.bound is None:
+            raise RuntimeError("bind() the params first")
+        bads: list = []
+        out = self._run(self.bound, bads)
+        for bad in bads:
+            if int(bad.item()) != 0:
+                raise IndexError(f"tl.take: {int(bad.item())} index(es) outside the table")
+        return out
+
+    def _run(self, bound: dict, bads: list):
+        self._bad = bads
+        for n in self.nested:
+            n._bad = bads
+        vals = dict(bound)
+        for st, rel in zip(self.steps, self.release):
+            vals[st.out] = st.run([vals[i] for i in st.ins])
+            for i in rel:
+                if i not in bound:
+                    vals.pop(i, None)
+        return vals[self.output]
+
+    def sources(self) -> list:
+        return [f"{st.kind}: {st.source}" for st in self.steps]
+
+
+__all__ = ["PlanExecutor", "Step"]

@@ -535,7 +535,7 @@ def _map_chain_runner(region, grid, dtype):
         low = ewprog.lower(y, dims, leaves)
     except ewprog.Unlowerable as exc:
         raise Untranslatable(f"map-chain: {exc}") from None
-    idx = [_index(region, p) for p in low.operands]
+    idx = [_index(region, p) for p in low.bases]
     out_names = y.type.names
 
     def run(values):
@@ -643,7 +643,7 @@ def _contraction_runner(region, cb, grid, dtype):
         return ("chain", low)
 
     pa, pb = operand(cb["a"], a_order), operand(cb["b"], b_order)
-    epi_idx = [_index(region, p) for p in epi.operands]
+    epi_idx = [_index(region, p) for p in epi.bases]
 
     def run(values):
         torch = _torch()
@@ -653,7 +653,8 @@ def _contraction_runner(region, cb, grid, dtype):
             if spec[0] == "param":
                 return _upload(torch, values[spec[1]], node.type.names, order, dtype, pad_last=KP)
             low = spec[1]
-            ins = [_upload(torch, values[_index(region, p)], p.type.names, p.type.names, dtype) for p in low.operands]
+            ins = [_upload(torch, values[_index(region, b)], p.type.names, p.type.names, dtype)
+                   for p, b in zip(low.operands, low.bases)]
             st = [ewprog.strides_over(t.stride(), p.type.names, low.dims) for t, p in zip(ins, low.operands)]
             buf = torch.zeros((low.dims[0].size, rows, KP), device="cuda", dtype=tdt)
             prog = low.program(buf.stride(), st)

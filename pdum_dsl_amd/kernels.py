@@ -66,18 +66,28 @@ CAUSAL = Band(None, 0)
 
 
 def row_softmax(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """softmax over the last axis of an fp32 tensor (rows = all leading dims)."""
+    """softmax over the last axis (rows = all leading dims); fp32, bf16 or
+    f16 storage, fp32 arithmetic."""
     _require_cuda(x)
-    if x.dtype != torch.float32:
-        raise ValueError(f"row_softmax is fp32 (got {x.dtype})")
+    if x.dtype not in _DT:
+        raise ValueError(f"row_softmax stores f32, bf16 or f16 (got {x.dtype})")
     x2 = x.reshape(-1, x.shape[-1])
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     y = torch.empty_like(x2) if out is None else out.reshape(-1, x.shape[-1])
-    _lib.call(
-        "pdh_row_softmax",
-        _ptr(x2), _ptr(y), x2.shape[0], x2.shape[1], x2.stride(0), y.stride(0), C.c_void_p(_stream()),
-    )
+    if y.dtype != x.dtype or y.stride(-1) != 1:
+        raise ValueError("out must share x's element type and have contiguous rows")
+    if x.dtype == torch.float32:
+        _lib.call(
+            "pdh_row_softmax",
+            _ptr(x2), _ptr(y), x2.shape[0], x2.shape[1], x2.stride(0), y.stride(0), C.c_void_p(_stream()),
+        )
+    else:
+        _lib.call(
+            "pdh_row_softmax_dt",
+            _ptr(x2), _ptr(y), x2.shape[0], x2.shape[1], x2.stride(0), y.stride(0), _DT[x.dtype],
+            C.c_void_p(_stream()),
+        )
     return y.reshape(x.shape)
 
 
@@ -88,11 +98,14 @@ def layernorm(
     eps: float = 1e-5,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Two-pass layernorm over the last axis, fp32, optional affine epilogue."""
+    """Two-pass layernorm over the last axis, optional affine epilogue; fp32,
+    bf16 or f16 storage (x, gamma, beta alike), fp32 arithmetic."""
     _require_cuda(x, gamma, beta)
-    for t in (x, gamma, beta):
-        if t is not None and t.dtype != torch.float32:
-            raise ValueError("layernorm is fp32")
+    if x.dtype not in _DT:
+        raise ValueError(f"layernorm stores f32, bf16 or f16 (got {x.dtype})")
+    for t in (gamma, beta):
+        if t is not None and t.dtype != x.dtype:
+            raise ValueError("gamma / beta must share x's element type")
     n = x.shape[-1]
     for nm, t in (("gamma", gamma), ("beta", beta)):
         if t is not None and (t.numel() != n or not t.is_contiguous()):
@@ -101,12 +114,48 @@ def layernorm(
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     y = torch.empty_like(x2) if out is None else out.reshape(-1, n)
-    _lib.call(
-        "pdh_layernorm",
-        _ptr(x2), _ptr(gamma), _ptr(beta), _ptr(y), x2.shape[0], n, x2.stride(0), y.stride(0),
-        C.c_float(eps), C.c_void_p(_stream()),
-    )
+    if y.dtype != x.dtype or y.stride(-1) != 1:
+        raise ValueError("out must share x's element type and have contiguous rows")
+    if x.dtype == torch.float32:
+        _lib.call(
+            "pdh_layernorm",
+            _ptr(x2), _ptr(gamma), _ptr(beta), _ptr(y), x2.shape[0], n, x2.stride(0), y.stride(0),
+            C.c_float(eps), C.c_void_p(_stream()),
+        )
+    else:
+        _lib.call(
+            "pdh_layernorm_dt",
+            _ptr(x2), _ptr(gamma), _ptr(beta), _ptr(y), x2.shape[0], n, x2.stride(0), y.stride(0),
+            C.c_float(eps), _DT[x.dtype], C.c_void_p(_stream()),
+        )
     return y.reshape(x.shape)
+
+
+def take_rows(table: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None = None,
+              bad: torch.Tensor | None = None) -> torch.Tensor:
+    """out[i, ...] = table[idx[i], ...]: a gather along the table's leading
+    dim (idx int64, any shape; the rest of the table's dims ride). An index
+    out of range gives a zero row and counts in ``bad`` (an int32 device
+    scalar) when given."""
+    _require_cuda(table, idx)
+    if table.dtype not in _DT or idx.dtype != torch.int64:
+        raise ValueError("take_rows: table f32/bf16/f16, idx int64")
+    rows = table.reshape(table.shape[0], -1)
+    if rows.stride(-1) != 1:
+        raise ValueError("take_rows: the table's trailing dims must be contiguous")
+    flat = idx.reshape(-1).contiguous()
+    y = torch.empty((flat.numel(), rows.shape[1]), dtype=table.dtype, device=table.device) if out is None else \
+        out.reshape(flat.numel(), rows.shape[1])
+    if y.dtype != table.dtype or y.stride(-1) != 1:
+        raise ValueError("take_rows: out must share the table's element type with contiguous rows")
+    if bad is not None and (bad.dtype != torch.int32 or bad.numel() < 1):
+        raise ValueError("take_rows: bad is an int32 device scalar")
+    _lib.call(
+        "pdh_take_rows",
+        _ptr(rows), _ptr(flat), _ptr(y), flat.numel(), rows.shape[1], rows.shape[0], rows.stride(0), y.stride(0),
+        _DT[table.dtype], _ptr(bad), C.c_void_p(_stream()),
+    )
+    return y.reshape(tuple(idx.shape) + tuple(table.shape[1:]))
 
 
 # ----------------------------------------------------------------- attention

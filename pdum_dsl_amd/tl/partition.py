@@ -460,10 +460,12 @@ def _dissolve(claims, consumers, travel, region):
             _absorb_travel(mem, travel)
 
 
-def carve_model(region: Region):
+def carve_model(region: Region, dissolve: bool = True):
     """The partition alone (partition.py:458-582): returns (claims,
     interior_count, travel), claims as (root, members, artifacts) with members
-    keyed by id; a rootless claim is a multi-output residue."""
+    keyed by id; a rootless claim is a multi-output residue. ``dissolve=False``
+    skips root travel, so every claim's root stays a materialized boundary
+    (the device executor's policy for values it cannot re-derive per tile)."""
     interior, consumers = _graph(region)
     claimed: set = set()
     travel: dict = {}
@@ -573,7 +575,8 @@ def carve_model(region: Region):
                 claims.extend((rt, mem, ()) for rt, mem in parts)
                 break
             rootset.extend(promote)
-    _dissolve(claims, consumers, travel, region)
+    if dissolve:
+        _dissolve(claims, consumers, travel, region)
     return claims, len(interior), travel
 
 
@@ -584,13 +587,13 @@ def _core(x):
     return x
 
 
-def plan_model(region: Region, machine=None, floor: int = 1024) -> ModelPlan:
+def plan_model(region: Region, machine=None, floor: int = 1024, dissolve: bool = True) -> ModelPlan:
     """Carve ``region`` and plan each distinct carve once (partition.py:586-607).
     A flash joint is claimed whole first (the fused backward's carve)."""
     fj = match_flash_joint(region)
     if fj is not None:
         return _plan_joint(region, fj, machine, floor)
-    claims, interior, _travel = carve_model(region)
+    claims, interior, _travel = carve_model(region, dissolve=dissolve)
     seen: dict = {}
     carves = []
     counted: set = set()  # travel copies count once, in their first claim

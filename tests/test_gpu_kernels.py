@@ -211,5 +211,5 @@ def test_entry_points_refuse_bad_shapes_without_launching(K):
     q = torch.zeros((1, 1, 8, 96), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(PdhError, match="e == od"):
         K.flash_fwd(q, q, q)
-    with pytest.raises(ValueError, match="fp32"):
-        K.row_softmax(q)
+    with pytest.raises(ValueError, match="f32, bf16 or f16"):
+        K.row_softmax(q.double())
