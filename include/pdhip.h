@@ -237,10 +237,22 @@ int pdh_map_chain(const pdh_ew_program* prog, const void* const* operands, void*
  * program's output dims are (b, m, n) (ndim 3, shape {batch, m, n}); it reads
  * the accumulator with PDH_EW_ACC and may not LOAD more than n_operands.
  * dtype PDH_BF16 / PDH_F16: v_mfma_f32_32x32x16, fp32 accumulate, 128x128
- * workgroup tiles; PDH_F32: the fp32 column (VALU, fp32 throughout). The
+ * workgroup tiles (64x64 when 128x128 tiles would not give every compute
+ * unit one); PDH_F32: the fp32 column (VALU, fp32 throughout). The
  * sum over k is re-bracketed by 64-wide k tiles (license gemm.k-reassoc). */
 int pdh_contract(const void* a, const void* bt, int64_t batch, int64_t m, int64_t n, int64_t k, int64_t kp,
                  const pdh_ew_program* epi, const void* const* operands, void* out, int dtype, void* stream);
+
+/* The same batched contraction with a and bt read through element strides:
+ * a[b, r, :] starts at a + b*sa_b + r*sa_r, bt[b, r, :] at bt + b*sb_b + r*sb_r,
+ * and k (a positive multiple of 64) is contiguous, so a value stored in any
+ * dim order with its contracted dims innermost feeds the product without a
+ * copy (the carved-plan executor's boundary tensors: a head-major view of a
+ * (t, heads, head_dim) tensor is sa_b = head_dim, sa_r = heads*head_dim).
+ * Strides are multiples of 16 bytes; row strides are >= k. */
+int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, const void* bt, int64_t sb_b, int64_t sb_r,
+                         int64_t batch, int64_t m, int64_t n, int64_t k, const pdh_ew_program* epi,
+                         const void* const* operands, void* out, int dtype, void* stream);
 
 /* Runtime specialization of elementwise programs. pdh_map_chain and
  * pdh_contract first compile the program into straight-line code with hipRTC

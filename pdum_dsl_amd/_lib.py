@@ -35,6 +35,7 @@ EXPORTS = (
     "pdh_attn_decode",
     "pdh_map_chain",
     "pdh_contract",
+    "pdh_contract_strided",
     "pdh_ew_set_jit",
     "pdh_ew_jit_stats",
     "pdh_ew_jit_source",
@@ -111,6 +112,8 @@ def _declare(lib) -> None:
         "pdh_attn_decode": (i32, [vp, vp, vp, vp, vp, gp, i32, f32, i32, vp, C.c_size_t, vp]),
         "pdh_map_chain": (i32, [C.POINTER(EwProgram), C.POINTER(vp), vp, i32, vp]),
         "pdh_contract": (i32, [vp, vp, i64, i64, i64, i64, i64, C.POINTER(EwProgram), C.POINTER(vp), vp, i32, vp]),
+        "pdh_contract_strided": (
+            i32, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64, C.POINTER(EwProgram), C.POINTER(vp), vp, i32, vp]),
         "pdh_ew_set_jit": (i32, [i32]),
         "pdh_ew_jit_stats": (None, [C.POINTER(i64)]),
         "pdh_ew_jit_source": (C.c_size_t, [C.POINTER(EwProgram), i32, i32, C.c_char_p, C.c_size_t]),

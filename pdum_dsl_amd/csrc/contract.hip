@@ -20,8 +20,14 @@ __global__ __launch_bounds__(256) void map_chain_kernel(pdh_ew_program p, EwOper
 
 template <int DT>
 __global__ __launch_bounds__(256, 2) void contract_mfma(ContractArgs a, pdh_ew_program p, EwOperands ops) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kContractLds];
-  contract_mfma_body<DT, InterpEval>(a, p, ops, smem);
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[contract_lds<64>()];
+  contract_mfma_body<DT, 64, InterpEval>(a, p, ops, smem);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256, 4) void contract_mfma_small(ContractArgs a, pdh_ew_program p, EwOperands ops) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[contract_lds<32>()];
+  contract_mfma_body<DT, 32, InterpEval>(a, p, ops, smem);
 }
 
 __global__ __launch_bounds__(256) void contract_f32(ContractArgs a, pdh_ew_program p, EwOperands ops) {
@@ -126,67 +132,114 @@ extern "C" int pdh_map_chain(const pdh_ew_program* prog, const void* const* oper
   return check_launch("pdh_map_chain");
 }
 
+namespace pdh {
+namespace {
+
+int g_cus = 0;  // compute units of the device, read once
+
+// Validation shared by both entry points, then the launch: the 128 x 128
+// tiles, or the 64 x 64 ones when the big tiles would not give every compute
+// unit a workgroup.
+int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* const* operands, int64_t esize,
+                    hipStream_t st, const char* fn) {
+  int rc = check_program(epi, 3, true, fn);
+  if (rc) return rc;
+  const int64_t batch = ca.batch, m = ca.m, n = ca.n;
+  PDH_REQUIRE(epi->shape[0] == batch && epi->shape[1] == m && epi->shape[2] == n, PDH_EINVAL,
+              "%s: epilogue shape must be {batch, m, n}", fn);
+  PDH_REQUIRE(epi->n_operands == 0 || operands != nullptr, PDH_EINVAL, "%s: null operand table", fn);
+  if ((rc = check_view(epi, epi->out_stride, fn, "output"))) return rc;
+  EwOperands ops{};
+  for (int i = 0; i < epi->n_operands; ++i) {
+    PDH_REQUIRE(operands[i] != nullptr, PDH_EINVAL, "%s: operand %d is null", fn, i);
+    if ((rc = check_view(epi, epi->in_stride[i], fn, "operand"))) return rc;
+    ops.p[i] = operands[i];
+  }
+  // every 32-bit buffer offset (rows up to m + 128, k up to kp) stays representable
+  PDH_REQUIRE((m + 128) * ca.sa_r * esize + ca.kp * esize <= static_cast<int64_t>(UINT32_MAX) &&
+                  (n + 128) * ca.sb_r * esize + ca.kp * esize <= static_cast<int64_t>(UINT32_MAX),
+              PDH_EINVAL, "%s: one batch slice of a / bt must stay under 4 GiB", fn);
+  hipFunction_t fns[2];
+  const bool spec = jit_get(JitKind::Contract, *epi, ca.dtype, fns);
+  pdh_ew_program pe = *epi;
+  void* args[] = {&ca, &pe, &ops};
+  auto launch_spec = [&](hipFunction_t f, int64_t nblk) {
+    PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "%s: grid too large", fn);
+    PDH_REQUIRE(hipModuleLaunchKernel(f, static_cast<unsigned>(nblk), 1, 1, 256, 1, 1, 0, st, args, nullptr) ==
+                    hipSuccess,
+                PDH_ELAUNCH, "%s: specialized launch failed", fn);
+    jit_count_launch();
+    return PDH_OK;
+  };
+  if (ca.dtype == PDH_F32) {
+    ca.tiles_m = static_cast<int>((m + kFT - 1) / kFT);
+    ca.tiles_n = static_cast<int>((n + kFT - 1) / kFT);
+    const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
+    if (spec) return launch_spec(fns[0], nblk);
+    PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "%s: grid too large", fn);
+    contract_f32<<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
+    return check_launch(fn);
+  }
+  if (g_cus == 0) g_cus = pdh_device_cus() > 0 ? pdh_device_cus() : 256;
+  const int64_t big = batch * ((m + 127) / 128) * ((n + 127) / 128);
+  const bool small = big < g_cus;
+  const int bm = small ? 64 : 128;
+  ca.tiles_m = static_cast<int>((m + bm - 1) / bm);
+  ca.tiles_n = static_cast<int>((n + bm - 1) / bm);
+  const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
+  if (spec) return launch_spec(fns[small ? 1 : 0], nblk);
+  PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "%s: grid too large", fn);
+  const dim3 grid(static_cast<unsigned>(nblk));
+  if (ca.dtype == PDH_BF16) {
+    if (small)
+      contract_mfma_small<PDH_BF16><<<grid, 256, 0, st>>>(ca, *epi, ops);
+    else
+      contract_mfma<PDH_BF16><<<grid, 256, 0, st>>>(ca, *epi, ops);
+  } else {
+    if (small)
+      contract_mfma_small<PDH_F16><<<grid, 256, 0, st>>>(ca, *epi, ops);
+    else
+      contract_mfma<PDH_F16><<<grid, 256, 0, st>>>(ca, *epi, ops);
+  }
+  return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace pdh
+
 extern "C" int pdh_contract(const void* a, const void* bt, int64_t batch, int64_t m, int64_t n, int64_t k,
                             int64_t kp, const pdh_ew_program* epi, const void* const* operands, void* out, int dtype,
                             void* stream) {
-  int rc = check_program(epi, 3, true, "pdh_contract");
-  if (rc) return rc;
   PDH_REQUIRE(dtype_ok(dtype), PDH_EUNSUPPORTED, "pdh_contract: dtype %d", dtype);
   PDH_REQUIRE(a && bt && out, PDH_EINVAL, "pdh_contract: null pointer");
   PDH_REQUIRE(batch >= 1 && m >= 1 && n >= 1 && k >= 1, PDH_EINVAL, "pdh_contract: bad shape");
   PDH_REQUIRE(kp >= k && kp % kBK == 0, PDH_EINVAL, "pdh_contract: kp = %lld must be >= k and a multiple of %d",
               (long long)kp, kBK);
-  PDH_REQUIRE(epi->shape[0] == batch && epi->shape[1] == m && epi->shape[2] == n, PDH_EINVAL,
-              "pdh_contract: epilogue shape must be {batch, m, n}");
   PDH_REQUIRE(batch * m * n <= INT32_MAX && m <= INT32_MAX / 2 && n <= INT32_MAX / 2, PDH_EINVAL,
               "pdh_contract: output too large for one call");
   PDH_REQUIRE(aligned16(a) && aligned16(bt), PDH_EINVAL, "pdh_contract: a / bt must be 16-byte aligned");
-  PDH_REQUIRE(epi->n_operands == 0 || operands != nullptr, PDH_EINVAL, "pdh_contract: null operand table");
-  if ((rc = check_view(epi, epi->out_stride, "pdh_contract", "output"))) return rc;
-  EwOperands ops{};
-  for (int i = 0; i < epi->n_operands; ++i) {
-    PDH_REQUIRE(operands[i] != nullptr, PDH_EINVAL, "pdh_contract: operand %d is null", i);
-    if ((rc = check_view(epi, epi->in_stride[i], "pdh_contract", "operand"))) return rc;
-    ops.p[i] = operands[i];
-  }
-  hipStream_t st = as_stream(stream);
-  ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
-                  static_cast<int>(kp), 0, 0, dtype};
-  hipFunction_t fns[2];
-  const bool spec = jit_get(JitKind::Contract, *epi, dtype, fns);
-  pdh_ew_program pe = *epi;
-  void* args[] = {&ca, &pe, &ops};
-  if (dtype == PDH_F32) {
-    ca.tiles_m = static_cast<int>((m + kFT - 1) / kFT);
-    ca.tiles_n = static_cast<int>((n + kFT - 1) / kFT);
-    const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
-    PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_contract: grid too large");
-    if (spec) {
-      PDH_REQUIRE(hipModuleLaunchKernel(fns[0], static_cast<unsigned>(nblk), 1, 1, 256, 1, 1, 0, st, args, nullptr) ==
-                      hipSuccess,
-                  PDH_ELAUNCH, "pdh_contract: specialized launch failed");
-      jit_count_launch();
-      return PDH_OK;
-    }
-    contract_f32<<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
-    return check_launch("pdh_contract (f32)");
-  }
-  PDH_REQUIRE(m * kp * 2 <= UINT32_MAX && n * kp * 2 <= UINT32_MAX, PDH_EINVAL,
-              "pdh_contract: one batch slice of a / bt must stay under 4 GiB");
-  ca.tiles_m = static_cast<int>((m + kBM - 1) / kBM);
-  ca.tiles_n = static_cast<int>((n + kBN - 1) / kBN);
-  const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
-  PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_contract: grid too large");
-  if (spec) {
-    PDH_REQUIRE(hipModuleLaunchKernel(fns[0], static_cast<unsigned>(nblk), 1, 1, 256, 1, 1, 0, st, args, nullptr) ==
-                    hipSuccess,
-                PDH_ELAUNCH, "pdh_contract: specialized launch failed");
-    jit_count_launch();
-    return PDH_OK;
-  }
-  if (dtype == PDH_BF16)
-    contract_mfma<PDH_BF16><<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
-  else
-    contract_mfma<PDH_F16><<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
-  return check_launch("pdh_contract (mfma)");
+  const ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n),
+                        static_cast<int>(k), static_cast<int>(kp), 0, 0, dtype, m * kp, kp, n * kp, kp};
+  return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), "pdh_contract");
+}
+
+extern "C" int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, const void* bt, int64_t sb_b,
+                                    int64_t sb_r, int64_t batch, int64_t m, int64_t n, int64_t k,
+                                    const pdh_ew_program* epi, const void* const* operands, void* out, int dtype,
+                                    void* stream) {
+  PDH_REQUIRE(dtype_ok(dtype), PDH_EUNSUPPORTED, "pdh_contract_strided: dtype %d", dtype);
+  PDH_REQUIRE(a && bt && out, PDH_EINVAL, "pdh_contract_strided: null pointer");
+  PDH_REQUIRE(batch >= 1 && m >= 1 && n >= 1 && k >= 1 && k % kBK == 0, PDH_EINVAL,
+              "pdh_contract_strided: need batch, m, n >= 1 and k a positive multiple of %d", kBK);
+  PDH_REQUIRE(batch * m * n <= INT32_MAX && m <= INT32_MAX / 2 && n <= INT32_MAX / 2, PDH_EINVAL,
+              "pdh_contract_strided: output too large for one call");
+  const int64_t align = dtype == PDH_F32 ? 4 : 8;  // 16-byte rows and batch slices
+  PDH_REQUIRE(sa_r >= k && sb_r >= k && sa_b >= 0 && sb_b >= 0 && sa_r % align == 0 && sb_r % align == 0 &&
+                  sa_b % align == 0 && sb_b % align == 0,
+              PDH_EINVAL, "pdh_contract_strided: row strides must be >= k and all strides multiples of %lld",
+              (long long)align);
+  PDH_REQUIRE(aligned16(a) && aligned16(bt), PDH_EINVAL, "pdh_contract_strided: a / bt must be 16-byte aligned");
+  const ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n),
+                        static_cast<int>(k), static_cast<int>(k), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r};
+  return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), "pdh_contract_strided");
 }

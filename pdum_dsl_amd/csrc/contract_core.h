@@ -6,11 +6,14 @@
 //
 //   map_chain_body     one lane = EPT consecutive elements of the output's
 //                      last dim
-//   contract_mfma_body bf16 / f16: 128 x 128 workgroup tiles, 4 waves of
-//                      64 x 64 (2 x 2 v_mfma_f32_32x32x16), 64-wide k tiles
+//   contract_mfma_body bf16 / f16: 4 waves of WM x WM (WM = 64: 2 x 2
+//                      v_mfma_f32_32x32x16 per wave, 128 x 128 workgroup
+//                      tiles; WM = 32: one product per wave, 64 x 64 tiles
+//                      for grids too small to fill the chip), 64-wide k tiles
 //                      copied HBM -> LDS by direct buffer loads, double
 //                      buffered; XOR-swizzled 16-byte slots keep the b128
-//                      operand reads conflict-free for 32- and 64-bank LDS
+//                      operand reads conflict-free for 32- and 64-bank LDS;
+//                      a and bt are read through batch and row strides
 //   contract_f32_body  the fp32 column: 64 x 64 tiles, 4 x 4 outputs per
 //                      lane, VALU fma, k tiles of 16 through LDS
 // The epilogue program runs on the accumulators before the one store:
@@ -25,17 +28,22 @@ struct ContractArgs {
   const void* a;
   const void* bt;
   void* out;
-  int batch, m, n, k, kp;
+  int batch, m, n, k, kp;  // kp: the k extent read (a multiple of 64; columns k..kp-1 read as zero)
   int tiles_m, tiles_n;
   int dtype;
+  long long sa_b, sa_r, sb_b, sb_r;  // element strides of a and bt: per batch, per row (k is contiguous)
 };
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kRowB = kBK * 2;       // LDS bytes per tile row (64 16-bit k values)
-constexpr int kTileB = kBM * kRowB;  // 16 KB per operand tile
-constexpr int kAccRow = 68;          // floats per accumulator row in LDS (64 + pad)
-constexpr int kContractLds = 4 * kTileB > 4 * 64 * kAccRow * 4 ? 4 * kTileB : 4 * 64 * kAccRow * 4;
-constexpr int kFT = 64, kFK = 16;    // fp32 column tiles
+constexpr int kBK = 64;
+constexpr int kRowB = kBK * 2;  // LDS bytes per tile row (64 16-bit k values)
+constexpr int kFT = 64, kFK = 16;  // fp32 column tiles
+
+// LDS bytes of the WM variant: two double-buffered operand tiles of 2 WM rows,
+// or (epilogue) each wave's WM x WM accumulators with rows padded by 4 floats.
+template <int WM>
+constexpr int contract_lds() {
+  return 4 * (2 * WM) * kRowB > 4 * WM * (WM + 4) * 4 ? 4 * (2 * WM) * kRowB : 4 * WM * (WM + 4) * 4;
+}
 
 // ---------------------------------------------------------------- map chain
 
@@ -103,52 +111,62 @@ __device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const
   }
 }
 
-template <int DT, typename Eval>
+template <int DT, int WM, typename Eval>
 __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const pdh_ew_program& p,
                                                    const EwOperands& ops, unsigned char* smem) {
+  constexpr int BM = 2 * WM;          // workgroup tile (rows of a and of bt)
+  constexpr int TI = WM / 32;         // 32 x 32 products per wave and dim
+  constexpr int TILEB = BM * kRowB;   // LDS bytes per operand tile
+  constexpr int BLK = BM / 8 / 4;     // 8-row direct-load blocks per wave and operand
+  constexpr int ACCP = WM + 4;        // accumulator row pitch in LDS (floats)
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
-  const int wy = w >> 1, wx = w & 1;  // the wave's 64 x 64 quadrant
+  (void)tid;
+  const int wy = w >> 1, wx = w & 1;  // the wave's WM x WM quadrant
   const int per = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x / per, rest = blockIdx.x % per;
-  const int m0 = (rest / a.tiles_n) * kBM, n0 = (rest % a.tiles_n) * kBN;
-  const uint32_t rowb = static_cast<uint32_t>(a.kp) * 2u;
-  const uint16_t* abase = static_cast<const uint16_t*>(a.a) + static_cast<long long>(b) * a.m * a.kp;
-  const uint16_t* bbase = static_cast<const uint16_t*>(a.bt) + static_cast<long long>(b) * a.n * a.kp;
-  // rows past m (n) read as zero: the buffer ends at the batch slice's last row
-  const rsrc_t ar = make_rsrc(abase, static_cast<uint32_t>(static_cast<long long>(a.m) * rowb));
-  const rsrc_t br = make_rsrc(bbase, static_cast<uint32_t>(static_cast<long long>(a.n) * rowb));
+  const int m0 = (rest / a.tiles_n) * BM, n0 = (rest % a.tiles_n) * BM;
+  const uint32_t rowa = static_cast<uint32_t>(a.sa_r) * 2u, rowbb = static_cast<uint32_t>(a.sb_r) * 2u;
+  const uint16_t* abase = static_cast<const uint16_t*>(a.a) + b * a.sa_b;
+  const uint16_t* bbase = static_cast<const uint16_t*>(a.bt) + b * a.sb_b;
+  // the buffers end after the batch slice's last row: rows past m (n) read as zero
+  const rsrc_t ar = make_rsrc(abase, (static_cast<uint32_t>(a.m) - 1u) * rowa + static_cast<uint32_t>(a.kp) * 2u);
+  const rsrc_t br = make_rsrc(bbase, (static_cast<uint32_t>(a.n) - 1u) * rowbb + static_cast<uint32_t>(a.kp) * 2u);
 
   // direct loads: 1 KB = 8 tile rows; lane i -> row i / 8, slot i % 8 holds chunk slot ^ swz(row)
   const int lrow = lane >> 3, slot = lane & 7;
-  uint32_t dma_off[2];  // tile-row parity of the 8-row block decides the swizzle of row 8 j + lrow
+  uint32_t offa[2], offb[2];  // tile-row parity of the 8-row block decides the swizzle of row 8 j + lrow
 #pragma unroll
-  for (int par = 0; par < 2; ++par) dma_off[par] = lrow * rowb + ((slot ^ swz_gemm(8 * par + lrow)) << 4);
+  for (int par = 0; par < 2; ++par) {
+    const uint32_t sl = static_cast<uint32_t>((slot ^ swz_gemm(8 * par + lrow)) << 4);
+    offa[par] = lrow * rowa + sl;
+    offb[par] = lrow * rowbb + sl;
+  }
   auto stage = [&](int kt, int buf) {
-    unsigned char* at = smem + buf * kTileB;
-    unsigned char* bt = smem + (2 + buf) * kTileB;
+    unsigned char* at = smem + buf * TILEB;
+    unsigned char* bt = smem + (2 + buf) * TILEB;
+    const uint32_t koff = static_cast<uint32_t>(kt) * kBK * 2u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int blk = 4 * i + w;  // 16 blocks of 8 rows per operand tile
-      const uint32_t koff = static_cast<uint32_t>(kt) * kBK * 2u;
-      dma16(ar, at + blk * 1024, dma_off[blk & 1], static_cast<uint32_t>(m0 + 8 * blk) * rowb + koff);
-      dma16(br, bt + blk * 1024, dma_off[blk & 1], static_cast<uint32_t>(n0 + 8 * blk) * rowb + koff);
+    for (int i = 0; i < BLK; ++i) {
+      const int blk = 4 * i + w;  // BM / 8 blocks of 8 rows per operand tile
+      dma16(ar, at + blk * 1024, offa[blk & 1], static_cast<uint32_t>(m0 + 8 * blk) * rowa + koff);
+      dma16(br, bt + blk * 1024, offb[blk & 1], static_cast<uint32_t>(n0 + 8 * blk) * rowbb + koff);
     }
   };
-  // operand reads: row (64 q + 32 t + r32) of a tile, chunk 2 ks + g
-  int rd[2][4];
+  // operand reads: row (WM q + 32 t + r32) of a tile, chunk 2 ks + g
+  int rd[TI][4];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < TI; ++t)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int row = 32 * t + r32;  // + 64 q: a multiple of 16 rows, so the swizzle is unchanged
+      const int row = 32 * t + r32;  // + WM q: a multiple of 16 rows, so the swizzle is unchanged
       rd[t][ks] = row * kRowB + (((2 * ks + g) ^ swz_gemm(row)) << 4);
     }
 
-  f32x16 acc[2][2];
+  f32x16 acc[TI][TI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < TI; ++j) acc[i][j] = f32x16{};
 
   const int nkt = a.kp / kBK;
   stage(0, 0);
@@ -157,46 +175,46 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
     wait_vmcnt0();
     __syncthreads();
     if (kt + 1 < nkt) stage(kt + 1, buf ^ 1);
-    const unsigned char* at = smem + buf * kTileB + 64 * wy * kRowB;
-    const unsigned char* bt = smem + (2 + buf) * kTileB + 64 * wx * kRowB;
+    const unsigned char* at = smem + buf * TILEB + WM * wy * kRowB;
+    const unsigned char* bt = smem + (2 + buf) * TILEB + WM * wx * kRowB;
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      u32x4 af[2], bf[2];
+      u32x4 af[TI], bf[TI];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < TI; ++t) {
         af[t] = *reinterpret_cast<const u32x4*>(at + rd[t][ks]);
         bf[t] = *reinterpret_cast<const u32x4*>(bt + rd[t][ks]);
       }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32_dt<DT>(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < TI; ++j) acc[i][j] = mfma32_dt<DT>(af[i], bf[j], acc[i][j]);
     }
     __builtin_amdgcn_s_setprio(0);
   }
   wait_vmcnt0();
 
   // The epilogue reads the accumulators back from LDS (each wave its own
-  // 64 x 64 block, rows padded to 68 floats): one runtime loop, four
+  // WM x WM block, rows padded by 4 floats): one runtime loop, four
   // consecutive columns per lane, so one copy of the program's code.
   // Accumulator v of tile (i, j) is row 32 i + 8 (v / 4) + 4 g + v % 4,
   // column 32 j + r32 of the wave's block.
   __syncthreads();  // every wave is done with the operand tiles
-  float* blkf = reinterpret_cast<float*>(smem) + w * 64 * kAccRow;
+  float* blkf = reinterpret_cast<float*>(smem) + w * WM * ACCP;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TI; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) blkf[(32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * kAccRow + 32 * j + r32] = acc[i][j][v];
+      for (int v = 0; v < 16; ++v) blkf[(32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * ACCP + 32 * j + r32] = acc[i][j][v];
   __builtin_amdgcn_wave_barrier();  // the block is wave-private: in-order LDS, no workgroup barrier
-  for (int it = 0; it < 16; ++it) {
+  for (int it = 0; it < WM * WM / 256; ++it) {
     const int idx = it * 256 + lane * 4;
-    const int row = idx >> 6, col = idx & 63;
-    const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * kAccRow + col);
+    const int row = idx / WM, col = idx % WM;
+    const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * ACCP + col);
     const float av[4] = {av4[0], av4[1], av4[2], av4[3]};
-    contract_epilogue<DT, 4, Eval>(p, ops, a, b, m0 + 64 * wy + row, n0 + 64 * wx + col, av);
+    contract_epilogue<DT, 4, Eval>(p, ops, a, b, m0 + WM * wy + row, n0 + WM * wx + col, av);
   }
 }
 
@@ -209,15 +227,15 @@ __device__ __forceinline__ void contract_f32_body(const ContractArgs& a, const p
   const int per = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x / per, rest = blockIdx.x % per;
   const int m0 = (rest / a.tiles_n) * kFT, n0 = (rest % a.tiles_n) * kFT;
-  const float* abase = static_cast<const float*>(a.a) + static_cast<long long>(b) * a.m * a.kp;
-  const float* bbase = static_cast<const float*>(a.bt) + static_cast<long long>(b) * a.n * a.kp;
+  const float* abase = static_cast<const float*>(a.a) + b * a.sa_b;
+  const float* bbase = static_cast<const float*>(a.bt) + b * a.sb_b;
   const int lr = tid >> 2, lc = (tid & 3) * 4;  // this lane's tile row and 4 k values per load
   float acc[4][4] = {};
   for (int k0 = 0; k0 < a.kp; k0 += kFK) {
     const int am = m0 + lr, bn = n0 + lr;
     f32x4 av = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f};
-    if (am < a.m) av = *reinterpret_cast<const f32x4*>(abase + static_cast<long long>(am) * a.kp + k0 + lc);
-    if (bn < a.n) bv = *reinterpret_cast<const f32x4*>(bbase + static_cast<long long>(bn) * a.kp + k0 + lc);
+    if (am < a.m) av = *reinterpret_cast<const f32x4*>(abase + am * a.sa_r + k0 + lc);
+    if (bn < a.n) bv = *reinterpret_cast<const f32x4*>(bbase + bn * a.sb_r + k0 + lc);
     __syncthreads();  // the previous tile's reads are done
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

@@ -62,6 +62,25 @@ def _strides_by_name(names, shape) -> dict:
     return dict(zip(names, _dense_strides(shape)))
 
 
+def _strided_view(tt, riders, rows, kd):
+    """(batch, row) element strides under which a dense value of type ``tt``
+    reads as [batch][rows][k] with k contiguous, or None: its dims must be
+    exactly riders + rows + kd, the kd dims innermost in order, and the row
+    dims composing into one stride."""
+    names = tt.names
+    if set(names) != set(riders) | set(rows) | set(kd) or len(names) != len(riders) + len(rows) + len(kd):
+        return None
+    if tuple(names[len(names) - len(kd):]) != tuple(kd):
+        return None
+    st = _strides_by_name(names, tt.shape)
+    for a, b in zip(rows[:-1], rows[1:]):
+        if st[a] != st[b] * tt.dim(b).size:
+            return None
+    row = st[rows[-1]] if rows else 0
+    batch = st[riders[0]] if riders else 0
+    return (batch, row)
+
+
 def _yielding(k: Region, node) -> Region:
     """The region over k's params that yields ``node``."""
     return Region(params=k.params, body=(Builder(OPS).emit("core.yield", node),))
@@ -143,6 +162,7 @@ class _Pack:
     zero: bool = False
     pre: object = None
     pre_direct: bool = False
+    strides: tuple = ()  # (batch, row) element strides of the operand as the product reads it
 
 
 @dataclass
@@ -162,7 +182,7 @@ class PlanExecutor:
     """Runs a ModelPlan of ``region`` on the device. ``dtype`` is the element
     type of every floating value (f32, bf16 or f16)."""
 
-    def __init__(self, plan, region: Region, dtype: str = "bf16"):
+    def __init__(self, plan, region: Region, dtype: str = "bf16", _shared=None):
         if dtype not in _TORCH_DT:
             raise ValueError(f"dtype {dtype!r}: f32, bf16 or f16")
         self.region, self.dtype = region, dtype
@@ -170,6 +190,8 @@ class PlanExecutor:
         self.params = region.params
         self.nested: list = []
         self._bad: list = []
+        # weight packs and the ids of the bound floating tensors, shared with nested executors
+        self._packs, self._static = _shared if _shared is not None else ({}, set())
         have = {id(p) for p in region.params}
         self.alias: dict = {}  # rename view id -> the value id it reads
         pending = [c for c in plan.carves if c.root is not None]
@@ -254,7 +276,7 @@ class PlanExecutor:
         from .tl.partition import plan_model
 
         sub = _yielding(k, node)
-        nested = PlanExecutor(plan_model(sub, dissolve=False), sub, self.dtype)
+        nested = PlanExecutor(plan_model(sub, dissolve=False), sub, self.dtype, _shared=(self._packs, self._static))
         self.nested.append(nested)
 
         def run(vals):
@@ -320,16 +342,16 @@ class PlanExecutor:
             if len(lat) > L.EW_MAX_DIMS:
                 raise Untranslatable(f"an operand pack over {len(lat)} dims (max {L.EW_MAX_DIMS})")
             base = _base(core)
-            want = tuple(riders) + tuple(nm for nm in rows_names if not nm.startswith("_unit")) + tuple(kd)
-            if base.op == "core.param" and core.type.names == want and Kx == KP:
-                return _Pack(direct=self._index(k, base))
+            st = _strided_view(core.type, riders, [nm for nm in rows_names if not nm.startswith("_unit")], kd)
+            if base.op == "core.param" and st is not None and Kx == KP:
+                return _Pack(direct=self._index(k, base), strides=st)
             pre = None
             if any(n.op == "tl.reduce" for n in walk(_yielding(k, core))):
                 # carves dissolved into this operand (the traffic gate's
                 # re-derivation per tile): materialized once, by their own plan
                 pre = self._materialize(k, core)
-                if core.type.names == want and Kx == KP:
-                    return _Pack(direct=None, pre=pre, pre_direct=True)
+                if st is not None and Kx == KP:
+                    return _Pack(direct=None, pre=pre, pre_direct=True, strides=st)
             rs = KP * math.prod(size[nm].size for nm in rows_names)
             out_st = [rs if riders else 0]
             acc = KP
@@ -345,7 +367,7 @@ class PlanExecutor:
             out_st += kst
             low, prog = self._map_prog(k, core, lat, out_st, extra_leaves=(core,) if pre is not None else ())
             slots = tuple(None if (pre is not None and b is core) else self._index(k, b) for b in low.bases)
-            return _Pack(None, prog, slots, (B, nrows, KP), KP != Kx, pre)
+            return _Pack(None, prog, slots, (B, nrows, KP), KP != Kx, pre, strides=(nrows * KP, KP))
 
         pa, pb = pack(ca, mdims, M), pack(cb, ndims, N)
         y = k.body[-1].args[0] if yroot is None else yroot
@@ -375,22 +397,35 @@ class PlanExecutor:
 
             def build(p):
                 if p.direct is not None:
-                    return vals[p.direct].reshape(B, -1, KP)
+                    return vals[p.direct]
                 pv = p.pre(vals) if p.pre is not None else None
                 if p.pre_direct:
-                    return pv.reshape(B, -1, KP)
+                    return pv
+                ins = [pv if i is None else vals[i] for i in p.slots]
+                # a pack of bound parameters only (a weight's transpose) is
+                # made once per bind and reused by every run
+                key = (id(p), tuple(id(t) for t in ins))
+                static = pv is None and all(id(t) in self._static for t in ins)
+                if static and key in self._packs:
+                    return self._packs[key]
                 buf = (torch.zeros if p.zero else torch.empty)(p.shape, device="cuda", dtype=dt)
-                K.map_chain(p.prog, [pv if i is None else vals[i] for i in p.slots], buf)
+                K.map_chain(p.prog, ins, buf)
+                if static:
+                    self._packs[key] = buf
                 return buf
 
             a, bt = build(pa), build(pb)
             out = torch.empty(shape, device="cuda", dtype=dt)
-            K.contract(a, bt, Kx, prog, [vals[i] for i in eslots], out)
+            if KP == Kx:  # every operand as stored (or as packed), through its strides
+                K.contract_strided(a, pa.strides, bt, pb.strides, (B, M, N, Kx), prog,
+                                   [vals[i] for i in eslots], out)
+            else:  # zero-padded packs
+                K.contract(a, bt, Kx, prog, [vals[i] for i in eslots], out)
             return out
 
         def how(p):
-            return "direct" if p.direct is not None else ("contract" if p.pre_direct else
-                                                          ("contract+pack" if p.pre else "pack"))
+            return "direct" if p.direct is not None else ("plan" if p.pre_direct else
+                                                          ("plan+pack" if p.pre else "pack"))
 
         src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
         return run, src
@@ -509,6 +544,9 @@ class PlanExecutor:
                 t = t.to(device="cuda", dtype=dt)
             bound[id(p)] = t.contiguous()
         self.bound = bound
+        self._packs.clear()
+        self._static.clear()
+        self._static.update(id(t) for t in bound.values() if t.is_floating_point())
 
     def run(self):
         """One pass over the plan; returns the output (device tensor, dims in

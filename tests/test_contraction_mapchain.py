@@ -322,4 +322,4 @@ def test_specialized_kernels_compile_offline_for_every_element_type():
     src = buf.value.decode()
     assert n == len(src) and "0x1.988454p-1f" in src and "tanhf(" in src and "acc[e]" in src
     assert len(re.findall(r"^      r\d+ = ", src, re.M)) == epi.n_insns  # one statement per instruction
-    assert "contract_mfma_body<PDH_BF16, pdh::GenEval>" in src
+    assert "contract_mfma_body<PDH_BF16, 64, pdh::GenEval>" in src and "contract_mfma_body<PDH_BF16, 32, pdh::GenEval>" in src

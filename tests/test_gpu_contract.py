@@ -105,12 +105,13 @@ def test_a_prologue_chain_runs_before_the_contraction(dtype):
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-def test_the_abi_is_a_batched_gemm_with_an_identity_epilogue(dt):
+@pytest.mark.parametrize("B,M,N", [(2, 300, 260), (2, 1100, 2100)])  # 64x64 tiles; 128x128 tiles
+def test_the_abi_is_a_batched_gemm_with_an_identity_epilogue(dt, B, M, N):
     from pdum_dsl_amd import _lib as L
     from pdum_dsl_amd import kernels as K
 
     g = torch.Generator(device="cuda").manual_seed(11)
-    B, M, N, Kd = 2, 300, 260, 200
+    Kd = 200
     KP = 256
     a = torch.zeros(B, M, KP, device="cuda", dtype=dt)
     bt = torch.zeros(B, N, KP, device="cuda", dtype=dt)
@@ -129,6 +130,34 @@ def test_the_abi_is_a_batched_gemm_with_an_identity_epilogue(dt):
         torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-4)
     else:
         assert_lowp(out.float().cpu().numpy(), ref.cpu().numpy(), what="bf16 gemm")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,H", [(256, 4), (1024, 12)])
+def test_strided_operands_feed_a_head_major_product_without_copies(dt, T, H):
+    """scores[h, t, s] = sum_e q[t, h, e] k[s, h, e]: q and k stay in their
+    (t, heads, head_dim) storage; the batch is the head (stride head_dim), a
+    row is a position (stride heads * head_dim)."""
+    from pdum_dsl_amd import _lib as L
+    from pdum_dsl_amd import kernels as K
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    E = 64
+    q = torch.randn(T, H, E, device="cuda", generator=g).to(dt)
+    k = torch.randn(T + 7, H, E, device="cuda", generator=g).to(dt)
+    out = torch.empty(H, T, T + 7, device="cuda", dtype=dt)
+    p = L.EwProgram()
+    p.n_insns, p.n_operands, p.ndim, p.out_reg = 1, 0, 3, 0
+    for d, (ext, st) in enumerate(zip(out.shape, out.stride())):
+        p.shape[d], p.out_stride[d] = ext, st
+    p.insns[0].op = L.EW["ACC"]
+    K.contract_strided(q, (E, H * E), k, (E, H * E), (H, T, T + 7, E), p, [], out)
+    torch.cuda.synchronize()
+    ref = torch.einsum("the,she->hts", q.double().cpu(), k.double().cpu())
+    if dt == torch.float32:
+        torch.testing.assert_close(out.double().cpu(), ref, rtol=1e-5, atol=1e-4)
+    else:
+        assert_lowp(out.float().cpu().numpy(), ref.numpy(), what="strided bf16 gemm")
 
 
 def test_malformed_programs_refuse_without_launching():
