@@ -320,8 +320,10 @@ def _carved_plan_line(torch):
     """gpt2-small's shape (12 layers, t=1024, d=768, 12 heads of 64, mlp 3072,
     vocab 50257), random weights, bf16: planned by plan_model (the
     anchor-and-absorb partition) and run by the device executor, every
-    boundary in HBM. Checked against the same forward in fp32 on the same
-    bf16 weights; timed beside torch's own bf16 forward."""
+    boundary in HBM, the pass captured as one HIP graph (``ms``; the
+    per-kernel launched pass is ``ms_eager_launches``). Checked against the
+    same forward in fp32 on the same bf16 weights; timed beside torch's own
+    bf16 forward (eager)."""
     import time as _time
 
     from pdum_dsl_amd.executor import PlanExecutor
@@ -352,7 +354,13 @@ def _carved_plan_line(torch):
     err = float((gotv - want).abs().max())
     assert err < 5e-2 * scale, f"carved-plan parity failed: {err} vs scale {scale}"
     del W32, want, gotv
-    ms = time_events(ex.run, 10)
+    eager = ex.run().clone()
+    ms_eager = time_events(ex.run, 10)
+    ex.capture()
+    replayed = ex.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(replayed, eager), "the captured plan's replay differs from the eager pass"
+    ms = time_events(lambda: ex.replay(check=False), 20)
     ms_torch = time_events(lambda: _gpt2_torch(torch, W, cfg), 10)
     T, D, M, V, L_ = cfg.t, cfg.d, cfg.m, cfg.v, cfg.layers
     fl = 2.0 * T * (L_ * (4 * D * D + 2 * D * M) + D * V) + L_ * 4.0 * T * T * D
@@ -363,7 +371,8 @@ def _carved_plan_line(torch):
         "config": "gpt2-small shape, 12 layers, t=1024 tokens, d=768, 12x64 heads, mlp 3072, vocab 50257, bf16 "
                   "storage / fp32 accumulate; random weights",
         "carves": by, "device_steps": len(ex.steps) + sum(len(n.steps) for n in ex.nested),
-        "plan_s": round(plan_s, 2), "ms": round(ms, 4), "tokens_per_s": round(T / ms * 1e3, 1),
+        "plan_s": round(plan_s, 2), "ms": round(ms, 4), "ms_eager_launches": round(ms_eager, 4),
+        "tokens_per_s": round(T / ms * 1e3, 1),
         "TFLOP/s": round(fl / ms / 1e9, 1), "algorithmic_flop": fl,
         "torch_eager_ms": round(ms_torch, 4), "max_abs_err_vs_f32": err, "logit_scale": scale,
     }

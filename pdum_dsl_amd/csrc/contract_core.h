@@ -38,11 +38,28 @@ constexpr int kBK = 64;
 constexpr int kRowB = kBK * 2;  // LDS bytes per tile row (64 16-bit k values)
 constexpr int kFT = 64, kFK = 16;  // fp32 column tiles
 
-// LDS bytes of the WM variant: two double-buffered operand tiles of 2 WM rows,
+// k tiles in flight: the 128 x 128 variant double buffers (two workgroups
+// per CU hide the load latency), the 64 x 64 one, which serves grids of
+// under one workgroup per CU, keeps four k tiles in flight instead.
+template <int WM>
+constexpr int contract_stages() {
+  return WM == 64 ? 2 : 4;
+}
+
+// LDS bytes of the WM variant: the operand tiles of 2 WM rows of every stage,
 // or (epilogue) each wave's WM x WM accumulators with rows padded by 4 floats.
 template <int WM>
 constexpr int contract_lds() {
-  return 4 * (2 * WM) * kRowB > 4 * WM * (WM + 4) * 4 ? 4 * (2 * WM) * kRowB : 4 * WM * (WM + 4) * 4;
+  return 2 * contract_stages<WM>() * (2 * WM) * kRowB > 4 * WM * (WM + 4) * 4
+             ? 2 * contract_stages<WM>() * (2 * WM) * kRowB
+             : 4 * WM * (WM + 4) * 4;
+}
+
+// s_waitcnt vmcnt(N) with the other counters at their maxima (N < 64).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
 }
 
 // ---------------------------------------------------------------- map chain
@@ -119,6 +136,8 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
   constexpr int TILEB = BM * kRowB;   // LDS bytes per operand tile
   constexpr int BLK = BM / 8 / 4;     // 8-row direct-load blocks per wave and operand
   constexpr int ACCP = WM + 4;        // accumulator row pitch in LDS (floats)
+  constexpr int NS = contract_stages<WM>();
+  constexpr int PER_STAGE = 2 * BLK;  // direct loads per wave and k tile
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
   (void)tid;
   const int wy = w >> 1, wx = w & 1;  // the wave's WM x WM quadrant
@@ -141,9 +160,9 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
     offa[par] = lrow * rowa + sl;
     offb[par] = lrow * rowbb + sl;
   }
-  auto stage = [&](int kt, int buf) {
-    unsigned char* at = smem + buf * TILEB;
-    unsigned char* bt = smem + (2 + buf) * TILEB;
+  auto stage = [&](int kt, int buf) {  // stage buf: a tile at 2 buf, bt tile at 2 buf + 1
+    unsigned char* at = smem + (2 * buf) * TILEB;
+    unsigned char* bt = smem + (2 * buf + 1) * TILEB;
     const uint32_t koff = static_cast<uint32_t>(kt) * kBK * 2u;
 #pragma unroll
     for (int i = 0; i < BLK; ++i) {
@@ -169,14 +188,20 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
     for (int j = 0; j < TI; ++j) acc[i][j] = f32x16{};
 
   const int nkt = a.kp / kBK;
-  stage(0, 0);
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nkt) stage(s, s);
   for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    wait_vmcnt0();
-    __syncthreads();
-    if (kt + 1 < nkt) stage(kt + 1, buf ^ 1);
-    const unsigned char* at = smem + buf * TILEB + WM * wy * kRowB;
-    const unsigned char* bt = smem + (2 + buf) * TILEB + WM * wx * kRowB;
+    const int buf = kt % NS;
+    // tile kt has landed when at most the NS - 2 later tiles' loads are outstanding
+    if (kt + NS - 2 < nkt)
+      wait_vmcnt<(NS - 2) * PER_STAGE>();
+    else
+      wait_vmcnt0();
+    __syncthreads();  // every wave's loads of tile kt are done; everyone finished tile kt - 1
+    if (kt + NS - 1 < nkt) stage(kt + NS - 1, (kt + NS - 1) % NS);
+    const unsigned char* at = smem + (2 * buf) * TILEB + WM * wy * kRowB;
+    const unsigned char* bt = smem + (2 * buf + 1) * TILEB + WM * wx * kRowB;
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {

@@ -544,6 +544,7 @@ class PlanExecutor:
                 t = t.to(device="cuda", dtype=dt)
             bound[id(p)] = t.contiguous()
         self.bound = bound
+        self._graph = None
         self._packs.clear()
         self._static.clear()
         self._static.update(id(t) for t in bound.values() if t.is_floating_point())
@@ -559,6 +560,41 @@ class PlanExecutor:
             if int(bad.item()) != 0:
                 raise IndexError(f"tl.take: {int(bad.item())} index(es) outside the table")
         return out
+
+    def capture(self):
+        """Record one pass as a HIP graph (torch.cuda.CUDAGraph over the
+        stream every kernel here launches on), so a replay issues the whole
+        model with no host work per kernel. A warm-up pass first compiles the
+        specialized kernels and fills the weight-pack cache outside the
+        capture. Returns the graph's output tensor (rewritten by every
+        replay). Re-capture after ``bind``."""
+        torch = _torch()
+        if self.bound is None:
+            raise RuntimeError("bind() the params first")
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._run(self.bound, [])
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        bads: list = []
+        with torch.cuda.graph(graph):
+            out = self._run(self.bound, bads)
+        self._graph, self._graph_out, self._graph_bads = graph, out, bads
+        return out
+
+    def replay(self, check: bool = True):
+        """Replay the captured pass; with ``check``, synchronize and raise if a
+        gather saw an index out of range."""
+        if getattr(self, "_graph", None) is None:
+            raise RuntimeError("capture() first")
+        self._graph.replay()
+        if check:
+            for bad in self._graph_bads:
+                if int(bad.item()) != 0:
+                    raise IndexError(f"tl.take: {int(bad.item())} index(es) outside the table")
+        return self._graph_out
 
     def _run(self, bound: dict, bads: list):
         self._bad = bads

@@ -99,3 +99,26 @@ def test_take_rows_is_a_bit_exact_gather(dt):
     idx[1, 2] = 50
     got = K.take_rows(table, idx, bad=bad)
     assert int(bad.item()) == 1 and torch.count_nonzero(got[1, 2]).item() == 0
+
+
+def test_a_captured_plan_replays_the_eager_result():
+    """The whole carved forward as one HIP graph: replays, with eager work and
+    synchronizations between them, each give the eager pass's output."""
+    from pdum_dsl_amd import kernels as K
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import zoo
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    cfg = zoo.GPT2Config(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)
+    m = zoo.gpt2(cfg, seed=3)
+    ex = PlanExecutor(plan_model(m.region), m.region, "bf16")
+    ex.bind(m.values())
+    eager = ex.run().clone()
+    ex.capture()
+    for i in range(4):
+        junk = K.row_softmax(torch.randn(64, 256, device="cuda"))  # eager work between replays
+        torch.cuda.synchronize()
+        got = ex.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager), f"replay {i} differs from the eager pass"
+        del junk
