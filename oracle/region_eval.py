@@ -17,7 +17,8 @@ planner's numpy interpreter, so each can check the other:
                  (compute.py:184-214; region_evaluator.py:320-352)
   tl.repeat_like / tl.repeat / tl.split / tl.stage / tl.select / tl.iota /
   tl.const       layout views (region_evaluator.py:372-430)
-  tl.rename / tl.take   a relabeling; the gather (indexing.py:120-230)
+  tl.rename / tl.shift / tl.slice   relabelings and a window (layout.py)
+  tl.take        the gather (indexing.py:120-230)
   tl.fold        a Python loop over the scan dim, each element source
                  selected at the ABSOLUTE coordinate (dialect.py:1448-1470;
                  region_evaluator.py:431-465)
@@ -180,9 +181,15 @@ def _dispatch(n, ev):
         shape[ax] = hi - lo
         coords = torch.arange(lo, hi, dtype=torch.float64).reshape(shape)
         return V(coords.expand([d[2] - d[1] for d in dims]), dims)
-    if op == "tl.rename":  # layout.py rename: a relabeling, no data moves
+    if op in ("tl.rename", "tl.shift"):  # layout.py rename / shift: relabelings, no data moves
         x = ev(n.args[0])
         return V(x.t, tuple((d.name, d.start, d.stop) for d in n.type.dims))
+    if op == "tl.slice":  # layout.py slice: absolute [lo, hi) per dim
+        x = ev(n.args[0])
+        t = x.t
+        for ax, (d, o) in enumerate(zip(x.dims, n.type.dims)):
+            t = t.narrow(ax, o.start - d[1], o.stop - o.start)
+        return V(t, tuple((d.name, d.start, d.stop) for d in n.type.dims))
     if op == "tl.take":  # indexing.py:192-230: the taken dim replaced in place by idx's dims
         table, idx = ev(n.args[0]), ev(n.args[1])
         name = _attr(n, "dim")

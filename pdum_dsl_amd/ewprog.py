@@ -37,9 +37,28 @@ class Unlowerable(Exception):
 class Lowered:
     insns: list  # (op, dst, a, b, c, imm)
     out_reg: int
-    operands: tuple  # the node each LOAD slot reads (a leaf, or a tl.rename of one), slot order
+    operands: tuple  # the node each LOAD slot reads (a leaf, or a view chain over one), slot order
     dims: tuple  # output lattice dims (ir.Dim), outermost first
-    bases: tuple = ()  # the leaf under each slot (renames peeled)
+    bases: tuple = ()  # the leaf under each slot (views peeled)
+    views: tuple = ()  # per slot: (slot dim name -> leaf dim name, leaf dim name -> frame shift)
+
+    def operand_view(self, i: int, leaf_strides: dict) -> tuple:
+        """(element strides over ``dims``, element offset) at which slot ``i``
+        reads its leaf, given the leaf's strides by dim name: lattice index
+        j along dim d reads leaf coordinate d.start + j - shift, i.e. storage
+        index d.start + j - shift - leaf start."""
+        names, shift = self.views[i]
+        leaf = self.bases[i]
+        start = {d.name: d.start for d in leaf.type.dims}
+        strides, off = [], 0
+        for d in self.dims:
+            if d.name in names:
+                b = names[d.name]
+                strides.append(int(leaf_strides[b]))
+                off += (d.start - shift.get(b, 0) - start[b]) * int(leaf_strides[b])
+            else:
+                strides.append(0)
+        return strides, off
 
     def program(self, out_strides, operand_strides) -> L.EwProgram:
         """The C struct, given the output's and each operand's element
@@ -68,23 +87,40 @@ def _const_value(n):
     return None
 
 
-def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None) -> Lowered:
+def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, allow_views: bool = False) -> Lowered:
     """Lower the chain ending at ``root``. ``leaves`` maps id(node) -> node
-    for nodes read with LOAD (slot order = first use); a tl.rename of a leaf
-    is read as a LOAD of that leaf under the renamed dims (a rename moves no
-    data). ``acc`` is the node read with ACC (a contraction's fold), if any;
-    ``acc_scale`` multiplies it (a mean's finalize)."""
+    for nodes read with LOAD (slot order = first use). A chain of layout views
+    over a leaf (tl.rename, tl.stage; with ``allow_views`` also tl.shift and
+    tl.slice, whose reads start at an offset the caller applies through
+    ``Lowered.operand_view``) is one LOAD slot: views move no data. ``acc`` is
+    the node read with ACC (a contraction's fold), if any; ``acc_scale``
+    multiplies it (a mean's finalize)."""
     names = tuple(d.name for d in dims)
     order: list = []
     seen: set = set()
+    walkable = ("tl.rename", "tl.stage") + (("tl.shift", "tl.slice") if allow_views else ())
 
     def base_of(x):
-        while x.op == "tl.rename" and id(x) not in leaves:
+        while x.op in walkable and id(x) not in leaves:
             x = x.args[0]
         return x if id(x) in leaves else None
 
-    def is_leaf(x):
-        return id(x) in leaves or (x.op == "tl.rename" and base_of(x) is not None)
+    def is_leaf(x):  # a stage over a leaf is skipped as a view instead (the leaf is the slot)
+        return id(x) in leaves or (x.op in walkable and x.op != "tl.stage" and base_of(x) is not None)
+
+    def view_of(x):
+        to_cur = {n: n for n in x.type.names}  # slot name -> name in the current frame
+        shift: dict = {}  # current-frame name -> accumulated frame shift
+        while id(x) not in leaves:
+            if x.op == "tl.shift":
+                for nm, dl in x.attr("deltas"):
+                    shift[nm] = shift.get(nm, 0) + int(dl)
+            elif x.op == "tl.rename":
+                inv = {new: old for old, new in x.attr("mapping")}
+                to_cur = {k: inv.get(v, v) for k, v in to_cur.items()}
+                shift = {inv.get(k, k): v for k, v in shift.items()}
+            x = x.args[0]
+        return to_cur, shift
 
     def visit(n):  # post-order over the chain, stopping at leaves
         stack = [(n, False)]
@@ -205,7 +241,8 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None) ->
         reg[id(x)] = r
     if len(insns) > L.EW_MAX_INSNS:
         raise Unlowerable(f"{len(insns)} instructions (max {L.EW_MAX_INSNS})")
-    return Lowered(insns, reg[id(root_v)], tuple(slots), tuple(dims), tuple(base_of(x) for x in slots))
+    return Lowered(insns, reg[id(root_v)], tuple(slots), tuple(dims), tuple(base_of(x) for x in slots),
+                   tuple(view_of(x) for x in slots))
 
 
 def strides_over(arr_strides, arr_names, dims) -> list:

@@ -244,7 +244,7 @@ class PlanExecutor:
             run, src = self._softmax(k)
         elif tmpl == "row-statistics":
             run, src = self._layernorm(k)
-        elif tmpl == "map-chain":
+        elif tmpl in ("map-chain", "stencil"):
             run, src = self._map_chain(k)
         elif carve.group.confidence == "red" and any(n.op == "tl.take" for n in walk(k)):
             run, src = self._take(k)
@@ -285,9 +285,23 @@ class PlanExecutor:
         return run
 
     def _map_chain(self, k):
+        """A map chain or stencil carve: shifted / sliced reads of a value
+        are offset views of its one stored tensor."""
         y = k.body[-1].args[0]
-        low, prog = self._map_prog(k, y, y.type.dims, _dense_strides(y.type.shape))
-        slots = tuple(self._index(k, b) for b in low.bases)
+        leaves = {id(p): p for p in k.params}
+        try:
+            low = ewprog.lower(y, y.type.dims, leaves, allow_views=True)
+        except ewprog.Unlowerable as exc:
+            raise Untranslatable(f"map chain: {exc}") from None
+        slots, views = [], []
+        for j, base in enumerate(low.bases):
+            st, off = low.operand_view(j, _strides_by_name(base.type.names, base.type.shape))
+            if off < 0:
+                raise Untranslatable("a shifted read starts before its tensor")
+            slots.append(self._index(k, base))
+            views.append((st, off))
+        prog = low.program(_dense_strides(y.type.shape), [st for st, _off in views])
+        offs = [off for _st, off in views]
         shape = y.type.shape
 
         def run(vals):
@@ -295,10 +309,10 @@ class PlanExecutor:
             from . import kernels as K
 
             out = torch.empty(shape, device="cuda", dtype=getattr(torch, _TORCH_DT[self.dtype]))
-            K.map_chain(prog, [vals[i] for i in slots], out)
+            K.map_chain(prog, [vals[i].reshape(-1)[o:] for i, o in zip(slots, offs)], out)
             return out
 
-        return run, f"map_chain insns={len(low.insns)}"
+        return run, f"map_chain insns={len(low.insns)} shifted={sum(1 for o in offs if o)}"
 
     def _contraction(self, k, yroot=None):
         """GEMM-shaped contraction with its epilogue (and prologue chains)."""

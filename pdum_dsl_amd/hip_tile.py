@@ -496,7 +496,7 @@ def _flash_joint_runner(region, fj, grid, dtype):
 # ------------------------------------------- map-chain and contraction-epilogue
 
 _CHAIN_OPS = {"core.param", "core.yield", "core.const", "tl.const", "tl.iota", "tl.pointwise", "tl.repeat_like",
-              "tl.repeat", "tl.stage"}
+              "tl.repeat", "tl.stage", "tl.rename", "tl.shift", "tl.slice"}
 _TORCH_DT = {"f32": "float32", "bf16": "bfloat16", "f16": "float16"}
 
 
@@ -532,25 +532,36 @@ def _map_chain_runner(region, grid, dtype):
     dims = y.type.dims
     leaves = {id(p): p for p in region.params}
     try:
-        low = ewprog.lower(y, dims, leaves)
+        low = ewprog.lower(y, dims, leaves, allow_views=True)
     except ewprog.Unlowerable as exc:
         raise Untranslatable(f"map-chain: {exc}") from None
     idx = [_index(region, p) for p in low.bases]
     out_names = y.type.names
+    shifted = sum(1 for _names, sh in low.views if any(sh.values()))
 
     def run(values):
         torch = _torch()
-        ops = [_upload(torch, values[i], p.type.names, p.type.names, dtype) for i, p in zip(idx, low.operands)]
-        strides = [ewprog.strides_over(t.stride(), p.type.names, dims) for t, p in zip(ops, low.operands)]
+        uploaded = {}
+        ops, strides = [], []
+        for j, (i, base) in enumerate(zip(idx, low.bases)):
+            if i not in uploaded:  # each param once; shifted reads are offset views of it
+                uploaded[i] = _upload(torch, values[i], base.type.names, base.type.names, dtype)
+            t = uploaded[i]
+            st, off = low.operand_view(j, dict(zip(base.type.names, t.stride())))
+            if off < 0:
+                raise Untranslatable("a shifted read starts before its tensor")
+            ops.append(t.reshape(-1)[off:])
+            strides.append(st)
         out = torch.empty(tuple(d.size for d in dims), device="cuda", dtype=getattr(torch, _TORCH_DT[dtype]))
         prog = low.program(out.stride(), strides)
         K.map_chain(prog, ops, out)
         torch.cuda.synchronize()
         return out.float().cpu().numpy().reshape(tuple(d.size for d in dims))
 
+    tmpl = "stencil" if shifted else "map-chain"
     src = (f"hip:map_chain lattice=({','.join(out_names)}) insns={len(low.insns)} operands={len(low.operands)} "
-           "sweeps=1 stores=1")
-    return _finish(run, src, grid, "map-chain")
+           f"shifted_reads={shifted} sweeps=1 stores=1")
+    return _finish(run, src, grid, tmpl)
 
 
 def recognize_contraction(region: Region):

@@ -15,6 +15,8 @@ emit and consume (packages/tensorlib/src/pdum/tl/dialect.py:115-487):
   tl.const      value, dims     a constant field
   tl.fold       dim, state, element, out, step region
   tl.rename     mapping         renames dims in place (a view: no data moves)
+  tl.shift      deltas          moves dims' frames by integer deltas (a view)
+  tl.slice      ranges          restricts dims to absolute [lo, hi) (a view)
   tl.take       dim             out = table[idx, rest]: a gather, no template row
   tl.argtopk    (typed only: a non-template op the planner must refuse)
 """
@@ -177,6 +179,35 @@ def _r_rename(args, at, regions):
     return TensorType(tuple(Dim(mapping.get(d.name, d.name), d.start, d.stop) for d in x.dims))
 
 
+def _r_shift(args, at, regions):
+    """Moves dims' frames: [start, stop) -> [start + d, stop + d); the value at
+    new coordinate c is the input's at c - d (layout.py shift)."""
+    (x,) = args
+    deltas = dict(at["deltas"])
+    for nm in deltas:
+        x.dim(nm)
+    return TensorType(tuple(Dim(d.name, d.start + int(deltas.get(d.name, 0)), d.stop + int(deltas.get(d.name, 0)))
+                            for d in x.dims))
+
+
+def _r_slice(args, at, regions):
+    """Restricts dims to [lo, hi) in absolute coordinates, inside their domains."""
+    (x,) = args
+    ranges = dict(at["ranges"])
+    out = []
+    for d in x.dims:
+        if d.name in ranges:
+            lo, hi = (int(v) for v in ranges[d.name])
+            if not d.start <= lo <= hi <= d.stop:
+                raise TypeError(f"tl.slice {d.name}=[{lo}, {hi}) outside [{d.start}, {d.stop})")
+            out.append(Dim(d.name, lo, hi))
+        else:
+            out.append(d)
+    for nm in ranges:
+        x.dim(nm)
+    return TensorType(tuple(out))
+
+
 def _r_take(args, at, regions):
     """out = table[idx, rest]: the taken dim is replaced IN PLACE by idx's dims
     (indexing.py:120-138); idx dims the table already carries must align."""
@@ -223,6 +254,8 @@ OPS: dict[str, OpDef] = {
     "tl.fold": OpDef("tl.fold", _r_fold, nregions=1),
     "tl.argtopk": OpDef("tl.argtopk", _r_argtopk),
     "tl.rename": OpDef("tl.rename", _r_rename),
+    "tl.shift": OpDef("tl.shift", _r_shift),
+    "tl.slice": OpDef("tl.slice", _r_slice),
     "tl.take": OpDef("tl.take", _r_take),
 }
 

@@ -42,7 +42,7 @@ from .launch import fit_affine, propose, tri_eval
 
 _MAP_OPS = frozenset(
     {"core.param", "core.const", "core.yield", "tl.pointwise", "tl.iota", "tl.const", "tl.select", "tl.split",
-     "tl.repeat", "tl.repeat_like", "tl.rename"}
+     "tl.repeat", "tl.repeat_like", "tl.rename", "tl.shift", "tl.slice"}
 )
 _EXACT_OPS = frozenset({"tl.pointwise", "tl.repeat_like", "tl.rename", "tl.repeat", "tl.iota", "core.const",
                         "tl.const"})
@@ -619,6 +619,26 @@ def plan_region(region: Region, machine=None, floor: int = 1024) -> Plan:
     return Plan(tuple(groups))
 
 
+def _layout_root(n):
+    """The value under a chain of layout views (fusion.py:353-356)."""
+    while n.op in ("tl.shift", "tl.slice", "tl.stage", "tl.rename"):
+        n = n.args[0]
+    return n
+
+
+def neighborhood_params(region: Region) -> frozenset:
+    """The stencil signal (fusion.py:359-368): params read at two or more
+    DISTINCT shifts have overlapping neighborhoods, so staging their halo
+    once pays."""
+    shifts: dict = {}
+    for n in walk(region):
+        if n.op == "tl.shift":
+            root = _layout_root(n.args[0])
+            if root.op == "core.param":
+                shifts.setdefault(id(root), set()).add(n.attrs)
+    return frozenset(pid for pid, deltas in shifts.items() if len(deltas) >= 2)
+
+
 def _is_map_chain(region: Region):
     for n in walk(region):
         if n.op not in _MAP_OPS:
@@ -668,6 +688,12 @@ def _recognize(region: Region) -> Plan:
             return Plan((Group("row-statistics", kernel, _cert_fact(kernel, region, "exact"), "yellow"),))
     offender = _is_map_chain(region)
     if offender is None:
+        halos = neighborhood_params(region)
+        if halos:  # the stencil row (fusion.py:846-851): halos staged once, exact by erasure
+            kernel = stage_params(region, halos)
+            idxs = tuple(i for i, p in enumerate(region.params) if id(p) in halos)
+            return Plan((Group("stencil", kernel, _cert_fact(kernel, region, "exact"), "yellow",
+                               params=(("staged", idxs),)),))
         kernel = check_tier(region)
         return Plan((Group("map-chain", kernel, _cert_fact(kernel, region, "exact"), "yellow"),))
     return Plan(

@@ -147,9 +147,13 @@ def run_region(region: Region, values: list):
             shape[ax] = d.size
             coords = np.arange(d.start, d.stop, dtype=np.int64).reshape(shape)
             return Field(np.broadcast_to(coords, tt.shape), tt.dims)
-        if op == "tl.rename":
+        if op in ("tl.rename", "tl.shift"):  # relabelings: names or frames move, values stay
             x = ev(n.args[0])
             return Field(x.arr, n.type.dims)
+        if op == "tl.slice":
+            x = ev(n.args[0])
+            idx = tuple(slice(o.start - d.start, o.stop - d.start) for d, o in zip(x.dims, n.type.dims))
+            return Field(x.arr[idx], n.type.dims)
         if op == "tl.take":
             table, idx = ev(n.args[0]), ev(n.args[1])
             dim = n.attr("dim")

@@ -432,3 +432,87 @@ def gpt2(cfg: GPT2Config = GPT2Config(), seed: int = 7) -> Model:
         return hf_ @ inp["wte"].T
 
     return Model(region, inputs, ref, ("t", "v"), names)
+
+
+# -------------------------------------------------------- tile flagships
+
+
+@dataclass(frozen=True)
+class Flagship:
+    """A hand-written tile program beside its naive twin (zoo/tiles.py:32-40)."""
+
+    region: Region  # the tile-tier program
+    naive: Region  # the erased idiom: the denotation
+    inputs: list  # Field values, positional per param (both regions)
+    oracle: Callable  # list[np.ndarray] -> np.ndarray
+
+
+def stencil_tile(MI: int = 6, NI: int = 8, alpha: float = 0.1, seed: int = 17) -> Flagship:
+    """The fused 5-point stencil step (zoo/tiles.py:94-140): the halo u over
+    [0, MI+2) x [0, NI+2); neighbor(dx, dy) = u shifted by (-dx, -dy) and
+    sliced to the interior [1, MI+1) x [1, NI+1); out = u + alpha * (sum of
+    the four neighbors - 4 u). The tile program reads every neighbor from
+    the halo staged once to "shared"; the twin reads the param."""
+    rng = np.random.default_rng(seed)
+    U = rng.standard_normal((MI + 2, NI + 2))
+
+    def body(b, halo):
+        def neighbor(dx, dy):
+            sh = b.emit("tl.shift", halo, deltas=(("x", -dx), ("y", -dy)))
+            return b.emit("tl.slice", sh, ranges=(("x", (1, MI + 1)), ("y", (1, NI + 1))))
+
+        center = neighbor(0, 0)
+        ew = b.emit("tl.pointwise", neighbor(0, 1), neighbor(0, -1), f="add")
+        ns = b.emit("tl.pointwise", neighbor(1, 0), neighbor(-1, 0), f="add")
+        nsum = b.emit("tl.pointwise", ew, ns, f="add")
+        lap = b.emit("tl.pointwise", nsum, b.emit("tl.pointwise", _c(b, 4.0), center, f="mul"), f="sub")
+        return b.emit("tl.pointwise", center, b.emit("tl.pointwise", _c(b, alpha), lap, f="mul"), f="add")
+
+    b = Builder(OPS)
+    ph = b.param(0, tensor_type(("x", "y"), U.shape))
+    region = Region(params=(ph,), body=(b.emit("core.yield", body(b, b.emit("tl.stage", ph, level="shared"))),))
+    nb = Builder(OPS)
+    nh = nb.param(0, tensor_type(("x", "y"), U.shape))
+    naive = Region(params=(nh,), body=(nb.emit("core.yield", body(nb, nh)),))
+
+    def oracle(arrs):
+        u = np.asarray(arrs[0], dtype=np.float64)
+        lap = u[:-2, 1:-1] + u[2:, 1:-1] + u[1:-1, :-2] + u[1:-1, 2:] - 4 * u[1:-1, 1:-1]
+        return u[1:-1, 1:-1] + alpha * lap
+
+    return Flagship(check_tier(region), naive, [Field(U, ph.type.dims)], oracle)
+
+
+def gemm_tile(MI: int = 8, NI: int = 6, K: int = 8, KI: int = 2, seed: int = 13) -> Flagship:
+    """The GEMM flagship (zoo/tiles.py:43-91): acc carried through a fold over
+    k tiles, both operand slices staged, the contraction as
+    repeat_like / mul / reduce; the twin contracts unsplit."""
+    KO = K // KI
+    rng = np.random.default_rng(seed)
+    A = rng.standard_normal((MI, K))
+    Bm = rng.standard_normal((K, NI))
+    b = Builder(OPS)
+    pa = b.param(0, tensor_type(("mi", "k"), A.shape))
+    pb = b.param(1, tensor_type(("k", "ni"), Bm.shape))
+    at = b.emit("tl.split", pa, name="k", parts=(("ko", KO), ("ki", KI)))
+    bt = b.emit("tl.split", pb, name="k", parts=(("ko", KO), ("ki", KI)))
+    acc0 = b.emit("tl.const", value=0.0, dims=(("mi", MI), ("ni", NI)))
+    sb = Builder(OPS)
+    p_acc = sb.param(0, acc0.type)
+    p_a = sb.param(1, minus_dim(at.type, "ko"))
+    p_b = sb.param(2, minus_dim(bt.type, "ko"))
+    a_s = sb.emit("tl.stage", p_a, level="shared")
+    b_s = sb.emit("tl.stage", p_b, level="shared")
+    prod = sb.emit("tl.pointwise", sb.emit("tl.repeat_like", a_s, b_s), sb.emit("tl.repeat_like", b_s, a_s), f="mul")
+    part = sb.emit("tl.reduce", prod, dims=("ki",), f="sum")
+    step = Region(params=(p_acc, p_a, p_b), body=(sb.emit("core.yield", sb.emit("tl.pointwise", p_acc, part, f="add")),))
+    fold = b.emit("tl.fold", acc0, at, bt, regions=(step,), dim="ko", state=("acc",), element=("a", "b"),
+                  out=("final", 0))
+    region = Region(params=(pa, pb), body=(b.emit("core.yield", fold),))
+    nb = Builder(OPS)
+    na = nb.param(0, tensor_type(("mi", "k"), A.shape))
+    nbb = nb.param(1, tensor_type(("k", "ni"), Bm.shape))
+    nprod = nb.emit("tl.pointwise", nb.emit("tl.repeat_like", na, nbb), nb.emit("tl.repeat_like", nbb, na), f="mul")
+    naive = Region(params=(na, nbb), body=(nb.emit("core.yield", nb.emit("tl.reduce", nprod, dims=("k",), f="sum")),))
+    return Flagship(check_tier(region), naive, [Field(A, pa.type.dims), Field(Bm, pb.type.dims)],
+                    lambda arrs: np.asarray(arrs[0]) @ np.asarray(arrs[1]))
