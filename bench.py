@@ -284,12 +284,54 @@ def secondary(torch, K, cf, h, dev):
         out["map_chain"] = _map_chain_line(torch, K, dev, g)
     except Exception as exc:
         out["map_chain"] = {"error": str(exc)}
+    # ---------------- f4: stencil, the 5-point update over an 8192 x 8192 fp32 grid ----------------
+    try:
+        out["stencil"] = _stencil_line(torch, K, dev, g)
+    except Exception as exc:
+        out["stencil"] = {"error": str(exc)}
     # ---------------- f2: a gpt2-small forward, carved and run carve by carve ----------------
     try:
         out["carved_plan"] = _carved_plan_line(torch)
     except Exception as exc:
         out["carved_plan"] = {"error": str(exc)}
     return out
+
+
+def _stencil_line(torch, K, dev, g):
+    """The stencil template's 5-point update u + alpha * laplacian(u) over the
+    interior of an 8194 x 8194 fp32 halo, planned by plan_region (template
+    "stencil") and run as one elementwise program whose five neighbor reads
+    are offset views of u (reuse through L1 / L2)."""
+    from pdum_dsl_amd import ewprog
+    from pdum_dsl_amd.tl import fusion, zoo
+
+    MI = NI = 8192
+    s = zoo.stencil_tile(MI=MI, NI=NI, alpha=0.1, seed=3)
+    (grp,) = fusion.plan_region(s.naive).groups
+    y = s.naive.body[-1].args[0]
+    p = s.naive.params[0]
+    low = ewprog.lower(y, y.type.dims, {id(p): p}, allow_views=True)
+    u = torch.randn((MI + 2, NI + 2), generator=g, device=dev)
+    out = torch.empty((MI, NI), device=dev)
+    views = [low.operand_view(j, {"x": u.stride(0), "y": u.stride(1)}) for j in range(len(low.operands))]
+    prog = low.program(out.stride(), [st for st, _o in views])
+    ops = [u.reshape(-1)[o:] for _st, o in views]
+    K.map_chain(prog, ops, out)
+    torch.cuda.synchronize()
+    rows = [0, MI // 2, MI - 1]
+    uc = u.double().cpu().numpy()
+    want = s.oracle([uc])[rows]
+    err = float(np.abs(out[rows].double().cpu().numpy() - want).max())
+    assert err < 1e-5 * max(1.0, float(np.abs(want).max())), f"stencil parity failed: {err}"
+    ms = time_events(lambda: K.map_chain(prog, ops, out), 30)
+    nbytes = ((MI + 2) * (NI + 2) + MI * NI) * 4
+    return {
+        "config": f"u + 0.1 * (5-point laplacian) over [{MI}, {NI}] fp32 (halo [{MI + 2}, {NI + 2}]); template "
+                  f"{grp.template} ({grp.certificate.verdict}), {len(low.operands)} shifted views, "
+                  f"{len(low.insns)} instructions",
+        "ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1), "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
+        "bytes": nbytes, "max_abs_err": err,
+    }
 
 
 def _gpt2_torch(torch, W, cfg):

@@ -67,9 +67,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <int DT, int EPT, typename Eval>
 __device__ __forceinline__ void map_chain_body(const pdh_ew_program& p, const EwOperands& ops, void* out,
                                                uint32_t total) {
-  const uint32_t i0 = (static_cast<uint32_t>(blockIdx.x) * 256u + threadIdx.x) * EPT;
-  if (i0 >= total) return;
   const int ndim = p.ndim;
+  // Rows that are whole multiples of a wave's 64 EPT elements: lane l takes
+  // columns l, l + 64, ... of its wave's chunk, so every load and store
+  // instruction covers 64 consecutive elements. Otherwise a lane takes EPT
+  // consecutive columns.
+  const bool wide = EPT > 1 && p.shape[ndim - 1] % (64 * EPT) == 0;
+  const uint32_t gt = static_cast<uint32_t>(blockIdx.x) * 256u + threadIdx.x;
+  const uint32_t i0 = wide ? (gt & ~63u) * EPT + (gt & 63u) : gt * EPT;
+  const int es = wide ? 64 : 1;
+  if (i0 >= total) return;
   int c[PDH_EW_MAX_DIMS] = {0, 0, 0, 0};
   uint32_t rem = i0;
 #pragma unroll
@@ -83,12 +90,12 @@ __device__ __forceinline__ void map_chain_body(const pdh_ew_program& p, const Ew
   float acc[EPT], res[EPT];
 #pragma unroll
   for (int e = 0; e < EPT; ++e) acc[e] = 0.f;
-  Eval::template run<EPT>(p, ops, DT, c, acc, res);
+  Eval::template run<EPT>(p, ops, DT, c, acc, res, es);
   int off = 0;
 #pragma unroll
   for (int d = 0; d < PDH_EW_MAX_DIMS; ++d)
     if (d < ndim) off += c[d] * static_cast<int>(p.out_stride[d]);
-  const int step = static_cast<int>(p.out_stride[ndim - 1]);
+  const int step = es * static_cast<int>(p.out_stride[ndim - 1]);
 #pragma unroll
   for (int e = 0; e < EPT; ++e) st_dt<DT>(out, off + e * step, res[e]);
 }
@@ -112,7 +119,7 @@ __device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const
   if (col0 + EPT <= a.n) {
     const int c0[PDH_EW_MAX_DIMS] = {b, row, col0, 0};
     float res[EPT];
-    Eval::template run<EPT>(p, ops, DT, c0, acc, res);
+    Eval::template run<EPT>(p, ops, DT, c0, acc, res, 1);
 #pragma unroll
     for (int e = 0; e < EPT; ++e) st_dt<DT>(a.out, rbase + static_cast<long long>(col0 + e) * p.out_stride[2], res[e]);
     return;
@@ -123,7 +130,7 @@ __device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const
     const int c1[PDH_EW_MAX_DIMS] = {b, row, col0 + e, 0};
     const float a1[1] = {acc[e]};
     float r1[1];
-    Eval::template run<1>(p, ops, DT, c1, a1, r1);
+    Eval::template run<1>(p, ops, DT, c1, a1, r1, 1);
     st_dt<DT>(a.out, rbase + static_cast<long long>(col0 + e) * p.out_stride[2], r1[0]);
   }
 }

@@ -35,15 +35,16 @@ __device__ __forceinline__ void ew_store(void* base, long long off, float v, int
 struct InterpEval;
 
 // Runs program p for EPT elements: the element at output coordinates c0
-// and the next EPT - 1 along the last output dim (every caller's elements
-// are consecutive there). acc[e] is what PDH_EW_ACC reads; returns
-// r[out_reg] in res. Each instruction is decoded and dispatched once for
-// all EPT elements; operand offsets are 32-bit (callers keep every view
+// and EPT - 1 more along the last output dim, es apart (every caller's
+// elements lie on one row: es = 1 for consecutive columns, es = 64 when a
+// wave's lanes take consecutive columns). acc[e] is what PDH_EW_ACC reads;
+// returns r[out_reg] in res. Each instruction is decoded and dispatched once
+// for all EPT elements; operand offsets are 32-bit (callers keep every view
 // under 2^31 elements).
 template <int EPT>
 __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands& ops, int dtype,
                                        const int (&c0)[PDH_EW_MAX_DIMS], const float (&acc)[EPT],
-                                       float (&res)[EPT]) {
+                                       float (&res)[EPT], int es) {
   f32x16 r[EPT];
 #pragma unroll
   for (int e = 0; e < EPT; ++e) r[e] = f32x16{};
@@ -74,7 +75,7 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
 #pragma unroll
         for (int dd = 0; dd < PDH_EW_MAX_DIMS; ++dd)
           if (dd < ndim) off += c0[dd] * static_cast<int>(p.in_stride[ia][dd]);
-        const int step = static_cast<int>(p.in_stride[ia][last]);
+        const int step = es * static_cast<int>(p.in_stride[ia][last]);
         const void* base = ops.p[ia];
 #pragma unroll
         for (int e = 0; e < EPT; ++e) v[e] = ew_load(base, off + e * step, dtype);
@@ -93,7 +94,7 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
 #pragma unroll
         for (int dd = 0; dd < PDH_EW_MAX_DIMS; ++dd)
           if (dd == ia) c = c0[dd] + static_cast<int>(p.start[dd]);
-        const int inc = ia == last ? 1 : 0;
+        const int inc = ia == last ? es : 0;
 #pragma unroll
         for (int e = 0; e < EPT; ++e) v[e] = static_cast<float>(c + e * inc);
         break;
@@ -146,8 +147,8 @@ struct InterpEval {
   template <int EPT>
   static __device__ __forceinline__ void run(const pdh_ew_program& p, const EwOperands& ops, int dtype,
                                              const int (&c0)[PDH_EW_MAX_DIMS], const float (&acc)[EPT],
-                                             float (&res)[EPT]) {
-    ew_run<EPT>(p, ops, dtype, c0, acc, res);
+                                             float (&res)[EPT], int es) {
+    ew_run<EPT>(p, ops, dtype, c0, acc, res, es);
   }
 };
 
