@@ -120,6 +120,22 @@ __device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const
     const int c0[PDH_EW_MAX_DIMS] = {b, row, col0, 0};
     float res[EPT];
     Eval::template run<EPT>(p, ops, DT, c0, acc, res, 1);
+    if constexpr (EPT == 4) {
+      const long long o0 = rbase + col0;
+      if (p.out_stride[2] == 1 && (o0 & 3) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0) {
+        // four consecutive, aligned outputs: one 16-byte (fp32) or 8-byte (16-bit) store
+        if constexpr (DT == PDH_F32) {
+          *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + o0) = f32x4{res[0], res[1], res[2], res[3]};
+        } else {
+          uint16_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = DT == PDH_BF16 ? f32_to_bf16(res[e]) : f32_to_f16(res[e]);
+          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + o0) =
+              u32x2{h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16)};
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int e = 0; e < EPT; ++e) st_dt<DT>(a.out, rbase + static_cast<long long>(col0 + e) * p.out_stride[2], res[e]);
     return;

@@ -111,7 +111,7 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
       PDH_EW_CASE(PDH_EW_EXP, expf(a_))
       PDH_EW_CASE(PDH_EW_LOG, logf(a_))
       PDH_EW_CASE(PDH_EW_SQRT, sqrtf(a_))
-      PDH_EW_CASE(PDH_EW_TANH, tanhf(a_))
+      PDH_EW_CASE(PDH_EW_TANH, pdh_tanh(a_))
       PDH_EW_CASE(PDH_EW_SIN, sinf(a_))
       PDH_EW_CASE(PDH_EW_COS, cosf(a_))
       PDH_EW_CASE(PDH_EW_ABS, fabsf(a_))

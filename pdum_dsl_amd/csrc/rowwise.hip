@@ -36,6 +36,24 @@ __device__ __forceinline__ f32x4 ld4(const void* row, int i) {
   }
 }
 
+// The same four elements through the caches: gamma and beta are read by
+// every row, so they must stay resident (a nontemporal load would stream them
+// from HBM again for each row).
+template <int DT>
+__device__ __forceinline__ f32x4 ld4_cached(const void* row, int i) {
+  if constexpr (DT == PDH_F32) {
+    return static_cast<const f32x4*>(row)[i];
+  } else {
+    const u32x2 w = static_cast<const u32x2*>(row)[i];
+    if constexpr (DT == PDH_BF16)
+      return f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                   __uint_as_float(w.y & 0xffff0000u)};
+    else
+      return f32x4{f16_to_f32(static_cast<uint16_t>(w.x)), f16_to_f32(static_cast<uint16_t>(w.x >> 16)),
+                   f16_to_f32(static_cast<uint16_t>(w.y)), f16_to_f32(static_cast<uint16_t>(w.y >> 16))};
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ void st4(void* row, int i, f32x4 v) {
   if constexpr (DT == PDH_F32) {
@@ -147,8 +165,8 @@ __global__ __launch_bounds__(256) void layernorm_rows_v4(const void* __restrict_
     if (idx < nvec) {
       f32x4 o = v[j] * rstd;
       if (AFFINE) {
-        if (gamma) o *= ld4<DT>(gamma, idx);
-        if (beta) o += ld4<DT>(beta, idx);
+        if (gamma) o *= ld4_cached<DT>(gamma, idx);
+        if (beta) o += ld4_cached<DT>(beta, idx);
       }
       st4<DT>(yr, idx, o);
     }

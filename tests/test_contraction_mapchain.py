@@ -320,6 +320,21 @@ def test_specialized_kernels_compile_offline_for_every_element_type():
     buf = C.create_string_buffer(1 << 16)
     n = lib.pdh_ew_jit_source(C.byref(epi), 1, L.PDH_BF16, buf, len(buf))
     src = buf.value.decode()
-    assert n == len(src) and "0x1.988454p-1f" in src and "tanhf(" in src and "acc[e]" in src
+    assert n == len(src) and "0x1.988454p-1f" in src and "pdh_tanh(" in src and "acc[e]" in src
     assert len(re.findall(r"^      r\d+ = ", src, re.M)) == epi.n_insns  # one statement per instruction
     assert "contract_mfma_body<PDH_BF16, 64, pdh::GenEval>" in src and "contract_mfma_body<PDH_BF16, 32, pdh::GenEval>" in src
+
+
+def test_the_tanh_identity_the_kernels_use_is_accurate_in_fp32():
+    """dev.h's pdh_tanh: tanh|x| = 1 - 2 / (2^(2|x| log2 e) + 1), sign copied.
+    The same float32 steps in numpy (exp2 and a correctly rounded reciprocal
+    stand in for v_exp_f32 / v_rcp_f32, each within about an ulp) stay within
+    3e-7 of tanh over the whole line, are odd, and saturate to exactly 1."""
+    x = np.concatenate([np.linspace(-20, 20, 200001), np.geomspace(1e-30, 1e-3, 1000)]).astype(np.float32)
+    ax = np.abs(x)
+    e = np.exp2(ax * np.float32(2.8853900817779268))
+    t = np.float32(1) - np.float32(2) * (np.float32(1) / (e + np.float32(1)))
+    got = np.copysign(t, x)
+    assert np.abs(got.astype(np.float64) - np.tanh(x.astype(np.float64))).max() < 3e-7
+    assert np.all(got[x >= 10] == 1.0) and np.array_equal(np.copysign(t, -x), -got)
+    assert abs(2.8853900817779268 - 2 / np.log(2)) < 1e-15
