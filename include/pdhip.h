@@ -254,6 +254,17 @@ int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, const void* 
                          int64_t batch, int64_t m, int64_t n, int64_t k, const pdh_ew_program* epi,
                          const void* const* operands, void* out, int dtype, void* stream);
 
+/* The ROWSUM and PLAIN shapes of the contraction-epilogue group (fusion.py:
+ * 158-252: same-space operands multiplied and summed, or one operand summed,
+ * e.g. the backward's D = rowsum(dO * O) and a bias gradient):
+ *   out[r] = epi(sum_k summand(r, k))
+ * `summand` runs over the lattice (row dims..., k dims...) whose last nk dims
+ * are reduced; `epi` runs over the row dims (its ACC reads the fp32 sum).
+ * Both programs index one table of n_operands pointers. One wave per output
+ * element. */
+int pdh_reduce_rows(const pdh_ew_program* summand, int nk, const pdh_ew_program* epi, const void* const* operands,
+                    int n_operands, void* out, int dtype, void* stream);
+
 /* Runtime specialization of elementwise programs. pdh_map_chain and
  * pdh_contract first compile the program into straight-line code with hipRTC
  * (once per distinct program and element type, cached for the process) and

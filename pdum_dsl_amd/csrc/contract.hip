@@ -34,6 +34,12 @@ __global__ __launch_bounds__(256) void contract_f32(ContractArgs a, pdh_ew_progr
   contract_f32_body<InterpEval>(a, p, ops);
 }
 
+template <int DT>
+__global__ __launch_bounds__(256) void reduce_rows_kernel(pdh_ew_program ps, pdh_ew_program pe, EwOperands ops,
+                                                          void* out, int nk, int rows) {
+  reduce_rows_body<DT, InterpEval, InterpEval>(ps, pe, ops, out, nk, rows);
+}
+
 // -------------------------------------------------------------- validation
 
 // A program is checked in full on the host before any launch: opcodes,
@@ -242,4 +248,56 @@ extern "C" int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, c
   const ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n),
                         static_cast<int>(k), static_cast<int>(k), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r};
   return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), "pdh_contract_strided");
+}
+
+extern "C" int pdh_reduce_rows(const pdh_ew_program* summand, int nk, const pdh_ew_program* epi,
+                               const void* const* operands, int n_operands, void* out, int dtype, void* stream) {
+  int rc = check_program(summand, -1, false, "pdh_reduce_rows (summand)");
+  if (rc) return rc;
+  if ((rc = check_program(epi, -1, true, "pdh_reduce_rows (epilogue)"))) return rc;
+  PDH_REQUIRE(dtype_ok(dtype), PDH_EUNSUPPORTED, "pdh_reduce_rows: dtype %d", dtype);
+  PDH_REQUIRE(out != nullptr, PDH_EINVAL, "pdh_reduce_rows: null output");
+  PDH_REQUIRE(nk >= 1 && epi->ndim + nk == summand->ndim, PDH_EINVAL,
+              "pdh_reduce_rows: the summand's lattice must be the epilogue's plus nk = %d reduced dims", nk);
+  for (int d = 0; d < epi->ndim; ++d)
+    PDH_REQUIRE(summand->shape[d] == epi->shape[d] && summand->start[d] == epi->start[d], PDH_EINVAL,
+                "pdh_reduce_rows: summand dim %d differs from the epilogue's", d);
+  PDH_REQUIRE(n_operands >= 0 && n_operands <= PDH_EW_MAX_OPERANDS && summand->n_operands <= n_operands &&
+                  epi->n_operands <= n_operands,
+              PDH_EINVAL, "pdh_reduce_rows: %d operands for programs reading %d and %d", n_operands,
+              summand->n_operands, epi->n_operands);
+  PDH_REQUIRE(n_operands == 0 || operands != nullptr, PDH_EINVAL, "pdh_reduce_rows: null operand table");
+  int64_t rows = 1, ktot = 1;
+  for (int d = 0; d < epi->ndim; ++d) rows *= epi->shape[d];
+  for (int d = epi->ndim; d < summand->ndim; ++d) ktot *= summand->shape[d];
+  PDH_REQUIRE(rows <= INT32_MAX && ktot <= INT32_MAX, PDH_EINVAL, "pdh_reduce_rows: more than 2^31 rows or terms");
+  if ((rc = check_view(epi, epi->out_stride, "pdh_reduce_rows", "output"))) return rc;
+  EwOperands ops{};
+  for (int i = 0; i < n_operands; ++i) {
+    PDH_REQUIRE(operands[i] != nullptr, PDH_EINVAL, "pdh_reduce_rows: operand %d is null", i);
+    ops.p[i] = operands[i];
+  }
+  for (int i = 0; i < summand->n_operands; ++i)
+    if ((rc = check_view(summand, summand->in_stride[i], "pdh_reduce_rows", "summand operand"))) return rc;
+  for (int i = 0; i < epi->n_operands; ++i)
+    if ((rc = check_view(epi, epi->in_stride[i], "pdh_reduce_rows", "epilogue operand"))) return rc;
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  int r32 = static_cast<int>(rows);
+  hipFunction_t fn;
+  if (jit_get_reduce(*summand, *epi, dtype, &fn)) {
+    pdh_ew_program a = *summand, b = *epi;
+    void* args[] = {&a, &b, &ops, &out, &nk, &r32};
+    PDH_REQUIRE(hipModuleLaunchKernel(fn, grid.x, 1, 1, 256, 1, 1, 0, st, args, nullptr) == hipSuccess, PDH_ELAUNCH,
+                "pdh_reduce_rows: specialized launch failed");
+    jit_count_launch();
+    return PDH_OK;
+  }
+  if (dtype == PDH_F32)
+    reduce_rows_kernel<PDH_F32><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32);
+  else if (dtype == PDH_BF16)
+    reduce_rows_kernel<PDH_BF16><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32);
+  else
+    reduce_rows_kernel<PDH_F16><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32);
+  return check_launch("pdh_reduce_rows");
 }

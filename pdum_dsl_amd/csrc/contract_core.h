@@ -100,6 +100,74 @@ __device__ __forceinline__ void map_chain_body(const pdh_ew_program& p, const Ew
   for (int e = 0; e < EPT; ++e) st_dt<DT>(out, off + e * step, res[e]);
 }
 
+// ------------------------------------------------------------- row reduce
+
+// The ROWSUM and PLAIN contraction shapes: out[r] = epi(sum_k s(r, k)) where
+// the summand program s runs over the lattice (row dims..., k dims...) (the
+// last nk dims are reduced) and the epilogue program over the row dims with
+// ACC = the sum. One wave per output element; with one k dim a lane takes
+// k = lane, lane + 64, ... four at a time (every load covers 64 consecutive
+// k), otherwise one k at a time with its coordinates decoded. The sum is fp32.
+template <int DT, typename EvalS, typename EvalE>
+__device__ __forceinline__ void reduce_rows_body(const pdh_ew_program& ps, const pdh_ew_program& pe,
+                                                 const EwOperands& ops, void* out, int nk, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int r = static_cast<int>(blockIdx.x) * 4 + wave_id();
+  if (r >= rows) return;
+  const int nr = pe.ndim;
+  int c[PDH_EW_MAX_DIMS] = {0, 0, 0, 0};
+  int rem = r;
+  for (int d = nr - 1; d >= 0; --d) {  // the row's coordinates (a unit lattice when nr = 0)
+    const int ext = static_cast<int>(pe.shape[d]);
+    c[d] = rem % ext;
+    rem /= ext;
+  }
+  int ktot = 1;
+  for (int d = nr; d < nr + nk; ++d) ktot *= static_cast<int>(ps.shape[d]);
+  float sum = 0.f;
+  if (nk == 1) {
+    const float zero4[4] = {0.f, 0.f, 0.f, 0.f};
+    int base = 0;
+    for (; base + 256 <= ktot; base += 256) {
+      c[nr] = base + lane;
+      float res[4];
+      EvalS::template run<4>(ps, ops, DT, c, zero4, res, 64);
+      sum += (res[0] + res[1]) + (res[2] + res[3]);
+    }
+    for (int kk = base + lane; kk < ktot; kk += 64) {
+      c[nr] = kk;
+      const float z1[1] = {0.f};
+      float r1[1];
+      EvalS::template run<1>(ps, ops, DT, c, z1, r1, 1);
+      sum += r1[0];
+    }
+  } else {
+    for (int kk = lane; kk < ktot; kk += 64) {
+      int q = kk;
+      for (int d = nr + nk - 1; d >= nr; --d) {
+        const int ext = static_cast<int>(ps.shape[d]);
+        c[d] = q % ext;
+        q /= ext;
+      }
+      const float z1[1] = {0.f};
+      float r1[1];
+      EvalS::template run<1>(ps, ops, DT, c, z1, r1, 1);
+      sum += r1[0];
+    }
+  }
+  sum = wave_total(sum);
+  if (lane == 0) {
+    const float a1[1] = {sum};
+    float r1[1];
+    int co[PDH_EW_MAX_DIMS] = {c[0], c[1], c[2], c[3]};
+    for (int d = nr; d < PDH_EW_MAX_DIMS; ++d) co[d] = 0;
+    EvalE::template run<1>(pe, ops, DT, co, a1, r1, 1);
+    long long off = 0;
+    for (int d = 0; d < nr; ++d) off += static_cast<long long>(co[d]) * pe.out_stride[d];
+    st_dt<DT>(out, off, r1[0]);
+  }
+}
+
 // ------------------------------------------------------------ contraction
 
 // 16-byte slot of chunk c (0..7) of tile row r is c ^ swz_gemm(r): conflict

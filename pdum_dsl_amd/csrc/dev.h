@@ -23,6 +23,14 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Wave index as a scalar (uniform) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
+// Sum over the 64 lanes of a wave (butterfly of cross-lane moves); every lane
+// gets the total.
+__device__ __forceinline__ float wave_total(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 // ---- 16-bit element conversions (round to nearest even; NaN stays NaN) ----
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }

@@ -81,6 +81,24 @@ def _strided_view(tt, riders, rows, kd):
     return (batch, row)
 
 
+def _with_slots(prog, first: int, total: int):
+    """The program reading its operands from slots first.. of a table of
+    ``total`` (its LOADs and strides moved up by ``first``)."""
+    new = L.EwProgram()
+    new.n_insns, new.ndim, new.out_reg, new.n_operands = prog.n_insns, prog.ndim, prog.out_reg, total
+    for d in range(prog.ndim):
+        new.shape[d], new.start[d], new.out_stride[d] = prog.shape[d], prog.start[d], prog.out_stride[d]
+    for i in range(prog.n_operands):
+        for d in range(prog.ndim):
+            new.in_stride[first + i][d] = prog.in_stride[i][d]
+    for j in range(prog.n_insns):
+        src, dst = prog.insns[j], new.insns[j]
+        dst.op, dst.dst, dst.a, dst.b, dst.c, dst.imm = src.op, src.dst, src.a, src.b, src.c, src.imm
+        if src.op == L.EW["LOAD"]:
+            dst.a = src.a + first
+    return new
+
+
 def _yielding(k: Region, node) -> Region:
     """The region over k's params that yields ``node``."""
     return Region(params=k.params, body=(Builder(OPS).emit("core.yield", node),))
@@ -320,7 +338,7 @@ class PlanExecutor:
         if m is None:
             raise Untranslatable("contraction carve does not match the contraction row")
         if m["shape"] != "gemm":
-            raise Untranslatable(f"contraction-epilogue: only the GEMM shape runs on the device ({m['shape']})")
+            return self._reduce(k, m, yroot)
         red = m["reduce"]
         kd = (red.attr("dims"),) if isinstance(red.attr("dims"), str) else tuple(red.attr("dims"))
         ca, cb = m["a"], m["b"]
@@ -443,6 +461,55 @@ class PlanExecutor:
 
         src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
         return run, src
+
+    def _reduce(self, k, m, yroot=None):
+        """The ROWSUM / PLAIN contraction shapes: the summand (the product of
+        same-space operands, or the one operand chain) summed over the
+        contracted dims by pdh_reduce_rows, the epilogue on the sum."""
+        red = m["reduce"]
+        kd = (red.attr("dims"),) if isinstance(red.attr("dims"), str) else tuple(red.attr("dims"))
+        row_dims = tuple(red.type.dims) or (Dim("_unit_r", 0, 1),)
+        kdims = tuple(m["a"].type.dim(nm) for nm in kd)
+        lat_s = row_dims + kdims
+        if len(lat_s) > L.EW_MAX_DIMS:
+            raise Untranslatable(f"a reduction over {len(lat_s)} lattice dims (max {L.EW_MAX_DIMS})")
+        leaves = {id(p): p for p in k.params}
+        y = k.body[-1].args[0] if yroot is None else yroot
+        total = math.prod(d.size for d in kdims)
+        try:
+            ls = ewprog.lower(red.args[0], lat_s, leaves, allow_views=True)
+            le = ewprog.lower(y, row_dims, leaves, acc=red, acc_scale=(1.0 / total) if m["f"] == "mean" else None,
+                              allow_views=True)
+        except ewprog.Unlowerable as exc:
+            raise Untranslatable(f"row reduction: {exc}") from None
+        slots, views = [], []
+        for low in (ls, le):
+            for j, base in enumerate(low.bases):
+                st, off = low.operand_view(j, _strides_by_name(base.type.names, base.type.shape))
+                if off < 0:
+                    raise Untranslatable("a shifted read starts before its tensor")
+                slots.append(self._index(k, base))
+                views.append((st, off))
+        n_s = len(ls.operands)
+        if len(slots) > L.EW_MAX_OPERANDS:
+            raise Untranslatable(f"summand and epilogue read {len(slots)} operands (max {L.EW_MAX_OPERANDS})")
+        ps = ls.program([0] * len(lat_s), [st for st, _o in views[:n_s]])
+        pe = le.program(_over(y.type.names, y.type.shape, row_dims), [st for st, _o in views[n_s:]])
+        ps, pe = _with_slots(ps, 0, len(slots)), _with_slots(pe, n_s, len(slots))
+        offs = [o for _st, o in views]
+        shape = y.type.shape
+        nk = len(kdims)
+
+        def run(vals):
+            torch = _torch()
+            from . import kernels as K
+
+            out = torch.empty(shape, device="cuda", dtype=getattr(torch, _TORCH_DT[self.dtype]))
+            K.reduce_rows(ps, nk, pe, [vals[i].reshape(-1)[o:] for i, o in zip(slots, offs)], out)
+            return out
+
+        return run, f"reduce_rows {m['shape']} rows={math.prod(d.size for d in row_dims)} k={total} " \
+                    f"summand={len(ls.insns)} epilogue={len(le.insns)}"
 
     def _softmax(self, k):
         y = k.body[-1].args[0]

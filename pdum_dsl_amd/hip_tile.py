@@ -314,6 +314,8 @@ def compile_tile_hip(region: Region, launch: tuple = (), prune: tuple = (), *, d
     if lb is not None:
         return _layernorm_runner(region, lb, grid)
     cb = recognize_contraction(region)
+    if cb is not None and cb["shape"] != "gemm":
+        return _reduce_runner(region, cb, grid, dtype)
     if cb is not None:
         return _contraction_runner(region, cb, grid, dtype)
     if recognize_map_chain(region):
@@ -592,15 +594,24 @@ def recognize_contraction(region: Region):
     if part.op != "tl.reduce" or part.attr("f") != "sum":
         return None
     rdims = (part.attr("dims"),) if isinstance(part.attr("dims"), str) else tuple(part.attr("dims"))
-    if len(srcs) != 2:
-        raise Untranslatable("contraction-epilogue: only the GEMM shape runs on HIP (plain sum refused)")
+    contracted = (k,) + tuple(d for d in rdims if d != "ki")
     prod = part.args[0]
+    if len(srcs) == 1:  # PLAIN: the one operand chain summed
+        if prod.op != "tl.stage" or prod.args[0] is not step.params[1]:
+            return None
+        return {"fold": f, "k": k, "shape": "plain", "a": srcs[0].args[0], "b": None, "contracted": contracted}
+    if len(srcs) != 2:
+        return None
+    if prod.op == "tl.pointwise" and prod.attr("f") == "mul" and all(x.op == "tl.stage" for x in prod.args) and \
+            prod.args[0].args[0] is step.params[1] and prod.args[1].args[0] is step.params[2]:
+        return {"fold": f, "k": k, "shape": "rowsum", "a": srcs[0].args[0], "b": srcs[1].args[0],
+                "contracted": contracted}
     a_s = b_s = None
     if prod.op == "tl.pointwise" and prod.attr("f") == "mul" and all(x.op == "tl.repeat_like" for x in prod.args):
         a_s, b_s = prod.args[0].args[0], prod.args[1].args[0]
     if a_s is None or a_s.op != "tl.stage" or b_s.op != "tl.stage" or a_s.args[0] is not step.params[1] \
             or b_s.args[0] is not step.params[2]:
-        raise Untranslatable("contraction-epilogue: only the GEMM shape runs on HIP (rowsum refused)")
+        return None
     if rdims != ("ki",):
         raise Untranslatable(f"contraction-epilogue: one contracted dim on HIP (the step reduces {rdims})")
     ca, cb = srcs[0].args[0], srcs[1].args[0]
@@ -613,7 +624,59 @@ def recognize_contraction(region: Region):
         raise Untranslatable("contraction-epilogue: at most one batch, one m and one n dim on HIP")
     return {"fold": f, "k": k, "a": ca, "b": cb, "rider": riders[0] if riders else None,
             "m": mdims[0] if mdims else None, "n": ndims[0] if ndims else None,
-            "K": ca.type.dim(k).size}
+            "K": ca.type.dim(k).size, "shape": "gemm"}
+
+
+def _reduce_runner(region, cb, grid, dtype):
+    """The ROWSUM / PLAIN shapes: the summand (the same-space product, or the
+    one operand chain) over (output dims..., contracted dims...) summed by
+    pdh_reduce_rows, the epilogue on the sum."""
+    from . import ewprog
+    from . import kernels as K
+    from .tl.dialect import OPS
+    from .tl.ir import Builder, Dim
+
+    y = region.body[-1].args[0]
+    if y.op == "core.tuple":
+        raise Untranslatable("contraction-epilogue with several yields")
+    fold, ca, cbn = cb["fold"], cb["a"], cb["b"]
+    summand = ca if cb["shape"] == "plain" else Builder(OPS).emit("tl.pointwise", ca, cbn, f="mul")
+    rows = tuple(fold.type.dims) or (Dim("_unit_r", 0, 1),)
+    kdims = tuple(d for d in ca.type.dims if d.name in cb["contracted"])
+    lat = rows + kdims
+    if len(lat) > 4:
+        raise Untranslatable(f"a reduction over {len(lat)} lattice dims (max 4)")
+    leaves = {id(p): p for p in region.params}
+    try:
+        ls = ewprog.lower(summand, lat, leaves)
+        le = ewprog.lower(y, rows, leaves, acc=fold)
+    except ewprog.Unlowerable as exc:
+        raise Untranslatable(f"row reduction: {exc}") from None
+    from .executor import _with_slots
+
+    idx = [_index(region, b) for b in ls.bases + le.bases]
+    nodes = ls.operands + le.operands
+    n_s = len(ls.operands)
+
+    def run(values):
+        torch = _torch()
+        ops = [_upload(torch, values[i], nd.type.names, nd.type.names, dtype) for i, nd in zip(idx, nodes)]
+        st = [ewprog.strides_over(t.stride(), nd.type.names, lat) for t, nd in zip(ops[:n_s], nodes[:n_s])]
+        se = [ewprog.strides_over(t.stride(), nd.type.names, rows) for t, nd in zip(ops[n_s:], nodes[n_s:])]
+        out = torch.empty(tuple(d.size for d in rows), device="cuda", dtype=getattr(torch, _TORCH_DT[dtype]))
+        ps = _with_slots(ls.program([0] * len(lat), st), 0, len(ops))
+        pe = _with_slots(le.program(out.stride(), se), n_s, len(ops))
+        K.reduce_rows(ps, len(kdims), pe, ops, out)
+        torch.cuda.synchronize()
+        res = out.float().cpu().numpy()
+        if not y.type.dims:
+            return res.reshape(())
+        names = [d.name for d in rows]
+        return np.transpose(res, [names.index(nm) for nm in y.type.names])
+
+    src = (f"hip:reduce_rows shape={cb['shape']} rows={math.prod(d.size for d in rows)} "
+           f"k={math.prod(d.size for d in kdims)} summand_insns={len(ls.insns)} epilogue_insns={len(le.insns)} stores=1")
+    return _finish(run, src, grid, "contraction-epilogue")
 
 
 def _contraction_runner(region, cb, grid, dtype):

@@ -382,6 +382,30 @@ def contract_strided(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, s
     return out
 
 
+def reduce_rows(summand: _lib.EwProgram, nk: int, epi: _lib.EwProgram, operands: list,
+                out: torch.Tensor) -> torch.Tensor:
+    """out[r] = epi(sum over the last nk summand dims of summand(r, k)): the
+    rowsum / plain contraction shapes. Both programs read ``operands``."""
+    _require_cuda(out, *operands)
+    if out.dtype not in _DT:
+        raise ValueError(f"element type {out.dtype} (f32, bf16, f16)")
+    if summand.ndim != epi.ndim + nk or nk < 1:
+        raise ValueError("the summand's lattice is the epilogue's plus nk reduced dims")
+    for prog, nd in ((summand, summand.ndim), (epi, epi.ndim)):
+        for i in range(prog.n_operands):
+            t = operands[i]
+            if t.dtype != out.dtype:
+                raise ValueError(f"operand {i} is {t.dtype}, the output {out.dtype}")
+            if _max_offset(prog, prog.in_stride[i], nd) >= t.numel():
+                raise ValueError(f"operand {i}: a program's view reaches past the tensor")
+    if _max_offset(epi, epi.out_stride, epi.ndim) >= out.numel():
+        raise ValueError("the epilogue's output view reaches past the output tensor")
+    table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
+    _lib.call("pdh_reduce_rows", C.byref(summand), int(nk), C.byref(epi), table, len(operands), _ptr(out),
+              _DT[out.dtype], C.c_void_p(_stream()))
+    return out
+
+
 def pick_decode_splits(groups: int, s: int, cus: int | None = None) -> int:
     """Splits so the (batch x kv-head x split) grid covers the chip ~8 deep,
     with at least 256 keys per split."""
