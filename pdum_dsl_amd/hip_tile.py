@@ -304,15 +304,11 @@ def compile_tile_hip(region: Region, launch: tuple = (), prune: tuple = (), *, d
     if fj is not None:
         return _flash_joint_runner(region, fj, grid, dtype)
     sb = recognize_softmax(region)
-    if sb is not None and dtype != "f32":
-        raise Untranslatable(f"row templates run fp32 only (asked {dtype})")
     if sb is not None:
-        return _softmax_runner(region, sb, grid)
+        return _softmax_runner(region, sb, grid, dtype)
     lb = recognize_layernorm(region)
-    if lb is not None and dtype != "f32":
-        raise Untranslatable(f"row templates run fp32 only (asked {dtype})")
     if lb is not None:
-        return _layernorm_runner(region, lb, grid)
+        return _layernorm_runner(region, lb, grid, dtype)
     cb = recognize_contraction(region)
     if cb is not None and cb["shape"] != "gemm":
         return _reduce_runner(region, cb, grid, dtype)
@@ -390,7 +386,7 @@ def _from_rows(y: np.ndarray, shape, perm):
     return np.transpose(y.reshape(shape), inv)
 
 
-def _softmax_runner(region, sb, grid):
+def _softmax_runner(region, sb, grid, dtype="f32"):
     from . import kernels as K
 
     names = sb["x"].type.names
@@ -400,17 +396,18 @@ def _softmax_runner(region, sb, grid):
     def run(values):
         torch = _torch()
         rows, shape, perm = _to_rows(values[0], names, s)
-        y = K.row_softmax(torch.as_tensor(rows, device="cuda"))
+        x = torch.as_tensor(rows, device="cuda").to(getattr(torch, _TORCH_DT[dtype]))
+        y = K.row_softmax(x)
         torch.cuda.synchronize()
-        full = _from_rows(y.cpu().numpy(), shape, perm)  # param's dim order
+        full = _from_rows(y.float().cpu().numpy(), shape, perm)  # param's dim order
         return np.transpose(full, [names.index(n) for n in out_names])
 
     n_rows = math.prod(d.size for d in sb["x"].type.dims if d.name != s)
-    src = f"hip:row_softmax rows={n_rows} cols={sb['x'].type.dim(s).size} reduce={s} sweeps=1 stores=1"
+    src = f"hip:row_softmax rows={n_rows} cols={sb['x'].type.dim(s).size} reduce={s} dtype={dtype} sweeps=1 stores=1"
     return _finish(run, src, grid, "row-normalization")
 
 
-def _layernorm_runner(region, lb, grid):
+def _layernorm_runner(region, lb, grid, dtype="f32"):
     from . import kernels as K
 
     names = lb["x"].type.names
@@ -422,18 +419,19 @@ def _layernorm_runner(region, lb, grid):
 
     def run(values):
         torch = _torch()
+        tdt = getattr(torch, _TORCH_DT[dtype])
         rows, shape, perm = _to_rows(values[ix], names, feat)
-        g = None if ig is None else torch.as_tensor(np.asarray(values[ig], dtype=np.float32), device="cuda")
-        b = None if ib is None else torch.as_tensor(np.asarray(values[ib], dtype=np.float32), device="cuda")
-        y = K.layernorm(torch.as_tensor(rows, device="cuda"), g, b, eps=lb["eps"])
+        g = None if ig is None else torch.as_tensor(np.asarray(values[ig], dtype=np.float32), device="cuda").to(tdt)
+        b = None if ib is None else torch.as_tensor(np.asarray(values[ib], dtype=np.float32), device="cuda").to(tdt)
+        y = K.layernorm(torch.as_tensor(rows, device="cuda").to(tdt), g, b, eps=lb["eps"])
         torch.cuda.synchronize()
-        full = _from_rows(y.cpu().numpy(), shape, perm)
+        full = _from_rows(y.float().cpu().numpy(), shape, perm)
         return np.transpose(full, [names.index(n) for n in out_names])
 
     n_rows = math.prod(d.size for d in lb["x"].type.dims if d.name != feat)
     src = (
         f"hip:layernorm rows={n_rows} cols={lb['x'].type.dim(feat).size} mean/N=/ {lb['x'].type.dim(feat).size} "
-        f"eps={lb['eps']:g} affine={'gamma' if ig is not None else ''}{'+beta' if ib is not None else ''} "
+        f"eps={lb['eps']:g} affine={'gamma' if ig is not None else ''}{'+beta' if ib is not None else ''} dtype={dtype} "
         "sweeps=1 stores=1"
     )
     return _finish(run, src, grid, "row-statistics")

@@ -165,3 +165,23 @@ def test_the_rowstat_layernorm_runs_on_hip(affine):
     run = compile_tile_hip(g.kernel)
     assert "/ 768" in run.source  # the mean's divide-by-N, N static
     np.testing.assert_allclose(run(ln.numpy_inputs()), _oracle_out(ln), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_the_row_templates_run_on_16_bit_storage(dtype):
+    """The row groups at the seat's 16-bit columns (fp32 arithmetic, storage
+    rounded): within 2e-2 of the oracle on the rounded inputs."""
+    import torch
+
+    from pdum_dsl_amd.hip_tile import compile_tile_hip
+    from pdum_dsl_amd.tl import fusion, zoo
+
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    for subj in (zoo.row_softmax(33, 1024), zoo.layernorm(rows=9, feat=768, affine=True)):
+        (g,) = fusion.plan_region(subj.region).groups
+        run = compile_tile_hip(g.kernel, dtype=dtype)
+        assert f"dtype={dtype}" in run.source
+        vals = [torch.as_tensor(v).to(tdt).double().numpy() for v in subj.numpy_inputs()]
+        got = run(vals)
+        want = subj.oracle(vals)
+        assert np.abs(got - want).max() <= 2e-2 * max(1.0, np.abs(want).max())
