@@ -16,6 +16,7 @@ PDH_EW_MAX_OPERANDS or more instructions than PDH_EW_MAX_INSNS refuses.
 
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 from . import _lib as L
@@ -245,6 +246,72 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, al
                    tuple(view_of(x) for x in slots))
 
 
+def with_slots(prog, first: int, total: int):
+    """The program reading its operands from slots first.. of a table of
+    ``total`` (its LOADs and strides moved up by ``first``)."""
+    new = L.EwProgram()
+    new.n_insns, new.ndim, new.out_reg, new.n_operands = prog.n_insns, prog.ndim, prog.out_reg, total
+    for d in range(prog.ndim):
+        new.shape[d], new.start[d], new.out_stride[d] = prog.shape[d], prog.start[d], prog.out_stride[d]
+    for i in range(prog.n_operands):
+        for d in range(prog.ndim):
+            new.in_stride[first + i][d] = prog.in_stride[i][d]
+    for j in range(prog.n_insns):
+        src, dst = prog.insns[j], new.insns[j]
+        dst.op, dst.dst, dst.a, dst.b, dst.c, dst.imm = src.op, src.dst, src.a, src.b, src.c, src.imm
+        if src.op == L.EW["LOAD"]:
+            dst.a = src.a + first
+    return new
+
+
+def merge_dims(prog, groups):
+    """Merge groups of consecutive lattice dims of a program into one dim each
+    (e.g. (unit, t, nh, hk) -> (unit, t, nh*hk)). A group merges when every
+    view's strides over it compose densely (outer = inner * size) or are all
+    zero; an IOTA over a dim in a group of several refuses (Unlowerable)."""
+    n_old = prog.ndim
+    sizes = [int(prog.shape[d]) for d in range(n_old)]
+    for j in range(prog.n_insns):
+        ins = prog.insns[j]
+        if ins.op == L.EW["IOTA"]:
+            g = next(gi for gi, grp in enumerate(groups) if ins.a in grp)
+            if len(groups[g]) > 1:
+                raise Unlowerable("an iota over a flattened dim has no merged form")
+    if any(int(prog.start[d]) != 0 for grp in groups if len(grp) > 1 for d in grp):
+        raise Unlowerable("a flattened dim must start at 0")
+
+    def merge(strides):
+        out = []
+        for grp in groups:
+            st = [int(strides[d]) for d in grp]
+            if all(s == 0 for s in st):
+                out.append(0)
+                continue
+            for a, b in zip(grp[:-1], grp[1:]):
+                if int(strides[a]) != int(strides[b]) * sizes[b]:
+                    raise Unlowerable("a view's strides do not compose across a flattened dim")
+            out.append(st[-1])
+        return out
+
+    out_st = merge(prog.out_stride)
+    in_st = [merge(prog.in_stride[i]) for i in range(prog.n_operands)]
+    iota_dim = {d: gi for gi, grp in enumerate(groups) for d in grp}
+    new = L.EwProgram()
+    new.n_insns, new.n_operands, new.ndim, new.out_reg = prog.n_insns, prog.n_operands, len(groups), prog.out_reg
+    for gi, grp in enumerate(groups):
+        new.shape[gi] = math.prod(sizes[d] for d in grp)
+        new.start[gi] = int(prog.start[grp[0]]) if len(grp) == 1 else 0
+        new.out_stride[gi] = out_st[gi]
+        for i in range(prog.n_operands):
+            new.in_stride[i][gi] = in_st[i][gi]
+    for j in range(prog.n_insns):
+        src, dst = prog.insns[j], new.insns[j]
+        dst.op, dst.dst, dst.a, dst.b, dst.c, dst.imm = src.op, src.dst, src.a, src.b, src.c, src.imm
+        if src.op == L.EW["IOTA"]:
+            dst.a = iota_dim[src.a]
+    return new
+
+
 def strides_over(arr_strides, arr_names, dims) -> list:
     """Element strides of an array (dims ``arr_names``) over the lattice
     ``dims``: the array's stride where it has the dim, 0 (broadcast) where not."""
@@ -254,4 +321,4 @@ def strides_over(arr_strides, arr_names, dims) -> list:
     return out
 
 
-__all__ = ["Lowered", "Unlowerable", "lower", "strides_over"]
+__all__ = ["Lowered", "Unlowerable", "lower", "merge_dims", "strides_over", "with_slots"]

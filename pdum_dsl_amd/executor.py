@@ -7,6 +7,10 @@ test_partition.py:15-37, 124-193: a worklist, free views resolved at the
 edges, red groups through the evaluator). Here the same plan runs on HIP
 kernels, one step per carve:
 
+  flash                 pdh_flash_fwd, the closed mask bound as a band, the
+                        (m, den) artifacts when the carve yields them
+  flash-joint           pdh_flash_fwd with artifacts + pdh_flash_bwd seeded by
+                        the joint's last param: (out, *grads)
   contraction-epilogue  operand packs (pdh_map_chain: prologue chains,
                         transposes, zero padding of k) + pdh_contract with the
                         epilogue program; several m, n or k dims flatten into
@@ -15,7 +19,8 @@ kernels, one step per carve:
                         computed (a dissolved score contraction, or a map
                         chain), then pdh_row_softmax_dt over the reduced dim
   row-statistics        pdh_layernorm_dt with the affine epilogue
-  map-chain             pdh_map_chain
+  map-chain, stencil    pdh_map_chain (shifted reads as offset views)
+  ROWSUM / PLAIN        pdh_reduce_rows
   red, tl.take          pdh_take_rows for the gather, the rest of the carve
                         as a map chain; any other red carve refuses
 
@@ -81,24 +86,6 @@ def _strided_view(tt, riders, rows, kd):
     return (batch, row)
 
 
-def _with_slots(prog, first: int, total: int):
-    """The program reading its operands from slots first.. of a table of
-    ``total`` (its LOADs and strides moved up by ``first``)."""
-    new = L.EwProgram()
-    new.n_insns, new.ndim, new.out_reg, new.n_operands = prog.n_insns, prog.ndim, prog.out_reg, total
-    for d in range(prog.ndim):
-        new.shape[d], new.start[d], new.out_stride[d] = prog.shape[d], prog.start[d], prog.out_stride[d]
-    for i in range(prog.n_operands):
-        for d in range(prog.ndim):
-            new.in_stride[first + i][d] = prog.in_stride[i][d]
-    for j in range(prog.n_insns):
-        src, dst = prog.insns[j], new.insns[j]
-        dst.op, dst.dst, dst.a, dst.b, dst.c, dst.imm = src.op, src.dst, src.a, src.b, src.c, src.imm
-        if src.op == L.EW["LOAD"]:
-            dst.a = src.a + first
-    return new
-
-
 def _yielding(k: Region, node) -> Region:
     """The region over k's params that yields ``node``."""
     return Region(params=k.params, body=(Builder(OPS).emit("core.yield", node),))
@@ -115,54 +102,6 @@ def _over(view_names, view_shape, lattice) -> list:
     (0 where the value lacks a dim: a broadcast)."""
     st = _strides_by_name(view_names, view_shape)
     return [st.get(d.name, 0) for d in lattice]
-
-
-def _merge_program(prog, groups):
-    """Merge groups of consecutive lattice dims of a lowered program into one
-    dim each (e.g. (unit, t, nh, hk) -> (unit, t, nh*hk)). A group merges when
-    every view's strides over it compose densely (outer = inner * size) or
-    are all zero; an IOTA over a dim in a group of several refuses."""
-    n_old = prog.ndim
-    sizes = [int(prog.shape[d]) for d in range(n_old)]
-    for j in range(prog.n_insns):
-        ins = prog.insns[j]
-        if ins.op == L.EW["IOTA"]:
-            g = next(gi for gi, grp in enumerate(groups) if ins.a in grp)
-            if len(groups[g]) > 1:
-                raise Untranslatable("an iota over a flattened dim has no merged form")
-    if any(int(prog.start[d]) != 0 for grp in groups if len(grp) > 1 for d in grp):
-        raise Untranslatable("a flattened dim must start at 0")
-
-    def merge(strides):
-        out = []
-        for grp in groups:
-            st = [int(strides[d]) for d in grp]
-            if all(s == 0 for s in st):
-                out.append(0)
-                continue
-            for a, b in zip(grp[:-1], grp[1:]):
-                if int(strides[a]) != int(strides[b]) * sizes[b]:
-                    raise Untranslatable("a view's strides do not compose across a flattened dim")
-            out.append(st[-1])
-        return out
-
-    out_st = merge(prog.out_stride)
-    in_st = [merge(prog.in_stride[i]) for i in range(prog.n_operands)]
-    iota_dim = {d: gi for gi, grp in enumerate(groups) for d in grp}
-    new = L.EwProgram()
-    new.n_insns, new.n_operands, new.ndim, new.out_reg = prog.n_insns, prog.n_operands, len(groups), prog.out_reg
-    for gi, grp in enumerate(groups):
-        new.shape[gi] = math.prod(sizes[d] for d in grp)
-        new.start[gi] = int(prog.start[grp[0]]) if len(grp) == 1 else 0
-        new.out_stride[gi] = out_st[gi]
-        for i in range(prog.n_operands):
-            new.in_stride[i][gi] = in_st[i][gi]
-    for j in range(prog.n_insns):
-        src, dst = prog.insns[j], new.insns[j]
-        dst.op, dst.dst, dst.a, dst.b, dst.c, dst.imm = src.op, src.dst, src.a, src.b, src.c, src.imm
-        if src.op == L.EW["IOTA"]:
-            dst.a = iota_dim[src.a]
-    return new
 
 
 @dataclass
@@ -186,12 +125,12 @@ class _Pack:
 @dataclass
 class Step:
     """One launched carve: ``ins`` are value ids (positional per kernel param),
-    ``out`` the value id it defines."""
+    ``outs`` the value ids it defines (its root, then artifacts or the other
+    outputs of a joint), in the order ``run`` returns them."""
 
     kind: str
     ins: tuple
-    out: int
-    out_shape: tuple
+    outs: tuple
     run: object = field(repr=False)
     source: str = ""
 
@@ -204,7 +143,6 @@ class PlanExecutor:
         if dtype not in _TORCH_DT:
             raise ValueError(f"dtype {dtype!r}: f32, bf16 or f16")
         self.region, self.dtype = region, dtype
-        self.dt_code = {"f32": L.PDH_F32, "bf16": L.PDH_BF16, "f16": L.PDH_F16}[dtype]
         self.params = region.params
         self.nested: list = []
         self._bad: list = []
@@ -221,22 +159,25 @@ class PlanExecutor:
             for c in pending:
                 ins = [self._resolve(b, have) for b in c.bounds]
                 if all(i is not None for i in ins):
-                    self.steps.append(self._step(c, tuple(ins)))
-                    have.add(id(c.root))
+                    st = self._step(c, tuple(ins))
+                    self.steps.append(st)
+                    have.update(st.outs)
                     pending.remove(c)
                     break
             else:
                 raise Untranslatable("plan stalled: a carve's boundary is never produced")
         y = region.body[-1].args[0]
-        self.output = self._resolve(y, have)
-        if self.output is None:
-            raise Untranslatable("the model's output is not produced by any carve")
-        self.out_names = y.type.names
+        ys = y.args if y.op == "core.tuple" else (y,)
+        self.outputs = tuple(self._resolve(x, have) for x in ys)
+        if any(o is None for o in self.outputs):
+            raise Untranslatable("an output of the model is not produced by any carve")
+        self.single = y.op != "core.tuple"
         last: dict = {}
         for k, st in enumerate(self.steps):
             for i in st.ins:
                 last[i] = k
-        self.release = [[i for i, k in last.items() if k == s and i != self.output] for s in range(len(self.steps))]
+        keep = set(self.outputs)
+        self.release = [[i for i, k in last.items() if k == s and i not in keep] for s in range(len(self.steps))]
         self.bound: dict | None = None
 
     # ------------------------------------------------------------ building
@@ -256,7 +197,14 @@ class PlanExecutor:
     def _step(self, carve, ins):
         tmpl = carve.group.template
         k = carve.kernel
-        if tmpl == "contraction-epilogue":
+        outs = (id(carve.root),)
+        if tmpl == "flash":
+            run, src = self._flash(k)
+            outs = outs + tuple(id(a) for a in carve.artifacts)
+        elif tmpl == "flash-joint":
+            run, src = self._flash_joint(k)
+            outs = tuple(id(x) for x in k.body[-1].args[0].args)
+        elif tmpl == "contraction-epilogue":
             run, src = self._contraction(k)
         elif tmpl == "row-normalization":
             run, src = self._softmax(k)
@@ -268,8 +216,89 @@ class PlanExecutor:
             run, src = self._take(k)
         else:
             raise Untranslatable(f"carve {tmpl} ({carve.group.reason or carve.root_op}) has no device step")
+        return Step(tmpl, ins, outs, run, src)
+
+    def _flash(self, k):
+        """A flash carve (fusion.py:480-539 over the carve's params): the
+        forward kernel with the closed mask bound as a band, the (m, den)
+        artifacts when the carve yields them."""
+        from . import kernels as K
+        from .hip_tile import mask_to_band
+        from .tl.fusion import match_flash
+
+        fm = match_flash(k)
+        if fm is None:
+            raise Untranslatable("flash carve that the flash matcher does not bind")
+        t, s_, e, o = fm["t"], fm["s"], fm["e"], fm["o"]
+        q_, k_, v_ = fm["q"], fm["k"], fm["v"]
+        T, S, E, OD = q_.type.dim(t).size, fm["extent"], q_.type.dim(e).size, v_.type.dim(o).size
+        if self.dtype != "f32" and not (E == OD and E in (64, 128)):
+            raise Untranslatable(f"{self.dtype} flash needs e == od in {{64, 128}} (got {E}, {OD})")
+        band = mask_to_band(fm["mask"], t, s_, T, S)
+        kband = None if band[0] == "none" else K.Band(band[1], band[2])
+        iq, ik, iv = (self._index(k, x) for x in (q_, k_, v_))
         y = k.body[-1].args[0]
-        return Step(tmpl, ins, id(carve.root), y.type.shape, run, src)
+        out_names = (y.args[0] if y.op == "core.tuple" else y).type.names
+        arts, fill = fm["artifacts"], fm["fill"]
+
+        def mat(x, names, want, rows, cols):  # a dense (rows, cols) view in the kernel's order
+            return (x if names == want else x.t()).contiguous().view(1, 1, rows, cols)
+
+        def run(vals):
+            res = K.flash_fwd(mat(vals[iq], q_.type.names, (t, e), T, E), mat(vals[ik], k_.type.names, (s_, e), S, E),
+                              mat(vals[iv], v_.type.names, (s_, o), S, OD), scale=1.0, band=kband, fill=fill,
+                              want_lse=False, want_artifacts=arts)
+            out = res.o.view(T, OD)
+            out = out if out_names == (t, o) else out.t().contiguous()
+            return (out, res.m.view(T), res.den.view(T)) if arts else (out,)
+
+        return run, f"flash_fwd t={T} s={S} e={E} od={OD} band={band} artifacts={arts}"
+
+    def _flash_joint(self, k):
+        """The flash joint claimed whole: the forward with its artifacts and
+        the fused backward seeded by the joint's last param; returns (out,
+        *grads) in the joint's yield order."""
+        from . import kernels as K
+        from .hip_tile import mask_to_band
+        from .tl.partition import match_flash_joint
+
+        fj = match_flash_joint(k)
+        if fj is None:
+            raise Untranslatable("flash-joint carve that the joint matcher does not bind")
+        q_, k_, v_ = fj["q"], fj["k"], fj["v"]
+        t, s_, e, o = fj["t"], fj["s"], fj["e"], fj["o"]
+        T, S, E, OD = q_.type.dim(t).size, k_.type.dim(s_).size, q_.type.dim(e).size, v_.type.dim(o).size
+        if self.dtype != "f32" and not (E == OD and E in (64, 128)):
+            raise Untranslatable(f"{self.dtype} flash joint needs e == od in {{64, 128}} (got {E}, {OD})")
+        band = mask_to_band(fj["mask"], t, s_, T, S)
+        kband = None if band[0] == "none" else K.Band(band[1], band[2])
+        iq, ik, iv, iseed = (self._index(k, x) for x in (q_, k_, v_, k.params[-1]))
+        ys = k.body[-1].args[0].args
+        seed_names = k.params[-1].type.names
+
+        def mat(x, names, want, rows, cols):
+            return (x if names == want else x.t()).contiguous().view(1, 1, rows, cols)
+
+        def back(x, order, names, rows, cols):  # the kernel's (rows, cols) result in the output's dim order
+            x = x.view(rows, cols)
+            return x if tuple(names) == order else x.t().contiguous()
+
+        def run(vals):
+            q = mat(vals[iq], q_.type.names, (t, e), T, E)
+            kk = mat(vals[ik], k_.type.names, (s_, e), S, E)
+            v = mat(vals[iv], v_.type.names, (s_, o), S, OD)
+            do = mat(vals[iseed], seed_names, (t, o), T, OD)
+            res = K.flash_fwd(q, kk, v, scale=1.0, band=kband, fill=fj["fill"], want_artifacts=True)
+            dq, dk, dv = K.flash_bwd(q, kk, v, res.o, do, res.lse, m=res.m, den=res.den, scale=1.0, band=kband,
+                                     fill=fj["fill"])
+            grads = {"q": (dq, (t, e), T, E), "k": (dk, (s_, e), S, E), "v": (dv, (s_, o), S, OD)}
+            outs = [back(res.o, (t, o), ys[0].type.names, T, OD)]
+            for nm, g in zip(fj["wrt"], ys[1:]):
+                x, order, r, c = grads[nm]
+                outs.append(back(x, order, g.type.names, r, c))
+            return tuple(outs)
+
+        return run, f"flash_fwd + flash_bwd t={T} s={S} e={E} od={OD} band={band} wrt={','.join(fj['wrt'])}"
 
     def _index(self, region, node):
         return next(i for i, p in enumerate(region.params) if p is node)
@@ -416,7 +445,10 @@ class PlanExecutor:
         out_st = _over(y.type.names, y.type.shape, lat)
         prog = epi.program(out_st, [_over(op.type.names, op.type.shape, lat) for op in epi.operands])
         groups = [[0], list(range(1, 1 + len(mdims))), list(range(1 + len(mdims), len(lat)))]
-        prog = _merge_program(prog, groups)
+        try:
+            prog = ewprog.merge_dims(prog, groups)
+        except ewprog.Unlowerable as exc:
+            raise Untranslatable(f"contraction epilogue: {exc}") from None
         eslots = tuple(self._index(k, b) for b in epi.bases)
         shape = y.type.shape
         tdt = _TORCH_DT[self.dtype]
@@ -495,7 +527,7 @@ class PlanExecutor:
             raise Untranslatable(f"summand and epilogue read {len(slots)} operands (max {L.EW_MAX_OPERANDS})")
         ps = ls.program([0] * len(lat_s), [st for st, _o in views[:n_s]])
         pe = le.program(_over(y.type.names, y.type.shape, row_dims), [st for st, _o in views[n_s:]])
-        ps, pe = _with_slots(ps, 0, len(slots)), _with_slots(pe, n_s, len(slots))
+        ps, pe = ewprog.with_slots(ps, 0, len(slots)), ewprog.with_slots(pe, n_s, len(slots))
         offs = [o for _st, o in views]
         shape = y.type.shape
         nk = len(kdims)
@@ -683,11 +715,14 @@ class PlanExecutor:
             n._bad = bads
         vals = dict(bound)
         for st, rel in zip(self.steps, self.release):
-            vals[st.out] = st.run([vals[i] for i in st.ins])
+            got = st.run([vals[i] for i in st.ins])
+            for oid, t in zip(st.outs, got if isinstance(got, tuple) else (got,)):
+                vals[oid] = t
             for i in rel:
                 if i not in bound:
                     vals.pop(i, None)
-        return vals[self.output]
+        outs = tuple(vals[o] for o in self.outputs)
+        return outs[0] if self.single else outs
 
     def sources(self) -> list:
         return [f"{st.kind}: {st.source}" for st in self.steps]

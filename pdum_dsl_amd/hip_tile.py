@@ -650,8 +650,6 @@ def _reduce_runner(region, cb, grid, dtype):
         le = ewprog.lower(y, rows, leaves, acc=fold)
     except ewprog.Unlowerable as exc:
         raise Untranslatable(f"row reduction: {exc}") from None
-    from .executor import _with_slots
-
     idx = [_index(region, b) for b in ls.bases + le.bases]
     nodes = ls.operands + le.operands
     n_s = len(ls.operands)
@@ -662,8 +660,8 @@ def _reduce_runner(region, cb, grid, dtype):
         st = [ewprog.strides_over(t.stride(), nd.type.names, lat) for t, nd in zip(ops[:n_s], nodes[:n_s])]
         se = [ewprog.strides_over(t.stride(), nd.type.names, rows) for t, nd in zip(ops[n_s:], nodes[n_s:])]
         out = torch.empty(tuple(d.size for d in rows), device="cuda", dtype=getattr(torch, _TORCH_DT[dtype]))
-        ps = _with_slots(ls.program([0] * len(lat), st), 0, len(ops))
-        pe = _with_slots(le.program(out.stride(), se), n_s, len(ops))
+        ps = ewprog.with_slots(ls.program([0] * len(lat), st), 0, len(ops))
+        pe = ewprog.with_slots(le.program(out.stride(), se), n_s, len(ops))
         K.reduce_rows(ps, len(kdims), pe, ops, out)
         torch.cuda.synchronize()
         res = out.float().cpu().numpy()

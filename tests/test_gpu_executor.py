@@ -122,3 +122,54 @@ def test_a_captured_plan_replays_the_eager_result():
         torch.cuda.synchronize()
         assert torch.equal(got, eager), f"replay {i} differs from the eager pass"
         del junk
+
+
+@pytest.mark.parametrize("dtype,tol", [("f32", 1e-5), ("bf16", 2e-2)])
+def test_a_planned_attention_runs_its_flash_carve(dtype, tol):
+    """plan_model on the naive attention region gives one flash carve; the
+    executor binds it to the flash kernel (mask as a band)."""
+    from oracle import closed_forms as cf
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import zoo
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    s = zoo.attention(T=200, S=200, E=64, OD=64, mask="causal", seed=4)
+    plan = plan_model(s.region)
+    assert [c.group.template for c in plan.carves] == ["flash"]
+    ex = PlanExecutor(plan, s.region, dtype)
+    vals = s.numpy_inputs()
+    if dtype == "bf16":
+        vals = [torch.as_tensor(v).to(torch.bfloat16).double().numpy() for v in vals]
+    ex.bind(vals)
+    got = ex.run().double().cpu().numpy()
+    want = cf.attention(*vals, scale=1.0, band=(None, 0))[0]
+    assert np.abs(got - want).max() <= tol * max(1.0, np.abs(want).max())
+
+
+def test_a_planned_flash_joint_runs_forward_and_backward():
+    """The joint (out, dq, dk, dv) claimed whole by plan_model runs as the
+    forward with artifacts plus the fused backward, against the closed form."""
+    from oracle import closed_forms as cf
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import zoo
+    from pdum_dsl_amd.tl.autodiff import grad, region_names
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    s = zoo.attention(T=256, S=256, E=64, OD=64, mask="causal", seed=6)
+    rg = grad(s.region, "out", seed="dO", wrt=("q", "k", "v"), names=region_names(s.region, ("q", "k", "v"), ("out",)))
+    plan = plan_model(rg.region)
+    assert [c.group.template for c in plan.carves] == ["flash-joint"]
+    ex = PlanExecutor(plan, rg.region, "bf16")
+    rng = np.random.default_rng(2)
+    vals = s.numpy_inputs() + [rng.standard_normal((256, 64))]
+    vals = [torch.as_tensor(v).to(torch.bfloat16).double().numpy() for v in vals]
+    ex.bind(vals)
+    ys = rg.region.body[-1].args[0].args  # outputs come in their IR types' dim order
+    orders = (("t", "o"), ("t", "e"), ("s", "e"), ("s", "o"))
+    got = [np.transpose(x.double().cpu().numpy(), [y.type.names.index(n) for n in order])
+           for x, y, order in zip(ex.run(), ys, orders)]
+    q, k, v, do = vals
+    wo = cf.attention(q, k, v, scale=1.0, band=(None, 0))[0]
+    wq, wk, wv = cf.attention_bwd(q, k, v, do, scale=1.0, band=(None, 0))
+    for g, want in zip(got, (wo, wq, wk, wv)):
+        assert np.abs(g - want).max() <= 2e-2 * max(1.0, np.abs(want).max())
