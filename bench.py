@@ -2,12 +2,13 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 
-One step = one causal flash-attention forward over BASELINE.json's
-configs[2] (B=8, H=32, S=4096, D=128, bf16 in, fp32 accumulate, bf16 out +
-fp32 lse), inputs resident in HBM. The line also carries the other
-configurations of the metric, each timed the same way with HIP events on the
-launch stream: the fused row softmax and layernorm ([8192, 4096] fp32, HBM
-GB/s), split-K GQA decode and the causal backward.
+One step = one causal flash-attention forward at the headline shape
+(B=8, H=32, S=4096, D=128, bf16 in, fp32 accumulate, bf16 out + fp32 lse),
+inputs resident in HBM. The line also carries the other configurations of the
+metric, each timed the same way with HIP events on the launch stream: the
+fused row softmax and layernorm ([8192, 4096] fp32, HBM GB/s), split-K GQA
+decode, the causal backward, and the next rows (the fused GEMM epilogue, the
+map chain, the stencil and a carved gpt2-small forward).
 
 Every output is verified against the float64 oracle before timing
 (verify-before-time, as benchmarks/bench_zoo.py:142-150 in the reference).
@@ -91,7 +92,7 @@ def main():
     a = _args()
     if a.gpus != 1:
         print(
-            f"bench.py: this build measures one GPU only (asked for {a.gpus}); every BASELINE config fits one "
+            f"bench.py: this build measures one GPU only (asked for {a.gpus}); every benchmark config fits one "
             "MI355X and the hot path has no cross-GPU exchange to measure",
             file=sys.stderr,
         )

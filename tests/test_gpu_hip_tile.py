@@ -105,7 +105,7 @@ def test_other_closed_masks_bind_as_bands(mask):
 
 
 def test_config_c1_single_head_noncausal_template_attention():
-    """B=H=1, S=256, D=64, fp32, scale 1/sqrt(64) = 1/8
+    """The CPU-runnable headline config C1: B=H=1, S=256, D=64, fp32, scale 1/sqrt(64) = 1/8
     applied to q (exact: a power of two), non-causal via an always-true
     closed mask, through the fusion template."""
     from pdum_dsl_amd.hip_tile import compile_tile_hip
