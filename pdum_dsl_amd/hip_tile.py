@@ -323,7 +323,37 @@ def compile_tile_hip(region: Region, launch: tuple = (), prune: tuple = (), *, d
     )
 
 
-def _finish(run, source: str, grid: int, template: str):
+def _finish(dev, source: str, grid: int, template: str, region: Region, dtype: str):
+    """The seat's ``run(values)`` over the device form ``run.run_dev``.
+
+    ``run_dev(tensors)`` takes device tensors positional per param, each laid
+    out in its param's type-dim order (any float dtype; converted to the
+    column's), launches on the current stream and returns device tensors in
+    the yield's type-dim order, without synchronizing: the per-call host
+    copies stay out of a benchmark's timed region. ``run(values)`` is the
+    reference runner's contract (triton_tile.py:662-698): numpy in, upload,
+    launch, synchronize, numpy out."""
+    shapes = [tuple(d.size for d in p.type.dims) for p in region.params]
+
+    def run_dev(tensors):
+        torch = _torch()
+        tdt = getattr(torch, _TORCH_DT[dtype])
+        ts = []
+        for t, shp in zip(tensors, shapes):
+            if tuple(t.shape) != shp:
+                raise ValueError(f"a param tensor has shape {tuple(t.shape)}, the region wants {shp}")
+            ts.append(t.to(device="cuda", dtype=tdt).contiguous())
+        return dev(ts)
+
+    def run(values):
+        torch = _torch()
+        got = run_dev([torch.as_tensor(np.asarray(v, dtype=np.float32)) for v in values])
+        torch.cuda.synchronize()
+        if isinstance(got, tuple):
+            return tuple(g.float().cpu().numpy() for g in got)
+        return got.float().cpu().numpy()
+
+    run.run_dev = run_dev
     run.source = source
     run.grid = grid
     run.checked = True  # precision is by construction: the MFMA / VALU instruction is chosen, not inferred
@@ -342,26 +372,16 @@ def _flash_runner(region, fb, grid, prune, dtype):
     iq, ik, iv = (_index(region, fb[x]) for x in ("q", "k", "v"))
     tq = fb["q"].type.names
 
-    def run(values):
-        torch = _torch()
-        tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
-        qa = np.asarray(values[iq], dtype=np.float32)
-        if tq != (fb["t"], fb["e"]):
-            qa = qa.T
-        dev = torch.device("cuda")
-        q = torch.as_tensor(np.ascontiguousarray(qa)).to(device=dev, dtype=tdt).view(1, 1, T, E)
-        k = torch.as_tensor(np.ascontiguousarray(values[ik], dtype=np.float32)).to(device=dev, dtype=tdt)
-        v = torch.as_tensor(np.ascontiguousarray(values[iv], dtype=np.float32)).to(device=dev, dtype=tdt)
-        if fb["k"].type.names != (fb["s"], fb["e"]):
-            k = k.t().contiguous()
-        if fb["v"].type.names != (fb["s"], fb["o"]):
-            v = v.t().contiguous()
-        res = K.flash_fwd(q, k.view(1, 1, S, E), v.view(1, 1, S, OD), scale=1.0, band=kband, fill=fb["fill"],
-                          prune=prune, want_lse=False, want_artifacts=fb["artifacts"])
-        torch.cuda.synchronize()
-        out = res.o.view(T, OD).float().cpu().numpy()
+    def dev(ts):
+        def mat(t, names, want, rows, cols):
+            return (t if names == want else t.t()).contiguous().view(1, 1, rows, cols)
+
+        res = K.flash_fwd(mat(ts[iq], tq, (fb["t"], fb["e"]), T, E), mat(ts[ik], fb["k"].type.names, (fb["s"], fb["e"]), S, E),
+                          mat(ts[iv], fb["v"].type.names, (fb["s"], fb["o"]), S, OD), scale=1.0, band=kband,
+                          fill=fb["fill"], prune=prune, want_lse=False, want_artifacts=fb["artifacts"])
+        out = res.o.view(T, OD)
         if fb["artifacts"]:
-            return out, res.m.view(T).cpu().numpy(), res.den.view(T).cpu().numpy()
+            return out, res.m.view(T), res.den.view(T)
         return out
 
     kern = "flash_fwd_generic_f32" if dtype == "f32" else f"flash_fwd_mfma<{dtype},{E}>"
@@ -370,20 +390,7 @@ def _flash_runner(region, fb, grid, prune, dtype):
         f"hip:{kern} t={T} s={S} e={E} od={OD} si={fb['si']} mask={bdesc} fill={fb['fill']:g} "
         f"prune={'on' if prune else 'off'} sweeps=1 stores={3 if fb['artifacts'] else 1}"
     )
-    return _finish(run, src, grid, "flash")
-
-
-def _to_rows(arr: np.ndarray, names: tuple, s: str):
-    """Move dim s last and flatten the rest into rows."""
-    order = tuple(n for n in names if n != s) + (s,)
-    perm = [names.index(n) for n in order]
-    a = np.ascontiguousarray(np.transpose(np.asarray(arr, dtype=np.float32), perm))
-    return a.reshape(-1, a.shape[-1]), a.shape, perm
-
-
-def _from_rows(y: np.ndarray, shape, perm):
-    inv = np.argsort(perm)
-    return np.transpose(y.reshape(shape), inv)
+    return _finish(dev, src, grid, "flash", region, dtype)
 
 
 def _softmax_runner(region, sb, grid, dtype="f32"):
@@ -393,18 +400,15 @@ def _softmax_runner(region, sb, grid, dtype="f32"):
     s = sb["s"]
     out_names = region.body[-1].args[0].type.names
 
-    def run(values):
-        torch = _torch()
-        rows, shape, perm = _to_rows(values[0], names, s)
-        x = torch.as_tensor(rows, device="cuda").to(getattr(torch, _TORCH_DT[dtype]))
+    def dev(ts):
+        order = tuple(n for n in names if n != s) + (s,)
+        x = ts[0].permute([names.index(n) for n in order]).contiguous()
         y = K.row_softmax(x)
-        torch.cuda.synchronize()
-        full = _from_rows(y.float().cpu().numpy(), shape, perm)  # param's dim order
-        return np.transpose(full, [names.index(n) for n in out_names])
+        return y.permute([order.index(n) for n in out_names])
 
     n_rows = math.prod(d.size for d in sb["x"].type.dims if d.name != s)
     src = f"hip:row_softmax rows={n_rows} cols={sb['x'].type.dim(s).size} reduce={s} dtype={dtype} sweeps=1 stores=1"
-    return _finish(run, src, grid, "row-normalization")
+    return _finish(dev, src, grid, "row-normalization", region, dtype)
 
 
 def _layernorm_runner(region, lb, grid, dtype="f32"):
@@ -417,16 +421,11 @@ def _layernorm_runner(region, lb, grid, dtype="f32"):
     ig = _index(region, lb["gamma"]) if lb["gamma"] is not None else None
     ib = _index(region, lb["beta"]) if lb["beta"] is not None else None
 
-    def run(values):
-        torch = _torch()
-        tdt = getattr(torch, _TORCH_DT[dtype])
-        rows, shape, perm = _to_rows(values[ix], names, feat)
-        g = None if ig is None else torch.as_tensor(np.asarray(values[ig], dtype=np.float32), device="cuda").to(tdt)
-        b = None if ib is None else torch.as_tensor(np.asarray(values[ib], dtype=np.float32), device="cuda").to(tdt)
-        y = K.layernorm(torch.as_tensor(rows, device="cuda").to(tdt), g, b, eps=lb["eps"])
-        torch.cuda.synchronize()
-        full = _from_rows(y.float().cpu().numpy(), shape, perm)
-        return np.transpose(full, [names.index(n) for n in out_names])
+    def dev(ts):
+        order = tuple(n for n in names if n != feat) + (feat,)
+        x = ts[ix].permute([names.index(n) for n in order]).contiguous()
+        y = K.layernorm(x, None if ig is None else ts[ig], None if ib is None else ts[ib], eps=lb["eps"])
+        return y.permute([order.index(n) for n in out_names])
 
     n_rows = math.prod(d.size for d in lb["x"].type.dims if d.name != feat)
     src = (
@@ -434,7 +433,7 @@ def _layernorm_runner(region, lb, grid, dtype="f32"):
         f"eps={lb['eps']:g} affine={'gamma' if ig is not None else ''}{'+beta' if ib is not None else ''} dtype={dtype} "
         "sweeps=1 stores=1"
     )
-    return _finish(run, src, grid, "row-statistics")
+    return _finish(dev, src, grid, "row-statistics", region, dtype)
 
 
 def _flash_joint_runner(region, fj, grid, dtype):
@@ -456,32 +455,22 @@ def _flash_joint_runner(region, fj, grid, dtype):
     wrt = fj["wrt"]
     out_names = y.args[0].type.names
 
-    def run(values):
-        torch = _torch()
-        tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
-        dev = torch.device("cuda")
+    def dev(ts):
+        def mat(t, node, order, rows, cols):
+            return t.permute([node.type.names.index(n) for n in order]).contiguous().view(1, 1, rows, cols)
 
-        def up(i, node, order, rows, cols):
-            a = np.asarray(values[i], dtype=np.float32)
-            a = np.transpose(a, [node.type.names.index(n) for n in order])
-            return torch.as_tensor(np.ascontiguousarray(a)).to(device=dev, dtype=tdt).view(1, 1, rows, cols)
-
-        q = up(iq, q_, (t, e), T, E)
-        k = up(ik, k_, (s, e), S, E)
-        v = up(iv, v_, (s, o), S, OD)
-        seed_node = region.params[iseed]
-        do = up(iseed, seed_node, (t, o), T, OD)
+        q = mat(ts[iq], q_, (t, e), T, E)
+        k = mat(ts[ik], k_, (s, e), S, E)
+        v = mat(ts[iv], v_, (s, o), S, OD)
+        do = mat(ts[iseed], region.params[iseed], (t, o), T, OD)
         res = K.flash_fwd(q, k, v, scale=1.0, band=kband, fill=fj["fill"], want_artifacts=True)
         dq, dk, dv = K.flash_bwd(q, k, v, res.o, do, res.lse, m=res.m, den=res.den, scale=1.0, band=kband,
                                  fill=fj["fill"])
-        torch.cuda.synchronize()
-        host = lambda x, rows, cols: x.view(rows, cols).float().cpu().numpy()  # noqa: E731
-        outs = {"q": (host(dq, T, E), (t, e)), "k": (host(dk, S, E), (s, e)), "v": (host(dv, S, OD), (s, o))}
-        out = host(res.o, T, OD)
-        ys = [np.transpose(out, [(t, o).index(n) for n in out_names])]
+        outs = {"q": (dq.view(T, E), (t, e)), "k": (dk.view(S, E), (s, e)), "v": (dv.view(S, OD), (s, o))}
+        ys = [res.o.view(T, OD).permute([(t, o).index(n) for n in out_names])]
         for nm, gt in zip(wrt, grad_types):
-            arr, order = outs[nm]
-            ys.append(np.transpose(arr, [order.index(n) for n in gt.names]))
+            x, order = outs[nm]
+            ys.append(x.permute([order.index(n) for n in gt.names]))
         return tuple(ys)
 
     kern = "flash_fwd_generic_f32 + bwd_rows_f32" if dtype == "f32" else f"flash_fwd_mfma<{dtype},{E}> + bwd_main<{dtype},{E}>"
@@ -490,7 +479,7 @@ def _flash_joint_runner(region, fj, grid, dtype):
         f"hip:{kern} t={T} s={S} e={E} od={OD} mask={bdesc} fill={fj['fill']:g} wrt={','.join(wrt)} "
         "artifacts=m,den launches=fwd+bwd"
     )
-    return _finish(run, src, grid, "flash-joint")
+    return _finish(dev, src, grid, "flash-joint", region, dtype)
 
 
 # ------------------------------------------- map-chain and contraction-epilogue
@@ -507,21 +496,18 @@ def recognize_map_chain(region: Region) -> bool:
     return all(n.op in _CHAIN_OPS for n in walk(region))
 
 
-def _upload(torch, arr, names, order, dtype, pad_last=None, zero_fill=False):
-    """A param's numpy array (dims ``names``) as a contiguous device tensor
-    with dims ``order`` (absent dims as size 1), optionally zero-padded in the
-    last dim to ``pad_last``."""
-    a = np.asarray(arr, dtype=np.float32)
-    perm = [names.index(n) for n in order if n in names]
-    a = np.transpose(a, perm)
-    shape = [a.shape[perm.index(names.index(n))] if n in names else 1 for n in order]
-    a = a.reshape(shape)
-    t = torch.as_tensor(np.ascontiguousarray(a)).to(device="cuda", dtype=getattr(torch, _TORCH_DT[dtype]))
+def _arrange(torch, t, names, order, pad_last=None):
+    """A device tensor with dims ``names`` as a contiguous tensor with dims
+    ``order`` (absent dims as size 1), optionally zero-padded in the last dim
+    to ``pad_last``."""
+    x = t.permute([names.index(n) for n in order if n in names]).contiguous()
+    shape = [t.shape[names.index(n)] if n in names else 1 for n in order]
+    x = x.reshape(shape)
     if pad_last is not None and pad_last != shape[-1]:
         full = torch.zeros(shape[:-1] + [pad_last], device="cuda", dtype=t.dtype)
-        full[..., : shape[-1]] = t
-        t = full
-    return t
+        full[..., : shape[-1]] = x
+        x = full
+    return x
 
 
 def _map_chain_runner(region, grid, dtype):
@@ -539,29 +525,24 @@ def _map_chain_runner(region, grid, dtype):
     out_names = y.type.names
     shifted = sum(1 for _names, sh in low.views if any(sh.values()))
 
-    def run(values):
+    def dev(ts):
         torch = _torch()
-        uploaded = {}
         ops, strides = [], []
         for j, (i, base) in enumerate(zip(idx, low.bases)):
-            if i not in uploaded:  # each param once; shifted reads are offset views of it
-                uploaded[i] = _upload(torch, values[i], base.type.names, base.type.names, dtype)
-            t = uploaded[i]
+            t = ts[i]  # each param once; shifted reads are offset views of it
             st, off = low.operand_view(j, dict(zip(base.type.names, t.stride())))
             if off < 0:
                 raise Untranslatable("a shifted read starts before its tensor")
             ops.append(t.reshape(-1)[off:])
             strides.append(st)
         out = torch.empty(tuple(d.size for d in dims), device="cuda", dtype=getattr(torch, _TORCH_DT[dtype]))
-        prog = low.program(out.stride(), strides)
-        K.map_chain(prog, ops, out)
-        torch.cuda.synchronize()
-        return out.float().cpu().numpy().reshape(tuple(d.size for d in dims))
+        K.map_chain(low.program(out.stride(), strides), ops, out)
+        return out
 
     tmpl = "stencil" if shifted else "map-chain"
     src = (f"hip:map_chain lattice=({','.join(out_names)}) insns={len(low.insns)} operands={len(low.operands)} "
            f"shifted_reads={shifted} sweeps=1 stores=1")
-    return _finish(run, src, grid, tmpl)
+    return _finish(dev, src, grid, tmpl, region, dtype)
 
 
 def recognize_contraction(region: Region):
@@ -654,25 +635,23 @@ def _reduce_runner(region, cb, grid, dtype):
     nodes = ls.operands + le.operands
     n_s = len(ls.operands)
 
-    def run(values):
+    def dev(ts):
         torch = _torch()
-        ops = [_upload(torch, values[i], nd.type.names, nd.type.names, dtype) for i, nd in zip(idx, nodes)]
+        ops = [ts[i] for i in idx]
         st = [ewprog.strides_over(t.stride(), nd.type.names, lat) for t, nd in zip(ops[:n_s], nodes[:n_s])]
         se = [ewprog.strides_over(t.stride(), nd.type.names, rows) for t, nd in zip(ops[n_s:], nodes[n_s:])]
         out = torch.empty(tuple(d.size for d in rows), device="cuda", dtype=getattr(torch, _TORCH_DT[dtype]))
         ps = ewprog.with_slots(ls.program([0] * len(lat), st), 0, len(ops))
         pe = ewprog.with_slots(le.program(out.stride(), se), n_s, len(ops))
         K.reduce_rows(ps, len(kdims), pe, ops, out)
-        torch.cuda.synchronize()
-        res = out.float().cpu().numpy()
         if not y.type.dims:
-            return res.reshape(())
+            return out.reshape(())
         names = [d.name for d in rows]
-        return np.transpose(res, [names.index(nm) for nm in y.type.names])
+        return out.permute([names.index(nm) for nm in y.type.names])
 
     src = (f"hip:reduce_rows shape={cb['shape']} rows={math.prod(d.size for d in rows)} "
            f"k={math.prod(d.size for d in kdims)} summand_insns={len(ls.insns)} epilogue_insns={len(le.insns)} stores=1")
-    return _finish(run, src, grid, "contraction-epilogue")
+    return _finish(dev, src, grid, "contraction-epilogue", region, dtype)
 
 
 def _contraction_runner(region, cb, grid, dtype):
@@ -715,35 +694,31 @@ def _contraction_runner(region, cb, grid, dtype):
     pa, pb = operand(cb["a"], a_order), operand(cb["b"], b_order)
     epi_idx = [_index(region, p) for p in epi.bases]
 
-    def run(values):
+    def dev(ts):
         torch = _torch()
         tdt = getattr(torch, _TORCH_DT[dtype])
 
         def build(spec, node, order, rows):
             if spec[0] == "param":
-                return _upload(torch, values[spec[1]], node.type.names, order, dtype, pad_last=KP)
+                return _arrange(torch, ts[spec[1]], node.type.names, order, pad_last=KP)
             low = spec[1]
-            ins = [_upload(torch, values[_index(region, b)], p.type.names, p.type.names, dtype)
-                   for p, b in zip(low.operands, low.bases)]
+            ins = [ts[_index(region, b)] for b in low.bases]
             st = [ewprog.strides_over(t.stride(), p.type.names, low.dims) for t, p in zip(ins, low.operands)]
             buf = torch.zeros((low.dims[0].size, rows, KP), device="cuda", dtype=tdt)
-            prog = low.program(buf.stride(), st)
-            K.map_chain(prog, ins, buf)
+            K.map_chain(low.program(buf.stride(), st), ins, buf)
             return buf
 
         a = build(pa, cb["a"], a_order, M_)
         bt = build(pb, cb["b"], b_order, N_)
-        ops = [_upload(torch, values[i], p.type.names, p.type.names, dtype) for i, p in zip(epi_idx, epi.operands)]
+        ops = [ts[i] for i in epi_idx]
         st = [ewprog.strides_over(t.stride(), p.type.names, lattice) for t, p in zip(ops, epi.operands)]
         out = torch.empty((B_, M_, N_), device="cuda", dtype=tdt)
-        prog = epi.program(out.stride(), st)
-        K.contract(a, bt, Kdim, prog, ops, out)
-        torch.cuda.synchronize()
+        K.contract(a, bt, Kdim, epi.program(out.stride(), st), ops, out)
         present = [nm for nm in lnames if nm in y.type.names]  # the unit stand-ins drop out
-        full = out.float().cpu().numpy().reshape(tuple(size[nm].size for nm in present))
-        return np.transpose(full, [present.index(nm) for nm in y.type.names])
+        full = out.reshape(tuple(size[nm].size for nm in present))
+        return full.permute([present.index(nm) for nm in y.type.names])
 
     kern = "contract_f32" if dtype == "f32" else f"contract_mfma<{dtype}>"
     src = (f"hip:{kern} batch={B_} m={M_} n={N_} k={Kdim} kp={KP} prologue={pa[0]},{pb[0]} "
            f"epilogue_insns={len(epi.insns)} operands={len(epi.operands)} stores=1")
-    return _finish(run, src, grid, "contraction-epilogue")
+    return _finish(dev, src, grid, "contraction-epilogue", region, dtype)
