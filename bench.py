@@ -364,7 +364,9 @@ def _carved_plan_line(torch):
     vocab 50257), random weights, bf16: planned by plan_model (the
     anchor-and-absorb partition) and run by the device executor, every
     boundary in HBM, the pass captured as one HIP graph (``ms``; the
-    per-kernel launched pass is ``ms_eager_launches``). Checked against the
+    per-kernel launched pass is ``ms_eager_launches``; each layer's softmax
+    and PV carves run as one flash launch, and ``ms_without_attention_chains``
+    times the same plan with every carve launched apart). Checked against the
     same forward in fp32 on the same bf16 weights; timed beside torch's own
     bf16 forward (eager)."""
     import time as _time
@@ -405,6 +407,12 @@ def _carved_plan_line(torch):
     assert torch.equal(replayed, eager), "the captured plan's replay differs from the eager pass"
     ms = time_events(lambda: ex.replay(check=False), 20)
     ms_torch = time_events(lambda: _gpt2_torch(torch, W, cfg), 10)
+    # the same plan with every carve its own launch (scores, softmax and PV apart)
+    ex2 = PlanExecutor(plan, m.region, "bf16", fuse_attention=False)
+    ex2.bind(m.values())
+    ex2.capture()
+    ms_unfused = time_events(lambda: ex2.replay(check=False), 20)
+    del ex2
     T, D, M, V, L_ = cfg.t, cfg.d, cfg.m, cfg.v, cfg.layers
     fl = 2.0 * T * (L_ * (4 * D * D + 2 * D * M) + D * V) + L_ * 4.0 * T * T * D
     by = {}
@@ -414,6 +422,8 @@ def _carved_plan_line(torch):
         "config": "gpt2-small shape, 12 layers, t=1024 tokens, d=768, 12x64 heads, mlp 3072, vocab 50257, bf16 "
                   "storage / fp32 accumulate; random weights",
         "carves": by, "device_steps": len(ex.steps) + sum(len(n.steps) for n in ex.nested),
+        "attention_chains": sum(st.kind == "flash-chain" for st in ex.steps),
+        "ms_without_attention_chains": round(ms_unfused, 4),
         "plan_s": round(plan_s, 2), "ms": round(ms, 4), "ms_eager_launches": round(ms_eager, 4),
         "tokens_per_s": round(T / ms * 1e3, 1),
         "TFLOP/s": round(fl / ms / 1e9, 1), "algorithmic_flop": fl,

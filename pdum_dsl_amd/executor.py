@@ -21,6 +21,10 @@ kernels, one step per carve:
   row-statistics        pdh_layernorm_dt with the affine epilogue
   map-chain, stencil    pdh_map_chain (shifted reads as offset views)
   ROWSUM / PLAIN        pdh_reduce_rows
+  softmax + PV carves   when they compute banded attention per head (the
+                        scores dissolved into the softmax carve, its
+                        probabilities read by one contraction carve alone):
+                        one pdh_flash_fwd launch for the pair
   red, tl.take          pdh_take_rows for the gather, the rest of the carve
                         as a map chain; any other red carve refuses
 
@@ -41,7 +45,7 @@ from . import _lib as L
 from . import ewprog
 from .hip_tile import Untranslatable, recognize_layernorm
 from .tl.dialect import OPS
-from .tl.fusion import match_contraction_epilogue, match_softmax, plan_region
+from .tl.fusion import contract_core, forest_is_closed, match_contraction_epilogue, match_softmax, plan_region
 from .tl.ir import Builder, Dim, Region, walk
 
 _TORCH_DT = {"f32": "float32", "bf16": "bfloat16", "f16": "float16"}
@@ -104,6 +108,157 @@ def _over(view_names, view_shape, lattice) -> list:
     return [st.get(d.name, 0) for d in lattice]
 
 
+def _under_renames(n):
+    while n.op == "tl.rename":
+        n = n.args[0]
+    return n
+
+
+def _band_has_empty_row(T: int, S: int, lo, hi) -> bool:
+    import numpy as np
+
+    r = np.arange(T)
+    first = np.zeros(T, np.int64) if lo is None else np.maximum(0, r + lo)
+    last = np.full(T, S - 1, np.int64) if hi is None else np.minimum(S - 1, r + hi)
+    return bool((first > last).any())
+
+
+@dataclass(frozen=True)
+class _AttentionChain:
+    """A softmax carve and the contraction carve reading its probabilities,
+    launched as one flash forward (``_attention_chains``)."""
+
+    soft: object  # the row-normalization Carve
+    pv: object  # the contraction-epilogue Carve
+    drop: tuple  # the carves the launch replaces besides pv: soft, and the score carve when there is one
+    nodes: tuple  # the model nodes q, k, v
+    sources: tuple  # per q, k, v: None (a boundary value, read as is) or (region, bounds) computing it
+    bounds: tuple  # every boundary node the launch reads, per q, k, v in turn
+    root: object  # the attention output: pv's root
+    t: str
+    s: str
+    e: str
+    o: str
+    heads: tuple  # the shared head dim (or none)
+    band: tuple  # mask_to_band of the closed mask
+    fill: float
+
+
+def _attention_chains(carves, region, dtype: str) -> list:
+    """Banded attention that the reference plan carves in two or three: a
+    row-normalization carve softmax_s(where(mask, sum_e q*k, fill)) whose
+    score contraction is dissolved into it (over boundary values q and k) or
+    carved on its own (a contraction carve with no epilogue, read by the
+    softmax alone), and a contraction carve sum_s p*v over its probabilities
+    p and a boundary value v (partition.py:458-607 on the attention of
+    zoo/gpt2.py, the traffic gate choosing between the two forms: the head
+    dim keeps fusion.py:480-539's flash matcher from claiming it whole). Per head
+    the pair is flash attention, so the executor launches pdh_flash_fwd once
+    for it instead of a score GEMM, a row softmax and a PV GEMM, and the
+    (t, s) scores never reach HBM.
+
+    A pair is bound only where that is exact: a closed mask forest that is a
+    band with a live key in every row; a fill at or below -1e6 (a masked
+    score then adds exp(fill - max) == 0 in fp32, so dead key tiles may be
+    skipped); the probabilities read by the PV carve alone and yielded by
+    nothing; no artifacts; t and s starting at 0; at most one shared head
+    dim; and the flash kernel's widths (16-bit: e == od in {64, 128}; fp32:
+    od <= 512). q, k and v are boundary values, or values the carves compute
+    from theirs (a projection the traffic gate dissolved into its consumer):
+    those are extracted as regions and materialized first."""
+    from .hip_tile import mask_to_band
+    from .tl.partition import _extract
+
+    def source(x, carve):
+        cb = {id(n) for n in carve.bounds}
+        if id(x) in cb:
+            return None, (x,)
+        members, todo = set(), [x]
+        while todo:
+            n = todo.pop()
+            if id(n) in members or id(n) in cb:
+                continue
+            members.add(id(n))
+            todo.extend(n.args)
+        sub, sb = _extract(x, members)
+        return (sub, sb), sb
+
+    reads: dict = {}
+    for c in carves:
+        for b in c.bounds:
+            i = id(_under_renames(b))
+            reads[i] = reads.get(i, 0) + 1
+    y = region.body[-1].args[0]
+    yielded = {id(_under_renames(x)) for x in (y.args if y.op == "core.tuple" else (y,))}
+    soft = {id(c.root): c for c in carves if c.root is not None and c.group.template == "row-normalization"}
+    contr = {id(c.root): c for c in carves if c.root is not None and c.group.template == "contraction-epilogue"}
+    out = []
+    for c in carves:
+        if c.root is None or c.group.template != "contraction-epilogue" or c.artifacts:
+            continue
+        core = contract_core(c.root)
+        if core is None:
+            continue
+        x, w, s = core
+        pairs = [(p, v) for p, v in ((x, w), (w, x)) if id(p) in soft]
+        if len(pairs) != 1:
+            continue
+        pr, v = pairs[0]
+        sc = soft[id(pr)]
+        if sc.artifacts or reads.get(id(pr)) != 1 or id(pr) in yielded:
+            continue
+        sm = match_softmax(pr)
+        if sm is None or sm["s"] != s:
+            continue
+        wh = sm["sm"]
+        if wh.op != "tl.pointwise" or wh.attr("f") != "where" or len(wh.args) != 3:
+            continue
+        mask, scores, fill = wh.args
+        if fill.op not in ("core.const", "tl.const") or float(fill.attr("value")) > -1e6:
+            continue
+        if not forest_is_closed(mask):
+            continue
+        core2 = contract_core(scores)
+        if core2 is None:
+            continue
+        a, b, e = core2
+        q, k = (b, a) if s in a.type.names else (a, b)
+        drop, qk_carve = (sc,), sc
+        if id(scores) in {id(n) for n in sc.bounds}:  # the scores carved on their own
+            scc = contr.get(id(scores))
+            if scc is None or scc.artifacts or reads.get(id(scores)) != 1 or id(scores) in yielded:
+                continue
+            drop, qk_carve = (sc, scc), scc
+        if id(v) == id(pr):
+            continue
+        qn, kn, vn, on = (tuple(n.type.names) for n in (q, k, v, c.root))
+        heads = tuple(d for d in qn if d != e and d in kn)
+        ts = [d for d in qn if d not in heads and d != e]
+        os_ = [d for d in vn if d not in heads and d != s]
+        if len(heads) > 1 or len(ts) != 1 or len(os_) != 1 or s in qn:
+            continue
+        t, o = ts[0], os_[0]
+        if set(kn) != {s, e, *heads} or set(vn) != {s, o, *heads} or set(on) != {t, o, *heads}:
+            continue
+        if any(n.type.dim(h) != q.type.dim(h) for n in (k, v) for h in heads) or v.type.dim(s) != k.type.dim(s):
+            continue
+        if q.type.dim(t).start != 0 or k.type.dim(s).start != 0:
+            continue
+        T, S, E, OD = q.type.dim(t).size, k.type.dim(s).size, q.type.dim(e).size, v.type.dim(o).size
+        if (dtype != "f32" and not (E == OD and E in (64, 128))) or OD > 512:
+            continue
+        try:
+            band = mask_to_band(mask, t, s, T, S)
+        except Untranslatable:
+            continue
+        if band[0] == "band" and _band_has_empty_row(T, S, band[1], band[2]):
+            continue
+        srcs = [source(q, qk_carve), source(k, qk_carve), source(v, c)]
+        out.append(_AttentionChain(sc, c, drop, (q, k, v), tuple(x for x, _ in srcs), tuple(b for _, bs in srcs for b in bs),
+                                   c.root, t, s, e, o, heads, band, float(fill.attr("value"))))
+    return out
+
+
 @dataclass
 class _Pack:
     """One contraction operand laid out [batch][rows][kp] (k contiguous, zero
@@ -139,7 +294,7 @@ class PlanExecutor:
     """Runs a ModelPlan of ``region`` on the device. ``dtype`` is the element
     type of every floating value (f32, bf16 or f16)."""
 
-    def __init__(self, plan, region: Region, dtype: str = "bf16", _shared=None):
+    def __init__(self, plan, region: Region, dtype: str = "bf16", fuse_attention: bool = True, _shared=None):
         if dtype not in _TORCH_DT:
             raise ValueError(f"dtype {dtype!r}: f32, bf16 or f16")
         self.region, self.dtype = region, dtype
@@ -154,6 +309,11 @@ class PlanExecutor:
         rootless = [c for c in plan.carves if c.root is None]
         if rootless:
             raise Untranslatable(f"a multi-output residue cannot run on the device: {rootless[0].group.reason}")
+        if fuse_attention:  # a softmax carve and its PV carve as one flash launch
+            chains = _attention_chains(pending, region, dtype)
+            dropped = {id(d) for ch in chains for d in ch.drop}
+            by_pv = {id(ch.pv): ch for ch in chains}
+            pending = [by_pv.get(id(c), c) for c in pending if id(c) not in dropped]
         self.steps: list = []
         while pending:
             for c in pending:
@@ -195,6 +355,9 @@ class PlanExecutor:
         return None
 
     def _step(self, carve, ins):
+        if isinstance(carve, _AttentionChain):
+            run, src = self._attention(carve)
+            return Step("flash-chain", ins, (id(carve.root),), run, src)
         tmpl = carve.group.template
         k = carve.kernel
         outs = (id(carve.root),)
@@ -253,6 +416,71 @@ class PlanExecutor:
             return (out, res.m.view(T), res.den.view(T)) if arts else (out,)
 
         return run, f"flash_fwd t={T} s={S} e={E} od={OD} band={band} artifacts={arts}"
+
+    def _attention(self, ch):
+        """The pair of ``_attention_chains`` as one pdh_flash_fwd launch: q, k,
+        v (materialized first by nested plans where a carve computed them)
+        and the output read as [1, heads, rows, features] views of dense
+        tensors (copied only where the feature dim is not the innermost or a
+        stride breaks the kernel's 16-byte rows)."""
+        from . import kernels as K
+        from .tl.partition import plan_model
+
+        q_, k_, v_ = ch.nodes
+        getters, at = [], 0
+        for src in ch.sources:
+            if src is None:
+                getters.append((None, None, at, 1))
+                at += 1
+            else:
+                sub, sb = src
+                nested = PlanExecutor(plan_model(sub, dissolve=False), sub, self.dtype,
+                                      _shared=(self._packs, self._static))
+                self.nested.append(nested)
+                getters.append((nested, sub, at, len(sb)))
+                at += len(sb)
+
+        def operand(vals, g):
+            nested, sub, i, n = g
+            if nested is None:
+                return vals[i]
+            return nested._run({id(p): v for p, v in zip(sub.params, vals[i:i + n])}, self._bad)
+        t, s_, e, o, heads = ch.t, ch.s, ch.e, ch.o, ch.heads
+        T, S, E, OD = q_.type.dim(t).size, k_.type.dim(s_).size, q_.type.dim(e).size, v_.type.dim(o).size
+        H = q_.type.dim(heads[0]).size if heads else 1
+        kband = None if ch.band[0] == "none" else K.Band(ch.band[1], ch.band[2])
+        out_names, out_shape = ch.root.type.names, ch.root.type.shape
+
+        def perm(names, rows, feat):
+            return [names.index(h) for h in heads] + [names.index(rows), names.index(feat)]
+
+        plans = [perm(n.type.names, r, f) for n, r, f in ((q_, t, e), (k_, s_, e), (v_, s_, o))]
+        oplan = perm(out_names, t, o)
+
+        def usable(x):
+            return x.stride(-1) == 1 and all(st % 8 == 0 for st in x.stride()[:-1]) and x.data_ptr() % 16 == 0
+
+        def heads4(x):
+            return x.unsqueeze(0) if heads else x.unsqueeze(0).unsqueeze(0)
+
+        def run(vals):
+            torch = _torch()
+            ops = []
+            for g, pm in zip(getters, plans):
+                xv = operand(vals, g).permute(*pm)
+                ops.append(heads4(xv if usable(xv) else xv.contiguous()))
+            out = torch.empty(out_shape, dtype=ops[0].dtype, device=ops[0].device)
+            ov = out.permute(*oplan)
+            direct = usable(ov)
+            o4 = heads4(ov) if direct else None
+            res = K.flash_fwd(*ops, scale=1.0, band=kband, fill=ch.fill, want_lse=False, out=o4)
+            if not direct:
+                ov.copy_(res.o.view(ov.shape))
+            return (out,)
+
+        made = "".join("b" if x is None else "m" for x in ch.sources)
+        return run, (f"flash_fwd (softmax + PV carves) heads={H} t={T} s={S} e={E} od={OD} band={ch.band} "
+                     f"qkv={made}")
 
     def _flash_joint(self, k):
         """The flash joint claimed whole: the forward with its artifacts and

@@ -33,6 +33,7 @@ computes on the host.
 
 from __future__ import annotations
 
+import contextlib
 import math
 
 import numpy as np
@@ -326,24 +327,26 @@ def compile_tile_hip(region: Region, launch: tuple = (), prune: tuple = (), *, d
 def _finish(dev, source: str, grid: int, template: str, region: Region, dtype: str):
     """The seat's ``run(values)`` over the device form ``run.run_dev``.
 
-    ``run_dev(tensors)`` takes device tensors positional per param, each laid
-    out in its param's type-dim order (any float dtype; converted to the
-    column's), launches on the current stream and returns device tensors in
+    ``run_dev(tensors, stream=None)`` takes device tensors positional per
+    param, each laid out in its param's type-dim order (any float dtype;
+    converted to the column's), launches on ``stream`` (a torch stream; the
+    current one when None) and returns device tensors in
     the yield's type-dim order, without synchronizing: the per-call host
     copies stay out of a benchmark's timed region. ``run(values)`` is the
     reference runner's contract (triton_tile.py:662-698): numpy in, upload,
     launch, synchronize, numpy out."""
     shapes = [tuple(d.size for d in p.type.dims) for p in region.params]
 
-    def run_dev(tensors):
+    def run_dev(tensors, stream=None):
         torch = _torch()
         tdt = getattr(torch, _TORCH_DT[dtype])
-        ts = []
+        if len(tensors) != len(shapes):
+            raise ValueError(f"{len(tensors)} param tensors given, the region has {len(shapes)} params")
         for t, shp in zip(tensors, shapes):
             if tuple(t.shape) != shp:
                 raise ValueError(f"a param tensor has shape {tuple(t.shape)}, the region wants {shp}")
-            ts.append(t.to(device="cuda", dtype=tdt).contiguous())
-        return dev(ts)
+        with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
+            return dev([t.to(device="cuda", dtype=tdt).contiguous() for t in tensors])
 
     def run(values):
         torch = _torch()

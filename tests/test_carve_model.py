@@ -122,3 +122,23 @@ def _nodes(region):
     from pdum_dsl_amd.tl.ir import walk
 
     return walk(region)
+
+
+def test_the_executor_finds_the_attention_chains_of_each_carve_form():
+    """Host-side: the softmax + PV carve pairs the executor launches as one
+    flash forward, per traffic-gate form, and the 16-bit width rule."""
+    from pdum_dsl_amd.executor import _attention_chains
+    from pdum_dsl_amd.tl import zoo
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    def chains(t, hk, dtype):
+        m = zoo.gpt2(zoo.GPT2Config(t=t, d=128, nh=128 // hk, hk=hk, m=512, layers=1, v=64), seed=3)
+        return _attention_chains(list(plan_model(m.region).carves), m.region, dtype)
+
+    for t, drop, made in ((64, 2, [None] * 3), (128, 1, [None] * 3), (256, 1, ["m"] * 3)):
+        (ch,) = chains(t, 64, "bf16")
+        assert len(ch.drop) == drop and (ch.t, ch.s, ch.e, ch.o, ch.heads) == ("t", "s", "hk", "hk", ("nh",))
+        assert ch.band == ("band", None, 0) and ch.fill <= -1e6
+        assert [None if x is None else "m" for x in ch.sources] == made
+        assert len(ch.bounds) == (3 if made[0] is None else sum(len(x[1]) for x in ch.sources))
+    assert chains(128, 32, "bf16") == [] and len(chains(128, 32, "f32")) == 1  # 16-bit flash wants e in {64, 128}

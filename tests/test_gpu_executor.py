@@ -18,13 +18,13 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-def _run(cfg, dtype, seed=7):
+def _run(cfg, dtype, seed=7, fuse=True):
     from pdum_dsl_amd.executor import PlanExecutor
     from pdum_dsl_amd.tl import zoo
     from pdum_dsl_amd.tl.partition import plan_model
 
     m = zoo.gpt2(cfg, seed=seed)
-    ex = PlanExecutor(plan_model(m.region), m.region, dtype)
+    ex = PlanExecutor(plan_model(m.region), m.region, dtype, fuse_attention=fuse)
     ex.bind(m.values())
     out = ex.run()
     torch.cuda.synchronize()
@@ -37,21 +37,49 @@ def _run(cfg, dtype, seed=7):
 def test_the_toy_gpt2_runs_carve_by_carve_at_f32():
     from pdum_dsl_amd.tl import zoo
 
-    got, want, ex = _run(zoo.GPT2Config(), "f32")
+    got, want, ex = _run(zoo.GPT2Config(), "f32", fuse=False)
     assert len(ex.steps) == 23
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-4 * np.abs(want).max())
+    # each layer's softmax carve and PV carve launched as one flash forward
+    got, want, ex = _run(zoo.GPT2Config(), "f32")
+    assert len(ex.steps) == 21 and sum(st.kind == "flash-chain" for st in ex.steps) == 2
     np.testing.assert_allclose(got, want, rtol=0, atol=1e-4 * np.abs(want).max())
 
 
+@pytest.mark.parametrize("fuse", [True, False])
 @pytest.mark.parametrize("dtype,tol", [("f32", 1e-4), ("bf16", 3e-2)])
-def test_a_sized_gpt2_matches_the_numpy_model(dtype, tol):
+def test_a_sized_gpt2_matches_the_numpy_model(dtype, tol, fuse):
     from pdum_dsl_amd.tl import zoo
 
     cfg = zoo.GPT2Config(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)
-    got, want, ex = _run(cfg, dtype, seed=3)
+    got, want, ex = _run(cfg, dtype, seed=3, fuse=fuse)
     src = " | ".join(ex.sources())
     assert "a=direct" in src  # layernorm outputs feed the projections without a pack
+    assert ("softmax + PV carves" in src) == fuse
     err = np.abs(got - want).max()
     assert err <= tol * np.abs(want).max(), f"{dtype}: max err {err} vs scale {np.abs(want).max()}"
+
+
+@pytest.mark.parametrize("t,form", [(64, "scores carved"), (128, "scores dissolved"), (256, "projections dissolved")])
+@pytest.mark.parametrize("dtype,tol", [("f32", 1e-4), ("bf16", 3e-2)])
+def test_attention_chains_in_each_carve_form(t, form, dtype, tol):
+    """The softmax + PV carves launched as one flash forward in each form the
+    traffic gate gives them: the scores a carve of their own (t=64), the
+    scores dissolved into the softmax carve (t=128), and the q/k/v
+    projections dissolved too, so the launch materializes them first
+    (t=256). Against the numpy model, and against the unfused plan."""
+    from pdum_dsl_amd.tl import zoo
+
+    cfg = zoo.GPT2Config(t=t, d=128, nh=2, hk=64, m=512, layers=1, v=64)
+    got, want, ex = _run(cfg, dtype, seed=3)
+    chains = [st for st in ex.steps if st.kind == "flash-chain"]
+    assert len(chains) == 1
+    made = {"scores carved": "qkv=bbb", "scores dissolved": "qkv=bbb", "projections dissolved": "qkv=mmm"}[form]
+    assert made in chains[0].source
+    n_unfused = len(_run(cfg, dtype, seed=3, fuse=False)[2].steps)
+    assert len(ex.steps) == n_unfused - (2 if form == "scores carved" else 1)
+    err = np.abs(got - want).max()
+    assert err <= tol * np.abs(want).max(), f"{dtype} {form}: max err {err} vs scale {np.abs(want).max()}"
 
 
 def test_an_out_of_range_token_id_is_refused():

@@ -212,3 +212,10 @@ def test_run_dev_takes_device_tensors_and_matches_run():
         assert all(d.is_cuda for d in dev)
         for d, h in zip(dev, host):
             np.testing.assert_array_equal(d.cpu().numpy(), h)
+    # the stencil's runner on a side stream the caller names: the same bits once it is synchronized
+    side = torch.cuda.Stream()
+    x = torch.as_tensor(np.asarray(st.inputs[0].arr), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    got = run.run_dev([x], stream=side)
+    side.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), run([st.inputs[0].arr]))
