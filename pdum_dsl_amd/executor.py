@@ -142,9 +142,44 @@ class _AttentionChain:
     heads: tuple  # the shared head dim (or none)
     band: tuple  # mask_to_band of the closed mask
     fill: float
+    merged: tuple | None = None  # (activation, (wq, wk, wv), contracted dim, q scale): one GEMM makes q, k, v
 
 
-def _attention_chains(carves, region, dtype: str) -> list:
+def _merged_projection(q, k, v, t, s, e, o, heads):
+    """q, k and v as projections of one activation by three weight params,
+    q optionally times a positive constant (the attention scale folded into
+    q): (activation, (wq, wk, wv), contracted dim, scale), or None. The
+    three then come out of one GEMM over the concatenated weights (a third
+    of the launches, three times the workgroups), and the scale moves into
+    the flash launch (it multiplies q.k in fp32 there instead of q before
+    rounding)."""
+    scale = 1.0
+    if q.op == "tl.pointwise" and q.attr("f") == "mul" and len(q.args) == 2:
+        x, c = q.args
+        if c.op not in ("core.const", "tl.const"):
+            x, c = c, x
+        if c.op in ("core.const", "tl.const") and float(c.attr("value")) > 0:
+            q, scale = x, float(c.attr("value"))
+    acts, ws, dn = [], [], None
+    for node, rows, feat in ((q, t, e), (k, s, e), (v, s, o)):
+        core = contract_core(node)
+        if core is None:
+            return None
+        x, y, d = core
+        w, a = (x, y) if feat in x.type.names else (y, x)
+        if w.op != "core.param" or dn not in (None, d) or set(w.type.names) != {d, feat, *heads}:
+            return None
+        if tuple(a.type.names) != (rows, d) or a.type.dim(d).start != 0:
+            return None
+        dn = d
+        acts.append(_under_renames(a))
+        ws.append(w)
+    if not (acts[0] is acts[1] is acts[2]) or tuple(acts[0].type.names) != (t, dn):
+        return None
+    return acts[0], tuple(ws), dn, scale
+
+
+def _attention_chains(carves, region, dtype: str, merge: bool = True) -> list:
     """Banded attention that the reference plan carves in two or three: a
     row-normalization carve softmax_s(where(mask, sum_e q*k, fill)) whose
     score contraction is dissolved into it (over boundary values q and k) or
@@ -254,8 +289,14 @@ def _attention_chains(carves, region, dtype: str) -> list:
         if band[0] == "band" and _band_has_empty_row(T, S, band[1], band[2]):
             continue
         srcs = [source(q, qk_carve), source(k, qk_carve), source(v, c)]
-        out.append(_AttentionChain(sc, c, drop, (q, k, v), tuple(x for x, _ in srcs), tuple(b for _, bs in srcs for b in bs),
-                                   c.root, t, s, e, o, heads, band, float(fill.attr("value"))))
+        bounds = tuple(b for _, bs in srcs for b in bs)
+        merged = None
+        if merge and all(x is not None for x, _ in srcs):  # all computed: one GEMM where they share an activation
+            merged = _merged_projection(q, k, v, t, s, e, o, heads)
+            if merged is not None:
+                bounds = (merged[0],) + merged[1]
+        out.append(_AttentionChain(sc, c, drop, (q, k, v), tuple(x for x, _ in srcs), bounds,
+                                   c.root, t, s, e, o, heads, band, float(fill.attr("value")), merged))
     return out
 
 
@@ -292,9 +333,13 @@ class Step:
 
 class PlanExecutor:
     """Runs a ModelPlan of ``region`` on the device. ``dtype`` is the element
-    type of every floating value (f32, bf16 or f16)."""
+    type of every floating value (f32, bf16 or f16). ``fuse_attention``
+    launches a softmax carve and its PV carve as one flash forward where they
+    compute banded attention (``_attention_chains``); ``merge_projections``
+    then makes q, k and v with one GEMM where they project one activation."""
 
-    def __init__(self, plan, region: Region, dtype: str = "bf16", fuse_attention: bool = True, _shared=None):
+    def __init__(self, plan, region: Region, dtype: str = "bf16", fuse_attention: bool = True,
+                 merge_projections: bool = True, _shared=None):
         if dtype not in _TORCH_DT:
             raise ValueError(f"dtype {dtype!r}: f32, bf16 or f16")
         self.region, self.dtype = region, dtype
@@ -310,7 +355,7 @@ class PlanExecutor:
         if rootless:
             raise Untranslatable(f"a multi-output residue cannot run on the device: {rootless[0].group.reason}")
         if fuse_attention:  # a softmax carve and its PV carve as one flash launch
-            chains = _attention_chains(pending, region, dtype)
+            chains = _attention_chains(pending, region, dtype, merge_projections)
             dropped = {id(d) for ch in chains for d in ch.drop}
             by_pv = {id(ch.pv): ch for ch in chains}
             pending = [by_pv.get(id(c), c) for c in pending if id(c) not in dropped]
@@ -427,6 +472,8 @@ class PlanExecutor:
         from .tl.partition import plan_model
 
         q_, k_, v_ = ch.nodes
+        if ch.merged is not None:
+            return self._attention_merged(ch)
         getters, at = [], 0
         for src in ch.sources:
             if src is None:
@@ -481,6 +528,66 @@ class PlanExecutor:
         made = "".join("b" if x is None else "m" for x in ch.sources)
         return run, (f"flash_fwd (softmax + PV carves) heads={H} t={T} s={S} e={E} od={OD} band={ch.band} "
                      f"qkv={made}")
+
+    def _attention_merged(self, ch):
+        """An attention chain whose q, k, v are projections of one activation:
+        one GEMM against the weights concatenated along n (packed once per
+        bind), q, k and v read as strided views of its output, then the flash
+        launch with q's scale."""
+        from . import kernels as K
+        from .tl.ir import TensorType
+
+        act, ws, dn, scale = ch.merged
+        t, e, o, heads = ch.t, ch.e, ch.o, ch.heads
+        T, D = act.type.dim(t).size, act.type.dim(dn).size
+        H = ws[0].type.dim(heads[0]).size if heads else 1
+        E, OD = ws[0].type.dim(e).size, ws[2].type.dim(o).size
+        widths = (H * E, H * E, H * OD)
+        NT = sum(widths)
+        b = Builder(OPS)
+        A = b.param(0, act.type)
+        Bt = b.param(1, TensorType((Dim("_qkv", 0, NT), Dim(dn, 0, D))))
+        prod = b.emit("tl.pointwise", b.emit("tl.repeat_like", A, Bt), b.emit("tl.repeat_like", Bt, A), f="mul")
+        red = b.emit("tl.reduce", prod, dims=(dn,), f="sum")
+        gemm, gsrc = self._contraction(Region(params=(A, Bt), body=(b.emit("core.yield", red),)))
+        transposed = red.type.names[0] != t
+        perms = [[w.type.names.index(h) for h in heads] + [w.type.names.index(f), w.type.names.index(dn)]
+                 for w, f in zip(ws, (e, e, o))]
+        kband = None if ch.band[0] == "none" else K.Band(ch.band[1], ch.band[2])
+        out_names, out_shape = ch.root.type.names, ch.root.type.shape
+        oplan = [out_names.index(h) for h in heads] + [out_names.index(t), out_names.index(o)]
+
+        def usable(x):
+            return x.stride(-1) == 1 and all(st % 8 == 0 for st in x.stride()[:-1]) and x.data_ptr() % 16 == 0
+
+        def run(vals):
+            torch = _torch()
+            a, wq, wk, wv = vals
+            key = ("qkv", id(wq), id(wk), id(wv))
+            bt = self._packs.get(key)
+            if bt is None:
+                bt = torch.cat([w.permute(*pm).reshape(wd, D) for w, pm, wd in zip((wq, wk, wv), perms, widths)])
+                if all(id(w) in self._static for w in (wq, wk, wv)):
+                    self._packs[key] = bt
+            y = gemm([a, bt])
+            y = y.t() if transposed else y  # (T, NT)
+            ops, at = [], 0
+            for wd, f in zip(widths, (E, E, OD)):
+                x = y[:, at:at + wd].reshape(T, H, f).permute(1, 0, 2).unsqueeze(0)  # [1, H, T, f]
+                ops.append(x if usable(x) else x.contiguous())
+                at += wd
+            out = torch.empty(out_shape, dtype=a.dtype, device=a.device)
+            ov = out.permute(*oplan)
+            ov = ov if heads else ov.unsqueeze(0)
+            direct = usable(ov)
+            res = K.flash_fwd(*ops, scale=scale, band=kband, fill=ch.fill, want_lse=False,
+                              out=ov.unsqueeze(0) if direct else None)
+            if not direct:
+                ov.copy_(res.o.view(ov.shape))
+            return (out,)
+
+        return run, (f"flash_fwd (softmax + PV carves) heads={H} t={T} s={T} e={E} od={OD} band={ch.band} "
+                     f"qkv=merged scale={scale:g} [{gsrc}]")
 
     def _flash_joint(self, k):
         """The flash joint claimed whole: the forward with its artifacts and

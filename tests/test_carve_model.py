@@ -140,5 +140,10 @@ def test_the_executor_finds_the_attention_chains_of_each_carve_form():
         assert len(ch.drop) == drop and (ch.t, ch.s, ch.e, ch.o, ch.heads) == ("t", "s", "hk", "hk", ("nh",))
         assert ch.band == ("band", None, 0) and ch.fill <= -1e6
         assert [None if x is None else "m" for x in ch.sources] == made
-        assert len(ch.bounds) == (3 if made[0] is None else sum(len(x[1]) for x in ch.sources))
+        if made[0] is None:
+            assert len(ch.bounds) == 3 and ch.merged is None
+        else:  # one activation projected by three weight params, q scaled by 1/sqrt(64)
+            act, ws, dn, scale = ch.merged
+            assert act.type.names == ("t", "d") and dn == "d" and scale == 0.125
+            assert all(w.op == "core.param" for w in ws) and ch.bounds == (act,) + ws
     assert chains(128, 32, "bf16") == [] and len(chains(128, 32, "f32")) == 1  # 16-bit flash wants e in {64, 128}

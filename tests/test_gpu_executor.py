@@ -18,13 +18,13 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-def _run(cfg, dtype, seed=7, fuse=True):
+def _run(cfg, dtype, seed=7, fuse=True, merge=True):
     from pdum_dsl_amd.executor import PlanExecutor
     from pdum_dsl_amd.tl import zoo
     from pdum_dsl_amd.tl.partition import plan_model
 
     m = zoo.gpt2(cfg, seed=seed)
-    ex = PlanExecutor(plan_model(m.region), m.region, dtype, fuse_attention=fuse)
+    ex = PlanExecutor(plan_model(m.region), m.region, dtype, fuse_attention=fuse, merge_projections=merge)
     ex.bind(m.values())
     out = ex.run()
     torch.cuda.synchronize()
@@ -60,21 +60,25 @@ def test_a_sized_gpt2_matches_the_numpy_model(dtype, tol, fuse):
     assert err <= tol * np.abs(want).max(), f"{dtype}: max err {err} vs scale {np.abs(want).max()}"
 
 
-@pytest.mark.parametrize("t,form", [(64, "scores carved"), (128, "scores dissolved"), (256, "projections dissolved")])
+@pytest.mark.parametrize("t,form", [(64, "scores carved"), (128, "scores dissolved"), (256, "projections dissolved"),
+                                    (256, "projections merged")])
 @pytest.mark.parametrize("dtype,tol", [("f32", 1e-4), ("bf16", 3e-2)])
 def test_attention_chains_in_each_carve_form(t, form, dtype, tol):
     """The softmax + PV carves launched as one flash forward in each form the
     traffic gate gives them: the scores a carve of their own (t=64), the
     scores dissolved into the softmax carve (t=128), and the q/k/v
-    projections dissolved too, so the launch materializes them first
-    (t=256). Against the numpy model, and against the unfused plan."""
+    projections dissolved too (t=256), so the launch makes them first: by
+    three nested plans, or by one GEMM over the concatenated weights with the
+    scale moved into the flash launch. Against the numpy model, and against
+    the unfused plan."""
     from pdum_dsl_amd.tl import zoo
 
     cfg = zoo.GPT2Config(t=t, d=128, nh=2, hk=64, m=512, layers=1, v=64)
-    got, want, ex = _run(cfg, dtype, seed=3)
+    got, want, ex = _run(cfg, dtype, seed=3, merge=form == "projections merged")
     chains = [st for st in ex.steps if st.kind == "flash-chain"]
     assert len(chains) == 1
-    made = {"scores carved": "qkv=bbb", "scores dissolved": "qkv=bbb", "projections dissolved": "qkv=mmm"}[form]
+    made = {"scores carved": "qkv=bbb", "scores dissolved": "qkv=bbb", "projections dissolved": "qkv=mmm",
+            "projections merged": "qkv=merged scale=0.125"}[form]
     assert made in chains[0].source
     n_unfused = len(_run(cfg, dtype, seed=3, fuse=False)[2].steps)
     assert len(ex.steps) == n_unfused - (2 if form == "scores carved" else 1)
