@@ -143,6 +143,23 @@ int pdh_flash_fwd(const void* q, const void* k, const void* v, void* o, float* m
                   float* lse_out, const pdh_attn_geom* geom, int dtype, float scale, float fill,
                   int mask_kind, int64_t band_lo, int64_t band_hi, int prune, void* stream);
 
+/* The same forward split over the key axis, for grids too small to fill the
+ * chip (few instances x query blocks, long rows: a batch-1 prefill). Each
+ * query block's key-tile range is cut into `nsplit` runs swept by separate
+ * workgroups, which store partial (o, running max, denominator) to `ws`; a
+ * second kernel merges them with the associative online-softmax combine
+ * (zoo/attention.py:40-46) and stores o and the optional m / den / lse as
+ * pdh_flash_fwd does. The result equals pdh_flash_fwd's up to fp32 rounding
+ * order (bf16 / f16 only; PDH_F32 runs unsplit). nsplit in [1, 64]; ws must
+ * be 16-byte aligned and hold pdh_flash_fwd_workspace(geom, nsplit) bytes
+ * (0 for nsplit <= 1). No counterpart in the reference: a launch shape of
+ * the flash template's run (fusion.py:542-615). */
+size_t pdh_flash_fwd_workspace(const pdh_attn_geom* geom, int nsplit);
+int pdh_flash_fwd_split(const void* q, const void* k, const void* v, void* o, float* m_out, float* den_out,
+                        float* lse_out, const pdh_attn_geom* geom, int dtype, float scale, float fill,
+                        int mask_kind, int64_t band_lo, int64_t band_hi, int prune, int nsplit, void* ws,
+                        size_t ws_bytes, void* stream);
+
 /* Flash-attention backward (the closed form of the flash joint's gradients,
  * autodiff.py:102-122 over zoo/tiles.py:238-252's naive twin):
  *   P = exp(scale*q k^T - lse), dV = P^T dO, dP = dO v^T, delta = rowsum(dO * o),

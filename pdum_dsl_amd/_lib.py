@@ -30,6 +30,8 @@ EXPORTS = (
     "pdh_layernorm_dt",
     "pdh_take_rows",
     "pdh_flash_fwd",
+    "pdh_flash_fwd_workspace",
+    "pdh_flash_fwd_split",
     "pdh_flash_bwd",
     "pdh_attn_decode_workspace",
     "pdh_attn_decode",
@@ -108,6 +110,9 @@ def _declare(lib) -> None:
         "pdh_layernorm_dt": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, f32, i32, vp]),
         "pdh_take_rows": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, vp]),
         "pdh_flash_fwd": (i32, [vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, i32, vp]),
+        "pdh_flash_fwd_workspace": (C.c_size_t, [gp, i32]),
+        "pdh_flash_fwd_split": (i32, [vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, i32, i32, vp,
+                                      C.c_size_t, vp]),
         "pdh_flash_bwd": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, vp]),
         "pdh_attn_decode_workspace": (C.c_size_t, [gp, i32]),
         "pdh_attn_decode": (i32, [vp, vp, vp, vp, vp, gp, i32, f32, i32, vp, C.c_size_t, vp]),

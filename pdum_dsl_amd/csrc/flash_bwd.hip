@@ -285,8 +285,9 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
         const int rem = static_cast<int>(S_ - kl0 < 1024 ? S_ - kl0 : 1024);
         const int64_t dl0 = kl0 - qrow;
         auto clampi = [](int64_t x) { return static_cast<int>(x < -4096 ? -4096 : (x > 4096 ? 4096 : x)); };
-        const int lo = a.masked ? clampi(a.band_lo - dl0) : -4096;
-        const int hi = a.masked ? clampi(a.band_hi - dl0) : 4096;
+        // an unbounded end (INT64_MIN / INT64_MAX) must not enter the subtraction: it would wrap
+        const int lo = (a.masked && a.band_lo > INT64_MIN / 4) ? clampi(a.band_lo - dl0) : -4096;
+        const int hi = (a.masked && a.band_hi < INT64_MAX / 4) ? clampi(a.band_hi - dl0) : 4096;
         const bool rowok = qrow < T_;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {

@@ -55,6 +55,12 @@ struct FwdArgs {
   int prune;    // skip dead tiles
   int nqb;      // query blocks per instance
   int xcd_remap;
+  // split over the key axis (nsplit > 1): workgroup (block, split c) sweeps key
+  // tiles [lo + c * split_tiles, ...) of its block's range and stores partial
+  // (o referred to mused, mused, mtrue, den) to ws; flash_fwd_combine merges
+  int nsplit, split_tiles;
+  float* ws;      // [nsplit][plane][D] partial o, then [3][nsplit][plane] mused, mtrue, den
+  int64_t plane;  // instances * t: rows per split
 };
 
 template <int D>
@@ -91,6 +97,11 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
 
   // workgroup -> (instance, query block); heavy (late) query blocks first
   int bid = blockIdx.x;
+  int split = 0;
+  if (a.nsplit > 1) {  // the splits of one query block are adjacent workgroups
+    split = bid % a.nsplit;
+    bid /= a.nsplit;
+  }
   if (a.xcd_remap) {
     const int per = gridDim.x >> 3;
     bid = (bid & 7) * per + (bid >> 3);
@@ -153,6 +164,15 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
       }
     }
     if (kf_lo > kf_hi) kf_lo = kf_hi = kt_hi;
+  }
+  if (a.nsplit > 1) {  // this split's share of the range; the run boundaries clamp into it
+    const int s_lo = kt_lo + split * a.split_tiles;
+    const int lo2 = s_lo < kt_hi ? s_lo : kt_hi;
+    const int hi2 = s_lo + a.split_tiles < kt_hi ? s_lo + a.split_tiles : kt_hi;
+    kf_lo = kf_lo < lo2 ? lo2 : (kf_lo > hi2 ? hi2 : kf_lo);
+    kf_hi = kf_hi < lo2 ? lo2 : (kf_hi > hi2 ? hi2 : kf_hi);
+    kt_lo = lo2;
+    kt_hi = hi2;
   }
 
   // ---- staging: each wave copies 1 KB blocks of the next K and V tiles
@@ -241,8 +261,9 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
       const int rem = static_cast<int>(S_ - kl < 1024 ? S_ - kl : 1024);
       const int64_t dl = kl - qrow;
       auto clampi = [](int64_t x) { return static_cast<int>(x < -4096 ? -4096 : (x > 4096 ? 4096 : x)); };
-      const int lo = a.masked ? clampi(a.band_lo - dl) : -4096;
-      const int hi = a.masked ? clampi(a.band_hi - dl) : 4096;
+      // an unbounded end (INT64_MIN / INT64_MAX) must not enter the subtraction: it would wrap
+      const int lo = (a.masked && a.band_lo > INT64_MIN / 4) ? clampi(a.band_lo - dl) : -4096;
+      const int hi = (a.masked && a.band_hi < INT64_MAX / 4) ? clampi(a.band_hi - dl) : 4096;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int c = (i >> 3) * 16 + (i & 7);
@@ -313,6 +334,25 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
 
   // epilogue: combine the two lane halves' partial denominators, normalize, store
   const float den = lsum + __shfl_xor(lsum, 32, 64);
+  if (a.nsplit > 1) {  // the partial state, unnormalized, for flash_fwd_combine
+    if (qrow < T_) {
+      const int64_t srow = split * a.plane + inst * T_ + qrow;
+      float* wo = a.ws + srow * D + 4 * g;
+#pragma unroll
+      for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4)
+          *reinterpret_cast<f32x4*>(wo + db * 32 + a4 * 8) =
+              f32x4{oacc[db][4 * a4 + 0], oacc[db][4 * a4 + 1], oacc[db][4 * a4 + 2], oacc[db][4 * a4 + 3]};
+      if (g == 0) {
+        float* st = a.ws + a.nsplit * a.plane * D;
+        st[srow] = mused;
+        st[a.nsplit * a.plane + srow] = mtrue;
+        st[2 * a.nsplit * a.plane + srow] = den;
+      }
+    }
+    return;
+  }
   if (qrow < T_) {
     const float inv = den > 0.f ? 1.0f / den : 0.f;
     uint16_t* obase = op + static_cast<int64_t>(qw0) * a.o_st;  // wave-uniform
@@ -428,6 +468,48 @@ __global__ __launch_bounds__(256) void flash_fwd_generic_f32(GenArgs a, int64_t 
   }
 }
 
+// The splits of a key-split forward merged per row (the associative
+// online-softmax combine of zoo/attention.py:40-46): with M the largest of the
+// splits' mused, o = sum_c o_c 2^((mused_c - M) c2) / den and den = sum_c den_c
+// 2^((mused_c - M) c2); the artifacts as the unsplit kernel stores them. One
+// thread per (row, 4 features).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void flash_fwd_combine(FwdArgs a) {
+  constexpr int TPR = D / 4;
+  const int64_t gt = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t row = gt / TPR;
+  const int f4 = static_cast<int>(gt % TPR);
+  if (row >= a.plane) return;
+  const int64_t P = a.plane, NS = a.nsplit;
+  const float* mu = a.ws + NS * P * D;
+  const float* mt = mu + NS * P;
+  const float* dn = mt + NS * P;
+  float M = -kInf, MT = -kInf;
+  for (int c = 0; c < a.nsplit; ++c) {
+    M = fmaxf(M, mu[c * P + row]);
+    MT = fmaxf(MT, mt[c * P + row]);
+  }
+  float den = 0.f;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < a.nsplit; ++c) {
+    const float m_c = mu[c * P + row];
+    const float w = m_c > -kInf ? fast_exp2((m_c - M) * a.c2) : 0.f;  // an empty split adds nothing
+    den += dn[c * P + row] * w;
+    const f32x4 oc = *reinterpret_cast<const f32x4*>(a.ws + (c * P + row) * D + 4 * f4);
+    acc += oc * w;
+  }
+  const float inv = den > 0.f ? 1.0f / den : 0.f;
+  const int64_t inst = row / a.t, tq = row % a.t;
+  const int64_t b = inst / a.heads_q, hq = inst % a.heads_q;
+  uint16_t* orow = static_cast<uint16_t*>(a.o) + b * a.o_sb + hq * a.o_sh + tq * a.o_st + 4 * f4;
+  *reinterpret_cast<u32x2*>(orow) = u32x2{pack2<T>(acc[0] * inv, acc[1] * inv), pack2<T>(acc[2] * inv, acc[3] * inv)};
+  if (f4 == 0) {
+    if (a.m_out) a.m_out[row] = MT * a.scale;
+    if (a.den_out) a.den_out[row] = den * fast_exp2((M - MT) * a.c2);
+    if (a.lse_out) a.lse_out[row] = M * a.scale + __logf(den);
+  }
+}
+
 bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
   // row t has a live key iff max(0, t + lo) <= min(S - 1, t + hi); the
   // tightest rows are t = 0 (needs hi >= 0) and t = T - 1 (needs T-1+lo <= S-1)
@@ -444,6 +526,19 @@ int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
   const int64_t nblk = ninst * a.nqb;
   PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: grid too large (%lld workgroups)", (long long)nblk);
   FwdArgs aa = a;
+  if (a.nsplit > 1) {
+    const int64_t ntiles = (a.s + C::BN - 1) / C::BN;
+    aa.split_tiles = static_cast<int>((ntiles + a.nsplit - 1) / a.nsplit);
+    aa.xcd_remap = 0;
+    PDH_REQUIRE(nblk * a.nsplit <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd_split: grid too large");
+    flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk * a.nsplit)), C::THREADS, C::LDS, st>>>(aa);
+    int rc = check_launch("pdh_flash_fwd_split");
+    if (rc) return rc;
+    const int64_t nthr = a.plane * (D / 4);
+    PDH_REQUIRE((nthr + 255) / 256 <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd_split: too many rows");
+    flash_fwd_combine<T, D><<<dim3(static_cast<unsigned>((nthr + 255) / 256)), 256, 0, st>>>(aa);
+    return check_launch("pdh_flash_fwd_split (combine)");
+  }
   aa.xcd_remap = (nblk % 8 == 0) ? 1 : 0;
   flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk)), C::THREADS, C::LDS, st>>>(aa);
   return check_launch("pdh_flash_fwd");
@@ -454,9 +549,12 @@ int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
 
 using namespace pdh;
 
-extern "C" int pdh_flash_fwd(const void* q, const void* k, const void* v, void* o, float* m_out, float* den_out,
-                             float* lse_out, const pdh_attn_geom* gm, int dtype, float scale, float fill,
-                             int mask_kind, int64_t band_lo, int64_t band_hi, int prune, void* stream) {
+namespace {
+
+int flash_fwd_impl(const void* q, const void* k, const void* v, void* o, float* m_out, float* den_out,
+                   float* lse_out, const pdh_attn_geom* gm, int dtype, float scale, float fill, int mask_kind,
+                   int64_t band_lo, int64_t band_hi, int prune, int nsplit, void* ws, size_t ws_bytes,
+                   void* stream) {
   PDH_REQUIRE(gm != nullptr, PDH_EINVAL, "pdh_flash_fwd: null geometry");
   const pdh_attn_geom G = *gm;
   PDH_REQUIRE(G.batch >= 0 && G.heads_q >= 1 && G.heads_kv >= 1 && G.t >= 0 && G.s >= 1 && G.e >= 1 && G.od >= 1,
@@ -507,8 +605,41 @@ extern "C" int pdh_flash_fwd(const void* q, const void* k, const void* v, void* 
             G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st, G.o_sb, G.o_sh, G.o_st,
             scale, scale * kLog2e, fill / scale, masked, band_lo, band_hi, prune_ok,
             static_cast<int>((G.t + FwdCfg<128>::BM - 1) / FwdCfg<128>::BM), 0};
+  a.nsplit = 1;
+  if (nsplit > 1) {
+    const size_t need = pdh_flash_fwd_workspace(gm, nsplit);
+    PDH_REQUIRE(ws != nullptr && ws_bytes >= need && aligned16(ws), PDH_EINVAL,
+                "pdh_flash_fwd_split: ws must be 16-byte aligned and hold %zu bytes (got %zu)", need, ws_bytes);
+    a.nsplit = nsplit;
+    a.ws = static_cast<float*>(ws);
+    a.plane = ninst * G.t;
+  }
   if (dtype == PDH_BF16) {
     return G.e == 128 ? launch_mfma<__hip_bfloat16, 128>(a, ninst, st) : launch_mfma<__hip_bfloat16, 64>(a, ninst, st);
   }
   return G.e == 128 ? launch_mfma<_Float16, 128>(a, ninst, st) : launch_mfma<_Float16, 64>(a, ninst, st);
+}
+
+}  // namespace
+
+extern "C" size_t pdh_flash_fwd_workspace(const pdh_attn_geom* gm, int nsplit) {
+  if (gm == nullptr || nsplit <= 1) return 0;
+  const int64_t rows = gm->batch * gm->heads_q * gm->t;
+  return static_cast<size_t>(nsplit) * static_cast<size_t>(rows) * static_cast<size_t>(gm->od + 3) * sizeof(float);
+}
+
+extern "C" int pdh_flash_fwd(const void* q, const void* k, const void* v, void* o, float* m_out, float* den_out,
+                             float* lse_out, const pdh_attn_geom* gm, int dtype, float scale, float fill,
+                             int mask_kind, int64_t band_lo, int64_t band_hi, int prune, void* stream) {
+  return flash_fwd_impl(q, k, v, o, m_out, den_out, lse_out, gm, dtype, scale, fill, mask_kind, band_lo, band_hi,
+                        prune, 1, nullptr, 0, stream);
+}
+
+extern "C" int pdh_flash_fwd_split(const void* q, const void* k, const void* v, void* o, float* m_out,
+                                   float* den_out, float* lse_out, const pdh_attn_geom* gm, int dtype, float scale,
+                                   float fill, int mask_kind, int64_t band_lo, int64_t band_hi, int prune,
+                                   int nsplit, void* ws, size_t ws_bytes, void* stream) {
+  PDH_REQUIRE(nsplit >= 1 && nsplit <= 64, PDH_EINVAL, "pdh_flash_fwd_split: nsplit %d outside [1, 64]", nsplit);
+  return flash_fwd_impl(q, k, v, o, m_out, den_out, lse_out, gm, dtype, scale, fill, mask_kind, band_lo, band_hi,
+                        prune, nsplit, ws, ws_bytes, stream);
 }

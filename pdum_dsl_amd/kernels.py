@@ -204,12 +204,15 @@ def flash_fwd(
     want_lse: bool = True,
     want_artifacts: bool = False,
     out: torch.Tensor | None = None,
+    nsplit: int | None = None,
 ) -> FlashOut:
     """Flash-attention forward over [B, H, T, E] q and [B, Hkv, S, E] k / v.
 
     ``band`` None means every key is live; masked scores take ``fill``.
     Returns the output plus lse and, with ``want_artifacts``, the reference's
-    (m, den) artifacts ([B, H, T] fp32)."""
+    (m, den) artifacts ([B, H, T] fp32). ``nsplit`` > 1 splits each query
+    block's keys over that many workgroups (pdh_flash_fwd_split); None picks
+    it (``pick_fwd_splits``): 1 unless the grid is too small to fill the chip."""
     _require_cuda(q, k, v)
     if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DT:
         raise ValueError(f"q/k/v must share one dtype of f32/bf16/f16 (got {q.dtype}, {k.dtype}, {v.dtype})")
@@ -222,12 +225,38 @@ def flash_fwd(
     den = torch.empty((B, H, T), **st) if want_artifacts else None
     sc = 1.0 / math.sqrt(q.shape[3]) if scale is None else float(scale)
     kind, (lo, hi) = (PDH_MASK_NONE, (0, 0)) if band is None else (PDH_MASK_BAND, band.c_args())
+    if nsplit is None:
+        nsplit = pick_fwd_splits(B * H, T, k.shape[2]) if q.dtype != torch.float32 else 1
+    if nsplit > 1 and q.dtype != torch.float32:
+        need = _lib.lib().pdh_flash_fwd_workspace(C.byref(g), int(nsplit))
+        ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=q.device)
+        _lib.call(
+            "pdh_flash_fwd_split",
+            _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(m), _ptr(den), _ptr(lse), C.byref(g), _DT[q.dtype],
+            C.c_float(sc), C.c_float(fill), kind, lo, hi, int(bool(prune)), int(nsplit), _ptr(ws),
+            C.c_size_t(ws.numel() * 4), C.c_void_p(_stream()),
+        )
+        return FlashOut(o, lse, m, den)
     _lib.call(
         "pdh_flash_fwd",
         _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(m), _ptr(den), _ptr(lse), C.byref(g), _DT[q.dtype],
         C.c_float(sc), C.c_float(fill), kind, lo, hi, int(bool(prune)), C.c_void_p(_stream()),
     )
     return FlashOut(o, lse, m, den)
+
+
+def pick_fwd_splits(ninst: int, t: int, s: int, cus: int | None = None) -> int:
+    """Key splits for the 16-bit forward: 1 when the instances x 128-row query
+    blocks give every CU two workgroups, or a row has under 16 key tiles
+    (512 keys); otherwise runs of at least 8 key tiles (256 keys), up to
+    three workgroups per CU in all."""
+    if cus is None:
+        cus = _lib.lib().pdh_device_cus() or 256
+    blocks = ninst * ((t + 127) // 128)
+    ntiles = (s + 31) // 32
+    if blocks == 0 or blocks >= 2 * cus or ntiles < 16:
+        return 1
+    return int(max(1, min(ntiles // 8, (3 * cus) // blocks, 64)))
 
 
 def flash_bwd(

@@ -45,3 +45,17 @@ def test_validation_errors_need_no_device():
     rc = lib.pdh_flash_fwd(None, None, None, None, None, None, None, C.byref(g), 1, 1.0, -1e9, 0, 0, 0, 1, None)
     assert rc == _lib.PDH_EINVAL and "multiple of heads_kv" in _lib.last_error()
     assert lib.pdh_attn_decode_workspace(C.byref(g), 4) == 1 * 3 * 8 * 4 * (2 + 64) * 4
+
+
+def test_the_forward_split_picker():
+    """Key splits only for grids that cannot fill the chip: gpt2's 12 heads x
+    1024 rows take 4 runs of 8 key tiles; the C3 headline (8192 query blocks)
+    and short rows take none."""
+    pytest.importorskip("torch")
+    from pdum_dsl_amd.kernels import pick_fwd_splits
+
+    assert pick_fwd_splits(12, 1024, 1024, cus=256) == 4
+    assert pick_fwd_splits(8 * 32, 4096, 4096, cus=256) == 1
+    assert pick_fwd_splits(1, 4096, 4096, cus=256) == 16
+    assert pick_fwd_splits(4, 256, 256, cus=256) == 1  # 8 key tiles a row
+    assert pick_fwd_splits(0, 0, 1, cus=256) == 1

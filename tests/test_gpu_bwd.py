@@ -29,6 +29,8 @@ def _host(t):
         (1, 2, 160, 128, None),
         (1, 1, 130, 64, (None, -1)),  # row 0 fully masked: uniform softmax, no pruning
         (1, 1, 300, 64, (-63, 0)),  # sliding window
+        (1, 1, 256, 64, (None, 5)),  # unbounded below, keys past the diagonal live
+        (1, 1, 256, 128, (-40, None)),  # unbounded above
     ],
 )
 def test_flash_bwd_matches_oracle(dtype, B, H, T, D, band):

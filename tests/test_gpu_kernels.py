@@ -173,6 +173,20 @@ def test_a_fully_masked_row_keeps_uniform_softmax(K, dtype):
     np.testing.assert_allclose(_host(res.o)[0, 0, 0], _host(v)[0, 0].mean(axis=0), rtol=2e-2, atol=2e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("band", [(None, 5), (None, 100), (3, None), (-40, None), (None, 1500)])
+def test_half_open_bands(K, dtype, band):
+    """Bands with one unbounded end: the masked tiles' per-key limits are
+    computed from the bounded end only (an unbounded end entering the
+    subtraction would wrap and mask every key of those tiles)."""
+    rng = np.random.default_rng(41)
+    D = 64 if dtype != torch.float32 else 40
+    q, k, v = _qkv(rng, 1, 2, 2, 200, 600, D, D, dtype)
+    res = K.flash_fwd(q, k, v, scale=0.125, band=K.Band(*band), want_artifacts=True, nsplit=1)
+    torch.cuda.synchronize()
+    _check_fwd(res, q, k, v, 0.125, band, lowp=dtype != torch.float32)
+
+
 def test_sliding_window_band(K):
     rng = np.random.default_rng(21)
     q, k, v = _qkv(rng, 1, 2, 2, 300, 300, 128, 128, torch.bfloat16)
@@ -180,6 +194,55 @@ def test_sliding_window_band(K):
     res = K.flash_fwd(q, k, v, band=K.Band(*band), want_artifacts=True)
     torch.cuda.synchronize()
     _check_fwd(res, q, k, v, 1 / np.sqrt(128), band, lowp=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,T,S,D,band,nsplit",
+    [
+        (1, 12, 12, 1024, 1024, 64, (None, 0), 4),  # gpt2's attention, the split the picker chooses
+        (2, 3, 3, 700, 900, 128, None, 3),  # ragged rows and keys, every key live
+        (1, 4, 2, 1000, 1000, 64, (-200, 0), 5),  # a window (most splits of a block empty), GQA
+        (1, 2, 2, 600, 600, 128, (None, -1), 2),  # strict causal: row 0 fully masked, no pruning
+        (1, 1, 1, 64, 2048, 128, (None, 1500), 7),  # one query block, splits ragged at the key tail
+    ],
+)
+def test_the_key_split_forward_matches_the_oracle_and_the_unsplit_sweep(K, dtype, B, Hq, Hkv, T, S, D, band,
+                                                                         nsplit):
+    """pdh_flash_fwd_split: the splits' partial (o, max, den) merged by the
+    online-softmax combine. Against the float64 closed form (bf16 / f16
+    tolerance), and against the unsplit sweep: the m artifact is a max, so
+    bit-equal; lse and den within fp32 rounding; o within two 16-bit ulps."""
+    rng = np.random.default_rng(T + S + D + nsplit)
+    q, k, v = _qkv(rng, B, Hq, Hkv, T, S, D, D, dtype)
+    scale = 1.0 / np.sqrt(D)
+    kb = K.Band(*band) if band else None
+    one = K.flash_fwd(q, k, v, scale=scale, band=kb, want_artifacts=True, nsplit=1)
+    res = K.flash_fwd(q, k, v, scale=scale, band=kb, want_artifacts=True, nsplit=nsplit)
+    torch.cuda.synchronize()
+    _check_fwd(res, q, k, v, scale, band, lowp=True)
+    assert torch.equal(one.m, res.m)
+    assert (one.lse - res.lse).abs().max().item() < 1e-4
+    assert ((one.den - res.den).abs() / one.den.abs()).max().item() < 1e-4
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    assert (one.o.float() - res.o.float()).abs().max().item() <= 2 * ulp * max(1.0, one.o.float().abs().max().item())
+
+
+def test_the_key_split_refuses_a_short_workspace(K):
+    import ctypes as C
+
+    from pdum_dsl_amd import _lib as L
+
+    q, k, v = _qkv(np.random.default_rng(1), 1, 2, 2, 256, 1024, 64, 64, torch.bfloat16)
+    o = torch.empty_like(q)
+    g = K._geom(q, k, v, o)
+    need = L.lib().pdh_flash_fwd_workspace(C.byref(g), 4)
+    assert need == 4 * 2 * 256 * (64 + 3) * 4
+    ws = torch.empty(need // 4, dtype=torch.float32, device="cuda")
+    with pytest.raises(Exception, match="ws must"):
+        L.call("pdh_flash_fwd_split", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), None, None, None,
+               C.byref(g), 1, C.c_float(0.125), C.c_float(-1e9), 0, 0, 0, 1, 4, ws.data_ptr(), C.c_size_t(need - 16),
+               None)
 
 
 # ------------------------------------------------------------------- decode
