@@ -38,7 +38,15 @@ _PW = {
     "floor": torch.floor, "eq": torch.eq, "ne": torch.ne, "le": torch.le, "lt": torch.lt, "ge": torch.ge,
     "gt": torch.gt, "stop_gradient": lambda x: x,
     "zoo.gelu": lambda x: 0.5 * x * (1 + torch.tanh(0.7978845608028654 * (x + 0.044715 * x * x * x))),
+    # the derived partial marker zoo.gelu.d0 (autodiff.py:303-309): d/dx of the body above
+    "zoo.gelu.d0": lambda x: _gelu_d0(x),
 }
+
+
+def _gelu_d0(x):
+    c = 0.7978845608028654
+    t = torch.tanh(c * (x + 0.044715 * x * x * x))
+    return 0.5 * (1 + t) + 0.5 * x * (1 - t * t) * c * (1 + 0.134145 * x * x)
 
 
 class V:

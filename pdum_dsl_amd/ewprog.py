@@ -217,6 +217,23 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, al
                       ("MUL", r, c, r, 0, 0.0)]
             free.append(c)
             release(src)
+        elif x.op == "tl.pointwise" and x.attr("f") == "zoo.gelu.d0":
+            # the marker's partial: 0.5 ((1 + t) + x (1 - t^2) c (1 + 3 * 0.044715 x^2)), t = tanh(u)
+            src = skip_view(x.args[0])
+            xr = reg[id(src)]
+            r, c, s_, w = alloc(), alloc(), alloc(), alloc()
+            insns += [("CONST", c, 0, 0, 0, 0.044715), ("MUL", r, c, xr, 0, 0.0), ("MUL", r, r, xr, 0, 0.0),
+                      ("MUL", r, r, xr, 0, 0.0), ("ADD", r, xr, r, 0, 0.0), ("CONST", c, 0, 0, 0, _GELU_C),
+                      ("MUL", r, c, r, 0, 0.0), ("TANH", r, r, 0, 0, 0.0),  # r = t
+                      ("MUL", s_, xr, xr, 0, 0.0), ("CONST", c, 0, 0, 0, 0.134145), ("MUL", s_, c, s_, 0, 0.0),
+                      ("CONST", c, 0, 0, 0, 1.0), ("ADD", s_, s_, c, 0, 0.0), ("CONST", w, 0, 0, 0, _GELU_C),
+                      ("MUL", s_, w, s_, 0, 0.0),  # s = c (1 + 3 a x^2)
+                      ("MUL", w, r, r, 0, 0.0), ("SUB", w, c, w, 0, 0.0), ("MUL", s_, s_, w, 0, 0.0),
+                      ("MUL", s_, s_, xr, 0, 0.0),  # s = x (1 - t^2) c (1 + 3 a x^2)
+                      ("ADD", r, r, c, 0, 0.0), ("ADD", r, r, s_, 0, 0.0), ("CONST", c, 0, 0, 0, 0.5),
+                      ("MUL", r, c, r, 0, 0.0)]
+            free.extend((c, s_, w))
+            release(src)
         elif x.op == "tl.pointwise":
             f = x.attr("f")
             srcs = [skip_view(a) for a in x.args]

@@ -227,6 +227,8 @@ def _pointwise_rule(n, c, contribute, pw, const):
         contribute(A[0], pw("div", c, pw("mul", n, const(2.0))))
     elif f == "tanh":
         contribute(A[0], pw("mul", c, pw("sub", const(1.0), pw("mul", n, n))))
+    elif f == "zoo.gelu":  # a composite marker: its derived partial marker f.d0 (autodiff.py:303-309)
+        contribute(A[0], pw("mul", c, pw("zoo.gelu.d0", A[0])))
     elif f == "sin":
         contribute(A[0], pw("mul", c, pw("cos", A[0])))
     elif f == "cos":

@@ -27,7 +27,7 @@ from .ir import F64, BOOL, Builder, Dim, OpDef, Region, Scalar, TensorType, Tupl
 
 MARKERS = (
     "add sub mul div neg exp log maximum minimum tanh sqrt sin cos abs floor "
-    "where eq ne le lt ge gt stop_gradient zoo.gelu"
+    "where eq ne le lt ge gt stop_gradient zoo.gelu zoo.gelu.d0"
 ).split()
 REDUCERS = ("sum", "max", "min", "prod", "mean")
 

@@ -31,7 +31,19 @@ _PW = {
     "gt": np.greater, "stop_gradient": np.positive,
     # the composite marker zoo_common.py:20 registers: 0.5 x (1 + tanh(c (x + 0.044715 x^3)))
     "zoo.gelu": lambda x: 0.5 * x * (1 + np.tanh(0.7978845608028654 * (x + 0.044715 * x * x * x))),
+    # its partial, the derived marker f.d0 (autodiff.py:303-309 derives it from the body)
+    "zoo.gelu.d0": lambda x: _gelu_d0(np, x),
 }
+
+
+def _gelu_d0(lib, x):
+    """d/dx of 0.5 x (1 + tanh(u)), u = c (x + 0.044715 x^3):
+    0.5 (1 + tanh u) + 0.5 x (1 - tanh^2 u) c (1 + 3 * 0.044715 x^2)."""
+    c = 0.7978845608028654
+    t = lib.tanh(c * (x + 0.044715 * x * x * x))
+    return 0.5 * (1 + t) + 0.5 * x * (1 - t * t) * c * (1 + 0.134145 * x * x)
+
+
 _RED = {"sum": (np.add, 0.0), "prod": (np.multiply, 1.0), "max": (np.maximum, None), "min": (np.minimum, None)}
 
 

@@ -149,3 +149,39 @@ def test_plan_model_of_a_single_template_region_is_its_plan_region():
         mp = plan_model(subj.region)
         assert [c.group.template for c in mp.carves] == [tmpl]
         assert mp.coverage() == 1.0
+
+
+def test_the_gelu_marker_differentiates_through_its_derived_partial():
+    """grad of zoo.gelu (the composite marker, zoo_common.py:20) emits the
+    derived partial marker zoo.gelu.d0, as autodiff.py:303-309 derives f.d{i}.
+    Pinned by torch's own tanh-approximate gelu and its autograd (a separate
+    implementation), on the planner's interpreter, the float64 oracle and the
+    lowered elementwise program."""
+    from pdum_dsl_amd import ewprog
+    from pdum_dsl_amd.tl.dialect import OPS
+    from pdum_dsl_amd.tl.ir import Builder, Dim, Region, TensorType
+    from tests.test_contraction_mapchain import emulate
+
+    b = Builder(OPS)
+    x = b.param(0, TensorType((Dim("i", 0, 9), Dim("j", 0, 11))))
+    y = b.emit("tl.pointwise", x, f="zoo.gelu")
+    region = Region(params=(x,), body=(b.emit("core.yield", y),))
+    names = region_names(region, ("x",), ("y",))
+    rg = grad(region, "y", seed="dy", names=names)
+    rng = np.random.default_rng(5)
+    xv, dy = rng.standard_normal((9, 11)) * 3, rng.standard_normal((9, 11))
+    xt = torch.tensor(xv, requires_grad=True)
+    torch.nn.functional.gelu(xt, approximate="tanh").backward(torch.tensor(dy))
+    res = interp.run_region(rg.region, [interp.field(xv, ("i", "j")), interp.field(dy, ("i", "j"))])
+    np.testing.assert_allclose(res[1].to_numpy(("i", "j")), xt.grad.numpy(), rtol=1e-12, atol=1e-14)
+    got = rev.evaluate(rg.region, [rev.value(xv, x.type), rev.value(dy, rg.region.params[1].type)])
+    np.testing.assert_allclose(got[1].numpy(), xt.grad.numpy(), rtol=1e-12, atol=1e-14)
+    from pdum_dsl_amd.tl.ir import walk
+
+    assert any(n.op == "tl.pointwise" and n.attr("f") == "zoo.gelu.d0" for n in walk(rg.region))
+    bb = Builder(OPS)
+    xp = bb.param(0, x.type)
+    dn = bb.emit("tl.pointwise", xp, f="zoo.gelu.d0")
+    low = ewprog.lower(dn, dn.type.dims, {id(xp): xp})
+    want = xt.grad.numpy() / dy
+    np.testing.assert_allclose(emulate(low, [xv]), want, rtol=1e-9, atol=1e-12)
