@@ -134,11 +134,17 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
         return acc
 
     order = [n for n in _ancestors_of(tnode)]
+    # only nodes with a wrt param among their ancestors carry a cotangent anyone reads
+    wanted = {id(by_name[nm]) for nm in wrt}
+    live: set = set()
+    for n in order:  # operands before users
+        if id(n) in wanted or any(id(a) in live for a in n.args):
+            live.add(id(n))
     final: dict[int, Node] = {}
     for n in reversed(order):
         c = total(n)
         final[id(n)] = c
-        if c is None or n.op == "core.param":
+        if c is None or n.op == "core.param" or id(n) not in live:
             continue
         op = n.op
         if op in ("core.const", "tl.const", "tl.iota"):
@@ -172,6 +178,9 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
             contribute(x, b.emit("tl.reduce", c, dims=added, f="sum") if added else c)
         elif op == "tl.repeat":
             contribute(n.args[0], b.emit("tl.reduce", c, dims=(n.attr("name"),), f="sum"))
+        elif op == "tl.rename":  # a relabelling: the cotangent takes the operand's names back
+            back = tuple(sorted((new, old) for old, new in n.attr("mapping")))
+            contribute(n.args[0], b.emit("tl.rename", c, mapping=back))
         else:
             raise NotImplementedError(
                 f"{op} has no adjoint rule in this build (a primitive joins the AD with its linearization)"

@@ -185,3 +185,90 @@ def test_the_gelu_marker_differentiates_through_its_derived_partial():
     low = ewprog.lower(dn, dn.type.dims, {id(xp): xp})
     want = xt.grad.numpy() / dy
     np.testing.assert_allclose(emulate(low, [xv]), want, rtol=1e-9, atol=1e-12)
+
+
+def test_rename_adjoint_and_wrt_pruning():
+    """A rename's cotangent takes the operand's names back; nodes with no wrt
+    param among their ancestors are not differentiated (the joint of gpt2's
+    weights without its embedding tables then needs no adjoint for the
+    gather). Against torch autograd."""
+    from pdum_dsl_amd.tl.dialect import OPS
+    from pdum_dsl_amd.tl.ir import Builder, Dim, Region, TensorType, walk
+
+    b = Builder(OPS)
+    x = b.param(0, TensorType((Dim("t", 0, 5), Dim("d", 0, 3))))
+    w = b.param(1, TensorType((Dim("d", 0, 3),)))
+    r = b.emit("tl.rename", x, mapping=(("t", "s"),))
+    y = b.emit("tl.pointwise", b.emit("tl.pointwise", r, f="tanh"), b.emit("tl.repeat_like", w, r), f="mul")
+    region = Region(params=(x, w), body=(b.emit("core.yield", y),))
+    names = region_names(region, ("x", "w"), ("y",))
+    rng = np.random.default_rng(8)
+    xv, wv, dy = rng.standard_normal((5, 3)), rng.standard_normal(3), rng.standard_normal((5, 3))
+    xt, wt = torch.tensor(xv, requires_grad=True), torch.tensor(wv, requires_grad=True)
+    (torch.tanh(xt) * wt).backward(torch.tensor(dy))
+    full = grad(region, "y", seed="dy", names=names)
+    res = interp.run_region(full.region, [interp.field(xv, ("t", "d")), interp.field(wv, ("d",)),
+                                          interp.field(dy, ("s", "d"))])
+    np.testing.assert_allclose(res[1].to_numpy(("t", "d")), xt.grad.numpy(), rtol=1e-12)
+    np.testing.assert_allclose(res[2].to_numpy(("d",)), wt.grad.numpy(), rtol=1e-12)
+    only_w = grad(region, "y", seed="dy", wrt=("w",), names=names)
+    assert len(list(walk(only_w.region))) < len(list(walk(full.region)))  # no tanh' or rename back for x
+    res_w = interp.run_region(only_w.region, [interp.field(xv, ("t", "d")), interp.field(wv, ("d",)),
+                                              interp.field(dy, ("s", "d"))])
+    np.testing.assert_allclose(res_w[1].to_numpy(("d",)), wt.grad.numpy(), rtol=1e-12)
+
+
+def test_the_gpt2_weight_joint_builds_and_plans():
+    """grad of the gpt2 zoo model's logits w.r.t. every weight but the
+    embedding tables: the joint plans into contraction, map-chain and
+    row-statistics carves (the residue: the forward gather and the
+    softmax's bare row max)."""
+    from collections import Counter
+
+    m = zoo.gpt2(zoo.GPT2Config(t=16, d=64, nh=2, hk=32, m=128, layers=1, v=32), seed=3)
+    pn = tuple(m.names[id(p)] for p in m.region.params)
+    names = region_names(m.region, pn, ("logits",))
+    wrt = tuple(n for n in pn if n not in ("ids", "wte", "wpe"))
+    rg = grad(m.region, "logits", seed="dlogits", wrt=wrt, names=names)
+    assert set(rg.grads) == set(wrt) and all(rg.grads[n] for n in wrt)
+    counts = Counter(c.group.template for c in plan_model(rg.region).carves)
+    assert counts["contraction-epilogue"] > 0 and counts["map-chain"] > 0
+    # the joint's values against torch autograd of the same forward (zoo.gpt2's ref, float64)
+    inp = {k: torch.tensor(v) for k, v in m.inputs.items()}
+    for nm in wrt:
+        inp[nm].requires_grad_(True)
+    T, K = 16, 32
+
+    def ln(x, g, b_):
+        mu = x.mean(-1, keepdim=True)
+        xc = x - mu
+        return xc / torch.sqrt((xc * xc).mean(-1, keepdim=True) + 1e-5) * g + b_
+
+    hh = inp["wte"][inp["ids"]] + inp["wpe"]
+    mask = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    p = "h.0."
+    a = ln(hh, inp[p + "attn.ln1g"], inp[p + "attn.ln1b"])
+    q = torch.einsum("td,dhk->thk", a, inp[p + "attn.wq"]) / np.sqrt(K)
+    kk = torch.einsum("sd,dhk->shk", a, inp[p + "attn.wk"])
+    vv = torch.einsum("sd,dhk->shk", a, inp[p + "attn.wv"])
+    sc = torch.where(mask[:, :, None], torch.einsum("thk,shk->tsh", q, kk), torch.tensor(-1e9, dtype=torch.float64))
+    ctx = torch.einsum("tsh,shk->thk", torch.softmax(sc, dim=1), vv)
+    hh = hh + torch.einsum("thk,hkd->td", ctx, inp[p + "attn.wo"])
+    a2 = ln(hh, inp[p + "mlp.ln2g"], inp[p + "mlp.ln2b"])
+    mm = torch.nn.functional.gelu(a2 @ inp[p + "mlp.w1"] + inp[p + "mlp.b1"], approximate="tanh")
+    hh = hh + mm @ inp[p + "mlp.w2"] + inp[p + "mlp.b2"]
+    logits = ln(hh, inp["lnfg"], inp["lnfb"]) @ inp["wte"].T
+    y = m.region.body[-1].args[0]
+    dl = np.random.default_rng(2).standard_normal(tuple(y.type.shape))
+    dl_tv = np.transpose(dl, [y.type.names.index(n) for n in ("t", "v")])
+    logits.backward(torch.tensor(dl_tv))
+    vals = [rev.value(m.inputs[m.names[id(p_)]], p_.type) for p_ in m.region.params]
+    res = rev.evaluate(rg.region, vals + [rev.value(dl, rg.region.params[-1].type)])
+    by = dict(zip(rg.outputs, res))
+    for nm in wrt:
+        pt = next(p_ for p_ in m.region.params if m.names[id(p_)] == nm).type
+        got = by[rg.grads[nm]].numpy()
+        g_names = rg.nodes[rg.grads[nm]].type.names
+        got = np.transpose(got, [g_names.index(d) for d in pt.names])
+        want = inp[nm].grad.numpy()
+        np.testing.assert_allclose(got, want, rtol=1e-7, atol=1e-9 * max(1.0, np.abs(want).max()), err_msg=nm)
