@@ -281,6 +281,12 @@ int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, const void* 
  * element. */
 int pdh_reduce_rows(const pdh_ew_program* summand, int nk, const pdh_ew_program* epi, const void* const* operands,
                     int n_operands, void* out, int dtype, void* stream);
+/* The same with the reducer chosen: 0 sum (pdh_reduce_rows), 1 max, 2 min.
+ * A bare max / min over dims is a group the reference leaves red and serves on
+ * its evaluator (partition.py:586-607); the carved-plan executor runs it here
+ * (a softmax's row max that a backward joint materializes). */
+int pdh_reduce_rows_ex(const pdh_ew_program* summand, int nk, const pdh_ew_program* epi,
+                       const void* const* operands, int n_operands, void* out, int dtype, int reducer, void* stream);
 
 /* Runtime specialization of elementwise programs. pdh_map_chain and
  * pdh_contract first compile the program into straight-line code with hipRTC

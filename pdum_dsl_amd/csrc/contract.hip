@@ -36,8 +36,8 @@ __global__ __launch_bounds__(256) void contract_f32(ContractArgs a, pdh_ew_progr
 
 template <int DT>
 __global__ __launch_bounds__(256) void reduce_rows_kernel(pdh_ew_program ps, pdh_ew_program pe, EwOperands ops,
-                                                          void* out, int nk, int rows) {
-  reduce_rows_body<DT, InterpEval, InterpEval>(ps, pe, ops, out, nk, rows);
+                                                          void* out, int nk, int rows, int reducer) {
+  reduce_rows_body<DT, InterpEval, InterpEval>(ps, pe, ops, out, nk, rows, reducer);
 }
 
 // -------------------------------------------------------------- validation
@@ -252,6 +252,13 @@ extern "C" int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, c
 
 extern "C" int pdh_reduce_rows(const pdh_ew_program* summand, int nk, const pdh_ew_program* epi,
                                const void* const* operands, int n_operands, void* out, int dtype, void* stream) {
+  return pdh_reduce_rows_ex(summand, nk, epi, operands, n_operands, out, dtype, 0, stream);
+}
+
+extern "C" int pdh_reduce_rows_ex(const pdh_ew_program* summand, int nk, const pdh_ew_program* epi,
+                                  const void* const* operands, int n_operands, void* out, int dtype, int reducer,
+                                  void* stream) {
+  PDH_REQUIRE(reducer >= 0 && reducer <= 2, PDH_EINVAL, "pdh_reduce_rows: reducer %d (0 sum, 1 max, 2 min)", reducer);
   int rc = check_program(summand, -1, false, "pdh_reduce_rows (summand)");
   if (rc) return rc;
   if ((rc = check_program(epi, -1, true, "pdh_reduce_rows (epilogue)"))) return rc;
@@ -287,17 +294,17 @@ extern "C" int pdh_reduce_rows(const pdh_ew_program* summand, int nk, const pdh_
   hipFunction_t fn;
   if (jit_get_reduce(*summand, *epi, dtype, &fn)) {
     pdh_ew_program a = *summand, b = *epi;
-    void* args[] = {&a, &b, &ops, &out, &nk, &r32};
+    void* args[] = {&a, &b, &ops, &out, &nk, &r32, &reducer};
     PDH_REQUIRE(hipModuleLaunchKernel(fn, grid.x, 1, 1, 256, 1, 1, 0, st, args, nullptr) == hipSuccess, PDH_ELAUNCH,
                 "pdh_reduce_rows: specialized launch failed");
     jit_count_launch();
     return PDH_OK;
   }
   if (dtype == PDH_F32)
-    reduce_rows_kernel<PDH_F32><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32);
+    reduce_rows_kernel<PDH_F32><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32, reducer);
   else if (dtype == PDH_BF16)
-    reduce_rows_kernel<PDH_BF16><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32);
+    reduce_rows_kernel<PDH_BF16><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32, reducer);
   else
-    reduce_rows_kernel<PDH_F16><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32);
+    reduce_rows_kernel<PDH_F16><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32, reducer);
   return check_launch("pdh_reduce_rows");
 }

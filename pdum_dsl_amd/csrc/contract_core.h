@@ -110,7 +110,7 @@ __device__ __forceinline__ void map_chain_body(const pdh_ew_program& p, const Ew
 // k), otherwise one k at a time with its coordinates decoded. The sum is fp32.
 template <int DT, typename EvalS, typename EvalE>
 __device__ __forceinline__ void reduce_rows_body(const pdh_ew_program& ps, const pdh_ew_program& pe,
-                                                 const EwOperands& ops, void* out, int nk, int rows) {
+                                                 const EwOperands& ops, void* out, int nk, int rows, int reducer) {
   const int lane = threadIdx.x & 63;
   const int r = static_cast<int>(blockIdx.x) * 4 + wave_id();
   if (r >= rows) return;
@@ -124,7 +124,9 @@ __device__ __forceinline__ void reduce_rows_body(const pdh_ew_program& ps, const
   }
   int ktot = 1;
   for (int d = nr; d < nr + nk; ++d) ktot *= static_cast<int>(ps.shape[d]);
-  float sum = 0.f;
+  // reducer 0: sum; 1: max; 2: min (wave-uniform, so the branches do not diverge)
+  auto comb = [reducer](float x, float y) { return reducer == 0 ? x + y : (reducer == 1 ? fmaxf(x, y) : fminf(x, y)); };
+  float sum = reducer == 0 ? 0.f : (reducer == 1 ? -__builtin_inff() : __builtin_inff());
   if (nk == 1) {
     const float zero4[4] = {0.f, 0.f, 0.f, 0.f};
     int base = 0;
@@ -132,14 +134,14 @@ __device__ __forceinline__ void reduce_rows_body(const pdh_ew_program& ps, const
       c[nr] = base + lane;
       float res[4];
       EvalS::template run<4>(ps, ops, DT, c, zero4, res, 64);
-      sum += (res[0] + res[1]) + (res[2] + res[3]);
+      sum = comb(sum, comb(comb(res[0], res[1]), comb(res[2], res[3])));
     }
     for (int kk = base + lane; kk < ktot; kk += 64) {
       c[nr] = kk;
       const float z1[1] = {0.f};
       float r1[1];
       EvalS::template run<1>(ps, ops, DT, c, z1, r1, 1);
-      sum += r1[0];
+      sum = comb(sum, r1[0]);
     }
   } else {
     for (int kk = lane; kk < ktot; kk += 64) {
@@ -152,10 +154,15 @@ __device__ __forceinline__ void reduce_rows_body(const pdh_ew_program& ps, const
       const float z1[1] = {0.f};
       float r1[1];
       EvalS::template run<1>(ps, ops, DT, c, z1, r1, 1);
-      sum += r1[0];
+      sum = comb(sum, r1[0]);
     }
   }
-  sum = wave_total(sum);
+  if (reducer == 0) {
+    sum = wave_total(sum);
+  } else {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum = comb(sum, __shfl_xor(sum, off, 64));
+  }
   if (lane == 0) {
     const float a1[1] = {sum};
     float r1[1];

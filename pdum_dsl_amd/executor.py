@@ -21,6 +21,8 @@ kernels, one step per carve:
   row-statistics        pdh_layernorm_dt with the affine epilogue
   map-chain, stencil    pdh_map_chain (shifted reads as offset views)
   ROWSUM / PLAIN        pdh_reduce_rows
+  red bare max / min    pdh_reduce_rows_ex (a softmax's row max a backward
+                        joint materializes)
   softmax + PV carves   when they compute banded attention per head (the
                         scores dissolved into the softmax carve, its
                         probabilities read by one contraction carve alone):
@@ -422,6 +424,12 @@ class PlanExecutor:
             run, src = self._map_chain(k)
         elif carve.group.confidence == "red" and any(n.op == "tl.take" for n in walk(k)):
             run, src = self._take(k)
+        elif (carve.group.confidence == "red" and k.body[-1].args[0].op == "tl.reduce"
+              and k.body[-1].args[0].attr("f") in ("max", "min")):
+            # a bare row max / min (a softmax's max a backward joint keeps): pdh_reduce_rows_ex
+            red = k.body[-1].args[0]
+            run, src = self._reduce(k, {"reduce": red, "a": red.args[0], "f": red.attr("f"),
+                                        "shape": f"bare-{red.attr('f')}"}, reducer=red.attr("f"))
         else:
             raise Untranslatable(f"carve {tmpl} ({carve.group.reason or carve.root_op}) has no device step")
         return Step(tmpl, ins, outs, run, src)
@@ -829,7 +837,7 @@ class PlanExecutor:
         src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
         return run, src
 
-    def _reduce(self, k, m, yroot=None):
+    def _reduce(self, k, m, yroot=None, reducer="sum"):
         """The ROWSUM / PLAIN contraction shapes: the summand (the product of
         same-space operands, or the one operand chain) summed over the
         contracted dims by pdh_reduce_rows, the epilogue on the sum."""
@@ -872,7 +880,7 @@ class PlanExecutor:
             from . import kernels as K
 
             out = torch.empty(shape, device="cuda", dtype=getattr(torch, _TORCH_DT[self.dtype]))
-            K.reduce_rows(ps, nk, pe, [vals[i].reshape(-1)[o:] for i, o in zip(slots, offs)], out)
+            K.reduce_rows(ps, nk, pe, [vals[i].reshape(-1)[o:] for i, o in zip(slots, offs)], out, reducer)
             return out
 
         return run, f"reduce_rows {m['shape']} rows={math.prod(d.size for d in row_dims)} k={total} " \

@@ -411,8 +411,11 @@ def contract_strided(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, s
     return out
 
 
+_REDUCERS = {"sum": 0, "max": 1, "min": 2}
+
+
 def reduce_rows(summand: _lib.EwProgram, nk: int, epi: _lib.EwProgram, operands: list,
-                out: torch.Tensor) -> torch.Tensor:
+                out: torch.Tensor, reducer: str = "sum") -> torch.Tensor:
     """out[r] = epi(sum over the last nk summand dims of summand(r, k)): the
     rowsum / plain contraction shapes. Both programs read ``operands``."""
     _require_cuda(out, *operands)
@@ -430,8 +433,8 @@ def reduce_rows(summand: _lib.EwProgram, nk: int, epi: _lib.EwProgram, operands:
     if _max_offset(epi, epi.out_stride, epi.ndim) >= out.numel():
         raise ValueError("the epilogue's output view reaches past the output tensor")
     table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
-    _lib.call("pdh_reduce_rows", C.byref(summand), int(nk), C.byref(epi), table, len(operands), _ptr(out),
-              _DT[out.dtype], C.c_void_p(_stream()))
+    _lib.call("pdh_reduce_rows_ex", C.byref(summand), int(nk), C.byref(epi), table, len(operands), _ptr(out),
+              _DT[out.dtype], _REDUCERS[reducer], C.c_void_p(_stream()))
     return out
 
 

@@ -205,3 +205,56 @@ def test_a_planned_flash_joint_runs_forward_and_backward():
     wq, wk, wv = cf.attention_bwd(q, k, v, do, scale=1.0, band=(None, 0))
     for g, want in zip(got, (wo, wq, wk, wv)):
         assert np.abs(g - want).max() <= 2e-2 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("f", ["max", "min"])
+def test_a_bare_row_max_or_min_runs_on_the_device(f):
+    """A bare max / min reduction is a red group in the reference's plan; the
+    executor runs it with pdh_reduce_rows_ex (exact: a max selects a value)."""
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl.dialect import OPS
+    from pdum_dsl_amd.tl.ir import Builder, Dim, Region, TensorType
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    b = Builder(OPS)
+    x = b.param(0, TensorType((Dim("t", 0, 37), Dim("h", 0, 3), Dim("s", 0, 700))))
+    y = b.emit("tl.reduce", x, dims=("s",), f=f)
+    region = Region(params=(x,), body=(b.emit("core.yield", y),))
+    ex = PlanExecutor(plan_model(region), region, "f32")
+    xv = np.random.default_rng(4).standard_normal((37, 3, 700))
+    ex.bind([xv])
+    got = ex.run().cpu().numpy()
+    torch.cuda.synchronize()
+    want = getattr(np, f)(xv.astype(np.float32), axis=2)
+    np.testing.assert_array_equal(got, np.transpose(want, [("t", "h").index(n) for n in y.type.names]))
+
+
+@pytest.mark.parametrize("dtype,tol", [("f32", 1e-4), ("bf16", 1e-1)])
+def test_the_gpt2_weight_gradients_run_carve_by_carve(dtype, tol):
+    """grad of gpt2's logits w.r.t. every weight but the embedding tables,
+    planned by plan_model and run on the device (contractions with their
+    epilogues, map chains, the layernorm, the gather and the bare row max),
+    against the float64 oracle's evaluation of the same joint. Per output,
+    tol of its scale (bf16: every boundary of ~75 carves rounded)."""
+    from oracle import region_eval as rev
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import zoo
+    from pdum_dsl_amd.tl.autodiff import grad, region_names
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    m = zoo.gpt2(zoo.GPT2Config(t=64, d=128, nh=2, hk=64, m=512, layers=1, v=64), seed=3)
+    pn = tuple(m.names[id(p)] for p in m.region.params)
+    wrt = tuple(n for n in pn if n not in ("ids", "wte", "wpe"))
+    rg = grad(m.region, "logits", seed="dlogits", wrt=wrt, names=region_names(m.region, pn, ("logits",)))
+    dl = np.random.default_rng(2).standard_normal(tuple(rg.region.params[-1].type.shape))
+    vals = m.values() + [dl]
+    ex = PlanExecutor(plan_model(rg.region), rg.region, dtype)
+    ex.bind(vals)
+    outs = ex.run()
+    torch.cuda.synchronize()
+    want = rev.evaluate(rg.region, [rev.value(v, p.type) for v, p in zip(vals, rg.region.params)])
+    assert len(outs) == len(want) == 1 + len(wrt)
+    for name, g, w in zip(rg.outputs, outs, want):
+        w = w.numpy()
+        err = np.abs(g.float().cpu().numpy() - w).max()
+        assert err <= tol * max(np.abs(w).max(), 1e-6), f"{dtype} {name}: max err {err} vs scale {np.abs(w).max()}"
