@@ -295,6 +295,11 @@ def secondary(torch, K, cf, h, dev):
         out["carved_plan"] = _carved_plan_line(torch)
     except Exception as exc:
         out["carved_plan"] = {"error": str(exc)}
+    # ---------------- f2: the same model's weight gradients, carved and run ----------------
+    try:
+        out["carved_grad"] = _carved_grad_line(torch)
+    except Exception as exc:
+        out["carved_grad"] = {"error": str(exc)}
     return out
 
 
@@ -428,6 +433,91 @@ def _carved_plan_line(torch):
         "tokens_per_s": round(T / ms * 1e3, 1),
         "TFLOP/s": round(fl / ms / 1e9, 1), "algorithmic_flop": fl,
         "torch_eager_ms": round(ms_torch, 4), "max_abs_err_vs_f32": err, "logit_scale": scale,
+    }
+
+
+def _carved_grad_line(torch, dtype="f32"):
+    """A gpt2-small training step's compute: the joint of the forward and the
+    gradients of every weight but the embedding tables (autodiff.grad of the
+    logits, seeded by a random cotangent), planned by plan_model and run by
+    the device executor as one HIP graph. fp32 storage: the carved backward
+    rounds every boundary to the storage type, and in bf16 the layernorm and
+    softmax backward carves cancel (layer 0's gradients drift far from fp32
+    over 12 layers). Checked against torch fp32 autograd of the same forward
+    on the same weights (three gradients), timed beside torch's forward +
+    backward (eager autograd, the same weights and type)."""
+    import time as _time
+
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import zoo
+    from pdum_dsl_amd.tl.autodiff import grad, region_names
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    cfg = zoo.GPT2Config(t=1024, d=768, nh=12, hk=64, m=3072, layers=12, v=50257)
+    t0 = _time.perf_counter()
+    m = zoo.gpt2(cfg, seed=7)
+    pn = tuple(m.names[id(p)] for p in m.region.params)
+    wrt = tuple(n for n in pn if n not in ("ids", "wte", "wpe"))
+    rg = grad(m.region, "logits", seed="dlogits", wrt=wrt, names=region_names(m.region, pn, ("logits",)))
+    plan = plan_model(rg.region)
+    ex = PlanExecutor(plan, rg.region, dtype)
+    plan_s = _time.perf_counter() - t0
+    seed_t = rg.region.params[-1].type
+    dl = np.random.default_rng(9).standard_normal(tuple(seed_t.shape)) * 1e-2
+    ex.bind(m.values() + [dl])
+    outs = ex.run()
+    torch.cuda.synchronize()
+    ex.capture()
+    ms = time_events(lambda: ex.replay(check=False), 10)
+    # torch: the same forward with autograd on the same bf16 weights
+    W = {m.names[id(p)]: ex.bound[id(p)] for p in m.region.params}
+    W32 = {}
+    for k_, v_ in W.items():
+        W32[k_] = v_.float().clone().requires_grad_(k_ in wrt) if v_.is_floating_point() else v_
+    for i in range(cfg.layers):
+        p = f"h.{i}."
+        for nm in ("wq", "wk", "wv"):
+            W32[p + f"attn.{nm}2"] = W32[p + f"attn.{nm}"].reshape(cfg.d, cfg.nh * cfg.hk)
+        W32[p + "attn.wo2"] = W32[p + "attn.wo"].reshape(cfg.nh * cfg.hk, cfg.d)
+    W32["wteT"] = W32["wte"].t().contiguous()
+    y = m.region.body[-1].args[0]
+    dlt = torch.as_tensor(dl, dtype=torch.float32, device="cuda").to(ex.bound[id(rg.region.params[-1])].dtype).float()
+    dlt = dlt.permute([seed_t.names.index(n) for n in m.order])
+    _gpt2_torch(torch, W32, cfg).backward(dlt)
+    errs = {}
+    by = dict(zip(rg.outputs, outs))
+    for nm in ("h.0.mlp.w1", "h.11.mlp.w2", "lnfg"):
+        node = rg.nodes[rg.grads[nm]]
+        pt = next(p for p in m.region.params if m.names[id(p)] == nm).type
+        got = by[rg.grads[nm]].float().permute([node.type.names.index(d) for d in pt.names])
+        want = W32[nm].grad
+        errs[nm] = float((got - want).abs().max() / want.abs().max())
+    assert max(errs.values()) < (1e-3 if dtype == "f32" else 0.25), f"carved-gradient parity failed: {errs}"
+    del W32
+    Wb = {}
+    for k_, v_ in W.items():
+        Wb[k_] = v_.clone().requires_grad_(k_ in wrt) if v_.is_floating_point() else v_
+    dlb = dlt.to(torch.bfloat16)
+
+    def torch_step():
+        for i in range(cfg.layers):
+            p = f"h.{i}."
+            for nm in ("wq", "wk", "wv"):
+                Wb[p + f"attn.{nm}2"] = Wb[p + f"attn.{nm}"].reshape(cfg.d, cfg.nh * cfg.hk)
+            Wb[p + "attn.wo2"] = Wb[p + "attn.wo"].reshape(cfg.nh * cfg.hk, cfg.d)
+        Wb["wteT"] = Wb["wte"].t().contiguous()
+        torch.autograd.grad(_gpt2_torch(torch, Wb, cfg), [Wb[n] for n in wrt], dlb)
+
+    ms_torch = time_events(torch_step, 5)
+    by_t = {}
+    for c in plan.carves:
+        by_t[c.group.template] = by_t.get(c.group.template, 0) + 1
+    return {
+        "config": "gpt2-small shape (as the carved_plan line), forward + gradients of every weight but the "
+                  f"embedding tables, {dtype} storage / fp32 accumulate; random weights and cotangent",
+        "carves": by_t, "device_steps": len(ex.steps), "plan_s": round(plan_s, 2), "ms": round(ms, 4),
+        "tokens_per_s": round(cfg.t / ms * 1e3, 1), "torch_eager_fwd_bwd_ms": round(ms_torch, 4),
+        "max_rel_err_vs_torch_f32": errs,
     }
 
 

@@ -427,9 +427,7 @@ class PlanExecutor:
         elif (carve.group.confidence == "red" and k.body[-1].args[0].op == "tl.reduce"
               and k.body[-1].args[0].attr("f") in ("max", "min")):
             # a bare row max / min (a softmax's max a backward joint keeps): pdh_reduce_rows_ex
-            red = k.body[-1].args[0]
-            run, src = self._reduce(k, {"reduce": red, "a": red.args[0], "f": red.attr("f"),
-                                        "shape": f"bare-{red.attr('f')}"}, reducer=red.attr("f"))
+            run, src = self._bare_reduce(k)
         else:
             raise Untranslatable(f"carve {tmpl} ({carve.group.reason or carve.root_op}) has no device step")
         return Step(tmpl, ins, outs, run, src)
@@ -837,6 +835,50 @@ class PlanExecutor:
         src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
         return run, src
 
+    def _bare_reduce(self, k):
+        """A red carve that is one max / min reduction: pdh_reduce_rows_ex over
+        its operand chain, or, when the operand holds a dissolved contraction
+        (the scores under a softmax's max), over that operand materialized
+        first by its own plan."""
+        red = k.body[-1].args[0]
+        f, x = red.attr("f"), red.args[0]
+        if not any(n.op == "tl.reduce" for n in walk(_yielding(k, x))):
+            return self._reduce(k, {"reduce": red, "a": x, "f": f, "shape": f"bare-{f}"}, reducer=f)
+        pre = self._materialize(k, x)
+        b = Builder(OPS)
+        xp = b.param(0, x.type)
+        r2 = b.emit("tl.reduce", xp, dims=red.attr("dims"), f=f)
+        sub = Region(params=(xp,), body=(b.emit("core.yield", r2),))
+        run2, src = self._reduce(sub, {"reduce": r2, "a": xp, "f": f, "shape": f"bare-{f}"}, reducer=f)
+
+        def run(vals):
+            return run2([pre(vals)])
+
+        return run, f"{src} input=plan"
+
+    def _reduce_materialized(self, k, m, y, reducer):
+        """A row reduction whose summand holds a dissolved contraction (the
+        probabilities under a softmax backward's rowsum): the summand is
+        materialized by its own plan, then reduced, with the epilogue, as a
+        region over k's params plus that tensor."""
+        from .tl.partition import rebuild_into
+
+        red, x = m["reduce"], m["reduce"].args[0]
+        pre = self._materialize(k, x)
+        b = Builder(OPS)
+        memo = {id(p): b.param(i, p.type) for i, p in enumerate(k.params)}
+        xp = b.param(len(k.params), x.type)
+        memo[id(x)] = xp
+        y2 = rebuild_into(b, memo, y)
+        sub = Region(params=tuple(memo[id(p)] for p in k.params) + (xp,), body=(b.emit("core.yield", y2),))
+        red2 = next(n for n in walk(sub) if n.op == "tl.reduce" and n.args[0] is xp)
+        run2, src = self._reduce(sub, dict(m, reduce=red2, a=xp), reducer=reducer)
+
+        def run(vals):
+            return run2(list(vals) + [pre(vals)])
+
+        return run, f"{src} summand=plan"
+
     def _reduce(self, k, m, yroot=None, reducer="sum"):
         """The ROWSUM / PLAIN contraction shapes: the summand (the product of
         same-space operands, or the one operand chain) summed over the
@@ -851,6 +893,8 @@ class PlanExecutor:
         leaves = {id(p): p for p in k.params}
         y = k.body[-1].args[0] if yroot is None else yroot
         total = math.prod(d.size for d in kdims)
+        if any(n.op == "tl.reduce" for n in walk(_yielding(k, red.args[0]))):
+            return self._reduce_materialized(k, m, y, reducer)
         try:
             ls = ewprog.lower(red.args[0], lat_s, leaves, allow_views=True)
             le = ewprog.lower(y, row_dims, leaves, acc=red, acc_scale=(1.0 / total) if m["f"] == "mean" else None,
