@@ -45,6 +45,16 @@ def test_validation_errors_need_no_device():
     rc = lib.pdh_flash_fwd(None, None, None, None, None, None, None, C.byref(g), 1, 1.0, -1e9, 0, 0, 0, 1, None)
     assert rc == _lib.PDH_EINVAL and "multiple of heads_kv" in _lib.last_error()
     assert lib.pdh_attn_decode_workspace(C.byref(g), 4) == 1 * 3 * 8 * 4 * (2 + 64) * 4
+    # the key-split forward: its workspace, and an nsplit out of range refused before anything runs
+    assert lib.pdh_flash_fwd_workspace(C.byref(g), 5) == 5 * (1 * 3 * 8) * (64 + 3) * 4
+    assert lib.pdh_flash_fwd_workspace(C.byref(g), 1) == 0
+    rc = lib.pdh_flash_fwd_split(None, None, None, None, None, None, None, C.byref(g), 1, 1.0, -1e9, 0, 0, 0, 1, 65,
+                                 None, 0, None)
+    assert rc == _lib.PDH_EINVAL and "nsplit 65" in _lib.last_error()
+    # the row reduction's reducer code
+    p = _lib.EwProgram()
+    rc = lib.pdh_reduce_rows_ex(C.byref(p), 1, C.byref(p), None, 0, None, 0, 3, None)
+    assert rc == _lib.PDH_EINVAL and "reducer 3" in _lib.last_error()
 
 
 def test_the_forward_split_picker():
