@@ -219,14 +219,33 @@ def certify(tile: Region, naive: Region, *, licenses=(), families=()) -> Certifi
     ran = []
     for fname, factory in families:
         vals = list(factory())
-        got_n = run_region(naive, vals)
-        got_t = run_region(tile, vals)
+        # overflow / invalid / divide-by-zero inside either evaluation means
+        # the draw left the operators' domain, where a comparison checks
+        # nothing: refuse rather than compare inf or NaN
+        try:
+            with np.errstate(over="raise", invalid="raise", divide="raise"):
+                got_n = run_region(naive, vals)
+                got_t = run_region(tile, vals)
+        except FloatingPointError as exc:
+            raise ValueError(
+                f"family {fname!r} left the operators' domain ({exc}): the draw certifies nothing "
+                f"({', '.join(names)})"
+            ) from None
         outs_n = got_n if isinstance(got_n, tuple) else (got_n,)
         outs_t = got_t if isinstance(got_t, tuple) else (got_t,)
         for gt, gn in zip(outs_t, outs_n):
             assert isinstance(gt, Field) and isinstance(gn, Field)
+            want, got = gn.arr, gt.to_numpy(gn.names)
+            # a draw outside an operator's domain checks nothing: NaN against
+            # NaN would "agree" — such a family refuses instead of passing
+            for side, arr in (("naive twin", want), ("tile program", got)):
+                if not np.isfinite(arr).all():
+                    raise ValueError(
+                        f"family {fname!r} left the operators' domain: the {side}'s output is not finite, "
+                        f"so the draw certifies nothing ({', '.join(names)})"
+                    )
             np.testing.assert_allclose(
-                gt.to_numpy(gn.names), gn.arr, rtol=rtol, atol=atol,
+                got, want, rtol=rtol, atol=atol, equal_nan=False,
                 err_msg=f"family {fname!r} exceeded the declared license bound ({', '.join(names)})",
             )
         ran.append(fname)

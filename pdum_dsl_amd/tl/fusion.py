@@ -359,16 +359,65 @@ def generate_contraction(region: Region, m: dict, ki: int) -> Region:
     return check_tier(fused)
 
 
+# pointwise markers defined on part of the line only: a param that reaches
+# one of their arguments is drawn inside the domain
+_HALF_LINE = frozenset(("sqrt", "log"))
+
+
+def domain_restricted_params(region: Region) -> frozenset:
+    """Positions of the params whose values flow (through any path) into the
+    argument of a sqrt or log of ``region``."""
+    pos = {id(p): i for i, p in enumerate(region.params)}
+    reach: dict[int, frozenset] = {}
+    hit: set[int] = set()
+    for n in walk(region):
+        acc = {pos[id(n)]} if id(n) in pos else set()
+        for a in n.args:
+            acc |= reach.get(id(a), frozenset())
+        reach[id(n)] = frozenset(acc)
+        if n.op == "tl.pointwise" and n.attr("f") in _HALF_LINE:
+            for a in n.args:
+                hit |= reach.get(id(a), frozenset())
+    return frozenset(hit)
+
+
 def contraction_families(region: Region, seed: int = 5):
     """Adversarial draws for a contraction's differential tier (used when
     normalization cannot walk back, e.g. a mean's finalize): unit-normal and
-    wide-magnitude operands."""
-    from .interp import field
+    wide-magnitude operands, drawn inside the operators' domains (the
+    "finite operands" domain gemm.k-reassoc declares):
+
+    * params that reach a sqrt or log are drawn positive, (|z| + 1/2) scaled;
+    * the wide family starts at x64 and is narrowed by factors of 8 until the
+      naive twin evaluates without overflow or an invalid operation (an exp
+      of a wide product saturates long before x64), never below x1.
+
+    A draw that still leaves the domain is refused by ``certify``."""
+    from .interp import field, run_region
+
+    positive = domain_restricted_params(region)
+
+    def values(scale, s):
+        rng = np.random.default_rng(s)
+        vals = []
+        for i, p in enumerate(region.params):
+            z = rng.standard_normal(p.type.shape)
+            vals.append(field(((np.abs(z) + 0.5) if i in positive else z) * scale, p.type.names))
+        return vals
 
     def draw(scale, s):
         def factory():
-            rng = np.random.default_rng(s)
-            return [field(rng.standard_normal(p.type.shape) * scale, p.type.names) for p in region.params]
+            sc = scale
+            while True:
+                vals = values(sc, s)
+                if sc <= 1.0:
+                    return vals
+                try:
+                    with np.errstate(over="raise", invalid="raise", divide="raise"):
+                        run_region(region, vals)
+                    return vals
+                except FloatingPointError:
+                    sc = max(1.0, sc / 8.0)
 
         return factory
 
