@@ -122,6 +122,9 @@ def _check_fwd(res, q, k, v, scale, band, lowp):
         (1, 2, 1, 77, 333, 64, False),
         (2, 1, 1, 384, 384, 64, True),
         (1, 1, 1, 1, 1, 128, True),
+        # instances in multiples of 32: the shader-engine-balanced block order
+        (2, 16, 4, 256, 256, 128, True),
+        (1, 32, 8, 128, 300, 64, False),
     ],
 )
 def test_flash_fwd_mfma_matches_oracle(K, dtype, B, Hq, Hkv, T, S, D, causal):
