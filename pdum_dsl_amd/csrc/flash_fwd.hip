@@ -561,7 +561,6 @@ int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
     flash_fwd_combine<T, D><<<dim3(static_cast<unsigned>((nthr + 255) / 256)), 256, 0, st>>>(aa);
     return check_launch("pdh_flash_fwd_split (combine)");
   }
-  const int64_t ninst = nblk / a.nqb;
   aa.xcd_remap = (nblk % 8 == 0) ? ((ninst % 32 == 0) ? 2 : 1) : 0;
   flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk)), C::THREADS, C::LDS, st>>>(aa);
   return check_launch("pdh_flash_fwd");
