@@ -514,6 +514,23 @@ template <typename T, int D>
 __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_main(BwdArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
   int bid = blockIdx.x;
+  if (a.xcd_remap == 2) {
+    // Within an XCD (bid % 8) workgroups go in order round-robin to its four
+    // shader engines (r % 4): four consecutive r take the same role and block
+    // position of four instances, so every engine receives the same sequence
+    // of workgroup lengths (the roles alternate, heavy blocks first) and
+    // in-order dispatch never stalls on an engine that drew the heavier work.
+    // Needs nkblk == nqblk and instances in multiples of 32.
+    const int x = bid & 7, r = bid >> 3, s4 = r & 3, m4 = r >> 2;
+    const int nb = a.nkblk, per_inst = 2 * nb;
+    const int ipx = (gridDim.x >> 3) / per_inst;  // instances per XCD
+    const int inst = x * ipx + (m4 / per_inst) * 4 + s4, step = m4 % per_inst;
+    if ((step & 1) == 0)
+      bwd_dkdv<T, D>(a, inst * nb + (step >> 1), smem);
+    else
+      bwd_dq<T, D>(a, inst * nb + (step >> 1), smem);
+    return;
+  }
   if (a.xcd_remap) {  // consecutive logical blocks (one instance's) share an XCD's L2
     const int per = gridDim.x >> 3;
     bid = (bid & 7) * per + (bid >> 3);
@@ -703,7 +720,7 @@ int launch_bwd(BwdArgs a, hipStream_t st) {
   constexpr int TB = Tile32<D>::BYTES;
   constexpr int lds = 4 * kSub * TB + 2 * kSub * 3 * 32 * 4;  // the larger of the two roles' needs (dK/dV)
   const int64_t nblk = static_cast<int64_t>(a.ninst) * (a.nkblk + a.nqblk);
-  a.xcd_remap = nblk % 8 == 0;
+  a.xcd_remap = nblk % 8 == 0 ? ((a.ninst % 32 == 0 && a.nkblk == a.nqblk) ? 2 : 1) : 0;
   bwd_main<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, lds, st>>>(a);
   return check_launch("pdh_flash_bwd (dk, dv, dq)");
 }

@@ -31,6 +31,9 @@ def _host(t):
         (1, 1, 300, 64, (-63, 0)),  # sliding window
         (1, 1, 256, 64, (None, 5)),  # unbounded below, keys past the diagonal live
         (1, 1, 256, 128, (-40, None)),  # unbounded above
+        # instances in multiples of 32: the shader-engine-balanced block order
+        (2, 16, 256, 64, (None, 0)),
+        (1, 32, 128, 128, None),
     ],
 )
 def test_flash_bwd_matches_oracle(dtype, B, H, T, D, band):
