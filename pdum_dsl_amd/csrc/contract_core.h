@@ -125,7 +125,7 @@ __device__ __forceinline__ void reduce_rows_body(const pdh_ew_program& ps, const
   int ktot = 1;
   for (int d = nr; d < nr + nk; ++d) ktot *= static_cast<int>(ps.shape[d]);
   // reducer 0: sum; 1: max; 2: min (wave-uniform, so the branches do not diverge)
-  auto comb = [reducer](float x, float y) { return reducer == 0 ? x + y : (reducer == 1 ? fmaxf(x, y) : fminf(x, y)); };
+  auto comb = [reducer](float x, float y) { return reducer == 0 ? x + y : (reducer == 1 ? nan_max(x, y) : nan_min(x, y)); };
   float sum = reducer == 0 ? 0.f : (reducer == 1 ? -__builtin_inff() : __builtin_inff());
   if (nk == 1) {
     const float zero4[4] = {0.f, 0.f, 0.f, 0.f};

@@ -60,6 +60,15 @@ __device__ __forceinline__ float pdh_tanh(float x) {
   return __builtin_copysignf(t, x);
 }
 
+// max / min that propagate NaN, as numpy's maximum / minimum and its max / min
+// reductions do (fmaxf / fminf return the non-NaN operand instead).
+__device__ __forceinline__ float nan_max(float x, float y) {
+  return (x != x || y != y) ? x + y : __builtin_fmaxf(x, y);
+}
+__device__ __forceinline__ float nan_min(float x, float y) {
+  return (x != x || y != y) ? x + y : __builtin_fminf(x, y);
+}
+
 // One element of a PDH_F32 / PDH_BF16 / PDH_F16 buffer as fp32, and back.
 template <int DT>
 __device__ __forceinline__ float ld_dt(const void* base, int off) {

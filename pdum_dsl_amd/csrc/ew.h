@@ -120,8 +120,8 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
       PDH_EW_CASE(PDH_EW_SUB, a_ - b_)
       PDH_EW_CASE(PDH_EW_MUL, a_ * b_)
       PDH_EW_CASE(PDH_EW_DIV, a_ / b_)
-      PDH_EW_CASE(PDH_EW_MAX, fmaxf(a_, b_))
-      PDH_EW_CASE(PDH_EW_MIN, fminf(a_, b_))
+      PDH_EW_CASE(PDH_EW_MAX, nan_max(a_, b_))
+      PDH_EW_CASE(PDH_EW_MIN, nan_min(a_, b_))
       PDH_EW_CASE(PDH_EW_EQ, a_ == b_ ? 1.f : 0.f)
       PDH_EW_CASE(PDH_EW_NE, a_ != b_ ? 1.f : 0.f)
       PDH_EW_CASE(PDH_EW_LT, a_ < b_ ? 1.f : 0.f)

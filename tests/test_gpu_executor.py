@@ -222,11 +222,16 @@ def test_a_bare_row_max_or_min_runs_on_the_device(f):
     region = Region(params=(x,), body=(b.emit("core.yield", y),))
     ex = PlanExecutor(plan_model(region), region, "f32")
     xv = np.random.default_rng(4).standard_normal((37, 3, 700))
+    # a NaN anywhere in a row makes its max / min NaN, as numpy's reductions
+    # (and the reference's float64 evaluator) have it
+    xv[5, 1, 0] = xv[11, 0, 333] = xv[36, 2, 699] = np.nan
     ex.bind([xv])
     got = ex.run().cpu().numpy()
     torch.cuda.synchronize()
     want = getattr(np, f)(xv.astype(np.float32), axis=2)
-    np.testing.assert_array_equal(got, np.transpose(want, [("t", "h").index(n) for n in y.type.names]))
+    want = np.transpose(want, [("t", "h").index(n) for n in y.type.names])
+    assert np.isnan(want).sum() == 3
+    np.testing.assert_array_equal(got, want)  # NaN positions must agree too
 
 
 @pytest.mark.parametrize("dtype,tol", [("f32", 1e-4), ("bf16", 1e-1)])
