@@ -194,6 +194,20 @@ int pdh_attn_decode(const void* q, const void* k, const void* v, void* o, float*
                     const pdh_attn_geom* geom, int dtype, float scale, int nsplit, void* ws,
                     size_t ws_bytes, void* stream);
 
+/* pdh_attn_decode without a workspace argument and without allocating: the
+ * split partials go to a device array the library holds, one per GPU, of
+ * PDH_DECODE_SCRATCH_BYTES, from the first call on that GPU until the process
+ * ends. No counterpart in the reference; it is for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc). The caller still passes inputs and outputs. A request
+ * whose pdh_attn_decode_workspace(geom, nsplit) exceeds the array is refused
+ * (PDH_EINVAL) before anything runs. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams or threads) race.
+ * Results equal pdh_attn_decode's bit for bit (the same kernels). */
+#define PDH_DECODE_SCRATCH_BYTES (16u << 20)
+int pdh_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o, float* lse_out,
+                            const pdh_attn_geom* geom, int dtype, float scale, int nsplit, void* stream);
+
 /* ------------------------------------------------------------------------
  * Elementwise programs. The pointwise chains of the map-chain template and
  * of a contraction's epilogue are lowered to a small register program, run

@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libpdhip.so"
 
 PDH_OK, PDH_EINVAL, PDH_EUNSUPPORTED, PDH_ELAUNCH = 0, 1, 2, 3
 PDH_F32, PDH_BF16, PDH_F16 = 0, 1, 2
+DECODE_SCRATCH_BYTES = 16 << 20  # PDH_DECODE_SCRATCH_BYTES: pdh_attn_decode_noalloc's per-GPU array
 PDH_MASK_NONE, PDH_MASK_BAND = 0, 1
 
 I64_MIN = -(2**63)
@@ -35,6 +36,7 @@ EXPORTS = (
     "pdh_flash_bwd",
     "pdh_attn_decode_workspace",
     "pdh_attn_decode",
+    "pdh_attn_decode_noalloc",
     "pdh_map_chain",
     "pdh_contract",
     "pdh_contract_strided",
@@ -117,6 +119,7 @@ def _declare(lib) -> None:
         "pdh_flash_bwd": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, vp]),
         "pdh_attn_decode_workspace": (C.c_size_t, [gp, i32]),
         "pdh_attn_decode": (i32, [vp, vp, vp, vp, vp, gp, i32, f32, i32, vp, C.c_size_t, vp]),
+        "pdh_attn_decode_noalloc": (i32, [vp, vp, vp, vp, vp, gp, i32, f32, i32, vp]),
         "pdh_map_chain": (i32, [C.POINTER(EwProgram), C.POINTER(vp), vp, i32, vp]),
         "pdh_contract": (i32, [vp, vp, i64, i64, i64, i64, i64, C.POINTER(EwProgram), C.POINTER(vp), vp, i32, vp]),
         "pdh_contract_strided": (

@@ -22,6 +22,8 @@
 //   m = max(mL, mR); den = denL e^(mL-m) + denR e^(mR-m); o likewise.
 #include "attn_common.h"
 
+#include <mutex>
+
 namespace pdh {
 namespace {
 
@@ -291,6 +293,49 @@ int launch_decode(const DecArgs& a, int64_t nrows, uint16_t* o, float* lse, int6
 
 using namespace pdh;
 
+// ---- the allocation-free variant: the split workspace in a library-held array
+//
+// One array per GPU, of PDH_DECODE_SCRATCH_BYTES, in the code object's device
+// memory (allocated when the library's code object loads on that GPU, held
+// until the process ends). Host code must never pass `pdh_decode_scratch` itself
+// to a kernel: in host code the name is a host-side stand-in, not a device
+// address. Its device address is looked up once per device, with that device
+// current, by hipGetSymbolAddress, and kept per device; only that address is
+// handed to the kernels. Every call on a GPU shares that GPU's array (calls
+// that overlap on one GPU race); each call writes every (row, split) partial
+// it reads, so nothing has to be cleared between calls.
+// External linkage on purpose: with `static` the array is a local (STB_LOCAL)
+// symbol of the device code object, which the runtime's symbol lookup behind
+// hipGetSymbolAddress cannot resolve; the pdh_ prefix keeps the name unique.
+__device__ __align__(256) unsigned char pdh_decode_scratch[PDH_DECODE_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+int decode_scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  PDH_REQUIRE(e == hipSuccess, PDH_ELAUNCH, "pdh_attn_decode_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  PDH_REQUIRE(dev >= 0 && dev < kMaxDevices, PDH_EUNSUPPORTED, "pdh_attn_decode_noalloc: device %d >= %d", dev,
+              kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(pdh_decode_scratch));
+    PDH_REQUIRE(e == hipSuccess && p != nullptr, PDH_ELAUNCH,
+                "pdh_attn_decode_noalloc: hipGetSymbolAddress(pdh_decode_scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return PDH_OK;
+}
+
+}  // namespace
+
 extern "C" size_t pdh_attn_decode_workspace(const pdh_attn_geom* g, int nsplit) {
   if (!g || nsplit < 1 || g->batch < 0 || g->heads_q < 1 || g->t < 0 || g->od < 1) return 0;
   return static_cast<size_t>(g->batch * g->heads_q * g->t) * static_cast<size_t>(nsplit) *
@@ -341,4 +386,19 @@ extern "C" int pdh_attn_decode(const void* q, const void* k, const void* v, void
   return G.e == 128
              ? launch_decode<_Float16, 128>(a, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st, groups, st)
              : launch_decode<_Float16, 64>(a, nrows, op, lse_out, G.o_sb, G.o_sh, G.o_st, groups, st);
+}
+
+extern "C" int pdh_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o, float* lse_out,
+                                       const pdh_attn_geom* gm, int dtype, float scale, int nsplit, void* stream) {
+  PDH_REQUIRE(gm != nullptr, PDH_EINVAL, "pdh_attn_decode_noalloc: null geometry");
+  PDH_REQUIRE(nsplit >= 1, PDH_EINVAL, "pdh_attn_decode_noalloc: nsplit must be >= 1");
+  const size_t need = pdh_attn_decode_workspace(gm, nsplit);
+  PDH_REQUIRE(need <= PDH_DECODE_SCRATCH_BYTES, PDH_EINVAL,
+              "pdh_attn_decode_noalloc: this request needs %zu bytes of split workspace; the library's scratch "
+              "array holds %zu (fewer splits or rows, or pdh_attn_decode with a caller workspace)",
+              need, static_cast<size_t>(PDH_DECODE_SCRATCH_BYTES));
+  void* ws = nullptr;
+  const int rc = decode_scratch_address(&ws);
+  if (rc != PDH_OK) return rc;
+  return pdh_attn_decode(q, k, v, o, lse_out, gm, dtype, scale, nsplit, ws, PDH_DECODE_SCRATCH_BYTES, stream);
 }

@@ -331,6 +331,32 @@ def attn_decode(
     return o, lse
 
 
+def attn_decode_static(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor | None,
+    *,
+    nsplit: int,
+    scale: float | None = None,
+) -> None:
+    """attn_decode into caller-provided o / lse with the split partials in the
+    library's per-GPU scratch array (pdh_attn_decode_noalloc): nothing is
+    allocated, so the call can be captured in a HIP graph. Calls that overlap
+    on one GPU share that array and race."""
+    _require_cuda(q, k, v, o, lse)
+    g = _geom(q, k, v, o)
+    if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous() or lse.shape != q.shape[:3]):
+        raise ValueError("lse must be contiguous fp32 [batch, heads_q, t]")
+    sc = 1.0 / math.sqrt(q.shape[3]) if scale is None else float(scale)
+    _lib.call(
+        "pdh_attn_decode_noalloc",
+        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), C.byref(g), _DT[q.dtype], C.c_float(sc), int(nsplit),
+        C.c_void_p(_stream()),
+    )
+
+
 # ------------------------------------------------- elementwise programs
 
 
