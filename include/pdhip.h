@@ -194,6 +194,20 @@ int pdh_attn_decode(const void* q, const void* k, const void* v, void* o, float*
                     const pdh_attn_geom* geom, int dtype, float scale, int nsplit, void* ws,
                     size_t ws_bytes, void* stream);
 
+/* Inclusive prefix reduce along one dim (tl.scan; the reference's
+ * compute.py:318-350, run by its evaluator as a red group: the
+ * first-occurrence max / min adjoint, autodiff.py:635-665, carries one).
+ * x, y: dense [outer][n][inner] of `dtype` (fp32 arithmetic); the scan runs
+ * along n: y[o][t][i] folds x[o][0..t][i] (reverse != 0: x[o][t..n-1][i]).
+ * A mean divides prefix t by its count. Max / min propagate NaN. y may be x. */
+#define PDH_SCAN_SUM 0
+#define PDH_SCAN_MAX 1
+#define PDH_SCAN_MIN 2
+#define PDH_SCAN_PROD 3
+#define PDH_SCAN_MEAN 4
+int pdh_scan(const void* x, void* y, int64_t outer, int64_t n, int64_t inner, int dtype, int reducer, int reverse,
+             void* stream);
+
 /* pdh_attn_decode without a workspace argument and without allocating: the
  * split partials go to a device array the library holds, one per GPU, of
  * PDH_DECODE_SCRATCH_BYTES, from the first call on that GPU until the process

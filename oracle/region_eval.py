@@ -15,6 +15,8 @@ planner's numpy interpreter, so each can check the other:
                  (region_evaluator.py:289-318; compute.py:95-123)
   tl.reduce      sum/prod/max/min via torch reductions; mean = sum / N
                  (compute.py:184-214; region_evaluator.py:320-352)
+  tl.scan        inclusive prefix along one dim: cumsum / cumprod / cummax /
+                 cummin; mean divides by the running count (compute.py:318-350)
   tl.repeat_like / tl.repeat / tl.split / tl.stage / tl.select / tl.iota /
   tl.const       layout views (region_evaluator.py:372-430)
   tl.rename / tl.shift / tl.slice   relabelings and a window (layout.py)
@@ -149,6 +151,27 @@ def _dispatch(n, ev):
             for a in sorted(axes, reverse=True):
                 out = out.amax(dim=a) if f == "max" else out.amin(dim=a)
         return V(out, tuple(d for d in x.dims if d[0] not in dims))
+    if op == "tl.scan":  # inclusive prefix reduce along one dim (compute.py:318-350)
+        x = ev(n.args[0])
+        ax = x.names.index(_attr(n, "dim"))
+        f = _attr(n, "f")
+        t = x.t.to(torch.float64) if x.t.dtype == torch.bool else x.t
+        rev = bool(_attr(n, "reverse") or False)
+        if rev:
+            t = torch.flip(t, dims=(ax,))
+        if f in ("sum", "mean"):
+            out = torch.cumsum(t, dim=ax)
+            if f == "mean":
+                shape = [1] * t.dim()
+                shape[ax] = t.shape[ax]
+                out = out / torch.arange(1, t.shape[ax] + 1, dtype=torch.float64).reshape(shape)
+        elif f == "prod":
+            out = torch.cumprod(t, dim=ax)
+        else:
+            out = (torch.cummax if f == "max" else torch.cummin)(t, dim=ax).values
+        if rev:
+            out = torch.flip(out, dims=(ax,))
+        return V(out, x.dims)
     if op == "tl.repeat_like":
         x, like = ev(n.args[0]), ev(n.args[1])
         extra = tuple(d for d in like.dims if d[0] not in x.names)

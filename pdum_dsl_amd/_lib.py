@@ -42,6 +42,7 @@ EXPORTS = (
     "pdh_contract_strided",
     "pdh_reduce_rows",
     "pdh_reduce_rows_ex",
+    "pdh_scan",
     "pdh_ew_set_jit",
     "pdh_ew_jit_stats",
     "pdh_ew_jit_source",
@@ -127,6 +128,7 @@ def _declare(lib) -> None:
         "pdh_reduce_rows": (i32, [C.POINTER(EwProgram), i32, C.POINTER(EwProgram), C.POINTER(vp), i32, vp, i32, vp]),
         "pdh_reduce_rows_ex": (i32, [C.POINTER(EwProgram), i32, C.POINTER(EwProgram), C.POINTER(vp), i32, vp, i32, i32,
                                      vp]),
+        "pdh_scan": (i32, [vp, vp, i64, i64, i64, i32, i32, i32, vp]),
         "pdh_ew_set_jit": (i32, [i32]),
         "pdh_ew_jit_stats": (None, [C.POINTER(i64)]),
         "pdh_ew_jit_source": (C.c_size_t, [C.POINTER(EwProgram), i32, i32, C.c_char_p, C.c_size_t]),

@@ -424,6 +424,9 @@ class PlanExecutor:
             run, src = self._map_chain(k)
         elif carve.group.confidence == "red" and any(n.op == "tl.take" for n in walk(k)):
             run, src = self._take(k)
+        elif carve.group.confidence == "red" and any(n.op == "tl.scan" for n in walk(k)):
+            # the first-occurrence max / min adjoint's prefix count: pdh_scan
+            run, src = self._scan(k)
         elif (carve.group.confidence == "red" and k.body[-1].args[0].op == "tl.reduce"
               and k.body[-1].args[0].attr("f") in ("max", "min")):
             # a bare row max / min (a softmax's max a backward joint keeps): pdh_reduce_rows_ex
@@ -1024,6 +1027,53 @@ class PlanExecutor:
             return out
 
         return run, f"take_rows x{len(takes)}" + ("" if prog is None else f" + map_chain insns={len(low.insns)}")
+
+    def _scan(self, k):
+        """A red carve around one tl.scan (the reference serves it on its
+        evaluator): the scan's operand chain by pdh_map_chain (or the stored
+        param as is), the scan by pdh_scan along its dim, and the rest of the
+        carve as a map chain with the scan's result as one more leaf."""
+        scans = [n for n in walk(k) if n.op == "tl.scan"]
+        if len(scans) != 1 or any(n.op in ("tl.reduce", "tl.take", "tl.fold") for n in walk(k)):
+            raise Untranslatable("a red carve with several scans, or a scan beside a reduction / gather")
+        sc = scans[0]
+        xs = sc.args[0]
+        shape = xs.type.shape
+        ax = xs.type.names.index(sc.attr("dim"))
+        outer, inner = math.prod(shape[:ax]), math.prod(shape[ax + 1:])
+        f, rev = sc.attr("f"), bool(sc.attr("reverse", False))
+        if f not in ("sum", "max", "min", "prod", "mean"):
+            raise Untranslatable(f"tl.scan {f!r}")
+        pre = None if xs.op == "core.param" else self._map_prog(k, xs, xs.type.dims, _dense_strides(shape))
+        y = k.body[-1].args[0]
+        post = None if y is sc else self._map_prog(k, y, y.type.dims, _dense_strides(y.type.shape), extra_leaves=[sc])
+        tdt = _TORCH_DT[self.dtype]
+
+        def run(vals):
+            torch = _torch()
+            from . import kernels as K
+
+            dt = getattr(torch, tdt)
+            if pre is None:
+                x = vals[self._index(k, xs)]
+            else:
+                low, prog = pre
+                x = torch.empty(shape, device="cuda", dtype=dt)
+                K.map_chain(prog, [vals[self._index(k, b)] for b in low.bases], x)
+            s_out = K.scan(x.contiguous(), ax, f, reverse=rev)
+            if post is None:
+                return s_out
+            low2, prog2 = post
+            out = torch.empty(y.type.shape, device="cuda", dtype=dt)
+            K.map_chain(prog2, [s_out if b is sc else vals[self._index(k, b)] for b in low2.bases], out)
+            return out
+
+        src = "scan " + f + (" reverse" if rev else "") + f" along {sc.attr('dim')} [{outer} x {shape[ax]} x {inner}]"
+        if pre is not None:
+            src = f"map_chain insns={len(pre[0].insns)} + " + src
+        if post is not None:
+            src += f" + map_chain insns={len(post[0].insns)}"
+        return run, src
 
     # ------------------------------------------------------------- running
 

@@ -464,6 +464,33 @@ def reduce_rows(summand: _lib.EwProgram, nk: int, epi: _lib.EwProgram, operands:
     return out
 
 
+_SCAN = {"sum": 0, "max": 1, "min": 2, "prod": 3, "mean": 4}
+
+
+def scan(x: torch.Tensor, dim: int, f: str = "sum", *, reverse: bool = False,
+         out: torch.Tensor | None = None) -> torch.Tensor:
+    """Inclusive prefix reduce of contiguous ``x`` along ``dim`` (tl.scan):
+    sum, max, min, prod or mean (running count); ``reverse`` folds suffixes."""
+    _require_cuda(x)
+    if x.dtype not in _DT:
+        raise ValueError(f"scan stores f32, bf16 or f16 (got {x.dtype})")
+    if f not in _SCAN:
+        raise ValueError(f"scan reducer {f!r} (sum, max, min, prod, mean)")
+    if not x.is_contiguous():
+        raise ValueError("scan takes a contiguous tensor")
+    dim = dim % x.dim()
+    y = torch.empty_like(x) if out is None else out
+    if y.shape != x.shape or y.dtype != x.dtype or not y.is_contiguous():
+        raise ValueError("out must match x's shape and element type, contiguous")
+    if x.numel() == 0:
+        return y
+    outer = math.prod(x.shape[:dim])
+    inner = math.prod(x.shape[dim + 1:])
+    _lib.call("pdh_scan", _ptr(x), _ptr(y), outer, x.shape[dim], inner, _DT[x.dtype], _SCAN[f],
+              1 if reverse else 0, C.c_void_p(_stream()))
+    return y
+
+
 def pick_decode_splits(groups: int, s: int, cus: int | None = None) -> int:
     """Splits so the (batch x kv-head x split) grid covers the chip ~8 deep,
     with at least 256 keys per split."""

@@ -13,13 +13,12 @@ templates), over the vocabulary this backend reads:
   tl.pointwise   the derivative of each numpy marker (dsl/derivative.py's
                  table restated per marker below)
   tl.reduce      sum -> broadcast; mean -> broadcast / N;
-                 max / min -> the cotangent split over the positions that
-                 attain the extremum (the reference sends it to the FIRST
-                 such position through a tl.scan, autodiff.py:635-665; the
-                 two agree whenever the extremum is attained once, and in
-                 the softmax chain the extremum's total cotangent is zero
-                 by shift invariance, so either choice leaves q, k, v's
-                 gradients unchanged)
+                 max / min -> the cotangent to the FIRST position attaining
+                 the extremum along each reduced dim, found by a tl.scan
+                 prefix count of the hits (autodiff.py:635-665)
+  tl.scan        sum -> the scan of the cotangent the other way (a prefix
+                 sum's adjoint is a suffix sum, autodiff.py:667-677); other
+                 reducers refuse
   tl.repeat_like / tl.repeat   -> sum over the added dims
   tl.stage       identity
   core.const / tl.const / tl.iota / comparisons / stop_gradient: no flow
@@ -166,12 +165,32 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
                     cnt *= x.type.dim(d).size
                 contribute(x, rl(pw("div", c, const(cnt)), x))
             elif f in ("max", "min"):
-                hit = pw("eq", x, rl(n, x))
-                ones = pw("where", hit, const(1.0), const(0.0))
-                share = pw("div", c, b.emit("tl.reduce", ones, dims=dims, f="sum"))
-                contribute(x, pw("where", hit, rl(share, x), const(0.0)))
+                # The cotangent goes to the FIRST position attaining the
+                # extremum along each reduced dim (autodiff.py:635-665): hits
+                # are eq(x, extremum); an inclusive prefix count of hits
+                # (tl.scan sum) equals 1 from the first hit up to the second,
+                # so hit * (count == 1) keeps the first alone. A multi-dim
+                # reduce is taken one dim at a time, innermost link last.
+                links, src = [], x
+                for i, name in enumerate(dims):
+                    dst = n if i == len(dims) - 1 else b.emit("tl.reduce", src, dims=(name,), f=f)
+                    links.append((src, dst, name))
+                    src = dst
+                back = c
+                for src, dst, name in reversed(links):
+                    hit = pw("eq", src, rl(dst, src))
+                    count = b.emit("tl.scan", pw("where", hit, const(1.0), const(0.0)), dim=name, f="sum")
+                    first = pw("mul", hit, pw("eq", count, const(1.0)))
+                    back = pw("mul", first, rl(back, src))
+                contribute(x, back)
             else:
                 raise NotImplementedError(f"tl.reduce {f!r} has no adjoint rule here")
+        elif op == "tl.scan":
+            if n.attr("f") != "sum":
+                raise NotImplementedError(f"tl.scan {n.attr('f')!r} has no adjoint rule (only scan sum)")
+            rev = not n.attr("reverse", False)
+            extra = {"reverse": True} if rev else {}
+            contribute(n.args[0], b.emit("tl.scan", c, dim=n.attr("dim"), f="sum", **extra))
         elif op == "tl.repeat_like":
             x, like = n.args
             added = tuple(d.name for d in like.type.dims if not x.type.has(d.name))

@@ -6,6 +6,8 @@ emit and consume (packages/tensorlib/src/pdum/tl/dialect.py:115-487):
   core.param / core.const / core.tuple / core.yield
   tl.pointwise  f=<marker>      operands aligned BY NAME; scalars broadcast
   tl.reduce     f, dims         sum | max | min | prod | mean (mean = sum / N)
+  tl.scan       f, dim[, reverse]  inclusive prefix reduce along one dim (the
+                                dim keeps its domain); reverse folds suffixes
   tl.repeat_like x, like        adds like's missing dims (stride-0 broadcast)
   tl.repeat     name, extent    adds one stride-0 dim
   tl.split      name, parts     x -> (outer .. inner) blocking, x = sum w_j i_j
@@ -68,6 +70,20 @@ def _r_reduce(args, at, regions):
     for d in dims:
         x.dim(d)
     return TensorType(tuple(d for d in x.dims if d.name not in dims))
+
+
+def _r_scan(args, at, regions):
+    """Inclusive prefix reduce along ONE dim (compute.py:318-350 in the
+    reference): out[.., t, ..] folds x[.., start..t, ..]; a mean divides by the
+    running count. ``reverse=True`` folds the suffix x[.., t..stop, ..] instead
+    (the reference spells it flip . scan . flip)."""
+    (x,) = args
+    if at["f"] not in REDUCERS:
+        raise TypeError(f"unknown reducer {at['f']!r}")
+    if not isinstance(at["dim"], str):
+        raise TypeError("tl.scan folds exactly one dim (pass its name)")
+    x.dim(at["dim"])
+    return TensorType(x.dims)
 
 
 def _r_repeat_like(args, at, regions):
@@ -244,6 +260,7 @@ OPS: dict[str, OpDef] = {
     "core.yield": OpDef("core.yield", _r_yield),
     "tl.pointwise": OpDef("tl.pointwise", _r_pointwise),
     "tl.reduce": OpDef("tl.reduce", _r_reduce),
+    "tl.scan": OpDef("tl.scan", _r_scan),
     "tl.repeat_like": OpDef("tl.repeat_like", _r_repeat_like),
     "tl.repeat": OpDef("tl.repeat", _r_repeat),
     "tl.split": OpDef("tl.split", _r_split),

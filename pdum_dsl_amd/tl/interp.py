@@ -125,6 +125,22 @@ def run_region(region: Region, values: list):
                 fn, ident = _RED[f]
                 out = fn.reduce(arr, axis=axes) if ident is None else fn.reduce(arr, axis=axes, initial=ident)
             return Field(np.asarray(out), tuple(d for d in x.dims if d.name not in dims))
+        if op == "tl.scan":  # ufunc accumulate along the dim, as compute.py:340-350
+            x = ev(n.args[0])
+            ax = x.names.index(n.attr("dim"))
+            f = n.attr("f")
+            arr = x.arr.astype(np.float64) if x.arr.dtype == bool else x.arr
+            if n.attr("reverse", False):
+                arr = np.flip(arr, axis=ax)
+            fn = np.add if f == "mean" else _RED[f][0]
+            out = fn.accumulate(arr, axis=ax)
+            if f == "mean":
+                shape = [1] * arr.ndim
+                shape[ax] = arr.shape[ax]
+                out = out / np.arange(1, arr.shape[ax] + 1).reshape(shape)
+            if n.attr("reverse", False):
+                out = np.flip(out, axis=ax)
+            return Field(np.ascontiguousarray(out), x.dims)
         if op == "tl.repeat_like":
             x, like = ev(n.args[0]), ev(n.args[1])
             extra = tuple(d for d in like.dims if d.name not in x.names)
