@@ -28,7 +28,11 @@ kernels, one step per carve:
                         probabilities read by one contraction carve alone):
                         one pdh_flash_fwd launch for the pair
   red, tl.take          pdh_take_rows for the gather, the rest of the carve
-                        as a map chain; any other red carve refuses
+                        as a map chain
+  red, tl.scan          pdh_scan between two map chains; where the scan meets
+                        a reduction, a gather or another scan, the carve is
+                        split at its first scan and the operand and the rest
+                        run as nested plans. Any other red carve refuses
 
 Layout policy: every value (parameter, boundary, output) is a dense tensor in
 its IR type's dim order, so every program's strides are fixed when the
@@ -204,7 +208,7 @@ def _attention_chains(carves, region, dtype: str, merge: bool = True) -> list:
     from theirs (a projection the traffic gate dissolved into its consumer):
     those are extracted as regions and materialized first."""
     from .hip_tile import mask_to_band
-    from .tl.partition import _extract
+    from .tl.partition import extract
 
     def source(x, carve):
         cb = {id(n) for n in carve.bounds}
@@ -217,7 +221,7 @@ def _attention_chains(carves, region, dtype: str, merge: bool = True) -> list:
                 continue
             members.add(id(n))
             todo.extend(n.args)
-        sub, sb = _extract(x, members)
+        sub, sb = extract(x, members)
         return (sub, sb), sb
 
     reads: dict = {}
@@ -864,7 +868,7 @@ class PlanExecutor:
         probabilities under a softmax backward's rowsum): the summand is
         materialized by its own plan, then reduced, with the epilogue, as a
         region over k's params plus that tensor."""
-        from .tl.partition import rebuild_into
+        from .tl.fusion import rebuild_into
 
         red, x = m["reduce"], m["reduce"].args[0]
         pre = self._materialize(k, x)
@@ -1035,7 +1039,7 @@ class PlanExecutor:
         carve as a map chain with the scan's result as one more leaf."""
         scans = [n for n in walk(k) if n.op == "tl.scan"]
         if len(scans) != 1 or any(n.op in ("tl.reduce", "tl.take", "tl.fold") for n in walk(k)):
-            raise Untranslatable("a red carve with several scans, or a scan beside a reduction / gather")
+            return self._scan_split(k, scans[0])
         sc = scans[0]
         xs = sc.args[0]
         shape = xs.type.shape
@@ -1073,6 +1077,53 @@ class PlanExecutor:
             src = f"map_chain insns={len(pre[0].insns)} + " + src
         if post is not None:
             src += f" + map_chain insns={len(post[0].insns)}"
+        return run, src
+
+    def _scan_split(self, k, sc):
+        """A red carve in which a scan meets work a map chain cannot hold (a
+        reduction, a gather, further scans), split at ``sc``, its first scan
+        in program order: the scan's operand (no scan above it) is
+        materialized by a nested plan, the scan runs by pdh_scan, and the
+        rest of the carve, with the scan's result as one more param, is
+        planned again and run by a nested executor. Each level holds one
+        scan fewer, so the splitting ends."""
+        from .tl.fusion import rebuild_into
+        from .tl.partition import plan_model
+
+        xs = sc.args[0]
+        shape = xs.type.shape
+        ax = xs.type.names.index(sc.attr("dim"))
+        f, rev = sc.attr("f"), bool(sc.attr("reverse", False))
+        if f not in ("sum", "max", "min", "prod", "mean"):
+            raise Untranslatable(f"tl.scan {f!r}")
+        operand = None if xs.op == "core.param" else self._materialize(k, xs)
+        y = k.body[-1].args[0]
+        rest = None
+        if y is not sc:
+            b = Builder(OPS)
+            memo = {id(p): b.param(i, p.type) for i, p in enumerate(k.params)}
+            hole = memo[id(sc)] = b.param(len(k.params), sc.type)
+            params = tuple(memo[id(p)] for p in k.params) + (hole,)
+            region = Region(params=params, body=(b.emit("core.yield", rebuild_into(b, memo, y)),))
+            nested = PlanExecutor(plan_model(region, dissolve=False), region, self.dtype,
+                                  _shared=(self._packs, self._static))
+            self.nested.append(nested)
+            rest = (region, nested)
+
+        def run(vals):
+            from . import kernels as K
+
+            x = vals[self._index(k, xs)] if operand is None else operand(vals)
+            s_out = K.scan(x.contiguous(), ax, f, reverse=rev)
+            if rest is None:
+                return s_out
+            region, nested = rest
+            return nested._run({id(p): v for p, v in zip(region.params, [*vals, s_out])}, self._bad)
+
+        src = f"split at scan {f}" + (" reverse" if rev else "") + f" along {sc.attr('dim')}"
+        nested_parts = [w for w, there in (("operand", operand is not None), ("rest", rest is not None)) if there]
+        if nested_parts:
+            src += " (" + " and ".join(nested_parts) + " by nested plans)"
         return run, src
 
     # ------------------------------------------------------------- running

@@ -1,24 +1,26 @@
 """Analyses as cached facts, and measurements as a persistent ledger.
 
-Restates the reference's analysis cache
-(packages/tensorlib/src/pdum/tl/analysis.py:1-155):
+Behaviour follows the reference's analysis cache
+(packages/tensorlib/src/pdum/tl/analysis.py:1-155): an analysis is declared
+as name@version over a function; calling it yields a ``Fact`` keyed by the
+analysis, its inputs' content and its keyword parameters; a Fact passed as
+an input contributes its key and hands the function its value; a
+``ledger=True`` analysis is a MEASUREMENT whose plain-JSON value persists
+across sessions; inside ``no_reanalysis()`` every miss raises. There is no
+invalidation: regions are immutable and content-addressed, so a changed
+program is a different key.
 
-  * an ``Analysis`` is declared as name@version over a function; calling it
-    on inputs yields a ``Fact`` whose key is the sha256 of the fingerprint,
-    the canonical inputs and the keyword parameters (analysis.py:95-123);
-  * inputs canonicalize by content: a Fact contributes its KEY (so a fact
-    derived from another never recomputes its prefix), IR regions and nodes
-    their content key, plain data structurally, ndarrays by dtype, shape and
-    a digest of their bytes; anything else refuses (analysis.py:52-82);
-  * ``ledger=True`` marks a MEASUREMENT: its value must be plain JSON data
-    and it is recorded in ``LEDGER``, which ``save_ledger`` / ``load_ledger``
-    round-trip through a JSON file, so an identically keyed measurement is
-    never taken twice, across sessions too (analysis.py:126-155);
-  * ``no_reanalysis()`` is the warmth law: inside it, any cache miss raises
-    (the reference forbids the ``analysis.miss`` event, analysis.py:121-124).
+The design here is this module's own:
 
-There is no invalidation: regions are immutable and content-addressed, so a
-changed program is a different key.
+  * keys are the sha256 of a typed token stream (``_Digest``): each input is
+    walked once and written as tag, length and payload, so no intermediate
+    structure is built and no two differently typed inputs share a key;
+  * one ``_FactStore`` holds the facts, the measurement subset, the miss
+    count and the warm-loop depth;
+  * the ledger file is JSON Lines: a header line naming the format, then
+    one measurement per line, sorted by key, written to a temporary file
+    and renamed over the target, so an interrupted save never leaves half a
+    ledger. Loading never replaces a fact already held in this session.
 """
 
 from __future__ import annotations
@@ -26,11 +28,16 @@ from __future__ import annotations
 import contextlib
 import hashlib
 import json
+import math
+import os
+import struct
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Callable
 
 import numpy as np
+
+_LEDGER_HEADER = {"ledger": "pdum_dsl_amd.measurements", "format": 1}
 
 
 class Reanalysis(RuntimeError):
@@ -47,38 +54,88 @@ class Fact:
     value: object
 
 
-_CACHE: dict[str, Fact] = {}
-LEDGER: dict[str, Fact] = {}  # the measurement subset: what save/load persist
-_FORBID = [0]  # nesting depth of no_reanalysis()
-MISSES = [0]  # total misses this process (computations performed)
+class _Digest:
+    """sha256 over (tag, length, payload) records; ``add`` walks one value."""
+
+    def __init__(self) -> None:
+        self._h = hashlib.sha256()
+
+    def record(self, tag: bytes, payload: bytes = b"") -> None:
+        self._h.update(tag + struct.pack("<Q", len(payload)) + payload)
+
+    def add(self, x) -> None:
+        if isinstance(x, Fact):
+            self.record(b"fact", x.key.encode())
+        elif isinstance(getattr(x, "key", None), bytes):  # IR regions and nodes carry content keys
+            self.record(b"ir", x.key)
+        elif x is None:
+            self.record(b"none")
+        elif isinstance(x, (bool, np.bool_)):
+            self.record(b"bool", b"1" if x else b"0")
+        elif isinstance(x, (int, np.integer)):
+            self.record(b"int", str(int(x)).encode())
+        elif isinstance(x, (float, np.floating)):
+            v = float(x)
+            self.record(b"float", b"nan" if math.isnan(v) else v.hex().encode())
+        elif isinstance(x, str):
+            self.record(b"str", x.encode("utf-8", "surrogatepass"))
+        elif isinstance(x, (bytes, bytearray)):
+            self.record(b"bytes", bytes(x))
+        elif isinstance(x, (tuple, list)):
+            self.record(b"seq", str(len(x)).encode())
+            for e in x:
+                self.add(e)
+        elif isinstance(x, (set, frozenset)):
+            parts = sorted(_digest_of(e) for e in x)  # order-free: members by their own digests
+            self.record(b"set", b"".join(parts))
+        elif isinstance(x, dict):
+            self.record(b"map", str(len(x)).encode())
+            for k in sorted(x, key=lambda k: (type(k).__name__, str(k))):
+                self.add(k)
+                self.add(x[k])
+        elif isinstance(x, np.ndarray):
+            a = np.ascontiguousarray(x)
+            self.record(b"array", f"{a.dtype.str}{a.shape}".encode())
+            self._h.update(a.tobytes())
+        else:
+            raise TypeError(
+                f"an analysis input must be content-keyable (a Fact, an IR region or node, plain data or an "
+                f"ndarray), not {type(x).__name__}: without a content key the cache cannot tell two calls apart"
+            )
+
+    def hexdigest(self) -> str:
+        return self._h.hexdigest()
 
 
-def _canon(x):
-    """A stable content-addressed shape for one analysis input."""
-    if isinstance(x, Fact):
-        return ("fact", x.key)
-    k = getattr(x, "key", None)
-    if isinstance(k, bytes):
-        return ("ir", k.hex())
-    if x is None or isinstance(x, bool):
-        return ("lit", x)
-    if isinstance(x, (str, int, float)):
-        return ("lit", x)
-    if isinstance(x, bytes):
-        return ("bytes", x.hex())
-    if isinstance(x, (tuple, list)):
-        return ("seq", tuple(_canon(e) for e in x))
-    if isinstance(x, (set, frozenset)):
-        return ("set", tuple(sorted(repr(_canon(e)) for e in x)))
-    if isinstance(x, dict):
-        return ("map", tuple(sorted((str(kk), _canon(v)) for kk, v in x.items())))
-    if isinstance(x, np.ndarray):
-        a = np.ascontiguousarray(x)
-        return ("arr", str(a.dtype), a.shape, hashlib.sha256(a.tobytes()).hexdigest())
-    raise TypeError(
-        f"analysis inputs must be content-keyable (Fact, Region/Node, plain data, ndarray); got "
-        f"{type(x).__name__}: an unkeyable input has no honest cache identity"
-    )
+def _digest_of(x) -> bytes:
+    d = _Digest()
+    d.add(x)
+    return d._h.digest()
+
+
+class _FactStore:
+    """Every fact this process holds; ``measured`` is the ledger subset."""
+
+    def __init__(self) -> None:
+        self.facts: dict = {}
+        self.measured: dict = {}
+        self.misses = 0
+        self.warm_depth = 0
+
+    def adopt(self, fact: Fact, measured: bool) -> Fact:
+        held = self.facts.setdefault(fact.key, fact)
+        if measured:
+            self.measured.setdefault(fact.key, held)
+        return held
+
+
+_STORE = _FactStore()
+LEDGER = _STORE.measured  # the measurement facts save_ledger writes (read-only view by convention)
+
+
+def misses() -> int:
+    """Computations performed so far in this process (cache misses)."""
+    return _STORE.misses
 
 
 @dataclass(frozen=True)
@@ -91,35 +148,41 @@ class Analysis:
     fn: Callable
     ledger: bool = False
 
+    @property
+    def tag(self) -> str:
+        return f"{self.name}@v{self.version}"
+
     def key_of(self, *inputs, **params) -> str:
-        payload = ("analysis", self.name, self.version, _canon(inputs), _canon(params))
-        return hashlib.sha256(repr(payload).encode()).hexdigest()
+        d = _Digest()
+        d.record(b"analysis", self.tag.encode())
+        d.add(list(inputs))
+        d.add(params)
+        return d.hexdigest()
 
     def __call__(self, *inputs, **params) -> Fact:
         key = self.key_of(*inputs, **params)
-        hit = _CACHE.get(key)
-        if hit is not None:
-            return hit
-        if _FORBID[0]:
-            raise Reanalysis(f"analysis miss inside no_reanalysis(): {self.name}@v{self.version}")
-        MISSES[0] += 1
-        args = tuple(x.value if isinstance(x, Fact) else x for x in inputs)
-        value = self.fn(*args, **params)
+        held = _STORE.facts.get(key)
+        if held is not None:
+            return held
+        if _STORE.warm_depth:
+            raise Reanalysis(f"{self.tag} missed inside no_reanalysis() (key {key[:12]})")
+        _STORE.misses += 1
+        value = self.fn(*(x.value if isinstance(x, Fact) else x for x in inputs), **params)
         if self.ledger:
-            # measurements are records: normalized through JSON now, so the
-            # in-session value and a reloaded one are identical
-            try:
-                value = json.loads(json.dumps(value))
-            except TypeError as exc:
-                raise TypeError(
-                    f"ledger analysis {self.name!r} produced a non-JSON value ({type(value).__name__}): "
-                    "measurements are plain data"
-                ) from exc
-        fact = Fact(key, f"{self.name}@v{self.version}", value)
-        _CACHE[key] = fact
-        if self.ledger:
-            LEDGER[key] = fact
-        return fact
+            value = _as_record(self.tag, value)
+        return _STORE.adopt(Fact(key, self.tag, value), self.ledger)
+
+
+def _as_record(tag: str, value):
+    """A measurement's value as it will read back from the ledger file (tuples
+    become lists): the in-session fact and a reloaded one are identical."""
+    try:
+        return json.loads(json.dumps(value, allow_nan=False))
+    except (TypeError, ValueError) as exc:
+        raise TypeError(
+            f"measurement {tag} returned {type(value).__name__}, which is not plain data "
+            f"(JSON: dicts, lists, strings, finite numbers, booleans, null): {exc}"
+        ) from exc
 
 
 def defanalysis(name: str, version: int = 1, *, ledger: bool = False):
@@ -135,40 +198,60 @@ def defanalysis(name: str, version: int = 1, *, ledger: bool = False):
 @contextlib.contextmanager
 def no_reanalysis():
     """Everything inside must be a cache hit; a miss raises ``Reanalysis``."""
-    _FORBID[0] += 1
+    _STORE.warm_depth += 1
     try:
         yield
     finally:
-        _FORBID[0] -= 1
+        _STORE.warm_depth -= 1
 
 
 def save_ledger(path) -> int:
-    """Write the measurement facts to ``path`` as sorted JSON; returns the count.
-    Non-ledger facts never persist (they are rebuilt from their keys)."""
-    data = {k: {"analysis": f.analysis, "value": f.value} for k, f in sorted(LEDGER.items())}
-    Path(path).write_text(json.dumps(data, indent=1, sort_keys=True))
-    return len(data)
+    """Write every measurement to ``path`` (JSON Lines, see the module
+    docstring); returns how many. Other facts never persist: they are
+    recomputed from their inputs."""
+    path = Path(path)
+    lines = [json.dumps(_LEDGER_HEADER, sort_keys=True)]
+    for key in sorted(_STORE.measured):
+        f = _STORE.measured[key]
+        lines.append(json.dumps({"key": key, "analysis": f.analysis, "value": f.value}, sort_keys=True))
+    tmp = path.with_name(path.name + ".partial")
+    tmp.write_text("\n".join(lines) + "\n")
+    os.replace(tmp, path)
+    return len(lines) - 1
+
+
+def read_ledger(path) -> list:
+    """The measurement records of a ledger file, as Facts (nothing cached)."""
+    rows = [ln for ln in Path(path).read_text().splitlines() if ln.strip()]
+    if not rows or json.loads(rows[0]) != _LEDGER_HEADER:
+        raise ValueError(f"{path} is not a measurement ledger (its first line must be {json.dumps(_LEDGER_HEADER)})")
+    out = []
+    for n, ln in enumerate(rows[1:], start=2):
+        rec = json.loads(ln)
+        if not isinstance(rec, dict) or set(rec) != {"key", "analysis", "value"}:
+            raise ValueError(f"{path}:{n}: a ledger record holds exactly key, analysis and value")
+        out.append(Fact(rec["key"], rec["analysis"], rec["value"]))
+    return out
 
 
 def load_ledger(path) -> int:
-    """Seed the cache from a saved ledger: a reloaded measurement is a hit and
-    is never taken again. Loading is a cold act (do it outside warm loops)."""
-    data = json.loads(Path(path).read_text())
-    for key, rec in data.items():
-        fact = Fact(key, rec["analysis"], rec["value"])
-        LEDGER[key] = fact
-        _CACHE[key] = fact
-    return len(data)
+    """Seed the cache from a saved ledger, so a reloaded measurement is a hit
+    and is never taken again; returns how many records the file holds.
+    A measurement already taken in this session is kept."""
+    facts = read_ledger(path)
+    for f in facts:
+        _STORE.adopt(f, measured=True)
+    return len(facts)
 
 
 def clear(ledger_too: bool = False) -> None:
-    """Drop cached facts (tests use this to start cold)."""
-    _CACHE.clear()
+    """Drop cached facts; measurements stay hits unless ``ledger_too``."""
+    _STORE.facts.clear()
     if ledger_too:
-        LEDGER.clear()
+        _STORE.measured.clear()
     else:
-        _CACHE.update(LEDGER)  # measurements stay hits
+        _STORE.facts.update(_STORE.measured)
 
 
-__all__ = ["Analysis", "Fact", "LEDGER", "Reanalysis", "clear", "defanalysis", "load_ledger", "no_reanalysis",
-           "save_ledger"]
+__all__ = ["Analysis", "Fact", "LEDGER", "Reanalysis", "clear", "defanalysis", "load_ledger", "misses",
+           "no_reanalysis", "read_ledger", "save_ledger"]

@@ -1,50 +1,63 @@
-"""Whole-model plans: carve a region into template groups (the reference's
-packages/tensorlib/src/pdum/tl/partition.py, ``carve_model`` and
-``plan_model``).
+"""Whole-model plans: one model region carved into template-shaped groups.
 
-**The anchor-and-absorb partition** (partition.py:1-24, 458-582), restated:
-every reduce must live in some claim, and claims run most-specific first —
-flash compositions (three reduces), then bare row normalizations (two), then
-row statistics, then single-reduce contractions. Contraction claims absorb
-both ways: epilogues walk downstream while the root has exactly one
-consumer; operand prologues walk upstream through the recompute-exact
-vocabulary while every consumer lies inside the claim. A fork ends a walk
-and leaves a materialized boundary. A claim whose interior would be
-consumed outside it is refused (v1 groups have one output), except that a
-flash claim may surface its row statistics as ARTIFACTS and mark the other
-leaked values' cones as TRAVEL (copies consumers re-derive). The unclaimed
-residue splits into per-root components (map chains where pure map work,
-red groups where not). Finally claims whose root only feeds other claims
-DISSOLVE into them when re-deriving per tile moves fewer elements than
-materializing (the traffic gate), to fixpoint. Every claim is rebuilt as a
-canonical region (boundaries become params in first-use order) so repeated
-layers share one content key, and ``plan_model`` plans each distinct kernel
-once.
+Behaviour follows the reference's packages/tensorlib/src/pdum/tl/partition.py
+(``carve_model`` :458-582, ``plan_model`` :586-607); the gpt2 carve counts of
+its tests/test_partition.py:38-49 pin it. The implementation is this
+module's own: a dependence index built once (``_Deps``), a carver object
+that owns the ownership / travel state and climbs a ladder of claim rungs,
+a residue split by reverse-topological labelling, and a canonical extraction
+that numbers params in the order its own rebuild reaches them.
 
-**The MI355X joint claim.** The reference carves the autodiff joint of flash attention into a
-flash-with-artifacts group plus contraction carves for dV, dQ, dK and the
-row statistic D (partition.py:476-557), each compiled separately. On MI355X
-the whole joint runs as ONE forward-with-artifacts kernel and ONE fused
-backward launch, so this partitioner claims the joint whole, as the carve
-``flash-joint``:
+What a carve is. A claim is (root, members, artifacts): the members are the
+interior model nodes one kernel computes, the root the value it
+materializes, artifacts extra statistics it surfaces. Zero-cost views
+(constants, renames, broadcasts) are shared: they join every claim that
+reads them and are re-emitted per kernel, so they never block a claim and a
+claim's inputs are always real values.
 
-  * the joint's first yield must be a ``flash`` composition (fusion.match_flash
-    over q, k, v params);
-  * the rest of the yield must be exactly the vector-Jacobian product of that
-    forward — checked by REGENERATING it with ``autodiff.grad`` from the
-    extracted forward and comparing content keys, node for node (the same
-    recognize-by-regeneration law the HIP seat applies to flash tiles);
-  * its certificate is proved-exact (the key is reached), and the forward's
-    own flash certificate rides along in ``Group.params``.
+The ladder (most specific first, so a taller chain keeps its anchor):
 
-``plan_model`` tries that claim first; any other region goes through
-``carve_model``. What no row covers is a red carve with the reason — plans
-are data, never exceptions.
+  flash          a three-reduce attention composition over any q, k, v
+                 values. If an inner value is read outside, the claim
+                 survives only by surfacing its row statistics (m, den) and
+                 by marking the other leaked values' producer cones as TRAVEL
+                 (copies a consumer re-derives); a cone that reduces over a
+                 swept dim, or holds anything but map work, cannot travel;
+  row-norm       a bare softmax over any input;
+  row-stat       a layernorm-shaped statistics chain, its scale-shift tail
+                 absorbed downstream;
+  contraction    a sum / mean over one or two dims of a product (or of a
+                 plain operand): elementwise prologues are absorbed upstream
+                 while every reader of the absorbed value is already inside,
+                 elementwise epilogues downstream while the output has a
+                 single reader.
+
+A claim is admitted only when none of its members is owned already (travel
+copies excepted) and no member other than its root is read outside it: one
+kernel has one output. The unowned rest is split per weakly connected
+component into single-output parts, and a claim whose root only feeds other
+claims may then dissolve into them (its members become travel copies) when
+re-deriving it per consumer moves fewer elements than writing and reading it
+back. ``dissolve=False`` keeps every root materialized.
+
+The MI355X joint claim. The reference carves the autodiff joint of flash
+attention into a flash-with-artifacts group plus contraction carves for dV,
+dQ, dK and the row statistic D (partition.py:476-557). On MI355X the whole
+joint runs as ONE forward-with-artifacts kernel and ONE fused backward
+launch, so ``plan_model`` first tries to claim a joint whole, as the carve
+``flash-joint``: its first yield must be a ``flash`` composition
+(fusion.match_flash over q, k, v params) and the rest of the yield exactly
+the vector-Jacobian product of that forward, checked by REGENERATING it with
+``autodiff.grad`` and comparing content keys node for node. Plans are data:
+what no rung covers becomes a red carve with its reason, never an exception.
 """
 
 from __future__ import annotations
 
+import itertools
+from collections import Counter, defaultdict
 from dataclasses import dataclass, field
+from typing import NamedTuple
 
 from .autodiff import grad, region_names
 from .certify import Certificate
@@ -53,32 +66,30 @@ from .fusion import Group, contract_core, forest_is_closed, match_flash, match_r
 from .fusion import plan_region, rebuild_into
 from .ir import Builder, Region, walk
 
-_CONSTS = ("core.const", "tl.const")
-# zero-cost views: shared by claims, duplicated at rebuild (partition.py:47-53)
-_FREE = _CONSTS + ("tl.rename", "tl.repeat_like", "tl.repeat")
-_EPILOGUE = ("tl.pointwise", "tl.repeat_like")  # what an epilogue walk may absorb
-_COMPUTE = ("tl.pointwise", "tl.iota")  # what a prologue walk may absorb
-_SINKS = ("core.param", "core.yield", "core.tuple")
+_CONSTS = frozenset(("core.const", "tl.const"))
+# zero-cost views: shared between claims and re-emitted by every kernel that reads them
+_VIEWS = _CONSTS | {"tl.rename", "tl.repeat_like", "tl.repeat"}
+_TAIL = frozenset(("tl.pointwise", "tl.repeat_like"))  # what extends a claim downstream
+_RECOMPUTE = frozenset(("tl.pointwise", "tl.iota"))  # what extends a claim upstream, and may travel
 
 
 @dataclass(frozen=True)
 class Carve:
-    """One carved group (partition.py:58-70): the canonical kernel, the plan
-    the recognizer produced for it, and the claim's footprint in the model."""
+    """One carved group: the canonical kernel, the plan the recognizer made
+    for it, and the claim's footprint in the model."""
 
     kernel: Region = field(repr=False)
     group: Group
-    nodes: int  # interior (non-free) model nodes this carve claims
+    nodes: int  # interior model nodes counted to this carve (a travel copy counts once, where first held)
     root_op: str
     root: object = field(default=None, repr=False)
-    bounds: tuple = field(default=(), repr=False)  # the model nodes its params bind to, in param order
-    artifacts: tuple = field(default=(), repr=False)  # surfaced statistics, tuple-yield order
+    bounds: tuple = field(default=(), repr=False)  # the model values bound to the kernel's params, in order
+    artifacts: tuple = field(default=(), repr=False)  # surfaced statistics, in tuple-yield order
 
 
 @dataclass(frozen=True)
 class ModelPlan:
-    """A whole-model plan is data (partition.py:73-85): carves in dependency
-    order, the interior node count, coverage derived."""
+    """A whole-model plan: carves, the interior node count, coverage derived."""
 
     carves: tuple
     interior: int
@@ -92,8 +103,527 @@ class ModelPlan:
         return len({c.kernel.key for c in self.carves})
 
 
-def _interior(region: Region) -> list:
-    return [n for n in walk(region) if n.op not in _FREE and n.op not in _SINKS]
+class Claim(NamedTuple):
+    """(root, members keyed by node id, surfaced artifacts)."""
+
+    root: object
+    members: dict
+    artifacts: tuple = ()
+
+
+def _is_view(n) -> bool:
+    return n.op in _VIEWS
+
+
+def _dims_of(reduce_node) -> frozenset:
+    d = reduce_node.attr("dims")
+    return frozenset((d,) if isinstance(d, str) else d)
+
+
+def _extent(t) -> int:
+    total = 1
+    for d in getattr(t, "dims", ()):
+        total *= d.size
+    return total
+
+
+def _strip_broadcast(x):
+    """A contraction operand with its broadcasts peeled off."""
+    while x.op in ("tl.repeat_like", "tl.repeat"):
+        x = x.args[0]
+    return x
+
+
+# --------------------------------------------------------- the dependence index
+
+
+class _Deps:
+    """One region's interior (program order) and every value's readers."""
+
+    def __init__(self, region: Region):
+        out = region.body[-1]
+        self.exits = {id(out)}
+        if out.args[0].op == "core.tuple":
+            self.exits.add(id(out.args[0]))
+        params = {id(p) for p in region.params}
+        self.readers: dict = defaultdict(list)
+        self.interior: list = []
+        for n in walk(region):
+            if id(n) in params:
+                continue
+            for a in n.args:
+                self.readers[id(a)].append(n)
+            if n is out or n.op == "core.tuple" or _is_view(n):
+                continue
+            self.interior.append(n)
+
+    def read_outside(self, v, inside, export=None) -> bool:
+        """Does ``v``'s value reach a reader outside ``inside``? Views inside
+        only forward the value, so their readers are examined in turn;
+        ``export`` (the claim's output) is the sanctioned way out."""
+        pending, looked = [v], set()
+        while pending:
+            x = pending.pop()
+            for r in self.readers.get(id(x), ()):
+                if r is export:
+                    continue
+                if id(r) not in inside:
+                    return True
+                if _is_view(r) and id(r) not in looked:
+                    looked.add(id(r))
+                    pending.append(r)
+        return False
+
+    def value_readers(self, v) -> list:
+        """Every reader of ``v``'s value, views included and looked through."""
+        found, pending, looked = [], [v], set()
+        while pending:
+            x = pending.pop()
+            for r in self.readers.get(id(x), ()):
+                if id(r) in looked:
+                    continue
+                looked.add(id(r))
+                found.append(r)
+                if _is_view(r):
+                    pending.append(r)
+        return found
+
+
+def _producers(root, stop, within=None) -> dict:
+    """``root`` and what it is computed from, up to (excluding) ``stop`` and
+    params; with ``within``, only nodes in it (the root always)."""
+    got, pending = {}, [root]
+    while pending:
+        n = pending.pop()
+        if id(n) in got or id(n) in stop or n.op == "core.param":
+            continue
+        if within is not None and n is not root and id(n) not in within:
+            continue
+        got[id(n)] = n
+        pending.extend(n.args)
+    return got
+
+
+def _close(members: dict, travel=()) -> dict:
+    """Add the non-constant views members read and the travel copies they
+    read, transitively: a claim's inputs are real, materialized values."""
+    pending = list(members.values())
+    while pending:
+        n = pending.pop()
+        for a in n.args:
+            if id(a) in members:
+                continue
+            if id(a) in travel or (_is_view(a) and a.op not in _CONSTS):
+                members[id(a)] = a
+                pending.append(a)
+    return members
+
+
+def _flash_shape(r):
+    """The attention composition ending at reduce ``r``:
+    sum_s softmax_s(where(mask, sum_e q*k, fill)) * v with a closed mask
+    forest and a constant fill. q, k, v are any values (the carve makes
+    them params). Returns the bindings or None."""
+    outer = contract_core(r)
+    if outer is None:
+        return None
+    probs, v, s = outer
+    sm = match_softmax(probs)
+    if sm is None or sm["s"] != s:
+        return None
+    masked = sm["sm"]
+    if masked.op != "tl.pointwise" or masked.attr("f") != "where" or len(masked.args) != 3:
+        return None
+    mask, scores, fill = masked.args
+    if fill.op not in _CONSTS or not forest_is_closed(mask):
+        return None
+    inner = contract_core(scores)
+    if inner is None:
+        return None
+    q, k, e = inner
+    qn, kn, vn = q.type.names, k.type.names, v.type.names
+    if len(qn) != 2 or kn != (s, e) or len(vn) != 2 or vn[0] != s:
+        return None
+    (t,) = [d for d in qn if d != e]
+    return {"q": q, "k": k, "v": v, "m": sm["max"], "den": sm["den"], "t": t, "s": s}
+
+
+# ------------------------------------------------------------------ the carver
+
+
+class _Carver:
+    """Ownership state of one carving: the claims made so far, the interior
+    node ids they own, and the travel copies (nodes any claim may re-derive)."""
+
+    def __init__(self, region: Region):
+        self.region = region
+        self.deps = _Deps(region)
+        self.claims: list = []
+        self.owned: set = set()
+        self.travel: dict = {}
+
+    # -- admission
+
+    def _free(self, members) -> bool:
+        return all(i not in self.owned or i in self.travel for i in members)
+
+    def _record(self, claim: Claim) -> None:
+        self.claims.append(claim)
+        self.owned.update(i for i, m in claim.members.items() if not _is_view(m))
+
+    def _admit(self, root, members: dict) -> bool:
+        """Record a single-output claim unless a member other than its root
+        (or a view or travel copy) is read outside it."""
+        _close(members)
+        for m in members.values():
+            if m is root or _is_view(m) or id(m) in self.travel:
+                continue
+            if self.deps.read_outside(m, members, root):
+                return False
+        self._record(Claim(root, members))
+        return True
+
+    def _admit_with_statistics(self, root, shape, members: dict) -> bool:
+        """A flash claim whose inner values are read outside: it surfaces its
+        row statistics, and every other value read outside must be
+        re-derivable by its readers (map work, or reductions over neither of
+        the claim's swept dims); those producer cones become travel copies."""
+        _close(members)
+        stats = {id(shape["m"]), id(shape["den"])}
+        swept = {shape["t"], shape["s"]}
+        copies: dict = {}
+        for m in list(members.values()):
+            if m is root or id(m) in stats or not self.deps.read_outside(m, members, root):
+                continue
+            value = m
+            while _is_view(value) and value.args:  # a leaked view: the value it forwards
+                value = value.args[0]
+            if value is root or id(value) in stats or id(value) not in members:
+                continue
+            cone = _copyable(value, members, stats, swept)
+            if cone is None:
+                return False
+            copies.update(cone)
+        self._record(Claim(root, members, (shape["m"], shape["den"])))
+        self.travel.update(copies)
+        return True
+
+    # -- growth
+
+    def _grow_up(self, members: dict) -> dict:
+        """Prologue absorption: unowned elementwise producers join while
+        every reader of their value is already inside; travel copies and
+        views join unconditionally. Membership only grows and the condition
+        only gets easier, so rounds to a fixpoint give the least closure."""
+        while True:
+            _close(members, self.travel)
+            joining = {}
+            for m in list(members.values()):
+                for a in m.args:
+                    if id(a) in members or id(a) in joining or id(a) in self.owned or a.op not in _RECOMPUTE:
+                        continue
+                    if not self.deps.read_outside(a, members):
+                        joining[id(a)] = a
+            if not joining:
+                return members
+            members.update(joining)
+
+    def _grow_down(self, root, members: dict):
+        """Epilogue absorption: while the output's single reader is unowned
+        elementwise work, it joins and becomes the output. A broadcast of the
+        output onto another lattice ends the walk (that is another claim's
+        operand); a side operand broadcast onto a member's lattice rides along
+        (its value stays an input). Returns the final output."""
+        while True:
+            readers = self.deps.readers.get(id(root), ())
+            if len(readers) != 1:
+                return root
+            (nxt,) = readers
+            if nxt.op not in _TAIL or id(nxt) in self.owned or id(nxt) in self.deps.exits:
+                return root
+            if nxt.op == "tl.repeat_like" and nxt.args[0] is root:
+                return root
+            for side in nxt.args:
+                if side.op == "tl.repeat_like" and id(side) not in members and id(side.args[1]) in members:
+                    members[id(side)] = side
+            members[id(nxt)] = nxt
+            root = nxt
+
+    # -- the rungs (each called on unowned interior nodes in program order)
+
+    def rung_flash(self, n) -> None:
+        if n.op != "tl.reduce":
+            return
+        shape = _flash_shape(n)
+        if shape is None:
+            return
+        cone = _producers(n, {id(shape["q"]), id(shape["k"]), id(shape["v"])})
+        if self._free(cone) and not self._admit(n, dict(cone)):
+            self._admit_with_statistics(n, shape, cone)
+
+    def rung_row_norm(self, n) -> None:
+        sm = match_softmax(n)
+        if sm is None:
+            return
+        members = _close(_producers(n, {id(sm["sm"])}), self.travel)
+        if self._free(members):
+            self._admit(n, members)
+
+    def rung_row_stat(self, n) -> None:
+        rs = match_rowstat(n)
+        if rs is None:
+            return
+        members = _close(_producers(n, {id(rs["x"])}), self.travel)
+        if self._free(members):
+            self._admit(self._grow_down(n, members), members)
+
+    def rung_contraction(self, n) -> None:
+        if n.op != "tl.reduce" or n.attr("f") not in ("sum", "mean") or n.attr("zero") is not None:
+            return
+        dims = _dims_of(n)
+        if len(dims) not in (1, 2):
+            return
+        body = n.args[0]
+        product = body.op == "tl.pointwise" and body.attr("f") == "mul" and len(body.args) == 2
+        operands = [_strip_broadcast(x) for x in body.args] if product else [body]
+        for x in operands:  # every operand carries every contracted dim
+            if not hasattr(x.type, "dims") or not all(x.type.has(d) for d in dims):
+                return
+        kept = set()
+        for x in operands:
+            kept.update(nm for nm in x.type.names if nm not in dims)
+        if set(n.type.names) != kept:
+            return
+        seed = {id(n): n}
+        if product:  # a plain sum leaves its operand to absorption: it may be another claim's output
+            seed[id(body)] = body
+        if any(i in self.owned for i in seed):
+            return
+        members = self._grow_up(seed)
+        self._admit(self._grow_down(n, members), members)
+
+    # -- what the rungs leave
+
+    def split_residue(self) -> None:
+        rest = [n for n in self.deps.interior if id(n) not in self.owned]
+        for comp in _components(rest):
+            self._split(comp)
+
+    def _split(self, comp: list) -> None:
+        """Single-output parts of one residue component (``comp`` in program
+        order). Walking readers before producers, a node is an output when
+        something outside the component reads it, or when its readers inside
+        belong to different parts; otherwise it joins its readers' part.
+        Each part then takes the views and travel copies it reads."""
+        inside = {id(n) for n in comp}
+        part: dict = {}
+        for n in reversed(comp):
+            readers = self.deps.readers.get(id(n), ())
+            if any(id(r) not in inside for r in readers):
+                part[id(n)] = id(n)
+                continue
+            labels = {part[id(r)] for r in readers if id(r) in part}
+            if len(labels) == 1:
+                part[id(n)] = labels.pop()
+            elif labels:
+                part[id(n)] = id(n)
+        groups: dict = {}
+        for n in comp:
+            if id(n) in part:
+                groups.setdefault(part[id(n)], {})[id(n)] = n
+        for n in comp:
+            if part.get(id(n)) == id(n):
+                self._record(Claim(n, _close(groups[id(n)], self.travel)))
+
+    def let_roots_travel(self) -> None:
+        """A claim whose output only feeds other claims dissolves into them
+        (its members become travel copies each reader re-derives) when all
+        of: it surfaces no artifacts; its members are map work and
+        reductions; none of its reductions runs over a dim a reading claim
+        sweeps; nothing the region yields reads it; and re-deriving moves
+        fewer elements than materializing (2 x output elements, a write and a
+        read back, against readers x the elements of its inputs). Candidates
+        are tried fewest reductions first; repeated to a fixpoint."""
+        while True:
+            pick = self._traveller()
+            if pick is None:
+                return
+            gone = self.claims.pop(pick)
+            self.travel.update(gone.members)
+            self.travel[id(gone.root)] = gone.root
+            for c in self.claims:
+                _close(c.members, self.travel)
+
+    def _traveller(self):
+        holders: dict = defaultdict(set)
+        for ci, c in enumerate(self.claims):
+            for i in c.members:
+                holders[i].add(ci)
+        swept = [frozenset().union(*(_dims_of(m) for m in c.members.values()
+                                     if m.op == "tl.reduce" and id(m) not in self.travel))
+                 for c in self.claims]
+        reduces = [sum(m.op == "tl.reduce" for m in c.members.values()) for c in self.claims]
+        for ci in sorted(range(len(self.claims)), key=reduces.__getitem__):
+            if self._may_travel(ci, holders, swept):
+                return ci
+        return None
+
+    def _may_travel(self, ci, holders, swept) -> bool:
+        root, members, arts = self.claims[ci]
+        if root is None or arts:
+            return False
+        for m in members.values():
+            if id(m) not in self.travel and not (_is_view(m) or m.op in _RECOMPUTE or m.op == "tl.reduce"):
+                return False
+        readers = self.deps.value_readers(root)
+        if not readers:
+            return False
+        eaters: set = set()
+        for r in readers:
+            if id(r) in self.deps.exits:
+                return False
+            if _is_view(r):
+                continue
+            who = holders.get(id(r), set()) - {ci}
+            if not who:
+                return False
+            eaters |= who
+        mine = frozenset().union(*(_dims_of(m) for m in members.values() if m.op == "tl.reduce"))
+        if any(mine & swept[cj] for cj in eaters):
+            return False
+        inputs = {id(a): a for m in members.values() for a in m.args if id(a) not in members and a.op not in _CONSTS}
+        return 2 * _extent(root.type) > len(eaters) * sum(_extent(a.type) for a in inputs.values())
+
+
+def _copyable(x, members, stats, swept):
+    """``x``'s producers inside the claim, stopped at the statistics and at
+    the claim's inputs, if a reader can re-derive them per tile: views, map
+    work and reductions over none of the swept dims. Returns them or None."""
+    cone, pending = {}, [x]
+    while pending:
+        n = pending.pop()
+        if id(n) in cone or id(n) in stats or id(n) not in members:
+            continue
+        if n.op == "tl.reduce":
+            if _dims_of(n) & swept:
+                return None
+        elif not (_is_view(n) or n.op in _RECOMPUTE):
+            return None
+        cone[id(n)] = n
+        pending.extend(n.args)
+    return cone
+
+
+def _components(nodes: list) -> list:
+    """Weakly connected components of ``nodes`` under argument edges, each
+    listed in program order, ordered by their earliest node."""
+    index = {id(n): i for i, n in enumerate(nodes)}
+    parent = list(range(len(nodes)))
+
+    def find(i):
+        while parent[i] != i:
+            parent[i] = parent[parent[i]]
+            i = parent[i]
+        return i
+
+    for i, n in enumerate(nodes):
+        for a in n.args:
+            j = index.get(id(a))
+            if j is not None:
+                ri, rj = find(i), find(j)
+                if ri != rj:
+                    parent[max(ri, rj)] = min(ri, rj)
+    comps: dict = {}
+    for i, n in enumerate(nodes):
+        comps.setdefault(find(i), []).append(n)
+    return [comps[k] for k in sorted(comps)]
+
+
+# ---------------------------------------------------------------- extraction
+
+
+def extract(outputs, members):
+    """A claim as a standalone canonical region. The rebuild walks each
+    output's arguments left to right, depth first; a value outside
+    ``members`` (any container of node ids) becomes the next param the first
+    time the walk reaches it, constants are re-emitted. Identical claims
+    from different layers therefore rebuild to one content key. One output
+    is yielded bare, several as a tuple. Returns (region, bounds): bounds
+    are the model values bound to the params, in order."""
+    outputs = (outputs,) if not isinstance(outputs, (tuple, list)) else tuple(outputs)
+    bounds, seen = [], set()
+    for out in outputs:  # the rebuild's own visiting order, with an explicit stack of argument iterators
+        if id(out) in seen:
+            continue
+        seen.add(id(out))
+        frames = [iter(out.args)]
+        while frames:
+            a = next(frames[-1], None)
+            if a is None:
+                frames.pop()
+            elif id(a) not in seen:
+                seen.add(id(a))
+                if id(a) in members:
+                    frames.append(iter(a.args))
+                elif a.op not in _CONSTS:
+                    bounds.append(a)
+    b = Builder(OPS)
+    memo = {id(x): b.param(i, x.type) for i, x in enumerate(bounds)}
+    params = tuple(memo[id(x)] for x in bounds)
+    built = tuple(rebuild_into(b, memo, o) for o in outputs)
+    y = built[0] if len(built) == 1 else b.emit("core.tuple", *built)
+    return Region(params=params, body=(b.emit("core.yield", y),)), tuple(bounds)
+
+
+# ------------------------------------------------------------------- the API
+
+
+def carve_model(region: Region, dissolve: bool = True):
+    """The partition alone: (claims, interior_count, travel). Claims are
+    ``Claim(root, members, artifacts)`` with members keyed by node id;
+    travel holds the nodes any claim may re-derive. ``dissolve=False`` keeps
+    every claim's root a materialized value (the device executor's choice
+    for values it cannot re-derive per tile)."""
+    cv = _Carver(region)
+    for rung in (cv.rung_flash, cv.rung_row_norm, cv.rung_row_stat, cv.rung_contraction):
+        for n in cv.deps.interior:
+            if id(n) not in cv.owned:
+                rung(n)
+    cv.split_residue()
+    if dissolve:
+        cv.let_roots_travel()
+    return cv.claims, len(cv.deps.interior), cv.travel
+
+
+def plan_model(region: Region, machine=None, floor: int = 1024, dissolve: bool = True) -> ModelPlan:
+    """Carve ``region`` and plan each distinct kernel once. A flash joint is
+    claimed whole first (the fused backward's carve)."""
+    fj = match_flash_joint(region)
+    if fj is not None:
+        return _plan_joint(region, fj, machine, floor)
+    claims, interior, _travel = carve_model(region, dissolve=dissolve)
+    first_holder: dict = {}
+    for ci, c in enumerate(claims):
+        for i, m in c.members.items():
+            if not _is_view(m):
+                first_holder.setdefault(i, ci)
+    counts = Counter(first_holder.values())
+    planned: dict = {}
+    carves = []
+    for ci, (root, members, arts) in enumerate(claims):
+        if root is None:
+            ops = sorted({m.op for m in members.values() if not _is_view(m)})
+            g = Group("uncompiled", None, None, "red", reason=f"multi-output residue over {ops}")
+            carves.append(Carve(region, g, counts[ci], "residue"))
+            continue
+        kernel, bounds = extract((root, *arts), members)
+        if kernel.key not in planned:
+            planned[kernel.key] = plan_region(kernel, machine=machine, floor=floor).groups[0]
+        carves.append(Carve(kernel, planned[kernel.key], counts[ci], root.op, root, bounds, arts))
+    return ModelPlan(tuple(carves), interior)
+
+
+# ----------------------------------------------------------- the joint claim
 
 
 def match_flash_joint(region: Region):
@@ -107,23 +637,22 @@ def match_flash_joint(region: Region):
     fwd_params = region.params[:-1]
     if len(fwd_params) != 3 or seed.op != "core.param" or seed.type != out.type:
         return None
-    fwd = Region(params=fwd_params, body=(_yield(out),))
+    fwd = Region(params=fwd_params, body=(Builder(OPS).emit("core.yield", out),))
     fm = match_flash(fwd)
     if fm is None or fm["artifacts"]:
         return None
     pnames = {id(fm["q"]): "q", id(fm["k"]): "k", id(fm["v"]): "v"}
     order = tuple(pnames[id(p)] for p in fwd_params)
     names = region_names(fwd, order, ("out",))
-    # which params do the grads belong to? try every ordered subset the
-    # regenerated VJP could have been asked for (at most 3! + ... = 15)
-    for wrt in _wrt_candidates(len(grads)):
+    # which params do the grads belong to? every ordered subset of (q, k, v)
+    # of the right length is regenerated and compared (at most 6)
+    for wrt in itertools.permutations(("q", "k", "v"), len(grads)):
         rg = grad(fwd, "out", seed="dO", wrt=wrt, names=names)
         ys = rg.region.body[-1].args[0]
         rys = ys.args[1:] if ys.op == "core.tuple" else ()
         if len(rys) != len(grads):
             continue
-        # the regenerated joint's seed is a fresh param: compare against the
-        # given joint with its seed bound to the same index
+        # the regenerated joint's seed is a fresh param: it must match the given one's type
         if rg.region.params[-1].type != seed.type or rg.region.params[-1].attrs != seed.attrs:
             continue
         if all(a.key == b.key for a, b in zip(rys, grads)):
@@ -131,493 +660,11 @@ def match_flash_joint(region: Region):
     return None
 
 
-def _yield(n):
-    from .dialect import OPS
-    from .ir import Builder
-
-    return Builder(OPS).emit("core.yield", n)
-
-
-def _wrt_candidates(n: int):
-    import itertools
-
-    for combo in itertools.permutations(("q", "k", "v"), n):
-        yield combo
-
-
-
-
-# ------------------------------------------------------- the graph and claims
-
-
-def _graph(region: Region):
-    """Interior nodes in dependency order (params, sinks and free views
-    excluded) and the consumer lists of every value (partition.py:88-103)."""
-    params = {id(p) for p in region.params}
-    yld = region.body[-1]
-    order, consumers = [], {}
-    for n in walk(region):
-        if id(n) in params:
-            continue
-        for a in n.args:
-            consumers.setdefault(id(a), []).append(n)
-        if n is yld or n.op == "core.tuple":
-            continue
-        order.append(n)
-    return [n for n in order if n.op not in _FREE], consumers
-
-
-def _cone(root, stops: set, allow: set | None = None) -> dict:
-    """The producer cone of ``root`` (id -> node), exclusive of ``stops`` and
-    params, optionally restricted to ``allow`` (partition.py:106-118)."""
-    members, todo = {}, [root]
-    while todo:
-        n = todo.pop()
-        if id(n) in members or id(n) in stops or n.op == "core.param":
-            continue
-        if allow is not None and id(n) not in allow and n is not root:
-            continue
-        members[id(n)] = n
-        todo.extend(n.args)
-    return members
-
-
-def _attach_free_fringe(members: dict) -> dict:
-    """Free views (not consts) that members read join the claim, to fixpoint:
-    a boundary is always a real value, never a view (partition.py:121-133)."""
-    while True:
-        grown = [a for m in list(members.values()) for a in m.args
-                 if id(a) not in members and a.op in _FREE and a.op not in _CONSTS]
-        if not grown:
-            return members
-        for a in grown:
-            members[id(a)] = a
-
-
-def _outside(a, members, consumers, root=None) -> bool:
-    """Is ``a``'s value consumed outside ``members``? Free views forward their
-    value, so the check looks through them to their consumers; reaching the
-    claim's root is the export itself (partition.py:136-148)."""
-    for c in consumers.get(id(a), ()):
-        if c is root:
-            continue
-        if id(c) not in members:
-            return True
-        if c.op in _FREE and _outside(c, members, consumers, root):
-            return True
-    return False
-
-
-def _leaks(root, members, consumers, travel=()) -> bool:
-    """A non-root interior member consumed outside would need a second output
-    (partition.py:151-159); travel copies are exempt."""
-    return any(m is not root and m.op not in _FREE and id(m) not in travel and _outside(m, members, consumers, root)
-               for m in members.values())
-
-
-def _absorb_up(members, consumers, claimed, travel=()) -> dict:
-    """The prologue walk (partition.py:162-188): compute nodes join while every
-    consumer already lies inside the claim; travel copies join unconditionally."""
-    while True:
-        _attach_free_fringe(members)
-        added = False
-        for m in list(members.values()):
-            for a in m.args:
-                if id(a) in members:
-                    continue
-                if id(a) in travel:
-                    members[id(a)] = a
-                    added = True
-                elif id(a) not in claimed and a.op in _COMPUTE and not _outside(a, members, consumers):
-                    members[id(a)] = a
-                    added = True
-        if not added:
-            return members
-
-
-def _absorb_travel(members, travel) -> dict:
-    """Free views and travel copies only, to fixpoint (partition.py:191-205)."""
-    while True:
-        _attach_free_fringe(members)
-        grown = [a for m in list(members.values()) for a in m.args if id(a) not in members and id(a) in travel]
-        if not grown:
-            return members
-        for a in grown:
-            members[id(a)] = a
-
-
-def _absorb(root, members, consumers, claimed):
-    """The epilogue walk (partition.py:208-227): while the root has exactly one
-    consumer in the epilogue vocabulary, it joins and becomes the root; a
-    broadcast side operand of an absorbed node rides along."""
-    while True:
-        cs = consumers.get(id(root), ())
-        if len(cs) != 1:
-            return root
-        c = cs[0]
-        if c.op not in _EPILOGUE or id(c) in claimed or c.op == "core.yield":
-            return root
-        if c.op == "tl.repeat_like" and c.args[0] is root:
-            return root  # broadcasting INTO another claim's lattice is that claim's product
-        for side in c.args:
-            if side is root or id(side) in members or side.op in _CONSTS:
-                continue
-            if side.op == "tl.repeat_like" and id(side.args[1]) in members:
-                members[id(side)] = side
-        members[id(c)] = c
-        root = c
-
-
-def _claim_flash(r):
-    """The flash shape on bare nodes (partition.py:230-255): q, k, v are any
-    values (the carve makes them params); riders decline."""
-    out = contract_core(r)
-    if out is None:
-        return None
-    pr, v, s = out
-    sm = match_softmax(pr)
-    if sm is None or sm["s"] != s:
-        return None
-    smn = sm["sm"]
-    if smn.op != "tl.pointwise" or smn.attr("f") != "where" or len(smn.args) != 3:
-        return None
-    mask, sc, fill = smn.args
-    if fill.op not in _CONSTS or not forest_is_closed(mask):
-        return None
-    core = contract_core(sc)
-    if core is None:
-        return None
-    q, k, e = core
-    qd, kd, vd = (x.type.names for x in (q, k, v))
-    if len(qd) != 2 or kd != (s, e) or len(vd) != 2 or vd[0] != s:
-        return None
-    t = next(n for n in qd if n != e)
-    return {"q": q, "k": k, "v": v, "m": sm["max"], "den": sm["den"], "t": t, "s": s}
-
-
-def _reduce_dims(n) -> set:
-    d = n.attr("dims")
-    return {d} if isinstance(d, str) else set(d)
-
-
-def _duplicable_cone(x, members, stats, sweep):
-    """``x``'s cone inside the claim, stopped at artifacts and boundaries: map
-    work and tile-local reductions travel, a reduction over a swept dim does
-    not (partition.py:258-276). Returns the cone or None."""
-    cone, todo = {}, [x]
-    while todo:
-        n = todo.pop()
-        if id(n) in cone or id(n) in stats or id(n) not in members:
-            continue
-        if n.op == "tl.reduce":
-            if _reduce_dims(n) & sweep:
-                return None
-        elif n.op not in _FREE and n.op not in _COMPUTE:
-            return None
-        cone[id(n)] = n
-        todo.extend(n.args)
-    return cone
-
-
-def _extract(root, members, artifacts=()):
-    """Rebuild a claim as a canonical standalone region (partition.py:296-324):
-    boundaries become params in first-use order (a depth-first walk that
-    mirrors the rebuild's argument order), so structurally identical claims
-    from different layers share one content key. With artifacts the region
-    yields (output, *artifacts). Returns (region, bounds)."""
-    bounds, seen = [], set()
-    for r in (root, *artifacts):
-        todo = [r]
-        while todo:
-            n = todo.pop()
-            if id(n) in seen:
-                continue
-            seen.add(id(n))
-            for a in reversed(n.args):
-                if id(a) in members:
-                    todo.append(a)
-                elif id(a) not in seen and a.op not in _CONSTS:
-                    seen.add(id(a))
-                    bounds.append(a)
-    b = Builder(OPS)
-    memo = {id(x): b.param(i, x.type) for i, x in enumerate(bounds)}
-    params = tuple(memo[id(x)] for x in bounds)
-    built = tuple(rebuild_into(b, memo, r) for r in (root, *artifacts))
-    y = built[0] if len(built) == 1 else b.emit("core.tuple", *built)
-    return Region(params=params, body=(b.emit("core.yield", y),)), tuple(bounds)
-
-
-def _components(nodes, consumers):
-    """Weakly connected components of the unclaimed residue, each with the
-    members consumed outside it (its roots) (partition.py:327-355)."""
-    pool = {id(n): n for n in nodes}
-    nbr: dict = {}
-    for n in nodes:
-        for a in n.args:
-            if id(a) in pool:
-                nbr.setdefault(id(n), set()).add(id(a))
-                nbr.setdefault(id(a), set()).add(id(n))
-    seen, comps = set(), []
-    for n in nodes:
-        if id(n) in seen:
-            continue
-        comp, todo = [], [id(n)]
-        while todo:
-            i = todo.pop()
-            if i in seen:
-                continue
-            seen.add(i)
-            comp.append(pool[i])
-            todo.extend(nbr.get(i, ()))
-        ids = {id(x) for x in comp}
-        roots = [m for m in comp if any(id(c) not in ids for c in consumers.get(id(m), ()))]
-        comps.append((comp, roots))
-    return comps
-
-
-def _elems(t) -> int:
-    n = 1
-    for d in getattr(t, "dims", ()):
-        n *= d.size
-    return n
-
-
-def _dissolve(claims, consumers, travel, region):
-    """Root travel (partition.py:358-455): a claim whose root feeds only other
-    claims, with nothing but map work and reductions the consumers do not
-    sweep, dissolves into them when re-deriving it moves fewer elements than
-    materializing it (2 x root elements vs consumers x boundary inputs). Pure
-    map claims are tried first; repeats to fixpoint."""
-    yld = region.body[-1]
-    sinks = {id(yld)} | ({id(yld.args[0])} if yld.args[0].op == "core.tuple" else set())
-
-    def value_consumers(x, out, seen):
-        for c in consumers.get(id(x), ()):
-            if id(c) in seen:
-                continue
-            seen.add(id(c))
-            out.append(c)
-            if c.op in _FREE:
-                value_consumers(c, out, seen)
-        return out
-
-    while True:
-        owner: dict = {}
-        for ci, (_root, members, _arts) in enumerate(claims):
-            for i in members:
-                owner.setdefault(i, set()).add(ci)
-        sweeps = []
-        for _root, members, _arts in claims:
-            sw: set = set()
-            for m in members.values():
-                if m.op == "tl.reduce" and id(m) not in travel:
-                    sw |= _reduce_dims(m)
-            sweeps.append(sw)
-        order = sorted(range(len(claims)), key=lambda ci: sum(m.op == "tl.reduce" for m in claims[ci][1].values()))
-        gone = None
-        for ci in order:
-            root, members, arts = claims[ci]
-            if root is None or arts:
-                continue
-            if any(m.op not in _FREE and m.op not in _COMPUTE and m.op != "tl.reduce" and id(m) not in travel
-                   for m in members.values()):
-                continue
-            mine: set = set()
-            for m in members.values():
-                if m.op == "tl.reduce":
-                    mine |= _reduce_dims(m)
-            cons = value_consumers(root, [], set())
-            ok, eaters = bool(cons), set()
-            for c in cons:
-                if id(c) in sinks:
-                    ok = False
-                    break
-                if c.op in _FREE:
-                    continue
-                who = owner.get(id(c), set()) - {ci}
-                if not who:
-                    ok = False
-                    break
-                eaters |= who
-            if not ok or any(mine & sweeps[cj] for cj in eaters):
-                continue
-            binputs, seenb = 0, set()
-            for m in members.values():
-                for a in m.args:
-                    if id(a) not in members and id(a) not in seenb and a.op not in _CONSTS:
-                        seenb.add(id(a))
-                        binputs += _elems(a.type)
-            if 2 * _elems(root.type) <= len(eaters) * binputs:
-                continue  # materializing is cheaper: the carve stays
-            gone = ci
-            break
-        if gone is None:
-            return claims
-        root, members, _arts = claims.pop(gone)
-        travel.update(members)
-        travel[id(root)] = root
-        for _r, mem, _a in claims:
-            _absorb_travel(mem, travel)
-
-
-def carve_model(region: Region, dissolve: bool = True):
-    """The partition alone (partition.py:458-582): returns (claims,
-    interior_count, travel), claims as (root, members, artifacts) with members
-    keyed by id; a rootless claim is a multi-output residue. ``dissolve=False``
-    skips root travel, so every claim's root stays a materialized boundary
-    (the device executor's policy for values it cannot re-derive per tile)."""
-    interior, consumers = _graph(region)
-    claimed: set = set()
-    travel: dict = {}
-    claims: list = []
-
-    def take(root, members, arts=()):
-        _attach_free_fringe(members)
-        if _leaks(root, members, consumers, travel):
-            return False
-        claims.append((root, members, arts))
-        claimed.update(i for i, m in members.items() if m.op not in _FREE)
-        return True
-
-    def take_flash_artifacts(r, f, members):
-        _attach_free_fringe(members)
-        stats = {id(f["m"]), id(f["den"])}
-        sweep = {f["t"], f["s"]}
-        new_travel: dict = {}
-        for m in members.values():
-            if m is r or id(m) in stats or not _outside(m, members, consumers, r):
-                continue
-            while m.op in _FREE and m.args:  # a leaked view: classify the value it reads
-                m = m.args[0]
-            if m is r or id(m) in stats or id(m) not in members:
-                continue
-            cone = _duplicable_cone(m, members, stats, sweep)
-            if cone is None:
-                return False
-            new_travel.update(cone)
-        claims.append((r, members, (f["m"], f["den"])))
-        travel.update(new_travel)
-        claimed.update(i for i, m in members.items() if m.op not in _FREE)
-        return True
-
-    def free_of_claims(members):
-        return not any(i in claimed and i not in travel for i in members)
-
-    for r in interior:  # flash compositions: three reduces, most specific
-        if r.op != "tl.reduce" or id(r) in claimed:
-            continue
-        f = _claim_flash(r)
-        if f is not None:
-            members = _cone(r, {id(f["q"]), id(f["k"]), id(f["v"])})
-            if free_of_claims(members) and not take(r, dict(members)):
-                take_flash_artifacts(r, f, members)
-    for n in interior:  # bare row normalizations (two reduces)
-        if id(n) in claimed:
-            continue
-        sm = match_softmax(n)
-        if sm is None:
-            continue
-        members = _absorb_travel(_cone(n, {id(sm["sm"])}), travel)
-        if free_of_claims(members):
-            take(n, members)
-    for n in interior:  # row statistics, the scale-shift absorbed as epilogue
-        if id(n) in claimed:
-            continue
-        rs = match_rowstat(n)
-        if rs is None:
-            continue
-        members = _absorb_travel(_cone(n, {id(rs["x"])}), travel)
-        if free_of_claims(members):
-            take(_absorb(n, members, consumers, claimed), members)
-    for r in interior:  # single-reduce contractions: prologues up, epilogues down
-        if r.op != "tl.reduce" or id(r) in claimed:
-            continue
-        dims = tuple(_reduce_dims(r))
-        if r.attr("f") not in ("sum", "mean") or len(dims) not in (1, 2) or r.attr("zero") is not None:
-            continue
-        mul = r.args[0]
-        if mul.op == "tl.pointwise" and mul.attr("f") == "mul" and len(mul.args) == 2:
-            cores = [_core(x) for x in mul.args]
-        else:  # the plain shape: a sum with no product
-            cores = [mul]
-        if any(not hasattr(c.type, "dims") or not c.type.has(k) for c in cores for k in dims):
-            continue
-        keeps = [{nm for nm in c.type.names if nm not in dims} for c in cores]
-        if set(r.type.names) != set().union(*keeps):
-            continue
-        members = {id(r): r}
-        if len(cores) == 2:
-            members[id(mul)] = mul
-        if any(i in claimed for i in members):
-            continue
-        _absorb_up(members, consumers, claimed, travel)
-        take(_absorb(r, members, consumers, claimed), members)
-    residue = [n for n in interior if id(n) not in claimed]
-    for comp, roots in _components(residue, consumers):
-        comp_ids = {id(m) for m in comp}
-        allow = comp_ids | set(travel)
-        pool = {id(m): m for m in comp}
-        rootset = [id(x) for x in roots]
-        while True:  # one part per root; promote internal fan-ins until the parts tile
-            parts, used = [], set()
-            for ri in rootset:
-                stops = (set(rootset) - {ri}) | used
-                mem = _absorb_travel(_cone(pool[ri], stops, allow=allow), travel)
-                parts.append((pool[ri], mem))
-                used |= {i for i in mem if i in comp_ids}
-            promote = []
-            for _rt, mem in parts:
-                for m in mem.values():
-                    for a in m.args:
-                        if id(a) in comp_ids and id(a) not in mem and id(a) not in rootset and id(a) not in promote:
-                            promote.append(id(a))
-            if not promote:
-                claims.extend((rt, mem, ()) for rt, mem in parts)
-                break
-            rootset.extend(promote)
-    if dissolve:
-        _dissolve(claims, consumers, travel, region)
-    return claims, len(interior), travel
-
-
-def _core(x):
-    """A contraction operand under its broadcasts (fusion.py:98-122)."""
-    while x.op in ("tl.repeat_like", "tl.repeat"):
-        x = x.args[0]
-    return x
-
-
-def plan_model(region: Region, machine=None, floor: int = 1024, dissolve: bool = True) -> ModelPlan:
-    """Carve ``region`` and plan each distinct carve once (partition.py:586-607).
-    A flash joint is claimed whole first (the fused backward's carve)."""
-    fj = match_flash_joint(region)
-    if fj is not None:
-        return _plan_joint(region, fj, machine, floor)
-    claims, interior, _travel = carve_model(region, dissolve=dissolve)
-    seen: dict = {}
-    carves = []
-    counted: set = set()  # travel copies count once, in their first claim
-    for root, members, arts in claims:
-        n_interior = sum(1 for i, m in members.items() if m.op not in _FREE and i not in counted)
-        counted.update(i for i, m in members.items() if m.op not in _FREE)
-        if root is None:
-            ops = sorted({m.op for m in members.values() if m.op not in _FREE})
-            g = Group("uncompiled", None, None, "red", reason=f"multi-output residue over {ops}")
-            carves.append(Carve(region, g, n_interior, "residue"))
-            continue
-        kernel, bounds = _extract(root, members, arts)
-        g = seen.get(kernel.key)
-        if g is None:
-            g = plan_region(kernel, machine=machine, floor=floor).groups[0]
-            seen[kernel.key] = g
-        carves.append(Carve(kernel, g, n_interior, root.op, root, bounds, arts))
-    return ModelPlan(tuple(carves), interior)
-
-
 def _plan_joint(region: Region, fj, machine, floor) -> ModelPlan:
-    interior = _interior(region)
+    interior = [n for n in walk(region)
+                if not _is_view(n) and n.op not in ("core.param", "core.yield", "core.tuple")]
     out = region.body[-1].args[0].args[0]
-    fwd = Region(params=region.params[:-1], body=(_yield(out),))
+    fwd = Region(params=region.params[:-1], body=(Builder(OPS).emit("core.yield", out),))
     fplan = plan_region(fwd, machine=machine, floor=floor).groups[0]
     cert = Certificate("proved-exact", fplan.certificate.licenses if fplan.certificate else (), (), True)
     g = Group(
@@ -634,4 +681,4 @@ def _plan_joint(region: Region, fj, machine, floor) -> ModelPlan:
     return ModelPlan((carve,), len(interior))
 
 
-__all__ = ["Carve", "ModelPlan", "carve_model", "plan_model", "match_flash_joint"]
+__all__ = ["Carve", "Claim", "ModelPlan", "carve_model", "extract", "plan_model", "match_flash_joint"]

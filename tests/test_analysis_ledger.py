@@ -96,10 +96,11 @@ def test_measurements_are_json_records_and_the_ledger_round_trips(tmp_path):
     assert f.value == {"ms": 1.5, "shape": [2, 3]}
     with pytest.raises(TypeError, match="plain data"):
         bad(machine="gfx950")
-    path = tmp_path / "ledger.json"
+    path = tmp_path / "ledger.jsonl"
     assert A.save_ledger(path) == 1
-    data = json.loads(path.read_text())
-    assert data[f.key]["analysis"] == "t.ms@v1"
+    lines = path.read_text().splitlines()
+    assert len(lines) == 2 and json.loads(lines[1]) == {"key": f.key, "analysis": "t.ms@v1", "value": f.value}
+    assert [p.name for p in tmp_path.iterdir()] == ["ledger.jsonl"]  # saved by rename: no partial file left
     A.clear(ledger_too=True)
     assert A.load_ledger(path) == 1
     with A.no_reanalysis():  # a reloaded measurement is a hit: never measured again
@@ -113,8 +114,49 @@ def test_a_warm_replan_certifies_nothing():
     the same region performs zero analysis."""
     subj = zoo.attention(T=8, E=4, OD=4)
     first = fusion.plan_region(subj.region)
-    misses = A.MISSES[0]
+    misses = A.misses()
     with A.no_reanalysis():
         again = fusion.plan_region(subj.region)
-    assert A.MISSES[0] == misses
+    assert A.misses() == misses
     assert again.groups[0].certificate == first.groups[0].certificate
+
+
+def test_keys_are_typed_and_sets_are_order_free():
+    @A.defanalysis("t.k", 1)
+    def k(x):
+        return 0
+
+    keys = {k(x).key for x in (1, 1.0, True, "1", (1,), None)}
+    assert len(keys) == 6  # no two differently typed inputs share a key
+    assert k((1, 2)).key == k([1, 2]).key  # sequences are data: a tuple and a list of the same items agree
+    assert k({3, 1, 2}).key == k({2, 3, 1}).key and k({"a": 1, "b": 2}).key == k({"b": 2, "a": 1}).key
+    a = np.arange(6.0)
+    assert k(a.reshape(2, 3)).key != k(a.reshape(3, 2)).key != k(a).key  # shape is part of an array's key
+    assert k(a.astype(np.float32)).key != k(a).key
+
+
+def test_a_file_that_is_not_a_ledger_refuses(tmp_path):
+    bad = tmp_path / "other.json"
+    bad.write_text(json.dumps({"some": "thing"}))
+    with pytest.raises(ValueError, match="not a measurement ledger"):
+        A.load_ledger(bad)
+    torn = tmp_path / "torn.jsonl"
+    torn.write_text(json.dumps({"ledger": "pdum_dsl_amd.measurements", "format": 1}) + "\n" + json.dumps({"key": "k"}))
+    with pytest.raises(ValueError, match="exactly key, analysis and value"):
+        A.load_ledger(torn)
+
+
+def test_loading_keeps_a_measurement_taken_in_this_session(tmp_path):
+    @A.defanalysis("t.lap", 1, ledger=True)
+    def lap(*, machine):
+        return {"ms": len(machine)}
+
+    first = lap(machine="gfx950")
+    path = tmp_path / "l.jsonl"
+    A.save_ledger(path)
+    rows = path.read_text().splitlines()
+    rec = json.loads(rows[1])
+    rec["value"] = {"ms": 99}
+    path.write_text(rows[0] + "\n" + json.dumps(rec) + "\n")
+    assert A.load_ledger(path) == 1
+    assert lap(machine="gfx950").value == first.value == {"ms": 6}

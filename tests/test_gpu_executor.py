@@ -234,8 +234,12 @@ def test_a_bare_row_max_or_min_runs_on_the_device(f):
     np.testing.assert_array_equal(got, want)  # NaN positions must agree too
 
 
-@pytest.mark.parametrize("dtype,tol", [("f32", 1e-4), ("bf16", 1e-1)])
-def test_the_gpt2_weight_gradients_run_carve_by_carve(dtype, tol):
+_SMALL = dict(t=64, d=128, nh=2, hk=64, m=512, layers=1, v=64)
+_TWO_LAYER = dict(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)  # a scan shares a red carve with a reduction
+
+
+@pytest.mark.parametrize("cfg,dtype,tol", [(_SMALL, "f32", 1e-4), (_SMALL, "bf16", 1e-1), (_TWO_LAYER, "f32", 1e-4)])
+def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, tol):
     """grad of gpt2's logits w.r.t. every weight but the embedding tables,
     planned by plan_model and run on the device (contractions with their
     epilogues, map chains, the layernorm, the gather and the bare row max),
@@ -247,13 +251,15 @@ def test_the_gpt2_weight_gradients_run_carve_by_carve(dtype, tol):
     from pdum_dsl_amd.tl.autodiff import grad, region_names
     from pdum_dsl_amd.tl.partition import plan_model
 
-    m = zoo.gpt2(zoo.GPT2Config(t=64, d=128, nh=2, hk=64, m=512, layers=1, v=64), seed=3)
+    m = zoo.gpt2(zoo.GPT2Config(**cfg), seed=3)
     pn = tuple(m.names[id(p)] for p in m.region.params)
     wrt = tuple(n for n in pn if n not in ("ids", "wte", "wpe"))
     rg = grad(m.region, "logits", seed="dlogits", wrt=wrt, names=region_names(m.region, pn, ("logits",)))
     dl = np.random.default_rng(2).standard_normal(tuple(rg.region.params[-1].type.shape))
     vals = m.values() + [dl]
     ex = PlanExecutor(plan_model(rg.region), rg.region, dtype)
+    if cfg is _TWO_LAYER:
+        assert any("split at scan" in st.source for st in ex.steps)
     ex.bind(vals)
     outs = ex.run()
     torch.cuda.synchronize()

@@ -101,3 +101,38 @@ def test_the_executor_runs_a_tied_extremum_joint(f):
         want[t, int(np.flatnonzero(xv[t] == ext)[0])] = np.float32(dy[t])
     got = np.transpose(dx.cpu().numpy(), [rg.nodes["dx"].type.names.index(n) for n in ("t", "s")])
     np.testing.assert_array_equal(got, want)
+
+
+def _scan_then(kind):
+    """Regions whose red carve holds a scan beside other work a map chain
+    cannot hold: a row max over a prefix sum, and a scan of a scan."""
+    from pdum_dsl_amd.tl.dialect import OPS
+    from pdum_dsl_amd.tl.ir import Builder, Region, tensor_type
+
+    b = Builder(OPS)
+    x = b.param(0, tensor_type(("t", "s"), (19, 333)))
+    s1 = b.emit("tl.scan", x, dim="s", f="sum")
+    if kind == "max-of-scan":
+        y = b.emit("tl.reduce", b.emit("tl.pointwise", s1, s1, f="mul"), dims=("s",), f="max")
+    else:  # scan of a scan, reversed, then elementwise
+        s2 = b.emit("tl.scan", b.emit("tl.pointwise", s1, f="tanh"), dim="s", f="sum", reverse=True)
+        y = b.emit("tl.pointwise", s2, x, f="mul")
+    return Region(params=(x,), body=(b.emit("core.yield", y),))
+
+
+@pytest.mark.parametrize("kind", ["max-of-scan", "scan-of-scan"])
+def test_a_red_carve_splits_at_its_scan(kind):
+    from oracle import region_eval as rev
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    region = _scan_then(kind)
+    ex = PlanExecutor(plan_model(region), region, "f32")
+    assert any("split at scan" in st.source for st in ex.steps)
+    xv = np.random.default_rng(12).standard_normal((19, 333)) * 0.3
+    ex.bind([xv])
+    got = ex.run().cpu().numpy().astype(np.float64)
+    torch.cuda.synchronize()
+    y = region.body[-1].args[0]
+    want = rev.evaluate(region, [rev.value(xv, region.params[0].type)]).numpy(y.type.names)
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())

@@ -158,3 +158,22 @@ def test_the_scan_sum_adjoint_matches_finite_differences(reverse):
         fd[i] = (loss(xv + e) - loss(xv - e)) / (2 * h)
     np.testing.assert_allclose(g1, fd, rtol=1e-6, atol=1e-8)
     np.testing.assert_allclose(g2, fd, rtol=1e-6, atol=1e-8)
+
+
+def test_the_executor_splits_a_red_carve_at_its_scan():
+    """Host side only (no device): a red carve in which a scan meets a
+    reduction (a row max over a prefix sum) builds as one split step whose
+    remainder runs as a nested plan (the bare max)."""
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    b = Builder(OPS)
+    x = b.param(0, tensor_type(("t", "s"), (19, 333)))
+    s1 = b.emit("tl.scan", x, dim="s", f="sum")
+    y = b.emit("tl.reduce", b.emit("tl.pointwise", s1, s1, f="mul"), dims=("s",), f="max")
+    region = Region(params=(x,), body=(b.emit("core.yield", y),))
+    ex = PlanExecutor(plan_model(region), region, "f32")
+    (step,) = ex.steps
+    assert step.source == "split at scan sum along s (rest by nested plans)"
+    (rest,) = ex.nested
+    assert [st.source.split()[0] for st in rest.steps] == ["reduce_rows"]
