@@ -197,6 +197,22 @@ def main():
 def secondary(torch, K, cf, h, dev):
     out = {}
     g = torch.Generator(device=dev).manual_seed(1)
+    # ---------------- C1: single-head non-causal attention, S=256 D=64 fp32 ----------------
+    T1, D1 = 256, 64
+    q1, k1, v1 = (torch.randn((1, 1, T1, D1), generator=g, device=dev, dtype=torch.float32) for _ in range(3))
+    r1 = K.flash_fwd(q1, k1, v1, scale=D1**-0.5)
+    torch.cuda.synchronize()
+    wo = cf.attention(h(q1[0, 0]), h(k1[0, 0]), h(v1[0, 0]), scale=D1**-0.5)[0]
+    err = float(np.abs(h(r1.o[0, 0]) - wo).max())
+    assert err <= 1e-5 * max(1.0, float(np.abs(wo).max())), f"C1 parity failed: {err}"
+    ms = time_events(lambda: K.flash_fwd(q1, k1, v1, scale=D1**-0.5, out=r1.o), 200)
+    fl = 4.0 * D1 * T1 * T1
+    out["attention_c1"] = {
+        "config": "C1 B=1 H=1 S=256 D=64 non-causal fp32", "ms": round(ms, 5), "TFLOP/s": round(fl / ms / 1e9, 3),
+        "algorithmic_flop": fl, "max_abs_err": err,
+        "note": "one head: 4 query blocks on a 256-CU chip, launch-latency bound by construction",
+    }
+    del q1, k1, v1, r1
     # ---------------- C2: row softmax + layernorm, [8192, 4096] fp32 ----------------
     R, C = 8192, 4096
     x = torch.randn((R, C), generator=g, device=dev, dtype=torch.float32)
@@ -586,6 +602,89 @@ def _map_chain_line(torch, K, dev, g):
     }
 
 
+def host_facts() -> dict:
+    """The host the CPU rows ran on: CPU model, os.cpu_count() and the
+    threads torch's CPU kernels use (the region interpreter's parallelism)."""
+    import torch
+
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "torch_threads": int(torch.get_num_threads())}
+
+
+def median_laps(fn, budget_s: float, min_laps: int = 3, warmup: int = 1):
+    """(median seconds per call, laps): ``warmup`` untimed calls, then timed
+    calls until both ``min_laps`` and ``budget_s`` are reached (the
+    reference's bench_zoo.py:130-150 discipline: verify first, warm, median)."""
+    for _ in range(warmup):
+        fn()
+    laps, t_end = [], time.perf_counter() + budget_s
+    while len(laps) < min_laps or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        laps.append(time.perf_counter() - t0)
+    laps.sort()
+    return laps[len(laps) // 2], len(laps)
+
+
+def _tile_program(region):
+    """The kernel the fusion planner generates for a one-template region."""
+    from pdum_dsl_amd.tl import fusion
+
+    (g,) = fusion.plan_region(region).groups
+    return g
+
+
+def cpu_rows(cf, host) -> list:
+    """The reference's CPU evaluator on C1 and C2 whole: the generated tile
+    programs run by the float64 region interpreter (oracle.region_eval, the
+    torch-CPU evaluator restated), each verified against its closed form
+    before it is timed, each reported in its GPU row's own unit."""
+    from oracle import region_eval as rev
+    from pdum_dsl_amd.tl import zoo
+
+    rows = []
+    # C1: single-head non-causal attention, S=256 D=64, the flash tile program
+    T, D = 256, 64
+    subj = zoo.attention(T=T, S=T, E=D, OD=D, mask="all", seed=3, scale=D**-0.5)
+    g = _tile_program(subj.region)
+    vals = [rev.value(f.arr, p.type) for f, p in zip(subj.inputs, g.kernel.params)]
+    want = cf.attention(*subj.numpy_inputs(), scale=1.0)[0]
+    err = float(np.abs(rev.evaluate(g.kernel, vals).numpy(("t", "o")) - want).max())
+    assert err < 1e-9, f"C1 CPU row disagrees with the closed form: {err}"
+    sec, laps = median_laps(lambda: rev.evaluate(g.kernel, vals), 3.0)
+    fl = 4.0 * D * T * T
+    rows.append({"config": "C1 B=1 H=1 S=256 D=64 non-causal, whole", "template": g.template,
+                 "si": dict(g.params).get("si"), "value": round(fl / sec / 1e12, 8), "unit": "TFLOP/s",
+                 "ms": round(sec * 1e3, 3), "laps": laps, "max_abs_err": err, **host})
+    # C2a / C2b: row softmax and layernorm over [8192, 4096], whole
+    R, C = 8192, 4096
+    for name, subj, nbytes in (
+        ("C2a row softmax [8192,4096], whole", zoo.row_softmax(rows=R, cols=C, seed=1), 2 * R * C * 4),
+        ("C2b layernorm [8192,4096] + gamma/beta, whole", zoo.layernorm(rows=R, feat=C, seed=1),
+         2 * R * C * 4 + 2 * C * 4),
+    ):
+        g = _tile_program(subj.region)
+        vals = [rev.value(f.arr, p.type) for f, p in zip(subj.inputs, g.kernel.params)]
+        y = g.kernel.body[-1].args[0]
+        got = rev.evaluate(g.kernel, vals).numpy(y.type.names)
+        want = subj.oracle(subj.numpy_inputs())
+        err = float(np.abs(got - want).max())
+        assert err < 1e-9, f"{name}: CPU row disagrees with the closed form: {err}"
+        del got
+        sec, laps = median_laps(lambda: rev.evaluate(g.kernel, vals), 6.0)
+        rows.append({"config": name, "template": g.template, "value": round(nbytes / sec / 1e9, 3), "unit": "GB/s",
+                     "ms": round(sec * 1e3, 1), "laps": laps, "bytes": nbytes, "max_abs_err": err, **host})
+    return rows
+
+
 def cpu_baseline(cf):
     """The reference's CPU path restated — the flash template's generated tile
     program (fusion.plan_region over the naive attention region, the online-
@@ -594,15 +693,15 @@ def cpu_baseline(cf):
     Python loop, as dialect.run_region / the torch-CPU Evaluator run it) — on
     a bounded sample of C3: one (b, h) instance, its first R query rows against
     their causal keys, repeated for ~10 s on this host's cores; reported as
-    TFLOP/s of the same causal algorithmic count the GPU line uses."""
-    import torch
-
+    TFLOP/s of the same causal algorithmic count the GPU line uses. ``rows``
+    adds C1 and C2 whole, the same way."""
     from oracle import region_eval as rev
-    from pdum_dsl_amd.tl import fusion, zoo
+    from pdum_dsl_amd.tl import zoo
 
+    host = host_facts()
     R, D = 1024, 128
     subj = zoo.attention(T=R, S=R, E=D, OD=D, mask="causal", seed=3, scale=D**-0.5)
-    (g,) = fusion.plan_region(subj.region).groups
+    g = _tile_program(subj.region)
     vals = [rev.value(f.arr, p.type) for f, p in zip(subj.inputs, g.kernel.params)]
     want = cf.attention(*subj.numpy_inputs(), scale=1.0, band=(None, 0))[0]
     t0 = time.perf_counter()
@@ -619,11 +718,13 @@ def cpu_baseline(cf):
     return {
         "value": round(fl / el / 1e12, 8),
         "unit": "TFLOP/s",
-        "cores": int(torch.get_num_threads()),
+        "cores": host["torch_threads"],
         "kind": "port",
         "sample": f"oracle.region_eval (float64 torch-CPU interpreter) of the generated flash tile program "
         f"(si={dict(g.params)['si']}) on one C3 head, query rows [0,{R}) x their causal keys, {reps} reps in "
-        f"{el:.1f} s; host os.cpu_count()={os.cpu_count()}",
+        f"{el:.1f} s",
+        **host,
+        "rows": cpu_rows(cf, host),
     }
 
 
