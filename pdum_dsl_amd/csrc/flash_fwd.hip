@@ -16,6 +16,9 @@
 //     lane-half exactly the B operand (8 consecutive keys) of O^T += V^T P^T —
 //     no register shuffles between the two contractions;
 //   * V stays row-major in LDS and is read transposed by ds_read_b64_tr_b16;
+//     the LDS array is static and the key-tile loop runs in buffer pairs, so
+//     every operand read is a lane offset plus an immediate (no per-tile
+//     address arithmetic);
 //   * exp runs as exp2 on log2(e)-scaled scores (v_exp_f32); the running max
 //     is rescaled lazily (only when it grows by more than 2^8);
 //   * causal / band masks prune dead tiles (the mask-derived bounds of
@@ -95,7 +98,9 @@ constexpr float kTau = 8.0f;
 template <typename T, int D>
 __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs a) {
   using C = FwdCfg<D>;
-  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  // a static LDS array: its address is fixed when the kernel is compiled, so
+  // every operand read folds its buffer base into the immediate offset
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS];
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
 
   // workgroup -> (instance, query block); heavy (late) query blocks first
@@ -252,8 +257,9 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
   // One key tile: S^T = K Q^T, the masked (CUT) or unmasked softmax update,
   // then O^T += V^T P^T. CUT is a compile-time branch, so the common full tile
   // carries no per-element mask code.
-  auto tile = [&](int buf, int64_t key0, auto cutc) {
+  auto tile = [&](auto bufc, int64_t key0, auto cutc) {
     constexpr bool CUT = decltype(cutc)::value;
+    constexpr int buf = decltype(bufc)::value;  // a constant: every LDS address is a lane offset + an immediate
     const unsigned char* kt = smem + C::KBUF + buf * C::TILEB;
     const unsigned char* vt = smem + C::VBUF + buf * C::TILEB;
     f32x16 sacc = f32x16{};
@@ -334,20 +340,30 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
   };
 
   if (kt_lo < kt_hi) stage(kt_lo, 0);
-  auto sweep = [&](int from, int to, auto cutc) {
-    for (int kt = from; kt < to; ++kt) {
-      const int buf = (kt - kt_lo) & 1;
-      wait_vmcnt0();  // this wave's share of tile kt has landed
-      __syncthreads();  // ... and everyone's; everyone is done with tile kt - 1
-      if (kt + 1 < kt_hi) stage(kt + 1, buf ^ 1);  // the next tile, into the idle buffer
-      const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
-      bool dead = false;
-      if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's rows see no live key here
-        const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + C::BN - 1 - qw0;
-        dead = dmin > a.band_hi || dmax < a.band_lo;
-      }
-      if (!dead) tile(buf, key0, cutc);
+  // Tile kt lives in buffer (kt - kt_lo) & 1. The sweep runs tiles in pairs,
+  // buffer 0 then buffer 1, so the buffer is a compile-time constant in each
+  // copy of the tile body and its LDS addresses need no per-tile arithmetic.
+  auto one = [&](int kt, auto bufc, auto cutc) {
+    constexpr int buf = decltype(bufc)::value;
+    wait_vmcnt0();  // this wave's share of tile kt has landed
+    __syncthreads();  // ... and everyone's; everyone is done with tile kt - 1
+    if (kt + 1 < kt_hi) stage(kt + 1, buf ^ 1);  // the next tile, into the idle buffer
+    const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
+    bool dead = false;
+    if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's rows see no live key here
+      const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + C::BN - 1 - qw0;
+      dead = dmin > a.band_hi || dmax < a.band_lo;
     }
+    if (!dead) tile(bufc, key0, cutc);
+  };
+  auto sweep = [&](int from, int to, auto cutc) {
+    int kt = from;
+    if (kt < to && ((kt - kt_lo) & 1)) one(kt++, std::integral_constant<int, 1>{}, cutc);
+    for (; kt + 1 < to; kt += 2) {
+      one(kt, std::integral_constant<int, 0>{}, cutc);
+      one(kt + 1, std::integral_constant<int, 1>{}, cutc);
+    }
+    if (kt < to) one(kt, std::integral_constant<int, 0>{}, cutc);
   };
   sweep(kt_lo, kf_lo, std::true_type{});
   sweep(kf_lo, kf_hi, std::false_type{});
@@ -544,7 +560,7 @@ bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
 template <typename T, int D>
 int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
   using C = FwdCfg<D>;
-  static_assert(C::LDS <= 64 * 1024, "the forward's LDS fits the default dynamic limit");
+  static_assert(C::LDS <= 64 * 1024, "the forward's static LDS fits one workgroup's limit");
   const int64_t nblk = ninst * a.nqb;
   PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: grid too large (%lld workgroups)", (long long)nblk);
   FwdArgs aa = a;
@@ -553,7 +569,7 @@ int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
     aa.split_tiles = static_cast<int>((ntiles + a.nsplit - 1) / a.nsplit);
     aa.xcd_remap = 0;
     PDH_REQUIRE(nblk * a.nsplit <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd_split: grid too large");
-    flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk * a.nsplit)), C::THREADS, C::LDS, st>>>(aa);
+    flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk * a.nsplit)), C::THREADS, 0, st>>>(aa);
     int rc = check_launch("pdh_flash_fwd_split");
     if (rc) return rc;
     const int64_t nthr = a.plane * (D / 4);
@@ -562,7 +578,7 @@ int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
     return check_launch("pdh_flash_fwd_split (combine)");
   }
   aa.xcd_remap = (nblk % 8 == 0) ? ((ninst % 32 == 0) ? 2 : 1) : 0;
-  flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk)), C::THREADS, C::LDS, st>>>(aa);
+  flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk)), C::THREADS, 0, st>>>(aa);
   return check_launch("pdh_flash_fwd");
 }
 
