@@ -459,9 +459,13 @@ def _carved_grad_line(torch, dtype="f32"):
     the device executor as one HIP graph. fp32 storage: the carved backward
     rounds every boundary to the storage type, and in bf16 the layernorm and
     softmax backward carves cancel (layer 0's gradients drift far from fp32
-    over 12 layers). Checked against torch fp32 autograd of the same forward
-    on the same weights (three gradients), timed beside torch's forward +
-    backward (eager autograd, the same weights and type)."""
+    over 12 layers). The contractions run on the bf16 matrix cores with the
+    fp32 operands split into bf16 planes: six products per term (fp32 grade,
+    ``ms``), and, timed beside it, three (about 2^-16 of each product,
+    ``ms_bf16x3``).
+    Checked against torch fp32 autograd of the same forward on the same
+    weights (three gradients), and timed beside torch's forward + backward
+    (eager autograd, fp32, the same weights)."""
     import time as _time
 
     from pdum_dsl_amd.executor import PlanExecutor
@@ -476,7 +480,7 @@ def _carved_grad_line(torch, dtype="f32"):
     wrt = tuple(n for n in pn if n not in ("ids", "wte", "wpe"))
     rg = grad(m.region, "logits", seed="dlogits", wrt=wrt, names=region_names(m.region, pn, ("logits",)))
     plan = plan_model(rg.region)
-    ex = PlanExecutor(plan, rg.region, dtype)
+    ex = PlanExecutor(plan, rg.region, dtype, f32_contract="bf16x6")
     plan_s = _time.perf_counter() - t0
     seed_t = rg.region.params[-1].type
     dl = np.random.default_rng(9).standard_normal(tuple(seed_t.shape)) * 1e-2
@@ -485,7 +489,7 @@ def _carved_grad_line(torch, dtype="f32"):
     torch.cuda.synchronize()
     ex.capture()
     ms = time_events(lambda: ex.replay(check=False), 10)
-    # torch: the same forward with autograd on the same bf16 weights
+    # torch: the same forward with autograd on the same fp32 weights
     W = {m.names[id(p)]: ex.bound[id(p)] for p in m.region.params}
     W32 = {}
     for k_, v_ in W.items():
@@ -496,33 +500,45 @@ def _carved_grad_line(torch, dtype="f32"):
             W32[p + f"attn.{nm}2"] = W32[p + f"attn.{nm}"].reshape(cfg.d, cfg.nh * cfg.hk)
         W32[p + "attn.wo2"] = W32[p + "attn.wo"].reshape(cfg.nh * cfg.hk, cfg.d)
     W32["wteT"] = W32["wte"].t().contiguous()
-    y = m.region.body[-1].args[0]
     dlt = torch.as_tensor(dl, dtype=torch.float32, device="cuda").to(ex.bound[id(rg.region.params[-1])].dtype).float()
     dlt = dlt.permute([seed_t.names.index(n) for n in m.order])
     _gpt2_torch(torch, W32, cfg).backward(dlt)
-    errs = {}
-    by = dict(zip(rg.outputs, outs))
-    for nm in ("h.0.mlp.w1", "h.11.mlp.w2", "lnfg"):
-        node = rg.nodes[rg.grads[nm]]
-        pt = next(p for p in m.region.params if m.names[id(p)] == nm).type
-        got = by[rg.grads[nm]].float().permute([node.type.names.index(d) for d in pt.names])
-        want = W32[nm].grad
-        errs[nm] = float((got - want).abs().max() / want.abs().max())
+
+    def rel_errs(outs_):
+        errs_ = {}
+        by = dict(zip(rg.outputs, outs_))
+        for nm in ("h.0.mlp.w1", "h.11.mlp.w2", "lnfg"):
+            node = rg.nodes[rg.grads[nm]]
+            pt = next(p for p in m.region.params if m.names[id(p)] == nm).type
+            got = by[rg.grads[nm]].float().permute([node.type.names.index(d) for d in pt.names])
+            want = W32[nm].grad
+            errs_[nm] = float((got - want).abs().max() / want.abs().max())
+        return errs_
+
+    errs = rel_errs(outs)
     assert max(errs.values()) < (1e-3 if dtype == "f32" else 0.25), f"carved-gradient parity failed: {errs}"
-    del W32
-    Wb = {}
+    ex.release_graph()
+    ex_b = PlanExecutor(plan, rg.region, dtype, f32_contract="bf16x3")
+    ex_b.bind(m.values() + [dl])
+    errs_b = rel_errs(ex_b.run())
+    torch.cuda.synchronize()
+    assert max(errs_b.values()) < 5e-3, f"carved-gradient parity (bf16x3 contractions) failed: {errs_b}"
+    ex_b.capture()
+    ms_b = time_events(lambda: ex_b.replay(check=False), 10)
+    ex_b.release_graph()
+    del W32, ex_b
+    Wt = {}
     for k_, v_ in W.items():
-        Wb[k_] = v_.clone().requires_grad_(k_ in wrt) if v_.is_floating_point() else v_
-    dlb = dlt.to(torch.bfloat16)
+        Wt[k_] = v_.clone().requires_grad_(k_ in wrt) if v_.is_floating_point() else v_
 
     def torch_step():
         for i in range(cfg.layers):
             p = f"h.{i}."
             for nm in ("wq", "wk", "wv"):
-                Wb[p + f"attn.{nm}2"] = Wb[p + f"attn.{nm}"].reshape(cfg.d, cfg.nh * cfg.hk)
-            Wb[p + "attn.wo2"] = Wb[p + "attn.wo"].reshape(cfg.nh * cfg.hk, cfg.d)
-        Wb["wteT"] = Wb["wte"].t().contiguous()
-        torch.autograd.grad(_gpt2_torch(torch, Wb, cfg), [Wb[n] for n in wrt], dlb)
+                Wt[p + f"attn.{nm}2"] = Wt[p + f"attn.{nm}"].reshape(cfg.d, cfg.nh * cfg.hk)
+            Wt[p + "attn.wo2"] = Wt[p + "attn.wo"].reshape(cfg.nh * cfg.hk, cfg.d)
+        Wt["wteT"] = Wt["wte"].t().contiguous()
+        torch.autograd.grad(_gpt2_torch(torch, Wt, cfg), [Wt[n] for n in wrt], dlt)
 
     ms_torch = time_events(torch_step, 5)
     by_t = {}
@@ -532,8 +548,9 @@ def _carved_grad_line(torch, dtype="f32"):
         "config": "gpt2-small shape (as the carved_plan line), forward + gradients of every weight but the "
                   f"embedding tables, {dtype} storage / fp32 accumulate; random weights and cotangent",
         "carves": by_t, "device_steps": len(ex.steps), "plan_s": round(plan_s, 2), "ms": round(ms, 4),
-        "tokens_per_s": round(cfg.t / ms * 1e3, 1), "torch_eager_fwd_bwd_ms": round(ms_torch, 4),
-        "max_rel_err_vs_torch_f32": errs,
+        "tokens_per_s": round(cfg.t / ms * 1e3, 1), "ms_bf16x3": round(ms_b, 4),
+        "torch_eager_fwd_bwd_ms": round(ms_torch, 4), "torch_dtype": "f32",
+        "max_rel_err_vs_torch_f32": errs, "max_rel_err_vs_torch_f32_bf16x3": errs_b,
     }
 
 

@@ -283,8 +283,10 @@ int pdh_map_chain(const pdh_ew_program* prog, const void* const* operands, void*
  * the accumulator with PDH_EW_ACC and may not LOAD more than n_operands.
  * dtype PDH_BF16 / PDH_F16: v_mfma_f32_32x32x16, fp32 accumulate, 128x128
  * workgroup tiles (64x64 when 128x128 tiles would not give every compute
- * unit one); PDH_F32: the fp32 column (VALU, fp32 throughout). The
- * sum over k is re-bracketed by 64-wide k tiles (license gemm.k-reassoc). */
+ * unit one); PDH_F32: the same tiles on the bf16 matrix cores, each fp32
+ * operand split into bf16 planes and the cross products summed with fp32
+ * accumulation (pdh_contract_set_f32_mode). The sum over k is re-bracketed
+ * by k tiles (license gemm.k-reassoc). */
 int pdh_contract(const void* a, const void* bt, int64_t batch, int64_t m, int64_t n, int64_t k, int64_t kp,
                  const pdh_ew_program* epi, const void* const* operands, void* out, int dtype, void* stream);
 
@@ -299,6 +301,20 @@ int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, const void* 
                          int64_t batch, int64_t m, int64_t n, int64_t k, const pdh_ew_program* epi,
                          const void* const* operands, void* out, int dtype, void* stream);
 
+/* How PDH_F32 contractions run (pdh_contract, pdh_contract_strided): 6 (the
+ * default) splits each operand into three bf16 terms and sums the six cross
+ * products above 2^-24 of each product: fp32 grade; 3 keeps two terms and
+ * three products (about 2^-16 of each product, twice the rate); 1 rounds the
+ * operands to bf16 (fp32 accumulation and storage: the numerics of a bf16
+ * autocast); 0 runs fp32 VALU fma. In the split modes a workgroup that loads
+ * an inf, a NaN or a value beyond the bf16 range recomputes its tile by fp32
+ * fma, so those behave as in fp32. Returns the previous mode; other values
+ * are refused. The mode is
+ * process-wide: contractions launched while it changes race. Replaces the
+ * fp32 columns of the reference's contraction runners, which compute fp32
+ * products directly (conformance/triton_tile.py:662-698, f32 dtype). */
+int pdh_contract_set_f32_mode(int mode);
+
 /* The ROWSUM and PLAIN shapes of the contraction-epilogue group (fusion.py:
  * 158-252: same-space operands multiplied and summed, or one operand summed,
  * e.g. the backward's D = rowsum(dO * O) and a bias gradient):
@@ -306,7 +322,10 @@ int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, const void* 
  * `summand` runs over the lattice (row dims..., k dims...) whose last nk dims
  * are reduced; `epi` runs over the row dims (its ACC reads the fp32 sum).
  * Both programs index one table of n_operands pointers. One wave per output
- * element. */
+ * element; when the one reduced dim is strided in every summand operand and
+ * one operand is contiguous along the last output dim (a bias gradient), 16
+ * consecutive outputs per workgroup of 1024 lanes instead, 64 lanes each
+ * splitting k, so the loads stay coalesced. */
 int pdh_reduce_rows(const pdh_ew_program* summand, int nk, const pdh_ew_program* epi, const void* const* operands,
                     int n_operands, void* out, int dtype, void* stream);
 /* The same with the reducer chosen: 0 sum (pdh_reduce_rows), 1 max, 2 min.

@@ -44,6 +44,7 @@ EXPORTS = (
     "pdh_reduce_rows_ex",
     "pdh_scan",
     "pdh_ew_set_jit",
+    "pdh_contract_set_f32_mode",
     "pdh_ew_jit_stats",
     "pdh_ew_jit_source",
     "pdh_ew_jit_compile",
@@ -130,6 +131,7 @@ def _declare(lib) -> None:
                                      vp]),
         "pdh_scan": (i32, [vp, vp, i64, i64, i64, i32, i32, i32, vp]),
         "pdh_ew_set_jit": (i32, [i32]),
+        "pdh_contract_set_f32_mode": (i32, [i32]),
         "pdh_ew_jit_stats": (None, [C.POINTER(i64)]),
         "pdh_ew_jit_source": (C.c_size_t, [C.POINTER(EwProgram), i32, i32, C.c_char_p, C.c_size_t]),
         "pdh_ew_jit_compile": (i32, [C.POINTER(EwProgram), i32, i32]),

@@ -2,6 +2,7 @@
 // fusion.py:159-324): the C ABI, its validation, and the launch of either
 // the runtime-specialized kernels (jit.hip) or the interpreter kernels
 // (the bodies of contract_core.h with the program interpreter of ew.h).
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -25,7 +26,7 @@ __global__ __launch_bounds__(256, 2) void contract_mfma(ContractArgs a, pdh_ew_p
 }
 
 template <int DT>
-__global__ __launch_bounds__(256, 4) void contract_mfma_small(ContractArgs a, pdh_ew_program p, EwOperands ops) {
+__global__ __launch_bounds__(256, 2) void contract_mfma_small(ContractArgs a, pdh_ew_program p, EwOperands ops) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[contract_lds<32>()];
   contract_mfma_body<DT, 32, InterpEval>(a, p, ops, smem);
 }
@@ -34,10 +35,43 @@ __global__ __launch_bounds__(256) void contract_f32(ContractArgs a, pdh_ew_progr
   contract_f32_body<InterpEval>(a, p, ops);
 }
 
+template <int NSPLIT>
+__global__ __launch_bounds__(256, 2) void contract_split(ContractArgs a, pdh_ew_program p, EwOperands ops) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[split_lds<64, NSPLIT>()];
+  contract_split_body<PDH_F32, 64, NSPLIT, InterpEval>(a, p, ops, smem);
+}
+
+template <int NSPLIT>
+__global__ __launch_bounds__(256, 2) void contract_split_small(ContractArgs a, pdh_ew_program p, EwOperands ops) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[split_lds<32, NSPLIT>()];
+  contract_split_body<PDH_F32, 32, NSPLIT, InterpEval>(a, p, ops, smem);
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void reduce_rows_kernel(pdh_ew_program ps, pdh_ew_program pe, EwOperands ops,
                                                           void* out, int nk, int rows, int reducer) {
   reduce_rows_body<DT, InterpEval, InterpEval>(ps, pe, ops, out, nk, rows, reducer);
+}
+
+template <int DT>
+__global__ __launch_bounds__(1024) void reduce_cols_kernel(pdh_ew_program ps, pdh_ew_program pe, EwOperands ops,
+                                                           void* out, int nk, int rows, int reducer) {
+  __shared__ float part[kColOut * kColK];
+  (void)nk;
+  reduce_cols_body<DT, InterpEval, InterpEval>(ps, pe, ops, out, rows, reducer, part);
+}
+
+// The column variant pays when k is the strided dim: one reduced dim, every
+// summand operand strided (or broadcast) along it, and one of them
+// contiguous along the last output dim.
+bool reduce_by_columns(const pdh_ew_program& ps, int nk, int nr, int64_t rows) {
+  if (nk != 1 || nr < 1 || rows < kColOut || ps.n_operands < 1) return false;
+  bool contiguous = false;
+  for (int i = 0; i < ps.n_operands; ++i) {
+    if (ps.in_stride[i][nr] == 1) return false;
+    contiguous |= ps.in_stride[i][nr - 1] == 1;
+  }
+  return contiguous;
 }
 
 // -------------------------------------------------------------- validation
@@ -142,6 +176,7 @@ namespace pdh {
 namespace {
 
 int g_cus = 0;  // compute units of the device, read once
+std::atomic<int> g_f32_mode{6};  // fp32 contractions: 6 bf16 products per term (fp32 grade) by default
 
 // Validation shared by both entry points, then the launch: the 128 x 128
 // tiles, or the 64 x 64 ones when the big tiles would not give every compute
@@ -177,7 +212,8 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
     jit_count_launch();
     return PDH_OK;
   };
-  if (ca.dtype == PDH_F32) {
+  const int f32_mode = f32_contract_mode();
+  if (ca.dtype == PDH_F32 && f32_mode == 0) {
     ca.tiles_m = static_cast<int>((m + kFT - 1) / kFT);
     ca.tiles_n = static_cast<int>((n + kFT - 1) / kFT);
     const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
@@ -196,7 +232,24 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
   if (spec) return launch_spec(fns[small ? 1 : 0], nblk);
   PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "%s: grid too large", fn);
   const dim3 grid(static_cast<unsigned>(nblk));
-  if (ca.dtype == PDH_BF16) {
+  if (ca.dtype == PDH_F32) {  // on the bf16 matrix cores, split into planes
+    if (f32_mode == 1) {
+      if (small)
+        contract_split_small<1><<<grid, 256, 0, st>>>(ca, *epi, ops);
+      else
+        contract_split<1><<<grid, 256, 0, st>>>(ca, *epi, ops);
+    } else if (f32_mode == 3) {
+      if (small)
+        contract_split_small<3><<<grid, 256, 0, st>>>(ca, *epi, ops);
+      else
+        contract_split<3><<<grid, 256, 0, st>>>(ca, *epi, ops);
+    } else {
+      if (small)
+        contract_split_small<6><<<grid, 256, 0, st>>>(ca, *epi, ops);
+      else
+        contract_split<6><<<grid, 256, 0, st>>>(ca, *epi, ops);
+    }
+  } else if (ca.dtype == PDH_BF16) {
     if (small)
       contract_mfma_small<PDH_BF16><<<grid, 256, 0, st>>>(ca, *epi, ops);
     else
@@ -211,7 +264,16 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
 }
 
 }  // namespace
+
+int f32_contract_mode() { return g_f32_mode.load(); }
+
 }  // namespace pdh
+
+extern "C" int pdh_contract_set_f32_mode(int mode) {
+  PDH_REQUIRE(mode == 0 || mode == 1 || mode == 3 || mode == 6, PDH_EINVAL,
+              "pdh_contract_set_f32_mode: mode %d (0 VALU fma; 1, 3 or 6 bf16 products per term)", mode);
+  return g_f32_mode.exchange(mode);
+}
 
 extern "C" int pdh_contract(const void* a, const void* bt, int64_t batch, int64_t m, int64_t n, int64_t k,
                             int64_t kp, const pdh_ew_program* epi, const void* const* operands, void* out, int dtype,
@@ -289,22 +351,31 @@ extern "C" int pdh_reduce_rows_ex(const pdh_ew_program* summand, int nk, const p
   for (int i = 0; i < epi->n_operands; ++i)
     if ((rc = check_view(epi, epi->in_stride[i], "pdh_reduce_rows", "epilogue operand"))) return rc;
   hipStream_t st = as_stream(stream);
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  const bool cols = reduce_by_columns(*summand, nk, epi->ndim, rows);
+  const dim3 grid(static_cast<unsigned>(cols ? (rows + kColOut - 1) / kColOut : (rows + 3) / 4));
+  const unsigned threads = cols ? kColOut * kColK : 256;
   int r32 = static_cast<int>(rows);
-  hipFunction_t fn;
-  if (jit_get_reduce(*summand, *epi, dtype, &fn)) {
+  hipFunction_t fns[2];
+  if (jit_get_reduce(*summand, *epi, dtype, fns)) {
     pdh_ew_program a = *summand, b = *epi;
     void* args[] = {&a, &b, &ops, &out, &nk, &r32, &reducer};
-    PDH_REQUIRE(hipModuleLaunchKernel(fn, grid.x, 1, 1, 256, 1, 1, 0, st, args, nullptr) == hipSuccess, PDH_ELAUNCH,
-                "pdh_reduce_rows: specialized launch failed");
+    PDH_REQUIRE(hipModuleLaunchKernel(fns[cols ? 1 : 0], grid.x, 1, 1, threads, 1, 1, 0, st, args, nullptr) == hipSuccess,
+                PDH_ELAUNCH, "pdh_reduce_rows: specialized launch failed");
     jit_count_launch();
     return PDH_OK;
   }
+  auto go = [&](auto dt) {
+    constexpr int DT = decltype(dt)::value;
+    if (cols)
+      reduce_cols_kernel<DT><<<grid, threads, 0, st>>>(*summand, *epi, ops, out, nk, r32, reducer);
+    else
+      reduce_rows_kernel<DT><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32, reducer);
+  };
   if (dtype == PDH_F32)
-    reduce_rows_kernel<PDH_F32><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32, reducer);
+    go(std::integral_constant<int, PDH_F32>{});
   else if (dtype == PDH_BF16)
-    reduce_rows_kernel<PDH_BF16><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32, reducer);
+    go(std::integral_constant<int, PDH_BF16>{});
   else
-    reduce_rows_kernel<PDH_F16><<<grid, 256, 0, st>>>(*summand, *epi, ops, out, nk, r32, reducer);
+    go(std::integral_constant<int, PDH_F16>{});
   return check_launch("pdh_reduce_rows");
 }

@@ -14,8 +14,13 @@
 //                      buffered; XOR-swizzled 16-byte slots keep the b128
 //                      operand reads conflict-free for 32- and 64-bank LDS;
 //                      a and bt are read through batch and row strides
-//   contract_f32_body  the fp32 column: 64 x 64 tiles, 4 x 4 outputs per
-//                      lane, VALU fma, k tiles of 16 through LDS
+//   contract_split_body fp32 on the bf16 matrix cores: the same tiles, fp32
+//                      k tiles of 32 loaded to registers, split into two or
+//                      three bf16 planes in LDS, and the cross products of
+//                      the planes summed by v_mfma_f32_32x32x16_bf16 (3 or 6
+//                      products per term; 6 is fp32 grade)
+//   contract_f32_body  fp32 by VALU fma: 64 x 64 tiles, 4 x 4 outputs per
+//                      lane, k tiles of 16 through LDS
 // The epilogue program runs on the accumulators before the one store:
 // out = epi(acc, operands); the output never makes an HBM round trip.
 #pragma once
@@ -175,6 +180,67 @@ __device__ __forceinline__ void reduce_rows_body(const pdh_ew_program& ps, const
   }
 }
 
+// The same reduce when the summand's operands run along the outputs, not
+// along k (a bias gradient: sum over tokens of dy[t, f], f contiguous). A
+// workgroup of 1024 lanes takes 16 consecutive outputs: lane (q, c), c the
+// output column, q = 0..63 its k lane, sums k = 4 q' + ... in runs of four
+// (k = kk, kk + 64, kk + 128, kk + 192 per evaluation, four loads in flight),
+// so every load instruction covers 16 consecutive outputs at 4 consecutive
+// k. The 64 partials of each output are combined in LDS in a fixed order.
+// nk is 1.
+constexpr int kColOut = 16, kColK = 64;  // outputs per workgroup, k lanes per output
+
+template <int DT, typename EvalS, typename EvalE>
+__device__ __forceinline__ void reduce_cols_body(const pdh_ew_program& ps, const pdh_ew_program& pe,
+                                                 const EwOperands& ops, void* out, int rows, int reducer,
+                                                 float* part) {
+  const int tid = threadIdx.x, col = tid % kColOut, q = tid / kColOut;
+  const int r = static_cast<int>(blockIdx.x) * kColOut + col;
+  const int nr = pe.ndim;
+  auto comb = [reducer](float x, float y) { return reducer == 0 ? x + y : (reducer == 1 ? nan_max(x, y) : nan_min(x, y)); };
+  const float ident = reducer == 0 ? 0.f : (reducer == 1 ? -__builtin_inff() : __builtin_inff());
+  float sum = ident;
+  int c[PDH_EW_MAX_DIMS] = {0, 0, 0, 0};
+  if (r < rows) {
+    int rem = r;
+    for (int d = nr - 1; d >= 0; --d) {
+      const int ext = static_cast<int>(pe.shape[d]);
+      c[d] = rem % ext;
+      rem /= ext;
+    }
+    const int ktot = static_cast<int>(ps.shape[nr]);
+    const float zero4[4] = {0.f, 0.f, 0.f, 0.f};
+    int base = 0;
+    for (; base + 4 * kColK <= ktot; base += 4 * kColK) {
+      c[nr] = base + q;
+      float res[4];
+      EvalS::template run<4>(ps, ops, DT, c, zero4, res, kColK);
+      sum = comb(sum, comb(comb(res[0], res[1]), comb(res[2], res[3])));
+    }
+    const float z1[1] = {0.f};
+    for (int kk = base + q; kk < ktot; kk += kColK) {
+      c[nr] = kk;
+      float r1[1];
+      EvalS::template run<1>(ps, ops, DT, c, z1, r1, 1);
+      sum = comb(sum, r1[0]);
+    }
+  }
+  part[tid] = sum;
+  __syncthreads();
+  if (q == 0 && r < rows) {
+    float tot = part[col];
+    for (int j = 1; j < kColK; ++j) tot = comb(tot, part[col + kColOut * j]);
+    const float a1[1] = {tot};
+    float r1[1];
+    int co[PDH_EW_MAX_DIMS] = {c[0], c[1], c[2], c[3]};
+    for (int d = nr; d < PDH_EW_MAX_DIMS; ++d) co[d] = 0;
+    EvalE::template run<1>(pe, ops, DT, co, a1, r1, 1);
+    long long off = 0;
+    for (int d = 0; d < nr; ++d) off += static_cast<long long>(co[d]) * pe.out_stride[d];
+    st_dt<DT>(out, off, r1[0]);
+  }
+}
+
 // ------------------------------------------------------------ contraction
 
 // 16-byte slot of chunk c (0..7) of tile row r is c ^ swz_gemm(r): conflict
@@ -226,6 +292,36 @@ __device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const
   }
 }
 
+// The epilogue of a WM x WM-per-wave workgroup tile: the accumulators go
+// through LDS (each wave its own WM x WM block, rows padded by 4 floats) and
+// come back four consecutive columns per lane, so one runtime loop holds one
+// copy of the program's code. Accumulator v of tile (i, j) is row
+// 32 i + 8 (v / 4) + 4 g + v % 4, column 32 j + r32 of the wave's block. The
+// caller has passed a barrier after its last read of the operand tiles.
+template <int DT, int WM, typename Eval>
+__device__ __forceinline__ void contract_store(const ContractArgs& a, const pdh_ew_program& p, const EwOperands& ops,
+                                               unsigned char* smem, const f32x16 (&acc)[WM / 32][WM / 32], int b,
+                                               int m0, int n0) {
+  constexpr int TI = WM / 32, ACCP = WM + 4;
+  const int lane = threadIdx.x & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+  const int wy = w >> 1, wx = w & 1;
+  float* blkf = reinterpret_cast<float*>(smem) + w * WM * ACCP;
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TI; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) blkf[(32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * ACCP + 32 * j + r32] = acc[i][j][v];
+  __builtin_amdgcn_wave_barrier();  // the block is wave-private: in-order LDS, no workgroup barrier
+  for (int it = 0; it < WM * WM / 256; ++it) {
+    const int idx = it * 256 + lane * 4;
+    const int row = idx / WM, col = idx % WM;
+    const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * ACCP + col);
+    const float av[4] = {av4[0], av4[1], av4[2], av4[3]};
+    contract_epilogue<DT, 4, Eval>(p, ops, a, b, m0 + WM * wy + row, n0 + WM * wx + col, av);
+  }
+}
+
 template <int DT, int WM, typename Eval>
 __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const pdh_ew_program& p,
                                                    const EwOperands& ops, unsigned char* smem) {
@@ -233,7 +329,6 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
   constexpr int TI = WM / 32;         // 32 x 32 products per wave and dim
   constexpr int TILEB = BM * kRowB;   // LDS bytes per operand tile
   constexpr int BLK = BM / 8 / 4;     // 8-row direct-load blocks per wave and operand
-  constexpr int ACCP = WM + 4;        // accumulator row pitch in LDS (floats)
   constexpr int NS = contract_stages<WM>();
   constexpr int PER_STAGE = 2 * BLK;  // direct loads per wave and k tile
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
@@ -286,6 +381,7 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
     for (int j = 0; j < TI; ++j) acc[i][j] = f32x16{};
 
   const int nkt = a.kp / kBK;
+  static_assert(contract_lds<WM>() >= 2 * NS * TILEB, "operand stages fit the LDS block");
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nkt) stage(s, s);
@@ -317,39 +413,18 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
     __builtin_amdgcn_s_setprio(0);
   }
   wait_vmcnt0();
-
-  // The epilogue reads the accumulators back from LDS (each wave its own
-  // WM x WM block, rows padded by 4 floats): one runtime loop, four
-  // consecutive columns per lane, so one copy of the program's code.
-  // Accumulator v of tile (i, j) is row 32 i + 8 (v / 4) + 4 g + v % 4,
-  // column 32 j + r32 of the wave's block.
   __syncthreads();  // every wave is done with the operand tiles
-  float* blkf = reinterpret_cast<float*>(smem) + w * WM * ACCP;
-#pragma unroll
-  for (int i = 0; i < TI; ++i)
-#pragma unroll
-    for (int j = 0; j < TI; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) blkf[(32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * ACCP + 32 * j + r32] = acc[i][j][v];
-  __builtin_amdgcn_wave_barrier();  // the block is wave-private: in-order LDS, no workgroup barrier
-  for (int it = 0; it < WM * WM / 256; ++it) {
-    const int idx = it * 256 + lane * 4;
-    const int row = idx / WM, col = idx % WM;
-    const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * ACCP + col);
-    const float av[4] = {av4[0], av4[1], av4[2], av4[3]};
-    contract_epilogue<DT, 4, Eval>(p, ops, a, b, m0 + WM * wy + row, n0 + WM * wx + col, av);
-  }
+  contract_store<DT, WM, Eval>(a, p, ops, smem, acc, b, m0, n0);
 }
 
+// One 64 x 64 block (rows m0.., columns n0..) of batch b by fp32 VALU fma,
+// 4 x 4 outputs per lane, k tiles of 16 staged k-major through LDS (as, bs:
+// kFK x (kFT + 4) floats each), and the epilogue applied. Every lane of the
+// workgroup takes part (barriers inside).
 template <typename Eval>
-__device__ __forceinline__ void contract_f32_body(const ContractArgs& a, const pdh_ew_program& p,
-                                                  const EwOperands& ops) {
-  __shared__ float as[kFK][kFT + 4];  // k-major copies of the two 64-row tiles
-  __shared__ float bs[kFK][kFT + 4];
+__device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_ew_program& p, const EwOperands& ops,
+                                               int b, int m0, int n0, float (*as)[kFT + 4], float (*bs)[kFT + 4]) {
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  const int per = a.tiles_m * a.tiles_n;
-  const int b = blockIdx.x / per, rest = blockIdx.x % per;
-  const int m0 = (rest / a.tiles_n) * kFT, n0 = (rest % a.tiles_n) * kFT;
   const float* abase = static_cast<const float*>(a.a) + b * a.sa_b;
   const float* bbase = static_cast<const float*>(a.bt) + b * a.sb_b;
   const int lr = tid >> 2, lc = (tid & 3) * 4;  // this lane's tile row and 4 k values per load
@@ -376,11 +451,214 @@ __device__ __forceinline__ void contract_f32_body(const ContractArgs& a, const p
         for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(x[i], y[j], acc[i][j]);
     }
   }
+  __syncthreads();  // as / bs may be reused by the caller
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float av[4] = {acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
     contract_epilogue<PDH_F32, 4, Eval>(p, ops, a, b, m0 + 4 * ty + i, n0 + 4 * tx, av);
   }
+}
+
+template <typename Eval>
+__device__ __forceinline__ void contract_f32_body(const ContractArgs& a, const pdh_ew_program& p,
+                                                  const EwOperands& ops) {
+  __shared__ float as[kFK][kFT + 4];  // k-major copies of the two 64-row tiles
+  __shared__ float bs[kFK][kFT + 4];
+  const int per = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x / per, rest = blockIdx.x % per;
+  f32_valu_block<Eval>(a, p, ops, b, (rest / a.tiles_n) * kFT, (rest % a.tiles_n) * kFT, as, bs);
+}
+
+// ------------------------------------------- fp32 on the bf16 matrix cores
+
+// An fp32 value as a sum of bf16 terms, each the round-to-nearest of what the
+// previous ones leave: x = x1 + x2 + x3 + r with |x2| <= 2^-8 |x1|,
+// |x3| <= 2^-16 |x1|, |r| <= 2^-24 |x1| (each difference is exact in fp32).
+// The contraction keeps the cross products above 2^-24 |a b|: NSPLIT = 3
+// takes (1,1) (1,2) (2,1), about 2^-16 of each product; NSPLIT = 6 adds
+// (2,2) (1,3) (3,1), about 2^-24: fp32 grade. NSPLIT = 1 keeps x1 alone:
+// bf16-rounded operands with fp32 accumulation and fp32 storage (the
+// numerics of a bf16 autocast). A non-finite x1 (x itself non-finite, or
+// |x| above the largest bf16) is taken alone.
+template <int NSPLIT>
+constexpr int split_planes() {
+  static_assert(NSPLIT == 1 || NSPLIT == 3 || NSPLIT == 6, "NSPLIT is 1, 3 or 6");
+  return NSPLIT == 1 ? 1 : (NSPLIT == 3 ? 2 : 3);
+}
+constexpr int kSBK = 32;          // fp32 k values per k tile
+constexpr int kSRowB = kSBK * 2;  // bytes per row of one bf16 plane: four 16-byte slots of 8 k values
+
+// LDS bytes of the split variant: PL planes of both operand tiles, or the
+// epilogue's accumulator blocks.
+template <int WM, int NSPLIT>
+constexpr int split_lds() {
+  return split_planes<NSPLIT>() * 2 * (2 * WM) * kSRowB > 4 * WM * (WM + 4) * 4
+             ? split_planes<NSPLIT>() * 2 * (2 * WM) * kSRowB
+             : 4 * WM * (WM + 4) * 4;
+}
+
+// Slot s (0..3) of plane row r sits at s ^ swz_split(r): the b128 operand
+// reads of 16 consecutive rows at one slot then cover all 64 banks once.
+__device__ __forceinline__ int swz_split(int r) { return (r >> 2) & 3; }
+
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
+
+// Two fp32 as two bf16 (lo = x, hi = y), round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t rne_bf16x2(float x, float y) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_v{x, y}, bf16x2_v));
+}
+
+// Four consecutive fp32 of one row -> PL planes of four bf16 each; true when
+// a leading term is not finite.
+template <int PL>
+__device__ __forceinline__ bool split4(u32x4 v, u32x2 (&out)[PL]) {
+  float r[4];
+  bool odd = false;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float x0 = __uint_as_float(v[2 * j]), x1 = __uint_as_float(v[2 * j + 1]);
+    const uint32_t h = rne_bf16x2(x0, x1);
+    out[0][j] = h;
+    const float f0 = __uint_as_float(h << 16), f1 = __uint_as_float(h & 0xffff0000u);
+    const bool ok0 = __builtin_fabsf(f0) < __builtin_inff(), ok1 = __builtin_fabsf(f1) < __builtin_inff();
+    r[2 * j] = ok0 ? x0 - f0 : 0.f;
+    r[2 * j + 1] = ok1 ? x1 - f1 : 0.f;
+    odd |= !(ok0 && ok1);
+  }
+#pragma unroll
+  for (int p = 1; p < PL; ++p)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t h = rne_bf16x2(r[2 * j], r[2 * j + 1]);
+      out[p][j] = h;
+      if (p + 1 < PL) {
+        r[2 * j] -= __uint_as_float(h << 16);
+        r[2 * j + 1] -= __uint_as_float(h & 0xffff0000u);
+      }
+    }
+  return odd;
+}
+
+template <int DT, int WM, int NSPLIT, typename Eval>
+__device__ __forceinline__ void contract_split_body(const ContractArgs& a, const pdh_ew_program& p,
+                                                    const EwOperands& ops, unsigned char* smem) {
+  constexpr int BM = 2 * WM, TI = WM / 32, PL = split_planes<NSPLIT>();
+  constexpr int PLANEB = BM * kSRowB;  // one plane of one operand tile
+  constexpr int CH = BM / 32;          // 16-byte fp32 chunks per lane and operand: rows (tid / 8) + 32 c
+  static_assert(split_lds<WM, NSPLIT>() >= PL * 2 * PLANEB, "planes fit the LDS block");
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+  const int wy = w >> 1, wx = w & 1;
+  const int per = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x / per, rest = blockIdx.x % per;
+  const int m0 = (rest / a.tiles_n) * BM, n0 = (rest % a.tiles_n) * BM;
+  const uint32_t rowa = static_cast<uint32_t>(a.sa_r) * 4u, rowbb = static_cast<uint32_t>(a.sb_r) * 4u;
+  const float* abase = static_cast<const float*>(a.a) + b * a.sa_b;
+  const float* bbase = static_cast<const float*>(a.bt) + b * a.sb_b;
+  // the buffers end after the batch slice's last row: rows past m (n) read as zero
+  const rsrc_t ar = make_rsrc(abase, (static_cast<uint32_t>(a.m) - 1u) * rowa + static_cast<uint32_t>(a.kp) * 4u);
+  const rsrc_t br = make_rsrc(bbase, (static_cast<uint32_t>(a.n) - 1u) * rowbb + static_cast<uint32_t>(a.kp) * 4u);
+
+  // loads: lane tid takes k values 4 (tid % 8) .. + 3 of rows tid / 8 + 32 c
+  const int lrow = tid >> 3, lchunk = tid & 7;
+  const uint32_t la = lrow * rowa + lchunk * 16u, lb = lrow * rowbb + lchunk * 16u;
+  // where those four k values land in a plane: slot lchunk / 2 (swizzled), half lchunk % 2
+  int wr[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int row = lrow + 32 * c;
+    wr[c] = row * kSRowB + (((lchunk >> 1) ^ swz_split(row)) << 4) + ((lchunk & 1) << 3);
+  }
+  // operand reads: row 32 t + r32 (+ WM q) of a plane, slot 2 ks + g
+  int rd[TI][2];
+#pragma unroll
+  for (int t = 0; t < TI; ++t)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int row = 32 * t + r32;  // + WM q: a multiple of 32 rows, so the swizzle is unchanged
+      rd[t][ks] = row * kSRowB + (((2 * ks + g) ^ swz_split(row)) << 4);
+    }
+
+  u32x4 va[CH], vb[CH];
+  auto fetch = [&](int kt) {
+    const uint32_t koff = static_cast<uint32_t>(kt) * kSBK * 4u;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      va[c] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, la, static_cast<uint32_t>(m0 + 32 * c) * rowa + koff, 0));
+      vb[c] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, lb, static_cast<uint32_t>(n0 + 32 * c) * rowbb + koff, 0));
+    }
+  };
+
+  f32x16 acc[TI][TI];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TI; ++j) acc[i][j] = f32x16{};
+
+  const int nkt = a.kp / kSBK;
+  bool odd = false;  // a non-finite leading term (an inf, a NaN, |x| above the largest bf16) in this lane's loads
+  fetch(0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    __syncthreads();  // every wave is done reading the planes of tile kt - 1
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      u32x2 pa[PL], pb[PL];
+      odd |= split4<PL>(va[c], pa);
+      odd |= split4<PL>(vb[c], pb);
+#pragma unroll
+      for (int pl = 0; pl < PL; ++pl) {
+        *reinterpret_cast<u32x2*>(smem + (2 * pl) * PLANEB + wr[c]) = pa[pl];
+        *reinterpret_cast<u32x2*>(smem + (2 * pl + 1) * PLANEB + wr[c]) = pb[pl];
+      }
+    }
+    if (kt + 1 < nkt) fetch(kt + 1);  // in flight under this tile's products
+    __syncthreads();                  // the planes of tile kt are in LDS
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4 af[PL][TI], bf[PL][TI];
+#pragma unroll
+      for (int pl = 0; pl < PL; ++pl)
+#pragma unroll
+        for (int t = 0; t < TI; ++t) {
+          af[pl][t] = *reinterpret_cast<const u32x4*>(smem + (2 * pl) * PLANEB + WM * wy * kSRowB + rd[t][ks]);
+          bf[pl][t] = *reinterpret_cast<const u32x4*>(smem + (2 * pl + 1) * PLANEB + WM * wx * kSRowB + rd[t][ks]);
+        }
+      // smallest terms first; (pa, pb) plane pairs
+      constexpr int NP = NSPLIT;
+      constexpr int PA[6] = {NSPLIT == 6 ? 2 : (NSPLIT == 3 ? 1 : 0), 0, NSPLIT == 6 ? 1 : 0, 1, 0, 0};
+      constexpr int PB[6] = {0, NSPLIT == 6 ? 2 : 1, NSPLIT == 6 ? 1 : 0, 0, 1, 0};
+#pragma unroll
+      for (int q = 0; q < NP; ++q)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int j = 0; j < TI; ++j) acc[i][j] = mfma32_dt<PDH_BF16>(af[PA[q]][i], bf[PB[q]][j], acc[i][j]);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __syncthreads();  // every wave is done with the planes
+  // A plane product of an inf with an exact zero of the other operand's
+  // lower plane is NaN where IEEE arithmetic gives the inf: a workgroup that
+  // loaded any non-finite (or bf16-overflowing) value recomputes its tile by
+  // fp32 VALU fma instead, so such values behave as in fp32.
+  int* flags = reinterpret_cast<int*>(smem);
+  const bool wave_odd = __builtin_amdgcn_ballot_w64(odd) != 0;  // every lane votes
+  if (lane == 0) flags[w] = wave_odd ? 1 : 0;
+  __syncthreads();
+  const bool slow = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
+  __syncthreads();  // every wave has read the flags before the LDS is reused
+  if (slow) {
+    float(*as)[kFT + 4] = reinterpret_cast<float(*)[kFT + 4]>(smem);
+    float(*bs)[kFT + 4] = reinterpret_cast<float(*)[kFT + 4]>(smem + kFK * (kFT + 4) * 4);
+#pragma unroll 1
+    for (int ij = 0; ij < (BM / kFT) * (BM / kFT); ++ij)  // one copy of the block's code
+      f32_valu_block<Eval>(a, p, ops, b, m0 + kFT * (ij / (BM / kFT)), n0 + kFT * (ij % (BM / kFT)), as, bs);
+    return;
+  }
+  contract_store<DT, WM, Eval>(a, p, ops, smem, acc, b, m0, n0);
 }
 
 }  // namespace pdh

@@ -13,8 +13,12 @@ bool jit_enabled();
 // the kernel specialized for program p and element type dt; false when the
 // interpreter kernels must run it (disabled, or the compile failed).
 bool jit_get(JitKind kind, const pdh_ew_program& p, int dt, hipFunction_t fns[2]);
-// The row-reduce kernel specialized for (summand, epilogue), or false.
-bool jit_get_reduce(const pdh_ew_program& ps, const pdh_ew_program& pe, int dt, hipFunction_t* fn);
+// The row-reduce kernels specialized for (summand, epilogue): fns[0] one wave
+// per output, fns[1] the column variant; or false.
+bool jit_get_reduce(const pdh_ew_program& ps, const pdh_ew_program& pe, int dt, hipFunction_t fns[2]);
 void jit_count_launch();
+// How fp32 contractions run: 0 VALU fma; 1, 3 or 6 bf16 MFMA products per term
+// (pdh_contract_set_f32_mode).
+int f32_contract_mode();
 
 }  // namespace pdh

@@ -342,12 +342,20 @@ class PlanExecutor:
     type of every floating value (f32, bf16 or f16). ``fuse_attention``
     launches a softmax carve and its PV carve as one flash forward where they
     compute banded attention (``_attention_chains``); ``merge_projections``
-    then makes q, k and v with one GEMM where they project one activation."""
+    then makes q, k and v with one GEMM where they project one activation.
+    ``f32_contract`` (dtype f32) is how the contractions run: "bf16x6" (fp32
+    grade, the default), "bf16x3", "bf16" (operands rounded to bf16, fp32
+    accumulation and storage: the numerics of a bf16 autocast) or "fma"."""
 
     def __init__(self, plan, region: Region, dtype: str = "bf16", fuse_attention: bool = True,
-                 merge_projections: bool = True, _shared=None):
+                 merge_projections: bool = True, _shared=None, f32_contract: str = "bf16x6"):
         if dtype not in _TORCH_DT:
             raise ValueError(f"dtype {dtype!r}: f32, bf16 or f16")
+        from .kernels import F32_CONTRACT
+
+        if f32_contract not in F32_CONTRACT:
+            raise ValueError(f"f32_contract {f32_contract!r}: one of {sorted(F32_CONTRACT)}")
+        self.f32_contract = f32_contract
         self.region, self.dtype = region, dtype
         self.params = region.params
         self.nested: list = []
@@ -495,7 +503,7 @@ class PlanExecutor:
             else:
                 sub, sb = src
                 nested = PlanExecutor(plan_model(sub, dissolve=False), sub, self.dtype,
-                                      _shared=(self._packs, self._static))
+                                      _shared=(self._packs, self._static), f32_contract=self.f32_contract)
                 self.nested.append(nested)
                 getters.append((nested, sub, at, len(sb)))
                 at += len(sb)
@@ -671,7 +679,8 @@ class PlanExecutor:
         from .tl.partition import plan_model
 
         sub = _yielding(k, node)
-        nested = PlanExecutor(plan_model(sub, dissolve=False), sub, self.dtype, _shared=(self._packs, self._static))
+        nested = PlanExecutor(plan_model(sub, dissolve=False), sub, self.dtype, _shared=(self._packs, self._static),
+                              f32_contract=self.f32_contract)
         self.nested.append(nested)
 
         def run(vals):
@@ -830,9 +839,9 @@ class PlanExecutor:
             out = torch.empty(shape, device="cuda", dtype=dt)
             if KP == Kx:  # every operand as stored (or as packed), through its strides
                 K.contract_strided(a, pa.strides, bt, pb.strides, (B, M, N, Kx), prog,
-                                   [vals[i] for i in eslots], out)
+                                   [vals[i] for i in eslots], out, f32_mode=self.f32_contract)
             else:  # zero-padded packs
-                K.contract(a, bt, Kx, prog, [vals[i] for i in eslots], out)
+                K.contract(a, bt, Kx, prog, [vals[i] for i in eslots], out, f32_mode=self.f32_contract)
             return out
 
         def how(p):
@@ -840,6 +849,8 @@ class PlanExecutor:
                                                           ("plan+pack" if p.pre else "pack"))
 
         src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
+        if self.dtype == "f32":
+            src += f" f32={self.f32_contract}"
         return run, src
 
     def _bare_reduce(self, k):
@@ -1106,7 +1117,7 @@ class PlanExecutor:
             params = tuple(memo[id(p)] for p in k.params) + (hole,)
             region = Region(params=params, body=(b.emit("core.yield", rebuild_into(b, memo, y)),))
             nested = PlanExecutor(plan_model(region, dissolve=False), region, self.dtype,
-                                  _shared=(self._packs, self._static))
+                                  _shared=(self._packs, self._static), f32_contract=self.f32_contract)
             self.nested.append(nested)
             rest = (region, nested)
 
@@ -1184,6 +1195,11 @@ class PlanExecutor:
             out = self._run(self.bound, bads)
         self._graph, self._graph_out, self._graph_bads = graph, out, bads
         return out
+
+    def release_graph(self) -> None:
+        """Drop the captured graph and the tensors it holds (its output and
+        the memory pool torch keeps for it go with the last reference)."""
+        self._graph = self._graph_out = self._graph_bads = None
 
     def replay(self, check: bool = True):
         """Replay the captured pass; with ``check``, synchronize and raise if a

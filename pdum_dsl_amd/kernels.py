@@ -390,11 +390,36 @@ def map_chain(prog: _lib.EwProgram, operands: list, out: torch.Tensor) -> torch.
     return out
 
 
+# How fp32 contractions run (pdh_contract_set_f32_mode): bf16 matrix-core
+# products of split operands (6: fp32 grade, 3, or 1: bf16-rounded operands
+# with fp32 accumulation, an autocast's numerics), or fp32 VALU fma.
+F32_CONTRACT = {"bf16x6": 6, "bf16x3": 3, "bf16": 1, "fma": 0}
+
+
+def set_f32_contract(mode: str) -> str:
+    """Set how fp32 contractions run, process-wide; returns the previous mode."""
+    if mode not in F32_CONTRACT:
+        raise ValueError(f"f32 contraction mode {mode!r}: one of {sorted(F32_CONTRACT)}")
+    prev = _lib.lib().pdh_contract_set_f32_mode(F32_CONTRACT[mode])
+    return next(k for k, v in F32_CONTRACT.items() if v == prev)
+
+
+def _with_f32_mode(mode, dtype, launch):
+    if mode is None or dtype != torch.float32:
+        return launch()
+    prev = set_f32_contract(mode)
+    try:
+        return launch()
+    finally:
+        set_f32_contract(prev)
+
+
 def contract(a: torch.Tensor, bt: torch.Tensor, k: int, epi: _lib.EwProgram, operands: list,
-             out: torch.Tensor) -> torch.Tensor:
+             out: torch.Tensor, f32_mode: str | None = None) -> torch.Tensor:
     """acc[b, m, n] = sum_k a[b, m, k] bt[b, n, k]; out = epi(acc, operands).
     a: [batch, m, kp], bt: [batch, n, kp] contiguous, kp % 64 == 0, columns
-    k..kp-1 zero. The epilogue program's lattice is (batch, m, n)."""
+    k..kp-1 zero. The epilogue program's lattice is (batch, m, n).
+    ``f32_mode`` (fp32 operands only) picks F32_CONTRACT's mode for this call."""
     _require_cuda(a, bt, out, *operands)
     if a.dim() != 3 or bt.dim() != 3 or not a.is_contiguous() or not bt.is_contiguous():
         raise ValueError("a and bt must be contiguous [batch, rows, kp]")
@@ -406,15 +431,15 @@ def contract(a: torch.Tensor, bt: torch.Tensor, k: int, epi: _lib.EwProgram, ope
         raise ValueError("the epilogue's lattice must be (batch, m, n)")
     _check_views(epi, operands, out, 3)
     table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
-    _lib.call(
+    _with_f32_mode(f32_mode, a.dtype, lambda: _lib.call(
         "pdh_contract", _ptr(a), _ptr(bt), B, M, N, int(k), KP, C.byref(epi), table, _ptr(out), _DT[a.dtype],
         C.c_void_p(_stream()),
-    )
+    ))
     return out
 
 
 def contract_strided(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, shape, epi: _lib.EwProgram,
-                     operands: list, out: torch.Tensor) -> torch.Tensor:
+                     operands: list, out: torch.Tensor, f32_mode: str | None = None) -> torch.Tensor:
     """acc[b, m, n] = sum_k a[b, m, k] bt[b, n, k] with a and bt read through
     (batch, row) element strides from their tensors' first elements; k is
     contiguous and a multiple of 64. ``shape`` = (batch, m, n, k)."""
@@ -430,10 +455,10 @@ def contract_strided(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, s
         raise ValueError("the epilogue's lattice must be (batch, m, n)")
     _check_views(epi, operands, out, 3)
     table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
-    _lib.call(
+    _with_f32_mode(f32_mode, a.dtype, lambda: _lib.call(
         "pdh_contract_strided", _ptr(a), int(a_strides[0]), int(a_strides[1]), _ptr(bt), int(bt_strides[0]),
         int(bt_strides[1]), B, M, N, Kd, C.byref(epi), table, _ptr(out), _DT[a.dtype], C.c_void_p(_stream()),
-    )
+    ))
     return out
 
 

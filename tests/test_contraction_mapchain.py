@@ -325,6 +325,29 @@ def test_specialized_kernels_compile_offline_for_every_element_type():
     assert "contract_mfma_body<PDH_BF16, 64, pdh::GenEval>" in src and "contract_mfma_body<PDH_BF16, 32, pdh::GenEval>" in src
 
 
+def test_fp32_contractions_compile_in_every_mode():
+    """fp32 contractions run on the bf16 matrix cores (operands split into
+    bf16 planes, 6 or 3 cross products per term) or by VALU fma; the mode is
+    process-wide, refused outside {0, 3, 6}, and each mode's specialized
+    kernels compile offline."""
+    lib = L.lib()
+    epi, _chain = _zoo_programs()
+    prev = lib.pdh_contract_set_f32_mode(3)
+    try:
+        assert prev == 6  # the default: fp32 grade
+        assert lib.pdh_contract_set_f32_mode(7) == L.PDH_EINVAL and "mode 7" in L.last_error()
+        buf = C.create_string_buffer(1 << 16)
+        for mode, body in ((6, "contract_split_body<PDH_F32, 64, 6, pdh::GenEval>"),
+                           (3, "contract_split_body<PDH_F32, 32, 3, pdh::GenEval>"),
+                           (0, "contract_f32_body<pdh::GenEval>")):
+            lib.pdh_contract_set_f32_mode(mode)
+            assert lib.pdh_ew_jit_compile(C.byref(epi), 1, L.PDH_F32) == 0, L.last_error()
+            lib.pdh_ew_jit_source(C.byref(epi), 1, L.PDH_F32, buf, len(buf))
+            assert body in buf.value.decode()
+    finally:
+        lib.pdh_contract_set_f32_mode(prev)
+
+
 def test_the_tanh_identity_the_kernels_use_is_accurate_in_fp32():
     """dev.h's pdh_tanh: tanh|x| = 1 - 2 / (2^(2|x| log2 e) + 1), sign copied.
     The same float32 steps in numpy (exp2 and a correctly rounded reciprocal

@@ -216,3 +216,76 @@ def test_the_interpreter_and_the_specialized_kernels_agree(jit):
         assert (launched >= 2) if jit else (launched == 0)
     finally:
         lib.pdh_ew_set_jit(prev)
+
+
+def _identity_epilogue(out):
+    from pdum_dsl_amd import _lib as L
+
+    p = L.EwProgram()
+    p.n_insns, p.n_operands, p.ndim, p.out_reg = 1, 0, 3, 0
+    for d, (ext, st) in enumerate(zip(out.shape, out.stride())):
+        p.shape[d], p.out_stride[d] = ext, st
+    p.insns[0].op = L.EW["ACC"]
+    return p
+
+
+def _fp32_gemm(a, bt, kd, mode):
+    from pdum_dsl_amd import _lib as L
+    from pdum_dsl_amd import kernels as K
+
+    lib = L.lib()
+    out = torch.empty(a.shape[0], a.shape[1], bt.shape[1], device="cuda", dtype=torch.float32)
+    prev = lib.pdh_contract_set_f32_mode(mode)
+    try:
+        K.contract(a, bt, kd, _identity_epilogue(out), [], out)
+        torch.cuda.synchronize()
+    finally:
+        lib.pdh_contract_set_f32_mode(prev)
+    return out.double().cpu().numpy()
+
+
+# mode -> tolerance as a fraction of the output's scale: 6 bf16 products per
+# term and VALU fma are fp32 grade; 3 products keep about 2^-16 of each
+# product; 1 (bf16-rounded operands) is exact against bf16-rounded inputs
+@pytest.mark.parametrize("mode,tol", [(6, 1e-5), (3, 5e-5), (1, 1e-5), (0, 1e-5)])
+@pytest.mark.parametrize("B,M,N,Kd", [(2, 300, 260, 200), (1, 1100, 2100, 768)])  # 64x64 tiles; 128x128 tiles
+def test_fp32_contractions_against_float64(mode, tol, B, M, N, Kd):
+    """fp32 a @ bt^T on the bf16 matrix cores (the operands split into bf16
+    planes) or by VALU fma, against float64 numpy on the same fp32 inputs."""
+    g = torch.Generator(device="cuda").manual_seed(13)
+    KP = (Kd + 63) // 64 * 64
+    a = torch.zeros(B, M, KP, device="cuda")
+    bt = torch.zeros(B, N, KP, device="cuda")
+    a[..., :Kd] = torch.randn(B, M, Kd, device="cuda", generator=g)
+    bt[..., :Kd] = torch.randn(B, N, Kd, device="cuda", generator=g) * 3.0
+    got = _fp32_gemm(a, bt, Kd, mode)
+    an, bn = a.double().cpu().numpy(), bt.double().cpu().numpy()
+    if mode == 1:  # operands rounded to bf16 (nearest even), products and sums in fp32
+        an, bn = (t.to(torch.bfloat16).double().cpu().numpy() for t in (a, bt))
+    want = np.einsum("bmk,bnk->bmn", an, bn)
+    err = np.abs(got - want).max()
+    assert err <= tol * np.abs(want).max() * max(1.0, (Kd / 64) ** 0.5), f"mode {mode}: max err {err:.3e}"
+
+
+@pytest.mark.parametrize("mode", [6, 3])
+def test_non_finite_fp32_operands_behave_as_in_fp32(mode):
+    """An inf times a value exact in bf16 would meet a zero lower plane (inf *
+    0 = NaN); workgroups that load a non-finite value recompute by fp32 fma,
+    so infs and NaNs land where IEEE arithmetic puts them, and every other
+    workgroup keeps the split result."""
+    g = torch.Generator(device="cuda").manual_seed(17)
+    B, M, N, Kd = 1, 700, 600, 256
+    a = torch.randn(B, M, Kd, device="cuda", generator=g)
+    bt = torch.randn(B, N, Kd, device="cuda", generator=g).round()  # integers: exact in bf16, zero lower planes
+    bt[bt == 0] = 1.0
+    a[0, 5, 17] = float("inf")
+    a[0, 650, 3] = -float("inf")
+    bt[0, 333, 40] = float("nan")
+    got = _fp32_gemm(a, bt, Kd, mode)
+    want = np.einsum("bmk,bnk->bmn", a.double().cpu().numpy(), bt.double().cpu().numpy())
+    assert np.array_equal(np.isnan(got), np.isnan(want)) and np.isnan(want).sum() == M  # column 333
+    assert np.isinf(want).sum() == 2 * (N - 1)  # rows 5 and 650 away from column 333
+    assert np.array_equal(np.isinf(got), np.isinf(want)) and np.array_equal(got[np.isinf(got)], want[np.isinf(want)])
+    fin = np.isfinite(want)
+    tol = (1e-5 if mode == 6 else 5e-5) * np.abs(want[fin]).max() * 2.0
+    assert np.abs(got[fin] - want[fin]).max() <= tol

@@ -54,7 +54,7 @@ def _oracle(region, vals):
 
 
 CASES = [("rowsum", ("s",), None, "sum"), ("rowsum", ("s",), "scale_bias", "sum"), ("plain", ("t",), None, "sum"),
-         ("plain", ("s",), None, "mean"), ("plain", ("t", "s"), None, "sum")]
+         ("plain", ("t",), "scale_bias", "sum"), ("plain", ("s",), None, "mean"), ("plain", ("t", "s"), None, "sum")]
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -89,3 +89,33 @@ def test_the_executor_runs_a_rowsum_carve():
     got = ex.run().cpu().numpy()
     want = _oracle(region, vals)
     assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("f", ["sum", "max", "min"])
+@pytest.mark.parametrize("T,S", [(1024, 3072), (37, 307)])
+def test_a_reduction_over_the_strided_dim_runs_by_columns(f, T, S):
+    """x[t, s] reduced over t (s contiguous: a bias gradient's shape) takes the
+    column variant of pdh_reduce_rows_ex (16 consecutive outputs per
+    workgroup, coalesced loads); against numpy, NaN positions included."""
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl.dialect import OPS
+    from pdum_dsl_amd.tl.ir import Builder, Region, tensor_type
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    b = Builder(OPS)
+    x = b.param(0, tensor_type(("t", "s"), (T, S)))
+    y = b.emit("tl.reduce", x, dims=("t",), f=f)
+    region = Region(params=(x,), body=(b.emit("core.yield", y),))
+    ex = PlanExecutor(plan_model(region), region, "f32")
+    xv = np.random.default_rng(T + S).standard_normal((T, S))
+    xv[T // 2, 5] = np.nan
+    ex.bind([xv])
+    got = ex.run().cpu().numpy().astype(np.float64)
+    torch.cuda.synchronize()
+    want = {"sum": np.sum, "max": np.max, "min": np.min}[f](xv.astype(np.float32).astype(np.float64), axis=0)
+    assert np.array_equal(np.isnan(got), np.isnan(want)) and np.isnan(want).sum() == 1
+    ok = ~np.isnan(want)
+    if f == "sum":
+        assert np.abs(got[ok] - want[ok]).max() <= 1e-5 * max(1.0, np.abs(want[ok]).max()) * (T / 64) ** 0.5
+    else:
+        np.testing.assert_array_equal(got[ok], want[ok])
