@@ -176,7 +176,10 @@ int pdh_flash_fwd_split(const void* q, const void* k, const void* v, void* o, fl
  * statistic, masked-entry probability per row; written).
  * dtype PDH_BF16 / PDH_F16: MFMA kernels, e == od in {64, 128}, 16-byte
  * aligned tensors, strides multiples of 8 elements. PDH_F32: the fp32 column
- * (VALU), any 1 <= e, od <= 512. heads_q == heads_kv. */
+ * (VALU), any 1 <= e, od <= 512. Grouped-query heads (heads_q a multiple of
+ * heads_kv; query head h reads K / V head h / (heads_q / heads_kv)): dk / dv
+ * of a K / V head sum over the query heads of its group, each written by
+ * one workgroup (no atomics). */
 int pdh_flash_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
                   const float* lse, const float* m_in, const float* den_in, void* dq, void* dk, void* dv,
                   float* ws, const pdh_attn_geom* geom, int dtype, float scale, float fill,

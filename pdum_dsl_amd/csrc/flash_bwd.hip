@@ -17,6 +17,11 @@
 //   bwd_dq    : grid over 128-query blocks; sweeps key tiles:
 //                 S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T
 //
+// Grouped-query attention (heads_q = group x heads_kv, query head h reading
+// K / V head h / group): a dK / dV workgroup sweeps the query tiles of every
+// query head of its group in turn into the same accumulators, and a dQ
+// workgroup reads its group's K and V. Every output still has one owner.
+//
 // All products are v_mfma_f32_32x32x16 (bf16 / f16 in, fp32 accumulate).
 // LDS tiles whose rows become an MFMA A operand are stored with the
 // kperm_inv row permutation, so the score accumulators feed the next
@@ -42,15 +47,18 @@ struct BwdArgs {
   uint16_t* dk;
   uint16_t* dv;
   float* ws;            // [3][rows]: -delta, lse2, pm
-  int64_t rows;         // batch * heads * t
-  int64_t heads, t, s;
+  int64_t rows;         // batch * heads * t (query rows)
+  int64_t heads, t, s;  // heads: query heads
+  int64_t heads_kv;     // K / V heads; query head h reads K / V head h / group
+  int group;            // heads / heads_kv
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
   float scale, c2, fill2;
   int masked;
   int64_t band_lo, band_hi;
   int prune;
-  int ninst;          // batch * heads
-  int nkblk, nqblk;   // 128-key blocks (dK, dV) and 128-query blocks (dQ) per instance
+  int ninst;          // batch * heads (query instances)
+  int ninst_kv;       // batch * heads_kv (K / V instances)
+  int nkblk, nqblk;   // 128-key blocks (dK, dV) per K / V instance, 128-query blocks (dQ) per query instance
   int xcd_remap;
 };
 
@@ -189,10 +197,10 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
   const int64_t inst = bid / a.nqblk;
   const int qb = a.nqblk - 1 - (bid % a.nqblk);  // heavy (late) query blocks first
-  const int64_t b = inst / a.heads, h = inst % a.heads;
+  const int64_t b = inst / a.heads, h = inst % a.heads, hkv = h / a.group;
   const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-  const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-  const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+  const uint16_t* kp = a.k + b * a.k_sb + hkv * a.k_sh;
+  const uint16_t* vp = a.v + b * a.v_sb + hkv * a.v_sh;
   const uint16_t* dop = a.dout + b * a.o_sb + h * a.o_sh;
   const int64_t T_ = a.t, S_ = a.s;
   const int q0 = qb * BM;
@@ -331,13 +339,11 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
   constexpr int KS = TT::KS, DB = TT::DB, BK = 128, QT = 32;
   constexpr int STATB = 4 * kSub * TT::BYTES;  // [2][kSub][delta | lse2 | pm] x 32 floats
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
-  const int64_t inst = bid / a.nkblk;
+  const int64_t kinst = bid / a.nkblk;  // K / V instance
   const int kblk = bid % a.nkblk;  // early key blocks see the most queries under causal masks: launched first
-  const int64_t b = inst / a.heads, h = inst % a.heads;
-  const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-  const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-  const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
-  const uint16_t* dop = a.dout + b * a.o_sb + h * a.o_sh;
+  const int64_t b = kinst / a.heads_kv, hkv = kinst % a.heads_kv;
+  const uint16_t* kp = a.k + b * a.k_sb + hkv * a.k_sh;
+  const uint16_t* vp = a.v + b * a.v_sb + hkv * a.v_sh;
   const int64_t T_ = a.t, S_ = a.s;
   const int k0 = kblk * BK;
   const int kw0 = k0 + 32 * w;
@@ -375,32 +381,50 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
   }
 
   const uint32_t grq = static_cast<uint32_t>(a.q_st * 2), gro = static_cast<uint32_t>(a.o_st * 2);
-  const rsrc_t qr = make_rsrc(qp, static_cast<uint32_t>((T_ - 1) * a.q_st * 2 + D * 2));
-  const rsrc_t orr = make_rsrc(dop, static_cast<uint32_t>((T_ - 1) * a.o_st * 2 + D * 2));
   const rsrc_t sr = make_rsrc(a.ws, static_cast<uint32_t>(3 * a.rows * 4));
   TileLane<D> ql, ol;
   ql.init(lane, w, r32, g, grq);
   ol.init(lane, w, r32, g, gro);
+  // The sweep runs over (query head of the group, query tile) items, head-major,
+  // with two cursors kept by increments (no divisions): one staging a stage
+  // ahead, one computing.
+  struct Cursor {
+    int gq, qt;
+  };
+  const int nqt_live = qt_hi - qt_lo;
+  auto advance = [&](Cursor& c) {
+    if (++c.qt == qt_hi) {
+      c.qt = qt_lo;
+      ++c.gq;
+    }
+  };
   // stats: wave 0 loads delta (lanes 0-31) and lse2 (32-63), then pm (0-31)
-  const uint32_t st_off0 = static_cast<uint32_t>(((lane >> 5) * a.rows + inst * T_ + r32) * 4);
-  const uint32_t st_off1 = static_cast<uint32_t>((2 * a.rows + inst * T_ + r32) * 4);
+  const uint32_t st_lane0 = static_cast<uint32_t>(((lane >> 5) * a.rows + r32) * 4);
+  const uint32_t st_lane1 = static_cast<uint32_t>((2 * a.rows + r32) * 4);
+  const int64_t hq0 = hkv * a.group;  // the group's first query head
   auto qbuf = [&](int buf, int sub) { return smem + (buf * kSub + sub) * TT::BYTES; };
   auto obuf = [&](int buf, int sub) { return smem + ((2 + buf) * kSub + sub) * TT::BYTES; };
   auto sbuf = [&](int buf, int sub) {
     return reinterpret_cast<float*>(smem + STATB + (buf * kSub + sub) * 3 * QT * 4);
   };
-  auto stage = [&](int qt0, int buf) {  // tiles qt0 .. qt0 + kSub - 1 that the sweep reads
+  Cursor sc{0, qt_lo};  // the next item to stage
+  auto stage = [&](int buf) {  // the next kSub items, into buffer buf
 #pragma unroll
     for (int sub = 0; sub < kSub; ++sub) {
-      const int qt = qt0 + sub;
-      if (qt >= qt_hi) break;
-      ql.stage(qr, qbuf(buf, sub), static_cast<uint32_t>(qt * QT), grq, w);
-      ol.stage(orr, obuf(buf, sub), static_cast<uint32_t>(qt * QT), gro, w);
+      if (sc.gq >= a.group) break;
+      const int64_t hq = hq0 + sc.gq;
+      const rsrc_t qr = make_rsrc(a.q + b * a.q_sb + hq * a.q_sh, static_cast<uint32_t>((T_ - 1) * a.q_st * 2 + D * 2));
+      const rsrc_t orr =
+          make_rsrc(a.dout + b * a.o_sb + hq * a.o_sh, static_cast<uint32_t>((T_ - 1) * a.o_st * 2 + D * 2));
+      ql.stage(qr, qbuf(buf, sub), static_cast<uint32_t>(sc.qt * QT), grq, w);
+      ol.stage(orr, obuf(buf, sub), static_cast<uint32_t>(sc.qt * QT), gro, w);
       if (w == 0) {
         unsigned char* sl = reinterpret_cast<unsigned char*>(sbuf(buf, sub));
-        dma4(sr, sl, st_off0, static_cast<uint32_t>(qt * QT * 4));
-        if (lane < 32) dma4(sr, sl + 2 * QT * 4, st_off1, static_cast<uint32_t>(qt * QT * 4));
+        const uint32_t srow = static_cast<uint32_t>(((b * a.heads + hq) * T_ + sc.qt * QT) * 4);
+        dma4(sr, sl, st_lane0, srow);
+        if (lane < 32) dma4(sr, sl + 2 * QT * 4, st_lane1, srow);
       }
+      advance(sc);
     }
   };
 
@@ -411,16 +435,17 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
     dvacc[db] = f32x16{};
   }
 
-  if (qt_lo < qt_hi) stage(qt_lo, 0);
-  for (int qt0 = qt_lo; qt0 < qt_hi; qt0 += kSub) {
-    const int buf = ((qt0 - qt_lo) / kSub) & 1;
+  Cursor cc{0, qt_lo};  // the next item to compute
+  if (nqt_live > 0) stage(0);
+  for (int buf = 0; nqt_live > 0 && cc.gq < a.group; buf ^= 1) {
     wait_vmcnt0();
     __syncthreads();
-    if (qt0 + kSub < qt_hi) stage(qt0 + kSub, buf ^ 1);  // the next stage, into the idle buffers
+    if (sc.gq < a.group) stage(buf ^ 1);  // the next stage, into the idle buffers
 #pragma unroll
     for (int sub = 0; sub < kSub; ++sub) {
-      const int qt = qt0 + sub;
-      if (qt >= qt_hi) break;
+      if (cc.gq >= a.group) break;
+      const int qt = cc.qt;
+      advance(cc);
       const int64_t q0 = static_cast<int64_t>(qt) * QT;
       const int64_t dmin = kw0 - (q0 + QT - 1), dmax = kw0 + 31 - q0;  // key - q over the tile
       bool dead = false, cut = q0 + QT > T_ || kw0 + 32 > S_;
@@ -500,9 +525,9 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
   wait_vmcnt0();
 
   if (krow < S_) {
-    store_rows_t<T, D>(a.dk + b * a.k_sb + h * a.k_sh + static_cast<int64_t>(kw0) * a.k_st, a.k_st, r32, g, dkacc,
+    store_rows_t<T, D>(a.dk + b * a.k_sb + hkv * a.k_sh + static_cast<int64_t>(kw0) * a.k_st, a.k_st, r32, g, dkacc,
                        a.scale);
-    store_rows_t<T, D>(a.dv + b * a.v_sb + h * a.v_sh + static_cast<int64_t>(kw0) * a.v_st, a.v_st, r32, g, dvacc,
+    store_rows_t<T, D>(a.dv + b * a.v_sb + hkv * a.v_sh + static_cast<int64_t>(kw0) * a.v_st, a.v_st, r32, g, dvacc,
                        1.0f);
   }
 }
@@ -535,7 +560,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_main(BwdArgs a) {
     const int per = gridDim.x >> 3;
     bid = (bid & 7) * per + (bid >> 3);
   }
-  const int nk = a.ninst * a.nkblk, nq = a.ninst * a.nqblk;
+  const int nk = a.ninst_kv * a.nkblk, nq = a.ninst * a.nqblk;
   const int both = 2 * (nk < nq ? nk : nq);
   int role, idx;
   if (bid < both) {
@@ -572,7 +597,8 @@ struct GenBwdArgs {
   float* dk;
   float* dv;
   float* ws;
-  int64_t rows, heads, t, s, e, od;
+  int64_t rows, heads, t, s, e, od;  // heads: query heads
+  int64_t heads_kv, group;           // query head h reads K / V head h / group
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
   float scale, c2, fill2;
   int masked;
@@ -616,15 +642,11 @@ __global__ __launch_bounds__(256) void bwd_rows_f32(GenBwdArgs a, int64_t nrows)
   const int64_t grow = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (grow >= nrows) return;
   const int64_t len = ROLE == 0 ? a.t : a.s;  // rows per instance of the owned side
-  const int64_t inst = grow / len, r = grow % len;
-  const int64_t b = inst / a.heads, h = inst % a.heads;
-  const float* qp = a.q + b * a.q_sb + h * a.q_sh;
-  const float* kp = a.k + b * a.k_sb + h * a.k_sh;
-  const float* vp = a.v + b * a.v_sb + h * a.v_sh;
-  const float* dop = a.dout + b * a.o_sb + h * a.o_sh;
-  const float* delp = a.ws + inst * a.t;
-  const float* lsep = a.ws + a.rows + inst * a.t;
-  const float* pmp = a.ws + 2 * a.rows + inst * a.t;
+  const int64_t inst = grow / len, r = grow % len;  // ROLE 0: a query instance; ROLE 1: a K / V instance
+  const int64_t b = inst / (ROLE == 0 ? a.heads : a.heads_kv), hh = inst % (ROLE == 0 ? a.heads : a.heads_kv);
+  const int64_t hkv = ROLE == 0 ? hh / a.group : hh;
+  const float* kp = a.k + b * a.k_sb + hkv * a.k_sh;
+  const float* vp = a.v + b * a.v_sb + hkv * a.v_sh;
   const int64_t other = ROLE == 0 ? a.s : a.t;  // the swept side
   // swept range: live pairs satisfy band_lo <= key - query <= band_hi
   int64_t lo = 0, hi = other;
@@ -641,60 +663,69 @@ __global__ __launch_bounds__(256) void bwd_rows_f32(GenBwdArgs a, int64_t nrows)
   float acc0[kGenPerLane], acc1[kGenPerLane];  // dq | dk, dv
 #pragma unroll
   for (int j = 0; j < kGenPerLane; ++j) acc0[j] = acc1[j] = 0.f;
-  for (int64_t c0 = lo - (lo % 64); c0 < hi; c0 += 64) {
-    const int64_t x = c0 + lane;  // this lane's key (ROLE 0) or query (ROLE 1)
-    const int64_t tq = ROLE == 0 ? r : x, sk = ROLE == 0 ? x : r;
-    float p = 0.f, ds = 0.f;
-    if (x >= lo && x < hi) {
-      const float* qr = qp + tq * a.q_st;
-      const float* kr = kp + sk * a.k_st;
-      const float* vr = vp + sk * a.v_st;
-      const float* dr = dop + tq * a.o_st;
-      float sc = 0.f, dp = 0.f;
-      for (int64_t e = 0; e < a.e; ++e) sc = __builtin_fmaf(qr[e], kr[e], sc);
-      for (int64_t o = 0; o < a.od; ++o) dp = __builtin_fmaf(dr[o], vr[o], dp);
-      const int64_t d = sk - tq;
-      if (a.masked && (d < a.band_lo || d > a.band_hi)) {
-        p = pmp[tq];  // masked score: the row's masked-entry probability, no gradient
-      } else {
-        p = fast_exp2(__builtin_fmaf(sc, a.c2, -lsep[tq]));
-        ds = p * (dp + delp[tq]);  // delp holds -delta
-      }
-    }
-    const int64_t n = (hi - c0) < 64 ? (hi - c0) : 64;
-    for (int kk = 0; kk < n; ++kk) {
-      const float pk = __shfl(p, kk, 64), dk_ = __shfl(ds, kk, 64);
-      const int64_t xx = c0 + kk;
-      if (xx < lo) continue;
-      if (ROLE == 0) {  // dq_r += ds_(r, key xx) k_xx
-        const float* kr = kp + xx * a.k_st;
-#pragma unroll
-        for (int j = 0; j < kGenPerLane; ++j) {
-          const int64_t e = j * 64 + lane;
-          if (e < a.e) acc0[j] = __builtin_fmaf(dk_, kr[e], acc0[j]);
-        }
-      } else {  // dk_r += ds_(query xx, r) q_xx ; dv_r += p_(xx, r) dO_xx
-        const float* qr = qp + xx * a.q_st;
-        const float* dr = dop + xx * a.o_st;
-#pragma unroll
-        for (int j = 0; j < kGenPerLane; ++j) {
-          const int64_t e = j * 64 + lane;
-          if (e < a.e) acc0[j] = __builtin_fmaf(dk_, qr[e], acc0[j]);
-          if (e < a.od) acc1[j] = __builtin_fmaf(pk, dr[e], acc1[j]);
+  // ROLE 0 sweeps its own query head; ROLE 1 every query head of its group in turn
+  for (int64_t gq = 0; gq < (ROLE == 0 ? 1 : a.group); ++gq) {
+    const int64_t hq = ROLE == 0 ? hh : hkv * a.group + gq, qinst = b * a.heads + hq;
+    const float* qp = a.q + b * a.q_sb + hq * a.q_sh;
+    const float* dop = a.dout + b * a.o_sb + hq * a.o_sh;
+    const float* delp = a.ws + qinst * a.t;
+    const float* lsep = a.ws + a.rows + qinst * a.t;
+    const float* pmp = a.ws + 2 * a.rows + qinst * a.t;
+    for (int64_t c0 = lo - (lo % 64); c0 < hi; c0 += 64) {
+      const int64_t x = c0 + lane;  // this lane's key (ROLE 0) or query (ROLE 1)
+      const int64_t tq = ROLE == 0 ? r : x, sk = ROLE == 0 ? x : r;
+      float p = 0.f, ds = 0.f;
+      if (x >= lo && x < hi) {
+        const float* qr = qp + tq * a.q_st;
+        const float* kr = kp + sk * a.k_st;
+        const float* vr = vp + sk * a.v_st;
+        const float* dr = dop + tq * a.o_st;
+        float sc = 0.f, dp = 0.f;
+        for (int64_t e = 0; e < a.e; ++e) sc = __builtin_fmaf(qr[e], kr[e], sc);
+        for (int64_t o = 0; o < a.od; ++o) dp = __builtin_fmaf(dr[o], vr[o], dp);
+        const int64_t d = sk - tq;
+        if (a.masked && (d < a.band_lo || d > a.band_hi)) {
+          p = pmp[tq];  // masked score: the row's masked-entry probability, no gradient
+        } else {
+          p = fast_exp2(__builtin_fmaf(sc, a.c2, -lsep[tq]));
+          ds = p * (dp + delp[tq]);  // delp holds -delta
         }
       }
+      const int64_t n = (hi - c0) < 64 ? (hi - c0) : 64;
+      for (int kk = 0; kk < n; ++kk) {
+        const float pk = __shfl(p, kk, 64), dk_ = __shfl(ds, kk, 64);
+        const int64_t xx = c0 + kk;
+        if (xx < lo) continue;
+        if (ROLE == 0) {  // dq_r += ds_(r, key xx) k_xx
+          const float* kr = kp + xx * a.k_st;
+  #pragma unroll
+          for (int j = 0; j < kGenPerLane; ++j) {
+            const int64_t e = j * 64 + lane;
+            if (e < a.e) acc0[j] = __builtin_fmaf(dk_, kr[e], acc0[j]);
+          }
+        } else {  // dk_r += ds_(query xx, r) q_xx ; dv_r += p_(xx, r) dO_xx
+          const float* qr = qp + xx * a.q_st;
+          const float* dr = dop + xx * a.o_st;
+  #pragma unroll
+          for (int j = 0; j < kGenPerLane; ++j) {
+            const int64_t e = j * 64 + lane;
+            if (e < a.e) acc0[j] = __builtin_fmaf(dk_, qr[e], acc0[j]);
+            if (e < a.od) acc1[j] = __builtin_fmaf(pk, dr[e], acc1[j]);
+          }
+        }
+      }
     }
-  }
+  }  // query heads
   if (ROLE == 0) {
-    float* out = a.dq + b * a.q_sb + h * a.q_sh + r * a.q_st;
+    float* out = a.dq + b * a.q_sb + hh * a.q_sh + r * a.q_st;
 #pragma unroll
     for (int j = 0; j < kGenPerLane; ++j) {
       const int64_t e = j * 64 + lane;
       if (e < a.e) out[e] = acc0[j] * a.scale;
     }
   } else {
-    float* ok = a.dk + b * a.k_sb + h * a.k_sh + r * a.k_st;
-    float* ov = a.dv + b * a.v_sb + h * a.v_sh + r * a.v_st;
+    float* ok = a.dk + b * a.k_sb + hkv * a.k_sh + r * a.k_st;
+    float* ov = a.dv + b * a.v_sb + hkv * a.v_sh + r * a.v_st;
 #pragma unroll
     for (int j = 0; j < kGenPerLane; ++j) {
       const int64_t e = j * 64 + lane;
@@ -719,8 +750,8 @@ int launch_bwd(BwdArgs a, hipStream_t st) {
   if (rc) return rc;
   constexpr int TB = Tile32<D>::BYTES;
   constexpr int lds = 4 * kSub * TB + 2 * kSub * 3 * 32 * 4;  // the larger of the two roles' needs (dK/dV)
-  const int64_t nblk = static_cast<int64_t>(a.ninst) * (a.nkblk + a.nqblk);
-  a.xcd_remap = nblk % 8 == 0 ? ((a.ninst % 32 == 0 && a.nkblk == a.nqblk) ? 2 : 1) : 0;
+  const int64_t nblk = static_cast<int64_t>(a.ninst_kv) * a.nkblk + static_cast<int64_t>(a.ninst) * a.nqblk;
+  a.xcd_remap = nblk % 8 == 0 ? ((a.ninst % 32 == 0 && a.nkblk == a.nqblk && a.group == 1) ? 2 : 1) : 0;
   bwd_main<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, lds, st>>>(a);
   return check_launch("pdh_flash_bwd (dk, dv, dq)");
 }
@@ -736,10 +767,12 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
                              int64_t band_lo, int64_t band_hi, void* stream) {
   PDH_REQUIRE(gm != nullptr, PDH_EINVAL, "pdh_flash_bwd: null geometry");
   const pdh_attn_geom G = *gm;
-  PDH_REQUIRE(G.batch >= 0 && G.heads_q >= 1 && G.t >= 0 && G.s >= 1, PDH_EINVAL, "pdh_flash_bwd: bad shape");
-  PDH_REQUIRE(G.heads_q == G.heads_kv, PDH_EUNSUPPORTED,
-              "pdh_flash_bwd: grouped-query backward (heads_q %lld != heads_kv %lld) is not supported",
-              (long long)G.heads_q, (long long)G.heads_kv);
+  PDH_REQUIRE(G.batch >= 0 && G.heads_q >= 1 && G.heads_kv >= 1 && G.t >= 0 && G.s >= 1, PDH_EINVAL,
+              "pdh_flash_bwd: bad shape");
+  PDH_REQUIRE(G.heads_q % G.heads_kv == 0, PDH_EINVAL,
+              "pdh_flash_bwd: heads_q (%lld) must be a multiple of heads_kv (%lld)", (long long)G.heads_q,
+              (long long)G.heads_kv);
+  const int64_t group = G.heads_q / G.heads_kv;
   PDH_REQUIRE(mask_kind == PDH_MASK_NONE || mask_kind == PDH_MASK_BAND, PDH_EINVAL,
               "pdh_flash_bwd: unknown mask kind %d", mask_kind);
   PDH_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && ws, PDH_EINVAL, "pdh_flash_bwd: null pointer");
@@ -748,17 +781,17 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
     PDH_REQUIRE(G.e >= 1 && G.od >= 1 && G.e <= 64 * kGenPerLane && G.od <= 64 * kGenPerLane, PDH_EUNSUPPORTED,
                 "pdh_flash_bwd: fp32 needs 1 <= e, od <= %d (got %lld, %lld)", 64 * kGenPerLane, (long long)G.e,
                 (long long)G.od);
-    const int64_t ninst = G.batch * G.heads_q;
+    const int64_t ninst = G.batch * G.heads_q, ninst_kv = G.batch * G.heads_kv;
     if (ninst == 0 || G.t == 0) return PDH_OK;
-    PDH_REQUIRE((ninst * G.t + 3) / 4 <= INT32_MAX && (ninst * G.s + 3) / 4 <= INT32_MAX, PDH_EINVAL,
+    PDH_REQUIRE((ninst * G.t + 3) / 4 <= INT32_MAX && (ninst_kv * G.s + 3) / 4 <= INT32_MAX, PDH_EINVAL,
                 "pdh_flash_bwd: too many rows");
     const int masked = mask_kind == PDH_MASK_BAND;
     GenBwdArgs ga{static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
                   static_cast<const float*>(o), static_cast<const float*>(dout), lse, m_in, den_in,
                   static_cast<float*>(dq), static_cast<float*>(dk), static_cast<float*>(dv), ws, ninst * G.t,
-                  G.heads_q, G.t, G.s, G.e, G.od, G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh,
-                  G.v_st, G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi,
-                  masked && !band_has_empty_row(G.t, G.s, band_lo, band_hi)};
+                  G.heads_q, G.t, G.s, G.e, G.od, G.heads_kv, group, G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st,
+                  G.v_sb, G.v_sh, G.v_st, G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e, masked,
+                  band_lo, band_hi, masked && !band_has_empty_row(G.t, G.s, band_lo, band_hi)};
     hipStream_t st = as_stream(stream);
     bwd_stats_f32<<<dim3(static_cast<unsigned>((ga.rows + 3) / 4)), 256, 0, st>>>(ga);
     int rc = check_launch("pdh_flash_bwd (fp32 row stats)");
@@ -766,7 +799,7 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
     bwd_rows_f32<0><<<dim3(static_cast<unsigned>((ninst * G.t + 3) / 4)), 256, 0, st>>>(ga, ninst * G.t);
     rc = check_launch("pdh_flash_bwd (fp32 dq)");
     if (rc) return rc;
-    bwd_rows_f32<1><<<dim3(static_cast<unsigned>((ninst * G.s + 3) / 4)), 256, 0, st>>>(ga, ninst * G.s);
+    bwd_rows_f32<1><<<dim3(static_cast<unsigned>((ninst_kv * G.s + 3) / 4)), 256, 0, st>>>(ga, ninst_kv * G.s);
     return check_launch("pdh_flash_bwd (fp32 dk, dv)");
   }
   PDH_REQUIRE(dtype == PDH_BF16 || dtype == PDH_F16, PDH_EINVAL, "pdh_flash_bwd: unknown dtype %d", dtype);
@@ -786,8 +819,8 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
   PDH_REQUIRE(G.s * G.k_st * 2 < INT32_MAX && G.s * G.v_st * 2 < INT32_MAX && G.t * G.q_st * 2 < INT32_MAX &&
                   G.t * G.o_st * 2 < INT32_MAX,
               PDH_EINVAL, "pdh_flash_bwd: one instance's rows must span < 2 GiB");
-  PDH_REQUIRE(G.batch * G.heads_q * ((G.s + 127) / 128 + (G.t + 127) / 128) < INT32_MAX / 2, PDH_EINVAL,
-              "pdh_flash_bwd: grid too large");
+  PDH_REQUIRE(G.batch * (G.heads_kv * ((G.s + 127) / 128) + G.heads_q * ((G.t + 127) / 128)) < INT32_MAX / 2,
+              PDH_EINVAL, "pdh_flash_bwd: grid too large");
   PDH_REQUIRE(G.batch * G.heads_q * G.t * 12 < INT32_MAX, PDH_EINVAL,
               "pdh_flash_bwd: the row-statistics workspace must span < 2 GiB");
   const int64_t ninst = G.batch * G.heads_q;
@@ -797,9 +830,10 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
   BwdArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
             static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), lse, m_in, den_in,
             static_cast<uint16_t*>(dq), static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv), ws,
-            ninst * G.t, G.heads_q, G.t, G.s, G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st,
-            G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e, masked, band_lo, band_hi, prune_ok,
-            static_cast<int>(ninst), static_cast<int>((G.s + 127) / 128), static_cast<int>((G.t + 127) / 128), 0};
+            ninst * G.t, G.heads_q, G.t, G.s, G.heads_kv, static_cast<int>(group), G.q_sb, G.q_sh, G.q_st, G.k_sb,
+            G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st, G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e,
+            masked, band_lo, band_hi, prune_ok, static_cast<int>(ninst), static_cast<int>(G.batch * G.heads_kv),
+            static_cast<int>((G.s + 127) / 128), static_cast<int>((G.t + 127) / 128), 0};
   hipStream_t st = as_stream(stream);
   if (dtype == PDH_BF16)
     return G.e == 128 ? launch_bwd<__hip_bfloat16, 128>(a, st) : launch_bwd<__hip_bfloat16, 64>(a, st);
