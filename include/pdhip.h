@@ -125,6 +125,19 @@ int pdh_layernorm_dt(const void* x, const void* gamma, const void* beta, void* y
 int pdh_take_rows(const void* table, const int64_t* idx, void* out, int64_t n_idx, int64_t row_elems,
                   int64_t n_rows, int64_t ld_table, int64_t ld_out, int dtype, int* bad, void* stream);
 
+/* Row scatter-add: out[v, :] = sum of values[i, :] over the i < n_idx with
+ * idx[i] == v, for every v < n_rows (rows no index names are zero), rows of
+ * row_elems elements (strides ld_values / ld_out): tl.scatter_add, the
+ * adjoint of the gather above along the output's leading dim
+ * (indexing.py:153-190, 223-259; autodiff.py:846-856), which the reference
+ * plans red and runs on the CPU; the carved-plan executor runs a model's
+ * embedding gradient here. Deterministic: each row sums its value rows in
+ * increasing i in fp32 and rounds once. An index outside [0, n_rows) is
+ * dropped and adds 1 to *bad (device int, may be NULL). out must not overlap
+ * values; n_idx <= 2^24 (the cost grows as n_idx^2 / 256 index compares). */
+int pdh_scatter_add_rows(const void* values, const int64_t* idx, void* out, int64_t n_idx, int64_t row_elems,
+                         int64_t n_rows, int64_t ld_values, int64_t ld_out, int dtype, int* bad, void* stream);
+
 /* Flash-attention forward: the online-softmax fold of _generate_flash
  * (fusion.py:542-615) over every (batch, head) instance:
  *   sc[t, s]  = scale * sum_e q[t, e] k[s, e]         (masked entries -> fill)

@@ -21,6 +21,7 @@ planner's numpy interpreter, so each can check the other:
   tl.const       layout views (region_evaluator.py:372-430)
   tl.rename / tl.shift / tl.slice   relabelings and a window (layout.py)
   tl.take        the gather (indexing.py:120-230)
+  tl.scatter_add its adjoint, duplicates summed (indexing.py:153-190, 223-259)
   tl.fold        a Python loop over the scan dim, each element source
                  selected at the ABSOLUTE coordinate (dialect.py:1448-1470;
                  region_evaluator.py:431-465)
@@ -232,6 +233,25 @@ def _dispatch(n, ev):
         got = torch.index_select(table.t, ax, (it - lo).reshape(-1))
         shape = tuple(table.t.shape[:ax]) + tuple(it.shape) + tuple(table.t.shape[ax + 1:])
         return V(got.reshape(shape), tuple((d.name, d.start, d.stop) for d in n.type.dims))
+    if op == "tl.scatter_add":  # indexing.py:223-259: take's adjoint, duplicates summed
+        vals, idx = ev(n.args[0]), ev(n.args[1])
+        over = _attr(n, "over")
+        consumed = list(idx.names) if over is None else ([over] if isinstance(over, str) else list(over))
+        if any(nm not in consumed for nm in idx.names):
+            raise NotImplementedError("tl.scatter_add with aligned (riding) idx dims")
+        name = _attr(n, "dim")
+        od = next(d for d in n.type.dims if d.name == name)
+        it = idx.t.to(torch.int64).reshape(-1)
+        if it.numel() and (int(it.min()) < od.start or int(it.max()) >= od.stop):
+            raise IndexError(f"tl.scatter_add: index outside [{od.start}, {od.stop}) along {name!r}")
+        rest = [nm for nm in vals.names if nm not in consumed]
+        vt = vals.t.permute([vals.names.index(nm) for nm in list(idx.names) + rest])
+        vt = vt.reshape((it.numel(),) + tuple(vt.shape[len(idx.names):]))
+        acc = torch.zeros((od.stop - od.start,) + tuple(vt.shape[1:]), dtype=torch.float64)
+        acc.index_add_(0, it - od.start, vt)
+        src = [name] + rest
+        return V(acc.permute([src.index(d.name) for d in n.type.dims]),
+                 tuple((d.name, d.start, d.stop) for d in n.type.dims))
     if op == "tl.const":
         dims = tuple((d.name, d.start, d.stop) for d in n.type.dims)
         return V(torch.full([d[2] - d[1] for d in dims], float(_attr(n, "value")), dtype=torch.float64), dims)

@@ -30,6 +30,7 @@ EXPORTS = (
     "pdh_row_softmax_dt",
     "pdh_layernorm_dt",
     "pdh_take_rows",
+    "pdh_scatter_add_rows",
     "pdh_flash_fwd",
     "pdh_flash_fwd_workspace",
     "pdh_flash_fwd_split",
@@ -114,6 +115,7 @@ def _declare(lib) -> None:
         "pdh_row_softmax_dt": (i32, [vp, vp, i64, i64, i64, i64, i32, vp]),
         "pdh_layernorm_dt": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, f32, i32, vp]),
         "pdh_take_rows": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, vp]),
+        "pdh_scatter_add_rows": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, vp]),
         "pdh_flash_fwd": (i32, [vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, i32, vp]),
         "pdh_flash_fwd_workspace": (C.c_size_t, [gp, i32]),
         "pdh_flash_fwd_split": (i32, [vp, vp, vp, vp, vp, vp, vp, gp, i32, f32, f32, i32, i64, i64, i32, i32, vp,

@@ -8,6 +8,17 @@
 // (the widest the row's bytes and alignments allow). An index outside
 // [0, n_rows) writes a zero row and is counted in *bad (a device int the
 // caller clears and reads back), since a kernel cannot raise.
+//
+// Row scatter-add: out[v, :] = sum of values[i, :] over the i with
+// idx[i] == v — tl.scatter_add, the gather's adjoint (indexing.py:153-190,
+// 223-259), which a model's gradient needs for its embedding tables. It is
+// deterministic without sorting or scratch memory: rows start at zero, and
+// the workgroup of the FIRST position holding v owns row v (a later
+// position finds an earlier equal index and leaves), sums the matching
+// value rows in increasing position order in fp32 and rounds once. Finding
+// the owner and its matches reads the index array once per position
+// (n_idx^2 int64 compares from L2 in all), which suits embedding batches of
+// up to some ten thousand indices.
 #include "common.h"
 
 namespace pdh {
@@ -28,6 +39,68 @@ __global__ __launch_bounds__(256) void take_rows(const unsigned char* __restrict
   }
   const W* src = reinterpret_cast<const W*>(table + r * ld_table_b);
   for (int64_t w = threadIdx.x; w < words; w += blockDim.x) dst[w] = src[w];
+}
+
+template <typename W>
+__global__ __launch_bounds__(256) void zero_rows(unsigned char* __restrict__ out, int64_t n_rows, int64_t words,
+                                                 int64_t ld_out_b) {
+  for (int64_t r = blockIdx.x; r < n_rows; r += gridDim.x) {
+    W* dst = reinterpret_cast<W*>(out + r * ld_out_b);
+    for (int64_t w = threadIdx.x; w < words; w += blockDim.x) dst[w] = W{};
+  }
+}
+
+constexpr int kScatterCols = 4;  // columns per lane per pass over the matches: 1024 per workgroup
+
+// One workgroup per index position i (256 lanes, 4 waves).
+template <int DT>
+__global__ __launch_bounds__(256) void scatter_add_rows(const unsigned char* __restrict__ values,
+                                                        const int64_t* __restrict__ idx,
+                                                        unsigned char* __restrict__ out, int64_t n_idx,
+                                                        int64_t row_elems, int64_t n_rows, int64_t ld_values_b,
+                                                        int64_t ld_out_b, int* __restrict__ bad) {
+  __shared__ uint64_t hits[4];
+  const int64_t i = blockIdx.x;
+  const int64_t v = idx[i];
+  if (v < 0 || v >= n_rows) {  // dropped, and counted once per position
+    if (threadIdx.x == 0 && bad) atomicAdd(bad, 1);
+    return;
+  }
+  for (int64_t j0 = 0; j0 < i; j0 += 256) {  // an earlier equal index owns the row
+    const int64_t j = j0 + threadIdx.x;
+    if (__syncthreads_or(j < i && idx[j] == v)) return;
+  }
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int64_t c0 = 0; c0 < row_elems; c0 += 256 * kScatterCols) {
+    float acc[kScatterCols] = {};
+    for (int64_t j0 = i; j0 < n_idx; j0 += 256) {
+      const int64_t j = j0 + threadIdx.x;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(j < n_idx && idx[j] == v);
+      if (lane == 0) hits[wv] = m;
+      __syncthreads();
+      uint64_t h[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) h[q] = hits[q];
+      __syncthreads();  // the next chunk rewrites hits
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        for (uint64_t mm = h[q]; mm; mm &= mm - 1) {  // matches in increasing position order
+          const unsigned char* row = values + (j0 + q * 64 + __builtin_ctzll(mm)) * ld_values_b;
+#pragma unroll
+          for (int c = 0; c < kScatterCols; ++c) {
+            const int64_t col = c0 + threadIdx.x + c * 256;
+            if (col < row_elems) acc[c] += ld_dt<DT>(row, static_cast<int>(col));
+          }
+        }
+      }
+    }
+    unsigned char* orow = out + v * ld_out_b;
+#pragma unroll
+    for (int c = 0; c < kScatterCols; ++c) {
+      const int64_t col = c0 + threadIdx.x + c * 256;
+      if (col < row_elems) st_dt<DT>(orow, col, acc[c]);
+    }
+  }
 }
 
 }  // namespace
@@ -61,4 +134,43 @@ extern "C" int pdh_take_rows(const void* table, const int64_t* idx, void* out, i
   else
     take_rows<uint16_t><<<grid, 256, 0, s>>>(tb, idx, ob, n_rows, row_b / 2, lt, lo, bad);
   return check_launch("pdh_take_rows");
+}
+
+extern "C" int pdh_scatter_add_rows(const void* values, const int64_t* idx, void* out, int64_t n_idx,
+                                    int64_t row_elems, int64_t n_rows, int64_t ld_values, int64_t ld_out, int dtype,
+                                    int* bad, void* stream) {
+  PDH_REQUIRE(dtype == PDH_F32 || dtype == PDH_BF16 || dtype == PDH_F16, PDH_EUNSUPPORTED,
+              "pdh_scatter_add_rows: dtype %d", dtype);
+  PDH_REQUIRE(n_idx >= 0 && row_elems >= 1 && n_rows >= 1, PDH_EINVAL,
+              "pdh_scatter_add_rows: need n_idx >= 0, row_elems >= 1, n_rows >= 1");
+  PDH_REQUIRE(row_elems <= INT32_MAX, PDH_EINVAL, "pdh_scatter_add_rows: rows of more than 2^31 - 1 elements");
+  PDH_REQUIRE(ld_values >= row_elems && ld_out >= row_elems, PDH_EINVAL,
+              "pdh_scatter_add_rows: row strides must be >= row_elems");
+  PDH_REQUIRE(n_idx <= (int64_t{1} << 24), PDH_EINVAL, "pdh_scatter_add_rows: more than 2^24 indices");
+  PDH_REQUIRE(out && (n_idx == 0 || (values && idx)), PDH_EINVAL, "pdh_scatter_add_rows: null pointer");
+  const int64_t es = dtype == PDH_F32 ? 4 : 2;
+  const int64_t row_b = row_elems * es, lo = ld_out * es;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(out);
+  hipStream_t s = as_stream(stream);
+  auto* ob = static_cast<unsigned char*>(out);
+  const dim3 zgrid(static_cast<unsigned>(n_rows < 8192 ? n_rows : 8192));
+  auto fits = [&](int64_t w) { return row_b % w == 0 && lo % w == 0 && al % w == 0; };
+  if (fits(16))
+    zero_rows<u32x4><<<zgrid, 256, 0, s>>>(ob, n_rows, row_b / 16, lo);
+  else if (fits(4))
+    zero_rows<uint32_t><<<zgrid, 256, 0, s>>>(ob, n_rows, row_b / 4, lo);
+  else
+    zero_rows<uint16_t><<<zgrid, 256, 0, s>>>(ob, n_rows, row_b / 2, lo);
+  if (int rc = check_launch("pdh_scatter_add_rows (zero)"); rc != PDH_OK) return rc;
+  if (n_idx == 0) return PDH_OK;
+  const auto* vb = static_cast<const unsigned char*>(values);
+  const dim3 grid(static_cast<unsigned>(n_idx));
+  const int64_t lv = ld_values * es;
+  if (dtype == PDH_F32)
+    scatter_add_rows<PDH_F32><<<grid, 256, 0, s>>>(vb, idx, ob, n_idx, row_elems, n_rows, lv, lo, bad);
+  else if (dtype == PDH_BF16)
+    scatter_add_rows<PDH_BF16><<<grid, 256, 0, s>>>(vb, idx, ob, n_idx, row_elems, n_rows, lv, lo, bad);
+  else
+    scatter_add_rows<PDH_F16><<<grid, 256, 0, s>>>(vb, idx, ob, n_idx, row_elems, n_rows, lv, lo, bad);
+  return check_launch("pdh_scatter_add_rows");
 }

@@ -29,6 +29,8 @@ kernels, one step per carve:
                         one pdh_flash_fwd launch for the pair
   red, tl.take          pdh_take_rows for the gather, the rest of the carve
                         as a map chain
+  red, tl.scatter_add   pdh_scatter_add_rows (the gather's adjoint: an
+                        embedding table's gradient) over stored operands
   red, tl.scan          pdh_scan between two map chains; where the scan meets
                         a reduction, a gather or another scan, the carve is
                         split at its first scan and the operand and the rest
@@ -434,6 +436,8 @@ class PlanExecutor:
             run, src = self._layernorm(k)
         elif tmpl in ("map-chain", "stencil"):
             run, src = self._map_chain(k)
+        elif carve.group.confidence == "red" and any(n.op == "tl.scatter_add" for n in walk(k)):
+            run, src = self._scatter(k)
         elif carve.group.confidence == "red" and any(n.op == "tl.take" for n in walk(k)):
             run, src = self._take(k)
         elif carve.group.confidence == "red" and any(n.op == "tl.scan" for n in walk(k)):
@@ -1043,6 +1047,40 @@ class PlanExecutor:
 
         return run, f"take_rows x{len(takes)}" + ("" if prog is None else f" + map_chain insns={len(low.insns)}")
 
+    def _scatter(self, k):
+        """A red carve that is one tl.scatter_add over stored operands (the
+        reference evaluates it on its CPU oracle, indexing.py:223-259):
+        pdh_scatter_add_rows, with the consumed index dims leading the values
+        and the declared dim leading the result."""
+        y = k.body[-1].args[0]
+        if y.op != "tl.scatter_add" or sum(n.op == "tl.scatter_add" for n in walk(k)) != 1:
+            raise Untranslatable("a tl.scatter_add carve holding other computation")
+        vals_n, idx_n = y.args
+        if _base(vals_n).op != "core.param" or _base(idx_n).op != "core.param":
+            raise Untranslatable("tl.scatter_add over computed operands")
+        inames = idx_n.type.names
+        over = y.attr("over")
+        consumed = tuple(inames) if over is None else ((over,) if isinstance(over, str) else tuple(over))
+        if consumed != tuple(inames) or tuple(vals_n.type.names[:len(inames)]) != tuple(inames):
+            raise Untranslatable("tl.scatter_add needs every idx dim consumed, leading the values")
+        d = y.type.dim(y.attr("dim"))
+        if y.type.names[0] != d.name:
+            raise Untranslatable("tl.scatter_add's declared dim must lead its result")
+        iv, ii = self._index(k, _base(vals_n)), self._index(k, _base(idx_n))
+        shape, lo = y.type.shape, d.start
+
+        def run(vals):
+            torch = _torch()
+            from . import kernels as K
+
+            bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+            idx = vals[ii] if lo == 0 else vals[ii] - lo
+            out = K.scatter_add_rows(vals[iv], idx, shape[0], bad=bad)
+            self._bad.append(bad)
+            return out.reshape(shape)
+
+        return run, f"scatter_add_rows rows={shape[0]}"
+
     def _scan(self, k):
         """A red carve around one tl.scan (the reference serves it on its
         evaluator): the scan's operand chain by pdh_map_chain (or the stored
@@ -1163,14 +1201,15 @@ class PlanExecutor:
 
     def run(self):
         """One pass over the plan; returns the output (device tensor, dims in
-        the region's yield order). Raises if a gather saw an index out of range."""
+        the region's yield order). Raises if a gather or a scatter-add saw an
+        index out of range."""
         if self.bound is None:
             raise RuntimeError("bind() the params first")
         bads: list = []
         out = self._run(self.bound, bads)
         for bad in bads:
             if int(bad.item()) != 0:
-                raise IndexError(f"tl.take: {int(bad.item())} index(es) outside the table")
+                raise IndexError(f"tl.take / tl.scatter_add: {int(bad.item())} index(es) outside the table")
         return out
 
     def capture(self):
@@ -1210,7 +1249,7 @@ class PlanExecutor:
         if check:
             for bad in self._graph_bads:
                 if int(bad.item()) != 0:
-                    raise IndexError(f"tl.take: {int(bad.item())} index(es) outside the table")
+                    raise IndexError(f"tl.take / tl.scatter_add: {int(bad.item())} index(es) outside the table")
         return self._graph_out
 
     def _run(self, bound: dict, bads: list):

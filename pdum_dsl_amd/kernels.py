@@ -158,6 +158,41 @@ def take_rows(table: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None =
     return y.reshape(tuple(idx.shape) + tuple(table.shape[1:]))
 
 
+def scatter_add_rows(values: torch.Tensor, idx: torch.Tensor, n_rows: int, out: torch.Tensor | None = None,
+                     bad: torch.Tensor | None = None) -> torch.Tensor:
+    """out[v, ...] = sum of values[i, ...] over the positions i with
+    idx[i] == v: the gather's adjoint along out's leading dim (values has
+    idx's shape followed by the row dims; rows nothing lands in are zero).
+    Deterministic (increasing i, fp32 sums, one rounding). An index out of
+    range is dropped and counts in ``bad`` (an int32 device scalar) when
+    given."""
+    _require_cuda(values, idx)
+    if values.dtype not in _DT or idx.dtype != torch.int64:
+        raise ValueError("scatter_add_rows: values f32/bf16/f16, idx int64")
+    if tuple(values.shape[:idx.dim()]) != tuple(idx.shape):
+        raise ValueError(f"scatter_add_rows: values {tuple(values.shape)} do not lead with idx's shape {tuple(idx.shape)}")
+    rest = tuple(values.shape[idx.dim():])
+    n = idx.numel()
+    rows = values.reshape(n, -1) if n else values.new_empty((0, math.prod(rest)))
+    if rows.shape[1] < 1:
+        raise ValueError("scatter_add_rows: empty rows")
+    if n and rows.stride(-1) != 1:
+        raise ValueError("scatter_add_rows: the values' row dims must be contiguous")
+    y = torch.empty((n_rows, rows.shape[1]), dtype=values.dtype, device=values.device) if out is None else \
+        out.reshape(n_rows, rows.shape[1])
+    if y.dtype != values.dtype or y.stride(-1) != 1:
+        raise ValueError("scatter_add_rows: out must share the values' element type with contiguous rows")
+    if bad is not None and (bad.dtype != torch.int32 or bad.numel() < 1):
+        raise ValueError("scatter_add_rows: bad is an int32 device scalar")
+    flat = idx.reshape(-1).contiguous()
+    _lib.call(
+        "pdh_scatter_add_rows",
+        _ptr(rows), _ptr(flat), _ptr(y), n, rows.shape[1], n_rows, max(rows.stride(0), rows.shape[1]), y.stride(0),
+        _DT[values.dtype], _ptr(bad), C.c_void_p(_stream()),
+    )
+    return y.reshape((n_rows,) + rest)
+
+
 # ----------------------------------------------------------------- attention
 
 

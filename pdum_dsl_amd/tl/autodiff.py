@@ -20,6 +20,9 @@ templates), over the vocabulary this backend reads:
                  sum's adjoint is a suffix sum, autodiff.py:667-677); other
                  reducers refuse
   tl.repeat_like / tl.repeat   -> sum over the added dims
+  tl.take        -> tl.scatter_add of the cotangent at the same indices
+                 (duplicates sum), and tl.scatter_add -> tl.take
+                 (autodiff.py:846-856); indices carry no gradient
   tl.stage       identity
   core.const / tl.const / tl.iota / comparisons / stop_gradient: no flow
 
@@ -197,6 +200,17 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
             contribute(x, b.emit("tl.reduce", c, dims=added, f="sum") if added else c)
         elif op == "tl.repeat":
             contribute(n.args[0], b.emit("tl.reduce", c, dims=(n.attr("name"),), f="sum"))
+        elif op == "tl.take":
+            # the gather's adjoint is the scatter-add at the same indices: rows
+            # gathered twice receive the sum (autodiff.py:846-853); the
+            # indices carry no gradient
+            table, idx = n.args
+            d = table.type.dim(n.attr("dim"))
+            survivors = {x.name for x in table.type.dims if x.name != d.name}
+            spliced = tuple(nm for nm in idx.type.names if nm not in survivors)
+            contribute(table, b.emit("tl.scatter_add", c, idx, dim=d.name, extent=(d.start, d.stop), over=spliced))
+        elif op == "tl.scatter_add":  # and the scatter-add's is the gather (autodiff.py:854-856)
+            contribute(n.args[0], b.emit("tl.take", c, n.args[1], dim=n.attr("dim")))
         elif op == "tl.rename":  # a relabelling: the cotangent takes the operand's names back
             back = tuple(sorted((new, old) for old, new in n.attr("mapping")))
             contribute(n.args[0], b.emit("tl.rename", c, mapping=back))

@@ -20,6 +20,8 @@ emit and consume (packages/tensorlib/src/pdum/tl/dialect.py:115-487):
   tl.shift      deltas          moves dims' frames by integer deltas (a view)
   tl.slice      ranges          restricts dims to absolute [lo, hi) (a view)
   tl.take       dim             out = table[idx, rest]: a gather, no template row
+  tl.scatter_add dim, extent[, over]  take's adjoint: out[v, rest] = sum of
+                                values at the positions p with idx[p] == v
   tl.argtopk    (typed only: a non-template op the planner must refuse)
 """
 
@@ -240,6 +242,46 @@ def _r_take(args, at, regions):
     return TensorType(tuple(out))
 
 
+def _extent(v) -> tuple:
+    """An extent attr: an int width (start 0) or a (start, stop) pair."""
+    if isinstance(v, int):
+        return 0, v
+    lo, hi = (int(x) for x in v)
+    return lo, hi
+
+
+def _r_scatter_add(args, at, regions):
+    """take's adjoint (indexing.py:153-190, 223-259): the idx dims named by
+    ``over`` (default: all of them) are consumed, each a values dim with the
+    same domain; the declared dim (domain ``extent``) takes the place of the
+    first consumed dim; idx dims not consumed align and ride; the other
+    values dims stay verbatim."""
+    values, idx = args
+    over = at.get("over")
+    consumed = tuple(idx.names) if over is None else _dims_arg(over)
+    for n in idx.dims:
+        if not values.has(n.name):
+            raise TypeError(f"tl.scatter_add: idx dim {n.name!r} is not a values dim")
+        v = values.dim(n.name)
+        if (v.start, v.stop) != (n.start, n.stop):
+            raise TypeError(f"tl.scatter_add: idx dim {n.name!r} does not align with the values'")
+    for nm in consumed:
+        if nm not in idx.names:
+            raise TypeError(f"tl.scatter_add: over={nm!r} is not an idx dim {idx.names}")
+    if not consumed:
+        raise TypeError("tl.scatter_add consumes at least one idx dim")
+    lo, hi = _extent(at["extent"])
+    if values.has(at["dim"]) and at["dim"] not in consumed:
+        raise TypeError(f"tl.scatter_add: the declared dim {at['dim']!r} is already a values dim")
+    out = []
+    for x in values.dims:
+        if x.name == consumed[0]:
+            out.append(Dim(at["dim"], lo, hi))
+        elif x.name not in consumed:
+            out.append(x)
+    return TensorType(tuple(out))
+
+
 def _r_tuple(args, at, regions):
     return TupleType(tuple(args))
 
@@ -274,9 +316,10 @@ OPS: dict[str, OpDef] = {
     "tl.shift": OpDef("tl.shift", _r_shift),
     "tl.slice": OpDef("tl.slice", _r_slice),
     "tl.take": OpDef("tl.take", _r_take),
+    "tl.scatter_add": OpDef("tl.scatter_add", _r_scatter_add),
 }
 
-TILE_OPS = frozenset(OPS) - {"tl.argtopk", "tl.take"}
+TILE_OPS = frozenset(OPS) - {"tl.argtopk", "tl.take", "tl.scatter_add"}
 
 
 def builder() -> Builder:

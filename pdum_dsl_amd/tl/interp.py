@@ -197,6 +197,23 @@ def run_region(region: Region, values: list):
             ax = table.names.index(dim)
             got = np.take(table.arr, ia.astype(np.int64) - d.start, axis=ax)
             return Field(got.reshape(table.arr.shape[:ax] + ia.shape + table.arr.shape[ax + 1:]), n.type.dims)
+        if op == "tl.scatter_add":
+            vals, idx = ev(n.args[0]), ev(n.args[1])
+            over = n.attr("over")
+            consumed = list(idx.names) if over is None else ([over] if isinstance(over, str) else list(over))
+            if any(nm not in consumed for nm in idx.names):
+                raise NotImplementedError("run_region: batched tl.scatter_add (aligned idx dims) is not evaluated here")
+            d = n.type.dim(n.attr("dim"))
+            ia = np.asarray(idx.arr).astype(np.int64)
+            if ia.size and (ia.min() < d.start or ia.max() >= d.stop):
+                raise IndexError(f"tl.scatter_add: index outside [{d.start}, {d.stop}) along {d.name!r}")
+            rest = [nm for nm in vals.names if nm not in consumed]
+            va = vals.to_numpy(tuple(idx.names) + tuple(rest)).reshape((ia.size,) + tuple(
+                vals.dims[vals.names.index(nm)].size for nm in rest))
+            acc = np.zeros((d.size,) + va.shape[1:])
+            np.add.at(acc, ia.reshape(-1) - d.start, va)  # duplicates sum, in order
+            src = (d.name,) + tuple(rest)
+            return Field(np.transpose(acc, [src.index(x.name) for x in n.type.dims]), n.type.dims)
         if op == "tl.const":
             tt = n.type
             return Field(np.full(tt.shape, float(n.attr("value"))), tt.dims)

@@ -218,19 +218,25 @@ def test_rename_adjoint_and_wrt_pruning():
     np.testing.assert_allclose(res_w[1].to_numpy(("d",)), wt.grad.numpy(), rtol=1e-12)
 
 
-def test_the_gpt2_weight_joint_builds_and_plans():
-    """grad of the gpt2 zoo model's logits w.r.t. every weight but the
-    embedding tables: the joint plans into contraction, map-chain and
-    row-statistics carves (the residue: the forward gather and the
-    softmax's bare row max)."""
+@pytest.mark.parametrize("with_tables", [False, True])
+def test_the_gpt2_weight_joint_builds_and_plans(with_tables):
+    """grad of the gpt2 zoo model's logits w.r.t. every weight (with or
+    without the embedding tables, whose gradient comes through the take's
+    adjoint, a scatter-add, plus the tied head's product): the joint plans
+    into contraction, map-chain and row-statistics carves (the residue: the
+    forward gather, the scatter-add and the softmax's bare row max), and its
+    values equal torch autograd of the same forward in float64."""
     from collections import Counter
+
+    from pdum_dsl_amd.tl.ir import walk
 
     m = zoo.gpt2(zoo.GPT2Config(t=16, d=64, nh=2, hk=32, m=128, layers=1, v=32), seed=3)
     pn = tuple(m.names[id(p)] for p in m.region.params)
     names = region_names(m.region, pn, ("logits",))
-    wrt = tuple(n for n in pn if n not in ("ids", "wte", "wpe"))
+    wrt = tuple(n for n in pn if n not in (("ids",) if with_tables else ("ids", "wte", "wpe")))
     rg = grad(m.region, "logits", seed="dlogits", wrt=wrt, names=names)
     assert set(rg.grads) == set(wrt) and all(rg.grads[n] for n in wrt)
+    assert any(n.op == "tl.scatter_add" for n in walk(rg.region)) == with_tables
     counts = Counter(c.group.template for c in plan_model(rg.region).carves)
     assert counts["contraction-epilogue"] > 0 and counts["map-chain"] > 0
     # the joint's values against torch autograd of the same forward (zoo.gpt2's ref, float64)

@@ -10,6 +10,8 @@ storage (fp32 accumulation and statistics), 3e-2 of the logits' scale, the
 north-star 2e-2 bound widened for bf16 rounding compounded over 2 layers
 and 23 carves (each boundary is rounded to bf16)."""
 
+import math
+
 import numpy as np
 import pytest
 
@@ -133,6 +135,59 @@ def test_take_rows_is_a_bit_exact_gather(dt):
     assert int(bad.item()) == 1 and torch.count_nonzero(got[1, 2]).item() == 0
 
 
+def _add_at_reference(values, idx, n_rows, dt):
+    """Row v = the values rows at the positions holding v, summed in
+    increasing position order in fp32 and rounded once to dt (numpy's
+    unbuffered add.at applies the updates in index order)."""
+    row = math.prod(values.shape[idx.dim():])
+    v32 = values.float().cpu().numpy().reshape(idx.numel(), row)
+    acc = np.zeros((n_rows, row), dtype=np.float32)
+    ii = idx.cpu().numpy().reshape(-1)
+    keep = (ii >= 0) & (ii < n_rows)
+    np.add.at(acc, ii[keep], v32[keep])
+    return torch.from_numpy(acc).to(dt)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n_idx,n_rows,row", [(0, 5, 8), (1, 1, 1), (37, 50, 30), (1000, 37, 1500), (700, 5000, 7),
+                                              (300, 2, 2049)])
+def test_scatter_add_rows_sums_duplicates_in_position_order(dt, n_idx, n_rows, row):
+    """pdh_scatter_add_rows against numpy's add.at in fp32 rounded once:
+    bit-exact, rows nothing lands in zero, across index chunks (n_idx > 256),
+    column passes (rows over 1024 elements) and odd row widths."""
+    from pdum_dsl_amd import kernels as K
+
+    print(f"scatter_add_rows dt={dt} n_idx={n_idx} n_rows={n_rows} row={row}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(n_idx + row)
+    values = torch.randn((n_idx, row), generator=g, device="cuda").to(dt)
+    idx = torch.randint(0, n_rows, (n_idx,), generator=g, device="cuda")
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.full((n_rows, row), 7.0, device="cuda", dtype=dt)  # every row is rewritten
+    got = K.scatter_add_rows(values, idx, n_rows, out=out, bad=bad)
+    torch.cuda.synchronize()
+    want = _add_at_reference(values, idx, n_rows, dt)
+    assert int(bad.item()) == 0
+    assert torch.equal(got.cpu(), want)
+    again = K.scatter_add_rows(values, idx, n_rows)
+    assert torch.equal(again, got)  # deterministic: the same bits on every call
+
+
+def test_scatter_add_rows_counts_and_drops_bad_indices_and_takes_strided_rows():
+    from pdum_dsl_amd import kernels as K
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    wide = torch.randn((4, 6, 40), generator=g, device="cuda")
+    values = wide[..., :33]  # row stride 40, 33 elements a row
+    idx = torch.randint(0, 9, (4, 6), generator=g, device="cuda")
+    idx[0, 1], idx[3, 5] = -1, 9
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    assert not values.is_contiguous()
+    got = K.scatter_add_rows(values, idx, 9, bad=bad)
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 2
+    assert torch.equal(got.cpu(), _add_at_reference(values.contiguous(), idx, 9, torch.float32))
+
+
 def test_a_captured_plan_replays_the_eager_result():
     """The whole carved forward as one HIP graph: replays, with eager work and
     synchronizations between them, each give the eager pass's output."""
@@ -238,14 +293,18 @@ _SMALL = dict(t=64, d=128, nh=2, hk=64, m=512, layers=1, v=64)
 _TWO_LAYER = dict(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)  # a scan shares a red carve with a reduction
 
 
-@pytest.mark.parametrize("cfg,dtype,f32c,tol", [(_SMALL, "f32", "bf16x6", 1e-5), (_SMALL, "f32", "bf16x3", 2e-4),
-                                                (_SMALL, "f32", "bf16", 3e-2), (_SMALL, "f32", "fma", 1e-5),
-                                                (_SMALL, "bf16", "bf16x6", 5e-2), (_TWO_LAYER, "f32", "bf16x6", 3e-5),
-                                                (_TWO_LAYER, "f32", "bf16x3", 5e-4)])
-def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol):
-    """grad of gpt2's logits w.r.t. every weight but the embedding tables,
-    planned by plan_model and run on the device (contractions with their
-    epilogues, map chains, the layernorm, the gather and the bare row max),
+@pytest.mark.parametrize("cfg,dtype,f32c,tol,tables", [
+    (_SMALL, "f32", "bf16x6", 1e-5, False), (_SMALL, "f32", "bf16x3", 2e-4, False),
+    (_SMALL, "f32", "bf16", 3e-2, False), (_SMALL, "f32", "fma", 1e-5, False),
+    (_SMALL, "bf16", "bf16x6", 5e-2, False), (_TWO_LAYER, "f32", "bf16x6", 3e-5, False),
+    (_TWO_LAYER, "f32", "bf16x3", 5e-4, False), (_SMALL, "f32", "bf16x6", 1e-5, True),
+    (_SMALL, "bf16", "bf16x6", 5e-2, True), (_TWO_LAYER, "f32", "bf16x6", 3e-5, True)])
+def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol, tables):
+    """grad of gpt2's logits w.r.t. every weight (the embedding tables too
+    when ``tables``: their gradient is a scatter-add of the embedding's
+    cotangent, plus the tied head's product for wte), planned by plan_model
+    and run on the device (contractions with their epilogues, map chains,
+    the layernorm, the gather, the scatter-add and the bare row max),
     against the float64 oracle's evaluation of the same joint. Per output,
     tol of its scale. The zoo's weights (std 0.4) make the attention sharp,
     so rounding the score contraction's operands is amplified by the
@@ -262,11 +321,15 @@ def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol):
 
     m = zoo.gpt2(zoo.GPT2Config(**cfg), seed=3)
     pn = tuple(m.names[id(p)] for p in m.region.params)
-    wrt = tuple(n for n in pn if n not in ("ids", "wte", "wpe"))
+    wrt = tuple(n for n in pn if n not in (("ids",) if tables else ("ids", "wte", "wpe")))
     rg = grad(m.region, "logits", seed="dlogits", wrt=wrt, names=region_names(m.region, pn, ("logits",)))
     dl = np.random.default_rng(2).standard_normal(tuple(rg.region.params[-1].type.shape))
     vals = m.values() + [dl]
     ex = PlanExecutor(plan_model(rg.region), rg.region, dtype, f32_contract=f32c)
+    assert any(st.source.startswith("scatter_add_rows") for st in ex.steps) == tables
+    if tables:  # repeated tokens: the scatter-add must sum rows, not overwrite them
+        ids = vals[pn.index("ids")]
+        assert len(np.unique(ids)) < np.size(ids)
     if dtype == "f32":
         assert all(f"f32={f32c}" in st.source for st in ex.steps if st.source.startswith("contract"))
     if cfg is _TWO_LAYER:
