@@ -77,7 +77,9 @@ __device__ __forceinline__ void map_chain_body(const pdh_ew_program& p, const Ew
   // columns l, l + 64, ... of its wave's chunk, so every load and store
   // instruction covers 64 consecutive elements. Otherwise a lane takes EPT
   // consecutive columns.
-  const bool wide = EPT > 1 && p.shape[ndim - 1] % (64 * EPT) == 0;
+  // (An evaluator that reads fp32 operands four at a time, Eval::kVec, takes
+  // EPT consecutive columns per lane instead: one 16-byte access per operand.)
+  const bool wide = !Eval::kVec && EPT > 1 && p.shape[ndim - 1] % (64 * EPT) == 0;
   const uint32_t gt = static_cast<uint32_t>(blockIdx.x) * 256u + threadIdx.x;
   const uint32_t i0 = wide ? (gt & ~63u) * EPT + (gt & 63u) : gt * EPT;
   const int es = wide ? 64 : 1;
@@ -101,6 +103,12 @@ __device__ __forceinline__ void map_chain_body(const pdh_ew_program& p, const Ew
   for (int d = 0; d < PDH_EW_MAX_DIMS; ++d)
     if (d < ndim) off += c[d] * static_cast<int>(p.out_stride[d]);
   const int step = es * static_cast<int>(p.out_stride[ndim - 1]);
+  if constexpr (Eval::kVec && DT == PDH_F32 && EPT == 4) {
+    if (step == 1) {
+      *reinterpret_cast<f32x4u*>(static_cast<float*>(out) + off) = f32x4u{res[0], res[1], res[2], res[3]};
+      return;
+    }
+  }
 #pragma unroll
   for (int e = 0; e < EPT; ++e) st_dt<DT>(out, off + e * step, res[e]);
 }

@@ -14,6 +14,9 @@
 namespace pdh {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// four floats at any 4-byte boundary: one global_load_dwordx4 / store (the
+// hardware takes dword-aligned multi-dword accesses)
+typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));

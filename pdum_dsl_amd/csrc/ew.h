@@ -144,6 +144,7 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
 }
 
 struct InterpEval {
+  static constexpr bool kVec = false;  // operands read element by element
   template <int EPT>
   static __device__ __forceinline__ void run(const pdh_ew_program& p, const EwOperands& ops, int dtype,
                                              const int (&c0)[PDH_EW_MAX_DIMS], const float (&acc)[EPT],
