@@ -20,6 +20,8 @@ planner's numpy interpreter, so each can check the other:
   tl.repeat_like / tl.repeat / tl.split / tl.stage / tl.select / tl.iota /
   tl.const       layout views (region_evaluator.py:372-430)
   tl.rename / tl.shift / tl.slice   relabelings and a window (layout.py)
+  tl.pad / tl.flip / tl.merge       a widened frame, a reversal, split's inverse
+                 (layout.py)
   tl.take        the gather (indexing.py:120-230)
   tl.scatter_add its adjoint, duplicates summed (indexing.py:153-190, 223-259)
   tl.fold        a Python loop over the scan dim, each element source
@@ -221,6 +223,27 @@ def _dispatch(n, ev):
         t = x.t
         for ax, (d, o) in enumerate(zip(x.dims, n.type.dims)):
             t = t.narrow(ax, o.start - d[1], o.stop - o.start)
+        return V(t, tuple((d.name, d.start, d.stop) for d in n.type.dims))
+    if op == "tl.pad":  # layout.py pad: frames widened, new cells = fill
+        x = ev(n.args[0])
+        out_dims = tuple((d.name, d.start, d.stop) for d in n.type.dims)
+        t = torch.full([d[2] - d[1] for d in out_dims], float(_attr(n, "fill", 0.0)), dtype=torch.float64)
+        window = tuple(slice(xd[1] - od[1], xd[2] - od[1]) for xd, od in zip(x.dims, out_dims))
+        t[window] = x.t
+        return V(t, out_dims)
+    if op == "tl.flip":  # layout.py flip: coordinate c reads start + stop - 1 - c
+        x = ev(n.args[0])
+        return V(torch.flip(x.t, dims=(x.names.index(_attr(n, "name")),)), x.dims)
+    if op == "tl.merge":  # layout.py merge: split's inverse, parts outer first
+        x = ev(n.args[0])
+        parts = _attr(n, "parts")
+        parts = (parts,) if isinstance(parts, str) else tuple(parts)
+        rest = [nm for nm in x.names if nm not in parts]
+        first = x.names.index(parts[0])
+        at = first - sum(1 for nm in x.names[:first] if nm in parts)
+        order = rest[:at] + list(parts) + rest[at:]
+        t = x.order(tuple(order))
+        t = t.reshape(tuple(t.shape[:at]) + (-1,) + tuple(t.shape[at + len(parts):]))
         return V(t, tuple((d.name, d.start, d.stop) for d in n.type.dims))
     if op == "tl.take":  # indexing.py:192-230: the taken dim replaced in place by idx's dims
         table, idx = ev(n.args[0]), ev(n.args[1])

@@ -23,6 +23,11 @@ templates), over the vocabulary this backend reads:
   tl.take        -> tl.scatter_add of the cotangent at the same indices
                  (duplicates sum), and tl.scatter_add -> tl.take
                  (autodiff.py:846-856); indices carry no gradient
+  layout views (autodiff.py:765-806): tl.shift -> the opposite shift,
+                 tl.slice -> tl.pad with zeros back to the operand's frames,
+                 tl.pad -> tl.slice (the fill carries no gradient),
+                 tl.flip -> tl.flip, tl.select -> repeat at the point + pad,
+                 tl.split -> tl.merge, tl.merge -> tl.split
   tl.stage       identity
   core.const / tl.const / tl.iota / comparisons / stop_gradient: no flow
 
@@ -211,6 +216,35 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
             contribute(table, b.emit("tl.scatter_add", c, idx, dim=d.name, extent=(d.start, d.stop), over=spliced))
         elif op == "tl.scatter_add":  # and the scatter-add's is the gather (autodiff.py:854-856)
             contribute(n.args[0], b.emit("tl.take", c, n.args[1], dim=n.attr("dim")))
+        elif op == "tl.shift":  # a relabelling of frames: shift back
+            back = tuple((nm, -int(dv)) for nm, dv in n.attr("deltas"))
+            contribute(n.args[0], b.emit("tl.shift", c, deltas=back))
+        elif op == "tl.slice":  # the window's cotangent, zero outside it
+            x = n.args[0]
+            ext = tuple((nm, (x.type.dim(nm).start, x.type.dim(nm).stop)) for nm, _ in n.attr("ranges"))
+            contribute(x, b.emit("tl.pad", c, extents=ext, fill=0.0))
+        elif op == "tl.pad":  # the operand's cells; the fill is a constant
+            x = n.args[0]
+            rng = tuple((nm, (x.type.dim(nm).start, x.type.dim(nm).stop)) for nm, _ in n.attr("extents"))
+            contribute(x, b.emit("tl.slice", c, ranges=rng))
+        elif op == "tl.flip":
+            contribute(n.args[0], b.emit("tl.flip", c, name=n.attr("name")))
+        elif op == "tl.select":  # the point's cotangent, zero elsewhere along each fixed dim
+            x = n.args[0]
+            cur = c
+            for nm, i in n.attr("coords"):
+                cur = b.emit("tl.repeat", cur, name=nm, extent=(int(i), int(i) + 1))
+            ext = tuple((nm, (x.type.dim(nm).start, x.type.dim(nm).stop)) for nm, _ in n.attr("coords"))
+            contribute(x, b.emit("tl.pad", cur, extents=ext, fill=0.0))
+        elif op == "tl.split":  # the blocks merged back, outer first
+            parts = tuple(nm for nm, _ in n.attr("parts"))
+            contribute(n.args[0], b.emit("tl.merge", c, parts=parts, name=n.attr("name")))
+        elif op == "tl.merge":
+            x = n.args[0]
+            parts = n.attr("parts")
+            parts = (parts,) if isinstance(parts, str) else tuple(parts)
+            contribute(x, b.emit("tl.split", c, name=n.attr("name"),
+                                 parts=tuple((nm, x.type.dim(nm).size) for nm in parts)))
         elif op == "tl.rename":  # a relabelling: the cotangent takes the operand's names back
             back = tuple(sorted((new, old) for old, new in n.attr("mapping")))
             contribute(n.args[0], b.emit("tl.rename", c, mapping=back))

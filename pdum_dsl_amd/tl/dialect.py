@@ -19,6 +19,11 @@ emit and consume (packages/tensorlib/src/pdum/tl/dialect.py:115-487):
   tl.rename     mapping         renames dims in place (a view: no data moves)
   tl.shift      deltas          moves dims' frames by integer deltas (a view)
   tl.slice      ranges          restricts dims to absolute [lo, hi) (a view)
+  tl.pad        extents[, fill] widens dims' frames to [lo, hi), new cells = fill
+                                (slice's adjoint)
+  tl.flip       name            reverses one dim: out[c] = x[start + stop - 1 - c]
+  tl.merge      parts, name     (outer .. inner) dims -> one dim at [0, N):
+                                split's inverse (and adjoint)
   tl.take       dim             out = table[idx, rest]: a gather, no template row
   tl.scatter_add dim, extent[, over]  take's adjoint: out[v, rest] = sum of
                                 values at the positions p with idx[p] == v
@@ -226,6 +231,49 @@ def _r_slice(args, at, regions):
     return TensorType(tuple(out))
 
 
+def _r_pad(args, at, regions):
+    """Widens dims' frames to absolute [lo, hi) containing their domains
+    (layout.py pad): the new cells hold ``fill``."""
+    (x,) = args
+    ext = dict(at["extents"])
+    for nm, (lo, hi) in ext.items():
+        d = x.dim(nm)
+        if not int(lo) <= d.start <= d.stop <= int(hi):
+            raise TypeError(f"tl.pad {nm}=[{lo}, {hi}) does not contain [{d.start}, {d.stop})")
+    return TensorType(tuple(Dim(d.name, *(int(v) for v in ext[d.name])) if d.name in ext else d for d in x.dims))
+
+
+def _r_flip(args, at, regions):
+    (x,) = args
+    x.dim(at["name"])
+    return TensorType(x.dims)
+
+
+def _r_merge(args, at, regions):
+    """Merges the dims ``parts`` (outer first, each starting at 0) into one
+    dim ``name`` at [0, prod) placed where the first part is (layout.py merge)."""
+    (x,) = args
+    parts = _dims_arg(at["parts"])
+    if len(parts) < 1 or len(set(parts)) != len(parts):
+        raise TypeError(f"tl.merge parts {parts} must be distinct dims")
+    size = 1
+    for nm in parts:
+        d = x.dim(nm)
+        if d.start != 0:
+            raise TypeError(f"tl.merge: part {nm!r} must start at 0")
+        size *= d.size
+    name = at["name"]
+    if x.has(name) and name not in parts:
+        raise TypeError(f"tl.merge: dim {name!r} already exists")
+    out = []
+    for d in x.dims:
+        if d.name == parts[0]:
+            out.append(Dim(name, 0, size))
+        elif d.name not in parts:
+            out.append(d)
+    return TensorType(tuple(out))
+
+
 def _r_take(args, at, regions):
     """out = table[idx, rest]: the taken dim is replaced IN PLACE by idx's dims
     (indexing.py:120-138); idx dims the table already carries must align."""
@@ -315,11 +363,15 @@ OPS: dict[str, OpDef] = {
     "tl.rename": OpDef("tl.rename", _r_rename),
     "tl.shift": OpDef("tl.shift", _r_shift),
     "tl.slice": OpDef("tl.slice", _r_slice),
+    "tl.pad": OpDef("tl.pad", _r_pad),
+    "tl.flip": OpDef("tl.flip", _r_flip),
+    "tl.merge": OpDef("tl.merge", _r_merge),
     "tl.take": OpDef("tl.take", _r_take),
     "tl.scatter_add": OpDef("tl.scatter_add", _r_scatter_add),
 }
 
-TILE_OPS = frozenset(OPS) - {"tl.argtopk", "tl.take", "tl.scatter_add"}
+# ops no template row reads: a region holding one plans it red
+TILE_OPS = frozenset(OPS) - {"tl.argtopk", "tl.take", "tl.scatter_add", "tl.pad", "tl.flip", "tl.merge"}
 
 
 def builder() -> Builder:

@@ -96,7 +96,15 @@ def run_region(region: Region, values: list):
 
     def _ev(n: Node):
         if id(n) in bind:
-            return bind[id(n)]
+            v = bind[id(n)]
+            tt = n.type
+            if isinstance(v, Field) and isinstance(tt, TensorType):
+                # a value bound by names alone (field() frames start at 0) takes
+                # the param's declared frames: a seed aligned with an offset target
+                frames = {d.name: d for d in tt.dims}
+                if set(v.names) == set(frames) and all(d.size == frames[d.name].size for d in v.dims):
+                    v = Field(v.arr, tuple(frames[d.name] for d in v.dims))
+            return v
         op = n.op
         if op == "core.const":
             return float(n.attr("value"))
@@ -182,6 +190,23 @@ def run_region(region: Region, values: list):
             x = ev(n.args[0])
             idx = tuple(slice(o.start - d.start, o.stop - d.start) for d, o in zip(x.dims, n.type.dims))
             return Field(x.arr[idx], n.type.dims)
+        if op == "tl.pad":
+            x = ev(n.args[0])
+            widths = [(d.start - o.start, o.stop - d.stop) for d, o in zip(x.dims, n.type.dims)]
+            return Field(np.pad(x.arr, widths, constant_values=float(n.attr("fill", 0.0))), n.type.dims)
+        if op == "tl.flip":
+            x = ev(n.args[0])
+            return Field(np.flip(x.arr, axis=x.names.index(n.attr("name"))), x.dims)
+        if op == "tl.merge":
+            x = ev(n.args[0])
+            parts = n.attr("parts")
+            parts = (parts,) if isinstance(parts, str) else tuple(parts)
+            rest = [nm for nm in x.names if nm not in parts]
+            at = x.names.index(parts[0]) - sum(1 for nm in x.names[:x.names.index(parts[0])] if nm in parts)
+            order = rest[:at] + list(parts) + rest[at:]
+            arr = x.to_numpy(tuple(order))
+            shp = arr.shape[:at] + (int(np.prod(arr.shape[at:at + len(parts)])),) + arr.shape[at + len(parts):]
+            return Field(arr.reshape(shp), n.type.dims)
         if op == "tl.take":
             table, idx = ev(n.args[0]), ev(n.args[1])
             dim = n.attr("dim")
