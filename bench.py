@@ -454,9 +454,10 @@ def _carved_plan_line(torch):
 
 def _carved_grad_line(torch, dtype="f32"):
     """A gpt2-small training step's compute: the joint of the forward and the
-    gradients of every weight but the embedding tables (autodiff.grad of the
-    logits, seeded by a random cotangent), planned by plan_model and run by
-    the device executor as one HIP graph. fp32 storage: the carved backward
+    gradients of every weight, the embedding tables included (autodiff.grad
+    of the logits, seeded by a random cotangent; wte's gradient is the
+    scatter-add of the embedding's cotangent plus the tied head's product),
+    planned by plan_model and run by the device executor as one HIP graph. fp32 storage: the carved backward
     rounds every boundary to the storage type, and in bf16 the layernorm and
     softmax backward carves cancel (layer 0's gradients drift far from fp32
     over 12 layers). The contractions run on the bf16 matrix cores with the
@@ -464,8 +465,8 @@ def _carved_grad_line(torch, dtype="f32"):
     ``ms``), and, timed beside it, three (about 2^-16 of each product,
     ``ms_bf16x3``).
     Checked against torch fp32 autograd of the same forward on the same
-    weights (three gradients), and timed beside torch's forward + backward
-    (eager autograd, fp32, the same weights)."""
+    weights (four gradients, wte among them), and timed beside torch's
+    forward + backward (eager autograd, fp32, the same weights)."""
     import time as _time
 
     from pdum_dsl_amd.executor import PlanExecutor
@@ -477,7 +478,7 @@ def _carved_grad_line(torch, dtype="f32"):
     t0 = _time.perf_counter()
     m = zoo.gpt2(cfg, seed=7)
     pn = tuple(m.names[id(p)] for p in m.region.params)
-    wrt = tuple(n for n in pn if n not in ("ids", "wte", "wpe"))
+    wrt = tuple(n for n in pn if n != "ids")
     rg = grad(m.region, "logits", seed="dlogits", wrt=wrt, names=region_names(m.region, pn, ("logits",)))
     plan = plan_model(rg.region)
     ex = PlanExecutor(plan, rg.region, dtype, f32_contract="bf16x6")
@@ -507,7 +508,7 @@ def _carved_grad_line(torch, dtype="f32"):
     def rel_errs(outs_):
         errs_ = {}
         by = dict(zip(rg.outputs, outs_))
-        for nm in ("h.0.mlp.w1", "h.11.mlp.w2", "lnfg"):
+        for nm in ("h.0.mlp.w1", "h.11.mlp.w2", "lnfg", "wte"):
             node = rg.nodes[rg.grads[nm]]
             pt = next(p for p in m.region.params if m.names[id(p)] == nm).type
             got = by[rg.grads[nm]].float().permute([node.type.names.index(d) for d in pt.names])
@@ -545,8 +546,8 @@ def _carved_grad_line(torch, dtype="f32"):
     for c in plan.carves:
         by_t[c.group.template] = by_t.get(c.group.template, 0) + 1
     return {
-        "config": "gpt2-small shape (as the carved_plan line), forward + gradients of every weight but the "
-                  f"embedding tables, {dtype} storage / fp32 accumulate; random weights and cotangent",
+        "config": "gpt2-small shape (as the carved_plan line), forward + gradients of every weight (the "
+                  f"embedding tables included), {dtype} storage / fp32 accumulate; random weights and cotangent",
         "carves": by_t, "device_steps": len(ex.steps), "plan_s": round(plan_s, 2), "ms": round(ms, 4),
         "tokens_per_s": round(cfg.t / ms * 1e3, 1), "ms_bf16x3": round(ms_b, 4),
         "torch_eager_fwd_bwd_ms": round(ms_torch, 4), "torch_dtype": "f32",
