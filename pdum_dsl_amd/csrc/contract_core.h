@@ -256,6 +256,22 @@ __device__ __forceinline__ void reduce_cols_body(const pdh_ew_program& ps, const
 // 64 banks, 8 lanes on 32 banks).
 __device__ __forceinline__ int swz_gemm(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+// Four fp32 as four 16-bit elements, round to nearest even by the hardware
+// conversion (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32: one instruction a pair).
+template <int DT>
+__device__ __forceinline__ u32x2 pack4_16(const float (&r)[4]) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  if constexpr (DT == PDH_BF16) {
+    typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+    return u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(f2{r[0], r[1]}, h2)),
+                 __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{r[2], r[3]}, h2))};
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(f2{r[0], r[1]}, h2)),
+                 __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{r[2], r[3]}, h2))};
+  }
+}
+
 // Epilogue for EPT consecutive columns col0.. of one row. Elements past the
 // output are neither computed nor stored, so every operand read stays inside
 // its view: a full group runs once for all EPT columns, a ragged right edge
@@ -276,11 +292,7 @@ __device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const
         if constexpr (DT == PDH_F32) {
           *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + o0) = f32x4{res[0], res[1], res[2], res[3]};
         } else {
-          uint16_t h[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = DT == PDH_BF16 ? f32_to_bf16(res[e]) : f32_to_f16(res[e]);
-          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + o0) =
-              u32x2{h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16)};
+          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + o0) = pack4_16<DT>(res);
         }
         return;
       }
