@@ -281,6 +281,45 @@ def with_slots(prog, first: int, total: int):
     return new
 
 
+def splitk_sum(prog, S: int):
+    """The epilogue program ``prog`` (which reads the contraction's sum with
+    ACC) rewritten to read that sum as the total of S partial planes: slots
+    0..S-1 hold the planes (laid out like the output), prog's own operands
+    move up by S, and the sum, added in plane order, replaces ACC. None when
+    the operand table or the registers cannot hold it."""
+    if S < 2 or prog.n_operands + S > L.EW_MAX_OPERANDS or prog.n_insns + 2 * S > L.EW_MAX_INSNS:
+        return None
+    used = {int(prog.out_reg)} | {int(prog.insns[j].dst) for j in range(prog.n_insns)}
+    free = [r for r in range(L.EW_MAX_REGS) if r not in used]
+    if len(free) < 2:
+        return None
+    ra, rb = free[0], free[1]
+    new = L.EwProgram()
+    new.ndim, new.out_reg, new.n_operands = prog.ndim, prog.out_reg, prog.n_operands + S
+    for d in range(prog.ndim):
+        new.shape[d], new.start[d], new.out_stride[d] = prog.shape[d], prog.start[d], prog.out_stride[d]
+        for i in range(S):
+            new.in_stride[i][d] = prog.out_stride[d]
+        for i in range(prog.n_operands):
+            new.in_stride[S + i][d] = prog.in_stride[i][d]
+    seq = [(L.EW["LOAD"], ra, 0, 0, 0, 0.0)]
+    for i in range(1, S):
+        seq += [(L.EW["LOAD"], rb, i, 0, 0, 0.0), (L.EW["ADD"], ra, ra, rb, 0, 0.0)]
+    for j in range(prog.n_insns):
+        src = prog.insns[j]
+        op, dst, a, b, c, imm = src.op, src.dst, src.a, src.b, src.c, src.imm
+        if op == L.EW["ACC"]:
+            op, a, b = L.EW["MAX"], ra, ra  # max(x, x) = x, NaN included
+        elif op == L.EW["LOAD"]:
+            a = a + S
+        seq.append((op, dst, a, b, c, imm))
+    new.n_insns = len(seq)
+    for j, (op, dst, a, b, c, imm) in enumerate(seq):
+        ins = new.insns[j]
+        ins.op, ins.dst, ins.a, ins.b, ins.c, ins.imm = op, dst, a, b, c, imm
+    return new
+
+
 def merge_dims(prog, groups):
     """Merge groups of consecutive lattice dims of a program into one dim each
     (e.g. (unit, t, nh, hk) -> (unit, t, nh*hk)). A group merges when every

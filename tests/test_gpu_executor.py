@@ -188,6 +188,28 @@ def test_scatter_add_rows_counts_and_drops_bad_indices_and_takes_strided_rows():
     assert torch.equal(got.cpu(), _add_at_reference(values.contiguous(), idx, 9, torch.float32))
 
 
+@pytest.mark.parametrize("T,D,F,f32c", [(300, 1024, 200, "bf16x6"), (1024, 3072, 64, "bf16x3"), (64, 640, 96, "fma")])
+def test_a_small_fp32_contraction_splits_k(T, D, F, f32c):
+    """An fp32 contraction whose output tiles cannot fill the chip runs k in
+    slices (fp32 partial planes added in order by the epilogue's map chain):
+    against the float64 denotation at the mode's tolerance, and against the
+    unsplit kernel called directly."""
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import zoo
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    subj = zoo.linear_gelu(T=T, D=D, F=F, seed=T + D)
+    ex = PlanExecutor(plan_model(subj.region), subj.region, "f32", f32_contract=f32c)
+    assert any("ksplit=" in st.source for st in ex.steps), [st.source for st in ex.steps]
+    vals = [f.arr for f in subj.inputs]
+    ex.bind(vals)
+    got = ex.run().cpu().numpy().astype(np.float64)
+    torch.cuda.synchronize()
+    want = subj.oracle(vals)
+    tol = {"bf16x6": 1e-5, "bf16x3": 2e-4, "fma": 1e-5}[f32c]
+    assert np.abs(got - want).max() <= tol * max(1.0, np.abs(want).max())
+
+
 def test_a_captured_plan_replays_the_eager_result():
     """The whole carved forward as one HIP graph: replays, with eager work and
     synchronizations between them, each give the eager pass's output."""
