@@ -317,6 +317,20 @@ int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, const void* 
                          int64_t batch, int64_t m, int64_t n, int64_t k, const pdh_ew_program* epi,
                          const void* const* operands, void* out, int dtype, void* stream);
 
+/* pdh_contract_strided with each batch entry's k split into ksplit slices of
+ * k / ksplit (k a multiple of 64 * ksplit) that run as separate workgroups:
+ * batch index e * ksplit + s holds entry e's products over k columns
+ * [s k / ksplit, (s + 1) k / ksplit), and the epilogue's lattice is
+ * (batch * ksplit, m, n). With an identity epilogue into an fp32 buffer these
+ * are partial sums a second pass adds (the executor does so, in slice order,
+ * through the real epilogue): for grids whose output tiles cannot fill the
+ * chip. No counterpart in the reference, whose contraction kernels do not
+ * split k. */
+int pdh_contract_strided_ksplit(const void* a, int64_t sa_b, int64_t sa_r, const void* bt, int64_t sb_b, int64_t sb_r,
+                                int64_t batch, int64_t m, int64_t n, int64_t k, int64_t ksplit,
+                                const pdh_ew_program* epi, const void* const* operands, void* out, int dtype,
+                                void* stream);
+
 /* How PDH_F32 contractions run (pdh_contract, pdh_contract_strided): 6 (the
  * default) splits each operand into three bf16 terms and sums the six cross
  * products above 2^-24 of each product: fp32 grade; 3 keeps two terms and

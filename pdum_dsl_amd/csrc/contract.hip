@@ -287,29 +287,54 @@ extern "C" int pdh_contract(const void* a, const void* bt, int64_t batch, int64_
               "pdh_contract: output too large for one call");
   PDH_REQUIRE(aligned16(a) && aligned16(bt), PDH_EINVAL, "pdh_contract: a / bt must be 16-byte aligned");
   const ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n),
-                        static_cast<int>(k), static_cast<int>(kp), 0, 0, dtype, m * kp, kp, n * kp, kp};
+                        static_cast<int>(k), static_cast<int>(kp), 0, 0, dtype, m * kp, kp, n * kp, kp, 1};
   return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), "pdh_contract");
 }
+
+namespace {
+
+// pdh_contract_strided and its k-split form: batch entry e's k columns in
+// ksplit slices of k / ksplit, slice s of entry e as batch index e ksplit + s.
+int contract_strided_impl(const void* a, int64_t sa_b, int64_t sa_r, const void* bt, int64_t sb_b, int64_t sb_r,
+                          int64_t batch, int64_t m, int64_t n, int64_t k, int64_t ksplit,
+                          const pdh_ew_program* epi, const void* const* operands, void* out, int dtype,
+                          void* stream, const char* fn) {
+  PDH_REQUIRE(dtype_ok(dtype), PDH_EUNSUPPORTED, "%s: dtype %d", fn, dtype);
+  PDH_REQUIRE(a && bt && out, PDH_EINVAL, "%s: null pointer", fn);
+  PDH_REQUIRE(batch >= 1 && m >= 1 && n >= 1 && k >= 1 && k % kBK == 0, PDH_EINVAL,
+              "%s: need batch, m, n >= 1 and k a positive multiple of %d", fn, kBK);
+  PDH_REQUIRE(ksplit >= 1 && ksplit <= 64 && k % (kBK * ksplit) == 0, PDH_EINVAL,
+              "%s: ksplit = %lld must be in [1, 64] with k a multiple of %d * ksplit", fn, (long long)ksplit, kBK);
+  PDH_REQUIRE(batch * ksplit * m * n <= INT32_MAX && m <= INT32_MAX / 2 && n <= INT32_MAX / 2, PDH_EINVAL,
+              "%s: output too large for one call", fn);
+  const int64_t align = dtype == PDH_F32 ? 4 : 8;  // 16-byte rows and batch slices
+  PDH_REQUIRE(sa_r >= k && sb_r >= k && sa_b >= 0 && sb_b >= 0 && sa_r % align == 0 && sb_r % align == 0 &&
+                  sa_b % align == 0 && sb_b % align == 0,
+              PDH_EINVAL, "%s: row strides must be >= k and all strides multiples of %lld", fn, (long long)align);
+  PDH_REQUIRE(aligned16(a) && aligned16(bt), PDH_EINVAL, "%s: a / bt must be 16-byte aligned", fn);
+  const int64_t kc = k / ksplit;
+  const ContractArgs ca{a, bt, out, static_cast<int>(batch * ksplit), static_cast<int>(m), static_cast<int>(n),
+                        static_cast<int>(kc), static_cast<int>(kc), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r,
+                        static_cast<int>(ksplit)};
+  return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), fn);
+}
+
+}  // namespace
 
 extern "C" int pdh_contract_strided(const void* a, int64_t sa_b, int64_t sa_r, const void* bt, int64_t sb_b,
                                     int64_t sb_r, int64_t batch, int64_t m, int64_t n, int64_t k,
                                     const pdh_ew_program* epi, const void* const* operands, void* out, int dtype,
                                     void* stream) {
-  PDH_REQUIRE(dtype_ok(dtype), PDH_EUNSUPPORTED, "pdh_contract_strided: dtype %d", dtype);
-  PDH_REQUIRE(a && bt && out, PDH_EINVAL, "pdh_contract_strided: null pointer");
-  PDH_REQUIRE(batch >= 1 && m >= 1 && n >= 1 && k >= 1 && k % kBK == 0, PDH_EINVAL,
-              "pdh_contract_strided: need batch, m, n >= 1 and k a positive multiple of %d", kBK);
-  PDH_REQUIRE(batch * m * n <= INT32_MAX && m <= INT32_MAX / 2 && n <= INT32_MAX / 2, PDH_EINVAL,
-              "pdh_contract_strided: output too large for one call");
-  const int64_t align = dtype == PDH_F32 ? 4 : 8;  // 16-byte rows and batch slices
-  PDH_REQUIRE(sa_r >= k && sb_r >= k && sa_b >= 0 && sb_b >= 0 && sa_r % align == 0 && sb_r % align == 0 &&
-                  sa_b % align == 0 && sb_b % align == 0,
-              PDH_EINVAL, "pdh_contract_strided: row strides must be >= k and all strides multiples of %lld",
-              (long long)align);
-  PDH_REQUIRE(aligned16(a) && aligned16(bt), PDH_EINVAL, "pdh_contract_strided: a / bt must be 16-byte aligned");
-  const ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n),
-                        static_cast<int>(k), static_cast<int>(k), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r};
-  return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), "pdh_contract_strided");
+  return contract_strided_impl(a, sa_b, sa_r, bt, sb_b, sb_r, batch, m, n, k, 1, epi, operands, out, dtype, stream,
+                               "pdh_contract_strided");
+}
+
+extern "C" int pdh_contract_strided_ksplit(const void* a, int64_t sa_b, int64_t sa_r, const void* bt, int64_t sb_b,
+                                           int64_t sb_r, int64_t batch, int64_t m, int64_t n, int64_t k,
+                                           int64_t ksplit, const pdh_ew_program* epi, const void* const* operands,
+                                           void* out, int dtype, void* stream) {
+  return contract_strided_impl(a, sa_b, sa_r, bt, sb_b, sb_r, batch, m, n, k, ksplit, epi, operands, out, dtype,
+                               stream, "pdh_contract_strided_ksplit");
 }
 
 extern "C" int pdh_reduce_rows(const pdh_ew_program* summand, int nk, const pdh_ew_program* epi,

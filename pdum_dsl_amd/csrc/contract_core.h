@@ -37,7 +37,19 @@ struct ContractArgs {
   int tiles_m, tiles_n;
   int dtype;
   long long sa_b, sa_r, sb_b, sb_r;  // element strides of a and bt: per batch, per row (k is contiguous)
+  // k slices per batch entry: batch index bb is (bb / ksplit, slice bb % ksplit),
+  // and slice s reads k columns [s kp, (s + 1) kp) (1: no split)
+  int ksplit;
 };
+
+// Element offsets of batch index bb's a and bt rows (the batch entry's, moved
+// to its k slice).
+__device__ __forceinline__ long long contract_off_a(const ContractArgs& a, int bb) {
+  return static_cast<long long>(bb / a.ksplit) * a.sa_b + static_cast<long long>(bb % a.ksplit) * a.kp;
+}
+__device__ __forceinline__ long long contract_off_b(const ContractArgs& a, int bb) {
+  return static_cast<long long>(bb / a.ksplit) * a.sb_b + static_cast<long long>(bb % a.ksplit) * a.kp;
+}
 
 constexpr int kBK = 64;
 constexpr int kRowB = kBK * 2;  // LDS bytes per tile row (64 16-bit k values)
@@ -358,8 +370,8 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
   const int b = blockIdx.x / per, rest = blockIdx.x % per;
   const int m0 = (rest / a.tiles_n) * BM, n0 = (rest % a.tiles_n) * BM;
   const uint32_t rowa = static_cast<uint32_t>(a.sa_r) * 2u, rowbb = static_cast<uint32_t>(a.sb_r) * 2u;
-  const uint16_t* abase = static_cast<const uint16_t*>(a.a) + b * a.sa_b;
-  const uint16_t* bbase = static_cast<const uint16_t*>(a.bt) + b * a.sb_b;
+  const uint16_t* abase = static_cast<const uint16_t*>(a.a) + contract_off_a(a, b);
+  const uint16_t* bbase = static_cast<const uint16_t*>(a.bt) + contract_off_b(a, b);
   // the buffers end after the batch slice's last row: rows past m (n) read as zero
   const rsrc_t ar = make_rsrc(abase, (static_cast<uint32_t>(a.m) - 1u) * rowa + static_cast<uint32_t>(a.kp) * 2u);
   const rsrc_t br = make_rsrc(bbase, (static_cast<uint32_t>(a.n) - 1u) * rowbb + static_cast<uint32_t>(a.kp) * 2u);
@@ -445,8 +457,8 @@ template <typename Eval>
 __device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_ew_program& p, const EwOperands& ops,
                                                int b, int m0, int n0, float (*as)[kFT + 4], float (*bs)[kFT + 4]) {
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  const float* abase = static_cast<const float*>(a.a) + b * a.sa_b;
-  const float* bbase = static_cast<const float*>(a.bt) + b * a.sb_b;
+  const float* abase = static_cast<const float*>(a.a) + contract_off_a(a, b);
+  const float* bbase = static_cast<const float*>(a.bt) + contract_off_b(a, b);
   const int lr = tid >> 2, lc = (tid & 3) * 4;  // this lane's tile row and 4 k values per load
   float acc[4][4] = {};
   for (int k0 = 0; k0 < a.kp; k0 += kFK) {
@@ -573,8 +585,8 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
   const int b = blockIdx.x / per, rest = blockIdx.x % per;
   const int m0 = (rest / a.tiles_n) * BM, n0 = (rest % a.tiles_n) * BM;
   const uint32_t rowa = static_cast<uint32_t>(a.sa_r) * 4u, rowbb = static_cast<uint32_t>(a.sb_r) * 4u;
-  const float* abase = static_cast<const float*>(a.a) + b * a.sa_b;
-  const float* bbase = static_cast<const float*>(a.bt) + b * a.sb_b;
+  const float* abase = static_cast<const float*>(a.a) + contract_off_a(a, b);
+  const float* bbase = static_cast<const float*>(a.bt) + contract_off_b(a, b);
   // the buffers end after the batch slice's last row: rows past m (n) read as zero
   const rsrc_t ar = make_rsrc(abase, (static_cast<uint32_t>(a.m) - 1u) * rowa + static_cast<uint32_t>(a.kp) * 4u);
   const rsrc_t br = make_rsrc(bbase, (static_cast<uint32_t>(a.n) - 1u) * rowbb + static_cast<uint32_t>(a.kp) * 4u);

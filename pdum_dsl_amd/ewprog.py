@@ -281,12 +281,13 @@ def with_slots(prog, first: int, total: int):
     return new
 
 
-def splitk_sum(prog, S: int):
+def splitk_sum(prog, S: int, plane_strides=None):
     """The epilogue program ``prog`` (which reads the contraction's sum with
     ACC) rewritten to read that sum as the total of S partial planes: slots
-    0..S-1 hold the planes (laid out like the output), prog's own operands
-    move up by S, and the sum, added in plane order, replaces ACC. None when
-    the operand table or the registers cannot hold it."""
+    0..S-1 hold the planes (strides ``plane_strides`` over prog's lattice,
+    default the output's), prog's own operands move up by S, and the sum,
+    added in plane order, replaces ACC. None when the operand table or the
+    registers cannot hold it."""
     if S < 2 or prog.n_operands + S > L.EW_MAX_OPERANDS or prog.n_insns + 2 * S > L.EW_MAX_INSNS:
         return None
     used = {int(prog.out_reg)} | {int(prog.insns[j].dst) for j in range(prog.n_insns)}
@@ -299,7 +300,7 @@ def splitk_sum(prog, S: int):
     for d in range(prog.ndim):
         new.shape[d], new.start[d], new.out_stride[d] = prog.shape[d], prog.start[d], prog.out_stride[d]
         for i in range(S):
-            new.in_stride[i][d] = prog.out_stride[d]
+            new.in_stride[i][d] = prog.out_stride[d] if plane_strides is None else int(plane_strides[d])
         for i in range(prog.n_operands):
             new.in_stride[S + i][d] = prog.in_stride[i][d]
     seq = [(L.EW["LOAD"], ra, 0, 0, 0, 0.0)]

@@ -815,20 +815,21 @@ class PlanExecutor:
         shape = y.type.shape
         tdt = _TORCH_DT[self.dtype]
         # Split k: an fp32 contraction whose output tiles cannot fill the chip
-        # runs S slices of k as S workgroups per tile (partial sums to an fp32
-        # workspace), and a map chain adds the slices in order and applies the
-        # epilogue. S divides the k tiles, so every slice is a whole number of them.
+        # runs S slices of each batch entry's k as S workgroups per tile
+        # (pdh_contract_strided_ksplit: partial sums into an fp32 workspace
+        # [B][S][M][N]), and a map chain adds the slices in order and applies
+        # the epilogue. S divides the k tiles, so every slice is a whole number of them.
         S, fin, ident = 1, None, None
-        tiles = -(-M // 64) * -(-N // 64)
-        if self.dtype == "f32" and B == 1 and -(-M // 128) * -(-N // 128) < _CUS and KP // 64 >= 8:
+        tiles = B * -(-M // 64) * -(-N // 64)
+        if self.dtype == "f32" and B * -(-M // 128) * -(-N // 128) < _CUS and KP // 64 >= 8:
             cands = [d for d in range(2, 9) if (KP // 64) % d == 0 and KP // 64 // d >= 2]
             pick = next((d for d in cands if tiles * d >= 2 * _CUS), cands[-1] if cands else 1)
-            fin = ewprog.splitk_sum(prog, pick) if pick > 1 else None
+            fin = ewprog.splitk_sum(prog, pick, (pick * M * N, N, 1)) if pick > 1 else None
             if fin is not None:
                 S = pick
                 ident = L.EwProgram()
                 ident.n_insns, ident.n_operands, ident.ndim, ident.out_reg = 1, 0, 3, 0
-                for d, (ext, st) in enumerate(zip((S, M, N), (M * N, N, 1))):
+                for d, (ext, st) in enumerate(zip((B * S, M, N), (M * N, N, 1))):
                     ident.shape[d], ident.out_stride[d] = ext, st
                 ident.insns[0].op = L.EW["ACC"]
 
@@ -860,10 +861,9 @@ class PlanExecutor:
             a, bt = build(pa), build(pb)
             out = torch.empty(shape, device="cuda", dtype=dt)
             if S > 1:  # k in S slices: partial sums, then their total through the epilogue
-                chunk = KP // S
-                ws = torch.empty((S, M, N), device="cuda", dtype=torch.float32)
-                K.contract_strided(a, (chunk, pa.strides[1]), bt, (chunk, pb.strides[1]), (S, M, N, chunk), ident, [],
-                                   ws, f32_mode=self.f32_contract)
+                ws = torch.empty((B * S, M, N), device="cuda", dtype=torch.float32)
+                K.contract_strided(a, pa.strides, bt, pb.strides, (B, M, N, KP), ident, [], ws,
+                                   f32_mode=self.f32_contract, ksplit=S)
                 flat = ws.reshape(-1)
                 K.map_chain(fin, [flat[s_ * M * N:] for s_ in range(S)] + [vals[i] for i in eslots], out)
                 return out

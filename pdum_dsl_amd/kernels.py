@@ -474,26 +474,35 @@ def contract(a: torch.Tensor, bt: torch.Tensor, k: int, epi: _lib.EwProgram, ope
 
 
 def contract_strided(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, shape, epi: _lib.EwProgram,
-                     operands: list, out: torch.Tensor, f32_mode: str | None = None) -> torch.Tensor:
+                     operands: list, out: torch.Tensor, f32_mode: str | None = None, ksplit: int = 1) -> torch.Tensor:
     """acc[b, m, n] = sum_k a[b, m, k] bt[b, n, k] with a and bt read through
     (batch, row) element strides from their tensors' first elements; k is
-    contiguous and a multiple of 64. ``shape`` = (batch, m, n, k)."""
+    contiguous and a multiple of 64. ``shape`` = (batch, m, n, k). With
+    ``ksplit`` > 1 each batch entry's k runs in that many slices and the
+    epilogue's lattice is (batch * ksplit, m, n): index e * ksplit + s holds
+    entry e's products over the s-th slice (pdh_contract_strided_ksplit)."""
     _require_cuda(a, bt, out, *operands)
     B, M, N, Kd = (int(x) for x in shape)
-    if a.dtype != bt.dtype or out.dtype != a.dtype or a.dtype not in _DT:
+    if a.dtype != bt.dtype or a.dtype not in _DT or out.dtype != a.dtype:
         raise ValueError("a / bt / out element types disagree")
     for t, (sb, sr), rows in ((a, a_strides, M), (bt, bt_strides, N)):
         reach = t.storage_offset() + (B - 1) * sb + (rows - 1) * sr + Kd
         if reach > t.untyped_storage().nbytes() // t.element_size():
             raise ValueError("a strided operand's view reaches past its storage")
-    if tuple(epi.shape[d] for d in range(3)) != (B, M, N) or epi.ndim != 3:
-        raise ValueError("the epilogue's lattice must be (batch, m, n)")
+    if tuple(epi.shape[d] for d in range(3)) != (B * ksplit, M, N) or epi.ndim != 3:
+        raise ValueError("the epilogue's lattice must be (batch * ksplit, m, n)")
     _check_views(epi, operands, out, 3)
     table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
-    _with_f32_mode(f32_mode, a.dtype, lambda: _lib.call(
-        "pdh_contract_strided", _ptr(a), int(a_strides[0]), int(a_strides[1]), _ptr(bt), int(bt_strides[0]),
-        int(bt_strides[1]), B, M, N, Kd, C.byref(epi), table, _ptr(out), _DT[a.dtype], C.c_void_p(_stream()),
-    ))
+    if ksplit == 1:
+        call = lambda: _lib.call(  # noqa: E731
+            "pdh_contract_strided", _ptr(a), int(a_strides[0]), int(a_strides[1]), _ptr(bt), int(bt_strides[0]),
+            int(bt_strides[1]), B, M, N, Kd, C.byref(epi), table, _ptr(out), _DT[a.dtype], C.c_void_p(_stream()))
+    else:
+        call = lambda: _lib.call(  # noqa: E731
+            "pdh_contract_strided_ksplit", _ptr(a), int(a_strides[0]), int(a_strides[1]), _ptr(bt),
+            int(bt_strides[0]), int(bt_strides[1]), B, M, N, Kd, int(ksplit), C.byref(epi), table, _ptr(out),
+            _DT[a.dtype], C.c_void_p(_stream()))
+    _with_f32_mode(f32_mode, a.dtype, call)
     return out
 
 

@@ -244,6 +244,34 @@ def _fp32_gemm(a, bt, kd, mode):
     return out.double().cpu().numpy()
 
 
+@pytest.mark.parametrize("mode", [6, 0])
+def test_the_k_split_partials_are_the_slices_products(mode):
+    """pdh_contract_strided_ksplit: index e * S + s holds batch entry e's
+    product over the s-th k slice, bit for bit the unsplit kernel on that
+    slice alone, and the slices sum to the whole product."""
+    from pdum_dsl_amd import kernels as K
+
+    g = torch.Generator(device="cuda").manual_seed(12)
+    B, M, N, Kd, S = 3, 70, 90, 512, 4
+    a = torch.randn(B, M, Kd, generator=g, device="cuda")
+    bt = torch.randn(B, N, Kd, generator=g, device="cuda")
+    parts = torch.empty(B * S, M, N, device="cuda")
+    K.contract_strided(a, (M * Kd, Kd), bt, (N * Kd, Kd), (B, M, N, Kd), _identity_epilogue(parts), [], parts,
+                       f32_mode={6: "bf16x6", 0: "fma"}[mode], ksplit=S)
+    c = Kd // S
+    for s in range(S):
+        one = torch.empty(B, M, N, device="cuda")
+        K.contract_strided(a[:, :, s * c:], (M * Kd, Kd), bt[:, :, s * c:], (N * Kd, Kd), (B, M, N, c),
+                           _identity_epilogue(one), [], one, f32_mode={6: "bf16x6", 0: "fma"}[mode])
+        assert torch.equal(parts.view(B, S, M, N)[:, s], one)
+    whole = torch.bmm(a.double(), bt.double().transpose(1, 2).contiguous())
+    got = parts.view(B, S, M, N).double().sum(1)
+    assert ((got - whole).abs().max() / whole.abs().max()).item() < 1e-5
+    with pytest.raises(Exception, match="ksplit"):
+        K.contract_strided(a, (M * Kd, Kd), bt, (N * Kd, Kd), (B, M, N, Kd), _identity_epilogue(parts), [], parts,
+                           ksplit=3)
+
+
 # mode -> tolerance as a fraction of the output's scale: 6 bf16 products per
 # term and VALU fma are fp32 grade; 3 products keep about 2^-16 of each
 # product; 1 (bf16-rounded operands) is exact against bf16-rounded inputs

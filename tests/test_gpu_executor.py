@@ -210,6 +210,24 @@ def test_a_small_fp32_contraction_splits_k(T, D, F, f32c):
     assert np.abs(got - want).max() <= tol * max(1.0, np.abs(want).max())
 
 
+def test_a_batched_fp32_contraction_splits_k():
+    """A contraction batched over a rider dim (12 heads: 12 x 64 x 64 output
+    tiles, k = 1024) splits k per batch entry: against the float64 oracle."""
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl.partition import plan_model
+    from tests.test_contraction_mapchain import _oracle, gemm_subject
+
+    region, vals = gemm_subject(M=64, K=1024, N=60, epilogue="relu_bias", seed=7, rider=("h", 12))
+    ex = PlanExecutor(plan_model(region), region, "f32")
+    assert any("ksplit=" in st.source and "batch=12" in st.source for st in ex.steps), [st.source for st in ex.steps]
+    ex.bind(vals)
+    got = ex.run().cpu().numpy().astype(np.float64)
+    torch.cuda.synchronize()
+    y = region.body[-1].args[0]
+    want = _oracle(region, vals, y.type.names)
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+
+
 def test_a_captured_plan_replays_the_eager_result():
     """The whole carved forward as one HIP graph: replays, with eager work and
     synchronizations between them, each give the eager pass's output."""
