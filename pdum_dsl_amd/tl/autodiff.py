@@ -28,6 +28,8 @@ templates), over the vocabulary this backend reads:
                  tl.pad -> tl.slice (the fill carries no gradient),
                  tl.flip -> tl.flip, tl.select -> repeat at the point + pad,
                  tl.split -> tl.merge, tl.merge -> tl.split
+  softmax        the max of a max-subtracted softmax that feeds nothing else
+                 gets no cotangent (shift invariance: its terms sum to zero)
   tl.stage       identity
   core.const / tl.const / tl.iota / comparisons / stop_gradient: no flow
 
@@ -125,9 +127,10 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
         seed_node = seed_param
 
     cot: dict[int, list] = {id(tnode): [seed_node]}
+    inert = _softmax_shifts(tnode)
 
     def contribute(n, g):
-        if n.op in ("core.const", "tl.const", "tl.iota"):
+        if n.op in ("core.const", "tl.const", "tl.iota") or id(n) in inert:
             return
         cot.setdefault(id(n), []).append(g)
 
@@ -321,6 +324,42 @@ def _pointwise_rule(n, c, contribute, pw, const):
         contribute(y, pw("where", m, const(0.0), c))
     else:
         raise NotImplementedError(f"marker {f!r} has no entry in the derivative table")
+
+
+def _softmax_shifts(root: Node) -> set:
+    """ids of the max (and its broadcast) of every softmax
+    div(exp(x - rl(max x)), rl(sum exp(x - rl(max x)))) under ``root`` that
+    feeds nothing but that softmax. Softmax is invariant to the shift, so
+    the max's total derivative is zero in exact arithmetic: the reference's
+    rules route the cotangent through the max's first-occurrence adjoint
+    (autodiff.py:635-665), where the terms cancel (sum_s P_s (dP_s - delta) =
+    0); here they are not emitted at all."""
+    from .fusion import match_softmax
+
+    order = _ancestors_of(root)
+    users: dict[int, list] = {}
+    for n in order:
+        for a in n.args:
+            users.setdefault(id(a), []).append(n)
+    users.setdefault(id(root), []).append(None)  # the target is read by the joint
+
+    def only(n, *allowed):
+        us = users.get(id(n), [])
+        return bool(us) and all(u is not None and any(u is x for x in allowed) for u in us)
+
+    inert: set = set()
+    for n in order:
+        m = match_softmax(n)
+        if m is None:
+            continue
+        mx, den = m["max"], m["den"]
+        e, rld = n.args
+        sub = e.args[0]
+        rlm = sub.args[1]
+        if (only(mx, rlm) and only(rlm, sub) and only(sub, e) and only(e, n, den) and only(den, rld)
+                and only(rld, n)):
+            inert.update((id(mx), id(rlm)))
+    return inert
 
 
 def _ancestors_of(root: Node):

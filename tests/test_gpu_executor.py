@@ -330,15 +330,15 @@ def test_a_bare_row_max_or_min_runs_on_the_device(f):
 
 
 _SMALL = dict(t=64, d=128, nh=2, hk=64, m=512, layers=1, v=64)
-_TWO_LAYER = dict(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)  # a scan shares a red carve with a reduction
+_TWO_LAYER = dict(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)
 
 
 @pytest.mark.parametrize("cfg,dtype,f32c,tol,tables", [
     (_SMALL, "f32", "bf16x6", 1e-5, False), (_SMALL, "f32", "bf16x3", 2e-4, False),
     (_SMALL, "f32", "bf16", 3e-2, False), (_SMALL, "f32", "fma", 1e-5, False),
-    (_SMALL, "bf16", "bf16x6", 5e-2, False), (_TWO_LAYER, "f32", "bf16x6", 3e-5, False),
+    (_SMALL, "bf16", "bf16x6", 7e-2, False), (_TWO_LAYER, "f32", "bf16x6", 3e-5, False),
     (_TWO_LAYER, "f32", "bf16x3", 5e-4, False), (_SMALL, "f32", "bf16x6", 1e-5, True),
-    (_SMALL, "bf16", "bf16x6", 5e-2, True), (_TWO_LAYER, "f32", "bf16x6", 3e-5, True)])
+    (_SMALL, "bf16", "bf16x6", 7e-2, True), (_TWO_LAYER, "f32", "bf16x6", 3e-5, True)])
 def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol, tables):
     """grad of gpt2's logits w.r.t. every weight (the embedding tables too
     when ``tables``: their gradient is a scatter-add of the embedding's
@@ -349,7 +349,8 @@ def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol, tab
     tol of its scale. The zoo's weights (std 0.4) make the attention sharp,
     so rounding the score contraction's operands is amplified by the
     softmax: bf16 storage (every boundary of ~75 carves rounded) measures
-    4.1e-2 on the attention weights; fp32 storage with f32_contract "bf16"
+    5.2e-2 on the attention weights (4.1e-2 while the softmax's max still
+    took its cotangent, whose zero-sum terms re-centred each rounded row); fp32 storage with f32_contract "bf16"
     (only the contraction operands rounded, fp32 accumulation and
     boundaries: an autocast's numerics) 2.3e-2; "bf16x3" 5.5e-5; "bf16x6" and
     "fma" 2e-6 (1e-5 at two layers)."""
@@ -372,8 +373,8 @@ def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol, tab
         assert len(np.unique(ids)) < np.size(ids)
     if dtype == "f32":
         assert all(f"f32={f32c}" in st.source for st in ex.steps if st.source.startswith("contract"))
-    if cfg is _TWO_LAYER:
-        assert any("split at scan" in st.source for st in ex.steps)
+    # the softmax's max takes no cotangent (shift invariance): no scan, no bare max in the backward
+    assert not any("split at scan" in st.source for st in ex.steps)
     ex.bind(vals)
     outs = ex.run()
     torch.cuda.synchronize()
