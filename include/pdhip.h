@@ -331,6 +331,21 @@ int pdh_contract_strided_ksplit(const void* a, int64_t sa_b, int64_t sa_r, const
                                 const pdh_ew_program* epi, const void* const* operands, void* out, int dtype,
                                 void* stream);
 
+/* The fp32 contraction over operands read in place as views: a[b, r, k] at
+ * a + b sa_b + r sa_r + k sa_k, bt likewise. Each operand has k contiguous
+ * (sa_k == 1) or its rows contiguous (sa_r == 1, any sa_k: a transposed
+ * tensor such as P in P^T dO); k is any size, its columns in ksplit slices of
+ * whole 64-column tiles (the last one ragged, none empty), and the epilogue's
+ * lattice is (batch * ksplit, m, n) as in pdh_contract_strided_ksplit. Only
+ * 4-byte alignment is needed. This replaces the operand layouts the
+ * reference's contraction template lowers to strided loads
+ * (fusion.py:159-324: its operands are any views of the lattice), which the
+ * other entry points take only as zero-padded k-contiguous copies. PDH_F32
+ * only: PDH_EUNSUPPORTED otherwise. */
+int pdh_contract_views(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, const void* bt, int64_t sb_b,
+                       int64_t sb_r, int64_t sb_k, int64_t batch, int64_t m, int64_t n, int64_t k, int64_t ksplit,
+                       const pdh_ew_program* epi, const void* const* operands, void* out, int dtype, void* stream);
+
 /* How PDH_F32 contractions run (pdh_contract, pdh_contract_strided): 6 (the
  * default) splits each operand into three bf16 terms and sums the six cross
  * products above 2^-24 of each product: fp32 grade; 3 keeps two terms and
@@ -376,7 +391,8 @@ int pdh_reduce_rows_ex(const pdh_ew_program* summand, int nk, const pdh_ew_progr
 int pdh_ew_set_jit(int enable);
 void pdh_ew_jit_stats(int64_t* stats3);
 /* The generated source of a program's specialized kernels (kind 0: map
- * chain, 1: contraction epilogue) for `dtype`, NUL-terminated into buf
+ * chain, 1: contraction epilogue; 2, 3, 4: the fp32 contraction with a, bt or
+ * both read rows-contiguous, as pdh_contract_views) for `dtype`, NUL-terminated into buf
  * (truncated to n); returns its full length (0 for a malformed program).
  * The readable counterpart of the reference runner's run.source. */
 size_t pdh_ew_jit_source(const pdh_ew_program* prog, int kind, int dtype, char* buf, size_t n);

@@ -35,16 +35,37 @@ __global__ __launch_bounds__(256) void contract_f32(ContractArgs a, pdh_ew_progr
   contract_f32_body<InterpEval>(a, p, ops);
 }
 
-template <int NSPLIT>
+template <int NSPLIT, int LAY>
 __global__ __launch_bounds__(256, 2) void contract_split(ContractArgs a, pdh_ew_program p, EwOperands ops) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[split_lds<64, NSPLIT>()];
-  contract_split_body<PDH_F32, 64, NSPLIT, InterpEval>(a, p, ops, smem);
+  contract_split_body<PDH_F32, 64, NSPLIT, LAY, InterpEval>(a, p, ops, smem);
 }
 
-template <int NSPLIT>
+template <int NSPLIT, int LAY>
 __global__ __launch_bounds__(256, 2) void contract_split_small(ContractArgs a, pdh_ew_program p, EwOperands ops) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[split_lds<32, NSPLIT>()];
-  contract_split_body<PDH_F32, 32, NSPLIT, InterpEval>(a, p, ops, smem);
+  contract_split_body<PDH_F32, 32, NSPLIT, LAY, InterpEval>(a, p, ops, smem);
+}
+
+// The interpreter's split kernel for (mode, operand layouts), by value.
+template <int NSPLIT>
+void launch_split(bool small, int lay, dim3 grid, hipStream_t st, const ContractArgs& ca, const pdh_ew_program& epi,
+                  const EwOperands& ops) {
+  auto go = [&](auto lay_c) {
+    constexpr int L = decltype(lay_c)::value;
+    if (small)
+      contract_split_small<NSPLIT, L><<<grid, 256, 0, st>>>(ca, epi, ops);
+    else
+      contract_split<NSPLIT, L><<<grid, 256, 0, st>>>(ca, epi, ops);
+  };
+  if (lay == 0)
+    go(std::integral_constant<int, 0>{});
+  else if (lay == 1)
+    go(std::integral_constant<int, 1>{});
+  else if (lay == 2)
+    go(std::integral_constant<int, 2>{});
+  else
+    go(std::integral_constant<int, 3>{});
 }
 
 template <int DT>
@@ -178,9 +199,9 @@ namespace {
 int g_cus = 0;  // compute units of the device, read once
 std::atomic<int> g_f32_mode{6};  // fp32 contractions: 6 bf16 products per term (fp32 grade) by default
 
-// Validation shared by both entry points, then the launch: the 128 x 128
+// Validation shared by the entry points, then the launch: the 128 x 128
 // tiles, or the 64 x 64 ones when the big tiles would not give every compute
-// unit a workgroup.
+// unit a workgroup or an output side is 64 or under.
 int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* const* operands, int64_t esize,
                     hipStream_t st, const char* fn) {
   int rc = check_program(epi, 3, true, fn);
@@ -196,12 +217,16 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
     if ((rc = check_view(epi, epi->in_stride[i], fn, "operand"))) return rc;
     ops.p[i] = operands[i];
   }
-  // every 32-bit buffer offset (rows up to m + 128, k up to kp) stays representable
-  PDH_REQUIRE((m + 128) * ca.sa_r * esize + ca.kp * esize <= static_cast<int64_t>(UINT32_MAX) &&
-                  (n + 128) * ca.sb_r * esize + ca.kp * esize <= static_cast<int64_t>(UINT32_MAX),
-              PDH_EINVAL, "%s: one batch slice of a / bt must stay under 4 GiB", fn);
+  // every 32-bit buffer offset (rows up to m + 128, k up to kp) stays under
+  // 2^31, the offset that masked loads take
+  PDH_REQUIRE((m + 128) * ca.sa_r * esize + ca.kp * ca.sa_k * esize < (int64_t{1} << 31) &&
+                  (n + 128) * ca.sb_r * esize + ca.kp * ca.sb_k * esize < (int64_t{1} << 31),
+              PDH_EINVAL, "%s: one k slice of a / bt must span under 2 GiB", fn);
   hipFunction_t fns[2];
-  const bool spec = jit_get(JitKind::Contract, *epi, ca.dtype, fns);
+  // operand layouts of the fp32 split kernels: bit 0 a, bit 1 bt rows-contiguous
+  const int lay = (ca.sa_k != 1 ? 1 : 0) | (ca.sb_k != 1 ? 2 : 0);
+  PDH_REQUIRE(lay == 0 || ca.dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: 16-bit operands must have k contiguous", fn);
+  const bool spec = jit_get(JitKind::Contract, *epi, ca.dtype, fns, lay);
   pdh_ew_program pe = *epi;
   void* args[] = {&ca, &pe, &ops};
   auto launch_spec = [&](hipFunction_t f, int64_t nblk) {
@@ -224,7 +249,7 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
   }
   if (g_cus == 0) g_cus = pdh_device_cus() > 0 ? pdh_device_cus() : 256;
   const int64_t big = batch * ((m + 127) / 128) * ((n + 127) / 128);
-  const bool small = big < g_cus;
+  const bool small = big < g_cus || m <= 64 || n <= 64;  // a side of 64 or under would leave big tiles half empty
   const int bm = small ? 64 : 128;
   ca.tiles_m = static_cast<int>((m + bm - 1) / bm);
   ca.tiles_n = static_cast<int>((n + bm - 1) / bm);
@@ -233,22 +258,12 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
   PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "%s: grid too large", fn);
   const dim3 grid(static_cast<unsigned>(nblk));
   if (ca.dtype == PDH_F32) {  // on the bf16 matrix cores, split into planes
-    if (f32_mode == 1) {
-      if (small)
-        contract_split_small<1><<<grid, 256, 0, st>>>(ca, *epi, ops);
-      else
-        contract_split<1><<<grid, 256, 0, st>>>(ca, *epi, ops);
-    } else if (f32_mode == 3) {
-      if (small)
-        contract_split_small<3><<<grid, 256, 0, st>>>(ca, *epi, ops);
-      else
-        contract_split<3><<<grid, 256, 0, st>>>(ca, *epi, ops);
-    } else {
-      if (small)
-        contract_split_small<6><<<grid, 256, 0, st>>>(ca, *epi, ops);
-      else
-        contract_split<6><<<grid, 256, 0, st>>>(ca, *epi, ops);
-    }
+    if (f32_mode == 1)
+      launch_split<1>(small, lay, grid, st, ca, *epi, ops);
+    else if (f32_mode == 3)
+      launch_split<3>(small, lay, grid, st, ca, *epi, ops);
+    else
+      launch_split<6>(small, lay, grid, st, ca, *epi, ops);
   } else if (ca.dtype == PDH_BF16) {
     if (small)
       contract_mfma_small<PDH_BF16><<<grid, 256, 0, st>>>(ca, *epi, ops);
@@ -287,7 +302,7 @@ extern "C" int pdh_contract(const void* a, const void* bt, int64_t batch, int64_
               "pdh_contract: output too large for one call");
   PDH_REQUIRE(aligned16(a) && aligned16(bt), PDH_EINVAL, "pdh_contract: a / bt must be 16-byte aligned");
   const ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n),
-                        static_cast<int>(k), static_cast<int>(kp), 0, 0, dtype, m * kp, kp, n * kp, kp, 1};
+                        static_cast<int>(k), static_cast<int>(kp), 0, 0, dtype, m * kp, kp, n * kp, kp, 1, 1, 1};
   return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), "pdh_contract");
 }
 
@@ -314,8 +329,8 @@ int contract_strided_impl(const void* a, int64_t sa_b, int64_t sa_r, const void*
   PDH_REQUIRE(aligned16(a) && aligned16(bt), PDH_EINVAL, "%s: a / bt must be 16-byte aligned", fn);
   const int64_t kc = k / ksplit;
   const ContractArgs ca{a, bt, out, static_cast<int>(batch * ksplit), static_cast<int>(m), static_cast<int>(n),
-                        static_cast<int>(kc), static_cast<int>(kc), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r,
-                        static_cast<int>(ksplit)};
+                        static_cast<int>(k), static_cast<int>(kc), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r,
+                        static_cast<int>(ksplit), 1, 1};
   return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), fn);
 }
 
@@ -335,6 +350,34 @@ extern "C" int pdh_contract_strided_ksplit(const void* a, int64_t sa_b, int64_t 
                                            void* out, int dtype, void* stream) {
   return contract_strided_impl(a, sa_b, sa_r, bt, sb_b, sb_r, batch, m, n, k, ksplit, epi, operands, out, dtype,
                                stream, "pdh_contract_strided_ksplit");
+}
+
+extern "C" int pdh_contract_views(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, const void* bt,
+                                  int64_t sb_b, int64_t sb_r, int64_t sb_k, int64_t batch, int64_t m, int64_t n,
+                                  int64_t k, int64_t ksplit, const pdh_ew_program* epi, const void* const* operands,
+                                  void* out, int dtype, void* stream) {
+  const char* fn = "pdh_contract_views";
+  PDH_REQUIRE(dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: fp32 operands only (16-bit ones: pdh_contract_strided)", fn);
+  PDH_REQUIRE(a && bt && out, PDH_EINVAL, "%s: null pointer", fn);
+  PDH_REQUIRE(batch >= 1 && m >= 1 && n >= 1 && k >= 1, PDH_EINVAL, "%s: need batch, m, n, k >= 1", fn);
+  PDH_REQUIRE(ksplit >= 1 && ksplit <= 64, PDH_EINVAL, "%s: ksplit = %lld must be in [1, 64]", fn,
+              (long long)ksplit);
+  // slices of whole 64-column tiles; the last one may be ragged, none is empty
+  const int64_t kc = ((k + kBK - 1) / kBK + ksplit - 1) / ksplit * kBK;
+  PDH_REQUIRE((ksplit - 1) * kc < k, PDH_EINVAL, "%s: ksplit = %lld leaves a k slice empty (k = %lld)", fn,
+              (long long)ksplit, (long long)k);
+  PDH_REQUIRE(batch * ksplit * m * n <= INT32_MAX && m <= INT32_MAX / 2 && n <= INT32_MAX / 2 && k <= INT32_MAX / 2,
+              PDH_EINVAL, "%s: output too large for one call", fn);
+  PDH_REQUIRE(sa_b >= 0 && sa_r >= 0 && sa_k >= 0 && sb_b >= 0 && sb_r >= 0 && sb_k >= 0, PDH_EINVAL,
+              "%s: negative stride", fn);
+  PDH_REQUIRE((sa_k == 1 || sa_r == 1) && (sb_k == 1 || sb_r == 1), PDH_EINVAL,
+              "%s: each operand needs k or its rows contiguous (a stride of 1)", fn);
+  PDH_REQUIRE((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(bt)) % 4 == 0, PDH_EINVAL,
+              "%s: a / bt must be 4-byte aligned", fn);
+  const ContractArgs ca{a, bt, out, static_cast<int>(batch * ksplit), static_cast<int>(m), static_cast<int>(n),
+                        static_cast<int>(k), static_cast<int>(kc), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r,
+                        static_cast<int>(ksplit), sa_k, sb_k};
+  return contract_launch(ca, epi, operands, 4, as_stream(stream), fn);
 }
 
 extern "C" int pdh_reduce_rows(const pdh_ew_program* summand, int nk, const pdh_ew_program* epi,

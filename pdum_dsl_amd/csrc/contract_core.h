@@ -33,22 +33,33 @@ struct ContractArgs {
   const void* a;
   const void* bt;
   void* out;
-  int batch, m, n, k, kp;  // kp: the k extent read (a multiple of 64; columns k..kp-1 read as zero)
+  // k: the k columns of a batch entry that hold data; kp: the columns one k
+  // slice reads (a multiple of 64). The fp32 bodies read columns at or past k
+  // as zero; the 16-bit body reads them, so its operands are zero-padded.
+  int batch, m, n, k, kp;
   int tiles_m, tiles_n;
   int dtype;
-  long long sa_b, sa_r, sb_b, sb_r;  // element strides of a and bt: per batch, per row (k is contiguous)
+  long long sa_b, sa_r, sb_b, sb_r;  // element strides of a and bt: per batch, per row
   // k slices per batch entry: batch index bb is (bb / ksplit, slice bb % ksplit),
   // and slice s reads k columns [s kp, (s + 1) kp) (1: no split)
   int ksplit;
+  // element strides along k: 1 (k contiguous), or, for the fp32 bodies only,
+  // any stride of an operand whose rows are contiguous (row stride 1)
+  long long sa_k, sb_k;
 };
 
 // Element offsets of batch index bb's a and bt rows (the batch entry's, moved
 // to its k slice).
 __device__ __forceinline__ long long contract_off_a(const ContractArgs& a, int bb) {
-  return static_cast<long long>(bb / a.ksplit) * a.sa_b + static_cast<long long>(bb % a.ksplit) * a.kp;
+  return static_cast<long long>(bb / a.ksplit) * a.sa_b + static_cast<long long>(bb % a.ksplit) * a.kp * a.sa_k;
 }
 __device__ __forceinline__ long long contract_off_b(const ContractArgs& a, int bb) {
-  return static_cast<long long>(bb / a.ksplit) * a.sb_b + static_cast<long long>(bb % a.ksplit) * a.kp;
+  return static_cast<long long>(bb / a.ksplit) * a.sb_b + static_cast<long long>(bb % a.ksplit) * a.kp * a.sb_k;
+}
+
+// Columns of batch index bb's k slice that hold data (kp or fewer; <= 0 past k).
+__device__ __forceinline__ int contract_kvalid(const ContractArgs& a, int bb) {
+  return a.k - (bb % a.ksplit) * a.kp;
 }
 
 constexpr int kBK = 64;
@@ -460,12 +471,22 @@ __device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_
   const float* abase = static_cast<const float*>(a.a) + contract_off_a(a, b);
   const float* bbase = static_cast<const float*>(a.bt) + contract_off_b(a, b);
   const int lr = tid >> 2, lc = (tid & 3) * 4;  // this lane's tile row and 4 k values per load
+  const int kin = contract_kvalid(a, b) < a.kp ? contract_kvalid(a, b) : a.kp;  // columns past it read as zero
   float acc[4][4] = {};
   for (int k0 = 0; k0 < a.kp; k0 += kFK) {
     const int am = m0 + lr, bn = n0 + lr;
     f32x4 av = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f};
-    if (am < a.m) av = *reinterpret_cast<const f32x4*>(abase + am * a.sa_r + k0 + lc);
-    if (bn < a.n) bv = *reinterpret_cast<const f32x4*>(bbase + bn * a.sb_r + k0 + lc);
+    if (a.sa_k == 1 && a.sb_k == 1 && k0 + kFK <= kin) {  // k contiguous, whole tile
+      if (am < a.m) av = *reinterpret_cast<const f32x4u*>(abase + am * a.sa_r + k0 + lc);
+      if (bn < a.n) bv = *reinterpret_cast<const f32x4u*>(bbase + bn * a.sb_r + k0 + lc);
+    } else {  // any strides, one element at a time
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const long long kk = k0 + lc + j;
+        if (am < a.m && kk < kin) av[j] = abase[am * a.sa_r + kk * a.sa_k];
+        if (bn < a.n && kk < kin) bv[j] = bbase[bn * a.sb_r + kk * a.sb_k];
+      }
+    }
     __syncthreads();  // the previous tile's reads are done
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -529,9 +550,21 @@ constexpr int split_lds() {
              : 4 * WM * (WM + 4) * 4;
 }
 
-// Slot s (0..3) of plane row r sits at s ^ swz_split(r): the b128 operand
-// reads of 16 consecutive rows at one slot then cover all 64 banks once.
+// Tile row r of a plane is stored as plane row r ^ swz_split(r) (a
+// permutation within each aligned group of 16 rows), its slot s (0..3) at
+// s ^ swz_split(r). The b128 operand reads of 16 consecutive rows at one slot
+// then cover all 64 banks once, and so do the 8-byte writes of both load
+// layouts: (rows 8 w .. 8 w + 7 (+ 32 c), all 8 chunks) for a k-contiguous
+// operand and (rows 4 q + c, q = 8 w .. 8 w + 7, all 8 chunks) for a
+// rows-contiguous one.
 __device__ __forceinline__ int swz_split(int r) { return (r >> 2) & 3; }
+template <bool B>
+struct BoolC {  // a compile-time flag passed to generic lambdas
+  static constexpr bool value = B;
+};
+__device__ __forceinline__ int split_off(int r, int ch) {  // byte offset of (row r, 8-byte chunk ch) in a plane
+  return (r ^ swz_split(r)) * kSRowB + (((ch >> 1) ^ swz_split(r)) << 4) + ((ch & 1) << 3);
+}
 
 typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
 typedef float f32x2_v __attribute__((ext_vector_type(2)));
@@ -572,7 +605,9 @@ __device__ __forceinline__ bool split4(u32x4 v, u32x2 (&out)[PL]) {
   return odd;
 }
 
-template <int DT, int WM, int NSPLIT, typename Eval>
+// LAY bit 0: a is rows-contiguous (k strided), bit 1: bt is; otherwise k is
+// contiguous. The host picks LAY from the strides (sa_k, sb_k != 1).
+template <int DT, int WM, int NSPLIT, int LAY, typename Eval>
 __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const pdh_ew_program& p,
                                                     const EwOperands& ops, unsigned char* smem) {
   constexpr int BM = 2 * WM, TI = WM / 32, PL = split_planes<NSPLIT>();
@@ -584,43 +619,103 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
   const int per = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x / per, rest = blockIdx.x % per;
   const int m0 = (rest / a.tiles_n) * BM, n0 = (rest % a.tiles_n) * BM;
-  const uint32_t rowa = static_cast<uint32_t>(a.sa_r) * 4u, rowbb = static_cast<uint32_t>(a.sb_r) * 4u;
   const float* abase = static_cast<const float*>(a.a) + contract_off_a(a, b);
   const float* bbase = static_cast<const float*>(a.bt) + contract_off_b(a, b);
-  // the buffers end after the batch slice's last row: rows past m (n) read as zero
-  const rsrc_t ar = make_rsrc(abase, (static_cast<uint32_t>(a.m) - 1u) * rowa + static_cast<uint32_t>(a.kp) * 4u);
-  const rsrc_t br = make_rsrc(bbase, (static_cast<uint32_t>(a.n) - 1u) * rowbb + static_cast<uint32_t>(a.kp) * 4u);
+  // Columns at or past kin read as zero, and so do rows past m (n): such
+  // loads take the lane offset kOOB, past every buffer's extent (the host
+  // keeps every in-bounds byte offset under 2^31), so the hardware returns
+  // zero without a memory access.
+  constexpr uint32_t kOOB = 0x80000000u;
+  constexpr bool mna = (LAY & 1) != 0, mnb = (LAY & 2) != 0;
+  int kin = contract_kvalid(a, b);
+  kin = kin < 0 ? 0 : (kin > a.kp ? a.kp : kin);
+  const uint32_t rowa = static_cast<uint32_t>(a.sa_r) * 4u, rowbb = static_cast<uint32_t>(a.sb_r) * 4u;
+  const uint32_t ka = static_cast<uint32_t>(a.sa_k) * 4u, kb = static_cast<uint32_t>(a.sb_k) * 4u;
+  auto extent = [&](bool mn, int rows, uint32_t rowb, uint32_t kbs) -> uint32_t {
+    if (kin == 0) return 0u;
+    return mn ? static_cast<uint32_t>(kin - 1) * kbs + static_cast<uint32_t>(rows) * 4u
+              : static_cast<uint32_t>(rows - 1) * rowb + static_cast<uint32_t>(kin) * 4u;
+  };
+  const rsrc_t ar = make_rsrc(abase, extent(mna, a.m, rowa, ka));
+  const rsrc_t br = make_rsrc(bbase, extent(mnb, a.n, rowbb, kb));
 
-  // loads: lane tid takes k values 4 (tid % 8) .. + 3 of rows tid / 8 + 32 c
-  const int lrow = tid >> 3, lchunk = tid & 7;
-  const uint32_t la = lrow * rowa + lchunk * 16u, lb = lrow * rowbb + lchunk * 16u;
-  // where those four k values land in a plane: slot lchunk / 2 (swizzled), half lchunk % 2
-  int wr[CH];
+  // A lane holds four consecutive k values (columns 4 ch .. 4 ch + 3 of the
+  // tile) of CH rows. k-contiguous: lane tid = 8 q + ch, rows q + 32 c, one
+  // 16-byte load each (8 lanes read a row's 128-byte line). Rows-contiguous:
+  // rows CH q + c, four loads of CH consecutive rows (one per column),
+  // re-paired in registers; with CH = 4, lane tid = 8 q + ch as before, with
+  // CH = 2, 16 lanes of a wave cover 32 rows (so every load instruction reads
+  // whole 128-byte lines): q = 16 (w % 2) + lane % 16, ch = 4 (w / 2) + lane / 16.
+  const int lq = tid >> 3, lch = tid & 7;
+  const int mq = CH == 4 ? lq : 16 * (w & 1) + (lane & 15), mch = CH == 4 ? lch : 4 * (w >> 1) + (lane >> 4);
+  int wra[CH], wrb[CH];  // where chunk c lands in a plane
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int row = lrow + 32 * c;
-    wr[c] = row * kSRowB + (((lchunk >> 1) ^ swz_split(row)) << 4) + ((lchunk & 1) << 3);
+    wra[c] = mna ? split_off(CH * mq + c, mch) : split_off(lq + 32 * c, lch);
+    wrb[c] = mnb ? split_off(CH * mq + c, mch) : split_off(lq + 32 * c, lch);
   }
   // operand reads: row 32 t + r32 (+ WM q) of a plane, slot 2 ks + g
   int rd[TI][2];
 #pragma unroll
   for (int t = 0; t < TI; ++t)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int row = 32 * t + r32;  // + WM q: a multiple of 32 rows, so the swizzle is unchanged
-      rd[t][ks] = row * kSRowB + (((2 * ks + g) ^ swz_split(row)) << 4);
+    for (int ks = 0; ks < 2; ++ks) {  // + WM q rows: a multiple of 32, which the permutation keeps
+      const int row = 32 * t + r32;
+      rd[t][ks] = (row ^ swz_split(row)) * kSRowB + (((2 * ks + g) ^ swz_split(row)) << 4);
     }
 
-  u32x4 va[CH], vb[CH];
-  auto fetch = [&](int kt) {
-    const uint32_t koff = static_cast<uint32_t>(kt) * kSBK * 4u;
+  typedef uint32_t u32xCH __attribute__((ext_vector_type(CH)));
+  auto fetch1 = [&](auto mn_c, auto edge_c, const rsrc_t& r, uint32_t rowb, uint32_t kbs, int r0, int rows, int kt,
+                    u32x4(&v)[CH]) {
+    constexpr bool MN = decltype(mn_c)::value, EDGE = decltype(edge_c)::value;
+    const int k0 = kt * kSBK;
+    if constexpr (!MN) {
+      const uint32_t vo = static_cast<uint32_t>(lq) * rowb + static_cast<uint32_t>(lch) * 16u;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      va[c] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, la, static_cast<uint32_t>(m0 + 32 * c) * rowa + koff, 0));
-      vb[c] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, lb, static_cast<uint32_t>(n0 + 32 * c) * rowbb + koff, 0));
+      for (int c = 0; c < CH; ++c) {
+        const bool rin = r0 + lq + 32 * c < rows;
+        const uint32_t so = static_cast<uint32_t>(r0 + 32 * c) * rowb + static_cast<uint32_t>(k0) * 4u;
+        if constexpr (!EDGE) {
+          v[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, rin ? vo : kOOB, so, 0));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            v[c][j] = __builtin_amdgcn_raw_buffer_load_b32(
+                r, (rin && k0 + 4 * lch + j < kin) ? vo + 4u * j : kOOB, so, 0);
+        }
+      }
+    } else {
+      const int rv = rows - (r0 + CH * mq);  // rows of this lane's group inside the operand
+      const uint32_t vo = static_cast<uint32_t>(CH * mq) * 4u + static_cast<uint32_t>(4 * mch) * kbs;
+      u32xCH ld[4];
+      if (rv >= CH) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t so = static_cast<uint32_t>(r0) * 4u + static_cast<uint32_t>(k0 + j) * kbs;
+          const bool ok = !EDGE || k0 + 4 * mch + j < kin;
+          if constexpr (CH == 4)
+            ld[j] = __builtin_bit_cast(u32xCH, __builtin_amdgcn_raw_buffer_load_b128(r, ok ? vo : kOOB, so, 0));
+          else
+            ld[j] = __builtin_bit_cast(u32xCH, __builtin_amdgcn_raw_buffer_load_b64(r, ok ? vo : kOOB, so, 0));
+        }
+      } else {  // the last rows of the operand: one element at a time
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t so = static_cast<uint32_t>(r0) * 4u + static_cast<uint32_t>(k0 + j) * kbs;
+          const bool ok = !EDGE || k0 + 4 * mch + j < kin;
+#pragma unroll
+          for (int i = 0; i < CH; ++i)
+            ld[j][i] = __builtin_amdgcn_raw_buffer_load_b32(r, (ok && i < rv) ? vo + 4u * i : kOOB, so, 0);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < CH; ++c) v[c] = u32x4{ld[0][c], ld[1][c], ld[2][c], ld[3][c]};
     }
+  };
+  u32x4 va[CH], vb[CH];
+  auto fetch = [&](int kt, auto edge_c) {
+    fetch1(BoolC<mna>{}, edge_c, ar, rowa, ka, m0, a.m, kt, va);
+    fetch1(BoolC<mnb>{}, edge_c, br, rowbb, kb, n0, a.n, kt, vb);
   };
 
   f32x16 acc[TI][TI];
@@ -629,9 +724,17 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
 #pragma unroll
     for (int j = 0; j < TI; ++j) acc[i][j] = f32x16{};
 
-  const int nkt = a.kp / kSBK;
+  // the k tiles that hold data; the last one masked per element when ragged
+  const int nkt = (kin + kSBK - 1) / kSBK;
+  const bool ragged = kin % kSBK != 0;
+  auto fetch_tile = [&](int kt) {
+    if (ragged && kt == nkt - 1)
+      fetch(kt, BoolC<true>{});
+    else
+      fetch(kt, BoolC<false>{});
+  };
   bool odd = false;  // a non-finite leading term (an inf, a NaN, |x| above the largest bf16) in this lane's loads
-  fetch(0);
+  if (nkt > 0) fetch_tile(0);
   for (int kt = 0; kt < nkt; ++kt) {
     __syncthreads();  // every wave is done reading the planes of tile kt - 1
 #pragma unroll
@@ -641,11 +744,11 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
       odd |= split4<PL>(vb[c], pb);
 #pragma unroll
       for (int pl = 0; pl < PL; ++pl) {
-        *reinterpret_cast<u32x2*>(smem + (2 * pl) * PLANEB + wr[c]) = pa[pl];
-        *reinterpret_cast<u32x2*>(smem + (2 * pl + 1) * PLANEB + wr[c]) = pb[pl];
+        *reinterpret_cast<u32x2*>(smem + (2 * pl) * PLANEB + wra[c]) = pa[pl];
+        *reinterpret_cast<u32x2*>(smem + (2 * pl + 1) * PLANEB + wrb[c]) = pb[pl];
       }
     }
-    if (kt + 1 < nkt) fetch(kt + 1);  // in flight under this tile's products
+    if (kt + 1 < nkt) fetch_tile(kt + 1);  // in flight under this tile's products
     __syncthreads();                  // the planes of tile kt are in LDS
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll

@@ -57,7 +57,7 @@ from .tl.fusion import contract_core, forest_is_closed, match_contraction_epilog
 from .tl.ir import Builder, Dim, Region, walk
 
 _TORCH_DT = {"f32": "float32", "bf16": "bfloat16", "f16": "float16"}
-_CUS = 256  # MI355X compute units: a contraction with fewer output tiles than this splits k
+_CUS = 256  # MI355X compute units
 
 
 def _torch():
@@ -97,6 +97,69 @@ def _strided_view(tt, riders, rows, kd):
     row = st[rows[-1]] if rows else 0
     batch = st[riders[0]] if riders else 0
     return (batch, row)
+
+
+def _big_tiles(Bs, M, N):
+    """The launcher's tile choice (contract_launch in contract.hip): 128 x 128
+    workgroup tiles when they give every compute unit one and neither output
+    side is 64 or under; 64 x 64 otherwise."""
+    return Bs * -(-M // 128) * -(-N // 128) >= _CUS and M > 64 and N > 64
+
+
+# Microseconds per 64-column k tile of one workgroup of the fp32 split kernel
+# on MI355X, by workgroups resident on a compute unit: 64 x 64 tiles (up to
+# five resident), 128 x 128 tiles (two; one alone runs a little faster).
+_SMALL_STEP = {1: 1.7, 2: 2.0, 3: 2.7, 4: 3.4, 5: 4.2}
+_BIG_STEP2, _BIG_STEP1 = 5.0, 4.0
+
+
+def _ksplit_est(B, M, N, kt, S):
+    """Estimated microseconds of an fp32 contraction of B (M x N) outputs over
+    kt 64-column k tiles run as S k slices: the busiest compute unit's tiles at
+    the measured per-tile rates, plus a fixed 4 us, plus the pass that adds
+    the S partial planes (S + 1 planes of HBM traffic at 5 TB/s)."""
+    kc = -(-kt // S)
+    if _big_tiles(B * S, M, N):
+        per = -(-(B * S * -(-M // 128) * -(-N // 128)) // _CUS)
+        t = (per // 2) * kc * _BIG_STEP2 + (per % 2) * kc * _BIG_STEP1
+    else:
+        per = -(-(B * S * -(-M // 64) * -(-N // 64)) // _CUS)
+        t = (per // 5) * kc * _SMALL_STEP[5] + (kc * _SMALL_STEP[per % 5] if per % 5 else 0.0)
+    fin = (S + 1) * B * M * N * 4 / 5e6 if S > 1 else 0.0
+    return 4.0 + t + fin
+
+
+def _ksplit_order(B, M, N, kt):
+    """k slice counts (1..16, none empty, each of at least two k tiles) for
+    an fp32 contraction, cheapest first under :func:`_ksplit_est`, a model
+    fitted to measured times of the gpt2 gradient's contractions on MI355X."""
+    cands = [S for S in range(1, 17) if (S - 1) * -(-kt // S) < kt and (S == 1 or -(-kt // S) >= 2)]
+    return sorted(cands, key=lambda S: (_ksplit_est(B, M, N, kt, S), S))
+
+
+def _view3(tt, riders, rows, kd):
+    """(batch, row, k) element strides under which a dense value of type
+    ``tt`` reads as [batch][rows][k] in place, or None: its dims must be
+    exactly riders + rows + kd, in any order, with the row dims composing into
+    one stride and the k dims into another, and one of those two strides 1
+    (k contiguous, or the rows: a transposed tensor). The fp32 contraction
+    reads such operands directly (pdh_contract_views)."""
+    names = tt.names
+    if set(names) != set(riders) | set(rows) | set(kd) or len(names) != len(riders) + len(rows) + len(kd):
+        return None
+    st = _strides_by_name(names, tt.shape)
+
+    def one(group):
+        for a, b in zip(group[:-1], group[1:]):
+            if st[a] != st[b] * tt.dim(b).size:
+                return None
+        return st[group[-1]]
+
+    row = one(rows) if rows else 1  # a single row: any stride reads it
+    kst = one(kd)
+    if row is None or kst is None or (row != 1 and kst != 1):
+        return None
+    return (st[riders[0]] if riders else 0, row, kst)
 
 
 def _yielding(k: Region, node) -> Region:
@@ -765,15 +828,19 @@ class PlanExecutor:
             if len(lat) > L.EW_MAX_DIMS:
                 raise Untranslatable(f"an operand pack over {len(lat)} dims (max {L.EW_MAX_DIMS})")
             base = _base(core)
-            st = _strided_view(core.type, riders, [nm for nm in rows_names if not nm.startswith("_unit")], kd)
-            if base.op == "core.param" and st is not None and Kx == KP:
+            real_rows = [nm for nm in rows_names if not nm.startswith("_unit")]
+            if views:  # fp32: any dense view with k or its rows contiguous, read in place
+                st = _view3(core.type, riders, real_rows, kd)
+            else:
+                st = _strided_view(core.type, riders, real_rows, kd) if Kx == KP else None
+            if base.op == "core.param" and st is not None:
                 return _Pack(direct=self._index(k, base), strides=st)
             pre = None
             if any(n.op == "tl.reduce" for n in walk(_yielding(k, core))):
                 # carves dissolved into this operand (the traffic gate's
                 # re-derivation per tile): materialized once, by their own plan
                 pre = self._materialize(k, core)
-                if st is not None and Kx == KP:
+                if st is not None:
                     return _Pack(direct=None, pre=pre, pre_direct=True, strides=st)
             rs = KP * math.prod(size[nm].size for nm in rows_names)
             out_st = [rs if riders else 0]
@@ -790,8 +857,10 @@ class PlanExecutor:
             out_st += kst
             low, prog = self._map_prog(k, core, lat, out_st, extra_leaves=(core,) if pre is not None else ())
             slots = tuple(None if (pre is not None and b is core) else self._index(k, b) for b in low.bases)
-            return _Pack(None, prog, slots, (B, nrows, KP), KP != Kx, pre, strides=(nrows * KP, KP))
+            return _Pack(None, prog, slots, (B, nrows, KP), KP != Kx, pre,
+                         strides=(nrows * KP, KP, 1) if views else (nrows * KP, KP))
 
+        views = self.dtype == "f32"  # pdh_contract_views: operands in place, any k
         pa, pb = pack(ca, mdims, M), pack(cb, ndims, N)
         y = k.body[-1].args[0] if yroot is None else yroot
         if y.type.names and set(y.type.names) != set(out_names):
@@ -814,17 +883,19 @@ class PlanExecutor:
         eslots = tuple(self._index(k, b) for b in epi.bases)
         shape = y.type.shape
         tdt = _TORCH_DT[self.dtype]
-        # Split k: an fp32 contraction whose output tiles cannot fill the chip
-        # runs S slices of each batch entry's k as S workgroups per tile
-        # (pdh_contract_strided_ksplit: partial sums into an fp32 workspace
+        # Split k: an fp32 contraction whose output tiles would leave compute
+        # units idle or lightly loaded runs S slices of each batch entry's k
+        # (whole 64-column tiles, the last ragged) as S workgroups per tile
+        # (pdh_contract_views: partial sums into an fp32 workspace
         # [B][S][M][N]), and a map chain adds the slices in order and applies
-        # the epilogue. S divides the k tiles, so every slice is a whole number of them.
+        # the epilogue; S is the cheapest under the cost model whose sum fits
+        # one map-chain program.
         S, fin, ident = 1, None, None
-        tiles = B * -(-M // 64) * -(-N // 64)
-        if self.dtype == "f32" and B * -(-M // 128) * -(-N // 128) < _CUS and KP // 64 >= 8:
-            cands = [d for d in range(2, 9) if (KP // 64) % d == 0 and KP // 64 // d >= 2]
-            pick = next((d for d in cands if tiles * d >= 2 * _CUS), cands[-1] if cands else 1)
-            fin = ewprog.splitk_sum(prog, pick, (pick * M * N, N, 1)) if pick > 1 else None
+        if views and KP // 64 >= 4:
+            for pick in _ksplit_order(B, M, N, KP // 64):
+                fin = ewprog.splitk_sum(prog, pick, (pick * M * N, N, 1)) if pick > 1 else None
+                if pick == 1 or fin is not None:
+                    break
             if fin is not None:
                 S = pick
                 ident = L.EwProgram()
@@ -862,12 +933,15 @@ class PlanExecutor:
             out = torch.empty(shape, device="cuda", dtype=dt)
             if S > 1:  # k in S slices: partial sums, then their total through the epilogue
                 ws = torch.empty((B * S, M, N), device="cuda", dtype=torch.float32)
-                K.contract_strided(a, pa.strides, bt, pb.strides, (B, M, N, KP), ident, [], ws,
-                                   f32_mode=self.f32_contract, ksplit=S)
+                K.contract_views(a, pa.strides, bt, pb.strides, (B, M, N, Kx), ident, [], ws,
+                                 f32_mode=self.f32_contract, ksplit=S)
                 flat = ws.reshape(-1)
                 K.map_chain(fin, [flat[s_ * M * N:] for s_ in range(S)] + [vals[i] for i in eslots], out)
                 return out
-            if KP == Kx:  # every operand as stored (or as packed), through its strides
+            if views:
+                K.contract_views(a, pa.strides, bt, pb.strides, (B, M, N, Kx), prog, [vals[i] for i in eslots], out,
+                                 f32_mode=self.f32_contract)
+            elif KP == Kx:  # every operand as stored (or as packed), through its strides
                 K.contract_strided(a, pa.strides, bt, pb.strides, (B, M, N, Kx), prog,
                                    [vals[i] for i in eslots], out, f32_mode=self.f32_contract)
             else:  # zero-padded packs
@@ -875,8 +949,9 @@ class PlanExecutor:
             return out
 
         def how(p):
-            return "direct" if p.direct is not None else ("plan" if p.pre_direct else
-                                                          ("plan+pack" if p.pre else "pack"))
+            t = "^t" if len(p.strides) == 3 and p.strides[2] != 1 else ""  # read rows-contiguous (transposed)
+            return ("direct" + t) if p.direct is not None else (("plan" + t) if p.pre_direct else
+                                                                ("plan+pack" if p.pre else "pack"))
 
         src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
         if S > 1:

@@ -506,6 +506,35 @@ def contract_strided(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, s
     return out
 
 
+def contract_views(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, shape, epi: _lib.EwProgram,
+                   operands: list, out: torch.Tensor, f32_mode: str | None = None, ksplit: int = 1) -> torch.Tensor:
+    """The fp32 contraction over operands read in place (pdh_contract_views):
+    acc[b, m, n] = sum_k a[b, m, k] bt[b, n, k], a[b, m, k] at element
+    b sa_b + m sa_r + k sa_k of ``a`` (``a_strides`` = (sa_b, sa_r, sa_k)),
+    each operand with k or its rows contiguous; k (``shape`` = (batch, m, n,
+    k)) is any size. With ``ksplit`` > 1 the epilogue's lattice is
+    (batch * ksplit, m, n), as for :func:`contract_strided`."""
+    _require_cuda(a, bt, out, *operands)
+    B, M, N, Kd = (int(x) for x in shape)
+    if a.dtype != torch.float32 or bt.dtype != torch.float32 or out.dtype != torch.float32:
+        raise ValueError("contract_views takes fp32 a / bt / out")
+    for t, (sb, sr, sk), rows in ((a, a_strides, M), (bt, bt_strides, N)):
+        if min(sb, sr, sk) < 0 or (sk != 1 and sr != 1):
+            raise ValueError("each operand needs k or its rows contiguous, with non-negative strides")
+        reach = t.storage_offset() + (B - 1) * sb + (rows - 1) * sr + (Kd - 1) * sk + 1
+        if reach > t.untyped_storage().nbytes() // t.element_size():
+            raise ValueError("a strided operand's view reaches past its storage")
+    if tuple(epi.shape[d] for d in range(3)) != (B * ksplit, M, N) or epi.ndim != 3:
+        raise ValueError("the epilogue's lattice must be (batch * ksplit, m, n)")
+    _check_views(epi, operands, out, 3)
+    table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
+    sa, sb_ = [int(x) for x in a_strides], [int(x) for x in bt_strides]
+    _with_f32_mode(f32_mode, a.dtype, lambda: _lib.call(
+        "pdh_contract_views", _ptr(a), *sa, _ptr(bt), *sb_, B, M, N, Kd, int(ksplit), C.byref(epi), table,
+        _ptr(out), _DT[a.dtype], C.c_void_p(_stream())))
+    return out
+
+
 _REDUCERS = {"sum": 0, "max": 1, "min": 2}
 
 

@@ -55,6 +55,16 @@ def test_validation_errors_need_no_device():
     p = _lib.EwProgram()
     rc = lib.pdh_reduce_rows_ex(C.byref(p), 1, C.byref(p), None, 0, None, 0, 3, None)
     assert rc == _lib.PDH_EINVAL and "reducer 3" in _lib.last_error()
+    # in-place contraction views: fp32 only, one unit stride per operand, no empty k slice
+    fake = C.c_void_p(256)  # never dereferenced: every call below is refused first
+
+    def views(sa, sb, k=1000, ksplit=1, dt=_lib.PDH_F32):
+        return lib.pdh_contract_views(fake, *sa, fake, *sb, 1, 100, 100, k, ksplit, C.byref(p), None, fake, dt, None)
+
+    assert views((0, 1000, 1), (0, 1000, 1), dt=_lib.PDH_BF16) == _lib.PDH_EUNSUPPORTED
+    assert views((0, 1000, 2), (0, 1000, 1)) == _lib.PDH_EINVAL and "contiguous" in _lib.last_error()
+    assert views((0, 1, 100), (0, 1000, 1), ksplit=5) == _lib.PDH_EINVAL and "slice empty" in _lib.last_error()
+    assert views((0, 1, 100), (0, -1, 1)) == _lib.PDH_EINVAL and "negative" in _lib.last_error()
 
 
 def test_the_forward_split_picker():

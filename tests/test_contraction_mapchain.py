@@ -337,13 +337,19 @@ def test_fp32_contractions_compile_in_every_mode():
         assert prev == 6  # the default: fp32 grade
         assert lib.pdh_contract_set_f32_mode(7) == L.PDH_EINVAL and "mode 7" in L.last_error()
         buf = C.create_string_buffer(1 << 16)
-        for mode, body in ((6, "contract_split_body<PDH_F32, 64, 6, pdh::GenEval>"),
-                           (3, "contract_split_body<PDH_F32, 32, 3, pdh::GenEval>"),
+        for mode, body in ((6, "contract_split_body<PDH_F32, 64, 6, 0, pdh::GenEval>"),
+                           (3, "contract_split_body<PDH_F32, 32, 3, 0, pdh::GenEval>"),
                            (0, "contract_f32_body<pdh::GenEval>")):
             lib.pdh_contract_set_f32_mode(mode)
             assert lib.pdh_ew_jit_compile(C.byref(epi), 1, L.PDH_F32) == 0, L.last_error()
             lib.pdh_ew_jit_source(C.byref(epi), 1, L.PDH_F32, buf, len(buf))
             assert body in buf.value.decode()
+        # the rows-contiguous operand layouts of pdh_contract_views (kinds 2..4: a, bt, both)
+        lib.pdh_contract_set_f32_mode(6)
+        for kind in (2, 3, 4):
+            assert lib.pdh_ew_jit_compile(C.byref(epi), kind, L.PDH_F32) == 0, L.last_error()
+            lib.pdh_ew_jit_source(C.byref(epi), kind, L.PDH_F32, buf, len(buf))
+            assert f"contract_split_body<PDH_F32, 64, 6, {kind - 1}, pdh::GenEval>" in buf.value.decode()
     finally:
         lib.pdh_contract_set_f32_mode(prev)
 
