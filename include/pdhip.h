@@ -346,6 +346,22 @@ int pdh_contract_views(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, 
                        int64_t sb_r, int64_t sb_k, int64_t batch, int64_t m, int64_t n, int64_t k, int64_t ksplit,
                        const pdh_ew_program* epi, const void* const* operands, void* out, int dtype, void* stream);
 
+/* pdh_contract_views (no k split) whose epilogue values are not stored but
+ * reduced along each output row in runs of 32 columns: partials[b, r, j] =
+ * R over columns 32 j .. 32 j + 31 (those under n) of epi(acc)[b, r, col],
+ * R = sum / max / min (reducer 0 / 1 / 2; max and min propagate NaN), fp32
+ * [batch][m][ceil(n / 32)] dense. The caller finishes the rows with
+ * pdh_reduce_rows_ex over the partials. This is the device form of a
+ * contraction-epilogue group whose result feeds a row reduction (the
+ * softmax's max and denominator over the scores a @ bt^T): the reference
+ * runs that chain as two templates with the scores in between
+ * (fusion.py:159-324, then :371-443); here the scores never reach HBM.
+ * PDH_F32 only. */
+int pdh_contract_views_rowred(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, const void* bt, int64_t sb_b,
+                              int64_t sb_r, int64_t sb_k, int64_t batch, int64_t m, int64_t n, int64_t k,
+                              const pdh_ew_program* epi, const void* const* operands, int reducer, float* partials,
+                              int dtype, void* stream);
+
 /* How PDH_F32 contractions run (pdh_contract, pdh_contract_strided): 6 (the
  * default) splits each operand into three bf16 terms and sums the six cross
  * products above 2^-24 of each product: fp32 grade; 3 keeps two terms and
@@ -392,7 +408,8 @@ int pdh_ew_set_jit(int enable);
 void pdh_ew_jit_stats(int64_t* stats3);
 /* The generated source of a program's specialized kernels (kind 0: map
  * chain, 1: contraction epilogue; 2, 3, 4: the fp32 contraction with a, bt or
- * both read rows-contiguous, as pdh_contract_views) for `dtype`, NUL-terminated into buf
+ * both read rows-contiguous, as pdh_contract_views; 5, 6, 7: its row
+ * partials by sum, max, min, as pdh_contract_views_rowred) for `dtype`, NUL-terminated into buf
  * (truncated to n); returns its full length (0 for a malformed program).
  * The readable counterpart of the reference runner's run.source. */
 size_t pdh_ew_jit_source(const pdh_ew_program* prog, int kind, int dtype, char* buf, size_t n);

@@ -201,7 +201,7 @@ std::atomic<int> g_f32_mode{6};  // fp32 contractions: 6 bf16 products per term 
 
 // Validation shared by the entry points, then the launch: the 128 x 128
 // tiles, or the 64 x 64 ones when the big tiles would not give every compute
-// unit a workgroup or an output side is 64 or under.
+// unit a workgroup, an output side is 64 or under, or k is 128 or under.
 int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* const* operands, int64_t esize,
                     hipStream_t st, const char* fn) {
   int rc = check_program(epi, 3, true, fn);
@@ -226,7 +226,8 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
   // operand layouts of the fp32 split kernels: bit 0 a, bit 1 bt rows-contiguous
   const int lay = (ca.sa_k != 1 ? 1 : 0) | (ca.sb_k != 1 ? 2 : 0);
   PDH_REQUIRE(lay == 0 || ca.dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: 16-bit operands must have k contiguous", fn);
-  const bool spec = jit_get(JitKind::Contract, *epi, ca.dtype, fns, lay);
+  PDH_REQUIRE(ca.rowred < 0 || ca.dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: row partials of fp32 contractions only", fn);
+  const bool spec = jit_get(JitKind::Contract, *epi, ca.dtype, fns, lay, ca.rowred);
   pdh_ew_program pe = *epi;
   void* args[] = {&ca, &pe, &ops};
   auto launch_spec = [&](hipFunction_t f, int64_t nblk) {
@@ -249,7 +250,10 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
   }
   if (g_cus == 0) g_cus = pdh_device_cus() > 0 ? pdh_device_cus() : 256;
   const int64_t big = batch * ((m + 127) / 128) * ((n + 127) / 128);
-  const bool small = big < g_cus || m <= 64 || n <= 64;  // a side of 64 or under would leave big tiles half empty
+  // a side of 64 or under would leave big tiles half empty; a k of two tiles
+  // or fewer leaves each workgroup too little work to hide its load latency,
+  // which the small variant's higher occupancy does
+  const bool small = big < g_cus || m <= 64 || n <= 64 || ca.kp <= 2 * kBK;
   const int bm = small ? 64 : 128;
   ca.tiles_m = static_cast<int>((m + bm - 1) / bm);
   ca.tiles_n = static_cast<int>((n + bm - 1) / bm);
@@ -302,7 +306,7 @@ extern "C" int pdh_contract(const void* a, const void* bt, int64_t batch, int64_
               "pdh_contract: output too large for one call");
   PDH_REQUIRE(aligned16(a) && aligned16(bt), PDH_EINVAL, "pdh_contract: a / bt must be 16-byte aligned");
   const ContractArgs ca{a, bt, out, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n),
-                        static_cast<int>(k), static_cast<int>(kp), 0, 0, dtype, m * kp, kp, n * kp, kp, 1, 1, 1};
+                        static_cast<int>(k), static_cast<int>(kp), 0, 0, dtype, m * kp, kp, n * kp, kp, 1, 1, 1, -1};
   return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), "pdh_contract");
 }
 
@@ -330,7 +334,7 @@ int contract_strided_impl(const void* a, int64_t sa_b, int64_t sa_r, const void*
   const int64_t kc = k / ksplit;
   const ContractArgs ca{a, bt, out, static_cast<int>(batch * ksplit), static_cast<int>(m), static_cast<int>(n),
                         static_cast<int>(k), static_cast<int>(kc), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r,
-                        static_cast<int>(ksplit), 1, 1};
+                        static_cast<int>(ksplit), 1, 1, -1};
   return contract_launch(ca, epi, operands, dtype == PDH_F32 ? 4 : 2, as_stream(stream), fn);
 }
 
@@ -376,7 +380,32 @@ extern "C" int pdh_contract_views(const void* a, int64_t sa_b, int64_t sa_r, int
               "%s: a / bt must be 4-byte aligned", fn);
   const ContractArgs ca{a, bt, out, static_cast<int>(batch * ksplit), static_cast<int>(m), static_cast<int>(n),
                         static_cast<int>(k), static_cast<int>(kc), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r,
-                        static_cast<int>(ksplit), sa_k, sb_k};
+                        static_cast<int>(ksplit), sa_k, sb_k, -1};
+  return contract_launch(ca, epi, operands, 4, as_stream(stream), fn);
+}
+
+extern "C" int pdh_contract_views_rowred(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, const void* bt,
+                                         int64_t sb_b, int64_t sb_r, int64_t sb_k, int64_t batch, int64_t m, int64_t n,
+                                         int64_t k, const pdh_ew_program* epi, const void* const* operands,
+                                         int reducer, float* partials, int dtype, void* stream) {
+  const char* fn = "pdh_contract_views_rowred";
+  PDH_REQUIRE(dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: fp32 operands only", fn);
+  PDH_REQUIRE(reducer >= 0 && reducer <= 2, PDH_EINVAL, "%s: reducer %d (0 sum, 1 max, 2 min)", fn, reducer);
+  PDH_REQUIRE(a && bt && partials, PDH_EINVAL, "%s: null pointer", fn);
+  PDH_REQUIRE(batch >= 1 && m >= 1 && n >= 1 && k >= 1, PDH_EINVAL, "%s: need batch, m, n, k >= 1", fn);
+  PDH_REQUIRE(batch * m * ((n + 31) / 32) <= INT32_MAX && batch * m * n <= (int64_t{1} << 40) && m <= INT32_MAX / 2 &&
+                  n <= INT32_MAX / 2 && k <= INT32_MAX / 2,
+              PDH_EINVAL, "%s: too large for one call", fn);
+  PDH_REQUIRE(sa_b >= 0 && sa_r >= 0 && sa_k >= 0 && sb_b >= 0 && sb_r >= 0 && sb_k >= 0, PDH_EINVAL,
+              "%s: negative stride", fn);
+  PDH_REQUIRE((sa_k == 1 || sa_r == 1) && (sb_k == 1 || sb_r == 1), PDH_EINVAL,
+              "%s: each operand needs k or its rows contiguous (a stride of 1)", fn);
+  PDH_REQUIRE((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(bt)) % 4 == 0, PDH_EINVAL,
+              "%s: a / bt must be 4-byte aligned", fn);
+  const int64_t kc = (k + kBK - 1) / kBK * kBK;
+  const ContractArgs ca{a, bt, partials, static_cast<int>(batch), static_cast<int>(m), static_cast<int>(n),
+                        static_cast<int>(k), static_cast<int>(kc), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r,
+                        1, sa_k, sb_k, reducer};
   return contract_launch(ca, epi, operands, 4, as_stream(stream), fn);
 }
 

@@ -46,6 +46,10 @@ struct ContractArgs {
   // element strides along k: 1 (k contiguous), or, for the fp32 bodies only,
   // any stride of an operand whose rows are contiguous (row stride 1)
   long long sa_k, sb_k;
+  // -1: out receives the epilogue's values. 0 / 1 / 2 (fp32 bodies only): out
+  // receives their sum / max / min over each run of 32 output columns, fp32
+  // [batch][m][ceil(n / 32)] (row partials; columns past n take no part)
+  int rowred;
 };
 
 // Element offsets of batch index bb's a and bt rows (the batch entry's, moved
@@ -335,13 +339,74 @@ __device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const
   }
 }
 
+// Row partials. RED is the reduction (0 sum, 1 max, 2 min, as reduce_rows:
+// NaN-propagating), or kRedRuntime to read it from the arguments (the
+// interpreter kernels serve both stores).
+constexpr int kRedRuntime = 3;
+
+template <int RED>
+__device__ __forceinline__ int red_kind(const ContractArgs& a) {
+  return RED == kRedRuntime ? a.rowred : RED;
+}
+
+__device__ __forceinline__ float red_identity(int r) {
+  return r == 0 ? 0.f : (r == 1 ? -__builtin_inff() : __builtin_inff());
+}
+
+__device__ __forceinline__ float red_combine(int r, float x, float y) {
+  return r == 0 ? x + y : (r == 1 ? nan_max(x, y) : nan_min(x, y));
+}
+
+// The reduction r of the epilogue's values at columns col0 .. col0 + 3 of one
+// row; the identity for a row past m and for columns past n (whose operands
+// are never read).
+template <int DT, typename Eval>
+__device__ __forceinline__ float epilogue_reduced4(const pdh_ew_program& p, const EwOperands& ops,
+                                                   const ContractArgs& a, int r, int b, int row, int col0,
+                                                   const float (&acc)[4]) {
+  float v = red_identity(r);
+  if (row >= a.m) return v;
+  if (col0 + 4 <= a.n) {
+    const int c0[PDH_EW_MAX_DIMS] = {b, row, col0, 0};
+    float res[4];
+    Eval::template run<4>(p, ops, DT, c0, acc, res, 1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v = red_combine(r, v, res[e]);
+    return v;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (col0 + e >= a.n) break;
+    const int c1[PDH_EW_MAX_DIMS] = {b, row, col0 + e, 0};
+    const float a1[1] = {acc[e]};
+    float r1[1];
+    Eval::template run<1>(p, ops, DT, c1, a1, r1, 1);
+    v = red_combine(r, v, r1[0]);
+  }
+  return v;
+}
+
+// Eight consecutive lanes that hold 32 consecutive columns of one row
+// (columns col0.., col0 of the first a multiple of 32) combine their values by
+// a fixed butterfly, and the first writes the run's partial. Every lane of
+// the wave calls this (cross-lane moves).
+__device__ __forceinline__ void store_row_partial(const ContractArgs& a, int r, int b, int row, int col0, float v) {
+  v = red_combine(r, v, __shfl_xor(v, 1, 64));
+  v = red_combine(r, v, __shfl_xor(v, 2, 64));
+  v = red_combine(r, v, __shfl_xor(v, 4, 64));
+  if ((threadIdx.x & 7) == 0 && row < a.m && col0 < a.n) {
+    const long long nblk = (a.n + 31) / 32;
+    static_cast<float*>(a.out)[(static_cast<long long>(b) * a.m + row) * nblk + col0 / 32] = v;
+  }
+}
+
 // The epilogue of a WM x WM-per-wave workgroup tile: the accumulators go
 // through LDS (each wave its own WM x WM block, rows padded by 4 floats) and
 // come back four consecutive columns per lane, so one runtime loop holds one
 // copy of the program's code. Accumulator v of tile (i, j) is row
 // 32 i + 8 (v / 4) + 4 g + v % 4, column 32 j + r32 of the wave's block. The
 // caller has passed a barrier after its last read of the operand tiles.
-template <int DT, int WM, typename Eval>
+template <int DT, int WM, typename Eval, int RED = -1>
 __device__ __forceinline__ void contract_store(const ContractArgs& a, const pdh_ew_program& p, const EwOperands& ops,
                                                unsigned char* smem, const f32x16 (&acc)[WM / 32][WM / 32], int b,
                                                int m0, int n0) {
@@ -361,7 +426,14 @@ __device__ __forceinline__ void contract_store(const ContractArgs& a, const pdh_
     const int row = idx / WM, col = idx % WM;
     const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * ACCP + col);
     const float av[4] = {av4[0], av4[1], av4[2], av4[3]};
-    contract_epilogue<DT, 4, Eval>(p, ops, a, b, m0 + WM * wy + row, n0 + WM * wx + col, av);
+    // row partials: lanes 8 q .. 8 q + 7 hold 32 consecutive columns of one row
+    const int r = RED < 0 ? -1 : red_kind<RED>(a);
+    if (r >= 0) {
+      const int grow = m0 + WM * wy + row, gcol = n0 + WM * wx + col;
+      store_row_partial(a, r, b, grow, gcol, epilogue_reduced4<DT, Eval>(p, ops, a, r, b, grow, gcol, av));
+    } else {
+      contract_epilogue<DT, 4, Eval>(p, ops, a, b, m0 + WM * wy + row, n0 + WM * wx + col, av);
+    }
   }
 }
 
@@ -464,7 +536,7 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
 // 4 x 4 outputs per lane, k tiles of 16 staged k-major through LDS (as, bs:
 // kFK x (kFT + 4) floats each), and the epilogue applied. Every lane of the
 // workgroup takes part (barriers inside).
-template <typename Eval>
+template <typename Eval, int RED = -1>
 __device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_ew_program& p, const EwOperands& ops,
                                                int b, int m0, int n0, float (*as)[kFT + 4], float (*bs)[kFT + 4]) {
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -505,21 +577,26 @@ __device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_
     }
   }
   __syncthreads();  // as / bs may be reused by the caller
+  const int r = RED < 0 ? -1 : red_kind<RED>(a);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float av[4] = {acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
-    contract_epilogue<PDH_F32, 4, Eval>(p, ops, a, b, m0 + 4 * ty + i, n0 + 4 * tx, av);
+    if (r >= 0)  // lanes 16 ty + 8 h .. + 7 hold columns 32 h .. 32 h + 31 of row 4 ty + i
+      store_row_partial(a, r, b, m0 + 4 * ty + i, n0 + 4 * tx,
+                        epilogue_reduced4<PDH_F32, Eval>(p, ops, a, r, b, m0 + 4 * ty + i, n0 + 4 * tx, av));
+    else
+      contract_epilogue<PDH_F32, 4, Eval>(p, ops, a, b, m0 + 4 * ty + i, n0 + 4 * tx, av);
   }
 }
 
-template <typename Eval>
+template <typename Eval, int RED = kRedRuntime>
 __device__ __forceinline__ void contract_f32_body(const ContractArgs& a, const pdh_ew_program& p,
                                                   const EwOperands& ops) {
   __shared__ float as[kFK][kFT + 4];  // k-major copies of the two 64-row tiles
   __shared__ float bs[kFK][kFT + 4];
   const int per = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x / per, rest = blockIdx.x % per;
-  f32_valu_block<Eval>(a, p, ops, b, (rest / a.tiles_n) * kFT, (rest % a.tiles_n) * kFT, as, bs);
+  f32_valu_block<Eval, RED>(a, p, ops, b, (rest / a.tiles_n) * kFT, (rest % a.tiles_n) * kFT, as, bs);
 }
 
 // ------------------------------------------- fp32 on the bf16 matrix cores
@@ -607,7 +684,7 @@ __device__ __forceinline__ bool split4(u32x4 v, u32x2 (&out)[PL]) {
 
 // LAY bit 0: a is rows-contiguous (k strided), bit 1: bt is; otherwise k is
 // contiguous. The host picks LAY from the strides (sa_k, sb_k != 1).
-template <int DT, int WM, int NSPLIT, int LAY, typename Eval>
+template <int DT, int WM, int NSPLIT, int LAY, typename Eval, int RED = kRedRuntime>
 __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const pdh_ew_program& p,
                                                     const EwOperands& ops, unsigned char* smem) {
   constexpr int BM = 2 * WM, TI = WM / 32, PL = split_planes<NSPLIT>();
@@ -790,10 +867,10 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
     float(*bs)[kFT + 4] = reinterpret_cast<float(*)[kFT + 4]>(smem + kFK * (kFT + 4) * 4);
 #pragma unroll 1
     for (int ij = 0; ij < (BM / kFT) * (BM / kFT); ++ij)  // one copy of the block's code
-      f32_valu_block<Eval>(a, p, ops, b, m0 + kFT * (ij / (BM / kFT)), n0 + kFT * (ij % (BM / kFT)), as, bs);
+      f32_valu_block<Eval, RED>(a, p, ops, b, m0 + kFT * (ij / (BM / kFT)), n0 + kFT * (ij % (BM / kFT)), as, bs);
     return;
   }
-  contract_store<DT, WM, Eval>(a, p, ops, smem, acc, b, m0, n0);
+  contract_store<DT, WM, Eval, RED>(a, p, ops, smem, acc, b, m0, n0);
 }
 
 }  // namespace pdh

@@ -12,8 +12,9 @@ bool jit_enabled();
 // contraction) of
 // the kernel specialized for program p and element type dt; false when the
 // interpreter kernels must run it (disabled, or the compile failed).
-// lay: the fp32 contraction's operand layouts (contract_split_body's LAY).
-bool jit_get(JitKind kind, const pdh_ew_program& p, int dt, hipFunction_t fns[2], int lay = 0);
+// lay: the fp32 contraction's operand layouts (contract_split_body's LAY);
+// red: its row-partial reduction (ContractArgs::rowred, -1 for none).
+bool jit_get(JitKind kind, const pdh_ew_program& p, int dt, hipFunction_t fns[2], int lay = 0, int red = -1);
 // The row-reduce kernels specialized for (summand, epilogue): fns[0] one wave
 // per output, fns[1] the column variant; or false.
 bool jit_get_reduce(const pdh_ew_program& ps, const pdh_ew_program& pe, int dt, hipFunction_t fns[2]);

@@ -99,11 +99,12 @@ def _strided_view(tt, riders, rows, kd):
     return (batch, row)
 
 
-def _big_tiles(Bs, M, N):
+def _big_tiles(Bs, M, N, kc=64 * 64):
     """The launcher's tile choice (contract_launch in contract.hip): 128 x 128
-    workgroup tiles when they give every compute unit one and neither output
-    side is 64 or under; 64 x 64 otherwise."""
-    return Bs * -(-M // 128) * -(-N // 128) >= _CUS and M > 64 and N > 64
+    workgroup tiles when they give every compute unit one, neither output side
+    is 64 or under and a workgroup's k (kc columns) is over 128; 64 x 64
+    otherwise."""
+    return Bs * -(-M // 128) * -(-N // 128) >= _CUS and M > 64 and N > 64 and kc > 128
 
 
 # Microseconds per 64-column k tile of one workgroup of the fp32 split kernel
@@ -119,7 +120,7 @@ def _ksplit_est(B, M, N, kt, S):
     the measured per-tile rates, plus a fixed 4 us, plus the pass that adds
     the S partial planes (S + 1 planes of HBM traffic at 5 TB/s)."""
     kc = -(-kt // S)
-    if _big_tiles(B * S, M, N):
+    if _big_tiles(B * S, M, N, 64 * kc):
         per = -(-(B * S * -(-M // 128) * -(-N // 128)) // _CUS)
         t = (per // 2) * kc * _BIG_STEP2 + (per % 2) * kc * _BIG_STEP1
     else:
@@ -160,6 +161,23 @@ def _view3(tt, riders, rows, kd):
     if row is None or kst is None or (row != 1 and kst != 1):
         return None
     return (st[riders[0]] if riders else 0, row, kst)
+
+
+def _holds_reduce(node) -> bool:
+    """Whether a tl.reduce (a dissolved carve) feeds ``node``'s values. The
+    second operand of tl.repeat_like only gives the broadcast its shape and
+    is never read, so a contraction there does not count."""
+    stack, seen = [node], set()
+    while stack:
+        n = stack.pop()
+        if id(n) in seen or not hasattr(n, "op"):
+            continue
+        seen.add(id(n))
+        if n.op == "tl.reduce":
+            return True
+        if n.op != "core.param":
+            stack.extend(n.args[:1] if n.op == "tl.repeat_like" else n.args)
+    return False
 
 
 def _yielding(k: Region, node) -> Region:
@@ -786,8 +804,12 @@ class PlanExecutor:
 
         return run, f"map_chain insns={len(low.insns)} shifted={sum(1 for o in offs if o)}"
 
-    def _contraction(self, k, yroot=None):
-        """GEMM-shaped contraction with its epilogue (and prologue chains)."""
+    def _contraction(self, k, yroot=None, rowred=None):
+        """GEMM-shaped contraction with its epilogue (and prologue chains).
+        With ``rowred`` = (reducer, outer reduce, outer yield) the epilogue's
+        values are not stored but reduced over the contraction's n dims (the
+        outer reduce) by row partials (pdh_contract_views_rowred), which a row
+        reduction finishes through the outer yield's program."""
         m = match_contraction_epilogue(k)
         if m is None:
             raise Untranslatable("contraction carve does not match the contraction row")
@@ -836,7 +858,7 @@ class PlanExecutor:
             if base.op == "core.param" and st is not None:
                 return _Pack(direct=self._index(k, base), strides=st)
             pre = None
-            if any(n.op == "tl.reduce" for n in walk(_yielding(k, core))):
+            if _holds_reduce(core):
                 # carves dissolved into this operand (the traffic gate's
                 # re-derivation per tile): materialized once, by their own plan
                 pre = self._materialize(k, core)
@@ -891,7 +913,7 @@ class PlanExecutor:
         # the epilogue; S is the cheapest under the cost model whose sum fits
         # one map-chain program.
         S, fin, ident = 1, None, None
-        if views and KP // 64 >= 4:
+        if views and KP // 64 >= 4 and rowred is None:
             for pick in _ksplit_order(B, M, N, KP // 64):
                 fin = ewprog.splitk_sum(prog, pick, (pick * M * N, N, 1)) if pick > 1 else None
                 if pick == 1 or fin is not None:
@@ -904,32 +926,47 @@ class PlanExecutor:
                     ident.shape[d], ident.out_stride[d] = ext, st
                 ident.insns[0].op = L.EW["ACC"]
 
+        def build(p, vals, dt):
+            torch = _torch()
+            from . import kernels as K
+
+            if p.direct is not None:
+                return vals[p.direct]
+            pv = p.pre(vals) if p.pre is not None else None
+            if p.pre_direct:
+                return pv
+            ins = [pv if i is None else vals[i] for i in p.slots]
+            # a pack of bound parameters only (a weight's transpose) is
+            # made once per bind and reused by every run
+            key = (id(p), tuple(id(t) for t in ins))
+            static = pv is None and all(id(t) in self._static for t in ins)
+            if static and key in self._packs:
+                return self._packs[key]
+            buf = (torch.zeros if p.zero else torch.empty)(p.shape, device="cuda", dtype=dt)
+            K.map_chain(p.prog, ins, buf)
+            if static:
+                self._packs[key] = buf
+            return buf
+
+        def how(p):
+            t = "^t" if len(p.strides) == 3 and p.strides[2] != 1 else ""  # read rows-contiguous (transposed)
+            return ("direct" + t) if p.direct is not None else (("plan" + t) if p.pre_direct else
+                                                                ("plan+pack" if p.pre else "pack"))
+
+        src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
+        if rowred is not None:
+            if not views:
+                raise Untranslatable("row partials of a contraction: fp32 only")
+            return self._rowred_run(k, rowred, build, pa, pb, prog, eslots, (B, M, N, Kx), bdim, mdims, ndims, size,
+                                    riders, src + f" f32={self.f32_contract}")
+
         def run(vals):
             torch = _torch()
             from . import kernels as K
 
             dt = getattr(torch, tdt)
 
-            def build(p):
-                if p.direct is not None:
-                    return vals[p.direct]
-                pv = p.pre(vals) if p.pre is not None else None
-                if p.pre_direct:
-                    return pv
-                ins = [pv if i is None else vals[i] for i in p.slots]
-                # a pack of bound parameters only (a weight's transpose) is
-                # made once per bind and reused by every run
-                key = (id(p), tuple(id(t) for t in ins))
-                static = pv is None and all(id(t) in self._static for t in ins)
-                if static and key in self._packs:
-                    return self._packs[key]
-                buf = (torch.zeros if p.zero else torch.empty)(p.shape, device="cuda", dtype=dt)
-                K.map_chain(p.prog, ins, buf)
-                if static:
-                    self._packs[key] = buf
-                return buf
-
-            a, bt = build(pa), build(pb)
+            a, bt = build(pa, vals, dt), build(pb, vals, dt)
             out = torch.empty(shape, device="cuda", dtype=dt)
             if S > 1:  # k in S slices: partial sums, then their total through the epilogue
                 ws = torch.empty((B * S, M, N), device="cuda", dtype=torch.float32)
@@ -948,17 +985,97 @@ class PlanExecutor:
                 K.contract(a, bt, Kx, prog, [vals[i] for i in eslots], out, f32_mode=self.f32_contract)
             return out
 
-        def how(p):
-            t = "^t" if len(p.strides) == 3 and p.strides[2] != 1 else ""  # read rows-contiguous (transposed)
-            return ("direct" + t) if p.direct is not None else (("plan" + t) if p.pre_direct else
-                                                                ("plan+pack" if p.pre else "pack"))
-
-        src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
         if S > 1:
             src += f" ksplit={S}"
         if self.dtype == "f32":
             src += f" f32={self.f32_contract}"
         return run, src
+
+    def _rowred_run(self, k, rowred, build, pa, pb, prog, eslots, shape4, bdim, mdims, ndims, size, riders, src):
+        """The run of a row reduction over a contraction's epilogue values:
+        partials [B][M][ceil(N / 32)] by pdh_contract_views_rowred, then
+        pdh_reduce_rows_ex over them with the outer yield's program."""
+        reducer, ored, y = rowred
+        B, M, N, Kx = shape4
+        od = (ored.attr("dims"),) if isinstance(ored.attr("dims"), str) else tuple(ored.attr("dims"))
+        if set(od) != set(ndims) or any(nm.startswith("_unit") for nm in ndims):
+            raise Untranslatable("the row reduction is not over the contraction's n dims")
+        nblk = -(-N // 32)
+        row_lat = (bdim,) + tuple(size[nm] for nm in mdims)
+        if len(row_lat) + 1 > L.EW_MAX_DIMS:
+            raise Untranslatable(f"a row reduction over {len(row_lat) + 1} lattice dims (max {L.EW_MAX_DIMS})")
+        # the finishing summand: partial (b, m.., j) at ((b M) + m) nblk + j
+        pst, acc = [], nblk
+        for nm in reversed(mdims):
+            pst.insert(0, acc)
+            acc *= size[nm].size
+        pst = [M * nblk if riders else 0] + pst + [1]
+        ps = L.EwProgram()
+        ps.n_insns, ps.n_operands, ps.ndim, ps.out_reg = 1, 1, len(row_lat) + 1, 0
+        for d, dim in enumerate(row_lat + (Dim("_blk", 0, nblk),)):
+            ps.shape[d], ps.start[d], ps.in_stride[0][d] = dim.size, dim.start, pst[d]
+        ps.insns[0].op, ps.insns[0].dst, ps.insns[0].a = L.EW["LOAD"], 0, 0
+        leaves = {id(p): p for p in k.params}
+        try:
+            le = ewprog.lower(y, row_lat, leaves, acc=ored, acc_scale=(1.0 / N) if ored.attr("f") == "mean" else None,
+                              allow_views=True)
+        except ewprog.Unlowerable as exc:
+            raise Untranslatable(f"row reduction: {exc}") from None
+        slots, views = [], []
+        for j, base in enumerate(le.bases):
+            st, off = le.operand_view(j, _strides_by_name(base.type.names, base.type.shape))
+            if off < 0:
+                raise Untranslatable("a shifted read starts before its tensor")
+            slots.append(self._index(k, base))
+            views.append((st, off))
+        if 1 + len(slots) > L.EW_MAX_OPERANDS:
+            raise Untranslatable(f"the row epilogue reads {len(slots)} operands")
+        pe = le.program(_over(y.type.names, y.type.shape, row_lat), [st for st, _o in views])
+        ps, pe = ewprog.with_slots(ps, 0, 1 + len(slots)), ewprog.with_slots(pe, 1, 1 + len(slots))
+        offs = [o for _st, o in views]
+        tdt = _TORCH_DT[self.dtype]
+        yshape = y.type.shape
+
+        def run(vals):
+            torch = _torch()
+            from . import kernels as K
+
+            dt = getattr(torch, tdt)
+            a, bt = build(pa, vals, dt), build(pb, vals, dt)
+            part = torch.empty((B, M, nblk), device="cuda", dtype=torch.float32)
+            K.contract_views_rowred(a, pa.strides, bt, pb.strides, (B, M, N, Kx), prog, [vals[i] for i in eslots],
+                                    reducer, part, f32_mode=self.f32_contract)
+            out = torch.empty(yshape, device="cuda", dtype=dt)
+            K.reduce_rows(ps, 1, pe, [part.reshape(-1)] + [vals[i].reshape(-1)[o:] for i, o in zip(slots, offs)],
+                          out, reducer)
+            return out
+
+        return run, f"{src} rowred={reducer} + reduce_rows blocks={nblk} epilogue={len(le.insns)}"
+
+    def _reduce_rowred(self, k, m, y, reducer):
+        """A row reduction whose summand is one contraction under a
+        pointwise chain (a softmax's max or denominator over the scores), as
+        a contraction whose epilogue is that chain, reduced to row partials;
+        Untranslatable when the shape does not fit."""
+        red = m["reduce"]
+        x = red.args[0]
+        inner, stack, seen = [], [x], set()
+        while stack:  # the carves under the summand's values
+            n = stack.pop()
+            if id(n) in seen or not hasattr(n, "op"):
+                continue
+            seen.add(id(n))
+            if n.op == "tl.reduce":
+                inner.append(n)
+            elif n.op != "core.param":
+                stack.extend(n.args[:1] if n.op == "tl.repeat_like" else n.args)
+        if len(inner) != 1 or inner[0].attr("f") != "sum":
+            raise Untranslatable("the summand is not one contraction under a pointwise chain")
+        sub = Region(params=k.params, body=(Builder(OPS).emit("core.yield", x),))
+        mm = match_contraction_epilogue(sub)
+        if mm is None or mm["shape"] != "gemm" or mm["reduce"] is not inner[0]:
+            raise Untranslatable("the summand's contraction is not GEMM-shaped")
+        return self._contraction(sub, yroot=x, rowred=(reducer, red, y))
 
     def _bare_reduce(self, k):
         """A red carve that is one max / min reduction: pdh_reduce_rows_ex over
@@ -967,8 +1084,13 @@ class PlanExecutor:
         first by its own plan."""
         red = k.body[-1].args[0]
         f, x = red.attr("f"), red.args[0]
-        if not any(n.op == "tl.reduce" for n in walk(_yielding(k, x))):
+        if not _holds_reduce(x):
             return self._reduce(k, {"reduce": red, "a": x, "f": f, "shape": f"bare-{f}"}, reducer=f)
+        if self.dtype == "f32":
+            try:  # the scores never materialized: row partials of the contraction
+                return self._reduce_rowred(k, {"reduce": red, "a": x, "f": f, "shape": f"bare-{f}"}, red, f)
+            except Untranslatable:
+                pass
         pre = self._materialize(k, x)
         b = Builder(OPS)
         xp = b.param(0, x.type)
@@ -1018,7 +1140,12 @@ class PlanExecutor:
         leaves = {id(p): p for p in k.params}
         y = k.body[-1].args[0] if yroot is None else yroot
         total = math.prod(d.size for d in kdims)
-        if any(n.op == "tl.reduce" for n in walk(_yielding(k, red.args[0]))):
+        if _holds_reduce(red.args[0]):
+            if self.dtype == "f32":
+                try:  # the summand never materialized: row partials of its contraction
+                    return self._reduce_rowred(k, m, y, reducer)
+                except Untranslatable:
+                    pass
             return self._reduce_materialized(k, m, y, reducer)
         try:
             ls = ewprog.lower(red.args[0], lat_s, leaves, allow_views=True)

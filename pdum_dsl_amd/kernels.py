@@ -538,6 +538,43 @@ def contract_views(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, sha
 _REDUCERS = {"sum": 0, "max": 1, "min": 2}
 
 
+def contract_views_rowred(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, shape, epi: _lib.EwProgram,
+                          operands: list, reducer: str, partials: torch.Tensor,
+                          f32_mode: str | None = None) -> torch.Tensor:
+    """Row partials of an fp32 contraction's epilogue values
+    (pdh_contract_views_rowred): partials[b, r, j] = the ``reducer`` ("sum",
+    "max", "min") of epi(acc)[b, r, 32 j .. 32 j + 31] (columns under n),
+    fp32 [batch, m, ceil(n / 32)]. Operands as for :func:`contract_views`."""
+    _require_cuda(a, bt, partials, *operands)
+    B, M, N, Kd = (int(x) for x in shape)
+    if a.dtype != torch.float32 or bt.dtype != torch.float32:
+        raise ValueError("contract_views_rowred takes fp32 a / bt")
+    if reducer not in _REDUCERS:
+        raise ValueError(f"reducer {reducer!r} (sum, max, min)")
+    nblk = -(-N // 32)
+    if partials.dtype != torch.float32 or tuple(partials.shape) != (B, M, nblk) or not partials.is_contiguous():
+        raise ValueError(f"partials must be contiguous fp32 of shape {(B, M, nblk)}")
+    for t, (sb, sr, sk), rows in ((a, a_strides, M), (bt, bt_strides, N)):
+        if min(sb, sr, sk) < 0 or (sk != 1 and sr != 1):
+            raise ValueError("each operand needs k or its rows contiguous, with non-negative strides")
+        reach = t.storage_offset() + (B - 1) * sb + (rows - 1) * sr + (Kd - 1) * sk + 1
+        if reach > t.untyped_storage().nbytes() // t.element_size():
+            raise ValueError("a strided operand's view reaches past its storage")
+    if tuple(epi.shape[d] for d in range(3)) != (B, M, N) or epi.ndim != 3:
+        raise ValueError("the epilogue's lattice must be (batch, m, n)")
+    if len(operands) != epi.n_operands:
+        raise ValueError(f"program reads {epi.n_operands} operands, {len(operands)} given")
+    for i in range(epi.n_operands):
+        if _max_offset(epi, epi.in_stride[i], 3) >= operands[i].numel():
+            raise ValueError(f"epilogue operand {i}: its view reaches past the tensor")
+    table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
+    sa, sb_ = [int(x) for x in a_strides], [int(x) for x in bt_strides]
+    _with_f32_mode(f32_mode, a.dtype, lambda: _lib.call(
+        "pdh_contract_views_rowred", _ptr(a), *sa, _ptr(bt), *sb_, B, M, N, Kd, C.byref(epi), table,
+        _REDUCERS[reducer], _ptr(partials), _DT[a.dtype], C.c_void_p(_stream())))
+    return partials
+
+
 def reduce_rows(summand: _lib.EwProgram, nk: int, epi: _lib.EwProgram, operands: list,
                 out: torch.Tensor, reducer: str = "sum") -> torch.Tensor:
     """out[r] = epi(sum over the last nk summand dims of summand(r, k)): the

@@ -337,9 +337,9 @@ def test_fp32_contractions_compile_in_every_mode():
         assert prev == 6  # the default: fp32 grade
         assert lib.pdh_contract_set_f32_mode(7) == L.PDH_EINVAL and "mode 7" in L.last_error()
         buf = C.create_string_buffer(1 << 16)
-        for mode, body in ((6, "contract_split_body<PDH_F32, 64, 6, 0, pdh::GenEval>"),
-                           (3, "contract_split_body<PDH_F32, 32, 3, 0, pdh::GenEval>"),
-                           (0, "contract_f32_body<pdh::GenEval>")):
+        for mode, body in ((6, "contract_split_body<PDH_F32, 64, 6, 0, pdh::GenEval, -1>"),
+                           (3, "contract_split_body<PDH_F32, 32, 3, 0, pdh::GenEval, -1>"),
+                           (0, "contract_f32_body<pdh::GenEval, -1>")):
             lib.pdh_contract_set_f32_mode(mode)
             assert lib.pdh_ew_jit_compile(C.byref(epi), 1, L.PDH_F32) == 0, L.last_error()
             lib.pdh_ew_jit_source(C.byref(epi), 1, L.PDH_F32, buf, len(buf))
@@ -349,7 +349,12 @@ def test_fp32_contractions_compile_in_every_mode():
         for kind in (2, 3, 4):
             assert lib.pdh_ew_jit_compile(C.byref(epi), kind, L.PDH_F32) == 0, L.last_error()
             lib.pdh_ew_jit_source(C.byref(epi), kind, L.PDH_F32, buf, len(buf))
-            assert f"contract_split_body<PDH_F32, 64, 6, {kind - 1}, pdh::GenEval>" in buf.value.decode()
+            assert f"contract_split_body<PDH_F32, 64, 6, {kind - 1}, pdh::GenEval, -1>" in buf.value.decode()
+        # row partials (kinds 5..7: sum, max, min) for pdh_contract_views_rowred
+        for kind in (5, 6, 7):
+            assert lib.pdh_ew_jit_compile(C.byref(epi), kind, L.PDH_F32) == 0, L.last_error()
+            lib.pdh_ew_jit_source(C.byref(epi), kind, L.PDH_F32, buf, len(buf))
+            assert f"contract_split_body<PDH_F32, 64, 6, 0, pdh::GenEval, {kind - 5}>" in buf.value.decode()
     finally:
         lib.pdh_contract_set_f32_mode(prev)
 

@@ -156,3 +156,90 @@ def test_non_finite_values_of_a_transposed_operand(mode):
     fin = np.isfinite(want)
     tol = (1e-5 if mode == 6 else 5e-5) * np.abs(want[fin]).max() * 2.0
     assert np.abs(got[fin] - want[fin]).max() <= tol
+
+
+def _softmax_stat_program(B, T, S, scale, with_max):
+    """The pointwise chain of a causal softmax statistic over the scores
+    acc[b, t, s]: where(s <= t, scale acc, -1e9), less the row max m[b, t]
+    (operand 0) and exponentiated when ``with_max``."""
+    from pdum_dsl_amd import _lib as L
+
+    p = L.EwProgram()
+    p.ndim = 3
+    for d, (ext, st) in enumerate(zip((B, T, S), (T * S, S, 1))):
+        p.shape[d], p.out_stride[d] = ext, st
+    ins = [("ACC", 0, 0, 0, 0, 0.0), ("CONST", 1, 0, 0, 0, scale), ("MUL", 0, 0, 1, 0, 0.0),
+           ("IOTA", 2, 2, 0, 0, 0.0), ("IOTA", 3, 1, 0, 0, 0.0), ("LE", 4, 2, 3, 0, 0.0),
+           ("CONST", 5, 0, 0, 0, -1e9), ("WHERE", 6, 4, 0, 5, 0.0)]
+    if with_max:
+        ins += [("LOAD", 7, 0, 0, 0, 0.0), ("SUB", 8, 6, 7, 0, 0.0), ("EXP", 9, 8, 0, 0, 0.0)]
+        p.n_operands = 1
+        for d, st in enumerate((T, 1, 0)):
+            p.in_stride[0][d] = st
+    for i, (op, dst, a, b, c, imm) in enumerate(ins):
+        q = p.insns[i]
+        q.op, q.dst, q.a, q.b, q.c, q.imm = L.EW[op], dst, a, b, c, imm
+    p.n_insns, p.out_reg = len(ins), ins[-1][1]
+    return p
+
+
+@pytest.mark.parametrize("la,lb", [("k", "k"), ("r", "r")])
+@pytest.mark.parametrize("mode", [6, 0])
+@pytest.mark.parametrize("B,T,S,E", [(3, 200, 300, 64), (2, 1024, 1024, 64)])
+def test_row_partials_of_softmax_statistics(la, lb, mode, B, T, S, E):
+    """pdh_contract_views_rowred: per 32-column run, the max of the masked
+    scaled scores and the sum of their exponentials less the row max, against
+    float64 numpy; ragged runs (S = 300) leave out the columns past S."""
+    from pdum_dsl_amd import kernels as K
+
+    x, y = _inputs(B, T, S, E, seed=26)
+    (a, sa), (bt, sb) = _lay(x, la), _lay(y, lb)
+    scale = E ** -0.5
+    sc = np.einsum("bte,bse->bts", x.double().cpu().numpy(), y.double().cpu().numpy()) * scale
+    causal = np.arange(S)[None, None, :] <= np.arange(T)[None, :, None]
+    masked = np.where(causal, sc, -1e9)
+    nblk = -(-S // 32)
+    pad = np.full((B, T, nblk * 32), -np.inf)
+    pad[..., :S] = masked
+    want_max = pad.reshape(B, T, nblk, 32).max(-1)
+    part = torch.empty(B, T, nblk, device="cuda")
+    K.contract_views_rowred(a, sa, bt, sb, (B, T, S, E), _softmax_stat_program(B, T, S, scale, False), [], "max",
+                            part, f32_mode=MODES[mode])
+    torch.cuda.synchronize()
+    got = part.double().cpu().numpy()
+    assert np.abs(got - want_max).max() <= 1e-5 * np.abs(sc).max()
+    m = torch.tensor(masked.max(-1), device="cuda", dtype=torch.float32)
+    e = np.exp(masked - m.double().cpu().numpy()[..., None])
+    pad = np.zeros((B, T, nblk * 32))
+    pad[..., :S] = e
+    want_sum = pad.reshape(B, T, nblk, 32).sum(-1)
+    K.contract_views_rowred(a, sa, bt, sb, (B, T, S, E), _softmax_stat_program(B, T, S, scale, True), [m], "sum",
+                            part, f32_mode=MODES[mode])
+    torch.cuda.synchronize()
+    got = part.double().cpu().numpy()
+    assert np.abs(got - want_sum).max() <= 1e-5 * 32 * max(1.0, np.abs(sc).max())
+
+
+def test_row_partials_propagate_nan_and_leave_clean_runs_alone():
+    """A NaN in one score poisons its row's max run (as the row reduction's
+    max does) and only that run; min is the max's mirror."""
+    from pdum_dsl_amd import kernels as K
+
+    B, T, S, E = 1, 130, 100, 64
+    x, y = _inputs(B, T, S, E, seed=27)
+    x[0, 7, 5] = float("nan")
+    (a, sa), (bt, sb) = _lay(x, "k"), _lay(y, "k")
+    part = torch.empty(B, T, 4, device="cuda")
+    ident = _identity(B, T, S)
+    for red in ("max", "min"):
+        K.contract_views_rowred(a, sa, bt, sb, (B, T, S, E), ident, [], red, part)
+        torch.cuda.synchronize()
+        got = part.double().cpu().numpy()
+        nan = np.isnan(got)
+        assert nan[0, 7].all() and nan.sum() == 4  # row 7: every run reads the NaN through the product
+        sc = np.einsum("bte,bse->bts", x.double().cpu().numpy(), y.double().cpu().numpy())
+        pad = np.full((B, T, 128), -np.inf if red == "max" else np.inf)
+        pad[..., :S] = sc
+        want = getattr(pad.reshape(B, T, 4, 32), red)(-1)
+        ok = ~nan
+        assert np.abs(got[ok] - want[ok]).max() <= 1e-5 * np.abs(sc[np.isfinite(sc)]).max()

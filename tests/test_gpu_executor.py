@@ -331,6 +331,7 @@ def test_a_bare_row_max_or_min_runs_on_the_device(f):
 
 _SMALL = dict(t=64, d=128, nh=2, hk=64, m=512, layers=1, v=64)
 _TWO_LAYER = dict(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)
+_LONG = dict(t=512, d=128, nh=2, hk=64, m=512, layers=1, v=64)  # the softmax statistics as row partials
 
 
 @pytest.mark.parametrize("cfg,dtype,f32c,tol,tables", [
@@ -338,7 +339,8 @@ _TWO_LAYER = dict(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)
     (_SMALL, "f32", "bf16", 3e-2, False), (_SMALL, "f32", "fma", 1e-5, False),
     (_SMALL, "bf16", "bf16x6", 7e-2, False), (_TWO_LAYER, "f32", "bf16x6", 3e-5, False),
     (_TWO_LAYER, "f32", "bf16x3", 5e-4, False), (_SMALL, "f32", "bf16x6", 1e-5, True),
-    (_SMALL, "bf16", "bf16x6", 7e-2, True), (_TWO_LAYER, "f32", "bf16x6", 3e-5, True)])
+    (_SMALL, "bf16", "bf16x6", 7e-2, True), (_TWO_LAYER, "f32", "bf16x6", 3e-5, True),
+    (_LONG, "f32", "bf16x6", 3e-5, False), (_LONG, "f32", "fma", 3e-5, False)])
 def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol, tables):
     """grad of gpt2's logits w.r.t. every weight (the embedding tables too
     when ``tables``: their gradient is a scatter-add of the embedding's
@@ -375,6 +377,8 @@ def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol, tab
         assert all(f"f32={f32c}" in st.source for st in ex.steps if st.source.startswith("contract"))
     # the softmax's max takes no cotangent (shift invariance): no scan, no bare max in the backward
     assert not any("split at scan" in st.source for st in ex.steps)
+    if cfg is _LONG:  # the recomputed max and denominator never store the scores
+        assert sum("rowred=" in st.source for st in ex.steps) == 2, [st.source for st in ex.steps]
     ex.bind(vals)
     outs = ex.run()
     torch.cuda.synchronize()
