@@ -24,7 +24,9 @@ planner's numpy interpreter, so each can check the other:
                  (layout.py)
   tl.take        the gather (indexing.py:120-230)
   tl.scatter_add its adjoint, duplicates summed (indexing.py:153-190, 223-259)
-  tl.fold        a Python loop over the scan dim, each element source
+  tl.fold        a Python loop over the scan dim (out ('final', i): the last
+                 state i; ('emit',): each step's last yield stacked along the
+                 scan dim), each element source
                  selected at the ABSOLUTE coordinate (dialect.py:1448-1470;
                  region_evaluator.py:431-465)
 
@@ -286,12 +288,21 @@ def _dispatch(n, ev):
         carried, srcs = list(vals[:k]), vals[k:]
         d = next(x for x in srcs[0].dims if x[0] == dim)
         step = n.regions[0]
+        out = tuple(_attr(n, "out"))
+        emitted = []
         for q in range(d[1], d[2]):
             sel = []
             for s in srcs:
                 ax = s.names.index(dim)
                 sel.append(V(s.t.select(ax, q - s.dims[ax][1]), s.dims[:ax] + s.dims[ax + 1:]))
             res = evaluate(step, carried + sel)
-            carried = list(res) if isinstance(res, tuple) else [res]
-        return carried[_attr(n, "out")[1]]
+            res = list(res) if isinstance(res, tuple) else [res]
+            carried = res[:k]
+            if out[0] == "emit":  # the step's last yield, stacked along the scan dim (last)
+                e = res[k]
+                want = [x.name for x in n.type.dims if x.name != dim]
+                emitted.append(e.t.permute([e.names.index(nm) for nm in want]))
+        if out[0] == "emit":
+            return V(torch.stack(emitted, dim=-1), tuple((x.name, x.start, x.stop) for x in n.type.dims))
+        return carried[out[1]]
     raise NotImplementedError(f"oracle evaluator: no rule for {op}")

@@ -33,7 +33,13 @@ templates), over the vocabulary this backend reads:
   tl.stage       identity
   core.const / tl.const / tl.iota / comparisons / stop_gradient: no flow
 
-Anything else (fold, split, select, argtopk) refuses by name: a primitive
+  tl.fold        read at its final state: a reverse fold over the flipped
+                 sequences whose step is the forward step's VJP (grad of the
+                 step against the carried cotangent), states before each step
+                 from the forward trajectory (autodiff.py:411-605, one
+                 segment, no checkpointing)
+
+Anything else (argtopk, an emitting fold) refuses by name: a primitive
 joins the AD with its linearization, or not at all.
 """
 
@@ -112,7 +118,12 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
     b = Builder(OPS)
     const = lambda v: b.emit("core.const", type=F64, value=float(v))  # noqa: E731
     pw = lambda f, *xs: b.emit("tl.pointwise", *xs, f=f)  # noqa: E731
-    rl = lambda x, like: b.emit("tl.repeat_like", x, like)  # noqa: E731
+
+    def rl(x, like):  # x broadcast over like's dims (a scalar cotangent onto a zero field of like's shape)
+        if _is_tensor(x):
+            return b.emit("tl.repeat_like", x, like)
+        zero = b.emit("tl.const", value=0.0, dims=tuple((d.name, (d.start, d.stop)) for d in like.type.dims))
+        return b.emit("tl.pointwise", zero, x, f="add")
 
     if seed is None:
         if _is_tensor(tnode) and tnode.type.dims:
@@ -251,6 +262,8 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
         elif op == "tl.rename":  # a relabelling: the cotangent takes the operand's names back
             back = tuple(sorted((new, old) for old, new in n.attr("mapping")))
             contribute(n.args[0], b.emit("tl.rename", c, mapping=back))
+        elif op == "tl.fold":
+            _fold_rule(b, n, c, contribute, const)
         else:
             raise NotImplementedError(
                 f"{op} has no adjoint rule in this build (a primitive joins the AD with its linearization)"
@@ -277,6 +290,110 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
     y = b.emit("core.tuple", *ys) if len(ys) > 1 else ys[0]
     joint = Region(params=params, body=(b.emit("core.yield", y),))
     return RegionGrad(joint, grads, jnames, tuple(outputs), nodes)
+
+
+def _fold_rule(b, n, c, contribute, const):
+    """The adjoint of a fold read at its final state o (autodiff.py:411-605,
+    one segment, no checkpointing): a reverse fold over the flipped sequences
+    whose carry is the cotangent of the states after each step.
+
+    - The states before step t: each state's trajectory (an emitting fold of
+      the same step) shifted one step later, the initial state at t = start.
+    - The reverse step is the VJP of the forward step: ``grad`` of the scalar
+      sum_i <ct_i, step(s, e)_i> with respect to the step's own params, the
+      ct_i bound as extra params. Its state gradients are the next carry, its
+      element gradients the emissions.
+    - The reverse carry starts at (c for state o, zero for the others): the
+      cotangent of the final states. The reference injects c at the last step
+      through a padded sequence instead; the sum is the same.
+    The carry's final value is the initial states' cotangent; the emissions,
+    flipped back, the element sources'. Nested folds in the step differentiate
+    through the same rule (grad recurses)."""
+    state = tuple(n.attr("state"))
+    k = len(state)
+    dim = n.attr("dim")
+    out = tuple(n.attr("out"))
+    if out[0] != "final":
+        raise NotImplementedError("tl.fold: only a fold read at its final state has an adjoint here")
+    o = out[1]
+    inits, elems = n.args[:k], n.args[k:]
+    d = elems[0].type.dim(dim)
+    start, stop = d.start, d.stop
+    step = n.regions[0]
+    y = step.body[-1].args[0]
+    ynodes = tuple(y.args) if y.op == "core.tuple" else (y,)
+    sp, ep = step.params[:k], step.params[k:]
+    fat = {"dim": dim, "state": state, "element": tuple(n.attr("element"))}
+
+    def zeros(tt):
+        return b.emit("tl.const", value=0.0, dims=tuple((x.name, (x.start, x.stop)) for x in tt.dims))
+
+    if stop == start:  # no step runs: the fold is its initial state
+        contribute(inits[o], c)
+        return
+
+    def with_yield(vals):
+        wb = Builder(OPS)
+        yy = vals[0] if len(vals) == 1 else wb.emit("core.tuple", *vals)
+        return Region(params=step.params, body=(wb.emit("core.yield", yy),))
+
+    # the states before each step
+    prev = []
+    for i in range(k):
+        traj = b.emit("tl.fold", *inits, *elems, regions=(with_yield(ynodes[:k] + (ynodes[i],)),), out=("emit",),
+                      **fat)
+        if stop - start > 1:
+            later = b.emit("tl.slice", b.emit("tl.shift", traj, deltas=((dim, 1),)), ranges=((dim, (start + 1, stop)),))
+            later = b.emit("tl.pad", later, extents=((dim, (start, stop)),), fill=0.0)
+        else:
+            later = zeros(traj.type)
+        first = b.emit("tl.pointwise", b.emit("tl.iota", later, name=dim), const(start), f="eq")
+        init_t = b.emit("tl.repeat", inits[i], name=dim, extent=(start, stop))
+        prev.append(b.emit("tl.pointwise", first, init_t, later, f="where"))
+
+    # the step's VJP: grad of sum_i <ct_i, y_i> over the step's params
+    wb = Builder(OPS)
+    cts = tuple(wb.param(("fold.ct", i), ynodes[i].type) for i in range(k))
+    tgt = None
+    for i in range(k):
+        t_ = wb.emit("tl.pointwise", ynodes[i], cts[i], f="mul")
+        if t_.type.dims:
+            t_ = wb.emit("tl.reduce", t_, dims=tuple(x.name for x in t_.type.dims), f="sum")
+        tgt = t_ if tgt is None else wb.emit("tl.pointwise", tgt, t_, f="add")
+    wrapper = Region(params=tuple(step.params) + cts, body=(wb.emit("core.yield", tgt),))
+    pnames = tuple(f"s{i}" for i in range(k)) + tuple(f"e{j}" for j in range(len(ep))) + tuple(
+        f"ct{i}" for i in range(k))
+    vjp = grad(wrapper, "fold.vjp", wrt=pnames[:k + len(ep)], names=region_names(wrapper, pnames, ("fold.vjp",)))
+
+    def g_of(nm, tt):
+        gname = vjp.grads.get(nm)
+        return zeros(tt) if gname is None else vjp.nodes[gname]
+
+    dstate = tuple(g_of(f"s{i}", sp[i].type) for i in range(k))
+    # reverse step: carries ct, elements (states before the step, the step's elements)
+    rparams = cts + tuple(step.params)
+    rat = {"dim": dim, "state": tuple(f"fold.ct{i}" for i in range(k)),
+           "element": tuple(f"fold.prev{i}" for i in range(k)) + fat["element"]}
+
+    def rstep(extra=()):
+        rb = Builder(OPS)
+        vals = dstate + tuple(extra)
+        yy = vals[0] if len(vals) == 1 else rb.emit("core.tuple", *vals)
+        return Region(params=rparams, body=(rb.emit("core.yield", yy),))
+
+    flip = lambda v: b.emit("tl.flip", v, name=dim)  # noqa: E731
+    rinit = tuple(c if i == o else zeros(inits[i].type) for i in range(k))
+    rsrc = tuple(flip(v) for v in prev) + tuple(flip(v) for v in elems)
+    for i in range(k):
+        if vjp.grads.get(f"s{i}") is None:
+            continue
+        contribute(inits[i], b.emit("tl.fold", *rinit, *rsrc, regions=(rstep(),), out=("final", i), **rat))
+    for j, ev_ in enumerate(elems):
+        if vjp.grads.get(f"e{j}") is None:
+            continue
+        em = b.emit("tl.fold", *rinit, *rsrc, regions=(rstep((vjp.nodes[vjp.grads[f"e{j}"]],)),), out=("emit",),
+                    **rat)
+        contribute(ev_, flip(em))
 
 
 def _pointwise_rule(n, c, contribute, pw, const):

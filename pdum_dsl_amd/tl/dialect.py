@@ -15,7 +15,9 @@ emit and consume (packages/tensorlib/src/pdum/tl/dialect.py:115-487):
   tl.select     coords          fixes dims to points
   tl.iota       name            the coordinate field along a dim of the lattice
   tl.const      value, dims     a constant field
-  tl.fold       dim, state, element, out, step region
+  tl.fold       dim, state, element, out, step region; out ('final', i) is
+                the last value of state i, ('emit',) stacks each step's extra
+                (last) yield along the scan dim
   tl.rename     mapping         renames dims in place (a view: no data moves)
   tl.shift      deltas          moves dims' frames by integer deltas (a view)
   tl.slice      ranges          restricts dims to absolute [lo, hi) (a view)
@@ -183,14 +185,22 @@ def _r_fold(args, at, regions):
         raise TypeError("tl.fold: step binders do not match (state inits + element slices)")
     y = step.body[-1].args[0]
     ytypes = tuple(a.type for a in y.args) if y.op == "core.tuple" else (y.type,)
-    if len(ytypes) != k:
-        raise TypeError(f"tl.fold: the step must yield the {k} next state(s)")
+    out = tuple(at["out"])
+    if out[0] not in ("final", "emit"):
+        raise TypeError("tl.fold: out is ('final', i) or ('emit',)")
+    emit = out[0] == "emit"
+    if len(ytypes) != k + (1 if emit else 0):
+        raise TypeError(f"tl.fold: the step must yield the {k} next state(s)" + (" and the emission" if emit else ""))
     for i in range(k):
         if _frames(ytypes[i]) != _frames(inits[i]):
             raise TypeError(f"tl.fold: carry {state[i]!r} changes the state type")
-    out = tuple(at["out"])
-    if out[0] != "final":
-        raise TypeError("tl.fold: only out=('final', i) folds are read by this backend")
+    if emit:  # every step's last yield, stacked along the scan dim (its frame from the element sources)
+        d = srcs[0].dim(dim) if srcs else None
+        if d is None:
+            raise TypeError("tl.fold: an emitting fold needs an element source")
+        if ytypes[k].has(dim):
+            raise TypeError(f"tl.fold: the emission already has the scan dim {dim!r}")
+        return TensorType(ytypes[k].dims + (Dim(dim, d.start, d.stop),))
     return inits[out[1]]
 
 

@@ -250,10 +250,18 @@ def run_region(region: Region, values: list):
             carried, srcs = list(vals[:k]), vals[k:]
             d = n.args[k].type.dim(dim)
             step = n.regions[0]
+            out = tuple(n.attr("out"))
+            emitted = []
             for q in range(d.start, d.stop):
                 res = run_region(step, carried + [s.select(dim, q) for s in srcs])
-                carried = list(res) if isinstance(res, tuple) else [res]
-            return carried[n.attr("out")[1]]
+                res = list(res) if isinstance(res, tuple) else [res]
+                carried = res[:k]
+                if out[0] == "emit":  # the emission in the node's dim order, less the scan dim
+                    e = res[k]
+                    emitted.append(e.to_numpy(tuple(x.name for x in n.type.dims if x.name != dim)))
+            if out[0] == "emit":
+                return Field(np.stack(emitted, axis=-1), n.type.dims)
+            return carried[out[1]]
         raise NotImplementedError(f"run_region: {op} has no evaluation rule here")
 
     return ev(region.body[-1])
