@@ -522,6 +522,9 @@ class PlanExecutor:
             run, src = self._scatter(k)
         elif carve.group.confidence == "red" and any(n.op == "tl.take" for n in walk(k)):
             run, src = self._take(k)
+        elif carve.group.confidence == "red" and any(n.op == "tl.pad" for n in walk(k)):
+            # zero-padded views (a stencil's adjoint): the pads materialized, then one map chain
+            run, src = self._padded(k)
         elif carve.group.confidence == "red" and any(n.op == "tl.scan" for n in walk(k)):
             # the first-occurrence max / min adjoint's prefix count: pdh_scan
             run, src = self._scan(k)
@@ -773,6 +776,79 @@ class PlanExecutor:
             return nested._run({id(p): v for p, v in zip(sub.params, vals)}, self._bad)
 
         return run
+
+    def _padded(self, k):
+        """A pointwise carve over tl.pad views (the reference leaves it red:
+        tl.pad has no template row). Each pad, inner ones first, is
+        materialized once: a buffer of its frame filled with its fill, its
+        operand's chain written into the interior by a map chain whose output
+        view starts at the operand's frame. The carve's value is then one map
+        chain reading the pad buffers through their shifted / sliced views
+        (in-bounds offset reads, as a stencil reads its halo)."""
+        y = k.body[-1].args[0]
+        if y.op == "core.tuple" or not y.type.names:
+            raise Untranslatable("a padded carve with one tensor output")
+        pads, seen, stack = [], set(), [(y, False)]
+        while stack:  # post-order: a pad after the pads inside its operand
+            n, done = stack.pop()
+            if done:
+                if n.op == "tl.pad":
+                    pads.append(n)
+                continue
+            if id(n) in seen or not hasattr(n, "op") or n.op == "core.param":
+                continue
+            seen.add(id(n))
+            stack.append((n, True))
+            stack.extend((a, False) for a in (n.args[:1] if n.op == "tl.repeat_like" else n.args))
+        leaves = {id(p): p for p in k.params}
+        idx = {id(p): i for i, p in enumerate(k.params)}
+        plans = []
+        tdt = _TORCH_DT[self.dtype]
+
+        def chain(x, dims, out_st, out_off):
+            try:
+                low = ewprog.lower(x, dims, leaves, allow_views=True)
+            except ewprog.Unlowerable as exc:
+                raise Untranslatable(f"padded carve: {exc}") from None
+            slots, views = [], []
+            for j, base in enumerate(low.bases):
+                st, off = low.operand_view(j, _strides_by_name(base.type.names, base.type.shape))
+                if off < 0:
+                    raise Untranslatable("a shifted read starts before its tensor")
+                slots.append(("p", idx[id(base)]) if id(base) in idx else ("pad", id(base)))
+                views.append((st, off))
+            return low.program(out_st, [st for st, _o in views]), slots, [o for _s, o in views], out_off, len(low.insns)
+
+        for pad in pads:
+            x = pad.args[0]
+            pst = _strides_by_name(pad.type.names, pad.type.shape)
+            off = sum((x.type.dim(nm).start - pad.type.dim(nm).start) * pst[nm] for nm in x.type.names)
+            plans.append((pad, chain(x, x.type.dims, [pst[d.name] for d in x.type.dims], off)))
+            leaves[id(pad)] = pad
+        final = chain(y, y.type.dims, _dense_strides(y.type.shape), 0)
+        shape = y.type.shape
+
+        def run(vals):
+            torch = _torch()
+            from . import kernels as K
+
+            dt = getattr(torch, tdt)
+            bufs = {}
+
+            def operand(slot, o):
+                t = vals[slot[1]] if slot[0] == "p" else bufs[slot[1]]
+                return t.reshape(-1)[o:]
+
+            for pad, (prog, slots, offs, out_off, _n) in plans:
+                buf = torch.full(pad.type.shape, float(pad.attr("fill")), device="cuda", dtype=dt)
+                K.map_chain(prog, [operand(sl, o) for sl, o in zip(slots, offs)], buf.reshape(-1)[out_off:])
+                bufs[id(pad)] = buf
+            prog, slots, offs, _o, _n = final
+            out = torch.empty(shape, device="cuda", dtype=dt)
+            K.map_chain(prog, [operand(sl, o) for sl, o in zip(slots, offs)], out)
+            return out
+
+        return run, f"padded pads={len(pads)} + map_chain insns={final[4]}"
 
     def _map_chain(self, k):
         """A map chain or stencil carve: shifted / sliced reads of a value
