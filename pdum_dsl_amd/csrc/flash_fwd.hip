@@ -20,7 +20,14 @@
 //     every operand read is a lane offset plus an immediate (no per-tile
 //     address arithmetic);
 //   * exp runs as exp2 on log2(e)-scaled scores (v_exp_f32); the running max
-//     is rescaled lazily (only when it grows by more than 2^8);
+//     is rescaled lazily (only when it grows by more than 2^8). Without the
+//     (m, den) artifacts, full tiles skip the row max altogether: their
+//     exponentials are referred to the running reference, and a tile takes
+//     the exact path (row max, rescale, exponentials again) only when a lane's
+//     partial sum leaves (0, 2^8]. On gfx950 VALU work adds to MFMA time
+//     almost one for one once the matrix pipe is busy (only ~4 VALU
+//     instructions hide under each 32x32x16 product), so every VALU
+//     instruction taken out of the tile body is time saved;
 //   * causal / band masks prune dead tiles (the mask-derived bounds of
 //     fusion.py:659-690) and mask only the tiles the band cuts;
 //   * heavy (late) query blocks launch first, and the workgroup index is
@@ -95,14 +102,19 @@ struct FwdCfg {
 // same quotient (exact in real arithmetic).
 constexpr float kTau = 8.0f;
 
-template <typename T, int D>
-__global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs a) {
-  using C = FwdCfg<D>;
-  // a static LDS array: its address is fixed when the kernel is compiled, so
-  // every operand read folds its buffer base into the immediate offset
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS];
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+// A workgroup's place in the grid and its key-tile ranges: the instance and
+// query block it owns (heavy late blocks first, in an XCD- and shader-engine-
+// aware order), the live key tiles [kt_lo, kt_hi) after the mask-derived
+// prune, the run [kf_lo, kf_hi) of tiles live for every row of the block, and,
+// for a split launch, this split's share of the range.
+struct BlockPlan {
+  int64_t inst;
+  int qb, split;
+  int kt_lo, kt_hi, kf_lo, kf_hi;
+};
 
+template <int BM, int BN>
+__device__ __forceinline__ BlockPlan block_plan(const FwdArgs& a) {
   // workgroup -> (instance, query block); heavy (late) query blocks first
   int bid = blockIdx.x;
   int split = 0;
@@ -132,6 +144,126 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
     inst = bid / a.nqb;
     qb = a.nqb - 1 - (bid % a.nqb);
   }
+  const int64_t T_ = a.t, S_ = a.s;
+  const int q0 = qb * BM;
+  // key-tile range of the workgroup (mask-derived prune, absolute tile grid)
+  const int ntiles = static_cast<int>((S_ + BN - 1) / BN);
+  int kt_lo = 0, kt_hi = ntiles;
+  if (a.masked && a.prune) {
+    const int64_t qlast = (q0 + BM - 1 < T_ ? q0 + BM - 1 : T_ - 1);
+    if (a.band_hi < INT64_MAX / 4) {
+      const int64_t smax = qlast + a.band_hi;  // last live key of the block
+      kt_hi = smax < 0 ? 0 : static_cast<int>(smax / BN + 1 < ntiles ? smax / BN + 1 : ntiles);
+    }
+    if (a.band_lo > INT64_MIN / 4) {
+      const int64_t smin = q0 + a.band_lo;  // first live key of the block
+      kt_lo = smin <= 0 ? 0 : static_cast<int>(smin / BN);
+    }
+  }
+  // Tiles fully live for every row of the workgroup form one run [kf_lo, kf_hi);
+  // the tiles before it (a window's left edge) and after it (the diagonal, the
+  // key tail) take the masked body.
+  int kf_lo = kt_lo, kf_hi = kt_hi;
+  {
+    const int64_t full_end_keys = S_ / BN;
+    kf_hi = kf_hi < full_end_keys ? kf_hi : static_cast<int>(full_end_keys);
+    if (a.masked) {
+      const int64_t qlo = q0, qhi = q0 + BM - 1;
+      if (a.band_hi < INT64_MAX / 4) {  // key0 + BN - 1 - qlo <= hi
+        const int64_t lim = qlo + a.band_hi - (BN - 1);
+        const int64_t n = lim < 0 ? 0 : lim / BN + 1;
+        kf_hi = kf_hi < n ? kf_hi : static_cast<int>(n);
+      }
+      if (a.band_lo > INT64_MIN / 4) {  // key0 - qhi >= lo
+        const int64_t lim = qhi + a.band_lo;
+        const int64_t n = lim <= 0 ? 0 : (lim + BN - 1) / BN;
+        kf_lo = kf_lo > n ? kf_lo : static_cast<int>(n);
+      }
+    }
+    if (kf_lo > kf_hi) kf_lo = kf_hi = kt_hi;
+  }
+  if (a.nsplit > 1) {  // this split's share of the range; the run boundaries clamp into it
+    const int s_lo = kt_lo + split * a.split_tiles;
+    const int lo2 = s_lo < kt_hi ? s_lo : kt_hi;
+    const int hi2 = s_lo + a.split_tiles < kt_hi ? s_lo + a.split_tiles : kt_hi;
+    kf_lo = kf_lo < lo2 ? lo2 : (kf_lo > hi2 ? hi2 : kf_lo);
+    kf_hi = kf_hi < lo2 ? lo2 : (kf_hi > hi2 ? hi2 : kf_hi);
+    kt_lo = lo2;
+    kt_hi = hi2;
+  }
+
+  return BlockPlan{inst, qb, split, kt_lo, kt_hi, kf_lo, kf_hi};
+}
+
+// Stores a wave's 32 query rows: o = oacc / den and the optional m, den and lse
+// rows, or, for a split launch, the unnormalized partial state that
+// flash_fwd_combine merges. lsum is this lane-half's share of the row's
+// denominator; mused the max the exponentials are referred to, mtrue the true
+// running max (the m artifact).
+template <typename T, int D>
+__device__ __forceinline__ void fwd_store(const FwdArgs& a, int64_t inst, int split, int qw0, int r32, int g,
+                                          uint16_t* op, const f32x16 (&oacc)[D / 32], float mused, float mtrue,
+                                          float lsum) {
+  constexpr int DB = D / 32;
+  const int64_t T_ = a.t;
+  const int qrow = qw0 + r32;
+  // combine the two lane halves' partial denominators, normalize, store
+  const float den = lsum + __shfl_xor(lsum, 32, 64);
+  if (a.nsplit > 1) {  // the partial state, unnormalized, for flash_fwd_combine
+    if (qrow < T_) {
+      const int64_t srow = split * a.plane + inst * T_ + qrow;
+      float* wo = a.ws + srow * D + 4 * g;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4)
+          *reinterpret_cast<f32x4*>(wo + db * 32 + a4 * 8) =
+              f32x4{oacc[db][4 * a4 + 0], oacc[db][4 * a4 + 1], oacc[db][4 * a4 + 2], oacc[db][4 * a4 + 3]};
+      if (g == 0) {
+        float* st = a.ws + a.nsplit * a.plane * D;
+        st[srow] = mused;
+        st[a.nsplit * a.plane + srow] = mtrue;
+        st[2 * a.nsplit * a.plane + srow] = den;
+      }
+    }
+    return;
+  }
+  if (qrow < T_) {
+    const float inv = den > 0.f ? 1.0f / den : 0.f;
+    uint16_t* obase = op + static_cast<int64_t>(qw0) * a.o_st;  // wave-uniform
+    const uint32_t o_lane = static_cast<uint32_t>(r32 * a.o_st * 2 + g * 8);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d0 = db * 32 + a4 * 8;  // + 4 g, carried by o_lane
+        const u32x2 wv = {pack2<T>(oacc[db][4 * a4 + 0] * inv, oacc[db][4 * a4 + 1] * inv),
+                          pack2<T>(oacc[db][4 * a4 + 2] * inv, oacc[db][4 * a4 + 3] * inv)};
+        gstore<u32x2>(obase + d0, o_lane, wv);
+      }
+    }
+    if (g == 0) {
+      const int64_t srow = inst * T_ + qrow;
+      // den sums exp(s - mused); the artifacts are referred to the true max
+      if (a.m_out) a.m_out[srow] = mtrue * a.scale;
+      if (a.den_out) a.den_out[srow] = den * fast_exp2((mused - mtrue) * a.c2);
+      if (a.lse_out) a.lse_out[srow] = mused * a.scale + __logf(den);
+    }
+  }
+}
+
+template <typename T, int D, bool ART>
+__global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs a) {
+  using C = FwdCfg<D>;
+  // a static LDS array: its address is fixed when the kernel is compiled, so
+  // every operand read folds its buffer base into the immediate offset
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS];
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+
+  const BlockPlan bp = block_plan<C::BM, C::BN>(a);
+  const int64_t inst = bp.inst;
+  const int qb = bp.qb, split = bp.split;
+  const int kt_lo = bp.kt_lo, kt_hi = bp.kt_hi, kf_lo = bp.kf_lo, kf_hi = bp.kf_hi;
   const int64_t b = inst / a.heads_q, hq = inst % a.heads_q;
   const int64_t hk = hq / (a.heads_q / a.heads_kv);
   const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.q_sb + hq * a.q_sh;
@@ -151,52 +283,6 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks)
       qreg[ks] = qrow < T_ ? gload<u32x4>(qbase + ks * 16, q_lane) : u32x4{0u, 0u, 0u, 0u};
-  }
-
-  // key-tile range of the workgroup (mask-derived prune, absolute tile grid)
-  const int ntiles = static_cast<int>((S_ + C::BN - 1) / C::BN);
-  int kt_lo = 0, kt_hi = ntiles;
-  if (a.masked && a.prune) {
-    const int64_t qlast = (q0 + C::BM - 1 < T_ ? q0 + C::BM - 1 : T_ - 1);
-    if (a.band_hi < INT64_MAX / 4) {
-      const int64_t smax = qlast + a.band_hi;  // last live key of the block
-      kt_hi = smax < 0 ? 0 : static_cast<int>(smax / C::BN + 1 < ntiles ? smax / C::BN + 1 : ntiles);
-    }
-    if (a.band_lo > INT64_MIN / 4) {
-      const int64_t smin = q0 + a.band_lo;  // first live key of the block
-      kt_lo = smin <= 0 ? 0 : static_cast<int>(smin / C::BN);
-    }
-  }
-  // Tiles fully live for every row of the workgroup form one run [kf_lo, kf_hi);
-  // the tiles before it (a window's left edge) and after it (the diagonal, the
-  // key tail) take the masked body.
-  int kf_lo = kt_lo, kf_hi = kt_hi;
-  {
-    const int64_t full_end_keys = S_ / C::BN;
-    kf_hi = kf_hi < full_end_keys ? kf_hi : static_cast<int>(full_end_keys);
-    if (a.masked) {
-      const int64_t qlo = q0, qhi = q0 + C::BM - 1;
-      if (a.band_hi < INT64_MAX / 4) {  // key0 + BN - 1 - qlo <= hi
-        const int64_t lim = qlo + a.band_hi - (C::BN - 1);
-        const int64_t n = lim < 0 ? 0 : lim / C::BN + 1;
-        kf_hi = kf_hi < n ? kf_hi : static_cast<int>(n);
-      }
-      if (a.band_lo > INT64_MIN / 4) {  // key0 - qhi >= lo
-        const int64_t lim = qhi + a.band_lo;
-        const int64_t n = lim <= 0 ? 0 : (lim + C::BN - 1) / C::BN;
-        kf_lo = kf_lo > n ? kf_lo : static_cast<int>(n);
-      }
-    }
-    if (kf_lo > kf_hi) kf_lo = kf_hi = kt_hi;
-  }
-  if (a.nsplit > 1) {  // this split's share of the range; the run boundaries clamp into it
-    const int s_lo = kt_lo + split * a.split_tiles;
-    const int lo2 = s_lo < kt_hi ? s_lo : kt_hi;
-    const int hi2 = s_lo + a.split_tiles < kt_hi ? s_lo + a.split_tiles : kt_hi;
-    kf_lo = kf_lo < lo2 ? lo2 : (kf_lo > hi2 ? hi2 : kf_lo);
-    kf_hi = kf_hi < lo2 ? lo2 : (kf_hi > hi2 ? hi2 : kf_hi);
-    kt_lo = lo2;
-    kt_hi = hi2;
   }
 
   // ---- staging: each wave copies 1 KB blocks of the next K and V tiles
@@ -298,36 +384,64 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
           sacc[i] = a.fill_raw;
       }
     }
-    float mloc = -kInf;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, sacc[i]);
-    {  // the other lane half holds the row's other 16 keys: swap halves in registers
-      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
-      mloc = __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    }
-    mtrue = fmaxf(mtrue, mloc);
-    if (__builtin_amdgcn_ballot_w64((mloc - mused) * a.c2 > kTau) != 0) {
-      const float mnew = fmaxf(mused, mloc);
-      const float alpha = fast_exp2((mused - mnew) * a.c2);
-      mused = mnew;
-      lsum *= alpha;
-#pragma unroll
-      for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
-    }
-    const float mc = mused * a.c2;
+    // exponentials referred to mused, packed as the PV operand; the lane-half's
+    // partial denominator in fp32
     u32x4 p[2];
+    auto expo = [&](float& part) {
+      const float mc = mused * a.c2;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float e[8];
+      for (int h = 0; h < 2; ++h) {
+        float e[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        // Full tiles hold live (bounded) scores: one fma. Masked tiles may hold
-        // fill-level scores equal to the running max, where only (s - m) * c
-        // cancels exactly (a fully-masked row: every p is exp2(0) = 1).
-        e[j] = CUT ? fast_exp2((sacc[8 * h + j] - mused) * a.c2) : fast_exp2(__builtin_fmaf(sacc[8 * h + j], a.c2, -mc));
-        lsum += e[j];  // fp32 probabilities: lse / den keep fp32 accuracy
+        for (int j = 0; j < 8; ++j) {
+          // Full tiles hold live (bounded) scores: one fma. Masked tiles may hold
+          // fill-level scores equal to the running max, where only (s - m) * c
+          // cancels exactly (a fully-masked row: every p is exp2(0) = 1).
+          e[j] = CUT ? fast_exp2((sacc[8 * h + j] - mused) * a.c2) : fast_exp2(__builtin_fmaf(sacc[8 * h + j], a.c2, -mc));
+          part += e[j];  // fp32 probabilities: lse / den keep fp32 accuracy
+        }
+        p[h] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
       }
-      p[h] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
+    };
+    auto rowmax = [&]() {
+      float m = -kInf;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) m = fmaxf(m, sacc[i]);
+      // the other lane half holds the row's other 16 keys: swap halves in registers
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+      return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    };
+    if constexpr (!CUT && !ART) {
+      // A full tile of a launch without the (m, den) artifacts skips the row
+      // max: the exponentials are referred to mused as it stands, and only when
+      // some lane's partial sum leaves (0, 2^kTau] (a row's scores grew by more
+      // than kTau in log2 units, or mused is still -inf) does the wave take the
+      // exact path. lse = mused * scale + log(den) holds for any reference.
+      float part = 0.f;
+      expo(part);
+      if (__builtin_amdgcn_ballot_w64(!(part <= (1 << static_cast<int>(kTau)))) != 0) {
+        const float mnew = fmaxf(mused, rowmax());
+        const float alpha = mnew == mused ? 1.f : fast_exp2((mused - mnew) * a.c2);
+        mused = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
+        part = 0.f;
+        expo(part);
+      }
+      lsum += part;
+    } else {
+      const float mloc = rowmax();
+      mtrue = fmaxf(mtrue, mloc);
+      if (__builtin_amdgcn_ballot_w64((mloc - mused) * a.c2 > kTau) != 0) {
+        const float mnew = fmaxf(mused, mloc);
+        const float alpha = fast_exp2((mused - mnew) * a.c2);
+        mused = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
+      }
+      expo(lsum);
     }
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -370,49 +484,7 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
   sweep(kf_hi, kt_hi, std::true_type{});
   wait_vmcnt0();  // no load may be in flight into LDS when the workgroup exits
 
-  // epilogue: combine the two lane halves' partial denominators, normalize, store
-  const float den = lsum + __shfl_xor(lsum, 32, 64);
-  if (a.nsplit > 1) {  // the partial state, unnormalized, for flash_fwd_combine
-    if (qrow < T_) {
-      const int64_t srow = split * a.plane + inst * T_ + qrow;
-      float* wo = a.ws + srow * D + 4 * g;
-#pragma unroll
-      for (int db = 0; db < C::DB; ++db)
-#pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4)
-          *reinterpret_cast<f32x4*>(wo + db * 32 + a4 * 8) =
-              f32x4{oacc[db][4 * a4 + 0], oacc[db][4 * a4 + 1], oacc[db][4 * a4 + 2], oacc[db][4 * a4 + 3]};
-      if (g == 0) {
-        float* st = a.ws + a.nsplit * a.plane * D;
-        st[srow] = mused;
-        st[a.nsplit * a.plane + srow] = mtrue;
-        st[2 * a.nsplit * a.plane + srow] = den;
-      }
-    }
-    return;
-  }
-  if (qrow < T_) {
-    const float inv = den > 0.f ? 1.0f / den : 0.f;
-    uint16_t* obase = op + static_cast<int64_t>(qw0) * a.o_st;  // wave-uniform
-    const uint32_t o_lane = static_cast<uint32_t>(r32 * a.o_st * 2 + g * 8);
-#pragma unroll
-    for (int db = 0; db < C::DB; ++db) {
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        const int d0 = db * 32 + a4 * 8;  // + 4 g, carried by o_lane
-        const u32x2 wv = {pack2<T>(oacc[db][4 * a4 + 0] * inv, oacc[db][4 * a4 + 1] * inv),
-                          pack2<T>(oacc[db][4 * a4 + 2] * inv, oacc[db][4 * a4 + 3] * inv)};
-        gstore<u32x2>(obase + d0, o_lane, wv);
-      }
-    }
-    if (g == 0) {
-      const int64_t srow = inst * T_ + qrow;
-      // den sums exp(s - mused); the artifacts are referred to the true max
-      if (a.m_out) a.m_out[srow] = mtrue * a.scale;
-      if (a.den_out) a.den_out[srow] = den * fast_exp2((mused - mtrue) * a.c2);
-      if (a.lse_out) a.lse_out[srow] = mused * a.scale + __logf(den);
-    }
-  }
+  fwd_store<T, D>(a, inst, split, qw0, r32, g, op, oacc, mused, ART ? mtrue : mused, lsum);
 }
 
 // ---------------------------------------------------------------- generic fp32
@@ -557,6 +629,15 @@ bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
   return false;
 }
 
+
+template <typename T, int D>
+void fwd_kernel(const FwdArgs& a, unsigned nblocks, hipStream_t st) {
+  if (a.m_out || a.den_out)
+    flash_fwd_mfma<T, D, true><<<dim3(nblocks), FwdCfg<D>::THREADS, 0, st>>>(a);
+  else
+    flash_fwd_mfma<T, D, false><<<dim3(nblocks), FwdCfg<D>::THREADS, 0, st>>>(a);
+}
+
 template <typename T, int D>
 int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
   using C = FwdCfg<D>;
@@ -569,7 +650,7 @@ int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
     aa.split_tiles = static_cast<int>((ntiles + a.nsplit - 1) / a.nsplit);
     aa.xcd_remap = 0;
     PDH_REQUIRE(nblk * a.nsplit <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd_split: grid too large");
-    flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk * a.nsplit)), C::THREADS, 0, st>>>(aa);
+    fwd_kernel<T, D>(aa, static_cast<unsigned>(nblk * a.nsplit), st);
     int rc = check_launch("pdh_flash_fwd_split");
     if (rc) return rc;
     const int64_t nthr = a.plane * (D / 4);
@@ -578,7 +659,7 @@ int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
     return check_launch("pdh_flash_fwd_split (combine)");
   }
   aa.xcd_remap = (nblk % 8 == 0) ? ((ninst % 32 == 0) ? 2 : 1) : 0;
-  flash_fwd_mfma<T, D><<<dim3(static_cast<unsigned>(nblk)), C::THREADS, 0, st>>>(aa);
+  fwd_kernel<T, D>(aa, static_cast<unsigned>(nblk), st);
   return check_launch("pdh_flash_fwd");
 }
 
