@@ -457,32 +457,38 @@ __device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned cha
       const unsigned char* q_l = qbuf(buf, sub);
       const unsigned char* o_l = obuf(buf, sub);
       const float* stl = sbuf(buf, sub);
+      // accumulator i of lane-half g: query q0 + 16 (i / 8) + 8 g + i % 8, key krow.
+      // dP - delta accumulates from the rows' -delta (the MFMA adds it).
+      f32x16 sacc = f32x16{}, pacc;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int rb = 16 * hh + 8 * g;
+        const f32x4 d0 = *reinterpret_cast<const f32x4*>(stl + rb);  // -delta
+        const f32x4 d1 = *reinterpret_cast<const f32x4*>(stl + rb + 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pacc[8 * hh + j] = j < 4 ? d0[j] : d1[j - 4];
+      }
       __builtin_amdgcn_s_setprio(1);
-      f32x16 sacc = f32x16{}, pacc = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         sacc = mfma32<T>(ql.row_frag(q_l, ks), kreg[ks], sacc);
         pacc = mfma32<T>(ol.row_frag(o_l, ks), vreg[ks], pacc);
       }
       __builtin_amdgcn_s_setprio(0);
-      // accumulator i of lane-half g: query q0 + 16 (i / 8) + 8 g + i % 8, key krow;
       // masks in 32-bit offsets from the tile (band limits clamped to +-2^30)
       const int dk0 = static_cast<int>(krow - q0);
       const int qlim = krow < S_ ? static_cast<int>(T_ - q0 < (1 << 30) ? T_ - q0 : (1 << 30)) : 0;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int rb = 16 * hh + 8 * g;
-        const f32x4 d0 = *reinterpret_cast<const f32x4*>(stl + rb);  // -delta
-        const f32x4 d1 = *reinterpret_cast<const f32x4*>(stl + rb + 4);
         const f32x4 l0 = *reinterpret_cast<const f32x4*>(stl + QT + rb);
         const f32x4 l1 = *reinterpret_cast<const f32x4*>(stl + QT + rb + 4);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int i = 8 * hh + j;
           const float lv = j < 4 ? l0[j] : l1[j - 4];
-          const float ndv = j < 4 ? d0[j] : d1[j - 4];
           const float p = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lv));
-          pacc[i] = p * (pacc[i] + ndv);
+          pacc[i] = p * pacc[i];
           sacc[i] = p;
         }
       }
