@@ -114,6 +114,44 @@ def _check_fwd(res, q, k, v, scale, band, lowp):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize(
+    "B,Hq,Hkv,T,S,D,causal,growth",
+    [
+        (1, 2, 2, 256, 256, 128, True, 1.0),
+        (1, 2, 1, 77, 333, 64, False, 1.0),
+        (2, 4, 4, 128, 1024, 128, False, 1.0),
+        # key rows scaled up along the key axis: a row's scores keep outgrowing
+        # the running reference by far more than 2^8, so full tiles take the
+        # exact path (row max, rescale, exponentials again) over and over
+        (1, 2, 2, 512, 512, 128, True, 6.0),
+        (1, 2, 2, 64, 2048, 128, False, 6.0),
+        (1, 2, 2, 300, 700, 64, False, 6.0),
+    ],
+)
+def test_the_lse_only_forward_matches_the_oracle_and_the_artifact_launch(K, dtype, B, Hq, Hkv, T, S, D, causal, growth):
+    """A launch without the (m, den) artifacts refers full tiles' exponentials
+    to the running reference without a per-tile row max and takes the exact
+    path only when a lane's partial sum leaves (0, 2^8]. Its o and lse must
+    match the float64 closed form and the launch that keeps the max on every
+    tile (the reference's recurrence, fusion.py:542-615)."""
+    rng = np.random.default_rng(B * 100 + T + S + D + int(growth))
+    q = _dev(rng.standard_normal((B, Hq, T, D)), dtype)
+    ramp = 1.0 + (growth - 1.0) * np.linspace(0.0, 1.0, S)[:, None]  # key s scaled by 1 .. growth
+    k = _dev(rng.standard_normal((B, Hkv, S, D)) * ramp, dtype)
+    v = _dev(rng.standard_normal((B, Hkv, S, D)), dtype)
+    band = (None, 0) if causal else None
+    scale = 1.0 / np.sqrt(D)
+    kb = K.Band(*band) if band else None
+    lse_only = K.flash_fwd(q, k, v, scale=scale, band=kb)
+    full = K.flash_fwd(q, k, v, scale=scale, band=kb, want_artifacts=True)
+    torch.cuda.synchronize()
+    assert lse_only.m is None and full.m is not None
+    _check_fwd(lse_only, q, k, v, scale, band, lowp=True)
+    assert_lowp(_host(lse_only.o), _host(full.o), what="lse-only vs artifact launch: out")
+    np.testing.assert_allclose(_host(lse_only.lse), _host(full.lse), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(
     "B,Hq,Hkv,T,S,D,causal",
     [
         (1, 2, 2, 128, 128, 128, True),
