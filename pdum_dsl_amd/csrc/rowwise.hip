@@ -127,48 +127,66 @@ __global__ __launch_bounds__(256) void softmax_rows_v4(const void* __restrict__ 
   }
 }
 
-template <int DT, int NV, bool AFFINE>
+// RPW rows per wave: the affine epilogue reads each gamma / beta chunk once for
+// all of them (those reads come from L2 and, one row per wave, add as many L2
+// bytes again as the row itself). Two rows per wave for rows of 2048+ columns:
+// +5.6% on [8192, 4096] fp32 (5.43 -> 5.73 TB/s, same process), at 172 VGPRs.
+template <int DT, int NV, bool AFFINE, int RPW = 1>
 __global__ __launch_bounds__(256) void layernorm_rows_v4(const void* __restrict__ x, const void* __restrict__ gamma,
                                                          const void* __restrict__ beta, void* __restrict__ y,
                                                          int64_t rows, int cols, int64_t ldx, int64_t ldy,
                                                          float eps) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const void* xr = row_at<DT>(x, row, ldx);
-  void* yr = row_at<DT>(y, row, ldy);
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6)) * RPW;
+  if (row0 >= rows) return;
   const int nvec = cols >> 2;
-  f32x4 v[NV];
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int idx = j * 64 + lane;
-    v[j] = idx < nvec ? ld4<DT>(xr, idx) : f32x4{0.f, 0.f, 0.f, 0.f};
-    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-  }
   const float inv_n = 1.0f / static_cast<float>(cols);
-  const float mu = wave_sum(s) * inv_n;
-  float ss = 0.f;
+  f32x4 v[RPW][NV];
+  float mu[RPW], rstd[RPW];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int idx = j * 64 + lane;
-    if (idx < nvec) {
-      v[j] -= mu;
-      ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+  for (int r = 0; r < RPW; ++r) {
+    const bool live = row0 + r < rows;
+    const void* xr = row_at<DT>(x, live ? row0 + r : row0, ldx);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int idx = j * 64 + lane;
+      v[r][j] = idx < nvec ? ld4<DT>(xr, idx) : f32x4{0.f, 0.f, 0.f, 0.f};
+      s += (v[r][j].x + v[r][j].y) + (v[r][j].z + v[r][j].w);
     }
+    mu[r] = wave_sum(s) * inv_n;
   }
-  const float var = wave_sum(ss) * inv_n;
-  const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int idx = j * 64 + lane;
+      if (idx < nvec) {
+        v[r][j] -= mu[r];
+        ss += (v[r][j].x * v[r][j].x + v[r][j].y * v[r][j].y) + (v[r][j].z * v[r][j].z + v[r][j].w * v[r][j].w);
+      }
+    }
+    const float var = wave_sum(ss) * inv_n;
+    rstd[r] = 1.0f / sqrtf(var + eps);
+  }
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int idx = j * 64 + lane;
     if (idx < nvec) {
-      f32x4 o = v[j] * rstd;
+      f32x4 gm = f32x4{1.f, 1.f, 1.f, 1.f}, bt = f32x4{0.f, 0.f, 0.f, 0.f};
       if (AFFINE) {
-        if (gamma) o *= ld4_cached<DT>(gamma, idx);
-        if (beta) o += ld4_cached<DT>(beta, idx);
+        if (gamma) gm = ld4_cached<DT>(gamma, idx);
+        if (beta) bt = ld4_cached<DT>(beta, idx);
       }
-      st4<DT>(yr, idx, o);
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        if (row0 + r < rows) {
+          f32x4 o = v[r][j] * rstd[r];
+          if (AFFINE) o = o * gm + bt;
+          st4<DT>(row_at<DT>(y, row0 + r, ldy), idx, o);
+        }
+      }
     }
   }
 }
@@ -299,12 +317,16 @@ void launch_layernorm(const void* x, const void* gamma, const void* beta, void* 
     const dim3 grid(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
     const int c = static_cast<int>(cols);
     const bool aff = gamma || beta;
-#define PDH_LN(NV)                                                                                       \
-  do {                                                                                                   \
-    if (aff)                                                                                             \
-      layernorm_rows_v4<DT, NV, true><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, c, ldx, ldy, eps);  \
-    else                                                                                                 \
-      layernorm_rows_v4<DT, NV, false><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, c, ldx, ldy, eps); \
+    // affine rows of 2048+ columns: two rows per wave share the gamma / beta reads
+    const dim3 grid2(static_cast<unsigned>((rows + 2 * kRowsPerBlock - 1) / (2 * kRowsPerBlock)));
+#define PDH_LN(NV)                                                                                          \
+  do {                                                                                                      \
+    if (aff && NV >= 8)                                                                        \
+      layernorm_rows_v4<DT, NV, true, 2><<<grid2, 256, 0, s>>>(x, gamma, beta, y, rows, c, ldx, ldy, eps); \
+    else if (aff)                                                                                           \
+      layernorm_rows_v4<DT, NV, true><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, c, ldx, ldy, eps);     \
+    else                                                                                                    \
+      layernorm_rows_v4<DT, NV, false><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, c, ldx, ldy, eps);    \
   } while (0)
     switch (pick_nv(cols)) {
       case 1: PDH_LN(1); break;
