@@ -72,7 +72,9 @@ def test_row_softmax_strided_rows(K):
 
 
 @pytest.mark.parametrize("affine", [False, True])
-@pytest.mark.parametrize("rows,cols", [(4, 4), (33, 768), (64, 4096), (3, 5000), (7, 129)])
+@pytest.mark.parametrize(
+    "rows,cols", [(4, 4), (33, 768), (64, 4096), (3, 5000), (7, 129), (7, 4096), (1, 2048), (9, 2048)]
+)
 def test_layernorm_matches_oracle(K, rows, cols, affine):
     rng = np.random.default_rng(rows + 31 * cols)
     x = rng.standard_normal((rows, cols)) + 0.5
@@ -83,6 +85,22 @@ def test_layernorm_matches_oracle(K, rows, cols, affine):
     f = lambda a: None if a is None else a.astype(np.float32).astype(np.float64)  # noqa: E731
     want = cf.np_layernorm(f(x), f(g), f(b), eps=1e-5)
     assert_fp32(_host(y), want, rtol=1e-5, atol=1e-5, what=f"layernorm {rows}x{cols}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,cols", [(7, 4096), (8, 2048), (33, 768)])
+def test_layernorm_16bit_storage_matches_oracle(K, dtype, rows, cols):
+    """bf16 / f16 storage, fp32 arithmetic: odd and even row counts through the
+    one- and two-rows-per-wave kernels, against the float64 oracle on the same
+    rounded inputs."""
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = _dev(rng.standard_normal((rows, cols)) + 0.5, dtype)
+    g = _dev(1 + 0.1 * rng.standard_normal(cols), dtype)
+    b = _dev(0.1 * rng.standard_normal(cols), dtype)
+    y = K.layernorm(x, g, b, eps=1e-5)
+    torch.cuda.synchronize()
+    want = cf.np_layernorm(_host(x), _host(g), _host(b), eps=1e-5)
+    assert_lowp(_host(y), want, what=f"layernorm {dtype} {rows}x{cols}")
 
 
 # ---------------------------------------------------------- flash forward
