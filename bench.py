@@ -47,7 +47,7 @@ def _args():
 
 
 COPY_PROBE_BYTES = 256 << 20  # bytes read (and bytes written) by one calibration copy
-PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "flash_fwd_mfma_c3_pmc.md")
+PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "flash_fwd_m16_c3_pmc.md")
 
 
 def measured_traffic():
@@ -173,7 +173,7 @@ def main():
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "flash_fwd_mfma<bf16,128>",
+            "kernel": "flash_fwd_m16<bf16,128>",
             "bound": "mfma",
             "achieved": round(tflops, 2),
             "peak": PEAK_BF16_TFLOPS,

@@ -75,23 +75,6 @@ __device__ __forceinline__ uint32_t perm_halves(uint32_t hi_src, uint32_t lo_src
 
 __device__ __forceinline__ int swap_bits23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
-// K rows are read as MFMA A operands, lane l reading row swap_bits23(l % 32)
-// (see kperm_inv) at one 16-byte chunk: rows {0..3, 8..11} (8 lanes) and
-// rows 0..15 (16 lanes) land on distinct 16-byte bank groups.
-template <int D>
-__device__ __forceinline__ int swz_k(int row) {
-  return swap_bits23(row & 15) & (D / 8 - 1);
-}
-
-// V rows are read with ds_read_b64_tr_b16: each 16-lane group reads 4
-// consecutive rows x 32 contiguous bytes (two slots). These masks spread the
-// 4 rows' slot pairs over distinct banks for 32- and 64-bank LDS.
-template <int D>
-__device__ __forceinline__ int swz_v(int row) {
-  const int kk = row & 3;
-  return D == 128 ? ((kk << 2) ^ ((kk >> 1) << 1)) : (kk << 1);
-}
-
 // Tiles read BOTH as rows (b128 A operands, lane row swap_bits23(l % 32)) and
 // transposed (ds_read_b64_tr_b16) — the backward's Q / dO / K tiles — use one
 // table per row % 16, found by exhaustive check to keep both read patterns

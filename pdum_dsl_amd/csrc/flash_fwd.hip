@@ -9,12 +9,12 @@
 //   * K and V tiles go HBM -> LDS by direct buffer loads (no VGPR staging, no
 //     LDS write instructions) into unpadded rows whose 16-byte slots are
 //     XOR-swizzled so every operand read is bank-conflict free;
-//   * scores are computed TRANSPOSED, S^T = K Q^T with v_mfma_f32_32x32x16,
-//     so lane l owns query row (l % 32): the running max / denominator live in
-//     registers and the row max needs one cross-half shuffle per tile. Lane l
-//     reads K row swap_bits23(l % 32), which makes the S^T accumulators of a
-//     lane-half exactly the B operand (8 consecutive keys) of O^T += V^T P^T —
-//     no register shuffles between the two contractions;
+//   * scores are computed TRANSPOSED, S^T = K Q^T with v_mfma_f32_16x16x32
+//     (the matrix cores' faster shape on gfx950): lane 16 G + c owns query
+//     rows c and 16 + c of its wave's 32, so the running max / denominator
+//     live in registers; its eight keys of each 32-key tile are exactly the
+//     B operand of O^T += V^T P^T (no register shuffles between the two
+//     contractions; see the 16x16x32 section below);
 //   * V stays row-major in LDS and is read transposed by ds_read_b64_tr_b16;
 //     the LDS array is static and the key-tile loop runs in buffer pairs, so
 //     every operand read is a lane offset plus an immediate (no per-tile
@@ -25,17 +25,16 @@
 //     exponentials are referred to the running reference, and a tile takes
 //     the exact path (row max, rescale, exponentials again) only when a lane's
 //     partial sum leaves (0, 2^8]. On gfx950 VALU work adds to MFMA time
-//     almost one for one once the matrix pipe is busy (only ~4 VALU
-//     instructions hide under each 32x32x16 product), so every VALU
-//     instruction taken out of the tile body is time saved;
+//     almost one for one once the matrix pipe is busy, so every VALU
+//     instruction taken out of the tile body is time saved (a full tile is
+//     32 products and 60 other VALU instructions per wave);
 //   * causal / band masks prune dead tiles (the mask-derived bounds of
 //     fusion.py:659-690) and mask only the tiles the band cuts;
 //   * heavy (late) query blocks launch first, and the workgroup index is
 //     remapped so each XCD works through whole (batch, head) instances — the
-//     instance's K/V stays in that XCD's L2 — and, when instances come in
-//     multiples of 32, each of an XCD's four shader engines receives the same
-//     sequence of block lengths (in-order dispatch then never stalls on an
-//     engine that drew the heavier blocks).
+//     instance's K/V stays in that XCD's L2 — taking an instance's blocks in
+//     groups of four of alternating direction, so each of an XCD's four
+//     shader engines receives the same total work.
 //
 // Generic fp32 kernel (any e, od, t, s): one wave per query row, keys in
 // chunks of 64 (one per lane), the same recurrence in fp32 — the column the
@@ -74,26 +73,9 @@ struct FwdArgs {
   int nsplit, split_tiles;
   float* ws;      // [nsplit][plane][D] partial o, then [3][nsplit][plane] mused, mtrue, den
   int64_t plane;  // instances * t: rows per split
-};
-
-template <int D>
-struct FwdCfg {
-  static constexpr int WAVES = 4;
-  static constexpr int THREADS = 64 * WAVES;
-  static constexpr int BM = 32 * WAVES;          // query rows per workgroup (32 per wave)
-  static constexpr int BN = 32;                  // keys per tile
-  static constexpr int ROWB = D * 2;             // LDS bytes per key row (swizzled, unpadded)
-  static constexpr int CPR = D / 8;              // 16-byte chunks per row
-  static constexpr int TILEB = BN * ROWB;        // one K or V tile
-  static constexpr int KBUF = 0, VBUF = 2 * TILEB;
-  static constexpr int LDS = 4 * TILEB;          // K and V, double buffered: 32 KB at D = 128
-  static constexpr int RPK = 1024 / ROWB;        // rows per 1 KB direct-load block
-  static constexpr int NBLK = TILEB / 1024;      // 1 KB blocks per tile
-  static constexpr int NDMA = (NBLK + WAVES - 1) / WAVES;
-  static constexpr int KS = D / 16;              // k-steps of Q K^T
-  static constexpr int DB = D / 32;              // 32-feature blocks of O
-  static constexpr int NPV = 2 * DB;             // (16-key step, feature block) operands of P V
-  static constexpr int PF = 3;                   // V operands in flight ahead of their MFMA
+  // the band clamped to +-(2^29 + 64): with t, s <= 2^29 every key - row
+  // difference compares the same against these as against the 64-bit band
+  int band_lo32, band_hi32;
 };
 
 // Lazy rescaling: the running max used for the exponentials only moves when a
@@ -124,18 +106,20 @@ __device__ __forceinline__ BlockPlan block_plan(const FwdArgs& a) {
   }
   int64_t inst;
   int qb;
-  if (a.xcd_remap == 2) {
-    // Workgroups are dispatched round-robin over the 8 XCDs (bid % 8) and,
-    // within an XCD, in order round-robin over its 4 shader engines (r % 4).
-    // Each group of four consecutive r takes the same query block of four
-    // instances, so every engine receives the same sequence of workgroup
-    // lengths (heavy first) and in-order dispatch never waits on an engine
-    // that drew the heavier blocks; an XCD still works through whole
-    // instances, whose K / V stay in its L2.
-    const int x = bid & 7, r = bid >> 3, s4 = r & 3, m4 = r >> 2;
-    const int64_t ipx = static_cast<int64_t>(gridDim.x >> 3) / a.nqb;  // instances per XCD
-    inst = x * ipx + static_cast<int64_t>(m4 / a.nqb) * 4 + s4;
-    qb = a.nqb - 1 - (m4 % a.nqb);
+  if (a.xcd_remap == 3) {
+    // Workgroups are dispatched round-robin over the 8 XCDs (bid % 8); each
+    // XCD works through whole instances, heavy query blocks first. Its
+    // workgroups go round-robin to its four shader engines (r % 4), so the
+    // blocks are taken in groups of four whose direction alternates (31 30
+    // 29 28, 24 25 26 27, 23 ...): over an instance every engine then draws
+    // the same total work, and the XCD's L2 holds the K / V of the few
+    // instances it is sweeping.
+    const int per = gridDim.x >> 3;
+    const int x = bid & 7, r = bid >> 3;
+    const int64_t lin = static_cast<int64_t>(x) * per + r;
+    inst = lin / a.nqb;
+    const int j = static_cast<int>(lin % a.nqb), grp = j >> 2, e = j & 3;
+    qb = a.nqb - 1 - (4 * grp + ((grp & 1) ? 3 - e : e));
   } else {
     if (a.xcd_remap) {
       const int per = gridDim.x >> 3;
@@ -195,74 +179,122 @@ __device__ __forceinline__ BlockPlan block_plan(const FwdArgs& a) {
   return BlockPlan{inst, qb, split, kt_lo, kt_hi, kf_lo, kf_hi};
 }
 
-// Stores a wave's 32 query rows: o = oacc / den and the optional m, den and lse
-// rows, or, for a split launch, the unnormalized partial state that
-// flash_fwd_combine merges. lsum is this lane-half's share of the row's
-// denominator; mused the max the exponentials are referred to, mtrue the true
-// running max (the m artifact).
+// ------------------------------------------------ 16x16x32 MFMA forward
+//
+// The same sweep on v_mfma_f32_16x16x32 products. A wave still owns 32 query
+// rows, as two 16-row halves: lane l = 16 G + c owns query rows c and 16 + c
+// of the wave's 32, and within each 32-key tile the keys {4G .. 4G+3} and
+// {16+4G .. 16+4G+3}. Those eight keys are exactly the B operand (k = 8G + j)
+// of O^T += V^T P^T once the k index j is read as key 4G + j (j < 4) or
+// 16 + 4G + j - 4 (j >= 4); the V operand follows the same k order, which the
+// transposed LDS read gives for free (each 16-lane group names its own four
+// rows). So, as in the 32x32x16 kernel, the score accumulators feed the
+// second product with no register shuffle.
+
+template <int D>
+struct F16Cfg {
+  static constexpr int WAVES = 4;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int BM = 32 * WAVES;    // query rows per workgroup (32 per wave)
+  static constexpr int BN = 32;            // keys per tile
+  static constexpr int ROWB = D * 2;       // LDS bytes per key row (swizzled, unpadded)
+  static constexpr int CPR = D / 8;        // 16-byte chunks per row
+  static constexpr int TILEB = BN * ROWB;  // one K or V tile
+  static constexpr int KBUF = 0, VBUF = 2 * TILEB;
+  static constexpr int LDS = 4 * TILEB;    // K and V, double buffered: 32 KB at D = 128
+  static constexpr int RPK = 1024 / ROWB;  // rows per 1 KB direct-load block
+  static constexpr int NBLK = TILEB / 1024;
+  static constexpr int NDMA = (NBLK + WAVES - 1) / WAVES;
+  static constexpr int KS = D / 32;        // k-steps of Q K^T (32 features each)
+  static constexpr int FB = D / 16;        // 16-feature blocks of O
+  static constexpr int PF = 2;             // V operands in flight ahead of their MFMA
+  static constexpr int KPF = 3;            // K operands in flight
+};
+
+// K rows are read as A operands: lanes 16 G + c read row c (of a 16-row
+// half) at chunk 4 ks + G. XOR masks that put the 16 rows of one chunk on 16
+// distinct 16-byte bank groups (64 banks), and any 8 consecutive rows on 8
+// (32 banks). At D = 64 two rows share 256 bytes.
+template <int D>
+__device__ __forceinline__ int swz16_k(int row) {
+  return D == 128 ? (row & 15) : ((row & 7) ^ ((row >> 3) & 1));
+}
+
+// V rows are read with ds_read_b64_tr_b16: 16-lane group G reads rows
+// 4G .. 4G+3 (and 16 + those), 32 contiguous bytes each (two slots). Even
+// masks keep a slot pair adjacent; lanes 0-31 (rows 0-7) then cover all 64
+// banks, and each group's four rows distinct banks of 32.
+template <int D>
+__device__ __forceinline__ int swz16_v(int row) {
+  return D == 128 ? 2 * (row & 7) : 2 * ((row & 3) ^ ((row >> 2) & 1));
+}
+
+// Row-wise combine across the four 16-lane groups (v_permlane32_swap and
+// v_permlane16_swap exchange lane l with l ^ 32 and l ^ 16).
+__device__ __forceinline__ float max4g(float m) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  m = __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return __builtin_fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
+__device__ __forceinline__ float sum4g(float v) {
+  v += __shfl_xor(v, 32, 64);
+  return v + __shfl_xor(v, 16, 64);
+}
+
+// Stores a wave's 32 query rows (two halves of 16) from the 16x16 layout:
+// o = oacc / den and the optional m, den and lse rows, or, for a split
+// launch, the unnormalized partial state flash_fwd_combine merges.
 template <typename T, int D>
-__device__ __forceinline__ void fwd_store(const FwdArgs& a, int64_t inst, int split, int qw0, int r32, int g,
-                                          uint16_t* op, const f32x16 (&oacc)[D / 32], float mused, float mtrue,
-                                          float lsum) {
-  constexpr int DB = D / 32;
+__device__ __forceinline__ void fwd16_store(const FwdArgs& a, int64_t inst, int split, int qw0, int c, int G,
+                                            uint16_t* op, const f32x4 (&oacc)[D / 16][2], const float (&mused)[2],
+                                            const float (&mtrue)[2], const float (&lsum)[2]) {
+  constexpr int FB = D / 16;
   const int64_t T_ = a.t;
-  const int qrow = qw0 + r32;
-  // combine the two lane halves' partial denominators, normalize, store
-  const float den = lsum + __shfl_xor(lsum, 32, 64);
-  if (a.nsplit > 1) {  // the partial state, unnormalized, for flash_fwd_combine
-    if (qrow < T_) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int qrow = qw0 + 16 * h + c;
+    const float den = sum4g(lsum[h]);
+    if (qrow >= T_) continue;
+    if (a.nsplit > 1) {  // the partial state, unnormalized, for flash_fwd_combine
       const int64_t srow = split * a.plane + inst * T_ + qrow;
-      float* wo = a.ws + srow * D + 4 * g;
+      float* wo = a.ws + srow * D + 4 * G;
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4)
-          *reinterpret_cast<f32x4*>(wo + db * 32 + a4 * 8) =
-              f32x4{oacc[db][4 * a4 + 0], oacc[db][4 * a4 + 1], oacc[db][4 * a4 + 2], oacc[db][4 * a4 + 3]};
-      if (g == 0) {
+      for (int fb = 0; fb < FB; ++fb) *reinterpret_cast<f32x4*>(wo + 16 * fb) = oacc[fb][h];
+      if (G == 0) {
         float* st = a.ws + a.nsplit * a.plane * D;
-        st[srow] = mused;
-        st[a.nsplit * a.plane + srow] = mtrue;
+        st[srow] = mused[h];
+        st[a.nsplit * a.plane + srow] = mtrue[h];
         st[2 * a.nsplit * a.plane + srow] = den;
       }
+      continue;
     }
-    return;
-  }
-  if (qrow < T_) {
     const float inv = den > 0.f ? 1.0f / den : 0.f;
-    uint16_t* obase = op + static_cast<int64_t>(qw0) * a.o_st;  // wave-uniform
-    const uint32_t o_lane = static_cast<uint32_t>(r32 * a.o_st * 2 + g * 8);
+    uint16_t* obase = op + static_cast<int64_t>(qw0 + 16 * h) * a.o_st;  // wave-uniform
+    const uint32_t o_lane = static_cast<uint32_t>(c * a.o_st * 2 + G * 8);
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        const int d0 = db * 32 + a4 * 8;  // + 4 g, carried by o_lane
-        const u32x2 wv = {pack2<T>(oacc[db][4 * a4 + 0] * inv, oacc[db][4 * a4 + 1] * inv),
-                          pack2<T>(oacc[db][4 * a4 + 2] * inv, oacc[db][4 * a4 + 3] * inv)};
-        gstore<u32x2>(obase + d0, o_lane, wv);
-      }
+    for (int fb = 0; fb < FB; ++fb) {
+      const f32x4 x = oacc[fb][h];
+      gstore<u32x2>(obase + 16 * fb, o_lane, u32x2{pack2<T>(x[0] * inv, x[1] * inv), pack2<T>(x[2] * inv, x[3] * inv)});
     }
-    if (g == 0) {
+    if (G == 0) {
       const int64_t srow = inst * T_ + qrow;
-      // den sums exp(s - mused); the artifacts are referred to the true max
-      if (a.m_out) a.m_out[srow] = mtrue * a.scale;
-      if (a.den_out) a.den_out[srow] = den * fast_exp2((mused - mtrue) * a.c2);
-      if (a.lse_out) a.lse_out[srow] = mused * a.scale + __logf(den);
+      if (a.m_out) a.m_out[srow] = mtrue[h] * a.scale;
+      if (a.den_out) a.den_out[srow] = den * fast_exp2((mused[h] - mtrue[h]) * a.c2);
+      if (a.lse_out) a.lse_out[srow] = mused[h] * a.scale + __logf(den);
     }
   }
 }
 
 template <typename T, int D, bool ART>
-__global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs a) {
-  using C = FwdCfg<D>;
-  // a static LDS array: its address is fixed when the kernel is compiled, so
-  // every operand read folds its buffer base into the immediate offset
+__global__ __launch_bounds__(F16Cfg<D>::THREADS, 3) void flash_fwd_m16(FwdArgs a) {
+  using C = F16Cfg<D>;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS];
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), c = lane & 15, G = lane >> 4;
 
   const BlockPlan bp = block_plan<C::BM, C::BN>(a);
   const int64_t inst = bp.inst;
-  const int qb = bp.qb, split = bp.split;
   const int kt_lo = bp.kt_lo, kt_hi = bp.kt_hi, kf_lo = bp.kf_lo, kf_hi = bp.kf_hi;
   const int64_t b = inst / a.heads_q, hq = inst % a.heads_q;
   const int64_t hk = hq / (a.heads_q / a.heads_kv);
@@ -270,34 +302,36 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
   const uint16_t* kp = static_cast<const uint16_t*>(a.k) + b * a.k_sb + hk * a.k_sh;
   const uint16_t* vp = static_cast<const uint16_t*>(a.v) + b * a.v_sb + hk * a.v_sh;
   uint16_t* op = static_cast<uint16_t*>(a.o) + b * a.o_sb + hq * a.o_sh;
-  const int64_t T_ = a.t, S_ = a.s;
-  const int q0 = qb * C::BM;
-  const int qw0 = q0 + 32 * w;  // this wave's first row
-  const int qrow = qw0 + r32;   // this lane's row
+  // sequence lengths are bounded by 2^29 on the host: row / key arithmetic is 32-bit
+  const int T_ = static_cast<int>(a.t), S_ = static_cast<int>(a.s);
+  const int qw0 = bp.qb * C::BM + 32 * w;  // this wave's first row
+  const int qr0 = qw0 + c, qr1 = qw0 + 16 + c;
 
-  // Q as the B operand of S^T = K Q^T: lane holds q[row][16 ks + 8 g .. +8]
-  u32x4 qreg[C::KS];
+  // Q as the B operand of S^T = K Q^T: lane holds q[row h][32 ks + 8 G .. +8]
+  u32x4 qreg[2][C::KS];
   {
     const uint16_t* qbase = qp + static_cast<int64_t>(qw0) * a.q_st;  // wave-uniform
-    const uint32_t q_lane = static_cast<uint32_t>(r32 * a.q_st * 2 + g * 16);
+    const uint32_t q_lane = static_cast<uint32_t>(c * a.q_st * 2 + G * 16);
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks)
-      qreg[ks] = qrow < T_ ? gload<u32x4>(qbase + ks * 16, q_lane) : u32x4{0u, 0u, 0u, 0u};
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks)
+        qreg[h][ks] = (h ? qr1 : qr0) < T_ ? gload<u32x4>(qbase + 16 * h * a.q_st + ks * 32, q_lane)
+                                           : u32x4{0u, 0u, 0u, 0u};
   }
 
-  // ---- staging: each wave copies 1 KB blocks of the next K and V tiles
-  // straight into LDS; rows past the last key read as zero (buffer range check)
+  // ---- staging: 1 KB direct-load blocks; rows past the last key read as zero
   const uint32_t grk = static_cast<uint32_t>(a.k_st * 2), grv = static_cast<uint32_t>(a.v_st * 2);
-  const rsrc_t kr = make_rsrc(kp, static_cast<uint32_t>((S_ - 1) * a.k_st * 2 + D * 2));
-  const rsrc_t vr = make_rsrc(vp, static_cast<uint32_t>((S_ - 1) * a.v_st * 2 + D * 2));
-  const int lrow = lane / C::CPR, slot = lane % C::CPR;  // row within a 1 KB block, 16-byte slot
-  uint32_t dk[C::NDMA];
+  const rsrc_t kr = make_rsrc(kp, static_cast<uint32_t>((a.s - 1) * a.k_st * 2 + D * 2));
+  const rsrc_t vr = make_rsrc(vp, static_cast<uint32_t>((a.s - 1) * a.v_st * 2 + D * 2));
+  const int lrow = lane / C::CPR, slot = lane % C::CPR;
+  uint32_t dk[C::NDMA], dv[C::NDMA];
 #pragma unroll
   for (int i = 0; i < C::NDMA; ++i) {
     const int rho = (i * C::WAVES + w) * C::RPK + lrow;
-    dk[i] = lrow * grk + ((slot ^ swz_k<D>(rho)) << 4);
+    dk[i] = lrow * grk + ((slot ^ swz16_k<D>(rho)) << 4);
+    dv[i] = lrow * grv + ((slot ^ swz16_v<D>(rho)) << 4);
   }
-  const uint32_t dv = lrow * grv + ((slot ^ swz_v<D>(lrow)) << 4);  // RPK is a multiple of 4
   auto stage = [&](int tile, int buf) {
 #pragma unroll
     for (int i = 0; i < C::NDMA; ++i) {
@@ -305,168 +339,157 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
       if (C::NBLK % C::WAVES != 0 && blk >= C::NBLK) break;
       const uint32_t row0 = static_cast<uint32_t>(tile * C::BN + blk * C::RPK);
       dma16(kr, smem + C::KBUF + buf * C::TILEB + blk * 1024, dk[i], row0 * grk);
-      dma16(vr, smem + C::VBUF + buf * C::TILEB + blk * 1024, dv, row0 * grv);
+      dma16(vr, smem + C::VBUF + buf * C::TILEB + blk * 1024, dv[i], row0 * grv);
     }
   };
 
-  // ---- per-lane operand offsets (tile and buffer parts are immediates)
-  int ka[C::KS];  // K row swap_bits23(r32), chunk 2 ks + g
-  {
-    const int row = swap_bits23(r32);
+  // ---- per-lane operand offsets (tile, buffer and 16-row half are immediates)
+  int ka[C::KS];  // K row c, chunk 4 ks + G
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) ka[ks] = row * C::ROWB + (((2 * ks + g) ^ swz_k<D>(row)) << 4);
-  }
-  int va[C::DB];  // transposed V reads: rows 8 (G / 2) + kk (+16 s + 4 h), features 32 db + 16 (G % 2) + 4 c
+  for (int ks = 0; ks < C::KS; ++ks) ka[ks] = c * C::ROWB + (((4 * ks + G) ^ swz16_k<D>(c)) << 4);
+  int va[C::FB];  // transposed V reads: row 4 G + k4 (+ 16), features 16 fb + 4 cc .. + 3
   {
-    const int G = lane >> 4, kk = (lane >> 2) & 3, c4 = lane & 3;
+    const int k4 = (lane >> 2) & 3, cc = lane & 3, row = 4 * G + k4;
 #pragma unroll
-    for (int db = 0; db < C::DB; ++db)
-      va[db] = (8 * (G >> 1) + kk) * C::ROWB + (((4 * db + 2 * (G & 1) + (c4 >> 1)) ^ swz_v<D>(kk)) << 4) +
-               ((c4 & 1) << 3);
+    for (int fb = 0; fb < C::FB; ++fb)
+      va[fb] = row * C::ROWB + (((2 * fb + (cc >> 1)) ^ swz16_v<D>(row)) << 4) + ((cc & 1) << 3);
   }
 
-  // Online-softmax state per lane (query row r32, this lane-half's keys):
-  // mused is the max the exponentials are referred to (raw scores q.k; scale > 0
-  // commutes with max), mtrue the true running max (the m artifact).
-  float mused = -kInf, mtrue = -kInf, lsum = 0.f;
-  f32x16 oacc[C::DB];
+  float mused[2] = {-kInf, -kInf}, mtrue[2] = {-kInf, -kInf}, lsum[2] = {0.f, 0.f};
+  f32x4 oacc[C::FB][2];
 #pragma unroll
-  for (int db = 0; db < C::DB; ++db) oacc[db] = f32x16{};
+  for (int fb = 0; fb < C::FB; ++fb) oacc[fb][0] = oacc[fb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto vfrag = [&](const unsigned char* vt, int n) {  // operand n = (16-key step s, feature block db)
-    const int s_ = n / C::DB, db = n % C::DB;
-    const u32x2 lo = ds_read_tr16(vt + (16 * s_) * C::ROWB + va[db]);
-    const u32x2 hi = ds_read_tr16(vt + (16 * s_ + 4) * C::ROWB + va[db]);
+  auto vfrag = [&](const unsigned char* vt, int fb) {
+    const u32x2 lo = ds_read_tr16(vt + va[fb]);
+    const u32x2 hi = ds_read_tr16(vt + 16 * C::ROWB + va[fb]);
     return u32x4{lo.x, lo.y, hi.x, hi.y};
   };
 
-  // One key tile: S^T = K Q^T, the masked (CUT) or unmasked softmax update,
-  // then O^T += V^T P^T. CUT is a compile-time branch, so the common full tile
-  // carries no per-element mask code.
-  auto tile = [&](auto bufc, int64_t key0, auto cutc) {
+  auto tile = [&](auto bufc, int key0, auto cutc) {
     constexpr bool CUT = decltype(cutc)::value;
-    constexpr int buf = decltype(bufc)::value;  // a constant: every LDS address is a lane offset + an immediate
+    constexpr int buf = decltype(bufc)::value;
     const unsigned char* kt = smem + C::KBUF + buf * C::TILEB;
     const unsigned char* vt = smem + C::VBUF + buf * C::TILEB;
-    f32x16 sacc = f32x16{};
-    u32x4 kf[2];
-    kf[0] = *reinterpret_cast<const u32x4*>(kt + ka[0]);
-    // MFMA stretches run at raised wave priority, the softmax at the base one:
-    // the SIMD's arbiter then prefers feeding the matrix core from whichever
-    // wave has MFMAs ready while the others' VALU work fills in behind it
+    f32x4 sacc[2][2];  // [key half][query half]: S^T[16 kb + 4 G + i][16 h + c]
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) sacc[kb][0] = sacc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // K operands n = 2 ks + kb, read C::KPF ahead of their two products
+    auto kfrag = [&](int n) { return *reinterpret_cast<const u32x4*>(kt + (n & 1) * 16 * C::ROWB + ka[n >> 1]); };
+    u32x4 kf[C::KPF];
+#pragma unroll
+    for (int n = 0; n < C::KPF; ++n) kf[n] = kfrag(n);
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      if (ks + 1 < C::KS) kf[(ks + 1) & 1] = *reinterpret_cast<const u32x4*>(kt + ka[ks + 1]);
-      sacc = mfma32<T>(kf[ks & 1], qreg[ks], sacc);
+    for (int n = 0; n < 2 * C::KS; ++n) {
+      const u32x4 kk = kf[n % C::KPF];
+      if (n + C::KPF < 2 * C::KS) kf[n % C::KPF] = kfrag(n + C::KPF);
+      const int ks = n >> 1, kb = n & 1;
+      sacc[kb][0] = mfma16<T>(kk, qreg[0][ks], sacc[kb][0]);
+      sacc[kb][1] = mfma16<T>(kk, qreg[1][ks], sacc[kb][1]);
     }
-    u32x4 vf[C::PF];  // first V operands, in flight during the softmax
+    u32x4 vf[C::PF];
 #pragma unroll
     for (int n = 0; n < C::PF; ++n) vf[n] = vfrag(vt, n);
     __builtin_amdgcn_s_setprio(0);
 
     if constexpr (CUT) {
-      // 32-bit offsets from this lane's first key kl = key0 + 8 g: accumulator
-      // i holds key kl + 16 (i / 8) + i % 8; band limits clamped to the tile
-      const int64_t kl = key0 + 8 * g;
-      const int rem = static_cast<int>(S_ - kl < 1024 ? S_ - kl : 1024);
-      const int64_t dl = kl - qrow;
-      auto clampi = [](int64_t x) { return static_cast<int>(x < -4096 ? -4096 : (x > 4096 ? 4096 : x)); };
-      // an unbounded end (INT64_MIN / INT64_MAX) must not enter the subtraction: it would wrap
-      const int lo = (a.masked && a.band_lo > INT64_MIN / 4) ? clampi(a.band_lo - dl) : -4096;
-      const int hi = (a.masked && a.band_hi < INT64_MAX / 4) ? clampi(a.band_hi - dl) : 4096;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int c = (i >> 3) * 16 + (i & 7);
-        if (c >= rem)
-          sacc[i] = -kInf;
-        else if (c < lo || c > hi)
-          sacc[i] = a.fill_raw;
-      }
-    }
-    // exponentials referred to mused, packed as the PV operand; the lane-half's
-    // partial denominator in fp32
-    u32x4 p[2];
-    auto expo = [&](float& part) {
-      const float mc = mused * a.c2;
+      // key of accumulator (kb, i) = kl + 16 kb + i; limits relative to it,
+      // clamped to the tile (32-bit: |key - row| < 2^29 + 64)
+      const int kl = key0 + 4 * G;
+      const int rem = S_ - kl < 1024 ? S_ - kl : 1024;
+      auto clampi = [](int x) { return x < -4096 ? -4096 : (x > 4096 ? 4096 : x); };
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        float e[8];
+        const int dl = kl - (h ? qr1 : qr0);
+        const int lo = a.masked ? clampi(a.band_lo32 - dl) : -4096;
+        const int hi = a.masked ? clampi(a.band_hi32 - dl) : 4096;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          // Full tiles hold live (bounded) scores: one fma. Masked tiles may hold
-          // fill-level scores equal to the running max, where only (s - m) * c
-          // cancels exactly (a fully-masked row: every p is exp2(0) = 1).
-          e[j] = CUT ? fast_exp2((sacc[8 * h + j] - mused) * a.c2) : fast_exp2(__builtin_fmaf(sacc[8 * h + j], a.c2, -mc));
-          part += e[j];  // fp32 probabilities: lse / den keep fp32 accuracy
-        }
-        p[h] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int cc = 16 * kb + i;
+            const float x = (cc < lo || cc > hi) ? a.fill_raw : sacc[kb][h][i];
+            sacc[kb][h][i] = cc >= rem ? -kInf : x;
+          }
       }
+    }
+    u32x4 p[2];
+    auto expo = [&](int h, float& part) {
+      const float mc = mused[h] * a.c2;
+      float e[8];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x = sacc[kb][h][i];
+          e[4 * kb + i] = CUT ? fast_exp2((x - mused[h]) * a.c2) : fast_exp2(__builtin_fmaf(x, a.c2, -mc));
+          part += e[4 * kb + i];
+        }
+      p[h] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
     };
-    auto rowmax = [&]() {
+    auto rowmax = [&](int h) {
       float m = -kInf;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) m = fmaxf(m, sacc[i]);
-      // the other lane half holds the row's other 16 keys: swap halves in registers
-      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-      return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, sacc[kb][h][i]);
+      return max4g(m);
+    };
+    auto rescale = [&](int h, float mnew) {
+      const float alpha = mnew == mused[h] ? 1.f : fast_exp2((mused[h] - mnew) * a.c2);
+      mused[h] = mnew;
+      lsum[h] *= alpha;
+#pragma unroll
+      for (int fb = 0; fb < C::FB; ++fb) oacc[fb][h] *= alpha;
     };
     if constexpr (!CUT && !ART) {
-      // A full tile of a launch without the (m, den) artifacts skips the row
-      // max: the exponentials are referred to mused as it stands, and only when
-      // some lane's partial sum leaves (0, 2^kTau] (a row's scores grew by more
-      // than kTau in log2 units, or mused is still -inf) does the wave take the
-      // exact path. lse = mused * scale + log(den) holds for any reference.
-      float part = 0.f;
-      expo(part);
-      if (__builtin_amdgcn_ballot_w64(!(part <= (1 << static_cast<int>(kTau)))) != 0) {
-        const float mnew = fmaxf(mused, rowmax());
-        const float alpha = mnew == mused ? 1.f : fast_exp2((mused - mnew) * a.c2);
-        mused = mnew;
-        lsum *= alpha;
-#pragma unroll
-        for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
-        part = 0.f;
-        expo(part);
+      float part0 = 0.f, part1 = 0.f;
+      expo(0, part0);
+      expo(1, part1);
+      const float lim = static_cast<float>(1 << static_cast<int>(kTau));
+      if (__builtin_amdgcn_ballot_w64(!(part0 <= lim) || !(part1 <= lim)) != 0) {
+        rescale(0, fmaxf(mused[0], rowmax(0)));
+        rescale(1, fmaxf(mused[1], rowmax(1)));
+        part0 = part1 = 0.f;
+        expo(0, part0);
+        expo(1, part1);
       }
-      lsum += part;
+      lsum[0] += part0;
+      lsum[1] += part1;
     } else {
-      const float mloc = rowmax();
-      mtrue = fmaxf(mtrue, mloc);
-      if (__builtin_amdgcn_ballot_w64((mloc - mused) * a.c2 > kTau) != 0) {
-        const float mnew = fmaxf(mused, mloc);
-        const float alpha = fast_exp2((mused - mnew) * a.c2);
-        mused = mnew;
-        lsum *= alpha;
-#pragma unroll
-        for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
+      const float m0 = rowmax(0), m1 = rowmax(1);
+      mtrue[0] = fmaxf(mtrue[0], m0);
+      mtrue[1] = fmaxf(mtrue[1], m1);
+      if (__builtin_amdgcn_ballot_w64((m0 - mused[0]) * a.c2 > kTau || (m1 - mused[1]) * a.c2 > kTau) != 0) {
+        rescale(0, fmaxf(mused[0], m0));
+        rescale(1, fmaxf(mused[1], m1));
       }
-      expo(lsum);
+      expo(0, lsum[0]);
+      expo(1, lsum[1]);
     }
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int n = 0; n < C::NPV; ++n) {
-      const u32x4 vv = vf[n % C::PF];
-      if (n + C::PF < C::NPV) vf[n % C::PF] = vfrag(vt, n + C::PF);
-      oacc[n % C::DB] = mfma32<T>(vv, p[n / C::DB], oacc[n % C::DB]);
+    for (int fb = 0; fb < C::FB; ++fb) {
+      const u32x4 vv = vf[fb % C::PF];
+      if (fb + C::PF < C::FB) vf[fb % C::PF] = vfrag(vt, fb + C::PF);
+      oacc[fb][0] = mfma16<T>(vv, p[0], oacc[fb][0]);
+      oacc[fb][1] = mfma16<T>(vv, p[1], oacc[fb][1]);
     }
     __builtin_amdgcn_s_setprio(0);
   };
 
   if (kt_lo < kt_hi) stage(kt_lo, 0);
-  // Tile kt lives in buffer (kt - kt_lo) & 1. The sweep runs tiles in pairs,
-  // buffer 0 then buffer 1, so the buffer is a compile-time constant in each
-  // copy of the tile body and its LDS addresses need no per-tile arithmetic.
   auto one = [&](int kt, auto bufc, auto cutc) {
     constexpr int buf = decltype(bufc)::value;
-    wait_vmcnt0();  // this wave's share of tile kt has landed
-    __syncthreads();  // ... and everyone's; everyone is done with tile kt - 1
-    if (kt + 1 < kt_hi) stage(kt + 1, buf ^ 1);  // the next tile, into the idle buffer
-    const int64_t key0 = static_cast<int64_t>(kt) * C::BN;
+    wait_vmcnt0();
+    __syncthreads();
+    if (kt + 1 < kt_hi) stage(kt + 1, buf ^ 1);
+    const int key0 = kt * C::BN;
     bool dead = false;
     if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's rows see no live key here
-      const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + C::BN - 1 - qw0;
-      dead = dmin > a.band_hi || dmax < a.band_lo;
+      const int dmin = key0 - (qw0 + 31), dmax = key0 + C::BN - 1 - qw0;
+      dead = dmin > a.band_hi32 || dmax < a.band_lo32;
     }
     if (!dead) tile(bufc, key0, cutc);
   };
@@ -484,7 +507,8 @@ __global__ __launch_bounds__(FwdCfg<D>::THREADS, 3) void flash_fwd_mfma(FwdArgs 
   sweep(kf_hi, kt_hi, std::true_type{});
   wait_vmcnt0();  // no load may be in flight into LDS when the workgroup exits
 
-  fwd_store<T, D>(a, inst, split, qw0, r32, g, op, oacc, mused, ART ? mtrue : mused, lsum);
+  const float mt[2] = {ART ? mtrue[0] : mused[0], ART ? mtrue[1] : mused[1]};
+  fwd16_store<T, D>(a, inst, bp.split, qw0, c, G, op, oacc, mused, mt, lsum);
 }
 
 // ---------------------------------------------------------------- generic fp32
@@ -633,14 +657,14 @@ bool band_has_empty_row(int64_t T, int64_t S, int64_t lo, int64_t hi) {
 template <typename T, int D>
 void fwd_kernel(const FwdArgs& a, unsigned nblocks, hipStream_t st) {
   if (a.m_out || a.den_out)
-    flash_fwd_mfma<T, D, true><<<dim3(nblocks), FwdCfg<D>::THREADS, 0, st>>>(a);
+    flash_fwd_m16<T, D, true><<<dim3(nblocks), F16Cfg<D>::THREADS, 0, st>>>(a);
   else
-    flash_fwd_mfma<T, D, false><<<dim3(nblocks), FwdCfg<D>::THREADS, 0, st>>>(a);
+    flash_fwd_m16<T, D, false><<<dim3(nblocks), F16Cfg<D>::THREADS, 0, st>>>(a);
 }
 
 template <typename T, int D>
 int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
-  using C = FwdCfg<D>;
+  using C = F16Cfg<D>;
   static_assert(C::LDS <= 64 * 1024, "the forward's static LDS fits one workgroup's limit");
   const int64_t nblk = ninst * a.nqb;
   PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: grid too large (%lld workgroups)", (long long)nblk);
@@ -658,7 +682,7 @@ int launch_mfma(const FwdArgs& a, int64_t ninst, hipStream_t st) {
     flash_fwd_combine<T, D><<<dim3(static_cast<unsigned>((nthr + 255) / 256)), 256, 0, st>>>(aa);
     return check_launch("pdh_flash_fwd_split (combine)");
   }
-  aa.xcd_remap = (nblk % 8 == 0) ? ((ninst % 32 == 0) ? 2 : 1) : 0;
+  aa.xcd_remap = (nblk % 32 == 0 && a.nqb % 8 == 0) ? 3 : ((nblk % 8 == 0) ? 1 : 0);
   fwd_kernel<T, D>(aa, static_cast<unsigned>(nblk), st);
   return check_launch("pdh_flash_fwd");
 }
@@ -715,7 +739,7 @@ int flash_fwd_impl(const void* q, const void* k, const void* v, void* o, float* 
                   G.k_sh % 8 == 0 && G.v_sh % 8 == 0 && G.o_sh % 8 == 0 && G.q_sb % 8 == 0 && G.k_sb % 8 == 0 &&
                   G.v_sb % 8 == 0 && G.o_sb % 8 == 0,
               PDH_EINVAL, "pdh_flash_fwd: 16-bit strides must be multiples of 8 elements");
-  PDH_REQUIRE(G.t <= INT32_MAX / 2 && G.s <= INT32_MAX / 2, PDH_EINVAL, "pdh_flash_fwd: sequence too long");
+  PDH_REQUIRE(G.t <= (1 << 29) && G.s <= (1 << 29), PDH_EINVAL, "pdh_flash_fwd: sequence too long (t, s <= 2^29)");
   PDH_REQUIRE(G.q_st < (1 << 24) && G.k_st < (1 << 24) && G.v_st < (1 << 24) && G.o_st < (1 << 24), PDH_EINVAL,
               "pdh_flash_fwd: row strides must be < 2^24 elements");
   PDH_REQUIRE(G.s * G.k_st * 2 < INT32_MAX && G.s * G.v_st * 2 < INT32_MAX, PDH_EINVAL,
@@ -723,7 +747,13 @@ int flash_fwd_impl(const void* q, const void* k, const void* v, void* o, float* 
   FwdArgs a{q, k, v, o, m_out, den_out, lse_out, G.heads_q, G.heads_kv, G.t, G.s,
             G.q_sb, G.q_sh, G.q_st, G.k_sb, G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st, G.o_sb, G.o_sh, G.o_st,
             scale, scale * kLog2e, fill / scale, masked, band_lo, band_hi, prune_ok,
-            static_cast<int>((G.t + FwdCfg<128>::BM - 1) / FwdCfg<128>::BM), 0};
+            static_cast<int>((G.t + F16Cfg<128>::BM - 1) / F16Cfg<128>::BM), 0};
+  {
+    constexpr int64_t kBand32 = (int64_t{1} << 29) + 64;
+    auto clamp32 = [](int64_t x) { return static_cast<int>(x < -kBand32 ? -kBand32 : (x > kBand32 ? kBand32 : x)); };
+    a.band_lo32 = clamp32(band_lo);
+    a.band_hi32 = clamp32(band_hi);
+  }
   a.nsplit = 1;
   if (nsplit > 1) {
     const size_t need = pdh_flash_fwd_workspace(gm, nsplit);

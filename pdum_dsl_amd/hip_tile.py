@@ -387,7 +387,7 @@ def _flash_runner(region, fb, grid, prune, dtype):
             return out, res.m.view(T), res.den.view(T)
         return out
 
-    kern = "flash_fwd_generic_f32" if dtype == "f32" else f"flash_fwd_mfma<{dtype},{E}>"
+    kern = "flash_fwd_generic_f32" if dtype == "f32" else f"flash_fwd_m16<{dtype},{E}>"
     bdesc = "all" if kband is None else f"band({band[1]},{band[2]})"
     src = (
         f"hip:{kern} t={T} s={S} e={E} od={OD} si={fb['si']} mask={bdesc} fill={fb['fill']:g} "
@@ -476,7 +476,7 @@ def _flash_joint_runner(region, fj, grid, dtype):
             ys.append(x.permute([order.index(n) for n in gt.names]))
         return tuple(ys)
 
-    kern = "flash_fwd_generic_f32 + bwd_rows_f32" if dtype == "f32" else f"flash_fwd_mfma<{dtype},{E}> + bwd_main<{dtype},{E}>"
+    kern = "flash_fwd_generic_f32 + bwd_rows_f32" if dtype == "f32" else f"flash_fwd_m16<{dtype},{E}> + bwd_main<{dtype},{E}>"
     bdesc = "all" if kband is None else f"band({band[1]},{band[2]})"
     src = (
         f"hip:{kern} t={T} s={S} e={E} od={OD} mask={bdesc} fill={fj['fill']:g} wrt={','.join(wrt)} "

@@ -128,7 +128,7 @@ def test_the_bf16_column_binds_the_mfma_kernel():
     a = zoo.attention(T=192, S=192, E=64, OD=64, mask="causal", seed=2, scale=0.125)
     (g,) = fusion.plan_region(a.region).groups
     run = compile_tile_hip(g.kernel, dtype="bf16")
-    assert "flash_fwd_mfma<bf16,64>" in run.source
+    assert "flash_fwd_m16<bf16,64>" in run.source
     q, k, v = (torch.as_tensor(x).to(torch.bfloat16).double().numpy() for x in a.numpy_inputs())
     assert_lowp(run(a.numpy_inputs()), cf.attention(q, k, v, band=(None, 0))[0])
 

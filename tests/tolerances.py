@@ -25,3 +25,15 @@ def assert_lowp(got, want, *, tol=BF16_TOL, what=""):
     err = np.max(np.abs(got - want)) if got.size else 0.0
     bound = tol * max(1.0, float(np.max(np.abs(want))) if want.size else 1.0)
     assert err <= bound, f"{what}: max abs err {err:.3e} > {bound:.3e}"
+
+
+def assert_lse(got, want, *, rtol=FP32_RTOL, what=""):
+    """fp32 log-sum-exp rows: |got - want| <= rtol * max(1, |want|) per row
+    (an lse near zero is held to rtol absolute)."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"
+    err = np.abs(got - want)
+    bound = rtol * np.maximum(1.0, np.abs(want))
+    bad = err > bound
+    assert not bad.any(), f"{what}: lse err {err.max():.3e} > {rtol:g} relative (worst at {np.argmax(err - bound)})"
