@@ -29,7 +29,9 @@ templates), over the vocabulary this backend reads:
                  tl.flip -> tl.flip, tl.select -> repeat at the point + pad,
                  tl.split -> tl.merge, tl.merge -> tl.split
   softmax        the max of a max-subtracted softmax that feeds nothing else
-                 gets no cotangent (shift invariance: its terms sum to zero)
+                 gets no cotangent (shift invariance: its terms sum to zero);
+                 grad(..., shift_invariant_softmax=False) keeps the
+                 reference's route through the max's adjoint
   tl.stage       identity
   core.const / tl.const / tl.iota / comparisons / stop_gradient: no flow
 
@@ -88,15 +90,61 @@ def _is_tensor(n) -> bool:
     return isinstance(n.type, TensorType)
 
 
-def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None = None, *, names=None) -> RegionGrad:
-    """Reverse-mode AD of ``region``'s node named ``target`` (autodiff.py:102).
+def grad(
+    region: Region,
+    target: str,
+    inputs: dict | None = None,
+    seed: str | None = None,
+    wrt: tuple | None = None,
+    target_unit=None,
+    fold_segments: int | None = None,
+    fold_slots: int | None = None,
+    *,
+    names=None,
+    shift_invariant_softmax: bool = True,
+) -> RegionGrad:
+    """Reverse-mode AD of ``region``'s node named ``target``, with the
+    reference's signature and positional order (autodiff.py:102-113).
 
     ``seed`` names the target's cotangent (required for a non-scalar target:
     reverse mode computes vector-Jacobian products); it becomes the joint's
     last param. ``wrt`` names the params to differentiate (all params by
-    default)."""
+    default).
+
+    ``inputs`` (input signatures) and ``target_unit`` feed the reference's
+    unit inference, which this backend does not model: a dict of inputs is
+    accepted and ignored, a target unit other than None refuses.
+    ``fold_segments`` / ``fold_slots`` pick the reference's checkpointed fold
+    schedules (uniform K-way segments / binomial revolve); they trade
+    recomputation for memory and leave the gradient's values unchanged. Only
+    the one-segment schedule is built here: ``fold_segments`` of None or 1
+    and ``fold_slots`` of None are accepted, other values refuse by name
+    after the reference's own argument checks (autodiff.py:181-187).
+
+    ``shift_invariant_softmax`` (keyword only, on by default): the max of a
+    max-subtracted softmax that feeds nothing else takes no cotangent. With
+    False the max's cotangent flows through the first-occurrence adjoint as
+    in the reference, and the joint carries its tl.scan."""
     if names is None:
         raise ValueError("grad joins on names — pass names=region_names(region, param_names)")
+    if inputs is not None and not isinstance(inputs, dict):
+        raise TypeError(f"inputs must be a dict of input signatures (got {type(inputs).__name__})")
+    if fold_segments is not None and fold_slots is not None:
+        raise ValueError(
+            "pass fold_segments (uniform K-way checkpointing) OR fold_slots (binomial revolve), not both — "
+            "they name different schedules"
+        )
+    if fold_slots is not None and int(fold_slots) < 1:
+        raise ValueError("fold_slots must be >= 1 (the number of checkpoint slots)")
+    if fold_segments is not None and int(fold_segments) < 1:
+        raise ValueError("fold_segments must be >= 1")
+    if target_unit is not None:
+        raise NotImplementedError("grad: target_unit — units are not modelled by this backend; pass None")
+    if (fold_segments is not None and int(fold_segments) != 1) or fold_slots is not None:
+        raise NotImplementedError(
+            "grad: checkpointed fold schedules (fold_segments > 1, fold_slots) are not built; the one-segment "
+            "fold adjoint gives the same values — pass fold_segments=None"
+        )
     by_name: dict = {}
     for p in region.params:
         by_name.setdefault(names[id(p)], p)
@@ -138,7 +186,7 @@ def grad(region: Region, target: str, seed: str | None = None, wrt: tuple | None
         seed_node = seed_param
 
     cot: dict[int, list] = {id(tnode): [seed_node]}
-    inert = _softmax_shifts(tnode)
+    inert = _softmax_shifts(tnode) if shift_invariant_softmax else set()
 
     def contribute(n, g):
         if n.op in ("core.const", "tl.const", "tl.iota") or id(n) in inert:
@@ -473,7 +521,8 @@ def _softmax_shifts(root: Node) -> set:
         e, rld = n.args
         sub = e.args[0]
         rlm = sub.args[1]
-        if (only(mx, rlm) and only(rlm, sub) and only(sub, e) and only(e, n, den) and only(den, rld)
+        # rld = repeat_like(den, e) reads e for its shape only
+        if (only(mx, rlm) and only(rlm, sub) and only(sub, e) and only(e, n, den, rld) and only(den, rld)
                 and only(rld, n)):
             inert.update((id(mx), id(rlm)))
     return inert
