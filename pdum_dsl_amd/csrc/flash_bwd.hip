@@ -4,17 +4,16 @@
 // Like the reference's carving, every output is owned by exactly one program
 // (330 §7.8 ruling 4): no atomics.
 //
-//   bwd_stats : per query row: -delta (delta = sum_d dO O), the log2-domain statistic
-//               lse2 (P = exp2(x - lse2) for live scores) and pm, the
-//               probability of a MASKED score (0 unless every key of the
-//               row is masked; then 1/den, the uniform-softmax row)  (HBM-bound)
-//   bwd_dkdv  : grid over 128-key blocks (4 waves x 32 keys); sweeps query
+//   bwd_stats : per query row: -delta (delta = sum_d dO O), -lse / scale and
+//               pm, the probability of a MASKED score (0 unless every key of
+//               the row is masked; then 1/den, the uniform-softmax row)  (HBM-bound)
+//   bwd16_dkdv: grid over 128-key blocks (4 waves x 32 keys); sweeps query
 //               tiles; each wave keeps its K and V rows in registers and
 //               accumulates dK^T, dV^T:
-//                 S = Q K^T, dP = dO V^T          (A = Q / dO rows from LDS)
-//                 P = exp(scale S - lse), dS = P (dP - delta)
-//                 dV^T += dO^T P, dK^T += Q^T dS  (A = dO^T / Q^T from LDS)
-//   bwd_dq    : grid over 128-query blocks; sweeps key tiles:
+//                 S = Q K^T - lse, dP = dO V^T - delta  (A = Q / dO rows from LDS)
+//                 P = exp(scale S), dS = P dP
+//                 dV^T += dO^T P, dK^T += Q^T dS        (A = dO^T / Q^T from LDS)
+//   bwd16_dq  : grid over 128-query blocks; sweeps key tiles:
 //                 S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T
 //
 // Grouped-query attention (heads_q = group x heads_kv, query head h reading
@@ -22,14 +21,16 @@
 // query head of its group in turn into the same accumulators, and a dQ
 // workgroup reads its group's K and V. Every output still has one owner.
 //
-// All products are v_mfma_f32_32x32x16 (bf16 / f16 in, fp32 accumulate).
-// LDS tiles whose rows become an MFMA A operand are stored with the
-// kperm_inv row permutation, so the score accumulators feed the next
-// contraction's k operand directly (see attn_common.h). Transposed copies
-// (Q^T, dO^T, K^T) are formed in registers on the way into LDS.
-// Masks: a masked score's probability is the row's pm (0 for any row with a
-// live key) and carries no gradient (dS = 0), as the where() adjoint.
+// All products are v_mfma_f32_16x16x32 (bf16 / f16 in, fp32 accumulate), in
+// the forward's layout (see the 16x16x32 section): the score accumulators
+// feed the next contraction's k operand with no register shuffle, and the
+// transposed operands (Q^T, dO^T, K^T) are read from the same LDS tiles by
+// ds_read_b64_tr_b16. Tiles live for the whole workgroup run a mask-free
+// body; masked tiles give a masked score its row's pm as probability (0 for
+// any row with a live key) and no gradient (dS = 0), as the where() adjoint.
 #include "attn_common.h"
+
+#include <type_traits>
 
 namespace pdh {
 namespace {
@@ -60,6 +61,9 @@ struct BwdArgs {
   int ninst_kv;       // batch * heads_kv (K / V instances)
   int nkblk, nqblk;   // 128-key blocks (dK, dV) per K / V instance, 128-query blocks (dQ) per query instance
   int xcd_remap;
+  // the band clamped to +-(2^29 + 64): with t, s <= 2^29 every key - query
+  // difference compares the same against these as against the 64-bit band
+  int band_lo32, band_hi32;
 };
 
 // ---------------------------------------------------------------- row stats
@@ -96,105 +100,150 @@ __global__ __launch_bounds__(256) void bwd_stats(BwdArgs a) {
       if (a.masked) pm = (lse2 - a.fill2 < 64.f) ? 1.0f / static_cast<float>(a.s) : fast_exp2(a.fill2 - lse2);
     }
     a.ws[row] = -acc;  // -delta: the dP accumulators start from it
-    a.ws[a.rows + row] = lse2;
+    a.ws[a.rows + row] = -lse2 / a.c2;  // -lse / scale: the S accumulators of the dK / dV role start from it
     a.ws[2 * a.rows + row] = pm;
   }
 }
 
-// Store a 32-row x D accumulator set held transposed (acc[db][i] is element
-// (d = 32 db + 8(i/4) + 4g + i%4, row = r32)) to a row-major 16-bit output.
-template <typename T, int D>
-__device__ __forceinline__ void store_rows_t(uint16_t* base, int64_t ld, int r32, int g, const f32x16* acc,
-                                             float mul) {
-  const uint32_t off = static_cast<uint32_t>(r32 * ld * 2 + g * 8);
-#pragma unroll
-  for (int db = 0; db < D / 32; ++db) {
-#pragma unroll
-    for (int a4 = 0; a4 < 4; ++a4) {
-      const int d0 = db * 32 + a4 * 8;
-      const u32x2 wv = {pack2<T>(acc[db][4 * a4 + 0] * mul, acc[db][4 * a4 + 1] * mul),
-                        pack2<T>(acc[db][4 * a4 + 2] * mul, acc[db][4 * a4 + 3] * mul)};
-      gstore<u32x2>(base + d0, off, wv);
-    }
-  }
-}
+// ---------------------------------------------------- 16x16x32 backward
+//
+// Both roles in the forward's layout: v_mfma_f32_16x16x32 products, a wave
+// owning 32 rows of its role's side as two 16-row halves (lane 16 G + c owns
+// rows c and 16 + c), the swept tiles' 32 rows seen by a lane as {4G .. 4G+3}
+// and {16+4G .. 16+4G+3}. Those eight rows are the k operand (k = 8G + j:
+// row 4G + j for j < 4, 16 + 4G + j - 4 for j >= 4) of the second
+// contraction, and the transposed LDS read names the same rows per 16-lane
+// group, so the score accumulators feed it with no register shuffle. Tiles
+// fully live for the whole workgroup run a mask-free body; the sweep runs in
+// buffer pairs so every LDS address is a lane offset plus an immediate.
 
-// A 32-row tile of a [rows, D] 16-bit operand in LDS: unpadded rows of D * 2
-// bytes whose 16-byte slots are XOR-swizzled by swz_rt, filled by direct
-// buffer loads (1 KB per wave instruction). The same tile is read as rows
-// (b128, MFMA A operand) and transposed (ds_read_b64_tr_b16, MFMA A operand
-// with the row index as k).
 template <int D>
-struct Tile32 {
-  static constexpr int ROWB = D * 2, CPR = D / 8, BYTES = 32 * ROWB, RPK = 1024 / ROWB, NBLK = BYTES / 1024;
-  static constexpr int KS = D / 16, DB = D / 32;
+struct B16 {
+  static constexpr int ROWB = D * 2, CPR = D / 8, TILEB = 32 * ROWB, RPK = 1024 / ROWB, NBLK = TILEB / 1024;
+  static constexpr int NDMA = (NBLK + 3) / 4;
+  static constexpr int KS = D / 32;  // k-steps of 32 features
+  static constexpr int FB = D / 16;  // 16-feature output blocks
 };
 
-// Tiles staged per barrier: each stage holds kSub consecutive 32-row tiles,
-// so a wave runs kSub tiles of MFMA / softmax work between barriers.
-constexpr int kSub = 2;
-
-// Per-lane offsets of the tile's three access patterns.
+// One XOR mask per row % 16 that keeps both read patterns of a tile
+// conflict-free for 32- and 64-bank LDS: row reads (lanes 16 G + c read row
+// c at chunk 4 ks + G) and transposed reads (16-lane group G reads rows
+// 4 G .. 4 G + 3, 32 bytes each); the conditions are re-checked by
+// tests/test_lds_layout.py.
 template <int D>
-struct TileLane {
-  using TT = Tile32<D>;
-  uint32_t dma[(TT::NBLK + 3) / 4];  // direct-load offsets (4 waves share the blocks)
-  int rowr[TT::KS];                 // row reads: row swap_bits23(r32), chunk 2 ks + g
-  int tr[2][TT::DB];                // transposed reads, half h, feature block db (+ 16 s rows: immediate)
+__device__ __forceinline__ int swz16_rt(int row) {
+  constexpr uint64_t kTable = D == 128 ? 0x75a8ec31fdb96420ull : 0x4602753157136420ull;
+  return static_cast<int>((kTable >> (4 * (row & 15))) & 15u);
+}
 
-  __device__ __forceinline__ void init(int lane, int w, int r32, int g, uint32_t grb) {
-    const int lrow = lane / TT::CPR, slot = lane % TT::CPR;
+// Per-lane offsets into a 32-row tile (the same for every tensor: they share
+// the layout) and the direct-load offsets of one tensor.
+template <int D>
+struct Lane16 {
+  using C = B16<D>;
+  int rowr[C::KS];  // row reads: row c, chunk 4 ks + G (+ 16 rows: immediate)
+  int tr[C::FB];    // transposed reads: row 4 G + k4, features 16 fb + 4 cc (+ 16 rows: immediate)
+  __device__ __forceinline__ void init(int lane) {
+    const int G = lane >> 4, c = lane & 15, k4 = (lane >> 2) & 3, cc = lane & 3, row = 4 * G + k4;
 #pragma unroll
-    for (int i = 0; i < (TT::NBLK + 3) / 4; ++i) {
-      const int rho = (i * 4 + w) * TT::RPK + lrow;
-      dma[i] = lrow * grb + ((slot ^ swz_rt<D>(rho)) << 4);
-    }
-    const int row = swap_bits23(r32);
+    for (int ks = 0; ks < C::KS; ++ks) rowr[ks] = c * C::ROWB + (((4 * ks + G) ^ swz16_rt<D>(c)) << 4);
 #pragma unroll
-    for (int ks = 0; ks < TT::KS; ++ks) rowr[ks] = row * TT::ROWB + (((2 * ks + g) ^ swz_rt<D>(row)) << 4);
-    const int G = lane >> 4, kk = (lane >> 2) & 3, c4 = lane & 3;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int trow = 8 * (G >> 1) + 4 * h + kk;
-#pragma unroll
-      for (int db = 0; db < TT::DB; ++db)
-        tr[h][db] = trow * TT::ROWB + (((4 * db + 2 * (G & 1) + (c4 >> 1)) ^ swz_rt<D>(trow)) << 4) + ((c4 & 1) << 3);
-    }
+    for (int fb = 0; fb < C::FB; ++fb)
+      tr[fb] = row * C::ROWB + (((2 * fb + (cc >> 1)) ^ swz16_rt<D>(row)) << 4) + ((cc & 1) << 3);
   }
-  // rows [row0, row0 + 32) of a buffer into an LDS tile (all 4 waves call this)
-  __device__ __forceinline__ void stage(rsrc_t r, unsigned char* lds, uint32_t row0, uint32_t grb, int w) const {
-#pragma unroll
-    for (int i = 0; i < (TT::NBLK + 3) / 4; ++i) {
-      const int blk = i * 4 + w;
-      if (TT::NBLK % 4 != 0 && blk >= TT::NBLK) break;
-      dma16(r, lds + blk * 1024, dma[i], (row0 + blk * TT::RPK) * grb);
-    }
+  // A operand: rows 16 half + (0..15) x features 32 ks .. +32
+  __device__ __forceinline__ u32x4 row_frag(const unsigned char* t, int half, int ks) const {
+    return *reinterpret_cast<const u32x4*>(t + half * 16 * C::ROWB + rowr[ks]);
   }
-  // MFMA A operand: 32 rows x 16 features (k-step ks) of the tile
-  __device__ __forceinline__ u32x4 row_frag(const unsigned char* t, int ks) const {
-    return *reinterpret_cast<const u32x4*>(t + rowr[ks]);
-  }
-  // MFMA A operand, transposed: features 32 db .. +32 x tile rows 16 s .. +16
-  __device__ __forceinline__ u32x4 tr_frag(const unsigned char* t, int s, int db) const {
-    const u32x2 lo = ds_read_tr16(t + 16 * s * TT::ROWB + tr[0][db]);
-    const u32x2 hi = ds_read_tr16(t + 16 * s * TT::ROWB + tr[1][db]);
+  // A operand, transposed: features 16 fb .. +16 x the tile's 32 rows in k order
+  __device__ __forceinline__ u32x4 tr_frag(const unsigned char* t, int fb) const {
+    const u32x2 lo = ds_read_tr16(t + tr[fb]);
+    const u32x2 hi = ds_read_tr16(t + 16 * C::ROWB + tr[fb]);
     return u32x4{lo.x, lo.y, hi.x, hi.y};
   }
 };
 
+template <int D>
+__device__ __forceinline__ void dma_offsets(uint32_t (&off)[B16<D>::NDMA], int lane, int w, uint32_t gr) {
+  using C = B16<D>;
+  const int lrow = lane / C::CPR, slot = lane % C::CPR;
+#pragma unroll
+  for (int i = 0; i < C::NDMA; ++i) {
+    const int rho = (i * 4 + w) * C::RPK + lrow;
+    off[i] = lrow * gr + ((slot ^ swz16_rt<D>(rho)) << 4);
+  }
+}
+
+// rows [row0, row0 + 32) of a tensor into a tile (every wave calls this)
+template <int D>
+__device__ __forceinline__ void dma_tile(rsrc_t r, unsigned char* lds, const uint32_t (&off)[B16<D>::NDMA],
+                                         uint32_t row0, uint32_t gr, int w) {
+  using C = B16<D>;
+#pragma unroll
+  for (int i = 0; i < C::NDMA; ++i) {
+    const int blk = i * 4 + w;
+    if (C::NBLK % 4 != 0 && blk >= C::NBLK) break;
+    dma16(r, lds + blk * 1024, off[i], (row0 + blk * C::RPK) * gr);
+  }
+}
+
+// The swept tiles of a 128-row owned block: the live range [lo, hi) and the
+// run [flo, fhi) of tiles live for every (owned row, swept row) pair and
+// inside the swept extent. d = key - query; owner_is_query picks the side.
+struct Sweep {
+  int lo, hi, flo, fhi;
+};
+
+__device__ __forceinline__ Sweep sweep_plan(const BwdArgs& a, int o0, int ext, bool owner_is_query) {
+  constexpr int BO = 128, BT = 32;
+  const int ntiles = (ext + BT - 1) / BT;
+  int lo = 0, hi = ntiles;
+  const int blo = a.band_lo32, bhi = a.band_hi32;
+  if (a.masked && a.prune) {
+    // swept rows x live for some owned row o in [o0, o0 + BO): lo_d <= d <= hi_d
+    const int xmin = owner_is_query ? o0 + blo : o0 - bhi;
+    const int xmax = owner_is_query ? o0 + BO - 1 + bhi : o0 + BO - 1 - blo;
+    lo = xmin <= 0 ? 0 : (xmin / BT < ntiles ? xmin / BT : ntiles);
+    hi = xmax < 0 ? 0 : (xmax / BT + 1 < ntiles ? xmax / BT + 1 : ntiles);
+  }
+  // fully live tiles: every d over the (owned block, tile) box inside the band, the tile inside ext
+  int flo = lo, fhi = ext / BT < hi ? ext / BT : hi;
+  if (a.masked) {
+    // d ranges over [x0 - (o0 + BO - 1), x0 + BT - 1 - o0] (owner query) or [o0 - x0 - BT + 1, o0 + BO - 1 - x0]
+    if (owner_is_query) {
+      // x0 >= o0 + BO - 1 + blo and x0 + BT - 1 <= o0 + bhi
+      const int a0 = o0 + BO - 1 + blo, b0 = o0 + bhi - (BT - 1);
+      const int f0 = a0 <= 0 ? 0 : (a0 + BT - 1) / BT;
+      const int f1 = b0 < 0 ? 0 : b0 / BT + 1;
+      flo = flo > f0 ? flo : f0;
+      fhi = fhi < f1 ? fhi : f1;
+    } else {
+      // o0 - (x0 + BT - 1) >= blo and o0 + BO - 1 - x0 <= bhi
+      const int a0 = o0 + BO - 1 - bhi, b0 = o0 - blo - (BT - 1);
+      const int f0 = a0 <= 0 ? 0 : (a0 + BT - 1) / BT;
+      const int f1 = b0 < 0 ? 0 : b0 / BT + 1;
+      flo = flo > f0 ? flo : f0;
+      fhi = fhi < f1 ? fhi : f1;
+    }
+  }
+  if (flo < lo) flo = lo;
+  if (fhi > hi) fhi = hi;
+  if (flo >= fhi) flo = fhi = hi;
+  return Sweep{lo, hi, flo, fhi};
+}
+
 // -------------------------------------------------------------------- dQ
 //
-// Workgroup: 4 waves x 32 query rows; key tiles of 32 rows (K, V) staged by
-// direct loads kSub tiles per barrier, double buffered. Per wave and tile:
-//   S^T = K Q^T, dP^T = V dO^T       (A = K / V rows, B = Q / dO in registers)
-//   dS^T = P^T (dP^T - delta)        (lane = query row: lse, delta are scalars)
-//   dQ^T += K^T dS^T                 (A = K transposed from LDS)
+// Workgroup: 4 waves x 32 query rows; key tiles of 32 rows (K, V) double
+// buffered. Per wave and tile (lane: queries c, 16 + c; keys 4G + i, 16 + 4G + i):
+//   S^T = K Q^T, dP^T = V dO^T (from -delta)   (A = K / V rows, B = Q / dO in registers)
+//   dS^T = exp2(S^T c2 - lse2) dP^T
+//   dQ^T += K^T dS^T                           (A = K transposed from LDS)
 
 template <typename T, int D>
-__device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char* smem) {  // smem: K[2], V[2]
-  using TT = Tile32<D>;
-  constexpr int KS = TT::KS, DB = TT::DB, BM = 128, BN = 32;
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
+__device__ __forceinline__ void bwd16_dq(const BwdArgs& a, int bid, unsigned char* smem) {  // smem: K[2], V[2]
+  using C = B16<D>;
+  const int lane = threadIdx.x & 63, w = wave_id(), c = lane & 15, G = lane >> 4;
   const int64_t inst = bid / a.nqblk;
   const int qb = a.nqblk - 1 - (bid % a.nqblk);  // heavy (late) query blocks first
   const int64_t b = inst / a.heads, h = inst % a.heads, hkv = h / a.group;
@@ -202,339 +251,381 @@ __device__ __forceinline__ void bwd_dq(const BwdArgs& a, int bid, unsigned char*
   const uint16_t* kp = a.k + b * a.k_sb + hkv * a.k_sh;
   const uint16_t* vp = a.v + b * a.v_sb + hkv * a.v_sh;
   const uint16_t* dop = a.dout + b * a.o_sb + h * a.o_sh;
-  const int64_t T_ = a.t, S_ = a.s;
-  const int q0 = qb * BM;
-  const int qw0 = q0 + 32 * w;
-  const int qrow = qw0 + r32;
+  const int T_ = static_cast<int>(a.t), S_ = static_cast<int>(a.s);
+  const int q0 = qb * 128, qw0 = q0 + 32 * w;
+  const int qr[2] = {qw0 + c, qw0 + 16 + c};
+  const int cmg = c - 4 * G;
 
-  u32x4 qreg[KS], doreg[KS];
+  u32x4 qreg[2][C::KS], doreg[2][C::KS];
+  float ndl[2], lse2[2];
   {
-    const uint32_t qoff = static_cast<uint32_t>(r32 * a.q_st * 2 + g * 16);
-    const uint32_t ooff = static_cast<uint32_t>(r32 * a.o_st * 2 + g * 16);
-    const uint16_t* qbs = qp + static_cast<int64_t>(qw0) * a.q_st;
-    const uint16_t* obs = dop + static_cast<int64_t>(qw0) * a.o_st;
+    const uint32_t qoff = static_cast<uint32_t>(c * a.q_st * 2 + G * 16);
+    const uint32_t ooff = static_cast<uint32_t>(c * a.o_st * 2 + G * 16);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qreg[ks] = qrow < T_ ? gload<u32x4>(qbs + ks * 16, qoff) : u32x4{0u, 0u, 0u, 0u};
-      doreg[ks] = qrow < T_ ? gload<u32x4>(obs + ks * 16, ooff) : u32x4{0u, 0u, 0u, 0u};
+    for (int hh = 0; hh < 2; ++hh) {
+      const bool ok = qr[hh] < T_;
+      const uint16_t* qbs = qp + static_cast<int64_t>(qw0 + 16 * hh) * a.q_st;
+      const uint16_t* obs = dop + static_cast<int64_t>(qw0 + 16 * hh) * a.o_st;
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) {
+        qreg[hh][ks] = ok ? gload<u32x4>(qbs + ks * 32, qoff) : u32x4{0u, 0u, 0u, 0u};
+        doreg[hh][ks] = ok ? gload<u32x4>(obs + ks * 32, ooff) : u32x4{0u, 0u, 0u, 0u};
+      }
+      const int64_t srow = inst * a.t + qr[hh];
+      ndl[hh] = ok ? a.ws[srow] : 0.f;  // -delta
+      lse2[hh] = ok ? -a.ws[a.rows + srow] * a.c2 : 0.f;  // the stat is -lse / scale
     }
   }
-  const int64_t srow = inst * T_ + qrow;
-  const float ndl = qrow < T_ ? a.ws[srow] : 0.f;  // -delta
-  const float lse2 = qrow < T_ ? a.ws[a.rows + srow] : 0.f;
-
-  const int ntiles = static_cast<int>((S_ + BN - 1) / BN);
-  int kt_lo = 0, kt_hi = ntiles;
-  if (a.masked && a.prune) {
-    const int64_t qlast = (q0 + BM - 1 < T_ ? q0 + BM - 1 : T_ - 1);
-    if (a.band_hi < INT64_MAX / 4) {
-      const int64_t smax = qlast + a.band_hi;
-      kt_hi = smax < 0 ? 0 : static_cast<int>(smax / BN + 1 < ntiles ? smax / BN + 1 : ntiles);
-    }
-    if (a.band_lo > INT64_MIN / 4) {
-      const int64_t smin = q0 + a.band_lo;
-      kt_lo = smin <= 0 ? 0 : static_cast<int>(smin / BN);
-    }
-  }
+  const Sweep sw = sweep_plan(a, q0, S_, true);
 
   const uint32_t grk = static_cast<uint32_t>(a.k_st * 2), grv = static_cast<uint32_t>(a.v_st * 2);
-  const rsrc_t kr = make_rsrc(kp, static_cast<uint32_t>((S_ - 1) * a.k_st * 2 + D * 2));
-  const rsrc_t vr = make_rsrc(vp, static_cast<uint32_t>((S_ - 1) * a.v_st * 2 + D * 2));
-  TileLane<D> kl, vl;  // K and V tiles share the slot layout; only the source stride differs
-  kl.init(lane, w, r32, g, grk);
-  vl.init(lane, w, r32, g, grv);
-  auto kbuf = [&](int buf, int sub) { return smem + (buf * kSub + sub) * TT::BYTES; };
-  auto vbuf = [&](int buf, int sub) { return smem + ((2 + buf) * kSub + sub) * TT::BYTES; };
-  auto stage = [&](int tile0, int buf) {  // tiles tile0 .. tile0 + kSub - 1 that the sweep reads
-#pragma unroll
-    for (int sub = 0; sub < kSub; ++sub) {
-      if (tile0 + sub >= kt_hi) break;
-      kl.stage(kr, kbuf(buf, sub), static_cast<uint32_t>((tile0 + sub) * BN), grk, w);
-      vl.stage(vr, vbuf(buf, sub), static_cast<uint32_t>((tile0 + sub) * BN), grv, w);
-    }
+  const rsrc_t kr = make_rsrc(kp, static_cast<uint32_t>((a.s - 1) * a.k_st * 2 + D * 2));
+  const rsrc_t vr = make_rsrc(vp, static_cast<uint32_t>((a.s - 1) * a.v_st * 2 + D * 2));
+  uint32_t dk_off[C::NDMA], dv_off[C::NDMA];
+  dma_offsets<D>(dk_off, lane, w, grk);
+  dma_offsets<D>(dv_off, lane, w, grv);
+  Lane16<D> L;
+  L.init(lane);
+  auto stage = [&](int tile, int buf) {
+    dma_tile<D>(kr, smem + buf * C::TILEB, dk_off, static_cast<uint32_t>(tile * 32), grk, w);
+    dma_tile<D>(vr, smem + (2 + buf) * C::TILEB, dv_off, static_cast<uint32_t>(tile * 32), grv, w);
   };
 
-  f32x16 dqacc[DB];
+  f32x4 dqacc[C::FB][2];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
+  for (int fb = 0; fb < C::FB; ++fb) dqacc[fb][0] = dqacc[fb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  auto tile = [&](auto bufc, int key0, auto cutc) {
+    constexpr bool CUT = decltype(cutc)::value;
+    constexpr int buf = decltype(bufc)::value;
+    const unsigned char* kt = smem + buf * C::TILEB;
+    const unsigned char* vt = smem + (2 + buf) * C::TILEB;
+    f32x4 sacc[2][2], pacc[2][2];  // [key half][query half]
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        sacc[kb][hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+        pacc[kb][hh] = f32x4{ndl[hh], ndl[hh], ndl[hh], ndl[hh]};
+      }
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int n = 0; n < 2 * C::KS; ++n) {
+      const int ks = n >> 1, kb = n & 1;
+      const u32x4 kk = L.row_frag(kt, kb, ks);
+      const u32x4 vv = L.row_frag(vt, kb, ks);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        sacc[kb][hh] = mfma16<T>(kk, qreg[hh][ks], sacc[kb][hh]);
+        pacc[kb][hh] = mfma16<T>(vv, doreg[hh][ks], pacc[kb][hh]);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    u32x4 ds[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float e[8];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          e[4 * kb + i] = fast_exp2(__builtin_fmaf(sacc[kb][hh][i], a.c2, -lse2[hh])) * pacc[kb][hh][i];
+      if constexpr (CUT) {
+        // live: key < s, query < t, lo <= key - query <= hi (32-bit: |key - query| < 2^29 + 64)
+        // key - query = (key0 - qw0 - 16 hh) - (c - 4 G) + (16 kb + i): a scalar plus one lane constant
+        const int dl = (key0 - qw0 - 16 * hh) - cmg;
+        const bool rowok = qw0 + 16 * hh + c < T_;
+        const int kl = S_ - key0 - 4 * G;  // key 16 kb + i of the tile exists below this
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int cc = 16 * kb + i, d = dl + cc;
+            const bool live = rowok && cc < kl && (!a.masked || (d >= a.band_lo32 && d <= a.band_hi32));
+            e[4 * kb + i] = live ? e[4 * kb + i] : 0.f;
+          }
+      }
+      ds[hh] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
+    }
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int fb = 0; fb < C::FB; ++fb) {
+      const u32x4 kf = L.tr_frag(kt, fb);
+      dqacc[fb][0] = mfma16<T>(kf, ds[0], dqacc[fb][0]);
+      dqacc[fb][1] = mfma16<T>(kf, ds[1], dqacc[fb][1]);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  const int kt_lo = sw.lo, kt_hi = sw.hi;
   if (kt_lo < kt_hi) stage(kt_lo, 0);
-  for (int kt0 = kt_lo; kt0 < kt_hi; kt0 += kSub) {
-    const int buf = ((kt0 - kt_lo) / kSub) & 1;
+  auto one = [&](int kt, auto bufc, auto cutc) {
+    constexpr int buf = decltype(bufc)::value;
     wait_vmcnt0();
     __syncthreads();
-    if (kt0 + kSub < kt_hi) stage(kt0 + kSub, buf ^ 1);  // the next stage, into the idle buffers
-#pragma unroll
-    for (int sub = 0; sub < kSub; ++sub) {
-      const int kt = kt0 + sub;
-      if (kt >= kt_hi) break;
-      const int64_t key0 = static_cast<int64_t>(kt) * BN;
-      const int64_t dmin = key0 - (qw0 + 31), dmax = key0 + BN - 1 - qw0;
-      bool dead = false, cut = key0 + BN > S_ || qw0 + 32 > T_;
-      if (a.masked) {
-        dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
-        cut = cut || dmin < a.band_lo || dmax > a.band_hi;
-      }
-      if (dead) continue;
-      const unsigned char* kt_l = kbuf(buf, sub);
-      const unsigned char* vt_l = vbuf(buf, sub);
-      __builtin_amdgcn_s_setprio(1);
-      f32x16 sacc = f32x16{};
-      f32x16 pacc = ndl - f32x16{};  // dP^T - delta accumulates from -delta
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        sacc = mfma32<T>(kl.row_frag(kt_l, ks), qreg[ks], sacc);
-        pacc = mfma32<T>(vl.row_frag(vt_l, ks), doreg[ks], pacc);
-      }
-      __builtin_amdgcn_s_setprio(0);
-      // accumulator i of lane-half g: key key0 + 16 (i / 8) + 8 g + i % 8, query qrow
-      if (cut) {
-        const int64_t kl0 = key0 + 8 * g;
-        const int rem = static_cast<int>(S_ - kl0 < 1024 ? S_ - kl0 : 1024);
-        const int64_t dl0 = kl0 - qrow;
-        auto clampi = [](int64_t x) { return static_cast<int>(x < -4096 ? -4096 : (x > 4096 ? 4096 : x)); };
-        // an unbounded end (INT64_MIN / INT64_MAX) must not enter the subtraction: it would wrap
-        const int lo = (a.masked && a.band_lo > INT64_MIN / 4) ? clampi(a.band_lo - dl0) : -4096;
-        const int hi = (a.masked && a.band_hi < INT64_MAX / 4) ? clampi(a.band_hi - dl0) : 4096;
-        const bool rowok = qrow < T_;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int c = (i >> 3) * 16 + (i & 7);
-          const bool live = rowok && c < rem && c >= lo && c <= hi;
-          pacc[i] = live ? fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * pacc[i] : 0.f;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) pacc[i] = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse2)) * pacc[i];
-      }
-      const u32x4 ds0 = pack8<T>(pacc, 0), ds1 = pack8<T>(pacc, 1);
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        dqacc[db] = mfma32<T>(kl.tr_frag(kt_l, 0, db), ds0, dqacc[db]);
-        dqacc[db] = mfma32<T>(kl.tr_frag(kt_l, 1, db), ds1, dqacc[db]);
-      }
-      __builtin_amdgcn_s_setprio(0);
+    if (kt + 1 < kt_hi) stage(kt + 1, buf ^ 1);
+    const int key0 = kt * 32;
+    bool dead = false;
+    if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's rows see no live key here
+      const int dmin = key0 - (qw0 + 31), dmax = key0 + 31 - qw0;
+      dead = dmin > a.band_hi32 || dmax < a.band_lo32;
     }
-  }
+    if (!dead) tile(bufc, key0, cutc);
+  };
+  auto sweep = [&](int from, int to, auto cutc) {
+    int kt = from;
+    if (kt < to && ((kt - kt_lo) & 1)) one(kt++, std::integral_constant<int, 1>{}, cutc);
+    for (; kt + 1 < to; kt += 2) {
+      one(kt, std::integral_constant<int, 0>{}, cutc);
+      one(kt + 1, std::integral_constant<int, 1>{}, cutc);
+    }
+    if (kt < to) one(kt, std::integral_constant<int, 0>{}, cutc);
+  };
+  sweep(kt_lo, sw.flo, std::true_type{});
+  sweep(sw.flo, sw.fhi, std::false_type{});
+  sweep(sw.fhi, kt_hi, std::true_type{});
   wait_vmcnt0();
 
-  if (qrow < T_)
-    store_rows_t<T, D>(a.dq + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(qw0) * a.q_st, a.q_st, r32, g, dqacc,
-                       a.scale);
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    if (qr[hh] >= T_) continue;
+    uint16_t* base = a.dq + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(qw0 + 16 * hh) * a.q_st;
+    const uint32_t off = static_cast<uint32_t>(c * a.q_st * 2 + G * 8);
+#pragma unroll
+    for (int fb = 0; fb < C::FB; ++fb) {
+      const f32x4 x = dqacc[fb][hh];
+      gstore<u32x2>(base + 16 * fb, off,
+                    u32x2{pack2<T>(x[0] * a.scale, x[1] * a.scale), pack2<T>(x[2] * a.scale, x[3] * a.scale)});
+    }
+  }
 }
 
 // ---------------------------------------------------------------- dK / dV
 //
 // Workgroup: 4 waves x 32 key rows (K, V in registers as B operands); query
-// tiles of 32 rows (Q, dO and the rows' delta / lse2 / pm) staged by direct
-// loads kSub tiles per barrier, double buffered. Per wave and tile:
-//   S = Q K^T, dP = dO V^T           (A = Q / dO rows; lane = key, acc = query)
-//   P = exp2(S c2 - lse2), dS = P (dP - delta)
-//   dV^T += dO^T P, dK^T += Q^T dS   (A = dO / Q transposed from LDS)
+// tiles of 32 rows (Q, dO and their rows' -delta / lse2 / pm) double
+// buffered; grouped-query: the group's query heads one after another into
+// the same accumulators. Per wave and tile (lane: keys c, 16 + c; queries
+// 4G + i, 16 + 4G + i):
+//   S = Q K^T, dP = dO V^T (from -delta)        (A = Q / dO rows from LDS)
+//   P = exp2(S c2 - lse2), dS = P dP
+//   dV^T += dO^T P, dK^T += Q^T dS               (A = dO / Q transposed from LDS)
 
 template <typename T, int D>
-__device__ __forceinline__ void bwd_dkdv(const BwdArgs& a, int bid, unsigned char* smem) {  // Q[2], dO[2], stats[2]
-  using TT = Tile32<D>;
-  constexpr int KS = TT::KS, DB = TT::DB, BK = 128, QT = 32;
-  constexpr int STATB = 4 * kSub * TT::BYTES;  // [2][kSub][delta | lse2 | pm] x 32 floats
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), r32 = lane & 31, g = lane >> 5;
-  const int64_t kinst = bid / a.nkblk;  // K / V instance
+__device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned char* smem) {  // Q[2], dO[2], stats[2]
+  using C = B16<D>;
+  constexpr int STATB = 4 * C::TILEB;  // [2][-delta | lse2 | pm] x 32 floats
+  const int lane = threadIdx.x & 63, w = wave_id(), c = lane & 15, G = lane >> 4;
+  const int64_t kinst = bid / a.nkblk;
   const int kblk = bid % a.nkblk;  // early key blocks see the most queries under causal masks: launched first
   const int64_t b = kinst / a.heads_kv, hkv = kinst % a.heads_kv;
   const uint16_t* kp = a.k + b * a.k_sb + hkv * a.k_sh;
   const uint16_t* vp = a.v + b * a.v_sb + hkv * a.v_sh;
-  const int64_t T_ = a.t, S_ = a.s;
-  const int k0 = kblk * BK;
-  const int kw0 = k0 + 32 * w;
-  const int krow = kw0 + r32;
-  auto clamp30 = [](int64_t x) { return static_cast<int>(x < -(1 << 30) ? -(1 << 30) : (x > (1 << 30) ? (1 << 30) : x)); };
-  const int blo = a.masked ? clamp30(a.band_lo) : -(1 << 30);
-  const int bhi = a.masked ? clamp30(a.band_hi) : (1 << 30);
+  const int T_ = static_cast<int>(a.t), S_ = static_cast<int>(a.s);
+  const int k0 = kblk * 128, kw0 = k0 + 32 * w;
+  const int cmg = c - 4 * G;
 
-  // this wave's K and V rows as B operands (lane: row r32, features 16 ks + 8 g .. +8)
-  u32x4 kreg[KS], vreg[KS];
+  u32x4 kreg[2][C::KS], vreg[2][C::KS];
   {
-    const uint32_t koff = static_cast<uint32_t>(r32 * a.k_st * 2 + g * 16);
-    const uint32_t voff = static_cast<uint32_t>(r32 * a.v_st * 2 + g * 16);
-    const uint16_t* kbs = kp + static_cast<int64_t>(kw0) * a.k_st;
-    const uint16_t* vbs = vp + static_cast<int64_t>(kw0) * a.v_st;
+    const uint32_t koff = static_cast<uint32_t>(c * a.k_st * 2 + G * 16);
+    const uint32_t voff = static_cast<uint32_t>(c * a.v_st * 2 + G * 16);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kreg[ks] = krow < S_ ? gload<u32x4>(kbs + ks * 16, koff) : u32x4{0u, 0u, 0u, 0u};
-      vreg[ks] = krow < S_ ? gload<u32x4>(vbs + ks * 16, voff) : u32x4{0u, 0u, 0u, 0u};
+    for (int hh = 0; hh < 2; ++hh) {
+      const bool ok = kw0 + 16 * hh + c < S_;
+      const uint16_t* kbs = kp + static_cast<int64_t>(kw0 + 16 * hh) * a.k_st;
+      const uint16_t* vbs = vp + static_cast<int64_t>(kw0 + 16 * hh) * a.v_st;
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) {
+        kreg[hh][ks] = ok ? gload<u32x4>(kbs + ks * 32, koff) : u32x4{0u, 0u, 0u, 0u};
+        vreg[hh][ks] = ok ? gload<u32x4>(vbs + ks * 32, voff) : u32x4{0u, 0u, 0u, 0u};
+      }
     }
   }
-
-  const int nqt = static_cast<int>((T_ + QT - 1) / QT);
-  int qt_lo = 0, qt_hi = nqt;
-  if (a.masked && a.prune) {
-    const int64_t klast = (k0 + BK - 1 < S_ ? k0 + BK - 1 : S_ - 1);
-    if (a.band_hi < INT64_MAX / 4) {  // q >= key - hi
-      const int64_t qmin = k0 - a.band_hi;
-      qt_lo = qmin <= 0 ? 0 : static_cast<int>(qmin / QT < nqt ? qmin / QT : nqt);
-    }
-    if (a.band_lo > INT64_MIN / 4) {  // q <= key - lo
-      const int64_t qmax = klast - a.band_lo;
-      qt_hi = qmax < 0 ? 0 : static_cast<int>(qmax / QT + 1 < nqt ? qmax / QT + 1 : nqt);
-    }
-  }
+  const Sweep sw = sweep_plan(a, k0, T_, false);
+  const int nlive = sw.hi - sw.lo;
 
   const uint32_t grq = static_cast<uint32_t>(a.q_st * 2), gro = static_cast<uint32_t>(a.o_st * 2);
+  uint32_t dq_off[C::NDMA], do_off[C::NDMA];
+  dma_offsets<D>(dq_off, lane, w, grq);
+  dma_offsets<D>(do_off, lane, w, gro);
+  Lane16<D> L;
+  L.init(lane);
   const rsrc_t sr = make_rsrc(a.ws, static_cast<uint32_t>(3 * a.rows * 4));
-  TileLane<D> ql, ol;
-  ql.init(lane, w, r32, g, grq);
-  ol.init(lane, w, r32, g, gro);
-  // The sweep runs over (query head of the group, query tile) items, head-major,
-  // with two cursors kept by increments (no divisions): one staging a stage
-  // ahead, one computing.
-  struct Cursor {
-    int gq, qt;
-  };
-  const int nqt_live = qt_hi - qt_lo;
-  auto advance = [&](Cursor& c) {
-    if (++c.qt == qt_hi) {
-      c.qt = qt_lo;
-      ++c.gq;
-    }
-  };
-  // stats: wave 0 loads delta (lanes 0-31) and lse2 (32-63), then pm (0-31)
-  const uint32_t st_lane0 = static_cast<uint32_t>(((lane >> 5) * a.rows + r32) * 4);
-  const uint32_t st_lane1 = static_cast<uint32_t>((2 * a.rows + r32) * 4);
+  // stats: wave 0 loads -delta (lanes 0-31) and lse2 (32-63), then pm (0-31)
+  const uint32_t st_lane = static_cast<uint32_t>(((lane >> 5) * a.rows + (lane & 31)) * 4);
   const int64_t hq0 = hkv * a.group;  // the group's first query head
-  auto qbuf = [&](int buf, int sub) { return smem + (buf * kSub + sub) * TT::BYTES; };
-  auto obuf = [&](int buf, int sub) { return smem + ((2 + buf) * kSub + sub) * TT::BYTES; };
-  auto sbuf = [&](int buf, int sub) {
-    return reinterpret_cast<float*>(smem + STATB + (buf * kSub + sub) * 3 * QT * 4);
-  };
-  Cursor sc{0, qt_lo};  // the next item to stage
-  auto stage = [&](int buf) {  // the next kSub items, into buffer buf
-#pragma unroll
-    for (int sub = 0; sub < kSub; ++sub) {
-      if (sc.gq >= a.group) break;
-      const int64_t hq = hq0 + sc.gq;
-      const rsrc_t qr = make_rsrc(a.q + b * a.q_sb + hq * a.q_sh, static_cast<uint32_t>((T_ - 1) * a.q_st * 2 + D * 2));
-      const rsrc_t orr =
-          make_rsrc(a.dout + b * a.o_sb + hq * a.o_sh, static_cast<uint32_t>((T_ - 1) * a.o_st * 2 + D * 2));
-      ql.stage(qr, qbuf(buf, sub), static_cast<uint32_t>(sc.qt * QT), grq, w);
-      ol.stage(orr, obuf(buf, sub), static_cast<uint32_t>(sc.qt * QT), gro, w);
-      if (w == 0) {
-        unsigned char* sl = reinterpret_cast<unsigned char*>(sbuf(buf, sub));
-        const uint32_t srow = static_cast<uint32_t>(((b * a.heads + hq) * T_ + sc.qt * QT) * 4);
-        dma4(sr, sl, st_lane0, srow);
-        if (lane < 32) dma4(sr, sl + 2 * QT * 4, st_lane1, srow);
-      }
-      advance(sc);
+  // the staging cursor: (query head of the group, query tile), head-major
+  int s_gq = 0, s_qt = sw.lo;
+  auto stage = [&](int buf) {
+    const int64_t hq = hq0 + s_gq;
+    const rsrc_t qr = make_rsrc(a.q + b * a.q_sb + hq * a.q_sh, static_cast<uint32_t>((a.t - 1) * a.q_st * 2 + D * 2));
+    const rsrc_t orr =
+        make_rsrc(a.dout + b * a.o_sb + hq * a.o_sh, static_cast<uint32_t>((a.t - 1) * a.o_st * 2 + D * 2));
+    dma_tile<D>(qr, smem + buf * C::TILEB, dq_off, static_cast<uint32_t>(s_qt * 32), grq, w);
+    dma_tile<D>(orr, smem + (2 + buf) * C::TILEB, do_off, static_cast<uint32_t>(s_qt * 32), gro, w);
+    if (w == 0) {
+      unsigned char* sl = smem + STATB + buf * 3 * 32 * 4;
+      const uint32_t srow = static_cast<uint32_t>(((b * a.heads + hq) * a.t + s_qt * 32) * 4);
+      dma4(sr, sl, st_lane, srow);
+      if (lane < 32) dma4(sr, sl + 2 * 32 * 4, st_lane, srow + static_cast<uint32_t>(2 * a.rows * 4));
+    }
+    if (++s_qt == sw.hi) {
+      s_qt = sw.lo;
+      ++s_gq;
     }
   };
 
-  f32x16 dkacc[DB], dvacc[DB];
+  f32x4 dkacc[C::FB][2], dvacc[C::FB][2];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    dkacc[db] = f32x16{};
-    dvacc[db] = f32x16{};
-  }
+  for (int fb = 0; fb < C::FB; ++fb)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) dkacc[fb][hh] = dvacc[fb][hh] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  Cursor cc{0, qt_lo};  // the next item to compute
-  if (nqt_live > 0) stage(0);
-  for (int buf = 0; nqt_live > 0 && cc.gq < a.group; buf ^= 1) {
+  auto tile = [&](auto bufc, int q0, auto cutc) {
+    constexpr bool CUT = decltype(cutc)::value;
+    constexpr int buf = decltype(bufc)::value;
+    const unsigned char* qt = smem + buf * C::TILEB;
+    const unsigned char* ot = smem + (2 + buf) * C::TILEB;
+    const float* stl = reinterpret_cast<const float*>(smem + STATB + buf * 3 * 32 * 4);
+    // S accumulates from -lse (score units) and dP from -delta, both per query
+    // row, so the products leave S - lse and dP - delta
+    f32x4 sacc[2][2], pacc[2][2];  // [query half][key half]
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh) {
+      const f32x4 nd = *reinterpret_cast<const f32x4*>(stl + 16 * qh + 4 * G);  // -delta of queries 16 qh + 4 G + i
+      const f32x4 nl = *reinterpret_cast<const f32x4*>(stl + 32 + 16 * qh + 4 * G);  // -lse / scale
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        sacc[qh][hh] = nl;
+        pacc[qh][hh] = nd;
+      }
+    }
+    // operands n = 2 ks + qh, read one step ahead of their four products
+    u32x4 qq[2], oo[2];
+    qq[0] = L.row_frag(qt, 0, 0);
+    oo[0] = L.row_frag(ot, 0, 0);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int n = 0; n < 2 * C::KS; ++n) {
+      const int ks = n >> 1, qh = n & 1;
+      if (n + 1 < 2 * C::KS) {
+        qq[(n + 1) & 1] = L.row_frag(qt, (n + 1) & 1, (n + 1) >> 1);
+        oo[(n + 1) & 1] = L.row_frag(ot, (n + 1) & 1, (n + 1) >> 1);
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        sacc[qh][hh] = mfma16<T>(qq[n & 1], kreg[hh][ks], sacc[qh][hh]);
+        pacc[qh][hh] = mfma16<T>(oo[n & 1], vreg[hh][ks], pacc[qh][hh]);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 p[2], ds[2];
+    f32x4 pmv[2];
+    if constexpr (CUT) {
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh) pmv[qh] = *reinterpret_cast<const f32x4*>(stl + 64 + 16 * qh + 4 * G);
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float e[8], g[8];
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pr = fast_exp2(sacc[qh][hh][i] * a.c2);
+          e[4 * qh + i] = pr;
+          g[4 * qh + i] = pr * pacc[qh][hh][i];
+        }
+      if constexpr (CUT) {
+        // live: query < t, lo <= key - query <= hi; a masked score's probability
+        // is its row's pm (0 unless the row is fully masked) and carries no gradient
+        // key - query = (kw0 + 16 hh - q0) + (c - 4 G) - (16 qh + i): a scalar plus one lane constant
+        const int dl = (kw0 + 16 * hh - q0) + cmg;
+        const int rl = T_ - q0 - 4 * G;  // query 16 qh + i of the tile is live below this
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int cc = 16 * qh + i, d = dl - cc;
+            const bool rowok = cc < rl;
+            const bool inb = !a.masked || (d >= a.band_lo32 && d <= a.band_hi32);
+            e[4 * qh + i] = rowok ? (inb ? e[4 * qh + i] : pmv[qh][i]) : 0.f;
+            g[4 * qh + i] = rowok && inb ? g[4 * qh + i] : 0.f;
+          }
+      }
+      p[hh] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
+      ds[hh] = u32x4{pack2<T>(g[0], g[1]), pack2<T>(g[2], g[3]), pack2<T>(g[4], g[5]), pack2<T>(g[6], g[7])};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
+    u32x4 of[2], qf[2];
+    of[0] = L.tr_frag(ot, 0);
+    qf[0] = L.tr_frag(qt, 0);
+#pragma unroll
+    for (int fb = 0; fb < C::FB; ++fb) {
+      if (fb + 1 < C::FB) {
+        of[(fb + 1) & 1] = L.tr_frag(ot, fb + 1);
+        qf[(fb + 1) & 1] = L.tr_frag(qt, fb + 1);
+      }
+      dvacc[fb][0] = mfma16<T>(of[fb & 1], p[0], dvacc[fb][0]);
+      dvacc[fb][1] = mfma16<T>(of[fb & 1], p[1], dvacc[fb][1]);
+      dkacc[fb][0] = mfma16<T>(qf[fb & 1], ds[0], dkacc[fb][0]);
+      dkacc[fb][1] = mfma16<T>(qf[fb & 1], ds[1], dkacc[fb][1]);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // item j = gq * nlive + (qt - lo) lives in buffer j & 1; the staging cursor runs one item ahead
+  const int nitems = a.group * nlive;
+  if (nitems > 0) stage(0);
+  auto one = [&](int j, int qt, auto bufc, auto cutc) {
+    constexpr int buf = decltype(bufc)::value;
     wait_vmcnt0();
     __syncthreads();
-    if (sc.gq < a.group) stage(buf ^ 1);  // the next stage, into the idle buffers
-#pragma unroll
-    for (int sub = 0; sub < kSub; ++sub) {
-      if (cc.gq >= a.group) break;
-      const int qt = cc.qt;
-      advance(cc);
-      const int64_t q0 = static_cast<int64_t>(qt) * QT;
-      const int64_t dmin = kw0 - (q0 + QT - 1), dmax = kw0 + 31 - q0;  // key - q over the tile
-      bool dead = false, cut = q0 + QT > T_ || kw0 + 32 > S_;
-      if (a.masked) {
-        dead = a.prune && (dmin > a.band_hi || dmax < a.band_lo);
-        cut = cut || dmin < a.band_lo || dmax > a.band_hi;
-      }
-      if (dead) continue;
-      const unsigned char* q_l = qbuf(buf, sub);
-      const unsigned char* o_l = obuf(buf, sub);
-      const float* stl = sbuf(buf, sub);
-      // accumulator i of lane-half g: query q0 + 16 (i / 8) + 8 g + i % 8, key krow.
-      // dP - delta accumulates from the rows' -delta (the MFMA adds it).
-      f32x16 sacc = f32x16{}, pacc;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int rb = 16 * hh + 8 * g;
-        const f32x4 d0 = *reinterpret_cast<const f32x4*>(stl + rb);  // -delta
-        const f32x4 d1 = *reinterpret_cast<const f32x4*>(stl + rb + 4);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pacc[8 * hh + j] = j < 4 ? d0[j] : d1[j - 4];
-      }
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        sacc = mfma32<T>(ql.row_frag(q_l, ks), kreg[ks], sacc);
-        pacc = mfma32<T>(ol.row_frag(o_l, ks), vreg[ks], pacc);
-      }
-      __builtin_amdgcn_s_setprio(0);
-      // masks in 32-bit offsets from the tile (band limits clamped to +-2^30)
-      const int dk0 = static_cast<int>(krow - q0);
-      const int qlim = krow < S_ ? static_cast<int>(T_ - q0 < (1 << 30) ? T_ - q0 : (1 << 30)) : 0;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int rb = 16 * hh + 8 * g;
-        const f32x4 l0 = *reinterpret_cast<const f32x4*>(stl + QT + rb);
-        const f32x4 l1 = *reinterpret_cast<const f32x4*>(stl + QT + rb + 4);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int i = 8 * hh + j;
-          const float lv = j < 4 ? l0[j] : l1[j - 4];
-          const float p = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lv));
-          pacc[i] = p * pacc[i];
-          sacc[i] = p;
-        }
-      }
-      // Masked tiles (uniform branch) fix up the probabilities with selects that
-      // read the rows' pm values as vectors: no per-element branches, which
-      // would split the tile into basic blocks the scheduler cannot interleave
-      // with the MFMAs.
-      if (cut) {
-        asm volatile("" ::: "memory");  // keeps the branch: if-converted, every tile would pay the selects
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int rb = 16 * hh + 8 * g;
-          const f32x4 m0 = *reinterpret_cast<const f32x4*>(stl + 2 * QT + rb);
-          const f32x4 m1 = *reinterpret_cast<const f32x4*>(stl + 2 * QT + rb + 4);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int i = 8 * hh + j;
-            const float pm = j < 4 ? m0[j] : m1[j - 4];  // the row's masked-score probability (0 unless fully masked)
-            const int dd = dk0 - rb - j;                  // key - query
-            const bool row_live = rb + j < qlim;
-            const bool in_band = dd >= blo && dd <= bhi;
-            sacc[i] = row_live ? (in_band ? sacc[i] : pm) : 0.f;
-            pacc[i] = row_live && in_band ? pacc[i] : 0.f;
-          }
-        }
-      }
-      const u32x4 p0 = pack8<T>(sacc, 0), p1 = pack8<T>(sacc, 1);
-      const u32x4 s0 = pack8<T>(pacc, 0), s1 = pack8<T>(pacc, 1);
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        dvacc[db] = mfma32<T>(ol.tr_frag(o_l, 0, db), p0, dvacc[db]);
-        dvacc[db] = mfma32<T>(ol.tr_frag(o_l, 1, db), p1, dvacc[db]);
-        dkacc[db] = mfma32<T>(ql.tr_frag(q_l, 0, db), s0, dkacc[db]);
-        dkacc[db] = mfma32<T>(ql.tr_frag(q_l, 1, db), s1, dkacc[db]);
-      }
-      __builtin_amdgcn_s_setprio(0);
+    if (j + 1 < nitems) stage(buf ^ 1);
+    const int q0 = qt * 32;
+    bool dead = false;
+    if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's keys see no live query here
+      const int dmin = kw0 - (q0 + 31), dmax = kw0 + 31 - q0;
+      dead = dmin > a.band_hi32 || dmax < a.band_lo32;
     }
+    if (!dead) tile(bufc, q0, cutc);
+  };
+  for (int gq = 0; gq < a.group && nlive > 0; ++gq) {
+    const int j0 = gq * nlive - sw.lo;  // item of query tile qt: j0 + qt
+    auto sweep = [&](int from, int to, auto cutc) {
+      int qt = from;
+      if (qt < to && ((j0 + qt) & 1)) {
+        one(j0 + qt, qt, std::integral_constant<int, 1>{}, cutc);
+        ++qt;
+      }
+      for (; qt + 1 < to; qt += 2) {
+        one(j0 + qt, qt, std::integral_constant<int, 0>{}, cutc);
+        one(j0 + qt + 1, qt + 1, std::integral_constant<int, 1>{}, cutc);
+      }
+      if (qt < to) one(j0 + qt, qt, std::integral_constant<int, 0>{}, cutc);
+    };
+    sweep(sw.lo, sw.flo, std::true_type{});
+    sweep(sw.flo, sw.fhi, std::false_type{});
+    sweep(sw.fhi, sw.hi, std::true_type{});
   }
   wait_vmcnt0();
 
-  if (krow < S_) {
-    store_rows_t<T, D>(a.dk + b * a.k_sb + hkv * a.k_sh + static_cast<int64_t>(kw0) * a.k_st, a.k_st, r32, g, dkacc,
-                       a.scale);
-    store_rows_t<T, D>(a.dv + b * a.v_sb + hkv * a.v_sh + static_cast<int64_t>(kw0) * a.v_st, a.v_st, r32, g, dvacc,
-                       1.0f);
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    if (kw0 + 16 * hh + c >= S_) continue;
+    const uint32_t koff = static_cast<uint32_t>(c * a.k_st * 2 + G * 8);
+    const uint32_t voff = static_cast<uint32_t>(c * a.v_st * 2 + G * 8);
+    uint16_t* kbase = a.dk + b * a.k_sb + hkv * a.k_sh + static_cast<int64_t>(kw0 + 16 * hh) * a.k_st;
+    uint16_t* vbase = a.dv + b * a.v_sb + hkv * a.v_sh + static_cast<int64_t>(kw0 + 16 * hh) * a.v_st;
+#pragma unroll
+    for (int fb = 0; fb < C::FB; ++fb) {
+      const f32x4 x = dkacc[fb][hh], y = dvacc[fb][hh];
+      gstore<u32x2>(kbase + 16 * fb, koff,
+                    u32x2{pack2<T>(x[0] * a.scale, x[1] * a.scale), pack2<T>(x[2] * a.scale, x[3] * a.scale)});
+      gstore<u32x2>(vbase + 16 * fb, voff, u32x2{pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])});
+    }
   }
 }
 
@@ -545,6 +636,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_main(BwdArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
   int bid = blockIdx.x;
+  int role, idx;
   if (a.xcd_remap == 2) {
     // Within an XCD (bid % 8) workgroups go in order round-robin to its four
     // shader engines (r % 4): four consecutive r take the same role and block
@@ -556,30 +648,28 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void bwd_main(BwdArgs a) {
     const int nb = a.nkblk, per_inst = 2 * nb;
     const int ipx = (gridDim.x >> 3) / per_inst;  // instances per XCD
     const int inst = x * ipx + (m4 / per_inst) * 4 + s4, step = m4 % per_inst;
-    if ((step & 1) == 0)
-      bwd_dkdv<T, D>(a, inst * nb + (step >> 1), smem);
-    else
-      bwd_dq<T, D>(a, inst * nb + (step >> 1), smem);
-    return;
-  }
-  if (a.xcd_remap) {  // consecutive logical blocks (one instance's) share an XCD's L2
-    const int per = gridDim.x >> 3;
-    bid = (bid & 7) * per + (bid >> 3);
-  }
-  const int nk = a.ninst_kv * a.nkblk, nq = a.ninst * a.nqblk;
-  const int both = 2 * (nk < nq ? nk : nq);
-  int role, idx;
-  if (bid < both) {
-    role = bid & 1;
-    idx = bid >> 1;
+    role = step & 1;
+    idx = inst * nb + (step >> 1);
   } else {
-    role = nk > nq ? 0 : 1;
-    idx = both / 2 + (bid - both);
+    if (a.xcd_remap) {  // consecutive logical blocks (one instance's) share an XCD's L2
+      const int per = gridDim.x >> 3;
+      bid = (bid & 7) * per + (bid >> 3);
+    }
+    const int nk = a.ninst_kv * a.nkblk, nq = a.ninst * a.nqblk;
+    const int both = 2 * (nk < nq ? nk : nq);
+    if (bid < both) {
+      role = bid & 1;
+      idx = bid >> 1;
+    } else {
+      role = nk > nq ? 0 : 1;
+      idx = both / 2 + (bid - both);
+    }
   }
+  // one call site per role: each role's code appears once in the kernel
   if (role == 0)
-    bwd_dkdv<T, D>(a, idx, smem);
+    bwd16_dkdv<T, D>(a, idx, smem);
   else
-    bwd_dq<T, D>(a, idx, smem);
+    bwd16_dq<T, D>(a, idx, smem);
 }
 
 // ---------------------------------------------------------------- fp32 column
@@ -754,8 +844,7 @@ int launch_bwd(BwdArgs a, hipStream_t st) {
   bwd_stats<T, D><<<dim3(static_cast<unsigned>((a.rows + RPB - 1) / RPB)), 256, 0, st>>>(a);
   int rc = check_launch("pdh_flash_bwd (row stats)");
   if (rc) return rc;
-  constexpr int TB = Tile32<D>::BYTES;
-  constexpr int lds = 4 * kSub * TB + 2 * kSub * 3 * 32 * 4;  // the larger of the two roles' needs (dK/dV)
+  constexpr int lds = 4 * B16<D>::TILEB + 2 * 3 * 32 * 4;  // the larger of the two roles' needs (dK/dV)
   const int64_t nblk = static_cast<int64_t>(a.ninst_kv) * a.nkblk + static_cast<int64_t>(a.ninst) * a.nqblk;
   a.xcd_remap = nblk % 8 == 0 ? ((a.ninst % 32 == 0 && a.nkblk == a.nqblk && a.group == 1) ? 2 : 1) : 0;
   bwd_main<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, lds, st>>>(a);
@@ -821,7 +910,7 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
               PDH_EINVAL, "pdh_flash_bwd: strides must be multiples of 8 elements");
   PDH_REQUIRE(G.q_st < (1 << 24) && G.k_st < (1 << 24) && G.v_st < (1 << 24) && G.o_st < (1 << 24), PDH_EINVAL,
               "pdh_flash_bwd: row strides must be < 2^24 elements");
-  PDH_REQUIRE(G.t <= INT32_MAX / 2 && G.s <= INT32_MAX / 2, PDH_EINVAL, "pdh_flash_bwd: sequence too long");
+  PDH_REQUIRE(G.t <= (1 << 29) && G.s <= (1 << 29), PDH_EINVAL, "pdh_flash_bwd: sequence too long (t, s <= 2^29)");
   PDH_REQUIRE(G.s * G.k_st * 2 < INT32_MAX && G.s * G.v_st * 2 < INT32_MAX && G.t * G.q_st * 2 < INT32_MAX &&
                   G.t * G.o_st * 2 < INT32_MAX,
               PDH_EINVAL, "pdh_flash_bwd: one instance's rows must span < 2 GiB");
@@ -840,6 +929,12 @@ extern "C" int pdh_flash_bwd(const void* q, const void* k, const void* v, const 
             G.k_sh, G.k_st, G.v_sb, G.v_sh, G.v_st, G.o_sb, G.o_sh, G.o_st, scale, scale * kLog2e, fill * kLog2e,
             masked, band_lo, band_hi, prune_ok, static_cast<int>(ninst), static_cast<int>(G.batch * G.heads_kv),
             static_cast<int>((G.s + 127) / 128), static_cast<int>((G.t + 127) / 128), 0};
+  {
+    constexpr int64_t kBand32 = (int64_t{1} << 29) + 64;
+    auto clamp32 = [](int64_t x) { return static_cast<int>(x < -kBand32 ? -kBand32 : (x > kBand32 ? kBand32 : x)); };
+    a.band_lo32 = clamp32(band_lo);
+    a.band_hi32 = clamp32(band_hi);
+  }
   hipStream_t st = as_stream(stream);
   if (dtype == PDH_BF16)
     return G.e == 128 ? launch_bwd<__hip_bfloat16, 128>(a, st) : launch_bwd<__hip_bfloat16, 64>(a, st);
