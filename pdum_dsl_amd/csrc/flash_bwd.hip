@@ -117,8 +117,13 @@ __global__ __launch_bounds__(256) void bwd_stats(BwdArgs a) {
 // fully live for the whole workgroup run a mask-free body; the sweep runs in
 // buffer pairs so every LDS address is a lane offset plus an immediate.
 
+#ifndef PDH_BWD_SUB
+#define PDH_BWD_SUB 2
+#endif
+
 template <int D>
 struct B16 {
+  static constexpr int NSUB = D == 64 ? PDH_BWD_SUB : 1;  // tiles staged per barrier (double buffered)
   static constexpr int ROWB = D * 2, CPR = D / 8, TILEB = 32 * ROWB, RPK = 1024 / ROWB, NBLK = TILEB / 1024;
   static constexpr int NDMA = (NBLK + 3) / 4;
   static constexpr int KS = D / 32;  // k-steps of 32 features
@@ -232,6 +237,30 @@ __device__ __forceinline__ Sweep sweep_plan(const BwdArgs& a, int o0, int ext, b
   return Sweep{lo, hi, flo, fhi};
 }
 
+// f(integral_constant<0>), ..., f(integral_constant<N - 1>), in order.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+}
+
+// Stages of NSUB tiles from sw.lo: stages [0, f0) and [f1, n) hold a tile
+// outside the fully-live run (or past the range), stages [f0, f1) only
+// fully-live tiles.
+struct Stages {
+  int n, f0, f1;
+};
+
+template <int NSUB>
+__device__ __forceinline__ Stages stage_plan(const Sweep& sw) {
+  const int n = (sw.hi - sw.lo + NSUB - 1) / NSUB;
+  int f0 = (sw.flo - sw.lo + NSUB - 1) / NSUB, f1 = (sw.fhi - sw.lo) / NSUB;
+  if (f1 < f0) f1 = f0;
+  return Stages{n, f0, f1};
+}
+
 // -------------------------------------------------------------------- dQ
 //
 // Workgroup: 4 waves x 32 query rows; key tiles of 32 rows (K, V) double
@@ -286,20 +315,27 @@ __device__ __forceinline__ void bwd16_dq(const BwdArgs& a, int bid, unsigned cha
   dma_offsets<D>(dv_off, lane, w, grv);
   Lane16<D> L;
   L.init(lane);
-  auto stage = [&](int tile, int buf) {
-    dma_tile<D>(kr, smem + buf * C::TILEB, dk_off, static_cast<uint32_t>(tile * 32), grk, w);
-    dma_tile<D>(vr, smem + (2 + buf) * C::TILEB, dv_off, static_cast<uint32_t>(tile * 32), grv, w);
+  const int kt_lo = sw.lo, kt_hi = sw.hi;
+  // K tiles [buf][sub] from 0, V tiles after them
+  auto stage = [&](int st, int buf) {
+#pragma unroll
+    for (int j = 0; j < C::NSUB; ++j) {
+      const int tile = kt_lo + st * C::NSUB + j;
+      if (tile >= kt_hi) break;
+      dma_tile<D>(kr, smem + (buf * C::NSUB + j) * C::TILEB, dk_off, static_cast<uint32_t>(tile * 32), grk, w);
+      dma_tile<D>(vr, smem + ((2 + buf) * C::NSUB + j) * C::TILEB, dv_off, static_cast<uint32_t>(tile * 32), grv, w);
+    }
   };
 
   f32x4 dqacc[C::FB][2];
 #pragma unroll
   for (int fb = 0; fb < C::FB; ++fb) dqacc[fb][0] = dqacc[fb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto tile = [&](auto bufc, int key0, auto cutc) {
+  auto tile = [&](auto slotc, int key0, auto cutc) {
     constexpr bool CUT = decltype(cutc)::value;
-    constexpr int buf = decltype(bufc)::value;
-    const unsigned char* kt = smem + buf * C::TILEB;
-    const unsigned char* vt = smem + (2 + buf) * C::TILEB;
+    constexpr int slot = decltype(slotc)::value;  // buf * NSUB + sub
+    const unsigned char* kt = smem + slot * C::TILEB;
+    const unsigned char* vt = smem + (2 * C::NSUB + slot) * C::TILEB;
     f32x4 sacc[2][2], pacc[2][2];  // [key half][query half]
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -357,33 +393,39 @@ __device__ __forceinline__ void bwd16_dq(const BwdArgs& a, int bid, unsigned cha
     __builtin_amdgcn_s_setprio(0);
   };
 
-  const int kt_lo = sw.lo, kt_hi = sw.hi;
-  if (kt_lo < kt_hi) stage(kt_lo, 0);
-  auto one = [&](int kt, auto bufc, auto cutc) {
+  const Stages sp = stage_plan<C::NSUB>(sw);
+  if (sp.n > 0) stage(0, 0);
+  // stage st lives in buffer st & 1; its tiles run with that buffer a
+  // compile-time constant, so every LDS address is a lane offset plus an immediate
+  auto one = [&](int st, auto bufc, auto cutc) {
     constexpr int buf = decltype(bufc)::value;
     wait_vmcnt0();
     __syncthreads();
-    if (kt + 1 < kt_hi) stage(kt + 1, buf ^ 1);
-    const int key0 = kt * 32;
-    bool dead = false;
-    if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's rows see no live key here
-      const int dmin = key0 - (qw0 + 31), dmax = key0 + 31 - qw0;
-      dead = dmin > a.band_hi32 || dmax < a.band_lo32;
-    }
-    if (!dead) tile(bufc, key0, cutc);
+    if (st + 1 < sp.n) stage(st + 1, buf ^ 1);
+    static_for<C::NSUB>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      const int kt = kt_lo + st * C::NSUB + j;
+      bool dead = decltype(cutc)::value && kt >= kt_hi;  // past the range (last stage only)
+      const int key0 = kt * 32;
+      if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's rows see no live key here
+        const int dmin = key0 - (qw0 + 31), dmax = key0 + 31 - qw0;
+        dead = dead || dmin > a.band_hi32 || dmax < a.band_lo32;
+      }
+      if (!dead) tile(std::integral_constant<int, buf * C::NSUB + j>{}, key0, cutc);
+    });
   };
   auto sweep = [&](int from, int to, auto cutc) {
-    int kt = from;
-    if (kt < to && ((kt - kt_lo) & 1)) one(kt++, std::integral_constant<int, 1>{}, cutc);
-    for (; kt + 1 < to; kt += 2) {
-      one(kt, std::integral_constant<int, 0>{}, cutc);
-      one(kt + 1, std::integral_constant<int, 1>{}, cutc);
+    int st = from;
+    if (st < to && (st & 1)) one(st++, std::integral_constant<int, 1>{}, cutc);
+    for (; st + 1 < to; st += 2) {
+      one(st, std::integral_constant<int, 0>{}, cutc);
+      one(st + 1, std::integral_constant<int, 1>{}, cutc);
     }
-    if (kt < to) one(kt, std::integral_constant<int, 0>{}, cutc);
+    if (st < to) one(st, std::integral_constant<int, 0>{}, cutc);
   };
-  sweep(kt_lo, sw.flo, std::true_type{});
-  sweep(sw.flo, sw.fhi, std::false_type{});
-  sweep(sw.fhi, kt_hi, std::true_type{});
+  sweep(0, sp.f0, std::true_type{});
+  sweep(sp.f0, sp.f1, std::false_type{});
+  sweep(sp.f1, sp.n, std::true_type{});
   wait_vmcnt0();
 
 #pragma unroll
@@ -414,7 +456,7 @@ __device__ __forceinline__ void bwd16_dq(const BwdArgs& a, int bid, unsigned cha
 template <typename T, int D>
 __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned char* smem) {  // Q[2], dO[2], stats[2]
   using C = B16<D>;
-  constexpr int STATB = 4 * C::TILEB;  // [2][-delta | lse2 | pm] x 32 floats
+  constexpr int STATB = 4 * C::NSUB * C::TILEB;  // [2 * NSUB][-delta | -lse / scale | pm] x 32 floats
   const int lane = threadIdx.x & 63, w = wave_id(), c = lane & 15, G = lane >> 4;
   const int64_t kinst = bid / a.nkblk;
   const int kblk = bid % a.nkblk;  // early key blocks see the most queries under causal masks: launched first
@@ -455,22 +497,31 @@ __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned c
   const uint32_t st_lane = static_cast<uint32_t>(((lane >> 5) * a.rows + (lane & 31)) * 4);
   const int64_t hq0 = hkv * a.group;  // the group's first query head
   // the staging cursor: (query head of the group, query tile), head-major
-  int s_gq = 0, s_qt = sw.lo;
+  const Stages sp = stage_plan<C::NSUB>(sw);
+  // the staging cursor: (query head of the group, stage), head-major; Q tiles
+  // [buf][sub] from 0, dO tiles after them, then the rows' statistics
+  int s_gq = 0, s_st = 0;
   auto stage = [&](int buf) {
     const int64_t hq = hq0 + s_gq;
     const rsrc_t qr = make_rsrc(a.q + b * a.q_sb + hq * a.q_sh, static_cast<uint32_t>((a.t - 1) * a.q_st * 2 + D * 2));
     const rsrc_t orr =
         make_rsrc(a.dout + b * a.o_sb + hq * a.o_sh, static_cast<uint32_t>((a.t - 1) * a.o_st * 2 + D * 2));
-    dma_tile<D>(qr, smem + buf * C::TILEB, dq_off, static_cast<uint32_t>(s_qt * 32), grq, w);
-    dma_tile<D>(orr, smem + (2 + buf) * C::TILEB, do_off, static_cast<uint32_t>(s_qt * 32), gro, w);
-    if (w == 0) {
-      unsigned char* sl = smem + STATB + buf * 3 * 32 * 4;
-      const uint32_t srow = static_cast<uint32_t>(((b * a.heads + hq) * a.t + s_qt * 32) * 4);
-      dma4(sr, sl, st_lane, srow);
-      if (lane < 32) dma4(sr, sl + 2 * 32 * 4, st_lane, srow + static_cast<uint32_t>(2 * a.rows * 4));
+#pragma unroll
+    for (int j = 0; j < C::NSUB; ++j) {
+      const int qt = sw.lo + s_st * C::NSUB + j;
+      if (qt >= sw.hi) break;
+      const int slot = buf * C::NSUB + j;
+      dma_tile<D>(qr, smem + slot * C::TILEB, dq_off, static_cast<uint32_t>(qt * 32), grq, w);
+      dma_tile<D>(orr, smem + (2 * C::NSUB + slot) * C::TILEB, do_off, static_cast<uint32_t>(qt * 32), gro, w);
+      if (w == 0) {
+        unsigned char* sl = smem + STATB + slot * 3 * 32 * 4;
+        const uint32_t srow = static_cast<uint32_t>(((b * a.heads + hq) * a.t + qt * 32) * 4);
+        dma4(sr, sl, st_lane, srow);
+        if (lane < 32) dma4(sr, sl + 2 * 32 * 4, st_lane, srow + static_cast<uint32_t>(2 * a.rows * 4));
+      }
     }
-    if (++s_qt == sw.hi) {
-      s_qt = sw.lo;
+    if (++s_st == sp.n) {
+      s_st = 0;
       ++s_gq;
     }
   };
@@ -481,12 +532,12 @@ __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned c
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) dkacc[fb][hh] = dvacc[fb][hh] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto tile = [&](auto bufc, int q0, auto cutc) {
+  auto tile = [&](auto slotc, int q0, auto cutc) {
     constexpr bool CUT = decltype(cutc)::value;
-    constexpr int buf = decltype(bufc)::value;
-    const unsigned char* qt = smem + buf * C::TILEB;
-    const unsigned char* ot = smem + (2 + buf) * C::TILEB;
-    const float* stl = reinterpret_cast<const float*>(smem + STATB + buf * 3 * 32 * 4);
+    constexpr int slot = decltype(slotc)::value;  // buf * NSUB + sub
+    const unsigned char* qt = smem + slot * C::TILEB;
+    const unsigned char* ot = smem + (2 * C::NSUB + slot) * C::TILEB;
+    const float* stl = reinterpret_cast<const float*>(smem + STATB + slot * 3 * 32 * 4);
     // S accumulates from -lse (score units) and dP from -delta, both per query
     // row, so the products leave S - lse and dP - delta
     f32x4 sacc[2][2], pacc[2][2];  // [query half][key half]
@@ -576,39 +627,43 @@ __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned c
     __builtin_amdgcn_s_setprio(0);
   };
 
-  // item j = gq * nlive + (qt - lo) lives in buffer j & 1; the staging cursor runs one item ahead
-  const int nitems = a.group * nlive;
-  if (nitems > 0) stage(0);
-  auto one = [&](int j, int qt, auto bufc, auto cutc) {
+  // stage J = gq * sp.n + st lives in buffer J & 1; the staging cursor runs one stage ahead
+  const int nst = nlive > 0 ? a.group * sp.n : 0;
+  if (nst > 0) stage(0);
+  auto one = [&](int J, int st, auto bufc, auto cutc) {
     constexpr int buf = decltype(bufc)::value;
     wait_vmcnt0();
     __syncthreads();
-    if (j + 1 < nitems) stage(buf ^ 1);
-    const int q0 = qt * 32;
-    bool dead = false;
-    if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's keys see no live query here
-      const int dmin = kw0 - (q0 + 31), dmax = kw0 + 31 - q0;
-      dead = dmin > a.band_hi32 || dmax < a.band_lo32;
-    }
-    if (!dead) tile(bufc, q0, cutc);
+    if (J + 1 < nst) stage(buf ^ 1);
+    static_for<C::NSUB>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      const int qt = sw.lo + st * C::NSUB + j;
+      bool dead = decltype(cutc)::value && qt >= sw.hi;  // past the range (last stage only)
+      const int q0 = qt * 32;
+      if (decltype(cutc)::value && a.masked && a.prune) {  // this wave's keys see no live query here
+        const int dmin = kw0 - (q0 + 31), dmax = kw0 + 31 - q0;
+        dead = dead || dmin > a.band_hi32 || dmax < a.band_lo32;
+      }
+      if (!dead) tile(std::integral_constant<int, buf * C::NSUB + j>{}, q0, cutc);
+    });
   };
   for (int gq = 0; gq < a.group && nlive > 0; ++gq) {
-    const int j0 = gq * nlive - sw.lo;  // item of query tile qt: j0 + qt
+    const int J0 = gq * sp.n;  // stage st of this head: J0 + st
     auto sweep = [&](int from, int to, auto cutc) {
-      int qt = from;
-      if (qt < to && ((j0 + qt) & 1)) {
-        one(j0 + qt, qt, std::integral_constant<int, 1>{}, cutc);
-        ++qt;
+      int st = from;
+      if (st < to && ((J0 + st) & 1)) {
+        one(J0 + st, st, std::integral_constant<int, 1>{}, cutc);
+        ++st;
       }
-      for (; qt + 1 < to; qt += 2) {
-        one(j0 + qt, qt, std::integral_constant<int, 0>{}, cutc);
-        one(j0 + qt + 1, qt + 1, std::integral_constant<int, 1>{}, cutc);
+      for (; st + 1 < to; st += 2) {
+        one(J0 + st, st, std::integral_constant<int, 0>{}, cutc);
+        one(J0 + st + 1, st + 1, std::integral_constant<int, 1>{}, cutc);
       }
-      if (qt < to) one(j0 + qt, qt, std::integral_constant<int, 0>{}, cutc);
+      if (st < to) one(J0 + st, st, std::integral_constant<int, 0>{}, cutc);
     };
-    sweep(sw.lo, sw.flo, std::true_type{});
-    sweep(sw.flo, sw.fhi, std::false_type{});
-    sweep(sw.fhi, sw.hi, std::true_type{});
+    sweep(0, sp.f0, std::true_type{});
+    sweep(sp.f0, sp.f1, std::false_type{});
+    sweep(sp.f1, sp.n, std::true_type{});
   }
   wait_vmcnt0();
 
@@ -844,7 +899,8 @@ int launch_bwd(BwdArgs a, hipStream_t st) {
   bwd_stats<T, D><<<dim3(static_cast<unsigned>((a.rows + RPB - 1) / RPB)), 256, 0, st>>>(a);
   int rc = check_launch("pdh_flash_bwd (row stats)");
   if (rc) return rc;
-  constexpr int lds = 4 * B16<D>::TILEB + 2 * 3 * 32 * 4;  // the larger of the two roles' needs (dK/dV)
+  // the larger of the two roles' needs: dK/dV's Q, dO and row statistics, [2 buffers][NSUB] each
+  constexpr int lds = 2 * B16<D>::NSUB * (2 * B16<D>::TILEB + 3 * 32 * 4);
   const int64_t nblk = static_cast<int64_t>(a.ninst_kv) * a.nkblk + static_cast<int64_t>(a.ninst) * a.nqblk;
   a.xcd_remap = nblk % 8 == 0 ? ((a.ninst % 32 == 0 && a.nkblk == a.nqblk && a.group == 1) ? 2 : 1) : 0;
   bwd_main<T, D><<<dim3(static_cast<unsigned>(nblk)), 256, lds, st>>>(a);
