@@ -134,7 +134,8 @@ int pdh_take_rows(const void* table, const int64_t* idx, void* out, int64_t n_id
  * embedding gradient here. Deterministic: each row sums its value rows in
  * increasing i in fp32 and rounds once. An index outside [0, n_rows) is
  * dropped and adds 1 to *bad (device int, may be NULL). out must not overlap
- * values; n_idx <= 2^24 (the cost grows as n_idx^2 / 256 index compares). */
+ * values. n_idx <= 2^16 (the owner scan grows as n_idx^2 index compares);
+ * larger batches return PDH_EUNSUPPORTED. */
 int pdh_scatter_add_rows(const void* values, const int64_t* idx, void* out, int64_t n_idx, int64_t row_elems,
                          int64_t n_rows, int64_t ld_values, int64_t ld_out, int dtype, int* bad, void* stream);
 

@@ -17,8 +17,11 @@
 // position finds an earlier equal index and leaves), sums the matching
 // value rows in increasing position order in fp32 and rounds once. Finding
 // the owner and its matches reads the index array once per position
-// (n_idx^2 int64 compares from L2 in all), which suits embedding batches of
-// up to some ten thousand indices.
+// (n_idx^2 / 2 int64 compares from L2 in all), so the entry point accepts
+// at most kScatterMaxIdx = 2^16 indices (an embedding batch of 64K tokens:
+// ~2^31 compares, some milliseconds) and refuses more. The owner records
+// the matches as 64-bit lane masks in LDS (8 KB at the limit) once, so rows
+// wider than one 1024-column pass do not repeat the scan.
 #include "common.h"
 
 namespace pdh {
@@ -50,7 +53,8 @@ __global__ __launch_bounds__(256) void zero_rows(unsigned char* __restrict__ out
   }
 }
 
-constexpr int kScatterCols = 4;  // columns per lane per pass over the matches: 1024 per workgroup
+constexpr int kScatterCols = 4;                 // columns per lane per pass over the matches: 1024 per workgroup
+constexpr int64_t kScatterMaxIdx = int64_t{1} << 16;  // positions per launch (the scan is quadratic)
 
 // One workgroup per index position i (256 lanes, 4 waves).
 template <int DT>
@@ -59,7 +63,8 @@ __global__ __launch_bounds__(256) void scatter_add_rows(const unsigned char* __r
                                                         unsigned char* __restrict__ out, int64_t n_idx,
                                                         int64_t row_elems, int64_t n_rows, int64_t ld_values_b,
                                                         int64_t ld_out_b, int* __restrict__ bad) {
-  __shared__ uint64_t hits[4];
+  // hit masks of positions [i, n_idx): mask k covers positions i + 64 k .. + 63
+  __shared__ uint64_t hits[kScatterMaxIdx / 64];
   const int64_t i = blockIdx.x;
   const int64_t v = idx[i];
   if (v < 0 || v >= n_rows) {  // dropped, and counted once per position
@@ -70,27 +75,23 @@ __global__ __launch_bounds__(256) void scatter_add_rows(const unsigned char* __r
     const int64_t j = j0 + threadIdx.x;
     if (__syncthreads_or(j < i && idx[j] == v)) return;
   }
-  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63;
+  const int64_t nm = (n_idx - i + 63) / 64;  // masks over [i, n_idx)
+  for (int64_t k0 = 0; k0 < nm; k0 += 4) {
+    const int64_t k = k0 + (threadIdx.x >> 6), j = i + 64 * k + lane;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(j < n_idx && idx[j] == v);
+    if (lane == 0 && k < nm) hits[k] = m;
+  }
+  __syncthreads();
   for (int64_t c0 = 0; c0 < row_elems; c0 += 256 * kScatterCols) {
     float acc[kScatterCols] = {};
-    for (int64_t j0 = i; j0 < n_idx; j0 += 256) {
-      const int64_t j = j0 + threadIdx.x;
-      const uint64_t m = __builtin_amdgcn_ballot_w64(j < n_idx && idx[j] == v);
-      if (lane == 0) hits[wv] = m;
-      __syncthreads();
-      uint64_t h[4];
+    for (int64_t k = 0; k < nm; ++k) {
+      for (uint64_t mm = hits[k]; mm; mm &= mm - 1) {  // matches in increasing position order
+        const unsigned char* row = values + (i + 64 * k + __builtin_ctzll(mm)) * ld_values_b;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) h[q] = hits[q];
-      __syncthreads();  // the next chunk rewrites hits
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        for (uint64_t mm = h[q]; mm; mm &= mm - 1) {  // matches in increasing position order
-          const unsigned char* row = values + (j0 + q * 64 + __builtin_ctzll(mm)) * ld_values_b;
-#pragma unroll
-          for (int c = 0; c < kScatterCols; ++c) {
-            const int64_t col = c0 + threadIdx.x + c * 256;
-            if (col < row_elems) acc[c] += ld_dt<DT>(row, static_cast<int>(col));
-          }
+        for (int c = 0; c < kScatterCols; ++c) {
+          const int64_t col = c0 + threadIdx.x + c * 256;
+          if (col < row_elems) acc[c] += ld_dt<DT>(row, static_cast<int>(col));
         }
       }
     }
@@ -146,7 +147,9 @@ extern "C" int pdh_scatter_add_rows(const void* values, const int64_t* idx, void
   PDH_REQUIRE(row_elems <= INT32_MAX, PDH_EINVAL, "pdh_scatter_add_rows: rows of more than 2^31 - 1 elements");
   PDH_REQUIRE(ld_values >= row_elems && ld_out >= row_elems, PDH_EINVAL,
               "pdh_scatter_add_rows: row strides must be >= row_elems");
-  PDH_REQUIRE(n_idx <= (int64_t{1} << 24), PDH_EINVAL, "pdh_scatter_add_rows: more than 2^24 indices");
+  PDH_REQUIRE(n_idx <= kScatterMaxIdx, PDH_EUNSUPPORTED,
+              "pdh_scatter_add_rows: %lld indices, more than the %lld one launch takes (the owner scan is quadratic)",
+              (long long)n_idx, (long long)kScatterMaxIdx);
   PDH_REQUIRE(out && (n_idx == 0 || (values && idx)), PDH_EINVAL, "pdh_scatter_add_rows: null pointer");
   const int64_t es = dtype == PDH_F32 ? 4 : 2;
   const int64_t row_b = row_elems * es, lo = ld_out * es;

@@ -1374,6 +1374,10 @@ class PlanExecutor:
             raise Untranslatable("tl.scatter_add's declared dim must lead its result")
         iv, ii = self._index(k, _base(vals_n)), self._index(k, _base(idx_n))
         shape, lo = y.type.shape, d.start
+        from .kernels import SCATTER_MAX_IDX
+
+        if math.prod(idx_n.type.shape) > SCATTER_MAX_IDX:
+            raise Untranslatable(f"tl.scatter_add over more than {SCATTER_MAX_IDX} positions")
 
         def run(vals):
             torch = _torch()

@@ -158,6 +158,9 @@ def take_rows(table: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None =
     return y.reshape(tuple(idx.shape) + tuple(table.shape[1:]))
 
 
+SCATTER_MAX_IDX = 1 << 16  # positions pdh_scatter_add_rows takes per launch
+
+
 def scatter_add_rows(values: torch.Tensor, idx: torch.Tensor, n_rows: int, out: torch.Tensor | None = None,
                      bad: torch.Tensor | None = None) -> torch.Tensor:
     """out[v, ...] = sum of values[i, ...] over the positions i with
@@ -165,7 +168,8 @@ def scatter_add_rows(values: torch.Tensor, idx: torch.Tensor, n_rows: int, out: 
     idx's shape followed by the row dims; rows nothing lands in are zero).
     Deterministic (increasing i, fp32 sums, one rounding). An index out of
     range is dropped and counts in ``bad`` (an int32 device scalar) when
-    given."""
+    given. At most ``SCATTER_MAX_IDX`` positions (the kernel's owner scan is
+    quadratic in them); more raise ``PdhError``."""
     _require_cuda(values, idx)
     if values.dtype not in _DT or idx.dtype != torch.int64:
         raise ValueError("scatter_add_rows: values f32/bf16/f16, idx int64")

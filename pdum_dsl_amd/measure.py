@@ -17,7 +17,12 @@ a ledger written on one MI355X is valid on another. Two measurements:
     count, timed with HIP events on the launch stream.
 
 ``tune_decode_splits`` is the autotune-lite pick over the decode's split
-ladder; its per-candidate facts are what makes the pick a fact. The HIP
+ladder; its per-candidate facts are what makes the pick a fact.
+
+``no_compiles`` is the warmth law of the reference's timed loops
+(``events.forbid(*WARMTH)``, benchmarks/bench_zoo.py:128-152): inside it no
+elementwise program may be compiled by hipRTC, so a first-use compile can
+never be timed as kernel work. The HIP
 attention, row and contraction kernels have fixed tile shapes on this part,
 so the launch ladder of the plan changes no launched work there and is not
 measured.
@@ -25,6 +30,8 @@ measured.
 
 from __future__ import annotations
 
+import contextlib
+import ctypes as C
 import time
 from dataclasses import replace
 
@@ -44,6 +51,34 @@ def machine_name() -> str:
         raise RuntimeError("measurements need a GPU: no HIP device is visible")
     arch = torch.cuda.get_device_properties(0).gcnArchName
     return arch.split(":")[0]
+
+
+def jit_stats() -> dict:
+    """The library's runtime-specialization counters: programs compiled by
+    hipRTC, launches through specialized kernels, compile failures."""
+    from . import _lib
+
+    st = (C.c_int64 * 3)()
+    _lib.lib().pdh_ew_jit_stats(st)
+    return {"compiled": int(st[0]), "launches": int(st[1]), "failures": int(st[2])}
+
+
+class WarmthError(RuntimeError):
+    """A hipRTC compile happened inside a region declared warm."""
+
+
+@contextlib.contextmanager
+def no_compiles(what: str = "timed region"):
+    """Raise ``WarmthError`` if any elementwise program is compiled (or a
+    compile fails) while the block runs: timed loops must run warm."""
+    before = jit_stats()
+    yield
+    after = jit_stats()
+    if after["compiled"] != before["compiled"] or after["failures"] != before["failures"]:
+        raise WarmthError(
+            f"{what}: {after['compiled'] - before['compiled']} hipRTC compile(s) and "
+            f"{after['failures'] - before['failures']} failure(s) inside a warm region — warm it up first"
+        )
 
 
 def _draw_inputs(kernel, seed: int) -> list:
@@ -128,4 +163,5 @@ def tune_decode_splits(B: int, Hq: int, Hkv: int, S: int, D: int, *, dtype: str 
     return best, facts
 
 
-__all__ = ["DECODE_SPLITS", "decode_split_ms", "hip_ms", "machine_name", "measured_green", "tune_decode_splits"]
+__all__ = ["DECODE_SPLITS", "WarmthError", "decode_split_ms", "hip_ms", "jit_stats", "machine_name", "measured_green",
+           "no_compiles", "tune_decode_splits"]

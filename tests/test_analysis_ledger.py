@@ -160,3 +160,14 @@ def test_loading_keeps_a_measurement_taken_in_this_session(tmp_path):
     path.write_text(rows[0] + "\n" + json.dumps(rec) + "\n")
     assert A.load_ledger(path) == 1
     assert lap(machine="gfx950").value == first.value == {"ms": 6}
+
+
+def test_the_jit_counters_read_without_a_device():
+    """measure.jit_stats reads the library's host-side counters (no GPU call):
+    the warmth guard of the timed loops compares them around the loop."""
+    from pdum_dsl_amd import measure as M
+
+    st = M.jit_stats()
+    assert set(st) == {"compiled", "launches", "failures"} and all(v >= 0 for v in st.values())
+    with M.no_compiles("nothing runs"):
+        pass

@@ -150,11 +150,13 @@ def _add_at_reference(values, idx, n_rows, dt):
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("n_idx,n_rows,row", [(0, 5, 8), (1, 1, 1), (37, 50, 30), (1000, 37, 1500), (700, 5000, 7),
-                                              (300, 2, 2049)])
+                                              (300, 2, 2049), (65536, 3, 1100)])
 def test_scatter_add_rows_sums_duplicates_in_position_order(dt, n_idx, n_rows, row):
     """pdh_scatter_add_rows against numpy's add.at in fp32 rounded once:
     bit-exact, rows nothing lands in zero, across index chunks (n_idx > 256),
-    column passes (rows over 1024 elements) and odd row widths."""
+    column passes (rows over 1024 elements), odd row widths, and the largest
+    batch one launch takes (2^16 positions on 3 rows: every owner's matches
+    span the whole mask cache, reused by a second column pass)."""
     from pdum_dsl_amd import kernels as K
 
     print(f"scatter_add_rows dt={dt} n_idx={n_idx} n_rows={n_rows} row={row}", flush=True)
@@ -170,6 +172,17 @@ def test_scatter_add_rows_sums_duplicates_in_position_order(dt, n_idx, n_rows, r
     assert torch.equal(got.cpu(), want)
     again = K.scatter_add_rows(values, idx, n_rows)
     assert torch.equal(again, got)  # deterministic: the same bits on every call
+
+
+def test_scatter_add_rows_refuses_more_positions_than_one_launch_takes():
+    from pdum_dsl_amd import kernels as K
+    from pdum_dsl_amd._lib import PdhError
+
+    n = K.SCATTER_MAX_IDX + 1
+    values = torch.zeros((n, 4), device="cuda")
+    idx = torch.zeros((n,), dtype=torch.int64, device="cuda")
+    with pytest.raises(PdhError, match="more than the 65536 one launch takes"):
+        K.scatter_add_rows(values, idx, 2)
 
 
 def test_scatter_add_rows_counts_and_drops_bad_indices_and_takes_strided_rows():

@@ -69,3 +69,41 @@ def test_decode_split_pick_is_measured_and_agrees_with_the_default():
     torch.cuda.synchronize()
     assert (o1.float() - o2.float()).abs().max().item() < 2e-2
     assert (l1 - l2).abs().max().item() < 1e-4
+
+
+def _scale_program(n, c):
+    """out = x * c over n elements: a program of its own (the constant makes
+    its specialized source, and so its compile, unique to the caller)."""
+    from pdum_dsl_amd import _lib as L
+
+    p = L.EwProgram()
+    p.n_insns, p.n_operands, p.ndim, p.out_reg = 3, 1, 1, 2
+    p.shape[0], p.start[0], p.out_stride[0] = n, 0, 1
+    p.in_stride[0][0] = 1
+    p.insns[0].op, p.insns[0].dst, p.insns[0].a = L.EW["LOAD"], 0, 0
+    p.insns[1].op, p.insns[1].dst, p.insns[1].imm = L.EW["CONST"], 1, c
+    p.insns[2].op, p.insns[2].dst, p.insns[2].a, p.insns[2].b = L.EW["MUL"], 2, 0, 1
+    return p
+
+
+def test_a_compile_inside_a_warm_region_raises_and_a_warm_run_passes():
+    """The warmth law of the timed loops (bench_zoo.py:128-152): the first
+    launch of a new program compiles it (hipRTC) and must stay out of timing."""
+    from pdum_dsl_amd import _lib as L
+    from pdum_dsl_amd import kernels as K
+    from pdum_dsl_amd import measure as M
+
+    if L.lib().pdh_ew_set_jit(1) == 0:  # restore the setting after the test
+        L.lib().pdh_ew_set_jit(0)
+        pytest.skip("runtime specialization is disabled in this process")
+    x = torch.arange(1024, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    prog = _scale_program(1024, 1.0625 + 2.0 ** -20)
+    with pytest.raises(M.WarmthError, match="1 hipRTC compile"):
+        with M.no_compiles("cold"):
+            K.map_chain(prog, [x], y)
+            torch.cuda.synchronize()
+    with M.no_compiles("warm"):  # the same program again: cached, no compile
+        K.map_chain(prog, [x], y)
+        torch.cuda.synchronize()
+    assert torch.equal(y, x * (1.0625 + 2.0 ** -20))
