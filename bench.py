@@ -37,6 +37,9 @@ def _args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--quick", action="store_true", help="skip the secondary configs and the CPU baseline")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--lines", default=None,
+                   help="comma-separated subset of the secondary lines to run (profiling one kernel): "
+                   + ", ".join(SECONDARY))
     p.add_argument("--gemm-ref", action="store_true", help="also time a plain bf16 GEMM (hipBLASLt) for reference")
     p.add_argument(
         "--copy-probe",
@@ -196,7 +199,7 @@ def main():
     }
 
     if not a.quick:
-        line["secondary"] = secondary(torch, K, cf, h, dev)
+        line["secondary"] = secondary(torch, K, cf, h, dev, None if a.lines is None else set(a.lines.split(",")))
     if a.gemm_ref:
         line["gemm_reference"] = gemm_reference(torch, dev)
     if not a.quick and not a.no_cpu:
@@ -204,10 +207,41 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def secondary(torch, K, cf, h, dev):
+SECONDARY = ("attention_c1", "row_softmax", "layernorm", "decode", "flash_bwd", "contraction_epilogue", "map_chain",
+             "stencil", "carved_plan", "carved_grad")
+
+
+def secondary(torch, K, cf, h, dev, sel=None):
+    """The secondary lines (all of SECONDARY, or the names in ``sel``), each
+    on inputs from its own seeded generator, each verified before it is
+    timed; a line that fails reports its error instead of a number."""
     out = {}
-    g = torch.Generator(device=dev).manual_seed(1)
-    # ---------------- C1: single-head non-causal attention, S=256 D=64 fp32 ----------------
+    on = lambda n: sel is None or n in sel  # noqa: E731
+    gen = lambda seed: torch.Generator(device=dev).manual_seed(seed)  # noqa: E731
+    lines = [
+        (("attention_c1",), lambda: _c1_line(torch, K, cf, h, dev, gen(1))),
+        (("row_softmax", "layernorm"), lambda: _c2_lines(torch, K, cf, h, dev, gen(2), on)),
+        (("decode",), lambda: _c4_line(torch, K, cf, h, dev, gen(4))),
+        (("flash_bwd",), lambda: _c5_line(torch, K, cf, h, dev, gen(5))),
+        (("contraction_epilogue",), lambda: _contraction_line(torch, K, dev, gen(6))),
+        (("map_chain",), lambda: _map_chain_line(torch, K, dev, gen(7))),
+        (("stencil",), lambda: _stencil_line(torch, K, dev, gen(8))),
+        (("carved_plan",), lambda: _carved_plan_line(torch)),
+        (("carved_grad",), lambda: _carved_grad_line(torch)),
+    ]
+    for names, fn in lines:
+        if not any(on(n) for n in names):
+            continue
+        try:
+            res = fn()
+            out.update(res if len(names) > 1 else {names[0]: res})
+        except Exception as exc:  # reported in the line, never hidden
+            out.update({n: {"error": str(exc)} for n in names if on(n)})
+    return out
+
+
+def _c1_line(torch, K, cf, h, dev, g):
+    """C1: single-head non-causal attention, S=256 D=64 fp32."""
     T1, D1 = 256, 64
     q1, k1, v1 = (torch.randn((1, 1, T1, D1), generator=g, device=dev, dtype=torch.float32) for _ in range(3))
     r1 = K.flash_fwd(q1, k1, v1, scale=D1**-0.5)
@@ -217,43 +251,50 @@ def secondary(torch, K, cf, h, dev):
     assert err <= 1e-5 * max(1.0, float(np.abs(wo).max())), f"C1 parity failed: {err}"
     ms = time_events(lambda: K.flash_fwd(q1, k1, v1, scale=D1**-0.5, out=r1.o), 200)
     fl = 4.0 * D1 * T1 * T1
-    out["attention_c1"] = {
+    return {
         "config": "C1 B=1 H=1 S=256 D=64 non-causal fp32", "ms": round(ms, 5), "TFLOP/s": round(fl / ms / 1e9, 3),
         "algorithmic_flop": fl, "max_abs_err": err,
         "note": "one head: 4 query blocks on a 256-CU chip, launch-latency bound by construction",
     }
-    del q1, k1, v1, r1
-    # ---------------- C2: row softmax + layernorm, [8192, 4096] fp32 ----------------
+
+
+def _c2_lines(torch, K, cf, h, dev, g, on):
+    """C2: row softmax and layernorm over [8192, 4096] fp32."""
+    out = {}
     R, C = 8192, 4096
     x = torch.randn((R, C), generator=g, device=dev, dtype=torch.float32)
     gamma = (1 + 0.1 * torch.randn((C,), generator=g, device=dev)).float()
     beta = (0.1 * torch.randn((C,), generator=g, device=dev)).float()
     y = torch.empty_like(x)
-    K.row_softmax(x, out=y)
-    torch.cuda.synchronize()
     rows = [0, R // 2, R - 1]
-    err = float(np.abs(h(y[rows]) - cf.np_softmax(h(x[rows]), axis=1)).max())
-    assert err < 1e-6, f"softmax parity failed: {err}"
-    ms = time_events(lambda: K.row_softmax(x, out=y), 50)
-    nbytes = 2 * R * C * 4
-    out["row_softmax"] = {
-        "config": "C2a [8192,4096] fp32", "ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
-        "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4), "bytes": nbytes, "max_abs_err": err,
-    }
-    K.layernorm(x, gamma, beta, 1e-5, out=y)
-    torch.cuda.synchronize()
-    want = cf.np_layernorm(h(x[rows]), h(gamma), h(beta), 1e-5)
-    err = float(np.abs(h(y[rows]) - want).max())
-    assert err < 1e-4, f"layernorm parity failed: {err}"
-    ms = time_events(lambda: K.layernorm(x, gamma, beta, 1e-5, out=y), 50)
-    nbytes = 2 * R * C * 4 + 2 * C * 4
-    out["layernorm"] = {
-        "config": "C2b [8192,4096] fp32 + gamma/beta", "ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
-        "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4), "bytes": nbytes, "max_abs_err": err,
-    }
-    del x, y
+    if on("row_softmax"):
+        K.row_softmax(x, out=y)
+        torch.cuda.synchronize()
+        err = float(np.abs(h(y[rows]) - cf.np_softmax(h(x[rows]), axis=1)).max())
+        assert err < 1e-6, f"softmax parity failed: {err}"
+        ms = time_events(lambda: K.row_softmax(x, out=y), 50)
+        nbytes = 2 * R * C * 4
+        out["row_softmax"] = {
+            "config": "C2a [8192,4096] fp32", "ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
+            "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4), "bytes": nbytes, "max_abs_err": err,
+        }
+    if on("layernorm"):
+        K.layernorm(x, gamma, beta, 1e-5, out=y)
+        torch.cuda.synchronize()
+        want = cf.np_layernorm(h(x[rows]), h(gamma), h(beta), 1e-5)
+        err = float(np.abs(h(y[rows]) - want).max())
+        assert err < 1e-4, f"layernorm parity failed: {err}"
+        ms = time_events(lambda: K.layernorm(x, gamma, beta, 1e-5, out=y), 50)
+        nbytes = 2 * R * C * 4 + 2 * C * 4
+        out["layernorm"] = {
+            "config": "C2b [8192,4096] fp32 + gamma/beta", "ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
+            "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4), "bytes": nbytes, "max_abs_err": err,
+        }
+    return out
 
-    # ---------------- C4: GQA decode, split-K ----------------
+
+def _c4_line(torch, K, cf, h, dev, g):
+    """C4: grouped-query decode, split-K."""
     Bd, Hq, Hkv, Sk, D = 64, 32, 8, 8192, 128
     qd = torch.randn((Bd, Hq, 1, D), generator=g, device=dev).to(torch.bfloat16)
     kc = torch.randn((Bd, Hkv, Sk, D), generator=g, device=dev).to(torch.bfloat16)
@@ -269,64 +310,34 @@ def secondary(torch, K, cf, h, dev):
     assert max(errs) < 2e-2, f"decode parity failed: {errs}"
     ms = time_events(lambda: K.attn_decode(qd, kc, vc, nsplit=nsplit, workspace=ws), 30)
     nbytes = 2 * Bd * Hkv * Sk * D * 2
-    out["decode"] = {
+    return {
         "config": "C4 B=64 Hq=32 Hkv=8 Sk=8192 D=128 bf16", "nsplit": nsplit, "ms": round(ms, 5),
         "GB/s": round(nbytes / ms / 1e6, 1), "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
         "kv_bytes": nbytes, "max_abs_err": max(errs),
     }
-    del kc, vc
 
-    # ---------------- C5: causal backward ----------------
+
+def _c5_line(torch, K, cf, h, dev, g):
+    """C5: causal backward, B=4 H=16 S=2048 D=64 bf16."""
     Bb, Hb, Sb, Db = 4, 16, 2048, 64
     qb, kb, vb, dob = (torch.randn((Bb, Hb, Sb, Db), generator=g, device=dev).to(torch.bfloat16) for _ in range(4))
     fw = K.flash_fwd(qb, kb, vb, band=K.CAUSAL)
-    try:
-        dq, dk, dv = K.flash_bwd(qb, kb, vb, fw.o, dob, fw.lse, band=K.CAUSAL)
-        torch.cuda.synchronize()
-        wq, wk, wv = cf.attention_bwd(h(qb[0, 0]), h(kb[0, 0]), h(vb[0, 0]), h(dob[0, 0]), scale=Db**-0.5,
-                                      band=(None, 0))
-        errs = {
-            nm: float(np.abs(h(t[0, 0]) - w).max() / max(1.0, np.abs(w).max()))
-            for nm, t, w in (("dq", dq, wq), ("dk", dk, wk), ("dv", dv, wv))
-        }
-        assert max(errs.values()) < 2e-2, f"backward parity failed: {errs}"
-        ms = time_events(lambda: K.flash_bwd(qb, kb, vb, fw.o, dob, fw.lse, band=K.CAUSAL), 20)
-        fl = 2.5 * causal_flops(Bb, Hb, Sb, Db)
-        out["flash_bwd"] = {
-            "config": "C5 causal bwd B=4 H=16 S=2048 D=64 bf16", "ms": round(ms, 5),
-            "TFLOP/s": round(fl / ms / 1e9, 2), "frac_mfma": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
-            "algorithmic_flop": fl, "rel_err": errs,
-        }
-    except Exception as exc:  # reported in the line, never hidden
-        out["flash_bwd"] = {"error": str(exc)}
-    del qb, kb, vb, dob, fw
-
-    # ---------------- f1: contraction-epilogue, gelu(x @ w + b) bf16 ----------------
-    try:
-        out["contraction_epilogue"] = _contraction_line(torch, K, dev, g)
-    except Exception as exc:
-        out["contraction_epilogue"] = {"error": str(exc)}
-    # ---------------- f4: map chain, where(j > i, tanh(x s) + exp(-|x|), 0) fp32 ----------------
-    try:
-        out["map_chain"] = _map_chain_line(torch, K, dev, g)
-    except Exception as exc:
-        out["map_chain"] = {"error": str(exc)}
-    # ---------------- f4: stencil, the 5-point update over an 8192 x 8192 fp32 grid ----------------
-    try:
-        out["stencil"] = _stencil_line(torch, K, dev, g)
-    except Exception as exc:
-        out["stencil"] = {"error": str(exc)}
-    # ---------------- f2: a gpt2-small forward, carved and run carve by carve ----------------
-    try:
-        out["carved_plan"] = _carved_plan_line(torch)
-    except Exception as exc:
-        out["carved_plan"] = {"error": str(exc)}
-    # ---------------- f2: the same model's weight gradients, carved and run ----------------
-    try:
-        out["carved_grad"] = _carved_grad_line(torch)
-    except Exception as exc:
-        out["carved_grad"] = {"error": str(exc)}
-    return out
+    dq, dk, dv = K.flash_bwd(qb, kb, vb, fw.o, dob, fw.lse, band=K.CAUSAL)
+    torch.cuda.synchronize()
+    wq, wk, wv = cf.attention_bwd(h(qb[0, 0]), h(kb[0, 0]), h(vb[0, 0]), h(dob[0, 0]), scale=Db**-0.5,
+                                  band=(None, 0))
+    errs = {
+        nm: float(np.abs(h(t[0, 0]) - w).max() / max(1.0, np.abs(w).max()))
+        for nm, t, w in (("dq", dq, wq), ("dk", dk, wk), ("dv", dv, wv))
+    }
+    assert max(errs.values()) < 2e-2, f"backward parity failed: {errs}"
+    ms = time_events(lambda: K.flash_bwd(qb, kb, vb, fw.o, dob, fw.lse, band=K.CAUSAL), 20)
+    fl = 2.5 * causal_flops(Bb, Hb, Sb, Db)
+    return {
+        "config": "C5 causal bwd B=4 H=16 S=2048 D=64 bf16", "ms": round(ms, 5),
+        "TFLOP/s": round(fl / ms / 1e9, 2), "frac_mfma": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+        "algorithmic_flop": fl, "rel_err": errs,
+    }
 
 
 def _stencil_line(torch, K, dev, g):

@@ -131,13 +131,19 @@ struct B16 {
 };
 
 // One XOR mask per row % 16 that keeps both read patterns of a tile
-// conflict-free for 32- and 64-bank LDS: row reads (lanes 16 G + c read row
-// c at chunk 4 ks + G) and transposed reads (16-lane group G reads rows
-// 4 G .. 4 G + 3, 32 bytes each); the conditions are re-checked by
-// tests/test_lds_layout.py.
+// bank-conflict free on gfx950's LDS, whose behaviour an in-bounds probe
+// measured: a ds_read_b128 serves 16 lanes per cycle over 256 bytes of
+// banks, and the 16 are not consecutive: within each 32-lane half, the
+// quads (lane / 4 = q, 0..7) of even bit parity {0, 3, 5, 6} share a cycle
+// and those of odd parity {1, 2, 4, 7} another, so their 16-byte slots must
+// differ mod 16; an 8-byte read (ds_read_b64, ds_read_b64_tr_b16) serves 32
+// consecutive lanes over 256 bytes (8-byte units mod 32). The patterns are
+// row reads (lanes 16 G + c read row c at chunk 4 ks + G) and transposed
+// reads (16-lane group G reads rows 4 G .. 4 G + 3, 32 bytes each);
+// tests/test_lds_layout.py re-checks both.
 template <int D>
 __device__ __forceinline__ int swz16_rt(int row) {
-  constexpr uint64_t kTable = D == 128 ? 0x75a8ec31fdb96420ull : 0x4602753157136420ull;
+  constexpr uint64_t kTable = D == 128 ? 0x6e4c2a08e6c4a280ull : 0x2266004466224400ull;
   return static_cast<int>((kTable >> (4 * (row & 15))) & 15u);
 }
 

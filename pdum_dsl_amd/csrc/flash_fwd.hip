@@ -212,18 +212,23 @@ struct F16Cfg {
 };
 
 // K rows are read as A operands: lanes 16 G + c read row c (of a 16-row
-// half) at chunk 4 ks + G. XOR masks that put the 16 rows of one chunk on 16
-// distinct 16-byte bank groups (64 banks), and any 8 consecutive rows on 8
-// (32 banks). At D = 64 two rows share 256 bytes.
+// half) at chunk 4 ks + G. On gfx950 a ds_read_b128 serves 16 lanes per
+// cycle over 256 bytes of banks (measured by an in-bounds probe): within
+// each 32-lane half, the quads of even bit parity of lane / 4 ({0, 3, 5, 6})
+// share a cycle and the odd ones ({1, 2, 4, 7}) another, so each cycle's 16
+// slots (address / 16 mod 16) must differ. At D = 128 (256-byte rows) the
+// row's own mask does it; at D = 64 rows 2 i and 2 i + 1 share 256 bytes
+// (row & 1 picks the half) and the mask 4 ((i ^ (i >> 2)) & 1) +
+// 2 ((i >> 1) & 1), i = row >> 1, gives each cycle's rows of one half distinct slots.
 template <int D>
 __device__ __forceinline__ int swz16_k(int row) {
-  return D == 128 ? (row & 15) : ((row & 7) ^ ((row >> 3) & 1));
+  return D == 128 ? (row & 15) : (4 * (((row >> 1) ^ (row >> 3)) & 1) | 2 * ((row >> 2) & 1));
 }
 
 // V rows are read with ds_read_b64_tr_b16: 16-lane group G reads rows
-// 4G .. 4G+3 (and 16 + those), 32 contiguous bytes each (two slots). Even
-// masks keep a slot pair adjacent; lanes 0-31 (rows 0-7) then cover all 64
-// banks, and each group's four rows distinct banks of 32.
+// 4G .. 4G+3 (and 16 + those), 32 contiguous bytes each (two slots). An
+// 8-byte read serves 32 lanes per cycle over 256 bytes of banks; even masks
+// keep a slot pair adjacent and put lanes 0-31 (rows 0-7) on distinct banks.
 template <int D>
 __device__ __forceinline__ int swz16_v(int row) {
   return D == 128 ? 2 * (row & 7) : 2 * ((row & 3) ^ ((row >> 2) & 1));

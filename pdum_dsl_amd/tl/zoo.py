@@ -342,12 +342,17 @@ class _B:
         return self.pw("div", e, self.rl(self.red("sum", e, k), sm))
 
 
-def gpt2(cfg: GPT2Config = GPT2Config(), seed: int = 7) -> Model:
+def gpt2(cfg: GPT2Config = GPT2Config(), seed: int = 7, init: str = "toy") -> Model:
     """GPT-2 from token ids to tied-head logits (zoo/gpt2.py:46-166): embedding
     gather + learned positions, ``layers`` pre-norm blocks (causal attention
     with heads as a dim, gelu MLP), final layernorm, head contracted against
     the embedding table. Inputs draw from ``default_rng(seed)``: ids first,
-    then every weight in declaration order, std 0.1 for wpe and 0.4 else."""
+    then every weight in declaration order. ``init="toy"`` (the reference
+    toy's draw): std 0.1 for wpe and 0.4 else. ``init="gpt2"`` (GPT-2's own
+    initialization scale): std 0.02 for the projections and wte, 0.01 for
+    wpe, layernorm gains 1 + 0.02 z and biases 0.02 z."""
+    if init not in ("toy", "gpt2"):
+        raise ValueError(f"init {init!r}: 'toy' or 'gpt2'")
     D, H, K, M = cfg.d, cfg.nh, cfg.hk, cfg.m
     rng = np.random.default_rng(seed)
     inputs = {"ids": rng.integers(0, cfg.v, cfg.t)}
@@ -355,8 +360,13 @@ def gpt2(cfg: GPT2Config = GPT2Config(), seed: int = 7) -> Model:
 
     def declare(name, **dims):
         shapes[name] = dims
-        std = 0.1 if name == "wpe" else 0.4
-        inputs[name] = std * rng.standard_normal(tuple(dims.values()))
+        z = rng.standard_normal(tuple(dims.values()))
+        if init == "toy":
+            inputs[name] = (0.1 if name == "wpe" else 0.4) * z
+        elif name.endswith("g") and "ln" in name:  # a layernorm gain
+            inputs[name] = 1.0 + 0.02 * z
+        else:
+            inputs[name] = (0.01 if name == "wpe" else 0.02) * z
 
     declare("wte", v=cfg.v, d=D)
     declare("wpe", t=cfg.t, d=D)

@@ -6,9 +6,13 @@ layernorms, the embedding gather), against the numpy denotation of the model
 16-bit row kernels and the gather the executor relies on.
 
 Tolerances: fp32 storage and arithmetic, 1e-4 of the logits' scale; bf16
-storage (fp32 accumulation and statistics), 3e-2 of the logits' scale, the
-north-star 2e-2 bound widened for bf16 rounding compounded over 2 layers
-and 23 carves (each boundary is rounded to bf16)."""
+storage (fp32 accumulation and statistics), the north-star 2e-2 of scale on
+GPT-2's own initialization scale (init="gpt2"). The reference toy's draw
+(std 0.4 weights and layernorm gains) makes the attention nearly one-hot,
+and the softmax amplifies the bf16 rounding of every carve boundary (~23 in
+the forward, ~75 in the gradients) beyond it: those stress cases keep their
+measured bounds (3e-2 forward, 7e-2 gradients), stated where they are
+asserted."""
 
 import math
 
@@ -20,12 +24,12 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-def _run(cfg, dtype, seed=7, fuse=True, merge=True):
+def _run(cfg, dtype, seed=7, fuse=True, merge=True, init="toy"):
     from pdum_dsl_amd.executor import PlanExecutor
     from pdum_dsl_amd.tl import zoo
     from pdum_dsl_amd.tl.partition import plan_model
 
-    m = zoo.gpt2(cfg, seed=seed)
+    m = zoo.gpt2(cfg, seed=seed, init=init)
     ex = PlanExecutor(plan_model(m.region), m.region, dtype, fuse_attention=fuse, merge_projections=merge)
     ex.bind(m.values())
     out = ex.run()
@@ -60,6 +64,18 @@ def test_a_sized_gpt2_matches_the_numpy_model(dtype, tol, fuse):
     assert ("softmax + PV carves" in src) == fuse
     err = np.abs(got - want).max()
     assert err <= tol * np.abs(want).max(), f"{dtype}: max err {err} vs scale {np.abs(want).max()}"
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+def test_a_sized_gpt2_at_gpt2_init_scale_holds_bf16_to_2e2(fuse):
+    """bf16 storage at GPT-2's initialization scale: the whole 2-layer
+    forward within the north star's 2e-2 of the logits' scale."""
+    from pdum_dsl_amd.tl import zoo
+
+    cfg = zoo.GPT2Config(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)
+    got, want, _ = _run(cfg, "bf16", seed=3, fuse=fuse, init="gpt2")
+    err = np.abs(got - want).max()
+    assert err <= 2e-2 * np.abs(want).max(), f"max err {err} vs scale {np.abs(want).max()}"
 
 
 @pytest.mark.parametrize("t,form", [(64, "scores carved"), (128, "scores dissolved"), (256, "projections dissolved"),
@@ -347,14 +363,15 @@ _TWO_LAYER = dict(t=256, d=256, nh=4, hk=64, m=1024, layers=2, v=512)
 _LONG = dict(t=512, d=128, nh=2, hk=64, m=512, layers=1, v=64)  # the softmax statistics as row partials
 
 
-@pytest.mark.parametrize("cfg,dtype,f32c,tol,tables", [
-    (_SMALL, "f32", "bf16x6", 1e-5, False), (_SMALL, "f32", "bf16x3", 2e-4, False),
-    (_SMALL, "f32", "bf16", 3e-2, False), (_SMALL, "f32", "fma", 1e-5, False),
-    (_SMALL, "bf16", "bf16x6", 7e-2, False), (_TWO_LAYER, "f32", "bf16x6", 3e-5, False),
-    (_TWO_LAYER, "f32", "bf16x3", 5e-4, False), (_SMALL, "f32", "bf16x6", 1e-5, True),
-    (_SMALL, "bf16", "bf16x6", 7e-2, True), (_TWO_LAYER, "f32", "bf16x6", 3e-5, True),
-    (_LONG, "f32", "bf16x6", 3e-5, False), (_LONG, "f32", "fma", 3e-5, False)])
-def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol, tables):
+@pytest.mark.parametrize("cfg,dtype,f32c,tol,tables,init", [
+    (_SMALL, "f32", "bf16x6", 1e-5, False, "toy"), (_SMALL, "f32", "bf16x3", 2e-4, False, "toy"),
+    (_SMALL, "f32", "bf16", 3e-2, False, "toy"), (_SMALL, "f32", "fma", 1e-5, False, "toy"),
+    (_SMALL, "bf16", "bf16x6", 7e-2, False, "toy"), (_TWO_LAYER, "f32", "bf16x6", 3e-5, False, "toy"),
+    (_TWO_LAYER, "f32", "bf16x3", 5e-4, False, "toy"), (_SMALL, "f32", "bf16x6", 1e-5, True, "toy"),
+    (_SMALL, "bf16", "bf16x6", 7e-2, True, "toy"), (_TWO_LAYER, "f32", "bf16x6", 3e-5, True, "toy"),
+    (_LONG, "f32", "bf16x6", 3e-5, False, "toy"), (_LONG, "f32", "fma", 3e-5, False, "toy"),
+    (_SMALL, "bf16", "bf16x6", 2e-2, True, "gpt2"), (_TWO_LAYER, "bf16", "bf16x6", 2e-2, False, "gpt2")])
+def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol, tables, init):
     """grad of gpt2's logits w.r.t. every weight (the embedding tables too
     when ``tables``: their gradient is a scatter-add of the embedding's
     cotangent, plus the tied head's product for wte), planned by plan_model
@@ -368,14 +385,15 @@ def test_the_gpt2_weight_gradients_run_carve_by_carve(cfg, dtype, f32c, tol, tab
     took its cotangent, whose zero-sum terms re-centred each rounded row); fp32 storage with f32_contract "bf16"
     (only the contraction operands rounded, fp32 accumulation and
     boundaries: an autocast's numerics) 2.3e-2; "bf16x3" 5.5e-5; "bf16x6" and
-    "fma" 2e-6 (1e-5 at two layers)."""
+    "fma" 2e-6 (1e-5 at two layers). At GPT-2's own initialization scale
+    (init="gpt2") bf16 storage holds the north star's 2e-2."""
     from oracle import region_eval as rev
     from pdum_dsl_amd.executor import PlanExecutor
     from pdum_dsl_amd.tl import zoo
     from pdum_dsl_amd.tl.autodiff import grad, region_names
     from pdum_dsl_amd.tl.partition import plan_model
 
-    m = zoo.gpt2(zoo.GPT2Config(**cfg), seed=3)
+    m = zoo.gpt2(zoo.GPT2Config(**cfg), seed=3, init=init)
     pn = tuple(m.names[id(p)] for p in m.region.params)
     wrt = tuple(n for n in pn if n not in (("ids",) if tables else ("ids", "wte", "wpe")))
     rg = grad(m.region, "logits", seed="dlogits", wrt=wrt, names=region_names(m.region, pn, ("logits",)))
