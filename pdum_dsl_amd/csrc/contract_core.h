@@ -312,14 +312,33 @@ __device__ __forceinline__ void contract_epilogue(const pdh_ew_program& p, const
     const int c0[PDH_EW_MAX_DIMS] = {b, row, col0, 0};
     float res[EPT];
     Eval::template run<EPT>(p, ops, DT, c0, acc, res, 1);
-    if constexpr (EPT == 4) {
+    if constexpr (EPT % 4 == 0) {
       const long long o0 = rbase + col0;
       if (p.out_stride[2] == 1 && (o0 & 3) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0) {
-        // four consecutive, aligned outputs: one 16-byte (fp32) or 8-byte (16-bit) store
+        // runs of four consecutive, aligned outputs: one 16-byte (fp32) or
+        // 8-byte (16-bit) store each; 16-bit runs of eight that start on a
+        // multiple of 8: one 16-byte store each
         if constexpr (DT == PDH_F32) {
-          *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + o0) = f32x4{res[0], res[1], res[2], res[3]};
+#pragma unroll
+          for (int q = 0; q < EPT / 4; ++q)
+            *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + o0 + 4 * q) =
+                f32x4{res[4 * q], res[4 * q + 1], res[4 * q + 2], res[4 * q + 3]};
         } else {
-          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + o0) = pack4_16<DT>(res);
+          uint16_t* o = static_cast<uint16_t*>(a.out) + o0;
+          u32x2 pk[EPT / 4];
+#pragma unroll
+          for (int q = 0; q < EPT / 4; ++q) {
+            const float r4[4] = {res[4 * q], res[4 * q + 1], res[4 * q + 2], res[4 * q + 3]};
+            pk[q] = pack4_16<DT>(r4);
+          }
+          if (EPT % 8 == 0 && (o0 & 7) == 0) {
+#pragma unroll
+            for (int q = 0; q < EPT / 8; ++q)
+              *reinterpret_cast<u32x4*>(o + 8 * q) = u32x4{pk[2 * q][0], pk[2 * q][1], pk[2 * q + 1][0], pk[2 * q + 1][1]};
+          } else {
+#pragma unroll
+            for (int q = 0; q < EPT / 4; ++q) *reinterpret_cast<u32x2*>(o + 4 * q) = pk[q];
+          }
         }
         return;
       }
@@ -421,18 +440,40 @@ __device__ __forceinline__ void contract_store(const ContractArgs& a, const pdh_
 #pragma unroll
       for (int v = 0; v < 16; ++v) blkf[(32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * ACCP + 32 * j + r32] = acc[i][j][v];
   __builtin_amdgcn_wave_barrier();  // the block is wave-private: in-order LDS, no workgroup barrier
-  for (int it = 0; it < WM * WM / 256; ++it) {
-    const int idx = it * 256 + lane * 4;
-    const int row = idx / WM, col = idx % WM;
-    const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * ACCP + col);
-    const float av[4] = {av4[0], av4[1], av4[2], av4[3]};
-    // row partials: lanes 8 q .. 8 q + 7 hold 32 consecutive columns of one row
-    const int r = RED < 0 ? -1 : red_kind<RED>(a);
-    if (r >= 0) {
-      const int grow = m0 + WM * wy + row, gcol = n0 + WM * wx + col;
-      store_row_partial(a, r, b, grow, gcol, epilogue_reduced4<DT, Eval>(p, ops, a, r, b, grow, gcol, av));
-    } else {
-      contract_epilogue<DT, 4, Eval>(p, ops, a, b, m0 + WM * wy + row, n0 + WM * wx + col, av);
+  if constexpr (RED < 0) {
+    // EPT consecutive outputs of one row per lane and evaluator call: the
+    // call issues every operand load of its EPT outputs before it waits, so
+    // a wave waits on operand latency WM * WM / (64 EPT) times, not WM * WM / 256
+    constexpr int EPT = Eval::kStoreRun < WM * WM / 64 ? Eval::kStoreRun : WM * WM / 64;
+    static_assert(WM % EPT == 0 && WM * WM % (64 * EPT) == 0, "runs stay in one row and cover the block");
+    for (int it = 0; it < WM * WM / (64 * EPT); ++it) {
+      const int idx = it * 64 * EPT + lane * EPT;
+      const int row = idx / WM, col = idx % WM;
+      float av[EPT];
+#pragma unroll
+      for (int q = 0; q < EPT / 4; ++q) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(blkf + row * ACCP + col + 4 * q);
+        av[4 * q] = v4[0];
+        av[4 * q + 1] = v4[1];
+        av[4 * q + 2] = v4[2];
+        av[4 * q + 3] = v4[3];
+      }
+      contract_epilogue<DT, EPT, Eval>(p, ops, a, b, m0 + WM * wy + row, n0 + WM * wx + col, av);
+    }
+  } else {
+    for (int it = 0; it < WM * WM / 256; ++it) {
+      const int idx = it * 256 + lane * 4;
+      const int row = idx / WM, col = idx % WM;
+      const f32x4 av4 = *reinterpret_cast<const f32x4*>(blkf + row * ACCP + col);
+      const float av[4] = {av4[0], av4[1], av4[2], av4[3]};
+      // row partials: lanes 8 q .. 8 q + 7 hold 32 consecutive columns of one row
+      const int r = red_kind<RED>(a);
+      if (r >= 0) {
+        const int grow = m0 + WM * wy + row, gcol = n0 + WM * wx + col;
+        store_row_partial(a, r, b, grow, gcol, epilogue_reduced4<DT, Eval>(p, ops, a, r, b, grow, gcol, av));
+      } else {
+        contract_epilogue<DT, 4, Eval>(p, ops, a, b, m0 + WM * wy + row, n0 + WM * wx + col, av);
+      }
     }
   }
 }

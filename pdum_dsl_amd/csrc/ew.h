@@ -145,6 +145,9 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
 
 struct InterpEval {
   static constexpr bool kVec = false;  // operands read element by element
+  // outputs per lane and call in the contraction's store: the interpreter's
+  // register file is 16 floats per element, so it runs four at a time
+  static constexpr int kStoreRun = 4;
   template <int EPT>
   static __device__ __forceinline__ void run(const pdh_ew_program& p, const EwOperands& ops, int dtype,
                                              const int (&c0)[PDH_EW_MAX_DIMS], const float (&acc)[EPT],
