@@ -35,6 +35,9 @@ def _args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=30)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--settle-ms", type=float, default=300.0,
+                   help="untimed back-to-back steps for this long (wall clock) before the warmup, so the timed "
+                        "steps run at the part's sustained clock, not its boost after idle (0: none)")
     p.add_argument("--quick", action="store_true", help="skip the secondary configs and the CPU baseline")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--lines", default=None,
@@ -143,6 +146,18 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    # settle: after idle the part first runs above its sustained clock, then
+    # its power management pulls the clock down under back-to-back load (a
+    # dip of up to ~30% per step before it levels off). Back-to-back steps
+    # for a fixed wall time (a sync every 8 keeps the wall clock honest and
+    # the queue full), then the W warmup steps, then exactly K timed steps:
+    # the timed steps measure the sustained rate.
+    n_settle, t_settle = 0, time.perf_counter()
+    while time.perf_counter() - t_settle < a.settle_ms / 1e3:
+        for _ in range(8):
+            step()
+        torch.cuda.synchronize()
+        n_settle += 8
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
@@ -169,6 +184,8 @@ def main():
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
+        "settle": {"steps": n_settle, "ms": a.settle_ms,
+                   "why": "untimed back-to-back steps before the warmup: the timed steps run at the sustained clock"},
         "ms_per_step": round(ms, 4),
         "wall_s_timed": round(wall, 4),
         "higher_is_better": True,
