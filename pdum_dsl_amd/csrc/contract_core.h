@@ -693,7 +693,9 @@ __device__ __forceinline__ uint32_t rne_bf16x2(float x, float y) {
 }
 
 // Four consecutive fp32 of one row -> PL planes of four bf16 each; true when
-// a leading term is not finite.
+// a leading term is not finite, or (with lower planes) nonzero below 2^-100:
+// there the lower planes would fall into the subnormal range and lose the
+// bits that make the split fp32 grade.
 template <int PL>
 __device__ __forceinline__ bool split4(u32x4 v, u32x2 (&out)[PL]) {
   float r[4];
@@ -708,6 +710,10 @@ __device__ __forceinline__ bool split4(u32x4 v, u32x2 (&out)[PL]) {
     r[2 * j] = ok0 ? x0 - f0 : 0.f;
     r[2 * j + 1] = ok1 ? x1 - f1 : 0.f;
     odd |= !(ok0 && ok1);
+    if constexpr (PL > 1) {
+      const float a0 = __builtin_fabsf(f0), a1 = __builtin_fabsf(f1);
+      odd |= (a0 > 0.f && a0 < 0x1p-100f) || (a1 > 0.f && a1 < 0x1p-100f);
+    }
   }
 #pragma unroll
   for (int p = 1; p < PL; ++p)
@@ -851,7 +857,9 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
     else
       fetch(kt, BoolC<false>{});
   };
-  bool odd = false;  // a non-finite leading term (an inf, a NaN, |x| above the largest bf16) in this lane's loads
+  // a non-finite leading term (an inf, a NaN, |x| above the largest bf16) in
+  // this lane's loads, or (with lower planes) a nonzero one below 2^-100
+  bool odd = false;
   if (nkt > 0) fetch_tile(0);
   for (int kt = 0; kt < nkt; ++kt) {
     __syncthreads();  // every wave is done reading the planes of tile kt - 1

@@ -387,17 +387,21 @@ def contraction_families(region: Region, seed: int = 5):
     wide-magnitude operands, drawn inside the operators' domains (the
     "finite operands" domain gemm.k-reassoc declares):
 
-    * params that reach a sqrt or log are drawn positive, (|z| + 1/2) scaled;
+    * every param is drawn signed first, so sign cancellations (the cases
+      that stress k-reassociation) are drawn wherever the domain allows;
     * the wide family starts at x64 and is narrowed by factors of 8 until the
       naive twin evaluates without overflow or an invalid operation (an exp
-      of a wide product saturates long before x64), never below x1.
+      of a wide product saturates long before x64), never below x1;
+    * only when the signed draw still leaves the domain at x1 (the naive
+      twin raises or returns a non-finite value) are the params that reach a
+      sqrt or log drawn positive, (|z| + 1/2) scaled, and narrowed the same way.
 
     A draw that still leaves the domain is refused by ``certify``."""
     from .interp import field, run_region
 
-    positive = domain_restricted_params(region)
+    restricted = domain_restricted_params(region)
 
-    def values(scale, s):
+    def values(scale, s, positive):
         rng = np.random.default_rng(s)
         vals = []
         for i, p in enumerate(region.params):
@@ -405,19 +409,28 @@ def contraction_families(region: Region, seed: int = 5):
             vals.append(field(((np.abs(z) + 0.5) if i in positive else z) * scale, p.type.names))
         return vals
 
+    def inside(vals):
+        try:
+            with np.errstate(over="raise", invalid="raise", divide="raise"):
+                out = run_region(region, vals)
+        except FloatingPointError:
+            return False
+        outs = out if isinstance(out, (tuple, list)) else (out,)
+        return all(np.isfinite(np.asarray(getattr(o, "arr", o), dtype=np.float64)).all() for o in outs)
+
     def draw(scale, s):
         def factory():
-            sc = scale
-            while True:
-                vals = values(sc, s)
-                if sc <= 1.0:
-                    return vals
-                try:
-                    with np.errstate(over="raise", invalid="raise", divide="raise"):
-                        run_region(region, vals)
-                    return vals
-                except FloatingPointError:
+            vals = None
+            for positive in (frozenset(), restricted) if restricted else (frozenset(),):
+                sc = scale
+                while True:
+                    vals = values(sc, s, positive)
+                    if inside(vals):
+                        return vals
+                    if sc <= 1.0:
+                        break
                     sc = max(1.0, sc / 8.0)
+            return vals
 
         return factory
 

@@ -83,3 +83,28 @@ def test_contraction_families_stay_inside_the_domain():
         with np.errstate(over="raise", invalid="raise", divide="raise"):
             out = run_region(region, vals)
         assert np.isfinite(out.arr).all()
+
+
+def _rmsnorm_region():
+    """y[t] = sum_e x[t, e] w[e] / sqrt(sum_e x[t, e]^2 + 1): x reaches the sqrt,
+    but through a square: its argument is positive whatever x's sign."""
+    b = Builder(OPS)
+    x = b.param(0, tensor_type(("t", "e"), (3, 5)))
+    w = b.param(1, tensor_type(("e",), (5,)))
+    prod = b.emit("tl.pointwise", x, b.emit("tl.repeat_like", w, x), f="mul")
+    s = b.emit("tl.reduce", prod, dims=("e",), f="sum")
+    sq = b.emit("tl.reduce", b.emit("tl.pointwise", x, x, f="mul"), dims=("e",), f="sum")
+    one = b.emit("core.const", type=F64, value=1.0)
+    den = b.emit("tl.pointwise", b.emit("tl.pointwise", sq, one, f="add"), f="sqrt")
+    y = b.emit("tl.pointwise", s, den, f="div")
+    return Region(params=(x, w), body=(b.emit("core.yield", y),))
+
+
+def test_params_reaching_a_sqrt_of_squares_keep_signed_draws():
+    """Signed first: a param is drawn positive only when a signed draw leaves
+    the domain, so an RMS-norm input keeps its sign cancellations."""
+    region = _rmsnorm_region()
+    assert fusion.domain_restricted_params(region) == frozenset({0})
+    for name, factory in fusion.contraction_families(region):
+        vals = factory()
+        assert (vals[0].arr < 0).any() and (vals[1].arr < 0).any(), name

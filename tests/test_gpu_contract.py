@@ -295,6 +295,28 @@ def test_fp32_contractions_against_float64(mode, tol, B, M, N, Kd):
     assert err <= tol * np.abs(want).max() * max(1.0, (Kd / 64) ** 0.5), f"mode {mode}: max err {err:.3e}"
 
 
+def test_tiny_fp32_operands_keep_fp32_grade():
+    """Leading terms below 2^-100 would leave the split's lower bf16 planes in
+    the subnormal range (a 1e-35 operand keeps ~8 of its 24 bits there); the
+    workgroups that load one recompute by fp32 fma, so every output stays
+    within fp32 accumulation error of the float64 product (1e-6 of the sum of
+    |a b|: a CPU simulation of the flushed planes errs by 2e-4 of it), tiny
+    rows and ordinary rows alike."""
+    g = torch.Generator(device="cuda").manual_seed(23)
+    B, M, N, Kd = 1, 300, 260, 256
+    a = torch.randn(B, M, Kd, device="cuda", generator=g)
+    a[0, :100] *= 1e-35  # tiny rows: one whole 64 x 64 tile and part of another
+    bt = torch.randn(B, N, Kd, device="cuda", generator=g) * 1e3
+    got = _fp32_gemm(a, bt, Kd, 6)
+    ad, bd = a.double().cpu().numpy(), bt.double().cpu().numpy()
+    want = np.einsum("bmk,bnk->bmn", ad, bd)
+    scale = np.einsum("bmk,bnk->bmn", np.abs(ad), np.abs(bd))
+    err = np.abs(got - want) / scale
+    assert err[:, :100].max() <= 1e-6, f"tiny rows: {err[:, :100].max():.3e} of sum |a b|"
+    assert err[:, 100:].max() <= 1e-6, f"ordinary rows: {err[:, 100:].max():.3e} of sum |a b|"
+    assert np.abs(want[:, :100]).max() < 1e-29 and np.abs(got[:, :100]).max() > 0  # the tiny products are normal fp32
+
+
 @pytest.mark.parametrize("mode", [6, 3])
 def test_non_finite_fp32_operands_behave_as_in_fp32(mode):
     """An inf times a value exact in bf16 would meet a zero lower plane (inf *
