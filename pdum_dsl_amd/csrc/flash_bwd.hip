@@ -507,11 +507,17 @@ __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned c
   // the staging cursor: (query head of the group, stage), head-major; Q tiles
   // [buf][sub] from 0, dO tiles after them, then the rows' statistics
   int s_gq = 0, s_st = 0;
+  // the staged head's Q and dO (buffer descriptors) and its first statistics
+  // row, advanced only when the cursor moves to the next head of the group:
+  // the per-stage work is 32-bit offsets from these
+  const uint32_t qbytes = static_cast<uint32_t>((a.t - 1) * a.q_st * 2 + D * 2);
+  const uint32_t obytes = static_cast<uint32_t>((a.t - 1) * a.o_st * 2 + D * 2);
+  const uint16_t* qh = a.q + b * a.q_sb + hq0 * a.q_sh;
+  const uint16_t* oh = a.dout + b * a.o_sb + hq0 * a.o_sh;
+  rsrc_t qr = make_rsrc(qh, qbytes), orr = make_rsrc(oh, obytes);
+  uint32_t srow_h = static_cast<uint32_t>((b * a.heads + hq0) * a.t * 4);
+  const uint32_t stat_plane = static_cast<uint32_t>(2 * a.rows * 4);
   auto stage = [&](int buf) {
-    const int64_t hq = hq0 + s_gq;
-    const rsrc_t qr = make_rsrc(a.q + b * a.q_sb + hq * a.q_sh, static_cast<uint32_t>((a.t - 1) * a.q_st * 2 + D * 2));
-    const rsrc_t orr =
-        make_rsrc(a.dout + b * a.o_sb + hq * a.o_sh, static_cast<uint32_t>((a.t - 1) * a.o_st * 2 + D * 2));
 #pragma unroll
     for (int j = 0; j < C::NSUB; ++j) {
       const int qt = sw.lo + s_st * C::NSUB + j;
@@ -521,14 +527,20 @@ __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned c
       dma_tile<D>(orr, smem + (2 * C::NSUB + slot) * C::TILEB, do_off, static_cast<uint32_t>(qt * 32), gro, w);
       if (w == 0) {
         unsigned char* sl = smem + STATB + slot * 3 * 32 * 4;
-        const uint32_t srow = static_cast<uint32_t>(((b * a.heads + hq) * a.t + qt * 32) * 4);
+        const uint32_t srow = srow_h + static_cast<uint32_t>(qt * 32 * 4);
         dma4(sr, sl, st_lane, srow);
-        if (lane < 32) dma4(sr, sl + 2 * 32 * 4, st_lane, srow + static_cast<uint32_t>(2 * a.rows * 4));
+        if (lane < 32) dma4(sr, sl + 2 * 32 * 4, st_lane, srow + stat_plane);
       }
     }
     if (++s_st == sp.n) {
       s_st = 0;
-      ++s_gq;
+      if (++s_gq < a.group) {
+        qh += a.q_sh;
+        oh += a.o_sh;
+        qr = make_rsrc(qh, qbytes);
+        orr = make_rsrc(oh, obytes);
+        srow_h += static_cast<uint32_t>(a.t * 4);
+      }
     }
   };
 
