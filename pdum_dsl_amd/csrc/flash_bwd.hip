@@ -174,6 +174,23 @@ struct Lane16 {
   }
 };
 
+// The tile rows cc (0..31, a compile-time index of each accumulator element)
+// a lane keeps in a masked tile, as the window lo <= cc <= lo + span: each
+// element's test is one unsigned compare whose result is used at once, so no
+// per-element lane masks stay live across the tile (they would not fit the
+// scalar registers). An empty window is lo = 32.
+struct CutWindow {
+  int lo;
+  uint32_t span;
+  __device__ __forceinline__ bool live(int cc) const { return static_cast<uint32_t>(cc - lo) <= span; }
+};
+__device__ __forceinline__ CutWindow cut_window(int lo, int hi) {
+  lo = lo > 0 ? lo : 0;
+  hi = hi < 31 ? hi : 31;
+  if (hi < lo) lo = hi = 32;
+  return CutWindow{lo, static_cast<uint32_t>(hi - lo)};
+}
+
 template <int D>
 __device__ __forceinline__ void dma_offsets(uint32_t (&off)[B16<D>::NDMA], int lane, int w, uint32_t gr) {
   using C = B16<D>;
@@ -378,14 +395,14 @@ __device__ __forceinline__ void bwd16_dq(const BwdArgs& a, int bid, unsigned cha
         const int dl = (key0 - qw0 - 16 * hh) - cmg;
         const bool rowok = qw0 + 16 * hh + c < T_;
         const int kl = S_ - key0 - 4 * G;  // key 16 kb + i of the tile exists below this
+        // band_lo <= dl + cc <= band_hi, cc < kl, and a live query row
+        int lo = a.masked ? a.band_lo32 - dl : 0, hi = kl - 1;
+        if (a.masked && a.band_hi32 - dl < hi) hi = a.band_hi32 - dl;
+        const CutWindow win = cut_window(rowok ? lo : 32, hi);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int cc = 16 * kb + i, d = dl + cc;
-            const bool live = rowok && cc < kl && (!a.masked || (d >= a.band_lo32 && d <= a.band_hi32));
-            e[4 * kb + i] = live ? e[4 * kb + i] : 0.f;
-          }
+          for (int i = 0; i < 4; ++i) e[4 * kb + i] = win.live(16 * kb + i) ? e[4 * kb + i] : 0.f;
       }
       ds[hh] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
     }
@@ -590,10 +607,15 @@ __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned c
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 p[2], ds[2];
-    f32x4 pmv[2];
+    f32x4 pmv[2];  // a masked score's probability per query row: its row's pm if the row exists, else 0
+    const int rl = T_ - q0 - 4 * G;  // query 16 qh + i of the tile exists below this
     if constexpr (CUT) {
 #pragma unroll
-      for (int qh = 0; qh < 2; ++qh) pmv[qh] = *reinterpret_cast<const f32x4*>(stl + 64 + 16 * qh + 4 * G);
+      for (int qh = 0; qh < 2; ++qh) {
+        pmv[qh] = *reinterpret_cast<const f32x4*>(stl + 64 + 16 * qh + 4 * G);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pmv[qh][i] = 16 * qh + i < rl ? pmv[qh][i] : 0.f;
+      }
     }
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
@@ -611,16 +633,17 @@ __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned c
         // is its row's pm (0 unless the row is fully masked) and carries no gradient
         // key - query = (kw0 + 16 hh - q0) + (c - 4 G) - (16 qh + i): a scalar plus one lane constant
         const int dl = (kw0 + 16 * hh - q0) + cmg;
-        const int rl = T_ - q0 - 4 * G;  // query 16 qh + i of the tile is live below this
+        // band_lo <= dl - cc <= band_hi and cc < rl
+        int lo = a.masked ? dl - a.band_hi32 : 0, hi = rl - 1;
+        if (a.masked && dl - a.band_lo32 < hi) hi = dl - a.band_lo32;
+        const CutWindow win = cut_window(lo, hi);
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int cc = 16 * qh + i, d = dl - cc;
-            const bool rowok = cc < rl;
-            const bool inb = !a.masked || (d >= a.band_lo32 && d <= a.band_hi32);
-            e[4 * qh + i] = rowok ? (inb ? e[4 * qh + i] : pmv[qh][i]) : 0.f;
-            g[4 * qh + i] = rowok && inb ? g[4 * qh + i] : 0.f;
+            const bool live = win.live(16 * qh + i);
+            e[4 * qh + i] = live ? e[4 * qh + i] : pmv[qh][i];
+            g[4 * qh + i] = live ? g[4 * qh + i] : 0.f;
           }
       }
       p[hh] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
