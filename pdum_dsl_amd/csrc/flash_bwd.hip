@@ -188,7 +188,11 @@ __device__ __forceinline__ CutWindow cut_window(int lo, int hi) {
   lo = lo > 0 ? lo : 0;
   hi = hi < 31 ? hi : 31;
   if (hi < lo) lo = hi = 32;
-  return CutWindow{lo, static_cast<uint32_t>(hi - lo)};
+  uint32_t span = static_cast<uint32_t>(hi - lo);
+  // opaque to the optimizer: the element tests are made here, per tile, not
+  // hoisted out of the sweep as lane masks that would not fit the scalar file
+  asm volatile("" : "+v"(lo), "+v"(span));
+  return CutWindow{lo, span};
 }
 
 template <int D>
