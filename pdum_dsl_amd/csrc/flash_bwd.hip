@@ -396,9 +396,13 @@ __device__ __forceinline__ void bwd16_dq(const BwdArgs& a, int bid, unsigned cha
       if constexpr (CUT) {
         // live: key < s, query < t, lo <= key - query <= hi (32-bit: |key - query| < 2^29 + 64)
         // key - query = (key0 - qw0 - 16 hh) - (c - 4 G) + (16 kb + i): a scalar plus one lane constant
-        int dl = (key0 - qw0 - 16 * hh) - cmg;
-        int kl = S_ - key0 - 4 * G;  // key 16 kb + i of the tile exists below this
-        asm volatile("" : "+v"(dl), "+v"(kl));  // per tile: no reassociated bounds kept live across the sweep
+        // the scalar parts fenced in scalar registers before the lane constants
+        // join them: no reassociated lane-dependent bounds kept live across the sweep
+        int sd = key0 - qw0 - 16 * hh, sk = S_ - key0;
+        asm volatile("" : "+s"(sd), "+s"(sk));
+        int dl = sd - cmg;
+        int kl = sk - 4 * G;  // key 16 kb + i of the tile exists below this
+        asm volatile("" : "+v"(dl), "+v"(kl));
         const bool rowok = qw0 + 16 * hh + c < T_;
         // band_lo <= dl + cc <= band_hi, cc < kl, and a live query row
         int lo = a.masked ? a.band_lo32 - dl : 0, hi = kl - 1;
@@ -613,8 +617,10 @@ __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned c
     __builtin_amdgcn_sched_barrier(0);
     u32x4 p[2], ds[2];
     f32x4 pmv[2];  // a masked score's probability per query row: its row's pm if the row exists, else 0
-    int rl = T_ - q0 - 4 * G;  // query 16 qh + i of the tile exists below this
-    if constexpr (CUT) asm volatile("" : "+v"(rl));  // per tile (as dl below)
+    int sr = T_ - q0;
+    if constexpr (CUT) asm volatile("" : "+s"(sr));  // per tile (as dl below)
+    int rl = sr - 4 * G;  // query 16 qh + i of the tile exists below this
+    if constexpr (CUT) asm volatile("" : "+v"(rl));
     if constexpr (CUT) {
 #pragma unroll
       for (int qh = 0; qh < 2; ++qh) {
@@ -638,7 +644,9 @@ __device__ __forceinline__ void bwd16_dkdv(const BwdArgs& a, int bid, unsigned c
         // live: query < t, lo <= key - query <= hi; a masked score's probability
         // is its row's pm (0 unless the row is fully masked) and carries no gradient
         // key - query = (kw0 + 16 hh - q0) + (c - 4 G) - (16 qh + i): a scalar plus one lane constant
-        int dl = (kw0 + 16 * hh - q0) + cmg;
+        int sd = kw0 + 16 * hh - q0;
+        asm volatile("" : "+s"(sd));
+        int dl = sd + cmg;
         asm volatile("" : "+v"(dl));
         // band_lo <= dl - cc <= band_hi and cc < rl
         int lo = a.masked ? dl - a.band_hi32 : 0, hi = rl - 1;
