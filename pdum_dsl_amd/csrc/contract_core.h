@@ -552,19 +552,21 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
     if (kt + NS - 1 < nkt) stage(kt + NS - 1, (kt + NS - 1) % NS);
     const unsigned char* at = smem + (2 * buf) * TILEB + WM * wy * kRowB;
     const unsigned char* bt = smem + (2 * buf + 1) * TILEB + WM * wx * kRowB;
+    u32x4 af[4][TI], bf[4][TI];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int t = 0; t < TI; ++t) {
+        af[ks][t] = *reinterpret_cast<const u32x4*>(at + rd[t][ks]);
+        bf[ks][t] = *reinterpret_cast<const u32x4*>(bt + rd[t][ks]);
+      }
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      u32x4 af[TI], bf[TI];
-#pragma unroll
-      for (int t = 0; t < TI; ++t) {
-        af[t] = *reinterpret_cast<const u32x4*>(at + rd[t][ks]);
-        bf[t] = *reinterpret_cast<const u32x4*>(bt + rd[t][ks]);
-      }
 #pragma unroll
       for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TI; ++j) acc[i][j] = mfma32_dt<DT>(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < TI; ++j) acc[i][j] = mfma32_dt<DT>(af[ks][i], bf[ks][j], acc[i][j]);
     }
     __builtin_amdgcn_s_setprio(0);
   }
