@@ -443,8 +443,12 @@ __device__ __forceinline__ void contract_store(const ContractArgs& a, const pdh_
   if constexpr (RED < 0) {
     // EPT consecutive outputs of one row per lane and evaluator call: the
     // call issues every operand load of its EPT outputs before it waits, so
-    // a wave waits on operand latency WM * WM / (64 EPT) times, not WM * WM / 256
-    constexpr int EPT = Eval::kStoreRun < WM * WM / 64 ? Eval::kStoreRun : WM * WM / 64;
+    // a wave waits on operand latency WM * WM / (64 EPT) times, not WM * WM / 256.
+    // fp32 outputs keep runs of four: a lane's 16 bytes, so eight lanes write a
+    // row's 128 bytes with one instruction (longer fp32 runs split every store
+    // instruction into 32-byte pieces of 32 rows, measured 30-40% slower).
+    constexpr int RUN = DT == PDH_F32 ? 4 : Eval::kStoreRun;
+    constexpr int EPT = RUN < WM * WM / 64 ? RUN : WM * WM / 64;
     static_assert(WM % EPT == 0 && WM * WM % (64 * EPT) == 0, "runs stay in one row and cover the block");
     for (int it = 0; it < WM * WM / (64 * EPT); ++it) {
       const int idx = it * 64 * EPT + lane * EPT;
