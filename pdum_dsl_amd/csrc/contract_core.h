@@ -698,27 +698,31 @@ __device__ __forceinline__ uint32_t rne_bf16x2(float x, float y) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_v{x, y}, bf16x2_v));
 }
 
-// Four consecutive fp32 of one row -> PL planes of four bf16 each; true when
-// a leading term is not finite, or (with lower planes) nonzero below 2^-100:
-// there the lower planes would fall into the subnormal range and lose the
-// bits that make the split fp32 grade.
+// Four consecutive fp32 of one row -> PL planes of four bf16 each. The
+// leading terms' magnitude bits (bf16, so an unsigned 16-bit compare orders
+// them as values) are folded into two packed running extrema per lane: big,
+// the largest (0x7f80 and above: an inf or NaN, x itself non-finite or above
+// the largest bf16), and low, the smallest of (bits - 1) (wrapping, so an
+// exact zero is 0xffff): below 0x0d7f is a nonzero term under 2^-100, whose
+// lower planes would fall into the subnormal range and lose the bits that make
+// the split fp32 grade. split_odd reads the verdict off the pair once per
+// block. The planes of such values are not used (the block recomputes in
+// fp32), so the remainders are formed without guards.
+typedef unsigned short u16x2_v __attribute__((ext_vector_type(2)));
 template <int PL>
-__device__ __forceinline__ bool split4(u32x4 v, u32x2 (&out)[PL]) {
+__device__ __forceinline__ void split4(u32x4 v, u32x2 (&out)[PL], u16x2_v& big, u16x2_v& low) {
   float r[4];
-  bool odd = false;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const float x0 = __uint_as_float(v[2 * j]), x1 = __uint_as_float(v[2 * j + 1]);
     const uint32_t h = rne_bf16x2(x0, x1);
     out[0][j] = h;
-    const float f0 = __uint_as_float(h << 16), f1 = __uint_as_float(h & 0xffff0000u);
-    const bool ok0 = __builtin_fabsf(f0) < __builtin_inff(), ok1 = __builtin_fabsf(f1) < __builtin_inff();
-    r[2 * j] = ok0 ? x0 - f0 : 0.f;
-    r[2 * j + 1] = ok1 ? x1 - f1 : 0.f;
-    odd |= !(ok0 && ok1);
+    const u16x2_v mag = __builtin_bit_cast(u16x2_v, h & 0x7fff7fffu);
+    big = __builtin_elementwise_max(big, mag);
     if constexpr (PL > 1) {
-      const float a0 = __builtin_fabsf(f0), a1 = __builtin_fabsf(f1);
-      odd |= (a0 > 0.f && a0 < 0x1p-100f) || (a1 > 0.f && a1 < 0x1p-100f);
+      low = __builtin_elementwise_min(low, mag - u16x2_v{1, 1});
+      r[2 * j] = x0 - __uint_as_float(h << 16);
+      r[2 * j + 1] = x1 - __uint_as_float(h & 0xffff0000u);
     }
   }
 #pragma unroll
@@ -732,7 +736,12 @@ __device__ __forceinline__ bool split4(u32x4 v, u32x2 (&out)[PL]) {
         r[2 * j + 1] -= __uint_as_float(h & 0xffff0000u);
       }
     }
-  return odd;
+}
+
+template <int PL>
+__device__ __forceinline__ bool split_odd(u16x2_v big, u16x2_v low) {
+  const bool nonfinite = big[0] >= 0x7f80 || big[1] >= 0x7f80;
+  return PL > 1 ? nonfinite || low[0] < 0x0d7f || low[1] < 0x0d7f : nonfinite;
 }
 
 // LAY bit 0: a is rows-contiguous (k strided), bit 1: bt is; otherwise k is
@@ -863,17 +872,18 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
     else
       fetch(kt, BoolC<false>{});
   };
-  // a non-finite leading term (an inf, a NaN, |x| above the largest bf16) in
-  // this lane's loads, or (with lower planes) a nonzero one below 2^-100
-  bool odd = false;
+  // the extrema of this lane's leading terms (split4): a non-finite one (an
+  // inf, a NaN, |x| above the largest bf16), or with lower planes a nonzero
+  // one below 2^-100, sends the block to the fp32 path
+  u16x2_v big = u16x2_v{0, 0}, low = u16x2_v{0xffff, 0xffff};
   if (nkt > 0) fetch_tile(0);
   for (int kt = 0; kt < nkt; ++kt) {
     __syncthreads();  // every wave is done reading the planes of tile kt - 1
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       u32x2 pa[PL], pb[PL];
-      odd |= split4<PL>(va[c], pa);
-      odd |= split4<PL>(vb[c], pb);
+      split4<PL>(va[c], pa, big, low);
+      split4<PL>(vb[c], pb, big, low);
 #pragma unroll
       for (int pl = 0; pl < PL; ++pl) {
         *reinterpret_cast<u32x2*>(smem + (2 * pl) * PLANEB + wra[c]) = pa[pl];
@@ -912,7 +922,7 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
   // loaded any non-finite (or bf16-overflowing) value recomputes its tile by
   // fp32 VALU fma instead, so such values behave as in fp32.
   int* flags = reinterpret_cast<int*>(smem);
-  const bool wave_odd = __builtin_amdgcn_ballot_w64(odd) != 0;  // every lane votes
+  const bool wave_odd = __builtin_amdgcn_ballot_w64(split_odd<PL>(big, low)) != 0;  // every lane votes
   if (lane == 0) flags[w] = wave_odd ? 1 : 0;
   __syncthreads();
   const bool slow = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
