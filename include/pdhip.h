@@ -347,6 +347,25 @@ int pdh_contract_views(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, 
                        int64_t sb_r, int64_t sb_k, int64_t batch, int64_t m, int64_t n, int64_t k, int64_t ksplit,
                        const pdh_ew_program* epi, const void* const* operands, void* out, int dtype, void* stream);
 
+/* pdh_contract_views with either operand (or both) computed in the k loop
+ * instead of read: pro_a, when not NULL, is an elementwise program over the
+ * lattice (batch, m, k) whose value at (b, r, kk) is a[b, r, kk], its LOADs
+ * indexing pro_a_operands (a and sa_* are then ignored); pro_b likewise over
+ * (batch, n, k) for bt. k counts from the batch entry's first column across k
+ * slices. The operand is evaluated once per element as the k tiles are
+ * loaded (the hipRTC-specialized straight-line evaluator by default, the
+ * interpreter otherwise) and never stored. Replaces the reference's operand
+ * re-derivation inside the contraction's k loop (conformance/triton_tile.py:
+ * 228-371, _dot_at / _reduce_at), where this library's other entry points take
+ * a computed operand only as a buffer a map chain has filled first. PDH_F32
+ * only; no row partials. */
+int pdh_contract_views_pro(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, const pdh_ew_program* pro_a,
+                           const void* const* pro_a_operands, const void* bt, int64_t sb_b, int64_t sb_r,
+                           int64_t sb_k, const pdh_ew_program* pro_b, const void* const* pro_b_operands,
+                           int64_t batch, int64_t m, int64_t n, int64_t k, int64_t ksplit,
+                           const pdh_ew_program* epi, const void* const* operands, void* out, int dtype,
+                           void* stream);
+
 /* pdh_contract_views (no k split) whose epilogue values are not stored but
  * reduced along each output row in runs of 32 columns: partials[b, r, j] =
  * R over columns 32 j .. 32 j + 31 (those under n) of epi(acc)[b, r, col],

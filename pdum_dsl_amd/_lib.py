@@ -43,6 +43,7 @@ EXPORTS = (
     "pdh_contract_strided",
     "pdh_contract_strided_ksplit",
     "pdh_contract_views",
+    "pdh_contract_views_pro",
     "pdh_contract_views_rowred",
     "pdh_reduce_rows",
     "pdh_reduce_rows_ex",
@@ -137,6 +138,9 @@ def _declare(lib) -> None:
         "pdh_contract_views": (
             i32, [vp, i64, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, i64, C.POINTER(EwProgram), C.POINTER(vp),
                   vp, i32, vp]),
+        "pdh_contract_views_pro": (
+            i32, [vp, i64, i64, i64, C.POINTER(EwProgram), C.POINTER(vp), vp, i64, i64, i64, C.POINTER(EwProgram),
+                  C.POINTER(vp), i64, i64, i64, i64, i64, C.POINTER(EwProgram), C.POINTER(vp), vp, i32, vp]),
         "pdh_contract_views_rowred": (
             i32, [vp, i64, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, C.POINTER(EwProgram), C.POINTER(vp), i32,
                   vp, i32, vp]),

@@ -47,13 +47,42 @@ __global__ __launch_bounds__(256, 2) void contract_split_small(ContractArgs a, p
   contract_split_body<PDH_F32, 32, NSPLIT, LAY, InterpEval>(a, p, ops, smem);
 }
 
-// The interpreter's split kernel for (mode, operand layouts), by value.
+// The prologue kernels: the same bodies with operands computed in the k
+// loop by the interpreter (ContractArgs::pro_a / pro_b say which).
+__global__ __launch_bounds__(256) void contract_f32_pro(ContractArgs a, pdh_ew_program p, EwOperands ops,
+                                                        ContractPro pa, ContractPro pb) {
+  contract_f32_body<InterpEval, kRedRuntime, InterpEval, InterpEval, true>(a, p, ops, &pa, &pb);
+}
+
+template <int NSPLIT, int LAY>
+__global__ __launch_bounds__(256, 2) void contract_split_pro(ContractArgs a, pdh_ew_program p, EwOperands ops,
+                                                             ContractPro pa, ContractPro pb) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[split_lds<64, NSPLIT>()];
+  contract_split_body<PDH_F32, 64, NSPLIT, LAY, InterpEval, kRedRuntime, InterpEval, InterpEval, true>(a, p, ops, smem,
+                                                                                                        &pa, &pb);
+}
+
+template <int NSPLIT, int LAY>
+__global__ __launch_bounds__(256, 2) void contract_split_pro_small(ContractArgs a, pdh_ew_program p, EwOperands ops,
+                                                                   ContractPro pa, ContractPro pb) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[split_lds<32, NSPLIT>()];
+  contract_split_body<PDH_F32, 32, NSPLIT, LAY, InterpEval, kRedRuntime, InterpEval, InterpEval, true>(a, p, ops, smem,
+                                                                                                        &pa, &pb);
+}
+
+// The interpreter's split kernel for (mode, operand layouts), by value; with
+// prologues (pro non-null) the prologue kernel.
 template <int NSPLIT>
 void launch_split(bool small, int lay, dim3 grid, hipStream_t st, const ContractArgs& ca, const pdh_ew_program& epi,
-                  const EwOperands& ops) {
+                  const EwOperands& ops, const ContractPro* pro = nullptr) {
   auto go = [&](auto lay_c) {
     constexpr int L = decltype(lay_c)::value;
-    if (small)
+    if (pro != nullptr) {
+      if (small)
+        contract_split_pro_small<NSPLIT, L><<<grid, 256, 0, st>>>(ca, epi, ops, pro[0], pro[1]);
+      else
+        contract_split_pro<NSPLIT, L><<<grid, 256, 0, st>>>(ca, epi, ops, pro[0], pro[1]);
+    } else if (small)
       contract_split_small<NSPLIT, L><<<grid, 256, 0, st>>>(ca, epi, ops);
     else
       contract_split<NSPLIT, L><<<grid, 256, 0, st>>>(ca, epi, ops);
@@ -203,7 +232,7 @@ std::atomic<int> g_f32_mode{6};  // fp32 contractions: 6 bf16 products per term 
 // tiles, or the 64 x 64 ones when the big tiles would not give every compute
 // unit a workgroup, an output side is 64 or under, or k is 128 or under.
 int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* const* operands, int64_t esize,
-                    hipStream_t st, const char* fn) {
+                    hipStream_t st, const char* fn, const ContractPro* pro = nullptr) {
   int rc = check_program(epi, 3, true, fn);
   if (rc) return rc;
   const int64_t batch = ca.batch, m = ca.m, n = ca.n;
@@ -224,12 +253,20 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
               PDH_EINVAL, "%s: one k slice of a / bt must span under 2 GiB", fn);
   hipFunction_t fns[2];
   // operand layouts of the fp32 split kernels: bit 0 a, bit 1 bt rows-contiguous
-  const int lay = (ca.sa_k != 1 ? 1 : 0) | (ca.sb_k != 1 ? 2 : 0);
+  // (a computed operand takes the k-contiguous layout)
+  const int lay = (ca.sa_k != 1 && !ca.pro_a ? 1 : 0) | (ca.sb_k != 1 && !ca.pro_b ? 2 : 0);
   PDH_REQUIRE(lay == 0 || ca.dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: 16-bit operands must have k contiguous", fn);
   PDH_REQUIRE(ca.rowred < 0 || ca.dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: row partials of fp32 contractions only", fn);
-  const bool spec = jit_get(JitKind::Contract, *epi, ca.dtype, fns, lay, ca.rowred);
+  PDH_REQUIRE(pro == nullptr || (ca.dtype == PDH_F32 && ca.rowred < 0), PDH_EUNSUPPORTED,
+              "%s: operand prologues: fp32 contractions without row partials only", fn);
+  const bool spec = pro != nullptr ? jit_get_pro(*epi, ca.pro_a ? &pro[0].p : nullptr, ca.pro_b ? &pro[1].p : nullptr,
+                                                 fns, lay)
+                                   : jit_get(JitKind::Contract, *epi, ca.dtype, fns, lay, ca.rowred);
   pdh_ew_program pe = *epi;
-  void* args[] = {&ca, &pe, &ops};
+  ContractPro pro_a = pro != nullptr ? pro[0] : ContractPro{}, pro_b = pro != nullptr ? pro[1] : ContractPro{};
+  void* args3[] = {&ca, &pe, &ops};
+  void* args5[] = {&ca, &pe, &ops, &pro_a, &pro_b};
+  void** args = pro != nullptr ? args5 : args3;
   auto launch_spec = [&](hipFunction_t f, int64_t nblk) {
     PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "%s: grid too large", fn);
     PDH_REQUIRE(hipModuleLaunchKernel(f, static_cast<unsigned>(nblk), 1, 1, 256, 1, 1, 0, st, args, nullptr) ==
@@ -245,7 +282,10 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
     const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
     if (spec) return launch_spec(fns[0], nblk);
     PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "%s: grid too large", fn);
-    contract_f32<<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
+    if (pro != nullptr)
+      contract_f32_pro<<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops, pro[0], pro[1]);
+    else
+      contract_f32<<<dim3(static_cast<unsigned>(nblk)), 256, 0, st>>>(ca, *epi, ops);
     return check_launch(fn);
   }
   if (g_cus == 0) g_cus = pdh_device_cus() > 0 ? pdh_device_cus() : 256;
@@ -263,11 +303,11 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
   const dim3 grid(static_cast<unsigned>(nblk));
   if (ca.dtype == PDH_F32) {  // on the bf16 matrix cores, split into planes
     if (f32_mode == 1)
-      launch_split<1>(small, lay, grid, st, ca, *epi, ops);
+      launch_split<1>(small, lay, grid, st, ca, *epi, ops, pro);
     else if (f32_mode == 3)
-      launch_split<3>(small, lay, grid, st, ca, *epi, ops);
+      launch_split<3>(small, lay, grid, st, ca, *epi, ops, pro);
     else
-      launch_split<6>(small, lay, grid, st, ca, *epi, ops);
+      launch_split<6>(small, lay, grid, st, ca, *epi, ops, pro);
   } else if (ca.dtype == PDH_BF16) {
     if (small)
       contract_mfma_small<PDH_BF16><<<grid, 256, 0, st>>>(ca, *epi, ops);
@@ -382,6 +422,77 @@ extern "C" int pdh_contract_views(const void* a, int64_t sa_b, int64_t sa_r, int
                         static_cast<int>(k), static_cast<int>(kc), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r,
                         static_cast<int>(ksplit), sa_k, sb_k, -1};
   return contract_launch(ca, epi, operands, 4, as_stream(stream), fn);
+}
+
+namespace {
+
+// An operand prologue checked against its lattice (batch, rows, k) and its
+// pointer table copied.
+int check_pro(const pdh_ew_program* pr, const void* const* operands, int64_t batch, int64_t rows, int64_t k,
+              ContractPro* out, const char* fn, const char* which) {
+  int rc = check_program(pr, 3, false, fn);
+  if (rc) return rc;
+  PDH_REQUIRE(pr->shape[0] == batch && pr->shape[1] == rows && pr->shape[2] == k, PDH_EINVAL,
+              "%s: the %s prologue's lattice must be {batch, %s, k}", fn, which, which[0] == 'a' ? "m" : "n");
+  PDH_REQUIRE(pr->n_operands == 0 || operands != nullptr, PDH_EINVAL, "%s: null %s prologue operand table", fn, which);
+  out->p = *pr;
+  out->ops = EwOperands{};
+  for (int i = 0; i < pr->n_operands; ++i) {
+    PDH_REQUIRE(operands[i] != nullptr, PDH_EINVAL, "%s: %s prologue operand %d is null", fn, which, i);
+    if ((rc = check_view(pr, pr->in_stride[i], fn, "prologue operand"))) return rc;
+    out->ops.p[i] = operands[i];
+  }
+  return PDH_OK;
+}
+
+}  // namespace
+
+extern "C" int pdh_contract_views_pro(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k,
+                                      const pdh_ew_program* pro_a, const void* const* pro_a_operands, const void* bt,
+                                      int64_t sb_b, int64_t sb_r, int64_t sb_k, const pdh_ew_program* pro_b,
+                                      const void* const* pro_b_operands, int64_t batch, int64_t m, int64_t n,
+                                      int64_t k, int64_t ksplit, const pdh_ew_program* epi,
+                                      const void* const* operands, void* out, int dtype, void* stream) {
+  const char* fn = "pdh_contract_views_pro";
+  PDH_REQUIRE(dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: fp32 operands only", fn);
+  PDH_REQUIRE(pro_a != nullptr || pro_b != nullptr, PDH_EINVAL, "%s: no prologue (pdh_contract_views reads both)", fn);
+  PDH_REQUIRE((pro_a || a) && (pro_b || bt) && out, PDH_EINVAL, "%s: null pointer", fn);
+  PDH_REQUIRE(batch >= 1 && m >= 1 && n >= 1 && k >= 1, PDH_EINVAL, "%s: need batch, m, n, k >= 1", fn);
+  PDH_REQUIRE(ksplit >= 1 && ksplit <= 64, PDH_EINVAL, "%s: ksplit = %lld must be in [1, 64]", fn,
+              (long long)ksplit);
+  const int64_t kc = ((k + kBK - 1) / kBK + ksplit - 1) / ksplit * kBK;
+  PDH_REQUIRE((ksplit - 1) * kc < k, PDH_EINVAL, "%s: ksplit = %lld leaves a k slice empty (k = %lld)", fn,
+              (long long)ksplit, (long long)k);
+  PDH_REQUIRE(batch * ksplit * m * n <= INT32_MAX && m <= INT32_MAX / 2 && n <= INT32_MAX / 2 && k <= INT32_MAX / 2,
+              PDH_EINVAL, "%s: output too large for one call", fn);
+  ContractPro pro[2];
+  int rc;
+  if (pro_a) {
+    if ((rc = check_pro(pro_a, pro_a_operands, batch, m, k, &pro[0], fn, "a"))) return rc;
+    a = nullptr;
+    sa_b = sa_r = 0;
+    sa_k = 1;
+  } else {
+    PDH_REQUIRE(sa_b >= 0 && sa_r >= 0 && sa_k >= 0 && (sa_k == 1 || sa_r == 1), PDH_EINVAL,
+                "%s: a needs k or its rows contiguous (a stride of 1), no negative stride", fn);
+    PDH_REQUIRE(reinterpret_cast<uintptr_t>(a) % 4 == 0, PDH_EINVAL, "%s: a must be 4-byte aligned", fn);
+  }
+  if (pro_b) {
+    if ((rc = check_pro(pro_b, pro_b_operands, batch, n, k, &pro[1], fn, "bt"))) return rc;
+    bt = nullptr;
+    sb_b = sb_r = 0;
+    sb_k = 1;
+  } else {
+    PDH_REQUIRE(sb_b >= 0 && sb_r >= 0 && sb_k >= 0 && (sb_k == 1 || sb_r == 1), PDH_EINVAL,
+                "%s: bt needs k or its rows contiguous (a stride of 1), no negative stride", fn);
+    PDH_REQUIRE(reinterpret_cast<uintptr_t>(bt) % 4 == 0, PDH_EINVAL, "%s: bt must be 4-byte aligned", fn);
+  }
+  ContractArgs ca{a, bt, out, static_cast<int>(batch * ksplit), static_cast<int>(m), static_cast<int>(n),
+                  static_cast<int>(k), static_cast<int>(kc), 0, 0, dtype, sa_b, sa_r, sb_b, sb_r,
+                  static_cast<int>(ksplit), sa_k, sb_k, -1};
+  ca.pro_a = pro_a != nullptr;
+  ca.pro_b = pro_b != nullptr;
+  return contract_launch(ca, epi, operands, 4, as_stream(stream), fn, pro);
 }
 
 extern "C" int pdh_contract_views_rowred(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, const void* bt,

@@ -50,7 +50,74 @@ struct ContractArgs {
   // receives their sum / max / min over each run of 32 output columns, fp32
   // [batch][m][ceil(n / 32)] (row partials; columns past n take no part)
   int rowred;
+  // nonzero: a (pro_a) / bt (pro_b) is not read but computed in the k loop by
+  // its prologue program (ContractPro; fp32 bodies of a prologue kernel only)
+  int pro_a, pro_b;
 };
+
+// An operand prologue: the program whose value at lattice point
+// (batch entry, row, k column) is the operand's element there (rows are the
+// m rows for a, the n rows for bt; k counts from the entry's first column,
+// across k slices), and the pointer table its LOADs index.
+struct ContractPro {
+  pdh_ew_program p;
+  EwOperands ops;
+};
+
+template <typename A, typename B>
+struct SameT {
+  static constexpr bool value = false;
+};
+template <typename A>
+struct SameT<A, A> {
+  static constexpr bool value = true;
+};
+
+// Four values of a computed operand at (batch entry, row rc, k columns
+// k0 .. k0 + 3 from the entry's first), those at or past kend zero; every
+// evaluated coordinate is clamped below kend, so every LOAD stays inside the
+// views the host checked. Whole runs take one evaluator call of four.
+template <typename PE>
+__device__ __forceinline__ void pro_run4(const ContractPro& pr, int be, int rc, int k0, int kend, float (&x)[4]) {
+  int c0[PDH_EW_MAX_DIMS] = {be, rc, k0, 0};
+  if (k0 + 3 < kend) {
+    const float zacc[4] = {0.f, 0.f, 0.f, 0.f};
+    PE::template run<4>(pr.p, pr.ops, PDH_F32, c0, zacc, x, 1);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c0[2] = k0 + j < kend ? k0 + j : kend - 1;
+      float y[1];
+      const float z1[1] = {0.f};
+      PE::template run<1>(pr.p, pr.ops, PDH_F32, c0, z1, y, 1);
+      x[j] = k0 + j < kend ? y[0] : 0.f;
+    }
+  }
+}
+
+// The interpreter's form, called rather than inlined: the interpreter is a
+// large switch, and the prologue kernels call it from many places.
+static __device__ __attribute__((noinline)) void pro_interp4(const ContractPro& pr, int be, int rc, int k0, int kend,
+                                                       float (&x)[4]) {
+  pro_run4<InterpEval>(pr, be, rc, k0, kend, x);
+}
+
+// Four operand values of one row, k columns kk .. kk + 3 of batch index bb's
+// slice, by prologue evaluator PE; columns at or past kin and rows at or past
+// rows are zero (the row is clamped into the lattice for the evaluation).
+template <typename PE>
+__device__ __forceinline__ f32x4 pro_eval4(const ContractPro& pr, const ContractArgs& a, int bb, int row, int rows,
+                                           int kk, int kin) {
+  const int rc = row < rows ? row : rows - 1;
+  const int kbase = (bb % a.ksplit) * a.kp;
+  float x[4];
+  if constexpr (SameT<PE, InterpEval>::value)
+    pro_interp4(pr, bb / a.ksplit, rc, kbase + kk, kbase + kin, x);
+  else
+    pro_run4<PE>(pr, bb / a.ksplit, rc, kbase + kk, kbase + kin, x);
+  const bool rin = row < rows;
+  return f32x4{rin ? x[0] : 0.f, rin ? x[1] : 0.f, rin ? x[2] : 0.f, rin ? x[3] : 0.f};
+}
 
 // Element offsets of batch index bb's a and bt rows (the batch entry's, moved
 // to its k slice).
@@ -583,9 +650,10 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
 // 4 x 4 outputs per lane, k tiles of 16 staged k-major through LDS (as, bs:
 // kFK x (kFT + 4) floats each), and the epilogue applied. Every lane of the
 // workgroup takes part (barriers inside).
-template <typename Eval, int RED = -1>
+template <typename Eval, int RED = -1, typename ProA = InterpEval, typename ProB = InterpEval, bool PRO = false>
 __device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_ew_program& p, const EwOperands& ops,
-                                               int b, int m0, int n0, float (*as)[kFT + 4], float (*bs)[kFT + 4]) {
+                                               int b, int m0, int n0, float (*as)[kFT + 4], float (*bs)[kFT + 4],
+                                               const ContractPro* pra = nullptr, const ContractPro* prb = nullptr) {
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const float* abase = static_cast<const float*>(a.a) + contract_off_a(a, b);
   const float* bbase = static_cast<const float*>(a.bt) + contract_off_b(a, b);
@@ -595,7 +663,24 @@ __device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_
   for (int k0 = 0; k0 < a.kp; k0 += kFK) {
     const int am = m0 + lr, bn = n0 + lr;
     f32x4 av = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f};
-    if (a.sa_k == 1 && a.sb_k == 1 && k0 + kFK <= kin) {  // k contiguous, whole tile
+    if (PRO && (a.pro_a || a.pro_b)) {  // computed operands (the other one read in place)
+      if (a.pro_a)
+        av = pro_eval4<ProA>(*pra, a, b, am, a.m, k0 + lc, kin);
+      else
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const long long kk = k0 + lc + j;
+          if (am < a.m && kk < kin) av[j] = abase[am * a.sa_r + kk * a.sa_k];
+        }
+      if (a.pro_b)
+        bv = pro_eval4<ProB>(*prb, a, b, bn, a.n, k0 + lc, kin);
+      else
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const long long kk = k0 + lc + j;
+          if (bn < a.n && kk < kin) bv[j] = bbase[bn * a.sb_r + kk * a.sb_k];
+        }
+    } else if (a.sa_k == 1 && a.sb_k == 1 && k0 + kFK <= kin) {  // k contiguous, whole tile
       if (am < a.m) av = *reinterpret_cast<const f32x4u*>(abase + am * a.sa_r + k0 + lc);
       if (bn < a.n) bv = *reinterpret_cast<const f32x4u*>(bbase + bn * a.sb_r + k0 + lc);
     } else {  // any strides, one element at a time
@@ -636,14 +721,16 @@ __device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_
   }
 }
 
-template <typename Eval, int RED = kRedRuntime>
+template <typename Eval, int RED = kRedRuntime, typename ProA = InterpEval, typename ProB = InterpEval, bool PRO = false>
 __device__ __forceinline__ void contract_f32_body(const ContractArgs& a, const pdh_ew_program& p,
-                                                  const EwOperands& ops) {
+                                                  const EwOperands& ops, const ContractPro* pra = nullptr,
+                                                  const ContractPro* prb = nullptr) {
   __shared__ float as[kFK][kFT + 4];  // k-major copies of the two 64-row tiles
   __shared__ float bs[kFK][kFT + 4];
   const int per = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x / per, rest = blockIdx.x % per;
-  f32_valu_block<Eval, RED>(a, p, ops, b, (rest / a.tiles_n) * kFT, (rest % a.tiles_n) * kFT, as, bs);
+  f32_valu_block<Eval, RED, ProA, ProB, PRO>(a, p, ops, b, (rest / a.tiles_n) * kFT, (rest % a.tiles_n) * kFT, as, bs,
+                                         pra, prb);
 }
 
 // ------------------------------------------- fp32 on the bf16 matrix cores
@@ -685,6 +772,10 @@ __device__ __forceinline__ int swz_split(int r) { return (r >> 2) & 3; }
 template <bool B>
 struct BoolC {  // a compile-time flag passed to generic lambdas
   static constexpr bool value = B;
+};
+template <typename T>
+struct TypeC {  // a type passed to generic lambdas
+  using type = T;
 };
 __device__ __forceinline__ int split_off(int r, int ch) {  // byte offset of (row r, 8-byte chunk ch) in a plane
   return (r ^ swz_split(r)) * kSRowB + (((ch >> 1) ^ swz_split(r)) << 4) + ((ch & 1) << 3);
@@ -746,9 +837,15 @@ __device__ __forceinline__ bool split_odd(u16x2_v big, u16x2_v low) {
 
 // LAY bit 0: a is rows-contiguous (k strided), bit 1: bt is; otherwise k is
 // contiguous. The host picks LAY from the strides (sa_k, sb_k != 1).
-template <int DT, int WM, int NSPLIT, int LAY, typename Eval, int RED = kRedRuntime>
+// PRO: a prologue kernel (ContractArgs::pro_a / pro_b name the operands its
+// evaluators ProA / ProB compute; such an operand takes the k-contiguous lane
+// layout, its LAY bit clear).
+template <int DT, int WM, int NSPLIT, int LAY, typename Eval, int RED = kRedRuntime, typename ProA = InterpEval,
+          typename ProB = InterpEval, bool PRO = false>
 __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const pdh_ew_program& p,
-                                                    const EwOperands& ops, unsigned char* smem) {
+                                                    const EwOperands& ops, unsigned char* smem,
+                                                    const ContractPro* pra = nullptr,
+                                                    const ContractPro* prb = nullptr) {
   constexpr int BM = 2 * WM, TI = WM / 32, PL = split_planes<NSPLIT>();
   constexpr int PLANEB = BM * kSRowB;  // one plane of one operand tile
   constexpr int CH = BM / 32;          // 16-byte fp32 chunks per lane and operand: rows (tid / 8) + 32 c
@@ -852,9 +949,23 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
     }
   };
   u32x4 va[CH], vb[CH];
+  // a computed operand: the lane's k-contiguous chunks (rows r0 + lq + 32 c,
+  // columns 4 lch .. 4 lch + 3 of the k tile) by its prologue
+  auto compute1 = [&](auto pe_c, const ContractPro& pr, int r0, int rows, int kt, u32x4(&v)[CH]) {
+    using PE = typename decltype(pe_c)::type;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+      v[c] = __builtin_bit_cast(u32x4, pro_eval4<PE>(pr, a, b, r0 + lq + 32 * c, rows, kt * kSBK + 4 * lch, kin));
+  };
   auto fetch = [&](int kt, auto edge_c) {
-    fetch1(BoolC<mna>{}, edge_c, ar, rowa, ka, m0, a.m, kt, va);
-    fetch1(BoolC<mnb>{}, edge_c, br, rowbb, kb, n0, a.n, kt, vb);
+    if (PRO && a.pro_a)
+      compute1(TypeC<ProA>{}, *pra, m0, a.m, kt, va);
+    else
+      fetch1(BoolC<mna>{}, edge_c, ar, rowa, ka, m0, a.m, kt, va);
+    if (PRO && a.pro_b)
+      compute1(TypeC<ProB>{}, *prb, n0, a.n, kt, vb);
+    else
+      fetch1(BoolC<mnb>{}, edge_c, br, rowbb, kb, n0, a.n, kt, vb);
   };
 
   f32x16 acc[TI][TI];
@@ -932,7 +1043,8 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
     float(*bs)[kFT + 4] = reinterpret_cast<float(*)[kFT + 4]>(smem + kFK * (kFT + 4) * 4);
 #pragma unroll 1
     for (int ij = 0; ij < (BM / kFT) * (BM / kFT); ++ij)  // one copy of the block's code
-      f32_valu_block<Eval, RED>(a, p, ops, b, m0 + kFT * (ij / (BM / kFT)), n0 + kFT * (ij % (BM / kFT)), as, bs);
+      f32_valu_block<Eval, RED, ProA, ProB, PRO>(a, p, ops, b, m0 + kFT * (ij / (BM / kFT)), n0 + kFT * (ij % (BM / kFT)),
+                                             as, bs, pra, prb);
     return;
   }
   contract_store<DT, WM, Eval, RED>(a, p, ops, smem, acc, b, m0, n0);

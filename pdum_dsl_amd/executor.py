@@ -406,6 +406,7 @@ class _Pack:
     pre: object = None
     pre_direct: bool = False
     strides: tuple = ()  # (batch, row) element strides of the operand as the product reads it
+    pro: object = None  # (program over (batch, rows, k), slots): computed in the k loop, never stored
 
 
 @dataclass
@@ -955,10 +956,26 @@ class PlanExecutor:
             out_st += kst
             low, prog = self._map_prog(k, core, lat, out_st, extra_leaves=(core,) if pre is not None else ())
             slots = tuple(None if (pre is not None and b is core) else self._index(k, b) for b in low.bases)
+            if fuse and pre is None and any(ins[0] != "LOAD" for ins in low.insns):
+                # a chain that computes: evaluated in the k loop (pdh_contract_views_pro)
+                # over (batch, rows, k); a pure relayout stays a (cacheable) pack
+                dense, acc = [], 1
+                for d in reversed(lat):
+                    dense.insert(0, acc)
+                    acc *= d.size
+                nr = len(rows_names)
+                try:
+                    p3 = ewprog.merge_dims(low.program(dense, [_over(op.type.names, op.type.shape, lat)
+                                                               for op in low.operands]),
+                                           [[0], list(range(1, 1 + nr)), list(range(1 + nr, len(lat)))])
+                    return _Pack(None, strides=(0, 0, 1), pro=(p3, slots))
+                except ewprog.Unlowerable:
+                    pass  # strides that do not flatten: materialized below
             return _Pack(None, prog, slots, (B, nrows, KP), KP != Kx, pre,
                          strides=(nrows * KP, KP, 1) if views else (nrows * KP, KP))
 
         views = self.dtype == "f32"  # pdh_contract_views: operands in place, any k
+        fuse = views and rowred is None  # computed operands in the k loop (pdh_contract_views_pro)
         pa, pb = pack(ca, mdims, M), pack(cb, ndims, N)
         y = k.body[-1].args[0] if yroot is None else yroot
         if y.type.names and set(y.type.names) != set(out_names):
@@ -1008,6 +1025,8 @@ class PlanExecutor:
 
             if p.direct is not None:
                 return vals[p.direct]
+            if p.pro is not None:
+                return None
             pv = p.pre(vals) if p.pre is not None else None
             if p.pre_direct:
                 return pv
@@ -1025,9 +1044,14 @@ class PlanExecutor:
             return buf
 
         def how(p):
+            if p.pro is not None:
+                return "prologue"
             t = "^t" if len(p.strides) == 3 and p.strides[2] != 1 else ""  # read rows-contiguous (transposed)
             return ("direct" + t) if p.direct is not None else (("plan" + t) if p.pre_direct else
                                                                 ("plan+pack" if p.pre else "pack"))
+
+        def pro_of(p, vals):
+            return None if p.pro is None else (p.pro[0], [vals[i] for i in p.pro[1]])
 
         src = f"contract batch={B} m={M} n={N} k={Kx} a={how(pa)} b={how(pb)} epilogue={len(epi.insns)}"
         if rowred is not None:
@@ -1043,17 +1067,24 @@ class PlanExecutor:
             dt = getattr(torch, tdt)
 
             a, bt = build(pa, vals, dt), build(pb, vals, dt)
+            pra, prb = pro_of(pa, vals), pro_of(pb, vals)
             out = torch.empty(shape, device="cuda", dtype=dt)
+
+            def views_call(e, ops, o, **kw):
+                if pra is None and prb is None:
+                    K.contract_views(a, pa.strides, bt, pb.strides, (B, M, N, Kx), e, ops, o, **kw)
+                else:
+                    K.contract_views_pro(a, pa.strides, bt, pb.strides, (B, M, N, Kx), e, ops, o, pro_a=pra,
+                                         pro_b=prb, **kw)
+
             if S > 1:  # k in S slices: partial sums, then their total through the epilogue
                 ws = torch.empty((B * S, M, N), device="cuda", dtype=torch.float32)
-                K.contract_views(a, pa.strides, bt, pb.strides, (B, M, N, Kx), ident, [], ws,
-                                 f32_mode=self.f32_contract, ksplit=S)
+                views_call(ident, [], ws, f32_mode=self.f32_contract, ksplit=S)
                 flat = ws.reshape(-1)
                 K.map_chain(fin, [flat[s_ * M * N:] for s_ in range(S)] + [vals[i] for i in eslots], out)
                 return out
             if views:
-                K.contract_views(a, pa.strides, bt, pb.strides, (B, M, N, Kx), prog, [vals[i] for i in eslots], out,
-                                 f32_mode=self.f32_contract)
+                views_call(prog, [vals[i] for i in eslots], out, f32_mode=self.f32_contract)
             elif KP == Kx:  # every operand as stored (or as packed), through its strides
                 K.contract_strided(a, pa.strides, bt, pb.strides, (B, M, N, Kx), prog,
                                    [vals[i] for i in eslots], out, f32_mode=self.f32_contract)

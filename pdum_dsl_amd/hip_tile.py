@@ -684,7 +684,9 @@ def _contraction_runner(region, cb, grid, dtype):
     b_order = (lnames[0], lnames[2], k)
 
     def operand(node, order):
-        """A param uploads as is; a prologue chain runs first through pdh_map_chain."""
+        """A param uploads as is. A prologue chain is computed in the k loop
+        (pdh_contract_views_pro) at fp32, and runs first through pdh_map_chain
+        at 16 bits."""
         if node.op == "core.param":
             return ("param", _index(region, node))
         adims = tuple(size.get(nm) or (node.type.dim(nm) if node.type.has(nm) else Dim(nm, 0, 1)) for nm in order)
@@ -697,9 +699,18 @@ def _contraction_runner(region, cb, grid, dtype):
     pa, pb = operand(cb["a"], a_order), operand(cb["b"], b_order)
     epi_idx = [_index(region, p) for p in epi.bases]
 
+    fused = dtype == "f32" and "chain" in (pa[0], pb[0])
+
     def dev(ts):
         torch = _torch()
         tdt = getattr(torch, _TORCH_DT[dtype])
+
+        def prologue(spec, rows):
+            """(program over (batch, rows, k), its operands) of a chain operand."""
+            low = spec[1]
+            ins = [ts[_index(region, b)] for b in low.bases]
+            st = [ewprog.strides_over(t.stride(), p.type.names, low.dims) for t, p in zip(ins, low.operands)]
+            return low.program((rows * Kdim, Kdim, 1), st), ins
 
         def build(spec, node, order, rows):
             if spec[0] == "param":
@@ -711,17 +722,29 @@ def _contraction_runner(region, cb, grid, dtype):
             K.map_chain(low.program(buf.stride(), st), ins, buf)
             return buf
 
-        a = build(pa, cb["a"], a_order, M_)
-        bt = build(pb, cb["b"], b_order, N_)
         ops = [ts[i] for i in epi_idx]
         st = [ewprog.strides_over(t.stride(), p.type.names, lattice) for t, p in zip(ops, epi.operands)]
         out = torch.empty((B_, M_, N_), device="cuda", dtype=tdt)
-        K.contract(a, bt, Kdim, epi.program(out.stride(), st), ops, out)
+        if fused:  # chain operands evaluated in the k loop, params read as packed
+            sides = []
+            for spec, node, order, rows in ((pa, cb["a"], a_order, M_), (pb, cb["b"], b_order, N_)):
+                if spec[0] == "chain":
+                    sides.append((None, None, prologue(spec, rows)))
+                else:
+                    t = build(spec, node, order, rows)
+                    sides.append((t, t.stride(), None))
+            (a, sta, pra), (bt, stb, prb) = sides
+            K.contract_views_pro(a, sta, bt, stb, (B_, M_, N_, Kdim), epi.program(out.stride(), st), ops, out,
+                                 pro_a=pra, pro_b=prb)
+        else:
+            a = build(pa, cb["a"], a_order, M_)
+            bt = build(pb, cb["b"], b_order, N_)
+            K.contract(a, bt, Kdim, epi.program(out.stride(), st), ops, out)
         present = [nm for nm in lnames if nm in y.type.names]  # the unit stand-ins drop out
         full = out.reshape(tuple(size[nm].size for nm in present))
         return full.permute([present.index(nm) for nm in y.type.names])
 
-    kern = "contract_f32" if dtype == "f32" else f"contract_mfma<{dtype}>"
+    kern = ("contract_views_pro" if fused else "contract_f32") if dtype == "f32" else f"contract_mfma<{dtype}>"
     src = (f"hip:{kern} batch={B_} m={M_} n={N_} k={Kdim} kp={KP} prologue={pa[0]},{pb[0]} "
            f"epilogue_insns={len(epi.insns)} operands={len(epi.operands)} stores=1")
     return _finish(dev, src, grid, "contraction-epilogue", region, dtype)

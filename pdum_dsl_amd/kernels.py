@@ -539,6 +539,62 @@ def contract_views(a: torch.Tensor, a_strides, bt: torch.Tensor, bt_strides, sha
     return out
 
 
+def contract_views_pro(a, a_strides, bt, bt_strides, shape, epi: _lib.EwProgram, operands: list,
+                       out: torch.Tensor, pro_a=None, pro_b=None, f32_mode: str | None = None,
+                       ksplit: int = 1) -> torch.Tensor:
+    """:func:`contract_views` with either operand computed in the k loop
+    (pdh_contract_views_pro): ``pro_a`` = (program, operands), the program over
+    the lattice (batch, m, k) whose value at (b, r, kk) is a[b, r, kk] (``a`` /
+    ``a_strides`` are then unused and may be None); ``pro_b`` likewise over
+    (batch, n, k) for bt. fp32."""
+    B, M, N, Kd = (int(x) for x in shape)
+    if pro_a is None and pro_b is None:
+        raise ValueError("contract_views_pro needs a prologue (contract_views reads both operands)")
+    _require_cuda(out, *operands, *[t for t in (a, bt) if t is not None],
+                  *[t for pr in (pro_a, pro_b) if pr is not None for t in pr[1]])
+    if out.dtype != torch.float32:
+        raise ValueError("contract_views_pro takes fp32")
+    tables, progs, reads = [], [], []
+    for t, st, pr, rows, nm in ((a, a_strides, pro_a, M, "a"), (bt, bt_strides, pro_b, N, "bt")):
+        if pr is None:
+            if t is None or t.dtype != torch.float32:
+                raise ValueError(f"{nm} must be an fp32 tensor when it has no prologue")
+            sb, sr, sk = (int(x) for x in st)
+            if min(sb, sr, sk) < 0 or (sk != 1 and sr != 1):
+                raise ValueError("each operand needs k or its rows contiguous, with non-negative strides")
+            reach = t.storage_offset() + (B - 1) * sb + (rows - 1) * sr + (Kd - 1) * sk + 1
+            if reach > t.untyped_storage().nbytes() // t.element_size():
+                raise ValueError("a strided operand's view reaches past its storage")
+            tables.append(None)
+            progs.append(None)
+            reads.append((_ptr(t), sb, sr, sk))
+            continue
+        prog, ops = pr
+        if prog.ndim != 3 or tuple(int(prog.shape[d]) for d in range(3)) != (B, rows, Kd):
+            raise ValueError(f"the {nm} prologue's lattice must be (batch, {'m' if nm == 'a' else 'n'}, k)")
+        if len(ops) != prog.n_operands:
+            raise ValueError(f"the {nm} prologue reads {prog.n_operands} operands, {len(ops)} given")
+        for i, o in enumerate(ops):
+            if o.dtype != torch.float32:
+                raise ValueError(f"{nm} prologue operand {i} is {o.dtype}: fp32 only")
+            if _max_offset(prog, prog.in_stride[i], 3) >= o.numel() or o.storage_offset() < 0:
+                raise ValueError(f"{nm} prologue operand {i}: the program's view reaches past the tensor")
+        tables.append((C.c_void_p * max(1, len(ops)))(*[o.data_ptr() for o in ops]))
+        progs.append(C.byref(prog))
+        reads.append((C.c_void_p(0), 0, 0, 1))
+    if tuple(epi.shape[d] for d in range(3)) != (B * ksplit, M, N) or epi.ndim != 3:
+        raise ValueError("the epilogue's lattice must be (batch * ksplit, m, n)")
+    _check_views(epi, operands, out, 3)
+    table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
+    null_prog = C.POINTER(_lib.EwProgram)()
+    (pa, sab, sar, sak), (pb, sbb, sbr, sbk) = reads
+    _with_f32_mode(f32_mode, torch.float32, lambda: _lib.call(
+        "pdh_contract_views_pro", pa, sab, sar, sak, progs[0] if progs[0] is not None else null_prog,
+        tables[0], pb, sbb, sbr, sbk, progs[1] if progs[1] is not None else null_prog, tables[1],
+        B, M, N, Kd, int(ksplit), C.byref(epi), table, _ptr(out), _DT[torch.float32], C.c_void_p(_stream())))
+    return out
+
+
 _REDUCERS = {"sum": 0, "max": 1, "min": 2}
 
 
