@@ -48,6 +48,7 @@ joins the AD with its linearization, or not at all.
 from __future__ import annotations
 
 from dataclasses import dataclass
+from functools import lru_cache
 
 from .dialect import OPS
 from .ir import F64, Builder, Node, Region, TensorType
@@ -115,11 +116,10 @@ def grad(
     unit inference, which this backend does not model: a dict of inputs is
     accepted and ignored, a target unit other than None refuses.
     ``fold_segments`` / ``fold_slots`` pick the reference's checkpointed fold
-    schedules (uniform K-way segments / binomial revolve); they trade
-    recomputation for memory and leave the gradient's values unchanged. Only
-    the one-segment schedule is built here: ``fold_segments`` of None or 1
-    and ``fold_slots`` of None are accepted, other values refuse by name
-    after the reference's own argument checks (autodiff.py:181-187).
+    schedules (autodiff.py:563-605): K uniform segments (K must divide the
+    fold's extent), or binomial revolve over ``fold_slots`` checkpoint slots.
+    Both trade recomputation for memory and leave the gradient's values
+    unchanged; None for both is the one-segment adjoint.
 
     ``shift_invariant_softmax`` (keyword only, on by default): the max of a
     max-subtracted softmax that feeds nothing else takes no cotangent. With
@@ -140,11 +140,7 @@ def grad(
         raise ValueError("fold_segments must be >= 1")
     if target_unit is not None:
         raise NotImplementedError("grad: target_unit — units are not modelled by this backend; pass None")
-    if (fold_segments is not None and int(fold_segments) != 1) or fold_slots is not None:
-        raise NotImplementedError(
-            "grad: checkpointed fold schedules (fold_segments > 1, fold_slots) are not built; the one-segment "
-            "fold adjoint gives the same values — pass fold_segments=None"
-        )
+    schedule = (None if fold_segments is None else int(fold_segments), None if fold_slots is None else int(fold_slots))
     by_name: dict = {}
     for p in region.params:
         by_name.setdefault(names[id(p)], p)
@@ -311,7 +307,7 @@ def grad(
             back = tuple(sorted((new, old) for old, new in n.attr("mapping")))
             contribute(n.args[0], b.emit("tl.rename", c, mapping=back))
         elif op == "tl.fold":
-            _fold_rule(b, n, c, contribute, const)
+            _fold_rule(b, n, c, contribute, const, *schedule)
         else:
             raise NotImplementedError(
                 f"{op} has no adjoint rule in this build (a primitive joins the AD with its linearization)"
@@ -340,13 +336,37 @@ def grad(
     return RegionGrad(joint, grads, jnames, tuple(outputs), nodes)
 
 
-def _fold_rule(b, n, c, contribute, const):
-    """The adjoint of a fold read at its final state o (autodiff.py:411-605,
-    one segment, no checkpointing): a reverse fold over the flipped sequences
-    whose carry is the cotangent of the states after each step.
+@lru_cache(maxsize=None)
+def revolve_cost(slots: int, steps: int) -> float:
+    """The fewest forward steps re-advanced to reverse ``steps`` fold steps
+    with ``slots`` checkpoint slots (Griewank & Walther's binomial revolve):
+    a range that fits the slots (or is one step) is reversed as stored; a
+    longer one advances a head of m steps, checkpoints, reverses the tail with
+    one slot fewer, then the head with the same slots."""
+    if steps <= 1 or slots >= steps:
+        return 0.0
+    if slots < 1:
+        return float("inf")
+    return min(m + revolve_cost(slots - 1, steps - m) + revolve_cost(slots, m) for m in range(1, steps))
+
+
+@lru_cache(maxsize=None)
+def revolve_split(slots: int, steps: int) -> int:
+    """The head length of an optimal revolve split (1 <= slots < steps, steps
+    >= 2), the longest among the optimal ones: the schedule the reference's
+    split rule picks (autodiff.py:88-99), so the joints agree in shape."""
+    best = revolve_cost(slots, steps)
+    return max(m for m in range(1, steps)
+               if m + revolve_cost(slots - 1, steps - m) + revolve_cost(slots, m) == best)
+
+
+def _fold_rule(b, n, c, contribute, const, fold_segments=None, fold_slots=None):
+    """The adjoint of a fold read at its final state o (autodiff.py:411-605):
+    reverse folds over the flipped sequences whose carry is the cotangent of
+    the states after each step.
 
     - The states before step t: each state's trajectory (an emitting fold of
-      the same step) shifted one step later, the initial state at t = start.
+      the same step) shifted one step later, the initial state at the first.
     - The reverse step is the VJP of the forward step: ``grad`` of the scalar
       sum_i <ct_i, step(s, e)_i> with respect to the step's own params, the
       ct_i bound as extra params. Its state gradients are the next carry, its
@@ -354,9 +374,16 @@ def _fold_rule(b, n, c, contribute, const):
     - The reverse carry starts at (c for state o, zero for the others): the
       cotangent of the final states. The reference injects c at the last step
       through a padded sequence instead; the sum is the same.
+    - The schedule: one segment (the whole range reversed from the stored
+      trajectory); ``fold_segments`` = K uniform segments, each reversed from
+      its start state, which a forward fold over the segments before it
+      re-advances; or ``fold_slots`` = S, binomial revolve: a range longer
+      than its slots is split (revolve_split), its tail reversed from a
+      checkpoint with one slot fewer, then its head.
     The carry's final value is the initial states' cotangent; the emissions,
-    flipped back, the element sources'. Nested folds in the step differentiate
-    through the same rule (grad recurses)."""
+    flipped back and padded to the whole range, the element sources'. Nested
+    folds in the step differentiate through the same rule (grad recurses,
+    one segment)."""
     state = tuple(n.attr("state"))
     k = len(state)
     dim = n.attr("dim")
@@ -385,20 +412,6 @@ def _fold_rule(b, n, c, contribute, const):
         yy = vals[0] if len(vals) == 1 else wb.emit("core.tuple", *vals)
         return Region(params=step.params, body=(wb.emit("core.yield", yy),))
 
-    # the states before each step
-    prev = []
-    for i in range(k):
-        traj = b.emit("tl.fold", *inits, *elems, regions=(with_yield(ynodes[:k] + (ynodes[i],)),), out=("emit",),
-                      **fat)
-        if stop - start > 1:
-            later = b.emit("tl.slice", b.emit("tl.shift", traj, deltas=((dim, 1),)), ranges=((dim, (start + 1, stop)),))
-            later = b.emit("tl.pad", later, extents=((dim, (start, stop)),), fill=0.0)
-        else:
-            later = zeros(traj.type)
-        first = b.emit("tl.pointwise", b.emit("tl.iota", later, name=dim), const(start), f="eq")
-        init_t = b.emit("tl.repeat", inits[i], name=dim, extent=(start, stop))
-        prev.append(b.emit("tl.pointwise", first, init_t, later, f="where"))
-
     # the step's VJP: grad of sum_i <ct_i, y_i> over the step's params
     wb = Builder(OPS)
     cts = tuple(wb.param(("fold.ct", i), ynodes[i].type) for i in range(k))
@@ -412,6 +425,7 @@ def _fold_rule(b, n, c, contribute, const):
     pnames = tuple(f"s{i}" for i in range(k)) + tuple(f"e{j}" for j in range(len(ep))) + tuple(
         f"ct{i}" for i in range(k))
     vjp = grad(wrapper, "fold.vjp", wrt=pnames[:k + len(ep)], names=region_names(wrapper, pnames, ("fold.vjp",)))
+    flows = tuple(vjp.grads.get(f"s{i}") is not None for i in range(k))
 
     def g_of(nm, tt):
         gname = vjp.grads.get(nm)
@@ -430,18 +444,72 @@ def _fold_rule(b, n, c, contribute, const):
         return Region(params=rparams, body=(rb.emit("core.yield", yy),))
 
     flip = lambda v: b.emit("tl.flip", v, name=dim)  # noqa: E731
-    rinit = tuple(c if i == o else zeros(inits[i].type) for i in range(k))
-    rsrc = tuple(flip(v) for v in prev) + tuple(flip(v) for v in elems)
+
+    def seg(lo, hi):  # the element sequences over steps [lo, hi)
+        if (lo, hi) == (start, stop):
+            return tuple(elems)
+        return tuple(b.emit("tl.slice", e, ranges=((dim, (lo, hi)),)) for e in elems)
+
+    def advance(s0, lo, hi):  # the states after steps [lo, hi), from s0
+        se = seg(lo, hi)
+        return tuple(b.emit("tl.fold", *s0, *se, regions=(step,), out=("final", i), **fat) for i in range(k))
+
+    def leaf(lo, hi, s0, cur):
+        """Steps [lo, hi) reversed from their start state s0 and the carry cur
+        after hi: the element cotangents contributed, the carry at lo returned."""
+        se = seg(lo, hi)
+        prev = []
+        for i in range(k):
+            traj = b.emit("tl.fold", *s0, *se, regions=(with_yield(ynodes[:k] + (ynodes[i],)),), out=("emit",),
+                          **fat)
+            if hi - lo > 1:
+                later = b.emit("tl.slice", b.emit("tl.shift", traj, deltas=((dim, 1),)), ranges=((dim, (lo + 1, hi)),))
+                later = b.emit("tl.pad", later, extents=((dim, (lo, hi)),), fill=0.0)
+            else:
+                later = zeros(traj.type)
+            first = b.emit("tl.pointwise", b.emit("tl.iota", later, name=dim), const(lo), f="eq")
+            init_t = b.emit("tl.repeat", s0[i], name=dim, extent=(lo, hi))
+            prev.append(b.emit("tl.pointwise", first, init_t, later, f="where"))
+        rsrc = tuple(flip(v) for v in prev) + tuple(flip(v) for v in se)
+        for j, ev_ in enumerate(elems):
+            if vjp.grads.get(f"e{j}") is None:
+                continue
+            em = flip(b.emit("tl.fold", *cur, *rsrc, regions=(rstep((vjp.nodes[vjp.grads[f"e{j}"]],)),),
+                             out=("emit",), **rat))
+            if (lo, hi) != (start, stop):
+                em = b.emit("tl.pad", em, extents=((dim, (start, stop)),), fill=0.0)
+            contribute(ev_, em)
+        return tuple(b.emit("tl.fold", *cur, *rsrc, regions=(rstep(),), out=("final", i), **rat) if flows[i]
+                     else zeros(inits[i].type) for i in range(k))
+
+    cur = tuple(c if i == o else zeros(inits[i].type) for i in range(k))
+    T = stop - start
+    if fold_slots is not None:
+        def revolve(lo, hi, slots, boundary):
+            nonlocal cur
+            if hi - lo <= 1 or slots >= hi - lo:
+                cur = leaf(lo, hi, boundary, cur)
+                return
+            mid = lo + revolve_split(slots, hi - lo)
+            revolve(mid, hi, slots - 1, advance(boundary, lo, mid))
+            revolve(lo, mid, slots, boundary)
+
+        revolve(start, stop, int(fold_slots), tuple(inits))
+    else:
+        K = 1 if fold_segments is None else min(int(fold_segments), T)
+        if K < 1:
+            raise ValueError("fold_segments must be >= 1")
+        if T % K:
+            raise ValueError(f"fold_segments={K} must divide the fold extent {T} (pad the dim or pick a divisor)")
+        L_ = T // K
+        starts = [tuple(inits)]
+        for j in range(K - 1):
+            starts.append(advance(starts[-1], start + j * L_, start + (j + 1) * L_))
+        for j in reversed(range(K)):
+            cur = leaf(start + j * L_, start + (j + 1) * L_, starts[j], cur)
     for i in range(k):
-        if vjp.grads.get(f"s{i}") is None:
-            continue
-        contribute(inits[i], b.emit("tl.fold", *rinit, *rsrc, regions=(rstep(),), out=("final", i), **rat))
-    for j, ev_ in enumerate(elems):
-        if vjp.grads.get(f"e{j}") is None:
-            continue
-        em = b.emit("tl.fold", *rinit, *rsrc, regions=(rstep((vjp.nodes[vjp.grads[f"e{j}"]],)),), out=("emit",),
-                    **rat)
-        contribute(ev_, flip(em))
+        if flows[i]:
+            contribute(inits[i], cur[i])
 
 
 def _pointwise_rule(n, c, contribute, pw, const):

@@ -190,3 +190,128 @@ def test_the_flash_tiles_gradient_is_causal_attentions():
         args_dn = [dn if a is arr else a for a in (q, k, v)]
         fd = (fwd(*args_up) - fwd(*args_dn)) / (2 * h)
         assert gi[nm].to_numpy(names)[idx] == pytest.approx(fd, rel=1e-6, abs=1e-9), nm
+
+
+# ------------------------------------------------ checkpointed schedules
+
+
+def test_revolve_costs_closed_forms():
+    """One slot re-advances L - 1, L - 2, ... steps: L (L - 1) / 2 in all; a
+    range that fits its slots is reversed as stored."""
+    from pdum_dsl_amd.tl.autodiff import revolve_cost, revolve_split
+
+    for L in range(1, 12):
+        assert revolve_cost(1, L) == L * (L - 1) // 2
+        for s in range(L, L + 3):
+            assert revolve_cost(s, L) == 0
+    assert revolve_cost(0, 3) == float("inf")
+    for s, L in ((1, 5), (2, 6), (3, 10), (2, 9)):
+        m = revolve_split(s, L)
+        assert 1 <= m < L
+        assert m + revolve_cost(s - 1, L - m) + revolve_cost(s, m) == revolve_cost(s, L)
+    # more slots never cost more; more steps never cost less
+    for s in range(1, 5):
+        for L in range(2, 14):
+            assert revolve_cost(s + 1, L) <= revolve_cost(s, L) <= revolve_cost(s, L + 1)
+
+
+def _readvanced(region, dim, full):
+    """Forward steps re-advanced in a joint: the extents of the folds that read
+    their final state over a strict sub-range of the scan dim (checkpoint
+    advances), counted once per distinct fold."""
+    from pdum_dsl_amd.tl.ir import walk
+
+    seen, total = set(), 0
+    for nd in walk(region):
+        if nd.op != "tl.fold" or nd.attr("dim") != dim or tuple(nd.attr("out"))[0] != "final":
+            continue
+        if tuple(nd.attr("state"))[0].startswith("fold.ct"):
+            continue  # a reverse fold
+        k = len(nd.attr("state"))
+        ext = nd.args[k].type.dim(dim)
+        if (ext.start, ext.stop) == (0, full):
+            continue  # the forward fold itself
+        key = (tuple(id(a) for a in nd.args), ext.start, ext.stop)
+        if key in seen:
+            continue
+        seen.add(key)
+        total += ext.size
+    return total
+
+
+@pytest.mark.parametrize("sched", [{"fold_segments": 7}, {"fold_segments": 2}, {"fold_slots": 1},
+                                   {"fold_slots": 2}, {"fold_slots": 3}, {"fold_slots": 14}])
+def test_checkpointed_schedules_give_the_one_segment_gradient(sched):
+    """The linear recurrence and the logsumexp fold (two states) under every
+    schedule: the same gradients as the one-segment adjoint to 1e-12, and the
+    closed forms; revolve re-advances exactly revolve_cost steps."""
+    from pdum_dsl_amd.tl.autodiff import grad, region_names, revolve_cost
+    from pdum_dsl_amd.tl.interp import Field
+
+    T, I = 14, 3
+    reg = _recurrence(T, I)
+    names = region_names(reg, ("a", "s0", "x"))
+    one = grad(reg, "out", seed="w", names=names)
+    chk = grad(reg, "out", None, "w", None, None, sched.get("fold_segments"), sched.get("fold_slots"), names=names)
+    rng = np.random.default_rng(5)
+    a, s0, x, w = (rng.uniform(0.5, 1.1, I), rng.standard_normal(I), rng.standard_normal((T, I)),
+                   rng.standard_normal(I))
+    vals = [Field(a, reg.params[0].type.dims), Field(s0, reg.params[1].type.dims), Field(x, reg.params[2].type.dims),
+            Field(w, one.region.params[-1].type.dims)]
+    got1, _ = _eval_both(one.region, vals)
+    gotc_i, gotc_o = _eval_both(chk.region, vals)
+    d1, dci, dco = dict(zip(one.outputs, got1)), dict(zip(chk.outputs, gotc_i)), dict(zip(chk.outputs, gotc_o))
+    dx = np.stack([w * a ** (T - 1 - t) for t in range(T)])
+    for nm, names_ in (("dx", ("t", "i")), ("da", ("i",)), ("ds0", ("i",))):
+        np.testing.assert_allclose(dci[nm].to_numpy(names_), d1[nm].to_numpy(names_), rtol=1e-12, atol=1e-13)
+        np.testing.assert_allclose(dco[nm].order(names_).numpy(), d1[nm].to_numpy(names_), rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(dci["dx"].to_numpy(("t", "i")), dx, rtol=1e-12)
+    if "fold_slots" in sched:
+        assert _readvanced(chk.region, "t", T) == revolve_cost(sched["fold_slots"], T)
+    if sched.get("fold_slots") == 14:  # enough slots: the stored trajectory, as one segment
+        assert chk.region.key == one.region.key
+
+    reg2 = _logsumexp_fold(12, 4)
+    n2 = region_names(reg2, ("x",))
+    segs = sched.get("fold_segments")
+    segs = None if segs is not None and 12 % segs else segs
+    r1 = grad(reg2, "out", seed="w", names=n2)
+    rc = grad(reg2, "out", None, "w", None, None, segs, sched.get("fold_slots"), names=n2)
+    x2, w2 = rng.standard_normal((12, 4)) * 3, rng.standard_normal(4)
+    v2 = [Field(x2, reg2.params[0].type.dims), Field(w2, r1.region.params[-1].type.dims)]
+    sm = np.exp(x2 - x2.max(0)) / np.exp(x2 - x2.max(0)).sum(0)
+    g_i, g_o = _eval_both(rc.region, v2)
+    np.testing.assert_allclose(dict(zip(rc.outputs, g_i))["dx"].to_numpy(("t", "i")), w2 * sm, rtol=1e-12,
+                               atol=1e-14)
+    np.testing.assert_allclose(dict(zip(rc.outputs, g_o))["dx"].order(("t", "i")).numpy(), w2 * sm, rtol=1e-12,
+                               atol=1e-14)
+
+
+def test_uniform_segments_must_divide_the_extent():
+    from pdum_dsl_amd.tl.autodiff import grad, region_names
+
+    reg = _recurrence(7, 2)
+    with pytest.raises(ValueError, match="must divide the fold extent"):
+        grad(reg, "out", None, "w", None, None, 3, None, names=region_names(reg, ("a", "s0", "x")))
+
+
+def test_the_flash_tile_under_revolve_matches_one_segment():
+    from pdum_dsl_amd.tl import zoo
+    from pdum_dsl_amd.tl.autodiff import grad, region_names
+    from pdum_dsl_amd.tl.interp import Field
+
+    subj = zoo.flash_tile(T=8, E=3, OD=2, SI=2, seed=9)
+    tile = subj.tile
+    nm = region_names(tile, ("q", "k", "v"))
+    one = grad(tile, "out", seed="dout", names=nm)
+    rev = grad(tile, "out", None, "dout", None, None, None, 2, names=nm)
+    rng = np.random.default_rng(6)
+    q, k, v = (f.arr for f in subj.inputs)
+    dout = rng.standard_normal(tuple(tile.body[-1].args[0].type.shape))
+    vals = [Field(q, tile.params[0].type.dims), Field(k, tile.params[1].type.dims),
+            Field(v, tile.params[2].type.dims), Field(dout, one.region.params[-1].type.dims)]
+    g1, _ = _eval_both(one.region, vals)
+    gr, _ = _eval_both(rev.region, vals)
+    d1, dr = dict(zip(one.outputs, g1)), dict(zip(rev.outputs, gr))
+    for nm_, names in (("dq", ("t", "e")), ("dk", ("s", "e")), ("dv", ("s", "o"))):
+        np.testing.assert_allclose(dr[nm_].to_numpy(names), d1[nm_].to_numpy(names), rtol=1e-11, atol=1e-13)

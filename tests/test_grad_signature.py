@@ -59,10 +59,10 @@ def test_fold_schedule_arguments_are_checked_like_the_reference():
         grad(subj.region, "out", None, "dO", None, None, 2, 3, names=nm)
     with pytest.raises(ValueError, match="fold_slots must be >= 1"):
         grad(subj.region, "out", None, "dO", fold_slots=0, names=nm)
-    with pytest.raises(NotImplementedError, match="checkpointed fold schedules"):
-        grad(subj.region, "out", None, "dO", fold_segments=4, names=nm)
-    with pytest.raises(NotImplementedError, match="checkpointed fold schedules"):
-        grad(subj.region, "out", None, "dO", fold_slots=2, names=nm)
+    # a region without folds: every schedule builds the one-segment joint
+    plain = grad(subj.region, "out", seed="dO", names=nm).region.key
+    assert grad(subj.region, "out", None, "dO", fold_segments=4, names=nm).region.key == plain
+    assert grad(subj.region, "out", None, "dO", fold_slots=2, names=nm).region.key == plain
     with pytest.raises(NotImplementedError, match="target_unit"):
         grad(subj.region, "out", None, "dO", None, "m", names=nm)
     one = grad(subj.region, "out", None, "dO", fold_segments=1, names=nm)
