@@ -420,7 +420,8 @@ __global__ __launch_bounds__(F16Cfg<D>::THREADS, 3) void flash_fwd_m16(FwdArgs a
       }
     }
     u32x4 p[2];
-    auto expo = [&](int h, float& part) {
+    // the tile's exponentials of query half h into p[h]; returns their sum
+    auto expo = [&](int h) {
       const float mc = mused[h] * a.c2;
       float e[8];
 #pragma unroll
@@ -429,9 +430,9 @@ __global__ __launch_bounds__(F16Cfg<D>::THREADS, 3) void flash_fwd_m16(FwdArgs a
         for (int i = 0; i < 4; ++i) {
           const float x = sacc[kb][h][i];
           e[4 * kb + i] = CUT ? fast_exp2((x - mused[h]) * a.c2) : fast_exp2(__builtin_fmaf(x, a.c2, -mc));
-          part += e[4 * kb + i];
         }
       p[h] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]), pack2<T>(e[6], e[7])};
+      return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
     };
     auto rowmax = [&](int h) {
       float m = -kInf;
@@ -449,16 +450,13 @@ __global__ __launch_bounds__(F16Cfg<D>::THREADS, 3) void flash_fwd_m16(FwdArgs a
       for (int fb = 0; fb < C::FB; ++fb) oacc[fb][h] *= alpha;
     };
     if constexpr (!CUT && !ART) {
-      float part0 = 0.f, part1 = 0.f;
-      expo(0, part0);
-      expo(1, part1);
+      float part0 = expo(0), part1 = expo(1);
       const float lim = static_cast<float>(1 << static_cast<int>(kTau));
       if (__builtin_amdgcn_ballot_w64(!(part0 <= lim) || !(part1 <= lim)) != 0) {
         rescale(0, fmaxf(mused[0], rowmax(0)));
         rescale(1, fmaxf(mused[1], rowmax(1)));
-        part0 = part1 = 0.f;
-        expo(0, part0);
-        expo(1, part1);
+        part0 = expo(0);
+        part1 = expo(1);
       }
       lsum[0] += part0;
       lsum[1] += part1;
@@ -470,8 +468,8 @@ __global__ __launch_bounds__(F16Cfg<D>::THREADS, 3) void flash_fwd_m16(FwdArgs a
         rescale(0, fmaxf(mused[0], m0));
         rescale(1, fmaxf(mused[1], m1));
       }
-      expo(0, lsum[0]);
-      expo(1, lsum[1]);
+      lsum[0] += expo(0);
+      lsum[1] += expo(1);
     }
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
