@@ -357,8 +357,12 @@ int pdh_contract_views(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, 
  * interpreter otherwise) and never stored. Replaces the reference's operand
  * re-derivation inside the contraction's k loop (conformance/triton_tile.py:
  * 228-371, _dot_at / _reduce_at), where this library's other entry points take
- * a computed operand only as a buffer a map chain has filled first. PDH_F32
- * only; no row partials. */
+ * a computed operand only as a buffer a map chain has filled first. No row
+ * partials. PDH_BF16 storage: both operands are computed (a stored
+ * operand as a one-LOAD program over its strides), their LOADs read 16-bit
+ * values, each operand value is rounded to bf16 (as a 16-bit operand a map
+ * chain materializes is) and the products accumulate in fp32; the output is
+ * rounded once to bf16. Other element types: PDH_EUNSUPPORTED. */
 int pdh_contract_views_pro(const void* a, int64_t sa_b, int64_t sa_r, int64_t sa_k, const pdh_ew_program* pro_a,
                            const void* const* pro_a_operands, const void* bt, int64_t sb_b, int64_t sb_r,
                            int64_t sb_k, const pdh_ew_program* pro_b, const void* const* pro_b_operands,

@@ -70,6 +70,23 @@ __global__ __launch_bounds__(256, 2) void contract_split_pro_small(ContractArgs 
                                                                                                         &pa, &pb);
 }
 
+// 16-bit storage with computed operands: the split body with one bf16 plane
+// (the operands' values rounded to bf16, as a materialized 16-bit operand is),
+// both operands computed by prologues that read 16-bit leaves.
+template <int DT>
+__global__ __launch_bounds__(256, 2) void contract_split16_pro(ContractArgs a, pdh_ew_program p, EwOperands ops,
+                                                               ContractPro pa, ContractPro pb) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[split_lds<64, 1>()];
+  contract_split_body<DT, 64, 1, 0, InterpEval, -1, InterpEval, InterpEval, true>(a, p, ops, smem, &pa, &pb);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256, 2) void contract_split16_pro_small(ContractArgs a, pdh_ew_program p, EwOperands ops,
+                                                                     ContractPro pa, ContractPro pb) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[split_lds<32, 1>()];
+  contract_split_body<DT, 32, 1, 0, InterpEval, -1, InterpEval, InterpEval, true>(a, p, ops, smem, &pa, &pb);
+}
+
 // The interpreter's split kernel for (mode, operand layouts), by value; with
 // prologues (pro non-null) the prologue kernel.
 template <int NSPLIT>
@@ -257,10 +274,10 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
   const int lay = (ca.sa_k != 1 && !ca.pro_a ? 1 : 0) | (ca.sb_k != 1 && !ca.pro_b ? 2 : 0);
   PDH_REQUIRE(lay == 0 || ca.dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: 16-bit operands must have k contiguous", fn);
   PDH_REQUIRE(ca.rowred < 0 || ca.dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: row partials of fp32 contractions only", fn);
-  PDH_REQUIRE(pro == nullptr || (ca.dtype == PDH_F32 && ca.rowred < 0), PDH_EUNSUPPORTED,
-              "%s: operand prologues: fp32 contractions without row partials only", fn);
+  PDH_REQUIRE(pro == nullptr || (ca.rowred < 0 && (ca.dtype == PDH_F32 || (ca.pro_a && ca.pro_b))), PDH_EUNSUPPORTED,
+              "%s: operand prologues: no row partials, and with 16-bit storage both operands computed", fn);
   const bool spec = pro != nullptr ? jit_get_pro(*epi, ca.pro_a ? &pro[0].p : nullptr, ca.pro_b ? &pro[1].p : nullptr,
-                                                 fns, lay)
+                                                 fns, lay, ca.dtype)
                                    : jit_get(JitKind::Contract, *epi, ca.dtype, fns, lay, ca.rowred);
   pdh_ew_program pe = *epi;
   ContractPro pro_a = pro != nullptr ? pro[0] : ContractPro{}, pro_b = pro != nullptr ? pro[1] : ContractPro{};
@@ -276,6 +293,23 @@ int contract_launch(ContractArgs ca, const pdh_ew_program* epi, const void* cons
     return PDH_OK;
   };
   const int f32_mode = f32_contract_mode();
+  if (ca.dtype != PDH_F32 && pro != nullptr) {  // 16-bit, computed operands: the one-plane split body
+    if (g_cus == 0) g_cus = pdh_device_cus() > 0 ? pdh_device_cus() : 256;
+    const bool small = batch * ((m + 127) / 128) * ((n + 127) / 128) < g_cus || m <= 64 || n <= 64 || ca.kp <= 2 * kBK;
+    const int bm = small ? 64 : 128;
+    ca.tiles_m = static_cast<int>((m + bm - 1) / bm);
+    ca.tiles_n = static_cast<int>((n + bm - 1) / bm);
+    const int64_t nblk = batch * ca.tiles_m * ca.tiles_n;
+    if (spec) return launch_spec(fns[small ? 1 : 0], nblk);
+    PDH_REQUIRE(nblk <= INT32_MAX, PDH_EINVAL, "%s: grid too large", fn);
+    const dim3 grid(static_cast<unsigned>(nblk));
+    PDH_REQUIRE(ca.dtype == PDH_BF16, PDH_EUNSUPPORTED, "%s: computed f16 operands", fn);
+    if (small)
+      contract_split16_pro_small<PDH_BF16><<<grid, 256, 0, st>>>(ca, *epi, ops, pro[0], pro[1]);
+    else
+      contract_split16_pro<PDH_BF16><<<grid, 256, 0, st>>>(ca, *epi, ops, pro[0], pro[1]);
+    return check_launch(fn);
+  }
   if (ca.dtype == PDH_F32 && f32_mode == 0) {
     ca.tiles_m = static_cast<int>((m + kFT - 1) / kFT);
     ca.tiles_n = static_cast<int>((n + kFT - 1) / kFT);
@@ -454,8 +488,11 @@ extern "C" int pdh_contract_views_pro(const void* a, int64_t sa_b, int64_t sa_r,
                                       int64_t k, int64_t ksplit, const pdh_ew_program* epi,
                                       const void* const* operands, void* out, int dtype, void* stream) {
   const char* fn = "pdh_contract_views_pro";
-  PDH_REQUIRE(dtype == PDH_F32, PDH_EUNSUPPORTED, "%s: fp32 operands only", fn);
+  PDH_REQUIRE(dtype == PDH_F32 || dtype == PDH_BF16, PDH_EUNSUPPORTED,
+              "%s: dtype %d (fp32 or bf16; f16 operands would lose bits in bf16 planes)", fn, dtype);
   PDH_REQUIRE(pro_a != nullptr || pro_b != nullptr, PDH_EINVAL, "%s: no prologue (pdh_contract_views reads both)", fn);
+  PDH_REQUIRE(dtype == PDH_F32 || (pro_a != nullptr && pro_b != nullptr), PDH_EUNSUPPORTED,
+              "%s: with 16-bit storage both operands are computed (a stored one as a one-LOAD program)", fn);
   PDH_REQUIRE((pro_a || a) && (pro_b || bt) && out, PDH_EINVAL, "%s: null pointer", fn);
   PDH_REQUIRE(batch >= 1 && m >= 1 && n >= 1 && k >= 1, PDH_EINVAL, "%s: need batch, m, n, k >= 1", fn);
   PDH_REQUIRE(ksplit >= 1 && ksplit <= 64, PDH_EINVAL, "%s: ksplit = %lld must be in [1, 64]", fn,

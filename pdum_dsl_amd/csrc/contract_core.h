@@ -51,7 +51,9 @@ struct ContractArgs {
   // [batch][m][ceil(n / 32)] (row partials; columns past n take no part)
   int rowred;
   // nonzero: a (pro_a) / bt (pro_b) is not read but computed in the k loop by
-  // its prologue program (ContractPro; fp32 bodies of a prologue kernel only)
+  // its prologue program (ContractPro; the split and VALU bodies of a prologue
+  // kernel only; with 16-bit storage both operands are computed, their LOADs
+  // reading 16-bit values, and the split body runs with one bf16 plane)
   int pro_a, pro_b;
 };
 
@@ -78,18 +80,19 @@ struct SameT<A, A> {
 // evaluated coordinate is clamped below kend, so every LOAD stays inside the
 // views the host checked. Whole runs take one evaluator call of four.
 template <typename PE>
-__device__ __forceinline__ void pro_run4(const ContractPro& pr, int be, int rc, int k0, int kend, float (&x)[4]) {
+__device__ __forceinline__ void pro_run4(const ContractPro& pr, int dt, int be, int rc, int k0, int kend,
+                                         float (&x)[4]) {
   int c0[PDH_EW_MAX_DIMS] = {be, rc, k0, 0};
   if (k0 + 3 < kend) {
     const float zacc[4] = {0.f, 0.f, 0.f, 0.f};
-    PE::template run<4>(pr.p, pr.ops, PDH_F32, c0, zacc, x, 1);
+    PE::template run<4>(pr.p, pr.ops, dt, c0, zacc, x, 1);
   } else {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       c0[2] = k0 + j < kend ? k0 + j : kend - 1;
       float y[1];
       const float z1[1] = {0.f};
-      PE::template run<1>(pr.p, pr.ops, PDH_F32, c0, z1, y, 1);
+      PE::template run<1>(pr.p, pr.ops, dt, c0, z1, y, 1);
       x[j] = k0 + j < kend ? y[0] : 0.f;
     }
   }
@@ -97,9 +100,9 @@ __device__ __forceinline__ void pro_run4(const ContractPro& pr, int be, int rc, 
 
 // The interpreter's form, called rather than inlined: the interpreter is a
 // large switch, and the prologue kernels call it from many places.
-static __device__ __attribute__((noinline)) void pro_interp4(const ContractPro& pr, int be, int rc, int k0, int kend,
-                                                       float (&x)[4]) {
-  pro_run4<InterpEval>(pr, be, rc, k0, kend, x);
+static __device__ __attribute__((noinline)) void pro_interp4(const ContractPro& pr, int dt, int be, int rc, int k0,
+                                                              int kend, float (&x)[4]) {
+  pro_run4<InterpEval>(pr, dt, be, rc, k0, kend, x);
 }
 
 // Four operand values of one row, k columns kk .. kk + 3 of batch index bb's
@@ -112,9 +115,9 @@ __device__ __forceinline__ f32x4 pro_eval4(const ContractPro& pr, const Contract
   const int kbase = (bb % a.ksplit) * a.kp;
   float x[4];
   if constexpr (SameT<PE, InterpEval>::value)
-    pro_interp4(pr, bb / a.ksplit, rc, kbase + kk, kbase + kin, x);
+    pro_interp4(pr, a.dtype, bb / a.ksplit, rc, kbase + kk, kbase + kin, x);
   else
-    pro_run4<PE>(pr, bb / a.ksplit, rc, kbase + kk, kbase + kin, x);
+    pro_run4<PE>(pr, a.dtype, bb / a.ksplit, rc, kbase + kk, kbase + kin, x);
   const bool rin = row < rows;
   return f32x4{rin ? x[0] : 0.f, rin ? x[1] : 0.f, rin ? x[2] : 0.f, rin ? x[3] : 0.f};
 }
@@ -650,7 +653,8 @@ __device__ __forceinline__ void contract_mfma_body(const ContractArgs& a, const 
 // 4 x 4 outputs per lane, k tiles of 16 staged k-major through LDS (as, bs:
 // kFK x (kFT + 4) floats each), and the epilogue applied. Every lane of the
 // workgroup takes part (barriers inside).
-template <typename Eval, int RED = -1, typename ProA = InterpEval, typename ProB = InterpEval, bool PRO = false>
+template <typename Eval, int RED = -1, typename ProA = InterpEval, typename ProB = InterpEval, bool PRO = false,
+          int ODT = PDH_F32>
 __device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_ew_program& p, const EwOperands& ops,
                                                int b, int m0, int n0, float (*as)[kFT + 4], float (*bs)[kFT + 4],
                                                const ContractPro* pra = nullptr, const ContractPro* prb = nullptr) {
@@ -717,7 +721,7 @@ __device__ __forceinline__ void f32_valu_block(const ContractArgs& a, const pdh_
       store_row_partial(a, r, b, m0 + 4 * ty + i, n0 + 4 * tx,
                         epilogue_reduced4<PDH_F32, Eval>(p, ops, a, r, b, m0 + 4 * ty + i, n0 + 4 * tx, av));
     else
-      contract_epilogue<PDH_F32, 4, Eval>(p, ops, a, b, m0 + 4 * ty + i, n0 + 4 * tx, av);
+      contract_epilogue<ODT, 4, Eval>(p, ops, a, b, m0 + 4 * ty + i, n0 + 4 * tx, av);
   }
 }
 
@@ -1043,8 +1047,8 @@ __device__ __forceinline__ void contract_split_body(const ContractArgs& a, const
     float(*bs)[kFT + 4] = reinterpret_cast<float(*)[kFT + 4]>(smem + kFK * (kFT + 4) * 4);
 #pragma unroll 1
     for (int ij = 0; ij < (BM / kFT) * (BM / kFT); ++ij)  // one copy of the block's code
-      f32_valu_block<Eval, RED, ProA, ProB, PRO>(a, p, ops, b, m0 + kFT * (ij / (BM / kFT)), n0 + kFT * (ij % (BM / kFT)),
-                                             as, bs, pra, prb);
+      f32_valu_block<Eval, RED, ProA, ProB, PRO, DT>(a, p, ops, b, m0 + kFT * (ij / (BM / kFT)),
+                                                 n0 + kFT * (ij % (BM / kFT)), as, bs, pra, prb);
     return;
   }
   contract_store<DT, WM, Eval, RED>(a, p, ops, smem, acc, b, m0, n0);

@@ -22,7 +22,7 @@ bool jit_get_reduce(const pdh_ew_program& ps, const pdh_ew_program& pe, int dt, 
 // specialized: fns[0] the 128 x 128-tile (or fp32-mode-0 VALU) kernel, fns[1]
 // the 64 x 64-tile one; or false.
 bool jit_get_pro(const pdh_ew_program& pe, const pdh_ew_program* pa, const pdh_ew_program* pb, hipFunction_t fns[2],
-                 int lay);
+                 int lay, int dt);
 void jit_count_launch();
 // How fp32 contractions run: 0 VALU fma; 1, 3 or 6 bf16 MFMA products per term
 // (pdh_contract_set_f32_mode).

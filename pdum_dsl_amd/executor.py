@@ -975,7 +975,9 @@ class PlanExecutor:
                          strides=(nrows * KP, KP, 1) if views else (nrows * KP, KP))
 
         views = self.dtype == "f32"  # pdh_contract_views: operands in place, any k
-        fuse = views and rowred is None  # computed operands in the k loop (pdh_contract_views_pro)
+        # computed operands in the k loop (pdh_contract_views_pro): fp32, and bf16
+        # (where the other operand is read through a one-LOAD program)
+        fuse = rowred is None and self.dtype in ("f32", "bf16")
         pa, pb = pack(ca, mdims, M), pack(cb, ndims, N)
         y = k.body[-1].args[0] if yroot is None else yroot
         if y.type.names and set(y.type.names) != set(out_names):
@@ -1085,6 +1087,16 @@ class PlanExecutor:
                 return out
             if views:
                 views_call(prog, [vals[i] for i in eslots], out, f32_mode=self.f32_contract)
+            elif pra is not None or prb is not None:  # bf16: both operands through programs
+
+                def as_prog(p, t, pr, rows):
+                    if pr is not None:
+                        return pr
+                    st = tuple(p.strides) if len(p.strides) == 3 else (p.strides[0], p.strides[1], 1)
+                    return K.view_program((B, rows, Kx), st), [t]
+
+                K.contract_views_pro(None, None, None, None, (B, M, N, Kx), prog, [vals[i] for i in eslots], out,
+                                     pro_a=as_prog(pa, a, pra, M), pro_b=as_prog(pb, bt, prb, N))
             elif KP == Kx:  # every operand as stored (or as packed), through its strides
                 K.contract_strided(a, pa.strides, bt, pb.strides, (B, M, N, Kx), prog,
                                    [vals[i] for i in eslots], out, f32_mode=self.f32_contract)

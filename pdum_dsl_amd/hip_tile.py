@@ -685,8 +685,9 @@ def _contraction_runner(region, cb, grid, dtype):
 
     def operand(node, order):
         """A param uploads as is. A prologue chain is computed in the k loop
-        (pdh_contract_views_pro) at fp32, and runs first through pdh_map_chain
-        at 16 bits."""
+        (pdh_contract_views_pro) at fp32 and bf16 (where the other operand,
+        a param, is then read by a one-LOAD program), and runs first through
+        pdh_map_chain at f16."""
         if node.op == "core.param":
             return ("param", _index(region, node))
         adims = tuple(size.get(nm) or (node.type.dim(nm) if node.type.has(nm) else Dim(nm, 0, 1)) for nm in order)
@@ -699,7 +700,7 @@ def _contraction_runner(region, cb, grid, dtype):
     pa, pb = operand(cb["a"], a_order), operand(cb["b"], b_order)
     epi_idx = [_index(region, p) for p in epi.bases]
 
-    fused = dtype == "f32" and "chain" in (pa[0], pb[0])
+    fused = dtype in ("f32", "bf16") and "chain" in (pa[0], pb[0])
 
     def dev(ts):
         torch = _torch()
@@ -730,6 +731,9 @@ def _contraction_runner(region, cb, grid, dtype):
             for spec, node, order, rows in ((pa, cb["a"], a_order, M_), (pb, cb["b"], b_order, N_)):
                 if spec[0] == "chain":
                     sides.append((None, None, prologue(spec, rows)))
+                elif dtype == "bf16":  # both computed at 16 bits: the param through a one-LOAD program
+                    t = _arrange(torch, ts[spec[1]], node.type.names, order)
+                    sides.append((None, None, (K.view_program(tuple(t.shape), t.stride()), [t])))
                 else:
                     t = build(spec, node, order, rows)
                     sides.append((t, t.stride(), None))
@@ -744,7 +748,7 @@ def _contraction_runner(region, cb, grid, dtype):
         full = out.reshape(tuple(size[nm].size for nm in present))
         return full.permute([present.index(nm) for nm in y.type.names])
 
-    kern = ("contract_views_pro" if fused else "contract_f32") if dtype == "f32" else f"contract_mfma<{dtype}>"
+    kern = "contract_views_pro" if fused else ("contract_f32" if dtype == "f32" else f"contract_mfma<{dtype}>")
     src = (f"hip:{kern} batch={B_} m={M_} n={N_} k={Kdim} kp={KP} prologue={pa[0]},{pb[0]} "
            f"epilogue_insns={len(epi.insns)} operands={len(epi.operands)} stores=1")
     return _finish(dev, src, grid, "contraction-epilogue", region, dtype)

@@ -546,14 +546,18 @@ def contract_views_pro(a, a_strides, bt, bt_strides, shape, epi: _lib.EwProgram,
     (pdh_contract_views_pro): ``pro_a`` = (program, operands), the program over
     the lattice (batch, m, k) whose value at (b, r, kk) is a[b, r, kk] (``a`` /
     ``a_strides`` are then unused and may be None); ``pro_b`` likewise over
-    (batch, n, k) for bt. fp32."""
+    (batch, n, k) for bt. fp32, or bf16 with both operands computed (a stored
+    one as :func:`view_program`)."""
     B, M, N, Kd = (int(x) for x in shape)
     if pro_a is None and pro_b is None:
         raise ValueError("contract_views_pro needs a prologue (contract_views reads both operands)")
     _require_cuda(out, *operands, *[t for t in (a, bt) if t is not None],
                   *[t for pr in (pro_a, pro_b) if pr is not None for t in pr[1]])
-    if out.dtype != torch.float32:
-        raise ValueError("contract_views_pro takes fp32")
+    dt = out.dtype
+    if dt not in (torch.float32, torch.bfloat16):
+        raise ValueError("contract_views_pro takes fp32 or bf16")
+    if dt != torch.float32 and (pro_a is None or pro_b is None):
+        raise ValueError("bf16 contract_views_pro computes both operands (a stored one as view_program)")
     tables, progs, reads = [], [], []
     for t, st, pr, rows, nm in ((a, a_strides, pro_a, M, "a"), (bt, bt_strides, pro_b, N, "bt")):
         if pr is None:
@@ -575,8 +579,8 @@ def contract_views_pro(a, a_strides, bt, bt_strides, shape, epi: _lib.EwProgram,
         if len(ops) != prog.n_operands:
             raise ValueError(f"the {nm} prologue reads {prog.n_operands} operands, {len(ops)} given")
         for i, o in enumerate(ops):
-            if o.dtype != torch.float32:
-                raise ValueError(f"{nm} prologue operand {i} is {o.dtype}: fp32 only")
+            if o.dtype != dt:
+                raise ValueError(f"{nm} prologue operand {i} is {o.dtype}, the output {dt}: one element type")
             if _max_offset(prog, prog.in_stride[i], 3) >= o.numel() or o.storage_offset() < 0:
                 raise ValueError(f"{nm} prologue operand {i}: the program's view reaches past the tensor")
         tables.append((C.c_void_p * max(1, len(ops)))(*[o.data_ptr() for o in ops]))
@@ -588,11 +592,27 @@ def contract_views_pro(a, a_strides, bt, bt_strides, shape, epi: _lib.EwProgram,
     table = (C.c_void_p * max(1, len(operands)))(*[t.data_ptr() for t in operands])
     null_prog = C.POINTER(_lib.EwProgram)()
     (pa, sab, sar, sak), (pb, sbb, sbr, sbk) = reads
-    _with_f32_mode(f32_mode, torch.float32, lambda: _lib.call(
+    _with_f32_mode(f32_mode, dt, lambda: _lib.call(
         "pdh_contract_views_pro", pa, sab, sar, sak, progs[0] if progs[0] is not None else null_prog,
         tables[0], pb, sbb, sbr, sbk, progs[1] if progs[1] is not None else null_prog, tables[1],
-        B, M, N, Kd, int(ksplit), C.byref(epi), table, _ptr(out), _DT[torch.float32], C.c_void_p(_stream())))
+        B, M, N, Kd, int(ksplit), C.byref(epi), table, _ptr(out), _DT[dt], C.c_void_p(_stream())))
     return out
+
+
+def view_program(shape3, strides) -> _lib.EwProgram:
+    """A one-LOAD prologue: operand 0 read through ``strides`` over the
+    lattice ``shape3`` = (batch, rows, k) (a stored operand of
+    :func:`contract_views_pro`)."""
+    p = _lib.EwProgram()
+    p.n_insns, p.n_operands, p.ndim, p.out_reg = 1, 1, 3, 0
+    acc = 1
+    for d in (2, 1, 0):
+        p.shape[d] = int(shape3[d])
+        p.out_stride[d] = acc
+        p.in_stride[0][d] = int(strides[d])
+        acc *= int(shape3[d])
+    p.insns[0].op = _lib.EW["LOAD"]
+    return p
 
 
 _REDUCERS = {"sum": 0, "max": 1, "min": 2}

@@ -69,17 +69,20 @@ def test_both_operands_computed(M, K, N):
     _check(got, _oracle(region, vals, ("t", "f")), "f32", f"both computed {M}x{K}x{N}", k=K)
 
 
-def test_the_executor_fuses_a_computed_operand():
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_the_executor_fuses_a_computed_operand(dtype):
     from pdum_dsl_amd.executor import PlanExecutor
     from pdum_dsl_amd.tl.partition import plan_model
+    from tests.test_gpu_contract import _bf16
 
     region, vals = _gelu_chain_subject(200, 448, 136, seed=5)
-    ex = PlanExecutor(plan_model(region), region, "f32")
+    ex = PlanExecutor(plan_model(region), region, dtype)
     assert any("a=prologue" in s for s in ex.sources())
     ex.bind(vals)
     got = ex.run()  # the one output, dims in the yield's order
     torch.cuda.synchronize()
-    _check(got.float().cpu().numpy(), _oracle(region, vals, ("t", "f")), "f32", "executor gelu(x) @ w + b", k=448)
+    want = _oracle(region, vals if dtype == "f32" else [_bf16(v) for v in vals], ("t", "f"))
+    _check(got.float().cpu().numpy(), want, dtype, f"executor gelu(x) @ w + b ({dtype})", k=448)
 
 
 def _programs(B, M, N, Kd, x, s):
@@ -204,3 +207,64 @@ def test_a_prologue_over_the_wrong_lattice_is_refused_before_launch():
                                         None, None, B, M, N, Kd, 1, C.byref(_identity((B, M, N), out)), None,
                                         C.c_void_p(out.data_ptr()), 0, None)
     assert rc != 0
+
+
+@pytest.mark.parametrize("M,K,N", [(96, 160, 72), (130, 1001, 70), (300, 640, 260)])
+def test_bf16_prologue_chains_are_computed_in_the_k_loop(M, K, N):
+    """At bf16 storage the seat computes the chain operand in the k loop too
+    (the param through a one-LOAD program), against the oracle on the same
+    bf16-rounded inputs."""
+    from tests.test_gpu_contract import _bf16
+
+    region, vals = _gelu_chain_subject(M, K, N, seed=M + 1)
+    _g, run = _seat(region, "bf16")
+    assert run.source.startswith("hip:contract_views_pro") and "prologue=chain,param" in run.source
+    got = run(vals)
+    _check(got, _oracle(region, [_bf16(v) for v in vals], ("t", "f")), "bf16", f"bf16 gelu(x) @ w + b {M}x{K}x{N}",
+           k=K)
+
+
+@pytest.mark.parametrize("jit", [True, False])
+@pytest.mark.parametrize("B,M,N,Kd", [(2, 130, 200, 333), (1, 300, 260, 700), (3, 64, 64, 5)])
+def test_bf16_computed_operands_match_the_materialized_ones(jit, B, M, N, Kd):
+    """bf16: the a prologue computed in the k loop and bt through a one-LOAD
+    program, against the operand materialized by the same program (a bf16
+    buffer) and the product of the bf16 operands by the 16-bit kernel."""
+    from pdum_dsl_amd import _lib as L
+    from pdum_dsl_amd import kernels as K
+
+    g = torch.Generator(device="cuda").manual_seed(B * 7 + Kd)
+    x = torch.randn(B, M, Kd, device="cuda", generator=g).to(torch.bfloat16)
+    s = (1.0 + 0.1 * torch.randn(B, Kd, device="cuda", generator=g)).to(torch.bfloat16)
+    bt = torch.randn(B, N, Kd, device="cuda", generator=g).to(torch.bfloat16)
+    pa = _programs(B, M, N, Kd, x, s)
+    out_f = torch.empty(B, M, N, device="cuda", dtype=torch.bfloat16)
+    prev = L.lib().pdh_ew_set_jit(1 if jit else 0)
+    try:
+        K.contract_views_pro(None, None, None, None, (B, M, N, Kd), _identity((B, M, N), out_f), [], out_f,
+                             pro_a=(pa, [x, s]), pro_b=(K.view_program((B, N, Kd), bt.stride()), [bt]))
+        a = torch.empty(B, M, Kd, device="cuda", dtype=torch.bfloat16)
+        K.map_chain(pa, [x, s], a)
+        torch.cuda.synchronize()
+    finally:
+        L.lib().pdh_ew_set_jit(prev)
+    ref = torch.bmm(a.double(), bt.double().transpose(1, 2).contiguous())
+    got = out_f.double()
+    what = f"bf16 jit={jit} B{B} M{M} N{N} K{Kd}"
+    # fp32 accumulation of the bf16 operands' exact products, one bf16 rounding of the result
+    scale = float(ref.abs().max())
+    assert float((got - ref).abs().max()) <= 2 ** -8 * scale + 1e-6 * scale * max(1.0, (Kd / 64) ** 0.5), what
+
+
+def test_f16_prologues_are_refused():
+    from pdum_dsl_amd import _lib as L
+    from pdum_dsl_amd import kernels as K
+
+    B, M, N, Kd = 1, 64, 64, 64
+    x = torch.randn(B, M, Kd, device="cuda").half()
+    bt = torch.randn(B, N, Kd, device="cuda").half()
+    out = torch.empty(B, M, N, device="cuda").half()
+    with pytest.raises((ValueError, L.PdhError)):
+        K.contract_views_pro(None, None, None, None, (B, M, N, Kd), _identity((B, M, N), out), [], out,
+                             pro_a=(K.view_program((B, M, Kd), x.stride()), [x]),
+                             pro_b=(K.view_program((B, N, Kd), bt.stride()), [bt]))
