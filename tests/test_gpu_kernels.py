@@ -206,6 +206,23 @@ def test_flash_fwd_fp32_generic_matches_oracle(K, T, S, E, OD, causal):
     _check_fwd(res, q, k, v, 0.125, band, lowp=False)
 
 
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,T,S,D,band",
+    [(1, 1, 1, 256, 256, 64, None), (1, 2, 2, 300, 290, 64, (None, 0)), (2, 4, 2, 130, 1000, 32, None),
+     (1, 2, 1, 200, 333, 64, (-70, 5)), (1, 3, 3, 65, 64, 32, (None, 600)), (1, 2, 2, 129, 129, 64, (None, -1))],
+)
+def test_flash_fwd_fp32_row_kernel_matches_oracle(K, B, Hq, Hkv, T, S, D, band):
+    """e = od = 32 or 64 at fp32 take the row kernel (lane = query row, K / V
+    rows as wave-uniform loads, the key range split over four waves): causal,
+    windowed, half-open and fully-masked-row bands (the last disables the
+    prune), grouped heads, row and key tails, the artifacts."""
+    rng = np.random.default_rng(T * 7 + S + D)
+    q, k, v = _qkv(rng, B, Hq, Hkv, T, S, D, D, torch.float32)
+    res = K.flash_fwd(q, k, v, scale=D**-0.5, band=K.Band(*band) if band else None, want_artifacts=True)
+    torch.cuda.synchronize()
+    _check_fwd(res, q, k, v, D**-0.5, band, lowp=False)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_pruned_sweep_is_bit_equal_to_the_full_sweep(K, dtype):
     rng = np.random.default_rng(11)
