@@ -24,6 +24,13 @@ planner's numpy interpreter, so each can check the other:
                  (layout.py)
   tl.take        the gather (indexing.py:120-230)
   tl.scatter_add its adjoint, duplicates summed (indexing.py:153-190, 223-259)
+  tl.window / tl.stencil / tl.decimate   gathers along one dim by index
+                 arithmetic (layout.py:700-771, guarded.py:463-520)
+  tl.diagonal    the cells whose parts agree (layout.py:669-698)
+  tl.round_to    nearest value of bf16 / f16 / f32, ties to even
+                 (encoding.py:40-51, compute.py:368-375)
+  composite tl.reduce / tl.scan   the sequential sweep of compute.py:230-260
+                 over the reducer's traced lift / combine / project
   tl.fold        a Python loop over the scan dim (out ('final', i): the last
                  state i; ('emit',): each step's last yield stacked along the
                  scan dim), each element source
@@ -85,6 +92,14 @@ def value(arr, ir_type) -> V:
     return V(t, dims)
 
 
+def _canon(x, tt):
+    """``x`` with its axes in its type's dim order (for ops that work by axis position)."""
+    names = tuple(d.name for d in tt.dims)
+    if not isinstance(x, V) or x.names == names:
+        return x
+    return V(x.order(names), tuple(x.dims[x.names.index(nm)] for nm in names))
+
+
 def _dims_arg(d):
     return (d,) if isinstance(d, str) else tuple(d)
 
@@ -112,8 +127,114 @@ def _attr(n, name, default=None):
     return default
 
 
+_BITS = {"f32": (24, -149, 3.4028234663852886e38), "f16": (11, -24, 65504.0),
+         "bf16": (8, -133, 3.3895313892515355e38)}
+
+
+def _round(t: torch.Tensor, enc: str) -> torch.Tensor:
+    bits, qmin, top = _BITS[enc]
+    m, e = torch.frexp(t)
+    q = torch.clamp(e - bits, min=qmin)
+    out = torch.round(torch.ldexp(m, (e - q).to(torch.float64))) * torch.pow(torch.tensor(2.0, dtype=torch.float64),
+                                                                            q.to(torch.float64))
+    if not torch.isfinite(out).all() or bool((out.abs() > top).any()):
+        raise ValueError(f"round_to({enc}): not finite in the format")
+    return out
+
+
+def _gather(x: V, n):
+    """window / stencil / decimate: out[.., c, ..] = x[.., src(c), ..]."""
+    name = _attr(n, "name")
+    ax = x.names.index(name)
+    _, lo, hi = x.dims[ax]
+    out_dims = tuple((d.name, d.start, d.stop) for d in n.type.dims)
+    od = next(d for d in n.type.dims if d.name == name)
+    if n.op == "tl.decimate":
+        f = _attr(n, "factor")
+        src = torch.arange(od.start, od.stop) * f + int(_attr(n, "phase", 0) or 0) % f
+        return V(torch.index_select(x.t, ax, src - lo), out_dims)
+    kn = _attr(n, "k_name") or f"{name}_k"
+    kd = next(d for d in n.type.dims if d.name == kn)
+    dil = _attr(n, "dilation", 1) or 1
+    src = torch.arange(od.start, od.stop).unsqueeze(1) + dil * torch.arange(kd.start, kd.stop).unsqueeze(0)
+    live = (src >= lo) & (src < hi)
+    safe = torch.where(live, src - lo, torch.zeros_like(src))
+    if hi == lo:
+        got = torch.zeros(tuple(x.t.shape[:ax]) + tuple(src.shape) + tuple(x.t.shape[ax + 1:]), dtype=torch.float64)
+    else:
+        got = torch.index_select(x.t, ax, safe.reshape(-1)).reshape(
+            tuple(x.t.shape[:ax]) + tuple(src.shape) + tuple(x.t.shape[ax + 1:]))
+    if n.op == "tl.stencil":
+        shape = (1,) * ax + tuple(live.shape) + (1,) * (x.t.dim() - ax - 1)
+        got = torch.where(live.reshape(shape), got, torch.tensor(float(_attr(n, "fill", 0.0) or 0.0),
+                                                                 dtype=torch.float64))
+    return V(got, out_dims)
+
+
+def _sweep(n, ev):
+    """A composite reducer: lift the first element, combine the rest in
+    order (compute.py:230-260); project the last state, or each (a scan)."""
+    from pdum_dsl_amd.tl.ir import minus_dim
+    from pdum_dsl_amd.tl.reducers import lookup, parts
+
+    f = lookup(_attr(n, "f"))
+    dim = _attr(n, "dim") if n.op == "tl.scan" else _dims_arg(_attr(n, "dims"))[0]
+    st = minus_dim(n.args[0].type, dim)
+    P = parts(f, st)
+    xs = [ev(a) for a in n.args]
+    ax = xs[0].names.index(dim)
+    _, lo, hi = xs[0].dims[ax]
+
+    def run(region, vals):
+        r = evaluate(region, list(vals))
+        return tuple(r) if isinstance(r, tuple) else (r,)
+
+    rest = tuple(d for d in xs[0].dims if d[0] != dim)
+    state, outs = None, []
+    for c in range(lo, hi):
+        el = []
+        for x in xs:
+            a = x.names.index(dim)
+            el.append(V(x.t.select(a, c - x.dims[a][1]), x.dims[:a] + x.dims[a + 1:]))
+        lifted = run(P.lift, el)
+        state = lifted if state is None else run(P.combine, state + lifted)
+        if n.op == "tl.scan":
+            outs.append(run(P.project, state)[0].order([d[0] for d in rest]))
+    names = [d[0] for d in rest]
+    if n.op == "tl.scan":
+        t = torch.stack(outs, dim=len(names)) if outs else torch.zeros([d[2] - d[1] for d in rest] + [0],
+                                                                        dtype=torch.float64)
+        src = names + [dim]
+        return V(t.permute([src.index(d.name) for d in n.type.dims]), tuple((d.name, d.start, d.stop)
+                                                                              for d in n.type.dims))
+    if state is None:
+        state = tuple(V(torch.full([d[2] - d[1] for d in rest], v, dtype=torch.float64), rest) for v in f.init)
+    out = run(P.project, state)[0]
+    return V(out.order([d.name for d in n.type.dims]), tuple((d.name, d.start, d.stop) for d in n.type.dims))
+
+
 def _dispatch(n, ev):
     op = n.op
+    if op in ("tl.reduce", "tl.scan"):
+        from pdum_dsl_amd.tl.reducers import is_composite
+
+        if is_composite(_attr(n, "f")):
+            return _sweep(n, ev)
+    if op in ("tl.window", "tl.stencil", "tl.decimate"):
+        return _gather(_canon(ev(n.args[0]), n.args[0].type), n)
+    if op == "tl.diagonal":
+        x = _canon(ev(n.args[0]), n.args[0].type)
+        parts = _dims_arg(_attr(n, "parts"))
+        axes = [x.names.index(nm) for nm in parts]
+        z = next(d for d in n.type.dims if d.name == _attr(n, "name"))
+        t = x.t.movedim(axes, list(range(len(axes))))
+        cz = torch.arange(z.start, z.stop)
+        got = t[tuple(cz - x.dims[a][1] for a in axes)]
+        at = [d.name for d in n.type.dims].index(z.name)
+        return V(got.movedim(0, at), tuple((d.name, d.start, d.stop) for d in n.type.dims))
+    if op == "tl.round_to":
+        x = ev(n.args[0])
+        return V(_round(x.t, _attr(n, "encoding")), x.dims)
     if op == "core.const":
         return float(_attr(n, "value"))
     if op == "core.yield":
@@ -218,17 +339,18 @@ def _dispatch(n, ev):
         coords = torch.arange(lo, hi, dtype=torch.float64).reshape(shape)
         return V(coords.expand([d[2] - d[1] for d in dims]), dims)
     if op in ("tl.rename", "tl.shift"):  # layout.py rename / shift: relabelings, no data moves
-        x = ev(n.args[0])
+        x = _canon(ev(n.args[0]), n.args[0].type)
         return V(x.t, tuple((d.name, d.start, d.stop) for d in n.type.dims))
-    if op == "tl.slice":  # layout.py slice: absolute [lo, hi) per dim
+    if op == "tl.slice":  # layout.py slice: absolute [lo, hi) per dim, matched by name
         x = ev(n.args[0])
         t = x.t
-        for ax, (d, o) in enumerate(zip(x.dims, n.type.dims)):
+        out = tuple(n.type.dim(d[0]) for d in x.dims)
+        for ax, (d, o) in enumerate(zip(x.dims, out)):
             t = t.narrow(ax, o.start - d[1], o.stop - o.start)
-        return V(t, tuple((d.name, d.start, d.stop) for d in n.type.dims))
+        return V(t, tuple((d.name, d.start, d.stop) for d in out))
     if op == "tl.pad":  # layout.py pad: frames widened, new cells = fill
         x = ev(n.args[0])
-        out_dims = tuple((d.name, d.start, d.stop) for d in n.type.dims)
+        out_dims = tuple((o.name, o.start, o.stop) for o in (n.type.dim(d[0]) for d in x.dims))
         t = torch.full([d[2] - d[1] for d in out_dims], float(_attr(n, "fill", 0.0)), dtype=torch.float64)
         window = tuple(slice(xd[1] - od[1], xd[2] - od[1]) for xd, od in zip(x.dims, out_dims))
         t[window] = x.t
@@ -237,7 +359,7 @@ def _dispatch(n, ev):
         x = ev(n.args[0])
         return V(torch.flip(x.t, dims=(x.names.index(_attr(n, "name")),)), x.dims)
     if op == "tl.merge":  # layout.py merge: split's inverse, parts outer first
-        x = ev(n.args[0])
+        x = _canon(ev(n.args[0]), n.args[0].type)
         parts = _attr(n, "parts")
         parts = (parts,) if isinstance(parts, str) else tuple(parts)
         rest = [nm for nm in x.names if nm not in parts]
@@ -248,7 +370,7 @@ def _dispatch(n, ev):
         t = t.reshape(tuple(t.shape[:at]) + (-1,) + tuple(t.shape[at + len(parts):]))
         return V(t, tuple((d.name, d.start, d.stop) for d in n.type.dims))
     if op == "tl.take":  # indexing.py:192-230: the taken dim replaced in place by idx's dims
-        table, idx = ev(n.args[0]), ev(n.args[1])
+        table, idx = _canon(ev(n.args[0]), n.args[0].type), _canon(ev(n.args[1]), n.args[1].type)
         name = _attr(n, "dim")
         ax = table.names.index(name)
         lo, hi = table.dims[ax][1], table.dims[ax][2]

@@ -18,7 +18,7 @@ templates), over the vocabulary this backend reads:
                  prefix count of the hits (autodiff.py:635-665)
   tl.scan        sum -> the scan of the cotangent the other way (a prefix
                  sum's adjoint is a suffix sum, autodiff.py:667-677); other
-                 reducers refuse
+                 primitive reducers refuse, as in the reference
   tl.repeat_like / tl.repeat   -> sum over the added dims
   tl.take        -> tl.scatter_add of the cotangent at the same indices
                  (duplicates sum), and tl.scatter_add -> tl.take
@@ -32,17 +32,32 @@ templates), over the vocabulary this backend reads:
                  gets no cotangent (shift invariance: its terms sum to zero);
                  grad(..., shift_invariant_softmax=False) keeps the
                  reference's route through the max's adjoint
+  taps and strides (autodiff.py:680-763): tl.window / tl.stencil -> each
+                 tap's slice of the cotangent shifted back (a stencil's fill
+                 carries nothing); tl.decimate -> the cotangent spread onto
+                 every factor-th cell, zero between; tl.diagonal -> the
+                 cotangent where all parts agree, zero elsewhere
+  tl.round_to    straight-through, or no flow with grad="zero"
+                 (autodiff.py:843-845)
   tl.stage       identity
   core.const / tl.const / tl.iota / comparisons / stop_gradient: no flow
 
-  tl.fold        read at its final state: a reverse fold over the flipped
-                 sequences whose step is the forward step's VJP (grad of the
-                 step against the carried cotangent), states before each step
-                 from the forward trajectory (autodiff.py:411-605, one
-                 segment, no checkpointing)
+  tl.fold        a reverse fold over the flipped sequences whose step is the
+                 forward step's VJP (grad of the step against the carried
+                 cotangent), states before each step from the forward
+                 trajectory (autodiff.py:411-605), under the reference's
+                 schedules (one segment, K uniform segments, binomial
+                 revolve). Read at its final state the carry starts at the
+                 cotangent; an emitting fold's reverse step also takes each
+                 emission's cotangent as an element.
+  composite tl.reduce / tl.scan   lowered to the fold they denote (the first
+                 element's lift, combine(state, lift(element)), the
+                 projection; pdum_dsl_amd.tl.reducers.lower) and
+                 differentiated as that fold: the composite sweep's
+                 back-propagation (autodiff.py:335-400)
 
-Anything else (argtopk, an emitting fold) refuses by name: a primitive
-joins the AD with its linearization, or not at all.
+Anything else (argtopk) refuses by name: a primitive joins the AD with its
+linearization, or not at all.
 """
 
 from __future__ import annotations
@@ -52,6 +67,7 @@ from functools import lru_cache
 
 from .dialect import OPS
 from .ir import F64, Builder, Node, Region, TensorType
+from .reducers import lower_region
 
 # markers through which no gradient flows (piecewise-constant or boolean)
 _FLAT = frozenset({"eq", "ne", "le", "lt", "ge", "gt", "floor", "stop_gradient"})
@@ -141,6 +157,8 @@ def grad(
     if target_unit is not None:
         raise NotImplementedError("grad: target_unit — units are not modelled by this backend; pass None")
     schedule = (None if fold_segments is None else int(fold_segments), None if fold_slots is None else int(fold_slots))
+    # composite reductions differentiate as the folds they are (first lift, combine, project)
+    region, names = lower_region(region, names)
     by_name: dict = {}
     for p in region.params:
         by_name.setdefault(names[id(p)], p)
@@ -308,6 +326,15 @@ def grad(
             contribute(n.args[0], b.emit("tl.rename", c, mapping=back))
         elif op == "tl.fold":
             _fold_rule(b, n, c, contribute, const, *schedule)
+        elif op in ("tl.window", "tl.stencil"):
+            _tap_rule(b, n, c, contribute)
+        elif op == "tl.decimate":
+            _decimate_rule(b, n, c, contribute, pw, const)
+        elif op == "tl.diagonal":
+            _diagonal_rule(b, n, c, contribute, pw, const)
+        elif op == "tl.round_to":  # straight-through unless declared zero (autodiff.py:843-845)
+            if n.attr("grad", "straight_through") != "zero":
+                contribute(n.args[0], c)
         else:
             raise NotImplementedError(
                 f"{op} has no adjoint rule in this build (a primitive joins the AD with its linearization)"
@@ -388,9 +415,8 @@ def _fold_rule(b, n, c, contribute, const, fold_segments=None, fold_slots=None):
     k = len(state)
     dim = n.attr("dim")
     out = tuple(n.attr("out"))
-    if out[0] != "final":
-        raise NotImplementedError("tl.fold: only a fold read at its final state has an adjoint here")
-    o = out[1]
+    emits = out[0] == "emit"  # c is then the cotangent of every step's emission, stacked along dim
+    o = None if emits else out[1]
     inits, elems = n.args[:k], n.args[k:]
     d = elems[0].type.dim(dim)
     start, stop = d.start, d.stop
@@ -403,8 +429,9 @@ def _fold_rule(b, n, c, contribute, const, fold_segments=None, fold_slots=None):
     def zeros(tt):
         return b.emit("tl.const", value=0.0, dims=tuple((x.name, (x.start, x.stop)) for x in tt.dims))
 
-    if stop == start:  # no step runs: the fold is its initial state
-        contribute(inits[o], c)
+    if stop == start:  # no step runs: the fold is its initial state (and emits nothing)
+        if not emits:
+            contribute(inits[o], c)
         return
 
     def with_yield(vals):
@@ -412,18 +439,22 @@ def _fold_rule(b, n, c, contribute, const, fold_segments=None, fold_slots=None):
         yy = vals[0] if len(vals) == 1 else wb.emit("core.tuple", *vals)
         return Region(params=step.params, body=(wb.emit("core.yield", yy),))
 
-    # the step's VJP: grad of sum_i <ct_i, y_i> over the step's params
+    if emits:  # the states alone, for the folds that re-advance them
+        step = with_yield(ynodes[:k])
+    # the step's VJP: grad of sum_i <ct_i, y_i> over the step's params (an
+    # emitting fold's emission y_k pairs with the emission's cotangent ct_k)
+    nct = k + (1 if emits else 0)
     wb = Builder(OPS)
-    cts = tuple(wb.param(("fold.ct", i), ynodes[i].type) for i in range(k))
+    cts = tuple(wb.param(("fold.ct", i), ynodes[i].type) for i in range(nct))
     tgt = None
-    for i in range(k):
+    for i in range(nct):
         t_ = wb.emit("tl.pointwise", ynodes[i], cts[i], f="mul")
         if t_.type.dims:
             t_ = wb.emit("tl.reduce", t_, dims=tuple(x.name for x in t_.type.dims), f="sum")
         tgt = t_ if tgt is None else wb.emit("tl.pointwise", tgt, t_, f="add")
     wrapper = Region(params=tuple(step.params) + cts, body=(wb.emit("core.yield", tgt),))
     pnames = tuple(f"s{i}" for i in range(k)) + tuple(f"e{j}" for j in range(len(ep))) + tuple(
-        f"ct{i}" for i in range(k))
+        f"ct{i}" for i in range(nct))
     vjp = grad(wrapper, "fold.vjp", wrt=pnames[:k + len(ep)], names=region_names(wrapper, pnames, ("fold.vjp",)))
     flows = tuple(vjp.grads.get(f"s{i}") is not None for i in range(k))
 
@@ -432,10 +463,11 @@ def _fold_rule(b, n, c, contribute, const, fold_segments=None, fold_slots=None):
         return zeros(tt) if gname is None else vjp.nodes[gname]
 
     dstate = tuple(g_of(f"s{i}", sp[i].type) for i in range(k))
-    # reverse step: carries ct, elements (states before the step, the step's elements)
-    rparams = cts + tuple(step.params)
+    # reverse step: carries ct, elements (states before the step, the step's
+    # elements, and for an emitting fold the emission's cotangent)
+    rparams = cts[:k] + tuple(step.params) + cts[k:]
     rat = {"dim": dim, "state": tuple(f"fold.ct{i}" for i in range(k)),
-           "element": tuple(f"fold.prev{i}" for i in range(k)) + fat["element"]}
+           "element": tuple(f"fold.prev{i}" for i in range(k)) + fat["element"] + (("fold.ce",) if emits else ())}
 
     def rstep(extra=()):
         rb = Builder(OPS)
@@ -471,6 +503,9 @@ def _fold_rule(b, n, c, contribute, const, fold_segments=None, fold_slots=None):
             init_t = b.emit("tl.repeat", s0[i], name=dim, extent=(lo, hi))
             prev.append(b.emit("tl.pointwise", first, init_t, later, f="where"))
         rsrc = tuple(flip(v) for v in prev) + tuple(flip(v) for v in se)
+        if emits:
+            ce = c if (lo, hi) == (start, stop) else b.emit("tl.slice", c, ranges=((dim, (lo, hi)),))
+            rsrc += (flip(ce),)
         for j, ev_ in enumerate(elems):
             if vjp.grads.get(f"e{j}") is None:
                 continue
@@ -482,7 +517,7 @@ def _fold_rule(b, n, c, contribute, const, fold_segments=None, fold_slots=None):
         return tuple(b.emit("tl.fold", *cur, *rsrc, regions=(rstep(),), out=("final", i), **rat) if flows[i]
                      else zeros(inits[i].type) for i in range(k))
 
-    cur = tuple(c if i == o else zeros(inits[i].type) for i in range(k))
+    cur = tuple(c if i == o else zeros(inits[i].type) for i in range(k))  # o is None for an emitting fold
     T = stop - start
     if fold_slots is not None:
         def revolve(lo, hi, slots, boundary):
@@ -510,6 +545,92 @@ def _fold_rule(b, n, c, contribute, const, fold_segments=None, fold_slots=None):
     for i in range(k):
         if flows[i]:
             contribute(inits[i], cur[i])
+
+
+def _tap_rule(b, n, c, contribute):
+    """tl.window / tl.stencil (autodiff.py:680-697): tap j read x at
+    x' + dilation j, so its slice of the cotangent shifts back by dilation j;
+    the cells a stencil tap read outside the domain (the fill) carry nothing."""
+    x = n.args[0]
+    name = n.attr("name")
+    d = x.type.dim(name)
+    kn = n.attr("k_name") or f"{name}_k"
+    kd, dil = n.type.dim(kn), n.attr("dilation", 1)
+    for j in range(kd.start, kd.stop):
+        t = b.emit("tl.shift", b.emit("tl.select", c, coords=((kn, j),)), deltas=((name, j * dil),))
+        sd = t.type.dim(name)
+        lo, hi = max(d.start, sd.start), min(d.stop, sd.stop)
+        if hi <= lo:
+            continue
+        if (lo, hi) != (sd.start, sd.stop):
+            t = b.emit("tl.slice", t, ranges=((name, (lo, hi)),))
+        if (lo, hi) != (d.start, d.stop):
+            t = b.emit("tl.pad", t, extents=((name, (d.start, d.stop)),), fill=0.0)
+        contribute(x, t)
+
+
+def _fresh(names, base):
+    i = 0
+    while f"_{base}{i}" in names:
+        i += 1
+    return f"_{base}{i}"
+
+
+def _decimate_rule(b, n, c, contribute, pw, const):
+    """tl.decimate (autodiff.py:699-736): output j read x at factor j + p.
+    The cotangent, renumbered from 0, gains a phase dim of size factor that
+    is zero except at phase 0; merged (outer j, inner phase) and shifted to
+    factor j0 + p it lands on the read cells, then is cut and padded to x's
+    domain. Any domain works (no divisibility needed)."""
+    x = n.args[0]
+    name, f = n.attr("name"), n.attr("factor")
+    p = int(n.attr("phase", 0)) % f
+    d, od = x.type.dim(name), n.type.dim(name)
+    if od.size == 0:
+        return
+    taken = set(n.type.names) | set(x.type.names)
+    cn = _fresh(taken, "c")
+    ph = _fresh(taken | {cn}, "ph")
+    r = b.emit("tl.shift", b.emit("tl.rename", c, mapping=((name, cn),)), deltas=((cn, -od.start),))
+    r = b.emit("tl.repeat", r, name=ph, extent=(0, f))
+    r = pw("where", pw("eq", b.emit("tl.iota", r, name=ph), const(0.0)), r, const(0.0))
+    r = b.emit("tl.merge", r, parts=(cn, ph), name=name)
+    lo = f * od.start + p
+    r = b.emit("tl.shift", r, deltas=((name, lo),))
+    hi = min(d.stop, lo + f * od.size)
+    if hi != lo + f * od.size:
+        r = b.emit("tl.slice", r, ranges=((name, (lo, hi)),))
+    if (lo, hi) != (d.start, d.stop):
+        r = b.emit("tl.pad", r, extents=((name, (d.start, d.stop)),), fill=0.0)
+    contribute(x, r)
+
+
+def _diagonal_rule(b, n, c, contribute, pw, const):
+    """tl.diagonal (autodiff.py:738-763, for any number of parts): the
+    cotangent at z goes to the cell where every part equals z. It takes the
+    first part's name, is repeated over the other parts' domains, kept where
+    their coordinates equal the first's, and padded to the first's domain."""
+    x = n.args[0]
+    parts = n.attr("parts")
+    parts = (parts,) if isinstance(parts, str) else tuple(parts)
+    z = n.attr("name")
+    zd = n.type.dim(z)
+    if zd.size == 0:
+        return
+    x0 = parts[0]
+    r = c if z == x0 else b.emit("tl.rename", c, mapping=((z, x0),))
+    for q in parts[1:]:
+        qd = x.type.dim(q)
+        r = b.emit("tl.repeat", r, name=q, extent=(qd.start, qd.stop))
+    keep = None
+    for q in parts[1:]:
+        m = pw("eq", b.emit("tl.iota", r, name=x0), b.emit("tl.iota", r, name=q))
+        keep = m if keep is None else pw("mul", keep, m)
+    r = pw("where", keep, r, const(0.0))
+    d0 = x.type.dim(x0)
+    if (zd.start, zd.stop) != (d0.start, d0.stop):
+        r = b.emit("tl.pad", r, extents=((x0, (d0.start, d0.stop)),), fill=0.0)
+    contribute(x, r)
 
 
 def _pointwise_rule(n, c, contribute, pw, const):

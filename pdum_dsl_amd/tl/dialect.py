@@ -29,6 +29,21 @@ emit and consume (packages/tensorlib/src/pdum/tl/dialect.py:115-487):
   tl.take       dim             out = table[idx, rest]: a gather, no template row
   tl.scatter_add dim, extent[, over]  take's adjoint: out[v, rest] = sum of
                                 values at the positions p with idx[p] == v
+  tl.window     name, k_name, k[, dilation]  a tap dim after name:
+                                out[x, j] = x[x + dilation j], name shrunk so
+                                every tap stays inside its old domain
+  tl.stencil    name, k[, k_name, fill, dilation]  the same taps over name's
+                                whole domain (k an INCLUSIVE range), fill where
+                                a tap leaves it
+  tl.decimate   name, factor[, phase]  every factor-th cell (i = phase mod
+                                factor), renumbered j = (i - phase) / factor
+  tl.diagonal   parts, name     the cells where all parts agree, as one dim
+                                over the intersection of their domains
+  tl.round_to   encoding[, grad]  encode-then-decode to bf16 / f16 / f32,
+                                round to nearest even (the one precision op)
+  tl.reduce / tl.scan with a composite reducer (pdum_dsl_amd.tl.reducers):
+                                m aligned element operands folded through
+                                its lift / combine / project
   tl.argtopk    (typed only: a non-template op the planner must refuse)
 """
 
@@ -71,11 +86,28 @@ def _r_pointwise(args, at, regions):
     return TensorType(ts[0].dims)
 
 
+def _composite(args, at, dims) -> TensorType:
+    """The element operands of a composite reduce / scan: as many as the
+    reducer's element count, aligned, folded along exactly one dim
+    (compute.py:216-240 in the reference)."""
+    from .reducers import lookup
+
+    f = lookup(at["f"])
+    if len(args) != f.element:
+        raise TypeError(f"{f.name} consumes {f.element} element operand(s), got {len(args)}")
+    _aligned(list(args))
+    if len(dims) != 1:
+        raise TypeError(f"{f.name}: composite reducers fold one dim at a time")
+    args[0].dim(dims[0])
+    return args[0]
+
+
 def _r_reduce(args, at, regions):
-    (x,) = args
     dims = _dims_arg(at["dims"])
     if at["f"] not in REDUCERS:
-        raise TypeError(f"unknown reducer {at['f']!r}")
+        x = _composite(args, at, dims)
+        return TensorType(tuple(d for d in x.dims if d.name not in dims))
+    (x,) = args
     for d in dims:
         x.dim(d)
     return TensorType(tuple(d for d in x.dims if d.name not in dims))
@@ -86,11 +118,13 @@ def _r_scan(args, at, regions):
     reference): out[.., t, ..] folds x[.., start..t, ..]; a mean divides by the
     running count. ``reverse=True`` folds the suffix x[.., t..stop, ..] instead
     (the reference spells it flip . scan . flip)."""
-    (x,) = args
-    if at["f"] not in REDUCERS:
-        raise TypeError(f"unknown reducer {at['f']!r}")
     if not isinstance(at["dim"], str):
         raise TypeError("tl.scan folds exactly one dim (pass its name)")
+    if at["f"] not in REDUCERS:
+        if at.get("reverse"):
+            raise TypeError("tl.scan: a composite reducer scans forward (flip the operands for a suffix scan)")
+        return TensorType(_composite(args, at, (at["dim"],)).dims)
+    (x,) = args
     x.dim(at["dim"])
     return TensorType(x.dims)
 
@@ -340,6 +374,113 @@ def _r_scatter_add(args, at, regions):
     return TensorType(tuple(out))
 
 
+def _taps(k) -> tuple:
+    """A window's half-open tap-index range: an int n is [0, n)."""
+    if isinstance(k, int):
+        return 0, int(k)
+    lo, hi = (int(v) for v in k)
+    return lo, hi
+
+
+def _dilation(at) -> int:
+    dil = at.get("dilation", 1)
+    if not isinstance(dil, int) or dil < 1:
+        raise TypeError(f"dilation must be a positive int, got {dil!r}")
+    return dil
+
+
+def _r_window(args, at, regions):
+    """layout.py:700-740: the tap dim k_name (half-open tap range k) goes
+    right after name, whose domain shrinks to the cells whose every tap
+    x + dilation j lands inside the old one."""
+    (x,) = args
+    d = x.dim(at["name"])
+    kn = at["k_name"]
+    if x.has(kn):
+        raise TypeError(f"tl.window: dim {kn!r} already exists")
+    dil = _dilation(at)
+    lo, hi = _taps(at["k"])
+    if hi <= lo:
+        raise TypeError(f"tl.window needs a non-empty tap range, got [{lo}, {hi})")
+    ns, ne = d.start - dil * lo, d.stop - dil * (hi - 1)
+    if ne < ns:
+        raise TypeError(f"tl.window: taps [{lo}, {hi}) x {dil} are wider than {d.name}'s domain")
+    out = []
+    for e in x.dims:
+        out.extend((Dim(e.name, ns, ne), Dim(kn, lo, hi)) if e.name == d.name else (e,))
+    return TensorType(tuple(out))
+
+
+def _r_stencil(args, at, regions):
+    """guarded.py:463-520: name keeps its domain; the tap dim (INCLUSIVE
+    tap range k = (kmin, kmax), named k_name or name + '_k') follows it.
+    Taps that leave the domain read the fill."""
+    (x,) = args
+    d = x.dim(at["name"])
+    kn = at.get("k_name") or f"{d.name}_k"
+    if x.has(kn):
+        raise TypeError(f"tl.stencil: dim {kn!r} already exists")
+    _dilation(at)
+    kmin, kmax = (int(v) for v in at["k"])
+    if kmax < kmin:
+        raise TypeError(f"tl.stencil: empty tap range ({kmin}, {kmax})")
+    out = []
+    for e in x.dims:
+        out.extend((e, Dim(kn, kmin, kmax + 1)) if e.name == d.name else (e,))
+    return TensorType(tuple(out))
+
+
+def _r_decimate(args, at, regions):
+    """layout.py:742-771: cells i = phase (mod factor) of name, renumbered
+    j = (i - phase) / factor over [ceil((start - p) / f), floor((stop - 1 - p) / f] + 1)."""
+    (x,) = args
+    d = x.dim(at["name"])
+    f = at["factor"]
+    if not isinstance(f, int) or f < 1:
+        raise TypeError(f"tl.decimate: factor must be a positive int, got {f!r}")
+    p = int(at.get("phase", 0)) % f
+    j0 = -((p - d.start) // f)
+    j1 = (d.stop - 1 - p) // f
+    return TensorType(tuple(Dim(e.name, j0, max(j0, j1 + 1)) if e.name == d.name else e for e in x.dims))
+
+
+def _r_diagonal(args, at, regions):
+    """layout.py:669-698: the parts (two or more) walked at once, as one dim
+    ``name`` over the intersection of their domains, placed where the first
+    of them sits in the operand."""
+    (x,) = args
+    parts = _dims_arg(at["parts"])
+    if len(parts) < 2 or len(set(parts)) != len(parts):
+        raise TypeError(f"tl.diagonal needs two or more distinct dims, got {parts}")
+    ds = [x.dim(nm) for nm in parts]
+    name = at["name"]
+    if x.has(name) and name not in parts:
+        raise TypeError(f"tl.diagonal: dim {name!r} already exists")
+    start = max(d.start for d in ds)
+    stop = max(start, min(d.stop for d in ds))
+    out, placed = [], False
+    for e in x.dims:
+        if e.name in parts:
+            if not placed:
+                out.append(Dim(name, start, stop))
+                placed = True
+        else:
+            out.append(e)
+    return TensorType(tuple(out))
+
+
+ENCODINGS = ("f32", "f16", "bf16")
+
+
+def _r_round_to(args, at, regions):
+    (x,) = args
+    if at["encoding"] not in ENCODINGS:
+        raise TypeError(f"tl.round_to: unknown encoding {at['encoding']!r} (one of {ENCODINGS})")
+    if at.get("grad", "straight_through") not in ("straight_through", "zero"):
+        raise TypeError("tl.round_to: grad is 'straight_through' or 'zero'")
+    return TensorType(x.dims)
+
+
 def _r_tuple(args, at, regions):
     return TupleType(tuple(args))
 
@@ -378,10 +519,16 @@ OPS: dict[str, OpDef] = {
     "tl.merge": OpDef("tl.merge", _r_merge),
     "tl.take": OpDef("tl.take", _r_take),
     "tl.scatter_add": OpDef("tl.scatter_add", _r_scatter_add),
+    "tl.window": OpDef("tl.window", _r_window),
+    "tl.stencil": OpDef("tl.stencil", _r_stencil),
+    "tl.decimate": OpDef("tl.decimate", _r_decimate),
+    "tl.diagonal": OpDef("tl.diagonal", _r_diagonal),
+    "tl.round_to": OpDef("tl.round_to", _r_round_to),
 }
 
 # ops no template row reads: a region holding one plans it red
-TILE_OPS = frozenset(OPS) - {"tl.argtopk", "tl.take", "tl.scatter_add", "tl.pad", "tl.flip", "tl.merge"}
+TILE_OPS = frozenset(OPS) - {"tl.argtopk", "tl.take", "tl.scatter_add", "tl.pad", "tl.flip", "tl.merge", "tl.window",
+                             "tl.stencil", "tl.decimate", "tl.diagonal", "tl.round_to"}
 
 
 def builder() -> Builder:
@@ -406,4 +553,4 @@ def check_tier(region: Region, tier: str = "tile") -> Region:
     return region
 
 
-__all__ = ["OPS", "MARKERS", "REDUCERS", "builder", "const", "check_tier", "F64", "BOOL", "Scalar", "TensorType"]
+__all__ = ["OPS", "MARKERS", "REDUCERS", "ENCODINGS", "builder", "const", "check_tier", "F64", "BOOL", "Scalar", "TensorType"]

@@ -174,9 +174,31 @@ def forest_is_closed(n) -> bool:
     return False
 
 
+def _flashsm_core(y):
+    """reduce(zoo.flashsm, (repeat_like(sm, v), repeat_like(v, sm)), s): the
+    masked scores fed to the online-softmax reducer (zoo/attention.py:180-186)
+    -> (sm, v, s); the same denotation as the softmax composition."""
+    from .reducers import is_composite, lookup
+    from .zoo import flashsm
+
+    if y.op != "tl.reduce" or not is_composite(y.attr("f")) or lookup(y.attr("f")) is not flashsm:
+        return None
+    dims = y.attr("dims")
+    dims = (dims,) if isinstance(dims, str) else tuple(dims)
+    se, ve = y.args
+    if len(dims) != 1 or se.op != "tl.repeat_like" or ve.op != "tl.repeat_like":
+        return None
+    sm, v = se.args[0], ve.args[0]
+    if se.args[1] is not v or ve.args[1] is not sm:
+        return None
+    return sm, v, dims[0]
+
+
 def match_flash(region: Region):
     """The flash composition over bare params q:(t,e), k:(s,e), v:(s,o), with
-    an optional artifact yield (out, max, den) (fusion.py:480-539)."""
+    an optional artifact yield (out, max, den) (fusion.py:480-539). The
+    masked scores may also reach v through the flashsm composite reducer:
+    the same program by its denotation, so the same row serves it."""
     y = region.body[-1].args[0]
     artifacts = False
     if y.op == "core.tuple":
@@ -184,18 +206,24 @@ def match_flash(region: Region):
             return None
         y, m_out, den_out = y.args
         artifacts = True
-    out = contract_core(y)
-    if out is None:
-        return None
-    pr, v, s = out
-    sm_m = match_softmax(pr)
-    if sm_m is None or sm_m["s"] != s:
-        return None
-    if artifacts and (m_out is not sm_m["max"] or den_out is not sm_m["den"]):
-        return None
-    if v.op != "core.param":
-        return None
-    smn = sm_m["sm"]
+    fsm = None if artifacts else _flashsm_core(y)
+    if fsm is not None:
+        smn, v, s = fsm
+        if v.op != "core.param":
+            return None
+    else:
+        out = contract_core(y)
+        if out is None:
+            return None
+        pr, v, s = out
+        sm_m = match_softmax(pr)
+        if sm_m is None or sm_m["s"] != s:
+            return None
+        if artifacts and (m_out is not sm_m["max"] or den_out is not sm_m["den"]):
+            return None
+        if v.op != "core.param":
+            return None
+        smn = sm_m["sm"]
     if smn.op != "tl.pointwise" or smn.attr("f") != "where" or len(smn.args) != 3:
         return None
     mask, sc, fill = smn.args

@@ -21,7 +21,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from .ir import Dim, Node, Region, TensorType
+from .ir import Dim, Node, Region, TensorType, minus_dim
+from .reducers import is_composite, lookup, parts
 
 _PW = {
     "add": np.add, "sub": np.subtract, "mul": np.multiply, "div": np.divide, "neg": np.negative,
@@ -45,6 +46,25 @@ def _gelu_d0(lib, x):
 
 
 _RED = {"sum": (np.add, 0.0), "prod": (np.multiply, 1.0), "max": (np.maximum, None), "min": (np.minimum, None)}
+
+# significant bits, exponent of the smallest quantum (subnormal), largest finite value
+_FORMATS = {"f32": (24, -149, 3.4028234663852886e38), "f16": (11, -24, 65504.0),
+            "bf16": (8, -133, 3.3895313892515355e38)}
+
+
+def round_to(arr, encoding: str) -> np.ndarray:
+    """encode-then-decode (encoding.py:40-42, compute.py:368-375): round to
+    the nearest value of the format, ties to even, subnormals kept; a value
+    that rounds past the largest finite one refuses, as non-finite patterns
+    refuse at decode (encoding.py:45-51)."""
+    bits, qmin, top = _FORMATS[encoding]
+    a = np.asarray(arr, dtype=np.float64)
+    _, e = np.frexp(a)  # a = m 2^e, 1/2 <= |m| < 1
+    q = np.maximum(e - bits, qmin)  # the quantum's exponent at a's binade
+    out = np.ldexp(np.rint(np.ldexp(a, -q)), q)
+    if not np.isfinite(out).all() or (np.abs(out) > top).any():
+        raise ValueError(f"tl.round_to({encoding}): a value is not finite in the format (inf/nan refuse at decode)")
+    return out
 
 
 @dataclass
@@ -70,6 +90,15 @@ class Field:
         ax = self.names.index(name)
         d = self.dims[ax]
         return Field(np.take(self.arr, i - d.start, axis=ax), tuple(x for x in self.dims if x.name != name))
+
+
+def _canon(x: Field, tt: TensorType) -> Field:
+    """``x`` with its axes in its type's dim order (values align by name, so
+    an op that works by axis position first puts the axes where the type has
+    them)."""
+    if not isinstance(x, Field) or x.names == tt.names:
+        return x
+    return Field(x.to_numpy(tt.names), tuple(x.dims[x.names.index(nm)] for nm in tt.names))
 
 
 def field(arr, names) -> Field:
@@ -117,6 +146,8 @@ def run_region(region: Region, values: list):
             ref = next(v for v in vals if isinstance(v, Field))
             arrs = [_as_field(v, ref) for v in vals]
             return Field(np.asarray(_PW[n.attr("f")](*arrs)), ref.dims)
+        if op in ("tl.reduce", "tl.scan") and is_composite(n.attr("f")):
+            return _composite(n, [ev(a) for a in n.args])
         if op == "tl.reduce":
             x = ev(n.args[0])
             dims = n.attr("dims")
@@ -159,7 +190,7 @@ def run_region(region: Region, values: list):
             (d,) = [e for e in n.type.dims if e.name == n.attr("name")]
             return Field(np.broadcast_to(x.arr[..., None], x.arr.shape + (d.size,)), x.dims + (d,))
         if op == "tl.split":
-            x = ev(n.args[0])
+            x = _canon(ev(n.args[0]), n.args[0].type)
             name = n.attr("name")
             ax = x.names.index(name)
             sizes = tuple(int(s) for _, s in n.attr("parts"))
@@ -184,21 +215,23 @@ def run_region(region: Region, values: list):
             coords = np.arange(d.start, d.stop, dtype=np.int64).reshape(shape)
             return Field(np.broadcast_to(coords, tt.shape), tt.dims)
         if op in ("tl.rename", "tl.shift"):  # relabelings: names or frames move, values stay
-            x = ev(n.args[0])
+            x = _canon(ev(n.args[0]), n.args[0].type)
             return Field(x.arr, n.type.dims)
-        if op == "tl.slice":
+        if op == "tl.slice":  # dims matched by name: a value's axis order may differ from its type's
             x = ev(n.args[0])
-            idx = tuple(slice(o.start - d.start, o.stop - d.start) for d, o in zip(x.dims, n.type.dims))
-            return Field(x.arr[idx], n.type.dims)
+            out = tuple(n.type.dim(d.name) for d in x.dims)
+            idx = tuple(slice(o.start - d.start, o.stop - d.start) for d, o in zip(x.dims, out))
+            return Field(x.arr[idx], out)
         if op == "tl.pad":
             x = ev(n.args[0])
-            widths = [(d.start - o.start, o.stop - d.stop) for d, o in zip(x.dims, n.type.dims)]
-            return Field(np.pad(x.arr, widths, constant_values=float(n.attr("fill", 0.0))), n.type.dims)
+            out = tuple(n.type.dim(d.name) for d in x.dims)
+            widths = [(d.start - o.start, o.stop - d.stop) for d, o in zip(x.dims, out)]
+            return Field(np.pad(x.arr, widths, constant_values=float(n.attr("fill", 0.0))), out)
         if op == "tl.flip":
             x = ev(n.args[0])
             return Field(np.flip(x.arr, axis=x.names.index(n.attr("name"))), x.dims)
         if op == "tl.merge":
-            x = ev(n.args[0])
+            x = _canon(ev(n.args[0]), n.args[0].type)
             parts = n.attr("parts")
             parts = (parts,) if isinstance(parts, str) else tuple(parts)
             rest = [nm for nm in x.names if nm not in parts]
@@ -208,7 +241,7 @@ def run_region(region: Region, values: list):
             shp = arr.shape[:at] + (int(np.prod(arr.shape[at:at + len(parts)])),) + arr.shape[at + len(parts):]
             return Field(arr.reshape(shp), n.type.dims)
         if op == "tl.take":
-            table, idx = ev(n.args[0]), ev(n.args[1])
+            table, idx = _canon(ev(n.args[0]), n.args[0].type), _canon(ev(n.args[1]), n.args[1].type)
             dim = n.attr("dim")
             d = table.dims[table.names.index(dim)]
             ia = np.asarray(idx.arr)
@@ -239,6 +272,22 @@ def run_region(region: Region, values: list):
             np.add.at(acc, ia.reshape(-1) - d.start, va)  # duplicates sum, in order
             src = (d.name,) + tuple(rest)
             return Field(np.transpose(acc, [src.index(x.name) for x in n.type.dims]), n.type.dims)
+        if op in ("tl.window", "tl.stencil", "tl.decimate"):
+            return _taps(n, _canon(ev(n.args[0]), n.args[0].type))
+        if op == "tl.diagonal":
+            x = _canon(ev(n.args[0]), n.args[0].type)
+            parts = n.attr("parts")
+            parts = (parts,) if isinstance(parts, str) else tuple(parts)
+            axes = [x.names.index(nm) for nm in parts]
+            z = n.type.dim(n.attr("name"))
+            arr = np.moveaxis(x.arr, axes, range(len(axes)))
+            cz = np.arange(z.start, z.stop)
+            got = arr[tuple(cz - x.dims[ax].start for ax in axes)]  # (z, the other dims in order)
+            at = n.type.names.index(z.name)
+            return Field(np.moveaxis(got, 0, at), n.type.dims)
+        if op == "tl.round_to":
+            x = ev(n.args[0])
+            return Field(round_to(x.arr, n.attr("encoding")), x.dims)
         if op == "tl.const":
             tt = n.type
             return Field(np.full(tt.shape, float(n.attr("value"))), tt.dims)
@@ -265,3 +314,61 @@ def run_region(region: Region, values: list):
         raise NotImplementedError(f"run_region: {op} has no evaluation rule here")
 
     return ev(region.body[-1])
+
+
+def _taps(n: Node, x: Field) -> Field:
+    """tl.window / tl.stencil / tl.decimate: gathers along one dim by an
+    index grid over the output's coordinates (layout.py:700-771,
+    guarded.py:463-520)."""
+    name = n.attr("name")
+    ax = x.names.index(name)
+    d = x.dims[ax]
+    if n.op == "tl.decimate":
+        f = n.attr("factor")
+        j = np.arange(n.type.dim(name).start, n.type.dim(name).stop)
+        idx = f * j + int(n.attr("phase", 0)) % f
+        return Field(np.take(x.arr, idx - d.start, axis=ax), n.type.dims)
+    dil = n.attr("dilation", 1)
+    kn = n.attr("k_name") or f"{name}_k"
+    xo, ko = n.type.dim(name), n.type.dim(kn)
+    idx = np.arange(xo.start, xo.stop)[:, None] + dil * np.arange(ko.start, ko.stop)[None, :]
+    if n.op == "tl.window":  # every tap lands inside by construction
+        return Field(np.take(x.arr, idx - d.start, axis=ax), n.type.dims)
+    live = (idx >= d.start) & (idx < d.stop)
+    got = np.take(x.arr, np.clip(idx - d.start, 0, max(d.size - 1, 0)), axis=ax) if d.size else \
+        np.zeros(x.arr.shape[:ax] + idx.shape + x.arr.shape[ax + 1:])
+    shape = (1,) * ax + live.shape + (1,) * (x.arr.ndim - ax - 1)
+    return Field(np.where(live.reshape(shape), got, float(n.attr("fill", 0.0))), n.type.dims)
+
+
+def _composite(n: Node, vals: list) -> Field:
+    """A composite reducer's sweep along its dim (compute.py:230-260): the
+    first element's lift, then combine(state, lift(element)) in order; a
+    reduce projects the last state (the declared init for an empty dim), a
+    scan each one."""
+    f = lookup(n.attr("f"))
+    dim = n.attr("dim") if n.op == "tl.scan" else ((lambda d: d if isinstance(d, str) else d[0])(n.attr("dims")))
+    tt = n.args[0].type
+    st = minus_dim(tt, dim)
+    P = parts(f, st)
+    d = tt.dim(dim)
+
+    def run(region, xs):
+        r = run_region(region, list(xs))
+        return tuple(r) if isinstance(r, tuple) else (r,)
+
+    order = st.names
+    state, outs = None, []
+    for q in range(d.start, d.stop):
+        lifted = run(P.lift, [v.select(dim, q) for v in vals])
+        state = lifted if state is None else run(P.combine, state + lifted)
+        if n.op == "tl.scan":
+            outs.append(run(P.project, state)[0].to_numpy(order))
+    if n.op == "tl.scan":
+        arr = np.stack(outs, axis=len(order)) if outs else np.zeros(st.shape + (0,))
+        names = order + (dim,)
+        return Field(np.transpose(arr, [names.index(x.name) for x in n.type.dims]), n.type.dims)
+    if state is None:  # an empty dim: the declared identity state
+        state = tuple(Field(np.full(st.shape, v), st.dims) for v in f.init)
+    out = run(P.project, state)[0]
+    return Field(out.to_numpy(n.type.names), n.type.dims)

@@ -17,6 +17,7 @@ import numpy as np
 from .dialect import OPS, check_tier
 from .interp import Field
 from .ir import F64, Builder, Region, minus_dim, tensor_type
+from .reducers import defreducer, exp, maximum
 
 FILL = -1e9
 
@@ -106,6 +107,39 @@ def attention(T=6, S=None, E=3, OD=2, *, mask="causal", artifacts=False, seed=7,
         return (p / p.sum(axis=1, keepdims=True)) @ v
 
     return Subject(region, inputs, oracle)
+
+
+def _flash_combine(left, right):
+    """The online-softmax merge (zoo/attention.py:40-46): both sides rescaled
+    to the joint max; associative."""
+    (ml, dl, ol), (mr, dr, or_) = left, right
+    m = maximum(ml, mr)
+    al, ar = exp(ml - m), exp(mr - m)
+    return m, dl * al + dr * ar, ol * al + or_ * ar
+
+
+# (running max, denominator, weighted sum) over (score, value) elements;
+# init is the identity (exp(-1e30 - m) underflows to 0) (zoo/attention.py:54-62)
+flashsm = defreducer("zoo.flashsm", state=3, element=2, lift=lambda s, v: (s, 1.0, v), combine=_flash_combine,
+                     init=(-1e30, 0.0, 0.0), project=lambda m, den, o: o / den)
+
+
+def flash_attention(T=5, E=3, OD=2, seed=6) -> Subject:
+    """Masked scores fed to the flashsm composite reducer
+    (zoo/attention.py:167-196): sm = where(s <= t, q k^T, -1e9), each score
+    and value repeated onto the (t, s, o) lattice, reduced over s. Same
+    denotation as ``attention(mask="causal")``; the gradient of the reduce
+    is the fold adjoint of its lowering."""
+    nv = attention(T, T, E, OD, mask="causal", seed=seed)
+    b = Builder(OPS)
+    pq, pk, pv = (b.param(i, p.type) for i, p in enumerate(nv.region.params))
+    sc = scores(b, pq, pk)
+    sm = b.emit("tl.pointwise", mask_forest(b, sc, "causal", T, T), sc, _c(b, FILL), f="where")
+    se = b.emit("tl.repeat_like", sm, pv)
+    ve = b.emit("tl.repeat_like", pv, sm)
+    out = b.emit("tl.reduce", se, ve, dims=("s",), f=flashsm.name)
+    region = Region(params=(pq, pk, pv), body=(b.emit("core.yield", out),))
+    return Subject(region, nv.inputs, nv.oracle)
 
 
 def flash_tile(T=6, E=3, OD=2, SI=2, seed=7) -> Subject:

@@ -94,22 +94,18 @@ def test_layernorm_joint_matches_torch_autograd():
 
 
 def test_grad_refuses_what_it_cannot_linearize():
-    # a fold read at its final state differentiates (tests/test_fold_adjoint.py);
-    # an emitting fold used as a value has no adjoint here
+    # folds differentiate, read at their final state or emitting
+    # (tests/test_fold_adjoint.py, tests/test_views_reducers.py); a top-k
+    # selection has no linearization here
     from pdum_dsl_amd.tl.dialect import OPS
-    from pdum_dsl_amd.tl.ir import Builder, Region
-    from tests.test_fold_adjoint import _recurrence
+    from pdum_dsl_amd.tl.ir import Builder, Region, tensor_type
 
-    reg = _recurrence(5, 2)
-    fold = reg.body[-1].args[0]
-    y = fold.regions[0].body[-1].args[0]
-    sb = Builder(OPS)
-    st2 = Region(params=fold.regions[0].params, body=(sb.emit("core.yield", sb.emit("core.tuple", y, y)),))
     b = Builder(OPS)
-    em = b.emit("tl.fold", *fold.args, regions=(st2,), out=("emit",), dim="t", state=("s",), element=("a", "x"))
-    r2 = Region(params=reg.params, body=(b.emit("core.yield", em),))
-    with pytest.raises(NotImplementedError, match="tl.fold"):
-        grad(r2, "out", seed="w", names=region_names(r2, ("a", "s0", "x")))
+    x = b.param(0, tensor_type(("r", "c"), (3, 5)))
+    top = b.emit("tl.argtopk", x, dim="c", k=2, k_name="j")
+    r2 = Region(params=(x,), body=(b.emit("core.yield", top),))
+    with pytest.raises(NotImplementedError, match="tl.argtopk"):
+        grad(r2, "out", seed="w", names=region_names(r2, ("x",)))
     subj = zoo.attention(T=6, E=3, OD=2, seed=7)
     with pytest.raises(ValueError, match="not a scalar"):
         grad(subj.region, "out", names=region_names(subj.region, ("q", "k", "v")))

@@ -302,6 +302,25 @@ def test_a_planned_attention_runs_its_flash_carve(dtype, tol):
     assert np.abs(got - want).max() <= tol * max(1.0, np.abs(want).max())
 
 
+def test_the_flashsm_program_runs_its_flash_carve():
+    """Attention spelled with the flashsm composite reducer: plan_model gives
+    one flash carve and the executor runs it on the flash kernel."""
+    from oracle import closed_forms as cf
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import zoo
+    from pdum_dsl_amd.tl.partition import plan_model
+
+    s = zoo.flash_attention(T=160, E=64, OD=64, seed=8)
+    plan = plan_model(s.region)
+    assert [c.group.template for c in plan.carves] == ["flash"]
+    ex = PlanExecutor(plan, s.region, "f32")
+    vals = s.numpy_inputs()
+    ex.bind(vals)
+    got = ex.run().double().cpu().numpy()
+    want = cf.attention(*vals, scale=1.0, band=(None, 0))[0]
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+
+
 def test_a_planned_flash_joint_runs_forward_and_backward():
     """The joint (out, dq, dk, dv) claimed whole by plan_model runs as the
     forward with artifacts plus the fused backward, against the closed form."""

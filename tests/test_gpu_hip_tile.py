@@ -43,6 +43,19 @@ def test_the_fused_flash_composition_runs_on_hip():
     assert "sweeps=1" in run.source and "stores=1" in run.source and run.grid == 1
 
 
+def test_the_flashsm_reducer_runs_as_the_flash_row():
+    """Attention spelled with the flashsm composite reducer plans as the
+    flash row and runs on the same kernel."""
+    from pdum_dsl_amd.hip_tile import compile_tile_hip
+    from pdum_dsl_amd.tl import fusion, zoo
+
+    f = zoo.flash_attention(T=96, E=16, OD=8, seed=4)
+    (g,) = fusion.plan_region(f.region).groups
+    assert g.template == "flash"
+    got = compile_tile_hip(g.kernel)(f.numpy_inputs())
+    np.testing.assert_allclose(got, f.oracle(f.numpy_inputs()), rtol=1e-4, atol=1e-6)
+
+
 def test_the_hand_written_flash_tile_runs_on_hip():
     from pdum_dsl_amd.hip_tile import compile_tile_hip
     from pdum_dsl_amd.tl import zoo
