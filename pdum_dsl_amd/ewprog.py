@@ -41,25 +41,28 @@ class Lowered:
     operands: tuple  # the node each LOAD slot reads (a leaf, or a view chain over one), slot order
     dims: tuple  # output lattice dims (ir.Dim), outermost first
     bases: tuple = ()  # the leaf under each slot (views peeled)
-    views: tuple = ()  # per slot: (slot dim name -> leaf dim name, leaf dim name -> frame shift)
+    # per slot: leaf dim name -> (coefficients by lattice dim name, constant):
+    # the leaf coordinate as an affine form of the slot's coordinates
+    views: tuple = ()
 
     def operand_view(self, i: int, leaf_strides: dict) -> tuple:
         """(element strides over ``dims``, element offset) at which slot ``i``
         reads its leaf, given the leaf's strides by dim name: lattice index
-        j along dim d reads leaf coordinate d.start + j - shift, i.e. storage
-        index d.start + j - shift - leaf start."""
-        names, shift = self.views[i]
-        leaf = self.bases[i]
-        start = {d.name: d.start for d in leaf.type.dims}
-        strides, off = [], 0
-        for d in self.dims:
-            if d.name in names:
-                b = names[d.name]
-                strides.append(int(leaf_strides[b]))
-                off += (d.start - shift.get(b, 0) - start[b]) * int(leaf_strides[b])
-            else:
-                strides.append(0)
+        j_d along dim d is coordinate d.start + j_d, the leaf coordinate along
+        b is sum_d coef_bd (d.start + j_d) + const_b, and its storage index
+        that minus b's start."""
+        forms = self.views[i]
+        start = {d.name: d.start for d in self.bases[i].type.dims}
+        strides = [sum(cf.get(d.name, 0) * int(leaf_strides[b]) for b, (cf, _c) in forms.items()) for d in self.dims]
+        first = {d.name: d.start for d in self.dims}
+        off = sum((c + sum(v * first[dn] for dn, v in cf.items()) - start[b]) * int(leaf_strides[b])
+                  for b, (cf, c) in forms.items())
         return strides, off
+
+    def offset_reads(self) -> int:
+        """Slots whose reads do not start at their leaf's first element in
+        lattice order (a shifted or strided view)."""
+        return sum(1 for forms in self.views if any(c or list(cf.values()) != [1] for cf, c in forms.values()))
 
     def program(self, out_strides, operand_strides) -> L.EwProgram:
         """The C struct, given the output's and each operand's element
@@ -91,15 +94,17 @@ def _const_value(n):
 def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, allow_views: bool = False) -> Lowered:
     """Lower the chain ending at ``root``. ``leaves`` maps id(node) -> node
     for nodes read with LOAD (slot order = first use). A chain of layout views
-    over a leaf (tl.rename, tl.stage; with ``allow_views`` also tl.shift and
-    tl.slice, whose reads start at an offset the caller applies through
-    ``Lowered.operand_view``) is one LOAD slot: views move no data. ``acc`` is
+    over a leaf (tl.rename, tl.stage; with ``allow_views`` also tl.shift,
+    tl.slice, tl.window, tl.decimate and tl.diagonal: affine views whose
+    offset and strides the caller applies through ``Lowered.operand_view``)
+    is one LOAD slot: views move no data. ``acc`` is
     the node read with ACC (a contraction's fold), if any; ``acc_scale``
     multiplies it (a mean's finalize)."""
     names = tuple(d.name for d in dims)
     order: list = []
     seen: set = set()
-    walkable = ("tl.rename", "tl.stage") + (("tl.shift", "tl.slice") if allow_views else ())
+    walkable = ("tl.rename", "tl.stage") + (
+        ("tl.shift", "tl.slice", "tl.window", "tl.decimate", "tl.diagonal") if allow_views else ())
 
     def base_of(x):
         while x.op in walkable and id(x) not in leaves:
@@ -110,18 +115,34 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, al
         return id(x) in leaves or (x.op in walkable and x.op != "tl.stage" and base_of(x) is not None)
 
     def view_of(x):
-        to_cur = {n: n for n in x.type.names}  # slot name -> name in the current frame
-        shift: dict = {}  # current-frame name -> accumulated frame shift
+        """Each dim of the frame being walked, as an affine form (coefficients
+        over the slot's dims, constant), from the slot down to its leaf."""
+        cur = {n: ({n: 1}, 0) for n in x.type.names}
         while id(x) not in leaves:
-            if x.op == "tl.shift":
-                for nm, dl in x.attr("deltas"):
-                    shift[nm] = shift.get(nm, 0) + int(dl)
+            if x.op == "tl.shift":  # in = out - delta
+                deltas = dict(x.attr("deltas"))
+                cur = {nm: (cf, c - int(deltas.get(nm, 0))) for nm, (cf, c) in cur.items()}
             elif x.op == "tl.rename":
                 inv = {new: old for old, new in x.attr("mapping")}
-                to_cur = {k: inv.get(v, v) for k, v in to_cur.items()}
-                shift = {inv.get(k, k): v for k, v in shift.items()}
-            x = x.args[0]
-        return to_cur, shift
+                cur = {inv.get(nm, nm): v for nm, v in cur.items()}
+            elif x.op == "tl.window":  # in[x] = out[x] + dilation out[k]
+                nm, dil = x.attr("name"), int(x.attr("dilation", 1))
+                (cx, c0), (ck, c1) = cur.pop(nm), cur.pop(x.attr("k_name"))
+                cf = dict(cx)
+                for k, v in ck.items():
+                    cf[k] = cf.get(k, 0) + dil * v
+                cur[nm] = (cf, c0 + dil * c1)
+            elif x.op == "tl.decimate":  # in[x] = factor out[x] + phase
+                nm, f = x.attr("name"), int(x.attr("factor"))
+                cx, c0 = cur[nm]
+                cur[nm] = ({k: f * v for k, v in cx.items()}, f * c0 + int(x.attr("phase", 0)) % f)
+            elif x.op == "tl.diagonal":  # every part reads the diagonal's coordinate
+                parts = x.attr("parts")
+                e = cur.pop(x.attr("name"))
+                for pn in ((parts,) if isinstance(parts, str) else tuple(parts)):
+                    cur[pn] = e
+            x = x.args[0]  # tl.slice / tl.stage: the same coordinates
+        return cur
 
     def visit(n):  # post-order over the chain, stopping at leaves
         stack = [(n, False)]

@@ -488,7 +488,7 @@ def _flash_joint_runner(region, fj, grid, dtype):
 # ------------------------------------------- map-chain and contraction-epilogue
 
 _CHAIN_OPS = {"core.param", "core.yield", "core.const", "tl.const", "tl.iota", "tl.pointwise", "tl.repeat_like",
-              "tl.repeat", "tl.stage", "tl.rename", "tl.shift", "tl.slice"}
+              "tl.repeat", "tl.stage", "tl.rename", "tl.shift", "tl.slice", "tl.window", "tl.decimate", "tl.diagonal"}
 _TORCH_DT = {"f32": "float32", "bf16": "bfloat16", "f16": "float16"}
 
 
@@ -526,7 +526,7 @@ def _map_chain_runner(region, grid, dtype):
         raise Untranslatable(f"map-chain: {exc}") from None
     idx = [_index(region, p) for p in low.bases]
     out_names = y.type.names
-    shifted = sum(1 for _names, sh in low.views if any(sh.values()))
+    shifted = low.offset_reads()
 
     def dev(ts):
         torch = _torch()

@@ -527,8 +527,8 @@ OPS: dict[str, OpDef] = {
 }
 
 # ops no template row reads: a region holding one plans it red
-TILE_OPS = frozenset(OPS) - {"tl.argtopk", "tl.take", "tl.scatter_add", "tl.pad", "tl.flip", "tl.merge", "tl.window",
-                             "tl.stencil", "tl.decimate", "tl.diagonal", "tl.round_to"}
+TILE_OPS = frozenset(OPS) - {"tl.argtopk", "tl.take", "tl.scatter_add", "tl.pad", "tl.flip", "tl.merge", "tl.stencil",
+                             "tl.round_to"}
 
 
 def builder() -> Builder:

@@ -42,8 +42,8 @@ from .launch import fit_affine, propose, tri_eval
 
 _MAP_OPS = frozenset(
     {"core.param", "core.const", "core.yield", "tl.pointwise", "tl.iota", "tl.const", "tl.select", "tl.split",
-     "tl.repeat", "tl.repeat_like", "tl.rename", "tl.shift", "tl.slice"}
-)
+     "tl.repeat", "tl.repeat_like", "tl.rename", "tl.shift", "tl.slice", "tl.window", "tl.decimate", "tl.diagonal"}
+)  # the affine views read in place (tl.stencil's fill needs a guarded read: it stays red)
 _EXACT_OPS = frozenset({"tl.pointwise", "tl.repeat_like", "tl.rename", "tl.repeat", "tl.iota", "core.const",
                         "tl.const"})
 

@@ -302,6 +302,26 @@ def test_a_planned_attention_runs_its_flash_carve(dtype, tol):
     assert np.abs(got - want).max() <= tol * max(1.0, np.abs(want).max())
 
 
+def test_window_decimate_diagonal_views_run_in_a_map_chain():
+    """A map chain over window / decimate / diagonal views reads them in
+    place (strides and offsets over the stored tensors) on the device."""
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import interp
+    from pdum_dsl_amd.tl.partition import plan_model
+    from tests.test_views_reducers import _affine_region
+
+    r = _affine_region()
+    plan = plan_model(r)
+    assert {c.group.template for c in plan.carves} == {"map-chain"}
+    rng = np.random.default_rng(14)
+    X, Y = rng.standard_normal((3, 30)), rng.standard_normal((12, 3, 14))
+    want = interp.run_region(r, [interp.Field(X, r.params[0].type.dims), interp.Field(Y, r.params[1].type.dims)])
+    ex = PlanExecutor(plan, r, "f32")
+    ex.bind([X, Y])
+    got = ex.run().double().cpu().numpy()
+    np.testing.assert_allclose(got, want.to_numpy(r.body[-1].args[0].type.names), rtol=1e-6, atol=1e-6)
+
+
 def test_the_flashsm_program_runs_its_flash_carve():
     """Attention spelled with the flashsm composite reducer: plan_model gives
     one flash carve and the executor runs it on the flash kernel."""

@@ -56,6 +56,21 @@ def test_the_flashsm_reducer_runs_as_the_flash_row():
     np.testing.assert_allclose(got, f.oracle(f.numpy_inputs()), rtol=1e-4, atol=1e-6)
 
 
+def test_affine_views_run_on_the_map_chain_seat():
+    from pdum_dsl_amd.hip_tile import compile_tile_hip
+    from pdum_dsl_amd.tl import fusion, interp
+    from tests.test_views_reducers import _affine_region
+
+    r = _affine_region()
+    (g,) = fusion.plan_region(r).groups
+    rng = np.random.default_rng(15)
+    X, Y = rng.standard_normal((3, 30)), rng.standard_normal((12, 3, 14))
+    run = compile_tile_hip(g.kernel)
+    want = interp.run_region(r, [interp.Field(X, r.params[0].type.dims), interp.Field(Y, r.params[1].type.dims)])
+    np.testing.assert_allclose(run([X, Y]), want.to_numpy(r.body[-1].args[0].type.names), rtol=1e-5, atol=1e-6)
+    assert "shifted_reads=3" in run.source
+
+
 def test_the_hand_written_flash_tile_runs_on_hip():
     from pdum_dsl_amd.hip_tile import compile_tile_hip
     from pdum_dsl_amd.tl import zoo

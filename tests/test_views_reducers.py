@@ -74,8 +74,10 @@ def test_view_types():
         b.emit("tl.diagonal", y, parts=("a",), name="z")
     with pytest.raises(TypeError, match="unknown encoding"):
         b.emit("tl.round_to", x, encoding="fp8")
+    # the views are tile vocabulary (the reference's LAYOUT family); round_to is not
+    check_tier(Region(params=(x,), body=(b.emit("core.yield", w),)))
     with pytest.raises(ValueError, match="host citizen"):
-        check_tier(Region(params=(x,), body=(b.emit("core.yield", w),)))
+        check_tier(Region(params=(x,), body=(b.emit("core.yield", b.emit("tl.round_to", x, encoding="bf16")),)))
 
 
 # ------------------------------------------------------------- evaluation
@@ -339,3 +341,53 @@ def test_the_flashsm_program_is_claimed_by_the_flash_row():
     y = sj.region.body[-1].args[0]
     alt = b.emit("tl.reduce", *y.args, dims=("s",), f=other.name)
     assert match_flash(Region(params=sj.region.params, body=(b.emit("core.yield", alt),))) is None
+
+
+def _affine_region():
+    """sin(window(x)) * decimate(shift(x)) + diagonal(y), over one lattice."""
+    b = Builder(OPS)
+    px = b.param(0, tensor_type(("r", "x"), (3, 30)))
+    py = b.param(1, tensor_type(("p", "r", "q"), (12, 3, 14)))
+    w = b.emit("tl.window", px, name="x", k_name="j", k=(-1, 3), dilation=2)  # x in [2, 26), j in [-1, 3)
+    w = b.emit("tl.slice", w, ranges=(("x", (4, 12)),))
+    d = b.emit("tl.decimate", b.emit("tl.shift", px, deltas=(("x", 5),)), name="x", factor=3, phase=2)  # x in [1, 11)
+    d = b.emit("tl.slice", d, ranges=(("x", (4, 10)),))
+    d = b.emit("tl.shift", d, deltas=(("x", 2),))  # [6, 12)
+    d = b.emit("tl.slice", d, ranges=(("x", (6, 12)),))
+    dg = b.emit("tl.diagonal", b.emit("tl.shift", py, deltas=(("q", -2),)), parts=("q", "p"), name="x")  # [0, 12)
+    dg = b.emit("tl.rename", b.emit("tl.slice", dg, ranges=(("x", (6, 12)),)), mapping=(("r", "r"),))
+    sw = b.emit("tl.slice", w, ranges=(("x", (6, 12)),))
+    y = b.emit("tl.pointwise", b.emit("tl.pointwise", sw, f="sin"), b.emit("tl.repeat_like", d, sw), f="mul")
+    y = b.emit("tl.pointwise", y, b.emit("tl.repeat_like", dg, sw), f="add")
+    return Region(params=(px, py), body=(b.emit("core.yield", y),))
+
+
+def test_affine_views_lower_to_strided_reads():
+    """The elementwise program reads window / decimate / diagonal views in
+    place: each slot's (strides, offset) over the stored tensor, applied as
+    an as_strided view, gives the interpreter's values of that slot."""
+    from numpy.lib.stride_tricks import as_strided
+
+    from pdum_dsl_amd import ewprog
+    from pdum_dsl_amd.tl.fusion import plan_region
+
+    r = _affine_region()
+    rng = np.random.default_rng(13)
+    X, Y = rng.standard_normal((3, 30)), rng.standard_normal((12, 3, 14))
+    y = r.body[-1].args[0]
+    low = ewprog.lower(y, y.type.dims, {id(p): p for p in r.params}, allow_views=True)
+    assert low.offset_reads() == len(low.operands) == 3
+    store = {id(r.params[0]): X, id(r.params[1]): Y}
+    for j, (slot, base) in enumerate(zip(low.operands, low.bases)):
+        arr = store[id(base)]
+        st, off = low.operand_view(j, dict(zip(base.type.names, (s // 8 for s in arr.strides))))
+        assert off >= 0
+        flat = np.ascontiguousarray(arr).reshape(-1)
+        got = as_strided(flat[off:], shape=y.type.shape, strides=[8 * s for s in st])
+        sub = Region(params=r.params, body=(Builder(OPS).emit("core.yield", slot),))
+        want = interp.run_region(sub, [interp.Field(X, r.params[0].type.dims), interp.Field(Y, r.params[1].type.dims)])
+        want = np.broadcast_to(want.to_numpy(tuple(n for n in y.type.names if n in want.names)).reshape(
+            [y.type.dim(n).size if n in want.names else 1 for n in y.type.names]), y.type.shape)
+        np.testing.assert_array_equal(got, want)
+    (g,) = plan_region(r).groups
+    assert (g.template, g.confidence) == ("map-chain", "yellow")
