@@ -95,7 +95,7 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, al
     """Lower the chain ending at ``root``. ``leaves`` maps id(node) -> node
     for nodes read with LOAD (slot order = first use). A chain of layout views
     over a leaf (tl.rename, tl.stage; with ``allow_views`` also tl.shift,
-    tl.slice, tl.window, tl.decimate and tl.diagonal: affine views whose
+    tl.slice, tl.select, tl.window, tl.decimate and tl.diagonal: affine views whose
     offset and strides the caller applies through ``Lowered.operand_view``)
     is one LOAD slot: views move no data. ``acc`` is
     the node read with ACC (a contraction's fold), if any; ``acc_scale``
@@ -104,7 +104,7 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, al
     order: list = []
     seen: set = set()
     walkable = ("tl.rename", "tl.stage") + (
-        ("tl.shift", "tl.slice", "tl.window", "tl.decimate", "tl.diagonal") if allow_views else ())
+        ("tl.shift", "tl.slice", "tl.select", "tl.window", "tl.decimate", "tl.diagonal") if allow_views else ())
 
     def base_of(x):
         while x.op in walkable and id(x) not in leaves:
@@ -136,6 +136,9 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, al
                 nm, f = x.attr("name"), int(x.attr("factor"))
                 cx, c0 = cur[nm]
                 cur[nm] = ({k: f * v for k, v in cx.items()}, f * c0 + int(x.attr("phase", 0)) % f)
+            elif x.op == "tl.select":  # the fixed dims read one coordinate
+                for nm, i in x.attr("coords"):
+                    cur[nm] = ({}, int(i))
             elif x.op == "tl.diagonal":  # every part reads the diagonal's coordinate
                 parts = x.attr("parts")
                 e = cur.pop(x.attr("name"))

@@ -180,6 +180,42 @@ def _holds_reduce(node) -> bool:
     return False
 
 
+def _stencils_as_windows(k: Region) -> Region:
+    """The carve with every tl.stencil written as a window over a pad of its
+    operand: stencil(x)[c, j] = x[c + dil j] inside x's domain, else the fill,
+    is window(pad(x, fill))[c, j] over a pad wide enough for every tap, cut
+    back to x's domain. Same values; the pads then materialize like any
+    other and the window is read in place."""
+    b = Builder(OPS)
+    memo: dict = {id(p): p for p in k.params}
+
+    def go(n):
+        if id(n) in memo:
+            return memo[id(n)]
+        args = tuple(go(a) for a in n.args)
+        if n.op == "tl.stencil":
+            (x,) = args
+            name, dil = n.attr("name"), int(n.attr("dilation", 1))
+            kmin, kmax = (int(v) for v in n.attr("k"))
+            d = x.type.dim(name)
+            lo, hi = min(d.start, d.start + dil * kmin), max(d.stop, d.stop + dil * kmax)
+            pad = b.emit("tl.pad", x, extents=((name, (lo, hi)),), fill=float(n.attr("fill", 0.0)))
+            out = b.emit("tl.window", pad, name=name, k_name=n.attr("k_name") or f"{name}_k", k=(kmin, kmax + 1),
+                         dilation=dil)
+            od = out.type.dim(name)
+            if (od.start, od.stop) != (d.start, d.stop):
+                out = b.emit("tl.slice", out, ranges=((name, (d.start, d.stop)),))
+        elif all(x is y for x, y in zip(args, n.args)):
+            out = n
+        else:
+            explicit = {} if OPS[n.op].type_rule is not None else {"type": n.type}
+            out = b.emit(n.op, *args, regions=n.regions, loc=n.loc, **explicit, **dict(n.attrs))
+        memo[id(n)] = out
+        return out
+
+    return Region(params=k.params, body=(go(k.body[-1]),))
+
+
 def _yielding(k: Region, node) -> Region:
     """The region over k's params that yields ``node``."""
     return Region(params=k.params, body=(Builder(OPS).emit("core.yield", node),))
@@ -523,9 +559,10 @@ class PlanExecutor:
             run, src = self._scatter(k)
         elif carve.group.confidence == "red" and any(n.op == "tl.take" for n in walk(k)):
             run, src = self._take(k)
-        elif carve.group.confidence == "red" and any(n.op == "tl.pad" for n in walk(k)):
-            # zero-padded views (a stencil's adjoint): the pads materialized, then one map chain
-            run, src = self._padded(k)
+        elif carve.group.confidence == "red" and any(n.op in ("tl.pad", "tl.stencil") for n in walk(k)):
+            # padded views (a stencil's adjoint; a tl.stencil, as a window over a pad of its
+            # fill): the pads materialized, then one map chain
+            run, src = self._padded(_stencils_as_windows(k))
         elif carve.group.confidence == "red" and any(n.op == "tl.scan" for n in walk(k)):
             # the first-occurrence max / min adjoint's prefix count: pdh_scan
             run, src = self._scan(k)
@@ -785,16 +822,30 @@ class PlanExecutor:
         operand's chain written into the interior by a map chain whose output
         view starts at the operand's frame. The carve's value is then one map
         chain reading the pad buffers through their shifted / sliced views
-        (in-bounds offset reads, as a stencil reads its halo)."""
+        (in-bounds offset reads, as a stencil reads its halo). A value that
+        a view reads and that is computed inside the carve (a tap's slice of
+        a cotangent) is materialized the same way first, densely."""
         y = k.body[-1].args[0]
         if y.op == "core.tuple" or not y.type.names:
             raise Untranslatable("a padded carve with one tensor output")
-        pads, seen, stack = [], set(), [(y, False)]
-        while stack:  # post-order: a pad after the pads inside its operand
+        views = ("tl.shift", "tl.slice", "tl.select", "tl.window", "tl.decimate", "tl.diagonal", "tl.rename", "tl.stage")
+
+        def under_views(n):
+            while n.op in views:
+                n = n.args[0]
+            return n
+
+        pads, seen, stack, mats = [], set(), [(y, False)], set()
+        while stack:  # post-order: a pad (or a viewed value) after those inside its operand
             n, done = stack.pop()
             if done:
                 if n.op == "tl.pad":
                     pads.append(n)
+                elif n.op in views[:6]:
+                    base = under_views(n)
+                    if base.op not in ("core.param", "tl.pad") and id(base) not in mats:
+                        mats.add(id(base))
+                        pads.append(base)
                 continue
             if id(n) in seen or not hasattr(n, "op") or n.op == "core.param":
                 continue
@@ -821,8 +872,12 @@ class PlanExecutor:
             return low.program(out_st, [st for st, _o in views]), slots, [o for _s, o in views], out_off, len(low.insns)
 
         for pad in pads:
-            x = pad.args[0]
             pst = _strides_by_name(pad.type.names, pad.type.shape)
+            if pad.op != "tl.pad":  # a viewed value, written densely
+                plans.append((pad, chain(pad, pad.type.dims, [pst[d.name] for d in pad.type.dims], 0)))
+                leaves[id(pad)] = pad
+                continue
+            x = pad.args[0]
             off = sum((x.type.dim(nm).start - pad.type.dim(nm).start) * pst[nm] for nm in x.type.names)
             plans.append((pad, chain(x, x.type.dims, [pst[d.name] for d in x.type.dims], off)))
             leaves[id(pad)] = pad
@@ -841,7 +896,10 @@ class PlanExecutor:
                 return t.reshape(-1)[o:]
 
             for pad, (prog, slots, offs, out_off, _n) in plans:
-                buf = torch.full(pad.type.shape, float(pad.attr("fill")), device="cuda", dtype=dt)
+                if pad.op == "tl.pad":
+                    buf = torch.full(pad.type.shape, float(pad.attr("fill")), device="cuda", dtype=dt)
+                else:
+                    buf = torch.empty(pad.type.shape, device="cuda", dtype=dt)
                 K.map_chain(prog, [operand(sl, o) for sl, o in zip(slots, offs)], buf.reshape(-1)[out_off:])
                 bufs[id(pad)] = buf
             prog, slots, offs, _o, _n = final

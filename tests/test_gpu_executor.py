@@ -322,6 +322,36 @@ def test_window_decimate_diagonal_views_run_in_a_map_chain():
     np.testing.assert_allclose(got, want.to_numpy(r.body[-1].args[0].type.names), rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("k,dil", [((-2, 1), 1), ((1, 3), 2)])
+def test_a_stencil_and_its_joint_run_on_the_device(k, dil):
+    """tl.stencil plans red; the executor runs it as a window over a pad of
+    its fill, and its joint (the taps' cotangents shifted back, padded) the
+    same way."""
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import interp
+    from pdum_dsl_amd.tl.autodiff import grad, region_names
+    from pdum_dsl_amd.tl.partition import plan_model
+    from tests.test_views_reducers import _stencil_region
+
+    r = _stencil_region(k, dil)
+    rng = np.random.default_rng(17)
+    X = rng.standard_normal((3, 40))
+    want = interp.run_region(r, [interp.field(X, ("r", "x"))])
+    ex = PlanExecutor(plan_model(r), r, "f32")
+    ex.bind([X])
+    got = ex.run().double().cpu().numpy()
+    np.testing.assert_allclose(got, want.to_numpy(r.body[-1].args[0].type.names), rtol=1e-6, atol=1e-7)
+    rg = grad(r, "out", seed="dy", names=region_names(r, ("x",)))
+    out_t = r.body[-1].args[0].type
+    dy = rng.standard_normal(out_t.shape)
+    wj = interp.run_region(rg.region, [interp.field(X, ("r", "x")), interp.Field(dy, out_t.dims)])
+    ej = PlanExecutor(plan_model(rg.region), rg.region, "f32")
+    ej.bind([X, dy])
+    gx = ej.run()[1].double().cpu().numpy()
+    np.testing.assert_allclose(gx, wj[1].to_numpy(rg.region.body[-1].args[0].args[1].type.names), rtol=1e-5,
+                               atol=1e-6)
+
+
 def test_the_flashsm_program_runs_its_flash_carve():
     """Attention spelled with the flashsm composite reducer: plan_model gives
     one flash carve and the executor runs it on the flash kernel."""

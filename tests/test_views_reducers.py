@@ -391,3 +391,25 @@ def test_affine_views_lower_to_strided_reads():
         np.testing.assert_array_equal(got, want)
     (g,) = plan_region(r).groups
     assert (g.template, g.confidence) == ("map-chain", "yellow")
+
+
+def _stencil_region(k, dil, fill=0.5):
+    b = Builder(OPS)
+    x = b.param(0, tensor_type(("r", "x"), (3, 40)))
+    st = b.emit("tl.stencil", x, name="x", k=k, fill=fill, dilation=dil)
+    return Region(params=(x,), body=(b.emit("core.yield", b.emit("tl.pointwise", st, f="exp")),))
+
+
+@pytest.mark.parametrize("k,dil", [((-2, 1), 1), ((1, 3), 2), ((-3, -1), 3), ((0, 0), 1)])
+def test_a_stencil_is_a_window_over_a_pad(k, dil):
+    """The executor's device form of tl.stencil: a window over a pad of the
+    fill, cut back to the domain. Bit-equal on the interpreter."""
+    from pdum_dsl_amd.executor import _stencils_as_windows
+
+    r = _stencil_region(k, dil)
+    X = np.random.default_rng(16).standard_normal((3, 40))
+    r2 = _stencils_as_windows(r)
+    assert not any(n.op == "tl.stencil" for n in walk(r2))
+    a = interp.run_region(r, [interp.field(X, ("r", "x"))]).to_numpy(("r", "x", "x_k"))
+    b2 = interp.run_region(r2, [interp.field(X, ("r", "x"))]).to_numpy(("r", "x", "x_k"))
+    np.testing.assert_array_equal(a, b2)
