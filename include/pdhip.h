@@ -268,6 +268,7 @@ enum pdh_ew_op {
   PDH_EW_ADD, PDH_EW_SUB, PDH_EW_MUL, PDH_EW_DIV, PDH_EW_MAX, PDH_EW_MIN,
   PDH_EW_EQ, PDH_EW_NE, PDH_EW_LT, PDH_EW_LE, PDH_EW_GT, PDH_EW_GE,
   PDH_EW_WHERE,
+  PDH_EW_RBF16, PDH_EW_RF16, /* round to the nearest bf16 / f16 value (ties to even) and back: tl.round_to */
   PDH_EW_NOPS
 };
 

@@ -81,7 +81,7 @@ class AttnGeom(C.Structure):
 EW_MAX_INSNS, EW_MAX_REGS, EW_MAX_OPERANDS, EW_MAX_DIMS = 64, 16, 8, 4
 EW_OPS = (
     "LOAD ACC CONST IOTA NEG EXP LOG SQRT TANH SIN COS ABS FLOOR ADD SUB MUL DIV MAX MIN "
-    "EQ NE LT LE GT GE WHERE"
+    "EQ NE LT LE GT GE WHERE RBF16 RF16"
 ).split()
 EW = {name: i for i, name in enumerate(EW_OPS)}
 

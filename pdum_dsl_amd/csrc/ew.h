@@ -128,6 +128,8 @@ __device__ __forceinline__ void ew_run(const pdh_ew_program& p, const EwOperands
       PDH_EW_CASE(PDH_EW_LE, a_ <= b_ ? 1.f : 0.f)
       PDH_EW_CASE(PDH_EW_GT, a_ > b_ ? 1.f : 0.f)
       PDH_EW_CASE(PDH_EW_GE, a_ >= b_ ? 1.f : 0.f)
+      PDH_EW_CASE(PDH_EW_RBF16, bf16_to_f32(f32_to_bf16(a_)))
+      PDH_EW_CASE(PDH_EW_RF16, f16_to_f32(f32_to_f16(a_)))
 #undef PDH_EW_CASE
       default:  // PDH_EW_WHERE
 #pragma unroll

@@ -160,7 +160,7 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, al
             stack.append((x, True))
             if is_leaf(x) or (acc is not None and x is acc):
                 continue
-            if x.op in _VIEW:
+            if x.op in _VIEW or x.op == "tl.round_to":
                 stack.append((x.args[0], False))
             elif x.op == "tl.pointwise":
                 for a in reversed(x.args):
@@ -175,7 +175,7 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, al
 
     uses: dict[int, int] = {}
     for x in order:
-        if x.op == "tl.pointwise" and not is_leaf(x) and x is not acc:
+        if x.op in ("tl.pointwise", "tl.round_to") and not is_leaf(x) and x is not acc:
             for a in x.args:
                 a = skip_view(a)
                 uses[id(a)] = uses.get(id(a), 0) + 1
@@ -222,6 +222,14 @@ def lower(root, dims, leaves: dict, acc=None, acc_scale: float | None = None, al
         elif _const_value(x) is not None:
             r = alloc()
             insns.append(("CONST", r, 0, 0, 0, _const_value(x)))
+        elif x.op == "tl.round_to":  # encode-then-decode; fp32 values already are f32
+            src = skip_view(x.args[0])
+            xr = reg[id(src)]
+            release(src)
+            r = alloc()
+            enc = x.attr("encoding")
+            insns.append(("MAX", r, xr, xr, 0, 0.0) if enc == "f32" else (("RBF16" if enc == "bf16" else "RF16"), r, xr,
+                                                                          0, 0, 0.0))
         elif x.op == "tl.iota":
             nm = x.attr("name")
             if nm not in names:

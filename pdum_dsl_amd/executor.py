@@ -563,6 +563,9 @@ class PlanExecutor:
             # padded views (a stencil's adjoint; a tl.stencil, as a window over a pad of its
             # fill): the pads materialized, then one map chain
             run, src = self._padded(_stencils_as_windows(k))
+        elif carve.group.confidence == "red" and any(n.op == "tl.round_to" for n in walk(k)):
+            # the precision op (compute vocabulary, so red): one map chain with its round trip
+            run, src = self._map_chain(k)
         elif carve.group.confidence == "red" and any(n.op == "tl.scan" for n in walk(k)):
             # the first-occurrence max / min adjoint's prefix count: pdh_scan
             run, src = self._scan(k)

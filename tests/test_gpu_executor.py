@@ -352,6 +352,28 @@ def test_a_stencil_and_its_joint_run_on_the_device(k, dil):
                                atol=1e-6)
 
 
+@pytest.mark.parametrize("enc", ["bf16", "f16", "f32"])
+def test_round_to_runs_as_a_map_chain(enc):
+    """round_to plans red (compute vocabulary); the executor runs its carve
+    as one map chain with the hardware round trip. On float32 values the
+    device's rounding is the interpreter's exactly."""
+    from pdum_dsl_amd.executor import PlanExecutor
+    from pdum_dsl_amd.tl import interp
+    from pdum_dsl_amd.tl.partition import plan_model
+    from tests.test_views_reducers import _round_region
+
+    r = _round_region(enc)
+    X = np.random.default_rng(18).standard_normal((64, 96)).astype(np.float32).astype(np.float64)
+    plan = plan_model(r)
+    ex = PlanExecutor(plan, r, "f32")
+    ex.bind([X])
+    got = ex.run().cpu().numpy()
+    # the interpreter on the device's float32 square, rounded, plus x in float32
+    sq = (X.astype(np.float32) * X.astype(np.float32)).astype(np.float64)
+    want = (interp.round_to(sq, enc).astype(np.float32) + X.astype(np.float32))
+    np.testing.assert_array_equal(got, want)
+
+
 def test_the_flashsm_program_runs_its_flash_carve():
     """Attention spelled with the flashsm composite reducer: plan_model gives
     one flash carve and the executor runs it on the flash kernel."""
