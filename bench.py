@@ -271,7 +271,7 @@ def _c1_line(torch, K, cf, h, dev, g):
     return {
         "config": "C1 B=1 H=1 S=256 D=64 non-causal fp32", "ms": round(ms, 5), "TFLOP/s": round(fl / ms / 1e9, 3),
         "algorithmic_flop": fl, "max_abs_err": err,
-        "note": "one head: 4 query blocks on a 256-CU chip, launch-latency bound by construction",
+        "note": "one head: 4 query workgroups on a 256-CU chip, latency-bound by construction",
     }
 
 

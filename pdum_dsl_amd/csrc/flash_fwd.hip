@@ -610,19 +610,21 @@ __global__ __launch_bounds__(256) void flash_fwd_generic_f32(GenArgs a, int64_t 
 // every lane, so they are read as wave-uniform (scalar) loads and each lane
 // runs its own row's recurrence with no cross-lane reduction; eight keys per
 // step give eight independent score chains. The groups of eight keys (on the
-// absolute key grid) go round-robin to the four waves, each sweeping its
+// absolute key grid) go round-robin to the NW waves, each sweeping its
 // groups in order over the workgroup's key range (the union of its rows'
-// ranges), and the four partial states (m, l, o) merge through LDS with the
-// associative combine (zoo/attention.py:40-46). Each row keeps the generic
+// ranges), and the NW partial states (m, l, o) merge through LDS with the
+// associative combine (zoo/attention.py:40-46). Grids that fill the chip run
+// four waves a workgroup; smaller ones eight, which halves each wave's serial
+// sweep (the scalar K / V reads are latency-bound). Each row keeps the generic
 // kernel's semantics: with pruning it sees exactly the 64-key chunks the band
 // leaves it, a masked score inside them is the fill, and keys past s take no
 // part. A group the prune skips holds only fill scores, whose exponentials
 // vanish against the row's live maximum, and the assignment of groups to
 // waves does not move with the range: pruned and unpruned sweeps agree bit
 // for bit.
-template <int E, int OD>
-__global__ __launch_bounds__(256) void flash_fwd_rows_f32(GenArgs a, int nqb) {
-  __shared__ float part[3][OD + 2][64];  // waves 1..3: o[0..OD), m, l per lane
+template <int E, int OD, int NW>
+__global__ __launch_bounds__(64 * NW) void flash_fwd_rows_f32(GenArgs a, int nqb) {
+  __shared__ float part[NW - 1][OD + 2][64];  // waves 1..NW-1: o[0..OD), m, l per lane
   const int lane = threadIdx.x & 63, w = wave_id();
   const int64_t inst = blockIdx.x / nqb;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x % nqb) * 64;
@@ -657,9 +659,9 @@ __global__ __launch_bounds__(256) void flash_fwd_rows_f32(GenArgs a, int nqb) {
   chunks((row0 + 63 < a.t ? row0 + 63 : a.t - 1), tmp, bhi);
   const int64_t klo = blo * 64, khi = (bhi * 64 < a.s ? bhi * 64 : a.s);  // keys of the workgroup
   const int64_t kr_lo = rlo * 64, kr_hi = rhi * 64;                       // keys of this row
-  // this wave's groups of eight keys: k0 = 8 g for g = w (mod 4) in the range
+  // this wave's groups of eight keys: k0 = 8 g for g = w (mod NW) in the range
   const int64_t gfirst = klo / 8, glast = (khi + 7) / 8;  // klo is a multiple of 64
-  const int64_t g0 = gfirst + ((w - gfirst % 4) + 4) % 4;
+  const int64_t g0 = gfirst + ((w - gfirst % NW) + NW) % NW;
 
   float q[E];
 #pragma unroll
@@ -668,7 +670,7 @@ __global__ __launch_bounds__(256) void flash_fwd_rows_f32(GenArgs a, int nqb) {
 #pragma unroll
   for (int f = 0; f < OD; ++f) acc[f] = 0.f;
 
-  for (int64_t g = g0; g < glast; g += 4) {
+  for (int64_t g = g0; g < glast; g += NW) {
     const int64_t k0 = 8 * g;
     // the step's eight K and V rows (wave-uniform; a key past the range reads
     // the last one and is excluded below)
@@ -719,7 +721,7 @@ __global__ __launch_bounds__(256) void flash_fwd_rows_f32(GenArgs a, int nqb) {
     }
   }
 
-  // merge: waves 1..3 publish, wave 0 combines and stores
+  // merge: waves 1..NW-1 publish, wave 0 combines and stores
   if (w > 0) {
     float (*pw)[64] = part[w - 1];
 #pragma unroll
@@ -729,19 +731,19 @@ __global__ __launch_bounds__(256) void flash_fwd_rows_f32(GenArgs a, int nqb) {
   }
   __syncthreads();
   if (w != 0) return;
-  float mw[3], M = m;
+  float mw[NW - 1], M = m;
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
+  for (int i = 0; i < NW - 1; ++i) {
     mw[i] = part[i][OD][lane];
     M = fmaxf(M, mw[i]);
   }
-  float wt[4];
+  float wt[NW];
   wt[0] = m == -kInf ? 0.f : __expf(m - M);
 #pragma unroll
-  for (int i = 0; i < 3; ++i) wt[i + 1] = mw[i] == -kInf ? 0.f : __expf(mw[i] - M);
+  for (int i = 0; i < NW - 1; ++i) wt[i + 1] = mw[i] == -kInf ? 0.f : __expf(mw[i] - M);
   float L = l * wt[0];
 #pragma unroll
-  for (int i = 0; i < 3; ++i) L += part[i][OD + 1][lane] * wt[i + 1];
+  for (int i = 0; i < NW - 1; ++i) L += part[i][OD + 1][lane] * wt[i + 1];
   if (!rin) return;
   const float inv = 1.0f / L;
   float* orow = a.o + b * a.o_sb + hq * a.o_sh + t * a.o_st;
@@ -749,7 +751,7 @@ __global__ __launch_bounds__(256) void flash_fwd_rows_f32(GenArgs a, int nqb) {
   for (int f = 0; f < OD; ++f) {
     float v = acc[f] * wt[0];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) v += part[i][f][lane] * wt[i + 1];
+    for (int i = 0; i < NW - 1; ++i) v += part[i][f][lane] * wt[i + 1];
     orow[f] = v * inv;
   }
   const int64_t grow = inst * a.t + t;
@@ -884,10 +886,16 @@ int flash_fwd_impl(const void* q, const void* k, const void* v, void* o, float* 
       const int64_t nqb = (G.t + 63) / 64;
       PDH_REQUIRE(ninst * nqb <= INT32_MAX && nqb <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: too many rows");
       const dim3 grid(static_cast<unsigned>(ninst * nqb));
-      if (G.e == 64)
-        flash_fwd_rows_f32<64, 64><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
+      const int cus = pdh_device_cus();
+      const bool small = ninst * nqb < (cus > 0 ? cus : 256);  // under one workgroup per compute unit
+      if (G.e == 64 && small)
+        flash_fwd_rows_f32<64, 64, 8><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
+      else if (G.e == 64)
+        flash_fwd_rows_f32<64, 64, 4><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
+      else if (small)
+        flash_fwd_rows_f32<32, 32, 8><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
       else
-        flash_fwd_rows_f32<32, 32><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
+        flash_fwd_rows_f32<32, 32, 4><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
       return check_launch("pdh_flash_fwd");
     }
     PDH_REQUIRE((nrows + 3) / 4 <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: too many rows");

@@ -209,13 +209,15 @@ def test_flash_fwd_fp32_generic_matches_oracle(K, T, S, E, OD, causal):
 @pytest.mark.parametrize(
     "B,Hq,Hkv,T,S,D,band",
     [(1, 1, 1, 256, 256, 64, None), (1, 2, 2, 300, 290, 64, (None, 0)), (2, 4, 2, 130, 1000, 32, None),
-     (1, 2, 1, 200, 333, 64, (-70, 5)), (1, 3, 3, 65, 64, 32, (None, 600)), (1, 2, 2, 129, 129, 64, (None, -1))],
+     (1, 2, 1, 200, 333, 64, (-70, 5)), (1, 3, 3, 65, 64, 32, (None, 600)), (1, 2, 2, 129, 129, 64, (None, -1)),
+     (4, 16, 8, 1024, 1024, 64, (None, 0)), (2, 32, 32, 500, 700, 32, None)],
 )
 def test_flash_fwd_fp32_row_kernel_matches_oracle(K, B, Hq, Hkv, T, S, D, band):
     """e = od = 32 or 64 at fp32 take the row kernel (lane = query row, K / V
-    rows as wave-uniform loads, the key range split over four waves): causal,
-    windowed, half-open and fully-masked-row bands (the last disables the
-    prune), grouped heads, row and key tails, the artifacts."""
+    rows as wave-uniform loads, the key range split over eight waves on grids
+    under one workgroup per CU, four on the last two cases' larger grids):
+    causal, windowed, half-open and fully-masked-row bands (the last disables
+    the prune), grouped heads, row and key tails, the artifacts."""
     rng = np.random.default_rng(T * 7 + S + D)
     q, k, v = _qkv(rng, B, Hq, Hkv, T, S, D, D, torch.float32)
     res = K.flash_fwd(q, k, v, scale=D**-0.5, band=K.Band(*band) if band else None, want_artifacts=True)
@@ -228,6 +230,19 @@ def test_pruned_sweep_is_bit_equal_to_the_full_sweep(K, dtype):
     rng = np.random.default_rng(11)
     D = 128 if dtype != torch.float32 else 40
     q, k, v = _qkv(rng, 1, 2, 2, 320, 320, D, D, dtype)
+    full = K.flash_fwd(q, k, v, band=K.CAUSAL, prune=False, want_artifacts=True)
+    pruned = K.flash_fwd(q, k, v, band=K.CAUSAL, prune=True, want_artifacts=True)
+    torch.cuda.synchronize()
+    assert torch.equal(full.o, pruned.o)
+    assert torch.equal(full.m, pruned.m) and torch.equal(full.den, pruned.den)
+
+
+@pytest.mark.parametrize("B,H,T", [(1, 2, 320), (8, 32, 256)])
+def test_the_row_kernel_prunes_bit_exactly(K, B, H, T):
+    """The fp32 row kernel at both wave counts (a grid under one workgroup
+    per CU, and one over): a causal prune leaves every bit as the full sweep."""
+    rng = np.random.default_rng(12)
+    q, k, v = _qkv(rng, B, H, H, T, T, 64, 64, torch.float32)
     full = K.flash_fwd(q, k, v, band=K.CAUSAL, prune=False, want_artifacts=True)
     pruned = K.flash_fwd(q, k, v, band=K.CAUSAL, prune=True, want_artifacts=True)
     torch.cuda.synchronize()
