@@ -614,8 +614,8 @@ __global__ __launch_bounds__(256) void flash_fwd_generic_f32(GenArgs a, int64_t 
 // groups in order over the workgroup's key range (the union of its rows'
 // ranges), and the NW partial states (m, l, o) merge through LDS with the
 // associative combine (zoo/attention.py:40-46). Grids that fill the chip run
-// four waves a workgroup; smaller ones eight, which halves each wave's serial
-// sweep (the scalar K / V reads are latency-bound). Each row keeps the generic
+// it with four waves a workgroup; smaller ones take flash_fwd_rows_f32_lds
+// (eight waves, K / V staged through LDS), whose waves each sweep fewer keys. Each row keeps the generic
 // kernel's semantics: with pruning it sees exactly the 64-key chunks the band
 // leaves it, a masked score inside them is the fill, and keys past s take no
 // part. A group the prune skips holds only fill scores, whose exponentials
@@ -728,6 +728,175 @@ __global__ __launch_bounds__(64 * NW) void flash_fwd_rows_f32(GenArgs a, int nqb
     for (int f = 0; f < OD; ++f) pw[f][lane] = acc[f];
     pw[OD][lane] = m;
     pw[OD + 1][lane] = l;
+  }
+  __syncthreads();
+  if (w != 0) return;
+  float mw[NW - 1], M = m;
+#pragma unroll
+  for (int i = 0; i < NW - 1; ++i) {
+    mw[i] = part[i][OD][lane];
+    M = fmaxf(M, mw[i]);
+  }
+  float wt[NW];
+  wt[0] = m == -kInf ? 0.f : __expf(m - M);
+#pragma unroll
+  for (int i = 0; i < NW - 1; ++i) wt[i + 1] = mw[i] == -kInf ? 0.f : __expf(mw[i] - M);
+  float L = l * wt[0];
+#pragma unroll
+  for (int i = 0; i < NW - 1; ++i) L += part[i][OD + 1][lane] * wt[i + 1];
+  if (!rin) return;
+  const float inv = 1.0f / L;
+  float* orow = a.o + b * a.o_sb + hq * a.o_sh + t * a.o_st;
+#pragma unroll
+  for (int f = 0; f < OD; ++f) {
+    float v = acc[f] * wt[0];
+#pragma unroll
+    for (int i = 0; i < NW - 1; ++i) v += part[i][f][lane] * wt[i + 1];
+    orow[f] = v * inv;
+  }
+  const int64_t grow = inst * a.t + t;
+  if (a.m_out) a.m_out[grow] = M;
+  if (a.den_out) a.den_out[grow] = L;
+  if (a.lse_out) a.lse_out[grow] = M + __logf(L);
+}
+
+// The same recurrence for grids under one workgroup per compute unit, with
+// eight waves and the keys staged through LDS: the workgroup copies each
+// 64-key chunk of K and V (coalesced rows, zero past the range) into LDS,
+// and each wave reads its group's rows as broadcast LDS reads instead of
+// latency-bound scalar loads. (Loading the next chunk during the sweep needs
+// registers this kernel does not have: it spilled and ran 10-15% slower.) A chunk is the
+// eight groups of eight keys the eight waves own (group g to wave g mod 8, as
+// in flash_fwd_rows_f32<E, OD, 8>, with the same arithmetic per key), so the
+// results are bit-identical to that kernel's (measured) and pruning changes no bit. The
+// chunk buffers become the merge slots once every wave is done with them.
+template <int E, int OD>
+__global__ __launch_bounds__(512) void flash_fwd_rows_f32_lds(GenArgs a, int nqb) {
+  constexpr int NW = 8, CH = 64;
+  constexpr int KS = CH * E, VS = CH * OD;       // floats of one staged chunk
+  constexpr int MS = (NW - 1) * (OD + 2) * 64;   // floats of the merge slots
+  constexpr int SM = KS + VS > MS ? KS + VS : MS;
+  constexpr int KPT = KS / (64 * NW), VPT = VS / (64 * NW);
+  static_assert(KS % (64 * NW) == 0 && VS % (64 * NW) == 0, "a chunk splits evenly over the threads");
+  __shared__ __attribute__((aligned(16))) float sm[SM];
+  float* ks = sm;
+  float* vs = sm + KS;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int64_t inst = blockIdx.x / nqb;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x % nqb) * 64;
+  const int64_t t = row0 + lane;
+  const bool rin = t < a.t;
+  const int64_t tc = rin ? t : a.t - 1;
+  const int64_t b = inst / a.heads_q, hq = inst % a.heads_q, hk = hq / (a.heads_q / a.heads_kv);
+  const float* __restrict__ qr = a.q + b * a.q_sb + hq * a.q_sh + tc * a.q_st;
+  const float* __restrict__ kp = a.k + b * a.k_sb + hk * a.k_sh;
+  const float* __restrict__ vp = a.v + b * a.v_sb + hk * a.v_sh;
+
+  auto chunks = [&](int64_t row, int64_t& lo, int64_t& hi) {
+    lo = 0;
+    hi = (a.s + 63) / 64;
+    if (a.masked && a.prune) {
+      if (a.band_hi < INT64_MAX / 4) {
+        const int64_t smax = row + a.band_hi;
+        hi = smax < 0 ? 0 : (smax / 64 + 1 < hi ? smax / 64 + 1 : hi);
+      }
+      if (a.band_lo > INT64_MIN / 4) {
+        const int64_t smin = row + a.band_lo;
+        lo = smin <= 0 ? 0 : smin / 64;
+      }
+    }
+  };
+  int64_t rlo, rhi, blo, bhi, tmp;
+  chunks(tc, rlo, rhi);
+  chunks(row0, blo, tmp);
+  chunks((row0 + 63 < a.t ? row0 + 63 : a.t - 1), tmp, bhi);
+  const int64_t klo = blo * 64, khi = (bhi * 64 < a.s ? bhi * 64 : a.s);
+  const int64_t kr_lo = rlo * 64, kr_hi = rhi * 64;
+
+  float q[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) q[e] = qr[e];
+  float m = -kInf, l = 0.f, acc[OD];
+#pragma unroll
+  for (int f = 0; f < OD; ++f) acc[f] = 0.f;
+
+  // thread tid stages floats tid, tid + 512, ... of the chunk's K rows (and V
+  // rows): consecutive threads read consecutive features of a row
+  float kreg[KPT], vreg[VPT];
+  auto fetch = [&](int64_t c0) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int idx = tid + 64 * NW * i;
+      const int64_t key = c0 + idx / E;
+      kreg[i] = key < khi ? kp[key * a.k_st + idx % E] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int idx = tid + 64 * NW * i;
+      const int64_t key = c0 + idx / OD;
+      vreg[i] = key < khi ? vp[key * a.v_st + idx % OD] : 0.f;
+    }
+  };
+  const int64_t nch = khi > klo ? (khi - klo + CH - 1) / CH : 0;  // klo is a multiple of 64
+  for (int64_t ci = 0; ci < nch; ++ci) {
+    const int64_t c0 = klo + ci * CH;
+    fetch(c0);
+    __syncthreads();  // every wave is done with the previous chunk
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) ks[tid + 64 * NW * i] = kreg[i];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) vs[tid + 64 * NW * i] = vreg[i];
+    __syncthreads();  // the chunk is in LDS
+    const int64_t k0 = c0 + 8 * w;     // this wave's group of the chunk
+    if (k0 >= khi) continue;
+    const float* __restrict__ kw = ks + 8 * w * E;
+    const float* __restrict__ vw = vs + 8 * w * OD;
+    float sc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sc[j] = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sc[j] = __builtin_fmaf(q[e], kw[j * E + e], sc[j]);
+    float mx = m;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t key = k0 + j;
+      float x = sc[j] * a.scale;
+      if (a.masked) {
+        const int64_t d = key - tc;
+        if (d < a.band_lo || d > a.band_hi) x = a.fill;
+      }
+      const bool in = key < khi && key >= kr_lo && key < kr_hi;
+      sc[j] = in ? x : -kInf;
+      mx = fmaxf(mx, sc[j]);
+    }
+    if (mx == -kInf) continue;
+    const float alpha = m == -kInf ? 0.f : __expf(m - mx);
+    float p[8], ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = sc[j] == -kInf ? 0.f : __expf(sc[j] - mx);
+      ps += p[j];
+    }
+    l = l * alpha + ps;
+    m = mx;
+#pragma unroll
+    for (int f = 0; f < OD; ++f) {
+      float s_ = acc[f] * alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s_ = __builtin_fmaf(p[j], vw[j * OD + f], s_);
+      acc[f] = s_;
+    }
+  }
+  __syncthreads();  // the chunk buffers become the merge slots
+
+  float (*part)[OD + 2][64] = reinterpret_cast<float (*)[OD + 2][64]>(sm);
+  if (w > 0) {
+#pragma unroll
+    for (int f = 0; f < OD; ++f) part[w - 1][f][lane] = acc[f];
+    part[w - 1][OD][lane] = m;
+    part[w - 1][OD + 1][lane] = l;
   }
   __syncthreads();
   if (w != 0) return;
@@ -886,14 +1055,15 @@ int flash_fwd_impl(const void* q, const void* k, const void* v, void* o, float* 
       const int64_t nqb = (G.t + 63) / 64;
       PDH_REQUIRE(ninst * nqb <= INT32_MAX && nqb <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: too many rows");
       const dim3 grid(static_cast<unsigned>(ninst * nqb));
-      const int cus = pdh_device_cus();
-      const bool small = ninst * nqb < (cus > 0 ? cus : 256);  // under one workgroup per compute unit
+      static int cus = 0;  // compute units, read once (one device per process)
+      if (cus == 0) cus = pdh_device_cus() > 0 ? pdh_device_cus() : 256;
+      const bool small = ninst * nqb < cus;  // under one workgroup per compute unit
       if (G.e == 64 && small)
-        flash_fwd_rows_f32<64, 64, 8><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
+        flash_fwd_rows_f32_lds<64, 64><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
       else if (G.e == 64)
         flash_fwd_rows_f32<64, 64, 4><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
       else if (small)
-        flash_fwd_rows_f32<32, 32, 8><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
+        flash_fwd_rows_f32_lds<32, 32><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
       else
         flash_fwd_rows_f32<32, 32, 4><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
       return check_launch("pdh_flash_fwd");

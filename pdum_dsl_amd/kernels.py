@@ -284,6 +284,47 @@ def flash_fwd(
     return FlashOut(o, lse, m, den)
 
 
+def flash_fwd_prepared(q, k, v, *, scale: float | None = None, band: Band | None = None, fill: float = -1e9,
+                       prune: bool = True, out: torch.Tensor | None = None, lse: torch.Tensor | None = None):
+    """``flash_fwd`` (one workgroup sweep per query block, no key split, no
+    artifacts) with its geometry, pointers and stream bound once: returns a
+    function of no arguments that launches the kernel into ``out`` (and
+    ``lse``) on the stream current now. For loops that call the same shapes
+    many times (serving, small heads), where the per-call wrapper's host work
+    outweighs the launch. The tensors must stay alive and in place."""
+    _require_cuda(q, k, v)
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DT:
+        raise ValueError(f"q/k/v must share one dtype of f32/bf16/f16 (got {q.dtype}, {k.dtype}, {v.dtype})")
+    B, H, T, _ = q.shape
+    o = torch.empty(q.shape[:3] + (v.shape[3],), dtype=q.dtype, device=q.device) if out is None else out
+    g = _geom(q, k, v, o)
+    if lse is None:
+        lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    elif lse.shape != (B, H, T) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("lse must be a contiguous fp32 [batch, heads, rows] tensor")
+    sc = 1.0 / math.sqrt(q.shape[3]) if scale is None else float(scale)
+    kind, (lo, hi) = (PDH_MASK_NONE, (0, 0)) if band is None else (PDH_MASK_BAND, band.c_args())
+    _lib.lib()  # loaded and declared (raises if the library is missing)
+    # the same symbol through a handle without argtypes: the arguments are built
+    # once as their exact C types, so a call does no per-argument conversion
+    fn = getattr(C.CDLL(str(_lib.LIB_PATH)), "pdh_flash_fwd")
+    fn.restype = C.c_int
+    i64, i32 = C.c_int64, C.c_int
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), C.c_void_p(None), C.c_void_p(None), _ptr(lse), C.byref(g),
+            i32(_DT[q.dtype]), C.c_float(sc), C.c_float(fill), i32(kind), i64(lo), i64(hi), i32(int(bool(prune))),
+            C.c_void_p(_stream()))
+    keep = (q, k, v, o, lse, g)  # the bound pointers' owners live as long as the call
+
+    def call():
+        rc = fn(*args)
+        if rc:
+            _lib.check("pdh_flash_fwd", rc)
+        return keep[3]
+
+    call.o, call.lse = o, lse
+    return call
+
+
 def pick_fwd_splits(ninst: int, t: int, s: int, cus: int | None = None) -> int:
     """Key splits for the 16-bit forward: 1 when the instances x 128-row query
     blocks give every CU two workgroups, or a row has under 16 key tiles

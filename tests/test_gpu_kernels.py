@@ -367,3 +367,18 @@ def test_entry_points_refuse_bad_shapes_without_launching(K):
         K.flash_fwd(q, q, q)
     with pytest.raises(ValueError, match="f32, bf16 or f16"):
         K.row_softmax(q.double())
+
+
+@pytest.mark.parametrize("dtype,D,band", [(torch.float32, 64, None), (torch.bfloat16, 128, (None, 0))])
+def test_the_prepared_forward_call_equals_the_wrapper(K, dtype, D, band):
+    """flash_fwd_prepared binds geometry, pointers and stream once; each call
+    launches the same kernel as flash_fwd (bit-equal output and lse)."""
+    rng = np.random.default_rng(21)
+    q, k, v = _qkv(rng, 1, 2, 2, 256, 256, D, D, dtype)
+    b = K.Band(*band) if band else None
+    want = K.flash_fwd(q, k, v, scale=D**-0.5, band=b, nsplit=1)
+    call = K.flash_fwd_prepared(q, k, v, scale=D**-0.5, band=b)
+    for _ in range(3):
+        o = call()
+    torch.cuda.synchronize()
+    assert torch.equal(o, want.o) and torch.equal(call.lse, want.lse)
