@@ -605,174 +605,30 @@ __global__ __launch_bounds__(256) void flash_fwd_generic_f32(GenArgs a, int64_t 
   }
 }
 
-// The fp32 kernel for heads of E = OD = 32 or 64 features: lane =
-// query row, 64 rows per workgroup. A key's K and V rows are the same for
-// every lane, so they are read as wave-uniform (scalar) loads and each lane
-// runs its own row's recurrence with no cross-lane reduction; eight keys per
-// step give eight independent score chains. The groups of eight keys (on the
-// absolute key grid) go round-robin to the NW waves, each sweeping its
-// groups in order over the workgroup's key range (the union of its rows'
-// ranges), and the NW partial states (m, l, o) merge through LDS with the
-// associative combine (zoo/attention.py:40-46). Grids that fill the chip run
-// it with four waves a workgroup; smaller ones take flash_fwd_rows_f32_lds
-// (eight waves, K / V staged through LDS), whose waves each sweep fewer keys. Each row keeps the generic
-// kernel's semantics: with pruning it sees exactly the 64-key chunks the band
-// leaves it, a masked score inside them is the fill, and keys past s take no
-// part. A group the prune skips holds only fill scores, whose exponentials
-// vanish against the row's live maximum, and the assignment of groups to
-// waves does not move with the range: pruned and unpruned sweeps agree bit
-// for bit.
-template <int E, int OD, int NW>
-__global__ __launch_bounds__(64 * NW) void flash_fwd_rows_f32(GenArgs a, int nqb) {
-  __shared__ float part[NW - 1][OD + 2][64];  // waves 1..NW-1: o[0..OD), m, l per lane
-  const int lane = threadIdx.x & 63, w = wave_id();
-  const int64_t inst = blockIdx.x / nqb;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x % nqb) * 64;
-  const int64_t t = row0 + lane;
-  const bool rin = t < a.t;
-  const int64_t tc = rin ? t : a.t - 1;  // clamped: every load stays inside q
-  const int64_t b = inst / a.heads_q, hq = inst % a.heads_q, hk = hq / (a.heads_q / a.heads_kv);
-  const float* __restrict__ qr = a.q + b * a.q_sb + hq * a.q_sh + tc * a.q_st;
-  const float* __restrict__ kp = a.k + b * a.k_sb + hk * a.k_sh;
-  const float* __restrict__ vp = a.v + b * a.v_sb + hk * a.v_sh;
-
-  // a row's 64-key chunks [c_lo, c_hi) (the generic kernel's prune); the
-  // workgroup's range is the union, from its first and last rows (the ends
-  // grow with the row)
-  auto chunks = [&](int64_t row, int64_t& lo, int64_t& hi) {
-    lo = 0;
-    hi = (a.s + 63) / 64;
-    if (a.masked && a.prune) {
-      if (a.band_hi < INT64_MAX / 4) {
-        const int64_t smax = row + a.band_hi;
-        hi = smax < 0 ? 0 : (smax / 64 + 1 < hi ? smax / 64 + 1 : hi);
-      }
-      if (a.band_lo > INT64_MIN / 4) {
-        const int64_t smin = row + a.band_lo;
-        lo = smin <= 0 ? 0 : smin / 64;
-      }
-    }
-  };
-  int64_t rlo, rhi, blo, bhi, tmp;
-  chunks(tc, rlo, rhi);
-  chunks(row0, blo, tmp);
-  chunks((row0 + 63 < a.t ? row0 + 63 : a.t - 1), tmp, bhi);
-  const int64_t klo = blo * 64, khi = (bhi * 64 < a.s ? bhi * 64 : a.s);  // keys of the workgroup
-  const int64_t kr_lo = rlo * 64, kr_hi = rhi * 64;                       // keys of this row
-  // this wave's groups of eight keys: k0 = 8 g for g = w (mod NW) in the range
-  const int64_t gfirst = klo / 8, glast = (khi + 7) / 8;  // klo is a multiple of 64
-  const int64_t g0 = gfirst + ((w - gfirst % NW) + NW) % NW;
-
-  float q[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) q[e] = qr[e];
-  float m = -kInf, l = 0.f, acc[OD];
-#pragma unroll
-  for (int f = 0; f < OD; ++f) acc[f] = 0.f;
-
-  for (int64_t g = g0; g < glast; g += NW) {
-    const int64_t k0 = 8 * g;
-    // the step's eight K and V rows (wave-uniform; a key past the range reads
-    // the last one and is excluded below)
-    const float* __restrict__ kr[8];
-    const float* __restrict__ vr[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t key = k0 + j < khi ? k0 + j : khi - 1;
-      kr[j] = kp + key * a.k_st;
-      vr[j] = vp + key * a.v_st;
-    }
-    float sc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sc[j] = 0.f;
-#pragma unroll
-    for (int e = 0; e < E; ++e)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sc[j] = __builtin_fmaf(q[e], kr[j][e], sc[j]);
-    float mx = m;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t key = k0 + j;
-      float x = sc[j] * a.scale;
-      if (a.masked) {
-        const int64_t d = key - tc;
-        if (d < a.band_lo || d > a.band_hi) x = a.fill;
-      }
-      const bool in = key < khi && key >= kr_lo && key < kr_hi;  // this row's chunks, under s
-      sc[j] = in ? x : -kInf;
-      mx = fmaxf(mx, sc[j]);
-    }
-    if (mx == -kInf) continue;  // no key of this step for this row (lanes that run on add zeros)
-    const float alpha = m == -kInf ? 0.f : __expf(m - mx);
-    float p[8], ps = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      p[j] = sc[j] == -kInf ? 0.f : __expf(sc[j] - mx);
-      ps += p[j];
-    }
-    l = l * alpha + ps;
-    m = mx;
-#pragma unroll
-    for (int f = 0; f < OD; ++f) {
-      float s_ = acc[f] * alpha;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s_ = __builtin_fmaf(p[j], vr[j][f], s_);
-      acc[f] = s_;
-    }
-  }
-
-  // merge: waves 1..NW-1 publish, wave 0 combines and stores
-  if (w > 0) {
-    float (*pw)[64] = part[w - 1];
-#pragma unroll
-    for (int f = 0; f < OD; ++f) pw[f][lane] = acc[f];
-    pw[OD][lane] = m;
-    pw[OD + 1][lane] = l;
-  }
-  __syncthreads();
-  if (w != 0) return;
-  float mw[NW - 1], M = m;
-#pragma unroll
-  for (int i = 0; i < NW - 1; ++i) {
-    mw[i] = part[i][OD][lane];
-    M = fmaxf(M, mw[i]);
-  }
-  float wt[NW];
-  wt[0] = m == -kInf ? 0.f : __expf(m - M);
-#pragma unroll
-  for (int i = 0; i < NW - 1; ++i) wt[i + 1] = mw[i] == -kInf ? 0.f : __expf(mw[i] - M);
-  float L = l * wt[0];
-#pragma unroll
-  for (int i = 0; i < NW - 1; ++i) L += part[i][OD + 1][lane] * wt[i + 1];
-  if (!rin) return;
-  const float inv = 1.0f / L;
-  float* orow = a.o + b * a.o_sb + hq * a.o_sh + t * a.o_st;
-#pragma unroll
-  for (int f = 0; f < OD; ++f) {
-    float v = acc[f] * wt[0];
-#pragma unroll
-    for (int i = 0; i < NW - 1; ++i) v += part[i][f][lane] * wt[i + 1];
-    orow[f] = v * inv;
-  }
-  const int64_t grow = inst * a.t + t;
-  if (a.m_out) a.m_out[grow] = M;
-  if (a.den_out) a.den_out[grow] = L;
-  if (a.lse_out) a.lse_out[grow] = M + __logf(L);
-}
-
-// The same recurrence for grids under one workgroup per compute unit, with
-// eight waves and the keys staged through LDS: the workgroup copies each
-// 64-key chunk of K and V (coalesced rows, zero past the range) into LDS,
-// and each wave reads its group's rows as broadcast LDS reads instead of
-// latency-bound scalar loads. (Loading the next chunk during the sweep needs
-// registers this kernel does not have: it spilled and ran 10-15% slower.) A chunk is the
-// eight groups of eight keys the eight waves own (group g to wave g mod 8, as
-// in flash_fwd_rows_f32<E, OD, 8>, with the same arithmetic per key), so the
-// results are bit-identical to that kernel's (measured) and pruning changes no bit. The
+// The fp32 kernel for heads of E = OD = 32 or 64 features: lane = query
+// row, 64 rows per workgroup, so each lane runs its own row's recurrence with
+// no cross-lane reduction, and a key's K and V rows are the same for every
+// lane. The workgroup copies each 64-key chunk of K and V (coalesced rows,
+// zero past the range) into LDS and the waves read their keys' rows as
+// broadcast LDS reads; eight keys per step give eight independent score
+// chains. The chunk's groups of eight keys (on the absolute key grid) go
+// round-robin to the NW waves (eight on grids under one workgroup per
+// compute unit, four otherwise), and the NW partial states (m, l, o) merge
+// through LDS with the associative combine (zoo/attention.py:40-46); the
 // chunk buffers become the merge slots once every wave is done with them.
-template <int E, int OD>
-__global__ __launch_bounds__(512) void flash_fwd_rows_f32_lds(GenArgs a, int nqb) {
-  constexpr int NW = 8, CH = 64;
+// Each row keeps the generic kernel's semantics: with pruning it sees exactly
+// the 64-key chunks the band leaves it, a masked score inside them is the
+// fill, and keys past s take no part. A group the prune skips holds only fill
+// scores, whose exponentials vanish against the row's live maximum, and the
+// assignment of groups to waves does not move with the range: pruned and
+// unpruned sweeps agree bit for bit. Measured against the same recurrence on
+// wave-uniform scalar loads (bit-equal results): 1.35-2.4x faster; loading
+// the next chunk during the sweep needs registers this kernel does not have
+// (it spilled and ran 10-15% slower).
+template <int E, int OD, int NW>
+__global__ __launch_bounds__(64 * NW) void flash_fwd_rows_f32_lds(GenArgs a, int nqb) {
+  constexpr int CH = 64;
+  static_assert(NW == 4 || NW == 8, "a chunk's eight groups split evenly over the waves");
   constexpr int KS = CH * E, VS = CH * OD;       // floats of one staged chunk
   constexpr int MS = (NW - 1) * (OD + 2) * 64;   // floats of the merge slots
   constexpr int SM = KS + VS > MS ? KS + VS : MS;
@@ -847,10 +703,11 @@ __global__ __launch_bounds__(512) void flash_fwd_rows_f32_lds(GenArgs a, int nqb
 #pragma unroll
     for (int i = 0; i < VPT; ++i) vs[tid + 64 * NW * i] = vreg[i];
     __syncthreads();  // the chunk is in LDS
-    const int64_t k0 = c0 + 8 * w;     // this wave's group of the chunk
+    for (int gi = w; gi < CH / 8; gi += NW) {  // this wave's groups of the chunk
+    const int64_t k0 = c0 + 8 * gi;
     if (k0 >= khi) continue;
-    const float* __restrict__ kw = ks + 8 * w * E;
-    const float* __restrict__ vw = vs + 8 * w * OD;
+    const float* __restrict__ kw = ks + 8 * gi * E;
+    const float* __restrict__ vw = vs + 8 * gi * OD;
     float sc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) sc[j] = 0.f;
@@ -887,6 +744,7 @@ __global__ __launch_bounds__(512) void flash_fwd_rows_f32_lds(GenArgs a, int nqb
 #pragma unroll
       for (int j = 0; j < 8; ++j) s_ = __builtin_fmaf(p[j], vw[j * OD + f], s_);
       acc[f] = s_;
+    }
     }
   }
   __syncthreads();  // the chunk buffers become the merge slots
@@ -1059,13 +917,13 @@ int flash_fwd_impl(const void* q, const void* k, const void* v, void* o, float* 
       if (cus == 0) cus = pdh_device_cus() > 0 ? pdh_device_cus() : 256;
       const bool small = ninst * nqb < cus;  // under one workgroup per compute unit
       if (G.e == 64 && small)
-        flash_fwd_rows_f32_lds<64, 64><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
+        flash_fwd_rows_f32_lds<64, 64, 8><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
       else if (G.e == 64)
-        flash_fwd_rows_f32<64, 64, 4><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
+        flash_fwd_rows_f32_lds<64, 64, 4><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
       else if (small)
-        flash_fwd_rows_f32_lds<32, 32><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
+        flash_fwd_rows_f32_lds<32, 32, 8><<<grid, 512, 0, st>>>(ga, static_cast<int>(nqb));
       else
-        flash_fwd_rows_f32<32, 32, 4><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
+        flash_fwd_rows_f32_lds<32, 32, 4><<<grid, 256, 0, st>>>(ga, static_cast<int>(nqb));
       return check_launch("pdh_flash_fwd");
     }
     PDH_REQUIRE((nrows + 3) / 4 <= INT32_MAX, PDH_EINVAL, "pdh_flash_fwd: too many rows");

@@ -214,7 +214,7 @@ def test_flash_fwd_fp32_generic_matches_oracle(K, T, S, E, OD, causal):
 )
 def test_flash_fwd_fp32_row_kernel_matches_oracle(K, B, Hq, Hkv, T, S, D, band):
     """e = od = 32 or 64 at fp32 take the row kernel (lane = query row, K / V
-    rows as wave-uniform loads, the key range split over eight waves on grids
+    chunks staged through LDS, the key range split over eight waves on grids
     under one workgroup per CU, four on the last two cases' larger grids):
     causal, windowed, half-open and fully-masked-row bands (the last disables
     the prune), grouped heads, row and key tails, the artifacts."""
