@@ -1,6 +1,6 @@
 // Flash-attention forward — the "flash" template row of the fusion registry
 // (fusion.py:480-615): the online-softmax fold over key tiles, with the
-// (out, m, den) artifacts of the §7.8 variant and lse = m + log(den).
+// (out, m, den) artifacts of the artifact variant (fusion.py:611-613) and lse = m + log(den).
 //
 // MFMA kernel (bf16 / f16 in, fp32 accumulate), e == od == D in {64, 128}:
 //   * workgroup = 4 waves x 32 query rows = 128 rows; key tiles of 32 rows,
